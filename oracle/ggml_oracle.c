@@ -1,0 +1,947 @@
+/*
+ * ggml_oracle.c -- TEST INFRASTRUCTURE ONLY (see ggml_oracle.h).
+ *
+ * Plain-C restatement of llama.rust's CPU kernels for the quantized ggml hot
+ * path.  Compiled with -ffp-contract=off so that every fused multiply-add is an
+ * explicit fmaf() where the reference uses f32::mul_add, and every other float
+ * operation rounds on its own, exactly as Rust evaluates it.
+ */
+#include "ggml_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define QK4_0 32
+#define QK8_0 32
+#define QK_K 256
+#define QK_MXFP4 32
+
+/* byte layouts: crates/ggml/src/blocks.rs:33-168 */
+typedef struct { uint16_t d; uint8_t qs[16]; } blk_q4_0;                       /* 18 B  */
+typedef struct { uint16_t d; int8_t qs[32]; } blk_q8_0;                        /* 34 B  */
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } blk_q4_K; /* 144 B */
+typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } blk_q6_K; /* 210 B */
+typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } blk_q8_K;       /* 292 B */
+typedef struct { uint8_t e; uint8_t qs[16]; } blk_mxfp4;                        /* 17 B  */
+
+_Static_assert(sizeof(blk_q4_0) == 18, "q4_0");
+_Static_assert(sizeof(blk_q8_0) == 34, "q8_0");
+_Static_assert(sizeof(blk_q4_K) == 144, "q4_K");
+_Static_assert(sizeof(blk_q6_K) == 210, "q6_K");
+_Static_assert(sizeof(blk_q8_K) == 292, "q8_K");
+_Static_assert(sizeof(blk_mxfp4) == 17, "mxfp4");
+
+double oracle_wtime(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return ts.tv_sec + 1e-9 * ts.tv_nsec;
+}
+
+/* ------------------------------------------------------------------ fp16 */
+
+static inline uint32_t fbits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float bitsf(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* IEEE binary32 -> binary16, round to nearest even (half 2.7.1 `f16::from_f32`). */
+uint16_t oracle_fp32_to_fp16(float f) {
+    uint32_t x = fbits(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t exp = (x >> 23) & 0xffu;
+    uint32_t man = x & 0x7fffffu;
+    if (exp == 0xff) {                              /* inf / NaN (quiet bit kept) */
+        return (uint16_t)(sign | 0x7c00u | (man ? (0x200u | (man >> 13)) : 0));
+    }
+    int32_t e = (int32_t)exp - 127 + 15;
+    if (e >= 0x1f) return (uint16_t)(sign | 0x7c00u); /* overflow */
+    if (e <= 0) {                                   /* subnormal half or zero */
+        if (e < -10) return (uint16_t)sign;
+        uint32_t m = man | 0x800000u;
+        uint32_t shift = (uint32_t)(14 - e);
+        uint32_t half_m = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1);
+        uint32_t halfway = 1u << (shift - 1);
+        if (rem > halfway || (rem == halfway && (half_m & 1))) half_m++;
+        return (uint16_t)(sign | half_m);
+    }
+    uint32_t h = sign | ((uint32_t)e << 10) | (man >> 13);
+    uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1))) h++; /* carries into exp correctly */
+    return (uint16_t)h;
+}
+
+float oracle_fp16_to_fp32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1fu;
+    uint32_t man = h & 0x3ffu;
+    if (exp == 0) {
+        if (man == 0) return bitsf(sign);
+        /* subnormal: man * 2^-24, exact */
+        float v = (float)man * bitsf(0x33800000u);
+        return sign ? -v : v;
+    }
+    if (exp == 0x1f) return bitsf(sign | 0x7f800000u | (man << 13));
+    return bitsf(sign | ((exp - 15 + 127) << 23) | (man << 13));
+}
+
+#define H2F(h) oracle_fp16_to_fp32(h)
+#define F2H(f) oracle_fp32_to_fp16(f)
+
+/* quants.rs:13 nearest_int -- magic-number round-to-nearest-even */
+int32_t oracle_nearest_int(float fval) {
+    float val = fval + 12582912.0f;
+    int32_t i;
+    memcpy(&i, &val, 4);
+    return (i & 0x007fffff) - 0x00400000;
+}
+#define nearest_int oracle_nearest_int
+
+static inline int imin_(int a, int b) { return a < b ? a : b; }
+static inline int imax_(int a, int b) { return a > b ? a : b; }
+
+/* quants.rs:660 KVALUES_MXFP4 */
+static const int8_t kvalues_mxfp4[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+
+/* quants.rs:682 e8m0_to_fp32_half: 2^(x-128) built from bits */
+float oracle_e8m0_to_fp32_half(uint8_t x) {
+    uint32_t bits = x < 2 ? (0x00200000u << x) : ((uint32_t)(x - 1) << 23);
+    return bitsf(bits);
+}
+
+/* ------------------------------------------------------------ quantizers */
+
+/* quants.rs:124-152 quantize_row_q4_0_ref */
+void oracle_quantize_row_q4_0_ref(const float *x, void *vy, int64_t k) {
+    blk_q4_0 *y = (blk_q4_0 *)vy;
+    const int64_t nb = k / QK4_0;
+    for (int64_t i = 0; i < nb; i++) {
+        float amax = 0.0f, max = 0.0f;
+        for (int j = 0; j < QK4_0; j++) {
+            const float v = x[i * QK4_0 + j];
+            if (amax < fabsf(v)) { amax = fabsf(v); max = v; }
+        }
+        const float d = max / -8.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        y[i].d = F2H(d);
+        for (int j = 0; j < QK4_0 / 2; j++) {
+            const float x0 = x[i * QK4_0 + j] * id;
+            const float x1 = x[i * QK4_0 + QK4_0 / 2 + j] * id;
+            const int8_t xi0 = (int8_t)imin_((int8_t)(x0 + 8.5f), 15);
+            const int8_t xi1 = (int8_t)imin_((int8_t)(x1 + 8.5f), 15);
+            y[i].qs[j] = (uint8_t)((xi0 & 0x0f) | ((xi1 & 0x0f) << 4));
+        }
+    }
+}
+
+/* quants.rs:302 quantize_row_q8_0_ref (roundf: half away from zero) */
+void oracle_quantize_row_q8_0_ref(const float *x, void *vy, int64_t k) {
+    blk_q8_0 *y = (blk_q8_0 *)vy;
+    const int64_t nb = k / QK8_0;
+    for (int64_t i = 0; i < nb; i++) {
+        float amax = 0.0f;
+        for (int j = 0; j < QK8_0; j++) amax = fmaxf(amax, fabsf(x[i * QK8_0 + j]));
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        y[i].d = F2H(d);
+        for (int j = 0; j < QK8_0; j++) y[i].qs[j] = (int8_t)roundf(x[i * QK8_0 + j] * id);
+    }
+}
+
+/* quants.rs:331-362 quantize_row_q8_0 (runtime AVX2 arithmetic): id = 127/amax,
+ * round-half-even, NaN/overflow -> -128. */
+void oracle_quantize_row_q8_0(const float *x, void *vy, int64_t k) {
+    blk_q8_0 *y = (blk_q8_0 *)vy;
+    const int64_t nb = k / QK8_0;
+    for (int64_t i = 0; i < nb; i++) {
+        float amax = 0.0f;
+        for (int j = 0; j < QK8_0; j++) amax = fmaxf(amax, fabsf(x[i * QK8_0 + j]));
+        const float d = amax / 127.0f;
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        y[i].d = F2H(d);
+        for (int j = 0; j < QK8_0; j++) {
+            const float r = nearbyintf(x[i * QK8_0 + j] * id);
+            y[i].qs[j] = (isnan(r) || fabsf(r) >= 2147483648.0f) ? (int8_t)-128 : (int8_t)(int)r;
+        }
+    }
+}
+
+/* quants.rs:615-650 quantize_row_q8_K_ref */
+void oracle_quantize_row_q8_K_ref(const float *x, void *vy, int64_t k) {
+    blk_q8_K *y = (blk_q8_K *)vy;
+    const int64_t nb = k / QK_K;
+    for (int64_t i = 0; i < nb; i++) {
+        const float *xb = x + i * QK_K;
+        float max = 0.0f, amax = 0.0f;
+        for (int j = 0; j < QK_K; j++) {
+            const float ax = fabsf(xb[j]);
+            if (ax > amax) { amax = ax; max = xb[j]; }
+        }
+        if (amax == 0.0f) {
+            memset(&y[i], 0, sizeof(blk_q8_K));
+            continue;
+        }
+        const float iscale = -127.0f / max;
+        for (int j = 0; j < QK_K; j++) {
+            const int v = nearest_int(iscale * xb[j]);
+            y[i].qs[j] = (int8_t)imin_(127, v);
+        }
+        for (int j = 0; j < QK_K / 16; j++) {
+            int sum = 0;
+            for (int ii = 0; ii < 16; ii++) sum += y[i].qs[j * 16 + ii];
+            y[i].bsums[j] = (int16_t)sum;
+        }
+        y[i].d = 1.0f / iscale;
+    }
+}
+
+/* repack.rs:1561-1620 quantize_mat_q8_K_4x8, per-row values: iscale = 127/amax,
+ * round-half-even, clamp to i8, d = 1/iscale; bsums over the stored values.
+ * Written as plain block_q8_K rows (the interleave only moves bytes). */
+void oracle_quantize_row_q8_K_mat(const float *x, void *vy, int64_t k) {
+    blk_q8_K *y = (blk_q8_K *)vy;
+    const int64_t nb = k / QK_K;
+    for (int64_t i = 0; i < nb; i++) {
+        const float *xb = x + i * QK_K;
+        float max_abs = 0.0f;
+        for (int j = 0; j < QK_K; j++) { const float a = fabsf(xb[j]); if (a > max_abs) max_abs = a; }
+        const float iscale = max_abs != 0.0f ? 127.0f / max_abs : 0.0f;
+        y[i].d = max_abs != 0.0f ? 1.0f / iscale : 0.0f;
+        for (int j = 0; j < QK_K; j++) {
+            float r = nearbyintf(iscale * xb[j]);
+            if (r < -128.0f) r = -128.0f;
+            if (r > 127.0f) r = 127.0f;
+            y[i].qs[j] = (int8_t)(int)r;
+        }
+        for (int j = 0; j < QK_K / 16; j++) {
+            int sum = 0;
+            for (int ii = 0; ii < 16; ii++) sum += y[i].qs[j * 16 + ii];
+            y[i].bsums[j] = (int16_t)sum;
+        }
+    }
+}
+
+/* quants_k.rs:1396-1490 make_qkx2_quants */
+static float make_qkx2_quants(int n, int nmax, const float *x, const float *weights,
+                              uint8_t *L, float *the_min, uint8_t *Laux,
+                              float rmin, float rdelta, int nstep, int use_mad) {
+    float min = x[0], max = x[0];
+    float sum_w = weights[0];
+    float sum_x = sum_w * x[0];
+    for (int i = 1; i < n; i++) {
+        if (x[i] < min) min = x[i];
+        if (x[i] > max) max = x[i];
+        const float w = weights[i];
+        sum_w += w;
+        sum_x += w * x[i];
+    }
+    if (min > 0.0f) min = 0.0f;
+    if (max == min) {
+        for (int i = 0; i < n; i++) L[i] = 0;
+        *the_min = -min;
+        return 0.0f;
+    }
+    float iscale = (float)nmax / (max - min);
+    float scale = 1.0f / iscale;
+    float best_error = 0.0f;
+    for (int i = 0; i < n; i++) {
+        const int l = nearest_int(iscale * (x[i] - min));
+        L[i] = (uint8_t)imax_(0, imin_(nmax, l));
+        float diff = scale * (float)L[i] + min - x[i];
+        diff = use_mad ? fabsf(diff) : diff * diff;
+        best_error += weights[i] * diff;
+    }
+    if (nstep < 1) { *the_min = -min; return scale; }
+    for (int is = 0; is <= nstep; is++) {
+        iscale = (rmin + rdelta * (float)is + (float)nmax) / (max - min);
+        float sum_l = 0.0f, sum_l2 = 0.0f, sum_xl = 0.0f;
+        for (int i = 0; i < n; i++) {
+            const int l = imax_(0, imin_(nmax, nearest_int(iscale * (x[i] - min))));
+            Laux[i] = (uint8_t)l;
+            const float w = weights[i];
+            sum_l += w * (float)l;
+            sum_l2 += w * (float)l * (float)l;
+            sum_xl += w * (float)l * x[i];
+        }
+        const float D = sum_w * sum_l2 - sum_l * sum_l;
+        if (D > 0.0f) {
+            float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
+            float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
+            if (this_min > 0.0f) { this_min = 0.0f; this_scale = sum_xl / sum_l2; }
+            float cur_error = 0.0f;
+            for (int i = 0; i < n; i++) {
+                float diff = this_scale * (float)Laux[i] + this_min - x[i];
+                diff = use_mad ? fabsf(diff) : diff * diff;
+                cur_error += weights[i] * diff;
+            }
+            if (cur_error < best_error) {
+                memcpy(L, Laux, (size_t)n);
+                best_error = cur_error;
+                scale = this_scale;
+                min = this_min;
+            }
+        }
+    }
+    *the_min = -min;
+    return scale;
+}
+
+/* quants_k.rs:1672 get_scale_min_k4 */
+static inline void get_scale_min_k4(int j, const uint8_t *q, uint8_t *d, uint8_t *m) {
+    if (j < 4) {
+        *d = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *d = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+    }
+}
+
+/* quants_k.rs:1861-1950 quantize_row_q4_K_ref */
+void oracle_quantize_row_q4_K_ref(const float *x, void *vy, int64_t k) {
+    blk_q4_K *y = (blk_q4_K *)vy;
+    const int64_t nb = k / QK_K;
+    uint8_t L[QK_K], Laux[32];
+    float weights[32], mins[QK_K / 32], scales[QK_K / 32];
+    for (int64_t i = 0; i < nb; i++) {
+        const float *xb = x + i * QK_K;
+        float max_scale = 0.0f, max_min = 0.0f;
+        for (int j = 0; j < QK_K / 32; j++) {
+            float sum_x2 = 0.0f;
+            for (int l = 0; l < 32; l++) sum_x2 += xb[32 * j + l] * xb[32 * j + l];
+            const float av_x = sqrtf(sum_x2 / 32.0f);
+            for (int l = 0; l < 32; l++) weights[l] = av_x + fabsf(xb[32 * j + l]);
+            scales[j] = make_qkx2_quants(32, 15, xb + 32 * j, weights, L + 32 * j, &mins[j], Laux,
+                                         -1.0f, 0.1f, 20, 0);
+            if (scales[j] > max_scale) max_scale = scales[j];
+            if (mins[j] > max_min) max_min = mins[j];
+        }
+        const float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
+        const float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
+        uint8_t sc[12];
+        memset(sc, 0, sizeof sc);
+        for (int j = 0; j < QK_K / 32; j++) {
+            uint8_t ls = (uint8_t)nearest_int(inv_scale * scales[j]);
+            uint8_t lm = (uint8_t)nearest_int(inv_min * mins[j]);
+            if (ls > 63) ls = 63;
+            if (lm > 63) lm = 63;
+            if (j < 4) {
+                sc[j] = ls;
+                sc[j + 4] = lm;
+            } else {
+                sc[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+                sc[j - 4] |= (uint8_t)((ls >> 4) << 6);
+                sc[j] |= (uint8_t)((lm >> 4) << 6);
+            }
+        }
+        const uint16_t dh = F2H(max_scale / 63.0f);
+        const uint16_t dminh = F2H(max_min / 63.0f);
+        for (int j = 0; j < QK_K / 32; j++) {
+            uint8_t s, m;
+            get_scale_min_k4(j, sc, &s, &m);
+            const float d = H2F(dh) * (float)s;
+            if (d == 0.0f) continue;
+            const float dm = H2F(dminh) * (float)m;
+            for (int ii = 0; ii < 32; ii++) {
+                const int l = nearest_int((xb[32 * j + ii] + dm) / d);
+                L[32 * j + ii] = (uint8_t)imax_(0, imin_(15, l));
+            }
+        }
+        y[i].d = dh;
+        y[i].dmin = dminh;
+        memcpy(y[i].scales, sc, 12);
+        uint8_t *q = y[i].qs;
+        for (int j = 0; j < QK_K; j += 64) {
+            for (int l = 0; l < 32; l++) q[l] = (uint8_t)(L[j + l] | (L[j + l + 32] << 4));
+            q += 32;
+        }
+    }
+}
+
+/* quants_k.rs:1170-1260 make_qx_quants (qw == NULL) */
+static float make_qx_quants(int n, int nmax, const float *x, int8_t *L, int rmse_type) {
+    float max = 0.0f, amax = 0.0f;
+    for (int i = 0; i < n; i++) {
+        const float ax = fabsf(x[i]);
+        if (ax > amax) { amax = ax; max = x[i]; }
+    }
+    if (amax < 1e-15f) {
+        for (int i = 0; i < n; i++) L[i] = 0;
+        return 0.0f;
+    }
+    float iscale = -(float)nmax / max;
+    if (rmse_type == 0) {
+        for (int i = 0; i < n; i++) {
+            const int l = nearest_int(iscale * x[i]);
+            L[i] = (int8_t)(nmax + imax_(-nmax, imin_(nmax - 1, l)));
+        }
+        return 1.0f / iscale;
+    }
+    int return_early = 0;
+    if (rmse_type < 0) { rmse_type = -rmse_type; return_early = 1; }
+#define WEIGHT(i) (rmse_type == 1 ? x[i] * x[i] : rmse_type == 2 ? 1.0f : rmse_type == 3 ? fabsf(x[i]) : sqrtf(fabsf(x[i])))
+    float sumlx = 0.0f, suml2 = 0.0f;
+    for (int i = 0; i < n; i++) {
+        int l = nearest_int(iscale * x[i]);
+        l = imax_(-nmax, imin_(nmax - 1, l));
+        L[i] = (int8_t)(l + nmax);
+        const float w = WEIGHT(i);
+        sumlx += w * x[i] * (float)l;
+        suml2 += w * (float)l * (float)l;
+    }
+    float scale = suml2 != 0.0f ? sumlx / suml2 : 0.0f;
+    if (return_early) return suml2 > 0.0f ? 0.5f * (scale + 1.0f / iscale) : 1.0f / iscale;
+    float best = scale * sumlx;
+    for (int is = -9; is <= 9; ++is) {
+        if (is == 0) continue;
+        iscale = -((float)nmax + 0.1f * (float)is) / max;
+        sumlx = suml2 = 0.0f;
+        for (int i = 0; i < n; i++) {
+            int l = nearest_int(iscale * x[i]);
+            l = imax_(-nmax, imin_(nmax - 1, l));
+            const float w = WEIGHT(i);
+            sumlx += w * x[i] * (float)l;
+            suml2 += w * (float)l * (float)l;
+        }
+        if (suml2 > 0.0f && sumlx * sumlx > best * suml2) {
+            for (int i = 0; i < n; i++) {
+                const int l = nearest_int(iscale * x[i]);
+                L[i] = (int8_t)(nmax + imax_(-nmax, imin_(nmax - 1, l)));
+            }
+            scale = sumlx / suml2;
+            best = scale * sumlx;
+        }
+    }
+#undef WEIGHT
+    return scale;
+}
+
+/* quants_k.rs:2058-2133 quantize_row_q6_K_ref */
+void oracle_quantize_row_q6_K_ref(const float *x, void *vy, int64_t k) {
+    blk_q6_K *y = (blk_q6_K *)vy;
+    const int64_t nb = k / QK_K;
+    int8_t L[QK_K];
+    float scales[QK_K / 16];
+    for (int64_t i = 0; i < nb; i++) {
+        const float *xb = x + i * QK_K;
+        float max_scale = 0.0f, max_abs_scale = 0.0f;
+        for (int ib = 0; ib < QK_K / 16; ib++) {
+            const float scale = make_qx_quants(16, 32, xb + 16 * ib, L + 16 * ib, 1);
+            scales[ib] = scale;
+            const float abs_scale = fabsf(scale);
+            if (abs_scale > max_abs_scale) { max_abs_scale = abs_scale; max_scale = scale; }
+        }
+        if (max_abs_scale < 1e-15f) {
+            memset(&y[i], 0, sizeof(blk_q6_K));
+            y[i].d = F2H(0.0f);
+            continue;
+        }
+        const float iscale = -128.0f / max_scale;
+        const uint16_t dh = F2H(1.0f / iscale);
+        int8_t sc[16];
+        for (int ib = 0; ib < QK_K / 16; ib++) sc[ib] = (int8_t)imin_(127, nearest_int(iscale * scales[ib]));
+        for (int j = 0; j < QK_K / 16; j++) {
+            const float d = H2F(dh) * (float)sc[j];
+            if (d == 0.0f) continue;
+            for (int ii = 0; ii < 16; ii++) {
+                int l = nearest_int(xb[16 * j + ii] / d);
+                l = imax_(-32, imin_(31, l));
+                L[16 * j + ii] = (int8_t)(l + 32);
+            }
+        }
+        uint8_t *ql = y[i].ql, *qh = y[i].qh;
+        for (int j = 0; j < QK_K; j += 128) {
+            for (int l = 0; l < 32; l++) {
+                const uint8_t q1 = L[j + l] & 0xF, q2 = L[j + l + 32] & 0xF;
+                const uint8_t q3 = L[j + l + 64] & 0xF, q4 = L[j + l + 96] & 0xF;
+                ql[l] = (uint8_t)(q1 | (q3 << 4));
+                ql[l + 32] = (uint8_t)(q2 | (q4 << 4));
+                qh[l] = (uint8_t)((L[j + l] >> 4) | ((L[j + l + 32] >> 4) << 2) |
+                                  ((L[j + l + 64] >> 4) << 4) | ((L[j + l + 96] >> 4) << 6));
+            }
+            ql += 64;
+            qh += 32;
+        }
+        memcpy(y[i].scales, sc, 16);
+        y[i].d = dh;
+    }
+}
+
+/* MXFP4 quantizer.  The reference has none (compute.rs:9861-9863); this is the
+ * published upstream ggml quantize_row_mxfp4_ref algorithm (ggml-quants.c),
+ * pinned by the SECT sections of parity/quants_ref_fp4.bin:
+ *   e = amax > 0 ? (u8)(floor(log2(amax)) - 2 + 127) : 0, d = e8m0_half(e),
+ *   nibble = argmin_i |kvalues[i]*d - x| (first minimum wins). */
+static int best_index_mxfp4(float x, float e) {
+    int best = 0;
+    float best_err = fabsf((float)kvalues_mxfp4[0] * e - x);
+    for (int i = 1; i < 16; i++) {
+        const float err = fabsf((float)kvalues_mxfp4[i] * e - x);
+        if (err < best_err) { best = i; best_err = err; }
+    }
+    return best;
+}
+
+void oracle_quantize_row_mxfp4_ref(const float *x, void *vy, int64_t k) {
+    blk_mxfp4 *y = (blk_mxfp4 *)vy;
+    const int64_t nb = k / QK_MXFP4;
+    for (int64_t i = 0; i < nb; i++) {
+        float amax = 0.0f;
+        for (int j = 0; j < QK_MXFP4; j++) {
+            const float v = x[i * QK_MXFP4 + j];
+            if (amax < fabsf(v)) amax = fabsf(v);
+        }
+        const uint8_t e = amax > 0.0f ? (uint8_t)(floorf(log2f(amax)) - 2 + 127) : 0;
+        const float d = oracle_e8m0_to_fp32_half(e);
+        y[i].e = e;
+        for (int j = 0; j < QK_MXFP4 / 2; j++) {
+            const int x0 = best_index_mxfp4(x[i * QK_MXFP4 + j], d);
+            const int x1 = best_index_mxfp4(x[i * QK_MXFP4 + QK_MXFP4 / 2 + j], d);
+            y[i].qs[j] = (uint8_t)(x0 | (x1 << 4));
+        }
+    }
+}
+
+/* ---------------------------------------------------------- dequantizers */
+
+/* quants.rs:142 / :363 / quants_k.rs via quants.rs:540,584 / quants.rs:732 */
+void oracle_dequantize_row(int type, const void *vx, float *y, int64_t k) {
+    if (type == OR_Q4_0) {
+        const blk_q4_0 *x = (const blk_q4_0 *)vx;
+        for (int64_t i = 0; i < k / QK4_0; i++) {
+            const float d = H2F(x[i].d);
+            for (int j = 0; j < 16; j++) {
+                y[i * 32 + j] = (float)((x[i].qs[j] & 0x0F) - 8) * d;
+                y[i * 32 + 16 + j] = (float)((x[i].qs[j] >> 4) - 8) * d;
+            }
+        }
+    } else if (type == OR_Q8_0) {
+        const blk_q8_0 *x = (const blk_q8_0 *)vx;
+        for (int64_t i = 0; i < k / QK8_0; i++) {
+            const float d = H2F(x[i].d);
+            for (int j = 0; j < 32; j++) y[i * 32 + j] = (float)x[i].qs[j] * d;
+        }
+    } else if (type == OR_Q4_K) {
+        const blk_q4_K *x = (const blk_q4_K *)vx;
+        for (int64_t i = 0; i < k / QK_K; i++) {
+            const float d = H2F(x[i].d), min = H2F(x[i].dmin);
+            const uint8_t *q = x[i].qs;
+            float *yy = y + i * QK_K;
+            int is = 0;
+            for (int j = 0; j < QK_K; j += 64) {
+                uint8_t sc, m;
+                get_scale_min_k4(is, x[i].scales, &sc, &m);
+                const float d1 = d * sc, m1 = min * m;
+                get_scale_min_k4(is + 1, x[i].scales, &sc, &m);
+                const float d2 = d * sc, m2 = min * m;
+                for (int l = 0; l < 32; l++) *yy++ = d1 * (float)(q[l] & 0xF) - m1;
+                for (int l = 0; l < 32; l++) *yy++ = d2 * (float)(q[l] >> 4) - m2;
+                q += 32;
+                is += 2;
+            }
+        }
+    } else if (type == OR_Q6_K) {
+        const blk_q6_K *x = (const blk_q6_K *)vx;
+        for (int64_t i = 0; i < k / QK_K; i++) {
+            const float d = H2F(x[i].d);
+            const uint8_t *ql = x[i].ql, *qh = x[i].qh;
+            const int8_t *sc = x[i].scales;
+            float *yy = y + i * QK_K;
+            for (int n = 0; n < QK_K; n += 128) {
+                for (int l = 0; l < 32; l++) {
+                    const int is = l / 16;
+                    const int8_t q1 = (int8_t)((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                    const int8_t q2 = (int8_t)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                    const int8_t q3 = (int8_t)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                    const int8_t q4 = (int8_t)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                    yy[l] = d * (float)sc[is + 0] * (float)q1;
+                    yy[l + 32] = d * (float)sc[is + 2] * (float)q2;
+                    yy[l + 64] = d * (float)sc[is + 4] * (float)q3;
+                    yy[l + 96] = d * (float)sc[is + 6] * (float)q4;
+                }
+                yy += 128;
+                ql += 64;
+                qh += 32;
+                sc += 8;
+            }
+        }
+    } else if (type == OR_MXFP4) {
+        const blk_mxfp4 *x = (const blk_mxfp4 *)vx;
+        for (int64_t i = 0; i < k / QK_MXFP4; i++) {
+            const float d = oracle_e8m0_to_fp32_half(x[i].e);
+            for (int j = 0; j < 16; j++) {
+                y[i * 32 + j] = (float)kvalues_mxfp4[x[i].qs[j] & 0x0F] * d;
+                y[i * 32 + 16 + j] = (float)kvalues_mxfp4[x[i].qs[j] >> 4] * d;
+            }
+        }
+    } else if (type == OR_Q8_K) {
+        const blk_q8_K *x = (const blk_q8_K *)vx;
+        for (int64_t i = 0; i < k / QK_K; i++)
+            for (int j = 0; j < QK_K; j++) y[i * QK_K + j] = x[i].d * (float)x[i].qs[j];
+    }
+}
+
+/* ------------------------------------------------------ integer partials */
+
+/* Exact integer partials of one (weight row, activation row, block).  These
+ * are what every route of the reference computes before any float op. */
+
+/* q4_0 x q8_0, one 32-block: sum (nib-8)*q8 (repack.rs:3351 / vec_dot.rs:599) */
+static inline int32_t isum_q4_0(const blk_q4_0 *x, const blk_q8_0 *y) {
+    int32_t s = 0;
+    for (int j = 0; j < 16; j++) {
+        s += ((x->qs[j] & 0x0F) - 8) * y->qs[j];
+        s += ((x->qs[j] >> 4) - 8) * y->qs[16 + j];
+    }
+    return s;
+}
+
+/* unpacked 6-bit scales/mins of a q4_K block (same values as
+ * unpack_q4k_scales_bytes, repack.rs:1323) */
+static inline void q4k_scales(const blk_q4_K *x, uint8_t s[8], uint8_t m[8]) {
+    for (int j = 0; j < 8; j++) get_scale_min_k4(j, x->scales, &s[j], &m[j]);
+}
+
+/* q4_K x q8_K, sub-block pair g (elements 64g..64g+63):
+ * iacc_g = s_2g*sum(lo*q8) + s_2g+1*sum(hi*q8); imin_g = m_2g*b_lo + m_2g+1*b_hi
+ * (repack.rs:1664-1680). */
+static inline void isum_q4_K_pair(const blk_q4_K *x, const blk_q8_K *y, int g,
+                                  const uint8_t s[8], const uint8_t m[8],
+                                  int32_t *iacc, int32_t *imin) {
+    int32_t lo = 0, hi = 0;
+    for (int e = 0; e < 32; e++) {
+        lo += (x->qs[32 * g + e] & 0x0F) * y->qs[64 * g + e];
+        hi += (x->qs[32 * g + e] >> 4) * y->qs[64 * g + 32 + e];
+    }
+    const int32_t b_lo = y->bsums[4 * g] + y->bsums[4 * g + 1];
+    const int32_t b_hi = y->bsums[4 * g + 2] + y->bsums[4 * g + 3];
+    *iacc = lo * s[2 * g] + hi * s[2 * g + 1];
+    *imin = m[2 * g] * b_lo + m[2 * g + 1] * b_hi;
+}
+
+/* q6_K value e of a super-block (0..63, unbiased) */
+static inline int q6_val(const blk_q6_K *x, int e) {
+    const int j = e / 128, k = (e % 128) / 32, ii = e % 32;
+    const uint8_t *ql = x->ql + 64 * j, *qh = x->qh + 32 * j;
+    switch (k) {
+    case 0: return (ql[ii] & 0x0F) | ((qh[ii] & 0x03) << 4);
+    case 1: return (ql[32 + ii] & 0x0F) | (((qh[ii] >> 2) & 0x03) << 4);
+    case 2: return (ql[ii] >> 4) | (qh[ii] & 0x30);
+    default: return (ql[32 + ii] >> 4) | ((qh[ii] & 0xC0) >> 2);
+    }
+}
+
+/* q6_K x q8_K, whole super-block: sum_s scale_s * sum (q6-32)*q8 */
+static inline int32_t isum_q6_K(const blk_q6_K *x, const blk_q8_K *y) {
+    int32_t s = 0;
+    for (int sb = 0; sb < 16; sb++) {
+        int32_t t = 0;
+        for (int e = 16 * sb; e < 16 * sb + 16; e++) t += (q6_val(x, e) - 32) * y->qs[e];
+        s += t * x->scales[sb];
+    }
+    return s;
+}
+
+/* mxfp4 x q8_0, one 32-block (repack.rs:1048-1075) */
+static inline int32_t isum_mxfp4(const blk_mxfp4 *x, const blk_q8_0 *y) {
+    int32_t s = 0;
+    for (int j = 0; j < 16; j++) {
+        s += kvalues_mxfp4[x->qs[j] & 0x0F] * y->qs[j];
+        s += kvalues_mxfp4[x->qs[j] >> 4] * y->qs[16 + j];
+    }
+    return s;
+}
+
+/* ------------------------------------------- dots in the reference order */
+
+/* vec_dot.rs:564 hsum8 */
+static inline float hsum8(const float a[8]) {
+    float r[4];
+    for (int i = 0; i < 4; i++) r[i] = a[i + 4] + a[i];
+    const float s0 = r[0] + r[2], s1 = r[1] + r[3];
+    return s0 + s1;
+}
+
+/* vec_dot.rs:599-618 */
+float oracle_vec_dot_q4_0_q8_0(int n, const void *vx, const void *vy) {
+    const blk_q4_0 *x = (const blk_q4_0 *)vx;
+    const blk_q8_0 *y = (const blk_q8_0 *)vy;
+    float acc[8] = {0};
+    for (int ib = 0; ib < n / QK8_0; ib++) {
+        const float d = H2F(x[ib].d) * H2F(y[ib].d);
+        for (int l = 0; l < 8; l++) {
+            int32_t q = 0;
+            for (int i = 0; i < 4; i++) {
+                const int e = 4 * l + i;
+                const int v = e < 16 ? (x[ib].qs[e] & 0x0F) : (x[ib].qs[e - 16] >> 4);
+                q += (v - 8) * y[ib].qs[e];
+            }
+            acc[l] = fmaf(d, (float)q, acc[l]);
+        }
+    }
+    return hsum8(acc);
+}
+
+/* vec_dot.rs:872-918 */
+float oracle_vec_dot_q4_K_q8_K(int n, const void *vx, const void *vy) {
+    const blk_q4_K *x = (const blk_q4_K *)vx;
+    const blk_q8_K *y = (const blk_q8_K *)vy;
+    float acc[8] = {0}, acc_m[4] = {0};
+    for (int i = 0; i < n / QK_K; i++) {
+        const float d = y[i].d * H2F(x[i].d);
+        const float dmin = -y[i].d * H2F(x[i].dmin);
+        uint8_t sc[8], mn[8];
+        q4k_scales(&x[i], sc, mn);
+        for (int l = 0; l < 4; l++) {
+            const int32_t lo = y[i].bsums[4 * l] + y[i].bsums[4 * l + 1];
+            const int32_t hi = y[i].bsums[4 * l + 2] + y[i].bsums[4 * l + 3];
+            const int32_t prod = mn[2 * l] * lo + mn[2 * l + 1] * hi;
+            acc_m[l] = fmaf(dmin, (float)prod, acc_m[l]);
+        }
+        int32_t sumi[8] = {0};
+        for (int j = 0; j < QK_K / 64; j++) {
+            for (int l = 0; l < 8; l++) {
+                int32_t a = 0, b = 0;
+                for (int ii = 0; ii < 4; ii++) {
+                    const int e = 4 * l + ii;
+                    a += (x[i].qs[32 * j + e] & 0x0F) * y[i].qs[64 * j + e];
+                    b += (x[i].qs[32 * j + e] >> 4) * y[i].qs[64 * j + 32 + e];
+                }
+                sumi[l] += sc[2 * j] * a + sc[2 * j + 1] * b;
+            }
+        }
+        for (int l = 0; l < 8; l++) acc[l] = fmaf(d, (float)sumi[l], acc[l]);
+    }
+    const float m0 = acc_m[0] + acc_m[2], m1 = acc_m[1] + acc_m[3];
+    return hsum8(acc) + (m0 + m1);
+}
+
+/* vec_dot.rs:990-1040 */
+float oracle_vec_dot_q6_K_q8_K(int n, const void *vx, const void *vy) {
+    const blk_q6_K *x = (const blk_q6_K *)vx;
+    const blk_q8_K *y = (const blk_q8_K *)vy;
+    float acc[8] = {0};
+    for (int i = 0; i < n / QK_K; i++) {
+        const float d = y[i].d * H2F(x[i].d);
+        const int8_t *sc = x[i].scales;
+        int32_t sumi[8] = {0};
+        for (int j = 0; j < 2; j++)
+            for (int k = 0; k < 4; k++)
+                for (int ii = 0; ii < 32; ii++) {
+                    const int e = 128 * j + 32 * k + ii;
+                    const int val = q6_val(&x[i], e);
+                    const int s = sc[8 * j + 2 * k + (ii >= 16)];
+                    sumi[ii / 4] += s * y[i].qs[e] * val;
+                }
+        for (int l = 0; l < 8; l++) {
+            const int32_t sub = (y[i].bsums[2 * l] * sc[2 * l] + y[i].bsums[2 * l + 1] * sc[2 * l + 1]) << 5;
+            sumi[l] -= sub;
+            acc[l] = fmaf(d, (float)sumi[l], acc[l]);
+        }
+    }
+    return hsum8(acc);
+}
+
+/* ------------------------------------------------------- routed MUL_MAT */
+
+static int omp_threads(int nthreads) {
+#ifdef _OPENMP
+    return nthreads > 0 ? nthreads : omp_get_max_threads();
+#else
+    (void)nthreads;
+    return 1;
+#endif
+}
+
+static int route_of(int type, int64_t rows, int64_t cols) {
+    if ((type == OR_Q4_0 || type == OR_Q4_K) && rows % 8 == 0) return ORACLE_ROUTE_REPACK;
+    if ((type == OR_Q4_K || type == OR_Q6_K) && cols >= 8) return ORACLE_ROUTE_TILED;
+    if (type == OR_Q4_0 && cols >= 2) return -1; /* tinyBLAS: out of scope */
+    return ORACLE_ROUTE_VECDOT;
+}
+
+static size_t act_row_size(int type, int64_t n) {
+    return type == OR_Q4_0 ? (size_t)(n / 32) * sizeof(blk_q8_0) : (size_t)(n / QK_K) * sizeof(blk_q8_K);
+}
+
+/* compute.rs:1504-1549 (wdata pass) and compute.rs:5350-5398 (repack wdata) */
+int oracle_mul_mat_act(int type, int64_t n, int64_t rows, const float *x, int64_t cols, void *act) {
+    const int route = route_of(type, rows, cols);
+    if (route < 0) return -1;
+    const size_t rs = act_row_size(type, n);
+    const int64_t nr4 = cols - cols % 4;
+    for (int64_t c = 0; c < cols; c++) {
+        uint8_t *dst = (uint8_t *)act + (size_t)c * rs;
+        if (type == OR_Q4_0)
+            oracle_quantize_row_q8_0(x + c * n, dst, n);
+        else if (type == OR_Q4_K && route == ORACLE_ROUTE_REPACK && c < nr4)
+            oracle_quantize_row_q8_K_mat(x + c * n, dst, n);
+        else
+            oracle_quantize_row_q8_K_ref(x + c * n, dst, n);
+    }
+    return route;
+}
+
+int oracle_mul_mat(int type, const void *w, int64_t n, int64_t rows, const float *x, int64_t cols,
+                   float *out, int32_t *subsums, int *route_out, int nthreads) {
+    const int route = route_of(type, rows, cols);
+    if (route_out) *route_out = route;
+    if (route < 0) return -1;
+    if (type != OR_Q4_0 && type != OR_Q4_K && type != OR_Q6_K) return -2;
+    const size_t rs = act_row_size(type, n);
+    uint8_t *act = (uint8_t *)malloc(rs * (size_t)cols);
+    if (!act) return -3;
+    oracle_mul_mat_act(type, n, rows, x, cols, act);
+    const int64_t nr4 = cols - cols % 4;
+    const int nth = omp_threads(nthreads);
+
+    if (type == OR_Q4_0) {
+        const int64_t nb = n / 32;
+#pragma omp parallel for num_threads(nth) schedule(static)
+        for (int64_t r = 0; r < rows; r++) {
+            const blk_q4_0 *wr = (const blk_q4_0 *)((const uint8_t *)w + (size_t)r * nb * 18);
+            for (int64_t c = 0; c < cols; c++) {
+                const blk_q8_0 *a = (const blk_q8_0 *)(act + (size_t)c * rs);
+                float v;
+                if (route == ORACLE_ROUTE_REPACK) {
+                    /* repack.rs:3351-3378 / :3380-3420: one fma per block */
+                    float acc = 0.0f;
+                    for (int64_t b = 0; b < nb; b++) {
+                        const int32_t is = isum_q4_0(&wr[b], &a[b]);
+                        if (subsums) subsums[((size_t)c * rows + r) * nb + b] = is;
+                        acc = fmaf((float)is, H2F(wr[b].d) * H2F(a[b].d), acc);
+                    }
+                    v = acc;
+                } else {
+                    if (subsums)
+                        for (int64_t b = 0; b < nb; b++)
+                            subsums[((size_t)c * rows + r) * nb + b] = isum_q4_0(&wr[b], &a[b]);
+                    v = oracle_vec_dot_q4_0_q8_0((int)n, wr, a);
+                }
+                out[c * rows + r] = v;
+            }
+        }
+    } else if (type == OR_Q4_K) {
+        const int64_t nb = n / QK_K;
+#pragma omp parallel for num_threads(nth) schedule(static)
+        for (int64_t r = 0; r < rows; r++) {
+            const blk_q4_K *wr = (const blk_q4_K *)((const uint8_t *)w + (size_t)r * nb * 144);
+            for (int64_t c = 0; c < cols; c++) {
+                const blk_q8_K *a = (const blk_q8_K *)(act + (size_t)c * rs);
+                float v = 0.0f;
+                float acc = 0.0f, accmin = 0.0f;
+                for (int64_t b = 0; b < nb; b++) {
+                    uint8_t s[8], m[8];
+                    q4k_scales(&wr[b], s, m);
+                    int32_t ia = 0, im = 0;
+                    const float d_col = H2F(wr[b].d), dmin_col = H2F(wr[b].dmin), d_row = a[b].d;
+                    for (int g = 0; g < 4; g++) {
+                        int32_t iag, img;
+                        isum_q4_K_pair(&wr[b], &a[b], g, s, m, &iag, &img);
+                        ia += iag;
+                        im += img;
+                        if (route == ORACLE_ROUTE_REPACK && c < nr4) {
+                            /* gemm: one fma per (super-block, pair), repack.rs:1742-1754 */
+                            acc = fmaf((float)iag, d_col * d_row, acc);
+                            accmin = fmaf((float)img, dmin_col * d_row, accmin);
+                        }
+                    }
+                    if (subsums) {
+                        subsums[(((size_t)c * rows + r) * nb + b) * 2 + 0] = ia;
+                        subsums[(((size_t)c * rows + r) * nb + b) * 2 + 1] = im;
+                    }
+                    if (route == ORACLE_ROUTE_REPACK && c >= nr4) {
+                        /* gemv: one fma per super-block, repack.rs:1681-1684 */
+                        acc = fmaf((float)ia, d_col * d_row, acc);
+                        accmin = fmaf((float)im, dmin_col * d_row, accmin);
+                    } else if (route == ORACLE_ROUTE_TILED) {
+                        /* tiled.rs:826-838: result = d0*f1; fnmadd(dmin, f2); fma(result, d1, buf) */
+                        float res = d_col * (float)ia;
+                        res = fmaf(-dmin_col, (float)im, res);
+                        acc = fmaf(res, d_row, acc);
+                    }
+                }
+                if (route == ORACLE_ROUTE_REPACK) v = acc - accmin;
+                else if (route == ORACLE_ROUTE_TILED) v = acc;
+                else v = oracle_vec_dot_q4_K_q8_K((int)n, wr, a);
+                out[c * rows + r] = v;
+            }
+        }
+    } else { /* Q6_K */
+        const int64_t nb = n / QK_K;
+#pragma omp parallel for num_threads(nth) schedule(static)
+        for (int64_t r = 0; r < rows; r++) {
+            const blk_q6_K *wr = (const blk_q6_K *)((const uint8_t *)w + (size_t)r * nb * 210);
+            for (int64_t c = 0; c < cols; c++) {
+                const blk_q8_K *a = (const blk_q8_K *)(act + (size_t)c * rs);
+                float v;
+                if (route == ORACLE_ROUTE_TILED) {
+                    float acc = 0.0f;
+                    for (int64_t b = 0; b < nb; b++) {
+                        const int32_t is = isum_q6_K(&wr[b], &a[b]);
+                        if (subsums) subsums[((size_t)c * rows + r) * nb + b] = is;
+                        const float res = H2F(wr[b].d) * (float)is;
+                        acc = fmaf(res, a[b].d, acc);
+                    }
+                    v = acc;
+                } else {
+                    if (subsums)
+                        for (int64_t b = 0; b < nb; b++)
+                            subsums[((size_t)c * rows + r) * nb + b] = isum_q6_K(&wr[b], &a[b]);
+                    v = oracle_vec_dot_q6_K_q8_K((int)n, wr, a);
+                }
+                out[c * rows + r] = v;
+            }
+        }
+    }
+    free(act);
+    return route;
+}
+
+/* ---------------------------------------------------- MUL_MAT_ID (MXFP4) */
+
+int oracle_mul_mat_id_mxfp4(const void *as, int64_t n, int64_t rows, int64_t n_as,
+                            const float *b, int64_t ne11, int64_t n_tokens,
+                            const int32_t *ids, int64_t n_ids, float *dst, int nthreads) {
+    const int64_t nb = n / 32;
+    const size_t rs = (size_t)nb * sizeof(blk_q8_0);
+    const size_t wrow = (size_t)nb * sizeof(blk_mxfp4);
+    uint8_t *act = (uint8_t *)malloc(rs * (size_t)(ne11 * n_tokens));
+    if (!act) return -3;
+    for (int64_t i = 0; i < ne11 * n_tokens; i++) oracle_quantize_row_q8_0(b + i * n, act + i * rs, n);
+    for (int64_t i = 0; i < n_ids * n_tokens; i++)
+        if (ids[i] < 0 || ids[i] >= n_as) { free(act); return -4; }
+    const int repack = rows % 8 == 0;
+    const int nth = omp_threads(nthreads);
+#pragma omp parallel for num_threads(nth) schedule(static)
+    for (int64_t ir = 0; ir < n_ids * n_tokens; ir++) {
+        const int64_t i1 = ir % n_ids, i2 = ir / n_ids;
+        const int64_t id = ids[i2 * n_ids + i1];
+        const int64_t i11 = i1 % ne11;
+        const blk_q8_0 *y = (const blk_q8_0 *)(act + (size_t)(i11 + i2 * ne11) * rs);
+        for (int64_t r = 0; r < rows; r++) {
+            const blk_mxfp4 *x = (const blk_mxfp4 *)((const uint8_t *)as + ((size_t)id * rows + r) * wrow);
+            float acc = 0.0f;
+            for (int64_t ib = 0; ib < nb; ib++) {
+                const int32_t dot = isum_mxfp4(&x[ib], &y[ib]);
+                if (repack) {
+                    /* repack.rs:1071-1073 */
+                    const float scale = oracle_e8m0_to_fp32_half(x[ib].e) * H2F(y[ib].d);
+                    acc = fmaf((float)dot, scale, acc);
+                } else {
+                    /* compute.rs:7140-7150 (non-fused) */
+                    const float d = H2F(y[ib].d) * oracle_e8m0_to_fp32_half(x[ib].e);
+                    acc += d * (float)dot;
+                }
+            }
+            dst[(i2 * n_ids + i1) * rows + r] = acc;
+        }
+    }
+    free(act);
+    return 0;
+}
+
+/* FLASH_ATTN_EXT lives in ggml_oracle_fa.c */

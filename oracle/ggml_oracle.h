@@ -1,0 +1,120 @@
+/*
+ * ggml_oracle.h -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of llama.rust's CPU arithmetic for the quantized
+ * MUL_MAT / MUL_MAT_ID / FLASH_ATTN_EXT path (the crates/ggml/src Rust files of
+ * fly88oj/llama.rust).  It is the checker the HIP kernels are compared with and
+ * the timed CPU baseline of bench.py.  Nothing in the product library links,
+ * loads or calls it; only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg do.
+ *
+ * Every function cites the reference file:line it restates.  Parity status of
+ * each function (what pins it) is listed beside its declaration.
+ */
+#ifndef GGML_ORACLE_H
+#define GGML_ORACLE_H
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids (crates/ggml/src/types.rs:15) */
+enum {
+    OR_F32 = 0, OR_F16 = 1, OR_Q4_0 = 2, OR_Q8_0 = 8, OR_Q4_K = 12,
+    OR_Q6_K = 14, OR_Q8_K = 15, OR_MXFP4 = 39
+};
+
+/* ---- scalar helpers ---- */
+uint16_t oracle_fp32_to_fp16(float f);            /* half 2.7.1 from_f32 (RNE); pinned by every fp16 d in quants_ref.bin */
+float    oracle_fp16_to_fp32(uint16_t h);
+int32_t  oracle_nearest_int(float f);             /* quants.rs:13 */
+float    oracle_e8m0_to_fp32_half(uint8_t e);     /* quants.rs:682; pinned by closed form 2^(e-128) */
+
+/* ---- weight quantizers (one-time prep) ---- */
+void oracle_quantize_row_q4_0_ref(const float *x, void *y, int64_t k);  /* quants.rs:124; quants_ref.bin */
+void oracle_quantize_row_q4_K_ref(const float *x, void *y, int64_t k);  /* quants_k.rs:1861; quants_ref.bin */
+void oracle_quantize_row_q6_K_ref(const float *x, void *y, int64_t k);  /* quants_k.rs:2058; quants_ref.bin */
+void oracle_quantize_row_mxfp4_ref(const float *x, void *y, int64_t k); /* absent in the reference; quants_ref_fp4.bin */
+void oracle_quantize_row_q8_0_ref(const float *x, void *y, int64_t k);  /* quants.rs:302; quants_ref.bin */
+
+/* ---- activation quantizers ---- */
+void oracle_quantize_row_q8_0(const float *x, void *y, int64_t k);      /* quants.rs:331; q4_0_repack_ref.bin */
+void oracle_quantize_row_q8_K_ref(const float *x, void *y, int64_t k);  /* quants.rs:615; quants_ref.bin, q4k_repack_ref.bin */
+/* quantize_mat_q8_K_4x8 values (repack.rs:1561), written as plain block_q8_K rows */
+void oracle_quantize_row_q8_K_mat(const float *x, void *y, int64_t k);  /* q4k_repack_ref.bin (values) */
+
+/* ---- dequantizers ---- */
+void oracle_dequantize_row(int type, const void *x, float *y, int64_t k);
+
+/* ---- dot kernels in the reference's own fp32 order ---- */
+float oracle_vec_dot_q4_0_q8_0(int n, const void *x, const void *y);  /* vec_dot.rs:599 */
+float oracle_vec_dot_q4_K_q8_K(int n, const void *x, const void *y);  /* vec_dot.rs:872 */
+float oracle_vec_dot_q6_K_q8_K(int n, const void *x, const void *y);  /* vec_dot.rs:990 */
+
+/*
+ * The reference's MUL_MAT routing for a 2-D quantized weight W [rows x n]
+ * (row-major GGUF blocks) and f32 activations X [cols x n]
+ * (compute.rs:1420-1839):
+ *   Q4_0, rows%8==0 -> 8x8 repack gemv/gemm, Q8_0 activations  (compute.rs:5192)
+ *   Q4_K, rows%8==0 -> 8x8 repack: 4-row groups quantized by quantize_mat_q8_K_4x8
+ *                      and run through the gemm, the cols%4 tail by
+ *                      quantize_row_q8_K_ref through the gemv   (compute.rs:5322)
+ *   K-quant, not repacked, cols>=8 -> tiled                     (tiled.rs:1656)
+ *   otherwise row vec_dot with quantize_row_q8_K_ref / quantize_row_q8_0
+ * Q4_0 with rows%8!=0 and cols>=2 would take tinyBLAS, which is out of scope:
+ * returns -1 there.
+ * out is [cols x rows] f32.  subsums (optional) receives the exact integer
+ * partials per (col, row, block) -- see ghip.h ghip_mul_mat_subsums for the
+ * layout.  route (optional) receives the route id (see ORACLE_ROUTE_*).
+ * nthreads<=0 uses every OpenMP thread.
+ */
+enum { ORACLE_ROUTE_REPACK = 1, ORACLE_ROUTE_TILED = 2, ORACLE_ROUTE_VECDOT = 3 };
+int oracle_mul_mat(int type, const void *w, int64_t n, int64_t rows,
+                   const float *x, int64_t cols, float *out,
+                   int32_t *subsums, int *route, int nthreads);
+
+/* the activation bytes the route above feeds the kernels with (plain rows of
+ * block_q8_0 / block_q8_K) */
+int oracle_mul_mat_act(int type, int64_t n, int64_t rows, const float *x,
+                       int64_t cols, void *act);
+
+/*
+ * MUL_MAT_ID with MXFP4 experts (compute.rs:1917-2202): as [n_as][rows][n],
+ * b [n_tokens][ne11][n] f32, ids [n_tokens][n_ids] i32, dst
+ * [n_tokens][n_ids][rows].  Activations quantize_row_q8_0; per 8-row group the
+ * repack gemv_mxfp4_8x8_q8_0 (repack.rs:1086) when rows%8==0, else
+ * vec_dot_mxfp4_q8_0 (compute.rs:7123).
+ */
+int oracle_mul_mat_id_mxfp4(const void *as, int64_t n, int64_t rows, int64_t n_as,
+                            const float *b, int64_t ne11, int64_t n_tokens,
+                            const int32_t *ids, int64_t n_ids, float *dst,
+                            int nthreads);
+
+/*
+ * FLASH_ATTN_EXT (compute.rs:4563, flash_attn.rs), f16 K/V, f16 mask, no
+ * ALiBi/softcap/sinks:
+ *   q    [n_q][H][D] f32 (ggml ne = [D, n_q, H], nb: see below)
+ *   k, v [H_kv][S][D] f16
+ *   mask [n_q][S] f16 (may be NULL)
+ *   dst  [n_q][H][D] f32
+ * The caller passes tensors in ggml's physical layout:
+ *   q:   element (d, t, h) at q[h*q_nb2 + t*q_nb1 + d]  (float strides)
+ *   k/v: element (d, s, h) at k[h*kv_nb2 + s*kv_nb1 + d] (half strides)
+ *   dst: element (d, h, t) at dst[t*H*D + h*D + d]
+ * n_chunks is the split-KV chunk count (= the reference's thread count).
+ */
+int oracle_flash_attn_ext(const float *q, int64_t q_nb1, int64_t q_nb2,
+                          const uint16_t *k, const uint16_t *v, int64_t kv_nb1, int64_t kv_nb2,
+                          const uint16_t *mask, int64_t mask_nb1,
+                          float *dst, int D, int n_q, int H, int S, int H_kv,
+                          float scale, float max_bias, float softcap,
+                          int n_chunks, int nthreads);
+
+double oracle_wtime(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,142 @@
+"""Parsers for the reference's golden fixtures (copied under tests/golden/ref/).
+
+Each parser follows the reader in the reference test that consumes the file:
+  quants_ref.bin / quants_ref_fp4.bin  quants.rs:791-860, :940-1010 (SECT / SRAW)
+  mulmat_ref*.bin                      vec_dot.rs:2246-2280 (VMM1)
+  q4k_repack_ref.bin, q4_0_repack_ref  repack.rs:5636-5676, :6046-6086
+  repack_ref.bin (MXFP4)               repack.rs:5010-5055
+  tiled_ref.bin                        tiled.rs:2020-2090 (VMT1)
+"""
+import os
+import struct
+
+import numpy as np
+
+REF_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ref")
+
+
+def path(name):
+    return os.path.join(REF_DIR, name)
+
+
+def read(name):
+    with open(path(name), "rb") as f:
+        return f.read()
+
+
+def ref_input(n):
+    """The LCG of parity/ref_quants_dump.c (quants.rs:779-788)."""
+    out = np.empty(n, dtype=np.float32)
+    state = 0x12345678
+    for i in range(n):
+        state = (state * 1664525 + 1013904223) & 0xFFFFFFFF
+        s = state - (1 << 32) if state >= (1 << 31) else state
+        out[i] = np.float32(np.float32(np.float32(s) / np.float32(1 << 30)) * np.float32(0.75)) - np.float32(0.125)
+    return out
+
+
+def quant_sections(name):
+    """[(magic, type_id, n, qbytes, deq f32)] until the 0xFFFF end marker."""
+    b = read(name)
+    o = 0
+    out = []
+    while True:
+        (magic,) = struct.unpack_from("<I", b, o)
+        o += 4
+        if magic == 0xFFFF:
+            break
+        tid, n, qlen = struct.unpack_from("<IQQ", b, o)
+        o += 20
+        q = np.frombuffer(b, dtype=np.uint8, count=qlen, offset=o).copy()
+        o += qlen
+        deq = np.frombuffer(b[o:o + 4 * n], dtype=np.float32).copy()
+        o += 4 * n
+        out.append((magic, tid, n, q, deq))
+    return out
+
+
+def mulmat_sections(name):
+    """VMM1 sections: [(type_id, n, rows, cols, xq, y[cols, n], dst[cols, rows])]."""
+    from oracle_lib import row_size, BLOCK
+    b = read(name)
+    o = 0
+    out = []
+    while True:
+        (magic,) = struct.unpack_from("<I", b, o)
+        o += 4
+        if magic == 0xFFFFFFFF:
+            break
+        assert magic == 0x314D4D56
+        tid, n, rows, cols = struct.unpack_from("<4I", b, o)
+        o += 16
+        if tid in BLOCK:
+            xl = row_size(tid, n) * rows
+        elif tid in (0,):
+            xl = 4 * n * rows
+        elif tid in (1, 30):
+            xl = 2 * n * rows
+        else:
+            xl = {3: 20, 6: 22, 7: 24, 10: 84, 11: 110, 13: 176}[tid] * (n // (256 if tid >= 10 else 32)) * rows
+        xq = np.frombuffer(b, dtype=np.uint8, count=xl, offset=o).copy()
+        o += xl
+        y = np.frombuffer(b, dtype=np.float32, count=n * cols, offset=o).reshape(cols, n).copy()
+        o += 4 * n * cols
+        dst = np.frombuffer(b, dtype=np.float32, count=rows * cols, offset=o).reshape(cols, rows).copy()
+        o += 4 * rows * cols
+        out.append((tid, n, rows, cols, xq, y, dst))
+    return out
+
+
+def tiled_sections(name="tiled_ref_q4k_q6k.bin"):
+    """VMT1 MUL_MAT sections: [(type_id, n, rows, cols, xq, y, dst)]."""
+    from oracle_lib import row_size
+    b = read(name)
+    o = 0
+    out = []
+    while True:
+        (magic,) = struct.unpack_from("<I", b, o)
+        o += 4
+        if magic == 0xFFFFFFFF:
+            break
+        assert magic == 0x31544D56
+        kind, tid, n, rows, cols = struct.unpack_from("<5I", b, o)
+        o += 20
+        assert kind == 0
+        xl = row_size(tid, n) * rows
+        xq = np.frombuffer(b, dtype=np.uint8, count=xl, offset=o).copy()
+        o += xl
+        y = np.frombuffer(b, dtype=np.float32, count=n * cols, offset=o).reshape(cols, n).copy()
+        o += 4 * n * cols
+        dst = np.frombuffer(b, dtype=np.float32, count=rows * cols, offset=o).reshape(cols, rows).copy()
+        o += 4 * rows * cols
+        out.append((tid, n, rows, cols, xq, y, dst))
+    return out
+
+
+def _len_sections(name):
+    b = read(name)
+    o = 0
+    secs = []
+    while o < len(b):
+        (ln,) = struct.unpack_from("<I", b, o)
+        o += 4
+        secs.append(b[o:o + ln])
+        o += ln
+    return secs
+
+
+def repack_dump(name):
+    """q4k_repack_ref.bin / q4_0_repack_ref.bin (tagged header) or repack_ref.bin (MXFP4)."""
+    s = _len_sections(name)
+    hdr = struct.unpack("<%dI" % (len(s[0]) // 4), s[0])
+    if name == "repack_ref.bin":
+        n, nrows, nr_gemv, nr_gemm, nc = hdr[0:5]
+    else:
+        n, nrows, nr_gemv, nr_gemm, nc = hdr[1:6]
+    u8 = lambda v: np.frombuffer(v, dtype=np.uint8).copy()
+    f32 = lambda v: np.frombuffer(v, dtype=np.float32).copy()
+    d = dict(n=n, nrows=nrows, nr_gemv=nr_gemv, nr_gemm=nr_gemm, nc=nc,
+             src=u8(s[1]), repacked=u8(s[2]), q8=u8(s[3]), q8x4=u8(s[4]),
+             gemv=f32(s[5]), gemm=f32(s[6]), gemv_gen=f32(s[7]), gemm_gen=f32(s[8]),
+             act_g=f32(s[9]), act_m=f32(s[10]))
+    return d

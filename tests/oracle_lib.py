@@ -1,0 +1,146 @@
+"""ctypes binding of the test-only CPU oracle (oracle/liboracle.so).
+
+Test infrastructure: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg only.
+"""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_DIR = os.path.join(ROOT, "oracle")
+LIB_PATH = os.path.join(ORACLE_DIR, "liboracle.so")
+
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, MXFP4 = 0, 1, 2, 8, 12, 14, 15, 39
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210),
+         Q8_K: (256, 292), MXFP4: (32, 17)}
+ROUTE_REPACK, ROUTE_TILED, ROUTE_VECDOT = 1, 2, 3
+
+
+def row_size(ty, n):
+    qk, sz = BLOCK[ty]
+    assert n % qk == 0
+    return n // qk * sz
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", ORACLE_DIR], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        vp, i64, fp = C.c_void_p, C.c_int64, C.POINTER(C.c_float)
+        L.oracle_fp32_to_fp16.restype = C.c_uint16
+        L.oracle_fp32_to_fp16.argtypes = [C.c_float]
+        L.oracle_fp16_to_fp32.restype = C.c_float
+        L.oracle_fp16_to_fp32.argtypes = [C.c_uint16]
+        L.oracle_nearest_int.restype = C.c_int32
+        L.oracle_nearest_int.argtypes = [C.c_float]
+        L.oracle_e8m0_to_fp32_half.restype = C.c_float
+        L.oracle_e8m0_to_fp32_half.argtypes = [C.c_uint8]
+        for f in ["quantize_row_q4_0_ref", "quantize_row_q4_K_ref", "quantize_row_q6_K_ref",
+                  "quantize_row_mxfp4_ref", "quantize_row_q8_0_ref", "quantize_row_q8_0",
+                  "quantize_row_q8_K_ref", "quantize_row_q8_K_mat"]:
+            fn = getattr(L, "oracle_" + f)
+            fn.restype = None
+            fn.argtypes = [vp, vp, i64]
+        L.oracle_dequantize_row.restype = None
+        L.oracle_dequantize_row.argtypes = [C.c_int, vp, vp, i64]
+        for f in ["vec_dot_q4_0_q8_0", "vec_dot_q4_K_q8_K", "vec_dot_q6_K_q8_K"]:
+            fn = getattr(L, "oracle_" + f)
+            fn.restype = C.c_float
+            fn.argtypes = [C.c_int, vp, vp]
+        L.oracle_mul_mat.restype = C.c_int
+        L.oracle_mul_mat.argtypes = [C.c_int, vp, i64, i64, vp, i64, vp, vp, vp, C.c_int]
+        L.oracle_mul_mat_act.restype = C.c_int
+        L.oracle_mul_mat_act.argtypes = [C.c_int, i64, i64, vp, i64, vp]
+        L.oracle_mul_mat_id_mxfp4.restype = C.c_int
+        L.oracle_mul_mat_id_mxfp4.argtypes = [vp, i64, i64, i64, vp, i64, i64, vp, i64, vp, C.c_int]
+        L.oracle_flash_attn_ext.restype = C.c_int
+        L.oracle_flash_attn_ext.argtypes = [vp, i64, i64, vp, vp, i64, i64, vp, i64, vp,
+                                            C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                            C.c_float, C.c_float, C.c_float, C.c_int, C.c_int]
+        L.oracle_wtime.restype = C.c_double
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p) if a is not None else None
+
+
+_QUANT = {Q4_0: "quantize_row_q4_0_ref", Q4_K: "quantize_row_q4_K_ref",
+          Q6_K: "quantize_row_q6_K_ref", MXFP4: "quantize_row_mxfp4_ref"}
+
+
+def quantize(ty, x, kind=None):
+    """Quantize rows of x (f32, last dim = row length) with the reference quantizer."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.shape[-1]
+    rows = x.size // n
+    name = kind or _QUANT[ty]
+    out_ty = {"quantize_row_q8_0_ref": Q8_0, "quantize_row_q8_0": Q8_0,
+              "quantize_row_q8_K_ref": Q8_K, "quantize_row_q8_K_mat": Q8_K}.get(name, ty)
+    out = np.zeros(rows * row_size(out_ty, n), dtype=np.uint8)
+    getattr(lib(), "oracle_" + name)(_p(x), _p(out), x.size)
+    return out
+
+
+def dequantize(ty, q, k):
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    out = np.zeros(k, dtype=np.float32)
+    lib().oracle_dequantize_row(ty, _p(q), _p(out), k)
+    return out
+
+
+def mul_mat(ty, w, n, rows, x, cols, want_subsums=False, nthreads=0):
+    """Routed MUL_MAT: returns (out [cols, rows] f32, route, subsums or None)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert x.size == n * cols
+    out = np.zeros((cols, rows), dtype=np.float32)
+    sub = None
+    if want_subsums:
+        per = {Q4_0: n // 32, Q4_K: (n // 256) * 2, Q6_K: n // 256}[ty]
+        sub = np.zeros((cols, rows, per), dtype=np.int32)
+    route = C.c_int(0)
+    rc = lib().oracle_mul_mat(ty, _p(np.ascontiguousarray(w)), n, rows, _p(x), cols, _p(out),
+                              _p(sub), C.byref(route), nthreads)
+    if rc < 0:
+        raise ValueError(f"oracle_mul_mat rc={rc}")
+    if sub is not None and ty == Q4_K:
+        sub = sub.reshape(cols, rows, n // 256, 2)
+    return out, route.value, sub
+
+
+def mul_mat_act(ty, n, rows, x, cols):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    act_ty = Q8_0 if ty == Q4_0 else Q8_K
+    act = np.zeros(cols * row_size(act_ty, n), dtype=np.uint8)
+    rc = lib().oracle_mul_mat_act(ty, n, rows, _p(x), cols, _p(act))
+    if rc < 0:
+        raise ValueError(f"oracle_mul_mat_act rc={rc}")
+    return act
+
+
+def mul_mat_id_mxfp4(as_q, n, rows, n_as, b, ne11, n_tokens, ids, n_ids, nthreads=0):
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    dst = np.zeros((n_tokens, n_ids, rows), dtype=np.float32)
+    rc = lib().oracle_mul_mat_id_mxfp4(_p(np.ascontiguousarray(as_q)), n, rows, n_as, _p(b), ne11,
+                                       n_tokens, _p(ids), n_ids, _p(dst), nthreads)
+    if rc < 0:
+        raise ValueError(f"oracle_mul_mat_id_mxfp4 rc={rc}")
+    return dst
+
+
+def wtime():
+    return lib().oracle_wtime()

@@ -1,0 +1,129 @@
+/*
+ * ghip.h -- C ABI of the MI355X (gfx950) backend for llama.rust's quantized
+ * ggml hot path: GGML_OP_MUL_MAT (Q4_0 / Q4_K / Q6_K weights),
+ * GGML_OP_MUL_MAT_ID (MXFP4 experts) and GGML_OP_FLASH_ATTN_EXT (f16 K/V).
+ *
+ * The entry points are what a Rust `ggml-hip` FFI crate binds (one extern "C"
+ * fn per declaration, no other glue); each comment names the reference
+ * interface it replaces (paths relative to fly88oj/llama.rust).
+ *
+ * Conventions
+ *  - Tensors are described with ggml's own geometry: ne[] in elements,
+ *    innermost first; nb[] in bytes; data is a DEVICE pointer.  Block layouts
+ *    are the GGUF ones, untouched (crates/ggml/src/blocks.rs:33-168).
+ *  - stream is a hipStream_t (NULL = the legacy default stream).  Every
+ *    compute call is asynchronous on that stream.
+ *  - Errors are returned as ghip_status (the values of enum ggml_status,
+ *    crates/ggml/src/backend.rs:54-62); ghip_last_error() explains the last
+ *    failure of a context.  Nothing falls back to the CPU: an unsupported
+ *    shape or type returns GHIP_STATUS_BACKEND_ERROR.
+ *  - A context may be used from any host thread, one thread at a time.
+ */
+#ifndef GHIP_H
+#define GHIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* enum ggml_status (crates/ggml/src/backend.rs:54-62) */
+typedef enum ghip_status {
+    GHIP_STATUS_SUCCESS = 0,
+    GHIP_STATUS_ALLOC_FAILED = 1,
+    GHIP_STATUS_OUT_OF_MEMORY = 2,
+    GHIP_STATUS_BACKEND_ERROR = 3,
+    GHIP_STATUS_ABORTED = 4,
+} ghip_status;
+
+/* enum ggml_type ids (crates/ggml/src/types.rs:15) for the types this
+ * backend reads or writes */
+enum {
+    GHIP_TYPE_F32 = 0,
+    GHIP_TYPE_F16 = 1,
+    GHIP_TYPE_Q4_0 = 2,
+    GHIP_TYPE_Q8_0 = 8,
+    GHIP_TYPE_Q4_K = 12,
+    GHIP_TYPE_Q6_K = 14,
+    GHIP_TYPE_Q8_K = 15,
+    GHIP_TYPE_I32 = 26,
+    GHIP_TYPE_MXFP4 = 39,
+};
+
+/* The ops of the hot path (GgmlOp::MulMat / MulMatId / FlashAttnExt,
+ * crates/ggml/src/ops.rs:1329, :1421, :2430). */
+enum {
+    GHIP_OP_MUL_MAT = 1,
+    GHIP_OP_MUL_MAT_ID = 2,
+    GHIP_OP_FLASH_ATTN_EXT = 3,
+};
+
+/* The subset of struct ggml_tensor the kernels read
+ * (GgmlCTensor, crates/ggml/src/sysffi.rs:212-228; TensorMeta tensor.rs:295-309). */
+typedef struct ghip_tensor {
+    int32_t type;
+    int64_t ne[4];
+    uint64_t nb[4];
+    void *data;            /* device pointer */
+    int32_t op_params[16]; /* FLASH_ATTN_EXT: [0] scale, [1] max_bias, [2] softcap as f32 bits */
+} ghip_tensor;
+
+typedef struct ghip_context ghip_context;
+
+/* Open the backend on HIP device `device`: loads the gfx950 code objects
+ * (hipModuleLoad) that sit next to this library.
+ * Replaces BackendDeviceI.init_backend (crates/ggml/src/backend.rs:966) /
+ * the dlopen entry ggml_backend_init (backend.rs:1354-1420). */
+ghip_status ghip_init(int device, ghip_context **out);
+
+/* Release the context (BackendI.free, backend.rs:666). */
+void ghip_free(ghip_context *ctx);
+
+/* Human-readable reason of the last non-success status on ctx ("" if none). */
+const char *ghip_last_error(const ghip_context *ctx);
+
+/* Wait for all work queued through ctx on `stream` (BackendI.synchronize,
+ * backend.rs:662). */
+ghip_status ghip_synchronize(ghip_context *ctx, void *stream);
+
+/* Capability check: 1 when the op with these operands runs on this backend,
+ * else 0.  srcs are the op's sources in ggml order (MUL_MAT: src0, src1;
+ * MUL_MAT_ID: as, b, ids; FLASH_ATTN_EXT: q, k, v, mask|NULL, sinks|NULL).
+ * Replaces BackendDeviceI.supports_op (backend.rs:980, CPU semantics
+ * backend.rs:2037-2071). */
+int ghip_supports_op(int op, const ghip_tensor *dst, const ghip_tensor *const *srcs, int n_srcs);
+
+/* dst = src0 x src1 (GGML_OP_MUL_MAT, forward_mul_mat compute.rs:1420-1839).
+ * src0: Q4_0 | Q4_K | Q6_K weight [ne00=K, ne01=N], rows contiguous;
+ * src1: F32 [K, ne11] (any row stride nb11, nb10 == 4);
+ * dst:  F32 [N, ne11] (nb0 == 4).
+ * Activations are quantized on the device exactly as the reference's route for
+ * this (type, N, ne11) does (Q8_0 for Q4_0; Q8_K for the K-quants, with the
+ * quantize_mat_q8_K_4x8 values for the leading ne11 - ne11 % 4 rows of a
+ * repacked Q4_K, compute.rs:5350-5398). */
+ghip_status ghip_mul_mat(ghip_context *ctx, const ghip_tensor *src0, const ghip_tensor *src1,
+                         const ghip_tensor *dst, void *stream);
+
+/* Parity hook with no reference counterpart (the reference exposes these
+ * integers only inside its kernels, e.g. repack.rs:1664-1680): writes the exact
+ * int32 partials ghip_mul_mat forms, per (activation row c, weight row r,
+ * block b), at subsums[(c*N + r)*P + ...]:
+ *   Q4_K: P = 2*nb, {iacc, imin} of super-block b
+ *   Q6_K: P = nb,   sum_s scale_s * sum (q6-32)*q8 of super-block b
+ *   Q4_0: P = nb,   sum (nib-8)*q8 of 32-block b
+ * subsums is a device pointer of ne11*N*P int32. */
+ghip_status ghip_mul_mat_subsums(ghip_context *ctx, const ghip_tensor *src0, const ghip_tensor *src1,
+                                 int32_t *subsums, void *stream);
+
+/* Parity hook with no reference counterpart: the activation blocks
+ * ghip_mul_mat feeds its kernels for (src0, src1) -- ne11 plain rows of
+ * block_q8_0 (Q4_0) or block_q8_K (Q4_K, Q6_K) -- written to the device
+ * pointer out.  Same quantizers as compute.rs:1504-1549 / :5350-5398. */
+ghip_status ghip_mul_mat_act(ghip_context *ctx, const ghip_tensor *src0, const ghip_tensor *src1,
+                             void *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,58 @@
+"""Build the gfx950 code objects and the C-ABI host library in-tree.
+
+    python llama.rust_amd/build.py
+
+Outputs (next to this file, git-ignored, shipped with the tree):
+  ghip_*.hsaco   one code object per kernel source, loaded with hipModuleLoad
+  libghip.so     the C ABI declared in include/ghip.h
+"""
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+
+KERNELS = ["ghip_quant", "ghip_gemv"]
+DEVICE_FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17",
+    # exact fp32 semantics: products and sums round on their own, fused
+    # multiply-adds only where the source calls fmaf()
+    "-ffp-contract=off",
+    # no packed-fp32 instructions (known to misbehave on this pool)
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-parameter",
+]
+
+
+def _run(cmd):
+    print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+
+
+def build_kernels():
+    for k in KERNELS:
+        src = os.path.join(CSRC, k + ".hip")
+        out = os.path.join(HERE, k + ".hsaco")
+        _run([HIPCC, "--genco", *DEVICE_FLAGS, "-I", CSRC, src, "-o", out])
+
+
+def build_host():
+    out = os.path.join(HERE, "libghip.so")
+    _run(["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wno-unused-result", "-D__HIP_PLATFORM_AMD__",
+          "-I", os.path.join(ROCM, "include"), "-I", os.path.join(ROOT, "include"),
+          os.path.join(CSRC, "ghip.cpp"), "-o", out,
+          "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-ldl", "-Wl,-rpath," + os.path.join(ROCM, "lib")])
+
+
+def build():
+    build_kernels()
+    build_host()
+
+
+if __name__ == "__main__":
+    build()
+    sys.exit(0)

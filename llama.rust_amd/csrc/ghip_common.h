@@ -1,0 +1,97 @@
+// ghip_common.h -- device-side helpers shared by the gfx950 kernels.
+//
+// Block layouts are the GGUF ones, unchanged (crates/ggml/src/blocks.rs:33-168):
+//   block_q4_0  18 B  {f16 d; u8 qs[16]}
+//   block_q8_0  34 B  {f16 d; i8 qs[32]}
+//   block_q4_K 144 B  {f16 d, dmin; u8 scales[12]; u8 qs[128]}
+//   block_q6_K 210 B  {u8 ql[128]; u8 qh[64]; i8 scales[16]; f16 d}
+//   block_q8_K 292 B  {f32 d; i8 qs[256]; i16 bsums[16]}
+//   block_mxfp4 17 B  {u8 e; u8 qs[16]}
+// Rows of these blocks are only 2-byte aligned in general; gfx950 runs in
+// unaligned-access mode, so a byte-pointer memcpy into a uint4 compiles to one
+// global_load_dwordx4.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#define DEV static __device__ __forceinline__
+
+constexpr int QK_K = 256;
+constexpr int Q4K_BYTES = 144;
+constexpr int Q6K_BYTES = 210;
+constexpr int Q8K_BYTES = 292;
+constexpr int Q4_0_BYTES = 18;
+constexpr int Q8_0_BYTES = 34;
+constexpr int MXFP4_BYTES = 17;
+
+DEV uint4 ld16(const uint8_t *p) {
+    uint4 v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
+}
+DEV uint2 ld8(const uint8_t *p) {
+    uint2 v;
+    __builtin_memcpy(&v, p, 8);
+    return v;
+}
+DEV uint32_t ld4(const uint8_t *p) {
+    uint32_t v;
+    __builtin_memcpy(&v, p, 4);
+    return v;
+}
+DEV uint16_t ld2(const uint8_t *p) {
+    uint16_t v;
+    __builtin_memcpy(&v, p, 2);
+    return v;
+}
+// non-temporal streaming load for weights that are read exactly once
+DEV uint4 ld16_stream(const uint8_t *p) {
+    uint4 v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
+}
+
+DEV float h2f(uint32_t bits16) {
+    return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu)));
+}
+
+DEV int dot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
+
+DEV float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+DEV int group8_sum(int v) {
+    v += __shfl_xor(v, 1, 64);
+    v += __shfl_xor(v, 2, 64);
+    v += __shfl_xor(v, 4, 64);
+    return v;
+}
+
+// byte i (0..11) of three little-endian dwords
+DEV uint32_t byte_of3(uint32_t a, uint32_t b, uint32_t c, int i) {
+    const uint32_t w = i < 4 ? a : (i < 8 ? b : c);
+    return (w >> (8 * (i & 3))) & 0xffu;
+}
+
+// get_scale_min_k4 (quants_k.rs:1672) on the 12 scale bytes held in s0..s2
+DEV void scale_min_k4(uint32_t s0, uint32_t s1, uint32_t s2, int j, int &sc, int &m) {
+    if (j < 4) {
+        sc = (int)(byte_of3(s0, s1, s2, j) & 63);
+        m = (int)(byte_of3(s0, s1, s2, j + 4) & 63);
+    } else {
+        sc = (int)((byte_of3(s0, s1, s2, j + 4) & 0xF) | ((byte_of3(s0, s1, s2, j - 4) >> 6) << 4));
+        m = (int)((byte_of3(s0, s1, s2, j + 4) >> 4) | ((byte_of3(s0, s1, s2, j) >> 6) << 4));
+    }
+}
+
+// KVALUES_MXFP4 (quants.rs:660)
+__device__ static const int8_t kvalues_mxfp4_dev[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+
+// e8m0_to_fp32_half (quants.rs:682): 2^(x-128) from bits
+DEV float e8m0_half(uint32_t x) {
+    const uint32_t bits = x < 2 ? (0x00200000u << x) : ((x - 1) << 23);
+    return __uint_as_float(bits);
+}

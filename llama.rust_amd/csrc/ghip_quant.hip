@@ -1,0 +1,116 @@
+// ghip_quant.hip -- activation quantizers for the MUL_MAT path, on the GPU.
+//
+// Bit-exact with the reference's CPU quantizers (the integer codes, bsums and
+// scales are what the dot kernels consume, so they must be identical):
+//   quantize_row_q8_K_ref   quants.rs:615-650   iscale = -127/max (signed max-abs),
+//                                               q = min(127, rne(iscale*x)), d = 1/iscale
+//   quantize_mat_q8_K_4x8   repack.rs:1561-1620 iscale = 127/amax, q = clamp(rne(iscale*x)),
+//                                               d = 1/iscale (values; plain block_q8_K layout)
+//   quantize_row_q8_0       quants.rs:331-362   d = f16(amax/127), q = rne(x*127/amax)
+// Compiled with -ffp-contract=off: every product is rounded before rne().
+#include "ghip_common.h"
+
+// One wavefront per 256-element super-block; each lane owns 4 consecutive
+// elements.  Rows r < n_mat use the quantize_mat_q8_K_4x8 values, the others
+// quantize_row_q8_K_ref (the reference's repack route quantizes the leading
+// ne11 - ne11 % 4 activation rows with the former, compute.rs:5350-5398).
+extern "C" __global__ void __launch_bounds__(256)
+ghip_quantize_q8_K(const float *__restrict__ x, int64_t x_stride, int64_t n, int64_t nrows,
+                   uint8_t *__restrict__ y, int64_t y_stride, int64_t n_mat) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nb = n / QK_K;
+    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wid >= nrows * nb) return;
+    const int64_t row = wid / nb, b = wid - row * nb;
+    float xs[4];
+    __builtin_memcpy(xs, x + row * x_stride + b * QK_K + lane * 4, 16);
+
+    // signed max-abs, first occurrence wins (strict '>' scan in element order)
+    float bax = 0.0f, bval = 0.0f;
+    int bidx = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float a = fabsf(xs[i]);
+        if (a > bax) { bax = a; bval = xs[i]; bidx = lane * 4 + i; }
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float oax = __shfl_xor(bax, o, 64);
+        const float oval = __shfl_xor(bval, o, 64);
+        const int oidx = __shfl_xor(bidx, o, 64);
+        if (oax > bax || (oax == bax && oidx < bidx)) { bax = oax; bval = oval; bidx = oidx; }
+    }
+
+    uint8_t *blk = y + row * y_stride + b * Q8K_BYTES;
+    const bool mat = row < n_mat;
+    int q[4];
+    float d;
+    if (bax == 0.0f) {
+        q[0] = q[1] = q[2] = q[3] = 0;
+        d = 0.0f;
+    } else if (!mat) {
+        const float iscale = __fdiv_rn(-127.0f, bval);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int v = (int)rintf(__fmul_rn(iscale, xs[i]));
+            q[i] = v < 127 ? v : 127;
+        }
+        d = __fdiv_rn(1.0f, iscale);
+    } else {
+        const float iscale = __fdiv_rn(127.0f, bax);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float r = rintf(__fmul_rn(iscale, xs[i]));
+            r = fminf(fmaxf(r, -128.0f), 127.0f);
+            q[i] = (int)r;
+        }
+        d = __fdiv_rn(1.0f, iscale);
+    }
+    const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
+                            ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+    __builtin_memcpy(blk + 4 + lane * 4, &packed, 4);
+    int s = q[0] + q[1] + q[2] + q[3];
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    if ((lane & 3) == 0) {
+        const int16_t s16 = (int16_t)s;
+        __builtin_memcpy(blk + 260 + 2 * (lane >> 2), &s16, 2);
+    }
+    if (lane == 0) __builtin_memcpy(blk, &d, 4);
+}
+
+// quantize_row_q8_0 (runtime AVX2 arithmetic, quants.rs:331-362): 8 lanes per
+// 32-element block, 8 blocks per wavefront.
+extern "C" __global__ void __launch_bounds__(256)
+ghip_quantize_q8_0(const float *__restrict__ x, int64_t x_stride, int64_t n, int64_t nrows,
+                   uint8_t *__restrict__ y, int64_t y_stride) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nb = n / 32;
+    const int64_t blk_id = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;
+    const int sub = lane & 7;
+    if (blk_id >= nrows * nb) return;  // whole 8-lane groups exit together
+    const int64_t row = blk_id / nb, b = blk_id - row * nb;
+    float xs[4];
+    __builtin_memcpy(xs, x + row * x_stride + b * 32 + sub * 4, 16);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) amax = fmaxf(amax, fabsf(xs[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    const float d = __fdiv_rn(amax, 127.0f);
+    const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float r = rintf(__fmul_rn(xs[i], id));
+        const int v = (r != r || fabsf(r) >= 2147483648.0f) ? -128 : (int)r;
+        packed |= (uint32_t)(v & 0xff) << (8 * i);
+    }
+    uint8_t *blk = y + row * y_stride + b * Q8_0_BYTES;
+    __builtin_memcpy(blk + 2 + sub * 4, &packed, 4);
+    if (sub == 0) {
+        const unsigned short dh = __half_as_ushort(__float2half_rn(d));
+        __builtin_memcpy(blk, &dh, 2);
+    }
+}

@@ -1,0 +1,157 @@
+"""ctypes binding of libghip.so (include/ghip.h) for torch-allocated device tensors.
+
+torch supplies device memory and streams only; every computation runs in the
+gfx950 kernels behind the C ABI.  There is no CPU fallback: if the library or
+its code objects are missing, GhipError is raised.
+"""
+import ctypes as C
+import os
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libghip.so")
+
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, I32, MXFP4 = 0, 1, 2, 8, 12, 14, 15, 26, 39
+OP_MUL_MAT, OP_MUL_MAT_ID, OP_FLASH_ATTN_EXT = 1, 2, 3
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210), Q8_K: (256, 292),
+         MXFP4: (32, 17), F32: (1, 4), F16: (1, 2), I32: (1, 4)}
+
+
+class GhipError(RuntimeError):
+    pass
+
+
+class Tensor(C.Structure):
+    _fields_ = [("type", C.c_int32), ("ne", C.c_int64 * 4), ("nb", C.c_uint64 * 4),
+                ("data", C.c_void_p), ("op_params", C.c_int32 * 16)]
+
+
+def row_size(ty, n):
+    qk, sz = BLOCK[ty]
+    if n % qk:
+        raise ValueError(f"row length {n} not a multiple of block size {qk}")
+    return n // qk * sz
+
+
+def describe(t, ty, ne0=None):
+    """ggml view of a torch tensor.  For quantized types `t` is uint8 with the
+    packed rows in its last dim and ne0 gives the logical row length."""
+    d = Tensor()
+    d.type = ty
+    if ty in (F32, F16, I32):
+        shape = list(t.shape)[::-1] + [1] * (4 - t.dim())
+        nb = [s * t.element_size() for s in t.stride()][::-1]
+        ne = shape[:4]
+    else:
+        assert t.dtype == torch.uint8
+        rows_shape = list(t.shape[:-1])[::-1]
+        ne = [ne0] + rows_shape + [1] * (3 - len(rows_shape))
+        nb = [BLOCK[ty][1]] + [s for s in t.stride()[:-1]][::-1]
+    while len(nb) < 4:
+        nb.append(nb[-1] * ne[len(nb) - 1])
+    for i in range(4):
+        d.ne[i] = int(ne[i])
+        d.nb[i] = int(nb[i])
+    d.data = t.data_ptr()
+    return d
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise GhipError(f"{LIB_PATH} is not built: run llama.rust_amd/build.py")
+        L = C.CDLL(LIB_PATH)
+        P = C.POINTER(Tensor)
+        L.ghip_init.restype = C.c_int
+        L.ghip_init.argtypes = [C.c_int, C.POINTER(C.c_void_p)]
+        L.ghip_free.restype = None
+        L.ghip_free.argtypes = [C.c_void_p]
+        L.ghip_last_error.restype = C.c_char_p
+        L.ghip_last_error.argtypes = [C.c_void_p]
+        L.ghip_synchronize.restype = C.c_int
+        L.ghip_synchronize.argtypes = [C.c_void_p, C.c_void_p]
+        L.ghip_supports_op.restype = C.c_int
+        L.ghip_supports_op.argtypes = [C.c_int, P, C.POINTER(P), C.c_int]
+        L.ghip_mul_mat.restype = C.c_int
+        L.ghip_mul_mat.argtypes = [C.c_void_p, P, P, P, C.c_void_p]
+        L.ghip_mul_mat_subsums.restype = C.c_int
+        L.ghip_mul_mat_subsums.argtypes = [C.c_void_p, P, P, C.c_void_p, C.c_void_p]
+        L.ghip_mul_mat_act.restype = C.c_int
+        L.ghip_mul_mat_act.argtypes = [C.c_void_p, P, P, C.c_void_p, C.c_void_p]
+        _lib = L
+    return _lib
+
+
+def _stream():
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+class Backend:
+    """One ghip context on one device (BackendI of the reference)."""
+
+    def __init__(self, device=0):
+        self.device = device
+        self._ctx = C.c_void_p()
+        st = lib().ghip_init(device, C.byref(self._ctx))
+        if st != 0:
+            raise GhipError(f"ghip_init({device}) failed with status {st}")
+
+    def close(self):
+        if self._ctx:
+            lib().ghip_free(self._ctx)
+            self._ctx = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, st, what):
+        if st != 0:
+            msg = lib().ghip_last_error(self._ctx).decode()
+            raise GhipError(f"{what}: status {st}: {msg}")
+
+    # ---- MUL_MAT
+    def mul_mat(self, w, wtype, k, x, out=None):
+        """out[M, N] = x[M, K] @ dequant(w[N, row_bytes]).T"""
+        n, m = w.shape[0], x.shape[0]
+        if out is None:
+            out = torch.empty((m, n), dtype=torch.float32, device=x.device)
+        a, b, d = describe(w, wtype, k), describe(x, F32), describe(out, F32)
+        self._check(lib().ghip_mul_mat(self._ctx, C.byref(a), C.byref(b), C.byref(d), _stream()), "ghip_mul_mat")
+        return out
+
+    def mul_mat_subsums(self, w, wtype, k, x):
+        n, m = w.shape[0], x.shape[0]
+        nb = k // BLOCK[wtype][0]
+        per = 2 * nb if wtype == Q4_K else nb
+        sub = torch.empty((m, n, per), dtype=torch.int32, device=x.device)
+        a, b = describe(w, wtype, k), describe(x, F32)
+        self._check(lib().ghip_mul_mat_subsums(self._ctx, C.byref(a), C.byref(b), C.c_void_p(sub.data_ptr()),
+                                               _stream()), "ghip_mul_mat_subsums")
+        if wtype == Q4_K:
+            sub = sub.view(m, n, nb, 2)
+        return sub
+
+    def mul_mat_act(self, w, wtype, k, x):
+        m = x.shape[0]
+        act_ty = Q8_0 if wtype == Q4_0 else Q8_K
+        out = torch.empty((m, row_size(act_ty, k)), dtype=torch.uint8, device=x.device)
+        a, b = describe(w, wtype, k), describe(x, F32)
+        self._check(lib().ghip_mul_mat_act(self._ctx, C.byref(a), C.byref(b), C.c_void_p(out.data_ptr()),
+                                           _stream()), "ghip_mul_mat_act")
+        return out
+
+    def supports_mul_mat(self, w, wtype, k, x, out):
+        a, b, d = describe(w, wtype, k), describe(x, F32), describe(out, F32)
+        srcs = (C.POINTER(Tensor) * 2)(C.pointer(a), C.pointer(b))
+        return bool(lib().ghip_supports_op(OP_MUL_MAT, C.byref(d), srcs, 2))
+
+    def synchronize(self):
+        self._check(lib().ghip_synchronize(self._ctx, _stream()), "ghip_synchronize")

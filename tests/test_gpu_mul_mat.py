@@ -1,0 +1,125 @@
+"""GPU parity of GGML_OP_MUL_MAT (Q4_0 / Q4_K / Q6_K) against the CPU oracle.
+
+Bar: Q8 activation bytes and int32 sub-sums bit-exact;
+fp32 outputs within 1e-5 of the reference path by the reference's own
+rel_err = max |a-b| / max(|b|, 1) (vec_dot.rs:2355).
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def be():
+    import ghip
+    b = ghip.Backend(0)
+    yield b
+    b.close()
+
+
+def rel_err(a, b):
+    return float(np.max(np.abs(a - b) / np.maximum(np.abs(b), 1.0))) if a.size else 0.0
+
+
+def make(ty, n, rows, cols, seed=0, scale=0.02):
+    rng = np.random.default_rng(seed)
+    wf = (rng.standard_normal((rows, n)) * scale).astype(np.float32)
+    w = O.quantize(ty, wf).reshape(rows, O.row_size(ty, n))
+    x = np.random.default_rng(seed + 1).standard_normal((cols, n)).astype(np.float32)
+    return w, x
+
+
+def run_case(be, ty, n, rows, cols, seed=0, x=None, check_sub=True):
+    w, x0 = make(ty, n, rows, cols, seed)
+    if x is None:
+        x = x0
+    want, route, want_sub = O.mul_mat(ty, w, n, rows, x, cols, want_subsums=check_sub)
+    wd = torch.from_numpy(w).cuda()
+    xd = torch.from_numpy(x).cuda()
+    print(f"case type={ty} n={n} rows={rows} cols={cols} route={route}", flush=True)
+    got = be.mul_mat(wd, ty, n, xd).cpu().numpy()
+    act = be.mul_mat_act(wd, ty, n, xd).cpu().numpy().reshape(-1)
+    assert np.array_equal(act, O.mul_mat_act(ty, n, rows, x, cols)), "activation bytes differ"
+    if check_sub:
+        sub = be.mul_mat_subsums(wd, ty, n, xd).cpu().numpy()
+        assert np.array_equal(sub, want_sub), "int32 sub-sums differ"
+    err = rel_err(got, want)
+    assert err <= TOL, f"rel_err {err:.3e}"
+    return err
+
+
+@pytest.mark.parametrize("ty", [O.Q4_0, O.Q4_K, O.Q6_K])
+@pytest.mark.parametrize("cols", [1, 2, 3, 4, 5, 8, 11])
+def test_small_shapes(be, ty, cols):
+    # 4 weight rows is not a multiple of 8: Q4_0 with >= 2 columns is then the
+    # reference's tinyBLAS route, which the oracle leaves out
+    for n, rows in [(512, 64), (1024, 72), (768, 100), (256, 8)]:
+        if ty == O.Q4_0 and rows % 8 and cols >= 2:
+            continue
+        run_case(be, ty, n, rows, cols, seed=cols)
+
+
+@pytest.mark.parametrize("ty", [O.Q4_0, O.Q4_K, O.Q6_K])
+def test_ragged_k(be, ty):
+    # K not a multiple of one wavefront's span; odd number of Q4_0 blocks
+    n = 2880 if ty == O.Q4_0 else 2816
+    if ty == O.Q4_0:
+        run_case(be, ty, 32 * 45, 16, 1)
+    run_case(be, ty, n, 24, 1)
+    run_case(be, ty, n, 24, 4)
+
+
+def test_q8K_edge_rows(be):
+    """Zero rows, ties of |max| with opposite signs, and a value whose scaled
+    product lands exactly on .5 -- the quantizer branches of quants.rs:615-650
+    and repack.rs:1561-1620."""
+    n, rows = 512, 16
+    w, _ = make(O.Q4_K, n, rows, 6)
+    x = np.random.default_rng(5).standard_normal((6, n)).astype(np.float32)
+    x[0] = 0.0
+    x[1, :] = 0.25
+    x[1, 7] = -3.0
+    x[1, 100] = 3.0
+    x[2, 3] = x[2].max() + 1.0
+    x[2, 4] = -x[2, 3]
+    x[5, 256:] = 0.0
+    for cols in (6, 4, 2):
+        run_case(be, O.Q4_K, n, rows, cols, x=x[:cols].copy())
+        run_case(be, O.Q6_K, n, rows, cols, x=x[:cols].copy())
+
+
+def test_empty(be):
+    n, rows = 256, 8
+    w, _ = make(O.Q4_K, n, rows, 1)
+    wd = torch.from_numpy(w).cuda()
+    x = torch.zeros((0, n), dtype=torch.float32, device="cuda")
+    out = be.mul_mat(wd, O.Q4_K, n, x)
+    assert out.shape == (0, rows)
+
+
+@pytest.mark.parametrize("name,ty,n,rows", [
+    ("q/o", O.Q4_K, 4096, 4096),
+    ("k/v", O.Q4_K, 4096, 1024),
+    ("gate/up", O.Q4_K, 4096, 14336),
+    ("down", O.Q6_K, 14336, 4096),
+    ("cfg1", O.Q4_0, 4096, 4096),
+])
+@pytest.mark.parametrize("cols", [1, 2, 4, 8])
+def test_llama3_decode_shapes(be, name, ty, n, rows, cols):
+    if ty == O.Q4_0 and cols > 1:
+        pytest.skip("config 1 is batch 1")
+    run_case(be, ty, n, rows, cols, seed=0, check_sub=(cols <= 2))
+
+
+def test_unsupported_type_raises(be):
+    import ghip
+    w = torch.zeros((8, 34), dtype=torch.uint8, device="cuda")
+    x = torch.zeros((1, 32), dtype=torch.float32, device="cuda")
+    with pytest.raises(ghip.GhipError):
+        be.mul_mat(w, O.Q8_0, 32, x)

@@ -123,6 +123,16 @@ ghip_status ghip_mul_mat_subsums(ghip_context *ctx, const ghip_tensor *src0, con
 ghip_status ghip_mul_mat_act(ghip_context *ctx, const ghip_tensor *src0, const ghip_tensor *src1,
                              void *out, void *stream);
 
+/* Quantize nrows rows of n_per_row f32 values (device pointer src) into
+ * GGUF blocks of `type` (Q4_0, Q4_K, Q6_K, MXFP4) at the device pointer dst,
+ * byte-identical to the reference's no-imatrix quantizers
+ * (ggml_quantize_chunk, crates/tools/quantize/src/rows.rs:63 ->
+ * quantize_row_q4_0_ref quants.rs:124, quantize_row_q4_K_ref
+ * quants_k.rs:1861, quantize_row_q6_K_ref quants_k.rs:2058; MXFP4 follows
+ * upstream ggml's quantize_row_mxfp4_ref, which the reference lacks). */
+ghip_status ghip_quantize_chunk(ghip_context *ctx, int type, const float *src, void *dst, int64_t nrows,
+                                int64_t n_per_row, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

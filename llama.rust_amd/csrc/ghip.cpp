@@ -16,7 +16,7 @@
 
 namespace {
 
-const char *const kModules[] = {"ghip_quant.hsaco", "ghip_gemv.hsaco"};
+const char *const kModules[] = {"ghip_quant.hsaco", "ghip_gemv.hsaco", "ghip_wquant.hsaco"};
 
 struct TypeInfo {
     int blck;
@@ -343,6 +343,28 @@ ghip_status ghip_mul_mat_act(ghip_context *ctx, const ghip_tensor *src0, const g
     if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
     if (!out) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat_act: null output");
     return mul_mat_impl(ctx, src0, src1, nullptr, nullptr, out, stream);
+}
+
+ghip_status ghip_quantize_chunk(ghip_context *ctx, int type, const float *src, void *dst, int64_t nrows,
+                                int64_t n_per_row, void *stream) {
+    if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    const TypeInfo ti = type_info(type);
+    const char *name = type == GHIP_TYPE_Q4_0   ? "ghip_wquant_q4_0"
+                       : type == GHIP_TYPE_Q4_K ? "ghip_wquant_q4_K"
+                       : type == GHIP_TYPE_Q6_K ? "ghip_wquant_q6_K"
+                       : type == GHIP_TYPE_MXFP4 ? "ghip_wquant_mxfp4"
+                                                 : nullptr;
+    if (!name) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "quantize_chunk: type %d not supported", type);
+    if (nrows < 0 || n_per_row <= 0 || n_per_row % ti.blck)
+        return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "quantize_chunk: n_per_row %% block size != 0");
+    if (!src || !dst) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "quantize_chunk: null pointer");
+    const int64_t nblocks = nrows * (n_per_row / ti.blck);
+    if (nblocks == 0) return GHIP_STATUS_SUCCESS;
+    if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    const unsigned tpb = ti.blck == 256 ? 64 : 256;
+    const unsigned grid = (unsigned)((nblocks + tpb - 1) / tpb);
+    return ctx->launch(name, dim3(grid), dim3(tpb), 0, (hipStream_t)stream, src, nblocks, (uint8_t *)dst);
 }
 
 }  // extern "C"

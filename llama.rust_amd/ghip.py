@@ -83,6 +83,9 @@ def lib():
         L.ghip_mul_mat_subsums.argtypes = [C.c_void_p, P, P, C.c_void_p, C.c_void_p]
         L.ghip_mul_mat_act.restype = C.c_int
         L.ghip_mul_mat_act.argtypes = [C.c_void_p, P, P, C.c_void_p, C.c_void_p]
+        L.ghip_quantize_chunk.restype = C.c_int
+        L.ghip_quantize_chunk.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64,
+                                          C.c_void_p]
         _lib = L
     return _lib
 
@@ -152,6 +155,16 @@ class Backend:
         a, b, d = describe(w, wtype, k), describe(x, F32), describe(out, F32)
         srcs = (C.POINTER(Tensor) * 2)(C.pointer(a), C.pointer(b))
         return bool(lib().ghip_supports_op(OP_MUL_MAT, C.byref(d), srcs, 2))
+
+    def quantize(self, x, ty):
+        """GGUF blocks of `ty` for the f32 rows of x [rows, n] (ggml_quantize_chunk)."""
+        x = x.contiguous()
+        n = x.shape[-1]
+        rows = x.numel() // n
+        out = torch.empty((rows, row_size(ty, n)), dtype=torch.uint8, device=x.device)
+        self._check(lib().ghip_quantize_chunk(self._ctx, ty, C.c_void_p(x.data_ptr()), C.c_void_p(out.data_ptr()),
+                                              rows, n, _stream()), "ghip_quantize_chunk")
+        return out
 
     def synchronize(self):
         self._check(lib().ghip_synchronize(self._ctx, _stream()), "ghip_synchronize")

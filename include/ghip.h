@@ -96,7 +96,9 @@ int ghip_supports_op(int op, const ghip_tensor *dst, const ghip_tensor *const *s
 
 /* dst = src0 x src1 (GGML_OP_MUL_MAT, forward_mul_mat compute.rs:1420-1839).
  * src0: Q4_0 | Q4_K | Q6_K weight [ne00=K, ne01=N], rows contiguous;
- * src1: F32 [K, ne11] (any row stride nb11, nb10 == 4);
+ * src1: F32 [K, ne11] (any row stride nb11, nb10 == 4), or already the
+ *       vec_dot type of src0 (Q8_0 for Q4_0, Q8_K otherwise; rows of blocks),
+ *       which skips the quantization (backend.rs:2057-2066 semantics);
  * dst:  F32 [N, ne11] (nb0 == 4).
  * Activations are quantized on the device exactly as the reference's route for
  * this (type, N, ne11) does (Q8_0 for Q4_0; Q8_K for the K-quants, with the

@@ -83,8 +83,8 @@ struct ghip_context {
                 fns[name] = f;
                 return f;
             }
+            (void)hipGetLastError();  // a miss in this module must not stay the thread's last error
         }
-        (void)hipGetLastError();
         return nullptr;
     }
 
@@ -135,6 +135,7 @@ struct MulMatPlan {
     int64_t act_row_bytes;
     int64_t n_mat;    // leading activation rows quantized with quantize_mat_q8_K_4x8 values
     int64_t nb;       // blocks per weight row
+    bool act_pre;     // src1 already holds the vec_dot_type blocks
 };
 
 bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b, const ghip_tensor *d,
@@ -146,16 +147,20 @@ bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b,
         return false;
     }
     const TypeInfo ti = type_info(a->type);
-    if (b->type != GHIP_TYPE_F32) { st = ctx->fail(st, "mul_mat: src1 must be F32 (compute.rs:1468)"); return false; }
+    const int vdt = a->type == GHIP_TYPE_Q4_0 ? GHIP_TYPE_Q8_0 : GHIP_TYPE_Q8_K;  // vec_dot_type
+    if (b->type != GHIP_TYPE_F32 && b->type != vdt) {
+        st = ctx->fail(st, "mul_mat: src1 must be F32 or the vec_dot type of src0 (backend.rs:2057-2066)");
+        return false;
+    }
     if (a->ne[0] != b->ne[0]) { st = ctx->fail(st, "mul_mat: ne00 != ne10"); return false; }
     if (a->ne[0] % ti.blck) { st = ctx->fail(st, "mul_mat: ne00 %% block size != 0"); return false; }
     if ((int64_t)a->nb[0] != ti.bytes) { st = ctx->fail(st, "mul_mat: permuted src0 (nb0 != type size)"); return false; }
-    if (b->nb[0] != 4) { st = ctx->fail(st, "mul_mat: permuted src1"); return false; }
+    if ((int64_t)b->nb[0] != type_info(b->type).bytes) { st = ctx->fail(st, "mul_mat: permuted src1"); return false; }
     if (a->ne[2] != 1 || a->ne[3] != 1 || b->ne[2] != 1 || b->ne[3] != 1) {
         st = ctx->fail(st, "mul_mat: only 2-D operands are supported");
         return false;
     }
-    if (b->nb[1] % 4) { st = ctx->fail(st, "mul_mat: src1 row stride not a multiple of 4"); return false; }
+    if (b->type == GHIP_TYPE_F32 && b->nb[1] % 4) { st = ctx->fail(st, "mul_mat: src1 row stride not a multiple of 4"); return false; }
     if (d) {
         if (d->type != GHIP_TYPE_F32 || d->nb[0] != 4 || d->ne[0] != a->ne[1] || d->ne[1] != b->ne[1] ||
             d->nb[1] % 4) {
@@ -180,6 +185,8 @@ bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b,
         // repacked Q4_K (ne01 % 8 == 0): quantize_mat_q8_K_4x8 for ne11 - ne11 % 4 rows
         p.n_mat = (a->type == GHIP_TYPE_Q4_K && p.N % 8 == 0) ? p.M - p.M % 4 : 0;
     }
+    p.act_pre = b->type != GHIP_TYPE_F32;
+    if (p.act_pre) p.act_row_bytes = (int64_t)b->nb[1];
     if (p.N > INT32_MAX || p.nb > INT32_MAX) { st = ctx->fail(st, "mul_mat: dimension too large"); return false; }
     if (p.M < 0 || p.N < 0) { st = ctx->fail(st, "mul_mat: negative dimension"); return false; }
     st = GHIP_STATUS_SUCCESS;
@@ -248,7 +255,7 @@ ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_ten
     if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
     if (!d && !sub && !act_out) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: no output");
     // workspace: [quantized activations | f32 scratch output when only sub-sums are wanted]
-    const size_t act_bytes = ((size_t)(p.M * p.act_row_bytes) + 255) & ~(size_t)255;
+    const size_t act_bytes = p.act_pre ? 0 : ((size_t)(p.M * p.act_row_bytes) + 255) & ~(size_t)255;
     const size_t need = (act_out ? 0 : act_bytes) + (d || act_out ? 0 : (size_t)(p.M * p.N * 4));
     void *ws = nullptr;
     if (need) {
@@ -256,8 +263,13 @@ ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_ten
         if (st != GHIP_STATUS_SUCCESS) return st;
     }
     void *act = act_out ? act_out : ws;
-    st = quantize_act(ctx, p, b, act, s);
-    if (st != GHIP_STATUS_SUCCESS || act_out) return st;
+    if (p.act_pre) {
+        if (act_out) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat_act: src1 is already quantized");
+        act = b->data;
+    } else {
+        st = quantize_act(ctx, p, b, act, s);
+        if (st != GHIP_STATUS_SUCCESS || act_out) return st;
+    }
     float *dst = d ? (float *)d->data : (float *)((uint8_t *)ws + act_bytes);
     const int64_t ldd = d ? (int64_t)d->nb[1] / 4 : p.N;
     return run_gemv(ctx, p, a->data, (const uint8_t *)act, dst, ldd, sub, s);

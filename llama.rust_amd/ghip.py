@@ -126,7 +126,8 @@ class Backend:
         n, m = w.shape[0], x.shape[0]
         if out is None:
             out = torch.empty((m, n), dtype=torch.float32, device=x.device)
-        a, b, d = describe(w, wtype, k), describe(x, F32), describe(out, F32)
+        xty = F32 if x.dtype == torch.float32 else (Q8_0 if wtype == Q4_0 else Q8_K)
+        a, b, d = describe(w, wtype, k), describe(x, xty, k), describe(out, F32)
         self._check(lib().ghip_mul_mat(self._ctx, C.byref(a), C.byref(b), C.byref(d), _stream()), "ghip_mul_mat")
         return out
 

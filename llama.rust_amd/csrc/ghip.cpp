@@ -16,7 +16,7 @@
 
 namespace {
 
-const char *const kModules[] = {"ghip_quant.hsaco", "ghip_gemv.hsaco", "ghip_wquant.hsaco"};
+const char *const kModules[] = {"ghip_quant.hsaco", "ghip_gemv.hsaco", "ghip_wquant.hsaco", "ghip_gemm.hsaco"};
 
 struct TypeInfo {
     int blck;
@@ -244,6 +244,21 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     return GHIP_STATUS_SUCCESS;
 }
 
+// Prefill path (Q4_K, many activation rows): int8 MFMA GEMM, 128 x 128 tiles.
+constexpr size_t kGemmSmem = 114176;  // sizeof(GemmSmem) in ghip_gemm.hip
+ghip_status run_gemm(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, float *dst,
+                     int64_t ldd, int32_t *sub, hipStream_t s) {
+    const unsigned grid = (unsigned)(((p.M + 127) / 128) * ((p.N + 127) / 128));
+    return ctx->launch("ghip_gemm_q4_K", dim3(grid), dim3(256), kGemmSmem, s, (const uint8_t *)w,
+                       (int64_t)p.w_row_bytes, (int)p.N, (int)p.nb, act, (int64_t)p.act_row_bytes, (int)p.M, dst,
+                       (int64_t)ldd, sub);
+}
+
+bool use_gemm(const MulMatPlan &p) {
+    const int min_m = env_int("GHIP_GEMM_MIN_ROWS", 16);
+    return p.wtype == GHIP_TYPE_Q4_K && p.M >= min_m && p.M <= INT32_MAX;
+}
+
 ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b, const ghip_tensor *d,
                          int32_t *sub, void *act_out, void *stream) {
     std::lock_guard<std::mutex> lock(ctx->mu);
@@ -272,6 +287,7 @@ ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_ten
     }
     float *dst = d ? (float *)d->data : (float *)((uint8_t *)ws + act_bytes);
     const int64_t ldd = d ? (int64_t)d->nb[1] / 4 : p.N;
+    if (use_gemm(p)) return run_gemm(ctx, p, a->data, (const uint8_t *)act, dst, ldd, sub, s);
     return run_gemv(ctx, p, a->data, (const uint8_t *)act, dst, ldd, sub, s);
 }
 

@@ -52,6 +52,16 @@ DEV uint4 ld16_stream(const uint8_t *p) {
     return v;
 }
 
+// Value barrier: keeps the compiler from folding the producing multiply into a
+// later conversion (e.g. v_fma_mix with a +0 addend, which turns -0 into +0).
+DEV float opaque(float x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
+// fp32 -> fp16 bits, round to nearest even, of exactly this fp32 value
+DEV uint16_t f2h_rn(float f) { return __half_as_ushort(__float2half_rn(opaque(f))); }
+
 DEV float h2f(uint32_t bits16) {
     return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu)));
 }

@@ -110,7 +110,7 @@ ghip_quantize_q8_0(const float *__restrict__ x, int64_t x_stride, int64_t n, int
     uint8_t *blk = y + row * y_stride + b * Q8_0_BYTES;
     __builtin_memcpy(blk + 2 + sub * 4, &packed, 4);
     if (sub == 0) {
-        const unsigned short dh = __half_as_ushort(__float2half_rn(d));
+        const unsigned short dh = f2h_rn(d);
         __builtin_memcpy(blk, &dh, 2);
     }
 }

@@ -12,7 +12,23 @@
 #include "ghip_common.h"
 
 DEV int nearest_int(float f) { return (int)rintf(f); }  // quants.rs:13 (RNE, |f| < 2^22)
-DEV uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
+DEV uint16_t f2h(float f) { return f2h_rn(f); }
+// Correctly rounded fp32 sqrt (the CPU's sqrtss): the hardware estimate is
+// within an ulp, so pick among its neighbours the one whose exact square (in
+// double, 48 significant bits) is closest to x.  A tie is impossible: the
+// midpoint of two floats squared needs more than 24 bits.
+DEV float sqrt_crt(float x) {
+    if (!(x > 0.0f) || x == __builtin_inff()) return sqrtf(x);
+    const float r = sqrtf(x);
+    const float c[3] = {__uint_as_float(__float_as_uint(r) - 1), r, __uint_as_float(__float_as_uint(r) + 1)};
+    float best = r;
+    double be = 1e300;
+    for (int i = 0; i < 3; i++) {
+        const double e = fabs((double)c[i] * (double)c[i] - (double)x);
+        if (e < be) { be = e; best = c[i]; }
+    }
+    return best;
+}
 DEV int imin(int a, int b) { return a < b ? a : b; }
 DEV int imax(int a, int b) { return a > b ? a : b; }
 
@@ -125,7 +141,7 @@ ghip_wquant_q4_K(const float *__restrict__ x, int64_t nblocks, uint8_t *__restri
     for (int j = 0; j < 8; j++) {
         float sum_x2 = 0.0f;
         for (int l = 0; l < 32; l++) sum_x2 += xb[32 * j + l] * xb[32 * j + l];
-        const float av_x = __fsqrt_rn(__fdiv_rn(sum_x2, 32.0f));
+        const float av_x = sqrt_crt(__fdiv_rn(sum_x2, 32.0f));
         for (int l = 0; l < 32; l++) weights[l] = av_x + fabsf(xb[32 * j + l]);
         scales[j] = make_qkx2_quants(32, 15, xb + 32 * j, weights, L + 32 * j, &mins[j], Laux, -1.0f, 0.1f, 20);
         if (scales[j] > max_scale) max_scale = scales[j];

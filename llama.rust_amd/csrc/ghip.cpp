@@ -224,21 +224,20 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     else
         waves_k = (int)((p.nb + 7) / 8);
     if (waves_k > 8) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: ne00 = %lld too large for the decode kernel", (long long)p.K);
-    const int rows_per_wg = env_int("GHIP_GEMV_ROWS", 8);
+    const int rows_per_wg = 8;  // RB in ghip_gemv.hip
     const unsigned grid = (unsigned)((p.N + rows_per_wg - 1) / rows_per_wg);
     for (int64_t c0 = 0; c0 < p.M; c0 += 8) {
         const int nc = (int)std::min<int64_t>(8, p.M - c0);
         const int NC = nc == 1 ? 1 : nc == 2 ? 2 : nc <= 4 ? 4 : 8;
         std::string name = std::string(gemv_base(p.wtype)) + (sub ? "_sub" : "") + "_c" + std::to_string(NC);
-        const size_t shmem = (size_t)rows_per_wg * waves_k * NC * sizeof(float);
         int32_t *sub_c = sub;
         if (sub) {
             const int64_t per = p.wtype == GHIP_TYPE_Q4_K ? 2 * p.nb : p.nb;
             sub_c = sub + c0 * p.N * per;
         }
-        ghip_status st = ctx->launch(name, dim3(grid), dim3(64 * waves_k), shmem, s, (const uint8_t *)w,
+        ghip_status st = ctx->launch(name, dim3(grid), dim3(64 * waves_k), 0, s, (const uint8_t *)w,
                                      (int64_t)p.w_row_bytes, (int)p.N, (int)p.nb, act + c0 * p.act_row_bytes,
-                                     (int64_t)p.act_row_bytes, nc, dst + c0 * ldd, (int64_t)ldd, rows_per_wg, sub_c);
+                                     (int64_t)p.act_row_bytes, nc, dst + c0 * ldd, (int64_t)ldd, sub_c);
         if (st != GHIP_STATUS_SUCCESS) return st;
     }
     return GHIP_STATUS_SUCCESS;

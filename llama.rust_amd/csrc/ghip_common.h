@@ -73,6 +73,34 @@ DEV float wave_sum(float v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
+// Transposed reduction of 8 per-row partials over a wavefront: on return every
+// lane of the 8-lane group g = lane>>3 holds the wavefront total of row g.
+// 10 cross-lane exchanges instead of 8 x 6.
+DEV float reduce8_rows(float v[8], int lane) {
+    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+    float u[4], w[2], x;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float send = b5 ? v[i] : v[i + 4];
+        const float keep = b5 ? v[i + 4] : v[i];
+        u[i] = keep + __shfl_xor(send, 32, 64);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const float send = b4 ? u[i] : u[i + 2];
+        const float keep = b4 ? u[i + 2] : u[i];
+        w[i] = keep + __shfl_xor(send, 16, 64);
+    }
+    {
+        const float send = b3 ? w[0] : w[1];
+        const float keep = b3 ? w[1] : w[0];
+        x = keep + __shfl_xor(send, 8, 64);
+    }
+    x += __shfl_xor(x, 4, 64);
+    x += __shfl_xor(x, 2, 64);
+    x += __shfl_xor(x, 1, 64);
+    return x;
+}
 DEV int group8_sum(int v) {
     v += __shfl_xor(v, 1, 64);
     v += __shfl_xor(v, 2, 64);

@@ -5,13 +5,15 @@
 //  * A workgroup is one "K-team": W_K wavefronts whose 64*W_K lanes tile the
 //    reduction dimension once (8 lanes per 256-block for the K-quants, one
 //    lane per pair of 32-blocks for Q4_0).  A lane's K position never changes,
-//    so its activation codes are loaded once into registers and reused for
-//    every weight row the team visits.
-//  * The team walks a tile of rows_per_wg consecutive weight rows; each row is
-//    a contiguous span, so a wavefront's loads are fully coalesced.
+//    so its activation codes are loaded once into registers.
+//  * The team owns RB = 8 consecutive weight rows.  Every lane issues the loads
+//    of all 8 rows before it consumes any (8 x 16 B per stream in flight per
+//    lane), which is what keeps enough HBM traffic in flight on a ~5 us
+//    kernel.  A wavefront's loads of one row are contiguous, so they coalesce.
 //  * Per row and activation column a lane forms an exact int32 partial
-//    (v_dot4_i32_i8 on unpacked nibbles), scales it in fp32, and the
-//    wavefront reduces; the W_K wave partials meet in LDS at the end.
+//    (v_dot4_i32_i8 on unpacked nibbles) and scales it in fp32; the 8 rows are
+//    reduced across the wavefront together (reduce8_rows), and the W_K
+//    wavefront partials meet in LDS.
 //
 // The exact integer sums of the reference (per row, column and block) are
 // available through the SUBSUMS instantiations, which reduce the 8 lanes of
@@ -21,19 +23,49 @@
 //   Q4_0: sum (nib-8) q8 per 32-block   (repack.rs:3351-3378)
 #include "ghip_common.h"
 
-constexpr int MAXC = 8;  // activation columns per launch
+constexpr int RB = 8;  // weight rows per workgroup
+
+// write the 8 row totals of column c (lanes with lane%8 == 0 hold them)
+DEV void stash_rows(float *red, float part[RB], int lane, int w, int nw, int c, int NC) {
+    const float t = reduce8_rows(part, lane);
+    if ((lane & 7) == 0) red[((lane >> 3) * nw + w) * NC + c] = t;
+}
+
+DEV void finish_rows(const float *red, int r0, int nrows, int ncols, int NC, int nw, float *dst, int64_t ldd) {
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < nrows * ncols; idx += blockDim.x) {
+        const int rr = idx / ncols, c = idx - rr * ncols;
+        float s = 0.0f;
+        for (int ww = 0; ww < nw; ww++) s += red[(rr * nw + ww) * NC + c];
+        dst[(int64_t)c * ldd + r0 + rr] = s;
+    }
+}
 
 // ---------------------------------------------------------------- Q4_K x Q8_K
 template <int NC, bool SUBSUMS>
 __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
                                               int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
                                               int ncols, float *__restrict__ dst, int64_t ldd,
-                                              int rows_per_wg, int32_t *__restrict__ sub) {
-    extern __shared__ float red[];  // [rows_per_wg][W_K][NC]
+                                              int32_t *__restrict__ sub) {
+    __shared__ float red[RB * 8 * NC];  // [row][wave][col], at most 8 waves
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int b = 8 * w + (lane >> 3), j = lane & 7, g = j >> 1, h = j & 1;
     const bool valid = b < nb;
+    const int r0 = blockIdx.x * RB;
+    const int nr = min(RB, rows - r0);
 
+    // weight loads first: RB rows x (header + one 16-byte qs chunk)
+    uint4 hdr[RB], q[RB];
+    const uint8_t *wb = W + (int64_t)r0 * w_row_bytes + (int64_t)b * Q4K_BYTES;
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        if (valid && rr < nr) {
+            hdr[rr] = ld16(wb + rr * w_row_bytes);
+            q[rr] = ld16(wb + rr * w_row_bytes + 16 + 16 * j);
+        } else {
+            hdr[rr] = q[rr] = make_uint4(0, 0, 0, 0);
+        }
+    }
     uint4 alo[NC], ahi[NC];
     int bp[NC];
     float da[NC];
@@ -53,19 +85,18 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
         }
     }
 
-    const int r0 = blockIdx.x * rows_per_wg;
-    const int r1 = min(rows, r0 + rows_per_wg);
-    const uint8_t *wb = W + (int64_t)b * Q4K_BYTES;
-
-    auto row_body = [&](int r, uint4 hdr, uint4 q) {
-        const float dw = h2f(hdr.x), dmin = h2f(hdr.x >> 16);
-        int slo, shi, sj, mj, mdummy;
-        scale_min_k4(hdr.y, hdr.z, hdr.w, 2 * g, slo, mdummy);
-        scale_min_k4(hdr.y, hdr.z, hdr.w, 2 * g + 1, shi, mdummy);
-        scale_min_k4(hdr.y, hdr.z, hdr.w, j, sj, mj);
-        const uint32_t l0 = q.x & 0x0f0f0f0f, l1 = q.y & 0x0f0f0f0f, l2 = q.z & 0x0f0f0f0f, l3 = q.w & 0x0f0f0f0f;
-        const uint32_t h0 = (q.x >> 4) & 0x0f0f0f0f, h1 = (q.y >> 4) & 0x0f0f0f0f;
-        const uint32_t h2 = (q.z >> 4) & 0x0f0f0f0f, h3 = (q.w >> 4) & 0x0f0f0f0f;
+    float part[NC][RB];
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        const uint4 hd = hdr[rr], qq = q[rr];
+        const float dw = h2f(hd.x), dmin = h2f(hd.x >> 16);
+        int slo, shi, mj, mdummy, sdummy;
+        scale_min_k4(hd.y, hd.z, hd.w, 2 * g, slo, mdummy);
+        scale_min_k4(hd.y, hd.z, hd.w, 2 * g + 1, shi, mdummy);
+        scale_min_k4(hd.y, hd.z, hd.w, j, sdummy, mj);
+        const uint32_t l0 = qq.x & 0x0f0f0f0f, l1 = qq.y & 0x0f0f0f0f, l2 = qq.z & 0x0f0f0f0f, l3 = qq.w & 0x0f0f0f0f;
+        const uint32_t h0 = (qq.x >> 4) & 0x0f0f0f0f, h1 = (qq.y >> 4) & 0x0f0f0f0f;
+        const uint32_t h2 = (qq.z >> 4) & 0x0f0f0f0f, h3 = (qq.w >> 4) & 0x0f0f0f0f;
 #pragma unroll
         for (int c = 0; c < NC; c++) {
             const int dl = dot4(l3, alo[c].w, dot4(l2, alo[c].z, dot4(l1, alo[c].y, dot4(l0, alo[c].x, 0))));
@@ -74,48 +105,18 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
             const int im = mj * bp[c];
             if (SUBSUMS) {
                 const int iab = group8_sum(ia), imb = group8_sum(im);
-                if (j == 0 && valid && c < ncols) {
-                    int32_t *s = sub + (((int64_t)c * rows + r) * nb + b) * 2;
+                if (j == 0 && valid && c < ncols && rr < nr) {
+                    int32_t *s = sub + (((int64_t)c * rows + r0 + rr) * nb + b) * 2;
                     s[0] = iab;
                     s[1] = imb;
                 }
             }
-            float part = valid ? da[c] * fmaf(dw, (float)ia, -(dmin * (float)im)) : 0.0f;
-            part = wave_sum(part);
-            if (lane == 0) red[((r - r0) * nw + w) * NC + c] = part;
+            part[c][rr] = da[c] * fmaf(dw, (float)ia, -(dmin * (float)im));
         }
-    };
-
-    int r = r0;
-    for (; r + 1 < r1; r += 2) {
-        uint4 hA = make_uint4(0, 0, 0, 0), qA = hA, hB = hA, qB = hA;
-        if (valid) {
-            const uint8_t *pA = wb + (int64_t)r * w_row_bytes;
-            const uint8_t *pB = pA + w_row_bytes;
-            hA = ld16(pA);
-            qA = ld16(pA + 16 + 16 * j);
-            hB = ld16(pB);
-            qB = ld16(pB + 16 + 16 * j);
-        }
-        row_body(r, hA, qA);
-        row_body(r + 1, hB, qB);
     }
-    if (r < r1) {
-        uint4 hA = make_uint4(0, 0, 0, 0), qA = hA;
-        if (valid) {
-            const uint8_t *pA = wb + (int64_t)r * w_row_bytes;
-            hA = ld16(pA);
-            qA = ld16(pA + 16 + 16 * j);
-        }
-        row_body(r, hA, qA);
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < (r1 - r0) * ncols; idx += blockDim.x) {
-        const int rr = idx / ncols, c = idx - rr * ncols;
-        float s = 0.0f;
-        for (int ww = 0; ww < nw; ww++) s += red[(rr * nw + ww) * NC + c];
-        dst[(int64_t)c * ldd + r0 + rr] = s;
-    }
+#pragma unroll
+    for (int c = 0; c < NC; c++) stash_rows(red, part[c], lane, w, nw, c, NC);
+    finish_rows(red, r0, nr, ncols, NC, nw, dst, ldd);
 }
 
 // ---------------------------------------------------------------- Q6_K x Q8_K
@@ -123,15 +124,35 @@ template <int NC, bool SUBSUMS>
 __device__ __forceinline__ void gemv_q6K_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
                                               int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
                                               int ncols, float *__restrict__ dst, int64_t ldd,
-                                              int rows_per_wg, int32_t *__restrict__ sub) {
-    extern __shared__ float red[];
+                                              int32_t *__restrict__ sub) {
+    __shared__ float red[RB * 8 * NC];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int b = 8 * w + (lane >> 3), j = lane & 7;
     const int jj = j >> 2, p = (j >> 1) & 1, t = j & 1;
     const bool valid = b < nb;
     const int ea = 128 * jj + 32 * p + 16 * t;  // first element of the low-nibble stream
     const int si = 8 * jj + 2 * p + t;          // its scale / bsum index; high stream is si+4
+    const int r0 = blockIdx.x * RB;
+    const int nr = min(RB, rows - r0);
 
+    uint4 ql[RB], qh[RB];
+    uint2 scv[RB];
+    uint32_t dv[RB];
+    const uint8_t *wb = W + (int64_t)r0 * w_row_bytes + (int64_t)b * Q6K_BYTES;
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        if (valid && rr < nr) {
+            const uint8_t *blk = wb + rr * w_row_bytes;
+            ql[rr] = ld16(blk + 64 * jj + 32 * p + 16 * t);
+            qh[rr] = ld16(blk + 128 + 32 * jj + 16 * t);
+            scv[rr] = ld8(blk + 192 + 8 * jj);
+            dv[rr] = ld2(blk + 208);
+        } else {
+            ql[rr] = qh[rr] = make_uint4(0, 0, 0, 0);
+            scv[rr] = make_uint2(0, 0);
+            dv[rr] = 0;
+        }
+    }
     uint4 ya[NC], yb[NC];
     int bsa[NC], bsb[NC];
     float da[NC];
@@ -150,19 +171,23 @@ __device__ __forceinline__ void gemv_q6K_impl(const uint8_t *__restrict__ W, int
             da[c] = 0.0f;
         }
     }
-    const int r0 = blockIdx.x * rows_per_wg;
-    const int r1 = min(rows, r0 + rows_per_wg);
-    const uint8_t *wb = W + (int64_t)b * Q6K_BYTES;
     const int sh = 2 * p;
-
-    auto row_body = [&](int r, uint4 ql, uint4 qh, int sca, int scb, float dw) {
+    const int sa_shift = 8 * ((2 * p + t) & 3);  // byte of sc[si] inside the 8-byte scale load
+    float part[NC][RB];
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
         uint32_t va[4], vb[4];
-        const uint32_t qlv[4] = {ql.x, ql.y, ql.z, ql.w}, qhv[4] = {qh.x, qh.y, qh.z, qh.w};
+        const uint32_t qlv[4] = {ql[rr].x, ql[rr].y, ql[rr].z, ql[rr].w};
+        const uint32_t qhv[4] = {qh[rr].x, qh[rr].y, qh[rr].z, qh[rr].w};
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             va[k] = (qlv[k] & 0x0f0f0f0f) | (((qhv[k] >> sh) & 0x03030303) << 4);
             vb[k] = ((qlv[k] >> 4) & 0x0f0f0f0f) | (((qhv[k] >> (sh + 4)) & 0x03030303) << 4);
         }
+        // sc[si] is byte (2p+t) of the low word, sc[si+4] the same byte of the high word
+        const int sca = (int)(int8_t)((scv[rr].x >> sa_shift) & 0xff);
+        const int scb = (int)(int8_t)((scv[rr].y >> sa_shift) & 0xff);
+        const float dw = h2f(dv[rr]);
 #pragma unroll
         for (int c = 0; c < NC; c++) {
             const int dA = dot4(va[3], ya[c].w, dot4(va[2], ya[c].z, dot4(va[1], ya[c].y, dot4(va[0], ya[c].x, 0))));
@@ -170,51 +195,14 @@ __device__ __forceinline__ void gemv_q6K_impl(const uint8_t *__restrict__ W, int
             const int is = sca * (dA - bsa[c]) + scb * (dB - bsb[c]);
             if (SUBSUMS) {
                 const int isb = group8_sum(is);
-                if (j == 0 && valid && c < ncols) sub[((int64_t)c * rows + r) * nb + b] = isb;
+                if (j == 0 && valid && c < ncols && rr < nr) sub[((int64_t)c * rows + r0 + rr) * nb + b] = isb;
             }
-            float part = valid ? (dw * (float)is) * da[c] : 0.0f;
-            part = wave_sum(part);
-            if (lane == 0) red[((r - r0) * nw + w) * NC + c] = part;
+            part[c][rr] = (dw * (float)is) * da[c];
         }
-    };
-    auto load = [&](int r, uint4 &ql, uint4 &qh, int &sca, int &scb, float &dw) {
-        if (valid) {
-            const uint8_t *blk = wb + (int64_t)r * w_row_bytes;
-            ql = ld16(blk + 64 * jj + 32 * p + 16 * t);
-            qh = ld16(blk + 128 + 32 * jj + 16 * t);
-            sca = (int)(int8_t)blk[192 + si];
-            scb = (int)(int8_t)blk[196 + si];
-            dw = h2f(ld2(blk + 208));
-        } else {
-            ql = qh = make_uint4(0, 0, 0, 0);
-            sca = scb = 0;
-            dw = 0.0f;
-        }
-    };
-    int r = r0;
-    for (; r + 1 < r1; r += 2) {
-        uint4 qlA, qhA, qlB, qhB;
-        int saA, sbA, saB, sbB;
-        float dA, dB;
-        load(r, qlA, qhA, saA, sbA, dA);
-        load(r + 1, qlB, qhB, saB, sbB, dB);
-        row_body(r, qlA, qhA, saA, sbA, dA);
-        row_body(r + 1, qlB, qhB, saB, sbB, dB);
     }
-    if (r < r1) {
-        uint4 qlA, qhA;
-        int saA, sbA;
-        float dA;
-        load(r, qlA, qhA, saA, sbA, dA);
-        row_body(r, qlA, qhA, saA, sbA, dA);
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < (r1 - r0) * ncols; idx += blockDim.x) {
-        const int rr = idx / ncols, c = idx - rr * ncols;
-        float s = 0.0f;
-        for (int ww = 0; ww < nw; ww++) s += red[(rr * nw + ww) * NC + c];
-        dst[(int64_t)c * ldd + r0 + rr] = s;
-    }
+#pragma unroll
+    for (int c = 0; c < NC; c++) stash_rows(red, part[c], lane, w, nw, c, NC);
+    finish_rows(red, r0, nr, ncols, NC, nw, dst, ldd);
 }
 
 // ---------------------------------------------------------------- Q4_0 x Q8_0
@@ -223,16 +211,38 @@ template <int NC, bool SUBSUMS>
 __device__ __forceinline__ void gemv_q4_0_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
                                                int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
                                                int ncols, float *__restrict__ dst, int64_t ldd,
-                                               int rows_per_wg, int32_t *__restrict__ sub) {
-    extern __shared__ float red[];
+                                               int32_t *__restrict__ sub) {
+    __shared__ float red[RB * 8 * NC];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int pr = 64 * w + lane;  // pair index
     const int b0 = 2 * pr, b1 = 2 * pr + 1;
     const bool v0 = b0 < nb, v1 = b1 < nb;
+    const int r0 = blockIdx.x * RB;
+    const int nr = min(RB, rows - r0);
 
+    uint4 wa[RB], wbq[RB];
+    uint32_t wc[RB];
+    const uint8_t *wb = W + (int64_t)r0 * w_row_bytes + (int64_t)pr * 36;
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        const uint8_t *p = wb + rr * w_row_bytes;
+        wa[rr] = wbq[rr] = make_uint4(0, 0, 0, 0);
+        wc[rr] = 0;
+        if (rr < nr) {
+            if (v1) {
+                wa[rr] = ld16(p);
+                wbq[rr] = ld16(p + 16);
+                wc[rr] = ld4(p + 32);
+            } else if (v0) {
+                wa[rr] = ld16(p);
+                wbq[rr] = make_uint4(ld2(p + 16), 0, 0, 0);
+            }
+        }
+    }
     uint4 y0l[NC], y0h[NC], y1l[NC], y1h[NC];
     int sy0[NC], sy1[NC];
     float d0[NC], d1[NC];
+    const uint32_t one = 0x01010101u;
 #pragma unroll
     for (int c = 0; c < NC; c++) {
         y0l[c] = y0h[c] = y1l[c] = y1h[c] = make_uint4(0, 0, 0, 0);
@@ -243,7 +253,6 @@ __device__ __forceinline__ void gemv_q4_0_impl(const uint8_t *__restrict__ W, in
             d0[c] = h2f(ld2(A));
             y0l[c] = ld16(A + 2);
             y0h[c] = ld16(A + 18);
-            const uint32_t one = 0x01010101u;
             sy0[c] = 8 * dot4(y0l[c].x, one, dot4(y0l[c].y, one, dot4(y0l[c].z, one, dot4(y0l[c].w, one,
                      dot4(y0h[c].x, one, dot4(y0h[c].y, one, dot4(y0h[c].z, one, dot4(y0h[c].w, one, 0))))))));
         }
@@ -252,36 +261,18 @@ __device__ __forceinline__ void gemv_q4_0_impl(const uint8_t *__restrict__ W, in
             d1[c] = h2f(ld2(A));
             y1l[c] = ld16(A + 2);
             y1h[c] = ld16(A + 18);
-            const uint32_t one = 0x01010101u;
             sy1[c] = 8 * dot4(y1l[c].x, one, dot4(y1l[c].y, one, dot4(y1l[c].z, one, dot4(y1l[c].w, one,
                      dot4(y1h[c].x, one, dot4(y1h[c].y, one, dot4(y1h[c].z, one, dot4(y1h[c].w, one, 0))))))));
         }
     }
-    const int r0 = blockIdx.x * rows_per_wg;
-    const int r1 = min(rows, r0 + rows_per_wg);
-    const uint8_t *wb = W + (int64_t)pr * 36;
-
-    auto load = [&](int r, uint4 &a, uint4 &bq, uint32_t &c8) {
-        const uint8_t *p = wb + (int64_t)r * w_row_bytes;
-        if (v1) {
-            a = ld16(p);
-            bq = ld16(p + 16);
-            c8 = ld4(p + 32);
-        } else if (v0) {
-            a = ld16(p);
-            const uint16_t t = ld2(p + 16);
-            bq = make_uint4(t, 0, 0, 0);
-            c8 = 0;
-        } else {
-            a = bq = make_uint4(0, 0, 0, 0);
-            c8 = 0;
-        }
-    };
-    auto row_body = [&](int r, uint4 a, uint4 bq, uint32_t c8) {
+    float part[NC][RB];
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        const uint4 a = wa[rr], bq = wbq[rr];
         const float dw0 = h2f(a.x), dw1 = h2f(bq.x >> 16);
         const uint32_t q0[4] = {__builtin_amdgcn_alignbyte(a.y, a.x, 2), __builtin_amdgcn_alignbyte(a.z, a.y, 2),
                                 __builtin_amdgcn_alignbyte(a.w, a.z, 2), __builtin_amdgcn_alignbyte(bq.x, a.w, 2)};
-        const uint32_t q1[4] = {bq.y, bq.z, bq.w, c8};
+        const uint32_t q1[4] = {bq.y, bq.z, bq.w, wc[rr]};
 #pragma unroll
         for (int c = 0; c < NC; c++) {
             const int s0 = dot4(q0[3] & 0x0f0f0f0f, y0l[c].w, dot4(q0[2] & 0x0f0f0f0f, y0l[c].z,
@@ -294,52 +285,31 @@ __device__ __forceinline__ void gemv_q4_0_impl(const uint8_t *__restrict__ W, in
                            dot4((q1[3] >> 4) & 0x0f0f0f0f, y1h[c].w, dot4((q1[2] >> 4) & 0x0f0f0f0f, y1h[c].z,
                            dot4((q1[1] >> 4) & 0x0f0f0f0f, y1h[c].y, dot4((q1[0] >> 4) & 0x0f0f0f0f, y1h[c].x,
                            -sy1[c]))))))));
-            if (SUBSUMS && c < ncols) {
-                int32_t *s = sub + ((int64_t)c * rows + r) * nb;
+            if (SUBSUMS && c < ncols && rr < nr) {
+                int32_t *s = sub + ((int64_t)c * rows + r0 + rr) * nb;
                 if (v0) s[b0] = s0;
                 if (v1) s[b1] = s1;
             }
-            float part = v0 ? (float)s0 * (dw0 * d0[c]) : 0.0f;
-            if (v1) part = fmaf((float)s1, dw1 * d1[c], part);
-            part = wave_sum(part);
-            if (lane == 0) red[((r - r0) * nw + w) * NC + c] = part;
+            float pp = v0 ? (float)s0 * (dw0 * d0[c]) : 0.0f;
+            if (v1) pp = fmaf((float)s1, dw1 * d1[c], pp);
+            part[c][rr] = pp;
         }
-    };
-    int r = r0;
-    for (; r + 1 < r1; r += 2) {
-        uint4 aA, bA, aB, bB;
-        uint32_t cA, cB;
-        load(r, aA, bA, cA);
-        load(r + 1, aB, bB, cB);
-        row_body(r, aA, bA, cA);
-        row_body(r + 1, aB, bB, cB);
     }
-    if (r < r1) {
-        uint4 aA, bA;
-        uint32_t cA;
-        load(r, aA, bA, cA);
-        row_body(r, aA, bA, cA);
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < (r1 - r0) * ncols; idx += blockDim.x) {
-        const int rr = idx / ncols, c = idx - rr * ncols;
-        float s = 0.0f;
-        for (int ww = 0; ww < nw; ww++) s += red[(rr * nw + ww) * NC + c];
-        dst[(int64_t)c * ldd + r0 + rr] = s;
-    }
+#pragma unroll
+    for (int c = 0; c < NC; c++) stash_rows(red, part[c], lane, w, nw, c, NC);
+    finish_rows(red, r0, nr, ncols, NC, nw, dst, ldd);
 }
 
 #define GEMV_ARGS                                                                                     \
     const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb, const uint8_t *__restrict__ act, \
-        int64_t act_row_bytes, int ncols, float *__restrict__ dst, int64_t ldd, int rows_per_wg,          \
-        int32_t *__restrict__ sub
-#define GEMV_PASS W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, rows_per_wg, sub
+        int64_t act_row_bytes, int ncols, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub
+#define GEMV_PASS W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub
 
 #define GEMV_INST(name, impl, NC)                                                                  \
-    extern "C" __global__ void __launch_bounds__(512) name##_c##NC(GEMV_ARGS) {                  \
+    extern "C" __global__ void __launch_bounds__(512) name##_c##NC(GEMV_ARGS) {                   \
         impl<NC, false>(GEMV_PASS);                                                                \
     }                                                                                              \
-    extern "C" __global__ void __launch_bounds__(512) name##_sub_c##NC(GEMV_ARGS) {              \
+    extern "C" __global__ void __launch_bounds__(512) name##_sub_c##NC(GEMV_ARGS) {               \
         impl<NC, true>(GEMV_PASS);                                                                 \
     }
 #define GEMV_ALL(name, impl) \

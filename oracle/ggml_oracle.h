@@ -93,24 +93,30 @@ int oracle_mul_mat_id_mxfp4(const void *as, int64_t n, int64_t rows, int64_t n_a
                             int nthreads);
 
 /*
- * FLASH_ATTN_EXT (compute.rs:4563, flash_attn.rs), f16 K/V, f16 mask, no
- * ALiBi/softcap/sinks:
- *   q    [n_q][H][D] f32 (ggml ne = [D, n_q, H], nb: see below)
- *   k, v [H_kv][S][D] f16
- *   mask [n_q][S] f16 (may be NULL)
- *   dst  [n_q][H][D] f32
- * The caller passes tensors in ggml's physical layout:
- *   q:   element (d, t, h) at q[h*q_nb2 + t*q_nb1 + d]  (float strides)
- *   k/v: element (d, s, h) at k[h*kv_nb2 + s*kv_nb1 + d] (half strides)
- *   dst: element (d, h, t) at dst[t*H*D + h*D + d]
- * n_chunks is the split-KV chunk count (= the reference's thread count).
+ * FLASH_ATTN_EXT (compute.rs:4563-4625, flash_attn.rs), dense tensors:
+ *   q    element (d, t, h) at q[h*q_nb2 + t*q_nb1 + d]       (f32; strides in floats)
+ *   k, v element (d, s, h) at k[h*k_nb2 + s*k_nb1 + d]       (f16 or f32; strides in elements)
+ *   mask element (s, t)    at mask[t*mask_nb1 + s]           (f16, may be NULL)
+ *   sinks[h] (may be NULL), dst element (d, h, t) at dst[(t*H + h)*DV + d]
+ * n_chunks: the split-KV chunk count of the single-row decode path (the
+ * reference uses its thread count).  Returns the path taken: 1 split-KV,
+ * 2 tiled, 3 one_chunk; < 0 on bad shapes.
  */
-int oracle_flash_attn_ext(const float *q, int64_t q_nb1, int64_t q_nb2,
-                          const uint16_t *k, const uint16_t *v, int64_t kv_nb1, int64_t kv_nb2,
-                          const uint16_t *mask, int64_t mask_nb1,
-                          float *dst, int D, int n_q, int H, int S, int H_kv,
-                          float scale, float max_bias, float softcap,
-                          int n_chunks, int nthreads);
+typedef struct oracle_fa_args {
+    const float *q;
+    int64_t q_nb1, q_nb2;
+    const void *k, *v;
+    int64_t k_nb1, k_nb2, v_nb1, v_nb2;
+    int kv_f16;
+    const uint16_t *mask;
+    int64_t mask_nb1;
+    const float *sinks;
+    float *dst;
+    int DK, DV, T, H, S, H_kv;
+    float scale, max_bias, softcap;
+    int n_chunks, nthreads;
+} oracle_fa_args;
+int oracle_flash_attn_ext(const oracle_fa_args *a);
 
 double oracle_wtime(void);
 

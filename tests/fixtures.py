@@ -140,3 +140,78 @@ def repack_dump(name):
              gemv=f32(s[5]), gemm=f32(s[6]), gemv_gen=f32(s[7]), gemm_gen=f32(s[8]),
              act_g=f32(s[9]), act_m=f32(s[10]))
     return d
+
+
+def fa_ref_cases():
+    """parity/fa_ref.bin (flash_attn.rs:2064-2117): per case a header of i64
+    {mode, dk, dv, h, h_kv, t, s_kv, k_type, v_type} and length-prefixed q, k, v,
+    mask, sinks, out, extra (scale, max_bias, softcap)."""
+    b = read("fa_ref.bin")
+    o = 0
+    cases = []
+
+    def nxt():
+        nonlocal o
+        (ln,) = struct.unpack_from("<I", b, o)
+        o += 4
+        v = b[o:o + ln]
+        o += ln
+        return v
+    while o < len(b):
+        hdr = nxt()
+        g = struct.unpack("<%dq" % (len(hdr) // 8), hdr)
+        q, k, v, mask, sinks, out, extra = (nxt() for _ in range(7))
+        mode, dk, dv, h, h_kv, t, s_kv, kt, vt = g[:9]
+        kdt = np.float16 if kt else np.float32
+        vdt = np.float16 if vt else np.float32
+        sc, mb, cap = struct.unpack("<3f", extra[:12])
+        cases.append(dict(
+            mode=mode, dk=dk, dv=dv, h=h, h_kv=h_kv, t=t, s=s_kv,
+            q=np.frombuffer(q, dtype=np.float32).reshape(h, t, dk),
+            k=np.frombuffer(k, dtype=kdt).reshape(h_kv, s_kv, dk),
+            v=np.frombuffer(v, dtype=vdt).reshape(h_kv, s_kv, dv),
+            mask=np.frombuffer(mask, dtype=np.float16).reshape(t, s_kv) if mask else None,
+            sinks=np.frombuffer(sinks, dtype=np.float32) if sinks else None,
+            out=np.frombuffer(out, dtype=np.float32).reshape(t, h, dv),
+            scale=sc, max_bias=mb, softcap=cap))
+    return cases
+
+
+def fa_probe_groups():
+    """parity/fa_probe.bin (flash_attn.rs:2541-2640): record groups
+    (geometry, knobs, q, k, v, mask, sinks) followed by 1 + t (+1 if t >= 2)
+    records {tag, t index, nth, out}: tag 0 = the T-row batch, tag 1 = row t
+    alone, tag 2 = rows 1..T-1."""
+    b = read("fa_probe.bin")
+    o = 0
+    groups = []
+
+    def nxt():
+        nonlocal o
+        (ln,) = struct.unpack_from("<I", b, o)
+        o += 4
+        v = b[o:o + ln]
+        o += ln
+        return v
+    while o + 4 <= len(b):
+        (magic,) = struct.unpack_from("<I", b, o)
+        assert magic == 0xF17E0001
+        o += 4
+        geom, knobs, q, k, v, m, s = (nxt() for _ in range(7))
+        dk, dv, h, h_kv, t, s_kv = struct.unpack("<6q", geom[:48])
+        sc, mb, cap = struct.unpack("<3f", knobs[:12])
+        recs = []
+        for _ in range(1 + t + (1 if t >= 2 else 0)):
+            tag, ti, nth = struct.unpack_from("<3I", b, o)
+            o += 12
+            out = np.frombuffer(nxt(), dtype=np.float32)
+            recs.append((tag, ti, nth, out))
+        groups.append(dict(
+            dk=dk, dv=dv, h=h, h_kv=h_kv, t=t, s=s_kv,
+            q=np.frombuffer(q, dtype=np.float32).reshape(h, t, dk),
+            k=np.frombuffer(k, dtype=np.float16).reshape(h_kv, s_kv, dk),
+            v=np.frombuffer(v, dtype=np.float16).reshape(h_kv, s_kv, dv),
+            mask=np.frombuffer(m, dtype=np.float16).reshape(t, s_kv) if m else None,
+            sinks=np.frombuffer(s, dtype=np.float32) if s else None,
+            scale=sc, max_bias=mb, softcap=cap, recs=recs))
+    return groups

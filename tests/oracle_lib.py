@@ -29,6 +29,17 @@ def build():
     subprocess.run(["make", "-s", "-C", ORACLE_DIR], check=True)
 
 
+class FaArgs(C.Structure):
+    _fields_ = [("q", C.c_void_p), ("q_nb1", C.c_int64), ("q_nb2", C.c_int64),
+                ("k", C.c_void_p), ("v", C.c_void_p),
+                ("k_nb1", C.c_int64), ("k_nb2", C.c_int64), ("v_nb1", C.c_int64), ("v_nb2", C.c_int64),
+                ("kv_f16", C.c_int), ("mask", C.c_void_p), ("mask_nb1", C.c_int64),
+                ("sinks", C.c_void_p), ("dst", C.c_void_p),
+                ("DK", C.c_int), ("DV", C.c_int), ("T", C.c_int), ("H", C.c_int), ("S", C.c_int),
+                ("H_kv", C.c_int), ("scale", C.c_float), ("max_bias", C.c_float), ("softcap", C.c_float),
+                ("n_chunks", C.c_int), ("nthreads", C.c_int)]
+
+
 _lib = None
 
 
@@ -66,9 +77,7 @@ def lib():
         L.oracle_mul_mat_id_mxfp4.restype = C.c_int
         L.oracle_mul_mat_id_mxfp4.argtypes = [vp, i64, i64, i64, vp, i64, i64, vp, i64, vp, C.c_int]
         L.oracle_flash_attn_ext.restype = C.c_int
-        L.oracle_flash_attn_ext.argtypes = [vp, i64, i64, vp, vp, i64, i64, vp, i64, vp,
-                                            C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
-                                            C.c_float, C.c_float, C.c_float, C.c_int, C.c_int]
+        L.oracle_flash_attn_ext.argtypes = [C.POINTER(FaArgs)]
         L.oracle_wtime.restype = C.c_double
         _lib = L
     return _lib
@@ -144,3 +153,38 @@ def mul_mat_id_mxfp4(as_q, n, rows, n_as, b, ne11, n_tokens, ids, n_ids, nthread
 
 def wtime():
     return lib().oracle_wtime()
+
+
+def flash_attn_ext(q, k, v, mask=None, sinks=None, scale=1.0, max_bias=0.0, softcap=0.0, n_chunks=1,
+                   nthreads=0):
+    """q [H, T, DK] f32, k [H_kv, S, DK], v [H_kv, S, DV] (float16 or float32),
+    mask [T, S] float16 or None, sinks [H] f32 or None.
+    Returns (dst [T, H, DV] f32, path)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    kv_f16 = k.dtype == np.float16
+    k = np.ascontiguousarray(k)
+    v = np.ascontiguousarray(v, dtype=k.dtype)
+    H, T, DK = q.shape
+    H_kv, S, _ = k.shape
+    DV = v.shape[2]
+    dst = np.zeros((T, H, DV), dtype=np.float32)
+    a = FaArgs()
+    a.q, a.q_nb1, a.q_nb2 = q.ctypes.data, DK, T * DK
+    a.k, a.v = k.ctypes.data, v.ctypes.data
+    a.k_nb1, a.k_nb2, a.v_nb1, a.v_nb2 = DK, S * DK, DV, S * DV
+    a.kv_f16 = int(kv_f16)
+    if mask is not None:
+        mask = np.ascontiguousarray(mask, dtype=np.float16)
+        a.mask, a.mask_nb1 = mask.ctypes.data, mask.shape[1]
+    if sinks is not None:
+        sinks = np.ascontiguousarray(sinks, dtype=np.float32)
+        a.sinks = sinks.ctypes.data
+    a.dst = dst.ctypes.data
+    a.DK, a.DV, a.T, a.H, a.S, a.H_kv = DK, DV, T, H, S, H_kv
+    a.scale, a.max_bias, a.softcap = scale, max_bias, softcap
+    a.n_chunks = n_chunks
+    a.nthreads = nthreads or (os.cpu_count() or 1)
+    path = lib().oracle_flash_attn_ext(C.byref(a))
+    if path < 0:
+        raise ValueError("oracle_flash_attn_ext: bad shape")
+    return dst, path

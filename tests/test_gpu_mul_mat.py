@@ -123,3 +123,33 @@ def test_unsupported_type_raises(be):
     x = torch.zeros((1, 32), dtype=torch.float32, device="cuda")
     with pytest.raises(ghip.GhipError):
         be.mul_mat(w, O.Q8_0, 32, x)
+
+
+# ---------------------------------------------------------------- prefill GEMM
+@pytest.mark.parametrize("n,rows,cols", [(256, 32, 16), (512, 136, 37), (1024, 128, 128),
+                                         (768, 200, 130), (4096, 256, 64)])
+def test_gemm_q4K_small(be, n, rows, cols):
+    """Q4_K with >= 16 activation rows takes the int8-MFMA GEMM; tile edges in
+    both M (tokens) and N (weight rows)."""
+    run_case(be, O.Q4_K, n, rows, cols, seed=rows)
+
+
+@pytest.mark.parametrize("tokens,n,rows", [(128, 4096, 4096), (512, 4096, 14336), (2048, 4096, 4096)])
+def test_gemm_q4K_prefill_shapes(be, tokens, n, rows):
+    """Config 3 shapes.  The GPU computes the whole product; the oracle checks
+    a 512-row slice of the weights (every token, every super-block), plus the
+    sub-sums of 64 of those rows."""
+    w, x = make(O.Q4_K, n, rows, tokens, seed=3)
+    sl = slice(rows // 3, rows // 3 + 512) if rows > 512 else slice(0, rows)
+    wsl = w[sl]
+    nr = wsl.shape[0]
+    print(f"gemm tokens={tokens} n={n} rows={rows}", flush=True)
+    got = be.mul_mat(torch.from_numpy(w).cuda(), O.Q4_K, n, torch.from_numpy(x).cuda()).cpu().numpy()
+    want, route, _ = O.mul_mat(O.Q4_K, wsl, n, nr, x, tokens)
+    assert route == O.ROUTE_REPACK
+    err = rel_err(got[:, sl], want)
+    assert err <= TOL, f"rel_err {err:.3e}"
+    w64 = np.ascontiguousarray(wsl[:64])
+    sub = be.mul_mat_subsums(torch.from_numpy(w64).cuda(), O.Q4_K, n, torch.from_numpy(x).cuda()).cpu().numpy()
+    _, _, want_sub = O.mul_mat(O.Q4_K, w64, n, 64, x, tokens, want_subsums=True)
+    assert np.array_equal(sub, want_sub)

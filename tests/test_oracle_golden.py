@@ -227,3 +227,61 @@ def test_q4k_subsums_brute_force():
         Af = O.dequantize(O.Q8_K, act, cols * n).reshape(cols, n).astype(np.float64)
         ref = Af @ Wf.T
         assert np.max(np.abs(out - ref) / np.maximum(np.abs(ref), 1)) < 1e-5
+
+
+def test_flash_attn_ref_dump_bit_exact():
+    """flash_attn.rs:2195 ref_dump_bitexact: all 15 cases (one_chunk and tiled,
+    F16/F32 K/V, sinks, softcap, ALiBi, DV != DK, padded KV tail)."""
+    cases = fx.fa_ref_cases()
+    assert len(cases) == 15
+    paths = set()
+    for c in cases:
+        out, path = O.flash_attn_ext(c["q"], c["k"], c["v"], c["mask"], c["sinks"], c["scale"],
+                                     c["max_bias"], c["softcap"])
+        paths.add(path)
+        assert path == (2 if c["t"] >= 64 else 3)
+        assert np.array_equal(out.view(np.uint32), c["out"].view(np.uint32)), f"mode {c['mode']}"
+    assert paths == {2, 3}
+
+
+def test_flash_attn_probe_split_kv_bit_exact():
+    """flash_attn.rs:2541 ref_probe_dump_bitexact: the T-row batch, each row
+    alone and rows 1..T-1, at nth = 1 and 8 -- single rows with S_kv >= 512
+    take split-KV with n_chunks = nth."""
+    groups = fx.fa_probe_groups()
+    n_split = 0
+    for g in groups:
+        for tag, ti, nth, ref in g["recs"]:
+            t0, t1 = {0: (0, g["t"]), 1: (ti, ti + 1), 2: (1, g["t"])}[tag]
+            q = g["q"][:, t0:t1]
+            m = g["mask"][t0:t1] if g["mask"] is not None else None
+            out, path = O.flash_attn_ext(q, g["k"], g["v"], m, g["sinks"], g["scale"], g["max_bias"],
+                                         g["softcap"], n_chunks=nth)
+            if path == 1 and nth > 1:
+                n_split += 1
+            assert np.array_equal(out.reshape(-1).view(np.uint32), ref.view(np.uint32)), \
+                f"T={g['t']} S={g['s']} tag={tag} t={ti} nth={nth}"
+    assert n_split > 0, "the probe must exercise the multi-chunk split-KV merge"
+
+
+def test_flash_attn_against_float64():
+    """Closed form: the oracle's three paths agree with a float64 softmax(QK^T)V
+    within the f16-accumulator error, and split-KV with 1 chunk equals one_chunk."""
+    rng = np.random.default_rng(2)
+    H, Hkv, D = 4, 2, 64
+    for T, S in [(1, 600), (3, 40), (70, 130)]:
+        q = rng.standard_normal((H, T, D)).astype(np.float32)
+        k = rng.standard_normal((Hkv, S, D)).astype(np.float16)
+        v = rng.standard_normal((Hkv, S, D)).astype(np.float16)
+        mask = np.zeros((T, S), dtype=np.float16)
+        for t in range(T):
+            mask[t, S - T + t + 1:] = -np.inf
+        out, _ = O.flash_attn_ext(q, k, v, mask, scale=1 / 8.0, n_chunks=3)
+        ref = np.zeros_like(out, dtype=np.float64)
+        for h in range(H):
+            kk = k[h // 2].astype(np.float64)
+            vv = v[h // 2].astype(np.float64)
+            s = (q[h].astype(np.float16).astype(np.float64) @ kk.T) / 8.0 + mask.astype(np.float64)
+            p = np.exp(s - s.max(1, keepdims=True))
+            ref[:, h] = (p / p.sum(1, keepdims=True)) @ vv
+        assert np.max(np.abs(out - ref)) < 2e-3

@@ -125,6 +125,42 @@ ghip_status ghip_mul_mat_subsums(ghip_context *ctx, const ghip_tensor *src0, con
 ghip_status ghip_mul_mat_act(ghip_context *ctx, const ghip_tensor *src0, const ghip_tensor *src1,
                              void *out, void *stream);
 
+/* dst = MUL_MAT_ID(as, b, ids) with MXFP4 experts (forward_mul_mat_id,
+ * compute.rs:1917-2202; the rows % 8 == 0 repack kernel repack.rs:1048-1100):
+ *   as:  MXFP4 [K, rows, n_as], expert rows contiguous blocks
+ *   b:   F32 [K, ne11, n_tokens] (nb0 == 4, nb2 == ne11 * nb1), 1 <= ne11 <= n_ids
+ *   ids: I32 [n_ids, n_tokens], expert index per (slot, token)
+ *   dst: F32 [rows, n_ids, n_tokens] (nb0 == 4)
+ * dst[t][s] = as[ids[t][s]] x quantize_q8_0(b[t][s % ne11]).  Each 32-block
+ * dot is exact and folded in block order with the reference's own operations
+ * (fma(dot, e * d, acc) for rows % 8 == 0, acc += (d * e) * dot otherwise), so
+ * outputs are bit-identical.  A pair whose id is outside [0, n_as) -- where
+ * the reference asserts -- gets a row of NaN. */
+ghip_status ghip_mul_mat_id(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b, const ghip_tensor *ids,
+                            const ghip_tensor *dst, void *stream);
+
+/* Parity hook with no reference counterpart: the int32 block dots
+ * sum kvalue * q8 that ghip_mul_mat_id folds, at
+ * subsums[((t * n_ids + s) * rows + r) * (K / 32) + block] (device pointer).
+ * Pairs with an invalid id are left unwritten. */
+ghip_status ghip_mul_mat_id_subsums(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b,
+                                    const ghip_tensor *ids, int32_t *subsums, void *stream);
+
+/* dst = FLASH_ATTN_EXT(q, k, v, mask, sinks) (forward_flash_attn_ext
+ * compute.rs:4563-4625; FlashAttn flash_attn.rs:273-386):
+ *   q:     F32 [DK, T, H]      (nb0 == 4, any nb1/nb2)
+ *   k, v:  F16 [DK, S, H_kv]   (nb0 == 2), DK == DV in {64, 128}, H % H_kv == 0,
+ *          H / H_kv <= 8
+ *   mask:  F16 [>= S, >= T] or NULL (rows contiguous)
+ *   sinks: F32 [H] or NULL
+ *   dst:   F32 [DV, H, T] contiguous
+ *   dst->op_params: [0] scale, [1] max_bias, [2] logit_softcap (f32 bits).
+ * The KV range is split across workgroups and merged in slice order; the
+ * result matches the reference within its f16-K/V tolerance (2e-3 max-abs). */
+ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const ghip_tensor *k, const ghip_tensor *v,
+                                const ghip_tensor *mask, const ghip_tensor *sinks, const ghip_tensor *dst,
+                                void *stream);
+
 /* Quantize nrows rows of n_per_row f32 values (device pointer src) into
  * GGUF blocks of `type` (Q4_0, Q4_K, Q6_K, MXFP4) at the device pointer dst,
  * byte-identical to the reference's no-imatrix quantizers

@@ -6,6 +6,7 @@
 
 #include <dlfcn.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -16,7 +17,7 @@
 
 namespace {
 
-const char *const kModules[] = {"ghip_quant.hsaco", "ghip_gemv.hsaco", "ghip_wquant.hsaco", "ghip_gemm.hsaco"};
+const char *const kModules[] = {"ghip_quant.hsaco", "ghip_gemv.hsaco", "ghip_wquant.hsaco", "ghip_gemm.hsaco", "ghip_fa.hsaco", "ghip_moe.hsaco"};
 
 struct TypeInfo {
     int blck;
@@ -215,29 +216,41 @@ const char *gemv_base(int wtype) {
     }
 }
 
-// Decode path: activation columns in groups of at most 8.
-ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, float *dst,
-                     int64_t ldd, int32_t *sub, hipStream_t s) {
+// Decode path: activation columns in groups of at most 8.  Q4_K reads the f32
+// activations and quantizes them inside the kernel when fused is set.
+ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, int64_t act_rb,
+                     bool fused, float *dst, int64_t ldd, int32_t *sub, hipStream_t s) {
     int waves_k;
     if (p.wtype == GHIP_TYPE_Q4_0)
         waves_k = (int)(((p.nb + 1) / 2 + 63) / 64);
     else
         waves_k = (int)((p.nb + 7) / 8);
     if (waves_k > 8) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: ne00 = %lld too large for the decode kernel", (long long)p.K);
-    const int rows_per_wg = 8;  // RB in ghip_gemv.hip
+    const bool q4k = p.wtype == GHIP_TYPE_Q4_K;
+    const int rows_per_wg = q4k ? std::max(8, env_int("GHIP_GEMV_ROWS", 16) / 8 * 8) : 8;
     const unsigned grid = (unsigned)((p.N + rows_per_wg - 1) / rows_per_wg);
     for (int64_t c0 = 0; c0 < p.M; c0 += 8) {
         const int nc = (int)std::min<int64_t>(8, p.M - c0);
         const int NC = nc == 1 ? 1 : nc == 2 ? 2 : nc <= 4 ? 4 : 8;
-        std::string name = std::string(gemv_base(p.wtype)) + (sub ? "_sub" : "") + "_c" + std::to_string(NC);
+        std::string name = std::string(gemv_base(p.wtype)) + (q4k && fused ? "_f" : "") + (sub ? "_sub" : "") +
+                           "_c" + std::to_string(NC);
         int32_t *sub_c = sub;
         if (sub) {
             const int64_t per = p.wtype == GHIP_TYPE_Q4_K ? 2 * p.nb : p.nb;
             sub_c = sub + c0 * p.N * per;
         }
-        ghip_status st = ctx->launch(name, dim3(grid), dim3(64 * waves_k), 0, s, (const uint8_t *)w,
-                                     (int64_t)p.w_row_bytes, (int)p.N, (int)p.nb, act + c0 * p.act_row_bytes,
-                                     (int64_t)p.act_row_bytes, nc, dst + c0 * ldd, (int64_t)ldd, sub_c);
+        ghip_status st;
+        if (q4k) {
+            const size_t shmem = (size_t)rows_per_wg * waves_k * NC * sizeof(float);
+            const int n_mat = (int)std::max<int64_t>(0, std::min<int64_t>(nc, p.n_mat - c0));
+            st = ctx->launch(name, dim3(grid), dim3(64 * waves_k), shmem, s, (const uint8_t *)w,
+                             (int64_t)p.w_row_bytes, (int)p.N, (int)p.nb, act + c0 * act_rb, (int64_t)act_rb, nc,
+                             dst + c0 * ldd, (int64_t)ldd, sub_c, rows_per_wg, n_mat);
+        } else {
+            st = ctx->launch(name, dim3(grid), dim3(64 * waves_k), 0, s, (const uint8_t *)w, (int64_t)p.w_row_bytes,
+                             (int)p.N, (int)p.nb, act + c0 * act_rb, (int64_t)act_rb, nc, dst + c0 * ldd,
+                             (int64_t)ldd, sub_c);
+        }
         if (st != GHIP_STATUS_SUCCESS) return st;
     }
     return GHIP_STATUS_SUCCESS;
@@ -277,22 +290,252 @@ ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_ten
         if (st != GHIP_STATUS_SUCCESS) return st;
     }
     void *act = act_out ? act_out : ws;
-    if (p.act_pre) {
-        if (act_out) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat_act: src1 is already quantized");
-        act = b->data;
-    } else {
-        st = quantize_act(ctx, p, b, act, s);
-        if (st != GHIP_STATUS_SUCCESS || act_out) return st;
+    if (act_out) {
+        if (p.act_pre) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat_act: src1 is already quantized");
+        return quantize_act(ctx, p, b, act, s);
     }
     float *dst = d ? (float *)d->data : (float *)((uint8_t *)ws + act_bytes);
     const int64_t ldd = d ? (int64_t)d->nb[1] / 4 : p.N;
-    if (use_gemm(p)) return run_gemm(ctx, p, a->data, (const uint8_t *)act, dst, ldd, sub, s);
-    return run_gemv(ctx, p, a->data, (const uint8_t *)act, dst, ldd, sub, s);
+    if (use_gemm(p)) {
+        if (!p.act_pre) {
+            st = quantize_act(ctx, p, b, act, s);
+            if (st != GHIP_STATUS_SUCCESS) return st;
+        } else {
+            act = b->data;
+        }
+        return run_gemm(ctx, p, a->data, (const uint8_t *)act, dst, ldd, sub, s);
+    }
+    if (p.act_pre) return run_gemv(ctx, p, a->data, (const uint8_t *)b->data, p.act_row_bytes, false, dst, ldd, sub, s);
+    if (p.wtype == GHIP_TYPE_Q4_K)  // quantization fused into the decode kernel
+        return run_gemv(ctx, p, a->data, (const uint8_t *)b->data, (int64_t)b->nb[1], true, dst, ldd, sub, s);
+    st = quantize_act(ctx, p, b, act, s);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    return run_gemv(ctx, p, a->data, (const uint8_t *)act, p.act_row_bytes, false, dst, ldd, sub, s);
+}
+
+// ------------------------------------------------------------ FLASH_ATTN_EXT
+
+// Mirror of FaParams in ghip_fa.hip (passed by value as the only kernel argument).
+struct FaParams {
+    const float *q;
+    int64_t q_nb1, q_nb2;
+    const uint16_t *k, *v;
+    int64_t k_nb1, k_nb2, v_nb1, v_nb2;
+    const uint16_t *mask;
+    int64_t mask_nb1;
+    float *dst;
+    float *part;
+    const float *sinks;  // [H] or null
+    int T, S, H, H_kv, nsplit, chunk;
+    float scale, softcap, m0, m1;
+    int n_head_log2;
+};
+
+float f32_param(const ghip_tensor *t, int i) {
+    float f;
+    memcpy(&f, &t->op_params[i], 4);
+    return f;
+}
+
+bool plan_fa(ghip_context *ctx, const ghip_tensor *q, const ghip_tensor *k, const ghip_tensor *v,
+             const ghip_tensor *mask, const ghip_tensor *sinks, const ghip_tensor *d, ghip_status &st) {
+    st = GHIP_STATUS_BACKEND_ERROR;
+    auto bad = [&](const char *why) { st = ctx->fail(GHIP_STATUS_BACKEND_ERROR, "flash_attn_ext: %s", why); return false; };
+    if (!q || !k || !v || !d) return bad("null operand");
+    if (q->type != GHIP_TYPE_F32 || q->nb[0] != 4) return bad("q must be F32 with nb0 == 4 (flash_attn.rs:322)");
+    if (k->type != GHIP_TYPE_F16 || v->type != GHIP_TYPE_F16 || k->nb[0] != 2 || v->nb[0] != 2)
+        return bad("k and v must be F16 rows");
+    if (k->ne[0] != q->ne[0] || v->ne[0] != k->ne[0]) return bad("DK == DV required");
+    if (k->ne[0] != 64 && k->ne[0] != 128) return bad("head size must be 64 or 128");
+    if (q->ne[3] != 1 || k->ne[3] != 1 || v->ne[3] != 1) return bad("4-D batches are not supported");
+    if (k->ne[1] != v->ne[1] || k->ne[2] != v->ne[2]) return bad("k/v shapes differ");
+    if (q->ne[2] % k->ne[2] || q->ne[2] / k->ne[2] > 8) return bad("H % H_kv != 0 or H/H_kv > 8");
+    if (k->nb[1] % 2 || k->nb[2] % 2 || v->nb[1] % 2 || v->nb[2] % 2 || q->nb[1] % 4 || q->nb[2] % 4)
+        return bad("strides must be element multiples");
+    if (mask) {
+        if (mask->type != GHIP_TYPE_F16 || mask->nb[0] != 2) return bad("mask must be F16 rows (ggml.c:5515)");
+        if (mask->ne[0] < k->ne[1] || mask->ne[1] < q->ne[1]) return bad("mask smaller than [S, T]");
+    }
+    if (sinks && (sinks->type != GHIP_TYPE_F32 || sinks->ne[0] < q->ne[2])) return bad("sinks must be F32 [H]");
+    if (d->type != GHIP_TYPE_F32 || d->ne[0] != v->ne[0] || d->ne[1] != q->ne[2] || d->ne[2] != q->ne[1] ||
+        d->nb[0] != 4 || d->nb[1] != (uint64_t)(4 * d->ne[0]) || d->nb[2] != (uint64_t)(4 * d->ne[0] * d->ne[1]))
+        return bad("dst must be contiguous F32 [DV, H, T]");
+    if (q->ne[1] > INT32_MAX || k->ne[1] > INT32_MAX) return bad("dimension too large");
+    st = GHIP_STATUS_SUCCESS;
+    return true;
+}
+
+
+// ------------------------------------------------------------ MUL_MAT_ID
+
+struct MoePlan {
+    int64_t K, rows, n_as, ne11, n_tokens, n_ids, nb;
+    int64_t act_row_bytes;
+};
+
+// forward_mul_mat_id (compute.rs:1917-2202) with MXFP4 experts.
+bool plan_moe(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b, const ghip_tensor *ids,
+              const ghip_tensor *d, MoePlan &p, ghip_status &st) {
+    st = GHIP_STATUS_BACKEND_ERROR;
+    auto bad = [&](const char *why) { st = ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat_id: %s", why); return false; };
+    if (!as || !b || !ids) return bad("null operand");
+    if (as->type != GHIP_TYPE_MXFP4) return bad("experts must be MXFP4");
+    if (as->ne[0] % 32) return bad("ne00 must be a multiple of 32");
+    p.K = as->ne[0];
+    p.rows = as->ne[1];
+    p.n_as = as->ne[2];
+    p.nb = p.K / 32;
+    if (as->ne[3] != 1) return bad("4-D experts are not supported");
+    if (as->nb[0] != 17 || as->nb[1] != (uint64_t)(p.nb * 17) || as->nb[2] < (uint64_t)(p.rows * p.nb * 17))
+        return bad("expert rows must be contiguous blocks");
+    if (b->type != GHIP_TYPE_F32 || b->nb[0] != 4 || b->ne[0] != p.K) return bad("b must be F32 [ne00, ...]");
+    p.ne11 = b->ne[1];
+    p.n_tokens = b->ne[2];
+    if (b->ne[3] != 1 || b->nb[1] % 4 || b->nb[2] != b->nb[1] * (uint64_t)p.ne11)
+        return bad("b must be [ne00, ne11, n_tokens] with rows at a uniform stride");
+    if (ids->type != GHIP_TYPE_I32 || ids->nb[0] != 4 || ids->nb[1] % 4) return bad("ids must be I32 rows");
+    p.n_ids = ids->ne[0];
+    if (ids->ne[1] != p.n_tokens) return bad("ids->ne[1] != b->ne[2]");
+    if (p.ne11 < 1 || p.ne11 > p.n_ids) return bad("need 1 <= ne11 <= n_ids (ggml.c mul_mat_id)");
+    if (p.n_as < 1 || p.n_as > 4096) return bad("n_as out of range");
+    if (p.n_ids * p.n_tokens > (1 << 24) || p.rows > INT32_MAX) return bad("too many (token, slot) pairs");
+    if (d && (d->type != GHIP_TYPE_F32 || d->nb[0] != 4 || d->ne[0] != p.rows || d->ne[1] != p.n_ids ||
+              d->ne[2] != p.n_tokens))
+        return bad("dst must be F32 [rows, n_ids, n_tokens]");
+    p.act_row_bytes = p.nb * 34;
+    st = GHIP_STATUS_SUCCESS;
+    return true;
+}
+
+// Q8_0 activations, routing, then the tiled MFMA kernel; pairs with an
+// invalid expert id get NaN rows (the reference asserts on them).
+ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b, const ghip_tensor *ids,
+                            const ghip_tensor *d, int32_t *sub, void *stream) {
+    if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    MoePlan p;
+    ghip_status st;
+    if (!plan_moe(ctx, as, b, ids, d, p, st)) return st;
+    const int64_t n_pairs = p.n_ids * p.n_tokens;
+    if (n_pairs == 0 || p.rows == 0) return GHIP_STATUS_SUCCESS;
+    hipStream_t s = (hipStream_t)stream;
+    if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    // 32-pair tiles when experts see few pairs each (decode, small batches)
+    const int tp = (n_pairs <= 48 * p.n_as || sub || env_int("GHIP_MOE_TILE", 0) == 32) ? 32 : 64;
+    const int64_t max_tiles = (n_pairs + tp - 1) / tp + p.n_as;
+    const size_t act_bytes = ((size_t)(p.ne11 * p.n_tokens * p.act_row_bytes) + 255) & ~(size_t)255;
+    const size_t route_bytes = (size_t)(2 + n_pairs + 3 * max_tiles) * 4;
+    const size_t out_bytes = d ? 0 : (size_t)(n_pairs * p.rows * 4);
+    void *ws = nullptr;
+    st = ctx->workspace(act_bytes + ((route_bytes + 255) & ~(size_t)255) + out_bytes, s, &ws);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    uint8_t *act = (uint8_t *)ws;
+    int32_t *route = (int32_t *)((uint8_t *)ws + act_bytes);
+    float *dst = d ? (float *)d->data : (float *)((uint8_t *)route + ((route_bytes + 255) & ~(size_t)255));
+    const int64_t dst_nb1 = d ? (int64_t)d->nb[1] / 4 : p.rows;
+    const int64_t dst_nb2 = d ? (int64_t)d->nb[2] / 4 : p.rows * p.n_ids;
+    const int64_t act_rows = p.ne11 * p.n_tokens;
+    const unsigned qgrid = (unsigned)((act_rows * p.nb * 8 + 255) / 256);
+    st = ctx->launch("ghip_quantize_q8_0", dim3(qgrid), dim3(256), 0, s, (const float *)b->data,
+                     (int64_t)b->nb[1] / 4, p.K, act_rows, act, p.act_row_bytes);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    const int64_t ids_nb1 = (int64_t)ids->nb[1] / 4;
+    st = ctx->launch("ghip_moe_route", dim3(1), dim3(1024), (unsigned)(2 * p.n_as * 4), s, (const int32_t *)ids->data,
+                     ids_nb1, (int)p.n_ids, (int)p.n_tokens, (int)p.n_as, route, (int)max_tiles, tp, dst, dst_nb1,
+                     dst_nb2, (int)p.rows);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    const bool repack = p.rows % 8 == 0;  // compute.rs:1965-1972 routes rows % 8 == 0 through the repack kernel
+    std::string name = std::string("ghip_moe_mxfp4_t") + (tp == 32 ? "32" : "64") + (repack ? "" : "_plain") + (sub ? "_sub" : "");
+    const dim3 grid((unsigned)max_tiles, (unsigned)((p.rows + 127) / 128));
+    return ctx->launch(name.c_str(), grid, dim3(256), 0, s, (const uint8_t *)as->data, (int64_t)as->nb[1],
+                       (int64_t)as->nb[2], (const uint8_t *)act, p.act_row_bytes, (int)p.ne11, (const int32_t *)route,
+                       (int)n_pairs, (int)p.n_ids, dst, dst_nb1, dst_nb2, (int)p.rows, (int)p.nb, sub);
 }
 
 }  // namespace
 
 extern "C" {
+
+ghip_status ghip_mul_mat_id(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b, const ghip_tensor *ids,
+                            const ghip_tensor *dst, void *stream) {
+    if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
+    if (!dst) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat_id: null dst");
+    return mul_mat_id_impl(ctx, as, b, ids, dst, nullptr, stream);
+}
+
+ghip_status ghip_mul_mat_id_subsums(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b,
+                                    const ghip_tensor *ids, int32_t *subsums, void *stream) {
+    if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
+    if (!subsums) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat_id_subsums: null output");
+    return mul_mat_id_impl(ctx, as, b, ids, nullptr, subsums, stream);
+}
+
+ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const ghip_tensor *k, const ghip_tensor *v,
+                                const ghip_tensor *mask, const ghip_tensor *sinks, const ghip_tensor *dst,
+                                void *stream) {
+    if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    ghip_status st;
+    if (!plan_fa(ctx, q, k, v, mask, sinks, dst, st)) return st;
+    const int D = (int)k->ne[0], T = (int)q->ne[1], H = (int)q->ne[2], S = (int)k->ne[1], H_kv = (int)k->ne[2];
+    if (T == 0 || H == 0) return GHIP_STATUS_SUCCESS;
+    hipStream_t s = (hipStream_t)stream;
+    if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    // slices of the KV range: enough workgroups to fill the GPU, 64-key multiples
+    const int qtiles = (T + 31) / 32;
+    const int max_split = std::max(1, (S + 63) / 64);
+    int nsplit = std::max(1, std::min(max_split, (env_int("GHIP_FA_WGS", 512) + qtiles * H_kv - 1) / (qtiles * H_kv)));
+    int chunk = ((S + nsplit - 1) / nsplit + 63) / 64 * 64;
+    if (chunk == 0) chunk = 64;
+    nsplit = std::max(1, (S + chunk - 1) / chunk);
+    void *ws = nullptr;
+    const size_t part_bytes = (size_t)T * H * nsplit * (2 + D) * sizeof(float);
+    st = ctx->workspace(part_bytes, s, &ws);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    FaParams p;
+    p.q = (const float *)q->data;
+    p.q_nb1 = (int64_t)q->nb[1] / 4;
+    p.q_nb2 = (int64_t)q->nb[2] / 4;
+    p.k = (const uint16_t *)k->data;
+    p.v = (const uint16_t *)v->data;
+    p.k_nb1 = (int64_t)k->nb[1] / 2;
+    p.k_nb2 = (int64_t)k->nb[2] / 2;
+    p.v_nb1 = (int64_t)v->nb[1] / 2;
+    p.v_nb2 = (int64_t)v->nb[2] / 2;
+    p.mask = mask ? (const uint16_t *)mask->data : nullptr;
+    p.mask_nb1 = mask ? (int64_t)mask->nb[1] / 2 : 0;
+    p.dst = (float *)dst->data;
+    p.part = (float *)ws;
+    p.T = T;
+    p.S = S;
+    p.H = H;
+    p.H_kv = H_kv;
+    p.nsplit = nsplit;
+    p.chunk = chunk;
+    const float scale = f32_param(dst, 0), max_bias = f32_param(dst, 1), softcap = f32_param(dst, 2);
+    // flash_attn.rs:391-413: scale is pre-divided by the softcap; ALiBi slopes
+    p.scale = softcap != 0.0f ? scale / softcap : scale;
+    p.softcap = softcap;
+    p.n_head_log2 = 1 << (int)std::floor(std::log2((double)H));
+    p.m0 = max_bias > 0.0f ? powf(2.0f, -max_bias / (float)p.n_head_log2) : 1.0f;
+    p.m1 = max_bias > 0.0f ? powf(2.0f, -(max_bias / 2.0f) / (float)p.n_head_log2) : 1.0f;
+    p.sinks = sinks ? (const float *)sinks->data : nullptr;
+    // flash_attn.rs:371-386 routes: single-row decode over >= 512 keys splits the
+    // KV range, >= 64 query rows take the tiled kernel (fp32 accumulators) --
+    // both run on the MFMA kernel below.  Fewer rows take the one-chunk walk
+    // with its f16 accumulator, reproduced by the row-sequential kernel.
+    if (!(T == 1 && S >= 512) && T < 64 && !env_int("GHIP_FA_FORCE_MFMA", 0)) {
+        const char *rs = D == 128 ? "ghip_fa_rowseq_d128" : "ghip_fa_rowseq_d64";
+        return ctx->launch(rs, dim3((unsigned)((T * H + 3) / 4)), dim3(256), 0, s, p);
+    }
+    const char *fwd = D == 128 ? "ghip_fa_fwd_d128" : "ghip_fa_fwd_d64";
+    st = ctx->launch(fwd, dim3(qtiles, H_kv, nsplit), dim3(64 * (H / H_kv)), 0, s, p);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    const float *sk = sinks ? (const float *)sinks->data : nullptr;
+    return ctx->launch("ghip_fa_merge", dim3((unsigned)((T * H + 3) / 4)), dim3(256), 0, s, (const float *)ws, sk,
+                       (float *)dst->data, T, H, nsplit, D);
+}
+
 
 ghip_status ghip_init(int device, ghip_context **out) {
     if (!out) return GHIP_STATUS_BACKEND_ERROR;
@@ -347,6 +590,20 @@ int ghip_supports_op(int op, const ghip_tensor *dst, const ghip_tensor *const *s
         MulMatPlan p;
         ghip_status st;
         return plan_mul_mat(&tmp, srcs[0], srcs[1], dst, p, st) ? 1 : 0;
+    }
+    if (op == GHIP_OP_MUL_MAT_ID) {
+        if (n_srcs < 3 || !srcs[0] || !srcs[1] || !srcs[2]) return 0;
+        ghip_context tmp;
+        MoePlan p;
+        ghip_status st;
+        return plan_moe(&tmp, srcs[0], srcs[1], srcs[2], dst, p, st) ? 1 : 0;
+    }
+    if (op == GHIP_OP_FLASH_ATTN_EXT) {
+        if (n_srcs < 3 || !dst) return 0;
+        ghip_context tmp;
+        ghip_status st;
+        return plan_fa(&tmp, srcs[0], srcs[1], srcs[2], n_srcs > 3 ? srcs[3] : nullptr,
+                       n_srcs > 4 ? srcs[4] : nullptr, dst, st) ? 1 : 0;
     }
     return 0;
 }

@@ -1,0 +1,354 @@
+// ghip_fa.hip -- GGML_OP_FLASH_ATTN_EXT with f16 K/V on the f16 matrix cores
+// (v_mfma_f32_32x32x16_f16), online softmax in fp32.
+//
+// Semantics (flash_attn.rs:273-386, compute.rs:4563-4625): for query row t of
+// head h,  s_k = scale * q.k  (softcap: s = softcap * tanh(s), scale being
+// pre-divided by softcap), s_k += slope_h * mask[t][k]; out = softmax(s) V,
+// rows whose keys are all masked give 0; sinks enter the softmax denominator
+// as one extra logit per head.
+//
+// Work layout.  A workgroup owns one KV head hk, 32 query positions and one
+// slice of the KV range; its G wavefronts are the G = H / H_kv query heads
+// that share hk (GQA), so every K/V tile staged in LDS serves G heads.  Per
+// 64-key tile each wavefront computes S^T = K Q^T (keys x queries), which
+// leaves all scores of one query in one lane pair (l, l^32): the row max and
+// row sum need one cross-lane exchange.  O^T += V^T P^T accumulates in 4 x 16
+// fp32 registers per lane (DV = 128).  The KV range is split over
+// workgroups (grid.z) so decode (1 query) and prefill both fill the GPU; the
+// per-slice (M, S, O) partials are merged in slice order by ghip_fa_merge,
+// exactly the reference's reduce_partials arithmetic shape (flash_attn.rs:779).
+#include "ghip_common.h"
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int FA_BQ = 32;   // query positions per workgroup
+constexpr int FA_BK = 64;   // keys per tile
+constexpr int FA_KPAD = 8;  // LDS row padding (halfs)
+
+DEV int crow32(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
+
+struct FaParams {
+    const float *q;
+    int64_t q_nb1, q_nb2;  // floats
+    const uint16_t *k, *v;
+    int64_t k_nb1, k_nb2, v_nb1, v_nb2;  // halfs
+    const uint16_t *mask;
+    int64_t mask_nb1;  // halfs
+    float *dst;        // [T][H][DV]
+    float *part;       // [(t*H + h)*nsplit + z][2 + DV]
+    const float *sinks;  // [H] or null
+    int T, S, H, H_kv, nsplit, chunk;
+    float scale, softcap, m0, m1;
+    int n_head_log2;
+};
+
+DEV float head_slope(const FaParams &p, int h) {
+    if (p.m0 == 1.0f && p.m1 == 1.0f) return 1.0f;
+    // max_bias > 0: m0^(h+1) for h < n_head_log2 else m1^(2(h-n)+1)
+    const float base = h < p.n_head_log2 ? p.m0 : p.m1;
+    int e = h < p.n_head_log2 ? h + 1 : 2 * (h - p.n_head_log2) + 1;
+    float r = 1.0f, a = base;
+    while (e) {
+        if (e & 1) r *= a;
+        e >>= 1;
+        if (e) a *= a;
+    }
+    return r;
+}
+
+template <int D>
+__device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[FA_BK * (D + FA_KPAD)];   // [key][d]
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[D * (FA_BK + FA_KPAD)];   // [d][key]
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, G = blockDim.x >> 6;
+    const int nthr = blockDim.x;
+    const int qt = blockIdx.x, hk = blockIdx.y, z = blockIdx.z;
+    const int h = hk * G + w;
+    const int li = lane & 31, h2 = lane >> 5;
+    const int t = qt * FA_BQ + li;  // this lane's query position
+    const bool tvalid = t < p.T;
+    const float slope = head_slope(p, h);
+
+    // Q fragment (B operand of S^T = K Q^T): d = 16*kk + 8*h2 + 0..7
+    v8h qf[D / 16];
+    {
+        const float *qr = p.q + (int64_t)h * p.q_nb2 + (int64_t)(tvalid ? t : 0) * p.q_nb1;
+#pragma unroll
+        for (int kk = 0; kk < D / 16; kk++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) qf[kk][e] = tvalid ? (_Float16)qr[16 * kk + 8 * h2 + e] : (_Float16)0.0f;
+    }
+    v16f o[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) o[dt][v] = 0.0f;
+    float m_run = -__builtin_inff(), l_run = 0.0f;
+
+    const int kb = z * p.chunk;
+    const int ke = min(p.S, kb + p.chunk);
+    const uint16_t *kbase = p.k + (int64_t)hk * p.k_nb2;
+    const uint16_t *vbase = p.v + (int64_t)hk * p.v_nb2;
+
+    for (int k0 = kb; k0 < ke; k0 += FA_BK) {
+        const int nk = min(FA_BK, ke - k0);
+        __syncthreads();  // the previous tile is consumed
+        // K tile -> Ks[key][d]; V tile -> Vt[d][key] (zero past the range)
+        for (int c = threadIdx.x; c < FA_BK * (D / 8); c += nthr) {
+            const int key = c / (D / 8), d8 = (c % (D / 8)) * 8;
+            uint4 kv = make_uint4(0, 0, 0, 0), vv = kv;
+            if (key < nk) {
+                kv = ld16((const uint8_t *)(kbase + (int64_t)(k0 + key) * p.k_nb1 + d8));
+                vv = ld16((const uint8_t *)(vbase + (int64_t)(k0 + key) * p.v_nb1 + d8));
+            }
+            *reinterpret_cast<uint4 *>(&Ks[key * (D + FA_KPAD) + d8]) = kv;
+            const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                Vt[(d8 + 2 * e) * (FA_BK + FA_KPAD) + key] = __builtin_bit_cast(_Float16, (uint16_t)(vw[e] & 0xffff));
+                Vt[(d8 + 2 * e + 1) * (FA_BK + FA_KPAD) + key] = __builtin_bit_cast(_Float16, (uint16_t)(vw[e] >> 16));
+            }
+        }
+        __syncthreads();
+
+        // scores of this lane: keys 32*jt + crow32(v), query t
+        float s[2][16];
+#pragma unroll
+        for (int jt = 0; jt < 2; jt++) {
+            v16f acc;
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[v] = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < D / 16; kk++) {
+                const v8h a = *reinterpret_cast<const v8h *>(&Ks[(32 * jt + li) * (D + FA_KPAD) + 16 * kk + 8 * h2]);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[kk], acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int key = 32 * jt + crow32(v, lane);
+                float x = acc[v] * p.scale;
+                if (p.softcap != 0.0f) x = p.softcap * tanhf(x);
+                if (p.mask && tvalid && key < nk) x += slope * h2f(p.mask[(int64_t)t * p.mask_nb1 + k0 + key]);
+                if (key >= nk || !tvalid) x = -__builtin_inff();
+                s[jt][v] = x;
+            }
+        }
+        // online softmax for query t (lanes l and l^32 share it)
+        float tmax = -__builtin_inff();
+#pragma unroll
+        for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) tmax = fmaxf(tmax, s[jt][v]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float m_new = fmaxf(m_run, tmax);
+        float alpha = 1.0f;
+        if (m_new == -__builtin_inff()) {
+            // every key so far is masked for this query: nothing accumulates
+#pragma unroll
+            for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) s[jt][v] = 0.0f;
+        } else {
+            alpha = __expf(m_run - m_new);  // 0 when m_run is -inf
+            float psum = 0.0f;
+#pragma unroll
+            for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const float e = __expf(s[jt][v] - m_new);
+                    s[jt][v] = e;
+                    psum += e;
+                }
+            psum += __shfl_xor(psum, 32, 64);
+            l_run = l_run * alpha + psum;
+            m_run = m_new;
+        }
+#pragma unroll
+        for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) o[dt][v] *= alpha;
+        // O^T += V^T P^T over the 64 keys: 4 MFMAs of 16 keys per d-tile
+#pragma unroll
+        for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                v8h pb;
+#pragma unroll
+                for (int e = 0; e < 8; e++) pb[e] = (_Float16)s[jt][8 * m + e];
+                // slot e <-> key 32*jt + 4*h2 + 8*(2m + e/4) + e%4 (matches the C layout of s)
+                const int key0 = 32 * jt + 4 * h2 + 16 * m;
+#pragma unroll
+                for (int dt = 0; dt < D / 32; dt++) {
+                    const int d = 32 * dt + li;
+                    const v4h lo = *reinterpret_cast<const v4h *>(&Vt[d * (FA_BK + FA_KPAD) + key0]);
+                    const v4h hi = *reinterpret_cast<const v4h *>(&Vt[d * (FA_BK + FA_KPAD) + key0 + 8]);
+                    v8h a;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) { a[e] = lo[e]; a[4 + e] = hi[e]; }
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[dt], 0, 0, 0);
+                }
+            }
+    }
+
+    // write this slice's partial (M, S, unnormalized O) for query t, head h;
+    // lanes l and l^32 hold complementary d ranges of the same query
+    if (tvalid) {
+        float *pp = p.part + (((int64_t)t * p.H + h) * p.nsplit + z) * (2 + D);
+        if (h2 == 0) {
+            pp[0] = m_run;
+            pp[1] = l_run;
+        }
+#pragma unroll
+        for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) pp[2 + 32 * dt + crow32(v, lane)] = o[dt][v];
+    }
+}
+
+// Merge the per-slice partials of one (query, head) row in slice order
+// (reduce_partials, flash_attn.rs:779-835), add the sink logit, normalize.
+// One wavefront per row; lanes own output columns.
+extern "C" __global__ void __launch_bounds__(256)
+ghip_fa_merge(const float *__restrict__ part, const float *__restrict__ sinks, float *__restrict__ dst, int T,
+              int H, int nsplit, int DV) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= T * H) return;
+    const int h = row % H;
+    const float *pr = part + (int64_t)row * nsplit * (2 + DV);
+    float M = -__builtin_inff(), S = 0.0f;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // DV <= 256
+    for (int z = 0; z < nsplit; z++) {
+        const float *pz = pr + (int64_t)z * (2 + DV);
+        const float mz = pz[0], sz = pz[1];
+        if (sz == 0.0f) continue;
+        const float mn = fmaxf(M, mz);
+        const float so = __expf(M - mn), sn = __expf(mz - mn);
+        for (int i = 0; i < 4; i++) {
+            const int d = lane + 64 * i;
+            if (d < DV) acc[i] = acc[i] * so + pz[2 + d] * sn;
+        }
+        S = S * so + sz * sn;
+        M = mn;
+    }
+    if (sinks) {
+        const float sv = sinks[h];
+        if (sv > M) {
+            const float ms = __expf(M - sv);
+            for (int i = 0; i < 4; i++) acc[i] *= ms;
+            S = S * ms + 1.0f;
+        } else {
+            S = S + __expf(sv - M);
+        }
+    }
+    const float sinv = S == 0.0f ? 0.0f : 1.0f / S;
+    for (int i = 0; i < 4; i++) {
+        const int d = lane + 64 * i;
+        if (d < DV) dst[(int64_t)row * DV + d] = acc[i] * sinv;
+    }
+}
+
+// Few-row route (one query chunk, flash_attn.rs:482-703): the reference walks
+// the keys of one (query, head) row in order and keeps the unnormalized V
+// accumulator in f16, rounding after every rescale and every multiply-add.
+// That rounding is part of the reference's result (it moves outputs by up to
+// a few 1e-3 at S ~ 1000), so this route reproduces the walk: one wavefront
+// per row, lane j scores key k0 + j of each 64-key tile (q rounded to f16,
+// fp32 dot), then the wavefront steps through the tile's keys in order, each
+// lane updating its D/64 accumulator elements with the reference's
+// operations -- skip masked (-inf) keys, new max => rescale by exp(Mold - M)
+// and round, then acc = f16(fma(v, vs, acc)), S = fma(S, ms, vs).
+template <int D>
+__device__ __forceinline__ void fa_rowseq_impl(const FaParams &p) {
+    constexpr int PL = D / 64;  // accumulator elements per lane
+    __shared__ float qs[4][D];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int row = blockIdx.x * 4 + w;  // row = t * H + h
+    const bool valid = row < p.T * p.H;
+    const int t = valid ? row / p.H : 0, h = valid ? row % p.H : 0;
+    const int hk = h / (p.H / p.H_kv);
+    const float slope = head_slope(p, h);
+    const float *qr = p.q + (int64_t)h * p.q_nb2 + (int64_t)t * p.q_nb1;
+    for (int d = lane; d < D; d += 64) qs[w][d] = h2f(f2h_rn(qr[d]));
+    __syncthreads();
+    if (!valid) return;
+    const uint16_t *kbase = p.k + (int64_t)hk * p.k_nb2;
+    const uint16_t *vbase = p.v + (int64_t)hk * p.v_nb2;
+    float acc[PL];
+#pragma unroll
+    for (int i = 0; i < PL; i++) acc[i] = 0.0f;
+    float M = -__builtin_inff(), S = 0.0f;
+    for (int k0 = 0; k0 < p.S; k0 += 64) {
+        const int key = k0 + lane;
+        float s = -__builtin_inff();
+        bool live = false;
+        if (key < p.S) {
+            const float mv = p.mask ? slope * h2f(p.mask[(int64_t)t * p.mask_nb1 + key]) : 0.0f;
+            if (mv != -__builtin_inff()) {
+                live = true;
+                const uint8_t *kr = (const uint8_t *)(kbase + (int64_t)key * p.k_nb1);
+                float dot = 0.0f;
+#pragma unroll 4
+                for (int d8 = 0; d8 < D; d8 += 8) {
+                    const uint4 kv = ld16(kr + 2 * d8);
+                    const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        dot = fmaf(h2f(kw[e] & 0xffff), qs[w][d8 + 2 * e], dot);
+                        dot = fmaf(h2f(kw[e] >> 16), qs[w][d8 + 2 * e + 1], dot);
+                    }
+                }
+                s = dot * p.scale;
+                if (p.softcap != 0.0f) s = p.softcap * tanhf(s);
+                s += mv;
+            }
+        }
+        const uint64_t livemask = __ballot(live);
+        const int nk = min(64, p.S - k0);
+        for (int j = 0; j < nk; j++) {
+            if (!((livemask >> j) & 1)) continue;
+            const float sj = __shfl(s, j, 64);
+            const uint16_t *vr = vbase + (int64_t)(k0 + j) * p.v_nb1 + PL * lane;
+            float vv[PL];
+#pragma unroll
+            for (int i = 0; i < PL; i++) vv[i] = h2f(vr[i]);
+            float ms = 1.0f, vs = 1.0f;
+            if (sj > M) {
+                const float Mold = M;
+                M = sj;
+                ms = expf(Mold - M);
+#pragma unroll
+                for (int i = 0; i < PL; i++) acc[i] = h2f(f2h_rn(acc[i] * ms));
+            } else {
+                vs = expf(sj - M);
+            }
+#pragma unroll
+            for (int i = 0; i < PL; i++) acc[i] = h2f(f2h_rn(fmaf(vv[i], vs, acc[i])));
+            S = fmaf(S, ms, vs);
+        }
+    }
+    if (p.sinks) {
+        const float sh = p.sinks[h];
+        float ms = 1.0f, vs = 1.0f;
+        if (sh > M) {
+            ms = expf(M - sh);
+            M = sh;
+#pragma unroll
+            for (int i = 0; i < PL; i++) acc[i] *= ms;
+        } else {
+            vs = expf(sh - M);
+        }
+        S = opaque(S * ms) + vs;  // unfused, as the reference
+    }
+    const float sinv = S == 0.0f ? 0.0f : 1.0f / S;
+    float *o = p.dst + (int64_t)row * D + PL * lane;
+#pragma unroll
+    for (int i = 0; i < PL; i++) o[i] = acc[i] * sinv;
+}
+
+extern "C" __global__ void __launch_bounds__(512) ghip_fa_fwd_d128(FaParams p) { fa_fwd_impl<128>(p); }
+extern "C" __global__ void __launch_bounds__(512) ghip_fa_fwd_d64(FaParams p) { fa_fwd_impl<64>(p); }
+extern "C" __global__ void __launch_bounds__(256) ghip_fa_rowseq_d128(FaParams p) { fa_rowseq_impl<128>(p); }
+extern "C" __global__ void __launch_bounds__(256) ghip_fa_rowseq_d64(FaParams p) { fa_rowseq_impl<64>(p); }

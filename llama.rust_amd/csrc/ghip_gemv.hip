@@ -42,81 +42,215 @@ DEV void finish_rows(const float *red, int r0, int nrows, int ncols, int NC, int
 }
 
 // ---------------------------------------------------------------- Q4_K x Q8_K
-template <int NC, bool SUBSUMS>
+// Activation codes of one lane: the 32 elements 64g+16h+[0,16) (low stream)
+// and 64g+32+16h+[0,16) (high stream) of super-block b, the pair sum of
+// subblock j for the min term, and the block scale.
+struct Q4KAct {
+    uint4 lo, hi;
+    int bp;
+    float d;
+};
+
+// Quantize this lane's share of activation row xr (f32) to Q8_K inside the
+// kernel, bit-identical to ghip_quantize_q8_K: the 8 lanes of a super-block
+// reduce its signed max-abs (first occurrence wins), then each lane codes its
+// 32 elements.  mat selects the quantize_mat_q8_K_4x8 values.
+struct XLane {
+    float l[16], h[16];
+};
+
+DEV XLane load_x_lane(const float *__restrict__ xr, int b, int g, int h, bool valid) {
+    XLane x;
+    if (valid) {
+        __builtin_memcpy(x.l, xr + (int64_t)b * QK_K + 64 * g + 16 * h, 64);
+        __builtin_memcpy(x.h, xr + (int64_t)b * QK_K + 64 * g + 32 + 16 * h, 64);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) x.l[i] = x.h[i] = 0.0f;
+    }
+    return x;
+}
+
+DEV Q4KAct quant_q8K_lane(const XLane &x, int g, int h, int j, bool mat) {
+    const float *xl = x.l, *xh = x.h;
+    // element index inside the block, for the first-occurrence tie break
+    const int base_l = 64 * g + 16 * h, base_h = base_l + 32;
+    float bax = 0.0f, bval = 0.0f;
+    int bidx = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float a = fabsf(xl[i]);
+        if (a > bax) { bax = a; bval = xl[i]; bidx = base_l + i; }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float a = fabsf(xh[i]);
+        if (a > bax || (a == bax && a > 0.0f && base_h + i < bidx)) { bax = a; bval = xh[i]; bidx = base_h + i; }
+    }
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {
+        const float oax = __shfl_xor(bax, o, 64);
+        const float oval = __shfl_xor(bval, o, 64);
+        const int oidx = __shfl_xor(bidx, o, 64);
+        if (oax > bax || (oax == bax && oidx < bidx)) { bax = oax; bval = oval; bidx = oidx; }
+    }
+    Q4KAct r;
+    int ql[16], qh[16];
+    if (bax == 0.0f) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) ql[i] = qh[i] = 0;
+        r.d = 0.0f;
+    } else if (!mat) {
+        const float iscale = __fdiv_rn(-127.0f, bval);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            ql[i] = min(127, (int)rintf(__fmul_rn(iscale, xl[i])));
+            qh[i] = min(127, (int)rintf(__fmul_rn(iscale, xh[i])));
+        }
+        r.d = __fdiv_rn(1.0f, iscale);
+    } else {
+        const float iscale = __fdiv_rn(127.0f, bax);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            ql[i] = (int)fminf(fmaxf(rintf(__fmul_rn(iscale, xl[i])), -128.0f), 127.0f);
+            qh[i] = (int)fminf(fmaxf(rintf(__fmul_rn(iscale, xh[i])), -128.0f), 127.0f);
+        }
+        r.d = __fdiv_rn(1.0f, iscale);
+    }
+    uint32_t pl[4], ph[4];
+    int sl = 0, sh = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        pl[k] = (uint32_t)(ql[4 * k] & 0xff) | ((uint32_t)(ql[4 * k + 1] & 0xff) << 8) |
+                ((uint32_t)(ql[4 * k + 2] & 0xff) << 16) | ((uint32_t)(ql[4 * k + 3] & 0xff) << 24);
+        ph[k] = (uint32_t)(qh[4 * k] & 0xff) | ((uint32_t)(qh[4 * k + 1] & 0xff) << 8) |
+                ((uint32_t)(qh[4 * k + 2] & 0xff) << 16) | ((uint32_t)(qh[4 * k + 3] & 0xff) << 24);
+        sl += ql[4 * k] + ql[4 * k + 1] + ql[4 * k + 2] + ql[4 * k + 3];
+        sh += qh[4 * k] + qh[4 * k + 1] + qh[4 * k + 2] + qh[4 * k + 3];
+    }
+    r.lo = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+    r.hi = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+    // subblock j = 2g' collects the low streams of lanes 2g', 2g'+1; 2g'+1 their high streams
+    const int ol = __shfl_xor(sl, 1, 64), oh = __shfl_xor(sh, 1, 64);
+    r.bp = (j & 1) ? (sh + oh) : (sl + ol);
+    return r;
+}
+
+DEV Q4KAct load_q8K_lane(const uint8_t *__restrict__ A, int g, int h, int j) {
+    Q4KAct r;
+    r.lo = ld16(A + 4 + 64 * g + 16 * h);
+    r.hi = ld16(A + 4 + 64 * g + 32 + 16 * h);
+    const uint32_t bs = ld4(A + 260 + 4 * j);
+    r.bp = (int)(int16_t)(bs & 0xffff) + (int)(int16_t)(bs >> 16);
+    r.d = __uint_as_float(ld4(A));
+    return r;
+}
+
+// One launch per MUL_MAT: FUSEQ kernels read the f32 activations and quantize
+// them in registers; the others read ready Q8_K rows.  Each workgroup walks
+// rows_per_wg rows in groups of RB, loading group i+1 while computing group i.
+template <int NC, bool SUBSUMS, bool FUSEQ>
 __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
                                               int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
                                               int ncols, float *__restrict__ dst, int64_t ldd,
-                                              int32_t *__restrict__ sub) {
-    __shared__ float red[RB * 8 * NC];  // [row][wave][col], at most 8 waves
+                                              int32_t *__restrict__ sub, int rows_per_wg, int n_mat) {
+    extern __shared__ float red[];  // [rows_per_wg][W_K][NC]
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int b = 8 * w + (lane >> 3), j = lane & 7, g = j >> 1, h = j & 1;
     const bool valid = b < nb;
-    const int r0 = blockIdx.x * RB;
-    const int nr = min(RB, rows - r0);
+    const int r0 = blockIdx.x * rows_per_wg;
+    const int r1 = min(rows, r0 + rows_per_wg);
+    const uint8_t *wb = W + (int64_t)b * Q4K_BYTES;
 
-    // weight loads first: RB rows x (header + one 16-byte qs chunk)
+    // Branch-free weight loads: rows past the tile and lanes past the row
+    // re-read a valid block (clamped index) and contribute zero (their
+    // activation codes and scale are zero).
+    const uint8_t *wbc = W + (int64_t)min(b, nb - 1) * Q4K_BYTES;
     uint4 hdr[RB], q[RB];
-    const uint8_t *wb = W + (int64_t)r0 * w_row_bytes + (int64_t)b * Q4K_BYTES;
+    auto load_group = [&](int rg, uint4 *hd, uint4 *qq) {
 #pragma unroll
-    for (int rr = 0; rr < RB; rr++) {
-        if (valid && rr < nr) {
-            hdr[rr] = ld16(wb + rr * w_row_bytes);
-            q[rr] = ld16(wb + rr * w_row_bytes + 16 + 16 * j);
-        } else {
-            hdr[rr] = q[rr] = make_uint4(0, 0, 0, 0);
+        for (int rr = 0; rr < RB; rr++) {
+            const uint8_t *p = wbc + (int64_t)min(rg + rr, r1 - 1) * w_row_bytes;
+            hd[rr] = ld16(p);
+            qq[rr] = ld16(p + 16 + 16 * j);
         }
-    }
-    uint4 alo[NC], ahi[NC];
-    int bp[NC];
-    float da[NC];
+    };
+    // Order of issue: the f32 activations of up to two columns, then the first
+    // weight group, then the activation quantization -- which waits on the
+    // activation loads only, with the weight loads still in flight.
+    constexpr int NX = FUSEQ ? (NC < 2 ? NC : 2) : 0;
+    XLane xs[NX > 0 ? NX : 1];
+#pragma unroll
+    for (int c = 0; c < NX; c++)
+        xs[c] = load_x_lane(reinterpret_cast<const float *>(act + c * act_row_bytes), b, g, h,
+                            valid && c < ncols);
+    load_group(r0, hdr, q);
+    Q4KAct a[NC];
 #pragma unroll
     for (int c = 0; c < NC; c++) {
-        if (valid && c < ncols) {
-            const uint8_t *A = act + c * act_row_bytes + (int64_t)b * Q8K_BYTES;
-            alo[c] = ld16(A + 4 + 64 * g + 16 * h);
-            ahi[c] = ld16(A + 4 + 64 * g + 32 + 16 * h);
-            const uint32_t bs = ld4(A + 260 + 4 * j);
-            bp[c] = (int)(int16_t)(bs & 0xffff) + (int)(int16_t)(bs >> 16);
-            da[c] = __uint_as_float(ld4(A));
+        if (c < ncols) {
+            if (FUSEQ) {
+                const XLane xv = c < NX ? xs[c]
+                                        : load_x_lane(reinterpret_cast<const float *>(act + c * act_row_bytes), b,
+                                                      g, h, valid);
+                a[c] = quant_q8K_lane(xv, g, h, j, c < n_mat);
+            } else if (valid) {
+                a[c] = load_q8K_lane(act + c * act_row_bytes + (int64_t)b * Q8K_BYTES, g, h, j);
+            } else {
+                a[c] = Q4KAct{make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), 0, 0.0f};
+            }
         } else {
-            alo[c] = ahi[c] = make_uint4(0, 0, 0, 0);
-            bp[c] = 0;
-            da[c] = 0.0f;
+            a[c] = Q4KAct{make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), 0, 0.0f};
         }
     }
 
-    float part[NC][RB];
+    auto compute_group = [&](int rg, const uint4 *hdr_, const uint4 *q_) {
+        float part[NC][RB];
 #pragma unroll
-    for (int rr = 0; rr < RB; rr++) {
-        const uint4 hd = hdr[rr], qq = q[rr];
-        const float dw = h2f(hd.x), dmin = h2f(hd.x >> 16);
-        int slo, shi, mj, mdummy, sdummy;
-        scale_min_k4(hd.y, hd.z, hd.w, 2 * g, slo, mdummy);
-        scale_min_k4(hd.y, hd.z, hd.w, 2 * g + 1, shi, mdummy);
-        scale_min_k4(hd.y, hd.z, hd.w, j, sdummy, mj);
-        const uint32_t l0 = qq.x & 0x0f0f0f0f, l1 = qq.y & 0x0f0f0f0f, l2 = qq.z & 0x0f0f0f0f, l3 = qq.w & 0x0f0f0f0f;
-        const uint32_t h0 = (qq.x >> 4) & 0x0f0f0f0f, h1 = (qq.y >> 4) & 0x0f0f0f0f;
-        const uint32_t h2 = (qq.z >> 4) & 0x0f0f0f0f, h3 = (qq.w >> 4) & 0x0f0f0f0f;
+        for (int rr = 0; rr < RB; rr++) {
+            const uint4 hd = hdr_[rr], qq = q_[rr];
+            const float dw = h2f(hd.x), dmin = h2f(hd.x >> 16);
+            int slo, shi, mj, mdummy, sdummy;
+            scale_min_k4(hd.y, hd.z, hd.w, 2 * g, slo, mdummy);
+            scale_min_k4(hd.y, hd.z, hd.w, 2 * g + 1, shi, mdummy);
+            scale_min_k4(hd.y, hd.z, hd.w, j, sdummy, mj);
+            const uint32_t l0 = qq.x & 0x0f0f0f0f, l1 = qq.y & 0x0f0f0f0f, l2 = qq.z & 0x0f0f0f0f, l3 = qq.w & 0x0f0f0f0f;
+            const uint32_t h0 = (qq.x >> 4) & 0x0f0f0f0f, h1 = (qq.y >> 4) & 0x0f0f0f0f;
+            const uint32_t h2 = (qq.z >> 4) & 0x0f0f0f0f, h3 = (qq.w >> 4) & 0x0f0f0f0f;
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                const int dl = dot4(l3, a[c].lo.w, dot4(l2, a[c].lo.z, dot4(l1, a[c].lo.y, dot4(l0, a[c].lo.x, 0))));
+                const int dh = dot4(h3, a[c].hi.w, dot4(h2, a[c].hi.z, dot4(h1, a[c].hi.y, dot4(h0, a[c].hi.x, 0))));
+                const int ia = slo * dl + shi * dh;
+                const int im = mj * a[c].bp;
+                if (SUBSUMS) {
+                    const int iab = group8_sum(ia), imb = group8_sum(im);
+                    if (j == 0 && valid && c < ncols && rg + rr < r1) {
+                        int32_t *s = sub + (((int64_t)c * rows + rg + rr) * nb + b) * 2;
+                        s[0] = iab;
+                        s[1] = imb;
+                    }
+                }
+                part[c][rr] = a[c].d * fmaf(dw, (float)ia, -(dmin * (float)im));
+            }
+        }
 #pragma unroll
         for (int c = 0; c < NC; c++) {
-            const int dl = dot4(l3, alo[c].w, dot4(l2, alo[c].z, dot4(l1, alo[c].y, dot4(l0, alo[c].x, 0))));
-            const int dh = dot4(h3, ahi[c].w, dot4(h2, ahi[c].z, dot4(h1, ahi[c].y, dot4(h0, ahi[c].x, 0))));
-            const int ia = slo * dl + shi * dh;
-            const int im = mj * bp[c];
-            if (SUBSUMS) {
-                const int iab = group8_sum(ia), imb = group8_sum(im);
-                if (j == 0 && valid && c < ncols && rr < nr) {
-                    int32_t *s = sub + (((int64_t)c * rows + r0 + rr) * nb + b) * 2;
-                    s[0] = iab;
-                    s[1] = imb;
-                }
-            }
-            part[c][rr] = da[c] * fmaf(dw, (float)ia, -(dmin * (float)im));
+            const float t = reduce8_rows(part[c], lane);
+            if ((lane & 7) == 0 && rg + (lane >> 3) < r1) red[((rg - r0 + (lane >> 3)) * nw + w) * NC + c] = t;
         }
+    };
+    // Ping-pong over two register buffers (no copies, so the next group's
+    // loads stay in flight while this group is computed).
+    uint4 hdr2[RB], q2[RB];
+    for (int rg = r0; rg < r1; rg += 2 * RB) {
+        if (rg + RB < r1) load_group(rg + RB, hdr2, q2);
+        compute_group(rg, hdr, q);
+        if (rg + RB >= r1) break;
+        if (rg + 2 * RB < r1) load_group(rg + 2 * RB, hdr, q);
+        compute_group(rg + RB, hdr2, q2);
     }
-#pragma unroll
-    for (int c = 0; c < NC; c++) stash_rows(red, part[c], lane, w, nw, c, NC);
-    finish_rows(red, r0, nr, ncols, NC, nw, dst, ldd);
+    finish_rows(red, r0, r1 - r0, ncols, NC, nw, dst, ldd);
 }
 
 // ---------------------------------------------------------------- Q6_K x Q8_K
@@ -315,6 +449,24 @@ __device__ __forceinline__ void gemv_q4_0_impl(const uint8_t *__restrict__ W, in
 #define GEMV_ALL(name, impl) \
     GEMV_INST(name, impl, 1) GEMV_INST(name, impl, 2) GEMV_INST(name, impl, 4) GEMV_INST(name, impl, 8)
 
-GEMV_ALL(ghip_gemv_q4_K, gemv_q4K_impl)
 GEMV_ALL(ghip_gemv_q6_K, gemv_q6K_impl)
 GEMV_ALL(ghip_gemv_q4_0, gemv_q4_0_impl)
+
+// Q4_K: "_f" kernels take f32 activations (fused Q8_K quantization), the
+// others ready Q8_K rows; "_sub" kernels also store the integer partials.
+#define Q4K_ARGS GEMV_ARGS, int rows_per_wg, int n_mat
+#define Q4K_PASS GEMV_PASS, rows_per_wg, n_mat
+#define Q4K_INST(NC)                                                                                              \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_c##NC(Q4K_ARGS) {                           \
+        gemv_q4K_impl<NC, false, false>(Q4K_PASS);                                                              \
+    }                                                                                                           \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_sub_c##NC(Q4K_ARGS) {                       \
+        gemv_q4K_impl<NC, true, false>(Q4K_PASS);                                                               \
+    }                                                                                                           \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_f_c##NC(Q4K_ARGS) {                         \
+        gemv_q4K_impl<NC, false, true>(Q4K_PASS);                                                               \
+    }                                                                                                           \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_f_sub_c##NC(Q4K_ARGS) {                     \
+        gemv_q4K_impl<NC, true, true>(Q4K_PASS);                                                                \
+    }
+Q4K_INST(1) Q4K_INST(2) Q4K_INST(4) Q4K_INST(8)

@@ -39,6 +39,8 @@ def describe(t, ty, ne0=None):
     packed rows in its last dim and ne0 gives the logical row length."""
     d = Tensor()
     d.type = ty
+    if t is None:
+        return None
     if ty in (F32, F16, I32):
         shape = list(t.shape)[::-1] + [1] * (4 - t.dim())
         nb = [s * t.element_size() for s in t.stride()][::-1]
@@ -86,6 +88,12 @@ def lib():
         L.ghip_quantize_chunk.restype = C.c_int
         L.ghip_quantize_chunk.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64,
                                           C.c_void_p]
+        L.ghip_mul_mat_id.restype = C.c_int
+        L.ghip_mul_mat_id.argtypes = [C.c_void_p, P, P, P, P, C.c_void_p]
+        L.ghip_mul_mat_id_subsums.restype = C.c_int
+        L.ghip_mul_mat_id_subsums.argtypes = [C.c_void_p, P, P, P, C.c_void_p, C.c_void_p]
+        L.ghip_flash_attn_ext.restype = C.c_int
+        L.ghip_flash_attn_ext.argtypes = [C.c_void_p, P, P, P, P, P, P, C.c_void_p]
         _lib = L
     return _lib
 
@@ -165,6 +173,42 @@ class Backend:
         out = torch.empty((rows, row_size(ty, n)), dtype=torch.uint8, device=x.device)
         self._check(lib().ghip_quantize_chunk(self._ctx, ty, C.c_void_p(x.data_ptr()), C.c_void_p(out.data_ptr()),
                                               rows, n, _stream()), "ghip_quantize_chunk")
+        return out
+
+    # ---- MUL_MAT_ID
+    def mul_mat_id(self, experts, k, b, ids, out=None):
+        """experts [n_as, rows, row_bytes] MXFP4, b [n_tokens, ne11, K] f32,
+        ids [n_tokens, n_ids] int32 -> out [n_tokens, n_ids, rows] f32."""
+        n_tokens, n_ids = ids.shape
+        if out is None:
+            out = torch.empty((n_tokens, n_ids, experts.shape[1]), dtype=torch.float32, device=b.device)
+        a, tb, ti, d = describe(experts, MXFP4, k), describe(b, F32), describe(ids, I32), describe(out, F32)
+        self._check(lib().ghip_mul_mat_id(self._ctx, C.byref(a), C.byref(tb), C.byref(ti), C.byref(d), _stream()),
+                    "ghip_mul_mat_id")
+        return out
+
+    def mul_mat_id_subsums(self, experts, k, b, ids):
+        n_tokens, n_ids = ids.shape
+        sub = torch.full((n_tokens, n_ids, experts.shape[1], k // 32), -1, dtype=torch.int32, device=b.device)
+        a, tb, ti = describe(experts, MXFP4, k), describe(b, F32), describe(ids, I32)
+        self._check(lib().ghip_mul_mat_id_subsums(self._ctx, C.byref(a), C.byref(tb), C.byref(ti),
+                                                  C.c_void_p(sub.data_ptr()), _stream()), "ghip_mul_mat_id_subsums")
+        return sub
+
+    # ---- FLASH_ATTN_EXT
+    def flash_attn_ext(self, q, k, v, mask=None, sinks=None, scale=1.0, max_bias=0.0, softcap=0.0, out=None):
+        """q [H, T, D] f32, k/v [H_kv, S, D] f16, mask [T, S] f16, sinks [H] f32 -> [T, H, D] f32."""
+        import struct
+        H, T, D = q.shape
+        if out is None:
+            out = torch.empty((T, H, v.shape[2]), dtype=torch.float32, device=q.device)
+        tq, tk, tv = describe(q, F32), describe(k, F16), describe(v, F16)
+        tm, ts, td = describe(mask, F16), describe(sinks, F32), describe(out, F32)
+        for i, f in enumerate((scale, max_bias, softcap)):
+            td.op_params[i] = struct.unpack("<i", struct.pack("<f", f))[0]
+        ref = lambda t: C.byref(t) if t is not None else None
+        self._check(lib().ghip_flash_attn_ext(self._ctx, ref(tq), ref(tk), ref(tv), ref(tm), ref(ts), ref(td),
+                                              _stream()), "ghip_flash_attn_ext")
         return out
 
     def synchronize(self):

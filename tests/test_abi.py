@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_code_objects_present():
-    for k in ("ghip_quant", "ghip_gemv", "ghip_wquant", "ghip_gemm"):
+    for k in ("ghip_quant", "ghip_gemv", "ghip_wquant", "ghip_gemm", "ghip_fa", "ghip_moe"):
         assert os.path.exists(os.path.join(ROOT, "llama.rust_amd", k + ".hsaco")), k
 
 

@@ -1,0 +1,84 @@
+"""GPU parity of GGML_OP_FLASH_ATTN_EXT (f16 K/V) against the CPU oracle.
+
+Bar: within 2e-3 max-abs of the reference path.  The
+oracle follows the reference's dispatch (split-KV for single-row decode with
+S >= 512, tiled for >= 64 query rows, one_chunk otherwise), pinned bit-exact
+on parity/fa_ref.bin and fa_probe.bin (test_oracle_golden.py).
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+@pytest.fixture(scope="module")
+def be():
+    import ghip
+    b = ghip.Backend(0)
+    yield b
+    b.close()
+
+
+def causal_mask(T, S):
+    m = np.zeros((T, S), dtype=np.float16)
+    for t in range(T):
+        m[t, S - T + t + 1:] = -np.inf
+    return m
+
+
+def run(be, H, Hkv, D, T, S, mask="causal", sinks=False, softcap=0.0, max_bias=0.0, seed=0, n_chunks=8):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((H, T, D)).astype(np.float32)
+    k = rng.standard_normal((Hkv, S, D)).astype(np.float16)
+    v = rng.standard_normal((Hkv, S, D)).astype(np.float16)
+    m = causal_mask(T, S) if mask == "causal" else (np.zeros((T, S), np.float16) if mask == "zero" else None)
+    sk = rng.standard_normal(H).astype(np.float32) if sinks else None
+    scale = 1.0 / np.sqrt(D)
+    want, path = O.flash_attn_ext(q, k, v, m, sk, scale, max_bias, softcap, n_chunks=n_chunks)
+    print(f"fa H={H} Hkv={Hkv} D={D} T={T} S={S} mask={mask} path={path}", flush=True)
+    t = lambda a: torch.from_numpy(a).cuda() if a is not None else None
+    got = be.flash_attn_ext(t(q), t(k), t(v), t(m), t(sk), scale, max_bias, softcap).cpu().numpy()
+    err = float(np.max(np.abs(got - want)))
+    assert err <= TOL, f"max-abs {err:.3e}"
+    return err
+
+
+@pytest.mark.parametrize("T,S", [(1, 64), (1, 100), (1, 600), (3, 40), (5, 700), (32, 96), (64, 64), (70, 130)])
+def test_small(be, T, S):
+    run(be, 4, 2, 64, T, S)
+    run(be, 8, 2, 128, T, S, seed=1)
+
+
+def test_variants(be):
+    run(be, 4, 4, 128, 2, 300, mask=None)
+    run(be, 4, 1, 64, 65, 200, sinks=True)
+    run(be, 4, 2, 64, 70, 200, softcap=15.0)
+    run(be, 8, 2, 64, 64, 128, max_bias=8.0, mask="zero")
+    run(be, 4, 2, 128, 1, 513, sinks=True)
+
+
+def test_fully_masked_rows(be):
+    """Rows whose keys are all masked produce zeros (S == 0 -> S_inv = 0)."""
+    H, Hkv, D, T, S = 4, 2, 64, 4, 80
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal((H, T, D)).astype(np.float32)
+    k = rng.standard_normal((Hkv, S, D)).astype(np.float16)
+    v = rng.standard_normal((Hkv, S, D)).astype(np.float16)
+    m = np.zeros((T, S), dtype=np.float16)
+    m[1, :] = -np.inf
+    want, _ = O.flash_attn_ext(q, k, v, m, None, 0.125)
+    got = be.flash_attn_ext(*(torch.from_numpy(a).cuda() for a in (q, k, v, m)), None, 0.125).cpu().numpy()
+    assert np.all(got[1] == 0.0)
+    assert np.max(np.abs(got - want)) <= TOL
+
+
+@pytest.mark.parametrize("T", [1, 512])
+def test_config5(be, T):
+    """Config 5: 32 query / 8 KV heads, D = 128, KV 8192, causal chunk at the
+    end of the cache (decode T = 1, prefill T = 512)."""
+    run(be, 32, 8, 128, T, 8192, seed=5, n_chunks=16)

@@ -22,6 +22,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "llama.rust_amd"))
 
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
 METRIC = "Q4_K GEMV GB/s (% of 8 TB/s HBM) + Q4_K prefill GEMM TOPS (% MFMA peak)"
 
 LAYER = [  # (name, weight type, K, N)
@@ -58,11 +59,43 @@ def step_bytes(batch):
 
 
 def time_layer(be, torch, sets, xs, outs, steps, warmup):
+    """Seconds per decode-layer step.  Each step is one replay of a HIP graph
+    holding the layer's 7 MUL_MATs (quantization + kernel each) for one of
+    the weight copies, so host launch gaps are not in the measurement."""
     def one(i):
         ws = sets[i % len(sets)]
         for (name, ty, k, n), w in zip(LAYER, ws):
             be.mul_mat(w, ty, k, xs[k], out=outs[name])
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(len(sets)):
+            one(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graphs = []
+    for i in range(len(sets)):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            one(i)
+        graphs.append(g)
     for i in range(warmup):
+        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def time_layer_eager(be, torch, sets, xs, outs, steps):
+    """Same step issued op by op from Python (host launch cost included)."""
+    def one(i):
+        ws = sets[i % len(sets)]
+        for (name, ty, k, n), w in zip(LAYER, ws):
+            be.mul_mat(w, ty, k, xs[k], out=outs[name])
+    for i in range(3):
         one(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -119,6 +152,78 @@ def gemv_roofline(be, torch, np, n_launch=64):
     return us, alg, wb
 
 
+def gemm_bench(be, torch, np):
+    """Config 3: Q4_K prefill MUL_MAT (Q8_K quantization + int8 MFMA GEMM)."""
+    import ghip
+    res = {}
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for m, k, n in [(512, 4096, 14336), (128, 4096, 4096), (2048, 4096, 4096)]:
+        wf = torch.randn((n, k), device="cuda", generator=g) * 0.02
+        w = be.quantize(wf, ghip.Q4_K)
+        del wf
+        x = torch.randn((m, k), device="cuda", generator=g)
+        out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        act = be.mul_mat_act(w, ghip.Q4_K, k, x)
+        us_op = graph_time_us(torch, lambda i: be.mul_mat(w, ghip.Q4_K, k, x, out=out), 10)
+        us_k = graph_time_us(torch, lambda i: be.mul_mat(w, ghip.Q4_K, k, act, out=out), 10)
+        ops = 2.0 * m * n * k
+        res[f"{m}x{k}->{n}"] = {"us_op": round(us_op, 2), "us_gemm_kernel": round(us_k, 2),
+                                "TOPS_op": round(ops / us_op / 1e6, 1), "TOPS_gemm_kernel": round(ops / us_k / 1e6, 1),
+                                "frac_int8_peak_kernel": round(ops / us_k / 1e6 / INT8_PEAK_TOPS, 4)}
+        log(f"GEMM {m}x{k}->{n}: op {us_op:.1f} us ({ops / us_op / 1e6:.1f} TOPS), kernel {us_k:.1f} us "
+            f"({ops / us_k / 1e6:.1f} TOPS)")
+        del w, x, out, act
+    return res
+
+
+def moe_bench(be, torch, np):
+    """Config 4: gpt-oss MoE MUL_MAT_ID, 32 MXFP4 experts, 256 tokens, top-4."""
+    import ghip
+    res = {}
+    n_as, n_tok, n_ids, k = 32, 256, 4, 2880
+    rng = np.random.default_rng(3)
+    ids = torch.from_numpy(np.argsort(-rng.standard_normal((n_tok, n_as)), axis=1)[:, :n_ids].astype(np.int32)).cuda()
+    g = torch.Generator(device="cuda").manual_seed(1)
+    for name, rows, ne11 in [("gate_up", 5760, 1), ("down", 2880, 4)]:
+        wf = torch.randn((n_as * rows, k), device="cuda", generator=g) * 0.02
+        w = be.quantize(wf, ghip.MXFP4).view(n_as, rows, -1)
+        del wf
+        b = torch.randn((n_tok, ne11, k), device="cuda", generator=g)
+        out = torch.empty((n_tok, n_ids, rows), dtype=torch.float32, device="cuda")
+        us = graph_time_us(torch, lambda i: be.mul_mat_id(w, k, b, ids, out=out), 10)
+        wbytes = w.numel()
+        flops = 2.0 * n_tok * n_ids * rows * k
+        res[name] = {"us": round(us, 2), "weight_GB/s": round(wbytes / us / 1e3, 1),
+                     "TFLOP/s": round(flops / us / 1e6, 1), "tokens_per_s": round(n_tok / us * 1e6, 1),
+                     "frac_hbm": round(wbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+        log(f"MoE {name}: {us:.1f} us, weights {wbytes / us / 1e3:.0f} GB/s, {flops / us / 1e6:.1f} TFLOP/s")
+        del w, b, out
+    return res
+
+
+def fa_bench(be, torch, np):
+    """Config 5: FLASH_ATTN_EXT, 32 q / 8 KV heads, D 128, KV 8192, causal."""
+    res = {}
+    H, Hkv, D, S = 32, 8, 128, 8192
+    g = torch.Generator(device="cuda").manual_seed(2)
+    k = torch.randn((Hkv, S, D), device="cuda", generator=g).half()
+    v = torch.randn((Hkv, S, D), device="cuda", generator=g).half()
+    for T in (1, 512):
+        q = torch.randn((H, T, D), device="cuda", generator=g)
+        mask = torch.zeros((T, S), dtype=torch.float16, device="cuda")
+        for t in range(T):
+            mask[t, S - T + t + 1:] = float("-inf")
+        out = torch.empty((T, H, D), dtype=torch.float32, device="cuda")
+        us = graph_time_us(torch, lambda i: be.flash_attn_ext(q, k, v, mask, None, 1.0 / D ** 0.5, out=out), 10)
+        kv_bytes = 2 * Hkv * S * D * 2
+        keys = sum(S - T + t + 1 for t in range(T))
+        flops = 4.0 * keys * D * H
+        res[f"T{T}"] = {"us": round(us, 2), "kv_GB/s": round(kv_bytes / us / 1e3, 1),
+                        "TFLOP/s": round(flops / us / 1e6, 2), "tokens_per_s": round(T / us * 1e6, 1)}
+        log(f"FA T={T}: {us:.1f} us, KV {kv_bytes / us / 1e3:.0f} GB/s, {flops / us / 1e6:.1f} TFLOP/s")
+    return res
+
+
 def cpu_baseline(budget_s=12.0):
     """llama.rust's CPU path for the same Q4_K 4096->14336 batch-1 MUL_MAT (the
     repack gemv route), as the C restatement, OpenMP over the host threads."""
@@ -152,6 +257,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip the prefill GEMM / MoE / FA lines")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -173,9 +279,11 @@ def main():
         outs = {name: torch.empty((batch, n), dtype=torch.float32, device="cuda") for name, _, _, n in LAYER}
         steps = args.steps if batch == 1 else max(10, args.steps // 4)
         t = time_layer(be, torch, sets, xs, outs, steps, args.warmup)
+        te = time_layer_eager(be, torch, sets, xs, outs, max(10, steps // 4))
         gbs = step_bytes(batch) / t / 1e9
         res_by_batch[batch] = {"ms_per_layer": round(t * 1e3, 4), "GB/s": round(gbs, 1),
-                               "tokens_per_s_layer": round(batch / t, 1)}
+                               "tokens_per_s_layer": round(batch / t, 1),
+                               "ms_per_layer_eager_launch": round(te * 1e3, 4)}
         log(f"batch {batch}: {t*1e6:.1f} us/layer  {gbs:.1f} GB/s")
         if batch == 1:
             ms_headline, value = t * 1e3, gbs
@@ -187,6 +295,13 @@ def main():
             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
             "kernel": "ghip_gemv_q4_K_f_c1 (Q4_K 4096->14336, batch 1, f32 activations, Q8_K quantization fused)",
             "avg_us": round(us, 3), "bytes_per_launch": alg}
+    extras = {}
+    if not args.no_extras:
+        del sets
+        torch.cuda.empty_cache()
+        extras["prefill_gemm_q4K"] = gemm_bench(be, torch, np)
+        extras["moe_mxfp4"] = moe_bench(be, torch, np)
+        extras["flash_attn_f16kv"] = fa_bench(be, torch, np)
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
@@ -196,7 +311,7 @@ def main():
         "config": {"workload": "Llama-3-8B decode layer MUL_MAT set (q,k,v,o,gate,up Q4_K; down Q6_K), batch 1",
                    "bytes_per_step": step_bytes(1), "weight_copies": 4},
         "roofline": roof, "cpu_baseline": cpu,
-        "decode_by_batch": res_by_batch,
+        "decode_by_batch": res_by_batch, **extras,
     }
     print(json.dumps(line), flush=True)
     be.close()

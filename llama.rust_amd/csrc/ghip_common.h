@@ -101,6 +101,46 @@ DEV float reduce8_rows(float v[8], int lane) {
     x += __shfl_xor(x, 1, 64);
     return x;
 }
+// Transposed reduction of R per-row partials across the wavefront: the rows
+// are halved with each of the first log2(R) exchanges (lane bit 5 first), the
+// rest of the lanes then sum normally.  Row r's total ends in the lanes whose
+// top log2(R) bits equal r (lane / (64 / R) == r).
+template <int R>
+DEV float reduce_rows(float v[R], int lane) {
+    if constexpr (R == 8) {
+        return reduce8_rows(v, lane);
+    } else if constexpr (R == 4) {
+        const bool b5 = lane & 32, b4 = lane & 16;
+        float u[2], x;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const float send = b5 ? v[i] : v[i + 2];
+            const float keep = b5 ? v[i + 2] : v[i];
+            u[i] = keep + __shfl_xor(send, 32, 64);
+        }
+        {
+            const float send = b4 ? u[0] : u[1];
+            const float keep = b4 ? u[1] : u[0];
+            x = keep + __shfl_xor(send, 16, 64);
+        }
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
+        return x;
+    } else if constexpr (R == 2) {
+        const bool b5 = lane & 32;
+        const float send = b5 ? v[0] : v[1];
+        float x = (b5 ? v[1] : v[0]) + __shfl_xor(send, 32, 64);
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
+        return x;
+    } else {
+        float x = v[0];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
+        return x;
+    }
+}
+
 DEV int group8_sum(int v) {
     v += __shfl_xor(v, 1, 64);
     v += __shfl_xor(v, 2, 64);

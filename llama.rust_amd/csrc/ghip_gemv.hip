@@ -23,7 +23,7 @@
 //   Q4_0: sum (nib-8) q8 per 32-block   (repack.rs:3351-3378)
 #include "ghip_common.h"
 
-constexpr int RB = 8;  // weight rows per workgroup
+constexpr int RB = 8;  // weight rows per workgroup (Q6_K, Q4_0; Q4_K takes it as a parameter)
 
 // write the 8 row totals of column c (lanes with lane%8 == 0 hold them)
 DEV void stash_rows(float *red, float part[RB], int lane, int w, int nw, int c, int NC) {
@@ -42,163 +42,195 @@ DEV void finish_rows(const float *red, int r0, int nrows, int ncols, int NC, int
 }
 
 // ---------------------------------------------------------------- Q4_K x Q8_K
-// Activation codes of one lane: the 32 elements 64g+16h+[0,16) (low stream)
-// and 64g+32+16h+[0,16) (high stream) of super-block b, the pair sum of
-// subblock j for the min term, and the block scale.
+// Q4_K workgroup = T row teams x W_K wavefronts (the K-team tiles the row
+// once, 8 lanes per super-block).  The activation columns are quantized to
+// Q8_K ONCE per workgroup, by all its lanes, into LDS; each lane then reads
+// the codes of its fixed K position from there.
+//
+// LDS (dynamic): codes [NC][K] int8 | d [NC][nb] f32 | sub-block sums
+// [NC][nb][8] int32 | row partials [T*rows_per_team][W_K][NC] f32.
 struct Q4KAct {
     uint4 lo, hi;
     int bp;
     float d;
 };
 
-// Quantize this lane's share of activation row xr (f32) to Q8_K inside the
-// kernel, bit-identical to ghip_quantize_q8_K: the 8 lanes of a super-block
-// reduce its signed max-abs (first occurrence wins), then each lane codes its
-// 32 elements.  mat selects the quantize_mat_q8_K_4x8 values.
-struct XLane {
-    float l[16], h[16];
+// Quantization of the activation rows into the LDS image, bit-identical to
+// ghip_quantize_q8_K: 16 lanes per super-block ("task" = one lane's 16
+// consecutive elements); the signed max-abs is reduced over the 16 lanes with
+// the first occurrence winning ties; rows c < n_mat take the
+// quantize_mat_q8_K_4x8 values.  Tasks run in rounds of blockDim lanes; every
+// lane of the workgroup takes part in every round (the shuffles need them).
+struct XTask {
+    float v[16];
 };
 
-DEV XLane load_x_lane(const float *__restrict__ xr, int b, int g, int h, bool valid) {
-    XLane x;
-    if (valid) {
-        __builtin_memcpy(x.l, xr + (int64_t)b * QK_K + 64 * g + 16 * h, 64);
-        __builtin_memcpy(x.h, xr + (int64_t)b * QK_K + 64 * g + 32 + 16 * h, 64);
+DEV XTask quant_q8K_load(const float *__restrict__ x, int64_t x_stride, int ncols, int nb, int total, int task) {
+    XTask t;
+    const int l = task & 15, blk = task >> 4;
+    const int c = blk / nb, b = blk - c * nb;
+    if (task < total && c < ncols) {
+        __builtin_memcpy(t.v, x + (int64_t)c * x_stride + (int64_t)b * QK_K + 16 * l, 64);
     } else {
 #pragma unroll
-        for (int i = 0; i < 16; i++) x.l[i] = x.h[i] = 0.0f;
+        for (int i = 0; i < 16; i++) t.v[i] = 0.0f;
     }
-    return x;
+    return t;
 }
 
-DEV Q4KAct quant_q8K_lane(const XLane &x, int g, int h, int j, bool mat) {
-    const float *xl = x.l, *xh = x.h;
-    // element index inside the block, for the first-occurrence tie break
-    const int base_l = 64 * g + 16 * h, base_h = base_l + 32;
+DEV void quant_q8K_store(const XTask &t, int nb, int n_mat, int total, int task, int8_t *codes, float *dq, int *bsum) {
+    const float *v = t.v;
+    const bool live = task < total;
+    const int l = task & 15, blk = task >> 4;
+    const int c = live ? blk / nb : 0, b = live ? blk - c * nb : 0;
     float bax = 0.0f, bval = 0.0f;
     int bidx = 0x7fffffff;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-        const float a = fabsf(xl[i]);
-        if (a > bax) { bax = a; bval = xl[i]; bidx = base_l + i; }
+        const float a = fabsf(v[i]);
+        if (a > bax) { bax = a; bval = v[i]; bidx = 16 * l + i; }
     }
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const float a = fabsf(xh[i]);
-        if (a > bax || (a == bax && a > 0.0f && base_h + i < bidx)) { bax = a; bval = xh[i]; bidx = base_h + i; }
-    }
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) {
+    for (int o = 1; o < 16; o <<= 1) {
         const float oax = __shfl_xor(bax, o, 64);
         const float oval = __shfl_xor(bval, o, 64);
         const int oidx = __shfl_xor(bidx, o, 64);
         if (oax > bax || (oax == bax && oidx < bidx)) { bax = oax; bval = oval; bidx = oidx; }
     }
-    Q4KAct r;
-    int ql[16], qh[16];
+    int q[16];
+    float d;
     if (bax == 0.0f) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) ql[i] = qh[i] = 0;
-        r.d = 0.0f;
-    } else if (!mat) {
+        for (int i = 0; i < 16; i++) q[i] = 0;
+        d = 0.0f;
+    } else if (c >= n_mat) {
         const float iscale = __fdiv_rn(-127.0f, bval);
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            ql[i] = min(127, (int)rintf(__fmul_rn(iscale, xl[i])));
-            qh[i] = min(127, (int)rintf(__fmul_rn(iscale, xh[i])));
-        }
-        r.d = __fdiv_rn(1.0f, iscale);
+        for (int i = 0; i < 16; i++) q[i] = min(127, (int)rintf(__fmul_rn(iscale, v[i])));
+        d = __fdiv_rn(1.0f, iscale);
     } else {
         const float iscale = __fdiv_rn(127.0f, bax);
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            ql[i] = (int)fminf(fmaxf(rintf(__fmul_rn(iscale, xl[i])), -128.0f), 127.0f);
-            qh[i] = (int)fminf(fmaxf(rintf(__fmul_rn(iscale, xh[i])), -128.0f), 127.0f);
-        }
-        r.d = __fdiv_rn(1.0f, iscale);
+        for (int i = 0; i < 16; i++) q[i] = (int)fminf(fmaxf(rintf(__fmul_rn(iscale, v[i])), -128.0f), 127.0f);
+        d = __fdiv_rn(1.0f, iscale);
     }
-    uint32_t pl[4], ph[4];
-    int sl = 0, sh = 0;
+    uint32_t pk[4];
+    int sum = 0;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        pl[k] = (uint32_t)(ql[4 * k] & 0xff) | ((uint32_t)(ql[4 * k + 1] & 0xff) << 8) |
-                ((uint32_t)(ql[4 * k + 2] & 0xff) << 16) | ((uint32_t)(ql[4 * k + 3] & 0xff) << 24);
-        ph[k] = (uint32_t)(qh[4 * k] & 0xff) | ((uint32_t)(qh[4 * k + 1] & 0xff) << 8) |
-                ((uint32_t)(qh[4 * k + 2] & 0xff) << 16) | ((uint32_t)(qh[4 * k + 3] & 0xff) << 24);
-        sl += ql[4 * k] + ql[4 * k + 1] + ql[4 * k + 2] + ql[4 * k + 3];
-        sh += qh[4 * k] + qh[4 * k + 1] + qh[4 * k + 2] + qh[4 * k + 3];
+        pk[k] = (uint32_t)(q[4 * k] & 0xff) | ((uint32_t)(q[4 * k + 1] & 0xff) << 8) |
+                ((uint32_t)(q[4 * k + 2] & 0xff) << 16) | ((uint32_t)(q[4 * k + 3] & 0xff) << 24);
+        sum += q[4 * k] + q[4 * k + 1] + q[4 * k + 2] + q[4 * k + 3];
     }
-    r.lo = make_uint4(pl[0], pl[1], pl[2], pl[3]);
-    r.hi = make_uint4(ph[0], ph[1], ph[2], ph[3]);
-    // subblock j = 2g' collects the low streams of lanes 2g', 2g'+1; 2g'+1 their high streams
-    const int ol = __shfl_xor(sl, 1, 64), oh = __shfl_xor(sh, 1, 64);
-    r.bp = (j & 1) ? (sh + oh) : (sl + ol);
-    return r;
+    sum += __shfl_xor(sum, 1, 64);  // a 32-element sub-block is two lanes
+    if (live) {
+        *reinterpret_cast<uint4 *>(codes + (int64_t)c * nb * QK_K + b * QK_K + 16 * l) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        if ((l & 1) == 0) bsum[(c * nb + b) * 8 + (l >> 1)] = sum;
+        if (l == 0) dq[c * nb + b] = d;
+    }
 }
 
-DEV Q4KAct load_q8K_lane(const uint8_t *__restrict__ A, int g, int h, int j) {
-    Q4KAct r;
-    r.lo = ld16(A + 4 + 64 * g + 16 * h);
-    r.hi = ld16(A + 4 + 64 * g + 32 + 16 * h);
-    const uint32_t bs = ld4(A + 260 + 4 * j);
-    r.bp = (int)(int16_t)(bs & 0xffff) + (int)(int16_t)(bs >> 16);
-    r.d = __uint_as_float(ld4(A));
-    return r;
+// Ready Q8_K rows (pre-quantized src1) copied into the same LDS image.
+DEV void load_q8K_lds(const uint8_t *__restrict__ act, int64_t act_row_bytes, int ncols, int NC, int nb,
+                      int8_t *codes, float *dq, int *bsum) {
+    const int K = nb * QK_K;
+    for (int task = threadIdx.x; task < NC * nb * 16; task += blockDim.x) {
+        const int l = task & 15, blk = task >> 4;
+        const int c = blk / nb, b = blk - c * nb;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        int sum = 0;
+        float d = 0.0f;
+        if (c < ncols) {
+            const uint8_t *A = act + (int64_t)c * act_row_bytes + (int64_t)b * Q8K_BYTES;
+            v = ld16(A + 4 + 16 * l);
+            const uint32_t bs = ld4(A + 260 + 4 * (l >> 1));
+            sum = (int)(int16_t)(bs & 0xffff) + (int)(int16_t)(bs >> 16);
+            d = __uint_as_float(ld4(A));
+        }
+        *reinterpret_cast<uint4 *>(codes + (int64_t)c * K + b * QK_K + 16 * l) = v;
+        if ((l & 1) == 0) bsum[(c * nb + b) * 8 + (l >> 1)] = sum;
+        if (l == 0) dq[c * nb + b] = d;
+    }
 }
 
-// One launch per MUL_MAT: FUSEQ kernels read the f32 activations and quantize
-// them in registers; the others read ready Q8_K rows.  Each workgroup walks
-// rows_per_wg rows in groups of RB, loading group i+1 while computing group i.
-template <int NC, bool SUBSUMS, bool FUSEQ>
+// scale / min of sub-blocks 2g, 2g+1 and j (get_scale_min_k4, quants_k.rs:1672)
+// without lane-divergent branches: sub-block i < 4 reads 6 bits of byte i
+// (scales) / i+4 (mins); i >= 4 reads a nibble of byte i+4 plus the top two
+// bits of byte i-4 (scales) / i (mins).
+DEV int k4_scale(uint32_t s0, uint32_t s2, int i) {
+    const int k = 8 * (i & 3);
+    return i < 4 ? (int)((s0 >> k) & 63) : (int)(((s2 >> k) & 15) | (((s0 >> (k + 6)) & 3) << 4));
+}
+DEV int k4_min(uint32_t s1, uint32_t s2, int i) {
+    const int k = 8 * (i & 3);
+    return i < 4 ? (int)((s1 >> k) & 63) : (int)(((s2 >> (k + 4)) & 15) | (((s1 >> (k + 6)) & 3) << 4));
+}
+
+template <int NC, bool SUBSUMS, bool FUSEQ, int RB>
 __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
                                               int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
                                               int ncols, float *__restrict__ dst, int64_t ldd,
-                                              int32_t *__restrict__ sub, int rows_per_wg, int n_mat) {
-    extern __shared__ float red[];  // [rows_per_wg][W_K][NC]
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+                                              int32_t *__restrict__ sub, int rows_per_team, int n_mat) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nwk = (nb + 7) >> 3;                 // wavefronts per K-team
+    const int T = (blockDim.x >> 6) / nwk;         // row teams
+    const int team = wave / nwk, w = wave - team * nwk;
+    const int K = nb * QK_K;
+    int8_t *codes = reinterpret_cast<int8_t *>(smem);
+    float *dq = reinterpret_cast<float *>(smem + NC * K);
+    int *bsum = reinterpret_cast<int *>(dq + NC * nb);
+    float *red = reinterpret_cast<float *>(bsum + NC * nb * 8);  // [T*rows_per_team][nwk][NC]
+
     const int b = 8 * w + (lane >> 3), j = lane & 7, g = j >> 1, h = j & 1;
     const bool valid = b < nb;
-    const int r0 = blockIdx.x * rows_per_wg;
-    const int r1 = min(rows, r0 + rows_per_wg);
-    const uint8_t *wb = W + (int64_t)b * Q4K_BYTES;
+    const int rw0 = blockIdx.x * T * rows_per_team;  // first row of the workgroup
+    const int r0 = rw0 + team * rows_per_team;
+    const int r1 = min(rows, r0 + rows_per_team);
 
     // Branch-free weight loads: rows past the tile and lanes past the row
     // re-read a valid block (clamped index) and contribute zero (their
     // activation codes and scale are zero).
     const uint8_t *wbc = W + (int64_t)min(b, nb - 1) * Q4K_BYTES;
-    uint4 hdr[RB], q[RB];
+    const int rlast = min(max(r0, r1 - 1), rows - 1);  // a team past the last row loads row rows-1, computes nothing
+    uint4 hdr[RB], q[RB], hdr2[RB], q2[RB];
     auto load_group = [&](int rg, uint4 *hd, uint4 *qq) {
 #pragma unroll
         for (int rr = 0; rr < RB; rr++) {
-            const uint8_t *p = wbc + (int64_t)min(rg + rr, r1 - 1) * w_row_bytes;
+            const uint8_t *p = wbc + (int64_t)min(rg + rr, rlast) * w_row_bytes;
             hd[rr] = ld16(p);
             qq[rr] = ld16(p + 16 + 16 * j);
         }
     };
-    // Order of issue: the f32 activations of up to two columns, then the first
-    // weight group, then the activation quantization -- which waits on the
-    // activation loads only, with the weight loads still in flight.
-    constexpr int NX = FUSEQ ? (NC < 2 ? NC : 2) : 0;
-    XLane xs[NX > 0 ? NX : 1];
-#pragma unroll
-    for (int c = 0; c < NX; c++)
-        xs[c] = load_x_lane(reinterpret_cast<const float *>(act + c * act_row_bytes), b, g, h,
-                            valid && c < ncols);
-    load_group(r0, hdr, q);
+    // Activations first (their wait then does not cover the weight loads),
+    // then the first two weight groups, then quantization into LDS.
+    if (FUSEQ) {
+        const float *x = reinterpret_cast<const float *>(act);
+        const int64_t xs = act_row_bytes / 4;
+        const int total = NC * nb * 16;
+        const XTask t0 = quant_q8K_load(x, xs, ncols, nb, total, threadIdx.x);
+        load_group(r0, hdr, q);
+        if (r0 + RB < r1) load_group(r0 + RB, hdr2, q2);
+        quant_q8K_store(t0, nb, n_mat, total, threadIdx.x, codes, dq, bsum);
+        for (int base = blockDim.x; base < total; base += blockDim.x) {
+            const XTask t = quant_q8K_load(x, xs, ncols, nb, total, base + threadIdx.x);
+            quant_q8K_store(t, nb, n_mat, total, base + threadIdx.x, codes, dq, bsum);
+        }
+    } else {
+        load_group(r0, hdr, q);
+        if (r0 + RB < r1) load_group(r0 + RB, hdr2, q2);
+        load_q8K_lds(act, act_row_bytes, ncols, NC, nb, codes, dq, bsum);
+    }
+    __syncthreads();
     Q4KAct a[NC];
 #pragma unroll
     for (int c = 0; c < NC; c++) {
-        if (c < ncols) {
-            if (FUSEQ) {
-                const XLane xv = c < NX ? xs[c]
-                                        : load_x_lane(reinterpret_cast<const float *>(act + c * act_row_bytes), b,
-                                                      g, h, valid);
-                a[c] = quant_q8K_lane(xv, g, h, j, c < n_mat);
-            } else if (valid) {
-                a[c] = load_q8K_lane(act + c * act_row_bytes + (int64_t)b * Q8K_BYTES, g, h, j);
-            } else {
-                a[c] = Q4KAct{make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), 0, 0.0f};
-            }
+        if (valid) {
+            const int8_t *cb = codes + (int64_t)c * K + b * QK_K;
+            a[c].lo = *reinterpret_cast<const uint4 *>(cb + 64 * g + 16 * h);
+            a[c].hi = *reinterpret_cast<const uint4 *>(cb + 64 * g + 32 + 16 * h);
+            a[c].bp = bsum[(c * nb + b) * 8 + j];
+            a[c].d = dq[c * nb + b];
         } else {
             a[c] = Q4KAct{make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), 0, 0.0f};
         }
@@ -210,10 +242,8 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
         for (int rr = 0; rr < RB; rr++) {
             const uint4 hd = hdr_[rr], qq = q_[rr];
             const float dw = h2f(hd.x), dmin = h2f(hd.x >> 16);
-            int slo, shi, mj, mdummy, sdummy;
-            scale_min_k4(hd.y, hd.z, hd.w, 2 * g, slo, mdummy);
-            scale_min_k4(hd.y, hd.z, hd.w, 2 * g + 1, shi, mdummy);
-            scale_min_k4(hd.y, hd.z, hd.w, j, sdummy, mj);
+            const int slo = k4_scale(hd.y, hd.w, 2 * g), shi = k4_scale(hd.y, hd.w, 2 * g + 1);
+            const int mj = k4_min(hd.z, hd.w, j);
             const uint32_t l0 = qq.x & 0x0f0f0f0f, l1 = qq.y & 0x0f0f0f0f, l2 = qq.z & 0x0f0f0f0f, l3 = qq.w & 0x0f0f0f0f;
             const uint32_t h0 = (qq.x >> 4) & 0x0f0f0f0f, h1 = (qq.y >> 4) & 0x0f0f0f0f;
             const uint32_t h2 = (qq.z >> 4) & 0x0f0f0f0f, h3 = (qq.w >> 4) & 0x0f0f0f0f;
@@ -234,23 +264,31 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
                 part[c][rr] = a[c].d * fmaf(dw, (float)ia, -(dmin * (float)im));
             }
         }
+        constexpr int LPR = 64 / RB;  // lanes per row after the transposed reduction
 #pragma unroll
         for (int c = 0; c < NC; c++) {
-            const float t = reduce8_rows(part[c], lane);
-            if ((lane & 7) == 0 && rg + (lane >> 3) < r1) red[((rg - r0 + (lane >> 3)) * nw + w) * NC + c] = t;
+            const float t = reduce_rows<RB>(part[c], lane);
+            if ((lane & (LPR - 1)) == 0 && rg + lane / LPR < r1)
+                red[((rg - rw0 + lane / LPR) * nwk + w) * NC + c] = t;
         }
     };
-    // Ping-pong over two register buffers (no copies, so the next group's
-    // loads stay in flight while this group is computed).
-    uint4 hdr2[RB], q2[RB];
+    // Ping-pong over two register buffers (no copies): the loads of the two
+    // groups ahead stay in flight while a group is computed.
     for (int rg = r0; rg < r1; rg += 2 * RB) {
-        if (rg + RB < r1) load_group(rg + RB, hdr2, q2);
         compute_group(rg, hdr, q);
         if (rg + RB >= r1) break;
         if (rg + 2 * RB < r1) load_group(rg + 2 * RB, hdr, q);
         compute_group(rg + RB, hdr2, q2);
+        if (rg + 3 * RB < r1) load_group(rg + 3 * RB, hdr2, q2);
     }
-    finish_rows(red, r0, r1 - r0, ncols, NC, nw, dst, ldd);
+    __syncthreads();
+    const int nrows = max(0, min(rows, rw0 + T * rows_per_team) - rw0);
+    for (int idx = threadIdx.x; idx < nrows * ncols; idx += blockDim.x) {
+        const int rr = idx / ncols, c = idx - rr * ncols;
+        float s = 0.0f;
+        for (int ww = 0; ww < nwk; ww++) s += red[(rr * nwk + ww) * NC + c];
+        dst[(int64_t)c * ldd + rw0 + rr] = s;
+    }
 }
 
 // ---------------------------------------------------------------- Q6_K x Q8_K
@@ -454,19 +492,20 @@ GEMV_ALL(ghip_gemv_q4_0, gemv_q4_0_impl)
 
 // Q4_K: "_f" kernels take f32 activations (fused Q8_K quantization), the
 // others ready Q8_K rows; "_sub" kernels also store the integer partials.
-#define Q4K_ARGS GEMV_ARGS, int rows_per_wg, int n_mat
-#define Q4K_PASS GEMV_PASS, rows_per_wg, n_mat
-#define Q4K_INST(NC)                                                                                              \
-    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_c##NC(Q4K_ARGS) {                           \
-        gemv_q4K_impl<NC, false, false>(Q4K_PASS);                                                              \
+#define Q4K_ARGS GEMV_ARGS, int rows_per_team, int n_mat
+#define Q4K_PASS GEMV_PASS, rows_per_team, n_mat
+#define Q4K_INST(NC, RB)                                                                                          \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_c##NC##_r##RB(Q4K_ARGS) {                   \
+        gemv_q4K_impl<NC, false, false, RB>(Q4K_PASS);                                                          \
     }                                                                                                           \
-    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_sub_c##NC(Q4K_ARGS) {                       \
-        gemv_q4K_impl<NC, true, false>(Q4K_PASS);                                                               \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_sub_c##NC##_r##RB(Q4K_ARGS) {               \
+        gemv_q4K_impl<NC, true, false, RB>(Q4K_PASS);                                                           \
     }                                                                                                           \
-    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_f_c##NC(Q4K_ARGS) {                         \
-        gemv_q4K_impl<NC, false, true>(Q4K_PASS);                                                               \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_f_c##NC##_r##RB(Q4K_ARGS) {                 \
+        gemv_q4K_impl<NC, false, true, RB>(Q4K_PASS);                                                           \
     }                                                                                                           \
-    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_f_sub_c##NC(Q4K_ARGS) {                     \
-        gemv_q4K_impl<NC, true, true>(Q4K_PASS);                                                                \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_f_sub_c##NC##_r##RB(Q4K_ARGS) {             \
+        gemv_q4K_impl<NC, true, true, RB>(Q4K_PASS);                                                            \
     }
-Q4K_INST(1) Q4K_INST(2) Q4K_INST(4) Q4K_INST(8)
+#define Q4K_INST_RB(NC) Q4K_INST(NC, 2) Q4K_INST(NC, 4) Q4K_INST(NC, 8)
+Q4K_INST_RB(1) Q4K_INST_RB(2) Q4K_INST_RB(4) Q4K_INST_RB(8)

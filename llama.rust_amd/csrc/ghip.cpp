@@ -223,24 +223,27 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     int waves_k;
     if (p.wtype == GHIP_TYPE_Q4_0)
         waves_k = (int)(((p.nb + 1) / 2 + 63) / 64);
+    else if (p.wtype == GHIP_TYPE_Q4_K)
+        waves_k = (int)((p.nb + 15) / 16);
     else
         waves_k = (int)((p.nb + 7) / 8);
     if (waves_k > 8) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: ne00 = %lld too large for the decode kernel", (long long)p.K);
     const bool q4k = p.wtype == GHIP_TYPE_Q4_K;
-    // Q4_K: T row teams of rows_per_team rows share one LDS copy of the
-    // quantized activations; rows_per_team is a multiple of the kernel's
-    // register row group RB.
-    const int rb = q4k ? env_int("GHIP_GEMV_RB", 8) : 8;
-    if (rb != 2 && rb != 4 && rb != 8) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "GHIP_GEMV_RB must be 2, 4 or 8");
-    const int rows_per_team = q4k ? std::max(rb, env_int("GHIP_GEMV_ROWS", 16) / rb * rb) : 8;
-    const int teams = q4k ? std::max(1, std::min(8 / waves_k, env_int("GHIP_GEMV_TEAMS", 2))) : 1;
+    // Q4_K: T row teams share one LDS copy of the quantized activations; a
+    // team's wavefronts hold NG groups of RB rows in flight at once.
+    const int rb = q4k ? env_int("GHIP_GEMV_RB", 2) : 8;
+    const int ng = q4k ? env_int("GHIP_GEMV_NG", 2) : 1;
+    if (q4k && !((rb == 2 && (ng == 2 || ng == 4 || ng == 8)) || (rb == 4 && (ng == 2 || ng == 4))))
+        return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "GHIP_GEMV_RB x GHIP_GEMV_NG must be 2x2, 2x4, 2x8, 4x2 or 4x4");
+    const int rows_per_team = rb * ng;
+    const int teams = q4k ? std::max(1, std::min(8 / waves_k, env_int("GHIP_GEMV_TEAMS", 8))) : 1;
     const int rows_per_wg = rows_per_team * teams;
     const unsigned grid = (unsigned)((p.N + rows_per_wg - 1) / rows_per_wg);
     for (int64_t c0 = 0; c0 < p.M; c0 += 8) {
         const int nc = (int)std::min<int64_t>(8, p.M - c0);
         const int NC = nc == 1 ? 1 : nc == 2 ? 2 : nc <= 4 ? 4 : 8;
         std::string name = std::string(gemv_base(p.wtype)) + (q4k && fused ? "_f" : "") + (sub ? "_sub" : "") +
-                           "_c" + std::to_string(NC) + (q4k ? "_r" + std::to_string(rb) : std::string());
+                           "_c" + std::to_string(NC) + (q4k ? "_r" + std::to_string(rb) + "x" + std::to_string(ng) : std::string());
         int32_t *sub_c = sub;
         if (sub) {
             const int64_t per = p.wtype == GHIP_TYPE_Q4_K ? 2 * p.nb : p.nb;
@@ -255,7 +258,7 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
             const int n_mat = (int)std::max<int64_t>(0, std::min<int64_t>(nc, p.n_mat - c0));
             st = ctx->launch(name, dim3(grid), dim3(64 * waves_k * teams), shmem, s, (const uint8_t *)w,
                              (int64_t)p.w_row_bytes, (int)p.N, (int)p.nb, act + c0 * act_rb, (int64_t)act_rb, nc,
-                             dst + c0 * ldd, (int64_t)ldd, sub_c, rows_per_team, n_mat);
+                             dst + c0 * ldd, (int64_t)ldd, sub_c, n_mat);
         } else {
             st = ctx->launch(name, dim3(grid), dim3(64 * waves_k), 0, s, (const uint8_t *)w, (int64_t)p.w_row_bytes,
                              (int)p.N, (int)p.nb, act + c0 * act_rb, (int64_t)act_rb, nc, dst + c0 * ldd,

@@ -141,6 +141,29 @@ DEV float reduce_rows(float v[R], int lane) {
     }
 }
 
+// Wave-wide float sum with DPP row operations (no LDS): quad xor 1 and 2,
+// half-row and row mirrors leave every lane of a 16-lane row holding the
+// row's sum; the four row sums are read as scalars.  The result is uniform.
+#define GHIP_DPP_ADD(v, ctrl) \
+    ((v) + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), (ctrl), 0xF, 0xF, false)))
+DEV float wave_sum_dpp(float v) {
+    v = GHIP_DPP_ADD(v, 0xB1);   // quad_perm [1,0,3,2]
+    v = GHIP_DPP_ADD(v, 0x4E);   // quad_perm [2,3,0,1]
+    v = GHIP_DPP_ADD(v, 0x141);  // row_half_mirror
+    v = GHIP_DPP_ADD(v, 0x140);  // row_mirror
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+// sum over the 4 lanes of each quad (every lane of the quad gets it)
+DEV int quad_sum_dpp(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+    return v;
+}
+
 DEV int group8_sum(int v) {
     v += __shfl_xor(v, 1, 64);
     v += __shfl_xor(v, 2, 64);

@@ -49,12 +49,6 @@ DEV void finish_rows(const float *red, int r0, int nrows, int ncols, int NC, int
 //
 // LDS (dynamic): codes [NC][K] int8 | d [NC][nb] f32 | sub-block sums
 // [NC][nb][8] int32 | row partials [T*rows_per_team][W_K][NC] f32.
-struct Q4KAct {
-    uint4 lo, hi;
-    int bp;
-    float d;
-};
-
 // Quantization of the activation rows into the LDS image, bit-identical to
 // ghip_quantize_q8_K: 16 lanes per super-block ("task" = one lane's 16
 // consecutive elements); the signed max-abs is reduced over the 16 lanes with
@@ -130,159 +124,231 @@ DEV void quant_q8K_store(const XTask &t, int nb, int n_mat, int total, int task,
     }
 }
 
-// Ready Q8_K rows (pre-quantized src1) copied into the same LDS image.
-DEV void load_q8K_lds(const uint8_t *__restrict__ act, int64_t act_row_bytes, int ncols, int NC, int nb,
-                      int8_t *codes, float *dq, int *bsum) {
-    const int K = nb * QK_K;
-    for (int task = threadIdx.x; task < NC * nb * 16; task += blockDim.x) {
-        const int l = task & 15, blk = task >> 4;
-        const int c = blk / nb, b = blk - c * nb;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        int sum = 0;
-        float d = 0.0f;
-        if (c < ncols) {
-            const uint8_t *A = act + (int64_t)c * act_row_bytes + (int64_t)b * Q8K_BYTES;
-            v = ld16(A + 4 + 16 * l);
-            const uint32_t bs = ld4(A + 260 + 4 * (l >> 1));
-            sum = (int)(int16_t)(bs & 0xffff) + (int)(int16_t)(bs >> 16);
-            d = __uint_as_float(ld4(A));
-        }
-        *reinterpret_cast<uint4 *>(codes + (int64_t)c * K + b * QK_K + 16 * l) = v;
-        if ((l & 1) == 0) bsum[(c * nb + b) * 8 + (l >> 1)] = sum;
-        if (l == 0) dq[c * nb + b] = d;
+// Ready Q8_K rows (pre-quantized src1) copied into the same LDS image, in
+// the same task shape (16 codes per lane).
+struct Q8KTask {
+    uint4 v;
+    int sum;
+    float d;
+};
+
+DEV Q8KTask q8K_load(const uint8_t *__restrict__ act, int64_t act_row_bytes, int ncols, int nb, int total, int task) {
+    Q8KTask t{make_uint4(0, 0, 0, 0), 0, 0.0f};
+    const int l = task & 15, blk = task >> 4;
+    const int c = blk / nb, b = blk - c * nb;
+    if (task < total && c < ncols) {
+        const uint8_t *A = act + (int64_t)c * act_row_bytes + (int64_t)b * Q8K_BYTES;
+        t.v = ld16(A + 4 + 16 * l);
+        const uint32_t bs = ld4(A + 260 + 4 * (l >> 1));
+        t.sum = (int)(int16_t)(bs & 0xffff) + (int)(int16_t)(bs >> 16);
+        t.d = __uint_as_float(ld4(A));
     }
+    return t;
 }
 
-// scale / min of sub-blocks 2g, 2g+1 and j (get_scale_min_k4, quants_k.rs:1672)
-// without lane-divergent branches: sub-block i < 4 reads 6 bits of byte i
-// (scales) / i+4 (mins); i >= 4 reads a nibble of byte i+4 plus the top two
-// bits of byte i-4 (scales) / i (mins).
-DEV int k4_scale(uint32_t s0, uint32_t s2, int i) {
-    const int k = 8 * (i & 3);
-    return i < 4 ? (int)((s0 >> k) & 63) : (int)(((s2 >> k) & 15) | (((s0 >> (k + 6)) & 3) << 4));
-}
-DEV int k4_min(uint32_t s1, uint32_t s2, int i) {
-    const int k = 8 * (i & 3);
-    return i < 4 ? (int)((s1 >> k) & 63) : (int)(((s2 >> (k + 4)) & 15) | (((s1 >> (k + 6)) & 3) << 4));
+DEV void q8K_store(const Q8KTask &t, int nb, int total, int task, int8_t *codes, float *dq, int *bsum) {
+    if (task >= total) return;
+    const int l = task & 15, blk = task >> 4;
+    const int c = blk / nb, b = blk - c * nb;
+    *reinterpret_cast<uint4 *>(codes + (int64_t)c * nb * QK_K + b * QK_K + 16 * l) = t.v;
+    if ((l & 1) == 0) bsum[(c * nb + b) * 8 + (l >> 1)] = t.sum;
+    if (l == 0) dq[c * nb + b] = t.d;
 }
 
-template <int NC, bool SUBSUMS, bool FUSEQ, int RB>
+// Scales and mins of sub-blocks 2i and 2i+1 (get_scale_min_k4,
+// quants_k.rs:1672) for this lane's fixed i, without lane-divergent branches:
+// for sub-block t < 4 the scale is bits 0-5 of byte t and the min bits 0-5
+// of byte t+4; for t >= 4 the scale is the low nibble of byte t+4 with the
+// top two bits of byte t-4 above it, the min the high nibble of byte t+4 with
+// the top two bits of byte t.  The lane's selectors come from ScaleSel.
+struct ScaleSel {
+    bool hi;     // i >= 2: sub-blocks 4..7
+    int o0, o1;  // bit offsets of the two sub-blocks' bytes (8 * (t & 3))
+};
+DEV ScaleSel scale_sel(int i) { return ScaleSel{i >= 2, 8 * ((2 * i) & 3), 8 * ((2 * i + 1) & 3)}; }
+DEV void k4_scales(uint32_t s0, uint32_t s1, uint32_t s2, const ScaleSel &q, int &sc0, int &sc1, int &m0, int &m1) {
+    const uint32_t a = q.hi ? s2 : s0;  // scale low bits
+    const uint32_t bm = q.hi ? s2 : s1; // min low bits
+    const uint32_t ts = q.hi ? s0 : 0u; // scale top bits
+    const uint32_t tm = q.hi ? s1 : 0u; // min top bits
+    const int ws = q.hi ? 4 : 6, om = q.hi ? 4 : 0;
+    sc0 = (int)(__builtin_amdgcn_ubfe(a, q.o0, ws) | (__builtin_amdgcn_ubfe(ts, q.o0 + 6, 2) << 4));
+    sc1 = (int)(__builtin_amdgcn_ubfe(a, q.o1, ws) | (__builtin_amdgcn_ubfe(ts, q.o1 + 6, 2) << 4));
+    m0 = (int)(__builtin_amdgcn_ubfe(bm, q.o0 + om, ws) | (__builtin_amdgcn_ubfe(tm, q.o0 + 6, 2) << 4));
+    m1 = (int)(__builtin_amdgcn_ubfe(bm, q.o1 + om, ws) | (__builtin_amdgcn_ubfe(tm, q.o1 + 6, 2) << 4));
+}
+
+// Activation codes of one lane: elements 64i..64i+31 (low nibbles, sub-block
+// 2i) and 64i+32..64i+63 (high nibbles, sub-block 2i+1) of super-block b, the
+// two sub-block sums and the block scale.
+struct Q4KAct {
+    uint4 lo0, lo1, hi0, hi1;
+    int bs0, bs1;
+    float d;
+};
+
+// Q4_K workgroup = T row teams x W_K wavefronts; a wavefront covers 16
+// super-blocks of a row with 4 lanes per super-block (lane i of a block owns
+// qs bytes 32i..32i+31), so K <= 4096 is one wavefront and a row's partials
+// never leave it.  Rows are processed in register groups of RB, two groups
+// in flight (ping-pong buffers).
+template <int NC, bool SUBSUMS, bool FUSEQ, int RB, int NG>
 __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
                                               int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
                                               int ncols, float *__restrict__ dst, int64_t ldd,
-                                              int32_t *__restrict__ sub, int rows_per_team, int n_mat) {
+                                              int32_t *__restrict__ sub, int n_mat) {
+    constexpr int RPT = RB * NG;  // rows per team
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nwk = (nb + 7) >> 3;                 // wavefronts per K-team
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nwk = (nb + 15) >> 4;                // wavefronts per K-team
     const int T = (blockDim.x >> 6) / nwk;         // row teams
     const int team = wave / nwk, w = wave - team * nwk;
     const int K = nb * QK_K;
     int8_t *codes = reinterpret_cast<int8_t *>(smem);
     float *dq = reinterpret_cast<float *>(smem + NC * K);
     int *bsum = reinterpret_cast<int *>(dq + NC * nb);
-    float *red = reinterpret_cast<float *>(bsum + NC * nb * 8);  // [T*rows_per_team][nwk][NC]
+    float *red = reinterpret_cast<float *>(bsum + NC * nb * 8);  // [T*RPT][nwk][NC], K-teams of > 1 wave
 
-    const int b = 8 * w + (lane >> 3), j = lane & 7, g = j >> 1, h = j & 1;
+    const int b = 16 * w + (lane >> 2), i = lane & 3;
     const bool valid = b < nb;
-    const int rw0 = blockIdx.x * T * rows_per_team;  // first row of the workgroup
-    const int r0 = rw0 + team * rows_per_team;
-    const int r1 = min(rows, r0 + rows_per_team);
+    const int rw0 = blockIdx.x * T * RPT;  // first row of the workgroup (uniform)
+    const int r0 = rw0 + team * RPT;       // first row of the team (uniform)
+    const int r1 = min(rows, r0 + RPT);
 
-    // Branch-free weight loads: rows past the tile and lanes past the row
-    // re-read a valid block (clamped index) and contribute zero (their
-    // activation codes and scale are zero).
-    const uint8_t *wbc = W + (int64_t)min(b, nb - 1) * Q4K_BYTES;
-    const int rlast = min(max(r0, r1 - 1), rows - 1);  // a team past the last row loads row rows-1, computes nothing
-    uint4 hdr[RB], q[RB], hdr2[RB], q2[RB];
-    auto load_group = [&](int rg, uint4 *hd, uint4 *qq) {
+    // Branch-free weight loads from a uniform row base: rows past the tile and
+    // lanes past the row re-read a valid block (clamped index) and contribute
+    // zero (their activation codes and scale are zero); a team past the last
+    // row loads row rows-1 and computes nothing.
+    const uint32_t boff = (uint32_t)min(b, nb - 1) * Q4K_BYTES;
+    const uint32_t qoff = boff + 16 + 32 * i;
+    const int rlast = min(max(r0, r1 - 1), rows - 1);
+    uint4 hdr[NG][RB], qa[NG][RB], qb[NG][RB];
+    auto load_all = [&]() {
 #pragma unroll
-        for (int rr = 0; rr < RB; rr++) {
-            const uint8_t *p = wbc + (int64_t)min(rg + rr, rlast) * w_row_bytes;
-            hd[rr] = ld16(p);
-            qq[rr] = ld16(p + 16 + 16 * j);
-        }
+        for (int gi = 0; gi < NG; gi++)
+#pragma unroll
+            for (int rr = 0; rr < RB; rr++) {
+                const uint8_t *rowp = W + (int64_t)min(r0 + gi * RB + rr, rlast) * w_row_bytes;
+                hdr[gi][rr] = ld16(rowp + boff);
+                qa[gi][rr] = ld16(rowp + qoff);
+                qb[gi][rr] = ld16(rowp + qoff + 16);
+            }
     };
     // Activations first (their wait then does not cover the weight loads),
-    // then the first two weight groups, then quantization into LDS.
+    // then ALL of the team's weight rows (NG groups of RB rows in flight at
+    // once), then the activation image in LDS.  Quantization tasks are 16
+    // elements; wavefronts without a task skip it.
+    const int total = NC * nb * 16;
+    const bool qwave = wave * 64 < total;
     if (FUSEQ) {
         const float *x = reinterpret_cast<const float *>(act);
         const int64_t xs = act_row_bytes / 4;
-        const int total = NC * nb * 16;
-        const XTask t0 = quant_q8K_load(x, xs, ncols, nb, total, threadIdx.x);
-        load_group(r0, hdr, q);
-        if (r0 + RB < r1) load_group(r0 + RB, hdr2, q2);
-        quant_q8K_store(t0, nb, n_mat, total, threadIdx.x, codes, dq, bsum);
+        XTask t0;
+        if (qwave) t0 = quant_q8K_load(x, xs, ncols, nb, total, threadIdx.x);
+        load_all();
+        if (qwave) quant_q8K_store(t0, nb, n_mat, total, threadIdx.x, codes, dq, bsum);
         for (int base = blockDim.x; base < total; base += blockDim.x) {
+            if (base + wave * 64 >= total) break;
             const XTask t = quant_q8K_load(x, xs, ncols, nb, total, base + threadIdx.x);
             quant_q8K_store(t, nb, n_mat, total, base + threadIdx.x, codes, dq, bsum);
         }
     } else {
-        load_group(r0, hdr, q);
-        if (r0 + RB < r1) load_group(r0 + RB, hdr2, q2);
-        load_q8K_lds(act, act_row_bytes, ncols, NC, nb, codes, dq, bsum);
-    }
-    __syncthreads();
-    Q4KAct a[NC];
-#pragma unroll
-    for (int c = 0; c < NC; c++) {
-        if (valid) {
-            const int8_t *cb = codes + (int64_t)c * K + b * QK_K;
-            a[c].lo = *reinterpret_cast<const uint4 *>(cb + 64 * g + 16 * h);
-            a[c].hi = *reinterpret_cast<const uint4 *>(cb + 64 * g + 32 + 16 * h);
-            a[c].bp = bsum[(c * nb + b) * 8 + j];
-            a[c].d = dq[c * nb + b];
-        } else {
-            a[c] = Q4KAct{make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), 0, 0.0f};
+        Q8KTask t0;
+        if (qwave) t0 = q8K_load(act, act_row_bytes, ncols, nb, total, threadIdx.x);
+        load_all();
+        if (qwave) q8K_store(t0, nb, total, threadIdx.x, codes, dq, bsum);
+        for (int base = blockDim.x; base < total; base += blockDim.x) {
+            const Q8KTask t = q8K_load(act, act_row_bytes, ncols, nb, total, base + threadIdx.x);
+            q8K_store(t, nb, total, base + threadIdx.x, codes, dq, bsum);
         }
     }
+    __syncthreads();
+    // Few columns: the lane's activation codes live in registers.  Four or
+    // more: they are re-read from LDS per row group (register pressure).
+    constexpr bool ACT_LDS = NC >= 4;
+    constexpr int NCR = ACT_LDS ? 1 : NC;
+    auto act_of = [&](int c) {
+        Q4KAct r;
+        if (valid) {
+            const int8_t *cb = codes + (int64_t)c * K + b * QK_K + 64 * i;
+            if (ACT_LDS) asm volatile("" : "+v"(cb));  // keep the loads inside the row loop
+            r.lo0 = *reinterpret_cast<const uint4 *>(cb);
+            r.lo1 = *reinterpret_cast<const uint4 *>(cb + 16);
+            r.hi0 = *reinterpret_cast<const uint4 *>(cb + 32);
+            r.hi1 = *reinterpret_cast<const uint4 *>(cb + 48);
+            r.bs0 = bsum[(c * nb + b) * 8 + 2 * i];
+            r.bs1 = bsum[(c * nb + b) * 8 + 2 * i + 1];
+            r.d = dq[c * nb + b];
+        } else {
+            const uint4 z = make_uint4(0, 0, 0, 0);
+            r = Q4KAct{z, z, z, z, 0, 0, 0.0f};
+        }
+        return r;
+    };
+    Q4KAct areg[NCR];
+#pragma unroll
+    for (int c = 0; c < NCR; c++) areg[c] = act_of(c);
+    const ScaleSel sel = scale_sel(i);
 
-    auto compute_group = [&](int rg, const uint4 *hdr_, const uint4 *q_) {
-        float part[NC][RB];
+    // A row group: decode the RB rows' nibbles and scales once, then one
+    // pass per activation column (dots, scaling, wave reduction per row).
+    auto compute_group = [&](int rg, const uint4 *hdr_, const uint4 *q0_, const uint4 *q1_) {
+        uint32_t lo[RB][8], hi[RB][8];
+        int sc0[RB], sc1[RB], m0[RB], m1[RB];
+        float dw[RB], dmin[RB];
 #pragma unroll
         for (int rr = 0; rr < RB; rr++) {
-            const uint4 hd = hdr_[rr], qq = q_[rr];
-            const float dw = h2f(hd.x), dmin = h2f(hd.x >> 16);
-            const int slo = k4_scale(hd.y, hd.w, 2 * g), shi = k4_scale(hd.y, hd.w, 2 * g + 1);
-            const int mj = k4_min(hd.z, hd.w, j);
-            const uint32_t l0 = qq.x & 0x0f0f0f0f, l1 = qq.y & 0x0f0f0f0f, l2 = qq.z & 0x0f0f0f0f, l3 = qq.w & 0x0f0f0f0f;
-            const uint32_t h0 = (qq.x >> 4) & 0x0f0f0f0f, h1 = (qq.y >> 4) & 0x0f0f0f0f;
-            const uint32_t h2 = (qq.z >> 4) & 0x0f0f0f0f, h3 = (qq.w >> 4) & 0x0f0f0f0f;
+            const uint4 hd = hdr_[rr], x0 = q0_[rr], x1 = q1_[rr];
+            dw[rr] = h2f(hd.x);
+            dmin[rr] = h2f(hd.x >> 16);
+            k4_scales(hd.y, hd.z, hd.w, sel, sc0[rr], sc1[rr], m0[rr], m1[rr]);
+            const uint32_t qv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-            for (int c = 0; c < NC; c++) {
-                const int dl = dot4(l3, a[c].lo.w, dot4(l2, a[c].lo.z, dot4(l1, a[c].lo.y, dot4(l0, a[c].lo.x, 0))));
-                const int dh = dot4(h3, a[c].hi.w, dot4(h2, a[c].hi.z, dot4(h1, a[c].hi.y, dot4(h0, a[c].hi.x, 0))));
-                const int ia = slo * dl + shi * dh;
-                const int im = mj * a[c].bp;
+            for (int k = 0; k < 8; k++) {
+                lo[rr][k] = qv[k] & 0x0f0f0f0f;
+                hi[rr][k] = (qv[k] >> 4) & 0x0f0f0f0f;
+            }
+        }
+#pragma unroll(ACT_LDS ? 1 : NC)
+        for (int c = 0; c < NC; c++) {
+            const Q4KAct ac = ACT_LDS ? act_of(c) : areg[ACT_LDS ? 0 : c];
+            const uint32_t al[8] = {ac.lo0.x, ac.lo0.y, ac.lo0.z, ac.lo0.w, ac.lo1.x, ac.lo1.y, ac.lo1.z, ac.lo1.w};
+            const uint32_t ah[8] = {ac.hi0.x, ac.hi0.y, ac.hi0.z, ac.hi0.w, ac.hi1.x, ac.hi1.y, ac.hi1.z, ac.hi1.w};
+#pragma unroll
+            for (int rr = 0; rr < RB; rr++) {
+                int dl = 0, dh = 0;
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    dl = dot4(lo[rr][k], al[k], dl);
+                    dh = dot4(hi[rr][k], ah[k], dh);
+                }
+                // |dl|, |dh| < 2^16 and scales < 64: 24-bit multiplies are exact
+                const int ia = __mul24(sc0[rr], dl) + __mul24(sc1[rr], dh);
+                const int im = __mul24(m0[rr], ac.bs0) + __mul24(m1[rr], ac.bs1);
                 if (SUBSUMS) {
-                    const int iab = group8_sum(ia), imb = group8_sum(im);
-                    if (j == 0 && valid && c < ncols && rg + rr < r1) {
+                    const int iab = quad_sum_dpp(ia), imb = quad_sum_dpp(im);
+                    if (i == 0 && valid && c < ncols && rg + rr < r1) {
                         int32_t *s = sub + (((int64_t)c * rows + rg + rr) * nb + b) * 2;
                         s[0] = iab;
                         s[1] = imb;
                     }
                 }
-                part[c][rr] = a[c].d * fmaf(dw, (float)ia, -(dmin * (float)im));
+                const float part = ac.d * fmaf(dw[rr], (float)ia, -(dmin[rr] * (float)im));
+                const float tot = wave_sum_dpp(part);
+                if (lane == 0 && rg + rr < r1) {
+                    if (nwk == 1) dst[(int64_t)c * ldd + rg + rr] = tot;
+                    else red[((rg + rr - rw0) * nwk + w) * NC + c] = tot;
+                }
             }
         }
-        constexpr int LPR = 64 / RB;  // lanes per row after the transposed reduction
-#pragma unroll
-        for (int c = 0; c < NC; c++) {
-            const float t = reduce_rows<RB>(part[c], lane);
-            if ((lane & (LPR - 1)) == 0 && rg + lane / LPR < r1)
-                red[((rg - rw0 + lane / LPR) * nwk + w) * NC + c] = t;
-        }
     };
-    // Ping-pong over two register buffers (no copies): the loads of the two
-    // groups ahead stay in flight while a group is computed.
-    for (int rg = r0; rg < r1; rg += 2 * RB) {
-        compute_group(rg, hdr, q);
-        if (rg + RB >= r1) break;
-        if (rg + 2 * RB < r1) load_group(rg + 2 * RB, hdr, q);
-        compute_group(rg + RB, hdr2, q2);
-        if (rg + 3 * RB < r1) load_group(rg + 3 * RB, hdr2, q2);
-    }
+#pragma unroll
+    for (int gi = 0; gi < NG; gi++)
+        if (r0 + gi * RB < r1) compute_group(r0 + gi * RB, hdr[gi], qa[gi], qb[gi]);
+    if (nwk == 1) return;
     __syncthreads();
-    const int nrows = max(0, min(rows, rw0 + T * rows_per_team) - rw0);
+    const int nrows = max(0, min(rows, rw0 + T * RPT) - rw0);
     for (int idx = threadIdx.x; idx < nrows * ncols; idx += blockDim.x) {
         const int rr = idx / ncols, c = idx - rr * ncols;
         float s = 0.0f;
@@ -492,20 +558,21 @@ GEMV_ALL(ghip_gemv_q4_0, gemv_q4_0_impl)
 
 // Q4_K: "_f" kernels take f32 activations (fused Q8_K quantization), the
 // others ready Q8_K rows; "_sub" kernels also store the integer partials.
-#define Q4K_ARGS GEMV_ARGS, int rows_per_team, int n_mat
-#define Q4K_PASS GEMV_PASS, rows_per_team, n_mat
-#define Q4K_INST(NC, RB)                                                                                          \
-    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_c##NC##_r##RB(Q4K_ARGS) {                   \
-        gemv_q4K_impl<NC, false, false, RB>(Q4K_PASS);                                                          \
+#define Q4K_ARGS GEMV_ARGS, int n_mat
+#define Q4K_PASS GEMV_PASS, n_mat
+#define Q4K_INST(NC, RB, NG)                                                                                      \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_c##NC##_r##RB##x##NG(Q4K_ARGS) {            \
+        gemv_q4K_impl<NC, false, false, RB, NG>(Q4K_PASS);                                                      \
     }                                                                                                           \
-    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_sub_c##NC##_r##RB(Q4K_ARGS) {               \
-        gemv_q4K_impl<NC, true, false, RB>(Q4K_PASS);                                                           \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_sub_c##NC##_r##RB##x##NG(Q4K_ARGS) {        \
+        gemv_q4K_impl<NC, true, false, RB, NG>(Q4K_PASS);                                                       \
     }                                                                                                           \
-    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_f_c##NC##_r##RB(Q4K_ARGS) {                 \
-        gemv_q4K_impl<NC, false, true, RB>(Q4K_PASS);                                                           \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_f_c##NC##_r##RB##x##NG(Q4K_ARGS) {          \
+        gemv_q4K_impl<NC, false, true, RB, NG>(Q4K_PASS);                                                       \
     }                                                                                                           \
-    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_f_sub_c##NC##_r##RB(Q4K_ARGS) {             \
-        gemv_q4K_impl<NC, true, true, RB>(Q4K_PASS);                                                            \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_f_sub_c##NC##_r##RB##x##NG(Q4K_ARGS) {      \
+        gemv_q4K_impl<NC, true, true, RB, NG>(Q4K_PASS);                                                        \
     }
-#define Q4K_INST_RB(NC) Q4K_INST(NC, 2) Q4K_INST(NC, 4) Q4K_INST(NC, 8)
+// register row groups (RB rows) x groups in flight (NG)
+#define Q4K_INST_RB(NC) Q4K_INST(NC, 2, 2) Q4K_INST(NC, 2, 4) Q4K_INST(NC, 4, 2) Q4K_INST(NC, 2, 8) Q4K_INST(NC, 4, 4)
 Q4K_INST_RB(1) Q4K_INST_RB(2) Q4K_INST_RB(4) Q4K_INST_RB(8)

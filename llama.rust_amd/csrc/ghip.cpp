@@ -270,10 +270,10 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
 }
 
 // Prefill path (Q4_K, many activation rows): int8 MFMA GEMM, 128 x 128 tiles.
-constexpr size_t kGemmSmem = 128000;  // sizeof(GemmSmem) in ghip_gemm.hip
+constexpr size_t kGemmSmem = 79872;  // sizeof(GemmSmem) in ghip_gemm.hip
 ghip_status run_gemm(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, float *dst,
                      int64_t ldd, int32_t *sub, hipStream_t s) {
-    const unsigned grid = (unsigned)(((p.M + 127) / 128) * ((p.N + 127) / 128));
+    const unsigned grid = (unsigned)(((p.M + 127) / 128) * ((p.N + 63) / 64));
     return ctx->launch(sub ? "ghip_gemm_q4_K_sub" : "ghip_gemm_q4_K", dim3(grid), dim3(256), kGemmSmem, s, (const uint8_t *)w,
                        (int64_t)p.w_row_bytes, (int)p.N, (int)p.nb, act, (int64_t)p.act_row_bytes, (int)p.M, dst,
                        (int64_t)ldd, sub);

@@ -8,20 +8,26 @@
 // and out[m,n] = sum_b  da[m,b] * (dw[n,b] * iacc - dmin[n,b] * imin).
 //
 // q4*sc reaches 945, too wide for an int8 operand, so the scale is split
-// sc = 8*sc_hi + sc_lo (3 bits each) and each weight operand is expanded in
-// registers into two int8 planes q4*sc_hi and q4*sc_lo (both <= 105):
+// sc = 8*sc_hi + sc_lo (3 bits each) and the weights are expanded into two
+// int8 planes q4*sc_hi and q4*sc_lo (both <= 105):
 //   iacc = 8 * (A . W_hi) + (A . W_lo)      -- two int8 MFMA chains, exact int32.
 // imin is a K=16 contraction of mn (<= 63) with bsum16 (|.| <= 2032), both
 // exact in fp16, with sums < 2^24: one v_mfma_f32_32x32x16_f16 per tile, exact.
 //
-// Tiling: a 256-thread workgroup owns a 128-token x 128-row output tile; its
-// four wavefronts each own 64 x 64 (2 x 2 MFMA tiles of 32 x 32).  The
-// activation codes and the raw Q4_K blocks of one super-block are staged in
-// LDS (double-buffered: the global loads of super-block b+1 are in flight
-// while b is multiplied).  K-step ks (32 elements) of super-block b is
-// qs-chunk c = ks/2, low nibbles for even ks and high for odd, so its 32
-// elements share one sub-block scale; lane half h takes bytes 16h..16h+15 of
-// the chunk, and the activation operand takes the same 16 elements.
+// Tiling: a 256-thread workgroup owns a 128-token x 64-row output tile; its
+// four wavefronts each own 32 tokens x 64 rows (two MFMA tiles of 32 x 32).
+// Two workgroups share a CU (78 KB of LDS each, two wavefronts per SIMD) and
+// run out of phase, so one's scaling epilogue overlaps the other's MFMAs.  Per super-block the workgroup expands the
+// weights ONCE into the two planes in LDS (double-buffered: super-block b+1
+// is expanded while b is multiplied); every wavefront streams its own
+// activation codes from global memory (L2) straight into registers, one
+// super-block ahead.
+//
+// K order inside a super-block: 16-element piece p = 2*(2*c + nh) + h holds
+// elements 64c + 32nh + 16h + [0, 16) -- bytes 32c + 16h + [0,16) of the
+// Q4_K qs, low nibbles for nh = 0, high for nh = 1 -- so MFMA K-step
+// ks = 2c + nh (32 elements) lies in one sub-block (scale index ks), and lane
+// half h of both operands carries piece 2*ks + h.
 #include "ghip_common.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -29,16 +35,19 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
-constexpr int BM = 128, BN = 128;
-constexpr int AROW = 256 + 16;  // LDS row stride (bytes) of the activation codes
-constexpr int QROW = 128 + 16;  // LDS row stride (bytes) of the weight nibbles
+constexpr int BM = 128, BN = 64;
+constexpr int PROW = 256;  // LDS row (bytes) of a weight plane; pieces XOR-swizzled by row
+
+// LDS byte offset of 16-element piece p of plane row r: piece p is stored at
+// slot p ^ (r % 16), so the 32 rows a wavefront half reads at one piece index
+// fall in 8 distinct 16-byte bank groups per 8 lanes.
+DEV int piece_off(int r, int p) { return r * PROW + 16 * (p ^ (r & 15)); }
 
 struct GemmStage {
-    uint8_t a[BM * AROW];    // activation codes            [token][k]
-    uint8_t q[BN * QROW];    // Q4_K qs (nibbles)           [row][128]
-    _Float16 bs[BM * 16];    // bsum16 as f16               [token][16]
-    _Float16 mn[BN * 16];    // mn[s] at k = 2s, 2s+1, f16  [row][16]
-    uint8_t sc[BN * 8];      // sub-block scales (6 bits)   [row][8]
+    uint8_t wlo[BN * PROW];  // q4 * sc_lo  [row][k]  (k in piece order)
+    uint8_t whi[BN * PROW];  // q4 * sc_hi  [row][k]
+    _Float16 bs[BM * 16];    // bsum16 as f16                [token][16]
+    _Float16 mn[BN * 16];    // mn[s] at k = 2s, 2s+1, f16   [row][16]
     float da[BM];
     float dw[BN];
     float dmin[BN];
@@ -51,41 +60,6 @@ struct GemmSmem {
 // i = 8*(v/4) + 4*(l/32) + v%4 for v = 0..15.
 DEV int crow(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
 
-// Global prefetch of one super-block for the workgroup, in two register
-// batches that are written to the free LDS stage at different points of the
-// previous super-block's multiply (fewer live registers).
-struct PrefetchA {
-    uint4 a[8];  // activation codes: token tid/2, 128-byte half tid%2
-    uint4 ab;    // bsum16 [8*half .. 8*half+7] of token tid/2
-    uint32_t ad; // activation d
-};
-struct PrefetchW {
-    uint4 w[4];  // weight: row tid/2, qs bytes 64*(tid%2) .. +63
-    uint4 wh;    // header of row tid/2
-};
-
-DEV void prefetch_a(PrefetchA &P, const uint8_t *__restrict__ act, int64_t act_row_bytes, int M, int m0, int b) {
-    const int tid = threadIdx.x;
-    const int r = tid >> 1, half = tid & 1;
-    // clamped rows re-read a valid token; their codes are never stored
-    const int m = min(m0 + r, M - 1);
-    const uint8_t *A = act + (int64_t)m * act_row_bytes + (int64_t)b * Q8K_BYTES;
-#pragma unroll
-    for (int k = 0; k < 8; k++) P.a[k] = ld16(A + 4 + 128 * half + 16 * k);
-    P.ab = ld16(A + 260 + 16 * half);
-    P.ad = ld4(A);
-}
-
-DEV void prefetch_w(PrefetchW &P, const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int n0, int b) {
-    const int tid = threadIdx.x;
-    const int r = tid >> 1, half = tid & 1;
-    const int n = min(n0 + r, N - 1);
-    const uint8_t *blk = W + (int64_t)n * w_row_bytes + (int64_t)b * Q4K_BYTES;
-#pragma unroll
-    for (int k = 0; k < 4; k++) P.w[k] = ld16(blk + 16 + 64 * half + 16 * k);
-    P.wh = ld16(blk);
-}
-
 // c ? v : 0 on a value (a select between two lvalues would take addresses
 // and keep the prefetch arrays out of registers)
 DEV uint4 keep_if(bool c, uint4 v) {
@@ -93,48 +67,96 @@ DEV uint4 keep_if(bool c, uint4 v) {
     return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
 }
 
-DEV void store_a(GemmStage &S, const PrefetchA &P, int M, int m0) {
-    const int tid = threadIdx.x;
-    const int r = tid >> 1, half = tid & 1;
-    const bool mv = m0 + r < M;
-#pragma unroll
-    for (int k = 0; k < 8; k++) *reinterpret_cast<uint4 *>(&S.a[r * AROW + 128 * half + 16 * k]) = keep_if(mv, P.a[k]);
-    // 8 bsum16 values (int16) of this half -> f16
-    const uint4 v = keep_if(mv, P.ab);
-    const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
-    v8h hv;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        hv[2 * e] = (_Float16)(float)(int16_t)(wv[e] & 0xffff);
-        hv[2 * e + 1] = (_Float16)(float)(int16_t)(wv[e] >> 16);
-    }
-    *reinterpret_cast<v8h *>(&S.bs[r * 16 + 8 * half]) = hv;
-    if (half == 0) S.da[r] = mv ? __uint_as_float(P.ad) : 0.0f;
+// Four packed nibbles (one per byte) times a 3-bit scale: each byte product is
+// <= 105, so two 16-bit lane multiplies (v_pk_mul_lo_u16) carry nothing
+// across bytes.
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+DEV uint32_t mul_bytes(uint32_t nib, uint32_t s) {
+    const us2 a = __builtin_bit_cast(us2, nib);
+    const us2 r = a * (us2){(unsigned short)s, (unsigned short)s};
+    return __builtin_bit_cast(uint32_t, r);
 }
 
-DEV void store_w(GemmStage &S, const PrefetchW &P, int N, int n0) {
-    const int tid = threadIdx.x;
-    const int r = tid >> 1, half = tid & 1;
-    const bool nv = n0 + r < N;
+// Weight prefetch of one super-block: thread t owns row t/4 and qs chunk
+// t%4 (32 bytes), and decodes the header; the epilogue data of token t/2
+// (bsum16[8*(t%2) .. +7] and d) come with it.
+struct PrefetchW {
+    uint4 q0, q1;  // qs bytes 32c .. 32c+31 of row t/4, c = t%4
+    uint4 hd;      // header
+    uint4 bsv;     // bsum16[8*(t%2) .. +7] of token t/2
+    uint32_t ad;   // the token's d
+};
+
+// wrow: this thread's weight row (t/4, clamped); arow: its token row (t/2, clamped)
+DEV void prefetch_w(PrefetchW &P, const uint8_t *__restrict__ wrow, const uint8_t *__restrict__ arow, int b) {
+    const int c = threadIdx.x & 3;
+    const uint8_t *blk = wrow + b * Q4K_BYTES;
+    P.q0 = ld16(blk + 16 + 32 * c);
+    P.q1 = ld16(blk + 32 + 32 * c);
+    P.hd = ld16(blk);
+    const uint8_t *A = arow + b * Q8K_BYTES;
+    P.bsv = ld16(A + 260 + 16 * (threadIdx.x & 1));
+    P.ad = ld4(A);
+}
+
+// Expand a prefetched super-block into the planes of stage S.
+DEV void store_w(GemmStage &S, const PrefetchW &P, int N, int n0, int M, int m0) {
+    const int t = threadIdx.x, r = t >> 2, c = t & 3;
+    const int tok = t >> 1, half = t & 1;
+    const bool nv = n0 + r < N, mv = m0 + tok < M;
+    const uint4 hd = keep_if(nv, P.hd);
+    int sc0, mn0, sc1, mn1;
+    scale_min_k4(hd.y, hd.z, hd.w, 2 * c, sc0, mn0);
+    scale_min_k4(hd.y, hd.z, hd.w, 2 * c + 1, sc1, mn1);
+    const uint4 q0 = keep_if(nv, P.q0), q1 = keep_if(nv, P.q1);
+    const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    // pieces of chunk c: (nh, h) -> k offset 64c + 32nh + 16h; bytes 16h.. of the chunk
 #pragma unroll
-    for (int k = 0; k < 4; k++) *reinterpret_cast<uint4 *>(&S.q[r * QROW + 64 * half + 16 * k]) = keep_if(nv, P.w[k]);
-    // header: this half decodes sub-blocks 4*half .. 4*half+3
-    const uint4 hd = keep_if(nv, P.wh);
-    uint32_t scb = 0;
-    v8h mv8;
+    for (int nh = 0; nh < 2; nh++) {
+        const uint32_t slo = nh ? (uint32_t)(sc1 & 7) : (uint32_t)(sc0 & 7);
+        const uint32_t shi = nh ? (uint32_t)(sc1 >> 3) : (uint32_t)(sc0 >> 3);
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-        int sc, m;
-        scale_min_k4(hd.y, hd.z, hd.w, 4 * half + t, sc, m);
-        scb |= (uint32_t)sc << (8 * t);
-        mv8[2 * t] = mv8[2 * t + 1] = (_Float16)(float)m;
+        for (int h = 0; h < 2; h++) {
+            uint32_t lo[4], hi[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t w = qw[4 * h + e];
+                const uint32_t nib = nh ? ((w >> 4) & 0x0f0f0f0f) : (w & 0x0f0f0f0f);
+                lo[e] = mul_bytes(nib, slo);
+                hi[e] = mul_bytes(nib, shi);
+            }
+            const int off = piece_off(r, 4 * c + 2 * nh + h);  // elements 64c + 32nh + 16h ..
+            *reinterpret_cast<uint4 *>(&S.wlo[off]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            *reinterpret_cast<uint4 *>(&S.whi[off]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        }
     }
-    *reinterpret_cast<uint32_t *>(&S.sc[r * 8 + 4 * half]) = scb;
-    *reinterpret_cast<v8h *>(&S.mn[r * 16 + 8 * half]) = mv8;
-    if (half == 0) {
+    // mn of sub-blocks 2c, 2c+1 at k = 4c .. 4c+3
+    const uint32_t m01 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)mn0) * 0x10001u;
+    const uint32_t m23 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)mn1) * 0x10001u;
+    *reinterpret_cast<uint2 *>(&S.mn[r * 16 + 4 * c]) = make_uint2(m01, m23);
+    if (c == 0) {
         S.dw[r] = h2f(hd.x);
         S.dmin[r] = h2f(hd.x >> 16);
     }
+    // token t/2: bsum16[8*half .. +7] -> f16, and d
+    const uint4 bv = keep_if(mv, P.bsv);
+    const uint32_t bw[4] = {bv.x, bv.y, bv.z, bv.w};
+    v8h hv;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        hv[2 * e] = (_Float16)(float)(int16_t)(bw[e] & 0xffff);
+        hv[2 * e + 1] = (_Float16)(float)(int16_t)(bw[e] >> 16);
+    }
+    *reinterpret_cast<v8h *>(&S.bs[tok * 16 + 8 * half]) = hv;
+    if (half == 0) S.da[tok] = mv ? __uint_as_float(P.ad) : 0.0f;
+}
+
+// Piece 2*ks + h of this lane's token (elements 32ks + 16h .. +15) of
+// super-block b; p points at the token's codes + 16h (rows past M re-read a
+// valid token; their results are never stored).
+DEV v4i load_piece(const uint8_t *__restrict__ p, int b, int ks) {
+    const uint4 v = ld16(p + b * Q8K_BYTES + 32 * ks);
+    return v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
 }
 
 template <bool SUBSUMS>
@@ -144,7 +166,7 @@ __device__ __forceinline__ void gemm_q4K_impl(const uint8_t *__restrict__ W, int
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
     GemmSmem &SM = *reinterpret_cast<GemmSmem *>(smem_raw);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave;  // 4 wavefronts along the tokens
     const int li = lane & 31, h = lane >> 5;
 
     // Tile order: the M-tiles of one N-tile are consecutive, and consecutive
@@ -156,139 +178,99 @@ __device__ __forceinline__ void gemm_q4K_impl(const uint8_t *__restrict__ W, int
     if (total % 8 == 0) id = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
     const int m0 = (id % n_tiles_m) * BM;
     const int n0 = (id / n_tiles_m) * BN;
+    const int mrow = m0 + 32 * wm + li;  // this lane's token for the A operand
 
-    v16f out[2][2];
+    v16f out[2];
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int c = 0; c < 2; c++)
 #pragma unroll
-        for (int c = 0; c < 2; c++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) out[a][c][v] = 0.0f;
+        for (int v = 0; v < 16; v++) out[c][v] = 0.0f;
 
-    {
-        PrefetchA PA;
-        PrefetchW PW;
-        prefetch_a(PA, act, act_row_bytes, M, m0, 0);
-        prefetch_w(PW, W, w_row_bytes, N, n0, 0);
-        store_a(SM.st[0], PA, M, m0);
-        store_w(SM.st[0], PW, N, n0);
-    }
+    const uint8_t *wrow = W + (int64_t)min(n0 + (tid >> 2), N - 1) * w_row_bytes;
+    const uint8_t *arow = act + (int64_t)min(m0 + (tid >> 1), M - 1) * act_row_bytes;
+    const uint8_t *apiece = act + (int64_t)min(mrow, M - 1) * act_row_bytes + 4 + 16 * h;
+
+    v4i A[8];
+    PrefetchW P;
+    prefetch_w(P, wrow, arow, 0);
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) A[ks] = load_piece(apiece, 0, ks);
+    store_w(SM.st[0], P, N, n0, M, m0);
     __syncthreads();
 
     for (int b = 0; b < nb; b++) {
+        // multiply super-block b from stage b&1; meanwhile super-block b+1's
+        // weights go to P (then the other stage) and each activation piece,
+        // once its MFMAs are issued, is reloaded with b+1's
         const GemmStage &S = SM.st[b & 1];
-        GemmStage &Snext = SM.st[(b + 1) & 1];
         const bool more = b + 1 < nb;
-        PrefetchA PA;
-        PrefetchW PW;
-        if (more) prefetch_a(PA, act, act_row_bytes, M, m0, b + 1);
-
-        v16i acc_lo[2][2], acc_hi[2][2];
+        if (more) prefetch_w(P, wrow, arow, b + 1);
+        const v16i zi = {};
+        v16i acc_lo[2], acc_hi[2];
 #pragma unroll
-        for (int a = 0; a < 2; a++)
+        for (int ks = 0; ks < 8; ks++) {
 #pragma unroll
-            for (int c = 0; c < 2; c++)
-#pragma unroll
-                for (int v = 0; v < 16; v++) acc_lo[a][c][v] = acc_hi[a][c][v] = 0;
-#pragma unroll
-        for (int c4 = 0; c4 < 4; c4++) {  // qs chunk: sub-blocks 2*c4 (low nibbles), 2*c4+1 (high)
-            // next super-block: activations land in the free stage after chunk 0,
-            // the weight loads are issued then and land after chunk 2
-            if (more && c4 == 1) {
-                store_a(Snext, PA, M, m0);
-                prefetch_w(PW, W, w_row_bytes, N, n0, b + 1);
+            for (int tn = 0; tn < 2; tn++) {
+                const int nl = tn * 32 + li;
+                const int off = piece_off(nl, 2 * ks + h);
+                const v4i blo = *reinterpret_cast<const v4i *>(&S.wlo[off]);
+                const v4i bhi = *reinterpret_cast<const v4i *>(&S.whi[off]);
+                acc_lo[tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[ks], blo, ks ? acc_lo[tn] : zi, 0, 0, 0);
+                acc_hi[tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[ks], bhi, ks ? acc_hi[tn] : zi, 0, 0, 0);
             }
-            if (more && c4 == 3) store_w(Snext, PW, N, n0);
-            v4i A[2][2];                 // [nibble half][m tile]
-#pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const uint8_t *ap = &S.a[(wm * 64 + t * 32 + li) * AROW + 64 * c4 + 16 * h];
-                A[0][t] = *reinterpret_cast<const v4i *>(ap);
-                A[1][t] = *reinterpret_cast<const v4i *>(ap + 32);
-            }
-            v4i Blo[2][2], Bhi[2][2];  // [nibble half][n tile]
-#pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const int nl = wn * 64 + t * 32 + li;
-                const uint4 qv = *reinterpret_cast<const uint4 *>(&S.q[nl * QROW + 32 * c4 + 16 * h]);
-                const uint32_t scp = *reinterpret_cast<const uint16_t *>(&S.sc[nl * 8 + 2 * c4]);
-                const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
-#pragma unroll
-                for (int nh = 0; nh < 2; nh++) {
-                    const uint32_t s = (scp >> (8 * nh)) & 0xff;
-                    const uint32_t slo = s & 7, shi = s >> 3;
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const uint32_t nib = nh ? ((qw[e] >> 4) & 0x0f0f0f0f) : (qw[e] & 0x0f0f0f0f);
-                        Blo[nh][t][e] = (int)(nib * slo);  // bytes stay <= 105: no carries
-                        Bhi[nh][t][e] = (int)(nib * shi);
-                    }
-                }
-            }
-#pragma unroll
-            for (int nh = 0; nh < 2; nh++)
-#pragma unroll
-                for (int tm = 0; tm < 2; tm++)
-#pragma unroll
-                    for (int tn = 0; tn < 2; tn++) {
-                        acc_lo[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[nh][tm], Blo[nh][tn], acc_lo[tm][tn], 0, 0, 0);
-                        acc_hi[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[nh][tm], Bhi[nh][tn], acc_hi[tm][tn], 0, 0, 0);
-                    }
+            if (more) A[ks] = load_piece(apiece, b + 1, ks);
         }
         // ---- min term (K = 16 bsum16 slots, one f16 MFMA per tile) and epilogue
         const int kq = 8 * h;
+        const v8h Am = *reinterpret_cast<const v8h *>(&S.bs[(wm * 32 + li) * 16 + kq]);
+        float dav[16];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const float4 d4 = *reinterpret_cast<const float4 *>(&S.da[wm * 32 + 8 * g + 4 * h]);
+            dav[4 * g] = d4.x;
+            dav[4 * g + 1] = d4.y;
+            dav[4 * g + 2] = d4.z;
+            dav[4 * g + 3] = d4.w;
+        }
+        const v16f zf = {};
 #pragma unroll
         for (int tn = 0; tn < 2; tn++) {
-            const int nl = wn * 64 + tn * 32 + li;
+            const int nl = tn * 32 + li;
             const float dw = S.dw[nl], dmin = S.dmin[nl];
             const v8h Bm = *reinterpret_cast<const v8h *>(&S.mn[nl * 16 + kq]);
-#pragma unroll
-            for (int tm = 0; tm < 2; tm++) {
-                const v8h Am = *reinterpret_cast<const v8h *>(&S.bs[(wm * 64 + tm * 32 + li) * 16 + kq]);
-                v16f zf;
-#pragma unroll
-                for (int v = 0; v < 16; v++) zf[v] = 0.0f;
-                const v16f accm = __builtin_amdgcn_mfma_f32_32x32x16_f16(Am, Bm, zf, 0, 0, 0);
-#pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const float4 da4 = *reinterpret_cast<const float4 *>(&S.da[wm * 64 + tm * 32 + 8 * g + 4 * h]);
-                    const float dav[4] = {da4.x, da4.y, da4.z, da4.w};
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int v = 4 * g + r;
-                        const int iacc = (acc_hi[tm][tn][v] << 3) + acc_lo[tm][tn][v];
-                        const float im = accm[v];
-                        if (SUBSUMS) {
-                            const int ml = wm * 64 + tm * 32 + crow(v, lane);
-                            if (m0 + ml < M && n0 + nl < N) {
-                                int32_t *sp = sub + (((int64_t)(m0 + ml) * N + (n0 + nl)) * nb + b) * 2;
-                                sp[0] = iacc;
-                                sp[1] = (int)im;
-                            }
-                        }
-                        const float t = fmaf(dw, (float)iacc, -(dmin * im));
-                        out[tm][tn][v] = fmaf(dav[r], t, out[tm][tn][v]);
-                    }
-                }
-            }
-        }
-        __syncthreads();
-    }
-    // ---- store
-#pragma unroll
-    for (int tm = 0; tm < 2; tm++)
-#pragma unroll
-        for (int tn = 0; tn < 2; tn++) {
-            const int n = n0 + wn * 64 + tn * 32 + li;
+            const v16f accm = __builtin_amdgcn_mfma_f32_32x32x16_f16(Am, Bm, zf, 0, 0, 0);
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const int m = m0 + wm * 64 + tm * 32 + crow(v, lane);
-                if (m < M && n < N) dst[(int64_t)m * ldd + n] = out[tm][tn][v];
+                const int iacc = (acc_hi[tn][v] << 3) + acc_lo[tn][v];
+                const float im = accm[v];
+                if (SUBSUMS) {
+                    const int ml = wm * 32 + crow(v, lane);
+                    if (m0 + ml < M && n0 + nl < N) {
+                        int32_t *sp = sub + (((int64_t)(m0 + ml) * N + (n0 + nl)) * nb + b) * 2;
+                        sp[0] = iacc;
+                        sp[1] = (int)im;
+                    }
+                }
+                const float t = fmaf(dw, (float)iacc, -(dmin * im));
+                out[tn][v] = fmaf(dav[v], t, out[tn][v]);
             }
         }
+        if (more) store_w(SM.st[(b + 1) & 1], P, N, n0, M, m0);
+        __syncthreads();
+    }
+    // ---- store: for each v, the 32 lanes of a half write 32 consecutive floats
+#pragma unroll
+    for (int tn = 0; tn < 2; tn++) {
+        const int n = n0 + tn * 32 + li;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int m = m0 + wm * 32 + crow(v, lane);
+            if (m < M && n < N) dst[(int64_t)m * ldd + n] = out[tn][v];
+        }
+    }
 }
 
-extern "C" __global__ void __launch_bounds__(256)
+extern "C" __global__ void __launch_bounds__(256, 2)
 ghip_gemm_q4_K(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb, const uint8_t *__restrict__ act,
                int64_t act_row_bytes, int M, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
     gemm_q4K_impl<false>(W, w_row_bytes, N, nb, act, act_row_bytes, M, dst, ldd, sub);
@@ -299,6 +281,5 @@ ghip_gemm_q4_K_sub(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, in
     gemm_q4K_impl<true>(W, w_row_bytes, N, nb, act, act_row_bytes, M, dst, ldd, sub);
 }
 
-static_assert(sizeof(GemmSmem) == 2 * (BM * AROW + BN * QROW + BM * 32 + BN * 32 + BN * 8 + 4 * (BM + 2 * BN)),
-              "LDS layout");
-static_assert(sizeof(GemmSmem) == 128000, "host code launches with this LDS size");
+static_assert(sizeof(GemmSmem) == 2 * (2 * BN * PROW + BM * 32 + BN * 32 + 4 * (BM + 2 * BN)), "LDS layout");
+static_assert(sizeof(GemmSmem) == 79872, "host code launches with this LDS size");

@@ -541,11 +541,29 @@ ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const g
         const char *rs = D == 128 ? "ghip_fa_rowseq_d128" : "ghip_fa_rowseq_d64";
         return ctx->launch(rs, dim3((unsigned)((T * H + 3) / 4)), dim3(256), 0, s, p);
     }
+    if (T == 1) {
+        // single-query split-KV route: the bandwidth-bound vector kernel, with
+        // enough key slices to give every CU several workgroups
+        int ns = std::max(1, std::min((S + 127) / 128, (env_int("GHIP_FA_DECODE_WGS", 512) + H_kv - 1) / H_kv));
+        int ch = (S + ns - 1) / ns;
+        ns = std::max(1, (S + ch - 1) / ch);
+        const size_t pb = (size_t)H * ns * (2 + D) * sizeof(float);
+        st = ctx->workspace(pb, s, &ws);
+        if (st != GHIP_STATUS_SUCCESS) return st;
+        p.part = (float *)ws;
+        p.nsplit = ns;
+        p.chunk = ch;
+        const char *dec = D == 128 ? "ghip_fa_decode_d128" : "ghip_fa_decode_d64";
+        st = ctx->launch(dec, dim3(H_kv, ns), dim3(256), 0, s, p);
+        if (st != GHIP_STATUS_SUCCESS) return st;
+        return ctx->launch("ghip_fa_merge", dim3((unsigned)H), dim3(256), 0, s, (const float *)ws, p.sinks,
+                           (float *)dst->data, 1, H, ns, D);
+    }
     const char *fwd = D == 128 ? "ghip_fa_fwd_d128" : "ghip_fa_fwd_d64";
     st = ctx->launch(fwd, dim3(qtiles, H_kv, nsplit), dim3(64 * (H / H_kv)), 0, s, p);
     if (st != GHIP_STATUS_SUCCESS) return st;
     const float *sk = sinks ? (const float *)sinks->data : nullptr;
-    return ctx->launch("ghip_fa_merge", dim3((unsigned)((T * H + 3) / 4)), dim3(256), 0, s, (const float *)ws, sk,
+    return ctx->launch("ghip_fa_merge", dim3((unsigned)(T * H)), dim3(256), 0, s, (const float *)ws, sk,
                        (float *)dst->data, T, H, nsplit, D);
 }
 

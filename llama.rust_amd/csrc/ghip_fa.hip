@@ -130,7 +130,10 @@ __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
                 const int key = 32 * jt + crow32(v, lane);
                 float x = acc[v] * p.scale;
                 if (p.softcap != 0.0f) x = p.softcap * tanhf(x);
-                if (p.mask && tvalid && key < nk) x += slope * h2f(p.mask[(int64_t)t * p.mask_nb1 + k0 + key]);
+                if (p.mask && tvalid && key < nk) {
+                    const float mv = h2f(p.mask[(int64_t)t * p.mask_nb1 + k0 + key]);
+                    x = mv == -__builtin_inff() ? mv : x + slope * mv;
+                }
                 if (key >= nk || !tvalid) x = -__builtin_inff();
                 s[jt][v] = x;
             }
@@ -207,46 +210,241 @@ __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
     }
 }
 
-// Merge the per-slice partials of one (query, head) row in slice order
-// (reduce_partials, flash_attn.rs:779-835), add the sink logit, normalize.
-// One wavefront per row; lanes own output columns.
+// Single-query decode over a long cache (the reference's split-KV route,
+// flash_attn.rs:779-862): grid (H_kv, nsplit); a 256-thread workgroup takes
+// one KV head, its G = H / H_kv query heads and one slice of the keys, and
+// writes the slice's (M, S, unnormalized O) partial per head for
+// ghip_fa_merge.  It is bound by reading K and V once, so it runs on the
+// vector ALUs with every wavefront streaming its own quarter of the slice in
+// steps of 32 keys, the next step's K and V in flight while one is computed:
+//  * scores: lane pair (2j, 2j+1) holds key j's two 64-dim halves and forms
+//    the G dots with v_dot2 on f16 (q is rounded to f16 as the reference
+//    does, products and sums in fp32);
+//  * softmax: per head, wave max / sum by DPP row operations;
+//  * P V: lane l owns dims 2l, 2l+1 and reads each key's probabilities as
+//    scalars (readlane).
+// The four wavefronts' (M, S, O) meet in LDS at the end.
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+DEV float dpp_max_wave(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+template <int D>
+__device__ __forceinline__ void fa_decode_impl(const FaParams &p) {
+    constexpr int HD = D / 2;        // dims per lane of a key pair
+    constexpr int NL = HD / 8;       // 16-byte K loads per lane per step
+    __shared__ __attribute__((aligned(16))) _Float16 qs[8][D];
+    __shared__ float wst[4][8][2];
+    __shared__ float wo[4][8][D];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int hk = blockIdx.x, z = blockIdx.y;
+    const int G = p.H / p.H_kv;
+    const int k0 = z * p.chunk, k1 = min(p.S, k0 + p.chunk);
+    const int cw = (p.chunk + 3) / 4;
+    const int wk0 = min(k1, k0 + w * cw), wk1 = min(k1, wk0 + cw);  // this wavefront's keys
+    for (int i = tid; i < G * D; i += 256) {
+        const int g = i / D, d = i - g * D;
+        qs[g][d] = __builtin_bit_cast(_Float16, f2h_rn(p.q[(int64_t)(hk * G + g) * p.q_nb2 + d]));
+    }
+    __syncthreads();
+    const uint16_t *kbase = p.k + (int64_t)hk * p.k_nb2;
+    const uint16_t *vbase = p.v + (int64_t)hk * p.v_nb2;
+    const int j = lane >> 1, hf = lane & 1;
+    const int dl = 2 * lane;  // P V dims (D = 128); D = 64 uses lanes < 32
+    const bool dv = dl < D;
+    float Mh[8], Sh[8], o0[8], o1[8];
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+        Mh[g] = -__builtin_inff();
+        Sh[g] = 0.0f;
+        o0[g] = o1[g] = 0.0f;
+    }
+    uint4 kq[NL];
+    uint32_t vq[32];
+    auto load_step = [&](int kb, uint4 *kk, uint32_t *vv) {
+        const int key = min(kb + j, wk1 - 1);
+        const uint8_t *kr = (const uint8_t *)(kbase + (int64_t)key * p.k_nb1) + hf * HD * 2;
+#pragma unroll
+        for (int l = 0; l < NL; l++) kk[l] = ld16(kr + 16 * l);
+#pragma unroll
+        for (int jj = 0; jj < 32; jj++) {
+            const int kj = min(kb + jj, wk1 - 1);
+            vv[jj] = dv ? ld4((const uint8_t *)(vbase + (int64_t)kj * p.v_nb1 + dl)) : 0u;
+        }
+    };
+    if (wk0 < wk1) load_step(wk0, kq, vq);
+    for (int kb = wk0; kb < wk1; kb += 32) {
+        const int nk = min(32, wk1 - kb);
+        // scores of key kb + j for the G heads
+        float sg[8];
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            float acc = 0.0f;
+            if (g < G) {
+#pragma unroll
+                for (int l = 0; l < NL; l++) {
+                    const uint4 qv = *reinterpret_cast<const uint4 *>(&qs[g][hf * HD + 8 * l]);
+                    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2v, kq[l].x), __builtin_bit_cast(h2v, qv.x), acc, false);
+                    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2v, kq[l].y), __builtin_bit_cast(h2v, qv.y), acc, false);
+                    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2v, kq[l].z), __builtin_bit_cast(h2v, qv.z), acc, false);
+                    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2v, kq[l].w), __builtin_bit_cast(h2v, qv.w), acc, false);
+                }
+            }
+            sg[g] = acc;
+        }
+        const uint32_t *vcur = vq;
+        uint32_t vnext[32];
+        uint4 knext[NL];
+        const bool more = kb + 32 < wk1;
+        if (more) load_step(kb + 32, knext, vnext);
+        const bool live = j < nk;
+        const float mk = (p.mask && live) ? h2f(p.mask[kb + j]) : 0.0f;
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            if (g >= G) continue;
+            float x = sg[g] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sg[g]), 0xB1, 0xF, 0xF, false));
+            x *= p.scale;
+            if (p.softcap != 0.0f) x = p.softcap * tanhf(x);
+            x += head_slope(p, hk * G + g) * mk;
+            if (!live || mk == -__builtin_inff()) x = -__builtin_inff();  // masked keys are skipped outright
+            const float m = dpp_max_wave(x);
+            const float mn = fmaxf(Mh[g], m);
+            float pj = 0.0f, alpha = 1.0f;
+            if (mn != -__builtin_inff()) {
+                alpha = __expf(Mh[g] - mn);  // 0 when Mh was -inf
+                pj = __expf(x - mn);         // 0 for masked keys
+                Mh[g] = mn;
+            }
+            Sh[g] = Sh[g] * alpha + 0.5f * wave_sum_dpp(pj);  // both lanes of a pair hold key j
+            float a0 = o0[g] * alpha, a1 = o1[g] * alpha;
+#pragma unroll
+            for (int jj = 0; jj < 32; jj++) {
+                const float pk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), 2 * jj));
+                if (pk == 0.0f) continue;  // masked or out-of-range key: its V is never read
+                const uint32_t vvv = vcur[jj];
+                a0 = fmaf(pk, h2f(vvv & 0xffff), a0);
+                a1 = fmaf(pk, h2f(vvv >> 16), a1);
+            }
+            o0[g] = a0;
+            o1[g] = a1;
+        }
+        if (more) {
+#pragma unroll
+            for (int l = 0; l < NL; l++) kq[l] = knext[l];
+#pragma unroll
+            for (int jj = 0; jj < 32; jj++) vq[jj] = vnext[jj];
+        }
+    }
+    // ---- the four wavefronts' partials -> the workgroup's
+    if (lane == 0)
+        for (int g = 0; g < G; g++) {
+            wst[w][g][0] = Mh[g];
+            wst[w][g][1] = Sh[g];
+        }
+    if (dv)
+        for (int g = 0; g < G; g++) {
+            wo[w][g][dl] = o0[g];
+            wo[w][g][dl + 1] = o1[g];
+        }
+    __syncthreads();
+    for (int i = tid; i < G * D; i += 256) {
+        const int g = i / D, d = i - g * D;
+        float M = -__builtin_inff();
+        for (int u = 0; u < 4; u++)
+            if (wst[u][g][1] != 0.0f) M = fmaxf(M, wst[u][g][0]);
+        float S = 0.0f, o = 0.0f;
+        if (M != -__builtin_inff())
+            for (int u = 0; u < 4; u++) {
+                if (wst[u][g][1] == 0.0f) continue;
+                const float e = __expf(wst[u][g][0] - M);
+                S += wst[u][g][1] * e;
+                o += wo[u][g][d] * e;
+            }
+        float *pp = p.part + ((int64_t)(hk * G + g) * p.nsplit + z) * (2 + D);
+        pp[2 + d] = o;
+        if (d == 0) {
+            pp[0] = M;
+            pp[1] = S;
+        }
+    }
+}
+
+// Merge the per-slice partials of one (query, head) row (reduce_partials,
+// flash_attn.rs:779-835): with M = max_z M_z, the row is
+// sum_z O_z e^(M_z - M) / sum_z S_z e^(M_z - M), then the sink logit joins
+// the denominator.  One 256-thread workgroup per row: the slice weights are
+// formed in parallel into LDS, then thread (d, part) sums slices
+// part, part + P, ... of column d with independent loads, and the parts meet
+// in LDS.  DV <= 256.
 extern "C" __global__ void __launch_bounds__(256)
 ghip_fa_merge(const float *__restrict__ part, const float *__restrict__ sinks, float *__restrict__ dst, int T,
               int H, int nsplit, int DV) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= T * H) return;
+    __shared__ float wz[1024];
+    __shared__ float red[256];
+    __shared__ float stat[8];
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int h = row % H;
     const float *pr = part + (int64_t)row * nsplit * (2 + DV);
-    float M = -__builtin_inff(), S = 0.0f;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // DV <= 256
-    for (int z = 0; z < nsplit; z++) {
+    // M = max over non-empty slices
+    float M = -__builtin_inff();
+    for (int z = tid; z < nsplit; z += 256) {
         const float *pz = pr + (int64_t)z * (2 + DV);
-        const float mz = pz[0], sz = pz[1];
-        if (sz == 0.0f) continue;
-        const float mn = fmaxf(M, mz);
-        const float so = __expf(M - mn), sn = __expf(mz - mn);
-        for (int i = 0; i < 4; i++) {
-            const int d = lane + 64 * i;
-            if (d < DV) acc[i] = acc[i] * so + pz[2 + d] * sn;
-        }
-        S = S * so + sz * sn;
-        M = mn;
+        if (pz[1] != 0.0f) M = fmaxf(M, pz[0]);
     }
-    if (sinks) {
-        const float sv = sinks[h];
-        if (sv > M) {
-            const float ms = __expf(M - sv);
-            for (int i = 0; i < 4; i++) acc[i] *= ms;
-            S = S * ms + 1.0f;
-        } else {
-            S = S + __expf(sv - M);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    if (lane == 0) stat[wv] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(stat[0], stat[1]), fmaxf(stat[2], stat[3]));
+    const int P = 256 / DV;  // slice parts per column
+    const int d = tid % DV, pt = tid / DV;
+    float acc = 0.0f, S = 0.0f;
+    for (int z0 = 0; z0 < nsplit; z0 += 1024) {
+        const int nz = min(1024, nsplit - z0);
+        __syncthreads();  // previous round's weights consumed
+        for (int z = tid; z < nz; z += 256) {
+            const float *pz = pr + (int64_t)(z0 + z) * (2 + DV);
+            const float sz = pz[1];
+            const float wgt = (sz != 0.0f && M != -__builtin_inff()) ? __expf(pz[0] - M) : 0.0f;
+            wz[z] = wgt;
+            S += sz * wgt;
+        }
+        __syncthreads();
+        if (pt < P) {
+#pragma unroll 8
+            for (int z = pt; z < nz; z += P) acc = fmaf(pr[(int64_t)(z0 + z) * (2 + DV) + 2 + d], wz[z], acc);
         }
     }
-    const float sinv = S == 0.0f ? 0.0f : 1.0f / S;
-    for (int i = 0; i < 4; i++) {
-        const int d = lane + 64 * i;
-        if (d < DV) dst[(int64_t)row * DV + d] = acc[i] * sinv;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) S += __shfl_xor(S, o, 64);
+    __syncthreads();
+    if (lane == 0) stat[4 + wv] = S;
+    red[tid] = acc;
+    __syncthreads();
+    if (tid < DV) {
+        float o = 0.0f;
+        for (int u = 0; u < P; u++) o += red[u * DV + tid];
+        S = (stat[4] + stat[5]) + (stat[6] + stat[7]);
+        if (sinks) {
+            const float sv = sinks[h];
+            if (sv > M) {
+                const float ms = __expf(M - sv);
+                o *= ms;
+                S = S * ms + 1.0f;
+            } else {
+                S = S + __expf(sv - M);
+            }
+        }
+        const float sinv = S == 0.0f ? 0.0f : 1.0f / S;
+        dst[(int64_t)row * DV + tid] = o * sinv;
     }
 }
 
@@ -352,3 +550,5 @@ extern "C" __global__ void __launch_bounds__(512) ghip_fa_fwd_d128(FaParams p) {
 extern "C" __global__ void __launch_bounds__(512) ghip_fa_fwd_d64(FaParams p) { fa_fwd_impl<64>(p); }
 extern "C" __global__ void __launch_bounds__(256) ghip_fa_rowseq_d128(FaParams p) { fa_rowseq_impl<128>(p); }
 extern "C" __global__ void __launch_bounds__(256) ghip_fa_rowseq_d64(FaParams p) { fa_rowseq_impl<64>(p); }
+extern "C" __global__ void __launch_bounds__(256) ghip_fa_decode_d128(FaParams p) { fa_decode_impl<128>(p); }
+extern "C" __global__ void __launch_bounds__(256) ghip_fa_decode_d64(FaParams p) { fa_decode_impl<64>(p); }

@@ -152,6 +152,64 @@ def gemv_roofline(be, torch, np, n_launch=64):
     return us, alg, wb
 
 
+def q4_0_bench(be, torch, np):
+    """Config 1 (the reference's CPU-runnable case): Q4_0 4096x4096 batch-1
+    MUL_MAT (Q8_0 activation quantization + GEMV), 16 rotating weight copies."""
+    import ghip
+    k = n = 4096
+    rng = np.random.default_rng(0)
+    wf = torch.from_numpy(rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)).cuda()
+    w0 = be.quantize(wf, ghip.Q4_0)
+    del wf
+    ws = [w0] + [w0.clone() for _ in range(31)]  # 32 x 9.4 MB > the 256 MB Infinity Cache
+    x = torch.from_numpy(np.random.default_rng(1).standard_normal((1, k), dtype=np.float32)).cuda()
+    out = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    us = graph_time_us(torch, lambda i: be.mul_mat(ws[i % 32], ghip.Q4_0, k, x, out=out), 64)
+    alg = w0.numel() + k * 4 + n * 4
+    log(f"Q4_0 4096x4096 GEMV op: {us:.2f} us, {alg / us / 1e3:.1f} GB/s")
+    return {"us_op": round(us, 2), "GB/s": round(alg / us / 1e3, 1), "bytes": alg,
+            "frac_hbm": round(alg / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (None when absent)."""
+    path = os.path.join(ROOT, "profiles", "gemv_q4K_4096x14336_b1.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1].strip())
+    except OSError:
+        pass
+    return None
+
+
+def profile_loop(what, n):
+    """Plain launch loops for rocprofv3 runs (no JSON): the dominant GEMV
+    kernel, or the copy kernel used to calibrate FETCH_SIZE / WRITE_SIZE."""
+    import numpy as np
+    import torch
+    import ghip
+    be = ghip.Backend(0)
+    k, nr = 4096, 14336
+    rng = np.random.default_rng(0)
+    wf = torch.from_numpy(rng.standard_normal((nr, k), dtype=np.float32) * np.float32(0.02)).cuda()
+    w0 = be.quantize(wf, ghip.Q4_K)
+    del wf
+    ws = [w0] + [w0.clone() for _ in range(15)]
+    x = torch.from_numpy(np.random.default_rng(1).standard_normal((1, k), dtype=np.float32)).cuda()
+    out = torch.empty((1, nr), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    for i in range(n):
+        if what == "gemv":
+            be.mul_mat(ws[i % 16], ghip.Q4_K, k, x, out=out)
+        else:  # copy: one 33,030,144-byte device-to-device copy per launch
+            ws[(i + 1) % 16].copy_(ws[i % 16])
+    torch.cuda.synchronize()
+    print(f"profile {what}: {n} launches, {w0.numel()} bytes per matrix", file=sys.stderr)
+
+
 def gemm_bench(be, torch, np):
     """Config 3: Q4_K prefill MUL_MAT (Q8_K quantization + int8 MFMA GEMM)."""
     import ghip
@@ -242,7 +300,7 @@ def cpu_baseline(budget_s=12.0):
         O.mul_mat(O.Q4_K, w, k, n, x, 1, nthreads=threads)
         reps += 1
         el = time.perf_counter() - t0
-        if el > budget_s or reps >= 5000:
+        if el > budget_s:
             break
     wb = O.row_size(O.Q4_K, k) * n
     alg = wb + k * 4 + n * 4
@@ -258,7 +316,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the prefill GEMM / MoE / FA lines")
+    ap.add_argument("--profile", choices=["gemv", "copy"], help="launch loop for rocprofv3 (no JSON line)")
+    ap.add_argument("--launches", type=int, default=100)
     args = ap.parse_args()
+    if args.profile:
+        profile_loop(args.profile, args.launches)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "the path shards by weight rows / experts / KV heads, see DESIGN.md", file=sys.stderr)
@@ -292,13 +355,14 @@ def main():
     ach = alg / (us * 1e-6) / 1e9
     log(f"Q4_K 4096x14336 GEMV kernel: {us:.2f} us, {ach:.1f} GB/s ({ach / HBM_PEAK_GBS * 100:.1f}% of HBM)")
     roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "ghip_gemv_q4_K_f_c1 (Q4_K 4096->14336, batch 1, f32 activations, Q8_K quantization fused)",
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+            "kernel": "ghip_gemv_q4_K_f_c1_r2x2 (Q4_K 4096->14336, batch 1, f32 activations, Q8_K quantization fused)",
             "avg_us": round(us, 3), "bytes_per_launch": alg}
     extras = {}
     if not args.no_extras:
         del sets
         torch.cuda.empty_cache()
+        extras["q4_0_gemv_4096"] = q4_0_bench(be, torch, np)
         extras["prefill_gemm_q4K"] = gemm_bench(be, torch, np)
         extras["moe_mxfp4"] = moe_bench(be, torch, np)
         extras["flash_attn_f16kv"] = fa_bench(be, torch, np)

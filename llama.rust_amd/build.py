@@ -33,11 +33,19 @@ def _run(cmd):
     subprocess.run(cmd, check=True)
 
 
+# MFMA results that the epilogue reads with vector ALU ops stay in VGPRs
+# (the AGPR form would add a v_accvgpr_read per element)
+EXTRA_FLAGS = {
+    "ghip_moe": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "ghip_fa": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def build_kernels():
     for k in KERNELS:
         src = os.path.join(CSRC, k + ".hip")
         out = os.path.join(HERE, k + ".hsaco")
-        _run([HIPCC, "--genco", *DEVICE_FLAGS, "-I", CSRC, src, "-o", out])
+        _run([HIPCC, "--genco", *DEVICE_FLAGS, *EXTRA_FLAGS.get(k, []), "-I", CSRC, src, "-o", out])
 
 
 def build_host():

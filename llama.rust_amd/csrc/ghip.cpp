@@ -436,21 +436,31 @@ ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip
     // 32-pair tiles when experts see few pairs each (decode, small batches)
     const int tp = (n_pairs <= 48 * p.n_as || sub || env_int("GHIP_MOE_TILE", 0) == 32) ? 32 : 64;
     const int64_t max_tiles = (n_pairs + tp - 1) / tp + p.n_as;
-    const size_t act_bytes = ((size_t)(p.ne11 * p.n_tokens * p.act_row_bytes) + 255) & ~(size_t)255;
-    const size_t route_bytes = (size_t)(2 + n_pairs + 3 * max_tiles) * 4;
+    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const int64_t act_rows = p.ne11 * p.n_tokens;
+    // workspace: Q8_0 rows | f16 slot codes | f32 scales | routing table | scratch output
+    const size_t act_bytes = up((size_t)(act_rows * p.act_row_bytes));
+    const size_t actf_bytes = up((size_t)act_rows * p.nb * 64);
+    const size_t actd_bytes = up((size_t)act_rows * p.nb * 4);
+    const size_t route_bytes = up((size_t)(2 + n_pairs + 3 * max_tiles) * 4);
     const size_t out_bytes = d ? 0 : (size_t)(n_pairs * p.rows * 4);
     void *ws = nullptr;
-    st = ctx->workspace(act_bytes + ((route_bytes + 255) & ~(size_t)255) + out_bytes, s, &ws);
+    st = ctx->workspace(act_bytes + actf_bytes + actd_bytes + route_bytes + out_bytes, s, &ws);
     if (st != GHIP_STATUS_SUCCESS) return st;
     uint8_t *act = (uint8_t *)ws;
-    int32_t *route = (int32_t *)((uint8_t *)ws + act_bytes);
-    float *dst = d ? (float *)d->data : (float *)((uint8_t *)route + ((route_bytes + 255) & ~(size_t)255));
+    uint16_t *actf = (uint16_t *)((uint8_t *)ws + act_bytes);  // f16 codes
+    float *actd = (float *)((uint8_t *)actf + actf_bytes);
+    int32_t *route = (int32_t *)((uint8_t *)actd + actd_bytes);
+    float *dst = d ? (float *)d->data : (float *)((uint8_t *)route + route_bytes);
     const int64_t dst_nb1 = d ? (int64_t)d->nb[1] / 4 : p.rows;
     const int64_t dst_nb2 = d ? (int64_t)d->nb[2] / 4 : p.rows * p.n_ids;
-    const int64_t act_rows = p.ne11 * p.n_tokens;
     const unsigned qgrid = (unsigned)((act_rows * p.nb * 8 + 255) / 256);
     st = ctx->launch("ghip_quantize_q8_0", dim3(qgrid), dim3(256), 0, s, (const float *)b->data,
                      (int64_t)b->nb[1] / 4, p.K, act_rows, act, p.act_row_bytes);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    const unsigned fgrid = (unsigned)((act_rows * p.nb * 4 + 255) / 256);
+    st = ctx->launch("ghip_moe_act_f16", dim3(fgrid), dim3(256), 0, s, (const uint8_t *)act, p.act_row_bytes,
+                     (int)act_rows, (int)p.nb, actf, actd);
     if (st != GHIP_STATUS_SUCCESS) return st;
     const int64_t ids_nb1 = (int64_t)ids->nb[1] / 4;
     st = ctx->launch("ghip_moe_route", dim3(1), dim3(1024), (unsigned)(2 * p.n_as * 4), s, (const int32_t *)ids->data,
@@ -461,8 +471,9 @@ ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip
     std::string name = std::string("ghip_moe_mxfp4_t") + (tp == 32 ? "32" : "64") + (repack ? "" : "_plain") + (sub ? "_sub" : "");
     const dim3 grid((unsigned)max_tiles, (unsigned)((p.rows + 127) / 128));
     return ctx->launch(name.c_str(), grid, dim3(256), 0, s, (const uint8_t *)as->data, (int64_t)as->nb[1],
-                       (int64_t)as->nb[2], (const uint8_t *)act, p.act_row_bytes, (int)p.ne11, (const int32_t *)route,
-                       (int)n_pairs, (int)p.n_ids, dst, dst_nb1, dst_nb2, (int)p.rows, (int)p.nb, sub);
+                       (int64_t)as->nb[2], (const uint16_t *)actf, (const float *)actd, (int)p.ne11,
+                       (const int32_t *)route, (int)n_pairs, (int)p.n_ids, dst, dst_nb1, dst_nb2, (int)p.rows,
+                       (int)p.nb, sub);
 }
 
 }  // namespace

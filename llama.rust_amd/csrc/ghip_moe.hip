@@ -20,7 +20,6 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int MOE_TR = 128;  // expert rows per workgroup (32 per wavefront)
-constexpr int MOE_KB = 8;    // 32-blocks staged in LDS at a time
 
 DEV int crowm(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
 
@@ -90,24 +89,57 @@ DEV uint32_t kv_pair_f16(int byte) {
     return lo | (hi << 16);
 }
 
+// ---------------------------------------------------------------- activations
+// Q8_0 activation rows -> f16 codes in MFMA K-slot order (exact: |q| <= 128),
+// once per call: actf [row][block][4 pieces][8 f16], piece (m, h2) slot e
+// holding element (e&1)*16 + 8m + 4*h2 + e/2; actd [row][block] = d as f32.
+extern "C" __global__ void __launch_bounds__(256)
+ghip_moe_act_f16(const uint8_t *__restrict__ q8, int64_t q8_row_bytes, int nrows, int nb,
+                 _Float16 *__restrict__ actf, float *__restrict__ actd) {
+    const int64_t task = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (row, block, piece)
+    if (task >= (int64_t)nrows * nb * 4) return;
+    const int piece = (int)(task & 3);
+    const int64_t rb = task >> 2;
+    const int64_t row = rb / nb;
+    const int b = (int)(rb - row * nb);
+    const int m = piece >> 1, hh = piece & 1;
+    const uint8_t *blk = q8 + row * q8_row_bytes + (int64_t)b * Q8_0_BYTES;
+    const uint32_t lo = ld4(blk + 2 + 8 * m + 4 * hh);       // elements 8m+4hh .. +3
+    const uint32_t hi = ld4(blk + 2 + 16 + 8 * m + 4 * hh);  // elements 16+8m+4hh .. +3
+    v8h val;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        val[2 * q] = (_Float16)(float)(int8_t)((lo >> (8 * q)) & 0xff);
+        val[2 * q + 1] = (_Float16)(float)(int8_t)((hi >> (8 * q)) & 0xff);
+    }
+    *reinterpret_cast<v8h *>(actf + (rb * 4 + piece) * 8) = val;
+    if (piece == 0) actd[rb] = h2f(ld2(blk));
+}
+
 // ---------------------------------------------------------------- GEMM
 // grid (tile, row block); 256 threads = 4 wavefronts x 32 expert rows; a tile
 // is NMT x 32 pairs of one expert.  MFMA orientation: C[i = pair][j = row]; a
 // lane owns row j = lane%32 of its wavefront and 16 pairs per 32-pair block.
 // K-slot e of MFMA half m for lane half h2 is element (e&1)*16 + 8m + 4h2 + e/2
 // of the 32-block: byte 8m+4h2+e/2 of the block's qs, low nibble for even e,
-// high for odd.  REPACK selects the reference's rows % 8 == 0 fold
+// high for odd.  The activation operand comes pre-expanded from L2 (one
+// block ahead); the expert row is read in 144-byte windows of 8 blocks (one
+// window ahead); only the nibble LUT and the tile's activation scales live
+// in LDS.  REPACK selects the reference's rows % 8 == 0 fold
 // (fma(dot, e*d, acc), repack.rs:1071) over the plain one (acc += (d*e)*dot,
 // compute.rs:7140).
+constexpr int MOE_WIN = 9;  // 16-byte loads per 8-block window (136 bytes used)
+
 template <int NMT, bool REPACK, bool SUBSUMS>
 __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, int64_t as_nb1, int64_t as_nb2,
-                                               const uint8_t *__restrict__ act, int64_t act_row_bytes, int ne11,
-                                               const int32_t *__restrict__ route, int n_pairs, int n_ids,
+                                               const _Float16 *__restrict__ actf, const float *__restrict__ actd,
+                                               int ne11, const int32_t *__restrict__ route, int n_pairs, int n_ids,
                                                float *__restrict__ dst, int64_t dst_nb1, int64_t dst_nb2, int rows,
                                                int nb, int32_t *__restrict__ sub) {
     constexpr int TP = 32 * NMT;
-    __shared__ __attribute__((aligned(16))) _Float16 As[MOE_KB * 2 * 2 * TP * 8];  // [kb][m][h2][pair][8]
-    __shared__ __attribute__((aligned(16))) float Ds[MOE_KB * TP];                // [kb][pair]
+    __shared__ __attribute__((aligned(16))) float ds_lds[2][8][TP];  // [stage][block][pair] activation scales
+    __shared__ __attribute__((aligned(16))) uint4 a_lds[2][8][4][TP];  // [stage][block][piece][pair] 8 f16 each
+    __shared__ __attribute__((aligned(16))) uint32_t w_lds[2][MOE_TR][MOE_WIN * 4];  // [stage][row][144-byte window]
     __shared__ uint32_t lut[256];
     __shared__ int pairs[TP];
     const int tile = blockIdx.x;
@@ -120,7 +152,87 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
     const bool rvalid = row < rows;
     if (threadIdx.x < TP) pairs[threadIdx.x] = threadIdx.x < np ? route[2 + first + threadIdx.x] : -1;
     lut[threadIdx.x] = kv_pair_f16(threadIdx.x);
+    __syncthreads();
+    // activation row of tile pair pi (null for padding pairs)
+    auto arow_all = [&](int pi) -> const _Float16 * {
+        const int p = pairs[pi];
+        if (p < 0) return nullptr;
+        const int t = p / n_ids, s = p - t * n_ids;
+        return actf + ((int64_t)t * ne11 + (s % ne11)) * nb * 32;
+    };
+    __syncthreads();
     const uint8_t *wrow = as + (int64_t)e * as_nb2 + (int64_t)(rvalid ? row : 0) * as_nb1;
+    const int row_bytes = nb * MXFP4_BYTES;
+
+    // A operand staging: group g's 8 blocks x 4 pieces x TP pairs (16 B each)
+    // -> registers (thread t: pair t % TP, pieces/blocks strided) -> LDS stage
+    constexpr int ACHUNK = 8 * 4 * TP / 256;  // 16-byte chunks per thread per group
+    // the group's activation scales: entry i = c*256 + t is (block i / TP, pair i % TP)
+    constexpr int DCH = 8 * TP / 256;
+    auto prefetch_d = [&](int g, float (&dr)[DCH]) {
+#pragma unroll
+        for (int c = 0; c < DCH; c++) {
+            const int i = c * 256 + threadIdx.x;
+            const int kb = i / TP, pi = i - kb * TP, b = 8 * g + kb;
+            const int p = pairs[pi];
+            float dv = 0.0f;
+            if (p >= 0 && b < nb) {
+                const int tk = p / n_ids, sl = p - tk * n_ids;
+                dv = actd[((int64_t)tk * ne11 + (sl % ne11)) * nb + b];
+            }
+            dr[c] = dv;
+        }
+    };
+    auto store_d = [&](int stage, const float (&dr)[DCH]) {
+#pragma unroll
+        for (int c = 0; c < DCH; c++) {
+            const int i = c * 256 + threadIdx.x;
+            ds_lds[stage][i / TP][i % TP] = dr[c];
+        }
+    };
+    auto prefetch_a = [&](int g, uint4 (&ar)[ACHUNK]) {
+#pragma unroll
+        for (int c = 0; c < ACHUNK; c++) {
+            const int idx = c * 256 + threadIdx.x;  // (block kb, piece, pair)
+            const int pi = idx % TP, rest = idx / TP, piece = rest & 3, kb = rest >> 2;
+            const int b = 8 * g + kb;
+            const _Float16 *src = arow_all(pi);
+            ar[c] = (src && b < nb) ? ld16((const uint8_t *)(src + ((int64_t)b * 4 + piece) * 8)) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto store_a = [&](int stage, const uint4 (&ar)[ACHUNK]) {
+#pragma unroll
+        for (int c = 0; c < ACHUNK; c++) {
+            const int idx = c * 256 + threadIdx.x;
+            const int pi = idx % TP, rest = idx / TP, piece = rest & 3, kb = rest >> 2;
+            a_lds[stage][kb][piece][pi] = ar[c];
+        }
+    };
+    // weight window of group g: bytes 136g .. 136g+143 of each of the
+    // workgroup's 128 rows, copied to LDS (16 B per chunk, clamped at the row
+    // end: the tail blocks past the last full window are read with exact loads)
+    constexpr int WCHUNK = (MOE_TR * MOE_WIN + 255) / 256;
+    const uint8_t *wexp = as + (int64_t)e * as_nb2;
+    auto prefetch_w = [&](int g, uint4 (&wr)[WCHUNK]) {
+#pragma unroll
+        for (int c = 0; c < WCHUNK; c++) {
+            const int idx = c * 256 + threadIdx.x;  // (row, chunk)
+            const int r = idx / MOE_WIN, l = idx - r * MOE_WIN;
+            const int grow = min(blockIdx.y * MOE_TR + r, rows - 1);
+            const int off = min(136 * g + 16 * l, row_bytes - 16);
+            wr[c] = idx < MOE_TR * MOE_WIN ? ld16(wexp + (int64_t)grow * as_nb1 + off) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto store_w = [&](int stage, const uint4 (&wr)[WCHUNK]) {
+#pragma unroll
+        for (int c = 0; c < WCHUNK; c++) {
+            const int idx = c * 256 + threadIdx.x;
+            if (idx < MOE_TR * MOE_WIN) {
+                const int r = idx / MOE_WIN, l = idx - r * MOE_WIN;
+                *reinterpret_cast<uint4 *>(&w_lds[stage][r][4 * l]) = wr[c];
+            }
+        }
+    };
 
     float acc[NMT][16];
 #pragma unroll
@@ -128,95 +240,106 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[mt][v] = 0.0f;
 
-    for (int kb0 = 0; kb0 < nb; kb0 += MOE_KB) {
-        const int nkb = min(MOE_KB, nb - kb0);
-        // this lane's weight bytes for the group (clamped to the last block)
-        uint32_t we[MOE_KB], wq[MOE_KB][2];
+    // one block: dots on the f16 matrix cores, then the reference's fold
+    auto do_block = [&](int b, const float *dsb, uint32_t e8, uint32_t q0, uint32_t q1, const v8h (&a)[NMT][2]) {
+        const float sw = e8m0_half(e8);
+        const uint32_t qm[2] = {q0, q1};
+        v16f c[NMT];
 #pragma unroll
-        for (int kb = 0; kb < MOE_KB; kb++) {
-            const uint8_t *wb = wrow + (int64_t)(kb0 + min(kb, nkb - 1)) * MXFP4_BYTES;
-            we[kb] = wb[0];
-            wq[kb][0] = ld4(wb + 1 + 4 * h2);
-            wq[kb][1] = ld4(wb + 1 + 8 + 4 * h2);
-        }
-        __syncthreads();  // previous group consumed (and pairs / lut visible)
-        // stage the Q8_0 codes of the tile's pairs as f16, in K-slot order
-        for (int c = threadIdx.x; c < TP * nkb * 4; c += blockDim.x) {
-            const int pi = c / (nkb * 4), rest = c - pi * nkb * 4, kb = rest >> 2, q4 = rest & 3;
-            const int m = q4 >> 1, hh = q4 & 1;
-            const int p = pairs[pi];
-            v8h val;
-            float dval = 0.0f;
-            if (p >= 0) {
-                const int t = p / n_ids, s = p - t * n_ids;
-                const uint8_t *blk = act + ((int64_t)t * ne11 + (s % ne11)) * act_row_bytes + (int64_t)(kb0 + kb) * Q8_0_BYTES;
-                const uint32_t lo = ld4(blk + 2 + 8 * m + 4 * hh);       // elements 8m+4hh .. +3
-                const uint32_t hi = ld4(blk + 2 + 16 + 8 * m + 4 * hh);  // elements 16+8m+4hh .. +3
+        for (int m = 0; m < 2; m++) {
+            v8h bw;
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    val[2 * q] = (_Float16)(float)(int8_t)((lo >> (8 * q)) & 0xff);
-                    val[2 * q + 1] = (_Float16)(float)(int8_t)((hi >> (8 * q)) & 0xff);
-                }
-                dval = h2f(ld2(blk));
-            } else {
-#pragma unroll
-                for (int q = 0; q < 8; q++) val[q] = (_Float16)0.0f;
+            for (int q = 0; q < 4; q++) {
+                const uint32_t pr = lut[(qm[m] >> (8 * q)) & 0xff];
+                bw[2 * q] = __builtin_bit_cast(_Float16, (uint16_t)(pr & 0xffff));
+                bw[2 * q + 1] = __builtin_bit_cast(_Float16, (uint16_t)(pr >> 16));
             }
-            if (q4 == 0) Ds[kb * TP + pi] = dval;
-            *reinterpret_cast<v8h *>(&As[(((kb * 2 + m) * 2 + hh) * TP + pi) * 8]) = val;
+#pragma unroll
+            for (int mt = 0; mt < NMT; mt++) {
+                const v16f z = {};
+                c[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mt][m], bw, m ? c[mt] : z, 0, 0, 0);
+            }
         }
-        __syncthreads();
+        // c[mt][v] is the exact int32 block dot of pair mt*32 + crowm(v)
 #pragma unroll
-        for (int kb = 0; kb < MOE_KB; kb++) {
-            if (kb >= nkb) break;
-            const int b = kb0 + kb;
-            const float sw = e8m0_half(we[kb]);
-            v16f c[NMT];
+        for (int mt = 0; mt < NMT; mt++)
 #pragma unroll
-            for (int m = 0; m < 2; m++) {
-                v8h bw;
+            for (int g = 0; g < 4; g++) {
+                const float4 d4 = *reinterpret_cast<const float4 *>(&dsb[mt * 32 + 8 * g + 4 * h2]);
+                const float dd[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const uint32_t pr = lut[(wq[kb][m] >> (8 * q)) & 0xff];
-                    bw[2 * q] = __builtin_bit_cast(_Float16, (uint16_t)(pr & 0xffff));
-                    bw[2 * q + 1] = __builtin_bit_cast(_Float16, (uint16_t)(pr >> 16));
-                }
-#pragma unroll
-                for (int mt = 0; mt < NMT; mt++) {
-                    const v8h a = *reinterpret_cast<const v8h *>(&As[(((kb * 2 + m) * 2 + h2) * TP + mt * 32 + li) * 8]);
-                    if (m == 0) {
-                        v16f z;
-#pragma unroll
-                        for (int v = 0; v < 16; v++) z[v] = 0.0f;
-                        c[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bw, z, 0, 0, 0);
+                for (int r = 0; r < 4; r++) {
+                    const int v = 4 * g + r;
+                    const float dot = c[mt][v];
+                    if (REPACK) {
+                        acc[mt][v] = fmaf(dot, sw * dd[r], acc[mt][v]);
                     } else {
-                        c[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bw, c[mt], 0, 0, 0);
+                        acc[mt][v] = acc[mt][v] + (dd[r] * sw) * dot;
+                    }
+                    if (SUBSUMS && rvalid) {
+                        const int pi = mt * 32 + crowm(v, lane);
+                        if (pi < np) sub[((int64_t)pairs[pi] * rows + row) * nb + b] = (int)dot;
                     }
                 }
             }
-            // c[mt][v] is the exact int32 block dot of pair mt*32 + crowm(v)
+    };
+
+    // full 8-block windows that end inside the row; the rest are tail blocks
+    int ngroups = nb / 8;
+    while (ngroups > 0 && 136 * (ngroups - 1) + 16 * MOE_WIN > row_bytes) ngroups--;
+    const int nga = (nb + 7) / 8;  // activation groups (the tail included)
+    auto a_of = [&](int stage, int kb, v8h (&a)[NMT][2]) {
 #pragma unroll
-            for (int mt = 0; mt < NMT; mt++)
+        for (int mt = 0; mt < NMT; mt++)
 #pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const float4 d4 = *reinterpret_cast<const float4 *>(&Ds[kb * TP + mt * 32 + 8 * g + 4 * h2]);
-                    const float dd[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int v = 4 * g + r;
-                        const float dot = c[mt][v];
-                        if (REPACK) {
-                            acc[mt][v] = fmaf(dot, sw * dd[r], acc[mt][v]);
-                        } else {
-                            acc[mt][v] = acc[mt][v] + (dd[r] * sw) * dot;
-                        }
-                        if (SUBSUMS && rvalid) {
-                            const int pi = mt * 32 + crowm(v, lane);
-                            if (pi < np) sub[((int64_t)pairs[pi] * rows + row) * nb + b] = (int)dot;
-                        }
-                    }
-                }
+            for (int m = 0; m < 2; m++) a[mt][m] = __builtin_bit_cast(v8h, a_lds[stage][kb][2 * m + h2][mt * 32 + li]);
+    };
+    uint4 ar[ACHUNK], wr[WCHUNK];
+    float dr[DCH];
+    const int rl = w * 32 + li;  // this lane's row inside the workgroup
+    prefetch_a(0, ar);
+    prefetch_d(0, dr);
+    if (ngroups > 0) prefetch_w(0, wr);
+    store_a(0, ar);
+    store_d(0, dr);
+    if (ngroups > 0) store_w(0, wr);
+    __syncthreads();
+    for (int g = 0; g < nga; g++) {
+        const int stage = g & 1;
+        const bool amore = g + 1 < nga, wmore = g + 1 < ngroups;
+        if (amore) {
+            prefetch_a(g + 1, ar);
+            prefetch_d(g + 1, dr);
         }
+        if (wmore) prefetch_w(g + 1, wr);
+        if (g < ngroups) {
+            const uint32_t *wl = w_lds[stage][rl];
+#pragma unroll 2
+            for (int kb = 0; kb < 8; kb++) {
+                // block kb of the window: e at byte 17kb, qs at 17kb+1; this lane
+                // half needs qs bytes 4h2.. (m = 0) and 8+4h2.. (m = 1)
+                const int o0 = 17 * kb + 1 + 4 * h2, o1 = o0 + 8;
+                const uint32_t e8 = (wl[(17 * kb) >> 2] >> (8 * ((17 * kb) & 3))) & 0xff;
+                const uint32_t q0 = __builtin_amdgcn_alignbyte(wl[(o0 >> 2) + 1], wl[o0 >> 2], o0 & 3);
+                const uint32_t q1 = __builtin_amdgcn_alignbyte(wl[(o1 >> 2) + 1], wl[o1 >> 2], o1 & 3);
+                v8h a[NMT][2];
+                a_of(stage, kb, a);
+                do_block(8 * g + kb, ds_lds[stage][kb], e8, q0, q1, a);
+            }
+        } else {
+            for (int kb = 0; kb < 8 && 8 * g + kb < nb; kb++) {  // tail blocks: exact loads
+                const uint8_t *wb = wrow + (int64_t)(8 * g + kb) * MXFP4_BYTES;
+                v8h a[NMT][2];
+                a_of(stage, kb, a);
+                do_block(8 * g + kb, ds_lds[stage][kb], wb[0], ld4(wb + 1 + 4 * h2), ld4(wb + 9 + 4 * h2), a);
+            }
+        }
+        if (amore) {
+            store_a(stage ^ 1, ar);
+            store_d(stage ^ 1, dr);
+        }
+        if (wmore) store_w(stage ^ 1, wr);
+        __syncthreads();
     }
     if (!rvalid) return;
 #pragma unroll
@@ -233,10 +356,10 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
 }
 
 #define MOE_ARGS                                                                                              \
-    const uint8_t *__restrict__ as, int64_t as_nb1, int64_t as_nb2, const uint8_t *__restrict__ act,          \
-        int64_t act_row_bytes, int ne11, const int32_t *__restrict__ route, int n_pairs, int n_ids,            \
+    const uint8_t *__restrict__ as, int64_t as_nb1, int64_t as_nb2, const _Float16 *__restrict__ actf,        \
+        const float *__restrict__ actd, int ne11, const int32_t *__restrict__ route, int n_pairs, int n_ids,   \
         float *__restrict__ dst, int64_t dst_nb1, int64_t dst_nb2, int rows, int nb, int32_t *__restrict__ sub
-#define MOE_PASS as, as_nb1, as_nb2, act, act_row_bytes, ne11, route, n_pairs, n_ids, dst, dst_nb1, dst_nb2, rows, nb, sub
+#define MOE_PASS as, as_nb1, as_nb2, actf, actd, ne11, route, n_pairs, n_ids, dst, dst_nb1, dst_nb2, rows, nb, sub
 
 #define MOE_KERNEL(name, NMT, REPACK, SUB) \
     extern "C" __global__ void __launch_bounds__(256) name(MOE_ARGS) { moe_mxfp4_impl<NMT, REPACK, SUB>(MOE_PASS); }

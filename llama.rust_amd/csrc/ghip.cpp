@@ -216,6 +216,13 @@ const char *gemv_base(int wtype) {
     }
 }
 
+// The whole-row decode kernels with the activation image in LDS: Q4_K always;
+// Q6_K for a single activation row (its 14336-wide rows make the per-workgroup
+// quantization of several columns cost more than it saves).
+bool gemv_v2(const MulMatPlan &p) {
+    return p.wtype == GHIP_TYPE_Q4_K || (p.wtype == GHIP_TYPE_Q6_K && p.M == 1);
+}
+
 // Decode path: activation columns in groups of at most 8.  Q4_K reads the f32
 // activations and quantizes them inside the kernel when fused is set.
 ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, int64_t act_rb,
@@ -223,14 +230,14 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     int waves_k;
     if (p.wtype == GHIP_TYPE_Q4_0)
         waves_k = (int)(((p.nb + 1) / 2 + 63) / 64);
-    else if (p.wtype == GHIP_TYPE_Q4_K)
+    else if (gemv_v2(p))
         waves_k = (int)((p.nb + 15) / 16);
     else
         waves_k = (int)((p.nb + 7) / 8);
     if (waves_k > 8) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: ne00 = %lld too large for the decode kernel", (long long)p.K);
-    const bool q4k = p.wtype == GHIP_TYPE_Q4_K;
-    // Q4_K: T row teams share one LDS copy of the quantized activations; a
-    // team's wavefronts hold NG groups of RB rows in flight at once.
+    // K-quants (Q4_K, Q6_K): T row teams share one LDS copy of the quantized
+    // activations; a team's wavefronts hold NG groups of RB rows in flight.
+    const bool q4k = gemv_v2(p);
     const int rb = q4k ? env_int("GHIP_GEMV_RB", 2) : 8;
     const int ng = q4k ? env_int("GHIP_GEMV_NG", 2) : 1;
     if (q4k && !((rb == 2 && (ng == 2 || ng == 4 || ng == 8)) || (rb == 4 && (ng == 2 || ng == 4))))
@@ -242,7 +249,8 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     for (int64_t c0 = 0; c0 < p.M; c0 += 8) {
         const int nc = (int)std::min<int64_t>(8, p.M - c0);
         const int NC = nc == 1 ? 1 : nc == 2 ? 2 : nc <= 4 ? 4 : 8;
-        std::string name = std::string(gemv_base(p.wtype)) + (q4k && fused ? "_f" : "") + (sub ? "_sub" : "") +
+        std::string name = std::string(gemv_base(p.wtype)) + (p.wtype == GHIP_TYPE_Q6_K && q4k ? "_v2" : "") +
+                           (q4k && fused ? "_f" : "") + (sub ? "_sub" : "") +
                            "_c" + std::to_string(NC) + (q4k ? "_r" + std::to_string(rb) + "x" + std::to_string(ng) : std::string());
         int32_t *sub_c = sub;
         if (sub) {
@@ -251,8 +259,8 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
         }
         ghip_status st;
         if (q4k) {
-            // LDS: codes [NC][K] | d [NC][nb] | sub-block sums [NC][nb][8] | partials
-            const size_t shmem = (size_t)NC * p.K + (size_t)NC * p.nb * 4 + (size_t)NC * p.nb * 8 * 4 +
+            // LDS: codes [NC][K] | d [NC][nb] | 16-element sums [NC][nb][16] | partials
+            const size_t shmem = (size_t)NC * p.K + (size_t)NC * p.nb * 4 + (size_t)NC * p.nb * 16 * 4 +
                                  (size_t)rows_per_wg * waves_k * NC * sizeof(float);
             if (shmem > 160 * 1024) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: decode LDS image too large");
             const int n_mat = (int)std::max<int64_t>(0, std::min<int64_t>(nc, p.n_mat - c0));
@@ -319,7 +327,7 @@ ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_ten
         return run_gemm(ctx, p, a->data, (const uint8_t *)act, dst, ldd, sub, s);
     }
     if (p.act_pre) return run_gemv(ctx, p, a->data, (const uint8_t *)b->data, p.act_row_bytes, false, dst, ldd, sub, s);
-    if (p.wtype == GHIP_TYPE_Q4_K)  // quantization fused into the decode kernel
+    if (gemv_v2(p))  // quantization fused into the decode kernel
         return run_gemv(ctx, p, a->data, (const uint8_t *)b->data, (int64_t)b->nb[1], true, dst, ldd, sub, s);
     st = quantize_act(ctx, p, b, act, s);
     if (st != GHIP_STATUS_SUCCESS) return st;

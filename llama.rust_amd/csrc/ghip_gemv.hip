@@ -47,8 +47,8 @@ DEV void finish_rows(const float *red, int r0, int nrows, int ncols, int NC, int
 // Q8_K ONCE per workgroup, by all its lanes, into LDS; each lane then reads
 // the codes of its fixed K position from there.
 //
-// LDS (dynamic): codes [NC][K] int8 | d [NC][nb] f32 | sub-block sums
-// [NC][nb][8] int32 | row partials [T*rows_per_team][W_K][NC] f32.
+// LDS (dynamic): codes [NC][K] int8 | d [NC][nb] f32 | 16-element sums
+// [NC][nb][16] int32 | row partials [T*rows_per_team][W_K][NC] f32.
 // Quantization of the activation rows into the LDS image, bit-identical to
 // ghip_quantize_q8_K: 16 lanes per super-block ("task" = one lane's 16
 // consecutive elements); the signed max-abs is reduced over the 16 lanes with
@@ -116,10 +116,9 @@ DEV void quant_q8K_store(const XTask &t, int nb, int n_mat, int total, int task,
                 ((uint32_t)(q[4 * k + 2] & 0xff) << 16) | ((uint32_t)(q[4 * k + 3] & 0xff) << 24);
         sum += q[4 * k] + q[4 * k + 1] + q[4 * k + 2] + q[4 * k + 3];
     }
-    sum += __shfl_xor(sum, 1, 64);  // a 32-element sub-block is two lanes
     if (live) {
         *reinterpret_cast<uint4 *>(codes + (int64_t)c * nb * QK_K + b * QK_K + 16 * l) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        if ((l & 1) == 0) bsum[(c * nb + b) * 8 + (l >> 1)] = sum;
+        bsum[(c * nb + b) * 16 + l] = sum;  // bsums[l] of block_q8_K
         if (l == 0) dq[c * nb + b] = d;
     }
 }
@@ -139,8 +138,7 @@ DEV Q8KTask q8K_load(const uint8_t *__restrict__ act, int64_t act_row_bytes, int
     if (task < total && c < ncols) {
         const uint8_t *A = act + (int64_t)c * act_row_bytes + (int64_t)b * Q8K_BYTES;
         t.v = ld16(A + 4 + 16 * l);
-        const uint32_t bs = ld4(A + 260 + 4 * (l >> 1));
-        t.sum = (int)(int16_t)(bs & 0xffff) + (int)(int16_t)(bs >> 16);
+        t.sum = (int)(int16_t)ld2(A + 260 + 2 * l);
         t.d = __uint_as_float(ld4(A));
     }
     return t;
@@ -151,7 +149,7 @@ DEV void q8K_store(const Q8KTask &t, int nb, int total, int task, int8_t *codes,
     const int l = task & 15, blk = task >> 4;
     const int c = blk / nb, b = blk - c * nb;
     *reinterpret_cast<uint4 *>(codes + (int64_t)c * nb * QK_K + b * QK_K + 16 * l) = t.v;
-    if ((l & 1) == 0) bsum[(c * nb + b) * 8 + (l >> 1)] = t.sum;
+    bsum[(c * nb + b) * 16 + l] = t.sum;
     if (l == 0) dq[c * nb + b] = t.d;
 }
 
@@ -208,7 +206,7 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
     int8_t *codes = reinterpret_cast<int8_t *>(smem);
     float *dq = reinterpret_cast<float *>(smem + NC * K);
     int *bsum = reinterpret_cast<int *>(dq + NC * nb);
-    float *red = reinterpret_cast<float *>(bsum + NC * nb * 8);  // [T*RPT][nwk][NC], K-teams of > 1 wave
+    float *red = reinterpret_cast<float *>(bsum + NC * nb * 16);  // [T*RPT][nwk][NC], K-teams of > 1 wave
 
     const int b = 16 * w + (lane >> 2), i = lane & 3;
     const bool valid = b < nb;
@@ -277,8 +275,9 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
             r.lo1 = *reinterpret_cast<const uint4 *>(cb + 16);
             r.hi0 = *reinterpret_cast<const uint4 *>(cb + 32);
             r.hi1 = *reinterpret_cast<const uint4 *>(cb + 48);
-            r.bs0 = bsum[(c * nb + b) * 8 + 2 * i];
-            r.bs1 = bsum[(c * nb + b) * 8 + 2 * i + 1];
+            const int *bs16 = bsum + (c * nb + b) * 16 + 4 * i;  // sub-blocks 2i, 2i+1 = 16-groups 4i .. 4i+3
+            r.bs0 = bs16[0] + bs16[1];
+            r.bs1 = bs16[2] + bs16[3];
             r.d = dq[c * nb + b];
         } else {
             const uint4 z = make_uint4(0, 0, 0, 0);
@@ -354,6 +353,185 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
         float s = 0.0f;
         for (int ww = 0; ww < nwk; ww++) s += red[(rr * nwk + ww) * NC + c];
         dst[(int64_t)c * ldd + rw0 + rr] = s;
+    }
+}
+
+// ---------------------------------------------------------------- Q6_K x Q8_K (v2)
+// Same workgroup shape, activation image and reductions as the Q4_K kernel.
+// Lane i of a super-block takes half j = i/2 (elements 128j ..) and the
+// 16-element column hh = i%2 of each of its four quarters q:
+// elements 128j + 32q + 16hh + [0, 16), from ql bytes 64j + 32(q&1) + 16hh
+// (low nibbles for q < 2, high for q >= 2), qh bytes 32j + 16hh (bits 2q,
+// 2q+1) and scale 8j + 2q + hh.  vec_dot_q6_K_q8_K (vec_dot.rs:982-1040):
+// is = sum_g sc_g * (sum q6*q8 - 32 * bsum16_g), out += (d * is) * d8.
+template <int NC, bool SUBSUMS, bool FUSEQ, int RB, int NG>
+__device__ __forceinline__ void gemv_q6K_v2_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
+                                                 int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
+                                                 int ncols, float *__restrict__ dst, int64_t ldd,
+                                                 int32_t *__restrict__ sub, int n_mat) {
+    constexpr int RPT = RB * NG;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nwk = (nb + 15) >> 4;
+    const int T = (blockDim.x >> 6) / nwk;
+    const int team = wave / nwk, w = wave - team * nwk;
+    const int K = nb * QK_K;
+    int8_t *codes = reinterpret_cast<int8_t *>(smem);
+    float *dq = reinterpret_cast<float *>(smem + NC * K);
+    int *bsum = reinterpret_cast<int *>(dq + NC * nb);
+    float *red = reinterpret_cast<float *>(bsum + NC * nb * 16);
+
+    const int b = 16 * w + (lane >> 2), i = lane & 3;
+    const int j = i >> 1, hh = i & 1;
+    const bool valid = b < nb;
+    const int rw0 = blockIdx.x * T * RPT;
+    const int r0 = rw0 + team * RPT;
+    const int r1 = min(rows, r0 + RPT);
+    const uint32_t boff = (uint32_t)min(b, nb - 1) * Q6K_BYTES;
+    const uint32_t o_ql = boff + 64 * j + 16 * hh, o_qh = boff + 128 + 32 * j + 16 * hh;
+    const uint32_t o_sc = boff + 192 + 8 * j, o_d = boff + 208;
+    const int rlast = min(max(r0, r1 - 1), rows - 1);
+    uint4 ql0[NG][RB], ql1[NG][RB], qhv[NG][RB];
+    uint2 scv[NG][RB];
+    uint32_t dv[NG][RB];
+    auto load_all = [&]() {
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++)
+#pragma unroll
+            for (int rr = 0; rr < RB; rr++) {
+                const uint8_t *rowp = W + (int64_t)min(r0 + gi * RB + rr, rlast) * w_row_bytes;
+                ql0[gi][rr] = ld16(rowp + o_ql);
+                ql1[gi][rr] = ld16(rowp + o_ql + 32);
+                qhv[gi][rr] = ld16(rowp + o_qh);
+                scv[gi][rr] = ld8(rowp + o_sc);
+                dv[gi][rr] = ld2(rowp + o_d);
+            }
+    };
+    const int total = NC * nb * 16;
+    const bool qwave = wave * 64 < total;
+    if (FUSEQ) {
+        const float *x = reinterpret_cast<const float *>(act);
+        const int64_t xs = act_row_bytes / 4;
+        XTask t0;
+        if (qwave) t0 = quant_q8K_load(x, xs, ncols, nb, total, threadIdx.x);
+        load_all();
+        if (qwave) quant_q8K_store(t0, nb, n_mat, total, threadIdx.x, codes, dq, bsum);
+        for (int base = blockDim.x; base < total; base += blockDim.x) {
+            if (base + wave * 64 >= total) break;
+            const XTask t = quant_q8K_load(x, xs, ncols, nb, total, base + threadIdx.x);
+            quant_q8K_store(t, nb, n_mat, total, base + threadIdx.x, codes, dq, bsum);
+        }
+    } else {
+        Q8KTask t0;
+        if (qwave) t0 = q8K_load(act, act_row_bytes, ncols, nb, total, threadIdx.x);
+        load_all();
+        if (qwave) q8K_store(t0, nb, total, threadIdx.x, codes, dq, bsum);
+        for (int base = blockDim.x; base < total; base += blockDim.x) {
+            const Q8KTask t = q8K_load(act, act_row_bytes, ncols, nb, total, base + threadIdx.x);
+            q8K_store(t, nb, total, base + threadIdx.x, codes, dq, bsum);
+        }
+    }
+    __syncthreads();
+    // activation codes of this lane (4 quarters x 16) and its four 16-sums x 32
+    struct Q6Act {
+        uint4 y[4];
+        int bs32[4];
+        float d;
+    };
+    constexpr bool ACT_LDS = NC >= 4;
+    constexpr int NCR = ACT_LDS ? 1 : NC;
+    auto act_of = [&](int c) {
+        Q6Act r;
+        if (valid) {
+            const int8_t *cb = codes + (int64_t)c * K + b * QK_K + 128 * j + 16 * hh;
+            if (ACT_LDS) asm volatile("" : "+v"(cb));
+            const int *bs16 = bsum + (c * nb + b) * 16 + 8 * j + hh;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                r.y[q] = *reinterpret_cast<const uint4 *>(cb + 32 * q);
+                r.bs32[q] = 32 * bs16[2 * q];
+            }
+            r.d = dq[c * nb + b];
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                r.y[q] = make_uint4(0, 0, 0, 0);
+                r.bs32[q] = 0;
+            }
+            r.d = 0.0f;
+        }
+        return r;
+    };
+    Q6Act areg[NCR];
+#pragma unroll
+    for (int c = 0; c < NCR; c++) areg[c] = act_of(c);
+
+    auto compute_group = [&](int rg, const uint4 *l0_, const uint4 *l1_, const uint4 *qh_, const uint2 *sc_,
+                             const uint32_t *d_) {
+        uint32_t q6[RB][4][4];
+        int sc[RB][4];
+        float dw[RB];
+#pragma unroll
+        for (int rr = 0; rr < RB; rr++) {
+            const uint32_t la[4] = {l0_[rr].x, l0_[rr].y, l0_[rr].z, l0_[rr].w};
+            const uint32_t lb[4] = {l1_[rr].x, l1_[rr].y, l1_[rr].z, l1_[rr].w};
+            const uint32_t hv[4] = {qh_[rr].x, qh_[rr].y, qh_[rr].z, qh_[rr].w};
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const uint32_t src = (q & 1) ? lb[k] : la[k];
+                    const uint32_t nib = (q & 2) ? ((src >> 4) & 0x0f0f0f0f) : (src & 0x0f0f0f0f);
+                    q6[rr][q][k] = nib | (((hv[k] >> (2 * q)) & 0x03030303) << 4);
+                }
+            // scales 8j + 2q + hh: bytes hh, 2+hh, 4+hh, 6+hh of the 8 loaded
+            const uint32_t s0 = sc_[rr].x, s1 = sc_[rr].y;
+            sc[rr][0] = (int)(int8_t)(s0 >> (8 * hh));
+            sc[rr][1] = (int)(int8_t)(s0 >> (8 * hh + 16));
+            sc[rr][2] = (int)(int8_t)(s1 >> (8 * hh));
+            sc[rr][3] = (int)(int8_t)(s1 >> (8 * hh + 16));
+            dw[rr] = h2f(d_[rr]);
+        }
+#pragma unroll(ACT_LDS ? 1 : NC)
+        for (int c = 0; c < NC; c++) {
+            const Q6Act ac = ACT_LDS ? act_of(c) : areg[ACT_LDS ? 0 : c];
+#pragma unroll
+            for (int rr = 0; rr < RB; rr++) {
+                int is = 0;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint4 y = ac.y[q];
+                    int dqv = dot4(q6[rr][q][0], y.x, 0);
+                    dqv = dot4(q6[rr][q][1], y.y, dqv);
+                    dqv = dot4(q6[rr][q][2], y.z, dqv);
+                    dqv = dot4(q6[rr][q][3], y.w, dqv);
+                    is += sc[rr][q] * (dqv - ac.bs32[q]);
+                }
+                if (SUBSUMS) {
+                    const int isb = quad_sum_dpp(is);
+                    if (i == 0 && valid && c < ncols && rg + rr < r1) sub[((int64_t)c * rows + rg + rr) * nb + b] = isb;
+                }
+                const float part = (dw[rr] * (float)is) * ac.d;
+                const float tot = wave_sum_dpp(part);
+                if (lane == 0 && rg + rr < r1) {
+                    if (nwk == 1) dst[(int64_t)c * ldd + rg + rr] = tot;
+                    else red[((rg + rr - rw0) * nwk + w) * NC + c] = tot;
+                }
+            }
+        }
+    };
+#pragma unroll
+    for (int gi = 0; gi < NG; gi++)
+        if (r0 + gi * RB < r1) compute_group(r0 + gi * RB, ql0[gi], ql1[gi], qhv[gi], scv[gi], dv[gi]);
+    if (nwk == 1) return;
+    __syncthreads();
+    const int nrows = max(0, min(rows, rw0 + T * RPT) - rw0);
+    for (int idx = threadIdx.x; idx < nrows * ncols; idx += blockDim.x) {
+        const int rr = idx / ncols, c = idx - rr * ncols;
+        float sacc = 0.0f;
+        for (int ww = 0; ww < nwk; ww++) sacc += red[(rr * nwk + ww) * NC + c];
+        dst[(int64_t)c * ldd + rw0 + rr] = sacc;
     }
 }
 
@@ -576,3 +754,20 @@ GEMV_ALL(ghip_gemv_q4_0, gemv_q4_0_impl)
 // register row groups (RB rows) x groups in flight (NG)
 #define Q4K_INST_RB(NC) Q4K_INST(NC, 2, 2) Q4K_INST(NC, 2, 4) Q4K_INST(NC, 4, 2) Q4K_INST(NC, 2, 8) Q4K_INST(NC, 4, 4)
 Q4K_INST_RB(1) Q4K_INST_RB(2) Q4K_INST_RB(4) Q4K_INST_RB(8)
+
+// Q6_K (v2): same shapes and naming, "_f" = fused Q8_K quantization
+#define Q6K_INST(NC, RB, NG)                                                                                      \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q6_K_v2_c##NC##_r##RB##x##NG(Q4K_ARGS) {         \
+        gemv_q6K_v2_impl<NC, false, false, RB, NG>(Q4K_PASS);                                                   \
+    }                                                                                                           \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q6_K_v2_sub_c##NC##_r##RB##x##NG(Q4K_ARGS) {     \
+        gemv_q6K_v2_impl<NC, true, false, RB, NG>(Q4K_PASS);                                                    \
+    }                                                                                                           \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q6_K_v2_f_c##NC##_r##RB##x##NG(Q4K_ARGS) {       \
+        gemv_q6K_v2_impl<NC, false, true, RB, NG>(Q4K_PASS);                                                    \
+    }                                                                                                           \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q6_K_v2_f_sub_c##NC##_r##RB##x##NG(Q4K_ARGS) {   \
+        gemv_q6K_v2_impl<NC, true, true, RB, NG>(Q4K_PASS);                                                     \
+    }
+#define Q6K_INST_RB(NC) Q6K_INST(NC, 2, 2) Q6K_INST(NC, 2, 4) Q6K_INST(NC, 4, 2)
+Q6K_INST_RB(1) Q6K_INST_RB(2) Q6K_INST_RB(4) Q6K_INST_RB(8)

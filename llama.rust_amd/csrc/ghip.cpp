@@ -514,7 +514,10 @@ ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const g
     hipStream_t s = (hipStream_t)stream;
     if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
     // slices of the KV range: enough workgroups to fill the GPU, 64-key multiples
-    const int qtiles = (T + 31) / 32;
+    // prefill workgroups hold G * QS wavefronts (G = H / H_kv heads times QS
+    // query tiles of 32) so that every staged K/V tile serves >= 4 of them
+    const int G = H / H_kv, QS = (4 + G - 1) / G;
+    const int qtiles = (T + 32 * QS - 1) / (32 * QS);
     const int max_split = std::max(1, (S + 63) / 64);
     int nsplit = std::max(1, std::min(max_split, (env_int("GHIP_FA_WGS", 512) + qtiles * H_kv - 1) / (qtiles * H_kv)));
     int chunk = ((S + nsplit - 1) / nsplit + 63) / 64 * 64;
@@ -579,7 +582,7 @@ ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const g
                            (float *)dst->data, 1, H, ns, D);
     }
     const char *fwd = D == 128 ? "ghip_fa_fwd_d128" : "ghip_fa_fwd_d64";
-    st = ctx->launch(fwd, dim3(qtiles, H_kv, nsplit), dim3(64 * (H / H_kv)), 0, s, p);
+    st = ctx->launch(fwd, dim3(qtiles, H_kv, nsplit), dim3(64 * G * QS), 0, s, p);
     if (st != GHIP_STATUS_SUCCESS) return st;
     const float *sk = sinks ? (const float *)sinks->data : nullptr;
     return ctx->launch("ghip_fa_merge", dim3((unsigned)(T * H)), dim3(256), 0, s, (const float *)ws, sk,

@@ -7,9 +7,12 @@
 // rows whose keys are all masked give 0; sinks enter the softmax denominator
 // as one extra logit per head.
 //
-// Work layout.  A workgroup owns one KV head hk, 32 query positions and one
-// slice of the KV range; its G wavefronts are the G = H / H_kv query heads
-// that share hk (GQA), so every K/V tile staged in LDS serves G heads.  Per
+// Work layout.  A workgroup owns one KV head hk, 32 * QS query positions and
+// one slice of the KV range; its G * QS wavefronts are the G = H / H_kv query
+// heads that share hk (GQA) times QS = ceil(4 / G) tiles of 32 queries, so
+// every K/V tile staged in LDS serves >= 4 wavefronts.
+// The next tile's K, V and mask values are loaded into registers while the
+// current one is computed.  Per
 // 64-key tile each wavefront computes S^T = K Q^T (keys x queries), which
 // leaves all scores of one query in one lane pair (l, l^32): the row max and
 // row sum need one cross-lane exchange.  O^T += V^T P^T accumulates in 4 x 16
@@ -60,16 +63,24 @@ DEV float head_slope(const FaParams &p, int h) {
 
 template <int D>
 __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
-    __shared__ __attribute__((aligned(16))) _Float16 Ks[FA_BK * (D + FA_KPAD)];   // [key][d]
-    __shared__ __attribute__((aligned(16))) _Float16 Vt[D * (FA_BK + FA_KPAD)];   // [d][key]
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, G = blockDim.x >> 6;
-    const int nthr = blockDim.x;
+    constexpr int KS = D + FA_KPAD, VS = FA_BK + FA_KPAD;
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[FA_BK * KS];  // [key][d]
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[D * VS];      // [d][key]
+    constexpr int NKC = FA_BK * D / 8;           // 16-byte K chunks per tile
+    constexpr int NVB = (FA_BK / 4) * (D / 8);   // 4-key x 8-dim V blocks per tile
+    // a workgroup has at least 4 wavefronts (G * QS >= 4)
+    constexpr int MAXK = (NKC + 255) / 256, MAXV = (NVB + 255) / 256;
+    constexpr float LOG2E = 1.4426950408889634f;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nthr = blockDim.x;
+    const int G = p.H / p.H_kv, QS = (nthr >> 6) / G;  // QS query tiles of 32 per workgroup
     const int qt = blockIdx.x, hk = blockIdx.y, z = blockIdx.z;
-    const int h = hk * G + w;
+    const int h = hk * G + w % G;
     const int li = lane & 31, h2 = lane >> 5;
-    const int t = qt * FA_BQ + li;  // this lane's query position
+    const int t = (qt * QS + w / G) * FA_BQ + li;  // this lane's query position
     const bool tvalid = t < p.T;
     const float slope = head_slope(p, h);
+    // scores are kept in log2 units: s2 = log2(e) * (scale q.k + slope mask)
+    const float sl2 = p.scale * LOG2E, ml2 = slope * LOG2E;
 
     // Q fragment (B operand of S^T = K Q^T): d = 16*kk + 8*h2 + 0..7
     v8h qf[D / 16];
@@ -91,27 +102,98 @@ __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
     const int ke = min(p.S, kb + p.chunk);
     const uint16_t *kbase = p.k + (int64_t)hk * p.k_nb2;
     const uint16_t *vbase = p.v + (int64_t)hk * p.v_nb2;
+    const uint16_t *mrow = p.mask ? p.mask + (int64_t)(tvalid ? t : 0) * p.mask_nb1 : nullptr;
 
+    // Next tile in registers while this one is computed: K chunks, V blocks of
+    // 4 keys x 8 dims (transposed on the way into LDS), and this lane's mask
+    // values (keys 32*jt + 8*gq + 4*h2 + 0..3, the layout of the scores).
+    uint4 kr[MAXK], vr[MAXV][4];
+    uint2 mr[2][4];
+    auto fetch = [&](int k0n) {
+        const int nkn = min(FA_BK, ke - k0n);
+#pragma unroll
+        for (int i = 0; i < MAXK; i++) {
+            const int c = tid + i * nthr;
+            if (c < NKC) {
+                const int key = c / (D / 8), d8 = (c % (D / 8)) * 8;
+                kr[i] = key < nkn ? ld16((const uint8_t *)(kbase + (int64_t)(k0n + key) * p.k_nb1 + d8))
+                                  : make_uint4(0, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < MAXV; i++) {
+            const int b = tid + i * nthr;
+            if (b < NVB) {
+                const int kq = b & 15, d8 = (b >> 4) * 8;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int key = 4 * kq + r;
+                    vr[i][r] = key < nkn ? ld16((const uint8_t *)(vbase + (int64_t)(k0n + key) * p.v_nb1 + d8))
+                                         : make_uint4(0, 0, 0, 0);
+                }
+            }
+        }
+        if (mrow) {
+#pragma unroll
+            for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+                for (int gq = 0; gq < 4; gq++) {
+                    const int key = 32 * jt + 8 * gq + 4 * h2;
+                    if (key + 4 <= nkn) {
+                        mr[jt][gq] = ld8((const uint8_t *)(mrow + k0n + key));
+                    } else {
+                        uint32_t e[4];
+#pragma unroll
+                        for (int r = 0; r < 4; r++) e[r] = key + r < nkn ? mrow[k0n + key + r] : 0u;
+                        mr[jt][gq] = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
+                    }
+                }
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < MAXK; i++) {
+            const int c = tid + i * nthr;
+            if (c < NKC) {
+                const int key = c / (D / 8), d8 = (c % (D / 8)) * 8;
+                *reinterpret_cast<uint4 *>(&Ks[key * KS + d8]) = kr[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < MAXV; i++) {
+            const int b = tid + i * nthr;
+            if (b < NVB) {
+                const int kq = b & 15, d8 = (b >> 4) * 8;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    uint32_t wv[4];
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        wv[r] = e == 0 ? vr[i][r].x : e == 1 ? vr[i][r].y : e == 2 ? vr[i][r].z : vr[i][r].w;
+                    // dims d8+2e (low halves) and d8+2e+1 (high halves) of keys 4kq..4kq+3
+                    const uint2 lo = make_uint2(__builtin_amdgcn_perm(wv[1], wv[0], 0x05040100u),
+                                                __builtin_amdgcn_perm(wv[3], wv[2], 0x05040100u));
+                    const uint2 hi = make_uint2(__builtin_amdgcn_perm(wv[1], wv[0], 0x07060302u),
+                                                __builtin_amdgcn_perm(wv[3], wv[2], 0x07060302u));
+                    *reinterpret_cast<uint2 *>(&Vt[(d8 + 2 * e) * VS + 4 * kq]) = lo;
+                    *reinterpret_cast<uint2 *>(&Vt[(d8 + 2 * e + 1) * VS + 4 * kq]) = hi;
+                }
+            }
+        }
+    };
+
+    if (kb < ke) fetch(kb);
     for (int k0 = kb; k0 < ke; k0 += FA_BK) {
         const int nk = min(FA_BK, ke - k0);
         __syncthreads();  // the previous tile is consumed
-        // K tile -> Ks[key][d]; V tile -> Vt[d][key] (zero past the range)
-        for (int c = threadIdx.x; c < FA_BK * (D / 8); c += nthr) {
-            const int key = c / (D / 8), d8 = (c % (D / 8)) * 8;
-            uint4 kv = make_uint4(0, 0, 0, 0), vv = kv;
-            if (key < nk) {
-                kv = ld16((const uint8_t *)(kbase + (int64_t)(k0 + key) * p.k_nb1 + d8));
-                vv = ld16((const uint8_t *)(vbase + (int64_t)(k0 + key) * p.v_nb1 + d8));
-            }
-            *reinterpret_cast<uint4 *>(&Ks[key * (D + FA_KPAD) + d8]) = kv;
-            const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+        stage();
+        uint2 mc[2][4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                Vt[(d8 + 2 * e) * (FA_BK + FA_KPAD) + key] = __builtin_bit_cast(_Float16, (uint16_t)(vw[e] & 0xffff));
-                Vt[(d8 + 2 * e + 1) * (FA_BK + FA_KPAD) + key] = __builtin_bit_cast(_Float16, (uint16_t)(vw[e] >> 16));
-            }
-        }
+        for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+            for (int gq = 0; gq < 4; gq++) mc[jt][gq] = mr[jt][gq];
         __syncthreads();
+        if (k0 + FA_BK < ke) fetch(k0 + FA_BK);
 
         // scores of this lane: keys 32*jt + crow32(v), query t
         float s[2][16];
@@ -122,21 +204,26 @@ __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
             for (int v = 0; v < 16; v++) acc[v] = 0.0f;
 #pragma unroll
             for (int kk = 0; kk < D / 16; kk++) {
-                const v8h a = *reinterpret_cast<const v8h *>(&Ks[(32 * jt + li) * (D + FA_KPAD) + 16 * kk + 8 * h2]);
+                const v8h a = *reinterpret_cast<const v8h *>(&Ks[(32 * jt + li) * KS + 16 * kk + 8 * h2]);
                 acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[kk], acc, 0, 0, 0);
             }
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const int key = 32 * jt + crow32(v, lane);
-                float x = acc[v] * p.scale;
-                if (p.softcap != 0.0f) x = p.softcap * tanhf(x);
-                if (p.mask && tvalid && key < nk) {
-                    const float mv = h2f(p.mask[(int64_t)t * p.mask_nb1 + k0 + key]);
-                    x = mv == -__builtin_inff() ? mv : x + slope * mv;
+                float x = acc[v] * sl2;
+                if (p.softcap != 0.0f) x = p.softcap * LOG2E * tanhf(acc[v] * p.scale);
+                if (mrow) {
+                    const uint32_t mw = (v & 2) ? mc[jt][v >> 2].y : mc[jt][v >> 2].x;
+                    x = fmaf(ml2, h2f((v & 1) ? mw >> 16 : mw), x);  // -inf for a masked key
                 }
-                if (key >= nk || !tvalid) x = -__builtin_inff();
                 s[jt][v] = x;
             }
+        }
+        if (nk < FA_BK) {
+#pragma unroll
+            for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+                for (int v = 0; v < 16; v++)
+                    if (32 * jt + crow32(v, lane) >= nk) s[jt][v] = -__builtin_inff();
         }
         // online softmax for query t (lanes l and l^32 share it)
         float tmax = -__builtin_inff();
@@ -146,32 +233,28 @@ __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
             for (int v = 0; v < 16; v++) tmax = fmaxf(tmax, s[jt][v]);
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
         const float m_new = fmaxf(m_run, tmax);
-        float alpha = 1.0f;
-        if (m_new == -__builtin_inff()) {
-            // every key so far is masked for this query: nothing accumulates
+        // every key so far masked: m_new = -inf; exponentiate against 0 so
+        // that all probabilities and alpha come out 0
+        const float m_use = m_new == -__builtin_inff() ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        float psum = 0.0f;
 #pragma unroll
-            for (int jt = 0; jt < 2; jt++)
+        for (int jt = 0; jt < 2; jt++)
 #pragma unroll
-                for (int v = 0; v < 16; v++) s[jt][v] = 0.0f;
-        } else {
-            alpha = __expf(m_run - m_new);  // 0 when m_run is -inf
-            float psum = 0.0f;
+            for (int v = 0; v < 16; v++) {
+                const float e = __builtin_amdgcn_exp2f(s[jt][v] - m_use);
+                s[jt][v] = e;
+                psum += e;
+            }
+        psum += __shfl_xor(psum, 32, 64);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        if (__ballot(alpha != 1.0f)) {
 #pragma unroll
-            for (int jt = 0; jt < 2; jt++)
+            for (int dt = 0; dt < D / 32; dt++)
 #pragma unroll
-                for (int v = 0; v < 16; v++) {
-                    const float e = __expf(s[jt][v] - m_new);
-                    s[jt][v] = e;
-                    psum += e;
-                }
-            psum += __shfl_xor(psum, 32, 64);
-            l_run = l_run * alpha + psum;
-            m_run = m_new;
+                for (int v = 0; v < 16; v++) o[dt][v] *= alpha;
         }
-#pragma unroll
-        for (int dt = 0; dt < D / 32; dt++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) o[dt][v] *= alpha;
         // O^T += V^T P^T over the 64 keys: 4 MFMAs of 16 keys per d-tile
 #pragma unroll
         for (int jt = 0; jt < 2; jt++)
@@ -185,8 +268,8 @@ __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
 #pragma unroll
                 for (int dt = 0; dt < D / 32; dt++) {
                     const int d = 32 * dt + li;
-                    const v4h lo = *reinterpret_cast<const v4h *>(&Vt[d * (FA_BK + FA_KPAD) + key0]);
-                    const v4h hi = *reinterpret_cast<const v4h *>(&Vt[d * (FA_BK + FA_KPAD) + key0 + 8]);
+                    const v4h lo = *reinterpret_cast<const v4h *>(&Vt[d * VS + key0]);
+                    const v4h hi = *reinterpret_cast<const v4h *>(&Vt[d * VS + key0 + 8]);
                     v8h a;
 #pragma unroll
                     for (int e = 0; e < 4; e++) { a[e] = lo[e]; a[4 + e] = hi[e]; }
@@ -195,12 +278,12 @@ __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
             }
     }
 
-    // write this slice's partial (M, S, unnormalized O) for query t, head h;
-    // lanes l and l^32 hold complementary d ranges of the same query
+    // write this slice's partial (M in natural-log units, S, unnormalized O)
+    // for query t, head h; lanes l and l^32 hold complementary d ranges
     if (tvalid) {
         float *pp = p.part + (((int64_t)t * p.H + h) * p.nsplit + z) * (2 + D);
         if (h2 == 0) {
-            pp[0] = m_run;
+            pp[0] = m_run * 0.6931471805599453f;
             pp[1] = l_run;
         }
 #pragma unroll

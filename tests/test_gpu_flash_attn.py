@@ -62,6 +62,14 @@ def test_variants(be):
     run(be, 4, 2, 128, 1, 513, sinks=True)
 
 
+@pytest.mark.parametrize("H,Hkv,D,T,S", [(4, 4, 128, 100, 301), (6, 2, 128, 100, 258), (6, 2, 64, 130, 67),
+                                         (8, 1, 128, 64, 150), (7, 1, 64, 96, 333), (16, 2, 128, 200, 1031)])
+def test_head_groups(be, H, Hkv, D, T, S):
+    """Tiled route for every head-group size: workgroups of G heads times
+    ceil(4 / G) query tiles, ragged key counts and ragged query tiles."""
+    run(be, H, Hkv, D, T, S, seed=H + T)
+
+
 def test_fully_masked_rows(be):
     """Rows whose keys are all masked produce zeros (S == 0 -> S_inv = 0)."""
     H, Hkv, D, T, S = 4, 2, 64, 4, 80

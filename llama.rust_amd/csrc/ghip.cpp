@@ -376,12 +376,15 @@ bool plan_fa(ghip_context *ctx, const ghip_tensor *q, const ghip_tensor *k, cons
     if (mask) {
         if (mask->type != GHIP_TYPE_F16 || mask->nb[0] != 2) return bad("mask must be F16 rows (ggml.c:5515)");
         if (mask->ne[0] < k->ne[1] || mask->ne[1] < q->ne[1]) return bad("mask smaller than [S, T]");
+        if ((uint64_t)q->ne[1] * mask->nb[1] >= (1ull << 31)) return bad("mask spans >= 2 GiB");
     }
     if (sinks && (sinks->type != GHIP_TYPE_F32 || sinks->ne[0] < q->ne[2])) return bad("sinks must be F32 [H]");
     if (d->type != GHIP_TYPE_F32 || d->ne[0] != v->ne[0] || d->ne[1] != q->ne[2] || d->ne[2] != q->ne[1] ||
         d->nb[0] != 4 || d->nb[1] != (uint64_t)(4 * d->ne[0]) || d->nb[2] != (uint64_t)(4 * d->ne[0] * d->ne[1]))
         return bad("dst must be contiguous F32 [DV, H, T]");
     if (q->ne[1] > INT32_MAX || k->ne[1] > INT32_MAX) return bad("dimension too large");
+    // the kernels address one KV head with 32-bit byte offsets
+    if ((uint64_t)k->ne[1] * std::max(k->nb[1], v->nb[1]) >= (1ull << 31)) return bad("a KV head spans >= 2 GiB");
     st = GHIP_STATUS_SUCCESS;
     return true;
 }
@@ -516,7 +519,8 @@ ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const g
     // slices of the KV range: enough workgroups to fill the GPU, 64-key multiples
     // prefill workgroups hold G * QS wavefronts (G = H / H_kv heads times QS
     // query tiles of 32) so that every staged K/V tile serves >= 4 of them
-    const int G = H / H_kv, QS = (4 + G - 1) / G;
+    const int G = H / H_kv, W = std::max(4, std::min(8, env_int("GHIP_FA_WAVES", 4)));
+    const int QS = std::max((4 + G - 1) / G, std::min((W + G - 1) / G, 8 / G));
     const int qtiles = (T + 32 * QS - 1) / (32 * QS);
     const int max_split = std::max(1, (S + 63) / 64);
     int nsplit = std::max(1, std::min(max_split, (env_int("GHIP_FA_WGS", 512) + qtiles * H_kv - 1) / (qtiles * H_kv)));
@@ -582,9 +586,12 @@ ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const g
                            (float *)dst->data, 1, H, ns, D);
     }
     const char *fwd = D == 128 ? "ghip_fa_fwd_d128" : "ghip_fa_fwd_d64";
-    st = ctx->launch(fwd, dim3(qtiles, H_kv, nsplit), dim3(64 * G * QS), 0, s, p);
+    st = ctx->launch(fwd, dim3((unsigned)(qtiles * H_kv * nsplit)), dim3(64 * G * QS), 0, s, p);
     if (st != GHIP_STATUS_SUCCESS) return st;
     const float *sk = sinks ? (const float *)sinks->data : nullptr;
+    if (nsplit <= 64)
+        return ctx->launch("ghip_fa_merge_rows", dim3((unsigned)((T * H + 3) / 4)), dim3(256), 0, s,
+                           (const float *)ws, sk, (float *)dst->data, T * H, H, nsplit, D);
     return ctx->launch("ghip_fa_merge", dim3((unsigned)(T * H)), dim3(256), 0, s, (const float *)ws, sk,
                        (float *)dst->data, T, H, nsplit, D);
 }

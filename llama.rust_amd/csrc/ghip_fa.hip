@@ -61,11 +61,9 @@ DEV float head_slope(const FaParams &p, int h) {
     return r;
 }
 
-template <int D>
-__device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
+template <int D, bool SOFTCAP>
+__device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks, _Float16 *Vt) {
     constexpr int KS = D + FA_KPAD, VS = FA_BK + FA_KPAD;
-    __shared__ __attribute__((aligned(16))) _Float16 Ks[FA_BK * KS];  // [key][d]
-    __shared__ __attribute__((aligned(16))) _Float16 Vt[D * VS];      // [d][key]
     constexpr int NKC = FA_BK * D / 8;           // 16-byte K chunks per tile
     constexpr int NVB = (FA_BK / 4) * (D / 8);   // 4-key x 8-dim V blocks per tile
     // a workgroup has at least 4 wavefronts (G * QS >= 4)
@@ -73,7 +71,13 @@ __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
     constexpr float LOG2E = 1.4426950408889634f;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nthr = blockDim.x;
     const int G = p.H / p.H_kv, QS = (nthr >> 6) / G;  // QS query tiles of 32 per workgroup
-    const int qt = blockIdx.x, hk = blockIdx.y, z = blockIdx.z;
+    // 1-D grid over (qt, hk, z), qt fastest.  Workgroups go to the 8 XCDs
+    // round-robin; remap so that each XCD takes a contiguous run of ids and
+    // the query tiles reading one K/V slice share that XCD's L2.
+    const int qtiles = (p.T + FA_BQ * QS - 1) / (FA_BQ * QS);
+    const int nwg = gridDim.x;
+    const int bid = (nwg & 7) ? (int)blockIdx.x : (int)(blockIdx.x & 7) * (nwg >> 3) + (int)(blockIdx.x >> 3);
+    const int qt = bid % qtiles, hk = (bid / qtiles) % p.H_kv, z = bid / (qtiles * p.H_kv);
     const int h = hk * G + w % G;
     const int li = lane & 31, h2 = lane >> 5;
     const int t = (qt * QS + w / G) * FA_BQ + li;  // this lane's query position
@@ -96,7 +100,9 @@ __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
     for (int dt = 0; dt < D / 32; dt++)
 #pragma unroll
         for (int v = 0; v < 16; v++) o[dt][v] = 0.0f;
-    float m_run = -__builtin_inff(), l_run = 0.0f;
+    // m_ref: reference max (log2 units, -inf until the first unmasked key);
+    // mneg = -m_ref, or 0 while unset
+    float m_ref = -__builtin_inff(), mneg = 0.0f, l_run = 0.0f;
 
     const int kb = z * p.chunk;
     const int ke = min(p.S, kb + p.chunk);
@@ -109,45 +115,51 @@ __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
     // values (keys 32*jt + 8*gq + 4*h2 + 0..3, the layout of the scores).
     uint4 kr[MAXK], vr[MAXV][4];
     uint2 mr[2][4];
+#pragma unroll
+    for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+        for (int gq = 0; gq < 4; gq++) mr[jt][gq] = make_uint2(0, 0);
+    // Buffer loads: the resources end at the slice's last key, so rows past
+    // it read as zero; offsets are this thread's fixed part plus a uniform
+    // tile part.  Mask groups that reach past the slice are reloaded with
+    // bound checks when the tail tile is computed.
+    const uint32_t krow = (uint32_t)p.k_nb1 * 2u, vrow = (uint32_t)p.v_nb1 * 2u;
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void *)kbase, 0, (int)(ke * krow), 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void *)vbase, 0, (int)(ke * vrow), 0x00020000);
+    // the mask resource is uniform (rows 0..T-1, the last one ending at the
+    // slice end); this lane's row is part of its offset
+    const uint32_t mrowb = (uint32_t)p.mask_nb1 * 2u;
+    const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.mask ? p.mask : p.k), 0, p.mask ? (int)((uint32_t)(p.T - 1) * mrowb + (uint32_t)ke * 2u) : 0, 0x00020000);
+    // thread parts: K chunk c = tid + i*nthr -> key c / (D/8), dims 8 * (c % (D/8));
+    // V block b = tid + i*nthr -> keys 4 * (b & 15) + r, dims 8 * (b >> 4)
+    const uint32_t kth = (uint32_t)(tid / (D / 8)) * krow + (uint32_t)(tid % (D / 8)) * 16u;
+    const uint32_t vth = (uint32_t)(4 * (tid & 15)) * vrow + (uint32_t)(tid >> 4) * 16u;
+    const uint32_t kstep = (uint32_t)(nthr / (D / 8)) * krow;  // per i
+    const uint32_t vstep = (uint32_t)(nthr >> 4) * 16u;
+    const uint32_t mth = (uint32_t)(tvalid ? t : 0) * mrowb + (uint32_t)(8 * h2);
     auto fetch = [&](int k0n) {
-        const int nkn = min(FA_BK, ke - k0n);
+        const uint32_t kt = (uint32_t)k0n * krow + kth, vt = (uint32_t)k0n * vrow + vth;
 #pragma unroll
-        for (int i = 0; i < MAXK; i++) {
-            const int c = tid + i * nthr;
-            if (c < NKC) {
-                const int key = c / (D / 8), d8 = (c % (D / 8)) * 8;
-                kr[i] = key < nkn ? ld16((const uint8_t *)(kbase + (int64_t)(k0n + key) * p.k_nb1 + d8))
-                                  : make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < MAXK; i++)
+            if (tid + i * nthr < NKC)
+                kr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, kt + i * kstep, 0, 0));
+#pragma unroll
+        for (int i = 0; i < MAXV; i++)
+            if (tid + i * nthr < NVB) {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    vr[i][r] = __builtin_bit_cast(
+                        uint4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vt + i * vstep + r * vrow, 0, 0));
             }
-        }
-#pragma unroll
-        for (int i = 0; i < MAXV; i++) {
-            const int b = tid + i * nthr;
-            if (b < NVB) {
-                const int kq = b & 15, d8 = (b >> 4) * 8;
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int key = 4 * kq + r;
-                    vr[i][r] = key < nkn ? ld16((const uint8_t *)(vbase + (int64_t)(k0n + key) * p.v_nb1 + d8))
-                                         : make_uint4(0, 0, 0, 0);
-                }
-            }
-        }
         if (mrow) {
+            const uint32_t mt = (uint32_t)k0n * 2u + mth;
 #pragma unroll
             for (int jt = 0; jt < 2; jt++)
 #pragma unroll
-                for (int gq = 0; gq < 4; gq++) {
-                    const int key = 32 * jt + 8 * gq + 4 * h2;
-                    if (key + 4 <= nkn) {
-                        mr[jt][gq] = ld8((const uint8_t *)(mrow + k0n + key));
-                    } else {
-                        uint32_t e[4];
-#pragma unroll
-                        for (int r = 0; r < 4; r++) e[r] = key + r < nkn ? mrow[k0n + key + r] : 0u;
-                        mr[jt][gq] = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
-                    }
-                }
+                for (int gq = 0; gq < 4; gq++)
+                    mr[jt][gq] = __builtin_bit_cast(
+                        uint2, __builtin_amdgcn_raw_buffer_load_b64(mrs, mt + 2u * (32 * jt + 8 * gq), 0, 0));
         }
     };
     auto stage = [&]() {
@@ -195,6 +207,21 @@ __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
         __syncthreads();
         if (k0 + FA_BK < ke) fetch(k0 + FA_BK);
 
+        if (nk < FA_BK && mrow) {
+            // tail tile: mask groups reaching past the range, with bound checks
+#pragma unroll
+            for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+                for (int gq = 0; gq < 4; gq++) {
+                    const int key = 32 * jt + 8 * gq + 4 * h2;
+                    if (key + 4 > nk) {
+                        uint32_t e[4];
+#pragma unroll
+                        for (int r = 0; r < 4; r++) e[r] = key + r < nk ? mrow[k0 + key + r] : 0u;
+                        mc[jt][gq] = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
+                    }
+                }
+        }
         // scores of this lane: keys 32*jt + crow32(v), query t
         float s[2][16];
 #pragma unroll
@@ -209,13 +236,12 @@ __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
             }
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                float x = acc[v] * sl2;
-                if (p.softcap != 0.0f) x = p.softcap * LOG2E * tanhf(acc[v] * p.scale);
-                if (mrow) {
-                    const uint32_t mw = (v & 2) ? mc[jt][v >> 2].y : mc[jt][v >> 2].x;
-                    x = fmaf(ml2, h2f((v & 1) ? mw >> 16 : mw), x);  // -inf for a masked key
-                }
-                s[jt][v] = x;
+                // relative to the reference max: x' = s2 - m_ref
+                float x = fmaf(acc[v], sl2, mneg);
+                if (SOFTCAP) x = p.softcap * LOG2E * tanhf(acc[v] * p.scale) + mneg;
+                // mask value (0 without a mask); -inf for a masked key
+                const uint32_t mw = (v & 2) ? mc[jt][v >> 2].y : mc[jt][v >> 2].x;
+                s[jt][v] = fmaf(ml2, h2f((v & 1) ? mw >> 16 : mw), x);
             }
         }
         if (nk < FA_BK) {
@@ -225,36 +251,44 @@ __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
                 for (int v = 0; v < 16; v++)
                     if (32 * jt + crow32(v, lane) >= nk) s[jt][v] = -__builtin_inff();
         }
-        // online softmax for query t (lanes l and l^32 share it)
+        // Online softmax for query t (lanes l and l^32 share it) with a lazy
+        // reference max: probabilities are exp2(s2 - m_ref), and m_ref moves
+        // only when a score exceeds it by more than 8 (P <= 256) or on the
+        // first unmasked key.  O and l are rescaled only then.
         float tmax = -__builtin_inff();
 #pragma unroll
         for (int jt = 0; jt < 2; jt++)
 #pragma unroll
             for (int v = 0; v < 16; v++) tmax = fmaxf(tmax, s[jt][v]);
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float m_new = fmaxf(m_run, tmax);
-        // every key so far masked: m_new = -inf; exponentiate against 0 so
-        // that all probabilities and alpha come out 0
-        const float m_use = m_new == -__builtin_inff() ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        const bool need = tmax > 8.0f || (m_ref == -__builtin_inff() && tmax != -__builtin_inff());
+        if (__ballot(need)) {
+            if (need) {
+                const float alpha = __builtin_amdgcn_exp2f(-tmax);  // o, l are 0 while m_ref is unset
+                m_ref = -mneg + tmax;
+                mneg = -m_ref;
+                l_run *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) o[dt][v] *= alpha;
+#pragma unroll
+                for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) s[jt][v] -= tmax;
+            }
+        }
         float psum = 0.0f;
 #pragma unroll
         for (int jt = 0; jt < 2; jt++)
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const float e = __builtin_amdgcn_exp2f(s[jt][v] - m_use);
+                const float e = __builtin_amdgcn_exp2f(s[jt][v]);
                 s[jt][v] = e;
                 psum += e;
             }
         psum += __shfl_xor(psum, 32, 64);
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-        if (__ballot(alpha != 1.0f)) {
-#pragma unroll
-            for (int dt = 0; dt < D / 32; dt++)
-#pragma unroll
-                for (int v = 0; v < 16; v++) o[dt][v] *= alpha;
-        }
+        l_run += psum;
         // O^T += V^T P^T over the 64 keys: 4 MFMAs of 16 keys per d-tile
 #pragma unroll
         for (int jt = 0; jt < 2; jt++)
@@ -283,7 +317,7 @@ __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
     if (tvalid) {
         float *pp = p.part + (((int64_t)t * p.H + h) * p.nsplit + z) * (2 + D);
         if (h2 == 0) {
-            pp[0] = m_run * 0.6931471805599453f;
+            pp[0] = m_ref * 0.6931471805599453f;
             pp[1] = l_run;
         }
 #pragma unroll
@@ -291,6 +325,16 @@ __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
 #pragma unroll
             for (int v = 0; v < 16; v++) pp[2 + 32 * dt + crow32(v, lane)] = o[dt][v];
     }
+}
+
+template <int D>
+__device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[FA_BK * (D + FA_KPAD)];  // [key][d]
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[D * (FA_BK + FA_KPAD)];  // [d][key]
+    if (p.softcap != 0.0f)
+        fa_fwd_body<D, true>(p, Ks, Vt);
+    else
+        fa_fwd_body<D, false>(p, Ks, Vt);
 }
 
 // Single-query decode over a long cache (the reference's split-KV route,
@@ -467,6 +511,50 @@ __device__ __forceinline__ void fa_decode_impl(const FaParams &p) {
 // formed in parallel into LDS, then thread (d, part) sums slices
 // part, part + P, ... of column d with independent loads, and the parts meet
 // in LDS.  DV <= 256.
+// Few slices per row (prefill): one wavefront per (query, head) row, four
+// rows per workgroup; lane l owns dims l and l + 64.  Slices are folded in
+// order with the same weights exp(M_z - M) as ghip_fa_merge.
+extern "C" __global__ void __launch_bounds__(256)
+ghip_fa_merge_rows(const float *__restrict__ part, const float *__restrict__ sinks, float *__restrict__ dst,
+                   int nrows, int H, int nsplit, int DV) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= nrows) return;
+    const float *pr = part + (int64_t)row * nsplit * (2 + DV);
+    // lane z < nsplit (<= 64) holds slice z's (M_z, S_z)
+    float mz = -__builtin_inff(), sz = 0.0f;
+    if (lane < nsplit) {
+        mz = pr[(int64_t)lane * (2 + DV)];
+        sz = pr[(int64_t)lane * (2 + DV) + 1];
+    }
+    const float M = dpp_max_wave(sz != 0.0f ? mz : -__builtin_inff());
+    const float wz = (sz != 0.0f && M != -__builtin_inff()) ? __expf(mz - M) : 0.0f;
+    float S = wave_sum_dpp(sz * wz);
+    const bool d1 = lane + 64 < DV;
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll 4
+    for (int z = 0; z < nsplit; z++) {
+        const float *pz = pr + (int64_t)z * (2 + DV) + 2;
+        const float wgt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wz), z));
+        if (lane < DV) a0 = fmaf(pz[lane], wgt, a0);
+        if (d1) a1 = fmaf(pz[64 + lane], wgt, a1);
+    }
+    if (sinks) {
+        const float sv = sinks[row % H];
+        if (sv > M) {
+            const float ms = __expf(M - sv);
+            a0 *= ms;
+            a1 *= ms;
+            S = S * ms + 1.0f;
+        } else {
+            S = S + __expf(sv - M);
+        }
+    }
+    const float sinv = S == 0.0f ? 0.0f : 1.0f / S;
+    if (lane < DV) dst[(int64_t)row * DV + lane] = a0 * sinv;
+    if (d1) dst[(int64_t)row * DV + 64 + lane] = a1 * sinv;
+}
+
 extern "C" __global__ void __launch_bounds__(256)
 ghip_fa_merge(const float *__restrict__ part, const float *__restrict__ sinks, float *__restrict__ dst, int T,
               int H, int nsplit, int DV) {

@@ -38,6 +38,7 @@ def _run(cmd):
 EXTRA_FLAGS = {
     "ghip_moe": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "ghip_fa": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "ghip_gemm": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

@@ -277,14 +277,28 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     return GHIP_STATUS_SUCCESS;
 }
 
-// Prefill path (Q4_K, many activation rows): int8 MFMA GEMM, 128 x 128 tiles.
-constexpr size_t kGemmSmem = 79872;  // sizeof(GemmSmem) in ghip_gemm.hip
+// Prefill path (Q4_K, many activation rows): the Q8_K activations are laid
+// out for the GEMM (codes | bsum16 | d, tokens padded to 128), then the int8
+// MFMA GEMM runs on 128 x 128 tiles.
+constexpr size_t kGemmSmem = 116224;  // sizeof(g3::Smem) in ghip_gemm.hip
+size_t gemm_layout_bytes(const MulMatPlan &p) {
+    const size_t Mpad = (size_t)(p.M + 127) / 128 * 128, nbk = (size_t)p.K / 256;
+    return (Mpad * (size_t)p.K + nbk * Mpad * 32 + nbk * Mpad * 4 + 255) & ~(size_t)255;
+}
 ghip_status run_gemm(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, float *dst,
-                     int64_t ldd, int32_t *sub, hipStream_t s) {
-    const unsigned grid = (unsigned)(((p.M + 127) / 128) * ((p.N + 63) / 64));
-    return ctx->launch(sub ? "ghip_gemm_q4_K_sub" : "ghip_gemm_q4_K", dim3(grid), dim3(256), kGemmSmem, s, (const uint8_t *)w,
-                       (int64_t)p.w_row_bytes, (int)p.N, (int)p.nb, act, (int64_t)p.act_row_bytes, (int)p.M, dst,
-                       (int64_t)ldd, sub);
+                     int64_t ldd, int32_t *sub, void *layout_ws, hipStream_t s) {
+    const int64_t Mpad = (p.M + 127) / 128 * 128, K = p.K, nbk = p.K / 256;
+    int8_t *codes = (int8_t *)layout_ws;
+    uint16_t *bsT = (uint16_t *)(codes + Mpad * K);
+    float *dT = (float *)(bsT + nbk * Mpad * 16);
+    const unsigned lgrid = (unsigned)((p.M * nbk + 3) / 4);
+    ghip_status st = ctx->launch("ghip_gemm_act_layout", dim3(lgrid), dim3(256), 0, s, act, (int64_t)p.act_row_bytes,
+                                 (int)p.M, (int)Mpad, (int)nbk, codes, bsT, dT);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    const unsigned grid = (unsigned)(((p.M + 127) / 128) * ((p.N + 127) / 128));
+    return ctx->launch(sub ? "ghip_gemm_q4_K_sub" : "ghip_gemm_q4_K", dim3(grid), dim3(512), kGemmSmem, s,
+                       (const uint8_t *)w, (int64_t)p.w_row_bytes, (int)p.N, (int)p.nb, (const int8_t *)codes,
+                       (const uint16_t *)bsT, (const float *)dT, (int)p.M, (int)Mpad, dst, (int64_t)ldd, sub);
 }
 
 bool use_gemm(const MulMatPlan &p) {
@@ -304,7 +318,8 @@ ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_ten
     if (!d && !sub && !act_out) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: no output");
     // workspace: [quantized activations | f32 scratch output when only sub-sums are wanted]
     const size_t act_bytes = p.act_pre ? 0 : ((size_t)(p.M * p.act_row_bytes) + 255) & ~(size_t)255;
-    const size_t need = (act_out ? 0 : act_bytes) + (d || act_out ? 0 : (size_t)(p.M * p.N * 4));
+    const size_t lay_bytes = !act_out && use_gemm(p) ? gemm_layout_bytes(p) : 0;
+    const size_t need = (act_out ? 0 : act_bytes) + lay_bytes + (d || act_out ? 0 : (size_t)(p.M * p.N * 4));
     void *ws = nullptr;
     if (need) {
         st = ctx->workspace(need, s, &ws);
@@ -315,7 +330,8 @@ ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_ten
         if (p.act_pre) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat_act: src1 is already quantized");
         return quantize_act(ctx, p, b, act, s);
     }
-    float *dst = d ? (float *)d->data : (float *)((uint8_t *)ws + act_bytes);
+    void *lay = lay_bytes ? (void *)((uint8_t *)ws + act_bytes) : nullptr;
+    float *dst = d ? (float *)d->data : (float *)((uint8_t *)ws + act_bytes + lay_bytes);
     const int64_t ldd = d ? (int64_t)d->nb[1] / 4 : p.N;
     if (use_gemm(p)) {
         if (!p.act_pre) {
@@ -324,7 +340,7 @@ ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_ten
         } else {
             act = b->data;
         }
-        return run_gemm(ctx, p, a->data, (const uint8_t *)act, dst, ldd, sub, s);
+        return run_gemm(ctx, p, a->data, (const uint8_t *)act, dst, ldd, sub, lay, s);
     }
     if (p.act_pre) return run_gemv(ctx, p, a->data, (const uint8_t *)b->data, p.act_row_bytes, false, dst, ldd, sub, s);
     if (gemv_v2(p))  // quantization fused into the decode kernel

@@ -13,21 +13,6 @@
 //   iacc = 8 * (A . W_hi) + (A . W_lo)      -- two int8 MFMA chains, exact int32.
 // imin is a K=16 contraction of mn (<= 63) with bsum16 (|.| <= 2032), both
 // exact in fp16, with sums < 2^24: one v_mfma_f32_32x32x16_f16 per tile, exact.
-//
-// Tiling: a 256-thread workgroup owns a 128-token x 64-row output tile; its
-// four wavefronts each own 32 tokens x 64 rows (two MFMA tiles of 32 x 32).
-// Two workgroups share a CU (78 KB of LDS each, two wavefronts per SIMD) and
-// run out of phase, so one's scaling epilogue overlaps the other's MFMAs.  Per super-block the workgroup expands the
-// weights ONCE into the two planes in LDS (double-buffered: super-block b+1
-// is expanded while b is multiplied); every wavefront streams its own
-// activation codes from global memory (L2) straight into registers, one
-// super-block ahead.
-//
-// K order inside a super-block: 16-element piece p = 2*(2*c + nh) + h holds
-// elements 64c + 32nh + 16h + [0, 16) -- bytes 32c + 16h + [0,16) of the
-// Q4_K qs, low nibbles for nh = 0, high for nh = 1 -- so MFMA K-step
-// ks = 2c + nh (32 elements) lies in one sub-block (scale index ks), and lane
-// half h of both operands carries piece 2*ks + h.
 #include "ghip_common.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -35,37 +20,9 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
-constexpr int BM = 128, BN = 64;
-constexpr int PROW = 256;  // LDS row (bytes) of a weight plane; pieces XOR-swizzled by row
-
-// LDS byte offset of 16-element piece p of plane row r: piece p is stored at
-// slot p ^ (r % 16), so the 32 rows a wavefront half reads at one piece index
-// fall in 8 distinct 16-byte bank groups per 8 lanes.
-DEV int piece_off(int r, int p) { return r * PROW + 16 * (p ^ (r & 15)); }
-
-struct GemmStage {
-    uint8_t wlo[BN * PROW];  // q4 * sc_lo  [row][k]  (k in piece order)
-    uint8_t whi[BN * PROW];  // q4 * sc_hi  [row][k]
-    _Float16 bs[BM * 16];    // bsum16 as f16                [token][16]
-    _Float16 mn[BN * 16];    // mn[s] at k = 2s, 2s+1, f16   [row][16]
-    float da[BM];
-    float dw[BN];
-    float dmin[BN];
-};
-struct GemmSmem {
-    GemmStage st[2];
-};
-
 // C layout of a 32x32 MFMA tile: lane l holds column j = l % 32 and rows
 // i = 8*(v/4) + 4*(l/32) + v%4 for v = 0..15.
 DEV int crow(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
-
-// c ? v : 0 on a value (a select between two lvalues would take addresses
-// and keep the prefetch arrays out of registers)
-DEV uint4 keep_if(bool c, uint4 v) {
-    const uint32_t m = c ? 0xffffffffu : 0u;
-    return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
-}
 
 // Four packed nibbles (one per byte) times a 3-bit scale: each byte product is
 // <= 105, so two 16-bit lane multiplies (v_pk_mul_lo_u16) carry nothing
@@ -77,209 +34,252 @@ DEV uint32_t mul_bytes(uint32_t nib, uint32_t s) {
     return __builtin_bit_cast(uint32_t, r);
 }
 
-// Weight prefetch of one super-block: thread t owns row t/4 and qs chunk
-// t%4 (32 bytes), and decodes the header; the epilogue data of token t/2
-// (bsum16[8*(t%2) .. +7] and d) come with it.
-struct PrefetchW {
-    uint4 q0, q1;  // qs bytes 32c .. 32c+31 of row t/4, c = t%4
-    uint4 hd;      // header
-    uint4 bsv;     // bsum16[8*(t%2) .. +7] of token t/2
-    uint32_t ad;   // the token's d
+// GEMM activation layout, written by ghip_gemm_act_layout from Q8_K rows
+// (tokens padded to a multiple of 128, so every staging load is in bounds):
+//   codes [Mpad][K] int8 | bsT [nb][Mpad][16] bsum16 as f16 | dT [nb][Mpad] f32
+// One wavefront per (token, super-block): lane l moves codes 4l .. 4l+3,
+// lanes 0..15 the sixteen bsum16 and lane 0 the block scale.
+extern "C" __global__ void __launch_bounds__(256)
+ghip_gemm_act_layout(const uint8_t *__restrict__ q8k, int64_t row_bytes, int M, int Mpad, int nb,
+                     int8_t *__restrict__ codes, _Float16 *__restrict__ bsT, float *__restrict__ dT) {
+    const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (task >= (int64_t)M * nb) return;
+    const int m = (int)(task / nb), b = (int)(task % nb);
+    const uint8_t *blk = q8k + (int64_t)m * row_bytes + (int64_t)b * Q8K_BYTES;
+    const int64_t K = (int64_t)nb * QK_K;
+    *reinterpret_cast<uint32_t *>(codes + (int64_t)m * K + b * QK_K + 4 * lane) = ld4(blk + 4 + 4 * lane);
+    if (lane < 16) bsT[((int64_t)b * Mpad + m) * 16 + lane] = (_Float16)(float)(int16_t)ld2(blk + 260 + 2 * lane);
+    if (lane == 0) dT[(int64_t)b * Mpad + m] = __uint_as_float(ld4(blk));
+}
+
+// Prefill GEMM: a 512-thread workgroup (one CU) owns 128 tokens x 128 rows,
+// each of its eight wavefronts 64 tokens x 32 rows (two 32 x 32 tiles).  Per
+// super-block the workgroup's operands arrive in LDS by direct global->LDS
+// loads (no registers, no vector ALU), double-buffered so super-block b+1
+// lands while b is multiplied:
+//   act   activation codes [token][256], 16-byte slots swizzled by token % 16
+//   wraw  raw Q4_K qs [row][128], 16-byte slots swizzled by row % 8
+//   hdr   Q4_K header [row][16] (d, dmin, packed 6-bit scales and mins)
+//   bs/da bsum16 (f16) and block scale of every token
+// Each wavefront decodes its rows' scales from hdr and expands the raw
+// nibbles in registers right before the MFMAs: one 16-byte read of qs gives
+// the B operands of two K-steps (low and high nibbles) for both planes
+// q4*sc_lo and q4*sc_hi (sc = 8*sc_hi + sc_lo, each product <= 105), so
+//   iacc = 8*(A.W_hi) + (A.W_lo)   in two exact int32 accumulator sets,
+//   imin = sum_s mn_s * (bsum16_2s + bsum16_2s+1)   (one exact f16 MFMA),
+//   out += da * (dw * iacc - dmin * imin)           (repack.rs:1692-1770).
+namespace g3 {
+constexpr int BM = 128, BN = 128, NW = 8;
+struct Buf {  // operands of one super-block (two, alternating)
+    uint8_t act[BM * 256];
+    uint8_t wraw[BN * 128];
+    uint8_t hdr[BN * 16];
 };
+struct Meta {  // per-token scaling data of one super-block (three, in a ring)
+    _Float16 bs[BM * 16];
+    float da[BM];
+};
+struct Smem {
+    Buf buf[2];
+    Meta meta[3];
+};
+}  // namespace g3
 
-// wrow: this thread's weight row (t/4, clamped); arow: its token row (t/2, clamped)
-DEV void prefetch_w(PrefetchW &P, const uint8_t *__restrict__ wrow, const uint8_t *__restrict__ arow, int b) {
-    const int c = threadIdx.x & 3;
-    const uint8_t *blk = wrow + b * Q4K_BYTES;
-    P.q0 = ld16(blk + 16 + 32 * c);
-    P.q1 = ld16(blk + 32 + 32 * c);
-    P.hd = ld16(blk);
-    const uint8_t *A = arow + b * Q8K_BYTES;
-    P.bsv = ld16(A + 260 + 16 * (threadIdx.x & 1));
-    P.ad = ld4(A);
-}
-
-// Expand a prefetched super-block into the planes of stage S.
-DEV void store_w(GemmStage &S, const PrefetchW &P, int N, int n0, int M, int m0) {
-    const int t = threadIdx.x, r = t >> 2, c = t & 3;
-    const int tok = t >> 1, half = t & 1;
-    const bool nv = n0 + r < N, mv = m0 + tok < M;
-    const uint4 hd = keep_if(nv, P.hd);
-    int sc0, mn0, sc1, mn1;
-    scale_min_k4(hd.y, hd.z, hd.w, 2 * c, sc0, mn0);
-    scale_min_k4(hd.y, hd.z, hd.w, 2 * c + 1, sc1, mn1);
-    const uint4 q0 = keep_if(nv, P.q0), q1 = keep_if(nv, P.q1);
-    const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    // pieces of chunk c: (nh, h) -> k offset 64c + 32nh + 16h; bytes 16h.. of the chunk
-#pragma unroll
-    for (int nh = 0; nh < 2; nh++) {
-        const uint32_t slo = nh ? (uint32_t)(sc1 & 7) : (uint32_t)(sc0 & 7);
-        const uint32_t shi = nh ? (uint32_t)(sc1 >> 3) : (uint32_t)(sc0 >> 3);
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            uint32_t lo[4], hi[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t w = qw[4 * h + e];
-                const uint32_t nib = nh ? ((w >> 4) & 0x0f0f0f0f) : (w & 0x0f0f0f0f);
-                lo[e] = mul_bytes(nib, slo);
-                hi[e] = mul_bytes(nib, shi);
-            }
-            const int off = piece_off(r, 4 * c + 2 * nh + h);  // elements 64c + 32nh + 16h ..
-            *reinterpret_cast<uint4 *>(&S.wlo[off]) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            *reinterpret_cast<uint4 *>(&S.whi[off]) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-        }
-    }
-    // mn of sub-blocks 2c, 2c+1 at k = 4c .. 4c+3
-    const uint32_t m01 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)mn0) * 0x10001u;
-    const uint32_t m23 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)mn1) * 0x10001u;
-    *reinterpret_cast<uint2 *>(&S.mn[r * 16 + 4 * c]) = make_uint2(m01, m23);
-    if (c == 0) {
-        S.dw[r] = h2f(hd.x);
-        S.dmin[r] = h2f(hd.x >> 16);
-    }
-    // token t/2: bsum16[8*half .. +7] -> f16, and d
-    const uint4 bv = keep_if(mv, P.bsv);
-    const uint32_t bw[4] = {bv.x, bv.y, bv.z, bv.w};
-    v8h hv;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        hv[2 * e] = (_Float16)(float)(int16_t)(bw[e] & 0xffff);
-        hv[2 * e + 1] = (_Float16)(float)(int16_t)(bw[e] >> 16);
-    }
-    *reinterpret_cast<v8h *>(&S.bs[tok * 16 + 8 * half]) = hv;
-    if (half == 0) S.da[tok] = mv ? __uint_as_float(P.ad) : 0.0f;
-}
-
-// Piece 2*ks + h of this lane's token (elements 32ks + 16h .. +15) of
-// super-block b; p points at the token's codes + 16h (rows past M re-read a
-// valid token; their results are never stored).
-DEV v4i load_piece(const uint8_t *__restrict__ p, int b, int ks) {
-    const uint4 v = ld16(p + b * Q8K_BYTES + 32 * ks);
-    return v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+typedef __attribute__((address_space(3))) void lds_void;
+// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
+DEV void g2lds(const void *gptr, void *lds) {
+    __builtin_amdgcn_global_load_lds(gptr, (lds_void *)lds, 16, 0, 0);
 }
 
 template <bool SUBSUMS>
 __device__ __forceinline__ void gemm_q4K_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb,
-                                              const uint8_t *__restrict__ act, int64_t act_row_bytes, int M,
-                                              float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
+                                               const int8_t *__restrict__ codes, const _Float16 *__restrict__ bsT,
+                                               const float *__restrict__ dT, int M, int Mpad,
+                                               float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
+    constexpr int BM = g3::BM, BN = g3::BN;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
-    GemmSmem &SM = *reinterpret_cast<GemmSmem *>(smem_raw);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave;  // 4 wavefronts along the tokens
+    g3::Smem &SM = *reinterpret_cast<g3::Smem *>(smem_raw);
+    g3::Buf *buf = SM.buf;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, wn = wave >> 1;  // 64-token half, 32-row quarter
     const int li = lane & 31, h = lane >> 5;
+    const int64_t K = (int64_t)nb * QK_K;
 
-    // Tile order: the M-tiles of one N-tile are consecutive, and consecutive
-    // tile ids go to the same XCD (workgroups are dealt to the 8 XCDs round
-    // robin), so one XCD's L2 serves a weight tile to all its token tiles.
     const int n_tiles_m = (M + BM - 1) / BM, n_tiles_n = (N + BN - 1) / BN;
     const int total = n_tiles_m * n_tiles_n;
     int id = blockIdx.x;
     if (total % 8 == 0) id = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
     const int m0 = (id % n_tiles_m) * BM;
     const int n0 = (id / n_tiles_m) * BN;
-    const int mrow = m0 + 32 * wm + li;  // this lane's token for the A operand
 
+    // ---- direct loads of super-block b into buf[b & 1]; wavefront w issues
+    // act pieces 4w..4w+3 (4 tokens each), wraw pieces 2w, 2w+1 (8 rows each),
+    // and one of: hdr (w = 0, 1), bs (w = 2..5), da (w = 6)
+    // (weight rows past N re-read row N-1; tokens past M are padding)
+    const uint8_t *wbase[3];
+    {
+        // this lane's rows for the wraw pieces and the hdr piece
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int row = 8 * (2 * wave + i) + (lane >> 3);
+            const int slot = (lane & 7) ^ (row & 7);
+            wbase[i] = W + (int64_t)min(n0 + row, N - 1) * w_row_bytes + 16 + 16 * slot;
+        }
+        wbase[2] = W + (int64_t)min(n0 + 64 * (wave & 1) + lane, N - 1) * w_row_bytes;
+    }
+    const int8_t *abase[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int tok = 4 * (4 * wave + i) + (lane >> 4);
+        const int slot = (lane & 15) ^ (tok & 15);
+        abase[i] = codes + (int64_t)(m0 + tok) * K + 16 * slot;
+    }
+    auto issue = [&](int b) {
+        g3::Buf &B = buf[b & 1];
+        g3::Meta &Mt = SM.meta[b % 3];
+#pragma unroll
+        for (int i = 0; i < 4; i++) g2lds(abase[i] + (int64_t)b * QK_K, B.act + 1024 * (4 * wave + i));
+#pragma unroll
+        for (int i = 0; i < 2; i++) g2lds(wbase[i] + (int64_t)b * Q4K_BYTES, B.wraw + 1024 * (2 * wave + i));
+        if (wave < 2) g2lds(wbase[2] + (int64_t)b * Q4K_BYTES, B.hdr + 1024 * wave);
+        else if (wave < 6) g2lds(bsT + ((int64_t)b * Mpad + m0 + 32 * (wave - 2)) * 16 + 8 * lane,
+                                 reinterpret_cast<uint8_t *>(Mt.bs) + 1024 * (wave - 2));
+        else if (wave == 6 && lane < 32) g2lds(dT + (int64_t)b * Mpad + m0 + 4 * lane, Mt.da);
+    };
+
+    v16i acc_h[2], acc_l[2];
     v16f out[2];
 #pragma unroll
-    for (int c = 0; c < 2; c++)
+    for (int tm = 0; tm < 2; tm++)
 #pragma unroll
-        for (int v = 0; v < 16; v++) out[c][v] = 0.0f;
+        for (int v = 0; v < 16; v++) out[tm][v] = 0.0f;
 
-    const uint8_t *wrow = W + (int64_t)min(n0 + (tid >> 2), N - 1) * w_row_bytes;
-    const uint8_t *arow = act + (int64_t)min(m0 + (tid >> 1), M - 1) * act_row_bytes;
-    const uint8_t *apiece = act + (int64_t)min(mrow, M - 1) * act_row_bytes + 4 + 16 * h;
+    const int wr = 32 * wn + li;  // this lane's weight row (B operand column)
+    const uint32_t raw_off0 = (uint32_t)wr * 128, wsw = (uint32_t)(wr & 7);
+    const uint32_t act_off[2] = {(uint32_t)(64 * wm + li) * 256, (uint32_t)(64 * wm + 32 + li) * 256};
+    const uint32_t asw = (uint32_t)(li & 15);  // rows 64wm + li and +32 share it
 
-    v4i A[8];
-    PrefetchW P;
-    prefetch_w(P, wrow, arow, 0);
-#pragma unroll
-    for (int ks = 0; ks < 8; ks++) A[ks] = load_piece(apiece, 0, ks);
-    store_w(SM.st[0], P, N, n0, M, m0);
+    issue(0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-
     for (int b = 0; b < nb; b++) {
-        // multiply super-block b from stage b&1; meanwhile super-block b+1's
-        // weights go to P (then the other stage) and each activation piece,
-        // once its MFMAs are issued, is reloaded with b+1's
-        const GemmStage &S = SM.st[b & 1];
-        const bool more = b + 1 < nb;
-        if (more) prefetch_w(P, wrow, arow, b + 1);
+        if (b + 1 < nb) issue(b + 1);
+        const g3::Buf &B = buf[b & 1];
+        const g3::Meta &Mt = SM.meta[b % 3];
+        // ---- this lane's row: scales of the 8 sub-blocks, d, dmin, and the
+        // min-term operand (mins of sub-blocks 4h .. 4h+3 at k = 8h .. 8h+7)
+        const uint4 hv = *reinterpret_cast<const uint4 *>(B.hdr + 16 * wr);
+        int sc[8], mn[8];
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            k4_scales(hv.y, hv.z, hv.w, scale_sel(c), sc[2 * c], sc[2 * c + 1], mn[2 * c], mn[2 * c + 1]);
+        const float dw = h2f(hv.x), dmin = h2f(hv.x >> 16);
+        v8h Bm;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int mlo = mn[j], mhi = mn[4 + j];  // values, not a select of array elements
+            const _Float16 m = (_Float16)(float)(h ? mhi : mlo);
+            Bm[2 * j] = m;
+            Bm[2 * j + 1] = m;
+        }
+        // ---- MFMAs: chunk c covers K-steps 2c (low nibbles) and 2c+1 (high);
+        // chunk c+1's operands are read from LDS while chunk c multiplies
         const v16i zi = {};
-        v16i acc_lo[2], acc_hi[2];
+        uint4 raw[2];
+        v4i av[2][2][2];  // [buffer][nh][tm]
+        auto load_chunk = [&](int c, uint4 &rw_, v4i (&a_)[2][2]) {
+            rw_ = *reinterpret_cast<const uint4 *>(B.wraw + raw_off0 + 16 * ((2 * c + h) ^ wsw));
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
+            for (int nh = 0; nh < 2; nh++)
 #pragma unroll
-            for (int tn = 0; tn < 2; tn++) {
-                const int nl = tn * 32 + li;
-                const int off = piece_off(nl, 2 * ks + h);
-                const v4i blo = *reinterpret_cast<const v4i *>(&S.wlo[off]);
-                const v4i bhi = *reinterpret_cast<const v4i *>(&S.whi[off]);
-                acc_lo[tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[ks], blo, ks ? acc_lo[tn] : zi, 0, 0, 0);
-                acc_hi[tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[ks], bhi, ks ? acc_hi[tn] : zi, 0, 0, 0);
+                for (int tm = 0; tm < 2; tm++)
+                    a_[nh][tm] = *reinterpret_cast<const v4i *>(B.act + act_off[tm] + 16 * ((2 * (2 * c + nh) + h) ^ asw));
+        };
+        load_chunk(0, raw[0], av[0]);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int cb = c & 1;
+            if (c < 3) load_chunk(c + 1, raw[cb ^ 1], av[cb ^ 1]);
+            __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of this chunk's work
+            const uint32_t rw[4] = {raw[cb].x, raw[cb].y, raw[cb].z, raw[cb].w};
+#pragma unroll
+            for (int nh = 0; nh < 2; nh++) {
+                const int ks = 2 * c + nh;
+                const uint32_t sv = (uint32_t)sc[ks];
+                const uint32_t slo = sv & 7u, shi = sv >> 3;
+                v4i blo, bhi;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t nib = nh ? ((rw[e] >> 4) & 0x0f0f0f0fu) : (rw[e] & 0x0f0f0f0fu);
+                    blo[e] = (int)mul_bytes(nib, slo);
+                    bhi[e] = (int)mul_bytes(nib, shi);
+                }
+#pragma unroll
+                for (int tm = 0; tm < 2; tm++) {
+                    acc_l[tm] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[cb][nh][tm], blo, ks == 0 ? zi : acc_l[tm], 0, 0, 0);
+                    acc_h[tm] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[cb][nh][tm], bhi, ks == 0 ? zi : acc_h[tm], 0, 0, 0);
+                }
             }
-            if (more) A[ks] = load_piece(apiece, b + 1, ks);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // ---- min term (K = 16 bsum16 slots, one f16 MFMA per tile) and epilogue
-        const int kq = 8 * h;
-        const v8h Am = *reinterpret_cast<const v8h *>(&S.bs[(wm * 32 + li) * 16 + kq]);
-        float dav[16];
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const float4 d4 = *reinterpret_cast<const float4 *>(&S.da[wm * 32 + 8 * g + 4 * h]);
-            dav[4 * g] = d4.x;
-            dav[4 * g + 1] = d4.y;
-            dav[4 * g + 2] = d4.z;
-            dav[4 * g + 3] = d4.w;
-        }
+        // ---- min term and scaling
         const v16f zf = {};
 #pragma unroll
-        for (int tn = 0; tn < 2; tn++) {
-            const int nl = tn * 32 + li;
-            const float dw = S.dw[nl], dmin = S.dmin[nl];
-            const v8h Bm = *reinterpret_cast<const v8h *>(&S.mn[nl * 16 + kq]);
+        for (int tm = 0; tm < 2; tm++) {
+            const int tl = 64 * wm + 32 * tm;
+            const v8h Am = *reinterpret_cast<const v8h *>(&Mt.bs[(tl + li) * 16 + 8 * h]);
             const v16f accm = __builtin_amdgcn_mfma_f32_32x32x16_f16(Am, Bm, zf, 0, 0, 0);
+            float dav[16];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 d4 = *reinterpret_cast<const float4 *>(&Mt.da[tl + 8 * g + 4 * h]);
+                dav[4 * g] = d4.x;
+                dav[4 * g + 1] = d4.y;
+                dav[4 * g + 2] = d4.z;
+                dav[4 * g + 3] = d4.w;
+            }
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const int iacc = (acc_hi[tn][v] << 3) + acc_lo[tn][v];
+                const int iacc = (acc_h[tm][v] << 3) + acc_l[tm][v];
                 const float im = accm[v];
                 if (SUBSUMS) {
-                    const int ml = wm * 32 + crow(v, lane);
-                    if (m0 + ml < M && n0 + nl < N) {
-                        int32_t *sp = sub + (((int64_t)(m0 + ml) * N + (n0 + nl)) * nb + b) * 2;
+                    const int ml = tl + crow(v, lane);
+                    if (m0 + ml < M && n0 + wr < N) {
+                        int32_t *sp = sub + (((int64_t)(m0 + ml) * N + (n0 + wr)) * nb + b) * 2;
                         sp[0] = iacc;
                         sp[1] = (int)im;
                     }
                 }
                 const float t = fmaf(dw, (float)iacc, -(dmin * im));
-                out[tn][v] = fmaf(dav[v], t, out[tn][v]);
+                out[tm][v] = fmaf(dav[v], t, out[tm][v]);
             }
         }
-        if (more) store_w(SM.st[(b + 1) & 1], P, N, n0, M, m0);
-        __syncthreads();
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // super-block b+1 is in LDS
+        __syncthreads();                                    // ... for every wavefront; buf[b&1] is free
     }
     // ---- store: for each v, the 32 lanes of a half write 32 consecutive floats
+    const int n = n0 + wr;
 #pragma unroll
-    for (int tn = 0; tn < 2; tn++) {
-        const int n = n0 + tn * 32 + li;
+    for (int tm = 0; tm < 2; tm++)
 #pragma unroll
         for (int v = 0; v < 16; v++) {
-            const int m = m0 + wm * 32 + crow(v, lane);
-            if (m < M && n < N) dst[(int64_t)m * ldd + n] = out[tn][v];
+            const int m = m0 + 64 * wm + 32 * tm + crow(v, lane);
+            if (m < M && n < N) dst[(int64_t)m * ldd + n] = out[tm][v];
         }
-    }
 }
 
-extern "C" __global__ void __launch_bounds__(256, 2)
-ghip_gemm_q4_K(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb, const uint8_t *__restrict__ act,
-               int64_t act_row_bytes, int M, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
-    gemm_q4K_impl<false>(W, w_row_bytes, N, nb, act, act_row_bytes, M, dst, ldd, sub);
+extern "C" __global__ void __launch_bounds__(512, 1)
+ghip_gemm_q4_K(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb, const int8_t *__restrict__ codes,
+                const _Float16 *__restrict__ bsT, const float *__restrict__ dT, int M, int Mpad,
+                float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
+    gemm_q4K_impl<false>(W, w_row_bytes, N, nb, codes, bsT, dT, M, Mpad, dst, ldd, sub);
 }
-extern "C" __global__ void __launch_bounds__(256)
-ghip_gemm_q4_K_sub(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb, const uint8_t *__restrict__ act,
-                   int64_t act_row_bytes, int M, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
-    gemm_q4K_impl<true>(W, w_row_bytes, N, nb, act, act_row_bytes, M, dst, ldd, sub);
+extern "C" __global__ void __launch_bounds__(512, 1)
+ghip_gemm_q4_K_sub(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb,
+                    const int8_t *__restrict__ codes, const _Float16 *__restrict__ bsT, const float *__restrict__ dT,
+                    int M, int Mpad, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
+    gemm_q4K_impl<true>(W, w_row_bytes, N, nb, codes, bsT, dT, M, Mpad, dst, ldd, sub);
 }
-
-static_assert(sizeof(GemmSmem) == 2 * (2 * BN * PROW + BM * 32 + BN * 32 + 4 * (BM + 2 * BN)), "LDS layout");
-static_assert(sizeof(GemmSmem) == 79872, "host code launches with this LDS size");
+static_assert(sizeof(g3::Smem) == 116224, "host code launches with this LDS size");

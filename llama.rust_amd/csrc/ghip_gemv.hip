@@ -153,29 +153,6 @@ DEV void q8K_store(const Q8KTask &t, int nb, int total, int task, int8_t *codes,
     if (l == 0) dq[c * nb + b] = t.d;
 }
 
-// Scales and mins of sub-blocks 2i and 2i+1 (get_scale_min_k4,
-// quants_k.rs:1672) for this lane's fixed i, without lane-divergent branches:
-// for sub-block t < 4 the scale is bits 0-5 of byte t and the min bits 0-5
-// of byte t+4; for t >= 4 the scale is the low nibble of byte t+4 with the
-// top two bits of byte t-4 above it, the min the high nibble of byte t+4 with
-// the top two bits of byte t.  The lane's selectors come from ScaleSel.
-struct ScaleSel {
-    bool hi;     // i >= 2: sub-blocks 4..7
-    int o0, o1;  // bit offsets of the two sub-blocks' bytes (8 * (t & 3))
-};
-DEV ScaleSel scale_sel(int i) { return ScaleSel{i >= 2, 8 * ((2 * i) & 3), 8 * ((2 * i + 1) & 3)}; }
-DEV void k4_scales(uint32_t s0, uint32_t s1, uint32_t s2, const ScaleSel &q, int &sc0, int &sc1, int &m0, int &m1) {
-    const uint32_t a = q.hi ? s2 : s0;  // scale low bits
-    const uint32_t bm = q.hi ? s2 : s1; // min low bits
-    const uint32_t ts = q.hi ? s0 : 0u; // scale top bits
-    const uint32_t tm = q.hi ? s1 : 0u; // min top bits
-    const int ws = q.hi ? 4 : 6, om = q.hi ? 4 : 0;
-    sc0 = (int)(__builtin_amdgcn_ubfe(a, q.o0, ws) | (__builtin_amdgcn_ubfe(ts, q.o0 + 6, 2) << 4));
-    sc1 = (int)(__builtin_amdgcn_ubfe(a, q.o1, ws) | (__builtin_amdgcn_ubfe(ts, q.o1 + 6, 2) << 4));
-    m0 = (int)(__builtin_amdgcn_ubfe(bm, q.o0 + om, ws) | (__builtin_amdgcn_ubfe(tm, q.o0 + 6, 2) << 4));
-    m1 = (int)(__builtin_amdgcn_ubfe(bm, q.o1 + om, ws) | (__builtin_amdgcn_ubfe(tm, q.o1 + 6, 2) << 4));
-}
-
 // Activation codes of one lane: elements 64i..64i+31 (low nibbles, sub-block
 // 2i) and 64i+32..64i+63 (high nibbles, sub-block 2i+1) of super-block b, the
 // two sub-block sums and the block scale.

@@ -281,9 +281,20 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
 // out for the GEMM (codes | bsum16 | d, tokens padded to 128), then the int8
 // MFMA GEMM runs on 128 x 128 tiles.
 constexpr size_t kGemmSmem = 116224;  // sizeof(g3::Smem) in ghip_gemm.hip
+// K slices for grids that would leave CUs idle (fewer than 128 tiles); the
+// slices' partial sums are added in order by ghip_gemm_splitk_reduce
+int gemm_nsplit(const MulMatPlan &p) {
+    const int64_t tiles = ((p.M + 127) / 128) * ((p.N + 127) / 128);
+    if (tiles >= 128 || p.N % 4) return 1;
+    const int64_t want = (256 + tiles - 1) / tiles;
+    const int64_t nbs = (p.nb + want - 1) / want;  // super-blocks per slice
+    return (int)((p.nb + nbs - 1) / nbs);
+}
 size_t gemm_layout_bytes(const MulMatPlan &p) {
     const size_t Mpad = (size_t)(p.M + 127) / 128 * 128, nbk = (size_t)p.K / 256;
-    return (Mpad * (size_t)p.K + nbk * Mpad * 32 + nbk * Mpad * 4 + 255) & ~(size_t)255;
+    const int ns = gemm_nsplit(p);
+    const size_t part = ns > 1 ? (size_t)ns * (size_t)p.M * (size_t)p.N * 4 : 0;
+    return ((Mpad * (size_t)p.K + nbk * Mpad * 32 + nbk * Mpad * 4 + 255) & ~(size_t)255) + part;
 }
 ghip_status run_gemm(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, float *dst,
                      int64_t ldd, int32_t *sub, void *layout_ws, hipStream_t s) {
@@ -296,9 +307,20 @@ ghip_status run_gemm(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
                                  (int)p.M, (int)Mpad, (int)nbk, codes, bsT, dT);
     if (st != GHIP_STATUS_SUCCESS) return st;
     const unsigned grid = (unsigned)(((p.M + 127) / 128) * ((p.N + 127) / 128));
-    return ctx->launch(sub ? "ghip_gemm_q4_K_sub" : "ghip_gemm_q4_K", dim3(grid), dim3(512), kGemmSmem, s,
-                       (const uint8_t *)w, (int64_t)p.w_row_bytes, (int)p.N, (int)p.nb, (const int8_t *)codes,
-                       (const uint16_t *)bsT, (const float *)dT, (int)p.M, (int)Mpad, dst, (int64_t)ldd, sub);
+    const int ns = gemm_nsplit(p);
+    const int nbs = (int)((p.nb + ns - 1) / ns);
+    float *part = ns > 1 ? (float *)((uint8_t *)layout_ws +
+                                     (((size_t)Mpad * K + nbk * Mpad * 32 + nbk * Mpad * 4 + 255) & ~(size_t)255))
+                         : dst;
+    const int64_t zstride = ns > 1 ? p.M * p.N : 0;
+    st = ctx->launch(sub ? "ghip_gemm_q4_K_sub" : "ghip_gemm_q4_K", dim3(grid, ns), dim3(512), kGemmSmem, s,
+                     (const uint8_t *)w, (int64_t)p.w_row_bytes, (int)p.N, (int)p.nb, (const int8_t *)codes,
+                     (const uint16_t *)bsT, (const float *)dT, (int)p.M, (int)Mpad, part,
+                     ns > 1 ? (int64_t)p.N : (int64_t)ldd, sub, nbs, zstride);
+    if (st != GHIP_STATUS_SUCCESS || ns == 1) return st;
+    const unsigned rgrid = (unsigned)((p.M * p.N / 4 + 255) / 256);
+    return ctx->launch("ghip_gemm_splitk_reduce", dim3(rgrid), dim3(256), 0, s, (const float *)part, ns, (int)p.M,
+                       (int)p.N, dst, (int64_t)ldd);
 }
 
 bool use_gemm(const MulMatPlan &p) {

@@ -96,8 +96,13 @@ template <bool SUBSUMS>
 __device__ __forceinline__ void gemm_q4K_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb,
                                                const int8_t *__restrict__ codes, const _Float16 *__restrict__ bsT,
                                                const float *__restrict__ dT, int M, int Mpad,
-                                               float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
+                                               float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub,
+                                               int nbs, int64_t zstride) {
     constexpr int BM = g3::BM, BN = g3::BN;
+    // split K: workgroup row blockIdx.y takes super-blocks [b0, b1) and writes
+    // its partial sums to dst + blockIdx.y * zstride
+    const int b0 = blockIdx.y * nbs, b1 = min(nb, b0 + nbs);
+    dst += blockIdx.y * zstride;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
     g3::Smem &SM = *reinterpret_cast<g3::Smem *>(smem_raw);
     g3::Buf *buf = SM.buf;
@@ -161,11 +166,11 @@ __device__ __forceinline__ void gemm_q4K_impl(const uint8_t *__restrict__ W, int
     const uint32_t act_off[2] = {(uint32_t)(64 * wm + li) * 256, (uint32_t)(64 * wm + 32 + li) * 256};
     const uint32_t asw = (uint32_t)(li & 15);  // rows 64wm + li and +32 share it
 
-    issue(0);
+    issue(b0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    for (int b = 0; b < nb; b++) {
-        if (b + 1 < nb) issue(b + 1);
+    for (int b = b0; b < b1; b++) {
+        if (b + 1 < b1) issue(b + 1);
         const g3::Buf &B = buf[b & 1];
         const g3::Meta &Mt = SM.meta[b % 3];
         // ---- this lane's row: scales of the 8 sub-blocks, d, dmin, and the
@@ -273,13 +278,36 @@ __device__ __forceinline__ void gemm_q4K_impl(const uint8_t *__restrict__ W, int
 extern "C" __global__ void __launch_bounds__(512, 1)
 ghip_gemm_q4_K(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb, const int8_t *__restrict__ codes,
                 const _Float16 *__restrict__ bsT, const float *__restrict__ dT, int M, int Mpad,
-                float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
-    gemm_q4K_impl<false>(W, w_row_bytes, N, nb, codes, bsT, dT, M, Mpad, dst, ldd, sub);
+                float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub, int nbs, int64_t zstride) {
+    gemm_q4K_impl<false>(W, w_row_bytes, N, nb, codes, bsT, dT, M, Mpad, dst, ldd, sub, nbs, zstride);
 }
 extern "C" __global__ void __launch_bounds__(512, 1)
 ghip_gemm_q4_K_sub(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb,
                     const int8_t *__restrict__ codes, const _Float16 *__restrict__ bsT, const float *__restrict__ dT,
-                    int M, int Mpad, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
-    gemm_q4K_impl<true>(W, w_row_bytes, N, nb, codes, bsT, dT, M, Mpad, dst, ldd, sub);
+                    int M, int Mpad, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub, int nbs,
+                    int64_t zstride) {
+    gemm_q4K_impl<true>(W, w_row_bytes, N, nb, codes, bsT, dT, M, Mpad, dst, ldd, sub, nbs, zstride);
+}
+// split-K partial sums [nsplit][M][N] -> dst, slices added in order; four
+// consecutive outputs per thread (N % 4 == 0)
+extern "C" __global__ void __launch_bounds__(256)
+ghip_gemm_splitk_reduce(const float *__restrict__ part, int nsplit, int M, int N, float *__restrict__ dst,
+                        int64_t ldd) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= (int64_t)M * N) return;
+    const int m = (int)(i / N), n = (int)(i % N);
+    float4 acc = *reinterpret_cast<const float4 *>(part + i);
+    for (int z = 1; z < nsplit; z++) {
+        const float4 v = *reinterpret_cast<const float4 *>(part + (int64_t)z * M * N + i);
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+    }
+    float *d = dst + (int64_t)m * ldd + n;
+    d[0] = acc.x;
+    d[1] = acc.y;
+    d[2] = acc.z;
+    d[3] = acc.w;
 }
 static_assert(sizeof(g3::Smem) == 116224, "host code launches with this LDS size");

@@ -280,11 +280,14 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
 // Prefill path (Q4_K, many activation rows): the Q8_K activations are laid
 // out for the GEMM (codes | bsum16 | d, tokens padded to 128), then the int8
 // MFMA GEMM runs on 128 x 128 tiles.
-constexpr size_t kGemmSmem = 116224;  // sizeof(g3::Smem) in ghip_gemm.hip
+constexpr size_t kGemmSmem128 = 116224, kGemmSmem64 = 76544;  // sizeof(g3::Smem<BM>) in ghip_gemm.hip
+// token tile: 64 (two workgroups per CU) unless GHIP_GEMM_BM=128
+int gemm_bm() { return env_int("GHIP_GEMM_BM", 64) == 128 ? 128 : 64; }
 // K slices for grids that would leave CUs idle (fewer than 128 tiles); the
 // slices' partial sums are added in order by ghip_gemm_splitk_reduce
 int gemm_nsplit(const MulMatPlan &p) {
-    const int64_t tiles = ((p.M + 127) / 128) * ((p.N + 127) / 128);
+    const int bm = gemm_bm();
+    const int64_t tiles = ((p.M + bm - 1) / bm) * ((p.N + 127) / 128);
     if (tiles >= 128 || p.N % 4) return 1;
     const int64_t want = (256 + tiles - 1) / tiles;
     const int64_t nbs = (p.nb + want - 1) / want;  // super-blocks per slice
@@ -306,14 +309,17 @@ ghip_status run_gemm(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     ghip_status st = ctx->launch("ghip_gemm_act_layout", dim3(lgrid), dim3(256), 0, s, act, (int64_t)p.act_row_bytes,
                                  (int)p.M, (int)Mpad, (int)nbk, codes, bsT, dT);
     if (st != GHIP_STATUS_SUCCESS) return st;
-    const unsigned grid = (unsigned)(((p.M + 127) / 128) * ((p.N + 127) / 128));
+    const int bm = gemm_bm();
+    const unsigned grid = (unsigned)(((p.M + bm - 1) / bm) * ((p.N + 127) / 128));
     const int ns = gemm_nsplit(p);
     const int nbs = (int)((p.nb + ns - 1) / ns);
     float *part = ns > 1 ? (float *)((uint8_t *)layout_ws +
                                      (((size_t)Mpad * K + nbk * Mpad * 32 + nbk * Mpad * 4 + 255) & ~(size_t)255))
                          : dst;
     const int64_t zstride = ns > 1 ? p.M * p.N : 0;
-    st = ctx->launch(sub ? "ghip_gemm_q4_K_sub" : "ghip_gemm_q4_K", dim3(grid, ns), dim3(512), kGemmSmem, s,
+    const char *kn = bm == 128 ? (sub ? "ghip_gemm_q4_K_sub" : "ghip_gemm_q4_K")
+                               : (sub ? "ghip_gemm_q4_K_m64_sub" : "ghip_gemm_q4_K_m64");
+    st = ctx->launch(kn, dim3(grid, ns), dim3(bm * 4), bm == 128 ? kGemmSmem128 : kGemmSmem64, s,
                      (const uint8_t *)w, (int64_t)p.w_row_bytes, (int)p.N, (int)p.nb, (const int8_t *)codes,
                      (const uint16_t *)bsT, (const float *)dT, (int)p.M, (int)Mpad, part,
                      ns > 1 ? (int64_t)p.N : (int64_t)ldd, sub, nbs, zstride);

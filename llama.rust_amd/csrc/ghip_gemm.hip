@@ -70,19 +70,19 @@ ghip_gemm_act_layout(const uint8_t *__restrict__ q8k, int64_t row_bytes, int M, 
 //   imin = sum_s mn_s * (bsum16_2s + bsum16_2s+1)   (one exact f16 MFMA),
 //   out += da * (dw * iacc - dmin * imin)           (repack.rs:1692-1770).
 namespace g3 {
-constexpr int BM = 128, BN = 128, NW = 8;
-struct Buf {  // operands of one super-block (two, alternating)
+constexpr int BN = 128;
+template <int BM> struct Buf {  // operands of one super-block (two, alternating)
     uint8_t act[BM * 256];
     uint8_t wraw[BN * 128];
     uint8_t hdr[BN * 16];
 };
-struct Meta {  // per-token scaling data of one super-block (three, in a ring)
+template <int BM> struct Meta {  // per-token scaling data of one super-block (three, in a ring)
     _Float16 bs[BM * 16];
     float da[BM];
 };
-struct Smem {
-    Buf buf[2];
-    Meta meta[3];
+template <int BM> struct Smem {
+    Buf<BM> buf[2];
+    Meta<BM> meta[3];
 };
 }  // namespace g3
 
@@ -92,23 +92,27 @@ DEV void g2lds(const void *gptr, void *lds) {
     __builtin_amdgcn_global_load_lds(gptr, (lds_void *)lds, 16, 0, 0);
 }
 
-template <bool SUBSUMS>
+// BM = 128 tokens: 8 wavefronts, one workgroup per CU; BM = 64: 4
+// wavefronts and half the LDS, two workgroups per CU.
+template <int BM, bool SUBSUMS>
 __device__ __forceinline__ void gemm_q4K_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb,
                                                const int8_t *__restrict__ codes, const _Float16 *__restrict__ bsT,
                                                const float *__restrict__ dT, int M, int Mpad,
                                                float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub,
                                                int nbs, int64_t zstride) {
-    constexpr int BM = g3::BM, BN = g3::BN;
+    constexpr int BN = g3::BN, NW = BM / 16, TPW = BM / 64;
+    constexpr int WRI = 16 / NW;                    // wraw pieces per wavefront
+    constexpr int DAW = BM == 128 ? 6 : 1;          // wavefront that loads da
     // split K: workgroup row blockIdx.y takes super-blocks [b0, b1) and writes
     // its partial sums to dst + blockIdx.y * zstride
     const int b0 = blockIdx.y * nbs, b1 = min(nb, b0 + nbs);
     dst += blockIdx.y * zstride;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
-    g3::Smem &SM = *reinterpret_cast<g3::Smem *>(smem_raw);
-    g3::Buf *buf = SM.buf;
+    g3::Smem<BM> &SM = *reinterpret_cast<g3::Smem<BM> *>(smem_raw);
+    g3::Buf<BM> *buf = SM.buf;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave & 1, wn = wave >> 1;  // 64-token half, 32-row quarter
+    const int wm = wave % TPW, wn = wave / TPW;  // 64-token slice, 32-row quarter
     const int li = lane & 31, h = lane >> 5;
     const int64_t K = (int64_t)nb * QK_K;
 
@@ -120,19 +124,19 @@ __device__ __forceinline__ void gemm_q4K_impl(const uint8_t *__restrict__ W, int
     const int n0 = (id / n_tiles_m) * BN;
 
     // ---- direct loads of super-block b into buf[b & 1]; wavefront w issues
-    // act pieces 4w..4w+3 (4 tokens each), wraw pieces 2w, 2w+1 (8 rows each),
-    // and one of: hdr (w = 0, 1), bs (w = 2..5), da (w = 6)
+    // act pieces 4w..4w+3 (4 tokens each), wraw pieces WRI*w .. (8 rows each),
+    // hdr (w = 0, 1), bs (w = 2 .. 2 + BM/32 - 1) and da (w = DAW)
     // (weight rows past N re-read row N-1; tokens past M are padding)
-    const uint8_t *wbase[3];
+    const uint8_t *wbase[WRI + 1];
     {
         // this lane's rows for the wraw pieces and the hdr piece
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int row = 8 * (2 * wave + i) + (lane >> 3);
+        for (int i = 0; i < WRI; i++) {
+            const int row = 8 * (WRI * wave + i) + (lane >> 3);
             const int slot = (lane & 7) ^ (row & 7);
             wbase[i] = W + (int64_t)min(n0 + row, N - 1) * w_row_bytes + 16 + 16 * slot;
         }
-        wbase[2] = W + (int64_t)min(n0 + 64 * (wave & 1) + lane, N - 1) * w_row_bytes;
+        wbase[WRI] = W + (int64_t)min(n0 + 64 * (wave & 1) + lane, N - 1) * w_row_bytes;
     }
     const int8_t *abase[4];
 #pragma unroll
@@ -142,16 +146,17 @@ __device__ __forceinline__ void gemm_q4K_impl(const uint8_t *__restrict__ W, int
         abase[i] = codes + (int64_t)(m0 + tok) * K + 16 * slot;
     }
     auto issue = [&](int b) {
-        g3::Buf &B = buf[b & 1];
-        g3::Meta &Mt = SM.meta[b % 3];
+        g3::Buf<BM> &B = buf[b & 1];
+        g3::Meta<BM> &Mt = SM.meta[b % 3];
 #pragma unroll
         for (int i = 0; i < 4; i++) g2lds(abase[i] + (int64_t)b * QK_K, B.act + 1024 * (4 * wave + i));
 #pragma unroll
-        for (int i = 0; i < 2; i++) g2lds(wbase[i] + (int64_t)b * Q4K_BYTES, B.wraw + 1024 * (2 * wave + i));
-        if (wave < 2) g2lds(wbase[2] + (int64_t)b * Q4K_BYTES, B.hdr + 1024 * wave);
-        else if (wave < 6) g2lds(bsT + ((int64_t)b * Mpad + m0 + 32 * (wave - 2)) * 16 + 8 * lane,
-                                 reinterpret_cast<uint8_t *>(Mt.bs) + 1024 * (wave - 2));
-        else if (wave == 6 && lane < 32) g2lds(dT + (int64_t)b * Mpad + m0 + 4 * lane, Mt.da);
+        for (int i = 0; i < WRI; i++) g2lds(wbase[i] + (int64_t)b * Q4K_BYTES, B.wraw + 1024 * (WRI * wave + i));
+        if (wave < 2) g2lds(wbase[WRI] + (int64_t)b * Q4K_BYTES, B.hdr + 1024 * wave);
+        if (wave >= 2 && wave < 2 + BM / 32)
+            g2lds(bsT + ((int64_t)b * Mpad + m0 + 32 * (wave - 2)) * 16 + 8 * lane,
+                  reinterpret_cast<uint8_t *>(Mt.bs) + 1024 * (wave - 2));
+        if (wave == DAW && lane < BM / 4) g2lds(dT + (int64_t)b * Mpad + m0 + 4 * lane, Mt.da);
     };
 
     v16i acc_h[2], acc_l[2];
@@ -171,8 +176,8 @@ __device__ __forceinline__ void gemm_q4K_impl(const uint8_t *__restrict__ W, int
     __syncthreads();
     for (int b = b0; b < b1; b++) {
         if (b + 1 < b1) issue(b + 1);
-        const g3::Buf &B = buf[b & 1];
-        const g3::Meta &Mt = SM.meta[b % 3];
+        const g3::Buf<BM> &B = buf[b & 1];
+        const g3::Meta<BM> &Mt = SM.meta[b % 3];
         // ---- this lane's row: scales of the 8 sub-blocks, d, dmin, and the
         // min-term operand (mins of sub-blocks 4h .. 4h+3 at k = 8h .. 8h+7)
         const uint4 hv = *reinterpret_cast<const uint4 *>(B.hdr + 16 * wr);
@@ -275,19 +280,22 @@ __device__ __forceinline__ void gemm_q4K_impl(const uint8_t *__restrict__ W, int
         }
 }
 
-extern "C" __global__ void __launch_bounds__(512, 1)
-ghip_gemm_q4_K(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb, const int8_t *__restrict__ codes,
-                const _Float16 *__restrict__ bsT, const float *__restrict__ dT, int M, int Mpad,
-                float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub, int nbs, int64_t zstride) {
-    gemm_q4K_impl<false>(W, w_row_bytes, N, nb, codes, bsT, dT, M, Mpad, dst, ldd, sub, nbs, zstride);
-}
-extern "C" __global__ void __launch_bounds__(512, 1)
-ghip_gemm_q4_K_sub(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb,
-                    const int8_t *__restrict__ codes, const _Float16 *__restrict__ bsT, const float *__restrict__ dT,
-                    int M, int Mpad, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub, int nbs,
-                    int64_t zstride) {
-    gemm_q4K_impl<true>(W, w_row_bytes, N, nb, codes, bsT, dT, M, Mpad, dst, ldd, sub, nbs, zstride);
-}
+#define GEMM_KERNELS(NAME, BM, NT, LB)                                                                            \
+    extern "C" __global__ void __launch_bounds__(NT, LB)                                                            \
+        NAME(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb, const int8_t *__restrict__ codes,    \
+             const _Float16 *__restrict__ bsT, const float *__restrict__ dT, int M, int Mpad,                        \
+             float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub, int nbs, int64_t zstride) {            \
+        gemm_q4K_impl<BM, false>(W, w_row_bytes, N, nb, codes, bsT, dT, M, Mpad, dst, ldd, sub, nbs, zstride);      \
+    }                                                                                                                \
+    extern "C" __global__ void __launch_bounds__(NT, LB)                                                            \
+        NAME##_sub(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb,                               \
+                   const int8_t *__restrict__ codes, const _Float16 *__restrict__ bsT, const float *__restrict__ dT, \
+                   int M, int Mpad, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub, int nbs,        \
+                   int64_t zstride) {                                                                                \
+        gemm_q4K_impl<BM, true>(W, w_row_bytes, N, nb, codes, bsT, dT, M, Mpad, dst, ldd, sub, nbs, zstride);       \
+    }
+GEMM_KERNELS(ghip_gemm_q4_K, 128, 512, 1)
+GEMM_KERNELS(ghip_gemm_q4_K_m64, 64, 256, 2)
 // split-K partial sums [nsplit][M][N] -> dst, slices added in order; four
 // consecutive outputs per thread (N % 4 == 0)
 extern "C" __global__ void __launch_bounds__(256)
@@ -310,4 +318,4 @@ ghip_gemm_splitk_reduce(const float *__restrict__ part, int nsplit, int M, int N
     d[2] = acc.z;
     d[3] = acc.w;
 }
-static_assert(sizeof(g3::Smem) == 116224, "host code launches with this LDS size");
+static_assert(sizeof(g3::Smem<128>) == 116224 && sizeof(g3::Smem<64>) == 76544, "host code launches with these LDS sizes");

@@ -243,7 +243,11 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     if (q4k && !((rb == 2 && (ng == 2 || ng == 4 || ng == 8)) || (rb == 4 && (ng == 2 || ng == 4))))
         return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "GHIP_GEMV_RB x GHIP_GEMV_NG must be 2x2, 2x4, 2x8, 4x2 or 4x4");
     const int rows_per_team = rb * ng;
-    const int teams = q4k ? std::max(1, std::min(8 / waves_k, env_int("GHIP_GEMV_TEAMS", 8))) : 1;
+    // 8 teams, except 4 for one or two activation rows on matrices under 8192
+    // rows: measured on 4096->1024 / 4096->4096 / 4096->14336 at batch 1-8
+    // (there, fewer and fuller workgroups quantize the activation fewer times)
+    const int dflt_teams = p.N < 8192 && p.M <= 2 ? 4 : 8;
+    const int teams = q4k ? std::max(1, std::min(8 / waves_k, env_int("GHIP_GEMV_TEAMS", dflt_teams))) : 1;
     const int rows_per_wg = rows_per_team * teams;
     const unsigned grid = (unsigned)((p.N + rows_per_wg - 1) / rows_per_wg);
     for (int64_t c0 = 0; c0 < p.M; c0 += 8) {

@@ -66,6 +66,14 @@ DEV float h2f(uint32_t bits16) {
     return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu)));
 }
 
+// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
+// (global_load_lds_dwordx4; lds is wave-uniform). The data is in LDS once the
+// issuing wavefront's vmcnt reaches zero.
+typedef __attribute__((address_space(3))) void lds_void;
+DEV void g2lds(const void *gptr, void *lds) {
+    __builtin_amdgcn_global_load_lds(gptr, (lds_void *)lds, 16, 0, 0);
+}
+
 DEV int dot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 
 DEV float wave_sum(float v) {

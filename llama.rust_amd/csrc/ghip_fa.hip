@@ -367,10 +367,15 @@ DEV float dpp_max_wave(float v) {
 template <int D>
 __device__ __forceinline__ void fa_decode_impl(const FaParams &p) {
     constexpr int HD = D / 2;        // dims per lane of a key pair
-    constexpr int NL = HD / 8;       // 16-byte K loads per lane per step
+    constexpr int NL = HD / 8;       // 16-byte K chunks per lane per key
+    constexpr int RB = D * 2;        // bytes per K or V row
+    constexpr int CPR = RB / 16;     // 16-byte chunks per row
+    // per wavefront: this step's 32 K rows and 32 V rows, staged by direct
+    // loads (chunk c of K row r at slot c ^ (r % CPR)); after the loop the
+    // same bytes hold the wavefronts' partials for the combine
+    __shared__ __attribute__((aligned(16))) uint8_t kv[4][2][32 * RB];
     __shared__ __attribute__((aligned(16))) _Float16 qs[8][D];
     __shared__ float wst[4][8][2];
-    __shared__ float wo[4][8][D];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int hk = blockIdx.x, z = blockIdx.y;
     const int G = p.H / p.H_kv;
@@ -387,6 +392,7 @@ __device__ __forceinline__ void fa_decode_impl(const FaParams &p) {
     const int j = lane >> 1, hf = lane & 1;
     const int dl = 2 * lane;  // P V dims (D = 128); D = 64 uses lanes < 32
     const bool dv = dl < D;
+    uint8_t *Ks = kv[w][0], *Vs = kv[w][1];
     float Mh[8], Sh[8], o0[8], o1[8];
 #pragma unroll
     for (int g = 0; g < 8; g++) {
@@ -394,23 +400,28 @@ __device__ __forceinline__ void fa_decode_impl(const FaParams &p) {
         Sh[g] = 0.0f;
         o0[g] = o1[g] = 0.0f;
     }
-    uint4 kq[NL];
-    uint32_t vq[32];
-    auto load_step = [&](int kb, uint4 *kk, uint32_t *vv) {
-        const int key = min(kb + j, wk1 - 1);
-        const uint8_t *kr = (const uint8_t *)(kbase + (int64_t)key * p.k_nb1) + hf * HD * 2;
+    // direct loads of keys kb .. kb+31 (rows past the range re-read the last
+    // one); instruction i moves 64 x 16 bytes = 1024 / RB rows
+    constexpr int RPI = 1024 / RB;  // rows per instruction
+    auto stage = [&](int kb) {
 #pragma unroll
-        for (int l = 0; l < NL; l++) kk[l] = ld16(kr + 16 * l);
-#pragma unroll
-        for (int jj = 0; jj < 32; jj++) {
-            const int kj = min(kb + jj, wk1 - 1);
-            vv[jj] = dv ? ld4((const uint8_t *)(vbase + (int64_t)kj * p.v_nb1 + dl)) : 0u;
+        for (int i = 0; i < 32 / RPI; i++) {
+            const int r = RPI * i + lane / CPR, slot = lane % CPR;
+            const int key = min(kb + r, wk1 - 1);
+            g2lds((const uint8_t *)(kbase + (int64_t)key * p.k_nb1) + 16 * (slot ^ (r % CPR)), Ks + 1024 * i);
+            g2lds((const uint8_t *)(vbase + (int64_t)key * p.v_nb1) + 16 * slot, Vs + 1024 * i);
         }
     };
-    if (wk0 < wk1) load_step(wk0, kq, vq);
     for (int kb = wk0; kb < wk1; kb += 32) {
         const int nk = min(32, wk1 - kb);
-        // scores of key kb + j for the G heads
+        stage(kb);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_wave_barrier();
+        // scores of key kb + j for the G heads (lane half hf: dims hf*HD ..)
+        uint4 kq[NL];
+#pragma unroll
+        for (int l = 0; l < NL; l++)
+            kq[l] = *reinterpret_cast<const uint4 *>(Ks + RB * j + 16 * ((hf * NL + l) ^ (j % CPR)));
         float sg[8];
 #pragma unroll
         for (int g = 0; g < 8; g++) {
@@ -427,13 +438,17 @@ __device__ __forceinline__ void fa_decode_impl(const FaParams &p) {
             }
             sg[g] = acc;
         }
-        const uint32_t *vcur = vq;
-        uint32_t vnext[32];
-        uint4 knext[NL];
-        const bool more = kb + 32 < wk1;
-        if (more) load_step(kb + 32, knext, vnext);
         const bool live = j < nk;
         const float mk = (p.mask && live) ? h2f(p.mask[kb + j]) : 0.0f;
+        // this lane's dims of the step's V rows; masked keys' rows are zeroed
+        // so that they add nothing whatever the cache holds
+        const uint64_t dead = __ballot(!live || mk == -__builtin_inff());
+        uint32_t vq[32];
+#pragma unroll
+        for (int jj = 0; jj < 32; jj++) {
+            const uint32_t v = dv ? *reinterpret_cast<const uint32_t *>(Vs + RB * jj + 2 * dl) : 0u;
+            vq[jj] = (dead >> (2 * jj)) & 1 ? 0u : v;
+        }
 #pragma unroll
         for (int g = 0; g < 8; g++) {
             if (g >= G) continue;
@@ -455,22 +470,20 @@ __device__ __forceinline__ void fa_decode_impl(const FaParams &p) {
 #pragma unroll
             for (int jj = 0; jj < 32; jj++) {
                 const float pk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), 2 * jj));
-                if (pk == 0.0f) continue;  // masked or out-of-range key: its V is never read
-                const uint32_t vvv = vcur[jj];
-                a0 = fmaf(pk, h2f(vvv & 0xffff), a0);
-                a1 = fmaf(pk, h2f(vvv >> 16), a1);
+                a0 = fmaf(pk, h2f(vq[jj] & 0xffff), a0);
+                a1 = fmaf(pk, h2f(vq[jj] >> 16), a1);
             }
             o0[g] = a0;
             o1[g] = a1;
         }
-        if (more) {
-#pragma unroll
-            for (int l = 0; l < NL; l++) kq[l] = knext[l];
-#pragma unroll
-            for (int jj = 0; jj < 32; jj++) vq[jj] = vnext[jj];
-        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();  // the tile is consumed before the next step's loads land
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    // ---- the four wavefronts' partials -> the workgroup's
+    // ---- the four wavefronts' partials -> the workgroup's (wo aliases kv)
+    float(*wo)[8][D] = reinterpret_cast<float(*)[8][D]>(&kv[0][0][0]);
+    static_assert(sizeof(kv) >= sizeof(float) * 4 * 8 * D, "partials fit the K/V tiles");
+    __syncthreads();  // every wavefront is done with its tile
     if (lane == 0)
         for (int g = 0; g < G; g++) {
             wst[w][g][0] = Mh[g];

@@ -86,11 +86,6 @@ template <int BM> struct Smem {
 };
 }  // namespace g3
 
-typedef __attribute__((address_space(3))) void lds_void;
-// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
-DEV void g2lds(const void *gptr, void *lds) {
-    __builtin_amdgcn_global_load_lds(gptr, (lds_void *)lds, 16, 0, 0);
-}
 
 // BM = 128 tokens: 8 wavefronts, one workgroup per CU; BM = 64: 4
 // wavefronts and half the LDS, two workgroups per CU.

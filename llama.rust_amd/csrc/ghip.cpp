@@ -630,6 +630,9 @@ ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const g
         const char *dec = D == 128 ? "ghip_fa_decode_d128" : "ghip_fa_decode_d64";
         st = ctx->launch(dec, dim3(H_kv, ns), dim3(256), 0, s, p);
         if (st != GHIP_STATUS_SUCCESS) return st;
+        if (ns <= 64)
+            return ctx->launch("ghip_fa_merge_rows4", dim3((unsigned)H), dim3(256), 0, s, (const float *)ws, p.sinks,
+                               (float *)dst->data, H, H, ns, D);
         return ctx->launch("ghip_fa_merge", dim3((unsigned)H), dim3(256), 0, s, (const float *)ws, p.sinks,
                            (float *)dst->data, 1, H, ns, D);
     }

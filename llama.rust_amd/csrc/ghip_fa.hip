@@ -524,17 +524,29 @@ __device__ __forceinline__ void fa_decode_impl(const FaParams &p) {
 // formed in parallel into LDS, then thread (d, part) sums slices
 // part, part + P, ... of column d with independent loads, and the parts meet
 // in LDS.  DV <= 256.
-// Few slices per row (prefill): one wavefront per (query, head) row, four
-// rows per workgroup; lane l owns dims l and l + 64.  Slices are folded in
-// order with the same weights exp(M_z - M) as ghip_fa_merge.
-extern "C" __global__ void __launch_bounds__(256)
-ghip_fa_merge_rows(const float *__restrict__ part, const float *__restrict__ sinks, float *__restrict__ dst,
-                   int nrows, int H, int nsplit, int DV) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= nrows) return;
+// Few slices per row (<= 64): WPR wavefronts per (query, head) row, 256 / WPR
+// rows per workgroup; lane l owns dims l and l + 64 and lane z holds slice
+// z's (M_z, S_z).  Wavefront u of a row folds slices u, u + WPR, ... in order
+// with the weights exp(M_z - M) of ghip_fa_merge; the first sixteen of them are
+// loaded before the weights are known, so the slice reads overlap the
+// statistics.  With WPR > 1 the wavefronts' sums meet in LDS in order.
+template <int WPR>
+__device__ __forceinline__ void fa_merge_rows_impl(const float *__restrict__ part, const float *__restrict__ sinks,
+                                                   float *__restrict__ dst, int nrows, int H, int nsplit, int DV) {
+    __shared__ float red[4][2][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, u = wv % WPR;
+    const int row = blockIdx.x * (4 / WPR) + wv / WPR;
+    if (row >= nrows) return;  // uniform per row: all WPR wavefronts leave together
     const float *pr = part + (int64_t)row * nsplit * (2 + DV);
-    // lane z < nsplit (<= 64) holds slice z's (M_z, S_z)
+    const int c0 = min(lane, DV - 1), c1 = min(64 + lane, DV - 1);
+    constexpr int PRE = 16;
+    float v0[PRE], v1[PRE];
+#pragma unroll
+    for (int i = 0; i < PRE; i++) {
+        const float *pz = pr + (int64_t)min(u + WPR * i, nsplit - 1) * (2 + DV) + 2;
+        v0[i] = pz[c0];
+        v1[i] = pz[c1];
+    }
     float mz = -__builtin_inff(), sz = 0.0f;
     if (lane < nsplit) {
         mz = pr[(int64_t)lane * (2 + DV)];
@@ -543,14 +555,34 @@ ghip_fa_merge_rows(const float *__restrict__ part, const float *__restrict__ sin
     const float M = dpp_max_wave(sz != 0.0f ? mz : -__builtin_inff());
     const float wz = (sz != 0.0f && M != -__builtin_inff()) ? __expf(mz - M) : 0.0f;
     float S = wave_sum_dpp(sz * wz);
-    const bool d1 = lane + 64 < DV;
     float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PRE; i++) {
+        const int z = u + WPR * i;
+        if (z < nsplit) {
+            const float wgt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wz), z));
+            a0 = fmaf(v0[i], wgt, a0);
+            a1 = fmaf(v1[i], wgt, a1);
+        }
+    }
 #pragma unroll 4
-    for (int z = 0; z < nsplit; z++) {
+    for (int z = u + WPR * PRE; z < nsplit; z += WPR) {
         const float *pz = pr + (int64_t)z * (2 + DV) + 2;
         const float wgt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wz), z));
-        if (lane < DV) a0 = fmaf(pz[lane], wgt, a0);
-        if (d1) a1 = fmaf(pz[64 + lane], wgt, a1);
+        a0 = fmaf(pz[c0], wgt, a0);
+        a1 = fmaf(pz[c1], wgt, a1);
+    }
+    if (WPR > 1) {
+        red[wv][0][lane] = a0;
+        red[wv][1][lane] = a1;
+        __syncthreads();
+        if (u != 0) return;
+        a0 = 0.0f;
+        a1 = 0.0f;
+        for (int i = 0; i < WPR; i++) {
+            a0 += red[wv + i][0][lane];
+            a1 += red[wv + i][1][lane];
+        }
     }
     if (sinks) {
         const float sv = sinks[row % H];
@@ -565,7 +597,19 @@ ghip_fa_merge_rows(const float *__restrict__ part, const float *__restrict__ sin
     }
     const float sinv = S == 0.0f ? 0.0f : 1.0f / S;
     if (lane < DV) dst[(int64_t)row * DV + lane] = a0 * sinv;
-    if (d1) dst[(int64_t)row * DV + 64 + lane] = a1 * sinv;
+    if (lane + 64 < DV) dst[(int64_t)row * DV + 64 + lane] = a1 * sinv;
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+ghip_fa_merge_rows(const float *__restrict__ part, const float *__restrict__ sinks, float *__restrict__ dst,
+                   int nrows, int H, int nsplit, int DV) {
+    fa_merge_rows_impl<1>(part, sinks, dst, nrows, H, nsplit, DV);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+ghip_fa_merge_rows4(const float *__restrict__ part, const float *__restrict__ sinks, float *__restrict__ dst,
+                    int nrows, int H, int nsplit, int DV) {
+    fa_merge_rows_impl<4>(part, sinks, dst, nrows, H, nsplit, DV);
 }
 
 extern "C" __global__ void __launch_bounds__(256)

@@ -5,6 +5,7 @@
 Outputs (next to this file, git-ignored, shipped with the tree):
   ghip_*.hsaco   one code object per kernel source, loaded with hipModuleLoad
   libghip.so     the C ABI declared in include/ghip.h
+  libggml-hip.so the dlopen module declared in include/ggml_hip_reg.h
 """
 import os
 import subprocess
@@ -57,9 +58,21 @@ def build_host():
           "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-ldl", "-Wl,-rpath," + os.path.join(ROCM, "lib")])
 
 
+def build_backend_module():
+    """libggml-hip.so: the dlopen module (ggml_backend_score / ggml_backend_init)
+    over libghip.so, found next to it at run time."""
+    out = os.path.join(HERE, "libggml-hip.so")
+    _run(["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-D__HIP_PLATFORM_AMD__",
+          "-I", os.path.join(ROCM, "include"), "-I", os.path.join(ROOT, "include"),
+          os.path.join(CSRC, "ghip_backend_reg.cpp"), "-o", out,
+          "-L", HERE, "-lghip", "-L", os.path.join(ROCM, "lib"), "-lamdhip64",
+          "-Wl,-rpath,$ORIGIN", "-Wl,-rpath," + os.path.join(ROCM, "lib")])
+
+
 def build():
     build_kernels()
     build_host()
+    build_backend_module()
 
 
 if __name__ == "__main__":

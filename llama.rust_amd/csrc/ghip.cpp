@@ -29,8 +29,10 @@ TypeInfo type_info(int t) {
     case GHIP_TYPE_F32: return {1, 4};
     case GHIP_TYPE_F16: return {1, 2};
     case GHIP_TYPE_Q4_0: return {32, 18};
+    case GHIP_TYPE_Q5_0: return {32, 22};
     case GHIP_TYPE_Q8_0: return {32, 34};
     case GHIP_TYPE_Q4_K: return {256, 144};
+    case GHIP_TYPE_Q5_K: return {256, 176};
     case GHIP_TYPE_Q6_K: return {256, 210};
     case GHIP_TYPE_Q8_K: return {256, 292};
     case GHIP_TYPE_I32: return {1, 4};
@@ -143,12 +145,14 @@ bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b,
                   MulMatPlan &p, ghip_status &st) {
     st = GHIP_STATUS_BACKEND_ERROR;
     if (!a || !b) { st = ctx->fail(st, "mul_mat: null operand"); return false; }
-    if (a->type != GHIP_TYPE_Q4_0 && a->type != GHIP_TYPE_Q4_K && a->type != GHIP_TYPE_Q6_K) {
-        st = ctx->fail(st, "mul_mat: src0 type %d not supported (Q4_0, Q4_K, Q6_K)", a->type);
+    if (a->type != GHIP_TYPE_Q4_0 && a->type != GHIP_TYPE_Q5_0 && a->type != GHIP_TYPE_Q8_0 &&
+        a->type != GHIP_TYPE_Q4_K && a->type != GHIP_TYPE_Q5_K && a->type != GHIP_TYPE_Q6_K) {
+        st = ctx->fail(st, "mul_mat: src0 type %d not supported (Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)", a->type);
         return false;
     }
     const TypeInfo ti = type_info(a->type);
-    const int vdt = a->type == GHIP_TYPE_Q4_0 ? GHIP_TYPE_Q8_0 : GHIP_TYPE_Q8_K;  // vec_dot_type
+    const bool q8_0_dot = a->type == GHIP_TYPE_Q4_0 || a->type == GHIP_TYPE_Q5_0 || a->type == GHIP_TYPE_Q8_0;
+    const int vdt = q8_0_dot ? GHIP_TYPE_Q8_0 : GHIP_TYPE_Q8_K;  // vec_dot_type (vec_dot.rs vec_dot_type)
     if (b->type != GHIP_TYPE_F32 && b->type != vdt) {
         st = ctx->fail(st, "mul_mat: src1 must be F32 or the vec_dot type of src0 (backend.rs:2057-2066)");
         return false;
@@ -176,7 +180,7 @@ bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b,
     p.nb = p.K / ti.blck;
     p.w_row_bytes = (int64_t)a->nb[1];
     if (p.w_row_bytes < p.nb * ti.bytes) { st = ctx->fail(st, "mul_mat: src0 nb1 too small"); return false; }
-    if (a->type == GHIP_TYPE_Q4_0) {
+    if (q8_0_dot) {
         p.act_type = GHIP_TYPE_Q8_0;
         p.act_row_bytes = p.K / 32 * 34;
         p.n_mat = 0;
@@ -211,16 +215,24 @@ ghip_status quantize_act(ghip_context *ctx, const MulMatPlan &p, const ghip_tens
 const char *gemv_base(int wtype) {
     switch (wtype) {
     case GHIP_TYPE_Q4_K: return "ghip_gemv_q4_K";
+    case GHIP_TYPE_Q5_K: return "ghip_gemv_q5_K";
     case GHIP_TYPE_Q6_K: return "ghip_gemv_q6_K";
+    case GHIP_TYPE_Q5_0: return "ghip_gemv_q5_0";
+    case GHIP_TYPE_Q8_0: return "ghip_gemv_q8_0";
     default: return "ghip_gemv_q4_0";
     }
 }
 
-// The whole-row decode kernels with the activation image in LDS: Q4_K always;
-// Q6_K for a single activation row (its 14336-wide rows make the per-workgroup
-// quantization of several columns cost more than it saves).
+// 32-element blocks with Q8_0 activations: one lane per pair of blocks
+bool gemv_pair(int wtype) {
+    return wtype == GHIP_TYPE_Q4_0 || wtype == GHIP_TYPE_Q5_0 || wtype == GHIP_TYPE_Q8_0;
+}
+
+// The whole-row decode kernels with the activation image in LDS: Q4_K and
+// Q5_K always; Q6_K for a single activation row (its 14336-wide rows make the
+// per-workgroup quantization of several columns cost more than it saves).
 bool gemv_v2(const MulMatPlan &p) {
-    return p.wtype == GHIP_TYPE_Q4_K || (p.wtype == GHIP_TYPE_Q6_K && p.M == 1);
+    return p.wtype == GHIP_TYPE_Q4_K || p.wtype == GHIP_TYPE_Q5_K || (p.wtype == GHIP_TYPE_Q6_K && p.M == 1);
 }
 
 // Decode path: activation columns in groups of at most 8.  Q4_K reads the f32
@@ -228,7 +240,7 @@ bool gemv_v2(const MulMatPlan &p) {
 ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, int64_t act_rb,
                      bool fused, float *dst, int64_t ldd, int32_t *sub, hipStream_t s) {
     int waves_k;
-    if (p.wtype == GHIP_TYPE_Q4_0)
+    if (gemv_pair(p.wtype))
         waves_k = (int)(((p.nb + 1) / 2 + 63) / 64);
     else if (gemv_v2(p))
         waves_k = (int)((p.nb + 15) / 16);
@@ -258,7 +270,7 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
                            "_c" + std::to_string(NC) + (q4k ? "_r" + std::to_string(rb) + "x" + std::to_string(ng) : std::string());
         int32_t *sub_c = sub;
         if (sub) {
-            const int64_t per = p.wtype == GHIP_TYPE_Q4_K ? 2 * p.nb : p.nb;
+            const int64_t per = (p.wtype == GHIP_TYPE_Q4_K || p.wtype == GHIP_TYPE_Q5_K) ? 2 * p.nb : p.nb;
             sub_c = sub + c0 * p.N * per;
         }
         ghip_status st;

@@ -167,7 +167,11 @@ struct Q4KAct {
 // qs bytes 32i..32i+31), so K <= 4096 is one wavefront and a row's partials
 // never leave it.  Rows are processed in register groups of RB, two groups
 // in flight (ping-pong buffers).
-template <int NC, bool SUBSUMS, bool FUSEQ, int RB, int NG>
+// Q5 = true reads Q5_K blocks (176 B: the Q4_K header, qh[32], qs[128]): the
+// same scales, mins and integer sums with each nibble's fifth bit taken from
+// qh -- bit 2i of qh[e] for sub-block 2i (low nibbles), bit 2i+1 for 2i+1
+// (vec_dot.rs:928-980).
+template <int NC, bool SUBSUMS, bool FUSEQ, int RB, int NG, bool Q5 = false>
 __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
                                               int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
                                               int ncols, float *__restrict__ dst, int64_t ldd,
@@ -195,10 +199,12 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
     // lanes past the row re-read a valid block (clamped index) and contribute
     // zero (their activation codes and scale are zero); a team past the last
     // row loads row rows-1 and computes nothing.
-    const uint32_t boff = (uint32_t)min(b, nb - 1) * Q4K_BYTES;
-    const uint32_t qoff = boff + 16 + 32 * i;
+    constexpr uint32_t BBYTES = Q5 ? 176 : Q4K_BYTES;
+    const uint32_t boff = (uint32_t)min(b, nb - 1) * BBYTES;
+    const uint32_t qoff = boff + (Q5 ? 48 : 16) + 32 * i;
     const int rlast = min(max(r0, r1 - 1), rows - 1);
     uint4 hdr[NG][RB], qa[NG][RB], qb[NG][RB];
+    uint4 xh0[NG][Q5 ? RB : 1], xh1[NG][Q5 ? RB : 1];  // Q5_K qh[0..15], qh[16..31]
     auto load_all = [&]() {
 #pragma unroll
         for (int gi = 0; gi < NG; gi++)
@@ -208,6 +214,10 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
                 hdr[gi][rr] = ld16(rowp + boff);
                 qa[gi][rr] = ld16(rowp + qoff);
                 qb[gi][rr] = ld16(rowp + qoff + 16);
+                if constexpr (Q5) {
+                    xh0[gi][rr] = ld16(rowp + boff + 16);
+                    xh1[gi][rr] = ld16(rowp + boff + 32);
+                }
             }
     };
     // Activations first (their wait then does not cover the weight loads),
@@ -269,7 +279,8 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
 
     // A row group: decode the RB rows' nibbles and scales once, then one
     // pass per activation column (dots, scaling, wave reduction per row).
-    auto compute_group = [&](int rg, const uint4 *hdr_, const uint4 *q0_, const uint4 *q1_) {
+    auto compute_group = [&](int rg, const uint4 *hdr_, const uint4 *q0_, const uint4 *q1_, const uint4 *h0_,
+                             const uint4 *h1_) {
         uint32_t lo[RB][8], hi[RB][8];
         int sc0[RB], sc1[RB], m0[RB], m1[RB];
         float dw[RB], dmin[RB];
@@ -284,6 +295,18 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
             for (int k = 0; k < 8; k++) {
                 lo[rr][k] = qv[k] & 0x0f0f0f0f;
                 hi[rr][k] = (qv[k] >> 4) & 0x0f0f0f0f;
+            }
+            if constexpr (Q5) {
+                // qh dword k covers elements 4k..4k+3; after >> 2i, bit 0 of a
+                // byte is sub-block 2i's fifth bit and bit 1 sub-block 2i+1's
+                const uint4 g0 = h0_[rr], g1 = h1_[rr];
+                const uint32_t hv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const uint32_t q2 = hv[k] >> (2 * i);
+                    lo[rr][k] |= (q2 & 0x01010101u) << 4;
+                    hi[rr][k] |= (q2 << 3) & 0x10101010u;
+                }
             }
         }
 #pragma unroll(ACT_LDS ? 1 : NC)
@@ -321,7 +344,7 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
     };
 #pragma unroll
     for (int gi = 0; gi < NG; gi++)
-        if (r0 + gi * RB < r1) compute_group(r0 + gi * RB, hdr[gi], qa[gi], qb[gi]);
+        if (r0 + gi * RB < r1) compute_group(r0 + gi * RB, hdr[gi], qa[gi], qb[gi], xh0[gi], xh1[gi]);
     if (nwk == 1) return;
     __syncthreads();
     const int nrows = max(0, min(rows, rw0 + T * RPT) - rw0);
@@ -693,6 +716,183 @@ __device__ __forceinline__ void gemv_q4_0_impl(const uint8_t *__restrict__ W, in
     finish_rows(red, r0, nr, ncols, NC, nw, dst, ldd);
 }
 
+// ---------------------------------------------------------------- Q5_0 / Q8_0 x Q8_0
+// The Q4_0 work layout: one lane per pair of 32-blocks, RB rows per
+// workgroup, all rows' loads issued before any is consumed.  Block values:
+//   Q8_0: the int8 codes                                  (vec_dot.rs:732-756)
+//   Q5_0: (nibble | bit e of qh << 4) - 16, the -16 folded in as
+//         -16 * sum(q8) per block, as Q4_0 folds its -8   (vec_dot.rs:661-686)
+// The integer block sums are the reference's exactly; they are scaled by
+// d_w * d_x in fp32 per block.
+constexpr int WT_Q5_0 = 6, WT_Q8_0 = 8;
+
+// bit j (< 4) of t moved to bit 4 of byte j: t * (2^4 + 2^11) puts bit j at
+// j+4 and j+11, the copy shifted by 14 adds j+18 and j+25; of these only
+// 4, 12, 20 and 28 survive the mask (one per j, no carries)
+DEV uint32_t spread4_bit4(uint32_t t) {
+    const uint32_t m = __mul24(t, 0x810u);
+    return ((m << 14) | m) & 0x10101010u;
+}
+
+template <int WT>
+DEV void pair_block_codes(const uint32_t *w, int blk, uint32_t (&q)[8], float &d) {
+    if constexpr (WT == WT_Q8_0) {
+        // block 0: d = bytes 0-1, codes 2..33; block 1: d = bytes 34-35, codes 36..67
+        if (blk == 0) {
+            d = h2f(w[0] & 0xffffu);
+#pragma unroll
+            for (int k = 0; k < 8; k++) q[k] = __builtin_amdgcn_alignbyte(w[k + 1], w[k], 2);
+        } else {
+            d = h2f(w[8] >> 16);
+#pragma unroll
+            for (int k = 0; k < 8; k++) q[k] = w[9 + k];
+        }
+    } else {
+        // block 0: d = bytes 0-1, qh 2..5, qs 6..21; block 1: d = 22-23, qh 24..27, qs 28..43
+        uint32_t qh, qs[4];
+        if (blk == 0) {
+            d = h2f(w[0] & 0xffffu);
+            qh = __builtin_amdgcn_alignbyte(w[1], w[0], 2);
+#pragma unroll
+            for (int k = 0; k < 4; k++) qs[k] = __builtin_amdgcn_alignbyte(w[k + 2], w[k + 1], 2);
+        } else {
+            d = h2f(w[5] >> 16);
+            qh = w[6];
+#pragma unroll
+            for (int k = 0; k < 4; k++) qs[k] = w[7 + k];
+        }
+        // elements 4k..4k+3 (low nibbles, qh bits 4k..) and 16+4k.. (high nibbles)
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            q[k] = (qs[k] & 0x0f0f0f0fu) | spread4_bit4(__builtin_amdgcn_ubfe(qh, 4 * k, 4));
+            q[4 + k] = ((qs[k] >> 4) & 0x0f0f0f0fu) | spread4_bit4(__builtin_amdgcn_ubfe(qh, 16 + 4 * k, 4));
+        }
+    }
+}
+
+template <int WT, int NC, bool SUBSUMS>
+__device__ __forceinline__ void gemv_pair_q8_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
+                                                  int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
+                                                  int ncols, float *__restrict__ dst, int64_t ldd,
+                                                  int32_t *__restrict__ sub) {
+    constexpr int PB = WT == WT_Q8_0 ? 68 : 44;  // bytes per block pair
+    constexpr int ND = PB / 4;                  // dwords per block pair
+    __shared__ float red[RB * 8 * NC];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int pr = 64 * w + lane;  // pair index
+    const int b0 = 2 * pr, b1 = 2 * pr + 1;
+    const bool v0 = b0 < nb, v1 = b1 < nb;
+    const int r0 = blockIdx.x * RB;
+    const int nr = min(RB, rows - r0);
+
+    uint32_t wq[RB][ND];
+    const uint8_t *wb = W + (int64_t)r0 * w_row_bytes + (int64_t)pr * PB;
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        const uint8_t *p = wb + rr * w_row_bytes;
+#pragma unroll
+        for (int k = 0; k < ND; k++) wq[rr][k] = 0;
+        if (rr < nr && v0) {
+            // the first block always; the second only when it exists (a lone
+            // last block reads its own 22 / 34 bytes, nothing past the row)
+            const uint4 a = ld16(p);
+            wq[rr][0] = a.x; wq[rr][1] = a.y; wq[rr][2] = a.z; wq[rr][3] = a.w;
+            if constexpr (WT == WT_Q8_0) {
+                const uint4 b = ld16(p + 16);
+                wq[rr][4] = b.x; wq[rr][5] = b.y; wq[rr][6] = b.z; wq[rr][7] = b.w;
+                if (v1) {
+                    const uint4 c = ld16(p + 32), e = ld16(p + 48);
+                    wq[rr][8] = c.x; wq[rr][9] = c.y; wq[rr][10] = c.z; wq[rr][11] = c.w;
+                    wq[rr][12] = e.x; wq[rr][13] = e.y; wq[rr][14] = e.z; wq[rr][15] = e.w;
+                    wq[rr][16] = ld4(p + 64);
+                } else {
+                    wq[rr][8] = ld2(p + 32);
+                }
+            } else {
+                if (v1) {
+                    const uint4 b = ld16(p + 16);
+                    const uint2 c = ld8(p + 32);
+                    wq[rr][4] = b.x; wq[rr][5] = b.y; wq[rr][6] = b.z; wq[rr][7] = b.w;
+                    wq[rr][8] = c.x; wq[rr][9] = c.y;
+                    wq[rr][10] = ld4(p + 40);
+                } else {
+                    wq[rr][4] = ld4(p + 16);
+                    wq[rr][5] = ld2(p + 20);
+                }
+            }
+        }
+    }
+    uint4 y0l[NC], y0h[NC], y1l[NC], y1h[NC];
+    int sy0[NC], sy1[NC];
+    float d0[NC], d1[NC];
+    const uint32_t one = 0x01010101u;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        y0l[c] = y0h[c] = y1l[c] = y1h[c] = make_uint4(0, 0, 0, 0);
+        sy0[c] = sy1[c] = 0;
+        d0[c] = d1[c] = 0.0f;
+        if (c < ncols && v0) {
+            const uint8_t *A = act + c * act_row_bytes + (int64_t)b0 * Q8_0_BYTES;
+            d0[c] = h2f(ld2(A));
+            y0l[c] = ld16(A + 2);
+            y0h[c] = ld16(A + 18);
+        }
+        if (c < ncols && v1) {
+            const uint8_t *A = act + c * act_row_bytes + (int64_t)b1 * Q8_0_BYTES;
+            d1[c] = h2f(ld2(A));
+            y1l[c] = ld16(A + 2);
+            y1h[c] = ld16(A + 18);
+        }
+        if constexpr (WT == WT_Q5_0) {
+            sy0[c] = 16 * dot4(y0l[c].x, one, dot4(y0l[c].y, one, dot4(y0l[c].z, one, dot4(y0l[c].w, one,
+                     dot4(y0h[c].x, one, dot4(y0h[c].y, one, dot4(y0h[c].z, one, dot4(y0h[c].w, one, 0))))))));
+            sy1[c] = 16 * dot4(y1l[c].x, one, dot4(y1l[c].y, one, dot4(y1l[c].z, one, dot4(y1l[c].w, one,
+                     dot4(y1h[c].x, one, dot4(y1h[c].y, one, dot4(y1h[c].z, one, dot4(y1h[c].w, one, 0))))))));
+        }
+    }
+    float part[NC][RB];
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        uint32_t q0[8], q1[8];
+        float dw0, dw1;
+        pair_block_codes<WT>(wq[rr], 0, q0, dw0);
+        pair_block_codes<WT>(wq[rr], 1, q1, dw1);
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int s0 = dot4(q0[7], y0h[c].w, dot4(q0[6], y0h[c].z, dot4(q0[5], y0h[c].y, dot4(q0[4], y0h[c].x,
+                           dot4(q0[3], y0l[c].w, dot4(q0[2], y0l[c].z, dot4(q0[1], y0l[c].y, dot4(q0[0], y0l[c].x,
+                           -sy0[c]))))))));
+            const int s1 = dot4(q1[7], y1h[c].w, dot4(q1[6], y1h[c].z, dot4(q1[5], y1h[c].y, dot4(q1[4], y1h[c].x,
+                           dot4(q1[3], y1l[c].w, dot4(q1[2], y1l[c].z, dot4(q1[1], y1l[c].y, dot4(q1[0], y1l[c].x,
+                           -sy1[c]))))))));
+            if (SUBSUMS && c < ncols && rr < nr) {
+                int32_t *s = sub + ((int64_t)c * rows + r0 + rr) * nb;
+                if (v0) s[b0] = s0;
+                if (v1) s[b1] = s1;
+            }
+            float pp = v0 ? (float)s0 * (dw0 * d0[c]) : 0.0f;
+            if (v1) pp = fmaf((float)s1, dw1 * d1[c], pp);
+            part[c][rr] = pp;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NC; c++) stash_rows(red, part[c], lane, w, nw, c, NC);
+    finish_rows(red, r0, nr, ncols, NC, nw, dst, ldd);
+}
+
+template <int NC, bool SUBSUMS>
+__device__ __forceinline__ void gemv_q5_0_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb,
+                                               const uint8_t *__restrict__ act, int64_t act_row_bytes, int ncols,
+                                               float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
+    gemv_pair_q8_impl<WT_Q5_0, NC, SUBSUMS>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub);
+}
+template <int NC, bool SUBSUMS>
+__device__ __forceinline__ void gemv_q8_0_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb,
+                                               const uint8_t *__restrict__ act, int64_t act_row_bytes, int ncols,
+                                               float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
+    gemv_pair_q8_impl<WT_Q8_0, NC, SUBSUMS>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub);
+}
+
 #define GEMV_ARGS                                                                                     \
     const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb, const uint8_t *__restrict__ act, \
         int64_t act_row_bytes, int ncols, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub
@@ -710,27 +910,34 @@ __device__ __forceinline__ void gemv_q4_0_impl(const uint8_t *__restrict__ W, in
 
 GEMV_ALL(ghip_gemv_q6_K, gemv_q6K_impl)
 GEMV_ALL(ghip_gemv_q4_0, gemv_q4_0_impl)
+GEMV_ALL(ghip_gemv_q5_0, gemv_q5_0_impl)
+GEMV_ALL(ghip_gemv_q8_0, gemv_q8_0_impl)
 
 // Q4_K: "_f" kernels take f32 activations (fused Q8_K quantization), the
 // others ready Q8_K rows; "_sub" kernels also store the integer partials.
 #define Q4K_ARGS GEMV_ARGS, int n_mat
 #define Q4K_PASS GEMV_PASS, n_mat
-#define Q4K_INST(NC, RB, NG)                                                                                      \
-    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_c##NC##_r##RB##x##NG(Q4K_ARGS) {            \
-        gemv_q4K_impl<NC, false, false, RB, NG>(Q4K_PASS);                                                      \
+#define QK45_INST(TN, Q5, NC, RB, NG)                                                                             \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_##TN##_c##NC##_r##RB##x##NG(Q4K_ARGS) {          \
+        gemv_q4K_impl<NC, false, false, RB, NG, Q5>(Q4K_PASS);                                                  \
     }                                                                                                           \
-    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_sub_c##NC##_r##RB##x##NG(Q4K_ARGS) {        \
-        gemv_q4K_impl<NC, true, false, RB, NG>(Q4K_PASS);                                                       \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_##TN##_sub_c##NC##_r##RB##x##NG(Q4K_ARGS) {      \
+        gemv_q4K_impl<NC, true, false, RB, NG, Q5>(Q4K_PASS);                                                   \
     }                                                                                                           \
-    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_f_c##NC##_r##RB##x##NG(Q4K_ARGS) {          \
-        gemv_q4K_impl<NC, false, true, RB, NG>(Q4K_PASS);                                                       \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_##TN##_f_c##NC##_r##RB##x##NG(Q4K_ARGS) {        \
+        gemv_q4K_impl<NC, false, true, RB, NG, Q5>(Q4K_PASS);                                                   \
     }                                                                                                           \
-    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_f_sub_c##NC##_r##RB##x##NG(Q4K_ARGS) {      \
-        gemv_q4K_impl<NC, true, true, RB, NG>(Q4K_PASS);                                                        \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_##TN##_f_sub_c##NC##_r##RB##x##NG(Q4K_ARGS) {    \
+        gemv_q4K_impl<NC, true, true, RB, NG, Q5>(Q4K_PASS);                                                    \
     }
+#define Q4K_INST(NC, RB, NG) QK45_INST(q4_K, false, NC, RB, NG)
 // register row groups (RB rows) x groups in flight (NG)
 #define Q4K_INST_RB(NC) Q4K_INST(NC, 2, 2) Q4K_INST(NC, 2, 4) Q4K_INST(NC, 4, 2) Q4K_INST(NC, 2, 8) Q4K_INST(NC, 4, 4)
 Q4K_INST_RB(1) Q4K_INST_RB(2) Q4K_INST_RB(4) Q4K_INST_RB(8)
+// Q5_K: the same shapes and naming as Q4_K
+#define Q5K_INST_RB(NC) QK45_INST(q5_K, true, NC, 2, 2) QK45_INST(q5_K, true, NC, 2, 4) \
+    QK45_INST(q5_K, true, NC, 4, 2) QK45_INST(q5_K, true, NC, 2, 8) QK45_INST(q5_K, true, NC, 4, 4)
+Q5K_INST_RB(1) Q5K_INST_RB(2) Q5K_INST_RB(4) Q5K_INST_RB(8)
 
 // Q6_K (v2): same shapes and naming, "_f" = fused Q8_K quantization
 #define Q6K_INST(NC, RB, NG)                                                                                      \

@@ -12,10 +12,12 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libghip.so")
 
-F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, I32, MXFP4 = 0, 1, 2, 8, 12, 14, 15, 26, 39
+F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, I32, MXFP4 = 0, 1, 2, 6, 8, 12, 13, 14, 15, 26, 39
 OP_MUL_MAT, OP_MUL_MAT_ID, OP_FLASH_ATTN_EXT = 1, 2, 3
-BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210), Q8_K: (256, 292),
-         MXFP4: (32, 17), F32: (1, 4), F16: (1, 2), I32: (1, 4)}
+BLOCK = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210),
+         Q8_K: (256, 292), MXFP4: (32, 17), F32: (1, 4), F16: (1, 2), I32: (1, 4)}
+# weight type -> the activation type of its dot (vec_dot_type)
+ACT_TYPE = {Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K}
 
 
 class GhipError(RuntimeError):
@@ -134,7 +136,7 @@ class Backend:
         n, m = w.shape[0], x.shape[0]
         if out is None:
             out = torch.empty((m, n), dtype=torch.float32, device=x.device)
-        xty = F32 if x.dtype == torch.float32 else (Q8_0 if wtype == Q4_0 else Q8_K)
+        xty = F32 if x.dtype == torch.float32 else ACT_TYPE[wtype]
         a, b, d = describe(w, wtype, k), describe(x, xty, k), describe(out, F32)
         self._check(lib().ghip_mul_mat(self._ctx, C.byref(a), C.byref(b), C.byref(d), _stream()), "ghip_mul_mat")
         return out
@@ -142,18 +144,18 @@ class Backend:
     def mul_mat_subsums(self, w, wtype, k, x):
         n, m = w.shape[0], x.shape[0]
         nb = k // BLOCK[wtype][0]
-        per = 2 * nb if wtype == Q4_K else nb
+        per = 2 * nb if wtype in (Q4_K, Q5_K) else nb
         sub = torch.empty((m, n, per), dtype=torch.int32, device=x.device)
         a, b = describe(w, wtype, k), describe(x, F32)
         self._check(lib().ghip_mul_mat_subsums(self._ctx, C.byref(a), C.byref(b), C.c_void_p(sub.data_ptr()),
                                                _stream()), "ghip_mul_mat_subsums")
-        if wtype == Q4_K:
+        if wtype in (Q4_K, Q5_K):
             sub = sub.view(m, n, nb, 2)
         return sub
 
     def mul_mat_act(self, w, wtype, k, x):
         m = x.shape[0]
-        act_ty = Q8_0 if wtype == Q4_0 else Q8_K
+        act_ty = ACT_TYPE[wtype]
         out = torch.empty((m, row_size(act_ty, k)), dtype=torch.uint8, device=x.device)
         a, b = describe(w, wtype, k), describe(x, F32)
         self._check(lib().ghip_mul_mat_act(self._ctx, C.byref(a), C.byref(b), C.c_void_p(out.data_ptr()),

@@ -28,6 +28,8 @@ typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } blk_q4
 typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } blk_q6_K; /* 210 B */
 typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } blk_q8_K;       /* 292 B */
 typedef struct { uint8_t e; uint8_t qs[16]; } blk_mxfp4;                        /* 17 B  */
+typedef struct { uint16_t d; uint8_t qh[4]; uint8_t qs[16]; } blk_q5_0;        /* 22 B  */
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; } blk_q5_K; /* 176 B */
 
 _Static_assert(sizeof(blk_q4_0) == 18, "q4_0");
 _Static_assert(sizeof(blk_q8_0) == 34, "q8_0");
@@ -35,6 +37,8 @@ _Static_assert(sizeof(blk_q4_K) == 144, "q4_K");
 _Static_assert(sizeof(blk_q6_K) == 210, "q6_K");
 _Static_assert(sizeof(blk_q8_K) == 292, "q8_K");
 _Static_assert(sizeof(blk_mxfp4) == 17, "mxfp4");
+_Static_assert(sizeof(blk_q5_0) == 22, "q5_0");
+_Static_assert(sizeof(blk_q5_K) == 176, "q5_K");
 
 double oracle_wtime(void) {
     struct timespec ts;
@@ -134,6 +138,33 @@ void oracle_quantize_row_q4_0_ref(const float *x, void *vy, int64_t k) {
             const int8_t xi1 = (int8_t)imin_((int8_t)(x1 + 8.5f), 15);
             y[i].qs[j] = (uint8_t)((xi0 & 0x0f) | ((xi1 & 0x0f) << 4));
         }
+    }
+}
+
+/* quants.rs:207-240 quantize_row_q5_0_ref */
+void oracle_quantize_row_q5_0_ref(const float *x, void *vy, int64_t k) {
+    blk_q5_0 *y = (blk_q5_0 *)vy;
+    const int64_t nb = k / QK8_0;
+    for (int64_t i = 0; i < nb; i++) {
+        float amax = 0.0f, max = 0.0f;
+        for (int j = 0; j < 32; j++) {
+            const float v = x[i * 32 + j];
+            if (amax < fabsf(v)) { amax = fabsf(v); max = v; }
+        }
+        const float d = max / -16.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint32_t qh = 0;
+        for (int j = 0; j < 16; j++) {
+            const float x0 = x[i * 32 + j] * id;
+            const float x1 = x[i * 32 + 16 + j] * id;
+            const uint8_t xi0 = (uint8_t)imin_((int8_t)(x0 + 16.5f), 31) & 0x1F;
+            const uint8_t xi1 = (uint8_t)imin_((int8_t)(x1 + 16.5f), 31) & 0x1F;
+            y[i].qs[j] = (uint8_t)((xi0 & 0x0F) | ((xi1 & 0x0F) << 4));
+            qh |= (uint32_t)((xi0 & 0x10) >> 4) << j;
+            qh |= (uint32_t)((xi1 & 0x10) >> 4) << (j + 16);
+        }
+        y[i].d = F2H(d);
+        for (int b = 0; b < 4; b++) y[i].qh[b] = (uint8_t)(qh >> (8 * b));
     }
 }
 
@@ -300,56 +331,67 @@ static inline void get_scale_min_k4(int j, const uint8_t *q, uint8_t *d, uint8_t
     }
 }
 
+/* The scale/min selection shared by quantize_row_q4_K_ref (quants_k.rs:1861-1950,
+ * nmax 15, rmin -1, 20 steps) and quantize_row_q5_K_ref (quants_k.rs:1952-2040,
+ * nmax 31, rmin -0.5, 15 steps): per super-block the 6-bit scales and mins,
+ * d, dmin and the levels L[256] in 0..nmax. */
+static void k_quant_levels(const float *xb, int nmax, float rmin, int nstep, uint8_t L[QK_K], uint8_t sc[12],
+                           uint16_t *dh_out, uint16_t *dminh_out) {
+    uint8_t Laux[32];
+    float weights[32], mins[QK_K / 32], scales[QK_K / 32];
+    float max_scale = 0.0f, max_min = 0.0f;
+    for (int j = 0; j < QK_K / 32; j++) {
+        float sum_x2 = 0.0f;
+        for (int l = 0; l < 32; l++) sum_x2 += xb[32 * j + l] * xb[32 * j + l];
+        const float av_x = sqrtf(sum_x2 / 32.0f);
+        for (int l = 0; l < 32; l++) weights[l] = av_x + fabsf(xb[32 * j + l]);
+        scales[j] = make_qkx2_quants(32, nmax, xb + 32 * j, weights, L + 32 * j, &mins[j], Laux,
+                                     rmin, 0.1f, nstep, 0);
+        if (scales[j] > max_scale) max_scale = scales[j];
+        if (mins[j] > max_min) max_min = mins[j];
+    }
+    const float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
+    const float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
+    memset(sc, 0, 12);
+    for (int j = 0; j < QK_K / 32; j++) {
+        uint8_t ls = (uint8_t)nearest_int(inv_scale * scales[j]);
+        uint8_t lm = (uint8_t)nearest_int(inv_min * mins[j]);
+        if (ls > 63) ls = 63;
+        if (lm > 63) lm = 63;
+        if (j < 4) {
+            sc[j] = ls;
+            sc[j + 4] = lm;
+        } else {
+            sc[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+            sc[j - 4] |= (uint8_t)((ls >> 4) << 6);
+            sc[j] |= (uint8_t)((lm >> 4) << 6);
+        }
+    }
+    const uint16_t dh = F2H(max_scale / 63.0f);
+    const uint16_t dminh = F2H(max_min / 63.0f);
+    for (int j = 0; j < QK_K / 32; j++) {
+        uint8_t s, m;
+        get_scale_min_k4(j, sc, &s, &m);
+        const float d = H2F(dh) * (float)s;
+        if (d == 0.0f) continue;
+        const float dm = H2F(dminh) * (float)m;
+        for (int ii = 0; ii < 32; ii++) {
+            const int l = nearest_int((xb[32 * j + ii] + dm) / d);
+            L[32 * j + ii] = (uint8_t)imax_(0, imin_(nmax, l));
+        }
+    }
+    *dh_out = dh;
+    *dminh_out = dminh;
+}
+
 /* quants_k.rs:1861-1950 quantize_row_q4_K_ref */
 void oracle_quantize_row_q4_K_ref(const float *x, void *vy, int64_t k) {
     blk_q4_K *y = (blk_q4_K *)vy;
     const int64_t nb = k / QK_K;
-    uint8_t L[QK_K], Laux[32];
-    float weights[32], mins[QK_K / 32], scales[QK_K / 32];
+    uint8_t L[QK_K], sc[12];
     for (int64_t i = 0; i < nb; i++) {
-        const float *xb = x + i * QK_K;
-        float max_scale = 0.0f, max_min = 0.0f;
-        for (int j = 0; j < QK_K / 32; j++) {
-            float sum_x2 = 0.0f;
-            for (int l = 0; l < 32; l++) sum_x2 += xb[32 * j + l] * xb[32 * j + l];
-            const float av_x = sqrtf(sum_x2 / 32.0f);
-            for (int l = 0; l < 32; l++) weights[l] = av_x + fabsf(xb[32 * j + l]);
-            scales[j] = make_qkx2_quants(32, 15, xb + 32 * j, weights, L + 32 * j, &mins[j], Laux,
-                                         -1.0f, 0.1f, 20, 0);
-            if (scales[j] > max_scale) max_scale = scales[j];
-            if (mins[j] > max_min) max_min = mins[j];
-        }
-        const float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
-        const float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
-        uint8_t sc[12];
-        memset(sc, 0, sizeof sc);
-        for (int j = 0; j < QK_K / 32; j++) {
-            uint8_t ls = (uint8_t)nearest_int(inv_scale * scales[j]);
-            uint8_t lm = (uint8_t)nearest_int(inv_min * mins[j]);
-            if (ls > 63) ls = 63;
-            if (lm > 63) lm = 63;
-            if (j < 4) {
-                sc[j] = ls;
-                sc[j + 4] = lm;
-            } else {
-                sc[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
-                sc[j - 4] |= (uint8_t)((ls >> 4) << 6);
-                sc[j] |= (uint8_t)((lm >> 4) << 6);
-            }
-        }
-        const uint16_t dh = F2H(max_scale / 63.0f);
-        const uint16_t dminh = F2H(max_min / 63.0f);
-        for (int j = 0; j < QK_K / 32; j++) {
-            uint8_t s, m;
-            get_scale_min_k4(j, sc, &s, &m);
-            const float d = H2F(dh) * (float)s;
-            if (d == 0.0f) continue;
-            const float dm = H2F(dminh) * (float)m;
-            for (int ii = 0; ii < 32; ii++) {
-                const int l = nearest_int((xb[32 * j + ii] + dm) / d);
-                L[32 * j + ii] = (uint8_t)imax_(0, imin_(15, l));
-            }
-        }
+        uint16_t dh, dminh;
+        k_quant_levels(x + i * QK_K, 15, -1.0f, 20, L, sc, &dh, &dminh);
         y[i].d = dh;
         y[i].dmin = dminh;
         memcpy(y[i].scales, sc, 12);
@@ -358,6 +400,29 @@ void oracle_quantize_row_q4_K_ref(const float *x, void *vy, int64_t k) {
             for (int l = 0; l < 32; l++) q[l] = (uint8_t)(L[j + l] | (L[j + l + 32] << 4));
             q += 32;
         }
+    }
+}
+
+/* quants_k.rs:1952-2056 quantize_row_q5_K_ref: levels 0..31, the fifth bit
+ * of sub-block 2j / 2j+1 element e in bit 2j / 2j+1 of qh[e] */
+void oracle_quantize_row_q5_K_ref(const float *x, void *vy, int64_t k) {
+    blk_q5_K *y = (blk_q5_K *)vy;
+    const int64_t nb = k / QK_K;
+    uint8_t L[QK_K], sc[12];
+    for (int64_t i = 0; i < nb; i++) {
+        uint16_t dh, dminh;
+        k_quant_levels(x + i * QK_K, 31, -0.5f, 15, L, sc, &dh, &dminh);
+        y[i].d = dh;
+        y[i].dmin = dminh;
+        memcpy(y[i].scales, sc, 12);
+        memset(y[i].qh, 0, 32);
+        for (int j = 0; j < 4; j++)
+            for (int e = 0; e < 32; e++) {
+                int l1 = L[64 * j + e], l2 = L[64 * j + 32 + e];
+                if (l1 > 15) { l1 -= 16; y[i].qh[e] |= (uint8_t)(1u << (2 * j)); }
+                if (l2 > 15) { l2 -= 16; y[i].qh[e] |= (uint8_t)(2u << (2 * j)); }
+                y[i].qs[32 * j + e] = (uint8_t)(l1 | (l2 << 4));
+            }
     }
 }
 
@@ -508,6 +573,56 @@ void oracle_quantize_row_mxfp4_ref(const float *x, void *vy, int64_t k) {
 /* ---------------------------------------------------------- dequantizers */
 
 /* quants.rs:142 / :363 / quants_k.rs via quants.rs:540,584 / quants.rs:732 */
+/* q5_0 value e of a 32-block: nibble | bit e of qh << 4, minus 16
+ * (vec_dot.rs:661-686) */
+static inline int q5_0_val(const blk_q5_0 *x, int e) {
+    const uint32_t qh = (uint32_t)x->qh[0] | ((uint32_t)x->qh[1] << 8) | ((uint32_t)x->qh[2] << 16) |
+                        ((uint32_t)x->qh[3] << 24);
+    const int lo = e < 16 ? (x->qs[e] & 0x0F) : (x->qs[e - 16] >> 4);
+    return (lo | (int)(((qh >> e) & 1u) << 4)) - 16;
+}
+
+/* q5_0 x q8_0 and q8_0 x q8_0, one 32-block: the exact block sum */
+static inline int32_t isum_q5_0(const blk_q5_0 *x, const blk_q8_0 *y) {
+    int32_t s = 0;
+    for (int e = 0; e < 32; e++) s += q5_0_val(x, e) * y->qs[e];
+    return s;
+}
+static inline int32_t isum_q8_0(const blk_q8_0 *x, const blk_q8_0 *y) {
+    int32_t s = 0;
+    for (int e = 0; e < 32; e++) s += x->qs[e] * y->qs[e];
+    return s;
+}
+
+/* q5_K 5-bit values of sub-blocks 2j (low nibbles, qh bit 2j) and 2j+1 (high
+ * nibbles, qh bit 2j+1), element e of 32 (vec_dot.rs:954-962) */
+static inline int q5k_lo(const blk_q5_K *x, int j, int e) {
+    return (x->qs[32 * j + e] & 0x0F) | (((x->qh[e] >> (2 * j)) & 1) << 4);
+}
+static inline int q5k_hi(const blk_q5_K *x, int j, int e) {
+    return (x->qs[32 * j + e] >> 4) | (((x->qh[e] >> (2 * j + 1)) & 1) << 4);
+}
+
+/* q5_K x q8_K, whole super-block: {iacc, imin} as for q4_K
+ * (iacc = sum_s sc_s * sum q5*q8, imin = sum_s m_s * bsum32_s) */
+static inline void isum_q5_K(const blk_q5_K *x, const blk_q8_K *y, int32_t *iacc, int32_t *imin) {
+    int32_t ia = 0, im = 0;
+    for (int j = 0; j < 4; j++) {
+        uint8_t s0, m0, s1, m1;
+        get_scale_min_k4(2 * j, x->scales, &s0, &m0);
+        get_scale_min_k4(2 * j + 1, x->scales, &s1, &m1);
+        int32_t a = 0, b = 0;
+        for (int e = 0; e < 32; e++) {
+            a += q5k_lo(x, j, e) * y->qs[64 * j + e];
+            b += q5k_hi(x, j, e) * y->qs[64 * j + 32 + e];
+        }
+        ia += s0 * a + s1 * b;
+        im += m0 * (y->bsums[4 * j] + y->bsums[4 * j + 1]) + m1 * (y->bsums[4 * j + 2] + y->bsums[4 * j + 3]);
+    }
+    *iacc = ia;
+    *imin = im;
+}
+
 void oracle_dequantize_row(int type, const void *vx, float *y, int64_t k) {
     if (type == OR_Q4_0) {
         const blk_q4_0 *x = (const blk_q4_0 *)vx;
@@ -516,6 +631,27 @@ void oracle_dequantize_row(int type, const void *vx, float *y, int64_t k) {
             for (int j = 0; j < 16; j++) {
                 y[i * 32 + j] = (float)((x[i].qs[j] & 0x0F) - 8) * d;
                 y[i * 32 + 16 + j] = (float)((x[i].qs[j] >> 4) - 8) * d;
+            }
+        }
+    } else if (type == OR_Q5_0) { /* quants.rs:242-258 */
+        const blk_q5_0 *x = (const blk_q5_0 *)vx;
+        for (int64_t i = 0; i < k / QK8_0; i++) {
+            const float d = H2F(x[i].d);
+            for (int e = 0; e < 32; e++) y[i * 32 + e] = (float)q5_0_val(&x[i], e) * d;
+        }
+    } else if (type == OR_Q5_K) { /* quants.rs:549-585 */
+        const blk_q5_K *x = (const blk_q5_K *)vx;
+        for (int64_t i = 0; i < k / QK_K; i++) {
+            const float d = H2F(x[i].d), mn = H2F(x[i].dmin);
+            for (int j = 0; j < 4; j++) {
+                uint8_t s0, m0, s1, m1;
+                get_scale_min_k4(2 * j, x[i].scales, &s0, &m0);
+                get_scale_min_k4(2 * j + 1, x[i].scales, &s1, &m1);
+                const float d1 = d * (float)s0, mm1 = mn * (float)m0, d2 = d * (float)s1, mm2 = mn * (float)m1;
+                for (int e = 0; e < 32; e++) {
+                    y[i * QK_K + 64 * j + e] = d1 * (float)q5k_lo(&x[i], j, e) - mm1;
+                    y[i * QK_K + 64 * j + 32 + e] = d2 * (float)q5k_hi(&x[i], j, e) - mm2;
+                }
             }
         }
     } else if (type == OR_Q8_0) {
@@ -745,6 +881,72 @@ float oracle_vec_dot_q6_K_q8_K(int n, const void *vx, const void *vy) {
     return hsum8(acc);
 }
 
+/* vec_dot.rs:661-686: lane l holds elements 4l..4l+3, one fma per block */
+float oracle_vec_dot_q5_0_q8_0(int n, const void *vx, const void *vy) {
+    const blk_q5_0 *x = (const blk_q5_0 *)vx;
+    const blk_q8_0 *y = (const blk_q8_0 *)vy;
+    float acc[8] = {0};
+    for (int ib = 0; ib < n / QK8_0; ib++) {
+        const float d = H2F(x[ib].d) * H2F(y[ib].d);
+        for (int l = 0; l < 8; l++) {
+            int32_t q = 0;
+            for (int i = 0; i < 4; i++) q += q5_0_val(&x[ib], 4 * l + i) * y[ib].qs[4 * l + i];
+            acc[l] = fmaf(d, (float)q, acc[l]);
+        }
+    }
+    return hsum8(acc);
+}
+
+/* vec_dot.rs:732-756 */
+float oracle_vec_dot_q8_0_q8_0(int n, const void *vx, const void *vy) {
+    const blk_q8_0 *x = (const blk_q8_0 *)vx;
+    const blk_q8_0 *y = (const blk_q8_0 *)vy;
+    float acc[8] = {0};
+    for (int ib = 0; ib < n / QK8_0; ib++) {
+        const float d = H2F(x[ib].d) * H2F(y[ib].d);
+        for (int l = 0; l < 8; l++) {
+            int32_t q = 0;
+            for (int i = 0; i < 4; i++) q += x[ib].qs[4 * l + i] * y[ib].qs[4 * l + i];
+            acc[l] = fmaf(d, (float)q, acc[l]);
+        }
+    }
+    return hsum8(acc);
+}
+
+/* vec_dot.rs:928-980: the min term folds into one scalar per super-block
+ * first (summs), then eight lanes of scaled 5-bit sums */
+float oracle_vec_dot_q5_K_q8_K(int n, const void *vx, const void *vy) {
+    const blk_q5_K *x = (const blk_q5_K *)vx;
+    const blk_q8_K *y = (const blk_q8_K *)vy;
+    float acc[8] = {0}, summs = 0.0f;
+    for (int i = 0; i < n / QK_K; i++) {
+        const float d = y[i].d * H2F(x[i].d);
+        const float dmin = -y[i].d * H2F(x[i].dmin);
+        uint8_t sc[8], mn[8];
+        for (int j = 0; j < 8; j++) get_scale_min_k4(j, x[i].scales, &sc[j], &mn[j]);
+        int32_t m = 0;
+        for (int l = 0; l < 4; l++) {
+            const int32_t lo = y[i].bsums[4 * l] + y[i].bsums[4 * l + 1];
+            const int32_t hi = y[i].bsums[4 * l + 2] + y[i].bsums[4 * l + 3];
+            m += mn[2 * l] * lo + mn[2 * l + 1] * hi;
+        }
+        summs = fmaf((float)m, dmin, summs);
+        int32_t sumi[8] = {0};
+        for (int j = 0; j < QK_K / 64; j++)
+            for (int l = 0; l < 8; l++) {
+                int32_t a = 0, b = 0;
+                for (int ii = 0; ii < 4; ii++) {
+                    const int e = 4 * l + ii;
+                    a += q5k_lo(&x[i], j, e) * y[i].qs[64 * j + e];
+                    b += q5k_hi(&x[i], j, e) * y[i].qs[64 * j + 32 + e];
+                }
+                sumi[l] += sc[2 * j] * a + sc[2 * j + 1] * b;
+            }
+        for (int l = 0; l < 8; l++) acc[l] = fmaf(d, (float)sumi[l], acc[l]);
+    }
+    return hsum8(acc) + summs;
+}
+
 /* ------------------------------------------------------- routed MUL_MAT */
 
 static int omp_threads(int nthreads) {
@@ -758,13 +960,14 @@ static int omp_threads(int nthreads) {
 
 static int route_of(int type, int64_t rows, int64_t cols) {
     if ((type == OR_Q4_0 || type == OR_Q4_K) && rows % 8 == 0) return ORACLE_ROUTE_REPACK;
-    if ((type == OR_Q4_K || type == OR_Q6_K) && cols >= 8) return ORACLE_ROUTE_TILED;
+    if ((type == OR_Q4_K || type == OR_Q5_K || type == OR_Q6_K) && cols >= 8) return ORACLE_ROUTE_TILED;
     if (type == OR_Q4_0 && cols >= 2) return -1; /* tinyBLAS: out of scope */
     return ORACLE_ROUTE_VECDOT;
 }
 
 static size_t act_row_size(int type, int64_t n) {
-    return type == OR_Q4_0 ? (size_t)(n / 32) * sizeof(blk_q8_0) : (size_t)(n / QK_K) * sizeof(blk_q8_K);
+    return (type == OR_Q4_0 || type == OR_Q5_0 || type == OR_Q8_0) ? (size_t)(n / 32) * sizeof(blk_q8_0)
+                                                                   : (size_t)(n / QK_K) * sizeof(blk_q8_K);
 }
 
 /* compute.rs:1504-1549 (wdata pass) and compute.rs:5350-5398 (repack wdata) */
@@ -775,7 +978,7 @@ int oracle_mul_mat_act(int type, int64_t n, int64_t rows, const float *x, int64_
     const int64_t nr4 = cols - cols % 4;
     for (int64_t c = 0; c < cols; c++) {
         uint8_t *dst = (uint8_t *)act + (size_t)c * rs;
-        if (type == OR_Q4_0)
+        if (type == OR_Q4_0 || type == OR_Q5_0 || type == OR_Q8_0)
             oracle_quantize_row_q8_0(x + c * n, dst, n);
         else if (type == OR_Q4_K && route == ORACLE_ROUTE_REPACK && c < nr4)
             oracle_quantize_row_q8_K_mat(x + c * n, dst, n);
@@ -790,7 +993,9 @@ int oracle_mul_mat(int type, const void *w, int64_t n, int64_t rows, const float
     const int route = route_of(type, rows, cols);
     if (route_out) *route_out = route;
     if (route < 0) return -1;
-    if (type != OR_Q4_0 && type != OR_Q4_K && type != OR_Q6_K) return -2;
+    if (type != OR_Q4_0 && type != OR_Q4_K && type != OR_Q6_K && type != OR_Q5_0 && type != OR_Q8_0 &&
+        type != OR_Q5_K)
+        return -2;
     const size_t rs = act_row_size(type, n);
     uint8_t *act = (uint8_t *)malloc(rs * (size_t)cols);
     if (!act) return -3;
@@ -868,6 +1073,50 @@ int oracle_mul_mat(int type, const void *w, int64_t n, int64_t rows, const float
                 else if (route == ORACLE_ROUTE_TILED) v = acc;
                 else v = oracle_vec_dot_q4_K_q8_K((int)n, wr, a);
                 out[c * rows + r] = v;
+            }
+        }
+    } else if (type == OR_Q5_0 || type == OR_Q8_0) {
+        /* the row vec_dot; tinyBLAS_Q0 (cols >= 2) keeps one accumulator per
+         * output with the same lanes and fma order (tinyblas.rs:55-75) */
+        const int64_t nb = n / 32;
+        const size_t wbs = type == OR_Q5_0 ? sizeof(blk_q5_0) : sizeof(blk_q8_0);
+#pragma omp parallel for num_threads(nth) schedule(static)
+        for (int64_t r = 0; r < rows; r++) {
+            const uint8_t *wr = (const uint8_t *)w + (size_t)r * nb * wbs;
+            for (int64_t c = 0; c < cols; c++) {
+                const blk_q8_0 *a = (const blk_q8_0 *)(act + (size_t)c * rs);
+                if (subsums)
+                    for (int64_t b = 0; b < nb; b++)
+                        subsums[((size_t)c * rows + r) * nb + b] =
+                            type == OR_Q5_0 ? isum_q5_0((const blk_q5_0 *)wr + b, &a[b])
+                                            : isum_q8_0((const blk_q8_0 *)wr + b, &a[b]);
+                out[c * rows + r] = type == OR_Q5_0 ? oracle_vec_dot_q5_0_q8_0((int)n, wr, a)
+                                                    : oracle_vec_dot_q8_0_q8_0((int)n, wr, a);
+            }
+        }
+    } else if (type == OR_Q5_K) {
+        const int64_t nb = n / QK_K;
+#pragma omp parallel for num_threads(nth) schedule(static)
+        for (int64_t r = 0; r < rows; r++) {
+            const blk_q5_K *wr = (const blk_q5_K *)((const uint8_t *)w + (size_t)r * nb * sizeof(blk_q5_K));
+            for (int64_t c = 0; c < cols; c++) {
+                const blk_q8_K *a = (const blk_q8_K *)(act + (size_t)c * rs);
+                float acc = 0.0f;
+                for (int64_t b = 0; b < nb; b++) {
+                    int32_t ia, im;
+                    isum_q5_K(&wr[b], &a[b], &ia, &im);
+                    if (subsums) {
+                        subsums[(((size_t)c * rows + r) * nb + b) * 2 + 0] = ia;
+                        subsums[(((size_t)c * rows + r) * nb + b) * 2 + 1] = im;
+                    }
+                    if (route == ORACLE_ROUTE_TILED) {
+                        /* tiled.rs:826-838 with the q5_K constants (tiled.rs:238) */
+                        float res = H2F(wr[b].d) * (float)ia;
+                        res = fmaf(-H2F(wr[b].dmin), (float)im, res);
+                        acc = fmaf(res, a[b].d, acc);
+                    }
+                }
+                out[c * rows + r] = route == ORACLE_ROUTE_TILED ? acc : oracle_vec_dot_q5_K_q8_K((int)n, wr, a);
             }
         }
     } else { /* Q6_K */

@@ -22,8 +22,8 @@ extern "C" {
 
 /* ggml type ids (crates/ggml/src/types.rs:15) */
 enum {
-    OR_F32 = 0, OR_F16 = 1, OR_Q4_0 = 2, OR_Q8_0 = 8, OR_Q4_K = 12,
-    OR_Q6_K = 14, OR_Q8_K = 15, OR_MXFP4 = 39
+    OR_F32 = 0, OR_F16 = 1, OR_Q4_0 = 2, OR_Q5_0 = 6, OR_Q8_0 = 8, OR_Q4_K = 12,
+    OR_Q5_K = 13, OR_Q6_K = 14, OR_Q8_K = 15, OR_MXFP4 = 39
 };
 
 /* ---- scalar helpers ---- */
@@ -36,6 +36,8 @@ float    oracle_e8m0_to_fp32_half(uint8_t e);     /* quants.rs:682; pinned by cl
 void oracle_quantize_row_q4_0_ref(const float *x, void *y, int64_t k);  /* quants.rs:124; quants_ref.bin */
 void oracle_quantize_row_q4_K_ref(const float *x, void *y, int64_t k);  /* quants_k.rs:1861; quants_ref.bin */
 void oracle_quantize_row_q6_K_ref(const float *x, void *y, int64_t k);  /* quants_k.rs:2058; quants_ref.bin */
+void oracle_quantize_row_q5_0_ref(const float *x, void *y, int64_t k);  /* quants.rs:207; quants_ref.bin */
+void oracle_quantize_row_q5_K_ref(const float *x, void *y, int64_t k);  /* quants_k.rs:1952; quants_ref.bin */
 void oracle_quantize_row_mxfp4_ref(const float *x, void *y, int64_t k); /* absent in the reference; quants_ref_fp4.bin */
 void oracle_quantize_row_q8_0_ref(const float *x, void *y, int64_t k);  /* quants.rs:302; quants_ref.bin */
 
@@ -52,6 +54,9 @@ void oracle_dequantize_row(int type, const void *x, float *y, int64_t k);
 float oracle_vec_dot_q4_0_q8_0(int n, const void *x, const void *y);  /* vec_dot.rs:599 */
 float oracle_vec_dot_q4_K_q8_K(int n, const void *x, const void *y);  /* vec_dot.rs:872 */
 float oracle_vec_dot_q6_K_q8_K(int n, const void *x, const void *y);  /* vec_dot.rs:990 */
+float oracle_vec_dot_q5_0_q8_0(int n, const void *x, const void *y);  /* vec_dot.rs:661; mulmat_ref*.bin type 6 */
+float oracle_vec_dot_q8_0_q8_0(int n, const void *x, const void *y);  /* vec_dot.rs:732; mulmat_ref*.bin type 8 */
+float oracle_vec_dot_q5_K_q8_K(int n, const void *x, const void *y);  /* vec_dot.rs:928; mulmat_ref*.bin type 13 */
 
 /*
  * The reference's MUL_MAT routing for a 2-D quantized weight W [rows x n]
@@ -64,7 +69,9 @@ float oracle_vec_dot_q6_K_q8_K(int n, const void *x, const void *y);  /* vec_dot
  *   K-quant, not repacked, cols>=8 -> tiled                     (tiled.rs:1656)
  *   otherwise row vec_dot with quantize_row_q8_K_ref / quantize_row_q8_0
  * Q4_0 with rows%8!=0 and cols>=2 would take tinyBLAS, which is out of scope:
- * returns -1 there.
+ * returns -1 there.  Q5_0 / Q8_0 always take the row vec_dot, whose values
+ * tinyBLAS_Q0 reproduces for cols>=2 (tinyblas.rs:55-75); Q5_K (no x86
+ * repack) takes tiled for cols>=8, else vec_dot.
  * out is [cols x rows] f32.  subsums (optional) receives the exact integer
  * partials per (col, row, block) -- see ghip.h ghip_mul_mat_subsums for the
  * layout.  route (optional) receives the route id (see ORACLE_ROUTE_*).

@@ -13,9 +13,11 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_DIR = os.path.join(ROOT, "oracle")
 LIB_PATH = os.path.join(ORACLE_DIR, "liboracle.so")
 
-F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, MXFP4 = 0, 1, 2, 8, 12, 14, 15, 39
-BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210),
-         Q8_K: (256, 292), MXFP4: (32, 17)}
+F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, MXFP4 = 0, 1, 2, 6, 8, 12, 13, 14, 15, 39
+BLOCK = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176),
+         Q6_K: (256, 210), Q8_K: (256, 292), MXFP4: (32, 17)}
+# weight type -> activation type of its dot (vec_dot_type)
+ACT_TYPE = {Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K}
 ROUTE_REPACK, ROUTE_TILED, ROUTE_VECDOT = 1, 2, 3
 
 
@@ -59,6 +61,7 @@ def lib():
         L.oracle_e8m0_to_fp32_half.restype = C.c_float
         L.oracle_e8m0_to_fp32_half.argtypes = [C.c_uint8]
         for f in ["quantize_row_q4_0_ref", "quantize_row_q4_K_ref", "quantize_row_q6_K_ref",
+                  "quantize_row_q5_0_ref", "quantize_row_q5_K_ref",
                   "quantize_row_mxfp4_ref", "quantize_row_q8_0_ref", "quantize_row_q8_0",
                   "quantize_row_q8_K_ref", "quantize_row_q8_K_mat"]:
             fn = getattr(L, "oracle_" + f)
@@ -66,7 +69,8 @@ def lib():
             fn.argtypes = [vp, vp, i64]
         L.oracle_dequantize_row.restype = None
         L.oracle_dequantize_row.argtypes = [C.c_int, vp, vp, i64]
-        for f in ["vec_dot_q4_0_q8_0", "vec_dot_q4_K_q8_K", "vec_dot_q6_K_q8_K"]:
+        for f in ["vec_dot_q4_0_q8_0", "vec_dot_q4_K_q8_K", "vec_dot_q6_K_q8_K", "vec_dot_q5_0_q8_0",
+                  "vec_dot_q8_0_q8_0", "vec_dot_q5_K_q8_K"]:
             fn = getattr(L, "oracle_" + f)
             fn.restype = C.c_float
             fn.argtypes = [C.c_int, vp, vp]
@@ -88,7 +92,8 @@ def _p(a):
 
 
 _QUANT = {Q4_0: "quantize_row_q4_0_ref", Q4_K: "quantize_row_q4_K_ref",
-          Q6_K: "quantize_row_q6_K_ref", MXFP4: "quantize_row_mxfp4_ref"}
+          Q6_K: "quantize_row_q6_K_ref", MXFP4: "quantize_row_mxfp4_ref",
+          Q5_0: "quantize_row_q5_0_ref", Q5_K: "quantize_row_q5_K_ref", Q8_0: "quantize_row_q8_0_ref"}
 
 
 def quantize(ty, x, kind=None):
@@ -118,21 +123,22 @@ def mul_mat(ty, w, n, rows, x, cols, want_subsums=False, nthreads=0):
     out = np.zeros((cols, rows), dtype=np.float32)
     sub = None
     if want_subsums:
-        per = {Q4_0: n // 32, Q4_K: (n // 256) * 2, Q6_K: n // 256}[ty]
+        per = {Q4_0: n // 32, Q5_0: n // 32, Q8_0: n // 32, Q4_K: (n // 256) * 2, Q5_K: (n // 256) * 2,
+               Q6_K: n // 256}[ty]
         sub = np.zeros((cols, rows, per), dtype=np.int32)
     route = C.c_int(0)
     rc = lib().oracle_mul_mat(ty, _p(np.ascontiguousarray(w)), n, rows, _p(x), cols, _p(out),
                               _p(sub), C.byref(route), nthreads)
     if rc < 0:
         raise ValueError(f"oracle_mul_mat rc={rc}")
-    if sub is not None and ty == Q4_K:
+    if sub is not None and ty in (Q4_K, Q5_K):
         sub = sub.reshape(cols, rows, n // 256, 2)
     return out, route.value, sub
 
 
 def mul_mat_act(ty, n, rows, x, cols):
     x = np.ascontiguousarray(x, dtype=np.float32)
-    act_ty = Q8_0 if ty == Q4_0 else Q8_K
+    act_ty = ACT_TYPE[ty]
     act = np.zeros(cols * row_size(act_ty, n), dtype=np.uint8)
     rc = lib().oracle_mul_mat_act(ty, n, rows, _p(x), cols, _p(act))
     if rc < 0:

@@ -119,10 +119,12 @@ def test_llama3_decode_shapes(be, name, ty, n, rows, cols):
 
 def test_unsupported_type_raises(be):
     import ghip
-    w = torch.zeros((8, 34), dtype=torch.uint8, device="cuda")
+    # Q4_1 (type 3, 20-byte blocks) has no kernel here: a status, no fallback
+    ghip.BLOCK.setdefault(3, (32, 20))
+    w = torch.zeros((8, 20), dtype=torch.uint8, device="cuda")
     x = torch.zeros((1, 32), dtype=torch.float32, device="cuda")
-    with pytest.raises(ghip.GhipError):
-        be.mul_mat(w, O.Q8_0, 32, x)
+    with pytest.raises(ghip.GhipError, match="not supported"):
+        be.mul_mat(w, 3, 32, x)
 
 
 # ---------------------------------------------------------------- prefill GEMM

@@ -1,0 +1,139 @@
+"""GPU parity of GGML_OP_MUL_MAT for the further decode weight types Q5_0, Q8_0
+(Q8_0 activations) and Q5_K (Q8_K activations), against the CPU oracle and
+against the reference's own dumps (mulmat_ref.bin / mulmat_ref_c1.bin,
+types 6, 8, 13).
+
+Two kinds of weights:
+  * the reference quantizers' output for N(0, 0.02) rows (quantize_row_q5_0_ref,
+    quantize_row_q8_0_ref, quantize_row_q5_K_ref) -- the bar: Q8 activation
+    bytes and int32 sub-sums bit-exact, fp32 within 1e-5 by
+    rel_err = max |a-b| / max(|b|, 1) (vec_dot.rs:2355);
+  * random block bytes with finite f16 scales, which reach every code, qh bit
+    and packed 6-bit scale: sub-sums bit-exact, fp32 within 1e-4.  Random
+    Q5_K mins up to 63 * dmin make the reference's own order (main and min
+    terms summed apart, subtracted at the end, vec_dot.rs:940-978) cancel
+    terms of ~1e3, so its fp32 result carries ~1e-3 of rounding of its own.
+"""
+import numpy as np
+import pytest
+
+import fixtures as fx
+import oracle_lib as O
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+TYPES = [O.Q5_0, O.Q8_0, O.Q5_K]
+
+
+@pytest.fixture(scope="module")
+def be():
+    import ghip
+    b = ghip.Backend(0)
+    yield b
+    b.close()
+
+
+def rel_err(a, b):
+    return float(np.max(np.abs(a - b) / np.maximum(np.abs(b), 1.0))) if a.size else 0.0
+
+
+def random_blocks(ty, n, rows, seed):
+    """rows x n of random `ty` blocks; d (and dmin) are f16 in [2^-10, 2^-4)"""
+    rng = np.random.default_rng(seed)
+    qk, bs = O.BLOCK[ty]
+    w = rng.integers(0, 256, size=(rows, n // qk, bs), dtype=np.uint8)
+    offs = (0, 2) if ty == O.Q5_K else (0,)
+    for off in offs:
+        e = rng.integers(0x1400, 0x2c00, size=(rows, n // qk), dtype=np.uint16)
+        w[:, :, off:off + 2] = e.view(np.uint8).reshape(rows, n // qk, 2)
+    return w.reshape(rows, (n // qk) * bs)
+
+
+def quantized(ty, n, rows, seed):
+    wf = (np.random.default_rng(seed).standard_normal((rows, n)) * 0.02).astype(np.float32)
+    return O.quantize(ty, wf).reshape(rows, O.row_size(ty, n))
+
+
+def run_case(be, ty, n, rows, cols, seed=0, check_sub=True, x=None, weights="quant"):
+    w = quantized(ty, n, rows, seed) if weights == "quant" else random_blocks(ty, n, rows, seed)
+    tol = TOL if weights == "quant" else 1e-4
+    if x is None:
+        x = np.random.default_rng(seed + 1).standard_normal((cols, n)).astype(np.float32)
+    want, route, want_sub = O.mul_mat(ty, w, n, rows, x, cols, want_subsums=check_sub)
+    wd = torch.from_numpy(w).cuda()
+    xd = torch.from_numpy(x).cuda()
+    print(f"case type={ty} n={n} rows={rows} cols={cols} route={route}", flush=True)
+    got = be.mul_mat(wd, ty, n, xd).cpu().numpy()
+    act = be.mul_mat_act(wd, ty, n, xd).cpu().numpy().reshape(-1)
+    assert np.array_equal(act, O.mul_mat_act(ty, n, rows, x, cols)), "activation bytes differ"
+    if check_sub:
+        sub = be.mul_mat_subsums(wd, ty, n, xd).cpu().numpy()
+        assert np.array_equal(sub, want_sub), "int32 sub-sums differ"
+    err = rel_err(got, want)
+    assert err <= tol, f"rel_err {err:.3e}"
+
+
+@pytest.mark.parametrize("ty", TYPES)
+@pytest.mark.parametrize("cols", [1, 2, 3, 4, 5, 8, 11])
+def test_small_shapes(be, ty, cols):
+    for n, rows in [(512, 64), (1024, 72), (768, 100), (256, 8)]:
+        run_case(be, ty, n, rows, cols, seed=cols + ty)
+        run_case(be, ty, n, rows, cols, seed=cols + ty, weights="random")
+
+
+@pytest.mark.parametrize("ty", TYPES)
+def test_ragged_k(be, ty):
+    """K not a multiple of one wavefront's span; an odd number of 32-blocks
+    (the last lane holds a lone block)"""
+    if ty == O.Q5_K:
+        run_case(be, ty, 2816, 24, 1)
+        run_case(be, ty, 2816, 24, 3, weights="random")
+    else:
+        run_case(be, ty, 32 * 45, 16, 1)
+        run_case(be, ty, 32 * 45, 13, 4, weights="random")
+        run_case(be, ty, 2880, 24, 2)
+
+
+@pytest.mark.parametrize("ty", TYPES)
+@pytest.mark.parametrize("n,rows", [(4096, 4096), (14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("cols", [1, 2, 8])
+def test_llama_decode_shapes(be, ty, n, rows, cols):
+    run_case(be, ty, n, rows, cols, seed=3, check_sub=(cols <= 2))
+
+
+@pytest.mark.parametrize("name", ["mulmat_ref_c1.bin", "mulmat_ref.bin"])
+def test_reference_dumps_on_gpu(be, name):
+    """the reference's own outputs (4 rows x 1024, 1 or 3 columns), computed by
+    the GPU from the dumped weight bytes and activations"""
+    seen = set()
+    for tid, n, rows, cols, xq, y, dst in fx.mulmat_sections(name):
+        if tid not in TYPES:
+            continue
+        wd = torch.from_numpy(np.ascontiguousarray(xq).reshape(rows, -1)).cuda()
+        xd = torch.from_numpy(np.ascontiguousarray(y, dtype=np.float32).reshape(cols, n)).cuda()
+        print(f"dump {name} type={tid}", flush=True)
+        got = be.mul_mat(wd, tid, n, xd).cpu().numpy()
+        assert rel_err(got, dst) <= TOL, (tid, rel_err(got, dst))
+        seen.add(tid)
+    assert seen == set(TYPES)
+
+
+def test_zero_and_extreme_codes(be):
+    """all-zero activations, and Q8_0 weights holding -128 (never produced by
+    the quantizer, valid for the dot)"""
+    n, rows = 1024, 16
+    x = np.zeros((2, n), dtype=np.float32)
+    x[1] = np.random.default_rng(9).standard_normal(n).astype(np.float32)
+    for ty in TYPES:
+        run_case(be, ty, n, rows, 2, seed=11, x=x.copy())
+        run_case(be, ty, n, rows, 2, seed=11, x=x.copy(), weights="random")
+    w = random_blocks(O.Q8_0, n, rows, 12).reshape(rows, n // 32, 34)
+    w[:, :, 2:] = 0x80
+    w = w.reshape(rows, -1)
+    want, _, want_sub = O.mul_mat(O.Q8_0, w, n, rows, x, 2, want_subsums=True)
+    got = be.mul_mat(torch.from_numpy(w).cuda(), O.Q8_0, n, torch.from_numpy(x).cuda()).cpu().numpy()
+    sub = be.mul_mat_subsums(torch.from_numpy(w).cuda(), O.Q8_0, n, torch.from_numpy(x).cuda()).cpu().numpy()
+    assert np.array_equal(sub, want_sub)
+    assert rel_err(got, want) <= 1e-4

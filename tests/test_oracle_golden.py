@@ -50,7 +50,8 @@ def test_e8m0_closed_form():
 
 QUANT_NAME = {O.Q4_0: "quantize_row_q4_0_ref", O.Q8_0: "quantize_row_q8_0_ref",
               O.Q4_K: "quantize_row_q4_K_ref", O.Q6_K: "quantize_row_q6_K_ref",
-              O.Q8_K: "quantize_row_q8_K_ref"}
+              O.Q8_K: "quantize_row_q8_K_ref", O.Q5_0: "quantize_row_q5_0_ref",
+              O.Q5_K: "quantize_row_q5_K_ref"}
 
 
 def test_quants_ref_bit_exact():
@@ -108,6 +109,65 @@ def test_mulmat_vec_dot_bit_exact(name):
             assert np.array_equal(out.view(np.uint32), dst.view(np.uint32)), f"type {tid} {name}"
         checked += 1
     assert checked == 3
+
+
+@pytest.mark.parametrize("name", ["mulmat_ref_c1.bin", "mulmat_ref.bin"])
+def test_mulmat_q5_0_q8_0_q5_K_bit_exact(name):
+    """The same dumps for Q5_0 (type 6), Q8_0 (type 8) and Q5_K (type 13): 4 rows,
+    1 or 3 columns, so the row vec_dot (vec_dot.rs:661/732/928) -- for Q5_0/Q8_0
+    with 3 columns the reference ran tinyBLAS_Q0, which keeps the vec_dot's
+    lanes and fma order (tinyblas.rs:55-75): bit-exact either way."""
+    seen = set()
+    for tid, n, rows, cols, xq, y, dst in fx.mulmat_sections(name):
+        if tid not in (O.Q5_0, O.Q8_0, O.Q5_K):
+            continue
+        out, route, sub = O.mul_mat(tid, xq, n, rows, y, cols, want_subsums=True)
+        assert route == O.ROUTE_VECDOT
+        assert np.array_equal(out.view(np.uint32), dst.view(np.uint32)), f"type {tid} {name}"
+        seen.add(tid)
+    assert seen == {O.Q5_0, O.Q8_0, O.Q5_K}
+
+
+@pytest.mark.parametrize("ty", ["Q5_0", "Q8_0", "Q5_K"])
+def test_new_type_subsums_brute_force(ty):
+    """Integer partials against a float64 brute force of the dequantized blocks:
+    random block bytes (finite d), random activations, the oracle's own Q8
+    activation rows; sum_s block scale * partial must equal the dot of the
+    dequantized values exactly (every product is an exact small integer)."""
+    t = getattr(O, ty)
+    rng = np.random.default_rng(7)
+    qk, bs = O.BLOCK[t]
+    n, rows = 512, 3
+    w = rng.integers(0, 256, size=rows * (n // qk) * bs, dtype=np.uint8)
+    wv = w.reshape(rows, n // qk, bs)
+    # finite f16 scales: d (and dmin) in [2^-10, 2^-5)
+    for off in ((0,) if qk == 32 else (0, 2)):
+        e = rng.integers(0x1400, 0x2800, size=(rows, n // qk), dtype=np.uint16)
+        wv[:, :, off:off + 2] = e.view(np.uint8).reshape(rows, n // qk, 2)
+    x = rng.standard_normal((1, n)).astype(np.float32)
+    out, route, sub = O.mul_mat(t, w, n, rows, x, 1, want_subsums=True)
+    act = O.mul_mat_act(t, n, rows, x, 1)
+    at = O.ACT_TYPE[t]
+    aq = O.dequantize(at, act, n).astype(np.float64)
+    for r in range(rows):
+        wf = O.dequantize(t, w[r * O.row_size(t, n):(r + 1) * O.row_size(t, n)], n).astype(np.float64)
+        ref = float(np.dot(wf, aq))
+        assert abs(float(out[0, r]) - ref) <= 1e-5 * max(abs(ref), 1.0), (ty, r)
+    # block sums: recompute from integer codes
+    codes = act.reshape(-1)
+    if qk == 32:
+        aqs = np.frombuffer(codes.tobytes(), dtype=np.uint8).reshape(n // 32, 34)[:, 2:].view(np.int8).astype(np.int64)
+        for r in range(rows):
+            for b in range(n // 32):
+                blk = wv[r, b]
+                if t == O.Q8_0:
+                    q = blk[2:].view(np.int8).astype(np.int64)
+                else:
+                    qh = int.from_bytes(bytes(blk[2:6]), "little")
+                    qs = blk[6:22].astype(np.int64)
+                    lo = np.concatenate([qs & 15, qs >> 4])
+                    q = (lo | (((qh >> np.arange(32)) & 1) << 4)) - 16
+                assert int(np.dot(q, aqs[b])) == int(sub[0, r, b]), (ty, r, b)
 
 
 def test_tiled_q4k_q6k_bit_exact():
@@ -285,3 +345,16 @@ def test_flash_attn_against_float64():
             p = np.exp(s - s.max(1, keepdims=True))
             ref[:, h] = (p / p.sum(1, keepdims=True)) @ vv
         assert np.max(np.abs(out - ref)) < 2e-3
+    if t == O.Q5_K:
+        # {iacc, imin} per super-block rebuild the float64 dot exactly:
+        # sum_b da_b * (d_b * iacc_b - dmin_b * imin_b)
+        ab = np.frombuffer(act.tobytes(), dtype=np.uint8).reshape(n // 256, 292)
+        da = ab[:, :4].copy().view(np.float32).reshape(-1).astype(np.float64)
+        for r in range(rows):
+            d = wv[r, :, 0:2].copy().view(np.float16).reshape(-1).astype(np.float64)
+            dmin = wv[r, :, 2:4].copy().view(np.float16).reshape(-1).astype(np.float64)
+            ia, im = sub[0, r, :, 0].astype(np.float64), sub[0, r, :, 1].astype(np.float64)
+            got = float(np.sum(da * (d * ia - dmin * im)))
+            wf = O.dequantize(t, w[r * O.row_size(t, n):(r + 1) * O.row_size(t, n)], n).astype(np.float64)
+            ref = float(np.dot(wf, aq))
+            assert abs(got - ref) <= 1e-9 * max(abs(ref), 1.0), (r, got, ref)

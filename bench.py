@@ -171,6 +171,36 @@ def q4_0_bench(be, torch, np):
             "frac_hbm": round(alg / us / 1e3 / HBM_PEAK_GBS, 4)}
 
 
+def more_types_bench(be, torch, np):
+    """Q5_0 / Q8_0 / Q5_K decode GEMV, 4096 -> 14336 at batch 1 (the gate/up
+    shape), 16 rotating weight copies.  Weights are random blocks with finite
+    f16 scales built on the device: the kernels' time does not depend on
+    the values."""
+    import ghip
+    k, n = 4096, 14336
+    res = {}
+    g = torch.Generator(device="cuda").manual_seed(4)
+    x = torch.randn((1, k), device="cuda", generator=g)
+    out = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    for name, ty in (("q5_0", ghip.Q5_0), ("q8_0", ghip.Q8_0), ("q5_K", ghip.Q5_K)):
+        qk, bs = ghip.BLOCK[ty]
+        w0 = torch.randint(0, 256, (n, k // qk, bs), dtype=torch.uint8, device="cuda", generator=g)
+        scale = torch.full((n, k // qk), 0x2000, dtype=torch.int16, device="cuda")  # f16 2^-7
+        w0[:, :, 0:2] = scale.view(torch.uint8).view(n, k // qk, 2)
+        if ty == ghip.Q5_K:
+            w0[:, :, 2:4] = scale.view(torch.uint8).view(n, k // qk, 2)
+        w0 = w0.view(n, -1).contiguous()
+        copies = max(2, min(16, (512 << 20) // w0.numel()))
+        ws = [w0] + [w0.clone() for _ in range(copies - 1)]
+        us = graph_time_us(torch, lambda i: be.mul_mat(ws[i % copies], ty, k, x, out=out), 64)
+        alg = w0.numel() + k * 4 + n * 4
+        log(f"{name} 4096->14336 GEMV op: {us:.2f} us, {alg / us / 1e3:.1f} GB/s")
+        res[name] = {"us_op": round(us, 2), "GB/s": round(alg / us / 1e3, 1), "bytes": alg,
+                     "frac_hbm": round(alg / us / 1e3 / HBM_PEAK_GBS, 4)}
+        del ws, w0
+    return res
+
+
 def measured_traffic():
     """HBM bytes per launch of the dominant kernel, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (None when absent)."""
@@ -363,6 +393,7 @@ def main():
         del sets
         torch.cuda.empty_cache()
         extras["q4_0_gemv_4096"] = q4_0_bench(be, torch, np)
+        extras["gemv_q5_0_q8_0_q5_K"] = more_types_bench(be, torch, np)
         extras["prefill_gemm_q4K"] = gemm_bench(be, torch, np)
         extras["moe_mxfp4"] = moe_bench(be, torch, np)
         extras["flash_attn_f16kv"] = fa_bench(be, torch, np)

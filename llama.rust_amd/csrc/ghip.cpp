@@ -648,7 +648,8 @@ ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const g
         return ctx->launch("ghip_fa_merge", dim3((unsigned)H), dim3(256), 0, s, (const float *)ws, p.sinks,
                            (float *)dst->data, 1, H, ns, D);
     }
-    const char *fwd = D == 128 ? "ghip_fa_fwd_d128" : "ghip_fa_fwd_d64";
+    const char *fwd = softcap != 0.0f ? (D == 128 ? "ghip_fa_fwd_sc_d128" : "ghip_fa_fwd_sc_d64")
+                                      : (D == 128 ? "ghip_fa_fwd_d128" : "ghip_fa_fwd_d64");
     st = ctx->launch(fwd, dim3((unsigned)(qtiles * H_kv * nsplit)), dim3(64 * G * QS), 0, s, p);
     if (st != GHIP_STATUS_SUCCESS) return st;
     const float *sk = sinks ? (const float *)sinks->data : nullptr;

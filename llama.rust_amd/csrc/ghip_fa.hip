@@ -28,7 +28,8 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int FA_BQ = 32;   // query positions per workgroup
 constexpr int FA_BK = 64;   // keys per tile
-constexpr int FA_KPAD = 8;  // LDS row padding (halfs)
+constexpr int FA_KPAD = 8;  // K row padding (halfs): 272-byte rows, 8 lanes' 16-byte reads hit distinct banks
+constexpr int FA_VPAD = 4;  // V^T row padding (halfs): 136-byte rows, 16 lanes' 8-byte reads hit distinct banks
 
 DEV int crow32(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
 
@@ -63,7 +64,7 @@ DEV float head_slope(const FaParams &p, int h) {
 
 template <int D, bool SOFTCAP>
 __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks, _Float16 *Vt) {
-    constexpr int KS = D + FA_KPAD, VS = FA_BK + FA_KPAD;
+    constexpr int KS = D + FA_KPAD, VS = FA_BK + FA_VPAD;
     constexpr int NKC = FA_BK * D / 8;           // 16-byte K chunks per tile
     constexpr int NVB = (FA_BK / 4) * (D / 8);   // 4-key x 8-dim V blocks per tile
     // a workgroup has at least 4 wavefronts (G * QS >= 4)
@@ -138,7 +139,7 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks, _Fl
     const uint32_t kstep = (uint32_t)(nthr / (D / 8)) * krow;  // per i
     const uint32_t vstep = (uint32_t)(nthr >> 4) * 16u;
     const uint32_t mth = (uint32_t)(tvalid ? t : 0) * mrowb + (uint32_t)(8 * h2);
-    auto fetch = [&](int k0n) {
+    auto fetch_kv = [&](int k0n) {
         const uint32_t kt = (uint32_t)k0n * krow + kth, vt = (uint32_t)k0n * vrow + vth;
 #pragma unroll
         for (int i = 0; i < MAXK; i++)
@@ -152,6 +153,11 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks, _Fl
                     vr[i][r] = __builtin_bit_cast(
                         uint4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vt + i * vstep + r * vrow, 0, 0));
             }
+    };
+    // the next tile's mask values are loaded at the end of an iteration, so
+    // mr is not live across P V (their latency hides behind the next tile's
+    // staging and K Q^T MFMAs)
+    auto fetch_mask = [&](int k0n) {
         if (mrow) {
             const uint32_t mt = (uint32_t)k0n * 2u + mth;
 #pragma unroll
@@ -194,18 +200,16 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks, _Fl
         }
     };
 
-    if (kb < ke) fetch(kb);
+    if (kb < ke) {
+        fetch_kv(kb);
+        fetch_mask(kb);
+    }
     for (int k0 = kb; k0 < ke; k0 += FA_BK) {
         const int nk = min(FA_BK, ke - k0);
         __syncthreads();  // the previous tile is consumed
         stage();
-        uint2 mc[2][4];
-#pragma unroll
-        for (int jt = 0; jt < 2; jt++)
-#pragma unroll
-            for (int gq = 0; gq < 4; gq++) mc[jt][gq] = mr[jt][gq];
         __syncthreads();
-        if (k0 + FA_BK < ke) fetch(k0 + FA_BK);
+        if (k0 + FA_BK < ke) fetch_kv(k0 + FA_BK);
 
         if (nk < FA_BK && mrow) {
             // tail tile: mask groups reaching past the range, with bound checks
@@ -218,10 +222,18 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks, _Fl
                         uint32_t e[4];
 #pragma unroll
                         for (int r = 0; r < 4; r++) e[r] = key + r < nk ? mrow[k0 + key + r] : 0u;
-                        mc[jt][gq] = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
+                        mr[jt][gq] = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
                     }
                 }
         }
+        // a tile whose mask values are all zero for the whole wavefront (the
+        // bulk of a causal mask) skips the per-score mask term
+        uint32_t mor = 0;
+#pragma unroll
+        for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+            for (int gq = 0; gq < 4; gq++) mor |= mr[jt][gq].x | mr[jt][gq].y;
+        const bool mzero = __ballot(mor != 0) == 0;
         // scores of this lane: keys 32*jt + crow32(v), query t
         float s[2][16];
 #pragma unroll
@@ -240,8 +252,12 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks, _Fl
                 float x = fmaf(acc[v], sl2, mneg);
                 if (SOFTCAP) x = p.softcap * LOG2E * tanhf(acc[v] * p.scale) + mneg;
                 // mask value (0 without a mask); -inf for a masked key
-                const uint32_t mw = (v & 2) ? mc[jt][v >> 2].y : mc[jt][v >> 2].x;
-                s[jt][v] = fmaf(ml2, h2f((v & 1) ? mw >> 16 : mw), x);
+                if (mzero) {
+                    s[jt][v] = x;
+                } else {
+                    const uint32_t mw = (v & 2) ? mr[jt][v >> 2].y : mr[jt][v >> 2].x;
+                    s[jt][v] = fmaf(ml2, h2f((v & 1) ? mw >> 16 : mw), x);
+                }
             }
         }
         if (nk < FA_BK) {
@@ -310,6 +326,7 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks, _Fl
                     o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[dt], 0, 0, 0);
                 }
             }
+        if (k0 + FA_BK < ke) fetch_mask(k0 + FA_BK);
     }
 
     // write this slice's partial (M in natural-log units, S, unnormalized O)
@@ -327,14 +344,13 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks, _Fl
     }
 }
 
-template <int D>
+// softcap != 0 takes its own kernel (tanh adds registers the plain body
+// does not need)
+template <int D, bool SOFTCAP>
 __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
     __shared__ __attribute__((aligned(16))) _Float16 Ks[FA_BK * (D + FA_KPAD)];  // [key][d]
-    __shared__ __attribute__((aligned(16))) _Float16 Vt[D * (FA_BK + FA_KPAD)];  // [d][key]
-    if (p.softcap != 0.0f)
-        fa_fwd_body<D, true>(p, Ks, Vt);
-    else
-        fa_fwd_body<D, false>(p, Ks, Vt);
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[D * (FA_BK + FA_VPAD)];  // [d][key]
+    fa_fwd_body<D, SOFTCAP>(p, Ks, Vt);
 }
 
 // Single-query decode over a long cache (the reference's split-KV route,
@@ -774,8 +790,10 @@ __device__ __forceinline__ void fa_rowseq_impl(const FaParams &p) {
     for (int i = 0; i < PL; i++) o[i] = acc[i] * sinv;
 }
 
-extern "C" __global__ void __launch_bounds__(512) ghip_fa_fwd_d128(FaParams p) { fa_fwd_impl<128>(p); }
-extern "C" __global__ void __launch_bounds__(512) ghip_fa_fwd_d64(FaParams p) { fa_fwd_impl<64>(p); }
+extern "C" __global__ void __launch_bounds__(512) ghip_fa_fwd_d128(FaParams p) { fa_fwd_impl<128, false>(p); }
+extern "C" __global__ void __launch_bounds__(512) ghip_fa_fwd_d64(FaParams p) { fa_fwd_impl<64, false>(p); }
+extern "C" __global__ void __launch_bounds__(512) ghip_fa_fwd_sc_d128(FaParams p) { fa_fwd_impl<128, true>(p); }
+extern "C" __global__ void __launch_bounds__(512) ghip_fa_fwd_sc_d64(FaParams p) { fa_fwd_impl<64, true>(p); }
 extern "C" __global__ void __launch_bounds__(256) ghip_fa_rowseq_d128(FaParams p) { fa_rowseq_impl<128>(p); }
 extern "C" __global__ void __launch_bounds__(256) ghip_fa_rowseq_d64(FaParams p) { fa_rowseq_impl<64>(p); }
 extern "C" __global__ void __launch_bounds__(256) ghip_fa_decode_d128(FaParams p) { fa_decode_impl<128>(p); }

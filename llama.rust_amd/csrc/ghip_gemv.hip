@@ -229,11 +229,16 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
     if (FUSEQ) {
         const float *x = reinterpret_cast<const float *>(act);
         const int64_t xs = act_row_bytes / 4;
-        XTask t0;
+        // the first two rounds of tasks are loaded before the weights, so
+        // their latencies overlap (a 14336-wide activation row is two rounds)
+        XTask t0, t1;
+        const bool qwave1 = (int)blockDim.x + wave * 64 < total;
         if (qwave) t0 = quant_q8K_load(x, xs, ncols, nb, total, threadIdx.x);
+        if (qwave1) t1 = quant_q8K_load(x, xs, ncols, nb, total, blockDim.x + threadIdx.x);
         load_all();
         if (qwave) quant_q8K_store(t0, nb, n_mat, total, threadIdx.x, codes, dq, bsum);
-        for (int base = blockDim.x; base < total; base += blockDim.x) {
+        if (qwave1) quant_q8K_store(t1, nb, n_mat, total, blockDim.x + threadIdx.x, codes, dq, bsum);
+        for (int base = 2 * blockDim.x; base < total; base += blockDim.x) {
             if (base + wave * 64 >= total) break;
             const XTask t = quant_q8K_load(x, xs, ncols, nb, total, base + threadIdx.x);
             quant_q8K_store(t, nb, n_mat, total, base + threadIdx.x, codes, dq, bsum);
@@ -413,11 +418,16 @@ __device__ __forceinline__ void gemv_q6K_v2_impl(const uint8_t *__restrict__ W, 
     if (FUSEQ) {
         const float *x = reinterpret_cast<const float *>(act);
         const int64_t xs = act_row_bytes / 4;
-        XTask t0;
+        // the first two rounds of tasks are loaded before the weights, so
+        // their latencies overlap (a 14336-wide activation row is two rounds)
+        XTask t0, t1;
+        const bool qwave1 = (int)blockDim.x + wave * 64 < total;
         if (qwave) t0 = quant_q8K_load(x, xs, ncols, nb, total, threadIdx.x);
+        if (qwave1) t1 = quant_q8K_load(x, xs, ncols, nb, total, blockDim.x + threadIdx.x);
         load_all();
         if (qwave) quant_q8K_store(t0, nb, n_mat, total, threadIdx.x, codes, dq, bsum);
-        for (int base = blockDim.x; base < total; base += blockDim.x) {
+        if (qwave1) quant_q8K_store(t1, nb, n_mat, total, blockDim.x + threadIdx.x, codes, dq, bsum);
+        for (int base = 2 * blockDim.x; base < total; base += blockDim.x) {
             if (base + wave * 64 >= total) break;
             const XTask t = quant_q8K_load(x, xs, ncols, nb, total, base + threadIdx.x);
             quant_q8K_store(t, nb, n_mat, total, base + threadIdx.x, codes, dq, bsum);

@@ -266,7 +266,7 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
         const int nc = (int)std::min<int64_t>(8, p.M - c0);
         const int NC = nc == 1 ? 1 : nc == 2 ? 2 : nc <= 4 ? 4 : 8;
         std::string name = std::string(gemv_base(p.wtype)) + (p.wtype == GHIP_TYPE_Q6_K && q4k ? "_v2" : "") +
-                           (q4k && fused ? "_f" : "") + (sub ? "_sub" : "") +
+                           (fused ? "_f" : "") + (sub ? "_sub" : "") +
                            "_c" + std::to_string(NC) + (q4k ? "_r" + std::to_string(rb) + "x" + std::to_string(ng) : std::string());
         int32_t *sub_c = sub;
         if (sub) {
@@ -387,7 +387,13 @@ ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_ten
         return run_gemm(ctx, p, a->data, (const uint8_t *)act, dst, ldd, sub, lay, s);
     }
     if (p.act_pre) return run_gemv(ctx, p, a->data, (const uint8_t *)b->data, p.act_row_bytes, false, dst, ldd, sub, s);
-    if (gemv_v2(p))  // quantization fused into the decode kernel
+    // Q8_0 quantization fused into the block-pair kernels for up to 4096 weight
+    // rows: every workgroup then quantizes its lanes' blocks itself, which
+    // beats a separate quantize launch there but adds more L2 reads and
+    // per-wavefront work than it saves on larger matrices (4096x4096 Q4_0:
+    // 7.25 -> 6.88 us; 4096->14336 Q5_0 / Q8_0: 13.9 -> 14.9 / 17.7 -> 18.2 us)
+    const bool fuse_pair = gemv_pair(p.wtype) && p.N <= env_int("GHIP_GEMV_FUSE_MAX_ROWS", 4096);
+    if (gemv_v2(p) || fuse_pair)  // quantization fused into the decode kernel
         return run_gemv(ctx, p, a->data, (const uint8_t *)b->data, (int64_t)b->nb[1], true, dst, ldd, sub, s);
     st = quantize_act(ctx, p, b, act, s);
     if (st != GHIP_STATUS_SUCCESS) return st;

@@ -633,7 +633,47 @@ __device__ __forceinline__ void gemv_q6K_impl(const uint8_t *__restrict__ W, int
 
 // ---------------------------------------------------------------- Q4_0 x Q8_0
 // One lane per pair of 32-blocks (36 bytes, 64 elements).
-template <int NC, bool SUBSUMS>
+// One 32-block of quantize_row_q8_0 (quants.rs:331-362) quantized by the lane
+// that consumes it, with the arithmetic of ghip_quantize_q8_0: amax over the
+// block, d = f16(amax / 127), q = rne(x * 127 / amax), NaN or out of range ->
+// -128.  Codes of elements 0..15 in lo, 16..31 in hi; d as the f32 value of
+// its f16.
+DEV void q8_0_quant_block(const float *__restrict__ xb, uint4 &lo, uint4 &hi, float &d) {
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint4 t = ld16(reinterpret_cast<const uint8_t *>(xb + 4 * i));
+        v[4 * i] = __uint_as_float(t.x);
+        v[4 * i + 1] = __uint_as_float(t.y);
+        v[4 * i + 2] = __uint_as_float(t.z);
+        v[4 * i + 3] = __uint_as_float(t.w);
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+    const float dd = __fdiv_rn(amax, 127.0f);
+    const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    uint32_t pk[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float r = rintf(__fmul_rn(v[4 * k + i], id));
+            const int q = (r != r || fabsf(r) >= 2147483648.0f) ? -128 : (int)r;
+            w |= (uint32_t)(q & 0xff) << (8 * i);
+        }
+        pk[k] = w;
+    }
+    lo = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    hi = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+    d = h2f(f2h_rn(dd));
+}
+
+// FUSEQ: act is the f32 activation rows (act_row_bytes apart) and each lane
+// quantizes its own two blocks per column (q8_0_quant_block); otherwise act
+// holds ready Q8_0 rows.
+template <int NC, bool SUBSUMS, bool FUSEQ>
 __device__ __forceinline__ void gemv_q4_0_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
                                                int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
                                                int ncols, float *__restrict__ dst, int64_t ldd,
@@ -674,22 +714,28 @@ __device__ __forceinline__ void gemv_q4_0_impl(const uint8_t *__restrict__ W, in
         y0l[c] = y0h[c] = y1l[c] = y1h[c] = make_uint4(0, 0, 0, 0);
         sy0[c] = sy1[c] = 0;
         d0[c] = d1[c] = 0.0f;
-        if (c < ncols && v0) {
+        if (c < ncols && v0 && FUSEQ) {
+            const float *xr = reinterpret_cast<const float *>(act + c * act_row_bytes) + (int64_t)b0 * 32;
+            q8_0_quant_block(xr, y0l[c], y0h[c], d0[c]);
+            if (v1) q8_0_quant_block(xr + 32, y1l[c], y1h[c], d1[c]);
+        }
+        if (c < ncols && v0 && !FUSEQ) {
             const uint8_t *A = act + c * act_row_bytes + (int64_t)b0 * Q8_0_BYTES;
             d0[c] = h2f(ld2(A));
             y0l[c] = ld16(A + 2);
             y0h[c] = ld16(A + 18);
-            sy0[c] = 8 * dot4(y0l[c].x, one, dot4(y0l[c].y, one, dot4(y0l[c].z, one, dot4(y0l[c].w, one,
-                     dot4(y0h[c].x, one, dot4(y0h[c].y, one, dot4(y0h[c].z, one, dot4(y0h[c].w, one, 0))))))));
         }
-        if (c < ncols && v1) {
+        if (c < ncols && v1 && !FUSEQ) {
             const uint8_t *A = act + c * act_row_bytes + (int64_t)b1 * Q8_0_BYTES;
             d1[c] = h2f(ld2(A));
             y1l[c] = ld16(A + 2);
             y1h[c] = ld16(A + 18);
-            sy1[c] = 8 * dot4(y1l[c].x, one, dot4(y1l[c].y, one, dot4(y1l[c].z, one, dot4(y1l[c].w, one,
-                     dot4(y1h[c].x, one, dot4(y1h[c].y, one, dot4(y1h[c].z, one, dot4(y1h[c].w, one, 0))))))));
         }
+        // the -8 of every nibble as -8 * sum(q8) (zero for absent blocks)
+        sy0[c] = 8 * dot4(y0l[c].x, one, dot4(y0l[c].y, one, dot4(y0l[c].z, one, dot4(y0l[c].w, one,
+                 dot4(y0h[c].x, one, dot4(y0h[c].y, one, dot4(y0h[c].z, one, dot4(y0h[c].w, one, 0))))))));
+        sy1[c] = 8 * dot4(y1l[c].x, one, dot4(y1l[c].y, one, dot4(y1l[c].z, one, dot4(y1l[c].w, one,
+                 dot4(y1h[c].x, one, dot4(y1h[c].y, one, dot4(y1h[c].z, one, dot4(y1h[c].w, one, 0))))))));
     }
     float part[NC][RB];
 #pragma unroll
@@ -780,7 +826,7 @@ DEV void pair_block_codes(const uint32_t *w, int blk, uint32_t (&q)[8], float &d
     }
 }
 
-template <int WT, int NC, bool SUBSUMS>
+template <int WT, int NC, bool SUBSUMS, bool FUSEQ>
 __device__ __forceinline__ void gemv_pair_q8_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
                                                   int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
                                                   int ncols, float *__restrict__ dst, int64_t ldd,
@@ -841,13 +887,18 @@ __device__ __forceinline__ void gemv_pair_q8_impl(const uint8_t *__restrict__ W,
         y0l[c] = y0h[c] = y1l[c] = y1h[c] = make_uint4(0, 0, 0, 0);
         sy0[c] = sy1[c] = 0;
         d0[c] = d1[c] = 0.0f;
-        if (c < ncols && v0) {
+        if (c < ncols && v0 && FUSEQ) {
+            const float *xr = reinterpret_cast<const float *>(act + c * act_row_bytes) + (int64_t)b0 * 32;
+            q8_0_quant_block(xr, y0l[c], y0h[c], d0[c]);
+            if (v1) q8_0_quant_block(xr + 32, y1l[c], y1h[c], d1[c]);
+        }
+        if (c < ncols && v0 && !FUSEQ) {
             const uint8_t *A = act + c * act_row_bytes + (int64_t)b0 * Q8_0_BYTES;
             d0[c] = h2f(ld2(A));
             y0l[c] = ld16(A + 2);
             y0h[c] = ld16(A + 18);
         }
-        if (c < ncols && v1) {
+        if (c < ncols && v1 && !FUSEQ) {
             const uint8_t *A = act + c * act_row_bytes + (int64_t)b1 * Q8_0_BYTES;
             d1[c] = h2f(ld2(A));
             y1l[c] = ld16(A + 2);
@@ -890,17 +941,17 @@ __device__ __forceinline__ void gemv_pair_q8_impl(const uint8_t *__restrict__ W,
     finish_rows(red, r0, nr, ncols, NC, nw, dst, ldd);
 }
 
-template <int NC, bool SUBSUMS>
+template <int NC, bool SUBSUMS, bool FUSEQ>
 __device__ __forceinline__ void gemv_q5_0_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb,
                                                const uint8_t *__restrict__ act, int64_t act_row_bytes, int ncols,
                                                float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
-    gemv_pair_q8_impl<WT_Q5_0, NC, SUBSUMS>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub);
+    gemv_pair_q8_impl<WT_Q5_0, NC, SUBSUMS, FUSEQ>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub);
 }
-template <int NC, bool SUBSUMS>
+template <int NC, bool SUBSUMS, bool FUSEQ>
 __device__ __forceinline__ void gemv_q8_0_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb,
                                                const uint8_t *__restrict__ act, int64_t act_row_bytes, int ncols,
                                                float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
-    gemv_pair_q8_impl<WT_Q8_0, NC, SUBSUMS>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub);
+    gemv_pair_q8_impl<WT_Q8_0, NC, SUBSUMS, FUSEQ>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub);
 }
 
 #define GEMV_ARGS                                                                                     \
@@ -919,9 +970,28 @@ __device__ __forceinline__ void gemv_q8_0_impl(const uint8_t *__restrict__ W, in
     GEMV_INST(name, impl, 1) GEMV_INST(name, impl, 2) GEMV_INST(name, impl, 4) GEMV_INST(name, impl, 8)
 
 GEMV_ALL(ghip_gemv_q6_K, gemv_q6K_impl)
-GEMV_ALL(ghip_gemv_q4_0, gemv_q4_0_impl)
-GEMV_ALL(ghip_gemv_q5_0, gemv_q5_0_impl)
-GEMV_ALL(ghip_gemv_q8_0, gemv_q8_0_impl)
+
+// 32-element blocks with Q8_0 activations: "_f" kernels take f32 activations
+// (quantization fused), the others ready Q8_0 rows
+#define GEMV_PAIR_INST(name, impl, NC)                                                             \
+    extern "C" __global__ void __launch_bounds__(512) name##_c##NC(GEMV_ARGS) {                   \
+        impl<NC, false, false>(GEMV_PASS);                                                         \
+    }                                                                                              \
+    extern "C" __global__ void __launch_bounds__(512) name##_sub_c##NC(GEMV_ARGS) {               \
+        impl<NC, true, false>(GEMV_PASS);                                                          \
+    }                                                                                              \
+    extern "C" __global__ void __launch_bounds__(512) name##_f_c##NC(GEMV_ARGS) {                 \
+        impl<NC, false, true>(GEMV_PASS);                                                          \
+    }                                                                                              \
+    extern "C" __global__ void __launch_bounds__(512) name##_f_sub_c##NC(GEMV_ARGS) {             \
+        impl<NC, true, true>(GEMV_PASS);                                                           \
+    }
+#define GEMV_PAIR_ALL(name, impl)                                                      \
+    GEMV_PAIR_INST(name, impl, 1) GEMV_PAIR_INST(name, impl, 2) GEMV_PAIR_INST(name, impl, 4) \
+        GEMV_PAIR_INST(name, impl, 8)
+GEMV_PAIR_ALL(ghip_gemv_q4_0, gemv_q4_0_impl)
+GEMV_PAIR_ALL(ghip_gemv_q5_0, gemv_q5_0_impl)
+GEMV_PAIR_ALL(ghip_gemv_q8_0, gemv_q8_0_impl)
 
 // Q4_K: "_f" kernels take f32 activations (fused Q8_K quantization), the
 // others ready Q8_K rows; "_sub" kernels also store the integer partials.

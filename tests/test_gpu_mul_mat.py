@@ -109,11 +109,12 @@ def test_empty(be):
     ("gate/up", O.Q4_K, 4096, 14336),
     ("down", O.Q6_K, 14336, 4096),
     ("cfg1", O.Q4_0, 4096, 4096),
+    ("q4_0 wide (separate Q8_0 quantization)", O.Q4_0, 4096, 14336),
 ])
 @pytest.mark.parametrize("cols", [1, 2, 4, 8])
 def test_llama3_decode_shapes(be, name, ty, n, rows, cols):
     if ty == O.Q4_0 and cols > 1:
-        pytest.skip("config 1 is batch 1")
+        pytest.skip("the Q4_0 configurations are batch 1")
     run_case(be, ty, n, rows, cols, seed=0, check_sub=(cols <= 2))
 
 

@@ -511,7 +511,8 @@ ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip
     hipStream_t s = (hipStream_t)stream;
     if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
     // 32-pair tiles when experts see few pairs each (decode, small batches)
-    const int tp = (n_pairs <= 48 * p.n_as || sub || env_int("GHIP_MOE_TILE", 0) == 32) ? 32 : 64;
+    const int tile_env = env_int("GHIP_MOE_TILE", 0);
+    const int tp = (sub || tile_env == 32) ? 32 : tile_env == 64 ? 64 : n_pairs <= 48 * p.n_as ? 32 : 64;
     const int64_t max_tiles = (n_pairs + tp - 1) / tp + p.n_as;
     auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
     const int64_t act_rows = p.ne11 * p.n_tokens;

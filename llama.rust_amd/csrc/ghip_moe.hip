@@ -80,13 +80,21 @@ ghip_moe_route(const int32_t *__restrict__ ids, int64_t ids_nb1, int n_ids, int 
     }
 }
 
-// byte -> {f16(kvalue(lo nibble)), f16(kvalue(hi nibble))} (KVALUES_MXFP4,
-// quants.rs:660; the values are small integers, exact in f16)
-DEV uint32_t kv_pair_f16(int byte) {
-    const int kv[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
-    const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)(float)kv[byte & 15]);
-    const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)(float)kv[byte >> 4]);
-    return lo | (hi << 16);
+// Eight MXFP4 codes (the nibbles of x) -> their kvalues as f16, slot order
+// [lo(b0), hi(b0), lo(b1), hi(b1), ...], with the magnitudes scaled by 2^k:
+// the f16 of |kvalue| in {0,1,2,3,4,6,8,12} differ only in the high byte
+// (00 3C 40 42 44 46 48 4A), so one v_perm over an 8-byte table gives four of
+// them at once; 2^k adds 4k to every non-zero table byte (exact while
+// 2^-14 <= 2^k and 12 * 2^k < 2^16), and the sign is bit 3 of the nibble.
+DEV uint4 kv_expand(uint32_t x, uint32_t t0, uint32_t t1) {
+    const uint32_t hbl = __builtin_amdgcn_perm(t1, t0, x & 0x07070707u) | ((x << 4) & 0x80808080u);
+    const uint32_t hbh = __builtin_amdgcn_perm(t1, t0, (x >> 4) & 0x07070707u) | (x & 0x80808080u);
+    uint4 r;
+    r.x = __builtin_amdgcn_perm(hbh, hbl, 0x040C000Cu);
+    r.y = __builtin_amdgcn_perm(hbh, hbl, 0x050C010Cu);
+    r.z = __builtin_amdgcn_perm(hbh, hbl, 0x060C020Cu);
+    r.w = __builtin_amdgcn_perm(hbh, hbl, 0x070C030Cu);
+    return r;
 }
 
 // ---------------------------------------------------------------- activations
@@ -140,7 +148,6 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
     __shared__ __attribute__((aligned(16))) float ds_lds[2][8][TP];  // [stage][block][pair] activation scales
     __shared__ __attribute__((aligned(16))) uint4 a_lds[2][8][4][TP];  // [stage][block][piece][pair] 8 f16 each
     __shared__ __attribute__((aligned(16))) uint32_t w_lds[2][MOE_TR][MOE_WIN * 4];  // [stage][row][144-byte window]
-    __shared__ uint32_t lut[256];
     __shared__ int pairs[TP];
     const int tile = blockIdx.x;
     if (tile >= route[0]) return;
@@ -151,7 +158,6 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
     const int row = blockIdx.y * MOE_TR + w * 32 + li;
     const bool rvalid = row < rows;
     if (threadIdx.x < TP) pairs[threadIdx.x] = threadIdx.x < np ? route[2 + first + threadIdx.x] : -1;
-    lut[threadIdx.x] = kv_pair_f16(threadIdx.x);
     __syncthreads();
     // activation row of tile pair pi (null for padding pairs)
     auto arow_all = [&](int pi) -> const _Float16 * {
@@ -169,18 +175,18 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
     constexpr int ACHUNK = 8 * 4 * TP / 256;  // 16-byte chunks per thread per group
     // the group's activation scales: entry i = c*256 + t is (block i / TP, pair i % TP)
     constexpr int DCH = 8 * TP / 256;
+    // Loop-invariant gather addresses: with 256 % TP == 0 every staging chunk
+    // of a thread belongs to the same pair, tid % TP, so its activation row
+    // (codes and scales) is found once here, not per group (pairs[] lives in
+    // LDS, which the compiler cannot hoist across the loop's barriers).
+    static_assert(256 % TP == 0, "one pair per thread");
+    const _Float16 *my_arow = arow_all(threadIdx.x % TP);
+    const float *my_drow = my_arow ? actd + (my_arow - actf) / 32 : nullptr;  // same row, [nb] scales
     auto prefetch_d = [&](int g, float (&dr)[DCH]) {
 #pragma unroll
         for (int c = 0; c < DCH; c++) {
-            const int i = c * 256 + threadIdx.x;
-            const int kb = i / TP, pi = i - kb * TP, b = 8 * g + kb;
-            const int p = pairs[pi];
-            float dv = 0.0f;
-            if (p >= 0 && b < nb) {
-                const int tk = p / n_ids, sl = p - tk * n_ids;
-                dv = actd[((int64_t)tk * ne11 + (sl % ne11)) * nb + b];
-            }
-            dr[c] = dv;
+            const int kb = (c * 256 + (int)threadIdx.x) / TP, b = 8 * g + kb;
+            dr[c] = (my_drow && b < nb) ? my_drow[b] : 0.0f;
         }
     };
     auto store_d = [&](int stage, const float (&dr)[DCH]) {
@@ -193,11 +199,11 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
     auto prefetch_a = [&](int g, uint4 (&ar)[ACHUNK]) {
 #pragma unroll
         for (int c = 0; c < ACHUNK; c++) {
-            const int idx = c * 256 + threadIdx.x;  // (block kb, piece, pair)
-            const int pi = idx % TP, rest = idx / TP, piece = rest & 3, kb = rest >> 2;
+            const int rest = (c * 256 + (int)threadIdx.x) / TP;  // (block kb, piece) of this chunk
+            const int piece = rest & 3, kb = rest >> 2;
             const int b = 8 * g + kb;
-            const _Float16 *src = arow_all(pi);
-            ar[c] = (src && b < nb) ? ld16((const uint8_t *)(src + ((int64_t)b * 4 + piece) * 8)) : make_uint4(0, 0, 0, 0);
+            ar[c] = (my_arow && b < nb) ? ld16((const uint8_t *)(my_arow + ((int64_t)b * 4 + piece) * 8))
+                                        : make_uint4(0, 0, 0, 0);
         }
     };
     auto store_a = [&](int stage, const uint4 (&ar)[ACHUNK]) {
@@ -213,14 +219,22 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
     // end: the tail blocks past the last full window are read with exact loads)
     constexpr int WCHUNK = (MOE_TR * MOE_WIN + 255) / 256;
     const uint8_t *wexp = as + (int64_t)e * as_nb2;
+    // weight chunk c of this thread: row r = idx / 9, 16-byte piece l = idx % 9
+    // (fixed for the whole loop: base pointer and piece offset found once)
+    const uint8_t *wbase[WCHUNK];
+    int wl16[WCHUNK];
+#pragma unroll
+    for (int c = 0; c < WCHUNK; c++) {
+        const int idx = c * 256 + threadIdx.x;
+        const int r = idx / MOE_WIN, l = idx - r * MOE_WIN;
+        wbase[c] = wexp + (int64_t)min((int)blockIdx.y * MOE_TR + r, rows - 1) * as_nb1;
+        wl16[c] = idx < MOE_TR * MOE_WIN ? 16 * l : -1;
+    }
     auto prefetch_w = [&](int g, uint4 (&wr)[WCHUNK]) {
 #pragma unroll
         for (int c = 0; c < WCHUNK; c++) {
-            const int idx = c * 256 + threadIdx.x;  // (row, chunk)
-            const int r = idx / MOE_WIN, l = idx - r * MOE_WIN;
-            const int grow = min(blockIdx.y * MOE_TR + r, rows - 1);
-            const int off = min(136 * g + 16 * l, row_bytes - 16);
-            wr[c] = idx < MOE_TR * MOE_WIN ? ld16(wexp + (int64_t)grow * as_nb1 + off) : make_uint4(0, 0, 0, 0);
+            const int off = min(136 * g + wl16[c], row_bytes - 16);
+            wr[c] = wl16[c] >= 0 ? ld16(wbase[c] + off) : make_uint4(0, 0, 0, 0);
         }
     };
     auto store_w = [&](int stage, const uint4 (&wr)[WCHUNK]) {
@@ -240,48 +254,67 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[mt][v] = 0.0f;
 
-    // one block: dots on the f16 matrix cores, then the reference's fold
+    // one block: dots on the f16 matrix cores, then the reference's fold.
+    // Fast path (every row of the wavefront has k = e - 128 in [-14, 12]): the
+    // block scale 2^k is folded into the weight operand, so the MFMA returns
+    // dot * 2^k exactly and the fold is fma(dot * 2^k, d, acc) -- the same
+    // real value as the reference's fma(dot, 2^k * d, acc) (2^k * d is exact),
+    // hence the same rounding.  Otherwise the exact dot and the reference's
+    // own fold.  The sub-sum instantiations always take the exact dot.
     auto do_block = [&](int b, const float *dsb, uint32_t e8, uint32_t q0, uint32_t q1, const v8h (&a)[NMT][2]) {
-        const float sw = e8m0_half(e8);
         const uint32_t qm[2] = {q0, q1};
         v16f c[NMT];
+        auto dots = [&](uint32_t k4) {
+            const uint32_t t0 = 0x42403C00u + k4 * 0x01010100u, t1 = 0x4A484644u + k4 * 0x01010101u;
 #pragma unroll
-        for (int m = 0; m < 2; m++) {
-            v8h bw;
+            for (int m = 0; m < 2; m++) {
+                const v8h bw = __builtin_bit_cast(v8h, kv_expand(qm[m], t0, t1));
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const uint32_t pr = lut[(qm[m] >> (8 * q)) & 0xff];
-                bw[2 * q] = __builtin_bit_cast(_Float16, (uint16_t)(pr & 0xffff));
-                bw[2 * q + 1] = __builtin_bit_cast(_Float16, (uint16_t)(pr >> 16));
-            }
-#pragma unroll
-            for (int mt = 0; mt < NMT; mt++) {
-                const v16f z = {};
-                c[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mt][m], bw, m ? c[mt] : z, 0, 0, 0);
-            }
-        }
-        // c[mt][v] is the exact int32 block dot of pair mt*32 + crowm(v)
-#pragma unroll
-        for (int mt = 0; mt < NMT; mt++)
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const float4 d4 = *reinterpret_cast<const float4 *>(&dsb[mt * 32 + 8 * g + 4 * h2]);
-                const float dd[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int v = 4 * g + r;
-                    const float dot = c[mt][v];
-                    if (REPACK) {
-                        acc[mt][v] = fmaf(dot, sw * dd[r], acc[mt][v]);
-                    } else {
-                        acc[mt][v] = acc[mt][v] + (dd[r] * sw) * dot;
-                    }
-                    if (SUBSUMS && rvalid) {
-                        const int pi = mt * 32 + crowm(v, lane);
-                        if (pi < np) sub[((int64_t)pairs[pi] * rows + row) * nb + b] = (int)dot;
-                    }
+                for (int mt = 0; mt < NMT; mt++) {
+                    const v16f z = {};
+                    c[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mt][m], bw, m ? c[mt] : z, 0, 0, 0);
                 }
             }
+        };
+        // each path holds its own MFMAs, so the uniform branch stays a branch
+        if (!SUBSUMS && __ballot(e8 < 114u || e8 > 140u) == 0) {
+            dots(4u * (e8 - 128u));
+#pragma unroll
+            for (int mt = 0; mt < NMT; mt++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const float4 d4 = *reinterpret_cast<const float4 *>(&dsb[mt * 32 + 8 * g + 4 * h2]);
+                    const float dd[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int v = 4 * g + r;
+                        if (REPACK) acc[mt][v] = fmaf(c[mt][v], dd[r], acc[mt][v]);
+                        else acc[mt][v] = acc[mt][v] + dd[r] * c[mt][v];
+                    }
+                }
+        } else {
+            dots(0u);
+            const float sw = e8m0_half(e8);
+            // c[mt][v] is the exact int32 block dot of pair mt*32 + crowm(v)
+#pragma unroll
+            for (int mt = 0; mt < NMT; mt++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const float4 d4 = *reinterpret_cast<const float4 *>(&dsb[mt * 32 + 8 * g + 4 * h2]);
+                    const float dd[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int v = 4 * g + r;
+                        const float dot = c[mt][v];
+                        if (REPACK) acc[mt][v] = fmaf(dot, sw * dd[r], acc[mt][v]);
+                        else acc[mt][v] = acc[mt][v] + (dd[r] * sw) * dot;
+                        if (SUBSUMS && rvalid) {
+                            const int pi = mt * 32 + crowm(v, lane);
+                            if (pi < np) sub[((int64_t)pairs[pi] * rows + row) * nb + b] = (int)dot;
+                        }
+                    }
+                }
+        }
     };
 
     // full 8-block windows that end inside the row; the rest are tail blocks
@@ -294,24 +327,34 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
 #pragma unroll
             for (int m = 0; m < 2; m++) a[mt][m] = __builtin_bit_cast(v8h, a_lds[stage][kb][2 * m + h2][mt * 32 + li]);
     };
-    uint4 ar[ACHUNK], wr[WCHUNK];
-    float dr[DCH];
+    // Two groups in flight: while group g is multiplied from LDS stage g&1,
+    // group g+1 sits in one register set (issued an iteration earlier) and
+    // group g+2 is issued into the other; g+1 goes to LDS after g's MFMAs.
+    // The loop is unrolled by two so that both sets have fixed registers.
+    uint4 ar0[ACHUNK], wr0[WCHUNK], ar1[ACHUNK], wr1[WCHUNK];
+    float dr0[DCH], dr1[DCH];
     const int rl = w * 32 + li;  // this lane's row inside the workgroup
-    prefetch_a(0, ar);
-    prefetch_d(0, dr);
-    if (ngroups > 0) prefetch_w(0, wr);
-    store_a(0, ar);
-    store_d(0, dr);
-    if (ngroups > 0) store_w(0, wr);
+    prefetch_a(0, ar0);
+    prefetch_d(0, dr0);
+    if (ngroups > 0) prefetch_w(0, wr0);
+    if (nga > 1) {
+        prefetch_a(1, ar1);
+        prefetch_d(1, dr1);
+    }
+    if (ngroups > 1) prefetch_w(1, wr1);
+    store_a(0, ar0);
+    store_d(0, dr0);
+    if (ngroups > 0) store_w(0, wr0);
     __syncthreads();
-    for (int g = 0; g < nga; g++) {
+    // iteration g: ra* (free) receive group g+2; rb* (group g+1) go to LDS
+    auto body = [&](int g, uint4 (&ra)[ACHUNK], float (&da)[DCH], uint4 (&wa)[WCHUNK], const uint4 (&rb)[ACHUNK],
+                    const float (&db)[DCH], const uint4 (&wb_)[WCHUNK]) {
         const int stage = g & 1;
-        const bool amore = g + 1 < nga, wmore = g + 1 < ngroups;
-        if (amore) {
-            prefetch_a(g + 1, ar);
-            prefetch_d(g + 1, dr);
+        if (g + 2 < nga) {
+            prefetch_a(g + 2, ra);
+            prefetch_d(g + 2, da);
         }
-        if (wmore) prefetch_w(g + 1, wr);
+        if (g + 2 < ngroups) prefetch_w(g + 2, wa);
         if (g < ngroups) {
             const uint32_t *wl = w_lds[stage][rl];
 #pragma unroll 2
@@ -334,12 +377,16 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
                 do_block(8 * g + kb, ds_lds[stage][kb], wb[0], ld4(wb + 1 + 4 * h2), ld4(wb + 9 + 4 * h2), a);
             }
         }
-        if (amore) {
-            store_a(stage ^ 1, ar);
-            store_d(stage ^ 1, dr);
+        if (g + 1 < nga) {
+            store_a(stage ^ 1, rb);
+            store_d(stage ^ 1, db);
         }
-        if (wmore) store_w(stage ^ 1, wr);
+        if (g + 1 < ngroups) store_w(stage ^ 1, wb_);
         __syncthreads();
+    };
+    for (int g = 0; g < nga; g += 2) {
+        body(g, ar0, dr0, wr0, ar1, dr1, wr1);
+        if (g + 1 < nga) body(g + 1, ar1, dr1, wr1, ar0, dr0, wr0);
     }
     if (!rvalid) return;
 #pragma unroll
@@ -369,3 +416,4 @@ MOE_KERNEL(ghip_moe_mxfp4_t32_plain, 1, false, false)
 MOE_KERNEL(ghip_moe_mxfp4_t64_plain, 2, false, false)
 MOE_KERNEL(ghip_moe_mxfp4_t32_sub, 1, true, true)
 MOE_KERNEL(ghip_moe_mxfp4_t32_plain_sub, 1, false, true)
+

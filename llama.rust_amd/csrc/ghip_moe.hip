@@ -261,61 +261,56 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
     // real value as the reference's fma(dot, 2^k * d, acc) (2^k * d is exact),
     // hence the same rounding.  Otherwise the exact dot and the reference's
     // own fold.  The sub-sum instantiations always take the exact dot.
-    auto do_block = [&](int b, const float *dsb, uint32_t e8, uint32_t q0, uint32_t q1, const v8h (&a)[NMT][2]) {
+    auto dots = [&](uint32_t k4, uint32_t q0, uint32_t q1, const v8h (&a)[NMT][2], v16f (&c)[NMT]) {
+        const uint32_t t0 = 0x42403C00u + k4 * 0x01010100u, t1 = 0x4A484644u + k4 * 0x01010101u;
         const uint32_t qm[2] = {q0, q1};
-        v16f c[NMT];
-        auto dots = [&](uint32_t k4) {
-            const uint32_t t0 = 0x42403C00u + k4 * 0x01010100u, t1 = 0x4A484644u + k4 * 0x01010101u;
 #pragma unroll
-            for (int m = 0; m < 2; m++) {
-                const v8h bw = __builtin_bit_cast(v8h, kv_expand(qm[m], t0, t1));
+        for (int m = 0; m < 2; m++) {
+            const v8h bw = __builtin_bit_cast(v8h, kv_expand(qm[m], t0, t1));
 #pragma unroll
-                for (int mt = 0; mt < NMT; mt++) {
-                    const v16f z = {};
-                    c[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mt][m], bw, m ? c[mt] : z, 0, 0, 0);
-                }
+            for (int mt = 0; mt < NMT; mt++) {
+                const v16f z = {};
+                c[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mt][m], bw, m ? c[mt] : z, 0, 0, 0);
             }
-        };
-        // each path holds its own MFMAs, so the uniform branch stays a branch
-        if (!SUBSUMS && __ballot(e8 < 114u || e8 > 140u) == 0) {
-            dots(4u * (e8 - 128u));
-#pragma unroll
-            for (int mt = 0; mt < NMT; mt++)
-#pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const float4 d4 = *reinterpret_cast<const float4 *>(&dsb[mt * 32 + 8 * g + 4 * h2]);
-                    const float dd[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int v = 4 * g + r;
-                        if (REPACK) acc[mt][v] = fmaf(c[mt][v], dd[r], acc[mt][v]);
-                        else acc[mt][v] = acc[mt][v] + dd[r] * c[mt][v];
-                    }
-                }
-        } else {
-            dots(0u);
-            const float sw = e8m0_half(e8);
-            // c[mt][v] is the exact int32 block dot of pair mt*32 + crowm(v)
-#pragma unroll
-            for (int mt = 0; mt < NMT; mt++)
-#pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const float4 d4 = *reinterpret_cast<const float4 *>(&dsb[mt * 32 + 8 * g + 4 * h2]);
-                    const float dd[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int v = 4 * g + r;
-                        const float dot = c[mt][v];
-                        if (REPACK) acc[mt][v] = fmaf(dot, sw * dd[r], acc[mt][v]);
-                        else acc[mt][v] = acc[mt][v] + (dd[r] * sw) * dot;
-                        if (SUBSUMS && rvalid) {
-                            const int pi = mt * 32 + crowm(v, lane);
-                            if (pi < np) sub[((int64_t)pairs[pi] * rows + row) * nb + b] = (int)dot;
-                        }
-                    }
-                }
         }
     };
+    // fast path (FAST): the block scale 2^k is in the weight operand, the MFMA
+    // returns dot * 2^k exactly and the fold is fma(dot * 2^k, d, acc), the
+    // real value of the reference's fma(dot, 2^k * d, acc) (2^k * d exact).
+    // Exact path: the integer dot and the reference's own fold.
+    auto do_block = [&](auto FAST, int b, const float *dsb, uint32_t e8, uint32_t q0, uint32_t q1,
+                        const v8h (&a)[NMT][2]) {
+        constexpr bool fast = decltype(FAST)::value;
+        v16f c[NMT];
+        dots(fast ? 4u * (e8 - 128u) : 0u, q0, q1, a, c);
+        const float sw = e8m0_half(e8);
+#pragma unroll
+        for (int mt = 0; mt < NMT; mt++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 d4 = *reinterpret_cast<const float4 *>(&dsb[mt * 32 + 8 * g + 4 * h2]);
+                const float dd[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int v = 4 * g + r;
+                    const float dot = c[mt][v];
+                    if (fast) {
+                        if (REPACK) acc[mt][v] = fmaf(dot, dd[r], acc[mt][v]);
+                        else acc[mt][v] = acc[mt][v] + dd[r] * dot;
+                    } else if (REPACK) {
+                        acc[mt][v] = fmaf(dot, sw * dd[r], acc[mt][v]);
+                    } else {
+                        acc[mt][v] = acc[mt][v] + (dd[r] * sw) * dot;
+                    }
+                    if (!fast && SUBSUMS && rvalid) {
+                        const int pi = mt * 32 + crowm(v, lane);
+                        if (pi < np) sub[((int64_t)pairs[pi] * rows + row) * nb + b] = (int)dot;
+                    }
+                }
+            }
+    };
+    // the 2^k fold holds for k = e - 128 in [-14, 12]
+    auto in_range = [](uint32_t e8) { return e8 >= 114u && e8 <= 140u; };
 
     // full 8-block windows that end inside the row; the rest are tail blocks
     int ngroups = nb / 8;
@@ -357,24 +352,33 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
         if (g + 2 < ngroups) prefetch_w(g + 2, wa);
         if (g < ngroups) {
             const uint32_t *wl = w_lds[stage][rl];
+            // block kb of the window: e at byte 17kb, qs at 17kb+1; this lane
+            // half needs qs bytes 4h2.. (m = 0) and 8+4h2.. (m = 1)
+            auto e_of = [&](int kb) { return (wl[(17 * kb) >> 2] >> (8 * ((17 * kb) & 3))) & 0xffu; };
+            auto window = [&](auto FAST) {
 #pragma unroll 2
-            for (int kb = 0; kb < 8; kb++) {
-                // block kb of the window: e at byte 17kb, qs at 17kb+1; this lane
-                // half needs qs bytes 4h2.. (m = 0) and 8+4h2.. (m = 1)
-                const int o0 = 17 * kb + 1 + 4 * h2, o1 = o0 + 8;
-                const uint32_t e8 = (wl[(17 * kb) >> 2] >> (8 * ((17 * kb) & 3))) & 0xff;
-                const uint32_t q0 = __builtin_amdgcn_alignbyte(wl[(o0 >> 2) + 1], wl[o0 >> 2], o0 & 3);
-                const uint32_t q1 = __builtin_amdgcn_alignbyte(wl[(o1 >> 2) + 1], wl[o1 >> 2], o1 & 3);
-                v8h a[NMT][2];
-                a_of(stage, kb, a);
-                do_block(8 * g + kb, ds_lds[stage][kb], e8, q0, q1, a);
-            }
+                for (int kb = 0; kb < 8; kb++) {
+                    const int o0 = 17 * kb + 1 + 4 * h2, o1 = o0 + 8;
+                    const uint32_t q0 = __builtin_amdgcn_alignbyte(wl[(o0 >> 2) + 1], wl[o0 >> 2], o0 & 3);
+                    const uint32_t q1 = __builtin_amdgcn_alignbyte(wl[(o1 >> 2) + 1], wl[o1 >> 2], o1 & 3);
+                    v8h a[NMT][2];
+                    a_of(stage, kb, a);
+                    do_block(FAST, 8 * g + kb, ds_lds[stage][kb], e_of(kb), q0, q1, a);
+                }
+            };
+            // one decision per 8-block window for the whole wavefront
+            bool ok = !SUBSUMS;
+#pragma unroll
+            for (int kb = 0; kb < 8; kb++) ok = ok && in_range(e_of(kb));
+            if (__ballot(!ok) == 0) window(std::true_type{});
+            else window(std::false_type{});
         } else {
-            for (int kb = 0; kb < 8 && 8 * g + kb < nb; kb++) {  // tail blocks: exact loads
+            for (int kb = 0; kb < 8 && 8 * g + kb < nb; kb++) {  // tail blocks: exact loads, exact path
                 const uint8_t *wb = wrow + (int64_t)(8 * g + kb) * MXFP4_BYTES;
                 v8h a[NMT][2];
                 a_of(stage, kb, a);
-                do_block(8 * g + kb, ds_lds[stage][kb], wb[0], ld4(wb + 1 + 4 * h2), ld4(wb + 9 + 4 * h2), a);
+                do_block(std::false_type{}, 8 * g + kb, ds_lds[stage][kb], wb[0], ld4(wb + 1 + 4 * h2),
+                         ld4(wb + 9 + 4 * h2), a);
             }
         }
         if (g + 1 < nga) {

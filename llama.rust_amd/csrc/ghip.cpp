@@ -518,8 +518,8 @@ ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip
     const int64_t act_rows = p.ne11 * p.n_tokens;
     // workspace: Q8_0 rows | f16 slot codes | f32 scales | routing table | scratch output
     const size_t act_bytes = up((size_t)(act_rows * p.act_row_bytes));
-    const size_t actf_bytes = up((size_t)act_rows * p.nb * 64);
-    const size_t actd_bytes = up((size_t)act_rows * p.nb * 4);
+    const size_t actf_bytes = up((size_t)n_pairs * p.nb * 64);  // per routed pair
+    const size_t actd_bytes = up((size_t)n_pairs * p.nb * 4);
     const size_t route_bytes = up((size_t)(2 + n_pairs + 3 * max_tiles) * 4);
     const size_t out_bytes = d ? 0 : (size_t)(n_pairs * p.rows * 4);
     void *ws = nullptr;
@@ -536,14 +536,15 @@ ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip
     st = ctx->launch("ghip_quantize_q8_0", dim3(qgrid), dim3(256), 0, s, (const float *)b->data,
                      (int64_t)b->nb[1] / 4, p.K, act_rows, act, p.act_row_bytes);
     if (st != GHIP_STATUS_SUCCESS) return st;
-    const unsigned fgrid = (unsigned)((act_rows * p.nb * 4 + 255) / 256);
-    st = ctx->launch("ghip_moe_act_f16", dim3(fgrid), dim3(256), 0, s, (const uint8_t *)act, p.act_row_bytes,
-                     (int)act_rows, (int)p.nb, actf, actd);
-    if (st != GHIP_STATUS_SUCCESS) return st;
     const int64_t ids_nb1 = (int64_t)ids->nb[1] / 4;
     st = ctx->launch("ghip_moe_route", dim3(1), dim3(1024), (unsigned)(2 * p.n_as * 4), s, (const int32_t *)ids->data,
                      ids_nb1, (int)p.n_ids, (int)p.n_tokens, (int)p.n_as, route, (int)max_tiles, tp, dst, dst_nb1,
                      dst_nb2, (int)p.rows);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    // f16 codes of every routed pair, in the routed order
+    const unsigned fgrid = (unsigned)((n_pairs * p.nb * 4 + 255) / 256);
+    st = ctx->launch("ghip_moe_act_f16", dim3(fgrid), dim3(256), 0, s, (const uint8_t *)act, p.act_row_bytes,
+                     (const int32_t *)route, (int)n_pairs, (int)p.n_ids, (int)p.ne11, (int)p.nb, actf, actd);
     if (st != GHIP_STATUS_SUCCESS) return st;
     const bool repack = p.rows % 8 == 0;  // compute.rs:1965-1972 routes rows % 8 == 0 through the repack kernel
     std::string name = std::string("ghip_moe_mxfp4_t") + (tp == 32 ? "32" : "64") + (repack ? "" : "_plain") + (sub ? "_sub" : "");

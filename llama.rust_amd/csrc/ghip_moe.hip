@@ -99,18 +99,24 @@ DEV uint4 kv_expand(uint32_t x, uint32_t t0, uint32_t t1) {
 
 // ---------------------------------------------------------------- activations
 // Q8_0 activation rows -> f16 codes in MFMA K-slot order (exact: |q| <= 128),
-// once per call: actf [row][block][4 pieces][8 f16], piece (m, h2) slot e
-// holding element (e&1)*16 + 8m + 4*h2 + e/2; actd [row][block] = d as f32.
+// once per call and per (token, slot) pair, in the routed order (after
+// ghip_moe_route), so that a tile's pairs are consecutive rows:
+// actf [slot][block][4 pieces][8 f16], piece (m, h2) slot e holding element
+// (e&1)*16 + 8m + 4*h2 + e/2; actd [slot][block] = d as f32.  Pair
+// p = t * n_ids + s reads activation row t * ne11 + s % ne11.
 extern "C" __global__ void __launch_bounds__(256)
-ghip_moe_act_f16(const uint8_t *__restrict__ q8, int64_t q8_row_bytes, int nrows, int nb,
-                 _Float16 *__restrict__ actf, float *__restrict__ actd) {
-    const int64_t task = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (row, block, piece)
-    if (task >= (int64_t)nrows * nb * 4) return;
+ghip_moe_act_f16(const uint8_t *__restrict__ q8, int64_t q8_row_bytes, const int32_t *__restrict__ route,
+                 int n_pairs, int n_ids, int ne11, int nb, _Float16 *__restrict__ actf, float *__restrict__ actd) {
+    const int64_t task = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (slot, block, piece)
+    const int n_valid = n_pairs - route[1];                         // pairs with a valid expert id
+    if (task >= (int64_t)n_valid * nb * 4) return;
     const int piece = (int)(task & 3);
     const int64_t rb = task >> 2;
-    const int64_t row = rb / nb;
-    const int b = (int)(rb - row * nb);
+    const int64_t slot = rb / nb;
+    const int b = (int)(rb - slot * nb);
     const int m = piece >> 1, hh = piece & 1;
+    const int p = route[2 + slot], t = p / n_ids, sl = p - t * n_ids;
+    const int64_t row = (int64_t)t * ne11 + sl % ne11;
     const uint8_t *blk = q8 + row * q8_row_bytes + (int64_t)b * Q8_0_BYTES;
     const uint32_t lo = ld4(blk + 2 + 8 * m + 4 * hh);       // elements 8m+4hh .. +3
     const uint32_t hi = ld4(blk + 2 + 16 + 8 * m + 4 * hh);  // elements 16+8m+4hh .. +3
@@ -159,13 +165,6 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
     const bool rvalid = row < rows;
     if (threadIdx.x < TP) pairs[threadIdx.x] = threadIdx.x < np ? route[2 + first + threadIdx.x] : -1;
     __syncthreads();
-    // activation row of tile pair pi (null for padding pairs)
-    auto arow_all = [&](int pi) -> const _Float16 * {
-        const int p = pairs[pi];
-        if (p < 0) return nullptr;
-        const int t = p / n_ids, s = p - t * n_ids;
-        return actf + ((int64_t)t * ne11 + (s % ne11)) * nb * 32;
-    };
     __syncthreads();
     const uint8_t *wrow = as + (int64_t)e * as_nb2 + (int64_t)(rvalid ? row : 0) * as_nb1;
     const int row_bytes = nb * MXFP4_BYTES;
@@ -180,8 +179,9 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
     // (codes and scales) is found once here, not per group (pairs[] lives in
     // LDS, which the compiler cannot hoist across the loop's barriers).
     static_assert(256 % TP == 0, "one pair per thread");
-    const _Float16 *my_arow = arow_all(threadIdx.x % TP);
-    const float *my_drow = my_arow ? actd + (my_arow - actf) / 32 : nullptr;  // same row, [nb] scales
+    const int my_pi = threadIdx.x % TP;
+    const _Float16 *my_arow = my_pi < np ? actf + (int64_t)(first + my_pi) * nb * 32 : nullptr;
+    const float *my_drow = my_pi < np ? actd + (int64_t)(first + my_pi) * nb : nullptr;
     auto prefetch_d = [&](int g, float (&dr)[DCH]) {
 #pragma unroll
         for (int c = 0; c < DCH; c++) {
@@ -262,7 +262,9 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
     // hence the same rounding.  Otherwise the exact dot and the reference's
     // own fold.  The sub-sum instantiations always take the exact dot.
     auto dots = [&](uint32_t k4, uint32_t q0, uint32_t q1, const v8h (&a)[NMT][2], v16f (&c)[NMT]) {
-        const uint32_t t0 = 0x42403C00u + k4 * 0x01010100u, t1 = 0x4A484644u + k4 * 0x01010101u;
+        // k4 * 0x01010101 (mod 2^32) by shift-adds (full rate, no v_mul_lo_u32)
+        const uint32_t y = k4 + (k4 << 8), z = y + (y << 16);
+        const uint32_t t0 = 0x42403C00u + (z << 8), t1 = 0x4A484644u + z;
         const uint32_t qm[2] = {q0, q1};
 #pragma unroll
         for (int m = 0; m < 2; m++) {

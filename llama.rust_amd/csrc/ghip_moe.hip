@@ -169,58 +169,25 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
     const uint8_t *wrow = as + (int64_t)e * as_nb2 + (int64_t)(rvalid ? row : 0) * as_nb1;
     const int row_bytes = nb * MXFP4_BYTES;
 
-    // A operand staging: group g's 8 blocks x 4 pieces x TP pairs (16 B each)
-    // -> registers (thread t: pair t % TP, pieces/blocks strided) -> LDS stage
+    // Staging of group g (8 blocks) into LDS stage g&1 with direct global->LDS
+    // loads (no registers, no LDS stores): the three layouts are contiguous in
+    // the thread index, chunk i = c*256 + tid at byte 16i (weights, A) or 4i
+    // (scales), so instruction c of wavefront w writes the 1 KB (256 B) at
+    // chunk c*256 + 64w.
+    //   A:      chunk i -> pair i % TP, block kb = (i / TP) >> 2, piece (i / TP) & 3
+    //   scales: chunk i -> pair i % TP, block kb = i / TP
+    //   window: chunk i -> row i / 9, 16-byte piece i % 9
+    // Padding pairs and blocks past the row read a valid row (the tile's first
+    // pair, the last block): those lanes' MFMA rows and folds are discarded.
     constexpr int ACHUNK = 8 * 4 * TP / 256;  // 16-byte chunks per thread per group
-    // the group's activation scales: entry i = c*256 + t is (block i / TP, pair i % TP)
-    constexpr int DCH = 8 * TP / 256;
-    // Loop-invariant gather addresses: with 256 % TP == 0 every staging chunk
-    // of a thread belongs to the same pair, tid % TP, so its activation row
-    // (codes and scales) is found once here, not per group (pairs[] lives in
-    // LDS, which the compiler cannot hoist across the loop's barriers).
+    constexpr int DCH = 8 * TP / 256;         // scale chunks per thread per group
     static_assert(256 % TP == 0, "one pair per thread");
     const int my_pi = threadIdx.x % TP;
-    const _Float16 *my_arow = my_pi < np ? actf + (int64_t)(first + my_pi) * nb * 32 : nullptr;
-    const float *my_drow = my_pi < np ? actd + (int64_t)(first + my_pi) * nb : nullptr;
-    auto prefetch_d = [&](int g, float (&dr)[DCH]) {
-#pragma unroll
-        for (int c = 0; c < DCH; c++) {
-            const int kb = (c * 256 + (int)threadIdx.x) / TP, b = 8 * g + kb;
-            dr[c] = (my_drow && b < nb) ? my_drow[b] : 0.0f;
-        }
-    };
-    auto store_d = [&](int stage, const float (&dr)[DCH]) {
-#pragma unroll
-        for (int c = 0; c < DCH; c++) {
-            const int i = c * 256 + threadIdx.x;
-            ds_lds[stage][i / TP][i % TP] = dr[c];
-        }
-    };
-    auto prefetch_a = [&](int g, uint4 (&ar)[ACHUNK]) {
-#pragma unroll
-        for (int c = 0; c < ACHUNK; c++) {
-            const int rest = (c * 256 + (int)threadIdx.x) / TP;  // (block kb, piece) of this chunk
-            const int piece = rest & 3, kb = rest >> 2;
-            const int b = 8 * g + kb;
-            ar[c] = (my_arow && b < nb) ? ld16((const uint8_t *)(my_arow + ((int64_t)b * 4 + piece) * 8))
-                                        : make_uint4(0, 0, 0, 0);
-        }
-    };
-    auto store_a = [&](int stage, const uint4 (&ar)[ACHUNK]) {
-#pragma unroll
-        for (int c = 0; c < ACHUNK; c++) {
-            const int idx = c * 256 + threadIdx.x;
-            const int pi = idx % TP, rest = idx / TP, piece = rest & 3, kb = rest >> 2;
-            a_lds[stage][kb][piece][pi] = ar[c];
-        }
-    };
-    // weight window of group g: bytes 136g .. 136g+143 of each of the
-    // workgroup's 128 rows, copied to LDS (16 B per chunk, clamped at the row
-    // end: the tail blocks past the last full window are read with exact loads)
+    const int my_slot = first + (my_pi < np ? my_pi : 0);
+    const _Float16 *my_arow = actf + (int64_t)my_slot * nb * 32;
+    const float *my_drow = actd + (int64_t)my_slot * nb;
     constexpr int WCHUNK = (MOE_TR * MOE_WIN + 255) / 256;
     const uint8_t *wexp = as + (int64_t)e * as_nb2;
-    // weight chunk c of this thread: row r = idx / 9, 16-byte piece l = idx % 9
-    // (fixed for the whole loop: base pointer and piece offset found once)
     const uint8_t *wbase[WCHUNK];
     int wl16[WCHUNK];
 #pragma unroll
@@ -228,26 +195,33 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
         const int idx = c * 256 + threadIdx.x;
         const int r = idx / MOE_WIN, l = idx - r * MOE_WIN;
         wbase[c] = wexp + (int64_t)min((int)blockIdx.y * MOE_TR + r, rows - 1) * as_nb1;
-        wl16[c] = idx < MOE_TR * MOE_WIN ? 16 * l : -1;
+        wl16[c] = 16 * l;
     }
-    auto prefetch_w = [&](int g, uint4 (&wr)[WCHUNK]) {
+    const int wv = threadIdx.x >> 6;
+    auto issue = [&](int g, int stage, bool with_w) {
 #pragma unroll
-        for (int c = 0; c < WCHUNK; c++) {
-            const int off = min(136 * g + wl16[c], row_bytes - 16);
-            wr[c] = wl16[c] >= 0 ? ld16(wbase[c] + off) : make_uint4(0, 0, 0, 0);
+        for (int c = 0; c < ACHUNK; c++) {
+            const int rest = (c * 256 + (int)threadIdx.x) / TP;
+            const int piece = rest & 3, b = min(8 * g + (rest >> 2), nb - 1);
+            g2lds(my_arow + ((int64_t)b * 4 + piece) * 8,
+                  reinterpret_cast<uint8_t *>(&a_lds[stage][0][0][0]) + (c * 256 + 64 * wv) * 16);
+        }
+#pragma unroll
+        for (int c = 0; c < DCH; c++) {
+            const int b = min(8 * g + (c * 256 + (int)threadIdx.x) / TP, nb - 1);
+            __builtin_amdgcn_global_load_lds(my_drow + b,
+                                             (lds_void *)(reinterpret_cast<uint8_t *>(&ds_lds[stage][0][0]) +
+                                                          (c * 256 + 64 * wv) * 4),
+                                             4, 0, 0);
+        }
+        if (with_w) {
+#pragma unroll
+            for (int c = 0; c < WCHUNK; c++)
+                if (c * 256 + 64 * wv < MOE_TR * MOE_WIN)  // whole wavefronts in or out
+                    g2lds(wbase[c] + min(136 * g + wl16[c], row_bytes - 16),
+                          reinterpret_cast<uint8_t *>(&w_lds[stage][0][0]) + (c * 256 + 64 * wv) * 16);
         }
     };
-    auto store_w = [&](int stage, const uint4 (&wr)[WCHUNK]) {
-#pragma unroll
-        for (int c = 0; c < WCHUNK; c++) {
-            const int idx = c * 256 + threadIdx.x;
-            if (idx < MOE_TR * MOE_WIN) {
-                const int r = idx / MOE_WIN, l = idx - r * MOE_WIN;
-                *reinterpret_cast<uint4 *>(&w_lds[stage][r][4 * l]) = wr[c];
-            }
-        }
-    };
-
     float acc[NMT][16];
 #pragma unroll
     for (int mt = 0; mt < NMT; mt++)
@@ -324,34 +298,14 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
 #pragma unroll
             for (int m = 0; m < 2; m++) a[mt][m] = __builtin_bit_cast(v8h, a_lds[stage][kb][2 * m + h2][mt * 32 + li]);
     };
-    // Two groups in flight: while group g is multiplied from LDS stage g&1,
-    // group g+1 sits in one register set (issued an iteration earlier) and
-    // group g+2 is issued into the other; g+1 goes to LDS after g's MFMAs.
-    // The loop is unrolled by two so that both sets have fixed registers.
-    uint4 ar0[ACHUNK], wr0[WCHUNK], ar1[ACHUNK], wr1[WCHUNK];
-    float dr0[DCH], dr1[DCH];
+    // group g+1 lands in LDS stage (g+1)&1 while group g is multiplied
     const int rl = w * 32 + li;  // this lane's row inside the workgroup
-    prefetch_a(0, ar0);
-    prefetch_d(0, dr0);
-    if (ngroups > 0) prefetch_w(0, wr0);
-    if (nga > 1) {
-        prefetch_a(1, ar1);
-        prefetch_d(1, dr1);
-    }
-    if (ngroups > 1) prefetch_w(1, wr1);
-    store_a(0, ar0);
-    store_d(0, dr0);
-    if (ngroups > 0) store_w(0, wr0);
-    __syncthreads();
-    // iteration g: ra* (free) receive group g+2; rb* (group g+1) go to LDS
-    auto body = [&](int g, uint4 (&ra)[ACHUNK], float (&da)[DCH], uint4 (&wa)[WCHUNK], const uint4 (&rb)[ACHUNK],
-                    const float (&db)[DCH], const uint4 (&wb_)[WCHUNK]) {
+    issue(0, 0, ngroups > 0);
+    for (int g = 0; g < nga; g++) {
         const int stage = g & 1;
-        if (g + 2 < nga) {
-            prefetch_a(g + 2, ra);
-            prefetch_d(g + 2, da);
-        }
-        if (g + 2 < ngroups) prefetch_w(g + 2, wa);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's share of group g is in LDS
+        __syncthreads();  // ... every thread's; and stage ^ 1 (group g-1) is no longer read
+        if (g + 1 < nga) issue(g + 1, stage ^ 1, g + 1 < ngroups);
         if (g < ngroups) {
             const uint32_t *wl = w_lds[stage][rl];
             // block kb of the window: e at byte 17kb, qs at 17kb+1; this lane
@@ -383,16 +337,6 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
                          ld4(wb + 9 + 4 * h2), a);
             }
         }
-        if (g + 1 < nga) {
-            store_a(stage ^ 1, rb);
-            store_d(stage ^ 1, db);
-        }
-        if (g + 1 < ngroups) store_w(stage ^ 1, wb_);
-        __syncthreads();
-    };
-    for (int g = 0; g < nga; g += 2) {
-        body(g, ar0, dr0, wr0, ar1, dr1, wr1);
-        if (g + 1 < nga) body(g + 1, ar1, dr1, wr1, ar0, dr0, wr0);
     }
     if (!rvalid) return;
 #pragma unroll

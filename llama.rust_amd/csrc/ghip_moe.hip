@@ -136,13 +136,15 @@ ghip_moe_act_f16(const uint8_t *__restrict__ q8, int64_t q8_row_bytes, const int
 // lane owns row j = lane%32 of its wavefront and 16 pairs per 32-pair block.
 // K-slot e of MFMA half m for lane half h2 is element (e&1)*16 + 8m + 4h2 + e/2
 // of the 32-block: byte 8m+4h2+e/2 of the block's qs, low nibble for even e,
-// high for odd.  The activation operand comes pre-expanded from L2 (one
-// block ahead); the expert row is read in 144-byte windows of 8 blocks (one
-// window ahead); only the nibble LUT and the tile's activation scales live
-// in LDS.  REPACK selects the reference's rows % 8 == 0 fold
+// high for odd.  Per group of MOE_GB blocks, the expert rows' 68-byte windows,
+// the tile's pre-expanded f16 activation codes and their scales are staged in
+// LDS by direct global->LDS loads, one group ahead (about 38 KB per
+// workgroup, four workgroups per CU).  REPACK selects the reference's rows % 8 == 0 fold
 // (fma(dot, e*d, acc), repack.rs:1071) over the plain one (acc += (d*e)*dot,
 // compute.rs:7140).
-constexpr int MOE_WIN = 9;  // 16-byte loads per 8-block window (136 bytes used)
+constexpr int MOE_GB = 4;                               // 32-blocks per staging group
+constexpr int MOE_WB = 17 * MOE_GB;                     // weight window bytes per row and group
+constexpr int MOE_WIN = (MOE_WB + 4 + 15) / 16;         // 16-byte loads per window (+ the dword the last reads touch)
 
 template <int NMT, bool REPACK, bool SUBSUMS>
 __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, int64_t as_nb1, int64_t as_nb2,
@@ -151,9 +153,9 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
                                                float *__restrict__ dst, int64_t dst_nb1, int64_t dst_nb2, int rows,
                                                int nb, int32_t *__restrict__ sub) {
     constexpr int TP = 32 * NMT;
-    __shared__ __attribute__((aligned(16))) float ds_lds[2][8][TP];  // [stage][block][pair] activation scales
-    __shared__ __attribute__((aligned(16))) uint4 a_lds[2][8][4][TP];  // [stage][block][piece][pair] 8 f16 each
-    __shared__ __attribute__((aligned(16))) uint32_t w_lds[2][MOE_TR][MOE_WIN * 4];  // [stage][row][144-byte window]
+    __shared__ __attribute__((aligned(16))) float ds_lds[2][MOE_GB][TP];  // [stage][block][pair] activation scales
+    __shared__ __attribute__((aligned(16))) uint4 a_lds[2][MOE_GB][4][TP];  // [stage][block][piece][pair] 8 f16 each
+    __shared__ __attribute__((aligned(16))) uint32_t w_lds[2][MOE_TR][MOE_WIN * 4];  // [stage][row][window]
     __shared__ int pairs[TP];
     const int tile = blockIdx.x;
     if (tile >= route[0]) return;
@@ -169,7 +171,7 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
     const uint8_t *wrow = as + (int64_t)e * as_nb2 + (int64_t)(rvalid ? row : 0) * as_nb1;
     const int row_bytes = nb * MXFP4_BYTES;
 
-    // Staging of group g (8 blocks) into LDS stage g&1 with direct global->LDS
+    // Staging of group g (MOE_GB blocks) into LDS stage g&1 with direct global->LDS
     // loads (no registers, no LDS stores): the three layouts are contiguous in
     // the thread index, chunk i = c*256 + tid at byte 16i (weights, A) or 4i
     // (scales), so instruction c of wavefront w writes the 1 KB (256 B) at
@@ -179,8 +181,8 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
     //   window: chunk i -> row i / 9, 16-byte piece i % 9
     // Padding pairs and blocks past the row read a valid row (the tile's first
     // pair, the last block): those lanes' MFMA rows and folds are discarded.
-    constexpr int ACHUNK = 8 * 4 * TP / 256;  // 16-byte chunks per thread per group
-    constexpr int DCH = 8 * TP / 256;         // scale chunks per thread per group
+    constexpr int ACHUNK = MOE_GB * 4 * TP / 256;        // 16-byte chunks per thread per group
+    constexpr int DCH = (MOE_GB * TP + 255) / 256;       // scale chunks per thread per group
     static_assert(256 % TP == 0, "one pair per thread");
     const int my_pi = threadIdx.x % TP;
     const int my_slot = first + (my_pi < np ? my_pi : 0);
@@ -202,13 +204,14 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
 #pragma unroll
         for (int c = 0; c < ACHUNK; c++) {
             const int rest = (c * 256 + (int)threadIdx.x) / TP;
-            const int piece = rest & 3, b = min(8 * g + (rest >> 2), nb - 1);
+            const int piece = rest & 3, b = min(MOE_GB * g + (rest >> 2), nb - 1);
             g2lds(my_arow + ((int64_t)b * 4 + piece) * 8,
                   reinterpret_cast<uint8_t *>(&a_lds[stage][0][0][0]) + (c * 256 + 64 * wv) * 16);
         }
 #pragma unroll
         for (int c = 0; c < DCH; c++) {
-            const int b = min(8 * g + (c * 256 + (int)threadIdx.x) / TP, nb - 1);
+            if (c * 256 + 64 * wv >= MOE_GB * TP) continue;  // whole wavefronts
+            const int b = min(MOE_GB * g + (c * 256 + (int)threadIdx.x) / TP, nb - 1);
             __builtin_amdgcn_global_load_lds(my_drow + b,
                                              (lds_void *)(reinterpret_cast<uint8_t *>(&ds_lds[stage][0][0]) +
                                                           (c * 256 + 64 * wv) * 4),
@@ -218,7 +221,7 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
 #pragma unroll
             for (int c = 0; c < WCHUNK; c++)
                 if (c * 256 + 64 * wv < MOE_TR * MOE_WIN)  // whole wavefronts in or out
-                    g2lds(wbase[c] + min(136 * g + wl16[c], row_bytes - 16),
+                    g2lds(wbase[c] + min(MOE_WB * g + wl16[c], row_bytes - 16),
                           reinterpret_cast<uint8_t *>(&w_lds[stage][0][0]) + (c * 256 + 64 * wv) * 16);
         }
     };
@@ -288,10 +291,10 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
     // the 2^k fold holds for k = e - 128 in [-14, 12]
     auto in_range = [](uint32_t e8) { return e8 >= 114u && e8 <= 140u; };
 
-    // full 8-block windows that end inside the row; the rest are tail blocks
-    int ngroups = nb / 8;
-    while (ngroups > 0 && 136 * (ngroups - 1) + 16 * MOE_WIN > row_bytes) ngroups--;
-    const int nga = (nb + 7) / 8;  // activation groups (the tail included)
+    // full windows that end inside the row; the rest are tail blocks
+    int ngroups = nb / MOE_GB;
+    while (ngroups > 0 && MOE_WB * (ngroups - 1) + 16 * MOE_WIN > row_bytes) ngroups--;
+    const int nga = (nb + MOE_GB - 1) / MOE_GB;  // activation groups (the tail included)
     auto a_of = [&](int stage, int kb, v8h (&a)[NMT][2]) {
 #pragma unroll
         for (int mt = 0; mt < NMT; mt++)
@@ -313,27 +316,27 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
             auto e_of = [&](int kb) { return (wl[(17 * kb) >> 2] >> (8 * ((17 * kb) & 3))) & 0xffu; };
             auto window = [&](auto FAST) {
 #pragma unroll 2
-                for (int kb = 0; kb < 8; kb++) {
+                for (int kb = 0; kb < MOE_GB; kb++) {
                     const int o0 = 17 * kb + 1 + 4 * h2, o1 = o0 + 8;
                     const uint32_t q0 = __builtin_amdgcn_alignbyte(wl[(o0 >> 2) + 1], wl[o0 >> 2], o0 & 3);
                     const uint32_t q1 = __builtin_amdgcn_alignbyte(wl[(o1 >> 2) + 1], wl[o1 >> 2], o1 & 3);
                     v8h a[NMT][2];
                     a_of(stage, kb, a);
-                    do_block(FAST, 8 * g + kb, ds_lds[stage][kb], e_of(kb), q0, q1, a);
+                    do_block(FAST, MOE_GB * g + kb, ds_lds[stage][kb], e_of(kb), q0, q1, a);
                 }
             };
-            // one decision per 8-block window for the whole wavefront
+            // one decision per window for the whole wavefront
             bool ok = !SUBSUMS;
 #pragma unroll
-            for (int kb = 0; kb < 8; kb++) ok = ok && in_range(e_of(kb));
+            for (int kb = 0; kb < MOE_GB; kb++) ok = ok && in_range(e_of(kb));
             if (__ballot(!ok) == 0) window(std::true_type{});
             else window(std::false_type{});
         } else {
-            for (int kb = 0; kb < 8 && 8 * g + kb < nb; kb++) {  // tail blocks: exact loads, exact path
-                const uint8_t *wb = wrow + (int64_t)(8 * g + kb) * MXFP4_BYTES;
+            for (int kb = 0; kb < MOE_GB && MOE_GB * g + kb < nb; kb++) {  // tail blocks: exact loads, exact path
+                const uint8_t *wb = wrow + (int64_t)(MOE_GB * g + kb) * MXFP4_BYTES;
                 v8h a[NMT][2];
                 a_of(stage, kb, a);
-                do_block(std::false_type{}, 8 * g + kb, ds_lds[stage][kb], wb[0], ld4(wb + 1 + 4 * h2),
+                do_block(std::false_type{}, MOE_GB * g + kb, ds_lds[stage][kb], wb[0], ld4(wb + 1 + 4 * h2),
                          ld4(wb + 9 + 4 * h2), a);
             }
         }

@@ -3,7 +3,10 @@
 Step (timed): one Llama-3-8B decode layer's MUL_MAT set at batch 1 --
 q, k, v, o, gate, up (Q4_K) and down (Q6_K) -- each op including its on-device
 Q8_K activation quantization, weights rotated over 4 layer copies (551 MB) so
-the 256 MB Infinity Cache cannot serve them.
+the 256 MB Infinity Cache cannot serve them.  The step is one
+ghip_graph_compute call over the 7 nodes (the reference's graph-level seam,
+which runs q/k/v and gate/up as one launch each); the same 7 nodes as
+separate ghip_mul_mat calls are reported beside it.
 value = algorithmic bytes of the step (weights + f32 activations in + f32
 outputs, BASELINE's per-matrix formula) / step time.
 
@@ -58,11 +61,21 @@ def step_bytes(batch):
     return sum(weight_bytes(ty, k, n) + batch * k * 4 + batch * n * 4 for _, ty, k, n in LAYER)
 
 
-def time_layer(be, torch, sets, xs, outs, steps, warmup):
+def time_layer(be, torch, sets, xs, outs, steps, warmup, graph=False):
     """Seconds per decode-layer step.  Each step is one replay of a HIP graph
     holding the layer's 7 MUL_MATs (quantization + kernel each) for one of
-    the weight copies, so host launch gaps are not in the measurement."""
+    the weight copies, so host launch gaps are not in the measurement.
+    graph=False: one ghip_mul_mat call per node; graph=True: one
+    ghip_graph_compute call over the 7 nodes (the reference's graph-level
+    seam), which runs q/k/v and gate/up as one launch each."""
+    import ghip
+    node_lists = [[ghip.mul_mat_node(w, ty, k, xs[k], outs[name]) for (name, ty, k, n), w in zip(LAYER, ws)]
+                  for ws in sets]
+
     def one(i):
+        if graph:
+            be.graph_compute(node_lists[i % len(sets)])
+            return
         ws = sets[i % len(sets)]
         for (name, ty, k, n), w in zip(LAYER, ws):
             be.mul_mat(w, ty, k, xs[k], out=outs[name])
@@ -371,13 +384,18 @@ def main():
         xs = {k: torch.from_numpy(xrng.standard_normal((batch, k), dtype=np.float32)).cuda() for k in (4096, 14336)}
         outs = {name: torch.empty((batch, n), dtype=torch.float32, device="cuda") for name, _, _, n in LAYER}
         steps = args.steps if batch == 1 else max(10, args.steps // 4)
-        t = time_layer(be, torch, sets, xs, outs, steps, args.warmup)
+        t_op = time_layer(be, torch, sets, xs, outs, steps, args.warmup)
+        t_graph = time_layer(be, torch, sets, xs, outs, steps, args.warmup, graph=True)
         te = time_layer_eager(be, torch, sets, xs, outs, max(10, steps // 4))
+        t = t_graph
         gbs = step_bytes(batch) / t / 1e9
         res_by_batch[batch] = {"ms_per_layer": round(t * 1e3, 4), "GB/s": round(gbs, 1),
                                "tokens_per_s_layer": round(batch / t, 1),
+                               "ms_per_layer_per_op_calls": round(t_op * 1e3, 4),
+                               "GB/s_per_op_calls": round(step_bytes(batch) / t_op / 1e9, 1),
                                "ms_per_layer_eager_launch": round(te * 1e3, 4)}
-        log(f"batch {batch}: {t*1e6:.1f} us/layer  {gbs:.1f} GB/s")
+        log(f"batch {batch}: graph_compute {t*1e6:.1f} us/layer  {gbs:.1f} GB/s; "
+            f"per-op calls {t_op*1e6:.1f} us/layer")
         if batch == 1:
             ms_headline, value = t * 1e3, gbs
 
@@ -403,7 +421,8 @@ def main():
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_headline, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic (numpy PCG64: weights N(0,0.02) seed 0 quantized on device, activations N(0,1) seed 1)",
-        "config": {"workload": "Llama-3-8B decode layer MUL_MAT set (q,k,v,o,gate,up Q4_K; down Q6_K), batch 1",
+        "config": {"workload": "Llama-3-8B decode layer MUL_MAT set (q,k,v,o,gate,up Q4_K; down Q6_K), batch 1, "
+                               "one ghip_graph_compute call per step",
                    "bytes_per_step": step_bytes(1), "weight_copies": 4},
         "roofline": roof, "cpu_baseline": cpu,
         "decode_by_batch": res_by_batch, **extras,

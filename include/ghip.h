@@ -167,6 +167,30 @@ ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const g
                                 const ghip_tensor *mask, const ghip_tensor *sinks, const ghip_tensor *dst,
                                 void *stream);
 
+/* One node of a graph: the op, its sources in ggml order (MUL_MAT: src0,
+ * src1; MUL_MAT_ID: as, b, ids; FLASH_ATTN_EXT: q, k, v, mask|NULL,
+ * sinks|NULL; unused slots NULL) and its destination
+ * (ggml_tensor.op / src[] / the node itself, GgmlCTensor sysffi.rs:212-228). */
+typedef struct ghip_node {
+    int32_t op; /* GHIP_OP_* */
+    const ghip_tensor *src[5];
+    const ghip_tensor *dst;
+} ghip_node;
+
+/* Compute the nodes in order on stream, each exactly as its single-op entry
+ * point above does (BackendI.graph_compute, crates/ggml/src/backend.rs:652-668
+ * -> cpu_backend_graph_compute backend.rs:2169 -> compute::graph_compute
+ * compute.rs:307).  Consecutive MUL_MAT nodes with 1-8 F32 activation rows
+ * (Q6_K: one) that read the same src1 (same data and geometry) with the same
+ * K-quant weight type (Q4_K, Q5_K, Q6_K) and the same K -- a layer's q/k/v
+ * or gate/up at decode -- run as one launch of up to four matrices, provided
+ * no node of the group reads or overlaps another's dst (and, for Q4_K at 4+
+ * rows, N % 8 == 0 holds for all or none: it selects the activation
+ * quantizer); their results are bit-identical to the single-op calls.  Returns the first failing node's status (the nodes before
+ * it have been enqueued); ghip_last_error names the failure.
+ * GHIP_GRAPH_FUSE=0 in the environment turns the grouping off. */
+ghip_status ghip_graph_compute(ghip_context *ctx, const ghip_node *nodes, int32_t n_nodes, void *stream);
+
 /* Quantize nrows rows of n_per_row f32 values (device pointer src) into
  * GGUF blocks of `type` (Q4_0, Q4_K, Q6_K, MXFP4) at the device pointer dst,
  * byte-identical to the reference's no-imatrix quantizers

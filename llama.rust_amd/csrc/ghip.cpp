@@ -555,6 +555,123 @@ ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip
                        (int)p.nb, sub);
 }
 
+// ------------------------------------------------------------ graph compute
+
+// Host mirror of GemvMulti in ghip_gemv.hip (kernel argument by value).
+struct GemvMulti {
+    const uint8_t *W[4];
+    float *dst[4];
+    int64_t ldd[4];
+    int rows[4];
+    int wg0[4];
+    int n;
+};
+
+// [first, last) byte range a tensor's elements span (dims with ne > 1)
+void byte_span(const ghip_tensor *t, uintptr_t &lo, uintptr_t &hi) {
+    const TypeInfo ti = type_info(t->type);
+    uint64_t ext = (uint64_t)(t->ne[0] / std::max(1, ti.blck)) * (uint64_t)ti.bytes;
+    for (int d = 1; d < 4; d++)
+        if (t->ne[d] > 1) ext += (uint64_t)(t->ne[d] - 1) * t->nb[d];
+    lo = (uintptr_t)t->data;
+    hi = lo + ext;
+}
+bool overlaps(const ghip_tensor *a, const ghip_tensor *b) {
+    if (!a || !b) return false;
+    uintptr_t alo, ahi, blo, bhi;
+    byte_span(a, alo, ahi);
+    byte_span(b, blo, bhi);
+    return alo < bhi && blo < ahi;
+}
+bool same_view(const ghip_tensor *a, const ghip_tensor *b) {
+    if (a->data != b->data || a->type != b->type) return false;
+    for (int d = 0; d < 4; d++)
+        if (a->ne[d] != b->ne[d] || a->nb[d] != b->nb[d]) return false;
+    return true;
+}
+// a MUL_MAT node the multi-matrix kernels take: K-quant weights, 1-8 F32
+// activation rows (Q6_K: one), a destination, the default 2x2 row groups
+bool multi_candidate(const ghip_node &n) {
+    if (n.op != GHIP_OP_MUL_MAT || !n.src[0] || !n.src[1] || !n.dst) return false;
+    const ghip_tensor *a = n.src[0], *b = n.src[1];
+    if (a->type != GHIP_TYPE_Q4_K && a->type != GHIP_TYPE_Q5_K && a->type != GHIP_TYPE_Q6_K) return false;
+    if (b->type != GHIP_TYPE_F32 || b->ne[1] < 1 || b->ne[1] > (a->type == GHIP_TYPE_Q6_K ? 1 : 8) ||
+        b->ne[2] != 1 || b->ne[3] != 1)
+        return false;
+    if (b->ne[1] >= env_int("GHIP_GEMM_MIN_ROWS", 16)) return false;  // the prefill GEMM's range
+    if (a->ne[2] != 1 || a->ne[3] != 1) return false;
+    return env_int("GHIP_GEMV_RB", 2) == 2 && env_int("GHIP_GEMV_NG", 2) == 2;
+}
+// node j joins the group nodes[i, j)
+bool joins_group(const ghip_node *nodes, int i, int j) {
+    const ghip_node &c = nodes[j], &h = nodes[i];
+    if (!multi_candidate(c) || c.src[0]->type != h.src[0]->type || c.src[0]->ne[0] != h.src[0]->ne[0] ||
+        !same_view(c.src[1], h.src[1]))
+        return false;
+    // Q4_K activations take the 4x8 values for the leading rows only when
+    // N % 8 == 0 (compute.rs:5350-5398): one quantization per group
+    if (c.src[0]->type == GHIP_TYPE_Q4_K && c.src[1]->ne[1] >= 4 && (c.src[0]->ne[1] % 8 == 0) != (h.src[0]->ne[1] % 8 == 0))
+        return false;
+    for (int k = i; k < j; k++) {
+        const ghip_node &o = nodes[k];
+        if (overlaps(o.dst, c.src[0]) || overlaps(o.dst, c.src[1]) || overlaps(c.dst, o.src[0]) ||
+            overlaps(c.dst, o.src[1]) || overlaps(c.dst, o.dst))
+            return false;
+    }
+    return true;
+}
+
+// 2..4 sibling MUL_MATs (joins_group holds) as one multi-matrix GEMV launch
+ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipStream_t s) {
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    MulMatPlan p[4];
+    ghip_status st;
+    int64_t total_rows = 0;
+    for (int i = 0; i < n; i++) {
+        if (!plan_mul_mat(ctx, nodes[i].src[0], nodes[i].src[1], nodes[i].dst, p[i], st)) return st;
+        if (p[i].M != p[0].M || p[i].M > 8 || !gemv_v2(p[i]) || p[i].act_pre)
+            return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "graph_compute: internal: node not groupable");
+        total_rows += p[i].N;
+    }
+    if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    const MulMatPlan &p0 = p[0];
+    const int waves_k = (int)((p0.nb + 15) / 16);
+    if (waves_k > 8) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: ne00 = %lld too large for the decode kernel", (long long)p0.K);
+    // the one-matrix rule (run_gemv) applied to the group's total rows
+    const int dflt_teams = total_rows < 8192 && p0.M <= 2 ? 4 : 8;
+    const int teams = std::max(1, std::min(8 / waves_k, env_int("GHIP_GEMV_TEAMS", dflt_teams)));
+    const int rows_per_wg = 4 * teams;
+    GemvMulti g{};
+    int wg = 0;
+    for (int i = 0; i < n; i++) {
+        g.W[i] = (const uint8_t *)nodes[i].src[0]->data;
+        g.dst[i] = (float *)nodes[i].dst->data;
+        g.ldd[i] = (int64_t)nodes[i].dst->nb[1] / 4;
+        g.rows[i] = (int)p[i].N;
+        g.wg0[i] = wg;
+        wg += (int)((p[i].N + rows_per_wg - 1) / rows_per_wg);
+    }
+    for (int i = n; i < 4; i++) {
+        g.W[i] = g.W[0];
+        g.dst[i] = g.dst[0];
+        g.ldd[i] = g.ldd[0];
+        g.rows[i] = 0;
+        g.wg0[i] = wg;
+    }
+    g.n = n;
+    const int nc = (int)p0.M;
+    const int NC = nc == 1 ? 1 : nc == 2 ? 2 : nc <= 4 ? 4 : 8;
+    const size_t shmem = (size_t)NC * p0.K + (size_t)NC * p0.nb * 4 + (size_t)NC * p0.nb * 16 * 4 +
+                         (size_t)rows_per_wg * waves_k * NC * sizeof(float);
+    if (shmem > 160 * 1024) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: decode LDS image too large");
+    const std::string name = std::string(gemv_base(p0.wtype)) + (p0.wtype == GHIP_TYPE_Q6_K ? "_v2" : "") + "_f_c" +
+                             std::to_string(NC) + "_r2x2_multi";
+    const int n_mat = (int)std::max<int64_t>(0, std::min<int64_t>(nc, p0.n_mat));
+    return ctx->launch(name, dim3((unsigned)wg), dim3(64 * waves_k * teams), shmem, s, g, (int64_t)p0.w_row_bytes,
+                       (int)p0.nb, (const uint8_t *)nodes[0].src[1]->data, (int64_t)nodes[0].src[1]->nb[1], nc,
+                       n_mat);
+}
+
 }  // namespace
 
 extern "C" {
@@ -759,6 +876,40 @@ ghip_status ghip_mul_mat_act(ghip_context *ctx, const ghip_tensor *src0, const g
     if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
     if (!out) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat_act: null output");
     return mul_mat_impl(ctx, src0, src1, nullptr, nullptr, out, stream);
+}
+
+ghip_status ghip_graph_compute(ghip_context *ctx, const ghip_node *nodes, int32_t n_nodes, void *stream) {
+    if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
+    if (n_nodes < 0 || (n_nodes > 0 && !nodes))
+        return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "graph_compute: bad node list");
+    const bool fuse = env_int("GHIP_GRAPH_FUSE", 1) != 0;
+    int i = 0;
+    while (i < n_nodes) {
+        const ghip_node &nd = nodes[i];
+        ghip_status st;
+        int next = i + 1;
+        switch (nd.op) {
+        case GHIP_OP_MUL_MAT:
+            if (fuse && multi_candidate(nd))
+                while (next < n_nodes && next - i < 4 && joins_group(nodes, i, next)) next++;
+            if (next - i >= 2)
+                st = mul_mat_multi(ctx, nodes + i, next - i, (hipStream_t)stream);
+            else
+                st = ghip_mul_mat(ctx, nd.src[0], nd.src[1], nd.dst, stream);
+            break;
+        case GHIP_OP_MUL_MAT_ID:
+            st = ghip_mul_mat_id(ctx, nd.src[0], nd.src[1], nd.src[2], nd.dst, stream);
+            break;
+        case GHIP_OP_FLASH_ATTN_EXT:
+            st = ghip_flash_attn_ext(ctx, nd.src[0], nd.src[1], nd.src[2], nd.src[3], nd.src[4], nd.dst, stream);
+            break;
+        default:
+            return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "graph_compute: node %d: op %d not supported", i, nd.op);
+        }
+        if (st != GHIP_STATUS_SUCCESS) return st;
+        i = next;
+    }
+    return GHIP_STATUS_SUCCESS;
 }
 
 ghip_status ghip_quantize_chunk(ghip_context *ctx, int type, const float *src, void *dst, int64_t nrows,

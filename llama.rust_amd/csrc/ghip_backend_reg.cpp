@@ -100,6 +100,7 @@ void *reg_proc_address(const ggml_hip_backend_reg *, const char *name) {
         {"ghip_mul_mat_id_subsums", (void *)&ghip_mul_mat_id_subsums},
         {"ghip_flash_attn_ext", (void *)&ghip_flash_attn_ext},
         {"ghip_quantize_chunk", (void *)&ghip_quantize_chunk},
+        {"ghip_graph_compute", (void *)&ghip_graph_compute},
     };
     if (!name) return nullptr;
     for (const Proc &p : procs)

@@ -175,7 +175,7 @@ template <int NC, bool SUBSUMS, bool FUSEQ, int RB, int NG, bool Q5 = false>
 __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
                                               int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
                                               int ncols, float *__restrict__ dst, int64_t ldd,
-                                              int32_t *__restrict__ sub, int n_mat) {
+                                              int32_t *__restrict__ sub, int n_mat, int wg = -1) {
     constexpr int RPT = RB * NG;  // rows per team
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = threadIdx.x & 63;
@@ -191,7 +191,8 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
 
     const int b = 16 * w + (lane >> 2), i = lane & 3;
     const bool valid = b < nb;
-    const int rw0 = blockIdx.x * T * RPT;  // first row of the workgroup (uniform)
+    // wg: this workgroup's index within the matrix (-1: blockIdx.x)
+    const int rw0 = (wg < 0 ? (int)blockIdx.x : wg) * T * RPT;  // first row of the workgroup (uniform)
     const int r0 = rw0 + team * RPT;       // first row of the team (uniform)
     const int r1 = min(rows, r0 + RPT);
 
@@ -340,7 +341,8 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
                 }
                 const float part = ac.d * fmaf(dw[rr], (float)ia, -(dmin[rr] * (float)im));
                 const float tot = wave_sum_dpp(part);
-                if (lane == 0 && rg + rr < r1) {
+                // columns past ncols (the NC - ncols padding columns) are not stored
+                if (lane == 0 && c < ncols && rg + rr < r1) {
                     if (nwk == 1) dst[(int64_t)c * ldd + rg + rr] = tot;
                     else red[((rg + rr - rw0) * nwk + w) * NC + c] = tot;
                 }
@@ -373,7 +375,7 @@ template <int NC, bool SUBSUMS, bool FUSEQ, int RB, int NG>
 __device__ __forceinline__ void gemv_q6K_v2_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
                                                  int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
                                                  int ncols, float *__restrict__ dst, int64_t ldd,
-                                                 int32_t *__restrict__ sub, int n_mat) {
+                                                 int32_t *__restrict__ sub, int n_mat, int wg = -1) {
     constexpr int RPT = RB * NG;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = threadIdx.x & 63;
@@ -390,7 +392,7 @@ __device__ __forceinline__ void gemv_q6K_v2_impl(const uint8_t *__restrict__ W, 
     const int b = 16 * w + (lane >> 2), i = lane & 3;
     const int j = i >> 1, hh = i & 1;
     const bool valid = b < nb;
-    const int rw0 = blockIdx.x * T * RPT;
+    const int rw0 = (wg < 0 ? (int)blockIdx.x : wg) * T * RPT;
     const int r0 = rw0 + team * RPT;
     const int r1 = min(rows, r0 + RPT);
     const uint32_t boff = (uint32_t)min(b, nb - 1) * Q6K_BYTES;
@@ -524,7 +526,8 @@ __device__ __forceinline__ void gemv_q6K_v2_impl(const uint8_t *__restrict__ W, 
                 }
                 const float part = (dw[rr] * (float)is) * ac.d;
                 const float tot = wave_sum_dpp(part);
-                if (lane == 0 && rg + rr < r1) {
+                // columns past ncols (the NC - ncols padding columns) are not stored
+                if (lane == 0 && c < ncols && rg + rr < r1) {
                     if (nwk == 1) dst[(int64_t)c * ldd + rg + rr] = tot;
                     else red[((rg + rr - rw0) * nwk + w) * NC + c] = tot;
                 }
@@ -1035,3 +1038,33 @@ Q5K_INST_RB(1) Q5K_INST_RB(2) Q5K_INST_RB(4) Q5K_INST_RB(8)
     }
 #define Q6K_INST_RB(NC) Q6K_INST(NC, 2, 2) Q6K_INST(NC, 2, 4) Q6K_INST(NC, 4, 2)
 Q6K_INST_RB(1) Q6K_INST_RB(2) Q6K_INST_RB(4) Q6K_INST_RB(8)
+
+// Sibling MUL_MATs in one launch (ghip_graph_compute): up to four weight
+// matrices of one type and K that read the same f32 activation rows, each
+// quantized per workgroup exactly as in the one-matrix kernels; workgroups
+// [wg0[i], wg0[i+1]) compute matrix i into dst[i] (row stride ldd[i]).
+// Passed by value; the host mirror in ghip.cpp has the same layout.
+struct GemvMulti {
+    const uint8_t *W[4];
+    float *dst[4];
+    int64_t ldd[4];
+    int rows[4];
+    int wg0[4];
+    int n;
+};
+#define GEMV_MULTI(TN, NC, IMPL, ...)                                                                            \
+    extern "C" __global__ void __launch_bounds__(512)                                                            \
+        ghip_gemv_##TN##_f_c##NC##_r2x2_multi(GemvMulti g, int64_t w_row_bytes, int nb,                         \
+                                              const uint8_t *__restrict__ act, int64_t act_row_bytes, int ncols, \
+                                              int n_mat) {                                                       \
+        const int bx = blockIdx.x;                                                                               \
+        int i = 0;                                                                                               \
+        _Pragma("unroll") for (int k = 1; k < 4; k++) if (k < g.n && bx >= g.wg0[k]) i = k;                     \
+        IMPL<NC, false, true, 2, 2, ##__VA_ARGS__>(g.W[i], w_row_bytes, g.rows[i], nb, act, act_row_bytes, ncols, \
+                                                   g.dst[i], g.ldd[i], nullptr, n_mat, bx - g.wg0[i]);           \
+    }
+GEMV_MULTI(q4_K, 1, gemv_q4K_impl, false) GEMV_MULTI(q4_K, 2, gemv_q4K_impl, false)
+GEMV_MULTI(q4_K, 4, gemv_q4K_impl, false) GEMV_MULTI(q4_K, 8, gemv_q4K_impl, false)
+GEMV_MULTI(q5_K, 1, gemv_q4K_impl, true) GEMV_MULTI(q5_K, 2, gemv_q4K_impl, true)
+GEMV_MULTI(q5_K, 4, gemv_q4K_impl, true) GEMV_MULTI(q5_K, 8, gemv_q4K_impl, true)
+GEMV_MULTI(q6_K_v2, 1, gemv_q6K_v2_impl)

@@ -29,6 +29,37 @@ class Tensor(C.Structure):
                 ("data", C.c_void_p), ("op_params", C.c_int32 * 16)]
 
 
+class GNode(C.Structure):
+    """struct ghip_node"""
+    _fields_ = [("op", C.c_int32), ("src", C.POINTER(Tensor) * 5), ("dst", C.POINTER(Tensor))]
+
+
+class Node:
+    """One graph node for Backend.graph_compute: the op and ggml views of its
+    sources and destination (kept alive with the node)."""
+
+    def __init__(self, op, srcs, dst):
+        self.op, self.srcs, self.dst = op, list(srcs), dst
+
+
+def mul_mat_node(w, wtype, k, x, out):
+    xty = F32 if x.dtype == torch.float32 else ACT_TYPE[wtype]
+    return Node(OP_MUL_MAT, [describe(w, wtype, k), describe(x, xty, k)], describe(out, F32))
+
+
+def mul_mat_id_node(experts, k, b, ids, out):
+    return Node(OP_MUL_MAT_ID, [describe(experts, MXFP4, k), describe(b, F32), describe(ids, I32)], describe(out, F32))
+
+
+def flash_attn_node(q, k, v, mask, sinks, out, scale=1.0, max_bias=0.0, softcap=0.0):
+    import struct
+    d = describe(out, F32)
+    for i, f in enumerate((scale, max_bias, softcap)):
+        d.op_params[i] = struct.unpack("<i", struct.pack("<f", f))[0]
+    return Node(OP_FLASH_ATTN_EXT, [describe(q, F32), describe(k, F16), describe(v, F16), describe(mask, F16),
+                                    describe(sinks, F32)], d)
+
+
 def row_size(ty, n):
     qk, sz = BLOCK[ty]
     if n % qk:
@@ -94,6 +125,8 @@ def lib():
         L.ghip_mul_mat_id.argtypes = [C.c_void_p, P, P, P, P, C.c_void_p]
         L.ghip_mul_mat_id_subsums.restype = C.c_int
         L.ghip_mul_mat_id_subsums.argtypes = [C.c_void_p, P, P, P, C.c_void_p, C.c_void_p]
+        L.ghip_graph_compute.restype = C.c_int
+        L.ghip_graph_compute.argtypes = [C.c_void_p, C.POINTER(GNode), C.c_int32, C.c_void_p]
         L.ghip_flash_attn_ext.restype = C.c_int
         L.ghip_flash_attn_ext.argtypes = [C.c_void_p, P, P, P, P, P, P, C.c_void_p]
         _lib = L
@@ -212,6 +245,17 @@ class Backend:
         self._check(lib().ghip_flash_attn_ext(self._ctx, ref(tq), ref(tk), ref(tv), ref(tm), ref(ts), ref(td),
                                               _stream()), "ghip_flash_attn_ext")
         return out
+
+    # ---- graph
+    def graph_compute(self, nodes):
+        """ghip_graph_compute over a list of Node (mul_mat_node, ...), in order."""
+        arr = (GNode * max(1, len(nodes)))()
+        for i, nd in enumerate(nodes):
+            arr[i].op = nd.op
+            for j, t in enumerate(nd.srcs[:5]):
+                arr[i].src[j] = C.pointer(t) if t is not None else None
+            arr[i].dst = C.pointer(nd.dst) if nd.dst is not None else None
+        self._check(lib().ghip_graph_compute(self._ctx, arr, len(nodes), _stream()), "ghip_graph_compute")
 
     def synchronize(self):
         self._check(lib().ghip_synchronize(self._ctx, _stream()), "ghip_synchronize")

@@ -118,6 +118,24 @@ def test_llama3_decode_shapes(be, name, ty, n, rows, cols):
     run_case(be, ty, n, rows, cols, seed=0, check_sub=(cols <= 2))
 
 
+@pytest.mark.parametrize("cols", [3, 5, 6, 7])
+def test_padding_columns_not_stored(be, cols):
+    """Batches that are not a kernel width (3 -> 4, 5..7 -> 8 columns): the
+    padding columns must not be written.  dst is the first `cols` rows of an
+    8-row buffer; the rows after it keep their canary values.  K = 4096 (one
+    wavefront per row) and 14336 output rows, the decode shapes."""
+    import ghip
+    k, n = 4096, 14336
+    g = torch.Generator(device="cuda").manual_seed(cols)
+    w = be.quantize(torch.randn((n, k), device="cuda", generator=g) * 0.02, ghip.Q4_K)
+    x = torch.randn((cols, k), device="cuda", generator=g)
+    full = torch.full((8, n), 12345.0, device="cuda")
+    be.mul_mat(w, ghip.Q4_K, k, x, out=full[:cols])
+    torch.cuda.synchronize()
+    assert bool((full[cols:] == 12345.0).all())
+    assert torch.isfinite(full[:cols]).all()
+
+
 def test_unsupported_type_raises(be):
     import ghip
     # Q4_1 (type 3, 20-byte blocks) has no kernel here: a status, no fallback

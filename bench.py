@@ -32,6 +32,12 @@ LAYER = [  # (name, weight type, K, N)
     ("q", 12, 4096, 4096), ("k", 12, 4096, 1024), ("v", 12, 4096, 1024), ("o", 12, 4096, 4096),
     ("gate", 12, 4096, 14336), ("up", 12, 4096, 14336), ("down", 14, 14336, 4096),
 ]
+# the activation each node reads, as in the model: q/k/v the attention-norm
+# output, o the attention output, gate/up the FFN-norm output, down the
+# gated FFN activation (so only q/k/v and gate/up share an input)
+LAYER_INPUT = {"q": "x_attn", "k": "x_attn", "v": "x_attn", "o": "attn_out", "gate": "x_ffn", "up": "x_ffn",
+               "down": "h_ffn"}
+INPUT_K = {"x_attn": 4096, "attn_out": 4096, "x_ffn": 4096, "h_ffn": 14336}
 
 
 def log(*a):
@@ -69,7 +75,7 @@ def time_layer(be, torch, sets, xs, outs, steps, warmup, graph=False):
     ghip_graph_compute call over the 7 nodes (the reference's graph-level
     seam), which runs q/k/v and gate/up as one launch each."""
     import ghip
-    node_lists = [[ghip.mul_mat_node(w, ty, k, xs[k], outs[name]) for (name, ty, k, n), w in zip(LAYER, ws)]
+    node_lists = [[ghip.mul_mat_node(w, ty, k, xs[LAYER_INPUT[name]], outs[name]) for (name, ty, k, n), w in zip(LAYER, ws)]
                   for ws in sets]
 
     def one(i):
@@ -78,7 +84,7 @@ def time_layer(be, torch, sets, xs, outs, steps, warmup, graph=False):
             return
         ws = sets[i % len(sets)]
         for (name, ty, k, n), w in zip(LAYER, ws):
-            be.mul_mat(w, ty, k, xs[k], out=outs[name])
+            be.mul_mat(w, ty, k, xs[LAYER_INPUT[name]], out=outs[name])
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -107,7 +113,7 @@ def time_layer_eager(be, torch, sets, xs, outs, steps):
     def one(i):
         ws = sets[i % len(sets)]
         for (name, ty, k, n), w in zip(LAYER, ws):
-            be.mul_mat(w, ty, k, xs[k], out=outs[name])
+            be.mul_mat(w, ty, k, xs[LAYER_INPUT[name]], out=outs[name])
     for i in range(3):
         one(i)
     torch.cuda.synchronize()
@@ -381,7 +387,8 @@ def main():
     res_by_batch = {}
     ms_headline = None
     for batch in (1, 2, 4, 8):
-        xs = {k: torch.from_numpy(xrng.standard_normal((batch, k), dtype=np.float32)).cuda() for k in (4096, 14336)}
+        xs = {nm: torch.from_numpy(xrng.standard_normal((batch, k), dtype=np.float32)).cuda()
+              for nm, k in INPUT_K.items()}
         outs = {name: torch.empty((batch, n), dtype=torch.float32, device="cuda") for name, _, _, n in LAYER}
         steps = args.steps if batch == 1 else max(10, args.steps // 4)
         t_op = time_layer(be, torch, sets, xs, outs, steps, args.warmup)

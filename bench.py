@@ -283,6 +283,31 @@ def gemm_bench(be, torch, np):
     return res
 
 
+def gemm_q6k_bench(be, torch, np):
+    """The Q4_K_M down projection at 512 tokens (Q6_K 14336 -> 4096): the
+    f16-MFMA GEMM (weight repack + f16 code layout + GEMM) against the
+    8-column decode kernels it replaces."""
+    import ghip
+    m, k, n = 512, 14336, 4096
+    g = torch.Generator(device="cuda").manual_seed(0)
+    wf = torch.randn((n, k), device="cuda", generator=g) * 0.02
+    w = be.quantize(wf, ghip.Q6_K)
+    del wf
+    x = torch.randn((m, k), device="cuda", generator=g)
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    us = graph_time_us(torch, lambda i: be.mul_mat(w, ghip.Q6_K, k, x, out=out), 10)
+    os.environ["GHIP_GEMM_Q6K_MIN_ROWS"] = str(1 << 30)
+    try:
+        us_gemv = graph_time_us(torch, lambda i: be.mul_mat(w, ghip.Q6_K, k, x, out=out), 2, reps=2)
+    finally:
+        del os.environ["GHIP_GEMM_Q6K_MIN_ROWS"]
+    ops = 2.0 * m * n * k
+    log(f"Q6_K GEMM {m}x{k}->{n}: op {us:.1f} us ({ops / us / 1e6:.1f} TOPS); 8-column decode kernels {us_gemv:.1f} us")
+    return {f"{m}x{k}->{n}": {"us_op": round(us, 2), "TOPS_op": round(ops / us / 1e6, 1),
+                              "frac_f16_peak": round(ops / us / 1e6 / 2500.0, 4),
+                              "us_op_8col_decode_kernels": round(us_gemv, 2)}}
+
+
 def moe_bench(be, torch, np):
     """Config 4: gpt-oss MoE MUL_MAT_ID, 32 MXFP4 experts, 256 tokens, top-4."""
     import ghip
@@ -420,6 +445,7 @@ def main():
         extras["q4_0_gemv_4096"] = q4_0_bench(be, torch, np)
         extras["gemv_q5_0_q8_0_q5_K"] = more_types_bench(be, torch, np)
         extras["prefill_gemm_q4K"] = gemm_bench(be, torch, np)
+        extras["prefill_gemm_q6K"] = gemm_q6k_bench(be, torch, np)
         extras["moe_mxfp4"] = moe_bench(be, torch, np)
         extras["flash_attn_f16kv"] = fa_bench(be, torch, np)
     cpu = None if args.no_cpu else cpu_baseline()

@@ -297,6 +297,7 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
 // out for the GEMM (codes | bsum16 | d, tokens padded to 128), then the int8
 // MFMA GEMM runs on 128 x 128 tiles.
 constexpr size_t kGemmSmem128 = 116224, kGemmSmem64 = 76544;  // sizeof(g3::Smem<BM>) in ghip_gemm.hip
+constexpr size_t kGemmSmemQ6 = 140032;                         // sizeof(g6::Smem) in ghip_gemm.hip
 // token tile: 64 (two workgroups per CU) unless GHIP_GEMM_BM=128
 int gemm_bm() { return env_int("GHIP_GEMM_BM", 64) == 128 ? 128 : 64; }
 // K slices for grids that would leave CUs idle (fewer than 128 tiles); the
@@ -309,14 +310,50 @@ int gemm_nsplit(const MulMatPlan &p) {
     const int64_t nbs = (p.nb + want - 1) / want;  // super-blocks per slice
     return (int)((p.nb + nbs - 1) / nbs);
 }
+// Q6_K prefill workspace: f16 codes [Mpad][K] | dT [nb][Mpad] | repacked weights [N][nb][288]
+constexpr size_t kQ6R = 288;
+size_t gemm_q6k_bytes(const MulMatPlan &p, size_t *codes_b, size_t *dt_b) {
+    const size_t Mpad = (size_t)(p.M + 127) / 128 * 128, nbk = (size_t)p.K / 256;
+    *codes_b = (Mpad * (size_t)p.K * 2 + 255) & ~(size_t)255;
+    *dt_b = (nbk * Mpad * 4 + 255) & ~(size_t)255;
+    return *codes_b + *dt_b + (size_t)p.N * nbk * kQ6R;
+}
 size_t gemm_layout_bytes(const MulMatPlan &p) {
+    if (p.wtype == GHIP_TYPE_Q6_K) {
+        size_t a, b;
+        return gemm_q6k_bytes(p, &a, &b);
+    }
     const size_t Mpad = (size_t)(p.M + 127) / 128 * 128, nbk = (size_t)p.K / 256;
     const int ns = gemm_nsplit(p);
     const size_t part = ns > 1 ? (size_t)ns * (size_t)p.M * (size_t)p.N * 4 : 0;
     return ((Mpad * (size_t)p.K + nbk * Mpad * 32 + nbk * Mpad * 4 + 255) & ~(size_t)255) + part;
 }
+// Q6_K: repack the weights into aligned records, lay the codes out as f16, then
+// the f16-MFMA GEMM on 64 x 128 tiles (one workgroup per CU, 137 KB of LDS)
+ghip_status run_gemm_q6k(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, float *dst,
+                         int64_t ldd, int32_t *sub, void *layout_ws, hipStream_t s) {
+    size_t codes_b, dt_b;
+    gemm_q6k_bytes(p, &codes_b, &dt_b);
+    const int64_t Mpad = (p.M + 127) / 128 * 128, nbk = p.K / 256;
+    uint16_t *codes = (uint16_t *)layout_ws;
+    float *dT = (float *)((uint8_t *)layout_ws + codes_b);
+    uint8_t *rep = (uint8_t *)layout_ws + codes_b + dt_b;
+    const int64_t rthreads = p.N * nbk * 64;
+    ghip_status st = ctx->launch("ghip_q6K_repack", dim3((unsigned)((rthreads + 255) / 256)), dim3(256), 0, s,
+                                 (const uint8_t *)w, (int64_t)p.w_row_bytes, (int)p.N, (int)nbk, rep);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    st = ctx->launch("ghip_gemm_act_layout_f16", dim3((unsigned)((p.M * nbk + 3) / 4)), dim3(256), 0, s, act,
+                     (int64_t)p.act_row_bytes, (int)p.M, (int)Mpad, (int)nbk, codes, dT);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    const unsigned grid = (unsigned)(((p.M + 63) / 64) * ((p.N + 127) / 128));
+    return ctx->launch(sub ? "ghip_gemm_q6_K_sub" : "ghip_gemm_q6_K", dim3(grid), dim3(256), kGemmSmemQ6, s,
+                       (const uint8_t *)rep, (int)p.N, (int)nbk, (const uint16_t *)codes, (const float *)dT, (int)p.M,
+                       (int)Mpad, dst, ldd, sub);
+}
+
 ghip_status run_gemm(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, float *dst,
                      int64_t ldd, int32_t *sub, void *layout_ws, hipStream_t s) {
+    if (p.wtype == GHIP_TYPE_Q6_K) return run_gemm_q6k(ctx, p, w, act, dst, ldd, sub, layout_ws, s);
     const int64_t Mpad = (p.M + 127) / 128 * 128, K = p.K, nbk = p.K / 256;
     int8_t *codes = (int8_t *)layout_ws;
     uint16_t *bsT = (uint16_t *)(codes + Mpad * K);
@@ -346,8 +383,11 @@ ghip_status run_gemm(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
 }
 
 bool use_gemm(const MulMatPlan &p) {
-    const int min_m = env_int("GHIP_GEMM_MIN_ROWS", 16);
-    return p.wtype == GHIP_TYPE_Q4_K && p.M >= min_m && p.M <= INT32_MAX;
+    if (p.M > INT32_MAX) return false;
+    if (p.wtype == GHIP_TYPE_Q4_K) return p.M >= env_int("GHIP_GEMM_MIN_ROWS", 16);
+    // Q6_K: the f16-MFMA GEMM from 64 activation rows (below, the 8-column decode kernels)
+    if (p.wtype == GHIP_TYPE_Q6_K) return p.M >= env_int("GHIP_GEMM_Q6K_MIN_ROWS", 64) && p.K >= 512;
+    return false;
 }
 
 ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b, const ghip_tensor *d,

@@ -291,6 +291,234 @@ __device__ __forceinline__ void gemm_q4K_impl(const uint8_t *__restrict__ W, int
     }
 GEMM_KERNELS(ghip_gemm_q4_K, 128, 512, 1)
 GEMM_KERNELS(ghip_gemm_q4_K_m64, 64, 256, 2)
+// ---------------------------------------------------------------- Q6_K prefill
+// Many activation rows with Q6_K weights (vec_dot_q6_K_q8_K, vec_dot.rs:982-1040,
+// per super-block  is = sum_s sc_s * sum_16 (q6 - 32) * q8,  out += (d * is) * d8).
+//
+// On the f16 matrix cores with exact operands:
+//  * activations: the Q8_K codes as f16 (exact), written by ghip_gemm_act_layout_f16;
+//  * weights: (q - 32) * sc with the signed scale split sc = 16*sh + sl
+//    (sl = sc & 15, sh = sc >> 4), two f16 planes per K-step:
+//      (q - 32) * sl        |.| <= 480,  an integer, exact in f16;
+//      (q - 32) * 16 * sh   a multiple of 16 with |.| <= 4096, exact in f16.
+//    Every product with a code (|q8| <= 128) is exact in fp32, and both planes
+//    add into one fp32 accumulator per super-block, which is then `is`.  The
+//    sub-sum kernels take a fresh accumulator per 16-element sub-block (all
+//    partial sums < 2^24) and add the sub-blocks as integers, so their `is`
+//    is exact whatever the data.
+// The 210-byte blocks start at odd 2-byte offsets; ghip_q6K_repack first
+// rewrites them per call into aligned 288-byte records:
+//   q[256] (6-bit values 0..63 in element order) | sc[16] int8 | d f32 | pad.
+constexpr int Q6R_BYTES = 288;
+
+// one thread per 4 elements of a block (64 threads per block)
+extern "C" __global__ void __launch_bounds__(256)
+ghip_q6K_repack(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb, uint8_t *__restrict__ out) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t blk = t >> 6;  // row * nb + block
+    if (blk >= (int64_t)N * nb) return;
+    const int u = (int)(t & 63), e4 = 4 * u;
+    const int64_t row = blk / nb;
+    const int b = (int)(blk - row * nb);
+    const uint8_t *src = W + row * w_row_bytes + (int64_t)b * Q6K_BYTES;
+    uint8_t *dst = out + blk * Q6R_BYTES;
+    // element i of half j = i / 128, l = i % 128: ql[64j + l % 64] nibble l / 64,
+    // qh[32j + l % 32] bits 2 * (l / 32) (dequantize_row_q6_K)
+    const int j = e4 >> 7, l = e4 & 127;
+    const uint8_t *ql = src + 64 * j + (l & 63);
+    const uint8_t *qh = src + 128 + 32 * j + (l & 31);
+    const int nsh = 4 * (l >> 6), hsh = 2 * (l >> 5);
+    uint32_t v = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) v |= (uint32_t)(((ql[k] >> nsh) & 15) | (((qh[k] >> hsh) & 3) << 4)) << (8 * k);
+    *reinterpret_cast<uint32_t *>(dst + e4) = v;
+    if (u < 4) {
+        const uint8_t *sc = src + 192 + 4 * u;
+        *reinterpret_cast<uint32_t *>(dst + 256 + 4 * u) =
+            (uint32_t)sc[0] | ((uint32_t)sc[1] << 8) | ((uint32_t)sc[2] << 16) | ((uint32_t)sc[3] << 24);
+    } else if (u == 4) {
+        *reinterpret_cast<float *>(dst + 272) = h2f(ld2(src + 208));
+    } else if (u < 8) {
+        *reinterpret_cast<uint32_t *>(dst + 276 + 4 * (u - 5)) = 0u;
+    }
+}
+
+// Q8_K rows -> f16 codes [Mpad][K] and block scales dT [nb][Mpad] (tokens padded
+// to a multiple of 128); one wavefront per (token, super-block)
+extern "C" __global__ void __launch_bounds__(256)
+ghip_gemm_act_layout_f16(const uint8_t *__restrict__ q8k, int64_t row_bytes, int M, int Mpad, int nb,
+                         _Float16 *__restrict__ codes, float *__restrict__ dT) {
+    const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (task >= (int64_t)M * nb) return;
+    const int m = (int)(task / nb), b = (int)(task % nb);
+    const uint8_t *blk = q8k + (int64_t)m * row_bytes + (int64_t)b * Q8K_BYTES;
+    const uint32_t c4 = ld4(blk + 4 + 4 * lane);
+    _Float16 *o = codes + (int64_t)m * nb * QK_K + b * QK_K + 4 * lane;
+#pragma unroll
+    for (int k = 0; k < 4; k++) o[k] = (_Float16)(float)(int8_t)(c4 >> (8 * k));
+    if (lane == 0) dT[(int64_t)b * Mpad + m] = __uint_as_float(ld4(blk));
+}
+
+namespace g6 {
+constexpr int BM = 64, BN = 128;
+struct Smem {
+    _Float16 act[2][BM * QK_K];     // [stage][token][256], 16-byte slots swizzled by token % 32
+    uint8_t w[2][BN * Q6R_BYTES];   // [stage][row][288]
+    float da[3][BM];                // block scales of the tokens, a 3-slot ring
+};
+}  // namespace g6
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+// 64 tokens x 128 rows per 256-thread workgroup; wavefront w owns rows
+// 32w .. 32w+31 and both 32-token tiles.  K-step ks (16 elements of
+// sub-block ks): lane l takes elements 16ks + 8(l/32) .. +7 of row l % 32 (B)
+// and of token l % 32 of each tile (A).
+template <bool SUBSUMS>
+__device__ __forceinline__ void gemm_q6K_impl(const uint8_t *__restrict__ R, int N, int nb,
+                                              const _Float16 *__restrict__ codes, const float *__restrict__ dT,
+                                              int M, int Mpad, float *__restrict__ dst, int64_t ldd,
+                                              int32_t *__restrict__ sub) {
+    constexpr int BM = g6::BM, BN = g6::BN;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
+    g6::Smem &SM = *reinterpret_cast<g6::Smem *>(smem_raw);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane & 31, h = lane >> 5;
+    const int64_t K = (int64_t)nb * QK_K;
+    const int n_tiles_m = (M + BM - 1) / BM, n_tiles_n = (N + BN - 1) / BN;
+    const int total = n_tiles_m * n_tiles_n;
+    int id = blockIdx.x;
+    if (total % 8 == 0) id = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+    const int m0 = (id % n_tiles_m) * BM;
+    const int n0 = (id / n_tiles_m) * BN;
+
+    // ---- direct loads of super-block b: wavefront w moves act pieces
+    // 8w .. 8w+7 (2 tokens each), weight pieces 9w .. 9w+8 (64 16-byte
+    // chunks each) and (w = 0) the block scales
+    auto issue = [&](int b, int p) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int tok = 2 * (8 * wave + i) + (lane >> 5);
+            const int slot = (lane & 31) ^ (tok & 31);
+            g2lds(codes + (int64_t)(m0 + tok) * K + (int64_t)b * QK_K + 8 * slot,
+                  reinterpret_cast<uint8_t *>(SM.act[p]) + 1024 * (8 * wave + i));
+        }
+#pragma unroll
+        for (int i = 0; i < 9; i++) {
+            const int c = 64 * (9 * wave + i) + lane;
+            const int row = c / 18, k16 = c - 18 * row;
+            g2lds(R + ((int64_t)min(n0 + row, N - 1) * nb + b) * Q6R_BYTES + 16 * k16, SM.w[p] + 1024 * (9 * wave + i));
+        }
+        if (wave == 0 && lane < BM / 4) g2lds(dT + (int64_t)b * Mpad + m0 + 4 * lane, SM.da[b % 3]);
+    };
+
+    v16f out[2];
+#pragma unroll
+    for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) out[tm][v] = 0.0f;
+    const int wr = 32 * wave + li;  // this lane's weight row (B operand column)
+    const uint32_t aoff[2] = {(uint32_t)li * QK_K, (uint32_t)(32 + li) * QK_K};  // halfs
+    const uint32_t asw = (uint32_t)(li & 31);
+    const v2h bias = {(_Float16)-1056.0f, (_Float16)-1056.0f};  // 1024 + 32
+
+    issue(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int b = 0; b < nb; b++) {
+        const int p = b & 1;
+        if (b + 1 < nb) issue(b + 1, p ^ 1);
+        const uint8_t *wrow = SM.w[p] + wr * Q6R_BYTES;
+        const uint4 sc4 = *reinterpret_cast<const uint4 *>(wrow + 256);
+        const float dw = *reinterpret_cast<const float *>(wrow + 272);
+        const uint32_t scw[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
+        v16f acc[2];
+        int isub[2][16];
+        const v16f zf = {};
+#pragma unroll
+        for (int tm = 0; tm < 2; tm++) {
+            acc[tm] = zf;
+#pragma unroll
+            for (int v = 0; v < 16; v++) isub[tm][v] = 0;
+        }
+#pragma unroll(SUBSUMS ? 1 : 16)
+        for (int ks = 0; ks < 16; ks++) {
+            const uint2 qv = *reinterpret_cast<const uint2 *>(wrow + 16 * ks + 8 * h);
+            // the sub-block's signed scale, split 16*sh + sl, as f16 pairs
+            const int sc = (int)(int8_t)(scw[ks >> 2] >> (8 * (ks & 3)));
+            const int sl = sc & 15, sh16 = sc - sl;
+            const _Float16 fl = (_Float16)(float)sl, fh = (_Float16)(float)sh16;
+            const v2h pl = {fl, fl}, ph = {fh, fh};
+            v8h blo, bhi;
+            const uint32_t qw[2] = {qv.x, qv.y};
+#pragma unroll
+            for (int d = 0; d < 2; d++) {
+                // bytes q -> f16 (1024 + q) by placing 0x64 above each byte, then - 1056
+                const v2h e0 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(0x64646464u, qw[d], 0x04010400u)) + bias;
+                const v2h e1 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(0x64646464u, qw[d], 0x04030402u)) + bias;
+                const v2h l0 = e0 * pl, l1 = e1 * pl, h0 = e0 * ph, h1 = e1 * ph;
+                blo[4 * d] = l0[0]; blo[4 * d + 1] = l0[1]; blo[4 * d + 2] = l1[0]; blo[4 * d + 3] = l1[1];
+                bhi[4 * d] = h0[0]; bhi[4 * d + 1] = h0[1]; bhi[4 * d + 2] = h1[0]; bhi[4 * d + 3] = h1[1];
+            }
+#pragma unroll
+            for (int tm = 0; tm < 2; tm++) {
+                const v8h a = *reinterpret_cast<const v8h *>(SM.act[p] + aoff[tm] + 8 * ((uint32_t)(2 * ks + h) ^ asw));
+                if constexpr (SUBSUMS) {
+                    // a fresh accumulator per sub-block: exact, then integer sums
+                    const v16f c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, blo, zf, 0, 0, 0);
+                    const v16f c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bhi, c1, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 16; v++) isub[tm][v] += __float2int_rn(c2[v]);
+                } else {
+                    acc[tm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, blo, acc[tm], 0, 0, 0);
+                    acc[tm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bhi, acc[tm], 0, 0, 0);
+                }
+            }
+        }
+        // ---- out += (d * is) * d8 (vec_dot_q6_K_q8_K's per-block order)
+        const float *dab = SM.da[b % 3];
+#pragma unroll
+        for (int tm = 0; tm < 2; tm++) {
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int tl = 32 * tm + crow(v, lane);
+                float is;
+                if constexpr (SUBSUMS) {
+                    is = (float)isub[tm][v];
+                    if (m0 + tl < M && n0 + wr < N) sub[((int64_t)(m0 + tl) * N + (n0 + wr)) * nb + b] = isub[tm][v];
+                } else {
+                    is = acc[tm][v];
+                }
+                out[tm][v] = fmaf(dw * is, dab[tl], out[tm][v]);
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // super-block b+1 is in LDS
+        __syncthreads();
+    }
+    const int n = n0 + wr;
+#pragma unroll
+    for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int m = m0 + 32 * tm + crow(v, lane);
+            if (m < M && n < N) dst[(int64_t)m * ldd + n] = out[tm][v];
+        }
+}
+extern "C" __global__ void __launch_bounds__(256, 1)
+    ghip_gemm_q6_K(const uint8_t *__restrict__ R, int N, int nb, const _Float16 *__restrict__ codes,
+                   const float *__restrict__ dT, int M, int Mpad, float *__restrict__ dst, int64_t ldd,
+                   int32_t *__restrict__ sub) {
+    gemm_q6K_impl<false>(R, N, nb, codes, dT, M, Mpad, dst, ldd, sub);
+}
+extern "C" __global__ void __launch_bounds__(256, 1)
+    ghip_gemm_q6_K_sub(const uint8_t *__restrict__ R, int N, int nb, const _Float16 *__restrict__ codes,
+                       const float *__restrict__ dT, int M, int Mpad, float *__restrict__ dst, int64_t ldd,
+                       int32_t *__restrict__ sub) {
+    gemm_q6K_impl<true>(R, N, nb, codes, dT, M, Mpad, dst, ldd, sub);
+}
+static_assert(sizeof(g6::Smem) == 140032, "host code launches with this LDS size");
+
 // split-K partial sums [nsplit][M][N] -> dst, slices added in order; four
 // consecutive outputs per thread (N % 4 == 0)
 extern "C" __global__ void __launch_bounds__(256)

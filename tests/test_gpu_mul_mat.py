@@ -155,6 +155,34 @@ def test_gemm_q4K_small(be, n, rows, cols):
     run_case(be, O.Q4_K, n, rows, cols, seed=rows)
 
 
+@pytest.mark.parametrize("n,rows,cols", [(512, 136, 64), (1024, 200, 100), (768, 128, 130), (4096, 256, 64),
+                                         (512, 8, 200)])
+def test_gemm_q6K_small(be, n, rows, cols):
+    """Q6_K with >= 64 activation rows takes the f16-MFMA GEMM (repacked
+    weights, exact split-scale planes); tile edges in tokens and rows; int32
+    sub-sums bit-exact."""
+    run_case(be, O.Q6_K, n, rows, cols, seed=rows + cols)
+
+
+def test_gemm_q6K_prefill_down(be):
+    """The Q4_K_M down projection at 512 tokens: 14336 -> 4096 Q6_K.  The GPU
+    computes the whole product; the oracle checks a 512-row slice, plus the
+    sub-sums of 32 of those rows."""
+    tokens, n, rows = 512, 14336, 4096
+    w, x = make(O.Q6_K, n, rows, tokens, seed=5)
+    sl = slice(1000, 1512)
+    wsl = w[sl]
+    print(f"gemm q6_K tokens={tokens} n={n} rows={rows}", flush=True)
+    got = be.mul_mat(torch.from_numpy(w).cuda(), O.Q6_K, n, torch.from_numpy(x).cuda()).cpu().numpy()
+    want, _, _ = O.mul_mat(O.Q6_K, wsl, n, 512, x, tokens)
+    err = rel_err(got[:, sl], want)
+    assert err <= TOL, f"rel_err {err:.3e}"
+    w32 = np.ascontiguousarray(wsl[:32])
+    sub = be.mul_mat_subsums(torch.from_numpy(w32).cuda(), O.Q6_K, n, torch.from_numpy(x).cuda()).cpu().numpy()
+    _, _, want_sub = O.mul_mat(O.Q6_K, w32, n, 32, x, tokens, want_subsums=True)
+    assert np.array_equal(sub, want_sub)
+
+
 @pytest.mark.parametrize("tokens,n,rows", [(128, 4096, 4096), (512, 4096, 14336), (2048, 4096, 4096)])
 def test_gemm_q4K_prefill_shapes(be, tokens, n, rows):
     """Config 3 shapes.  The GPU computes the whole product; the oracle checks

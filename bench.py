@@ -308,6 +308,27 @@ def gemm_q6k_bench(be, torch, np):
                               "us_op_8col_decode_kernels": round(us_gemv, 2)}}
 
 
+def prefill_layer_bench(be, torch, np, tokens=512):
+    """The decode layer's 7 MUL_MAT nodes at `tokens` activation rows (a
+    prefill step): q/k/v/o/gate/up on the Q4_K int8 GEMM, down on the Q6_K
+    f16 GEMM, one ghip_graph_compute call, each node reading its own input."""
+    import ghip
+    g = torch.Generator(device="cuda").manual_seed(7)
+    ws = {}
+    for name, ty, k, n in LAYER:
+        wf = torch.randn((n, k), device="cuda", generator=g) * 0.02
+        ws[name] = be.quantize(wf, ty)
+        del wf
+    xs = {nm: torch.randn((tokens, k), device="cuda", generator=g) for nm, k in INPUT_K.items()}
+    outs = {name: torch.empty((tokens, n), dtype=torch.float32, device="cuda") for name, _, _, n in LAYER}
+    nodes = [ghip.mul_mat_node(ws[name], ty, k, xs[LAYER_INPUT[name]], outs[name]) for name, ty, k, n in LAYER]
+    us = graph_time_us(torch, lambda i: be.graph_compute(nodes), 5)
+    ops = sum(2.0 * tokens * k * n for _, _, k, n in LAYER)
+    log(f"prefill layer ({tokens} tokens, 7 MUL_MATs): {us:.1f} us, {ops / us / 1e6:.1f} TOPS")
+    del ws, xs, outs, nodes
+    return {"tokens": tokens, "us": round(us, 1), "TOPS": round(ops / us / 1e6, 1), "tokens_per_s": round(tokens / us * 1e6, 1)}
+
+
 def moe_bench(be, torch, np):
     """Config 4: gpt-oss MoE MUL_MAT_ID, 32 MXFP4 experts, 256 tokens, top-4."""
     import ghip
@@ -446,6 +467,7 @@ def main():
         extras["gemv_q5_0_q8_0_q5_K"] = more_types_bench(be, torch, np)
         extras["prefill_gemm_q4K"] = gemm_bench(be, torch, np)
         extras["prefill_gemm_q6K"] = gemm_q6k_bench(be, torch, np)
+        extras["prefill_layer_mul_mats"] = prefill_layer_bench(be, torch, np)
         extras["moe_mxfp4"] = moe_bench(be, torch, np)
         extras["flash_attn_f16kv"] = fa_bench(be, torch, np)
     cpu = None if args.no_cpu else cpu_baseline()

@@ -338,8 +338,8 @@ ghip_status run_gemm_q6k(ghip_context *ctx, const MulMatPlan &p, const void *w, 
     uint16_t *codes = (uint16_t *)layout_ws;
     float *dT = (float *)((uint8_t *)layout_ws + codes_b);
     uint8_t *rep = (uint8_t *)layout_ws + codes_b + dt_b;
-    const int64_t rthreads = p.N * nbk * 64;
-    ghip_status st = ctx->launch("ghip_q6K_repack", dim3((unsigned)((rthreads + 255) / 256)), dim3(256), 0, s,
+    const int64_t nblk = p.N * nbk;  // four blocks per workgroup
+    ghip_status st = ctx->launch("ghip_q6K_repack", dim3((unsigned)((nblk + 3) / 4)), dim3(256), 0, s,
                                  (const uint8_t *)w, (int64_t)p.w_row_bytes, (int)p.N, (int)nbk, rep);
     if (st != GHIP_STATUS_SUCCESS) return st;
     st = ctx->launch("ghip_gemm_act_layout_f16", dim3((unsigned)((p.M * nbk + 3) / 4)), dim3(256), 0, s, act,

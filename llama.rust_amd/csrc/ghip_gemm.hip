@@ -311,33 +311,44 @@ GEMM_KERNELS(ghip_gemm_q4_K_m64, 64, 256, 2)
 //   q[256] (6-bit values 0..63 in element order) | sc[16] int8 | d f32 | pad.
 constexpr int Q6R_BYTES = 288;
 
-// one thread per 4 elements of a block (64 threads per block)
+// one 64-lane group per block: the block's bytes arrive with coalesced dword
+// loads from its 4-byte-aligned base into LDS, then lane u writes elements
+// 4u .. 4u+3 (and lanes 0..7 the scales, d and padding)
 extern "C" __global__ void __launch_bounds__(256)
 ghip_q6K_repack(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb, uint8_t *__restrict__ out) {
-    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t blk = t >> 6;  // row * nb + block
-    if (blk >= (int64_t)N * nb) return;
-    const int u = (int)(t & 63), e4 = 4 * u;
-    const int64_t row = blk / nb;
-    const int b = (int)(blk - row * nb);
+    __shared__ uint32_t stage[4][56];  // 224 bytes per group
+    const int grp = threadIdx.x >> 6, u = threadIdx.x & 63;
+    const int64_t blk = (int64_t)blockIdx.x * 4 + grp;  // row * nb + block
+    const bool live = blk < (int64_t)N * nb;
+    const int64_t row = live ? blk / nb : 0;
+    const int b = live ? (int)(blk - row * nb) : 0;
     const uint8_t *src = W + row * w_row_bytes + (int64_t)b * Q6K_BYTES;
+    const uintptr_t base4 = (uintptr_t)src & ~(uintptr_t)3;
+    const int sh = (int)((uintptr_t)src - base4);  // 0 or 2
+    const uintptr_t end = (uintptr_t)(W + (int64_t)(N - 1) * w_row_bytes + (int64_t)nb * Q6K_BYTES);
+    // dwords 0..53 cover the block's 210 bytes plus the shift; none past the matrix
+    if (live && u < 54 && base4 + 4 * u + 4 <= end)
+        stage[grp][u] = *reinterpret_cast<const uint32_t *>(base4 + 4 * u);
+    __syncthreads();
+    if (!live) return;
+    const uint8_t *blkb = reinterpret_cast<const uint8_t *>(stage[grp]) + sh;
     uint8_t *dst = out + blk * Q6R_BYTES;
     // element i of half j = i / 128, l = i % 128: ql[64j + l % 64] nibble l / 64,
     // qh[32j + l % 32] bits 2 * (l / 32) (dequantize_row_q6_K)
-    const int j = e4 >> 7, l = e4 & 127;
-    const uint8_t *ql = src + 64 * j + (l & 63);
-    const uint8_t *qh = src + 128 + 32 * j + (l & 31);
+    const int e4 = 4 * u, j = e4 >> 7, l = e4 & 127;
+    const uint8_t *ql = blkb + 64 * j + (l & 63);
+    const uint8_t *qh = blkb + 128 + 32 * j + (l & 31);
     const int nsh = 4 * (l >> 6), hsh = 2 * (l >> 5);
     uint32_t v = 0;
 #pragma unroll
     for (int k = 0; k < 4; k++) v |= (uint32_t)(((ql[k] >> nsh) & 15) | (((qh[k] >> hsh) & 3) << 4)) << (8 * k);
     *reinterpret_cast<uint32_t *>(dst + e4) = v;
     if (u < 4) {
-        const uint8_t *sc = src + 192 + 4 * u;
+        const uint8_t *sc = blkb + 192 + 4 * u;
         *reinterpret_cast<uint32_t *>(dst + 256 + 4 * u) =
             (uint32_t)sc[0] | ((uint32_t)sc[1] << 8) | ((uint32_t)sc[2] << 16) | ((uint32_t)sc[3] << 24);
     } else if (u == 4) {
-        *reinterpret_cast<float *>(dst + 272) = h2f(ld2(src + 208));
+        *reinterpret_cast<float *>(dst + 272) = h2f((uint32_t)blkb[208] | ((uint32_t)blkb[209] << 8));
     } else if (u < 8) {
         *reinterpret_cast<uint32_t *>(dst + 276 + 4 * (u - 5)) = 0u;
     }

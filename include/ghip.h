@@ -186,7 +186,11 @@ typedef struct ghip_node {
  * or gate/up at decode -- run as one launch of up to four matrices, provided
  * no node of the group reads or overlaps another's dst (and, for Q4_K at 4+
  * rows, N % 8 == 0 holds for all or none: it selects the activation
- * quantizer); their results are bit-identical to the single-op calls.  Returns the first failing node's status (the nodes before
+ * quantizer); their results are bit-identical to the single-op calls.
+ * Q4_K siblings with prefill batches (the GEMM's range, 16+ rows) likewise
+ * run as one GEMM launch over all their tiles after one activation
+ * quantization; results match the single-op calls within the MUL_MAT
+ * tolerance (a small matrix alone sums split-K slices in order).  Returns the first failing node's status (the nodes before
  * it have been enqueued); ghip_last_error names the failure.
  * GHIP_GRAPH_FUSE=0 in the environment turns the grouping off. */
 ghip_status ghip_graph_compute(ghip_context *ctx, const ghip_node *nodes, int32_t n_nodes, void *stream);

@@ -635,10 +635,11 @@ bool multi_candidate(const ghip_node &n) {
     if (n.op != GHIP_OP_MUL_MAT || !n.src[0] || !n.src[1] || !n.dst) return false;
     const ghip_tensor *a = n.src[0], *b = n.src[1];
     if (a->type != GHIP_TYPE_Q4_K && a->type != GHIP_TYPE_Q5_K && a->type != GHIP_TYPE_Q6_K) return false;
-    if (b->type != GHIP_TYPE_F32 || b->ne[1] < 1 || b->ne[1] > (a->type == GHIP_TYPE_Q6_K ? 1 : 8) ||
-        b->ne[2] != 1 || b->ne[3] != 1)
+    if (b->type != GHIP_TYPE_F32 || b->ne[1] < 1 || b->ne[2] != 1 || b->ne[3] != 1) return false;
+    if (b->ne[1] > (a->type == GHIP_TYPE_Q6_K ? 1 : 8) && b->ne[1] < env_int("GHIP_GEMM_MIN_ROWS", 16))
         return false;
-    if (b->ne[1] >= env_int("GHIP_GEMM_MIN_ROWS", 16)) return false;  // the prefill GEMM's range
+    if (b->ne[1] >= env_int("GHIP_GEMM_MIN_ROWS", 16))  // the prefill GEMM's range: Q4_K, 64-token tiles
+        return a->type == GHIP_TYPE_Q4_K && gemm_bm() == 64 && b->ne[1] <= INT32_MAX;
     if (a->ne[2] != 1 || a->ne[3] != 1) return false;
     return env_int("GHIP_GEMV_RB", 2) == 2 && env_int("GHIP_GEMV_NG", 2) == 2;
 }
@@ -659,6 +660,68 @@ bool joins_group(const ghip_node *nodes, int i, int j) {
             return false;
     }
     return true;
+}
+
+// Host mirror of GemmMulti in ghip_gemm.hip (kernel argument by value).
+struct GemmMulti {
+    const uint8_t *W[4];
+    float *dst[4];
+    int64_t ldd[4];
+    int N[4];
+    int t0[4];
+    int n, total;
+};
+
+// 2..4 sibling Q4_K MUL_MATs with prefill-sized batches: one Q8_K
+// quantization, one GEMM layout, one GEMM launch over all matrices' tiles
+ghip_status mul_mat_multi_gemm(ghip_context *ctx, const ghip_node *nodes, int n, hipStream_t s) {
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    MulMatPlan p[4];
+    ghip_status st;
+    for (int i = 0; i < n; i++) {
+        if (!plan_mul_mat(ctx, nodes[i].src[0], nodes[i].src[1], nodes[i].dst, p[i], st)) return st;
+        if (p[i].M != p[0].M || p[i].wtype != GHIP_TYPE_Q4_K || !use_gemm(p[i]) || p[i].act_pre)
+            return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "graph_compute: internal: node not groupable");
+    }
+    if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    const MulMatPlan &p0 = p[0];
+    const int64_t Mpad = (p0.M + 127) / 128 * 128, K = p0.K, nbk = p0.K / 256;
+    const size_t act_bytes = ((size_t)(p0.M * p0.act_row_bytes) + 255) & ~(size_t)255;
+    const size_t lay_bytes = (size_t)Mpad * K + (size_t)nbk * Mpad * 32 + (size_t)nbk * Mpad * 4;
+    void *ws = nullptr;
+    st = ctx->workspace(act_bytes + lay_bytes, s, &ws);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    st = quantize_act(ctx, p0, nodes[0].src[1], ws, s);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    int8_t *codes = (int8_t *)ws + act_bytes;
+    uint16_t *bsT = (uint16_t *)(codes + Mpad * K);
+    float *dT = (float *)(bsT + nbk * Mpad * 16);
+    st = ctx->launch("ghip_gemm_act_layout", dim3((unsigned)((p0.M * nbk + 3) / 4)), dim3(256), 0, s,
+                     (const uint8_t *)ws, (int64_t)p0.act_row_bytes, (int)p0.M, (int)Mpad, (int)nbk, codes, bsT, dT);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    GemmMulti g{};
+    const int tiles_m = (int)((p0.M + 63) / 64);
+    int t = 0;
+    for (int i = 0; i < n; i++) {
+        g.W[i] = (const uint8_t *)nodes[i].src[0]->data;
+        g.dst[i] = (float *)nodes[i].dst->data;
+        g.ldd[i] = (int64_t)nodes[i].dst->nb[1] / 4;
+        g.N[i] = (int)p[i].N;
+        g.t0[i] = t;
+        t += tiles_m * (int)((p[i].N + 127) / 128);
+    }
+    for (int i = n; i < 4; i++) {
+        g.W[i] = g.W[0];
+        g.dst[i] = g.dst[0];
+        g.ldd[i] = g.ldd[0];
+        g.N[i] = g.N[0];
+        g.t0[i] = t;
+    }
+    g.n = n;
+    g.total = t;
+    return ctx->launch("ghip_gemm_q4_K_m64_multi", dim3((unsigned)t), dim3(256), kGemmSmem64, s, g,
+                       (int64_t)p0.w_row_bytes, (int)nbk, (const int8_t *)codes, (const uint16_t *)bsT,
+                       (const float *)dT, (int)p0.M, (int)Mpad);
 }
 
 // 2..4 sibling MUL_MATs (joins_group holds) as one multi-matrix GEMV launch
@@ -933,7 +996,9 @@ ghip_status ghip_graph_compute(ghip_context *ctx, const ghip_node *nodes, int32_
             if (fuse && multi_candidate(nd))
                 while (next < n_nodes && next - i < 4 && joins_group(nodes, i, next)) next++;
             if (next - i >= 2)
-                st = mul_mat_multi(ctx, nodes + i, next - i, (hipStream_t)stream);
+                st = nd.src[1]->ne[1] >= env_int("GHIP_GEMM_MIN_ROWS", 16)
+                         ? mul_mat_multi_gemm(ctx, nodes + i, next - i, (hipStream_t)stream)
+                         : mul_mat_multi(ctx, nodes + i, next - i, (hipStream_t)stream);
             else
                 st = ghip_mul_mat(ctx, nd.src[0], nd.src[1], nd.dst, stream);
             break;

@@ -94,7 +94,7 @@ __device__ __forceinline__ void gemm_q4K_impl(const uint8_t *__restrict__ W, int
                                                const int8_t *__restrict__ codes, const _Float16 *__restrict__ bsT,
                                                const float *__restrict__ dT, int M, int Mpad,
                                                float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub,
-                                               int nbs, int64_t zstride) {
+                                               int nbs, int64_t zstride, int tile = -1) {
     constexpr int BN = g3::BN, NW = BM / 16, TPW = BM / 64;
     constexpr int WRI = 16 / NW;                    // wraw pieces per wavefront
     constexpr int DAW = BM == 128 ? 6 : 1;          // wavefront that loads da
@@ -113,8 +113,13 @@ __device__ __forceinline__ void gemm_q4K_impl(const uint8_t *__restrict__ W, int
 
     const int n_tiles_m = (M + BM - 1) / BM, n_tiles_n = (N + BN - 1) / BN;
     const int total = n_tiles_m * n_tiles_n;
-    int id = blockIdx.x;
-    if (total % 8 == 0) id = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+    // tile: this workgroup's tile of the matrix, tokens fastest (-1: from
+    // blockIdx.x, with consecutive ids on one XCD)
+    int id = tile;
+    if (id < 0) {
+        id = blockIdx.x;
+        if (total % 8 == 0) id = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+    }
     const int m0 = (id % n_tiles_m) * BM;
     const int n0 = (id / n_tiles_m) * BN;
 
@@ -291,6 +296,32 @@ __device__ __forceinline__ void gemm_q4K_impl(const uint8_t *__restrict__ W, int
     }
 GEMM_KERNELS(ghip_gemm_q4_K, 128, 512, 1)
 GEMM_KERNELS(ghip_gemm_q4_K_m64, 64, 256, 2)
+// Sibling MUL_MATs in one launch (ghip_graph_compute): up to four Q4_K
+// matrices of one K that read the same activation rows, so the Q8_K rows and
+// their GEMM layout are made once.  Tiles [t0[i], t0[i+1]) belong to matrix i;
+// the XCD remap runs over all of them.  Passed by value; the host mirror in
+// ghip.cpp has the same layout.
+struct GemmMulti {
+    const uint8_t *W[4];
+    float *dst[4];
+    int64_t ldd[4];
+    int N[4];
+    int t0[4];
+    int n, total;
+};
+extern "C" __global__ void __launch_bounds__(256, 2)
+    ghip_gemm_q4_K_m64_multi(GemmMulti g, int64_t w_row_bytes, int nb, const int8_t *__restrict__ codes,
+                             const _Float16 *__restrict__ bsT, const float *__restrict__ dT, int M, int Mpad) {
+    int id = blockIdx.x;
+    if (g.total % 8 == 0) id = (blockIdx.x & 7) * (g.total >> 3) + (blockIdx.x >> 3);
+    int i = 0;
+#pragma unroll
+    for (int k = 1; k < 4; k++)
+        if (k < g.n && id >= g.t0[k]) i = k;
+    gemm_q4K_impl<64, false>(g.W[i], w_row_bytes, g.N[i], nb, codes, bsT, dT, M, Mpad, g.dst[i], g.ldd[i], nullptr,
+                             nb, 0, id - g.t0[i]);
+}
+
 // ---------------------------------------------------------------- Q6_K prefill
 // Many activation rows with Q6_K weights (vec_dot_q6_K_q8_K, vec_dot.rs:982-1040,
 // per super-block  is = sum_s sc_s * sum_16 (q6 - 32) * q8,  out += (d * is) * d8).

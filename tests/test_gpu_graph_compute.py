@@ -84,6 +84,32 @@ def test_group_ragged_vs_oracle(be, ty, k, ns, m):
         assert torch.equal(o, single)
 
 
+@pytest.mark.parametrize("m,k,ns", [(16, 1024, (512, 128, 128)), (100, 768, (200, 64, 72)), (512, 1024, (256, 256))])
+def test_prefill_group_vs_oracle(be, m, k, ns):
+    """Q4_K siblings at prefill batches run as one GEMM launch (one Q8_K
+    quantization and layout for all): every member against the oracle at the
+    MUL_MAT bar, and against its single-op call within the same bar (alone,
+    a small matrix takes the split-K route, whose ordered slice sums round
+    differently)."""
+    import ghip
+    rng = np.random.default_rng(11)
+    wf = [(rng.standard_normal((n, k)) * 0.02).astype(np.float32) for n in ns]
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    wq = [O.quantize(12, w).reshape(w.shape[0], -1) for w in wf]
+    wd = [torch.from_numpy(q).cuda() for q in wq]
+    xd = torch.from_numpy(x).cuda()
+    outs = [torch.full((m, n), float("nan"), device="cuda") for n in ns]
+    be.graph_compute([ghip.mul_mat_node(w, 12, k, xd, o) for w, o in zip(wd, outs)])
+    torch.cuda.synchronize()
+    for q, w, n, o in zip(wq, wd, ns, outs):
+        ref, _, _ = O.mul_mat(12, q, k, n, x, m)
+        got = o.cpu().numpy()
+        assert np.isfinite(got).all()
+        assert rel_err(got, ref) <= TOL
+        single = be.mul_mat(w, 12, k, xd).cpu().numpy()
+        assert rel_err(got, single) <= TOL
+
+
 def test_dependent_and_aliased_nodes_keep_order(be):
     """a node reading its predecessor's dst, and two nodes writing the same
     dst, are not grouped: the graph computes them in order"""

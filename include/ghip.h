@@ -182,8 +182,9 @@ typedef struct ghip_node {
  * -> cpu_backend_graph_compute backend.rs:2169 -> compute::graph_compute
  * compute.rs:307).  Consecutive MUL_MAT nodes with 1-8 F32 activation rows
  * (Q6_K: one) that read the same src1 (same data and geometry) with the same
- * K-quant weight type (Q4_K, Q5_K, Q6_K) and the same K -- a layer's q/k/v
- * or gate/up at decode -- run as one launch of up to four matrices, provided
+ * weight type (Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K) and the same K -- a
+ * layer's q/k/v or gate/up at decode -- run as one launch of up to four
+ * matrices (Q4_0 / Q5_0 / Q8_0 after one Q8_0 quantization), provided
  * no node of the group reads or overlaps another's dst (and, for Q4_K at 4+
  * rows, N % 8 == 0 holds for all or none: it selects the activation
  * quantizer); their results are bit-identical to the single-op calls.

@@ -634,6 +634,10 @@ bool same_view(const ghip_tensor *a, const ghip_tensor *b) {
 bool multi_candidate(const ghip_node &n) {
     if (n.op != GHIP_OP_MUL_MAT || !n.src[0] || !n.src[1] || !n.dst) return false;
     const ghip_tensor *a = n.src[0], *b = n.src[1];
+    // Q4_0 / Q5_0 / Q8_0: 1-8 F32 activation rows (the decode kernels' range)
+    if (a->type == GHIP_TYPE_Q4_0 || a->type == GHIP_TYPE_Q5_0 || a->type == GHIP_TYPE_Q8_0)
+        return b->type == GHIP_TYPE_F32 && b->ne[1] >= 1 && b->ne[1] <= 8 && b->ne[2] == 1 && b->ne[3] == 1 &&
+               a->ne[2] == 1 && a->ne[3] == 1;
     if (a->type != GHIP_TYPE_Q4_K && a->type != GHIP_TYPE_Q5_K && a->type != GHIP_TYPE_Q6_K) return false;
     if (b->type != GHIP_TYPE_F32 || b->ne[1] < 1 || b->ne[2] != 1 || b->ne[3] != 1) return false;
     if (b->ne[1] > (a->type == GHIP_TYPE_Q6_K ? 1 : 8) && b->ne[1] < env_int("GHIP_GEMM_MIN_ROWS", 16))
@@ -731,11 +735,39 @@ ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipS
     ghip_status st;
     for (int i = 0; i < n; i++) {
         if (!plan_mul_mat(ctx, nodes[i].src[0], nodes[i].src[1], nodes[i].dst, p[i], st)) return st;
-        if (p[i].M != p[0].M || p[i].M > 8 || !gemv_v2(p[i]) || p[i].act_pre)
+        if (p[i].M != p[0].M || p[i].M > 8 || !(gemv_v2(p[i]) || gemv_pair(p[i].wtype)) || p[i].act_pre)
             return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "graph_compute: internal: node not groupable");
     }
     if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
     const MulMatPlan &p0 = p[0];
+    if (gemv_pair(p0.wtype)) {
+        // Q8_0 rows once for the group, then 8 weight rows per workgroup
+        const size_t act_bytes = ((size_t)(p0.M * p0.act_row_bytes) + 255) & ~(size_t)255;
+        void *ws = nullptr;
+        st = ctx->workspace(act_bytes, s, &ws);
+        if (st != GHIP_STATUS_SUCCESS) return st;
+        st = quantize_act(ctx, p0, nodes[0].src[1], ws, s);
+        if (st != GHIP_STATUS_SUCCESS) return st;
+        const int wk = (int)(((p0.nb + 1) / 2 + 63) / 64);
+        if (wk > 8) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: ne00 = %lld too large for the decode kernel", (long long)p0.K);
+        GemvMulti g{};
+        int wgs = 0;
+        for (int i = 0; i < 4; i++) {
+            const int j = i < n ? i : 0;
+            g.W[i] = (const uint8_t *)nodes[j].src[0]->data;
+            g.dst[i] = (float *)nodes[j].dst->data;
+            g.ldd[i] = (int64_t)nodes[j].dst->nb[1] / 4;
+            g.rows[i] = i < n ? (int)p[i].N : 0;
+            g.wg0[i] = wgs;
+            if (i < n) wgs += (int)((p[i].N + 7) / 8);
+        }
+        g.n = n;
+        const int nc = (int)p0.M;
+        const int NC = nc == 1 ? 1 : nc == 2 ? 2 : nc <= 4 ? 4 : 8;
+        return ctx->launch(std::string(gemv_base(p0.wtype)) + "_c" + std::to_string(NC) + "_multi", dim3((unsigned)wgs),
+                           dim3(64 * wk), 0, s, g, (int64_t)p0.w_row_bytes, (int)p0.nb, (const uint8_t *)ws,
+                           (int64_t)p0.act_row_bytes, nc);
+    }
     const int waves_k = (int)((p0.nb + 15) / 16);
     if (waves_k > 8) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: ne00 = %lld too large for the decode kernel", (long long)p0.K);
     // 8 row teams per workgroup: measured on q/k/v (4096 + 1024 + 1024 rows)

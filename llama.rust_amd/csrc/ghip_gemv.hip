@@ -553,7 +553,7 @@ template <int NC, bool SUBSUMS>
 __device__ __forceinline__ void gemv_q6K_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
                                               int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
                                               int ncols, float *__restrict__ dst, int64_t ldd,
-                                              int32_t *__restrict__ sub) {
+                                              int32_t *__restrict__ sub, int wg = -1) {
     __shared__ float red[RB * 8 * NC];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int b = 8 * w + (lane >> 3), j = lane & 7;
@@ -561,7 +561,7 @@ __device__ __forceinline__ void gemv_q6K_impl(const uint8_t *__restrict__ W, int
     const bool valid = b < nb;
     const int ea = 128 * jj + 32 * p + 16 * t;  // first element of the low-nibble stream
     const int si = 8 * jj + 2 * p + t;          // its scale / bsum index; high stream is si+4
-    const int r0 = blockIdx.x * RB;
+    const int r0 = (wg < 0 ? (int)blockIdx.x : wg) * RB;  // wg: index within the matrix
     const int nr = min(RB, rows - r0);
 
     uint4 ql[RB], qh[RB];
@@ -680,13 +680,13 @@ template <int NC, bool SUBSUMS, bool FUSEQ>
 __device__ __forceinline__ void gemv_q4_0_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
                                                int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
                                                int ncols, float *__restrict__ dst, int64_t ldd,
-                                               int32_t *__restrict__ sub) {
+                                               int32_t *__restrict__ sub, int wg = -1) {
     __shared__ float red[RB * 8 * NC];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int pr = 64 * w + lane;  // pair index
     const int b0 = 2 * pr, b1 = 2 * pr + 1;
     const bool v0 = b0 < nb, v1 = b1 < nb;
-    const int r0 = blockIdx.x * RB;
+    const int r0 = (wg < 0 ? (int)blockIdx.x : wg) * RB;  // wg: index within the matrix
     const int nr = min(RB, rows - r0);
 
     uint4 wa[RB], wbq[RB];
@@ -833,7 +833,7 @@ template <int WT, int NC, bool SUBSUMS, bool FUSEQ>
 __device__ __forceinline__ void gemv_pair_q8_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
                                                   int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
                                                   int ncols, float *__restrict__ dst, int64_t ldd,
-                                                  int32_t *__restrict__ sub) {
+                                                  int32_t *__restrict__ sub, int wg = -1) {
     constexpr int PB = WT == WT_Q8_0 ? 68 : 44;  // bytes per block pair
     constexpr int ND = PB / 4;                  // dwords per block pair
     __shared__ float red[RB * 8 * NC];
@@ -841,7 +841,7 @@ __device__ __forceinline__ void gemv_pair_q8_impl(const uint8_t *__restrict__ W,
     const int pr = 64 * w + lane;  // pair index
     const int b0 = 2 * pr, b1 = 2 * pr + 1;
     const bool v0 = b0 < nb, v1 = b1 < nb;
-    const int r0 = blockIdx.x * RB;
+    const int r0 = (wg < 0 ? (int)blockIdx.x : wg) * RB;  // wg: index within the matrix
     const int nr = min(RB, rows - r0);
 
     uint32_t wq[RB][ND];
@@ -947,14 +947,18 @@ __device__ __forceinline__ void gemv_pair_q8_impl(const uint8_t *__restrict__ W,
 template <int NC, bool SUBSUMS, bool FUSEQ>
 __device__ __forceinline__ void gemv_q5_0_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb,
                                                const uint8_t *__restrict__ act, int64_t act_row_bytes, int ncols,
-                                               float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
-    gemv_pair_q8_impl<WT_Q5_0, NC, SUBSUMS, FUSEQ>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub);
+                                               float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub,
+                                               int wg = -1) {
+    gemv_pair_q8_impl<WT_Q5_0, NC, SUBSUMS, FUSEQ>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub,
+                                                   wg);
 }
 template <int NC, bool SUBSUMS, bool FUSEQ>
 __device__ __forceinline__ void gemv_q8_0_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb,
                                                const uint8_t *__restrict__ act, int64_t act_row_bytes, int ncols,
-                                               float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
-    gemv_pair_q8_impl<WT_Q8_0, NC, SUBSUMS, FUSEQ>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub);
+                                               float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub,
+                                               int wg = -1) {
+    gemv_pair_q8_impl<WT_Q8_0, NC, SUBSUMS, FUSEQ>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub,
+                                                   wg);
 }
 
 #define GEMV_ARGS                                                                                     \
@@ -1068,3 +1072,21 @@ GEMV_MULTI(q4_K, 4, gemv_q4K_impl, false) GEMV_MULTI(q4_K, 8, gemv_q4K_impl, fal
 GEMV_MULTI(q5_K, 1, gemv_q4K_impl, true) GEMV_MULTI(q5_K, 2, gemv_q4K_impl, true)
 GEMV_MULTI(q5_K, 4, gemv_q4K_impl, true) GEMV_MULTI(q5_K, 8, gemv_q4K_impl, true)
 GEMV_MULTI(q6_K_v2, 1, gemv_q6K_v2_impl)
+
+// Q4_0 / Q5_0 / Q8_0 siblings: ready Q8_0 rows (one quantize launch for the
+// group), 8 weight rows per workgroup
+#define GEMV_PAIR_MULTI(TN, NC, IMPL)                                                                            \
+    extern "C" __global__ void __launch_bounds__(512)                                                            \
+        ghip_gemv_##TN##_c##NC##_multi(GemvMulti g, int64_t w_row_bytes, int nb, const uint8_t *__restrict__ act, \
+                                       int64_t act_row_bytes, int ncols) {                                       \
+        const int bx = blockIdx.x;                                                                               \
+        int i = 0;                                                                                               \
+        _Pragma("unroll") for (int k = 1; k < 4; k++) if (k < g.n && bx >= g.wg0[k]) i = k;                     \
+        IMPL<NC, false, false>(g.W[i], w_row_bytes, g.rows[i], nb, act, act_row_bytes, ncols, g.dst[i], g.ldd[i], \
+                               nullptr, bx - g.wg0[i]);                                                          \
+    }
+#define GEMV_PAIR_MULTI_ALL(TN, IMPL) \
+    GEMV_PAIR_MULTI(TN, 1, IMPL) GEMV_PAIR_MULTI(TN, 2, IMPL) GEMV_PAIR_MULTI(TN, 4, IMPL) GEMV_PAIR_MULTI(TN, 8, IMPL)
+GEMV_PAIR_MULTI_ALL(q4_0, gemv_q4_0_impl)
+GEMV_PAIR_MULTI_ALL(q5_0, gemv_q5_0_impl)
+GEMV_PAIR_MULTI_ALL(q8_0, gemv_q8_0_impl)

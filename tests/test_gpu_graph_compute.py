@@ -36,11 +36,12 @@ def weights(be, ty, n, k, seed):
     return be.quantize(torch.randn((n, k), device="cuda", generator=g) * 0.02, ty)
 
 
-@pytest.mark.parametrize("ty,m", [(12, 1), (12, 2), (12, 4), (12, 5), (12, 8), (14, 1), (14, 2)])
+@pytest.mark.parametrize("ty,m", [(12, 1), (12, 2), (12, 4), (12, 5), (12, 8), (14, 1), (14, 2), (2, 1), (2, 2), (2, 4)])
 def test_decode_layer_groups_bit_identical(be, ty, m):
     """q/k/v (4096 -> 4096, 1024, 1024) and gate/up (4096 -> 14336) as two
-    groups, o as a single node, at m activation rows (Q4_K, Q6_K; Q5_K groups
-    are in the ragged test): every output equals ghip_mul_mat's."""
+    groups, o as a single node, at m activation rows (Q4_K, Q6_K, Q4_0; Q5_K,
+    Q5_0 and Q8_0 groups are in the ragged test): every output equals
+    ghip_mul_mat's."""
     import ghip
     k = 4096
     shapes = [("q", 4096), ("k", 1024), ("v", 1024), ("o", 4096), ("gate", 14336), ("up", 14336)]
@@ -60,7 +61,9 @@ def test_decode_layer_groups_bit_identical(be, ty, m):
 
 @pytest.mark.parametrize("ty,k,ns,m", [(12, 1024, (96, 40, 8), 1), (13, 768, (33, 64), 1), (14, 512, (17, 31, 64, 5), 1),
                                        (12, 512, (96, 40, 8), 3), (13, 512, (24, 40, 8), 6),
-                                       (12, 512, (36, 40, 64, 20), 4)])  # N % 8 differs: two groups
+                                       (12, 512, (36, 40, 64, 20), 4),  # N % 8 differs: two groups
+                                       (2, 1024, (64, 40, 8), 1), (2, 512, (64, 40, 8), 3), (6, 512, (48, 16), 3),
+                                       (8, 768, (24, 40, 8, 16), 5), (6, 1024, (100, 36), 1)])
 def test_group_ragged_vs_oracle(be, ty, k, ns, m):
     """groups whose matrices end inside a workgroup's rows, at m activation
     rows, against the oracle"""

@@ -329,6 +329,30 @@ def prefill_layer_bench(be, torch, np, tokens=512):
     return {"tokens": tokens, "us": round(us, 1), "TOPS": round(ops / us / 1e6, 1), "tokens_per_s": round(tokens / us * 1e6, 1)}
 
 
+def q4_0_layer_bench(be, torch, np, copies=4):
+    """The decode layer's 7 MUL_MAT nodes with Q4_0 weights (the Q8_0
+    activation path, config 1's type) at batch 1: one ghip_graph_compute call
+    against 7 ghip_mul_mat calls, both captured in HIP graphs."""
+    import ghip
+    g = torch.Generator(device="cuda").manual_seed(9)
+    sets = [[be.quantize(torch.randn((n, k), device="cuda", generator=g) * 0.02, ghip.Q4_0) for _, _, k, n in LAYER]
+            for _ in range(copies)]
+    xs = {nm: torch.randn((1, k), device="cuda", generator=g) for nm, k in INPUT_K.items()}
+    outs = {name: torch.empty((1, n), dtype=torch.float32, device="cuda") for name, _, _, n in LAYER}
+    nodes = [[ghip.mul_mat_node(w, ghip.Q4_0, k, xs[LAYER_INPUT[name]], outs[name])
+              for (name, _, k, n), w in zip(LAYER, ws)] for ws in sets]
+
+    def per_op(i):
+        for (name, _, k, n), w in zip(LAYER, sets[i % copies]):
+            be.mul_mat(w, ghip.Q4_0, k, xs[LAYER_INPUT[name]], out=outs[name])
+    us_g = graph_time_us(torch, lambda i: be.graph_compute(nodes[i % copies]), 8)
+    us_op = graph_time_us(torch, per_op, 8)
+    wbytes = sum(ghip.row_size(ghip.Q4_0, k) * n + 4 * (k + n) for _, _, k, n in LAYER)
+    log(f"Q4_0 decode layer: graph_compute {us_g:.1f} us ({wbytes / us_g / 1e3:.0f} GB/s), per-op calls {us_op:.1f} us")
+    del sets, xs, outs, nodes
+    return {"us_graph_compute": round(us_g, 1), "GB/s": round(wbytes / us_g / 1e3, 1), "us_per_op_calls": round(us_op, 1)}
+
+
 def moe_bench(be, torch, np):
     """Config 4: gpt-oss MoE MUL_MAT_ID, 32 MXFP4 experts, 256 tokens, top-4."""
     import ghip
@@ -468,6 +492,7 @@ def main():
         extras["prefill_gemm_q4K"] = gemm_bench(be, torch, np)
         extras["prefill_gemm_q6K"] = gemm_q6k_bench(be, torch, np)
         extras["prefill_layer_mul_mats"] = prefill_layer_bench(be, torch, np)
+        extras["decode_layer_q4_0"] = q4_0_layer_bench(be, torch, np)
         extras["moe_mxfp4"] = moe_bench(be, torch, np)
         extras["flash_attn_f16kv"] = fa_bench(be, torch, np)
     cpu = None if args.no_cpu else cpu_baseline()

@@ -17,7 +17,18 @@
  *    crates/ggml/src/backend.rs:54-62); ghip_last_error() explains the last
  *    failure of a context.  Nothing falls back to the CPU: an unsupported
  *    shape or type returns GHIP_STATUS_BACKEND_ERROR.
- *  - A context may be used from any host thread, one thread at a time.
+ *  - A context may be used from any host thread; calls are serialised.
+ *  - Scratch memory (quantized activations, GEMM layouts, split partials,
+ *    routing tables) comes from one workspace per context.  By default the
+ *    library owns it and grows it on demand with hipMalloc; a call that would
+ *    grow it while its stream is being captured fails with
+ *    GHIP_STATUS_ALLOC_FAILED instead (run the call once before capturing, or
+ *    give a workspace with ghip_set_workspace).  Outgrown buffers are kept
+ *    until ghip_free, so graphs captured earlier stay valid.  A call on a
+ *    different stream than the previous call first waits for the previous
+ *    stream (an event), so two streams never use the workspace at once; when
+ *    either stream is being captured that wait cannot be recorded and the
+ *    caller orders the streams.
  */
 #ifndef GHIP_H
 #define GHIP_H
@@ -195,6 +206,23 @@ typedef struct ghip_node {
  * it have been enqueued); ghip_last_error names the failure.
  * GHIP_GRAPH_FUSE=0 in the environment turns the grouping off. */
 ghip_status ghip_graph_compute(ghip_context *ctx, const ghip_node *nodes, int32_t n_nodes, void *stream);
+
+/* Give the context caller-owned device memory as its workspace (no reference
+ * counterpart: the reference's CPU ops allocate their quantized-activation
+ * buffer inside each op, e.g. the wdata of forward_mul_mat, compute.rs:1499-1530).  From then on the context never
+ * allocates; a call that needs more than `bytes` fails with
+ * GHIP_STATUS_ALLOC_FAILED.  ptr = NULL, bytes = 0 returns to the owned
+ * workspace.  The memory must stay valid while queued work or captured graphs
+ * use it. */
+ghip_status ghip_set_workspace(ghip_context *ctx, void *ptr, size_t bytes);
+
+/* Workspace bytes one op needs (same operands as ghip_supports_op; dst is
+ * required), pure host arithmetic with no reference counterpart (there the
+ * size is implicit in each op's wdata, compute.rs:1499-1530).  For a node list, the maximum over its nodes is
+ * enough for ghip_graph_compute (grouped launches need no more than their
+ * members alone). */
+ghip_status ghip_workspace_size(int op, const ghip_tensor *dst, const ghip_tensor *const *srcs, int n_srcs,
+                                size_t *bytes);
 
 /* Quantize nrows rows of n_per_row f32 values (device pointer src) into
  * GGUF blocks of `type` (Q4_0, Q4_K, Q6_K, MXFP4) at the device pointer dst,

@@ -6,6 +6,7 @@
 
 #include <dlfcn.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -63,8 +64,23 @@ struct ghip_context {
     std::vector<hipModule_t> modules;
     std::unordered_map<std::string, hipFunction_t> fns;
     std::string err;
-    void *ws = nullptr;  // device workspace (quantized activations)
+    // Workspace (quantized activations, GEMM layouts, split partials, routing
+    // tables).  Three sources, first match wins:
+    //  - call_ws: the fixed scratch of a no-allocation entry point, for one call;
+    //  - user_ws: caller memory given with ghip_set_workspace (never grown);
+    //  - ws: owned by the library, grown on demand outside stream capture.
+    void *ws = nullptr;
     size_t ws_size = 0;
+    std::vector<void *> retired;  // outgrown owned workspaces: in-flight work or captured graphs may still read them
+    void *user_ws = nullptr;
+    size_t user_ws_size = 0;
+    void *call_ws = nullptr;
+    size_t call_ws_size = 0;
+    // the stream of the previous call: a call on another stream first waits
+    // for it, so the two never share the workspace concurrently
+    hipStream_t last_stream = nullptr;
+    bool have_last = false;
+    hipEvent_t order_ev = nullptr;
     std::mutex mu;
 
     ghip_status fail(ghip_status st, const char *fmt, ...) {
@@ -91,21 +107,60 @@ struct ghip_context {
         return nullptr;
     }
 
-    // grow-only workspace; waits for in-flight work before releasing the old one
-    ghip_status workspace(size_t bytes, hipStream_t s, void **out) {
-        if (bytes > ws_size) {
-            if (ws) {
-                hipStreamSynchronize(s);
-                hipDeviceSynchronize();
-                hipFree(ws);
-                ws = nullptr;
-                ws_size = 0;
+    static bool capturing(hipStream_t s) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+            (void)hipGetLastError();
+            return false;
+        }
+        return cs != hipStreamCaptureStatusNone;
+    }
+
+    // Called at the start of every op on stream s (device current, lock held).
+    ghip_status begin(hipStream_t s) {
+        if (have_last && last_stream != s && !capturing(s) && !capturing(last_stream)) {
+            if (hipEventRecord(order_ev, last_stream) != hipSuccess || hipStreamWaitEvent(s, order_ev, 0) != hipSuccess) {
+                (void)hipGetLastError();
+                return fail(GHIP_STATUS_BACKEND_ERROR, "cannot order stream %p after %p", (void *)s, (void *)last_stream);
             }
-            const size_t want = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
-            if (hipMalloc(&ws, want) != hipSuccess) {
+        }
+        last_stream = s;
+        have_last = true;
+        return GHIP_STATUS_SUCCESS;
+    }
+
+    ghip_status workspace(size_t bytes, hipStream_t s, void **out) {
+        if (call_ws) {
+            if (bytes > call_ws_size)
+                return fail(GHIP_STATUS_ALLOC_FAILED, "this call needs %zu bytes of scratch; the fixed scratch holds %zu",
+                            bytes, call_ws_size);
+            *out = call_ws;
+            return GHIP_STATUS_SUCCESS;
+        }
+        if (user_ws) {
+            if (bytes > user_ws_size)
+                return fail(GHIP_STATUS_ALLOC_FAILED,
+                            "this call needs %zu bytes of workspace; ghip_set_workspace gave %zu", bytes, user_ws_size);
+            *out = user_ws;
+            return GHIP_STATUS_SUCCESS;
+        }
+        if (bytes > ws_size) {
+            if (capturing(s))
+                return fail(GHIP_STATUS_ALLOC_FAILED,
+                            "the workspace must grow to %zu bytes while the stream is being captured: run the same "
+                            "call once before capturing, or give a workspace with ghip_set_workspace",
+                            bytes);
+            size_t want = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+            want = std::max(want, ws_size + ws_size / 2);
+            void *p = nullptr;
+            if (hipMalloc(&p, want) != hipSuccess) {
                 (void)hipGetLastError();
                 return fail(GHIP_STATUS_OUT_OF_MEMORY, "workspace hipMalloc(%zu) failed", want);
             }
+            // the old buffer is kept until ghip_free: queued kernels and
+            // captured graphs may still point at it
+            if (ws) retired.push_back(ws);
+            ws = p;
             ws_size = want;
         }
         *out = ws;
@@ -159,6 +214,7 @@ bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b,
     }
     if (a->ne[0] != b->ne[0]) { st = ctx->fail(st, "mul_mat: ne00 != ne10"); return false; }
     if (a->ne[0] % ti.blck) { st = ctx->fail(st, "mul_mat: ne00 %% block size != 0"); return false; }
+    if (a->ne[0] <= 0) { st = ctx->fail(st, "mul_mat: ne00 must be positive"); return false; }
     if ((int64_t)a->nb[0] != ti.bytes) { st = ctx->fail(st, "mul_mat: permuted src0 (nb0 != type size)"); return false; }
     if ((int64_t)b->nb[0] != type_info(b->type).bytes) { st = ctx->fail(st, "mul_mat: permuted src1"); return false; }
     if (a->ne[2] != 1 || a->ne[3] != 1 || b->ne[2] != 1 || b->ne[3] != 1) {
@@ -390,6 +446,16 @@ bool use_gemm(const MulMatPlan &p) {
     return false;
 }
 
+// workspace of one MUL_MAT: [quantized activations | GEMM layout | f32
+// scratch output when only sub-sums are wanted]
+size_t mul_mat_ws_bytes(const MulMatPlan &p, bool has_dst, bool act_out, size_t *act_b, size_t *lay_b) {
+    const size_t act_bytes = p.act_pre ? 0 : ((size_t)(p.M * p.act_row_bytes) + 255) & ~(size_t)255;
+    const size_t lay_bytes = !act_out && use_gemm(p) ? gemm_layout_bytes(p) : 0;
+    if (act_b) *act_b = act_bytes;
+    if (lay_b) *lay_b = lay_bytes;
+    return (act_out ? 0 : act_bytes) + lay_bytes + (has_dst || act_out ? 0 : (size_t)(p.M * p.N * 4));
+}
+
 ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b, const ghip_tensor *d,
                          int32_t *sub, void *act_out, void *stream) {
     std::lock_guard<std::mutex> lock(ctx->mu);
@@ -400,10 +466,10 @@ ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_ten
     if (p.M == 0 || p.N == 0) return GHIP_STATUS_SUCCESS;  // empty operands: nothing to compute
     if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
     if (!d && !sub && !act_out) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: no output");
-    // workspace: [quantized activations | f32 scratch output when only sub-sums are wanted]
-    const size_t act_bytes = p.act_pre ? 0 : ((size_t)(p.M * p.act_row_bytes) + 255) & ~(size_t)255;
-    const size_t lay_bytes = !act_out && use_gemm(p) ? gemm_layout_bytes(p) : 0;
-    const size_t need = (act_out ? 0 : act_bytes) + lay_bytes + (d || act_out ? 0 : (size_t)(p.M * p.N * 4));
+    st = ctx->begin(s);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    size_t act_bytes, lay_bytes;
+    const size_t need = mul_mat_ws_bytes(p, d != nullptr, act_out != nullptr, &act_bytes, &lay_bytes);
     void *ws = nullptr;
     if (need) {
         st = ctx->workspace(need, s, &ws);
@@ -482,6 +548,10 @@ bool plan_fa(ghip_context *ctx, const ghip_tensor *q, const ghip_tensor *k, cons
     if (mask) {
         if (mask->type != GHIP_TYPE_F16 || mask->nb[0] != 2) return bad("mask must be F16 rows (ggml.c:5515)");
         if (mask->ne[0] < k->ne[1] || mask->ne[1] < q->ne[1]) return bad("mask smaller than [S, T]");
+        // one mask plane shared by every head and batch: the kernels read
+        // mask row t at t * nb1 (a per-head plane, flash_attn.rs:30-37, is not
+        // supported)
+        if (mask->ne[2] != 1 || mask->ne[3] != 1) return bad("mask must be 2-D (one plane for all heads)");
         if ((uint64_t)q->ne[1] * mask->nb[1] >= (1ull << 31)) return bad("mask spans >= 2 GiB");
     }
     if (sinks && (sinks->type != GHIP_TYPE_F32 || sinks->ne[0] < q->ne[2])) return bad("sinks must be F32 [H]");
@@ -495,6 +565,43 @@ bool plan_fa(ghip_context *ctx, const ghip_tensor *q, const ghip_tensor *k, cons
     return true;
 }
 
+
+// Launch geometry and workspace (split partials) of one FLASH_ATTN_EXT.
+struct FaLayout {
+    int G, QS, qtiles, nsplit, chunk;
+    size_t ws_bytes;
+};
+FaLayout fa_layout(int D, int T, int H, int S, int H_kv) {
+    FaLayout L;
+    // prefill workgroups hold G * QS wavefronts (G = H / H_kv heads times QS
+    // query tiles of 32) so that every staged K/V tile serves >= 4 of them
+    L.G = H / H_kv;
+    const int W = std::max(4, std::min(8, env_int("GHIP_FA_WAVES", 4)));
+    L.QS = std::max((4 + L.G - 1) / L.G, std::min((W + L.G - 1) / L.G, 8 / L.G));
+    L.qtiles = (T + 32 * L.QS - 1) / (32 * L.QS);
+    if (T == 1 && S >= 512) {
+        // single-query split-KV route: enough key slices to give every CU
+        // several workgroups
+        int ns = std::max(1, std::min((S + 127) / 128, (env_int("GHIP_FA_DECODE_WGS", 512) + H_kv - 1) / H_kv));
+        const int ch = (S + ns - 1) / ns;
+        ns = std::max(1, (S + ch - 1) / ch);
+        L.nsplit = ns;
+        L.chunk = ch;
+        L.ws_bytes = (size_t)H * ns * (2 + D) * sizeof(float);
+        return L;
+    }
+    // slices of the KV range: enough workgroups to fill the GPU, 64-key multiples
+    const int max_split = std::max(1, (S + 63) / 64);
+    int nsplit = std::max(1, std::min(max_split, (env_int("GHIP_FA_WGS", 512) + L.qtiles * H_kv - 1) / (L.qtiles * H_kv)));
+    int chunk = ((S + nsplit - 1) / nsplit + 63) / 64 * 64;
+    if (chunk == 0) chunk = 64;
+    nsplit = std::max(1, (S + chunk - 1) / chunk);
+    L.nsplit = nsplit;
+    L.chunk = chunk;
+    const bool rowseq = T < 64 && !env_int("GHIP_FA_FORCE_MFMA", 0);  // one_chunk walk: no partials
+    L.ws_bytes = rowseq ? 0 : (size_t)T * H * nsplit * (2 + D) * sizeof(float);
+    return L;
+}
 
 // ------------------------------------------------------------ MUL_MAT_ID
 
@@ -510,7 +617,7 @@ bool plan_moe(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b, co
     auto bad = [&](const char *why) { st = ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat_id: %s", why); return false; };
     if (!as || !b || !ids) return bad("null operand");
     if (as->type != GHIP_TYPE_MXFP4) return bad("experts must be MXFP4");
-    if (as->ne[0] % 32) return bad("ne00 must be a multiple of 32");
+    if (as->ne[0] % 32 || as->ne[0] <= 0) return bad("ne00 must be a positive multiple of 32");
     p.K = as->ne[0];
     p.rows = as->ne[1];
     p.n_as = as->ne[2];
@@ -537,6 +644,30 @@ bool plan_moe(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b, co
     return true;
 }
 
+// MUL_MAT_ID workspace: Q8_0 rows | f16 slot codes | f32 scales | routing
+// table | scratch output (sub-sums only)
+struct MoeWs {
+    int tp;
+    int64_t max_tiles;
+    size_t act, actf, actd, route, out, total;
+};
+MoeWs moe_ws(const MoePlan &p, bool has_dst, bool sub) {
+    MoeWs L;
+    const int64_t n_pairs = p.n_ids * p.n_tokens;
+    // 32-pair tiles when experts see few pairs each (decode, small batches)
+    const int tile_env = env_int("GHIP_MOE_TILE", 0);
+    L.tp = (sub || tile_env == 32) ? 32 : tile_env == 64 ? 64 : n_pairs <= 48 * p.n_as ? 32 : 64;
+    L.max_tiles = (n_pairs + L.tp - 1) / L.tp + p.n_as;
+    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    L.act = up((size_t)(p.ne11 * p.n_tokens * p.act_row_bytes));
+    L.actf = up((size_t)n_pairs * p.nb * 64);  // per routed pair
+    L.actd = up((size_t)n_pairs * p.nb * 4);
+    L.route = up((size_t)(2 + n_pairs + 3 * L.max_tiles) * 4);
+    L.out = has_dst ? 0 : (size_t)(n_pairs * p.rows * 4);
+    L.total = L.act + L.actf + L.actd + L.route + L.out;
+    return L;
+}
+
 // Q8_0 activations, routing, then the tiled MFMA kernel; pairs with an
 // invalid expert id get NaN rows (the reference asserts on them).
 ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b, const ghip_tensor *ids,
@@ -550,20 +681,15 @@ ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip
     if (n_pairs == 0 || p.rows == 0) return GHIP_STATUS_SUCCESS;
     hipStream_t s = (hipStream_t)stream;
     if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
-    // 32-pair tiles when experts see few pairs each (decode, small batches)
-    const int tile_env = env_int("GHIP_MOE_TILE", 0);
-    const int tp = (sub || tile_env == 32) ? 32 : tile_env == 64 ? 64 : n_pairs <= 48 * p.n_as ? 32 : 64;
-    const int64_t max_tiles = (n_pairs + tp - 1) / tp + p.n_as;
-    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    st = ctx->begin(s);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    const MoeWs L = moe_ws(p, d != nullptr, sub != nullptr);
+    const int tp = L.tp;
+    const int64_t max_tiles = L.max_tiles;
     const int64_t act_rows = p.ne11 * p.n_tokens;
-    // workspace: Q8_0 rows | f16 slot codes | f32 scales | routing table | scratch output
-    const size_t act_bytes = up((size_t)(act_rows * p.act_row_bytes));
-    const size_t actf_bytes = up((size_t)n_pairs * p.nb * 64);  // per routed pair
-    const size_t actd_bytes = up((size_t)n_pairs * p.nb * 4);
-    const size_t route_bytes = up((size_t)(2 + n_pairs + 3 * max_tiles) * 4);
-    const size_t out_bytes = d ? 0 : (size_t)(n_pairs * p.rows * 4);
+    const size_t act_bytes = L.act, actf_bytes = L.actf, actd_bytes = L.actd, route_bytes = L.route;
     void *ws = nullptr;
-    st = ctx->workspace(act_bytes + actf_bytes + actd_bytes + route_bytes + out_bytes, s, &ws);
+    st = ctx->workspace(L.total, s, &ws);
     if (st != GHIP_STATUS_SUCCESS) return st;
     uint8_t *act = (uint8_t *)ws;
     uint16_t *actf = (uint16_t *)((uint8_t *)ws + act_bytes);  // f16 codes
@@ -688,6 +814,8 @@ ghip_status mul_mat_multi_gemm(ghip_context *ctx, const ghip_node *nodes, int n,
             return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "graph_compute: internal: node not groupable");
     }
     if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    st = ctx->begin(s);
+    if (st != GHIP_STATUS_SUCCESS) return st;
     const MulMatPlan &p0 = p[0];
     const int64_t Mpad = (p0.M + 127) / 128 * 128, K = p0.K, nbk = p0.K / 256;
     const size_t act_bytes = ((size_t)(p0.M * p0.act_row_bytes) + 255) & ~(size_t)255;
@@ -739,6 +867,8 @@ ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipS
             return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "graph_compute: internal: node not groupable");
     }
     if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    st = ctx->begin(s);
+    if (st != GHIP_STATUS_SUCCESS) return st;
     const MulMatPlan &p0 = p[0];
     if (gemv_pair(p0.wtype)) {
         // Q8_0 rows once for the group, then 8 weight rows per workgroup
@@ -836,21 +966,16 @@ ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const g
     if (T == 0 || H == 0) return GHIP_STATUS_SUCCESS;
     hipStream_t s = (hipStream_t)stream;
     if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
-    // slices of the KV range: enough workgroups to fill the GPU, 64-key multiples
-    // prefill workgroups hold G * QS wavefronts (G = H / H_kv heads times QS
-    // query tiles of 32) so that every staged K/V tile serves >= 4 of them
-    const int G = H / H_kv, W = std::max(4, std::min(8, env_int("GHIP_FA_WAVES", 4)));
-    const int QS = std::max((4 + G - 1) / G, std::min((W + G - 1) / G, 8 / G));
-    const int qtiles = (T + 32 * QS - 1) / (32 * QS);
-    const int max_split = std::max(1, (S + 63) / 64);
-    int nsplit = std::max(1, std::min(max_split, (env_int("GHIP_FA_WGS", 512) + qtiles * H_kv - 1) / (qtiles * H_kv)));
-    int chunk = ((S + nsplit - 1) / nsplit + 63) / 64 * 64;
-    if (chunk == 0) chunk = 64;
-    nsplit = std::max(1, (S + chunk - 1) / chunk);
-    void *ws = nullptr;
-    const size_t part_bytes = (size_t)T * H * nsplit * (2 + D) * sizeof(float);
-    st = ctx->workspace(part_bytes, s, &ws);
+    st = ctx->begin(s);
     if (st != GHIP_STATUS_SUCCESS) return st;
+    const FaLayout L = fa_layout(D, T, H, S, H_kv);
+    const int G = L.G, QS = L.QS, qtiles = L.qtiles;
+    int nsplit = L.nsplit, chunk = L.chunk;
+    void *ws = nullptr;
+    if (L.ws_bytes) {
+        st = ctx->workspace(L.ws_bytes, s, &ws);
+        if (st != GHIP_STATUS_SUCCESS) return st;
+    }
     FaParams p;
     p.q = (const float *)q->data;
     p.q_nb1 = (int64_t)q->nb[1] / 4;
@@ -888,17 +1013,8 @@ ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const g
         return ctx->launch(rs, dim3((unsigned)((T * H + 3) / 4)), dim3(256), 0, s, p);
     }
     if (T == 1) {
-        // single-query split-KV route: the bandwidth-bound vector kernel, with
-        // enough key slices to give every CU several workgroups
-        int ns = std::max(1, std::min((S + 127) / 128, (env_int("GHIP_FA_DECODE_WGS", 512) + H_kv - 1) / H_kv));
-        int ch = (S + ns - 1) / ns;
-        ns = std::max(1, (S + ch - 1) / ch);
-        const size_t pb = (size_t)H * ns * (2 + D) * sizeof(float);
-        st = ctx->workspace(pb, s, &ws);
-        if (st != GHIP_STATUS_SUCCESS) return st;
-        p.part = (float *)ws;
-        p.nsplit = ns;
-        p.chunk = ch;
+        // single-query split-KV route: the bandwidth-bound vector kernel
+        const int ns = nsplit;
         const char *dec = D == 128 ? "ghip_fa_decode_d128" : "ghip_fa_decode_d64";
         st = ctx->launch(dec, dim3(H_kv, ns), dim3(256), 0, s, p);
         if (st != GHIP_STATUS_SUCCESS) return st;
@@ -932,6 +1048,11 @@ ghip_status ghip_init(int device, ghip_context **out) {
     if (hipSetDevice(device) != hipSuccess) return GHIP_STATUS_BACKEND_ERROR;
     ghip_context *ctx = new ghip_context();
     ctx->device = device;
+    if (hipEventCreateWithFlags(&ctx->order_ev, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        delete ctx;
+        return GHIP_STATUS_BACKEND_ERROR;
+    }
     const std::string dir = library_dir();
     for (const char *m : kModules) {
         hipModule_t mod;
@@ -954,6 +1075,8 @@ void ghip_free(ghip_context *ctx) {
     hipSetDevice(ctx->device);
     hipDeviceSynchronize();
     if (ctx->ws) hipFree(ctx->ws);
+    for (void *p : ctx->retired) hipFree(p);
+    if (ctx->order_ev) hipEventDestroy(ctx->order_ev);
     for (hipModule_t m : ctx->modules) hipModuleUnload(m);
     delete ctx;
 }
@@ -1047,6 +1170,48 @@ ghip_status ghip_graph_compute(ghip_context *ctx, const ghip_node *nodes, int32_
         i = next;
     }
     return GHIP_STATUS_SUCCESS;
+}
+
+ghip_status ghip_set_workspace(ghip_context *ctx, void *ptr, size_t bytes) {
+    if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    if (!ptr && bytes) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "set_workspace: null pointer with a size");
+    ctx->user_ws = bytes ? ptr : nullptr;
+    ctx->user_ws_size = bytes;
+    return GHIP_STATUS_SUCCESS;
+}
+
+ghip_status ghip_workspace_size(int op, const ghip_tensor *dst, const ghip_tensor *const *srcs, int n_srcs,
+                                size_t *bytes) {
+    if (!bytes) return GHIP_STATUS_BACKEND_ERROR;
+    *bytes = 0;
+    ghip_context tmp;
+    ghip_status st = GHIP_STATUS_BACKEND_ERROR;
+    if (op == GHIP_OP_MUL_MAT) {
+        if (n_srcs < 2 || !srcs || !dst) return st;
+        MulMatPlan p;
+        if (!plan_mul_mat(&tmp, srcs[0], srcs[1], dst, p, st)) return st;
+        if (p.M == 0 || p.N == 0) return GHIP_STATUS_SUCCESS;
+        *bytes = mul_mat_ws_bytes(p, true, false, nullptr, nullptr);
+        return GHIP_STATUS_SUCCESS;
+    }
+    if (op == GHIP_OP_MUL_MAT_ID) {
+        if (n_srcs < 3 || !srcs || !dst) return st;
+        MoePlan p;
+        if (!plan_moe(&tmp, srcs[0], srcs[1], srcs[2], dst, p, st)) return st;
+        if (p.n_ids * p.n_tokens == 0 || p.rows == 0) return GHIP_STATUS_SUCCESS;
+        *bytes = moe_ws(p, true, false).total;
+        return GHIP_STATUS_SUCCESS;
+    }
+    if (op == GHIP_OP_FLASH_ATTN_EXT) {
+        if (n_srcs < 3 || !srcs || !dst) return st;
+        const ghip_tensor *q = srcs[0], *k = srcs[1], *v = srcs[2];
+        if (!plan_fa(&tmp, q, k, v, n_srcs > 3 ? srcs[3] : nullptr, n_srcs > 4 ? srcs[4] : nullptr, dst, st)) return st;
+        if (q->ne[1] == 0 || q->ne[2] == 0) return GHIP_STATUS_SUCCESS;
+        *bytes = fa_layout((int)k->ne[0], (int)q->ne[1], (int)q->ne[2], (int)k->ne[1], (int)k->ne[2]).ws_bytes;
+        return GHIP_STATUS_SUCCESS;
+    }
+    return st;
 }
 
 ghip_status ghip_quantize_chunk(ghip_context *ctx, int type, const float *src, void *dst, int64_t nrows,

@@ -101,6 +101,8 @@ void *reg_proc_address(const ggml_hip_backend_reg *, const char *name) {
         {"ghip_flash_attn_ext", (void *)&ghip_flash_attn_ext},
         {"ghip_quantize_chunk", (void *)&ghip_quantize_chunk},
         {"ghip_graph_compute", (void *)&ghip_graph_compute},
+        {"ghip_set_workspace", (void *)&ghip_set_workspace},
+        {"ghip_workspace_size", (void *)&ghip_workspace_size},
     };
     if (!name) return nullptr;
     for (const Proc &p : procs)

@@ -127,6 +127,10 @@ def lib():
         L.ghip_mul_mat_id_subsums.argtypes = [C.c_void_p, P, P, P, C.c_void_p, C.c_void_p]
         L.ghip_graph_compute.restype = C.c_int
         L.ghip_graph_compute.argtypes = [C.c_void_p, C.POINTER(GNode), C.c_int32, C.c_void_p]
+        L.ghip_set_workspace.restype = C.c_int
+        L.ghip_set_workspace.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
+        L.ghip_workspace_size.restype = C.c_int
+        L.ghip_workspace_size.argtypes = [C.c_int, P, C.POINTER(P), C.c_int, C.POINTER(C.c_size_t)]
         L.ghip_flash_attn_ext.restype = C.c_int
         L.ghip_flash_attn_ext.argtypes = [C.c_void_p, P, P, P, P, P, P, C.c_void_p]
         _lib = L
@@ -256,6 +260,25 @@ class Backend:
                 arr[i].src[j] = C.pointer(t) if t is not None else None
             arr[i].dst = C.pointer(nd.dst) if nd.dst is not None else None
         self._check(lib().ghip_graph_compute(self._ctx, arr, len(nodes), _stream()), "ghip_graph_compute")
+
+    # ---- workspace
+    def set_workspace(self, buf):
+        """Use the device tensor `buf` (kept alive here) as the context's
+        workspace; None returns to the library-owned one."""
+        self._ws = buf
+        ptr, n = (buf.data_ptr(), buf.numel() * buf.element_size()) if buf is not None else (None, 0)
+        self._check(lib().ghip_set_workspace(self._ctx, ptr, n), "ghip_set_workspace")
+
+    @staticmethod
+    def workspace_size(node):
+        """Workspace bytes of one graph node (ghip_workspace_size)."""
+        P = C.POINTER(Tensor)
+        srcs = (P * 5)(*[C.pointer(t) if t is not None else None for t in (node.srcs + [None] * 5)[:5]])
+        out = C.c_size_t(0)
+        st = lib().ghip_workspace_size(node.op, C.pointer(node.dst), srcs, len(node.srcs), C.byref(out))
+        if st != 0:
+            raise GhipError(f"ghip_workspace_size: status {st}")
+        return out.value
 
     def synchronize(self):
         self._check(lib().ghip_synchronize(self._ctx, _stream()), "ghip_synchronize")

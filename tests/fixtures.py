@@ -6,6 +6,7 @@ Each parser follows the reader in the reference test that consumes the file:
   q4k_repack_ref.bin, q4_0_repack_ref  repack.rs:5636-5676, :6046-6086
   repack_ref.bin (MXFP4)               repack.rs:5010-5055
   tiled_ref.bin                        tiled.rs:2020-2090 (VMT1)
+  *_goss_ref.bin, *_granite_ref.bin    vec_dot.rs:2730-2770 (real-weight dumps)
 """
 import os
 import struct
@@ -87,8 +88,11 @@ def mulmat_sections(name):
     return out
 
 
-def tiled_sections(name="tiled_ref_q4k_q6k.bin"):
-    """VMT1 MUL_MAT sections: [(type_id, n, rows, cols, xq, y, dst)]."""
+def tiled_sections(name="tiled_ref_kq.bin", kind=0):
+    """VMT1 sections (tiled.rs:2020-2090) of one kind.
+    kind 0 (MUL_MAT):    [(type_id, n, rows, cols, xq, y [cols, n], dst [cols, rows])]
+    kind 1 (MUL_MAT_ID): [(type_id, n, rows, ne11, n_as, n_ids, ne12, xq, y [ne12, ne11, n],
+                           ids [ne12, n_ids], dst [ne12, n_ids, rows])]"""
     from oracle_lib import row_size
     b = read(name)
     o = 0
@@ -99,18 +103,55 @@ def tiled_sections(name="tiled_ref_q4k_q6k.bin"):
         if magic == 0xFFFFFFFF:
             break
         assert magic == 0x31544D56
-        kind, tid, n, rows, cols = struct.unpack_from("<5I", b, o)
+        k, tid, n, rows, cols = struct.unpack_from("<5I", b, o)
         o += 20
-        assert kind == 0
-        xl = row_size(tid, n) * rows
+        n_as = n_ids = ne12 = 1
+        if k == 1:
+            n_as, n_ids, ne12 = struct.unpack_from("<3I", b, o)
+            o += 12
+        xl = row_size(tid, n) * rows * n_as
         xq = np.frombuffer(b, dtype=np.uint8, count=xl, offset=o).copy()
         o += xl
-        y = np.frombuffer(b, dtype=np.float32, count=n * cols, offset=o).reshape(cols, n).copy()
-        o += 4 * n * cols
-        dst = np.frombuffer(b, dtype=np.float32, count=rows * cols, offset=o).reshape(cols, rows).copy()
-        o += 4 * rows * cols
-        out.append((tid, n, rows, cols, xq, y, dst))
+        y = np.frombuffer(b, dtype=np.float32, count=n * cols * ne12, offset=o).copy()
+        o += 4 * n * cols * ne12
+        if k == 1:
+            ids = np.frombuffer(b, dtype=np.int32, count=n_ids * ne12, offset=o).reshape(ne12, n_ids).copy()
+            o += 4 * n_ids * ne12
+        dst = np.frombuffer(b, dtype=np.float32, count=rows * cols if k == 0 else rows * n_ids * ne12,
+                            offset=o).copy()
+        o += 4 * dst.size
+        if k != kind:
+            continue
+        if k == 0:
+            out.append((tid, n, rows, cols, xq, y.reshape(cols, n), dst.reshape(cols, rows)))
+        else:
+            out.append((tid, n, rows, cols, n_as, n_ids, ne12, xq.reshape(n_as, rows, -1),
+                        y.reshape(ne12, cols, n), ids, dst.reshape(ne12, n_ids, rows)))
     return out
+
+
+def real_weight_dump(name):
+    """parity/{q4k_goss,q4k_granite,q6k_granite,q5_0_goss,q8_0_goss,q5k_real}_ref.bin
+    (vec_dot.rs:2730-2770, written by parity/ref_q5k_dump.c): length-prefixed
+    sections hdr {type, n, rows, cols, flags}, xq, act f32 [cols, n], plain out,
+    repacked weights, repack out, q8k bytes, sgemm out.  flags & 1: the
+    reference's production path is the Q4_K 8x8 repack kernel (repack_out),
+    else the plain vec_dot (plain)."""
+    s = _len_sections(name)
+    ty, n, rows, cols, flags = struct.unpack_from("<5I", s[0])
+    f32 = lambda v: np.frombuffer(v, dtype=np.float32).copy()
+    d = dict(type=ty, n=n, rows=rows, cols=cols, flags=flags,
+             xq=np.frombuffer(s[1], dtype=np.uint8).copy(),
+             act=f32(s[2]).reshape(cols, n), plain=f32(s[3]).reshape(cols, rows),
+             repack_out=f32(s[5]).reshape(cols, rows) if s[5] else None,
+             q8k=np.frombuffer(s[6], dtype=np.uint8).copy(),
+             sgemm_out=f32(s[7]).reshape(cols, rows) if s[7] else None)
+    d["want"] = d["repack_out"] if flags & 1 else d["plain"]
+    return d
+
+
+REAL_WEIGHT_DUMPS = ["q4k_goss_ref.bin", "q4k_granite_ref.bin", "q6k_granite_ref.bin",
+                     "q5_0_goss_ref.bin", "q8_0_goss_ref.bin", "q5k_real_ref.bin"]
 
 
 def _len_sections(name):

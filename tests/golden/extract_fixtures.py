@@ -3,8 +3,9 @@
 The files under ``parity/`` of fly88oj/llama.rust (MIT licence, copyright 2026
 fly88oj) are golden vectors that an instrumented llama.cpp build produced.  They
 are data (inputs and expected outputs), copied verbatim -- except
-``tiled_ref.bin``, of which only the Q4_K / Q6_K MUL_MAT sections are kept (the
-other weight types are out of scope and the file is 18 MB).
+``tiled_ref.bin``, of which only the Q4_K, Q5_K and Q6_K MUL_MAT and
+MUL_MAT_ID sections are kept (the IQ types are out of scope and the whole file
+is 18 MB).
 
 Run once in a container where the reference tree is mounted:
     python tests/golden/extract_fixtures.py /root/reference/parity
@@ -18,11 +19,16 @@ WHOLE = [
     "quants_ref.bin", "quants_ref_fp4.bin", "mulmat_ref.bin", "mulmat_ref_c1.bin",
     "q4k_repack_ref.bin", "q4_0_repack_ref.bin", "repack_ref.bin",
     "fa_ref.bin", "fa_probe.bin",
+    # real GGUF tensors x the reference's production path (vec_dot.rs:2798-2807)
+    "q4k_goss_ref.bin", "q4k_granite_ref.bin", "q6k_granite_ref.bin",
+    "q5_0_goss_ref.bin", "q8_0_goss_ref.bin", "q5k_real_ref.bin",
 ]
 ROW_BYTES_PER_256 = {10: 84, 11: 110, 12: 144, 13: 176, 14: 210}
 
 
-def extract_tiled(src, dst, keep=(12, 14)):
+def extract_tiled(src, dst, keep=(12, 13, 14)):
+    """VMT1 sections (tiled.rs:2020-2090): kind 0 = MUL_MAT {xq, y, dst},
+    kind 1 = MUL_MAT_ID {n_as, n_ids, ne12; xq, y, ids, dst}."""
     b = open(src, "rb").read()
     o = 0
     out = bytearray()
@@ -34,13 +40,42 @@ def extract_tiled(src, dst, keep=(12, 14)):
         o += 4
         kind, ty, n, rows, cols = struct.unpack_from("<5I", b, o)
         o += 20
-        if kind != 0 or ty not in ROW_BYTES_PER_256:
-            break  # the Q2_K..Q6_K mm sections come first; stop at the rest
-        o += (n // 256) * ROW_BYTES_PER_256[ty] * rows + n * cols * 4 + rows * cols * 4
+        if ty not in ROW_BYTES_PER_256:
+            # an IQ type: its row size is not needed to skip, the K-quant
+            # sections of each kind come first in the file
+            if kind == 0:
+                # skip to the next kind-1 section by scanning is not possible
+                # without the row size; the K-quant mm sections are all before
+                # the first IQ mm section, so jump to the mmid part
+                o = find_mmid(b, start)
+                if o < 0:
+                    break
+                continue
+            break
+        rs = (n // 256) * ROW_BYTES_PER_256[ty]
+        if kind == 0:
+            o += rs * rows + n * cols * 4 + rows * cols * 4
+        else:
+            n_as, n_ids, ne12 = struct.unpack_from("<3I", b, o)
+            o += 12
+            o += rs * rows * n_as + n * cols * ne12 * 4 + n_ids * ne12 * 4 + rows * n_ids * ne12 * 4
         if ty in keep:
             out += b[start:o]
     out += struct.pack("<I", 0xFFFFFFFF)
     open(dst, "wb").write(bytes(out))
+
+
+def find_mmid(b, o):
+    """Offset of the first kind-1 VMT1 header at or after o (magic, kind == 1,
+    a K-quant type)."""
+    magic = struct.pack("<I", 0x31544D56)
+    while True:
+        o = b.find(magic, o + 1)
+        if o < 0:
+            return -1
+        kind, ty = struct.unpack_from("<2I", b, o + 4)
+        if kind == 1 and ty in ROW_BYTES_PER_256:
+            return o
 
 
 def main(parity_dir):
@@ -48,7 +83,7 @@ def main(parity_dir):
     os.makedirs(here, exist_ok=True)
     for f in WHOLE:
         shutil.copyfile(os.path.join(parity_dir, f), os.path.join(here, f))
-    extract_tiled(os.path.join(parity_dir, "tiled_ref.bin"), os.path.join(here, "tiled_ref_q4k_q6k.bin"))
+    extract_tiled(os.path.join(parity_dir, "tiled_ref.bin"), os.path.join(here, "tiled_ref_kq.bin"))
 
 
 if __name__ == "__main__":

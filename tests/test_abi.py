@@ -48,3 +48,62 @@ def test_supports_op_without_gpu():
     assert L.ghip_supports_op(ghip.OP_MUL_MAT, ctypes.byref(d), srcs, 2) == 1
     b.type = ghip.F16
     assert L.ghip_supports_op(ghip.OP_MUL_MAT, ctypes.byref(d), srcs, 2) == 0
+
+
+def _t(ty, ne, nb):
+    import sys
+    sys.path.insert(0, os.path.join(ROOT, "llama.rust_amd"))
+    import ghip
+    t = ghip.Tensor()
+    t.type, t.ne[:], t.nb[:] = ty, ne, nb
+    return t
+
+
+def test_supports_op_rejects_empty_rows():
+    """ne00 == 0 has no decode-kernel geometry: rejected (not a division by zero
+    in the host planner)."""
+    import ghip
+    a = _t(ghip.Q4_K, (0, 64, 1, 1), (144, 0, 0, 0))
+    b = _t(ghip.F32, (0, 3, 1, 1), (4, 0, 0, 0))
+    d = _t(ghip.F32, (64, 3, 1, 1), (4, 256, 768, 768))
+    P = ctypes.POINTER(ghip.Tensor)
+    srcs = (P * 2)(ctypes.pointer(a), ctypes.pointer(b))
+    assert ghip.lib().ghip_supports_op(ghip.OP_MUL_MAT, ctypes.byref(d), srcs, 2) == 0
+
+
+def test_supports_op_fa_mask_planes():
+    """FLASH_ATTN_EXT takes one 2-D mask for every head; a mask with per-head
+    planes (ne2 > 1) is rejected rather than read as plane 0."""
+    import ghip
+    D, T, H, S, Hkv = 128, 4, 8, 256, 2
+    q = _t(ghip.F32, (D, T, H, 1), (4, 4 * D, 4 * D * T, 4 * D * T * H))
+    k = _t(ghip.F16, (D, S, Hkv, 1), (2, 2 * D, 2 * D * S, 2 * D * S * Hkv))
+    v = _t(ghip.F16, (D, S, Hkv, 1), (2, 2 * D, 2 * D * S, 2 * D * S * Hkv))
+    m = _t(ghip.F16, (S, T, 1, 1), (2, 2 * S, 2 * S * T, 2 * S * T))
+    d = _t(ghip.F32, (D, H, T, 1), (4, 4 * D, 4 * D * H, 4 * D * H * T))
+    P = ctypes.POINTER(ghip.Tensor)
+    srcs = (P * 5)(ctypes.pointer(q), ctypes.pointer(k), ctypes.pointer(v), ctypes.pointer(m), None)
+    L = ghip.lib()
+    assert L.ghip_supports_op(ghip.OP_FLASH_ATTN_EXT, ctypes.byref(d), srcs, 5) == 1
+    m.ne[2], m.nb[3] = H, 2 * S * T * H
+    assert L.ghip_supports_op(ghip.OP_FLASH_ATTN_EXT, ctypes.byref(d), srcs, 5) == 0
+
+
+def test_workspace_size_query_without_gpu():
+    """ghip_workspace_size is host arithmetic: a Q4_K prefill GEMM needs the
+    Q8_K rows plus the GEMM layout; a fused decode GEMV needs none."""
+    import ghip
+    L = ghip.lib()
+    P = ctypes.POINTER(ghip.Tensor)
+
+    def need(m):
+        a = _t(ghip.Q4_K, (4096, 4096, 1, 1), (144, 2304, 2304 * 4096, 2304 * 4096))
+        b = _t(ghip.F32, (4096, m, 1, 1), (4, 16384, 16384 * m, 16384 * m))
+        d = _t(ghip.F32, (4096, m, 1, 1), (4, 16384, 16384 * m, 16384 * m))
+        srcs = (P * 2)(ctypes.pointer(a), ctypes.pointer(b))
+        out = ctypes.c_size_t(7)
+        assert L.ghip_workspace_size(ghip.OP_MUL_MAT, ctypes.byref(d), srcs, 2, ctypes.byref(out)) == 0
+        return out.value
+
+    assert need(512) >= 512 * 16 * 292 + 512 * 4096
+    assert need(1) >= 0

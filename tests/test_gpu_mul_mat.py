@@ -39,13 +39,24 @@ def run_case(be, ty, n, rows, cols, seed=0, x=None, check_sub=True):
     w, x0 = make(ty, n, rows, cols, seed)
     if x is None:
         x = x0
-    want, route, want_sub = O.mul_mat(ty, w, n, rows, x, cols, want_subsums=check_sub)
+    if ty == O.Q4_0 and rows % 8 and cols >= 2:
+        # the reference's tinyBLAS route (llamafile_sgemm), absent from the
+        # oracle: the same Q8_0 rows and integer block dots, checked against
+        # the row vec_dot per column (the fp32 order is all that differs)
+        per = [O.mul_mat(ty, w, n, rows, x[c:c + 1], 1, want_subsums=check_sub) for c in range(cols)]
+        want = np.concatenate([p[0] for p in per])
+        want_sub = np.concatenate([p[2] for p in per]) if check_sub else None
+        want_act = np.concatenate([O.mul_mat_act(ty, n, rows, x[c:c + 1], 1) for c in range(cols)])
+        route = "tinyBLAS (checked per column against vec_dot)"
+    else:
+        want, route, want_sub = O.mul_mat(ty, w, n, rows, x, cols, want_subsums=check_sub)
+        want_act = O.mul_mat_act(ty, n, rows, x, cols)
     wd = torch.from_numpy(w).cuda()
     xd = torch.from_numpy(x).cuda()
     print(f"case type={ty} n={n} rows={rows} cols={cols} route={route}", flush=True)
     got = be.mul_mat(wd, ty, n, xd).cpu().numpy()
     act = be.mul_mat_act(wd, ty, n, xd).cpu().numpy().reshape(-1)
-    assert np.array_equal(act, O.mul_mat_act(ty, n, rows, x, cols)), "activation bytes differ"
+    assert np.array_equal(act, want_act), "activation bytes differ"
     if check_sub:
         sub = be.mul_mat_subsums(wd, ty, n, xd).cpu().numpy()
         assert np.array_equal(sub, want_sub), "int32 sub-sums differ"
@@ -57,11 +68,7 @@ def run_case(be, ty, n, rows, cols, seed=0, x=None, check_sub=True):
 @pytest.mark.parametrize("ty", [O.Q4_0, O.Q4_K, O.Q6_K])
 @pytest.mark.parametrize("cols", [1, 2, 3, 4, 5, 8, 11])
 def test_small_shapes(be, ty, cols):
-    # 4 weight rows is not a multiple of 8: Q4_0 with >= 2 columns is then the
-    # reference's tinyBLAS route, which the oracle leaves out
     for n, rows in [(512, 64), (1024, 72), (768, 100), (256, 8)]:
-        if ty == O.Q4_0 and rows % 8 and cols >= 2:
-            continue
         run_case(be, ty, n, rows, cols, seed=cols)
 
 
@@ -201,4 +208,32 @@ def test_gemm_q4K_prefill_shapes(be, tokens, n, rows):
     w64 = np.ascontiguousarray(wsl[:64])
     sub = be.mul_mat_subsums(torch.from_numpy(w64).cuda(), O.Q4_K, n, torch.from_numpy(x).cuda()).cpu().numpy()
     _, _, want_sub = O.mul_mat(O.Q4_K, w64, n, 64, x, tokens, want_subsums=True)
+    assert np.array_equal(sub, want_sub)
+
+
+@pytest.mark.parametrize("n,rows,cols", [(1024, 204, 16), (2048, 204, 130), (512, 12, 64), (4096, 4100, 64)])
+def test_gemm_q4K_rows_not_multiple_of_8(be, n, rows, cols):
+    """Q4_K with N % 8 != 0 and >= 16 activation rows: the reference takes the
+    tiled route (compute.rs:1596) with quantize_row_q8_K_ref activations for
+    every row (no 4x8 values); the GPU runs its GEMM on those bytes.  The
+    activation bytes are compared in full; at 4100 rows the oracle checks the
+    last 516 rows (the ragged tile edge) and the sub-sums of the last 4."""
+    w, x = make(O.Q4_K, n, rows, cols, seed=rows + cols)
+    sl = slice(max(0, rows - 516), rows)
+    wsl = np.ascontiguousarray(w[sl])
+    nr = wsl.shape[0]
+    print(f"gemm q4_K n={n} rows={rows} cols={cols}", flush=True)
+    wd, xd = torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda()
+    got = be.mul_mat(wd, O.Q4_K, n, xd).cpu().numpy()
+    want, route, _ = O.mul_mat(O.Q4_K, wsl, n, nr, x, cols)
+    assert route == (O.ROUTE_TILED if nr % 8 else O.ROUTE_REPACK)
+    act = be.mul_mat_act(wd, O.Q4_K, n, xd).cpu().numpy().reshape(-1)
+    assert np.array_equal(act, O.mul_mat_act(O.Q4_K, n, rows, x, cols))
+    assert np.array_equal(act, np.concatenate([O.quantize(O.Q8_K, x[c], kind="quantize_row_q8_K_ref")
+                                               for c in range(cols)]))
+    err = rel_err(got[:, sl], want)
+    assert err <= TOL, f"rel_err {err:.3e}"
+    w4 = np.ascontiguousarray(w[rows - 4:])
+    sub = be.mul_mat_subsums(torch.from_numpy(w4).cuda(), O.Q4_K, n, xd).cpu().numpy()
+    _, _, want_sub = O.mul_mat(O.Q4_K, w4, n, 4, x, cols, want_subsums=True)
     assert np.array_equal(sub, want_sub)

@@ -168,16 +168,103 @@ def test_new_type_subsums_brute_force(ty):
                     lo = np.concatenate([qs & 15, qs >> 4])
                     q = (lo | (((qh >> np.arange(32)) & 1) << 4)) - 16
                 assert int(np.dot(q, aqs[b])) == int(sub[0, r, b]), (ty, r, b)
+    else:
+        # Q5_K: an integer brute force of {iacc, imin} from the raw block bytes
+        # (d, dmin, 12 scale bytes, qh[32], qs[128]; 6-bit scales/mins packed as
+        # in get_scale_min_k4) and the Q8_K codes; then the float64 dot of the
+        # dequantized values rebuilt from the integers
+        ab = np.frombuffer(codes.tobytes(), dtype=np.uint8).reshape(n // 256, 292)
+        da = ab[:, :4].copy().view(np.float32).reshape(-1).astype(np.float64)
+        q8 = ab[:, 4:260].copy().view(np.int8).astype(np.int64)
+        for r in range(rows):
+            for b in range(n // 256):
+                blk = wv[r, b].astype(np.int64)
+                sc8, qh, qs = blk[4:16], blk[16:48], blk[48:176]
+                ia = im = 0
+                for s in range(8):
+                    if s < 4:
+                        scl, mn = sc8[s] & 63, sc8[s + 4] & 63
+                    else:
+                        scl = (sc8[s + 4] & 15) | ((sc8[s - 4] >> 6) << 4)
+                        mn = (sc8[s + 4] >> 4) | ((sc8[s] >> 6) << 4)
+                    j = s // 2
+                    nib = (qs[32 * j:32 * j + 32] >> (4 * (s & 1))) & 15
+                    q5 = nib | (((qh >> s) & 1) << 4)
+                    a8 = q8[b, 32 * s:32 * s + 32]
+                    ia += int(scl) * int(np.dot(q5, a8))
+                    im += int(mn) * int(a8.sum())
+                assert (ia, im) == (int(sub[0, r, b, 0]), int(sub[0, r, b, 1])), (ty, r, b)
+            d = wv[r, :, 0:2].copy().view(np.float16).reshape(-1).astype(np.float64)
+            dmin = wv[r, :, 2:4].copy().view(np.float16).reshape(-1).astype(np.float64)
+            ia_, im_ = sub[0, r, :, 0].astype(np.float64), sub[0, r, :, 1].astype(np.float64)
+            got = float(np.sum(da * (d * ia_ - dmin * im_)))
+            wf = O.dequantize(t, w[r * O.row_size(t, n):(r + 1) * O.row_size(t, n)], n).astype(np.float64)
+            ref = float(np.dot(wf, aq))
+            # the dequantized reference rounds d*sc and dmin*m to fp32 per element
+            assert abs(got - ref) <= 1e-6 * max(abs(ref), 1.0), (r, got, ref)
 
 
-def test_tiled_q4k_q6k_bit_exact():
-    """tiled.rs:2183 tiled_mulmat_matches_reference_bit_exact (Q4_K / Q6_K sections)."""
+def test_tiled_kquant_bit_exact():
+    """tiled.rs:2183 tiled_mulmat_matches_reference_bit_exact (the Q4_K, Q5_K and
+    Q6_K MUL_MAT sections)."""
     secs = fx.tiled_sections()
-    assert len(secs) == 8
+    assert len(secs) == 12
     for tid, n, rows, cols, xq, y, dst in secs:
         out, route, _ = O.mul_mat(tid, xq, n, rows, y, cols)
         assert route == O.ROUTE_TILED
         assert np.array_equal(out.view(np.uint32), dst.view(np.uint32)), f"type {tid} {rows}x{cols}"
+
+
+def mul_mat_id_kquant(ty, xq, n, rows, ne11, n_as, n_ids, ne12, y, ids):
+    """forward_mul_mat_id (compute.rs:1917-2202) for a K-quant whose experts are
+    not repacked (rows % 8 != 0): every expert with >= 8 routed (slot, token)
+    pairs takes the tiled kernel over its pairs in (token outer, slot inner)
+    order (compute.rs:2011-2080); the other pairs take the row vec_dot.  Both
+    are the oracle's MUL_MAT routes on the gathered activation rows (Q8_K from
+    quantize_row_q8_K_ref in both)."""
+    dst = np.zeros((ne12, n_ids, rows), dtype=np.float32)
+    by_e = [[] for _ in range(n_as)]
+    for t in range(ne12):
+        for s in range(n_ids):
+            by_e[int(ids[t, s])].append((s, t))
+    for e, pairs in enumerate(by_e):
+        if not pairs:
+            continue
+        x = np.stack([y[t, s % ne11] for s, t in pairs])
+        if len(pairs) >= 8:
+            out, route, _ = O.mul_mat(ty, xq[e], n, rows, x, len(pairs))
+            assert route == O.ROUTE_TILED
+        else:
+            out = np.stack([O.mul_mat(ty, xq[e], n, rows, x[i:i + 1], 1)[0][0] for i in range(len(pairs))])
+        for i, (s, t) in enumerate(pairs):
+            dst[t, s] = out[i]
+    return dst
+
+
+def test_tiled_mul_mat_id_bit_exact():
+    """tiled.rs:2205 tiled_mulmat_id_matches_reference_bit_exact for Q4_K, Q5_K and
+    Q6_K experts (140 rows each, 5 experts, 4 of 16 tokens' slots routed)."""
+    secs = fx.tiled_sections(kind=1)
+    assert sorted(s[0] for s in secs) == [O.Q4_K, O.Q5_K, O.Q6_K]
+    for tid, n, rows, ne11, n_as, n_ids, ne12, xq, y, ids, dst in secs:
+        got = mul_mat_id_kquant(tid, xq, n, rows, ne11, n_as, n_ids, ne12, y, ids)
+        assert np.array_equal(got.view(np.uint32), dst.view(np.uint32)), f"mmid type {tid}"
+
+
+@pytest.mark.parametrize("name", fx.REAL_WEIGHT_DUMPS)
+def test_real_weight_dumps_bit_exact(name):
+    """vec_dot.rs:2798-2870 kquant_real_tensor_dump_vs_reference: real GGUF
+    tensors through the reference's production route (the Q4_K 8x8 repack gemv
+    where the tensor got the repack trait, else the row vec_dot), bit for bit,
+    and the Q8_K activation bytes of the K-quants."""
+    d = fx.real_weight_dump(name)
+    ty, n, rows, cols = d["type"], d["n"], d["rows"], d["cols"]
+    out, route, _ = O.mul_mat(ty, d["xq"], n, rows, d["act"], cols)
+    assert route == (O.ROUTE_REPACK if d["flags"] & 1 else O.ROUTE_VECDOT)
+    assert np.array_equal(out.view(np.uint32), d["want"].view(np.uint32)), name
+    if ty in (O.Q4_K, O.Q5_K, O.Q6_K):
+        q8 = np.concatenate([O.quantize(O.Q8_K, d["act"][c], kind="quantize_row_q8_K_ref") for c in range(cols)])
+        assert np.array_equal(q8, d["q8k"]), name
 
 
 def test_q4k_repack_dump_bit_exact():
@@ -345,16 +432,3 @@ def test_flash_attn_against_float64():
             p = np.exp(s - s.max(1, keepdims=True))
             ref[:, h] = (p / p.sum(1, keepdims=True)) @ vv
         assert np.max(np.abs(out - ref)) < 2e-3
-    if t == O.Q5_K:
-        # {iacc, imin} per super-block rebuild the float64 dot exactly:
-        # sum_b da_b * (d_b * iacc_b - dmin_b * imin_b)
-        ab = np.frombuffer(act.tobytes(), dtype=np.uint8).reshape(n // 256, 292)
-        da = ab[:, :4].copy().view(np.float32).reshape(-1).astype(np.float64)
-        for r in range(rows):
-            d = wv[r, :, 0:2].copy().view(np.float16).reshape(-1).astype(np.float64)
-            dmin = wv[r, :, 2:4].copy().view(np.float16).reshape(-1).astype(np.float64)
-            ia, im = sub[0, r, :, 0].astype(np.float64), sub[0, r, :, 1].astype(np.float64)
-            got = float(np.sum(da * (d * ia - dmin * im)))
-            wf = O.dequantize(t, w[r * O.row_size(t, n):(r + 1) * O.row_size(t, n)], n).astype(np.float64)
-            ref = float(np.dot(wf, aq))
-            assert abs(got - ref) <= 1e-9 * max(abs(ref), 1.0), (r, got, ref)

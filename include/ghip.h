@@ -122,6 +122,18 @@ int ghip_supports_op(int op, const ghip_tensor *dst, const ghip_tensor *const *s
 ghip_status ghip_mul_mat(ghip_context *ctx, const ghip_tensor *src0, const ghip_tensor *src1,
                          const ghip_tensor *dst, void *stream);
 
+/* ghip_mul_mat without any allocation.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * operands, kernels and results as ghip_mul_mat; the scratch is a fixed
+ * 32 MiB array in this library's code object, one per GPU, held until the
+ * process ends.  A call needing more scratch (e.g. the Q6_K prefill GEMM's
+ * per-call weight repack of a large matrix) fails with
+ * GHIP_STATUS_ALLOC_FAILED.  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams, other contexts) race. */
+ghip_status ghip_mul_mat_noalloc(ghip_context *ctx, const ghip_tensor *src0, const ghip_tensor *src1,
+                                 const ghip_tensor *dst, void *stream);
+
 /* Parity hook with no reference counterpart (the reference exposes these
  * integers only inside its kernels, e.g. repack.rs:1664-1680): writes the exact
  * int32 partials ghip_mul_mat forms, per (activation row c, weight row r,

@@ -51,10 +51,14 @@ def build_kernels():
 
 
 def build_host():
+    """libghip.so: the host library (g++) plus ghip_noalloc.hip (hipcc), whose
+    code object carries the fixed scratch array of ghip_mul_mat_noalloc."""
     out = os.path.join(HERE, "libghip.so")
+    obj = os.path.join(HERE, "ghip_noalloc.o")
+    _run([HIPCC, "-c", "-fPIC", *DEVICE_FLAGS, "-I", CSRC, os.path.join(CSRC, "ghip_noalloc.hip"), "-o", obj])
     _run(["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wno-unused-result", "-D__HIP_PLATFORM_AMD__",
           "-I", os.path.join(ROCM, "include"), "-I", os.path.join(ROOT, "include"),
-          os.path.join(CSRC, "ghip.cpp"), "-o", out,
+          os.path.join(CSRC, "ghip.cpp"), obj, "-o", out,
           "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-ldl", "-Wl,-rpath," + os.path.join(ROCM, "lib")])
 
 

@@ -1,6 +1,7 @@
 // ghip.cpp -- host side of the gfx950 backend: code-object loading, operand
 // validation, workspace management and kernel dispatch behind include/ghip.h.
 #include "../../include/ghip.h"
+#include "ghip_internal.h"
 
 #include <hip/hip_runtime.h>
 
@@ -457,8 +458,14 @@ size_t mul_mat_ws_bytes(const MulMatPlan &p, bool has_dst, bool act_out, size_t 
 }
 
 ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b, const ghip_tensor *d,
-                         int32_t *sub, void *act_out, void *stream) {
+                         int32_t *sub, void *act_out, void *stream, void *fixed_ws = nullptr, size_t fixed_bytes = 0) {
     std::lock_guard<std::mutex> lock(ctx->mu);
+    // a fixed scratch serves this call only
+    struct CallScratch {
+        ghip_context *c;
+        CallScratch(ghip_context *c_, void *p, size_t n) : c(c_) { c->call_ws = p; c->call_ws_size = n; }
+        ~CallScratch() { c->call_ws = nullptr; c->call_ws_size = 0; }
+    } call_scratch(ctx, fixed_ws, fixed_bytes);
     MulMatPlan p;
     ghip_status st;
     if (!plan_mul_mat(ctx, a, b, d, p, st)) return st;
@@ -1048,8 +1055,11 @@ ghip_status ghip_init(int device, ghip_context **out) {
     if (hipSetDevice(device) != hipSuccess) return GHIP_STATUS_BACKEND_ERROR;
     ghip_context *ctx = new ghip_context();
     ctx->device = device;
-    if (hipEventCreateWithFlags(&ctx->order_ev, hipEventDisableTiming) != hipSuccess) {
+    const char *why = "";
+    if (ghip_noalloc_setup(device, &why) != GHIP_STATUS_SUCCESS ||
+        hipEventCreateWithFlags(&ctx->order_ev, hipEventDisableTiming) != hipSuccess) {
         (void)hipGetLastError();
+        fprintf(stderr, "ghip: init on device %d failed: %s\n", device, *why ? why : "hipEventCreate failed");
         delete ctx;
         return GHIP_STATUS_BACKEND_ERROR;
     }
@@ -1121,6 +1131,19 @@ ghip_status ghip_mul_mat(ghip_context *ctx, const ghip_tensor *src0, const ghip_
     if (!dst) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: null dst");
     return mul_mat_impl(ctx, src0, src1, dst, nullptr, nullptr, stream);
 }
+
+}  // extern "C"
+
+ghip_status ghip_mul_mat_fixed_scratch(ghip_context *ctx, const ghip_tensor *src0, const ghip_tensor *src1,
+                                       const ghip_tensor *dst, void *scratch, size_t bytes, void *stream) {
+    if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
+    if (!dst) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: null dst");
+    return mul_mat_impl(ctx, src0, src1, dst, nullptr, nullptr, stream, scratch, bytes);
+}
+int ghip_context_device(const ghip_context *ctx) { return ctx ? ctx->device : -1; }
+ghip_status ghip_context_fail(ghip_context *ctx, ghip_status st, const char *msg) { return ctx->fail(st, "%s", msg); }
+
+extern "C" {
 
 ghip_status ghip_mul_mat_subsums(ghip_context *ctx, const ghip_tensor *src0, const ghip_tensor *src1,
                                  int32_t *subsums, void *stream) {

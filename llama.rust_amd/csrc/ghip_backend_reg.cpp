@@ -94,6 +94,7 @@ void *reg_proc_address(const ggml_hip_backend_reg *, const char *name) {
         {"ghip_synchronize", (void *)&ghip_synchronize},
         {"ghip_supports_op", (void *)&ghip_supports_op},
         {"ghip_mul_mat", (void *)&ghip_mul_mat},
+        {"ghip_mul_mat_noalloc", (void *)&ghip_mul_mat_noalloc},
         {"ghip_mul_mat_subsums", (void *)&ghip_mul_mat_subsums},
         {"ghip_mul_mat_act", (void *)&ghip_mul_mat_act},
         {"ghip_mul_mat_id", (void *)&ghip_mul_mat_id},

@@ -355,13 +355,36 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
 // MFMA GEMM runs on 128 x 128 tiles.
 constexpr size_t kGemmSmem128 = 116224, kGemmSmem64 = 76544;  // sizeof(g3::Smem<BM>) in ghip_gemm.hip
 constexpr size_t kGemmSmemQ6 = 140032;                         // sizeof(g6::Smem) in ghip_gemm.hip
-// token tile: 64 (two workgroups per CU) unless GHIP_GEMM_BM=128
+constexpr size_t kGemmSmemW8 = 148480;  // 2 * sizeof(g4::Stage<256>) in ghip_gemm.hip
+// GHIP_GEMM_BM=128 selects the 128 x 128 tiles of gemm_q4K_impl
 int gemm_bm() { return env_int("GHIP_GEMM_BM", 64) == 128 ? 128 : 64; }
+// Q4_K GEMM kernel: tile (tokens x rows), threads, LDS bytes
+struct GemmKernel {
+    const char *name, *name_sub, *name_multi;
+    int bm, bn, threads;
+    size_t smem;
+};
+const GemmKernel kGemmW8 = {"ghip_gemm_q4_K_w8", "ghip_gemm_q4_K_w8_sub", "ghip_gemm_q4_K_w8_multi", 128, 256, 512,
+                            kGemmSmemW8};
+const GemmKernel kGemmM64 = {"ghip_gemm_q4_K_m64", "ghip_gemm_q4_K_m64_sub", "ghip_gemm_q4_K_m64_multi", 64, 128, 256,
+                             kGemmSmem64};
+const GemmKernel kGemmM128 = {"ghip_gemm_q4_K", "ghip_gemm_q4_K_sub", nullptr, 128, 128, 512, kGemmSmem128};
+int64_t gemm_tiles(const GemmKernel &k, int64_t M, int64_t N) { return ((M + k.bm - 1) / k.bm) * ((N + k.bn - 1) / k.bn); }
+// The wide 128 x 256 tiles (one workgroup of 8 wavefronts per CU) when they
+// give at least half a wave of workgroups; otherwise 64 x 128 tiles (two per
+// CU) with split K.  GHIP_GEMM_KERNEL=w8|m64|m128 forces one.
+const GemmKernel &gemm_kernel(int64_t M, int64_t N) {
+    const char *v = getenv("GHIP_GEMM_KERNEL");
+    const std::string k = v ? v : "";
+    if (k == "w8") return kGemmW8;
+    if (k == "m64") return kGemmM64;
+    if (k == "m128" || gemm_bm() == 128) return kGemmM128;
+    return gemm_tiles(kGemmW8, M, N) >= 128 ? kGemmW8 : kGemmM64;
+}
 // K slices for grids that would leave CUs idle (fewer than 128 tiles); the
 // slices' partial sums are added in order by ghip_gemm_splitk_reduce
 int gemm_nsplit(const MulMatPlan &p) {
-    const int bm = gemm_bm();
-    const int64_t tiles = ((p.M + bm - 1) / bm) * ((p.N + 127) / 128);
+    const int64_t tiles = gemm_tiles(gemm_kernel(p.M, p.N), p.M, p.N);
     if (tiles >= 128 || p.N % 4) return 1;
     const int64_t want = (256 + tiles - 1) / tiles;
     const int64_t nbs = (p.nb + want - 1) / want;  // super-blocks per slice
@@ -387,8 +410,8 @@ size_t gemm_layout_bytes(const MulMatPlan &p) {
 }
 // Q6_K: repack the weights into aligned records, lay the codes out as f16, then
 // the f16-MFMA GEMM on 64 x 128 tiles (one workgroup per CU, 137 KB of LDS)
-ghip_status run_gemm_q6k(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, float *dst,
-                         int64_t ldd, int32_t *sub, void *layout_ws, hipStream_t s) {
+ghip_status run_gemm_q6k(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act,
+                         const ghip_tensor *bf, float *dst, int64_t ldd, int32_t *sub, void *layout_ws, hipStream_t s) {
     size_t codes_b, dt_b;
     gemm_q6k_bytes(p, &codes_b, &dt_b);
     const int64_t Mpad = (p.M + 127) / 128 * 128, nbk = p.K / 256;
@@ -399,8 +422,13 @@ ghip_status run_gemm_q6k(ghip_context *ctx, const MulMatPlan &p, const void *w, 
     ghip_status st = ctx->launch("ghip_q6K_repack", dim3((unsigned)((nblk + 3) / 4)), dim3(256), 0, s,
                                  (const uint8_t *)w, (int64_t)p.w_row_bytes, (int)p.N, (int)nbk, rep);
     if (st != GHIP_STATUS_SUCCESS) return st;
-    st = ctx->launch("ghip_gemm_act_layout_f16", dim3((unsigned)((p.M * nbk + 3) / 4)), dim3(256), 0, s, act,
-                     (int64_t)p.act_row_bytes, (int)p.M, (int)Mpad, (int)nbk, codes, dT);
+    if (bf)  // f32 activations: quantized straight into the layout
+        st = ctx->launch("ghip_gemm_act_q8K_f16", dim3((unsigned)((p.M * nbk + 3) / 4)), dim3(256), 0, s,
+                         (const float *)bf->data, (int64_t)bf->nb[1] / 4, (int)p.M, (int)Mpad, (int)nbk, (int)p.n_mat,
+                         codes, dT);
+    else
+        st = ctx->launch("ghip_gemm_act_layout_f16", dim3((unsigned)((p.M * nbk + 3) / 4)), dim3(256), 0, s, act,
+                         (int64_t)p.act_row_bytes, (int)p.M, (int)Mpad, (int)nbk, codes, dT);
     if (st != GHIP_STATUS_SUCCESS) return st;
     const unsigned grid = (unsigned)(((p.M + 63) / 64) * ((p.N + 127) / 128));
     return ctx->launch(sub ? "ghip_gemm_q6_K_sub" : "ghip_gemm_q6_K", dim3(grid), dim3(256), kGemmSmemQ6, s,
@@ -408,28 +436,31 @@ ghip_status run_gemm_q6k(ghip_context *ctx, const MulMatPlan &p, const void *w, 
                        (int)Mpad, dst, ldd, sub);
 }
 
-ghip_status run_gemm(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, float *dst,
-                     int64_t ldd, int32_t *sub, void *layout_ws, hipStream_t s) {
-    if (p.wtype == GHIP_TYPE_Q6_K) return run_gemm_q6k(ctx, p, w, act, dst, ldd, sub, layout_ws, s);
+// act: Q8_K rows (bf == nullptr), or bf: the f32 activations, quantized
+// straight into the GEMM layout
+ghip_status run_gemm(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, const ghip_tensor *bf,
+                     float *dst, int64_t ldd, int32_t *sub, void *layout_ws, hipStream_t s) {
+    if (p.wtype == GHIP_TYPE_Q6_K) return run_gemm_q6k(ctx, p, w, act, bf, dst, ldd, sub, layout_ws, s);
     const int64_t Mpad = (p.M + 127) / 128 * 128, K = p.K, nbk = p.K / 256;
     int8_t *codes = (int8_t *)layout_ws;
     uint16_t *bsT = (uint16_t *)(codes + Mpad * K);
     float *dT = (float *)(bsT + nbk * Mpad * 16);
     const unsigned lgrid = (unsigned)((p.M * nbk + 3) / 4);
-    ghip_status st = ctx->launch("ghip_gemm_act_layout", dim3(lgrid), dim3(256), 0, s, act, (int64_t)p.act_row_bytes,
-                                 (int)p.M, (int)Mpad, (int)nbk, codes, bsT, dT);
+    ghip_status st =
+        bf ? ctx->launch("ghip_gemm_act_q8K", dim3(lgrid), dim3(256), 0, s, (const float *)bf->data,
+                         (int64_t)bf->nb[1] / 4, (int)p.M, (int)Mpad, (int)nbk, (int)p.n_mat, codes, bsT, dT)
+           : ctx->launch("ghip_gemm_act_layout", dim3(lgrid), dim3(256), 0, s, act, (int64_t)p.act_row_bytes,
+                         (int)p.M, (int)Mpad, (int)nbk, codes, bsT, dT);
     if (st != GHIP_STATUS_SUCCESS) return st;
-    const int bm = gemm_bm();
-    const unsigned grid = (unsigned)(((p.M + bm - 1) / bm) * ((p.N + 127) / 128));
+    const GemmKernel &gk = gemm_kernel(p.M, p.N);
+    const unsigned grid = (unsigned)gemm_tiles(gk, p.M, p.N);
     const int ns = gemm_nsplit(p);
     const int nbs = (int)((p.nb + ns - 1) / ns);
     float *part = ns > 1 ? (float *)((uint8_t *)layout_ws +
                                      (((size_t)Mpad * K + nbk * Mpad * 32 + nbk * Mpad * 4 + 255) & ~(size_t)255))
                          : dst;
     const int64_t zstride = ns > 1 ? p.M * p.N : 0;
-    const char *kn = bm == 128 ? (sub ? "ghip_gemm_q4_K_sub" : "ghip_gemm_q4_K")
-                               : (sub ? "ghip_gemm_q4_K_m64_sub" : "ghip_gemm_q4_K_m64");
-    st = ctx->launch(kn, dim3(grid, ns), dim3(bm * 4), bm == 128 ? kGemmSmem128 : kGemmSmem64, s,
+    st = ctx->launch(sub ? gk.name_sub : gk.name, dim3(grid, ns), dim3(gk.threads), gk.smem, s,
                      (const uint8_t *)w, (int64_t)p.w_row_bytes, (int)p.N, (int)p.nb, (const int8_t *)codes,
                      (const uint16_t *)bsT, (const float *)dT, (int)p.M, (int)Mpad, part,
                      ns > 1 ? (int64_t)p.N : (int64_t)ldd, sub, nbs, zstride);
@@ -450,8 +481,10 @@ bool use_gemm(const MulMatPlan &p) {
 // workspace of one MUL_MAT: [quantized activations | GEMM layout | f32
 // scratch output when only sub-sums are wanted]
 size_t mul_mat_ws_bytes(const MulMatPlan &p, bool has_dst, bool act_out, size_t *act_b, size_t *lay_b) {
-    const size_t act_bytes = p.act_pre ? 0 : ((size_t)(p.M * p.act_row_bytes) + 255) & ~(size_t)255;
-    const size_t lay_bytes = !act_out && use_gemm(p) ? gemm_layout_bytes(p) : 0;
+    // (the GEMM quantizes f32 activations straight into its layout)
+    const bool gemm = !act_out && use_gemm(p);
+    const size_t act_bytes = p.act_pre || gemm ? 0 : ((size_t)(p.M * p.act_row_bytes) + 255) & ~(size_t)255;
+    const size_t lay_bytes = gemm ? gemm_layout_bytes(p) : 0;
     if (act_b) *act_b = act_bytes;
     if (lay_b) *lay_b = lay_bytes;
     return (act_out ? 0 : act_bytes) + lay_bytes + (has_dst || act_out ? 0 : (size_t)(p.M * p.N * 4));
@@ -490,15 +523,8 @@ ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_ten
     void *lay = lay_bytes ? (void *)((uint8_t *)ws + act_bytes) : nullptr;
     float *dst = d ? (float *)d->data : (float *)((uint8_t *)ws + act_bytes + lay_bytes);
     const int64_t ldd = d ? (int64_t)d->nb[1] / 4 : p.N;
-    if (use_gemm(p)) {
-        if (!p.act_pre) {
-            st = quantize_act(ctx, p, b, act, s);
-            if (st != GHIP_STATUS_SUCCESS) return st;
-        } else {
-            act = b->data;
-        }
-        return run_gemm(ctx, p, a->data, (const uint8_t *)act, dst, ldd, sub, lay, s);
-    }
+    if (use_gemm(p))
+        return run_gemm(ctx, p, a->data, (const uint8_t *)b->data, p.act_pre ? nullptr : b, dst, ldd, sub, lay, s);
     if (p.act_pre) return run_gemv(ctx, p, a->data, (const uint8_t *)b->data, p.act_row_bytes, false, dst, ldd, sub, s);
     // Q8_0 quantization fused into the block-pair kernels for up to 4096 weight
     // rows: every workgroup then quantizes its lanes' blocks itself, which
@@ -776,7 +802,8 @@ bool multi_candidate(const ghip_node &n) {
     if (b->ne[1] > (a->type == GHIP_TYPE_Q6_K ? 1 : 8) && b->ne[1] < env_int("GHIP_GEMM_MIN_ROWS", 16))
         return false;
     if (b->ne[1] >= env_int("GHIP_GEMM_MIN_ROWS", 16))  // the prefill GEMM's range: Q4_K, 64-token tiles
-        return a->type == GHIP_TYPE_Q4_K && gemm_bm() == 64 && b->ne[1] <= INT32_MAX;
+        return a->type == GHIP_TYPE_Q4_K && gemm_bm() == 64 && b->ne[1] <= INT32_MAX &&
+               std::string(getenv("GHIP_GEMM_KERNEL") ? getenv("GHIP_GEMM_KERNEL") : "") != "m128";
     if (a->ne[2] != 1 || a->ne[3] != 1) return false;
     return env_int("GHIP_GEMV_RB", 2) == 2 && env_int("GHIP_GEMV_NG", 2) == 2;
 }
@@ -825,21 +852,25 @@ ghip_status mul_mat_multi_gemm(ghip_context *ctx, const ghip_node *nodes, int n,
     if (st != GHIP_STATUS_SUCCESS) return st;
     const MulMatPlan &p0 = p[0];
     const int64_t Mpad = (p0.M + 127) / 128 * 128, K = p0.K, nbk = p0.K / 256;
-    const size_t act_bytes = ((size_t)(p0.M * p0.act_row_bytes) + 255) & ~(size_t)255;
     const size_t lay_bytes = (size_t)Mpad * K + (size_t)nbk * Mpad * 32 + (size_t)nbk * Mpad * 4;
     void *ws = nullptr;
-    st = ctx->workspace(act_bytes + lay_bytes, s, &ws);
+    st = ctx->workspace(lay_bytes, s, &ws);
     if (st != GHIP_STATUS_SUCCESS) return st;
-    st = quantize_act(ctx, p0, nodes[0].src[1], ws, s);
-    if (st != GHIP_STATUS_SUCCESS) return st;
-    int8_t *codes = (int8_t *)ws + act_bytes;
+    int8_t *codes = (int8_t *)ws;
     uint16_t *bsT = (uint16_t *)(codes + Mpad * K);
     float *dT = (float *)(bsT + nbk * Mpad * 16);
-    st = ctx->launch("ghip_gemm_act_layout", dim3((unsigned)((p0.M * nbk + 3) / 4)), dim3(256), 0, s,
-                     (const uint8_t *)ws, (int64_t)p0.act_row_bytes, (int)p0.M, (int)Mpad, (int)nbk, codes, bsT, dT);
+    const ghip_tensor *bf = nodes[0].src[1];
+    st = ctx->launch("ghip_gemm_act_q8K", dim3((unsigned)((p0.M * nbk + 3) / 4)), dim3(256), 0, s,
+                     (const float *)bf->data, (int64_t)bf->nb[1] / 4, (int)p0.M, (int)Mpad, (int)nbk, (int)p0.n_mat,
+                     codes, bsT, dT);
     if (st != GHIP_STATUS_SUCCESS) return st;
     GemmMulti g{};
-    const int tiles_m = (int)((p0.M + 63) / 64);
+    // the wide tiles when the group's tiles fill half a wave of workgroups
+    int64_t wide_tiles = 0;
+    for (int i = 0; i < n; i++) wide_tiles += gemm_tiles(kGemmW8, p0.M, p[i].N);
+    const char *force = getenv("GHIP_GEMM_KERNEL");
+    const bool wide = force && *force ? std::string(force) == "w8" : wide_tiles >= 128;
+    const GemmKernel &gk = wide ? kGemmW8 : kGemmM64;
     int t = 0;
     for (int i = 0; i < n; i++) {
         g.W[i] = (const uint8_t *)nodes[i].src[0]->data;
@@ -847,7 +878,7 @@ ghip_status mul_mat_multi_gemm(ghip_context *ctx, const ghip_node *nodes, int n,
         g.ldd[i] = (int64_t)nodes[i].dst->nb[1] / 4;
         g.N[i] = (int)p[i].N;
         g.t0[i] = t;
-        t += tiles_m * (int)((p[i].N + 127) / 128);
+        t += (int)gemm_tiles(gk, p0.M, p[i].N);
     }
     for (int i = n; i < 4; i++) {
         g.W[i] = g.W[0];
@@ -858,7 +889,7 @@ ghip_status mul_mat_multi_gemm(ghip_context *ctx, const ghip_node *nodes, int n,
     }
     g.n = n;
     g.total = t;
-    return ctx->launch("ghip_gemm_q4_K_m64_multi", dim3((unsigned)t), dim3(256), kGemmSmem64, s, g,
+    return ctx->launch(gk.name_multi, dim3((unsigned)t), dim3(gk.threads), gk.smem, s, g,
                        (int64_t)p0.w_row_bytes, (int)nbk, (const int8_t *)codes, (const uint16_t *)bsT,
                        (const float *)dT, (int)p0.M, (int)Mpad);
 }

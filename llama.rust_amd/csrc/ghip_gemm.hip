@@ -14,6 +14,7 @@
 // imin is a K=16 contraction of mn (<= 63) with bsum16 (|.| <= 2032), both
 // exact in fp16, with sums < 2^24: one v_mfma_f32_32x32x16_f16 per tile, exact.
 #include "ghip_common.h"
+#include "ghip_q8k.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -322,6 +323,231 @@ extern "C" __global__ void __launch_bounds__(256, 2)
                              nb, 0, id - g.t0[i]);
 }
 
+// ------------------------------------------------------------ wide Q4_K tiles
+// The same arithmetic as gemm_q4K_impl on wider wavefront tiles: every
+// wavefront owns 128 tokens x 32 weight rows (four 32 x 32 MFMA tiles per
+// plane), so one nibble expansion and one header decode feed four token
+// tiles.  A workgroup of NW wavefronts covers 128 tokens x 32*NW rows; its
+// operands arrive by buffer loads straight into LDS (addresses are per-lane
+// 32-bit offsets fixed for the whole loop plus a scalar per super-block
+// offset, so the loop spends no vector instructions on them), two stages.
+// Reads past the end of a buffer return zero, so rows past N need no clamp.
+namespace g4 {
+constexpr int BM = 128;
+template <int BN> struct Stage {
+    uint8_t act[BM * 256];  // [token][256], 16-byte slots swizzled by token % 16
+    uint8_t wraw[BN * 128]; // [row][128] Q4_K qs, 16-byte slots swizzled by row % 8
+    uint8_t hdr[BN * 16];   // [row] d, dmin, 12 scale bytes
+    _Float16 bs[BM * 16];   // [token][16] bsum16
+    float da[BM];           // block scale per token
+};
+}  // namespace g4
+typedef __amdgpu_buffer_rsrc_t brsrc;
+DEV brsrc make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+}
+DEV void b2lds(brsrc r, void *lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 16, voff, soff, 0, 0);
+}
+
+template <int NW, bool SUBSUMS>
+__device__ __forceinline__ void gemm_q4K_wide_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb,
+                                                   const int8_t *__restrict__ codes,
+                                                   const _Float16 *__restrict__ bsT, const float *__restrict__ dT,
+                                                   int M, int Mpad, float *__restrict__ dst, int64_t ldd,
+                                                   int32_t *__restrict__ sub, int nbs, int64_t zstride, int tile) {
+    constexpr int BM = g4::BM, BN = 32 * NW;
+    constexpr int APW = 32 / NW;  // activation pieces (1 KB) per wavefront
+    const int b0 = blockIdx.y * nbs, b1 = min(nb, b0 + nbs);
+    dst += blockIdx.y * zstride;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
+    g4::Stage<BN> *stg = reinterpret_cast<g4::Stage<BN> *>(smem_raw);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane & 31, h = lane >> 5;
+    const int K = nb * QK_K;
+    const int rb = (int)w_row_bytes;
+
+    const int n_tiles_m = (M + BM - 1) / BM, n_tiles_n = (N + BN - 1) / BN;
+    const int total = n_tiles_m * n_tiles_n;
+    int id = tile;
+    if (id < 0) {
+        id = blockIdx.x;
+        if (total % 8 == 0) id = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+    }
+    const int m0 = (id % n_tiles_m) * BM;
+    const int n0 = (id / n_tiles_m) * BN;
+
+    // buffer windows: this tile's activation rows, weight rows (to the end
+    // of the matrix), bsum16 and block-scale planes
+    const brsrc ra = make_rsrc(codes + (int64_t)m0 * K, (uint32_t)BM * (uint32_t)K);
+    const brsrc rw = make_rsrc(W + (int64_t)n0 * w_row_bytes, (uint32_t)min(BN, N - n0) * (uint32_t)rb);
+    const brsrc rs = make_rsrc(bsT + (int64_t)m0 * 16, (uint32_t)((int64_t)nb * Mpad * 32 - (int64_t)m0 * 32));
+    const brsrc rd = make_rsrc(dT + m0, (uint32_t)((int64_t)nb * Mpad * 4 - (int64_t)m0 * 4));
+    // per-lane offsets: activation piece p holds tokens 4p .. 4p+3; weight
+    // piece q rows 8q .. 8q+7; header piece r rows 64r .. 64r+63
+    uint32_t aoff[APW];
+#pragma unroll
+    for (int i = 0; i < APW; i++) {
+        const int tok = 4 * (APW * wave + i) + (lane >> 4);
+        aoff[i] = (uint32_t)tok * (uint32_t)K + 16u * (uint32_t)((lane & 15) ^ (tok & 15));
+    }
+    // (the row goes into the per-lane offset, which the buffer's range check
+    // covers, so rows past N read zero)
+    uint32_t woff[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        woff[i] = (uint32_t)(32 * wave + 8 * i + (lane >> 3)) * (uint32_t)rb + 16u +
+                  16u * (uint32_t)((lane & 7) ^ ((lane >> 3) & 7));
+    const uint32_t hoff = (uint32_t)(64 * wave + lane) * (uint32_t)rb;  // header piece `wave`
+    // bsum16 pieces wave - NW/2 and wave + NW/2
+    const uint32_t soff[2] = {1024u * (uint32_t)(wave - NW / 2) + 16u * (uint32_t)lane,
+                              1024u * (uint32_t)(wave + NW / 2) + 16u * (uint32_t)lane};
+    const uint32_t doff = 16u * (uint32_t)lane;
+    auto issue = [&](int b) {
+        g4::Stage<BN> &S = stg[(b - b0) & 1];
+#pragma unroll
+        for (int i = 0; i < APW; i++) b2lds(ra, S.act + 1024 * (APW * wave + i), aoff[i], (uint32_t)b * 256u);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            b2lds(rw, S.wraw + 1024 * (4 * wave + i), woff[i], (uint32_t)b * 144u);
+        // NW/2 header pieces, then 4 bsum16 pieces: piece e by wavefront e % NW
+#pragma unroll
+        for (int e = wave; e < NW / 2 + 4; e += NW) {
+            if (e < NW / 2) b2lds(rw, S.hdr + 1024 * e, hoff, (uint32_t)b * 144u);
+            else b2lds(rs, reinterpret_cast<uint8_t *>(S.bs) + 1024 * (e - NW / 2), soff[e >= NW], (uint32_t)b * (uint32_t)Mpad * 32u);
+        }
+        if (wave == NW - 1 && lane < BM / 4) b2lds(rd, S.da, doff, (uint32_t)b * (uint32_t)Mpad * 4u);
+    };
+
+    v16i acc_h[4], acc_l[4];
+    v16f out[4];
+#pragma unroll
+    for (int tm = 0; tm < 4; tm++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) out[tm][v] = 0.0f;
+
+    const int wr = 32 * wave + li;  // this lane's weight row in the tile (B column)
+    const uint32_t raw_off0 = (uint32_t)wr * 128, wsw = (uint32_t)(wr & 7);
+    const uint32_t asw = (uint32_t)(li & 15);
+
+    if (b0 < b1) issue(b0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int b = b0; b < b1; b++) {
+        if (b + 1 < b1) issue(b + 1);
+        const g4::Stage<BN> &S = stg[(b - b0) & 1];
+        const uint4 hv = *reinterpret_cast<const uint4 *>(S.hdr + 16 * wr);
+        const float dw = h2f(hv.x), dmin = h2f(hv.x >> 16);
+        v8h Bm;
+        {
+            int s0, s1, s2, s3, mA, mB, mC, mD;
+            k4_scales(hv.y, hv.z, hv.w, scale_sel(0), s0, s1, mA, mB);
+            k4_scales(hv.y, hv.z, hv.w, scale_sel(2), s2, s3, mC, mD);
+            int e0, e1, e2, e3, mE, mF, mG, mH;
+            k4_scales(hv.y, hv.z, hv.w, scale_sel(1), e0, e1, mE, mF);
+            k4_scales(hv.y, hv.z, hv.w, scale_sel(3), e2, e3, mG, mH);
+            (void)s0; (void)s1; (void)s2; (void)s3; (void)e0; (void)e1; (void)e2; (void)e3;
+            // mins of sub-blocks 4h .. 4h+3 at k = 8h .. 8h+7, each twice
+            const int q0 = h ? mC : mA, q1 = h ? mD : mB, q2 = h ? mG : mE, q3 = h ? mH : mF;
+            Bm[0] = Bm[1] = (_Float16)(float)q0;
+            Bm[2] = Bm[3] = (_Float16)(float)q1;
+            Bm[4] = Bm[5] = (_Float16)(float)q2;
+            Bm[6] = Bm[7] = (_Float16)(float)q3;
+        }
+        const v4i zi = {};
+        (void)zi;
+        const v16i z16 = {};
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint4 raw = *reinterpret_cast<const uint4 *>(S.wraw + raw_off0 + 16 * ((2 * c + h) ^ wsw));
+            int sa, sb2, mu0, mu1;
+            k4_scales(hv.y, hv.z, hv.w, scale_sel(c), sa, sb2, mu0, mu1);
+            (void)mu0; (void)mu1;
+            const uint32_t rwv[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+            for (int nh = 0; nh < 2; nh++) {
+                const int ks = 2 * c + nh;
+                const uint32_t sv = (uint32_t)(nh ? sb2 : sa);
+                const uint32_t slo = sv & 7u, shi = sv >> 3;
+                v4i blo, bhi;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t nib = nh ? ((rwv[e] >> 4) & 0x0f0f0f0fu) : (rwv[e] & 0x0f0f0f0fu);
+                    blo[e] = (int)mul_bytes(nib, slo);
+                    bhi[e] = (int)mul_bytes(nib, shi);
+                }
+#pragma unroll
+                for (int tm = 0; tm < 4; tm++) {
+                    const v4i a = *reinterpret_cast<const v4i *>(S.act + (32 * tm + li) * 256 + 16 * ((2 * ks + h) ^ asw));
+                    acc_l[tm] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, blo, ks == 0 ? z16 : acc_l[tm], 0, 0, 0);
+                    acc_h[tm] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bhi, ks == 0 ? z16 : acc_h[tm], 0, 0, 0);
+                }
+            }
+        }
+        // ---- min term and scaling
+        const v16f zf = {};
+#pragma unroll
+        for (int tm = 0; tm < 4; tm++) {
+            const int tl = 32 * tm;
+            const v8h Am = *reinterpret_cast<const v8h *>(&S.bs[(tl + li) * 16 + 8 * h]);
+            const v16f accm = __builtin_amdgcn_mfma_f32_32x32x16_f16(Am, Bm, zf, 0, 0, 0);
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 d4 = *reinterpret_cast<const float4 *>(&S.da[tl + 8 * g + 4 * h]);
+                const float dav[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int v = 4 * g + r;
+                    const int iacc = (acc_h[tm][v] << 3) + acc_l[tm][v];
+                    const float im = accm[v];
+                    if (SUBSUMS) {
+                        const int ml = tl + crow(v, lane);
+                        if (m0 + ml < M && n0 + wr < N) {
+                            int32_t *sp = sub + (((int64_t)(m0 + ml) * N + (n0 + wr)) * nb + b) * 2;
+                            sp[0] = iacc;
+                            sp[1] = (int)im;
+                        }
+                    }
+                    const float t = fmaf(dw, (float)iacc, -(dmin * im));
+                    out[tm][v] = fmaf(dav[r], t, out[tm][v]);
+                }
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+    const int n = n0 + wr;
+#pragma unroll
+    for (int tm = 0; tm < 4; tm++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int m = m0 + 32 * tm + crow(v, lane);
+            if (m < M && n < N) dst[(int64_t)m * ldd + n] = out[tm][v];
+        }
+}
+
+#define GEMM_WIDE_KERNELS(NAME, NW, LB)                                                                           \
+    extern "C" __global__ void __launch_bounds__(64 * NW, LB)                                                     \
+        NAME(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb, const int8_t *__restrict__ codes,  \
+             const _Float16 *__restrict__ bsT, const float *__restrict__ dT, int M, int Mpad,                      \
+             float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub, int nbs, int64_t zstride) {          \
+        gemm_q4K_wide_impl<NW, false>(W, w_row_bytes, N, nb, codes, bsT, dT, M, Mpad, dst, ldd, sub, nbs, zstride, \
+                                      -1);                                                                         \
+    }                                                                                                              \
+    extern "C" __global__ void __launch_bounds__(64 * NW, LB)                                                     \
+        NAME##_sub(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb,                             \
+                   const int8_t *__restrict__ codes, const _Float16 *__restrict__ bsT,                             \
+                   const float *__restrict__ dT, int M, int Mpad, float *__restrict__ dst, int64_t ldd,            \
+                   int32_t *__restrict__ sub, int nbs, int64_t zstride) {                                          \
+        gemm_q4K_wide_impl<NW, true>(W, w_row_bytes, N, nb, codes, bsT, dT, M, Mpad, dst, ldd, sub, nbs, zstride,  \
+                                     -1);                                                                          \
+    }
+GEMM_WIDE_KERNELS(ghip_gemm_q4_K_w8, 8, 1)
+
+
+
+
 // ---------------------------------------------------------------- Q6_K prefill
 // Many activation rows with Q6_K weights (vec_dot_q6_K_q8_K, vec_dot.rs:982-1040,
 // per super-block  is = sum_s sc_s * sum_16 (q6 - 32) * q8,  out += (d * is) * d8).
@@ -584,3 +810,61 @@ ghip_gemm_splitk_reduce(const float *__restrict__ part, int nsplit, int M, int N
     d[3] = acc.w;
 }
 static_assert(sizeof(g3::Smem<128>) == 116224 && sizeof(g3::Smem<64>) == 76544, "host code launches with these LDS sizes");
+static_assert(2 * sizeof(g4::Stage<256>) == 148480, "host code launches with this LDS size");
+// Sibling MUL_MATs in one launch on the wide tiles (see GemmMulti above).
+extern "C" __global__ void __launch_bounds__(512, 1)
+    ghip_gemm_q4_K_w8_multi(GemmMulti g, int64_t w_row_bytes, int nb, const int8_t *__restrict__ codes,
+                            const _Float16 *__restrict__ bsT, const float *__restrict__ dT, int M, int Mpad) {
+    int id = blockIdx.x;
+    if (g.total % 8 == 0) id = (blockIdx.x & 7) * (g.total >> 3) + (blockIdx.x >> 3);
+    int i = 0;
+#pragma unroll
+    for (int k = 1; k < 4; k++)
+        if (k < g.n && id >= g.t0[k]) i = k;
+    gemm_q4K_wide_impl<8, false>(g.W[i], w_row_bytes, g.N[i], nb, codes, bsT, dT, M, Mpad, g.dst[i], g.ldd[i],
+                                 nullptr, nb, 0, id - g.t0[i]);
+}
+
+// Prefill activations straight from f32: the Q8_K quantization of
+// ghip_quantize_q8_K (same arithmetic, ghip_q8k.h) written directly in the
+// GEMM layouts, so the Q8_K rows never go through HBM.  One wavefront per
+// (token, super-block); rows m < n_mat take the quantize_mat_q8_K_4x8 values.
+//   F16 = false (Q4_K GEMM): codes [Mpad][K] int8 | bsT [nb][Mpad][16] f16 | dT [nb][Mpad]
+//   F16 = true  (Q6_K GEMM): codes [Mpad][K] f16  | dT [nb][Mpad]
+template <bool F16>
+__device__ __forceinline__ void act_q8K_layout(const float *__restrict__ x, int64_t x_stride, int M, int Mpad, int nb,
+                                               int n_mat, void *__restrict__ codes, _Float16 *__restrict__ bsT,
+                                               float *__restrict__ dT) {
+    const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (task >= (int64_t)M * nb) return;
+    const int m = (int)(task / nb), b = (int)(task % nb);
+    float xs[4];
+    __builtin_memcpy(xs, x + (int64_t)m * x_stride + (int64_t)b * QK_K + 4 * lane, 16);
+    int q[4];
+    float d;
+    q8K_block(xs, lane, m < n_mat, q, d);
+    const int64_t e = (int64_t)m * nb * QK_K + (int64_t)b * QK_K + 4 * lane;
+    if constexpr (F16) {
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        const h4 v = {(_Float16)(float)q[0], (_Float16)(float)q[1], (_Float16)(float)q[2], (_Float16)(float)q[3]};
+        *reinterpret_cast<h4 *>(reinterpret_cast<_Float16 *>(codes) + e) = v;
+    } else {
+        const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
+                                ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+        *reinterpret_cast<uint32_t *>(reinterpret_cast<int8_t *>(codes) + e) = packed;
+        const int s = q8K_bsum16(q, lane);
+        if ((lane & 3) == 0) bsT[((int64_t)b * Mpad + m) * 16 + (lane >> 2)] = (_Float16)(float)s;
+    }
+    if (lane == 0) dT[(int64_t)b * Mpad + m] = d;
+}
+extern "C" __global__ void __launch_bounds__(256)
+ghip_gemm_act_q8K(const float *__restrict__ x, int64_t x_stride, int M, int Mpad, int nb, int n_mat,
+                  int8_t *__restrict__ codes, _Float16 *__restrict__ bsT, float *__restrict__ dT) {
+    act_q8K_layout<false>(x, x_stride, M, Mpad, nb, n_mat, codes, bsT, dT);
+}
+extern "C" __global__ void __launch_bounds__(256)
+ghip_gemm_act_q8K_f16(const float *__restrict__ x, int64_t x_stride, int M, int Mpad, int nb, int n_mat,
+                      _Float16 *__restrict__ codes, float *__restrict__ dT) {
+    act_q8K_layout<true>(x, x_stride, M, Mpad, nb, n_mat, codes, nullptr, dT);
+}

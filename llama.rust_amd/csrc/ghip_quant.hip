@@ -9,6 +9,7 @@
 //   quantize_row_q8_0       quants.rs:331-362   d = f16(amax/127), q = rne(x*127/amax)
 // Compiled with -ffp-contract=off: every product is rounded before rne().
 #include "ghip_common.h"
+#include "ghip_q8k.h"
 
 // One wavefront per 256-element super-block; each lane owns 4 consecutive
 // elements.  Rows r < n_mat use the quantize_mat_q8_K_4x8 values, the others
@@ -24,54 +25,14 @@ ghip_quantize_q8_K(const float *__restrict__ x, int64_t x_stride, int64_t n, int
     const int64_t row = wid / nb, b = wid - row * nb;
     float xs[4];
     __builtin_memcpy(xs, x + row * x_stride + b * QK_K + lane * 4, 16);
-
-    // signed max-abs, first occurrence wins (strict '>' scan in element order)
-    float bax = 0.0f, bval = 0.0f;
-    int bidx = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float a = fabsf(xs[i]);
-        if (a > bax) { bax = a; bval = xs[i]; bidx = lane * 4 + i; }
-    }
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const float oax = __shfl_xor(bax, o, 64);
-        const float oval = __shfl_xor(bval, o, 64);
-        const int oidx = __shfl_xor(bidx, o, 64);
-        if (oax > bax || (oax == bax && oidx < bidx)) { bax = oax; bval = oval; bidx = oidx; }
-    }
-
-    uint8_t *blk = y + row * y_stride + b * Q8K_BYTES;
-    const bool mat = row < n_mat;
     int q[4];
     float d;
-    if (bax == 0.0f) {
-        q[0] = q[1] = q[2] = q[3] = 0;
-        d = 0.0f;
-    } else if (!mat) {
-        const float iscale = __fdiv_rn(-127.0f, bval);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int v = (int)rintf(__fmul_rn(iscale, xs[i]));
-            q[i] = v < 127 ? v : 127;
-        }
-        d = __fdiv_rn(1.0f, iscale);
-    } else {
-        const float iscale = __fdiv_rn(127.0f, bax);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float r = rintf(__fmul_rn(iscale, xs[i]));
-            r = fminf(fmaxf(r, -128.0f), 127.0f);
-            q[i] = (int)r;
-        }
-        d = __fdiv_rn(1.0f, iscale);
-    }
+    q8K_block(xs, lane, row < n_mat, q, d);
+    uint8_t *blk = y + row * y_stride + b * Q8K_BYTES;
     const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
                             ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
     __builtin_memcpy(blk + 4 + lane * 4, &packed, 4);
-    int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
+    const int s = q8K_bsum16(q, lane);
     if ((lane & 3) == 0) {
         const int16_t s16 = (int16_t)s;
         __builtin_memcpy(blk + 260 + 2 * (lane >> 2), &s16, 2);

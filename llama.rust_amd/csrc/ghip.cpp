@@ -292,6 +292,19 @@ bool gemv_v2(const MulMatPlan &p) {
     return p.wtype == GHIP_TYPE_Q4_K || p.wtype == GHIP_TYPE_Q5_K || (p.wtype == GHIP_TYPE_Q6_K && p.M == 1);
 }
 
+// Row groups of the whole-row decode kernels (RB rows per register group, NG
+// groups per row team, streamed two deep).  Batch 1 streams one-row groups
+// deeper on large matrices: Q4_K 4096 -> 14336 9.6 -> 9.2 us, Q6_K 14336 ->
+// 4096 16.0 -> 14.8 us; smaller matrices keep 2 x 2 (4096 -> 4096: 4.5 us
+// against 5.2 with 1 x 4).
+void gemv_groups(int wtype, int64_t M, int64_t N, int &rb, int &ng) {
+    rb = 2;
+    ng = 2;
+    if (M != 1) return;
+    if (wtype == GHIP_TYPE_Q6_K) rb = 1, ng = 8;
+    else if (wtype == GHIP_TYPE_Q4_K && N >= 8192) rb = 1, ng = 4;
+}
+
 // Decode path: activation columns in groups of at most 8.  Q4_K reads the f32
 // activations and quantizes them inside the kernel when fused is set.
 ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, int64_t act_rb,
@@ -307,9 +320,13 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     // K-quants (Q4_K, Q6_K): T row teams share one LDS copy of the quantized
     // activations; a team's wavefronts hold NG groups of RB rows in flight.
     const bool q4k = gemv_v2(p);
-    const int rb = q4k ? env_int("GHIP_GEMV_RB", 2) : 8;
-    const int ng = q4k ? env_int("GHIP_GEMV_NG", 2) : 1;
-    if (q4k && !((rb == 2 && (ng == 2 || ng == 4 || ng == 8)) || (rb == 4 && (ng == 2 || ng == 4))))
+    int rb_d, ng_d;
+    gemv_groups(p.wtype, p.M, p.N, rb_d, ng_d);
+    const int rb = q4k ? env_int("GHIP_GEMV_RB", rb_d) : 8;
+    const int ng = q4k ? env_int("GHIP_GEMV_NG", ng_d) : 1;
+    if (q4k && !((rb == 2 && (ng == 2 || ng == 4 || ng == 8)) || (rb == 4 && (ng == 2 || ng == 4)) ||
+                 (rb == 1 && p.wtype == GHIP_TYPE_Q4_K && p.M == 1 && (ng == 2 || ng == 4 || ng == 8)) ||
+                 (p.wtype == GHIP_TYPE_Q6_K && p.M == 1 && ((rb == 2 && ng == 8) || (rb == 1 && (ng == 4 || ng == 8))))))
         return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "GHIP_GEMV_RB x GHIP_GEMV_NG must be 2x2, 2x4, 2x8, 4x2 or 4x4");
     const int rows_per_team = rb * ng;
     // 8 teams, except 4 for one or two activation rows on matrices under 8192
@@ -943,7 +960,12 @@ ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipS
     // gate/up (2 x 14336) within 2 % either way
     const int dflt_teams = 8;
     const int teams = std::max(1, std::min(8 / waves_k, env_int("GHIP_GEMV_TEAMS", dflt_teams)));
-    const int rows_per_wg = 4 * teams;
+    int64_t rows_total = 0;
+    for (int i = 0; i < n; i++) rows_total += p[i].N;
+    int rb, ng;
+    gemv_groups(p0.wtype, p0.M, rows_total, rb, ng);
+    if (p0.wtype == GHIP_TYPE_Q5_K) rb = ng = 2;
+    const int rows_per_wg = rb * ng * teams;
     GemvMulti g{};
     int wg = 0;
     for (int i = 0; i < n; i++) {
@@ -968,7 +990,7 @@ ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipS
                          (size_t)rows_per_wg * waves_k * NC * sizeof(float);
     if (shmem > 160 * 1024) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: decode LDS image too large");
     const std::string name = std::string(gemv_base(p0.wtype)) + (p0.wtype == GHIP_TYPE_Q6_K ? "_v2" : "") + "_f_c" +
-                             std::to_string(NC) + "_r2x2_multi";
+                             std::to_string(NC) + "_r" + std::to_string(rb) + "x" + std::to_string(ng) + "_multi";
     const int n_mat = (int)std::max<int64_t>(0, std::min<int64_t>(nc, p0.n_mat));
     return ctx->launch(name, dim3((unsigned)wg), dim3(64 * waves_k * teams), shmem, s, g, (int64_t)p0.w_row_bytes,
                        (int)p0.nb, (const uint8_t *)nodes[0].src[1]->data, (int64_t)nodes[0].src[1]->nb[1], nc,

@@ -204,22 +204,30 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
     const uint32_t boff = (uint32_t)min(b, nb - 1) * BBYTES;
     const uint32_t qoff = boff + (Q5 ? 48 : 16) + 32 * i;
     const int rlast = min(max(r0, r1 - 1), rows - 1);
-    uint4 hdr[NG][RB], qa[NG][RB], qb[NG][RB];
-    uint4 xh0[NG][Q5 ? RB : 1], xh1[NG][Q5 ? RB : 1];  // Q5_K qh[0..15], qh[16..31]
+    // Row groups stream through two register slots: group g + 2 is loaded
+    // into g's slot as soon as g is computed, so each wavefront keeps two
+    // groups in flight and computes its early rows while its later rows are
+    // still on the way (with every group loaded up front, most data would
+    // land at the end and all of the arithmetic would follow the last byte).
+    constexpr int NS = NG < 2 ? NG : 2;  // register slots
+    uint4 hdr[NS][RB], qa[NS][RB], qb[NS][RB];
+    uint4 xh0[NS][Q5 ? RB : 1], xh1[NS][Q5 ? RB : 1];  // Q5_K qh[0..15], qh[16..31]
+    auto load_group = [&](int gi, int slot) {
+#pragma unroll
+        for (int rr = 0; rr < RB; rr++) {
+            const uint8_t *rowp = W + (int64_t)min(r0 + gi * RB + rr, rlast) * w_row_bytes;
+            hdr[slot][rr] = ld16(rowp + boff);
+            qa[slot][rr] = ld16(rowp + qoff);
+            qb[slot][rr] = ld16(rowp + qoff + 16);
+            if constexpr (Q5) {
+                xh0[slot][rr] = ld16(rowp + boff + 16);
+                xh1[slot][rr] = ld16(rowp + boff + 32);
+            }
+        }
+    };
     auto load_all = [&]() {
 #pragma unroll
-        for (int gi = 0; gi < NG; gi++)
-#pragma unroll
-            for (int rr = 0; rr < RB; rr++) {
-                const uint8_t *rowp = W + (int64_t)min(r0 + gi * RB + rr, rlast) * w_row_bytes;
-                hdr[gi][rr] = ld16(rowp + boff);
-                qa[gi][rr] = ld16(rowp + qoff);
-                qb[gi][rr] = ld16(rowp + qoff + 16);
-                if constexpr (Q5) {
-                    xh0[gi][rr] = ld16(rowp + boff + 16);
-                    xh1[gi][rr] = ld16(rowp + boff + 32);
-                }
-            }
+        for (int gi = 0; gi < NS; gi++) load_group(gi, gi);
     };
     // Activations first (their wait then does not cover the weight loads),
     // then ALL of the team's weight rows (NG groups of RB rows in flight at
@@ -350,8 +358,11 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
         }
     };
 #pragma unroll
-    for (int gi = 0; gi < NG; gi++)
-        if (r0 + gi * RB < r1) compute_group(r0 + gi * RB, hdr[gi], qa[gi], qb[gi], xh0[gi], xh1[gi]);
+    for (int gi = 0; gi < NG; gi++) {
+        const int sl = gi % NS;
+        if (r0 + gi * RB < r1) compute_group(r0 + gi * RB, hdr[sl], qa[sl], qb[sl], xh0[sl], xh1[sl]);
+        if (gi + NS < NG && r0 + (gi + NS) * RB < r1) load_group(gi + NS, sl);
+    }
     if (nwk == 1) return;
     __syncthreads();
     const int nrows = max(0, min(rows, rw0 + T * RPT) - rw0);
@@ -399,21 +410,25 @@ __device__ __forceinline__ void gemv_q6K_v2_impl(const uint8_t *__restrict__ W, 
     const uint32_t o_ql = boff + 64 * j + 16 * hh, o_qh = boff + 128 + 32 * j + 16 * hh;
     const uint32_t o_sc = boff + 192 + 8 * j, o_d = boff + 208;
     const int rlast = min(max(r0, r1 - 1), rows - 1);
-    uint4 ql0[NG][RB], ql1[NG][RB], qhv[NG][RB];
-    uint2 scv[NG][RB];
-    uint32_t dv[NG][RB];
+    // two register slots of row groups in flight, as in gemv_q4K_impl
+    constexpr int NS = NG < 2 ? NG : 2;
+    uint4 ql0[NS][RB], ql1[NS][RB], qhv[NS][RB];
+    uint2 scv[NS][RB];
+    uint32_t dv[NS][RB];
+    auto load_group = [&](int gi, int slot) {
+#pragma unroll
+        for (int rr = 0; rr < RB; rr++) {
+            const uint8_t *rowp = W + (int64_t)min(r0 + gi * RB + rr, rlast) * w_row_bytes;
+            ql0[slot][rr] = ld16(rowp + o_ql);
+            ql1[slot][rr] = ld16(rowp + o_ql + 32);
+            qhv[slot][rr] = ld16(rowp + o_qh);
+            scv[slot][rr] = ld8(rowp + o_sc);
+            dv[slot][rr] = ld2(rowp + o_d);
+        }
+    };
     auto load_all = [&]() {
 #pragma unroll
-        for (int gi = 0; gi < NG; gi++)
-#pragma unroll
-            for (int rr = 0; rr < RB; rr++) {
-                const uint8_t *rowp = W + (int64_t)min(r0 + gi * RB + rr, rlast) * w_row_bytes;
-                ql0[gi][rr] = ld16(rowp + o_ql);
-                ql1[gi][rr] = ld16(rowp + o_ql + 32);
-                qhv[gi][rr] = ld16(rowp + o_qh);
-                scv[gi][rr] = ld8(rowp + o_sc);
-                dv[gi][rr] = ld2(rowp + o_d);
-            }
+        for (int gi = 0; gi < NS; gi++) load_group(gi, gi);
     };
     const int total = NC * nb * 16;
     const bool qwave = wave * 64 < total;
@@ -535,8 +550,11 @@ __device__ __forceinline__ void gemv_q6K_v2_impl(const uint8_t *__restrict__ W, 
         }
     };
 #pragma unroll
-    for (int gi = 0; gi < NG; gi++)
-        if (r0 + gi * RB < r1) compute_group(r0 + gi * RB, ql0[gi], ql1[gi], qhv[gi], scv[gi], dv[gi]);
+    for (int gi = 0; gi < NG; gi++) {
+        const int sl = gi % NS;
+        if (r0 + gi * RB < r1) compute_group(r0 + gi * RB, ql0[sl], ql1[sl], qhv[sl], scv[sl], dv[sl]);
+        if (gi + NS < NG && r0 + (gi + NS) * RB < r1) load_group(gi + NS, sl);
+    }
     if (nwk == 1) return;
     __syncthreads();
     const int nrows = max(0, min(rows, rw0 + T * RPT) - rw0);
@@ -1021,6 +1039,7 @@ GEMV_PAIR_ALL(ghip_gemv_q8_0, gemv_q8_0_impl)
 // register row groups (RB rows) x groups in flight (NG)
 #define Q4K_INST_RB(NC) Q4K_INST(NC, 2, 2) Q4K_INST(NC, 2, 4) Q4K_INST(NC, 4, 2) Q4K_INST(NC, 2, 8) Q4K_INST(NC, 4, 4)
 Q4K_INST_RB(1) Q4K_INST_RB(2) Q4K_INST_RB(4) Q4K_INST_RB(8)
+Q4K_INST(1, 1, 4) Q4K_INST(1, 1, 8) Q4K_INST(1, 1, 2)
 // Q5_K: the same shapes and naming as Q4_K
 #define Q5K_INST_RB(NC) QK45_INST(q5_K, true, NC, 2, 2) QK45_INST(q5_K, true, NC, 2, 4) \
     QK45_INST(q5_K, true, NC, 4, 2) QK45_INST(q5_K, true, NC, 2, 8) QK45_INST(q5_K, true, NC, 4, 4)
@@ -1042,6 +1061,7 @@ Q5K_INST_RB(1) Q5K_INST_RB(2) Q5K_INST_RB(4) Q5K_INST_RB(8)
     }
 #define Q6K_INST_RB(NC) Q6K_INST(NC, 2, 2) Q6K_INST(NC, 2, 4) Q6K_INST(NC, 4, 2)
 Q6K_INST_RB(1) Q6K_INST_RB(2) Q6K_INST_RB(4) Q6K_INST_RB(8)
+Q6K_INST(1, 2, 8) Q6K_INST(1, 1, 4) Q6K_INST(1, 1, 8)
 
 // Sibling MUL_MATs in one launch (ghip_graph_compute): up to four weight
 // matrices of one type and K that read the same f32 activation rows, each
@@ -1056,22 +1076,26 @@ struct GemvMulti {
     int wg0[4];
     int n;
 };
-#define GEMV_MULTI(TN, NC, IMPL, ...)                                                                            \
+#define GEMV_MULTI_RN(TN, NC, RB, NG, IMPL, ...)                                                                 \
     extern "C" __global__ void __launch_bounds__(512)                                                            \
-        ghip_gemv_##TN##_f_c##NC##_r2x2_multi(GemvMulti g, int64_t w_row_bytes, int nb,                         \
-                                              const uint8_t *__restrict__ act, int64_t act_row_bytes, int ncols, \
-                                              int n_mat) {                                                       \
+        ghip_gemv_##TN##_f_c##NC##_r##RB##x##NG##_multi(GemvMulti g, int64_t w_row_bytes, int nb,               \
+                                                        const uint8_t *__restrict__ act, int64_t act_row_bytes, \
+                                                        int ncols, int n_mat) {                                  \
         const int bx = blockIdx.x;                                                                               \
         int i = 0;                                                                                               \
         _Pragma("unroll") for (int k = 1; k < 4; k++) if (k < g.n && bx >= g.wg0[k]) i = k;                     \
-        IMPL<NC, false, true, 2, 2, ##__VA_ARGS__>(g.W[i], w_row_bytes, g.rows[i], nb, act, act_row_bytes, ncols, \
-                                                   g.dst[i], g.ldd[i], nullptr, n_mat, bx - g.wg0[i]);           \
+        IMPL<NC, false, true, RB, NG, ##__VA_ARGS__>(g.W[i], w_row_bytes, g.rows[i], nb, act, act_row_bytes,     \
+                                                     ncols, g.dst[i], g.ldd[i], nullptr, n_mat, bx - g.wg0[i]);  \
     }
+#define GEMV_MULTI(TN, NC, IMPL, ...) GEMV_MULTI_RN(TN, NC, 2, 2, IMPL, ##__VA_ARGS__)
 GEMV_MULTI(q4_K, 1, gemv_q4K_impl, false) GEMV_MULTI(q4_K, 2, gemv_q4K_impl, false)
 GEMV_MULTI(q4_K, 4, gemv_q4K_impl, false) GEMV_MULTI(q4_K, 8, gemv_q4K_impl, false)
 GEMV_MULTI(q5_K, 1, gemv_q4K_impl, true) GEMV_MULTI(q5_K, 2, gemv_q4K_impl, true)
 GEMV_MULTI(q5_K, 4, gemv_q4K_impl, true) GEMV_MULTI(q5_K, 8, gemv_q4K_impl, true)
 GEMV_MULTI(q6_K_v2, 1, gemv_q6K_v2_impl)
+// one-row groups streamed four (Q4_K) or eight (Q6_K) deep: the batch-1 shapes of large matrices
+GEMV_MULTI_RN(q4_K, 1, 1, 4, gemv_q4K_impl, false)
+GEMV_MULTI_RN(q6_K_v2, 1, 1, 8, gemv_q6K_v2_impl)
 
 // Q4_0 / Q5_0 / Q8_0 siblings: ready Q8_0 rows (one quantize launch for the
 // group), 8 weight rows per workgroup

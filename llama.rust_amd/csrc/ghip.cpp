@@ -19,7 +19,7 @@
 
 namespace {
 
-const char *const kModules[] = {"ghip_quant.hsaco", "ghip_gemv.hsaco", "ghip_wquant.hsaco", "ghip_gemm.hsaco", "ghip_fa.hsaco", "ghip_moe.hsaco"};
+const char *const kModules[] = {"ghip_quant.hsaco", "ghip_gemv.hsaco", "ghip_wquant.hsaco", "ghip_gemm.hsaco", "ghip_fa.hsaco", "ghip_moe.hsaco", "ghip_skinny.hsaco"};
 
 struct TypeInfo {
     int blck;
@@ -305,10 +305,50 @@ void gemv_groups(int wtype, int64_t M, int64_t N, int &rb, int &ng) {
     else if (wtype == GHIP_TYPE_Q4_K && N >= 8192) rb = 1, ng = 4;
 }
 
+// Q4_K at 2..15 activation rows on the int8 matrix cores (ghip_skinny.hip):
+// RT row tiles of 16 rows x KS K-slices per 8-wavefront workgroup, tokens
+// padded to NC in {2, 4, 8, 16}.
+// From 4 rows (at 2 and 3 the VALU kernels are as fast).  The activation
+// rows are quantized once by ghip_quantize_q8_K and copied into each
+// workgroup's LDS: quantizing them in every workgroup cost 5.6 us of 21.2 at
+// 8 rows on 4096 -> 14336 (15.6 us with the rows quantized once).
+bool use_skinny(const MulMatPlan &p) {
+    return p.wtype == GHIP_TYPE_Q4_K && p.M >= env_int("GHIP_MMA_MIN_ROWS", 4) && p.M < 16 &&
+           env_int("GHIP_MMA", 1) != 0;
+}
+// The K split sets the fp32 summation order, so it is fixed (2 row tiles x
+// 4 K-slices) for every matrix size: a matrix alone and in a grouped launch
+// give the same bits.  GHIP_MMA_RT=1|4 overrides it (single-op calls only).
+// Measured at 8 rows (pre-quantized): 4096 -> 14336 15.6 us (1 x 8: 20.0),
+// 4096 -> 4096 9.1 us (1 x 8: 7.4).
+void skinny_shape(int64_t M, int &NC, int &RT, int &KS) {
+    NC = M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16;
+    RT = env_int("GHIP_MMA_RT", 2);
+    if (RT != 1 && RT != 2 && RT != 4) RT = 2;
+    KS = 8 / RT;
+}
+size_t skinny_lds(int NC, int64_t K, int64_t nb) {
+    return (size_t)NC * K + (size_t)NC * nb * 4 + (size_t)NC * nb * 16 * 4 + (size_t)8 * 16 * 16 * 4;
+}
+ghip_status run_skinny(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, int64_t act_rb,
+                       bool fused, float *dst, int64_t ldd, int32_t *sub, hipStream_t s) {
+    int NC, RT, KS;
+    skinny_shape(p.M, NC, RT, KS);
+    const size_t shmem = skinny_lds(NC, p.K, p.nb);
+    if (shmem > 160 * 1024) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: decode LDS image too large");
+    const std::string name = std::string("ghip_mma_q4_K") + (fused ? "_f" : "") + (sub ? "_sub" : "") + "_c" +
+                             std::to_string(NC) + "_r" + std::to_string(RT) + "k" + std::to_string(KS);
+    const unsigned grid = (unsigned)((p.N + 16 * RT - 1) / (16 * RT));
+    const int n_mat = (int)std::max<int64_t>(0, std::min<int64_t>(p.M, p.n_mat));
+    return ctx->launch(name, dim3(grid), dim3(512), shmem, s, (const uint8_t *)w, (int64_t)p.w_row_bytes, (int)p.N,
+                       (int)p.nb, act, act_rb, (int)p.M, dst, ldd, sub, n_mat);
+}
+
 // Decode path: activation columns in groups of at most 8.  Q4_K reads the f32
 // activations and quantizes them inside the kernel when fused is set.
 ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, int64_t act_rb,
                      bool fused, float *dst, int64_t ldd, int32_t *sub, hipStream_t s) {
+    if (use_skinny(p)) return run_skinny(ctx, p, w, act, act_rb, fused, dst, ldd, sub, s);
     int waves_k;
     if (gemv_pair(p.wtype))
         waves_k = (int)(((p.nb + 1) / 2 + 63) / 64);
@@ -549,7 +589,7 @@ ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_ten
     // per-wavefront work than it saves on larger matrices (4096x4096 Q4_0:
     // 7.25 -> 6.88 us; 4096->14336 Q5_0 / Q8_0: 13.9 -> 14.9 / 17.7 -> 18.2 us)
     const bool fuse_pair = gemv_pair(p.wtype) && p.N <= env_int("GHIP_GEMV_FUSE_MAX_ROWS", 4096);
-    if (gemv_v2(p) || fuse_pair)  // quantization fused into the decode kernel
+    if ((gemv_v2(p) && !use_skinny(p)) || fuse_pair)  // quantization fused into the decode kernel
         return run_gemv(ctx, p, a->data, (const uint8_t *)b->data, (int64_t)b->nb[1], true, dst, ldd, sub, s);
     st = quantize_act(ctx, p, b, act, s);
     if (st != GHIP_STATUS_SUCCESS) return st;
@@ -952,6 +992,38 @@ ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipS
         return ctx->launch(std::string(gemv_base(p0.wtype)) + "_c" + std::to_string(NC) + "_multi", dim3((unsigned)wgs),
                            dim3(64 * wk), 0, s, g, (int64_t)p0.w_row_bytes, (int)p0.nb, (const uint8_t *)ws,
                            (int64_t)p0.act_row_bytes, nc);
+    }
+    if (use_skinny(p0)) {
+        // Q4_K at 4..15 rows: the activation rows quantized once, then the
+        // matrix-core decode kernel over all members
+        int NC, RT, KS;
+        skinny_shape(p0.M, NC, RT, KS);
+        RT = 2, KS = 4;  // the single-op default (grouped kernels exist for it)
+        const size_t shmem = skinny_lds(NC, p0.K, p0.nb);
+        if (shmem > 160 * 1024) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: decode LDS image too large");
+        const size_t act_bytes = ((size_t)(p0.M * p0.act_row_bytes) + 255) & ~(size_t)255;
+        void *ws = nullptr;
+        st = ctx->workspace(act_bytes, s, &ws);
+        if (st != GHIP_STATUS_SUCCESS) return st;
+        st = quantize_act(ctx, p0, nodes[0].src[1], ws, s);
+        if (st != GHIP_STATUS_SUCCESS) return st;
+        GemvMulti g{};
+        int wg = 0;
+        for (int i = 0; i < 4; i++) {
+            const int j = i < n ? i : 0;
+            g.W[i] = (const uint8_t *)nodes[j].src[0]->data;
+            g.dst[i] = (float *)nodes[j].dst->data;
+            g.ldd[i] = (int64_t)nodes[j].dst->nb[1] / 4;
+            g.rows[i] = i < n ? (int)p[i].N : 0;
+            g.wg0[i] = wg;
+            if (i < n) wg += (int)((p[i].N + 16 * RT - 1) / (16 * RT));
+        }
+        g.n = n;
+        const int n_mat = (int)std::max<int64_t>(0, std::min<int64_t>(p0.M, p0.n_mat));
+        const std::string name = "ghip_mma_q4_K_c" + std::to_string(NC) + "_r" + std::to_string(RT) + "k" +
+                                 std::to_string(KS) + "_multi";
+        return ctx->launch(name, dim3((unsigned)wg), dim3(512), shmem, s, g, (int64_t)p0.w_row_bytes, (int)p0.nb,
+                           (const uint8_t *)ws, (int64_t)p0.act_row_bytes, (int)p0.M, n_mat);
     }
     const int waves_k = (int)((p0.nb + 15) / 16);
     if (waves_k > 8) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: ne00 = %lld too large for the decode kernel", (long long)p0.K);

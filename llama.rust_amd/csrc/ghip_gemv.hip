@@ -49,109 +49,7 @@ DEV void finish_rows(const float *red, int r0, int nrows, int ncols, int NC, int
 //
 // LDS (dynamic): codes [NC][K] int8 | d [NC][nb] f32 | 16-element sums
 // [NC][nb][16] int32 | row partials [T*rows_per_team][W_K][NC] f32.
-// Quantization of the activation rows into the LDS image, bit-identical to
-// ghip_quantize_q8_K: 16 lanes per super-block ("task" = one lane's 16
-// consecutive elements); the signed max-abs is reduced over the 16 lanes with
-// the first occurrence winning ties; rows c < n_mat take the
-// quantize_mat_q8_K_4x8 values.  Tasks run in rounds of blockDim lanes; every
-// lane of the workgroup takes part in every round (the shuffles need them).
-struct XTask {
-    float v[16];
-};
-
-DEV XTask quant_q8K_load(const float *__restrict__ x, int64_t x_stride, int ncols, int nb, int total, int task) {
-    XTask t;
-    const int l = task & 15, blk = task >> 4;
-    const int c = blk / nb, b = blk - c * nb;
-    if (task < total && c < ncols) {
-        __builtin_memcpy(t.v, x + (int64_t)c * x_stride + (int64_t)b * QK_K + 16 * l, 64);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; i++) t.v[i] = 0.0f;
-    }
-    return t;
-}
-
-DEV void quant_q8K_store(const XTask &t, int nb, int n_mat, int total, int task, int8_t *codes, float *dq, int *bsum) {
-    const float *v = t.v;
-    const bool live = task < total;
-    const int l = task & 15, blk = task >> 4;
-    const int c = live ? blk / nb : 0, b = live ? blk - c * nb : 0;
-    float bax = 0.0f, bval = 0.0f;
-    int bidx = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const float a = fabsf(v[i]);
-        if (a > bax) { bax = a; bval = v[i]; bidx = 16 * l + i; }
-    }
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-        const float oax = __shfl_xor(bax, o, 64);
-        const float oval = __shfl_xor(bval, o, 64);
-        const int oidx = __shfl_xor(bidx, o, 64);
-        if (oax > bax || (oax == bax && oidx < bidx)) { bax = oax; bval = oval; bidx = oidx; }
-    }
-    int q[16];
-    float d;
-    if (bax == 0.0f) {
-#pragma unroll
-        for (int i = 0; i < 16; i++) q[i] = 0;
-        d = 0.0f;
-    } else if (c >= n_mat) {
-        const float iscale = __fdiv_rn(-127.0f, bval);
-#pragma unroll
-        for (int i = 0; i < 16; i++) q[i] = min(127, (int)rintf(__fmul_rn(iscale, v[i])));
-        d = __fdiv_rn(1.0f, iscale);
-    } else {
-        const float iscale = __fdiv_rn(127.0f, bax);
-#pragma unroll
-        for (int i = 0; i < 16; i++) q[i] = (int)fminf(fmaxf(rintf(__fmul_rn(iscale, v[i])), -128.0f), 127.0f);
-        d = __fdiv_rn(1.0f, iscale);
-    }
-    uint32_t pk[4];
-    int sum = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        pk[k] = (uint32_t)(q[4 * k] & 0xff) | ((uint32_t)(q[4 * k + 1] & 0xff) << 8) |
-                ((uint32_t)(q[4 * k + 2] & 0xff) << 16) | ((uint32_t)(q[4 * k + 3] & 0xff) << 24);
-        sum += q[4 * k] + q[4 * k + 1] + q[4 * k + 2] + q[4 * k + 3];
-    }
-    if (live) {
-        *reinterpret_cast<uint4 *>(codes + (int64_t)c * nb * QK_K + b * QK_K + 16 * l) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        bsum[(c * nb + b) * 16 + l] = sum;  // bsums[l] of block_q8_K
-        if (l == 0) dq[c * nb + b] = d;
-    }
-}
-
-// Ready Q8_K rows (pre-quantized src1) copied into the same LDS image, in
-// the same task shape (16 codes per lane).
-struct Q8KTask {
-    uint4 v;
-    int sum;
-    float d;
-};
-
-DEV Q8KTask q8K_load(const uint8_t *__restrict__ act, int64_t act_row_bytes, int ncols, int nb, int total, int task) {
-    Q8KTask t{make_uint4(0, 0, 0, 0), 0, 0.0f};
-    const int l = task & 15, blk = task >> 4;
-    const int c = blk / nb, b = blk - c * nb;
-    if (task < total && c < ncols) {
-        const uint8_t *A = act + (int64_t)c * act_row_bytes + (int64_t)b * Q8K_BYTES;
-        t.v = ld16(A + 4 + 16 * l);
-        t.sum = (int)(int16_t)ld2(A + 260 + 2 * l);
-        t.d = __uint_as_float(ld4(A));
-    }
-    return t;
-}
-
-DEV void q8K_store(const Q8KTask &t, int nb, int total, int task, int8_t *codes, float *dq, int *bsum) {
-    if (task >= total) return;
-    const int l = task & 15, blk = task >> 4;
-    const int c = blk / nb, b = blk - c * nb;
-    *reinterpret_cast<uint4 *>(codes + (int64_t)c * nb * QK_K + b * QK_K + 16 * l) = t.v;
-    bsum[(c * nb + b) * 16 + l] = t.sum;
-    if (l == 0) dq[c * nb + b] = t.d;
-}
+#include "ghip_actq.h"
 
 // Activation codes of one lane: elements 64i..64i+31 (low nibbles, sub-block
 // 2i) and 64i+32..64i+63 (high nibbles, sub-block 2i+1) of super-block b, the

@@ -154,24 +154,35 @@ ghip_status ghip_mul_mat_subsums(ghip_context *ctx, const ghip_tensor *src0, con
 ghip_status ghip_mul_mat_act(ghip_context *ctx, const ghip_tensor *src0, const ghip_tensor *src1,
                              void *out, void *stream);
 
-/* dst = MUL_MAT_ID(as, b, ids) with MXFP4 experts (forward_mul_mat_id,
- * compute.rs:1917-2202; the rows % 8 == 0 repack kernel repack.rs:1048-1100):
- *   as:  MXFP4 [K, rows, n_as], expert rows contiguous blocks
+/* dst = MUL_MAT_ID(as, b, ids) with MXFP4, Q4_K, Q5_K or Q6_K experts
+ * (forward_mul_mat_id, compute.rs:1917-2202; the MXFP4 rows % 8 == 0 repack
+ * kernel repack.rs:1048-1100):
+ *   as:  [K, rows, n_as], expert rows contiguous blocks
  *   b:   F32 [K, ne11, n_tokens] (nb0 == 4, nb2 == ne11 * nb1), 1 <= ne11 <= n_ids
  *   ids: I32 [n_ids, n_tokens], expert index per (slot, token)
  *   dst: F32 [rows, n_ids, n_tokens] (nb0 == 4)
- * dst[t][s] = as[ids[t][s]] x quantize_q8_0(b[t][s % ne11]).  Each 32-block
- * dot is exact and folded in block order with the reference's own operations
- * (fma(dot, e * d, acc) for rows % 8 == 0, acc += (d * e) * dot otherwise), so
- * outputs are bit-identical.  A pair whose id is outside [0, n_as) -- where
- * the reference asserts -- gets a row of NaN. */
+ * MXFP4: dst[t][s] = as[ids[t][s]] x quantize_q8_0(b[t][s % ne11]).  Each
+ * 32-block dot is exact and folded in block order with the reference's own
+ * operations (fma(dot, e * d, acc) for rows % 8 == 0, acc += (d * e) * dot
+ * otherwise), so outputs are bit-identical.
+ * Q4_K / Q5_K / Q6_K (K % 256 == 0): the same with quantize_row_q8_K
+ * activations (compute.rs:1950-1980); each super-block's integer sums are
+ * exact and scaled once by d8 * d (vec_dot.rs:881-909, :998-1028), so outputs
+ * match the reference's routes to fp32 rounding of those per-block terms.
+ * A pair whose id is outside [0, n_as) -- where the reference asserts -- gets
+ * a row of NaN. */
 ghip_status ghip_mul_mat_id(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b, const ghip_tensor *ids,
                             const ghip_tensor *dst, void *stream);
 
-/* Parity hook with no reference counterpart: the int32 block dots
- * sum kvalue * q8 that ghip_mul_mat_id folds, at
- * subsums[((t * n_ids + s) * rows + r) * (K / 32) + block] (device pointer).
- * Pairs with an invalid id are left unwritten. */
+/* Parity hook with no reference counterpart: the int32 partials that
+ * ghip_mul_mat_id folds (device pointer), per (pair p = t * n_ids + s, row r):
+ *   MXFP4: the block dots sum kvalue * q8 at subsums[(p * rows + r) * (K / 32) + block];
+ *   Q4_K / Q5_K: (sum sc * dot, sum m * bsum) per super-block at
+ *     subsums[((p * rows + r) * (K / 256) + sb) * 2 + {0, 1}];
+ *   Q6_K: sum sc * (dot - 32 * bsum) per super-block at
+ *     subsums[(p * rows + r) * (K / 256) + sb]
+ * (the layouts of ghip_mul_mat_subsums).  Pairs with an invalid id are left
+ * unwritten. */
 ghip_status ghip_mul_mat_id_subsums(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b,
                                     const ghip_tensor *ids, int32_t *subsums, void *stream);
 

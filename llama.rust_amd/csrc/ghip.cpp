@@ -696,24 +696,31 @@ FaLayout fa_layout(int D, int T, int H, int S, int H_kv) {
 // ------------------------------------------------------------ MUL_MAT_ID
 
 struct MoePlan {
+    int wtype;  // MXFP4, or Q4_K / Q5_K / Q6_K experts
     int64_t K, rows, n_as, ne11, n_tokens, n_ids, nb;
     int64_t act_row_bytes;
 };
 
-// forward_mul_mat_id (compute.rs:1917-2202) with MXFP4 experts.
+// forward_mul_mat_id (compute.rs:1917-2202) with MXFP4, Q4_K, Q5_K or Q6_K
+// experts (the K-quants' vec_dot_type is Q8_K, compute.rs:1926-1929).
 bool plan_moe(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b, const ghip_tensor *ids,
               const ghip_tensor *d, MoePlan &p, ghip_status &st) {
     st = GHIP_STATUS_BACKEND_ERROR;
     auto bad = [&](const char *why) { st = ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat_id: %s", why); return false; };
     if (!as || !b || !ids) return bad("null operand");
-    if (as->type != GHIP_TYPE_MXFP4) return bad("experts must be MXFP4");
-    if (as->ne[0] % 32 || as->ne[0] <= 0) return bad("ne00 must be a positive multiple of 32");
+    p.wtype = as->type;
+    if (p.wtype != GHIP_TYPE_MXFP4 && p.wtype != GHIP_TYPE_Q4_K && p.wtype != GHIP_TYPE_Q5_K &&
+        p.wtype != GHIP_TYPE_Q6_K)
+        return bad("experts must be MXFP4, Q4_K, Q5_K or Q6_K");
+    const TypeInfo ti = type_info(p.wtype);
+    if (as->ne[0] % ti.blck || as->ne[0] <= 0) return bad("ne00 must be a positive multiple of the block size");
     p.K = as->ne[0];
     p.rows = as->ne[1];
     p.n_as = as->ne[2];
-    p.nb = p.K / 32;
+    p.nb = p.K / ti.blck;
     if (as->ne[3] != 1) return bad("4-D experts are not supported");
-    if (as->nb[0] != 17 || as->nb[1] != (uint64_t)(p.nb * 17) || as->nb[2] < (uint64_t)(p.rows * p.nb * 17))
+    if (as->nb[0] != (uint64_t)ti.bytes || as->nb[1] != (uint64_t)(p.nb * ti.bytes) ||
+        as->nb[2] < (uint64_t)(p.rows * p.nb * ti.bytes))
         return bad("expert rows must be contiguous blocks");
     if (b->type != GHIP_TYPE_F32 || b->nb[0] != 4 || b->ne[0] != p.K) return bad("b must be F32 [ne00, ...]");
     p.ne11 = b->ne[1];
@@ -729,7 +736,8 @@ bool plan_moe(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b, co
     if (d && (d->type != GHIP_TYPE_F32 || d->nb[0] != 4 || d->ne[0] != p.rows || d->ne[1] != p.n_ids ||
               d->ne[2] != p.n_tokens))
         return bad("dst must be F32 [rows, n_ids, n_tokens]");
-    p.act_row_bytes = p.nb * 34;
+    if (p.wtype != GHIP_TYPE_MXFP4 && p.nb > INT32_MAX / 256) return bad("ne00 too large");
+    p.act_row_bytes = p.wtype == GHIP_TYPE_MXFP4 ? p.nb * 34 : p.nb * 292;
     st = GHIP_STATUS_SUCCESS;
     return true;
 }
@@ -750,8 +758,11 @@ MoeWs moe_ws(const MoePlan &p, bool has_dst, bool sub) {
     L.max_tiles = (n_pairs + L.tp - 1) / L.tp + p.n_as;
     auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
     L.act = up((size_t)(p.ne11 * p.n_tokens * p.act_row_bytes));
-    L.actf = up((size_t)n_pairs * p.nb * 64);  // per routed pair
-    L.actd = up((size_t)n_pairs * p.nb * 4);
+    const bool kq = p.wtype != GHIP_TYPE_MXFP4;  // K-quants read the Q8_K rows directly
+    if (kq) L.tp = 32;
+    L.max_tiles = (n_pairs + L.tp - 1) / L.tp + p.n_as;
+    L.actf = kq ? 0 : up((size_t)n_pairs * p.nb * 64);  // per routed pair
+    L.actd = kq ? 0 : up((size_t)n_pairs * p.nb * 4);
     L.route = up((size_t)(2 + n_pairs + 3 * L.max_tiles) * 4);
     L.out = has_dst ? 0 : (size_t)(n_pairs * p.rows * 4);
     L.total = L.act + L.actf + L.actd + L.route + L.out;
@@ -788,15 +799,31 @@ ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip
     float *dst = d ? (float *)d->data : (float *)((uint8_t *)route + route_bytes);
     const int64_t dst_nb1 = d ? (int64_t)d->nb[1] / 4 : p.rows;
     const int64_t dst_nb2 = d ? (int64_t)d->nb[2] / 4 : p.rows * p.n_ids;
-    const unsigned qgrid = (unsigned)((act_rows * p.nb * 8 + 255) / 256);
-    st = ctx->launch("ghip_quantize_q8_0", dim3(qgrid), dim3(256), 0, s, (const float *)b->data,
-                     (int64_t)b->nb[1] / 4, p.K, act_rows, act, p.act_row_bytes);
+    const bool kq = p.wtype != GHIP_TYPE_MXFP4;
+    if (kq) {  // quantize_row_q8_K for every src1 row (the wdata pass, compute.rs:1950-1976)
+        const unsigned qgrid = (unsigned)((act_rows * p.nb + 3) / 4);
+        st = ctx->launch("ghip_quantize_q8_K", dim3(qgrid), dim3(256), 0, s, (const float *)b->data,
+                         (int64_t)b->nb[1] / 4, p.K, act_rows, act, p.act_row_bytes, (int64_t)0);
+    } else {
+        const unsigned qgrid = (unsigned)((act_rows * p.nb * 8 + 255) / 256);
+        st = ctx->launch("ghip_quantize_q8_0", dim3(qgrid), dim3(256), 0, s, (const float *)b->data,
+                         (int64_t)b->nb[1] / 4, p.K, act_rows, act, p.act_row_bytes);
+    }
     if (st != GHIP_STATUS_SUCCESS) return st;
     const int64_t ids_nb1 = (int64_t)ids->nb[1] / 4;
     st = ctx->launch("ghip_moe_route", dim3(1), dim3(1024), (unsigned)(2 * p.n_as * 4), s, (const int32_t *)ids->data,
                      ids_nb1, (int)p.n_ids, (int)p.n_tokens, (int)p.n_as, route, (int)max_tiles, tp, dst, dst_nb1,
                      dst_nb2, (int)p.rows);
     if (st != GHIP_STATUS_SUCCESS) return st;
+    if (kq) {
+        const char *tn = p.wtype == GHIP_TYPE_Q4_K ? "q4_K" : p.wtype == GHIP_TYPE_Q5_K ? "q5_K" : "q6_K";
+        const std::string name = std::string("ghip_mmid_") + tn + (sub ? "_sub" : "");
+        const dim3 grid((unsigned)max_tiles, (unsigned)((p.rows + 15) / 16));
+        return ctx->launch(name, grid, dim3(256), 0, s, (const uint8_t *)as->data, (int64_t)as->nb[1],
+                           (int64_t)as->nb[2], (const uint8_t *)act, p.act_row_bytes, (int)p.ne11,
+                           (const int32_t *)route, (int)n_pairs, (int)p.n_ids, dst, dst_nb1, dst_nb2, (int)p.rows,
+                           (int)p.nb, sub);
+    }
     // f16 codes of every routed pair, in the routed order
     const unsigned fgrid = (unsigned)((n_pairs * p.nb * 4 + 255) / 256);
     st = ctx->launch("ghip_moe_act_f16", dim3(fgrid), dim3(256), 0, s, (const uint8_t *)act, p.act_row_bytes,

@@ -370,3 +370,181 @@ MOE_KERNEL(ghip_moe_mxfp4_t64_plain, 2, false, false)
 MOE_KERNEL(ghip_moe_mxfp4_t32_sub, 1, true, true)
 MOE_KERNEL(ghip_moe_mxfp4_t32_plain_sub, 1, false, true)
 
+
+// ---------------------------------------------------------- K-quant experts
+// MUL_MAT_ID with Q4_K, Q5_K or Q6_K experts (forward_mul_mat_id,
+// compute.rs:1917-2202): the activation rows quantized once to Q8_K
+// (quantize_row_q8_K, the reference's wdata pass), the pairs routed by
+// ghip_moe_route, then per (tile, 16 expert rows) one workgroup of four
+// wavefronts, 4 rows each held in registers, walking the tile's pairs.  Per
+// (pair, row) the value is the decode GEMV's: the integer sums of
+// vec_dot_q4_K_q8_K / vec_dot_q5_K_q8_K / vec_dot_q6_K_q8_K per super-block
+// (vec_dot.rs:928-1040) and the same fp32 scaling, summed over the
+// wavefront.  A wavefront covers 16 super-blocks per pass (4 lanes each);
+// wider rows take several passes, their partials added in the lanes first.
+constexpr int MMID_RB = 4;  // rows per wavefront
+
+// Lane i's quarter of super-block b: its integer sums (the caller adds the
+// four quarters exactly before any rounding) and the block's scales.
+template <int TYPE>  // 12 Q4_K, 13 Q5_K, 14 Q6_K
+DEV void kq_lane_dot(const uint8_t *__restrict__ wrow, const uint8_t *__restrict__ arow, int b, int i, bool valid,
+                     int32_t *sub_ia, int32_t *sub_im, float *d8o, float *dwo, float *dmo) {
+    if (!valid) return;
+    const uint8_t *ab = arow + (int64_t)b * Q8K_BYTES;
+    const float d8 = __uint_as_float(ld4(ab));
+    *d8o = d8;
+    if constexpr (TYPE == 14) {
+        // lane i: half j = i / 2, 16-element column hh = i % 2 of each quarter q
+        const int j = i >> 1, hh = i & 1;
+        const uint8_t *blk = wrow + (int64_t)b * Q6K_BYTES;
+        const uint4 l0 = ld16(blk + 64 * j + 16 * hh), l1 = ld16(blk + 64 * j + 16 * hh + 32);
+        const uint4 qh = ld16(blk + 128 + 32 * j + 16 * hh);
+        const uint2 scv = ld8(blk + 192 + 8 * j);
+        const float dw = h2f(ld2(blk + 208));
+        const uint32_t la[4] = {l0.x, l0.y, l0.z, l0.w}, lb[4] = {l1.x, l1.y, l1.z, l1.w};
+        const uint32_t hv[4] = {qh.x, qh.y, qh.z, qh.w};
+        int is = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint4 y = ld16(ab + 4 + 128 * j + 16 * hh + 32 * q);
+            const uint32_t yv[4] = {y.x, y.y, y.z, y.w};
+            int dq = 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t src = (q & 1) ? lb[k] : la[k];
+                const uint32_t nib = (q & 2) ? ((src >> 4) & 0x0f0f0f0f) : (src & 0x0f0f0f0f);
+                dq = dot4(nib | (((hv[k] >> (2 * q)) & 0x03030303) << 4), yv[k], dq);
+            }
+            const int bs32 = 32 * (int)(int16_t)ld2(ab + 260 + 2 * (8 * j + hh + 2 * q));
+            const uint32_t sw = q < 2 ? scv.x : scv.y;
+            const int sc = (int)(int8_t)(sw >> (8 * hh + 16 * (q & 1)));
+            is += sc * (dq - bs32);
+        }
+        *sub_ia = is;
+        *dwo = dw;
+    } else {
+        constexpr bool Q5 = TYPE == 13;
+        constexpr int BB = Q5 ? 176 : Q4K_BYTES;
+        const uint8_t *blk = wrow + (int64_t)b * BB;
+        const uint4 hd = ld16(blk);
+        const uint4 x0 = ld16(blk + (Q5 ? 48 : 16) + 32 * i), x1 = ld16(blk + (Q5 ? 64 : 32) + 32 * i);
+        const float dw = h2f(hd.x), dmin = h2f(hd.x >> 16);
+        int sc0, sc1, m0, m1;
+        k4_scales(hd.y, hd.z, hd.w, scale_sel(i), sc0, sc1, m0, m1);
+        const uint32_t qv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            lo[k] = qv[k] & 0x0f0f0f0f;
+            hi[k] = (qv[k] >> 4) & 0x0f0f0f0f;
+        }
+        if constexpr (Q5) {
+            const uint4 g0 = ld16(blk + 16), g1 = ld16(blk + 32);
+            const uint32_t hv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint32_t q2 = hv[k] >> (2 * i);
+                lo[k] |= (q2 & 0x01010101u) << 4;
+                hi[k] |= (q2 << 3) & 0x10101010u;
+            }
+        }
+        const uint4 a0 = ld16(ab + 4 + 64 * i), a1 = ld16(ab + 20 + 64 * i);
+        const uint4 a2 = ld16(ab + 36 + 64 * i), a3 = ld16(ab + 52 + 64 * i);
+        const uint32_t al[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        const uint32_t ah[8] = {a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+        int dl = 0, dh = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            dl = dot4(lo[k], al[k], dl);
+            dh = dot4(hi[k], ah[k], dh);
+        }
+        const uint2 bsv = ld8(ab + 260 + 8 * i);  // bsum16 of 16-groups 4i .. 4i+3
+        const int bs0 = (int)(int16_t)(bsv.x & 0xffff) + (int)(int16_t)(bsv.x >> 16);
+        const int bs1 = (int)(int16_t)(bsv.y & 0xffff) + (int)(int16_t)(bsv.y >> 16);
+        const int ia = __mul24(sc0, dl) + __mul24(sc1, dh);
+        const int im = __mul24(m0, bs0) + __mul24(m1, bs1);
+        *sub_ia = ia;
+        *sub_im = im;
+        *dwo = dw;
+        *dmo = dmin;
+    }
+}
+
+// grid: (tiles, ceil(rows / 16)); route as written by ghip_moe_route
+template <int TYPE, bool SUBSUMS>
+__device__ __forceinline__ void mmid_kq_impl(const uint8_t *__restrict__ as, int64_t as_nb1, int64_t as_nb2,
+                                             const uint8_t *__restrict__ act, int64_t act_rb, int ne11,
+                                             const int32_t *__restrict__ route, int n_pairs, int n_ids,
+                                             float *__restrict__ dst, int64_t dst_nb1, int64_t dst_nb2, int rows,
+                                             int nb, int32_t *__restrict__ sub) {
+    const int tile = blockIdx.x;
+    if (tile >= route[0]) return;
+    const int32_t *tl = route + 2 + n_pairs + 3 * tile;
+    const int e = tl[0], first = tl[1], count = tl[2];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = (int)blockIdx.y * 16 + wave * MMID_RB;
+    const int i = lane & 3;
+    const uint8_t *ebase = as + (int64_t)e * as_nb2;
+    for (int pi = 0; pi < count; pi++) {
+        const int p = route[2 + first + pi];
+        const int t = p / n_ids, s = p - t * n_ids;
+        const uint8_t *arow = act + ((int64_t)t * ne11 + s % ne11) * act_rb;
+        float part[MMID_RB];
+#pragma unroll
+        for (int rr = 0; rr < MMID_RB; rr++) part[rr] = 0.0f;
+        for (int c = 0; c < nb; c += 16) {
+            const int b = c + (lane >> 2);
+            const bool valid = b < nb;
+#pragma unroll
+            for (int rr = 0; rr < MMID_RB; rr++) {
+                const int r = min(r0 + rr, rows - 1);
+                int32_t ia = 0, im = 0;
+                float d8 = 0.0f, dw = 0.0f, dm = 0.0f;
+                kq_lane_dot<TYPE>(ebase + (int64_t)r * as_nb1, arow, b, i, valid, &ia, &im, &d8, &dw, &dm);
+                // whole super-block sums (exact), then the block scale
+                // d = d8 * dw applied once per super-block (vec_dot.rs:881-909,
+                // vec_dot.rs:998-1028)
+                const int iab = quad_sum_dpp(ia), imb = TYPE == 14 ? 0 : quad_sum_dpp(im);
+                if (i == 0)
+                    part[rr] += TYPE == 14 ? (d8 * dw) * (float)iab
+                                           : fmaf(d8 * dw, (float)iab, (-d8 * dm) * (float)imb);
+                if (SUBSUMS) {
+                    if (i == 0 && valid && r0 + rr < rows) {
+                        int32_t *sp = sub + ((int64_t)p * rows + r0 + rr) * nb * (TYPE == 14 ? 1 : 2);
+                        if (TYPE == 14) sp[b] = iab;
+                        else {
+                            sp[2 * b] = iab;
+                            sp[2 * b + 1] = imb;
+                        }
+                    }
+                }
+            }
+        }
+        float *o = dst + (int64_t)t * dst_nb2 + (int64_t)s * dst_nb1;
+#pragma unroll
+        for (int rr = 0; rr < MMID_RB; rr++) {
+            const float tot = wave_sum_dpp(part[rr]);
+            if (lane == 0 && r0 + rr < rows) o[r0 + rr] = tot;
+        }
+    }
+}
+#define MMID_KQ(TN, TYPE)                                                                                           \
+    extern "C" __global__ void __launch_bounds__(256)                                                               \
+        ghip_mmid_##TN(const uint8_t *__restrict__ as, int64_t as_nb1, int64_t as_nb2,                             \
+                       const uint8_t *__restrict__ act, int64_t act_rb, int ne11, const int32_t *__restrict__ route, \
+                       int n_pairs, int n_ids, float *__restrict__ dst, int64_t dst_nb1, int64_t dst_nb2, int rows,  \
+                       int nb, int32_t *__restrict__ sub) {                                                          \
+        mmid_kq_impl<TYPE, false>(as, as_nb1, as_nb2, act, act_rb, ne11, route, n_pairs, n_ids, dst, dst_nb1,      \
+                                  dst_nb2, rows, nb, sub);                                                          \
+    }                                                                                                               \
+    extern "C" __global__ void __launch_bounds__(256)                                                               \
+        ghip_mmid_##TN##_sub(const uint8_t *__restrict__ as, int64_t as_nb1, int64_t as_nb2,                        \
+                             const uint8_t *__restrict__ act, int64_t act_rb, int ne11,                             \
+                             const int32_t *__restrict__ route, int n_pairs, int n_ids, float *__restrict__ dst,    \
+                             int64_t dst_nb1, int64_t dst_nb2, int rows, int nb, int32_t *__restrict__ sub) {       \
+        mmid_kq_impl<TYPE, true>(as, as_nb1, as_nb2, act, act_rb, ne11, route, n_pairs, n_ids, dst, dst_nb1,       \
+                                 dst_nb2, rows, nb, sub);                                                           \
+    }
+MMID_KQ(q4_K, 12)
+MMID_KQ(q5_K, 13)
+MMID_KQ(q6_K, 14)

@@ -47,8 +47,9 @@ def mul_mat_node(w, wtype, k, x, out):
     return Node(OP_MUL_MAT, [describe(w, wtype, k), describe(x, xty, k)], describe(out, F32))
 
 
-def mul_mat_id_node(experts, k, b, ids, out):
-    return Node(OP_MUL_MAT_ID, [describe(experts, MXFP4, k), describe(b, F32), describe(ids, I32)], describe(out, F32))
+def mul_mat_id_node(experts, k, b, ids, out, ty=None):
+    ty = MXFP4 if ty is None else ty
+    return Node(OP_MUL_MAT_ID, [describe(experts, ty, k), describe(b, F32), describe(ids, I32)], describe(out, F32))
 
 
 def flash_attn_node(q, k, v, mask, sinks, out, scale=1.0, max_bias=0.0, softcap=0.0):
@@ -215,21 +216,28 @@ class Backend:
         return out
 
     # ---- MUL_MAT_ID
-    def mul_mat_id(self, experts, k, b, ids, out=None):
-        """experts [n_as, rows, row_bytes] MXFP4, b [n_tokens, ne11, K] f32,
-        ids [n_tokens, n_ids] int32 -> out [n_tokens, n_ids, rows] f32."""
+    def mul_mat_id(self, experts, k, b, ids, out=None, ty=None):
+        """experts [n_as, rows, row_bytes] (MXFP4 unless ty is Q4_K, Q5_K or
+        Q6_K), b [n_tokens, ne11, K] f32, ids [n_tokens, n_ids] int32 ->
+        out [n_tokens, n_ids, rows] f32."""
+        ty = MXFP4 if ty is None else ty
         n_tokens, n_ids = ids.shape
         if out is None:
             out = torch.empty((n_tokens, n_ids, experts.shape[1]), dtype=torch.float32, device=b.device)
-        a, tb, ti, d = describe(experts, MXFP4, k), describe(b, F32), describe(ids, I32), describe(out, F32)
+        a, tb, ti, d = describe(experts, ty, k), describe(b, F32), describe(ids, I32), describe(out, F32)
         self._check(lib().ghip_mul_mat_id(self._ctx, C.byref(a), C.byref(tb), C.byref(ti), C.byref(d), _stream()),
                     "ghip_mul_mat_id")
         return out
 
-    def mul_mat_id_subsums(self, experts, k, b, ids):
+    def mul_mat_id_subsums(self, experts, k, b, ids, ty=None):
+        """MXFP4: the int32 block dots [n_tokens, n_ids, rows, K / 32];
+        Q4_K / Q5_K: (iacc, imin) per super-block [.., rows, K / 256, 2];
+        Q6_K: is per super-block [.., rows, K / 256]."""
+        ty = MXFP4 if ty is None else ty
         n_tokens, n_ids = ids.shape
-        sub = torch.full((n_tokens, n_ids, experts.shape[1], k // 32), -1, dtype=torch.int32, device=b.device)
-        a, tb, ti = describe(experts, MXFP4, k), describe(b, F32), describe(ids, I32)
+        per = {MXFP4: (k // 32,), Q4_K: (k // 256, 2), Q5_K: (k // 256, 2), Q6_K: (k // 256,)}[ty]
+        sub = torch.full((n_tokens, n_ids, experts.shape[1], *per), -1, dtype=torch.int32, device=b.device)
+        a, tb, ti = describe(experts, ty, k), describe(b, F32), describe(ids, I32)
         self._check(lib().ghip_mul_mat_id_subsums(self._ctx, C.byref(a), C.byref(tb), C.byref(ti),
                                                   C.c_void_p(sub.data_ptr()), _stream()), "ghip_mul_mat_id_subsums")
         return sub

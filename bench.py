@@ -234,29 +234,80 @@ def measured_traffic():
     return None
 
 
+def _profile_ops(be, torch, np, what):
+    """One launch closure per profiled kernel family, on the bench's shapes."""
+    import ghip
+    g = torch.Generator(device="cuda").manual_seed(0)
+    if what in ("gemv", "copy"):
+        k, nr = 4096, 14336
+        rng = np.random.default_rng(0)
+        wf = torch.from_numpy(rng.standard_normal((nr, k), dtype=np.float32) * np.float32(0.02)).cuda()
+        w0 = be.quantize(wf, ghip.Q4_K)
+        del wf
+        ws = [w0] + [w0.clone() for _ in range(15)]
+        x = torch.from_numpy(np.random.default_rng(1).standard_normal((1, k), dtype=np.float32)).cuda()
+        out = torch.empty((1, nr), dtype=torch.float32, device="cuda")
+        if what == "gemv":
+            return lambda i: be.mul_mat(ws[i % 16], ghip.Q4_K, k, x, out=out)
+        # one 33,030,144-byte device-to-device copy per launch
+        return lambda i: ws[(i + 1) % 16].copy_(ws[i % 16])
+    if what in ("gemm", "gemm_q6k", "decode_b8"):
+        ty, m, k, n = {"gemm": (ghip.Q4_K, 512, 4096, 14336), "gemm_q6k": (ghip.Q6_K, 512, 14336, 4096),
+                       "decode_b8": (ghip.Q4_K, 8, 4096, 14336)}[what]
+        copies = 16 if what == "decode_b8" else 1
+        wf = torch.randn((n, k), device="cuda", generator=g) * 0.02
+        ws = [be.quantize(wf, ty)]
+        del wf
+        ws += [ws[0].clone() for _ in range(copies - 1)]
+        x = torch.randn((m, k), device="cuda", generator=g)
+        out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        return lambda i: be.mul_mat(ws[i % copies], ty, k, x, out=out)
+    if what == "moe":
+        n_as, n_tok, n_ids, k, rows = 32, 256, 4, 2880, 5760
+        rng = np.random.default_rng(3)
+        ids = torch.from_numpy(np.argsort(-rng.standard_normal((n_tok, n_as)), axis=1)[:, :n_ids]
+                               .astype(np.int32)).cuda()
+        wf = torch.randn((n_as * rows, k), device="cuda", generator=g) * 0.02
+        w = be.quantize(wf, ghip.MXFP4).view(n_as, rows, -1)
+        del wf
+        b = torch.randn((n_tok, 1, k), device="cuda", generator=g)
+        out = torch.empty((n_tok, n_ids, rows), dtype=torch.float32, device="cuda")
+        return lambda i: be.mul_mat_id(w, k, b, ids, out=out)
+    if what in ("fa_decode", "fa_prefill"):
+        H, Hkv, D, S = 32, 8, 128, 8192
+        T = 1 if what == "fa_decode" else 512
+        kk = torch.randn((Hkv, S, D), device="cuda", generator=g).half()
+        v = torch.randn((Hkv, S, D), device="cuda", generator=g).half()
+        q = torch.randn((H, T, D), device="cuda", generator=g)
+        mask = torch.zeros((T, S), dtype=torch.float16, device="cuda")
+        for t in range(T):
+            mask[t, S - T + t + 1:] = float("-inf")
+        out = torch.empty((T, H, D), dtype=torch.float32, device="cuda")
+        return lambda i: be.flash_attn_ext(q, kk, v, mask, None, 1.0 / D ** 0.5, out=out)
+    raise ValueError(what)
+
+
+PROFILE_WORKLOADS = ["gemv", "copy", "gemm", "gemm_q6k", "decode_b8", "moe", "fa_decode", "fa_prefill"]
+
+
 def profile_loop(what, n):
-    """Plain launch loops for rocprofv3 runs (no JSON): the dominant GEMV
-    kernel, or the copy kernel used to calibrate FETCH_SIZE / WRITE_SIZE."""
+    """Plain launch loops for rocprofv3 runs (no JSON): one kernel family on
+    the bench's shape, or the copy kernel used to calibrate FETCH_SIZE /
+    WRITE_SIZE.  gemv: Q4_K 4096->14336 at batch 1 over 16 weight copies;
+    copy: 33,030,144-byte device copies; gemm: Q4_K 512x4096->14336;
+    gemm_q6k: Q6_K 512x14336->4096; decode_b8: Q4_K 4096->14336 at 8 rows over
+    16 copies; moe: MXFP4 gate_up (32 experts, 256 tokens, top-4);
+    fa_decode / fa_prefill: FLASH_ATTN_EXT 32/8 heads, D 128, KV 8192, T 1 / 512."""
     import numpy as np
     import torch
     import ghip
     be = ghip.Backend(0)
-    k, nr = 4096, 14336
-    rng = np.random.default_rng(0)
-    wf = torch.from_numpy(rng.standard_normal((nr, k), dtype=np.float32) * np.float32(0.02)).cuda()
-    w0 = be.quantize(wf, ghip.Q4_K)
-    del wf
-    ws = [w0] + [w0.clone() for _ in range(15)]
-    x = torch.from_numpy(np.random.default_rng(1).standard_normal((1, k), dtype=np.float32)).cuda()
-    out = torch.empty((1, nr), dtype=torch.float32, device="cuda")
+    launch = _profile_ops(be, torch, np, what)
     torch.cuda.synchronize()
     for i in range(n):
-        if what == "gemv":
-            be.mul_mat(ws[i % 16], ghip.Q4_K, k, x, out=out)
-        else:  # copy: one 33,030,144-byte device-to-device copy per launch
-            ws[(i + 1) % 16].copy_(ws[i % 16])
+        launch(i)
     torch.cuda.synchronize()
-    print(f"profile {what}: {n} launches, {w0.numel()} bytes per matrix", file=sys.stderr)
+    print(f"profile {what}: {n} launches", file=sys.stderr)
 
 
 def gemm_bench(be, torch, np):
@@ -435,7 +486,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the prefill GEMM / MoE / FA lines")
-    ap.add_argument("--profile", choices=["gemv", "copy"], help="launch loop for rocprofv3 (no JSON line)")
+    ap.add_argument("--profile", choices=PROFILE_WORKLOADS, help="launch loop for rocprofv3 (no JSON line)")
     ap.add_argument("--launches", type=int, default=100)
     args = ap.parse_args()
     if args.profile:

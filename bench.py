@@ -336,8 +336,9 @@ def gemm_bench(be, torch, np):
 
 def gemm_q6k_bench(be, torch, np):
     """The Q4_K_M down projection at 512 tokens (Q6_K 14336 -> 4096): the
-    f16-MFMA GEMM (weight repack + f16 code layout + GEMM) against the
-    8-column decode kernels it replaces."""
+    f16-MFMA GEMM (weight repack + f16 code layout + GEMM), the same with
+    the weight registered (repack kept on the device, as the reference's
+    repack cache), and the 8-column decode kernels it replaces."""
     import ghip
     m, k, n = 512, 14336, 4096
     g = torch.Generator(device="cuda").manual_seed(0)
@@ -347,15 +348,21 @@ def gemm_q6k_bench(be, torch, np):
     x = torch.randn((m, k), device="cuda", generator=g)
     out = torch.empty((m, n), dtype=torch.float32, device="cuda")
     us = graph_time_us(torch, lambda i: be.mul_mat(w, ghip.Q6_K, k, x, out=out), 10)
+    be.register_weight(w, ghip.Q6_K, k)  # the repacked records kept on the device
+    us_reg = graph_time_us(torch, lambda i: be.mul_mat(w, ghip.Q6_K, k, x, out=out), 10)
+    be.unregister_weight(w, ghip.Q6_K, k)
     os.environ["GHIP_GEMM_Q6K_MIN_ROWS"] = str(1 << 30)
     try:
         us_gemv = graph_time_us(torch, lambda i: be.mul_mat(w, ghip.Q6_K, k, x, out=out), 2, reps=2)
     finally:
         del os.environ["GHIP_GEMM_Q6K_MIN_ROWS"]
     ops = 2.0 * m * n * k
-    log(f"Q6_K GEMM {m}x{k}->{n}: op {us:.1f} us ({ops / us / 1e6:.1f} TOPS); 8-column decode kernels {us_gemv:.1f} us")
+    log(f"Q6_K GEMM {m}x{k}->{n}: op {us:.1f} us ({ops / us / 1e6:.1f} TOPS), registered weight {us_reg:.1f} us "
+        f"({ops / us_reg / 1e6:.1f} TOPS); 8-column decode kernels {us_gemv:.1f} us")
     return {f"{m}x{k}->{n}": {"us_op": round(us, 2), "TOPS_op": round(ops / us / 1e6, 1),
                               "frac_f16_peak": round(ops / us / 1e6 / 2500.0, 4),
+                              "us_op_registered_weight": round(us_reg, 2),
+                              "TOPS_op_registered_weight": round(ops / us_reg / 1e6, 1),
                               "us_op_8col_decode_kernels": round(us_gemv, 2)}}
 
 

@@ -247,6 +247,30 @@ ghip_status ghip_set_workspace(ghip_context *ctx, void *ptr, size_t bytes);
 ghip_status ghip_workspace_size(int op, const ghip_tensor *dst, const ghip_tensor *const *srcs, int n_srcs,
                                 size_t *bytes);
 
+/* Declare `w` (a 2-D weight in device memory, GGUF block layout) immutable
+ * and keep device-side copies of it in the layouts the kernels read, built
+ * once on `stream` now instead of on every call -- the reference's repack
+ * cache (repack_*_cached, crates/ggml/src/repack.rs:4250-4480, and the
+ * CPU_REPACK buffer it stands for).  Today that is the Q6_K prefill GEMM's
+ * aligned 288-byte records; other types are read in their GGUF layout and
+ * register as a no-op.  Later MUL_MAT calls whose src0 has the same data
+ * pointer, type, ne[0], ne[1] and nb[1] use the copy.  The same switches as
+ * the reference: LLAMA_RUST_REPACK=0 turns it off, LLAMA_RUST_REPACK_MAX_MB
+ * caps the bytes kept (default 16384); a weight over the cap is not kept and
+ * calls repack it per call as before (both return success).  Allocates
+ * (hipMalloc): fails with GHIP_STATUS_ALLOC_FAILED while `stream` is being
+ * captured.  The weight's bytes must not change until
+ * ghip_weight_unregister. */
+ghip_status ghip_weight_register(ghip_context *ctx, const ghip_tensor *w, void *stream);
+
+/* Drop the copies kept for `w` (waits for the device first, so queued work
+ * that reads them completes).  Unknown weights are a no-op. */
+ghip_status ghip_weight_unregister(ghip_context *ctx, const ghip_tensor *w);
+
+/* Copies kept, their bytes, and how many were built so far (hits do not
+ * count) -- repack_stats (repack.rs:4329-4334).  Any pointer may be NULL. */
+ghip_status ghip_weight_cache_stats(ghip_context *ctx, size_t *n_weights, size_t *bytes, size_t *built);
+
 /* Quantize nrows rows of n_per_row f32 values (device pointer src) into
  * GGUF blocks of `type` (Q4_0, Q4_K, Q6_K, MXFP4) at the device pointer dst,
  * byte-identical to the reference's no-imatrix quantizers

@@ -12,6 +12,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <strings.h>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -83,6 +84,29 @@ struct ghip_context {
     bool have_last = false;
     hipEvent_t order_ev = nullptr;
     std::mutex mu;
+    // Device copies of registered weights in the layouts the kernels read
+    // (ghip_weight_register), keyed by where and what the weight is.
+    struct WeightKey {
+        const void *data;
+        int type;
+        int64_t ne0, ne1;
+        uint64_t nb1;
+        bool operator==(const WeightKey &o) const {
+            return data == o.data && type == o.type && ne0 == o.ne0 && ne1 == o.ne1 && nb1 == o.nb1;
+        }
+    };
+    struct WeightKeyHash {
+        size_t operator()(const WeightKey &k) const {
+            size_t h = std::hash<const void *>()(k.data);
+            h = h * 31 + (size_t)k.type;
+            h = h * 31 + (size_t)k.ne0;
+            h = h * 31 + (size_t)k.ne1;
+            return h * 31 + (size_t)k.nb1;
+        }
+    };
+    std::unordered_map<WeightKey, void *, WeightKeyHash> wcache;
+    size_t wcache_bytes = 0;   // bytes held by wcache
+    size_t wcache_built = 0;   // copies materialized so far (hits do not count)
 
     ghip_status fail(ghip_status st, const char *fmt, ...) {
         char buf[512];
@@ -467,6 +491,18 @@ size_t gemm_layout_bytes(const MulMatPlan &p) {
 }
 // Q6_K: repack the weights into aligned records, lay the codes out as f16, then
 // the f16-MFMA GEMM on 64 x 128 tiles (one workgroup per CU, 137 KB of LDS)
+// The Q6_K weights as the GEMM's 288-byte records: rebuilt into the
+// workspace by every call, unless ghip_weight_register keeps a copy.
+ghip_status q6k_repack(ghip_context *ctx, const void *w, int64_t row_bytes, int64_t N, int64_t nbk, uint8_t *rep,
+                       hipStream_t s) {
+    const int64_t nblk = N * nbk;  // four blocks per workgroup
+    return ctx->launch("ghip_q6K_repack", dim3((unsigned)((nblk + 3) / 4)), dim3(256), 0, s, (const uint8_t *)w,
+                       row_bytes, (int)N, (int)nbk, rep);
+}
+const uint8_t *registered_q6k(ghip_context *ctx, const MulMatPlan &p, const void *w) {
+    auto it = ctx->wcache.find({w, GHIP_TYPE_Q6_K, p.K, p.N, (uint64_t)p.w_row_bytes});
+    return it == ctx->wcache.end() ? nullptr : (const uint8_t *)it->second;
+}
 ghip_status run_gemm_q6k(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act,
                          const ghip_tensor *bf, float *dst, int64_t ldd, int32_t *sub, void *layout_ws, hipStream_t s) {
     size_t codes_b, dt_b;
@@ -474,11 +510,14 @@ ghip_status run_gemm_q6k(ghip_context *ctx, const MulMatPlan &p, const void *w, 
     const int64_t Mpad = (p.M + 127) / 128 * 128, nbk = p.K / 256;
     uint16_t *codes = (uint16_t *)layout_ws;
     float *dT = (float *)((uint8_t *)layout_ws + codes_b);
-    uint8_t *rep = (uint8_t *)layout_ws + codes_b + dt_b;
-    const int64_t nblk = p.N * nbk;  // four blocks per workgroup
-    ghip_status st = ctx->launch("ghip_q6K_repack", dim3((unsigned)((nblk + 3) / 4)), dim3(256), 0, s,
-                                 (const uint8_t *)w, (int64_t)p.w_row_bytes, (int)p.N, (int)nbk, rep);
-    if (st != GHIP_STATUS_SUCCESS) return st;
+    const uint8_t *rep = registered_q6k(ctx, p, w);
+    ghip_status st = GHIP_STATUS_SUCCESS;
+    if (!rep) {
+        uint8_t *r = (uint8_t *)layout_ws + codes_b + dt_b;
+        st = q6k_repack(ctx, w, p.w_row_bytes, p.N, nbk, r, s);
+        if (st != GHIP_STATUS_SUCCESS) return st;
+        rep = r;
+    }
     if (bf)  // f32 activations: quantized straight into the layout
         st = ctx->launch("ghip_gemm_act_q8K_f16", dim3((unsigned)((p.M * nbk + 3) / 4)), dim3(256), 0, s,
                          (const float *)bf->data, (int64_t)bf->nb[1] / 4, (int)p.M, (int)Mpad, (int)nbk, (int)p.n_mat,
@@ -1238,9 +1277,85 @@ void ghip_free(ghip_context *ctx) {
     hipDeviceSynchronize();
     if (ctx->ws) hipFree(ctx->ws);
     for (void *p : ctx->retired) hipFree(p);
+    for (auto &kv : ctx->wcache) hipFree(kv.second);
     if (ctx->order_ev) hipEventDestroy(ctx->order_ev);
     for (hipModule_t m : ctx->modules) hipModuleUnload(m);
     delete ctx;
+}
+
+static bool repack_enabled() {
+    const char *v = getenv("LLAMA_RUST_REPACK");
+    return !v || !(strcmp(v, "0") == 0 || strcasecmp(v, "false") == 0);
+}
+
+static size_t repack_budget() {
+    const char *v = getenv("LLAMA_RUST_REPACK_MAX_MB");
+    const long long mb = v && *v ? atoll(v) : 16384;
+    return (size_t)std::max(0LL, mb) << 20;
+}
+
+ghip_status ghip_weight_register(ghip_context *ctx, const ghip_tensor *w, void *stream) {
+    if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    if (!w || !w->data) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: null weight");
+    if (w->ne[2] != 1 || w->ne[3] != 1) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: 2-D weights only");
+    if (w->ne[0] <= 0 || w->ne[1] <= 0) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: empty weight");
+    // every other type is read in its GGUF layout: nothing to build
+    if (w->type != GHIP_TYPE_Q6_K || !repack_enabled()) return GHIP_STATUS_SUCCESS;
+    if (w->ne[0] % 256 || w->nb[0] != 210 || w->nb[1] < (uint64_t)(w->ne[0] / 256 * 210))
+        return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: bad Q6_K geometry");
+    if (w->ne[1] > INT32_MAX || w->ne[0] / 256 > INT32_MAX)
+        return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: dimension too large");
+    const ghip_context::WeightKey key{w->data, w->type, w->ne[0], w->ne[1], w->nb[1]};
+    if (ctx->wcache.count(key)) return GHIP_STATUS_SUCCESS;
+    const int64_t N = w->ne[1], nbk = w->ne[0] / 256;
+    const size_t bytes = (size_t)N * (size_t)nbk * kQ6R;
+    if (ctx->wcache_bytes + bytes > repack_budget()) return GHIP_STATUS_SUCCESS;  // not kept: calls repack per call
+    hipStream_t s = (hipStream_t)stream;
+    if (ghip_context::capturing(s))
+        return ctx->fail(GHIP_STATUS_ALLOC_FAILED, "weight_register allocates: not while the stream is captured");
+    if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    ghip_status st = ctx->begin(s);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    void *rep = nullptr;
+    if (hipMalloc(&rep, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return ctx->fail(GHIP_STATUS_OUT_OF_MEMORY, "weight_register: hipMalloc(%zu) failed", bytes);
+    }
+    st = q6k_repack(ctx, w->data, (int64_t)w->nb[1], N, nbk, (uint8_t *)rep, s);
+    if (st != GHIP_STATUS_SUCCESS) {
+        hipFree(rep);
+        return st;
+    }
+    ctx->wcache.emplace(key, rep);
+    ctx->wcache_bytes += bytes;
+    ctx->wcache_built++;
+    return GHIP_STATUS_SUCCESS;
+}
+
+ghip_status ghip_weight_unregister(ghip_context *ctx, const ghip_tensor *w) {
+    if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    if (!w) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_unregister: null weight");
+    auto it = ctx->wcache.find({w->data, w->type, w->ne[0], w->ne[1], w->nb[1]});
+    if (it == ctx->wcache.end()) return GHIP_STATUS_SUCCESS;
+    if (hipSetDevice(ctx->device) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        (void)hipGetLastError();
+        return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_unregister: device synchronize failed");
+    }
+    hipFree(it->second);
+    ctx->wcache_bytes -= (size_t)w->ne[1] * (size_t)(w->ne[0] / 256) * kQ6R;
+    ctx->wcache.erase(it);
+    return GHIP_STATUS_SUCCESS;
+}
+
+ghip_status ghip_weight_cache_stats(ghip_context *ctx, size_t *n_weights, size_t *bytes, size_t *built) {
+    if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    if (n_weights) *n_weights = ctx->wcache.size();
+    if (bytes) *bytes = ctx->wcache_bytes;
+    if (built) *built = ctx->wcache_built;
+    return GHIP_STATUS_SUCCESS;
 }
 
 const char *ghip_last_error(const ghip_context *ctx) { return ctx ? ctx->err.c_str() : "null context"; }

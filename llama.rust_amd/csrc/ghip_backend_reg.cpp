@@ -104,6 +104,9 @@ void *reg_proc_address(const ggml_hip_backend_reg *, const char *name) {
         {"ghip_graph_compute", (void *)&ghip_graph_compute},
         {"ghip_set_workspace", (void *)&ghip_set_workspace},
         {"ghip_workspace_size", (void *)&ghip_workspace_size},
+        {"ghip_weight_register", (void *)&ghip_weight_register},
+        {"ghip_weight_unregister", (void *)&ghip_weight_unregister},
+        {"ghip_weight_cache_stats", (void *)&ghip_weight_cache_stats},
     };
     if (!name) return nullptr;
     for (const Proc &p : procs)

@@ -701,16 +701,18 @@ __device__ __forceinline__ void gemm_q6K_impl(const uint8_t *__restrict__ R, int
         const uint4 sc4 = *reinterpret_cast<const uint4 *>(wrow + 256);
         const float dw = *reinterpret_cast<const float *>(wrow + 272);
         const uint32_t scw[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
-        v16f acc[2];
-        int isub[2][16];
+        // One accumulator per scale plane: the low plane's sums stay below
+        // 256 * 480 * 127 < 2^24 and the high plane's are multiples of 16
+        // below 256 * 4096 * 127 < 2^28, so both are exact integers in fp32
+        // for any valid block, and so is is = lo + hi added as int32.
+        v16f accl[2], acch[2];
         const v16f zf = {};
 #pragma unroll
         for (int tm = 0; tm < 2; tm++) {
-            acc[tm] = zf;
-#pragma unroll
-            for (int v = 0; v < 16; v++) isub[tm][v] = 0;
+            accl[tm] = zf;
+            acch[tm] = zf;
         }
-#pragma unroll(SUBSUMS ? 1 : 16)
+#pragma unroll 16
         for (int ks = 0; ks < 16; ks++) {
             const uint2 qv = *reinterpret_cast<const uint2 *>(wrow + 16 * ks + 8 * h);
             // the sub-block's signed scale, split 16*sh + sl, as f16 pairs
@@ -732,16 +734,8 @@ __device__ __forceinline__ void gemm_q6K_impl(const uint8_t *__restrict__ R, int
 #pragma unroll
             for (int tm = 0; tm < 2; tm++) {
                 const v8h a = *reinterpret_cast<const v8h *>(SM.act[p] + aoff[tm] + 8 * ((uint32_t)(2 * ks + h) ^ asw));
-                if constexpr (SUBSUMS) {
-                    // a fresh accumulator per sub-block: exact, then integer sums
-                    const v16f c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, blo, zf, 0, 0, 0);
-                    const v16f c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bhi, c1, 0, 0, 0);
-#pragma unroll
-                    for (int v = 0; v < 16; v++) isub[tm][v] += __float2int_rn(c2[v]);
-                } else {
-                    acc[tm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, blo, acc[tm], 0, 0, 0);
-                    acc[tm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bhi, acc[tm], 0, 0, 0);
-                }
+                accl[tm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, blo, accl[tm], 0, 0, 0);
+                acch[tm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bhi, acch[tm], 0, 0, 0);
             }
         }
         // ---- out += (d * is) * d8 (vec_dot_q6_K_q8_K's per-block order)
@@ -751,14 +745,10 @@ __device__ __forceinline__ void gemm_q6K_impl(const uint8_t *__restrict__ R, int
 #pragma unroll
             for (int v = 0; v < 16; v++) {
                 const int tl = 32 * tm + crow(v, lane);
-                float is;
-                if constexpr (SUBSUMS) {
-                    is = (float)isub[tm][v];
-                    if (m0 + tl < M && n0 + wr < N) sub[((int64_t)(m0 + tl) * N + (n0 + wr)) * nb + b] = isub[tm][v];
-                } else {
-                    is = acc[tm][v];
-                }
-                out[tm][v] = fmaf(dw * is, dab[tl], out[tm][v]);
+                const int isi = (int)accl[tm][v] + (int)acch[tm][v];
+                if constexpr (SUBSUMS)
+                    if (m0 + tl < M && n0 + wr < N) sub[((int64_t)(m0 + tl) * N + (n0 + wr)) * nb + b] = isi;
+                out[tm][v] = fmaf(dw * (float)isi, dab[tl], out[tm][v]);
             }
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // super-block b+1 is in LDS

@@ -132,6 +132,12 @@ def lib():
         L.ghip_set_workspace.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
         L.ghip_workspace_size.restype = C.c_int
         L.ghip_workspace_size.argtypes = [C.c_int, P, C.POINTER(P), C.c_int, C.POINTER(C.c_size_t)]
+        L.ghip_weight_register.restype = C.c_int
+        L.ghip_weight_register.argtypes = [C.c_void_p, P, C.c_void_p]
+        L.ghip_weight_unregister.restype = C.c_int
+        L.ghip_weight_unregister.argtypes = [C.c_void_p, P]
+        L.ghip_weight_cache_stats.restype = C.c_int
+        L.ghip_weight_cache_stats.argtypes = [C.c_void_p] + [C.POINTER(C.c_size_t)] * 3
         L.ghip_flash_attn_ext.restype = C.c_int
         L.ghip_flash_attn_ext.argtypes = [C.c_void_p, P, P, P, P, P, P, C.c_void_p]
         _lib = L
@@ -204,6 +210,22 @@ class Backend:
         a, b, d = describe(w, wtype, k), describe(x, F32), describe(out, F32)
         srcs = (C.POINTER(Tensor) * 2)(C.pointer(a), C.pointer(b))
         return bool(lib().ghip_supports_op(OP_MUL_MAT, C.byref(d), srcs, 2))
+
+    # ---- weight cache
+    def register_weight(self, w, wtype, k):
+        """Keep the kernels' device layouts of weight w (immutable from now on)."""
+        a = describe(w, wtype, k)
+        self._check(lib().ghip_weight_register(self._ctx, C.byref(a), _stream()), "ghip_weight_register")
+
+    def unregister_weight(self, w, wtype, k):
+        a = describe(w, wtype, k)
+        self._check(lib().ghip_weight_unregister(self._ctx, C.byref(a)), "ghip_weight_unregister")
+
+    def weight_cache_stats(self):
+        """(weights kept, bytes kept, copies built so far)"""
+        v = [C.c_size_t() for _ in range(3)]
+        self._check(lib().ghip_weight_cache_stats(self._ctx, *[C.byref(x) for x in v]), "ghip_weight_cache_stats")
+        return tuple(x.value for x in v)
 
     def quantize(self, x, ty):
         """GGUF blocks of `ty` for the f32 rows of x [rows, n] (ggml_quantize_chunk)."""

@@ -252,7 +252,7 @@ ghip_status ghip_workspace_size(int op, const ghip_tensor *dst, const ghip_tenso
  * once on `stream` now instead of on every call -- the reference's repack
  * cache (repack_*_cached, crates/ggml/src/repack.rs:4250-4480, and the
  * CPU_REPACK buffer it stands for).  Today that is the Q6_K prefill GEMM's
- * aligned 288-byte records; other types are read in their GGUF layout and
+ * aligned 336-byte records; other types are read in their GGUF layout and
  * register as a no-op.  Later MUL_MAT calls whose src0 has the same data
  * pointer, type, ne[0], ne[1] and nb[1] use the copy.  The same switches as
  * the reference: LLAMA_RUST_REPACK=0 turns it off, LLAMA_RUST_REPACK_MAX_MB

@@ -435,7 +435,7 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
 // out for the GEMM (codes | bsum16 | d, tokens padded to 128), then the int8
 // MFMA GEMM runs on 128 x 128 tiles.
 constexpr size_t kGemmSmem128 = 116224, kGemmSmem64 = 76544;  // sizeof(g3::Smem<BM>) in ghip_gemm.hip
-constexpr size_t kGemmSmemQ6 = 140032;                         // sizeof(g6::Smem) in ghip_gemm.hip
+constexpr size_t kGemmSmemQ6 = 152320;                         // sizeof(g6::Smem) in ghip_gemm.hip
 constexpr size_t kGemmSmemW8 = 148480;  // 2 * sizeof(g4::Stage<256>) in ghip_gemm.hip
 // GHIP_GEMM_BM=128 selects the 128 x 128 tiles of gemm_q4K_impl
 int gemm_bm() { return env_int("GHIP_GEMM_BM", 64) == 128 ? 128 : 64; }
@@ -471,8 +471,8 @@ int gemm_nsplit(const MulMatPlan &p) {
     const int64_t nbs = (p.nb + want - 1) / want;  // super-blocks per slice
     return (int)((p.nb + nbs - 1) / nbs);
 }
-// Q6_K prefill workspace: f16 codes [Mpad][K] | dT [nb][Mpad] | repacked weights [N][nb][288]
-constexpr size_t kQ6R = 288;
+// Q6_K prefill workspace: f16 codes [Mpad][K] | dT [nb][Mpad] | repacked weights [N][nb][336]
+constexpr size_t kQ6R = 336;
 size_t gemm_q6k_bytes(const MulMatPlan &p, size_t *codes_b, size_t *dt_b) {
     const size_t Mpad = (size_t)(p.M + 127) / 128 * 128, nbk = (size_t)p.K / 256;
     *codes_b = (Mpad * (size_t)p.K * 2 + 255) & ~(size_t)255;
@@ -491,7 +491,7 @@ size_t gemm_layout_bytes(const MulMatPlan &p) {
 }
 // Q6_K: repack the weights into aligned records, lay the codes out as f16, then
 // the f16-MFMA GEMM on 64 x 128 tiles (one workgroup per CU, 137 KB of LDS)
-// The Q6_K weights as the GEMM's 288-byte records: rebuilt into the
+// The Q6_K weights as the GEMM's 336-byte records: rebuilt into the
 // workspace by every call, unless ghip_weight_register keeps a copy.
 ghip_status q6k_repack(ghip_context *ctx, const void *w, int64_t row_bytes, int64_t N, int64_t nbk, uint8_t *rep,
                        hipStream_t s) {

@@ -558,19 +558,18 @@ GEMM_WIDE_KERNELS(ghip_gemm_q4_K_w8, 8, 1)
 //    (sl = sc & 15, sh = sc >> 4), two f16 planes per K-step:
 //      (q - 32) * sl        |.| <= 480,  an integer, exact in f16;
 //      (q - 32) * 16 * sh   a multiple of 16 with |.| <= 4096, exact in f16.
-//    Every product with a code (|q8| <= 128) is exact in fp32, and both planes
-//    add into one fp32 accumulator per super-block, which is then `is`.  The
-//    sub-sum kernels take a fresh accumulator per 16-element sub-block (all
-//    partial sums < 2^24) and add the sub-blocks as integers, so their `is`
-//    is exact whatever the data.
-// The 210-byte blocks start at odd 2-byte offsets; ghip_q6K_repack first
-// rewrites them per call into aligned 288-byte records:
-//   q[256] (6-bit values 0..63 in element order) | sc[16] int8 | d f32 | pad.
-constexpr int Q6R_BYTES = 288;
+//    Every product with a code (|q8| <= 128) is exact in fp32; each plane has
+//    its own fp32 accumulator per super-block, whose sums stay exact integers
+//    (below 2^24, or multiples of 16 below 2^28), and is = lo + hi in int32.
+// The 210-byte blocks start at odd 2-byte offsets; ghip_q6K_repack rewrites
+// them (per call, or once for a registered weight) into aligned 336-byte
+// records:  q[256] (6-bit values 0..63 in element order) | 16 x (f16 sl,
+// f16 16*sh) | d f32 | pad.
+constexpr int Q6R_BYTES = 336;
 
 // one 64-lane group per block: the block's bytes arrive with coalesced dword
 // loads from its 4-byte-aligned base into LDS, then lane u writes elements
-// 4u .. 4u+3 (and lanes 0..7 the scales, d and padding)
+// 4u .. 4u+3 (and lanes 0..19 the scale pairs, d and padding)
 extern "C" __global__ void __launch_bounds__(256)
 ghip_q6K_repack(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb, uint8_t *__restrict__ out) {
     __shared__ uint32_t stage[4][56];  // 224 bytes per group
@@ -600,14 +599,18 @@ ghip_q6K_repack(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int n
 #pragma unroll
     for (int k = 0; k < 4; k++) v |= (uint32_t)(((ql[k] >> nsh) & 15) | (((qh[k] >> hsh) & 3) << 4)) << (8 * k);
     *reinterpret_cast<uint32_t *>(dst + e4) = v;
-    if (u < 4) {
-        const uint8_t *sc = blkb + 192 + 4 * u;
+    if (u < 16) {
+        // sub-block u's signed scale split 16 * sh + sl, as the f16 pair
+        // (sl, 16 * sh) the GEMM multiplies the weight planes by
+        const int sc = (int)(int8_t)blkb[192 + u];
+        const int sl = sc & 15;
+        const _Float16 fl = (_Float16)(float)sl, fh = (_Float16)(float)(sc - sl);
         *reinterpret_cast<uint32_t *>(dst + 256 + 4 * u) =
-            (uint32_t)sc[0] | ((uint32_t)sc[1] << 8) | ((uint32_t)sc[2] << 16) | ((uint32_t)sc[3] << 24);
-    } else if (u == 4) {
-        *reinterpret_cast<float *>(dst + 272) = h2f((uint32_t)blkb[208] | ((uint32_t)blkb[209] << 8));
-    } else if (u < 8) {
-        *reinterpret_cast<uint32_t *>(dst + 276 + 4 * (u - 5)) = 0u;
+            (uint32_t)__builtin_bit_cast(uint16_t, fl) | ((uint32_t)__builtin_bit_cast(uint16_t, fh) << 16);
+    } else if (u == 16) {
+        *reinterpret_cast<float *>(dst + 320) = h2f((uint32_t)blkb[208] | ((uint32_t)blkb[209] << 8));
+    } else if (u < 20) {
+        *reinterpret_cast<uint32_t *>(dst + 324 + 4 * (u - 17)) = 0u;
     }
 }
 
@@ -632,7 +635,7 @@ namespace g6 {
 constexpr int BM = 64, BN = 128;
 struct Smem {
     _Float16 act[2][BM * QK_K];     // [stage][token][256], 16-byte slots swizzled by token % 32
-    uint8_t w[2][BN * Q6R_BYTES];   // [stage][row][288]
+    uint8_t w[2][BN * Q6R_BYTES];   // [stage][row][336]
     float da[3][BM];                // block scales of the tokens, a 3-slot ring
 };
 }  // namespace g6
@@ -661,24 +664,39 @@ __device__ __forceinline__ void gemm_q6K_impl(const uint8_t *__restrict__ R, int
     const int m0 = (id % n_tiles_m) * BM;
     const int n0 = (id / n_tiles_m) * BN;
 
+    // buffer descriptors over this tile's activations, weight records and
+    // block scales; the per-lane offsets are fixed, super-block b adds a
+    // scalar offset.  Weight rows past N read as zeros (range-checked).
+    const brsrc ra = make_rsrc(codes + (int64_t)m0 * K, (uint32_t)((int64_t)BM * K * 2));
+    const brsrc rw = make_rsrc(R + (int64_t)n0 * nb * Q6R_BYTES, (uint32_t)((int64_t)min(BN, N - n0) * nb * Q6R_BYTES));
+    const brsrc rd = make_rsrc(dT + m0, (uint32_t)(((int64_t)nb * Mpad - m0) * 4));
+    uint32_t va[8], vw[11];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int tok = 2 * (8 * wave + i) + (lane >> 5);
+        const int slot = (lane & 31) ^ (tok & 31);
+        va[i] = (uint32_t)tok * (uint32_t)K * 2u + 16u * (uint32_t)slot;
+    }
+#pragma unroll
+    for (int i = 0; i < 11; i++) {
+        const int c = 64 * (4 * i + wave) + lane;
+        const int row = c / 21, k16 = c - 21 * row;
+        vw[i] = (uint32_t)row * (uint32_t)nb * Q6R_BYTES + 16u * (uint32_t)k16;
+    }
+
     // ---- direct loads of super-block b: wavefront w moves act pieces
-    // 8w .. 8w+7 (2 tokens each), weight pieces 9w .. 9w+8 (64 16-byte
-    // chunks each) and (w = 0) the block scales
+    // 8w .. 8w+7 (2 tokens each), weight pieces w, w+4, .. (64 16-byte
+    // chunks each, 21 per row) and (w = 0) the block scales
     auto issue = [&](int b, int p) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int tok = 2 * (8 * wave + i) + (lane >> 5);
-            const int slot = (lane & 31) ^ (tok & 31);
-            g2lds(codes + (int64_t)(m0 + tok) * K + (int64_t)b * QK_K + 8 * slot,
-                  reinterpret_cast<uint8_t *>(SM.act[p]) + 1024 * (8 * wave + i));
-        }
+        for (int i = 0; i < 8; i++)
+            b2lds(ra, reinterpret_cast<uint8_t *>(SM.act[p]) + 1024 * (8 * wave + i), va[i], (uint32_t)b * 512u);
 #pragma unroll
-        for (int i = 0; i < 9; i++) {
-            const int c = 64 * (9 * wave + i) + lane;
-            const int row = c / 18, k16 = c - 18 * row;
-            g2lds(R + ((int64_t)min(n0 + row, N - 1) * nb + b) * Q6R_BYTES + 16 * k16, SM.w[p] + 1024 * (9 * wave + i));
+        for (int i = 0; i < 11; i++) {
+            const int g = 4 * i + wave;  // 42 groups of 64 chunks
+            if (g < BN * (Q6R_BYTES / 16) / 64) b2lds(rw, SM.w[p] + 1024 * g, vw[i], (uint32_t)b * Q6R_BYTES);
         }
-        if (wave == 0 && lane < BM / 4) g2lds(dT + (int64_t)b * Mpad + m0 + 4 * lane, SM.da[b % 3]);
+        if (wave == 0 && lane < BM / 4) b2lds(rd, SM.da[b % 3], 16u * lane, (uint32_t)b * (uint32_t)Mpad * 4u);
     };
 
     v16f out[2];
@@ -698,9 +716,7 @@ __device__ __forceinline__ void gemm_q6K_impl(const uint8_t *__restrict__ R, int
         const int p = b & 1;
         if (b + 1 < nb) issue(b + 1, p ^ 1);
         const uint8_t *wrow = SM.w[p] + wr * Q6R_BYTES;
-        const uint4 sc4 = *reinterpret_cast<const uint4 *>(wrow + 256);
-        const float dw = *reinterpret_cast<const float *>(wrow + 272);
-        const uint32_t scw[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
+        const float dw = *reinterpret_cast<const float *>(wrow + 320);
         // One accumulator per scale plane: the low plane's sums stay below
         // 256 * 480 * 127 < 2^24 and the high plane's are multiples of 16
         // below 256 * 4096 * 127 < 2^28, so both are exact integers in fp32
@@ -715,11 +731,10 @@ __device__ __forceinline__ void gemm_q6K_impl(const uint8_t *__restrict__ R, int
 #pragma unroll 16
         for (int ks = 0; ks < 16; ks++) {
             const uint2 qv = *reinterpret_cast<const uint2 *>(wrow + 16 * ks + 8 * h);
-            // the sub-block's signed scale, split 16*sh + sl, as f16 pairs
-            const int sc = (int)(int8_t)(scw[ks >> 2] >> (8 * (ks & 3)));
-            const int sl = sc & 15, sh16 = sc - sl;
-            const _Float16 fl = (_Float16)(float)sl, fh = (_Float16)(float)sh16;
-            const v2h pl = {fl, fl}, ph = {fh, fh};
+            // the sub-block's signed scale split 16 * sh + sl, as f16 pairs
+            const uint32_t sp = *reinterpret_cast<const uint32_t *>(wrow + 256 + 4 * ks);
+            const v2h pl = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(sp, sp, 0x01000100u));
+            const v2h ph = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(sp, sp, 0x03020302u));
             v8h blo, bhi;
             const uint32_t qw[2] = {qv.x, qv.y};
 #pragma unroll
@@ -775,7 +790,7 @@ extern "C" __global__ void __launch_bounds__(256, 1)
                        int32_t *__restrict__ sub) {
     gemm_q6K_impl<true>(R, N, nb, codes, dT, M, Mpad, dst, ldd, sub);
 }
-static_assert(sizeof(g6::Smem) == 140032, "host code launches with this LDS size");
+static_assert(sizeof(g6::Smem) == 152320, "host code launches with this LDS size");
 
 // split-K partial sums [nsplit][M][N] -> dst, slices added in order; four
 // consecutive outputs per thread (N % 4 == 0)

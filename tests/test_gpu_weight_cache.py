@@ -49,7 +49,7 @@ def test_register_reuses_copy_bit_identical(be):
     be.register_weight(w, O.Q6_K, n)  # second registration: a hit
     n1, b1, built1 = be.weight_cache_stats()
     assert (n1, built1) == (n0 + 1, built0 + 1)
-    assert b1 - b0 == rows * (n // 256) * 288
+    assert b1 - b0 == rows * (n // 256) * 336  # one 336-byte GEMM record per super-block
     first = be.mul_mat(w, O.Q6_K, n, x).clone()
     second = be.mul_mat(w, O.Q6_K, n, x).clone()
     assert be.weight_cache_stats()[2] == built1  # calls read the copy, build nothing

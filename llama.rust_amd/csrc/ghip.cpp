@@ -734,6 +734,14 @@ FaLayout fa_layout(int D, int T, int H, int S, int H_kv) {
 
 // ------------------------------------------------------------ MUL_MAT_ID
 
+// MXFP4 expert kernel: the scaled-FP4 one (32-pair tiles) unless
+// GHIP_MOE_KERNEL=f16 asks for the f16 one
+bool moe_fp4(int tp) {
+    const char *v = getenv("GHIP_MOE_KERNEL");
+    (void)tp;
+    return !(v && strcmp(v, "f16") == 0);
+}
+
 struct MoePlan {
     int wtype;  // MXFP4, or Q4_K / Q5_K / Q6_K experts
     int64_t K, rows, n_as, ne11, n_tokens, n_ids, nb;
@@ -798,7 +806,7 @@ MoeWs moe_ws(const MoePlan &p, bool has_dst, bool sub) {
     auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
     L.act = up((size_t)(p.ne11 * p.n_tokens * p.act_row_bytes));
     const bool kq = p.wtype != GHIP_TYPE_MXFP4;  // K-quants read the Q8_K rows directly
-    if (kq) L.tp = 32;
+    if (kq) L.tp = 32;  // the K-quant kernel takes 32-pair tiles
     L.max_tiles = (n_pairs + L.tp - 1) / L.tp + p.n_as;
     L.actf = kq ? 0 : up((size_t)n_pairs * p.nb * 64);  // per routed pair
     L.actd = kq ? 0 : up((size_t)n_pairs * p.nb * 4);
@@ -863,13 +871,19 @@ ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip
                            (const int32_t *)route, (int)n_pairs, (int)p.n_ids, dst, dst_nb1, dst_nb2, (int)p.rows,
                            (int)p.nb, sub);
     }
-    // f16 codes of every routed pair, in the routed order
+    // The scaled-FP4 kernel (FP8 planes of the codes), or with GHIP_MOE_KERNEL=f16
+    // the f16 kernel (f16 codes); both write 64 bytes per routed pair and block
+    const bool fp4 = moe_fp4(tp);
     const unsigned fgrid = (unsigned)((n_pairs * p.nb * 4 + 255) / 256);
-    st = ctx->launch("ghip_moe_act_f16", dim3(fgrid), dim3(256), 0, s, (const uint8_t *)act, p.act_row_bytes,
-                     (const int32_t *)route, (int)n_pairs, (int)p.n_ids, (int)p.ne11, (int)p.nb, actf, actd);
+    st = ctx->launch(fp4 ? "ghip_moe_act_fp8" : "ghip_moe_act_f16", dim3(fgrid), dim3(256), 0, s, (const uint8_t *)act,
+                     p.act_row_bytes, (const int32_t *)route, (int)n_pairs, (int)p.n_ids, (int)p.ne11, (int)p.nb,
+                     actf, actd);
     if (st != GHIP_STATUS_SUCCESS) return st;
     const bool repack = p.rows % 8 == 0;  // compute.rs:1965-1972 routes rows % 8 == 0 through the repack kernel
-    std::string name = std::string("ghip_moe_mxfp4_t") + (tp == 32 ? "32" : "64") + (repack ? "" : "_plain") + (sub ? "_sub" : "");
+    std::string name = fp4 ? std::string("ghip_moe_fp4") + (tp == 64 ? "_t64" : "") + (repack ? "" : "_plain") +
+                                 (sub ? "_sub" : "")
+                           : std::string("ghip_moe_mxfp4_t") + (tp == 32 ? "32" : "64") + (repack ? "" : "_plain") +
+                                 (sub ? "_sub" : "");
     const dim3 grid((unsigned)max_tiles, (unsigned)((p.rows + 127) / 128));
     return ctx->launch(name.c_str(), grid, dim3(256), 0, s, (const uint8_t *)as->data, (int64_t)as->nb[1],
                        (int64_t)as->nb[2], (const uint16_t *)actf, (const float *)actd, (int)p.ne11,

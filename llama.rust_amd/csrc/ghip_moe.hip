@@ -257,11 +257,8 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
     // returns dot * 2^k exactly and the fold is fma(dot * 2^k, d, acc), the
     // real value of the reference's fma(dot, 2^k * d, acc) (2^k * d exact).
     // Exact path: the integer dot and the reference's own fold.
-    auto do_block = [&](auto FAST, int b, const float *dsb, uint32_t e8, uint32_t q0, uint32_t q1,
-                        const v8h (&a)[NMT][2]) {
+    auto fold_block = [&](auto FAST, int b, const float *dsb, uint32_t e8, const v16f (&c)[NMT]) {
         constexpr bool fast = decltype(FAST)::value;
-        v16f c[NMT];
-        dots(fast ? 4u * (e8 - 128u) : 0u, q0, q1, a, c);
         const float sw = e8m0_half(e8);
 #pragma unroll
         for (int mt = 0; mt < NMT; mt++)
@@ -288,6 +285,13 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
                 }
             }
     };
+    auto do_block = [&](auto FAST, int b, const float *dsb, uint32_t e8, uint32_t q0, uint32_t q1,
+                        const v8h (&a)[NMT][2]) {
+        constexpr bool fast = decltype(FAST)::value;
+        v16f c[NMT];
+        dots(fast ? 4u * (e8 - 128u) : 0u, q0, q1, a, c);
+        fold_block(FAST, b, dsb, e8, c);
+    };
     // the 2^k fold holds for k = e - 128 in [-14, 12]
     auto in_range = [](uint32_t e8) { return e8 >= 114u && e8 <= 140u; };
 
@@ -311,19 +315,36 @@ __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, i
         if (g + 1 < nga) issue(g + 1, stage ^ 1, g + 1 < ngroups);
         if (g < ngroups) {
             const uint32_t *wl = w_lds[stage][rl];
-            // block kb of the window: e at byte 17kb, qs at 17kb+1; this lane
-            // half needs qs bytes 4h2.. (m = 0) and 8+4h2.. (m = 1)
-            auto e_of = [&](int kb) { return (wl[(17 * kb) >> 2] >> (8 * ((17 * kb) & 3))) & 0xffu; };
+            // the row's whole window (17-byte blocks from byte 0; 20 dwords)
+            uint32_t W[4 * MOE_WIN];
+#pragma unroll
+            for (int i = 0; i < MOE_WIN; i++) {
+                const uint4 t = reinterpret_cast<const uint4 *>(wl)[i];
+                W[4 * i] = t.x; W[4 * i + 1] = t.y; W[4 * i + 2] = t.z; W[4 * i + 3] = t.w;
+            }
+            // block kb: e at byte 17kb (byte kb of dword 4kb), qs at 17kb+1; this
+            // lane half needs qs bytes 4h2.. (m = 0) and 8+4h2.. (m = 1)
+            auto e_of = [&](int kb) { return (W[(17 * kb) >> 2] >> (8 * ((17 * kb) & 3))) & 0xffu; };
+            auto q_of = [&](int kb, int m) {
+                const int o = 17 * kb + 1 + 8 * m, d = o >> 2, sh = o & 3;
+                const uint32_t lo = h2 ? W[d + 1] : W[d], hi = h2 ? W[d + 2] : W[d + 1];
+                return __builtin_amdgcn_alignbyte(hi, lo, sh);
+            };
+            // software-pipelined: the dots of block kb are issued before the
+            // fold of block kb-1, whose MFMA results are ready by then
             auto window = [&](auto FAST) {
-#pragma unroll 2
+                constexpr bool fast = decltype(FAST)::value;
+                v16f c[2][NMT];
+#pragma unroll
                 for (int kb = 0; kb < MOE_GB; kb++) {
-                    const int o0 = 17 * kb + 1 + 4 * h2, o1 = o0 + 8;
-                    const uint32_t q0 = __builtin_amdgcn_alignbyte(wl[(o0 >> 2) + 1], wl[o0 >> 2], o0 & 3);
-                    const uint32_t q1 = __builtin_amdgcn_alignbyte(wl[(o1 >> 2) + 1], wl[o1 >> 2], o1 & 3);
                     v8h a[NMT][2];
                     a_of(stage, kb, a);
-                    do_block(FAST, MOE_GB * g + kb, ds_lds[stage][kb], e_of(kb), q0, q1, a);
+                    dots(fast ? 4u * (e_of(kb) - 128u) : 0u, q_of(kb, 0), q_of(kb, 1), a, c[kb & 1]);
+                    if (kb > 0)
+                        fold_block(FAST, MOE_GB * g + kb - 1, ds_lds[stage][kb - 1], e_of(kb - 1), c[(kb - 1) & 1]);
                 }
+                fold_block(FAST, MOE_GB * g + MOE_GB - 1, ds_lds[stage][MOE_GB - 1], e_of(MOE_GB - 1),
+                           c[(MOE_GB - 1) & 1]);
             };
             // one decision per window for the whole wavefront
             bool ok = !SUBSUMS;
@@ -369,6 +390,274 @@ MOE_KERNEL(ghip_moe_mxfp4_t32_plain, 1, false, false)
 MOE_KERNEL(ghip_moe_mxfp4_t64_plain, 2, false, false)
 MOE_KERNEL(ghip_moe_mxfp4_t32_sub, 1, true, true)
 MOE_KERNEL(ghip_moe_mxfp4_t32_plain_sub, 1, false, true)
+
+// ------------------------------------------------- scaled FP4 matrix cores
+// The same MUL_MAT_ID on v_mfma_scale_f32_32x32x64_f8f6f4: the MXFP4 nibbles
+// are the FP4 (E2M1) A operand as they lie in memory (E2M1 values are the
+// kvalues / 2), and the Q8_0 codes enter as two exact FP8 (E4M3) planes,
+// q = ql + 16 * qh with ql = q & 15 and qh = q >> 4, in the two K halves of
+// one instruction: A holds the block's 32 weights in both halves, B the ql
+// plane (scale 2^0) and the qh plane (scale 2^4), so one MFMA returns
+// sum kvalue * q * 2^(e - 128) = dot * e8m0_half(e) exactly per 32-block
+// (A's scale is the block's own E8M0 byte; every partial sum is an integer
+// times a power of two below 2^24 of it).  The fold is then the reference's
+// fma(dot, e8m0_half(e) * d, acc) with the exact product dot * 2^k
+// (fma(dot * 2^k, d, acc), the fast path of moe_mxfp4_impl) for k = e - 128
+// in [-14, 12]; other windows and the sub-sum kernels take A's scale 2^0
+// (dot / 2, exact) and the reference's own fold.
+//
+// K order inside a lane: FP4 nibble n of the 16 qs bytes is element n / 2
+// (n even) or 16 + n / 2 (n odd) of the block (low nibble of qs[j] is element
+// j, the high one element j + 16); the FP8 planes use the same order.
+
+// E4M3 bytes of 0..15
+DEV uint32_t e4m3_small(uint32_t v) {
+    constexpr uint64_t lo = 0x4E4C4A4844403800ull, hi = 0x5756555453525150ull;
+    return (uint32_t)(((v < 8 ? lo : hi) >> (8 * (v & 7))) & 0xff);
+}
+
+// Q8_0 rows -> the two FP8 planes in MFMA K order, per (routed slot, block):
+// four 16-byte pieces (plane h, piece j) = 2h + j, piece j holding K positions
+// 16j..16j+15 (elements 8j..8j+7 interleaved with 16+8j..16+8j+7), stored
+// actq [block][piece][slot]; actd [block][slot] = d.
+extern "C" __global__ void __launch_bounds__(256)
+ghip_moe_act_fp8(const uint8_t *__restrict__ q8, int64_t q8_row_bytes, const int32_t *__restrict__ route,
+                 int n_pairs, int n_ids, int ne11, int nb, uint8_t *__restrict__ actq, float *__restrict__ actd) {
+    const int64_t task = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (slot, block, piece)
+    const int n_valid = n_pairs - route[1];
+    if (task >= (int64_t)n_valid * nb * 4) return;
+    const int piece = (int)(task & 3), hplane = piece >> 1, j = piece & 1;
+    const int64_t rb = task >> 2;
+    const int64_t slot = rb / nb;
+    const int b = (int)(rb - slot * nb);
+    const int p = route[2 + slot], t = p / n_ids, sl = p - t * n_ids;
+    const int64_t row = (int64_t)t * ne11 + sl % ne11;
+    const uint8_t *blk = q8 + row * q8_row_bytes + (int64_t)b * Q8_0_BYTES;
+    const uint2 lo = ld8(blk + 2 + 8 * j), hi = ld8(blk + 2 + 16 + 8 * j);
+    const uint32_t lw[2] = {lo.x, lo.y}, hw[2] = {hi.x, hi.y};
+    uint32_t out[4];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int qa = (int)(int8_t)(lw[i >> 2] >> (8 * (i & 3)));
+        const int qb = (int)(int8_t)(hw[i >> 2] >> (8 * (i & 3)));
+        uint32_t ba, bb;
+        if (hplane == 0) {
+            ba = e4m3_small((uint32_t)(qa & 15));
+            bb = e4m3_small((uint32_t)(qb & 15));
+        } else {
+            const int ha = qa >> 4, hb = qb >> 4;  // -8 .. 7
+            ba = e4m3_small((uint32_t)(ha < 0 ? -ha : ha)) | (ha < 0 ? 0x80u : 0u);
+            bb = e4m3_small((uint32_t)(hb < 0 ? -hb : hb)) | (hb < 0 ? 0x80u : 0u);
+        }
+        const uint32_t pair = ba | (bb << 8);  // K positions 2i, 2i+1
+        if ((i & 1) == 0) out[i >> 1] = pair;
+        else out[i >> 1] |= pair << 16;
+    }
+    // [block][piece][slot]: a tile's consecutive slots are consecutive 16-byte chunks
+    *reinterpret_cast<uint4 *>(actq + (((int64_t)b * 4 + piece) * n_pairs + slot) * 16) =
+        make_uint4(out[0], out[1], out[2], out[3]);
+    if (piece == 0) actd[(int64_t)b * n_pairs + slot] = h2f(ld2(blk));
+}
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+
+// grid (tile, row block of 128); 4 wavefronts x 32 expert rows; a tile is 32
+// pairs of one expert.  C[row][pair]: lane l holds pair l % 32 and the rows
+// crowm(v, l) of its wavefront's 32.  Staging as moe_mxfp4_impl (weight
+// windows of 4 blocks, the tile's planes and scales, one group ahead).
+template <int NMT, bool REPACK, bool SUBSUMS>
+__device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int64_t as_nb1, int64_t as_nb2,
+                                             const uint8_t *__restrict__ actq, const float *__restrict__ actd,
+                                             int ne11, const int32_t *__restrict__ route, int n_pairs, int n_ids,
+                                             float *__restrict__ dst, int64_t dst_nb1, int64_t dst_nb2, int rows,
+                                             int nb, int32_t *__restrict__ sub) {
+    constexpr int TP = 32 * NMT;
+    static_assert(256 % TP == 0, "one pair per thread");
+    __shared__ __attribute__((aligned(16))) float ds_lds[2][MOE_GB][TP];
+    __shared__ __attribute__((aligned(16))) uint4 a_lds[2][MOE_GB][4][TP];  // [stage][block][piece][pair]
+    __shared__ __attribute__((aligned(16))) uint32_t w_lds[2][MOE_TR][MOE_WIN * 4];
+    __shared__ int pairs[TP];
+    const int tile = blockIdx.x;
+    if (tile >= route[0]) return;
+    const int32_t *tinfo = route + 2 + n_pairs + 3 * tile;
+    const int e = tinfo[0], first = tinfo[1], np = tinfo[2];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int li = lane & 31, h2 = lane >> 5;
+    const int row0 = blockIdx.y * MOE_TR + w * 32;  // this wavefront's first row
+    if (threadIdx.x < TP) pairs[threadIdx.x] = threadIdx.x < np ? route[2 + first + threadIdx.x] : -1;
+    const int row_bytes = nb * MXFP4_BYTES;
+
+    constexpr int ACHUNK = MOE_GB * 4 * TP / 256;
+    constexpr int DCH = (MOE_GB * TP + 255) / 256;
+    const int my_pi = threadIdx.x % TP;
+    const int my_slot = first + (my_pi < np ? my_pi : 0);
+    const uint8_t *my_arow = actq + (int64_t)my_slot * 16;  // + (block * 4 + piece) * n_pairs * 16
+    const float *my_drow = actd + my_slot;                   // + block * n_pairs
+    constexpr int WCHUNK = (MOE_TR * MOE_WIN + 255) / 256;
+    const uint8_t *wexp = as + (int64_t)e * as_nb2;
+    const uint8_t *wbase[WCHUNK];
+    int wl16[WCHUNK];
+#pragma unroll
+    for (int c = 0; c < WCHUNK; c++) {
+        const int idx = c * 256 + threadIdx.x;
+        const int r = idx / MOE_WIN, l = idx - r * MOE_WIN;
+        wbase[c] = wexp + (int64_t)min((int)blockIdx.y * MOE_TR + r, rows - 1) * as_nb1;
+        wl16[c] = 16 * l;
+    }
+    const int wv = threadIdx.x >> 6;
+    auto issue = [&](int g, int stage, bool with_w) {
+#pragma unroll
+        for (int c = 0; c < ACHUNK; c++) {
+            const int rest = (c * 256 + (int)threadIdx.x) / TP;
+            const int piece = rest & 3, b = min(MOE_GB * g + (rest >> 2), nb - 1);
+            g2lds(my_arow + ((int64_t)b * 4 + piece) * n_pairs * 16,
+                  reinterpret_cast<uint8_t *>(&a_lds[stage][0][0][0]) + (c * 256 + 64 * wv) * 16);
+        }
+#pragma unroll
+        for (int c = 0; c < DCH; c++) {
+            if (c * 256 + 64 * wv >= MOE_GB * TP) continue;
+            const int b = min(MOE_GB * g + (c * 256 + (int)threadIdx.x) / TP, nb - 1);
+            __builtin_amdgcn_global_load_lds(my_drow + (int64_t)b * n_pairs,
+                                             (lds_void *)(reinterpret_cast<uint8_t *>(&ds_lds[stage][0][0]) +
+                                                          (c * 256 + 64 * wv) * 4),
+                                             4, 0, 0);
+        }
+        if (with_w) {
+#pragma unroll
+            for (int c = 0; c < WCHUNK; c++)
+                if (c * 256 + 64 * wv < MOE_TR * MOE_WIN)
+                    g2lds(wbase[c] + min(MOE_WB * g + wl16[c], row_bytes - 16),
+                          reinterpret_cast<uint8_t *>(&w_lds[stage][0][0]) + (c * 256 + 64 * wv) * 16);
+        }
+    };
+    float acc[NMT][16];
+#pragma unroll
+    for (int mt = 0; mt < NMT; mt++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[mt][v] = 0.0f;
+    const v16f zero = {};
+    const int scale_b = h2 ? 127 + 4 : 127;  // ql plane x 1, qh plane x 16
+    // E8M0 127 (2^0) held in a VGPR: a constant scale operand would be encoded
+    // as an f32 inline constant
+    int s127;
+    asm volatile("v_mov_b32 %0, 127" : "=v"(s127));
+
+    // dots of one block: A = the 16 qs bytes of row li, B = this lane's plane
+    auto mfma = [&](const uint32_t (&q)[4], int scale_a, int stage, int kb, int mt) {
+        // B lane half h2: bytes 0..15 = K 16h2.. (ql piece h2), bytes 16..31 =
+        // K 32+16h2.. (qh piece h2); A lane half h holds K 32h..32h+31
+        const uint4 b0 = a_lds[stage][kb][h2][mt * 32 + li], b1 = a_lds[stage][kb][2 + h2][mt * 32 + li];
+        const v8i A = {(int)q[0], (int)q[1], (int)q[2], (int)q[3], 0, 0, 0, 0};
+        const v8i B = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+        return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, B, zero, 4, 0, 0, scale_a, 0, scale_b);
+    };
+    // fast fold: c = dot * 2^k, acc = fma(c, d, acc) (REPACK) or acc + d * c
+    auto fold_fast = [&](const v16f &c, float d, int mt) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            if (REPACK) acc[mt][v] = fmaf(c[v], d, acc[mt][v]);
+            else acc[mt][v] = acc[mt][v] + d * c[v];
+        }
+    };
+    // exact fold: c = dot / 2; the row scales come from the lanes holding the rows
+    auto fold_exact = [&](const v16f &c, float d, uint32_t e8, int b, int mt) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int r = crowm(v, lane);
+            const float sw = e8m0_half((uint32_t)__shfl((int)e8, r, 64));
+            const float dot = 2.0f * c[v];
+            if (REPACK) acc[mt][v] = fmaf(dot, sw * d, acc[mt][v]);
+            else acc[mt][v] = acc[mt][v] + (d * sw) * dot;
+            if (SUBSUMS && mt * 32 + li < np && row0 + r < rows)
+                sub[((int64_t)pairs[mt * 32 + li] * rows + row0 + r) * nb + b] = (int)dot;
+        }
+    };
+    auto in_range = [](uint32_t e8) { return e8 >= 114u && e8 <= 140u; };
+
+    int ngroups = nb / MOE_GB;
+    while (ngroups > 0 && MOE_WB * (ngroups - 1) + 16 * MOE_WIN > row_bytes) ngroups--;
+    const int nga = (nb + MOE_GB - 1) / MOE_GB;
+    const int rl = w * 32 + li;
+    issue(0, 0, ngroups > 0);
+    for (int g = 0; g < nga; g++) {
+        const int stage = g & 1;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (g + 1 < nga) issue(g + 1, stage ^ 1, g + 1 < ngroups);
+        if (g < ngroups) {
+            const uint32_t *wl = w_lds[stage][rl];
+            uint32_t W[4 * MOE_WIN];
+#pragma unroll
+            for (int i = 0; i < MOE_WIN; i++) {
+                const uint4 t = reinterpret_cast<const uint4 *>(wl)[i];
+                W[4 * i] = t.x; W[4 * i + 1] = t.y; W[4 * i + 2] = t.z; W[4 * i + 3] = t.w;
+            }
+            auto e_of = [&](int kb) { return (W[(17 * kb) >> 2] >> (8 * ((17 * kb) & 3))) & 0xffu; };
+            auto q_of = [&](int kb, uint32_t (&q)[4]) {
+                const int o = 17 * kb + 1, d = o >> 2, sh = o & 3;
+#pragma unroll
+                for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbyte(W[d + i + 1], W[d + i], sh);
+            };
+            bool ok = !SUBSUMS;
+#pragma unroll
+            for (int kb = 0; kb < MOE_GB; kb++) ok = ok && in_range(e_of(kb));
+            if (__ballot(!ok) == 0) {
+#pragma unroll
+                for (int kb = 0; kb < MOE_GB; kb++) {
+                    uint32_t q[4];
+                    q_of(kb, q);
+#pragma unroll
+                    for (int mt = 0; mt < NMT; mt++)
+                        if (mt == 0 || np > 32 * mt)
+                            fold_fast(mfma(q, (int)e_of(kb), stage, kb, mt), ds_lds[stage][kb][mt * 32 + li], mt);
+                }
+            } else {
+                for (int kb = 0; kb < MOE_GB; kb++) {
+                    uint32_t q[4];
+                    q_of(kb, q);
+#pragma unroll
+                    for (int mt = 0; mt < NMT; mt++)
+                        if (mt == 0 || np > 32 * mt)
+                            fold_exact(mfma(q, s127, stage, kb, mt), ds_lds[stage][kb][mt * 32 + li], e_of(kb),
+                                       MOE_GB * g + kb, mt);
+                }
+            }
+        } else {
+            for (int kb = 0; kb < MOE_GB && MOE_GB * g + kb < nb; kb++) {  // tail blocks: global loads, exact fold
+                const int b = MOE_GB * g + kb;
+                const uint8_t *wb = as + (int64_t)e * as_nb2 + (int64_t)min(row0 + li, rows - 1) * as_nb1 +
+                                    (int64_t)b * MXFP4_BYTES;
+                const uint32_t q[4] = {ld4(wb + 1), ld4(wb + 5), ld4(wb + 9), ld4(wb + 13)};
+#pragma unroll
+                for (int mt = 0; mt < NMT; mt++)
+                    if (mt == 0 || np > 32 * mt)
+                        fold_exact(mfma(q, s127, stage, kb, mt), ds_lds[stage][kb][mt * 32 + li], wb[0], b, mt);
+            }
+        }
+    }
+#pragma unroll
+    for (int mt = 0; mt < NMT; mt++) {
+        if (mt * 32 + li >= np) continue;
+        const int p = pairs[mt * 32 + li];
+        const int t = p / n_ids, s = p - t * n_ids;
+        float *o = dst + (int64_t)t * dst_nb2 + (int64_t)s * dst_nb1;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int r = row0 + crowm(v, lane);
+            if (r < rows) o[r] = acc[mt][v];
+        }
+    }
+}
+#define MOE_FP4_KERNEL(name, NMT, REPACK, SUB)                                                                 \
+    extern "C" __global__ void __launch_bounds__(256) name(MOE_ARGS) { moe_fp4_impl<NMT, REPACK, SUB>(MOE_PASS_FP4); }
+#define MOE_PASS_FP4 \
+    as, as_nb1, as_nb2, (const uint8_t *)actf, actd, ne11, route, n_pairs, n_ids, dst, dst_nb1, dst_nb2, rows, nb, sub
+MOE_FP4_KERNEL(ghip_moe_fp4, 1, true, false)
+MOE_FP4_KERNEL(ghip_moe_fp4_plain, 1, false, false)
+MOE_FP4_KERNEL(ghip_moe_fp4_sub, 1, true, true)
+MOE_FP4_KERNEL(ghip_moe_fp4_plain_sub, 1, false, true)
+MOE_FP4_KERNEL(ghip_moe_fp4_t64, 2, true, false)
+MOE_FP4_KERNEL(ghip_moe_fp4_t64_plain, 2, false, false)
 
 
 // ---------------------------------------------------------- K-quant experts

@@ -89,11 +89,19 @@ struct ghip_context {
     struct WeightKey {
         const void *data;
         int type;
-        int64_t ne0, ne1;
-        uint64_t nb1;
+        int64_t ne0, ne1, ne2;
+        uint64_t nb1, nb2;
         bool operator==(const WeightKey &o) const {
-            return data == o.data && type == o.type && ne0 == o.ne0 && ne1 == o.ne1 && nb1 == o.nb1;
+            return data == o.data && type == o.type && ne0 == o.ne0 && ne1 == o.ne1 && ne2 == o.ne2 &&
+                   nb1 == o.nb1 && nb2 == o.nb2;
         }
+    };
+    static WeightKey key_of(const ghip_tensor *w) {
+        return {w->data, w->type, w->ne[0], w->ne[1], w->ne[2], w->nb[1], w->ne[2] > 1 ? w->nb[2] : 0};
+    }
+    struct WeightCopy {
+        void *p;
+        size_t bytes;
     };
     struct WeightKeyHash {
         size_t operator()(const WeightKey &k) const {
@@ -101,10 +109,11 @@ struct ghip_context {
             h = h * 31 + (size_t)k.type;
             h = h * 31 + (size_t)k.ne0;
             h = h * 31 + (size_t)k.ne1;
+            h = h * 31 + (size_t)k.ne2;
             return h * 31 + (size_t)k.nb1;
         }
     };
-    std::unordered_map<WeightKey, void *, WeightKeyHash> wcache;
+    std::unordered_map<WeightKey, WeightCopy, WeightKeyHash> wcache;
     size_t wcache_bytes = 0;   // bytes held by wcache
     size_t wcache_built = 0;   // copies materialized so far (hits do not count)
 
@@ -473,6 +482,10 @@ int gemm_nsplit(const MulMatPlan &p) {
 }
 // Q6_K prefill workspace: f16 codes [Mpad][K] | dT [nb][Mpad] | repacked weights [N][nb][336]
 constexpr size_t kQ6R = 336;
+// registered MXFP4 experts (ghip_mxfp4_repack): 128-row blocks, groups of 4
+// 17-byte blocks, 80-byte windows -> one 10240-byte run per (expert, row block, group)
+constexpr int64_t kMoeRows = 128, kMoeGroup = 4;
+constexpr size_t kMoeWindowRun = 128 * 80;
 size_t gemm_q6k_bytes(const MulMatPlan &p, size_t *codes_b, size_t *dt_b) {
     const size_t Mpad = (size_t)(p.M + 127) / 128 * 128, nbk = (size_t)p.K / 256;
     *codes_b = (Mpad * (size_t)p.K * 2 + 255) & ~(size_t)255;
@@ -500,8 +513,8 @@ ghip_status q6k_repack(ghip_context *ctx, const void *w, int64_t row_bytes, int6
                        row_bytes, (int)N, (int)nbk, rep);
 }
 const uint8_t *registered_q6k(ghip_context *ctx, const MulMatPlan &p, const void *w) {
-    auto it = ctx->wcache.find({w, GHIP_TYPE_Q6_K, p.K, p.N, (uint64_t)p.w_row_bytes});
-    return it == ctx->wcache.end() ? nullptr : (const uint8_t *)it->second;
+    auto it = ctx->wcache.find({w, GHIP_TYPE_Q6_K, p.K, p.N, 1, (uint64_t)p.w_row_bytes, 0});
+    return it == ctx->wcache.end() ? nullptr : (const uint8_t *)it->second.p;
 }
 ghip_status run_gemm_q6k(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act,
                          const ghip_tensor *bf, float *dst, int64_t ldd, int32_t *sub, void *layout_ws, hipStream_t s) {
@@ -885,6 +898,16 @@ ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip
                            : std::string("ghip_moe_mxfp4_t") + (tp == 32 ? "32" : "64") + (repack ? "" : "_plain") +
                                  (sub ? "_sub" : "");
     const dim3 grid((unsigned)max_tiles, (unsigned)((p.rows + 127) / 128));
+    if (fp4) {
+        // the registered copy of the experts, if any (ghip_weight_register)
+        auto it = ctx->wcache.find(ghip_context::key_of(as));
+        const uint8_t *wrep = it == ctx->wcache.end() ? nullptr : (const uint8_t *)it->second.p;
+        const int ngp = (int)((p.nb + kMoeGroup - 1) / kMoeGroup);
+        return ctx->launch(name.c_str(), grid, dim3(256), 0, s, (const uint8_t *)as->data, (int64_t)as->nb[1],
+                           (int64_t)as->nb[2], (const uint16_t *)actf, (const float *)actd, (int)p.ne11,
+                           (const int32_t *)route, (int)n_pairs, (int)p.n_ids, dst, dst_nb1, dst_nb2, (int)p.rows,
+                           (int)p.nb, sub, wrep, ngp);
+    }
     return ctx->launch(name.c_str(), grid, dim3(256), 0, s, (const uint8_t *)as->data, (int64_t)as->nb[1],
                        (int64_t)as->nb[2], (const uint16_t *)actf, (const float *)actd, (int)p.ne11,
                        (const int32_t *)route, (int)n_pairs, (int)p.n_ids, dst, dst_nb1, dst_nb2, (int)p.rows,
@@ -1291,7 +1314,7 @@ void ghip_free(ghip_context *ctx) {
     hipDeviceSynchronize();
     if (ctx->ws) hipFree(ctx->ws);
     for (void *p : ctx->retired) hipFree(p);
-    for (auto &kv : ctx->wcache) hipFree(kv.second);
+    for (auto &kv : ctx->wcache) hipFree(kv.second.p);
     if (ctx->order_ev) hipEventDestroy(ctx->order_ev);
     for (hipModule_t m : ctx->modules) hipModuleUnload(m);
     delete ctx;
@@ -1312,18 +1335,33 @@ ghip_status ghip_weight_register(ghip_context *ctx, const ghip_tensor *w, void *
     if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
     std::lock_guard<std::mutex> lock(ctx->mu);
     if (!w || !w->data) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: null weight");
-    if (w->ne[2] != 1 || w->ne[3] != 1) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: 2-D weights only");
-    if (w->ne[0] <= 0 || w->ne[1] <= 0) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: empty weight");
+    if (w->ne[0] <= 0 || w->ne[1] <= 0 || w->ne[2] <= 0 || w->ne[3] != 1)
+        return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: empty or 4-D weight");
+    const bool q6k = w->type == GHIP_TYPE_Q6_K, mx = w->type == GHIP_TYPE_MXFP4;
+    if (q6k && w->ne[2] != 1) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: Q6_K weights are 2-D");
     // every other type is read in its GGUF layout: nothing to build
-    if (w->type != GHIP_TYPE_Q6_K || !repack_enabled()) return GHIP_STATUS_SUCCESS;
-    if (w->ne[0] % 256 || w->nb[0] != 210 || w->nb[1] < (uint64_t)(w->ne[0] / 256 * 210))
-        return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: bad Q6_K geometry");
-    if (w->ne[1] > INT32_MAX || w->ne[0] / 256 > INT32_MAX)
-        return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: dimension too large");
-    const ghip_context::WeightKey key{w->data, w->type, w->ne[0], w->ne[1], w->nb[1]};
+    if (!(q6k || mx) || !repack_enabled()) return GHIP_STATUS_SUCCESS;
+    size_t bytes;
+    int64_t nbk = 0, nrb = 0, ngp = 0;
+    if (q6k) {
+        if (w->ne[0] % 256 || w->nb[0] != 210 || w->nb[1] < (uint64_t)(w->ne[0] / 256 * 210))
+            return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: bad Q6_K geometry");
+        if (w->ne[1] > INT32_MAX || w->ne[0] / 256 > INT32_MAX)
+            return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: dimension too large");
+        nbk = w->ne[0] / 256;
+        bytes = (size_t)w->ne[1] * (size_t)nbk * kQ6R;
+    } else {
+        if (w->ne[0] % 32 || w->nb[0] != 17 || w->nb[1] < (uint64_t)(w->ne[0] / 32 * 17) ||
+            (w->ne[2] > 1 && w->nb[2] < w->nb[1] * (uint64_t)w->ne[1]))
+            return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: bad MXFP4 geometry");
+        if (w->ne[1] > INT32_MAX || w->ne[2] > INT32_MAX)
+            return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: dimension too large");
+        nrb = (w->ne[1] + kMoeRows - 1) / kMoeRows;
+        ngp = (w->ne[0] / 32 + kMoeGroup - 1) / kMoeGroup;
+        bytes = (size_t)w->ne[2] * (size_t)nrb * (size_t)ngp * kMoeWindowRun;
+    }
+    const ghip_context::WeightKey key = ghip_context::key_of(w);
     if (ctx->wcache.count(key)) return GHIP_STATUS_SUCCESS;
-    const int64_t N = w->ne[1], nbk = w->ne[0] / 256;
-    const size_t bytes = (size_t)N * (size_t)nbk * kQ6R;
     if (ctx->wcache_bytes + bytes > repack_budget()) return GHIP_STATUS_SUCCESS;  // not kept: calls repack per call
     hipStream_t s = (hipStream_t)stream;
     if (ghip_context::capturing(s))
@@ -1336,12 +1374,19 @@ ghip_status ghip_weight_register(ghip_context *ctx, const ghip_tensor *w, void *
         (void)hipGetLastError();
         return ctx->fail(GHIP_STATUS_OUT_OF_MEMORY, "weight_register: hipMalloc(%zu) failed", bytes);
     }
-    st = q6k_repack(ctx, w->data, (int64_t)w->nb[1], N, nbk, (uint8_t *)rep, s);
+    if (q6k) {
+        st = q6k_repack(ctx, w->data, (int64_t)w->nb[1], w->ne[1], nbk, (uint8_t *)rep, s);
+    } else {
+        const int64_t chunks = (int64_t)(bytes / 16);
+        st = ctx->launch("ghip_mxfp4_repack", dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, s,
+                         (const uint8_t *)w->data, (int64_t)w->nb[1], (int64_t)(w->ne[2] > 1 ? w->nb[2] : 0),
+                         (int)w->ne[1], (int)(w->ne[0] / 32), (int)w->ne[2], (int)nrb, (int)ngp, (uint8_t *)rep);
+    }
     if (st != GHIP_STATUS_SUCCESS) {
         hipFree(rep);
         return st;
     }
-    ctx->wcache.emplace(key, rep);
+    ctx->wcache.emplace(key, ghip_context::WeightCopy{rep, bytes});
     ctx->wcache_bytes += bytes;
     ctx->wcache_built++;
     return GHIP_STATUS_SUCCESS;
@@ -1351,14 +1396,14 @@ ghip_status ghip_weight_unregister(ghip_context *ctx, const ghip_tensor *w) {
     if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
     std::lock_guard<std::mutex> lock(ctx->mu);
     if (!w) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_unregister: null weight");
-    auto it = ctx->wcache.find({w->data, w->type, w->ne[0], w->ne[1], w->nb[1]});
+    auto it = ctx->wcache.find(ghip_context::key_of(w));
     if (it == ctx->wcache.end()) return GHIP_STATUS_SUCCESS;
     if (hipSetDevice(ctx->device) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         (void)hipGetLastError();
         return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_unregister: device synchronize failed");
     }
-    hipFree(it->second);
-    ctx->wcache_bytes -= (size_t)w->ne[1] * (size_t)(w->ne[0] / 256) * kQ6R;
+    hipFree(it->second.p);
+    ctx->wcache_bytes -= it->second.bytes;
     ctx->wcache.erase(it);
     return GHIP_STATUS_SUCCESS;
 }

@@ -470,7 +470,8 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
                                              const uint8_t *__restrict__ actq, const float *__restrict__ actd,
                                              int ne11, const int32_t *__restrict__ route, int n_pairs, int n_ids,
                                              float *__restrict__ dst, int64_t dst_nb1, int64_t dst_nb2, int rows,
-                                             int nb, int32_t *__restrict__ sub) {
+                                             int nb, int32_t *__restrict__ sub, const uint8_t *__restrict__ wrep,
+                                             int ngp) {
     constexpr int TP = 32 * NMT;
     static_assert(256 % TP == 0, "one pair per thread");
     __shared__ __attribute__((aligned(16))) float ds_lds[2][MOE_GB][TP];
@@ -522,7 +523,14 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
                                                           (c * 256 + 64 * wv) * 4),
                                              4, 0, 0);
         }
-        if (with_w) {
+        if (wrep) {  // registered copy: the group's windows are one contiguous run in LDS order
+            const uint8_t *src = wrep + (((int64_t)e * gridDim.y + blockIdx.y) * ngp + g) * (MOE_TR * MOE_WIN * 16);
+#pragma unroll
+            for (int c = 0; c < WCHUNK; c++)
+                if (c * 256 + 64 * wv < MOE_TR * MOE_WIN)
+                    g2lds(src + (c * 256 + (int)threadIdx.x) * 16,
+                          reinterpret_cast<uint8_t *>(&w_lds[stage][0][0]) + (c * 256 + 64 * wv) * 16);
+        } else if (with_w) {
 #pragma unroll
             for (int c = 0; c < WCHUNK; c++)
                 if (c * 256 + 64 * wv < MOE_TR * MOE_WIN)
@@ -577,6 +585,7 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
     int ngroups = nb / MOE_GB;
     while (ngroups > 0 && MOE_WB * (ngroups - 1) + 16 * MOE_WIN > row_bytes) ngroups--;
     const int nga = (nb + MOE_GB - 1) / MOE_GB;
+    if (wrep) ngroups = nga;  // every window of the registered copy is whole (zero past the row)
     const int rl = w * 32 + li;
     issue(0, 0, ngroups > 0);
     for (int g = 0; g < nga; g++) {
@@ -598,12 +607,14 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
 #pragma unroll
                 for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbyte(W[d + i + 1], W[d + i], sh);
             };
+            const int nbl = nb - MOE_GB * g;  // blocks of this group inside the row
             bool ok = !SUBSUMS;
 #pragma unroll
-            for (int kb = 0; kb < MOE_GB; kb++) ok = ok && in_range(e_of(kb));
+            for (int kb = 0; kb < MOE_GB; kb++) ok = ok && (kb >= nbl || in_range(e_of(kb)));
             if (__ballot(!ok) == 0) {
 #pragma unroll
                 for (int kb = 0; kb < MOE_GB; kb++) {
+                    if (kb >= nbl) break;
                     uint32_t q[4];
                     q_of(kb, q);
 #pragma unroll
@@ -612,7 +623,7 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
                             fold_fast(mfma(q, (int)e_of(kb), stage, kb, mt), ds_lds[stage][kb][mt * 32 + li], mt);
                 }
             } else {
-                for (int kb = 0; kb < MOE_GB; kb++) {
+                for (int kb = 0; kb < MOE_GB && kb < nbl; kb++) {
                     uint32_t q[4];
                     q_of(kb, q);
 #pragma unroll
@@ -648,10 +659,15 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
         }
     }
 }
-#define MOE_FP4_KERNEL(name, NMT, REPACK, SUB)                                                                 \
-    extern "C" __global__ void __launch_bounds__(256) name(MOE_ARGS) { moe_fp4_impl<NMT, REPACK, SUB>(MOE_PASS_FP4); }
-#define MOE_PASS_FP4 \
-    as, as_nb1, as_nb2, (const uint8_t *)actf, actd, ne11, route, n_pairs, n_ids, dst, dst_nb1, dst_nb2, rows, nb, sub
+// wrep: the registered copy of the experts (ghip_mxfp4_repack) or null; ngp its groups per row
+#define MOE_FP4_KERNEL(name, NMT, REPACK, SUB)                                                                \
+    extern "C" __global__ void __launch_bounds__(256)                                                         \
+        name(MOE_ARGS, const uint8_t *__restrict__ wrep, int ngp) {                                           \
+        moe_fp4_impl<NMT, REPACK, SUB>(MOE_PASS_FP4);                                                         \
+    }
+#define MOE_PASS_FP4                                                                                          \
+    as, as_nb1, as_nb2, (const uint8_t *)actf, actd, ne11, route, n_pairs, n_ids, dst, dst_nb1, dst_nb2, rows, nb, \
+        sub, wrep, ngp
 MOE_FP4_KERNEL(ghip_moe_fp4, 1, true, false)
 MOE_FP4_KERNEL(ghip_moe_fp4_plain, 1, false, false)
 MOE_FP4_KERNEL(ghip_moe_fp4_sub, 1, true, true)
@@ -659,6 +675,38 @@ MOE_FP4_KERNEL(ghip_moe_fp4_plain_sub, 1, false, true)
 MOE_FP4_KERNEL(ghip_moe_fp4_t64, 2, true, false)
 MOE_FP4_KERNEL(ghip_moe_fp4_t64_plain, 2, false, false)
 
+
+
+// The registered layout of MXFP4 experts for moe_fp4_impl: per (expert, block
+// of 128 rows, group of MOE_GB 17-byte blocks) the 128 rows' windows, 80 bytes
+// each (68 of data, zero past the row and in the padding), one contiguous run
+// in the order the kernel stages them in LDS.  One thread per 16-byte chunk.
+extern "C" __global__ void __launch_bounds__(256)
+ghip_mxfp4_repack(const uint8_t *__restrict__ W, int64_t nb1, int64_t nb2, int rows, int nb, int n_as, int nrb,
+                  int ngp, uint8_t *__restrict__ out) {
+    constexpr int CH = MOE_TR * MOE_WIN;  // chunks per (expert, row block, group)
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)n_as * nrb * ngp * CH) return;
+    const int c = (int)(i % CH);
+    const int64_t rest = i / CH;
+    const int g = (int)(rest % ngp);
+    const int64_t erb = rest / ngp;
+    const int rb = (int)(erb % nrb), e = (int)(erb / nrb);
+    const int r = c / MOE_WIN, c16 = c - r * MOE_WIN;
+    const int row = rb * MOE_TR + r;
+    const int row_bytes = nb * MXFP4_BYTES;
+    uint32_t v[4] = {0u, 0u, 0u, 0u};
+    if (row < rows) {
+        const uint8_t *src = W + (int64_t)e * nb2 + (int64_t)row * nb1;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int o = 16 * c16 + k;  // byte of the window
+            const int pos = MOE_WB * g + o;
+            if (o < MOE_WB && pos < row_bytes) v[k >> 2] |= (uint32_t)src[pos] << (8 * (k & 3));
+        }
+    }
+    *reinterpret_cast<uint4 *>(out + i * 16) = make_uint4(v[0], v[1], v[2], v[3]);
+}
 
 // ---------------------------------------------------------- K-quant experts
 // MUL_MAT_ID with Q4_K, Q5_K or Q6_K experts (forward_mul_mat_id,

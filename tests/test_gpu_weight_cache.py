@@ -143,3 +143,32 @@ def test_q6K_gemm_extreme_blocks_exact(be):
     assert rel_err(got, want) <= 1e-5, rel_err(got, want)
     sub = be.mul_mat_subsums(wd, O.Q6_K, n, xd).cpu().numpy()
     assert np.array_equal(sub, want_sub)
+
+
+@pytest.mark.parametrize("n,rows,n_as,n_tok,n_ids", [
+    (2880, 264, 8, 40, 4),   # 90 blocks: 22 whole groups + a 2-block group; rows past 128 (and % 8 == 0)
+    (256, 100, 4, 24, 2),    # 8 blocks; rows % 8 != 0: the plain fold; one partial row block
+])
+def test_register_mxfp4_experts_bit_identical(be, n, rows, n_as, n_tok, n_ids):
+    """Registered MXFP4 experts (the windows laid out in the kernel's staging
+    order) give the same bits as the GGUF layout, and the sub-sums agree."""
+    import ghip
+    rng = np.random.default_rng(rows)
+    wf = torch.from_numpy((rng.standard_normal((n_as * rows, n)) * 0.02).astype(np.float32)).cuda()
+    w = be.quantize(wf, ghip.MXFP4).view(n_as, rows, -1)
+    b = torch.from_numpy(rng.standard_normal((n_tok, 1, n)).astype(np.float32)).cuda()
+    ids = torch.from_numpy(np.stack([rng.permutation(n_as)[:n_ids] for _ in range(n_tok)]).astype(np.int32)).cuda()
+    print(f"mxfp4 registered n={n} rows={rows} n_as={n_as} tokens={n_tok}", flush=True)
+    before = be.mul_mat_id(w, n, b, ids).clone()
+    sub0 = be.mul_mat_id_subsums(w, n, b, ids).clone()
+    n0, b0, built0 = be.weight_cache_stats()
+    be.register_weight(w, ghip.MXFP4, n)
+    n1, b1, built1 = be.weight_cache_stats()
+    assert (n1, built1) == (n0 + 1, built0 + 1)
+    assert b1 - b0 == n_as * ((rows + 127) // 128) * ((n // 32 + 3) // 4) * 128 * 80
+    after = be.mul_mat_id(w, n, b, ids)
+    assert torch.equal(after.view(torch.int32), before.view(torch.int32))
+    sub1 = be.mul_mat_id_subsums(w, n, b, ids)
+    assert torch.equal(sub1, sub0)
+    be.unregister_weight(w, ghip.MXFP4, n)
+    assert be.weight_cache_stats()[:2] == (n0, b0)

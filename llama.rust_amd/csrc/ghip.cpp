@@ -903,6 +903,7 @@ ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip
         auto it = ctx->wcache.find(ghip_context::key_of(as));
         const uint8_t *wrep = it == ctx->wcache.end() ? nullptr : (const uint8_t *)it->second.p;
         const int ngp = (int)((p.nb + kMoeGroup - 1) / kMoeGroup);
+        if (wrep) name += "_reg";
         return ctx->launch(name.c_str(), grid, dim3(256), 0, s, (const uint8_t *)as->data, (int64_t)as->nb[1],
                            (int64_t)as->nb[2], (const uint16_t *)actf, (const float *)actd, (int)p.ne11,
                            (const int32_t *)route, (int)n_pairs, (int)p.n_ids, dst, dst_nb1, dst_nb2, (int)p.rows,

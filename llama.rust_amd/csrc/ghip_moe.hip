@@ -145,6 +145,7 @@ ghip_moe_act_f16(const uint8_t *__restrict__ q8, int64_t q8_row_bytes, const int
 constexpr int MOE_GB = 4;                               // 32-blocks per staging group
 constexpr int MOE_WB = 17 * MOE_GB;                     // weight window bytes per row and group
 constexpr int MOE_WIN = (MOE_WB + 4 + 15) / 16;         // 16-byte loads per window (+ the dword the last reads touch)
+static_assert(MOE_WIN * 16 >= 17 * MOE_GB, "the registered window (qs at 16kb, e bytes after) fits");
 
 template <int NMT, bool REPACK, bool SUBSUMS>
 __device__ __forceinline__ void moe_mxfp4_impl(const uint8_t *__restrict__ as, int64_t as_nb1, int64_t as_nb2,
@@ -465,7 +466,7 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 // pairs of one expert.  C[row][pair]: lane l holds pair l % 32 and the rows
 // crowm(v, l) of its wavefront's 32.  Staging as moe_mxfp4_impl (weight
 // windows of 4 blocks, the tile's planes and scales, one group ahead).
-template <int NMT, bool REPACK, bool SUBSUMS>
+template <int NMT, bool REPACK, bool SUBSUMS, bool REG>
 __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int64_t as_nb1, int64_t as_nb2,
                                              const uint8_t *__restrict__ actq, const float *__restrict__ actd,
                                              int ne11, const int32_t *__restrict__ route, int n_pairs, int n_ids,
@@ -523,7 +524,7 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
                                                           (c * 256 + 64 * wv) * 4),
                                              4, 0, 0);
         }
-        if (wrep) {  // registered copy: the group's windows are one contiguous run in LDS order
+        if (REG) {  // registered copy: the group's windows are one contiguous run in LDS order
             const uint8_t *src = wrep + (((int64_t)e * gridDim.y + blockIdx.y) * ngp + g) * (MOE_TR * MOE_WIN * 16);
 #pragma unroll
             for (int c = 0; c < WCHUNK; c++)
@@ -585,7 +586,7 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
     int ngroups = nb / MOE_GB;
     while (ngroups > 0 && MOE_WB * (ngroups - 1) + 16 * MOE_WIN > row_bytes) ngroups--;
     const int nga = (nb + MOE_GB - 1) / MOE_GB;
-    if (wrep) ngroups = nga;  // every window of the registered copy is whole (zero past the row)
+    if (REG) ngroups = nga;  // every window of the registered copy is whole (zero past the row)
     const int rl = w * 32 + li;
     issue(0, 0, ngroups > 0);
     for (int g = 0; g < nga; g++) {
@@ -595,17 +596,32 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
         if (g + 1 < nga) issue(g + 1, stage ^ 1, g + 1 < ngroups);
         if (g < ngroups) {
             const uint32_t *wl = w_lds[stage][rl];
-            uint32_t W[4 * MOE_WIN];
+            // GGUF windows: 17-byte blocks from byte 0 (the whole window in
+            // registers); registered windows: qs of block kb at 16kb, the e
+            // bytes at 64 (aligned reads, no byte shifts)
+            uint32_t W[REG ? 1 : 4 * MOE_WIN];
+            if constexpr (REG) {
+                W[0] = wl[16];
+            } else {
 #pragma unroll
-            for (int i = 0; i < MOE_WIN; i++) {
-                const uint4 t = reinterpret_cast<const uint4 *>(wl)[i];
-                W[4 * i] = t.x; W[4 * i + 1] = t.y; W[4 * i + 2] = t.z; W[4 * i + 3] = t.w;
+                for (int i = 0; i < MOE_WIN; i++) {
+                    const uint4 t = reinterpret_cast<const uint4 *>(wl)[i];
+                    W[4 * i] = t.x; W[4 * i + 1] = t.y; W[4 * i + 2] = t.z; W[4 * i + 3] = t.w;
+                }
             }
-            auto e_of = [&](int kb) { return (W[(17 * kb) >> 2] >> (8 * ((17 * kb) & 3))) & 0xffu; };
+            auto e_of = [&](int kb) {
+                if constexpr (REG) return (W[0] >> (8 * kb)) & 0xffu;
+                else return (W[(17 * kb) >> 2] >> (8 * ((17 * kb) & 3))) & 0xffu;
+            };
             auto q_of = [&](int kb, uint32_t (&q)[4]) {
-                const int o = 17 * kb + 1, d = o >> 2, sh = o & 3;
+                if constexpr (REG) {
+                    const uint4 t = reinterpret_cast<const uint4 *>(wl)[kb];
+                    q[0] = t.x; q[1] = t.y; q[2] = t.z; q[3] = t.w;
+                } else {
+                    const int o = 17 * kb + 1, d = o >> 2, sh = o & 3;
 #pragma unroll
-                for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbyte(W[d + i + 1], W[d + i], sh);
+                    for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbyte(W[d + i + 1], W[d + i], sh);
+                }
             };
             const int nbl = nb - MOE_GB * g;  // blocks of this group inside the row
             bool ok = !SUBSUMS;
@@ -659,28 +675,39 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
         }
     }
 }
-// wrep: the registered copy of the experts (ghip_mxfp4_repack) or null; ngp its groups per row
-#define MOE_FP4_KERNEL(name, NMT, REPACK, SUB)                                                                \
+// wrep: the registered copy of the experts (ghip_mxfp4_repack; the _reg
+// kernels) or unused; ngp its groups per row.  Four workgroups per CU (38 KB
+// of LDS each) need at most 128 VGPRs: 4 wavefronts per SIMD measured 184 us
+// against 226 us at 2 (config 4 gate_up, registered).
+#define MOE_FP4_KERNEL(name, NMT, REPACK, SUB, REG)                                                           \
     extern "C" __global__ void __launch_bounds__(256)                                                         \
+        __attribute__((amdgpu_waves_per_eu(NMT == 1 && !SUB ? 4 : 1)))                                        \
         name(MOE_ARGS, const uint8_t *__restrict__ wrep, int ngp) {                                           \
-        moe_fp4_impl<NMT, REPACK, SUB>(MOE_PASS_FP4);                                                         \
+        moe_fp4_impl<NMT, REPACK, SUB, REG>(MOE_PASS_FP4);                                                    \
     }
 #define MOE_PASS_FP4                                                                                          \
     as, as_nb1, as_nb2, (const uint8_t *)actf, actd, ne11, route, n_pairs, n_ids, dst, dst_nb1, dst_nb2, rows, nb, \
         sub, wrep, ngp
-MOE_FP4_KERNEL(ghip_moe_fp4, 1, true, false)
-MOE_FP4_KERNEL(ghip_moe_fp4_plain, 1, false, false)
-MOE_FP4_KERNEL(ghip_moe_fp4_sub, 1, true, true)
-MOE_FP4_KERNEL(ghip_moe_fp4_plain_sub, 1, false, true)
-MOE_FP4_KERNEL(ghip_moe_fp4_t64, 2, true, false)
-MOE_FP4_KERNEL(ghip_moe_fp4_t64_plain, 2, false, false)
+MOE_FP4_KERNEL(ghip_moe_fp4, 1, true, false, false)
+MOE_FP4_KERNEL(ghip_moe_fp4_plain, 1, false, false, false)
+MOE_FP4_KERNEL(ghip_moe_fp4_sub, 1, true, true, false)
+MOE_FP4_KERNEL(ghip_moe_fp4_plain_sub, 1, false, true, false)
+MOE_FP4_KERNEL(ghip_moe_fp4_t64, 2, true, false, false)
+MOE_FP4_KERNEL(ghip_moe_fp4_t64_plain, 2, false, false, false)
+MOE_FP4_KERNEL(ghip_moe_fp4_reg, 1, true, false, true)
+MOE_FP4_KERNEL(ghip_moe_fp4_plain_reg, 1, false, false, true)
+MOE_FP4_KERNEL(ghip_moe_fp4_sub_reg, 1, true, true, true)
+MOE_FP4_KERNEL(ghip_moe_fp4_plain_sub_reg, 1, false, true, true)
+MOE_FP4_KERNEL(ghip_moe_fp4_t64_reg, 2, true, false, true)
+MOE_FP4_KERNEL(ghip_moe_fp4_t64_plain_reg, 2, false, false, true)
 
 
 
 // The registered layout of MXFP4 experts for moe_fp4_impl: per (expert, block
-// of 128 rows, group of MOE_GB 17-byte blocks) the 128 rows' windows, 80 bytes
-// each (68 of data, zero past the row and in the padding), one contiguous run
-// in the order the kernel stages them in LDS.  One thread per 16-byte chunk.
+// of 128 rows, group of MOE_GB blocks) the 128 rows' windows, 80 bytes each --
+// the qs of block kb at 16kb, the four e bytes at 64, zero past the row and
+// in the padding -- one contiguous run in the order the kernel stages them in
+// LDS.  One thread per 16-byte chunk.
 extern "C" __global__ void __launch_bounds__(256)
 ghip_mxfp4_repack(const uint8_t *__restrict__ W, int64_t nb1, int64_t nb2, int rows, int nb, int n_as, int nrb,
                   int ngp, uint8_t *__restrict__ out) {
@@ -700,9 +727,10 @@ ghip_mxfp4_repack(const uint8_t *__restrict__ W, int64_t nb1, int64_t nb2, int r
         const uint8_t *src = W + (int64_t)e * nb2 + (int64_t)row * nb1;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
-            const int o = 16 * c16 + k;  // byte of the window
-            const int pos = MOE_WB * g + o;
-            if (o < MOE_WB && pos < row_bytes) v[k >> 2] |= (uint32_t)src[pos] << (8 * (k & 3));
+            int pos = -1;  // byte of the row for byte k of this chunk
+            if (c16 < MOE_GB) pos = MXFP4_BYTES * (MOE_GB * g + c16) + 1 + k;        // qs of block c16
+            else if (c16 == MOE_GB && k < MOE_GB) pos = MXFP4_BYTES * (MOE_GB * g + k);  // e of block k
+            if (pos >= 0 && pos < row_bytes) v[k >> 2] |= (uint32_t)src[pos] << (8 * (k & 3));
         }
     }
     *reinterpret_cast<uint4 *>(out + i * 16) = make_uint4(v[0], v[1], v[2], v[3]);

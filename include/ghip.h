@@ -189,14 +189,17 @@ ghip_status ghip_mul_mat_id_subsums(ghip_context *ctx, const ghip_tensor *as, co
 /* dst = FLASH_ATTN_EXT(q, k, v, mask, sinks) (forward_flash_attn_ext
  * compute.rs:4563-4625; FlashAttn flash_attn.rs:273-386):
  *   q:     F32 [DK, T, H]      (nb0 == 4, any nb1/nb2)
- *   k, v:  F16 [DK, S, H_kv]   (nb0 == 2), DK == DV in {64, 128}, H % H_kv == 0,
- *          H / H_kv <= 8
+ *   k:     F16 or F32 [DK, S, H_kv], v: F16 or F32 [DV, S, H_kv] (rows
+ *          contiguous), DK and DV in 1..256, H % H_kv == 0 (flash_attn.rs:303-313)
  *   mask:  F16 [>= S, >= T] or NULL (rows contiguous)
  *   sinks: F32 [H] or NULL
  *   dst:   F32 [DV, H, T] contiguous
  *   dst->op_params: [0] scale, [1] max_bias, [2] logit_softcap (f32 bits).
- * The KV range is split across workgroups and merged in slice order; the
- * result matches the reference within its f16-K/V tolerance (2e-3 max-abs). */
+ * F16 K/V with DK == DV in {64, 128} and H / H_kv <= 8 run the matrix-core
+ * kernels (the KV range split across workgroups and merged in slice order);
+ * every other shape runs a row walk in key order (the reference's attn_row,
+ * with its f16 accumulator for an F16 V on that route).  The result matches
+ * the reference within 2e-3 max-abs. */
 ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const ghip_tensor *k, const ghip_tensor *v,
                                 const ghip_tensor *mask, const ghip_tensor *sinks, const ghip_tensor *dst,
                                 void *stream);

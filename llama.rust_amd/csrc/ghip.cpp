@@ -664,6 +664,8 @@ struct FaParams {
     int T, S, H, H_kv, nsplit, chunk;
     float scale, softcap, m0, m1;
     int n_head_log2;
+    int DK, DV;
+    int k_f32, v_f32;
 };
 
 float f32_param(const ghip_tensor *t, int i) {
@@ -678,14 +680,17 @@ bool plan_fa(ghip_context *ctx, const ghip_tensor *q, const ghip_tensor *k, cons
     auto bad = [&](const char *why) { st = ctx->fail(GHIP_STATUS_BACKEND_ERROR, "flash_attn_ext: %s", why); return false; };
     if (!q || !k || !v || !d) return bad("null operand");
     if (q->type != GHIP_TYPE_F32 || q->nb[0] != 4) return bad("q must be F32 with nb0 == 4 (flash_attn.rs:322)");
-    if (k->type != GHIP_TYPE_F16 || v->type != GHIP_TYPE_F16 || k->nb[0] != 2 || v->nb[0] != 2)
-        return bad("k and v must be F16 rows");
-    if (k->ne[0] != q->ne[0] || v->ne[0] != k->ne[0]) return bad("DK == DV required");
-    if (k->ne[0] != 64 && k->ne[0] != 128) return bad("head size must be 64 or 128");
+    auto kv_ok = [](const ghip_tensor *t) {
+        return (t->type == GHIP_TYPE_F16 && t->nb[0] == 2) || (t->type == GHIP_TYPE_F32 && t->nb[0] == 4);
+    };
+    if (!kv_ok(k) || !kv_ok(v)) return bad("k and v must be F16 or F32 rows (flash_attn.rs:305-313)");
+    if (k->ne[0] != q->ne[0]) return bad("DK of q and k differ");
+    if (k->ne[0] < 1 || k->ne[0] > 256 || v->ne[0] < 1 || v->ne[0] > 256) return bad("head sizes must be 1..256");
     if (q->ne[3] != 1 || k->ne[3] != 1 || v->ne[3] != 1) return bad("4-D batches are not supported");
     if (k->ne[1] != v->ne[1] || k->ne[2] != v->ne[2]) return bad("k/v shapes differ");
-    if (q->ne[2] % k->ne[2] || q->ne[2] / k->ne[2] > 8) return bad("H % H_kv != 0 or H/H_kv > 8");
-    if (k->nb[1] % 2 || k->nb[2] % 2 || v->nb[1] % 2 || v->nb[2] % 2 || q->nb[1] % 4 || q->nb[2] % 4)
+    if (q->ne[2] % k->ne[2]) return bad("H % H_kv != 0");
+    if (k->nb[1] % k->nb[0] || k->nb[2] % k->nb[0] || v->nb[1] % v->nb[0] || v->nb[2] % v->nb[0] || q->nb[1] % 4 ||
+        q->nb[2] % 4)
         return bad("strides must be element multiples");
     if (mask) {
         if (mask->type != GHIP_TYPE_F16 || mask->nb[0] != 2) return bad("mask must be F16 rows (ggml.c:5515)");
@@ -1240,6 +1245,20 @@ ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const g
     p.m0 = max_bias > 0.0f ? powf(2.0f, -max_bias / (float)p.n_head_log2) : 1.0f;
     p.m1 = max_bias > 0.0f ? powf(2.0f, -(max_bias / 2.0f) / (float)p.n_head_log2) : 1.0f;
     p.sinks = sinks ? (const float *)sinks->data : nullptr;
+    p.DK = D;
+    p.DV = (int)v->ne[0];
+    p.k_f32 = k->type == GHIP_TYPE_F32;
+    p.v_f32 = v->type == GHIP_TYPE_F32;
+    // shapes the tuned kernels do not take (F32 K or V, DK != DV, head sizes
+    // other than 64 / 128, H / H_kv > 8) run the general row walk: with the
+    // f16 accumulator where the reference's route is the row walk over an F16
+    // V, fp32 otherwise
+    const bool tuned = !p.k_f32 && !p.v_f32 && p.DK == p.DV && (D == 64 || D == 128) && G <= 8;
+    if (!tuned) {
+        const bool row_walk = !(T == 1 && S >= 512) && T < 64;
+        return ctx->launch(row_walk && !p.v_f32 ? "ghip_fa_rowgen_f16acc" : "ghip_fa_rowgen",
+                           dim3((unsigned)((T * H + 3) / 4)), dim3(256), 0, s, p);
+    }
     // flash_attn.rs:371-386 routes: single-row decode over >= 512 keys splits the
     // KV range, >= 64 query rows take the tiled kernel (fp32 accumulators) --
     // both run on the MFMA kernel below.  Fewer rows take the one-chunk walk

@@ -46,6 +46,8 @@ struct FaParams {
     int T, S, H, H_kv, nsplit, chunk;
     float scale, softcap, m0, m1;
     int n_head_log2;
+    int DK, DV;          // head sizes (the general kernel; the others are compiled per D)
+    int k_f32, v_f32;    // K / V element type: 1 = F32 (strides still counted in halfs)
 };
 
 DEV float head_slope(const FaParams &p, int h) {
@@ -789,6 +791,108 @@ __device__ __forceinline__ void fa_rowseq_impl(const FaParams &p) {
 #pragma unroll
     for (int i = 0; i < PL; i++) o[i] = acc[i] * sinv;
 }
+
+// General shapes (any DK, DV <= 256, F32 or F16 K and V, any H / H_kv): one
+// wavefront per (query, head) row walking the keys in order, as the
+// reference's row walk attn_row (flash_attn.rs:482-703) -- lane j scores key
+// k0 + j of each 64-key tile (q rounded to f16 for an F16 K, as
+// q_to_vec_dot), then each lane updates dims lane + 64i of the accumulator
+// per live key: new max => rescale by exp(Mold - M), else vs = exp(s - M);
+// acc = fma(v, vs, acc).  F16ACC rounds the accumulator to f16 after every
+// step (the reference's VKQ16 for an F16 V); otherwise it stays fp32 (an F32
+// V, and the fp32 accumulators of the tiled and split-KV routes, which this
+// kernel stands in for on shapes the other kernels do not take).
+template <bool F16ACC>
+__device__ __forceinline__ void fa_rowgen_impl(const FaParams &p) {
+    __shared__ float qs[4][256];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int row = blockIdx.x * 4 + w;  // row = t * H + h
+    const bool valid = row < p.T * p.H;
+    const int t = valid ? row / p.H : 0, h = valid ? row % p.H : 0;
+    const int hk = h / (p.H / p.H_kv);
+    const int DK = p.DK, DV = p.DV;
+    const float slope = head_slope(p, h);
+    const float *qr = p.q + (int64_t)h * p.q_nb2 + (int64_t)t * p.q_nb1;
+    for (int d = lane; d < DK; d += 64) qs[w][d] = p.k_f32 ? qr[d] : h2f(f2h_rn(qr[d]));
+    __syncthreads();
+    if (!valid) return;
+    const uint16_t *kbase = p.k + (int64_t)hk * p.k_nb2;
+    const uint16_t *vbase = p.v + (int64_t)hk * p.v_nb2;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float M = -__builtin_inff(), S = 0.0f;
+    for (int k0 = 0; k0 < p.S; k0 += 64) {
+        const int key = k0 + lane;
+        float s = -__builtin_inff();
+        bool live = false;
+        if (key < p.S) {
+            const float mv = p.mask ? slope * h2f(p.mask[(int64_t)t * p.mask_nb1 + key]) : 0.0f;
+            if (mv != -__builtin_inff()) {
+                live = true;
+                const uint16_t *kr = kbase + (int64_t)key * p.k_nb1;
+                float dot = 0.0f;
+                if (p.k_f32) {
+                    const float *kf = reinterpret_cast<const float *>(kr);
+                    for (int d = 0; d < DK; d++) dot = fmaf(kf[d], qs[w][d], dot);
+                } else {
+                    for (int d = 0; d < DK; d++) dot = fmaf(h2f(kr[d]), qs[w][d], dot);
+                }
+                s = dot * p.scale;
+                if (p.softcap != 0.0f) s = p.softcap * tanhf(s);
+                s += mv;
+            }
+        }
+        const uint64_t livemask = __ballot(live);
+        const int nk = min(64, p.S - k0);
+        for (int j = 0; j < nk; j++) {
+            if (!((livemask >> j) & 1)) continue;
+            const float sj = __shfl(s, j, 64);
+            const uint16_t *vr = vbase + (int64_t)(k0 + j) * p.v_nb1;
+            float vv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int d = lane + 64 * i;
+                vv[i] = d >= DV ? 0.0f : p.v_f32 ? reinterpret_cast<const float *>(vr)[d] : h2f(vr[d]);
+            }
+            float ms = 1.0f, vs = 1.0f;
+            if (sj > M) {
+                const float Mold = M;
+                M = sj;
+                ms = expf(Mold - M);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[i] = F16ACC ? h2f(f2h_rn(acc[i] * ms)) : acc[i] * ms;
+            } else {
+                vs = expf(sj - M);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float a = fmaf(vv[i], vs, acc[i]);
+                acc[i] = F16ACC ? h2f(f2h_rn(a)) : a;
+            }
+            S = fmaf(S, ms, vs);
+        }
+    }
+    if (p.sinks) {
+        const float sh = p.sinks[h];
+        float ms = 1.0f, vs = 1.0f;
+        if (sh > M) {
+            ms = expf(M - sh);
+            M = sh;
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] *= ms;
+        } else {
+            vs = expf(sh - M);
+        }
+        S = opaque(S * ms) + vs;  // unfused, as the reference
+    }
+    const float sinv = S == 0.0f ? 0.0f : 1.0f / S;
+    float *o = p.dst + (int64_t)row * DV;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        if (lane + 64 * i < DV) o[lane + 64 * i] = acc[i] * sinv;
+}
+
+extern "C" __global__ void __launch_bounds__(256) ghip_fa_rowgen_f16acc(FaParams p) { fa_rowgen_impl<true>(p); }
+extern "C" __global__ void __launch_bounds__(256) ghip_fa_rowgen(FaParams p) { fa_rowgen_impl<false>(p); }
 
 extern "C" __global__ void __launch_bounds__(512) ghip_fa_fwd_d128(FaParams p) { fa_fwd_impl<128, false>(p); }
 extern "C" __global__ void __launch_bounds__(512) ghip_fa_fwd_d64(FaParams p) { fa_fwd_impl<64, false>(p); }

@@ -57,7 +57,8 @@ def flash_attn_node(q, k, v, mask, sinks, out, scale=1.0, max_bias=0.0, softcap=
     d = describe(out, F32)
     for i, f in enumerate((scale, max_bias, softcap)):
         d.op_params[i] = struct.unpack("<i", struct.pack("<f", f))[0]
-    return Node(OP_FLASH_ATTN_EXT, [describe(q, F32), describe(k, F16), describe(v, F16), describe(mask, F16),
+    kvt = lambda t: F32 if t.dtype == torch.float32 else F16
+    return Node(OP_FLASH_ATTN_EXT, [describe(q, F32), describe(k, kvt(k)), describe(v, kvt(v)), describe(mask, F16),
                                     describe(sinks, F32)], d)
 
 
@@ -266,12 +267,14 @@ class Backend:
 
     # ---- FLASH_ATTN_EXT
     def flash_attn_ext(self, q, k, v, mask=None, sinks=None, scale=1.0, max_bias=0.0, softcap=0.0, out=None):
-        """q [H, T, D] f32, k/v [H_kv, S, D] f16, mask [T, S] f16, sinks [H] f32 -> [T, H, D] f32."""
+        """q [H, T, DK] f32, k [H_kv, S, DK] / v [H_kv, S, DV] f16 or f32, mask [T, S] f16,
+        sinks [H] f32 -> [T, H, DV] f32."""
         import struct
         H, T, D = q.shape
         if out is None:
             out = torch.empty((T, H, v.shape[2]), dtype=torch.float32, device=q.device)
-        tq, tk, tv = describe(q, F32), describe(k, F16), describe(v, F16)
+        kvt = lambda t: F32 if t.dtype == torch.float32 else F16
+        tq, tk, tv = describe(q, F32), describe(k, kvt(k)), describe(v, kvt(v))
         tm, ts, td = describe(mask, F16), describe(sinks, F32), describe(out, F32)
         for i, f in enumerate((scale, max_bias, softcap)):
             td.op_params[i] = struct.unpack("<i", struct.pack("<f", f))[0]

@@ -90,3 +90,37 @@ def test_config5(be, T):
     """Config 5: 32 query / 8 KV heads, D = 128, KV 8192, causal chunk at the
     end of the cache (decode T = 1, prefill T = 512)."""
     run(be, 32, 8, 128, T, 8192, seed=5, n_chunks=16)
+
+
+def run_general(be, H, Hkv, DK, DV, T, S, kv=np.float16, sinks=False, seed=0, n_chunks=8):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((H, T, DK)).astype(np.float32)
+    k = rng.standard_normal((Hkv, S, DK)).astype(kv)
+    v = rng.standard_normal((Hkv, S, DV)).astype(kv)
+    m = causal_mask(T, S)
+    sk = rng.standard_normal(H).astype(np.float32) if sinks else None
+    scale = 1.0 / np.sqrt(DK)
+    want, path = O.flash_attn_ext(q, k, v, m, sk, scale, 0.0, 0.0, n_chunks=n_chunks)
+    print(f"fa general H={H} Hkv={Hkv} DK={DK} DV={DV} T={T} S={S} kv={np.dtype(kv).name} path={path}", flush=True)
+    t = lambda a: torch.from_numpy(a).cuda() if a is not None else None
+    got = be.flash_attn_ext(t(q), t(k), t(v), t(m), t(sk), scale).cpu().numpy()
+    err = float(np.max(np.abs(got - want)))
+    assert err <= TOL, f"max-abs {err:.3e}"
+
+
+@pytest.mark.parametrize("H,Hkv,DK,DV,T,S,kv", [
+    (8, 2, 256, 256, 5, 300, np.float16),    # D = 256, row walk (f16 accumulator)
+    (8, 2, 256, 256, 70, 200, np.float16),   # D = 256, tiled route
+    (4, 2, 64, 128, 3, 90, np.float16),      # DK != DV
+    (4, 2, 192, 128, 66, 130, np.float16),   # DK != DV, tiled route
+    (4, 2, 32, 32, 40, 100, np.float16),
+    (4, 2, 64, 64, 10, 80, np.float32),      # F32 K/V, row walk
+    (4, 1, 128, 128, 64, 128, np.float32),   # F32 K/V, tiled route
+    (32, 2, 64, 64, 4, 120, np.float16),     # H / H_kv = 16
+    (16, 1, 80, 80, 1, 700, np.float16),     # split-KV route shape, head size 80
+])
+def test_general_shapes(be, H, Hkv, DK, DV, T, S, kv):
+    """Shapes outside the tuned kernels (F32 K/V, DK != DV, head sizes other
+    than 64 / 128, H / H_kv > 8) take the general row walk, still within 2e-3
+    of the oracle's route for the shape."""
+    run_general(be, H, Hkv, DK, DV, T, S, kv, sinks=(T % 2 == 1))

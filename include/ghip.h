@@ -274,6 +274,71 @@ ghip_status ghip_weight_unregister(ghip_context *ctx, const ghip_tensor *w);
  * count) -- repack_stats (repack.rs:4329-4334).  Any pointer may be NULL. */
 ghip_status ghip_weight_cache_stats(ghip_context *ctx, size_t *n_weights, size_t *bytes, size_t *built);
 
+/* ---- GGUF files (crates/ggml/src/gguf.rs:388-655, a port of
+ * gguf_init_from_file): the container is memory-mapped and parsed on the
+ * host; tensors are uploaded to device memory in their GGUF block layout
+ * and, if asked, registered (ghip_weight_register) so their repacked copies
+ * are built on the device once. */
+typedef struct ghip_gguf ghip_gguf;
+
+/* enum gguf_type (gguf.rs:49-63) */
+enum {
+    GHIP_GGUF_UINT8 = 0, GHIP_GGUF_INT8 = 1, GHIP_GGUF_UINT16 = 2, GHIP_GGUF_INT16 = 3,
+    GHIP_GGUF_UINT32 = 4, GHIP_GGUF_INT32 = 5, GHIP_GGUF_FLOAT32 = 6, GHIP_GGUF_BOOL = 7,
+    GHIP_GGUF_STRING = 8, GHIP_GGUF_ARRAY = 9, GHIP_GGUF_UINT64 = 10, GHIP_GGUF_INT64 = 11,
+    GHIP_GGUF_FLOAT64 = 12,
+};
+
+/* TensorInfo (gguf.rs:211-228): nb computed from the type as gguf.cpp does;
+ * offset relative to its part's data section; part = the split file. */
+typedef struct ghip_gguf_tensor_info {
+    char name[64];
+    int32_t type;
+    int64_t ne[4];
+    uint64_t nb[4];
+    uint64_t offset;
+    uint64_t size;
+    int32_t part;
+} ghip_gguf_tensor_info;
+
+/* Gguf::open (follow_splits != 0: the split.* pass, gguf.rs:388-480) or
+ * Gguf::open_single.  On failure returns GHIP_STATUS_BACKEND_ERROR and the
+ * reference's GgufError text (gguf.rs:278-300) in err. */
+ghip_status ghip_gguf_open(const char *path, int follow_splits, ghip_gguf **out, char *err, size_t err_len);
+void ghip_gguf_close(ghip_gguf *g);
+uint32_t ghip_gguf_version(const ghip_gguf *g);
+uint64_t ghip_gguf_alignment(const ghip_gguf *g);
+uint64_t ghip_gguf_data_offset(const ghip_gguf *g);   /* part 0's */
+int64_t ghip_gguf_n_parts(const ghip_gguf *g);
+int64_t ghip_gguf_n_kv(const ghip_gguf *g);
+const char *ghip_gguf_key(const ghip_gguf *g, int64_t i);
+int64_t ghip_gguf_find_key(const ghip_gguf *g, const char *key);  /* -1 if absent */
+int32_t ghip_gguf_kv_type(const ghip_gguf *g, int64_t i);         /* GHIP_GGUF_* */
+int32_t ghip_gguf_arr_type(const ghip_gguf *g, int64_t i);        /* element type, -1 if not an array */
+int64_t ghip_gguf_arr_n(const ghip_gguf *g, int64_t i);           /* element count, -1 if not an array */
+/* Value of kv i (j = -1) or of element j of array kv i; 1 on success, 0 if
+ * absent or of another type.  u32 / f32 follow Value::as_u32 / as_f32
+ * (gguf.rs:141-168), u16 the exact type (as_u16); i64 reads any integer. */
+int ghip_gguf_get_u32(const ghip_gguf *g, int64_t i, int64_t j, uint32_t *out);
+int ghip_gguf_get_u16(const ghip_gguf *g, int64_t i, int64_t j, uint16_t *out);
+int ghip_gguf_get_f32(const ghip_gguf *g, int64_t i, int64_t j, float *out);
+int ghip_gguf_get_i64(const ghip_gguf *g, int64_t i, int64_t j, int64_t *out);
+int ghip_gguf_get_f64(const ghip_gguf *g, int64_t i, int64_t j, double *out);
+int ghip_gguf_get_bool(const ghip_gguf *g, int64_t i, int64_t j, int *out);
+int ghip_gguf_get_str(const ghip_gguf *g, int64_t i, int64_t j, const char **s, size_t *n);
+int64_t ghip_gguf_n_tensors(const ghip_gguf *g);
+int64_t ghip_gguf_find_tensor(const ghip_gguf *g, const char *name);
+ghip_status ghip_gguf_tensor(const ghip_gguf *g, int64_t i, ghip_gguf_tensor_info *out);
+/* host pointer to tensor i's bytes in its part's mapping (tensor_data,
+ * gguf.rs:632-640); NULL when they lie outside the file */
+const void *ghip_gguf_tensor_data(const ghip_gguf *g, int64_t i);
+/* Copy tensor i's bytes to the device pointer dst (at least its size) on
+ * `stream` through pinned staging; returns when the copy is complete.  With
+ * register_weight != 0 the uploaded tensor is then registered
+ * (ghip_weight_register) and that build completes too. */
+ghip_status ghip_gguf_upload(ghip_context *ctx, const ghip_gguf *g, int64_t i, void *dst, int register_weight,
+                             void *stream);
+
 /* Quantize nrows rows of n_per_row f32 values (device pointer src) into
  * GGUF blocks of `type` (Q4_0, Q4_K, Q6_K, MXFP4) at the device pointer dst,
  * byte-identical to the reference's no-imatrix quantizers

@@ -58,7 +58,7 @@ def build_host():
     _run([HIPCC, "-c", "-fPIC", *DEVICE_FLAGS, "-I", CSRC, os.path.join(CSRC, "ghip_noalloc.hip"), "-o", obj])
     _run(["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wno-unused-result", "-D__HIP_PLATFORM_AMD__",
           "-I", os.path.join(ROCM, "include"), "-I", os.path.join(ROOT, "include"),
-          os.path.join(CSRC, "ghip.cpp"), obj, "-o", out,
+          os.path.join(CSRC, "ghip.cpp"), os.path.join(CSRC, "ghip_gguf.cpp"), obj, "-o", out,
           "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-ldl", "-Wl,-rpath," + os.path.join(ROCM, "lib")])
 
 

@@ -114,6 +114,10 @@ struct ghip_context {
         }
     };
     std::unordered_map<WeightKey, WeightCopy, WeightKeyHash> wcache;
+    // pinned host staging for ghip_gguf_upload: two buffers, each reused
+    // once the copy engine has drained it (its event)
+    void *stage[2] = {nullptr, nullptr};
+    hipEvent_t stage_ev[2] = {nullptr, nullptr};
     size_t wcache_bytes = 0;   // bytes held by wcache
     size_t wcache_built = 0;   // copies materialized so far (hits do not count)
 
@@ -1335,6 +1339,10 @@ void ghip_free(ghip_context *ctx) {
     if (ctx->ws) hipFree(ctx->ws);
     for (void *p : ctx->retired) hipFree(p);
     for (auto &kv : ctx->wcache) hipFree(kv.second.p);
+    for (int b = 0; b < 2; b++) {
+        if (ctx->stage[b]) hipHostFree(ctx->stage[b]);
+        if (ctx->stage_ev[b]) hipEventDestroy(ctx->stage_ev[b]);
+    }
     if (ctx->order_ev) hipEventDestroy(ctx->order_ev);
     for (hipModule_t m : ctx->modules) hipModuleUnload(m);
     delete ctx;
@@ -1487,6 +1495,41 @@ ghip_status ghip_mul_mat_fixed_scratch(ghip_context *ctx, const ghip_tensor *src
     return mul_mat_impl(ctx, src0, src1, dst, nullptr, nullptr, stream, scratch, bytes);
 }
 int ghip_context_device(const ghip_context *ctx) { return ctx ? ctx->device : -1; }
+
+ghip_status ghip_context_upload(ghip_context *ctx, void *dst, const void *src, size_t n, void *stream) {
+    constexpr size_t kStage = 32u << 20;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    hipStream_t s = (hipStream_t)stream;
+    if (ghip_context::capturing(s)) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "gguf_upload: stream is being captured");
+    if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    for (int b = 0; b < 2; b++) {
+        if (!ctx->stage[b] && (hipHostMalloc(&ctx->stage[b], kStage, hipHostMallocDefault) != hipSuccess ||
+                               hipEventCreateWithFlags(&ctx->stage_ev[b], hipEventDisableTiming) != hipSuccess)) {
+            (void)hipGetLastError();
+            return ctx->fail(GHIP_STATUS_OUT_OF_MEMORY, "gguf_upload: pinned staging allocation failed");
+        }
+    }
+    ghip_status st = ctx->begin(s);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    bool used[2] = {false, false};
+    for (size_t off = 0, k = 0; off < n; off += kStage, k++) {
+        const int b = (int)(k & 1);
+        const size_t len = std::min(kStage, n - off);
+        if (used[b] && hipEventSynchronize(ctx->stage_ev[b]) != hipSuccess) break;
+        memcpy(ctx->stage[b], (const uint8_t *)src + off, len);
+        if (hipMemcpyAsync((uint8_t *)dst + off, ctx->stage[b], len, hipMemcpyHostToDevice, s) != hipSuccess ||
+            hipEventRecord(ctx->stage_ev[b], s) != hipSuccess) {
+            (void)hipGetLastError();
+            return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "gguf_upload: host-to-device copy failed");
+        }
+        used[b] = true;
+    }
+    if (hipStreamSynchronize(s) != hipSuccess) {
+        (void)hipGetLastError();
+        return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "gguf_upload: copy did not complete");
+    }
+    return GHIP_STATUS_SUCCESS;
+}
 ghip_status ghip_context_fail(ghip_context *ctx, ghip_status st, const char *msg) { return ctx->fail(st, "%s", msg); }
 
 extern "C" {

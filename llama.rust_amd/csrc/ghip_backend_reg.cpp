@@ -107,6 +107,30 @@ void *reg_proc_address(const ggml_hip_backend_reg *, const char *name) {
         {"ghip_weight_register", (void *)&ghip_weight_register},
         {"ghip_weight_unregister", (void *)&ghip_weight_unregister},
         {"ghip_weight_cache_stats", (void *)&ghip_weight_cache_stats},
+        {"ghip_gguf_alignment", (void *)&ghip_gguf_alignment},
+        {"ghip_gguf_arr_n", (void *)&ghip_gguf_arr_n},
+        {"ghip_gguf_arr_type", (void *)&ghip_gguf_arr_type},
+        {"ghip_gguf_close", (void *)&ghip_gguf_close},
+        {"ghip_gguf_data_offset", (void *)&ghip_gguf_data_offset},
+        {"ghip_gguf_find_key", (void *)&ghip_gguf_find_key},
+        {"ghip_gguf_find_tensor", (void *)&ghip_gguf_find_tensor},
+        {"ghip_gguf_get_bool", (void *)&ghip_gguf_get_bool},
+        {"ghip_gguf_get_f32", (void *)&ghip_gguf_get_f32},
+        {"ghip_gguf_get_f64", (void *)&ghip_gguf_get_f64},
+        {"ghip_gguf_get_i64", (void *)&ghip_gguf_get_i64},
+        {"ghip_gguf_get_str", (void *)&ghip_gguf_get_str},
+        {"ghip_gguf_get_u16", (void *)&ghip_gguf_get_u16},
+        {"ghip_gguf_get_u32", (void *)&ghip_gguf_get_u32},
+        {"ghip_gguf_key", (void *)&ghip_gguf_key},
+        {"ghip_gguf_kv_type", (void *)&ghip_gguf_kv_type},
+        {"ghip_gguf_n_kv", (void *)&ghip_gguf_n_kv},
+        {"ghip_gguf_n_parts", (void *)&ghip_gguf_n_parts},
+        {"ghip_gguf_n_tensors", (void *)&ghip_gguf_n_tensors},
+        {"ghip_gguf_open", (void *)&ghip_gguf_open},
+        {"ghip_gguf_tensor", (void *)&ghip_gguf_tensor},
+        {"ghip_gguf_tensor_data", (void *)&ghip_gguf_tensor_data},
+        {"ghip_gguf_upload", (void *)&ghip_gguf_upload},
+        {"ghip_gguf_version", (void *)&ghip_gguf_version},
     };
     if (!name) return nullptr;
     for (const Proc &p : procs)

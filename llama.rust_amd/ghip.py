@@ -315,3 +315,171 @@ class Backend:
 
     def synchronize(self):
         self._check(lib().ghip_synchronize(self._ctx, _stream()), "ghip_synchronize")
+
+
+# ---------------------------------------------------------------- GGUF files
+class GgufTensorInfo(C.Structure):
+    _fields_ = [("name", C.c_char * 64), ("type", C.c_int32), ("ne", C.c_int64 * 4), ("nb", C.c_uint64 * 4),
+                ("offset", C.c_uint64), ("size", C.c_uint64), ("part", C.c_int32)]
+
+
+def _gguf_lib():
+    L = lib()
+    if not getattr(L, "_gguf_ready", False):
+        V, P = C.c_void_p, C.POINTER
+        sig = {
+            "ghip_gguf_open": (C.c_int, [C.c_char_p, C.c_int, P(V), C.c_char_p, C.c_size_t]),
+            "ghip_gguf_close": (None, [V]),
+            "ghip_gguf_version": (C.c_uint32, [V]), "ghip_gguf_alignment": (C.c_uint64, [V]),
+            "ghip_gguf_data_offset": (C.c_uint64, [V]), "ghip_gguf_n_parts": (C.c_int64, [V]),
+            "ghip_gguf_n_kv": (C.c_int64, [V]), "ghip_gguf_key": (C.c_char_p, [V, C.c_int64]),
+            "ghip_gguf_find_key": (C.c_int64, [V, C.c_char_p]), "ghip_gguf_kv_type": (C.c_int32, [V, C.c_int64]),
+            "ghip_gguf_arr_type": (C.c_int32, [V, C.c_int64]), "ghip_gguf_arr_n": (C.c_int64, [V, C.c_int64]),
+            "ghip_gguf_get_u32": (C.c_int, [V, C.c_int64, C.c_int64, P(C.c_uint32)]),
+            "ghip_gguf_get_u16": (C.c_int, [V, C.c_int64, C.c_int64, P(C.c_uint16)]),
+            "ghip_gguf_get_f32": (C.c_int, [V, C.c_int64, C.c_int64, P(C.c_float)]),
+            "ghip_gguf_get_i64": (C.c_int, [V, C.c_int64, C.c_int64, P(C.c_int64)]),
+            "ghip_gguf_get_f64": (C.c_int, [V, C.c_int64, C.c_int64, P(C.c_double)]),
+            "ghip_gguf_get_bool": (C.c_int, [V, C.c_int64, C.c_int64, P(C.c_int)]),
+            "ghip_gguf_get_str": (C.c_int, [V, C.c_int64, C.c_int64, P(C.c_void_p), P(C.c_size_t)]),
+            "ghip_gguf_n_tensors": (C.c_int64, [V]), "ghip_gguf_find_tensor": (C.c_int64, [V, C.c_char_p]),
+            "ghip_gguf_tensor": (C.c_int, [V, C.c_int64, P(GgufTensorInfo)]),
+            "ghip_gguf_tensor_data": (C.c_void_p, [V, C.c_int64]),
+            "ghip_gguf_upload": (C.c_int, [V, V, C.c_int64, V, C.c_int, V]),
+        }
+        for n, (r, a) in sig.items():
+            f = getattr(L, n)
+            f.restype, f.argtypes = r, a
+        L._gguf_ready = True
+    return L
+
+
+class Gguf:
+    """A GGUF file opened by the library's reader (ghip_gguf_open)."""
+
+    def __init__(self, path, follow_splits=True):
+        L = _gguf_lib()
+        self._g = C.c_void_p()
+        err = C.create_string_buffer(512)
+        if L.ghip_gguf_open(os.fsencode(path), int(follow_splits), C.byref(self._g), err, 512) != 0:
+            raise GhipError(err.value.decode())
+
+    def close(self):
+        if self._g:
+            _gguf_lib().ghip_gguf_close(self._g)
+            self._g = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def version(self):
+        return _gguf_lib().ghip_gguf_version(self._g)
+
+    @property
+    def alignment(self):
+        return _gguf_lib().ghip_gguf_alignment(self._g)
+
+    @property
+    def data_offset(self):
+        return _gguf_lib().ghip_gguf_data_offset(self._g)
+
+    @property
+    def n_parts(self):
+        return _gguf_lib().ghip_gguf_n_parts(self._g)
+
+    def keys(self):
+        L = _gguf_lib()
+        return [L.ghip_gguf_key(self._g, i).decode() for i in range(L.ghip_gguf_n_kv(self._g))]
+
+    def kv_type(self, key):
+        L = _gguf_lib()
+        return L.ghip_gguf_kv_type(self._g, L.ghip_gguf_find_key(self._g, key.encode()))
+
+    def _scalar(self, i, j):
+        """Python value of kv i (j = -1) or array element j, by its stored type."""
+        L = _gguf_lib()
+        ty = L.ghip_gguf_kv_type(self._g, i) if j < 0 else L.ghip_gguf_arr_type(self._g, i)
+        if ty == GGUF_STRING:
+            p, n = C.c_void_p(), C.c_size_t()
+            L.ghip_gguf_get_str(self._g, i, j, C.byref(p), C.byref(n))
+            return C.string_at(p, n.value).decode("utf-8", errors="surrogateescape")
+        if ty == GGUF_BOOL:
+            b = C.c_int()
+            L.ghip_gguf_get_bool(self._g, i, j, C.byref(b))
+            return bool(b.value)
+        if ty in (GGUF_FLOAT32, GGUF_FLOAT64):
+            f = C.c_double()
+            L.ghip_gguf_get_f64(self._g, i, j, C.byref(f))
+            return f.value
+        v = C.c_int64()
+        L.ghip_gguf_get_i64(self._g, i, j, C.byref(v))
+        return v.value
+
+    def get(self, key, default=None):
+        """The value of `key` (arrays as Python lists), default if absent."""
+        L = _gguf_lib()
+        i = L.ghip_gguf_find_key(self._g, key.encode())
+        if i < 0:
+            return default
+        if L.ghip_gguf_kv_type(self._g, i) == GGUF_ARRAY:
+            return [self._scalar(i, j) for j in range(L.ghip_gguf_arr_n(self._g, i))]
+        return self._scalar(i, -1)
+
+    def get_u32(self, key):
+        """Value::as_u32 semantics (None when it does not apply)."""
+        L = _gguf_lib()
+        out = C.c_uint32()
+        ok = L.ghip_gguf_get_u32(self._g, L.ghip_gguf_find_key(self._g, key.encode()), -1, C.byref(out))
+        return out.value if ok else None
+
+    def get_f32(self, key):
+        L = _gguf_lib()
+        out = C.c_float()
+        ok = L.ghip_gguf_get_f32(self._g, L.ghip_gguf_find_key(self._g, key.encode()), -1, C.byref(out))
+        return out.value if ok else None
+
+    def tensors(self):
+        L = _gguf_lib()
+        out = []
+        for i in range(L.ghip_gguf_n_tensors(self._g)):
+            t = GgufTensorInfo()
+            L.ghip_gguf_tensor(self._g, i, C.byref(t))
+            out.append({"name": t.name.decode(), "type": t.type, "ne": list(t.ne), "nb": list(t.nb),
+                        "offset": t.offset, "size": t.size, "part": t.part})
+        return out
+
+    def tensor_bytes(self, name):
+        """A copy of the tensor's bytes as stored in the file."""
+        L = _gguf_lib()
+        i = L.ghip_gguf_find_tensor(self._g, name.encode())
+        t = GgufTensorInfo()
+        if i < 0 or L.ghip_gguf_tensor(self._g, i, C.byref(t)) != 0:
+            raise KeyError(name)
+        p = L.ghip_gguf_tensor_data(self._g, i)
+        if not p:
+            raise GhipError(f"tensor {name}: bytes outside the file")
+        return C.string_at(p, t.size)
+
+    def upload(self, be, name, register=False):
+        """The tensor on the device as a uint8 tensor [rows..., row_bytes]
+        (ghip_gguf_upload), optionally registered with `be`."""
+        L = _gguf_lib()
+        i = L.ghip_gguf_find_tensor(self._g, name.encode())
+        t = GgufTensorInfo()
+        if i < 0 or L.ghip_gguf_tensor(self._g, i, C.byref(t)) != 0:
+            raise KeyError(name)
+        shape = [int(t.ne[3]), int(t.ne[2]), int(t.ne[1])]
+        while len(shape) > 1 and shape[0] == 1:
+            shape.pop(0)
+        dev = torch.empty(shape + [int(t.nb[1])], dtype=torch.uint8, device="cuda")
+        be._check(L.ghip_gguf_upload(be._ctx, self._g, i, C.c_void_p(dev.data_ptr()), int(register), _stream()),
+                  "ghip_gguf_upload")
+        return dev
+
+
+GGUF_UINT8, GGUF_INT8, GGUF_UINT16, GGUF_INT16, GGUF_UINT32, GGUF_INT32, GGUF_FLOAT32 = range(7)
+GGUF_BOOL, GGUF_STRING, GGUF_ARRAY, GGUF_UINT64, GGUF_INT64, GGUF_FLOAT64 = range(7, 13)

@@ -5,7 +5,10 @@ fly88oj) are golden vectors that an instrumented llama.cpp build produced.  They
 are data (inputs and expected outputs), copied verbatim -- except
 ``tiled_ref.bin``, of which only the Q4_K, Q5_K and Q6_K MUL_MAT and
 MUL_MAT_ID sections are kept (the IQ types are out of scope and the whole file
-is 18 MB).
+is 18 MB).  Also one GGUF file of the reference's tokenizer tests
+(crates/llama/tests/tokenizer_fixtures/vocab/ggml-vocab-llama-spm.gguf, a
+vocab-only model whose metadata vocab.rs:4290-4305 checks) for the GGUF
+reader's known-answer test.
 
 Run once in a container where the reference tree is mounted:
     python tests/golden/extract_fixtures.py /root/reference/parity
@@ -84,6 +87,9 @@ def main(parity_dir):
     for f in WHOLE:
         shutil.copyfile(os.path.join(parity_dir, f), os.path.join(here, f))
     extract_tiled(os.path.join(parity_dir, "tiled_ref.bin"), os.path.join(here, "tiled_ref_kq.bin"))
+    vocab = os.path.join(os.path.dirname(parity_dir), "crates", "llama", "tests", "tokenizer_fixtures", "vocab",
+                         "ggml-vocab-llama-spm.gguf")
+    shutil.copyfile(vocab, os.path.join(here, "ggml-vocab-llama-spm.gguf"))
 
 
 if __name__ == "__main__":

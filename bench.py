@@ -369,7 +369,8 @@ def gemm_q6k_bench(be, torch, np):
 def prefill_layer_bench(be, torch, np, tokens=512):
     """The decode layer's 7 MUL_MAT nodes at `tokens` activation rows (a
     prefill step): q/k/v/o/gate/up on the Q4_K int8 GEMM, down on the Q6_K
-    f16 GEMM, one ghip_graph_compute call, each node reading its own input."""
+    f16 GEMM, one ghip_graph_compute call, each node reading its own input;
+    the weights registered as a loaded model's are."""
     import ghip
     g = torch.Generator(device="cuda").manual_seed(7)
     ws = {}
@@ -379,8 +380,12 @@ def prefill_layer_bench(be, torch, np, tokens=512):
         del wf
     xs = {nm: torch.randn((tokens, k), device="cuda", generator=g) for nm, k in INPUT_K.items()}
     outs = {name: torch.empty((tokens, n), dtype=torch.float32, device="cuda") for name, _, _, n in LAYER}
+    for name, ty, k, n in LAYER:  # as a loaded model: weights registered (Q6_K keeps its GEMM records)
+        be.register_weight(ws[name], ty, k)
     nodes = [ghip.mul_mat_node(ws[name], ty, k, xs[LAYER_INPUT[name]], outs[name]) for name, ty, k, n in LAYER]
     us = graph_time_us(torch, lambda i: be.graph_compute(nodes), 5)
+    for name, ty, k, n in LAYER:
+        be.unregister_weight(ws[name], ty, k)
     ops = sum(2.0 * tokens * k * n for _, _, k, n in LAYER)
     log(f"prefill layer ({tokens} tokens, 7 MUL_MATs): {us:.1f} us, {ops / us / 1e6:.1f} TOPS")
     del ws, xs, outs, nodes

@@ -366,6 +366,44 @@ def gemm_q6k_bench(be, torch, np):
                               "us_op_8col_decode_kernels": round(us_gemv, 2)}}
 
 
+def gemm_q8_family_bench(be, torch, np):
+    """Prefill of 32-element-block weights (Q4_0, Q8_0) at 512 tokens,
+    4096 -> 14336: the int8-MFMA GEMM, per-call repack and registered weight,
+    against the 8-column decode kernels it replaces."""
+    import ghip
+    res = {}
+    m, k, n = 512, 4096, 14336
+    g = torch.Generator(device="cuda").manual_seed(4)
+    for name, ty in (("q4_0", ghip.Q4_0), ("q8_0", ghip.Q8_0)):
+        if ty == ghip.Q4_0:
+            w = be.quantize(torch.randn((n, k), device="cuda", generator=g) * 0.02, ty)
+        else:  # no device Q8_0 quantizer: valid blocks of random codes with a fixed f16 scale
+            blk = torch.randint(-127, 128, (n, k // 32, 34), device="cuda", generator=g, dtype=torch.int32)
+            blk = blk.to(torch.int8).view(torch.uint8)
+            blk[:, :, 0:2] = torch.tensor([0x1A, 0x14], dtype=torch.uint8, device="cuda")  # f16 0.001
+            w = blk.reshape(n, -1).contiguous()
+        x = torch.randn((m, k), device="cuda", generator=g)
+        out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        us = graph_time_us(torch, lambda i: be.mul_mat(w, ty, k, x, out=out), 10)
+        be.register_weight(w, ty, k)
+        us_reg = graph_time_us(torch, lambda i: be.mul_mat(w, ty, k, x, out=out), 10)
+        be.unregister_weight(w, ty, k)
+        os.environ["GHIP_GEMM_Q8_MIN_ROWS"] = str(1 << 30)
+        try:
+            us_gemv = graph_time_us(torch, lambda i: be.mul_mat(w, ty, k, x, out=out), 2, reps=2)
+        finally:
+            del os.environ["GHIP_GEMM_Q8_MIN_ROWS"]
+        ops = 2.0 * m * n * k
+        res[f"{name} {m}x{k}->{n}"] = {"us_op": round(us, 2), "us_op_registered_weight": round(us_reg, 2),
+                                       "TOPS_op_registered_weight": round(ops / us_reg / 1e6, 1),
+                                       "frac_int8_peak": round(ops / us_reg / 1e6 / INT8_PEAK_TOPS, 4),
+                                       "us_op_8col_decode_kernels": round(us_gemv, 2)}
+        log(f"{name} GEMM {m}x{k}->{n}: op {us:.1f} us, registered {us_reg:.1f} us "
+            f"({ops / us_reg / 1e6:.1f} TOPS); 8-column decode kernels {us_gemv:.1f} us")
+        del w, x, out
+    return res
+
+
 def prefill_layer_bench(be, torch, np, tokens=512):
     """The decode layer's 7 MUL_MAT nodes at `tokens` activation rows (a
     prefill step): q/k/v/o/gate/up on the Q4_K int8 GEMM, down on the Q6_K
@@ -561,6 +599,7 @@ def main():
         extras["gemv_q5_0_q8_0_q5_K"] = more_types_bench(be, torch, np)
         extras["prefill_gemm_q4K"] = gemm_bench(be, torch, np)
         extras["prefill_gemm_q6K"] = gemm_q6k_bench(be, torch, np)
+        extras["prefill_gemm_q4_0_q8_0"] = gemm_q8_family_bench(be, torch, np)
         extras["prefill_layer_mul_mats"] = prefill_layer_bench(be, torch, np)
         extras["decode_layer_q4_0"] = q4_0_layer_bench(be, torch, np)
         extras["moe_mxfp4"] = moe_bench(be, torch, np)

@@ -254,9 +254,11 @@ ghip_status ghip_workspace_size(int op, const ghip_tensor *dst, const ghip_tenso
  * and keep device-side copies of it in the layouts the kernels read, built
  * once on `stream` now instead of on every call -- the reference's repack
  * cache (repack_*_cached, crates/ggml/src/repack.rs:4250-4480, and the
- * CPU_REPACK buffer it stands for).  Today that is the Q6_K prefill GEMM's
- * aligned 336-byte records; other types are read in their GGUF layout and
- * register as a no-op.  Later MUL_MAT calls whose src0 has the same data
+ * CPU_REPACK buffer it stands for).  Today those are the Q6_K prefill
+ * GEMM's aligned 336-byte records, the Q4_0 / Q5_0 / Q8_0 prefill GEMM's
+ * int8 code plane with its f32 block scales, and (3-D MXFP4 expert weights)
+ * the MUL_MAT_ID kernel's 80-byte windows; other types are read in their
+ * GGUF layout and register as a no-op.  Later MUL_MAT calls whose src0 has the same data
  * pointer, type, ne[0], ne[1] and nb[1] use the copy.  The same switches as
  * the reference: LLAMA_RUST_REPACK=0 turns it off, LLAMA_RUST_REPACK_MAX_MB
  * caps the bytes kept (default 16384); a weight over the cap is not kept and

@@ -448,7 +448,8 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
 // out for the GEMM (codes | bsum16 | d, tokens padded to 128), then the int8
 // MFMA GEMM runs on 128 x 128 tiles.
 constexpr size_t kGemmSmem128 = 116224, kGemmSmem64 = 76544;  // sizeof(g3::Smem<BM>) in ghip_gemm.hip
-constexpr size_t kGemmSmemQ6 = 152320;                         // sizeof(g6::Smem) in ghip_gemm.hip
+constexpr size_t kGemmSmemQ6 = 152320;
+constexpr size_t kGemmSmemQ8 = 55296;                          // sizeof(g8::Smem) in ghip_gemm.hip                         // sizeof(g6::Smem) in ghip_gemm.hip
 constexpr size_t kGemmSmemW8 = 148480;  // 2 * sizeof(g4::Stage<256>) in ghip_gemm.hip
 // GHIP_GEMM_BM=128 selects the 128 x 128 tiles of gemm_q4K_impl
 int gemm_bm() { return env_int("GHIP_GEMM_BM", 64) == 128 ? 128 : 64; }
@@ -496,7 +497,30 @@ size_t gemm_q6k_bytes(const MulMatPlan &p, size_t *codes_b, size_t *dt_b) {
     *dt_b = (nbk * Mpad * 4 + 255) & ~(size_t)255;
     return *codes_b + *dt_b + (size_t)p.N * nbk * kQ6R;
 }
+// Q4_0 / Q5_0 / Q8_0 prefill workspace: act codes [Mpad][Kpad] | da [nbp][Mpad] |
+// weight codes [Npad][Kpad] | dw [nbp][Npad] (K padded to 128, rows to 128)
+struct Q8Layout {
+    int64_t Mpad, Npad, Kpad, nbp;
+    size_t act_b, da_b, w_b, dw_b;
+};
+Q8Layout q8_layout(int64_t M, int64_t N, int64_t K) {
+    Q8Layout L;
+    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    L.Mpad = (M + 127) / 128 * 128;
+    L.Npad = (N + 127) / 128 * 128;
+    L.Kpad = (K + 127) / 128 * 128;
+    L.nbp = L.Kpad / 32;
+    L.act_b = up((size_t)L.Mpad * L.Kpad);
+    L.da_b = up((size_t)L.nbp * L.Mpad * 4);
+    L.w_b = up((size_t)L.Npad * L.Kpad);
+    L.dw_b = up((size_t)L.nbp * L.Npad * 4);
+    return L;
+}
 size_t gemm_layout_bytes(const MulMatPlan &p) {
+    if (gemv_pair(p.wtype)) {
+        const Q8Layout L = q8_layout(p.M, p.N, p.K);
+        return L.act_b + L.da_b + L.w_b + L.dw_b;
+    }
     if (p.wtype == GHIP_TYPE_Q6_K) {
         size_t a, b;
         return gemm_q6k_bytes(p, &a, &b);
@@ -549,11 +573,56 @@ ghip_status run_gemm_q6k(ghip_context *ctx, const MulMatPlan &p, const void *w, 
                        (int)Mpad, dst, ldd, sub);
 }
 
+const char *q8w_repack_name(int wtype) {
+    return wtype == GHIP_TYPE_Q4_0 ? "ghip_gemm_q8w_repack_q4_0"
+           : wtype == GHIP_TYPE_Q5_0 ? "ghip_gemm_q8w_repack_q5_0" : "ghip_gemm_q8w_repack_q8_0";
+}
+ghip_status q8w_repack(ghip_context *ctx, int wtype, const void *w, int64_t row_bytes, int64_t N, int64_t nb,
+                       const Q8Layout &L, int8_t *codes, float *dw, hipStream_t s) {
+    const int64_t n = L.Npad * L.nbp;
+    return ctx->launch(q8w_repack_name(wtype), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                       (const uint8_t *)w, row_bytes, (int)N, (int)nb, (int)L.Kpad, (int)L.Npad, codes, dw);
+}
+// Q4_0 / Q5_0 / Q8_0 from f32 rows: Q8_0 codes into the layout, the weights as
+// int8 codes (kept if registered), then the int8-MFMA GEMM on 64 x 128 tiles
+ghip_status run_gemm_q8(ghip_context *ctx, const MulMatPlan &p, const void *w, const ghip_tensor *bf, float *dst,
+                        int64_t ldd, int32_t *sub, void *layout_ws, hipStream_t s) {
+    const Q8Layout L = q8_layout(p.M, p.N, p.K);
+    uint8_t *base = (uint8_t *)layout_ws;
+    int8_t *ac = (int8_t *)base;
+    float *da = (float *)(base + L.act_b);
+    const int8_t *wc;
+    const float *dw;
+    auto it = ctx->wcache.find({w, p.wtype, p.K, p.N, 1, (uint64_t)p.w_row_bytes, 0});
+    ghip_status st;
+    if (it != ctx->wcache.end()) {
+        wc = (const int8_t *)it->second.p;
+        dw = (const float *)((const uint8_t *)it->second.p + L.w_b);
+    } else {
+        int8_t *c = (int8_t *)(base + L.act_b + L.da_b);
+        float *d = (float *)(base + L.act_b + L.da_b + L.w_b);
+        st = q8w_repack(ctx, p.wtype, w, p.w_row_bytes, p.N, p.nb, L, c, d, s);
+        if (st != GHIP_STATUS_SUCCESS) return st;
+        wc = c;
+        dw = d;
+    }
+    const int64_t ablocks = L.Mpad * L.nbp;
+    st = ctx->launch("ghip_gemm_act_q8_0", dim3((unsigned)((ablocks * 8 + 255) / 256)), dim3(256), 0, s,
+                     (const float *)bf->data, (int64_t)bf->nb[1] / 4, (int)p.M, (int)L.Mpad, (int)p.nb, (int)L.Kpad,
+                     ac, da);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    const unsigned grid = (unsigned)(((p.M + 63) / 64) * ((p.N + 127) / 128));
+    return ctx->launch(sub ? "ghip_gemm_q8_sub" : "ghip_gemm_q8", dim3(grid), dim3(256), kGemmSmemQ8, s, wc, dw,
+                       (int)p.N, (int)L.Npad, (int)p.nb, (int)L.Kpad, (const int8_t *)ac, (const float *)da, (int)p.M,
+                       (int)L.Mpad, dst, ldd, sub);
+}
+
 // act: Q8_K rows (bf == nullptr), or bf: the f32 activations, quantized
 // straight into the GEMM layout
 ghip_status run_gemm(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, const ghip_tensor *bf,
                      float *dst, int64_t ldd, int32_t *sub, void *layout_ws, hipStream_t s) {
     if (p.wtype == GHIP_TYPE_Q6_K) return run_gemm_q6k(ctx, p, w, act, bf, dst, ldd, sub, layout_ws, s);
+    if (gemv_pair(p.wtype)) return run_gemm_q8(ctx, p, w, bf, dst, ldd, sub, layout_ws, s);
     const int64_t Mpad = (p.M + 127) / 128 * 128, K = p.K, nbk = p.K / 256;
     int8_t *codes = (int8_t *)layout_ws;
     uint16_t *bsT = (uint16_t *)(codes + Mpad * K);
@@ -588,6 +657,8 @@ bool use_gemm(const MulMatPlan &p) {
     if (p.wtype == GHIP_TYPE_Q4_K) return p.M >= env_int("GHIP_GEMM_MIN_ROWS", 16);
     // Q6_K: the f16-MFMA GEMM from 64 activation rows (below, the 8-column decode kernels)
     if (p.wtype == GHIP_TYPE_Q6_K) return p.M >= env_int("GHIP_GEMM_Q6K_MIN_ROWS", 64) && p.K >= 512;
+    // Q4_0 / Q5_0 / Q8_0 from f32 activations: the int8-MFMA GEMM from 32 rows
+    if (gemv_pair(p.wtype)) return !p.act_pre && p.M >= env_int("GHIP_GEMM_Q8_MIN_ROWS", 32);
     return false;
 }
 
@@ -1365,13 +1436,22 @@ ghip_status ghip_weight_register(ghip_context *ctx, const ghip_tensor *w, void *
     if (!w || !w->data) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: null weight");
     if (w->ne[0] <= 0 || w->ne[1] <= 0 || w->ne[2] <= 0 || w->ne[3] != 1)
         return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: empty or 4-D weight");
-    const bool q6k = w->type == GHIP_TYPE_Q6_K, mx = w->type == GHIP_TYPE_MXFP4;
-    if (q6k && w->ne[2] != 1) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: Q6_K weights are 2-D");
+    const bool q6k = w->type == GHIP_TYPE_Q6_K, mx = w->type == GHIP_TYPE_MXFP4, q8 = gemv_pair(w->type);
+    if ((q6k || q8) && w->ne[2] != 1)
+        return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: Q6_K / Q4_0 / Q5_0 / Q8_0 weights are 2-D");
     // every other type is read in its GGUF layout: nothing to build
-    if (!(q6k || mx) || !repack_enabled()) return GHIP_STATUS_SUCCESS;
+    if (!(q6k || mx || q8) || !repack_enabled()) return GHIP_STATUS_SUCCESS;
     size_t bytes;
     int64_t nbk = 0, nrb = 0, ngp = 0;
-    if (q6k) {
+    Q8Layout QL{};
+    if (q8) {
+        const TypeInfo ti = type_info(w->type);
+        if (w->ne[0] % 32 || w->nb[0] != (uint64_t)ti.bytes || w->nb[1] < (uint64_t)(w->ne[0] / 32 * ti.bytes))
+            return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: bad block geometry");
+        if (w->ne[1] > INT32_MAX) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: dimension too large");
+        QL = q8_layout(1, w->ne[1], w->ne[0]);
+        bytes = QL.w_b + QL.dw_b;
+    } else if (q6k) {
         if (w->ne[0] % 256 || w->nb[0] != 210 || w->nb[1] < (uint64_t)(w->ne[0] / 256 * 210))
             return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: bad Q6_K geometry");
         if (w->ne[1] > INT32_MAX || w->ne[0] / 256 > INT32_MAX)
@@ -1402,7 +1482,10 @@ ghip_status ghip_weight_register(ghip_context *ctx, const ghip_tensor *w, void *
         (void)hipGetLastError();
         return ctx->fail(GHIP_STATUS_OUT_OF_MEMORY, "weight_register: hipMalloc(%zu) failed", bytes);
     }
-    if (q6k) {
+    if (q8) {
+        st = q8w_repack(ctx, w->type, w->data, (int64_t)w->nb[1], w->ne[1], w->ne[0] / 32, QL, (int8_t *)rep,
+                        (float *)((uint8_t *)rep + QL.w_b), s);
+    } else if (q6k) {
         st = q6k_repack(ctx, w->data, (int64_t)w->nb[1], w->ne[1], nbk, (uint8_t *)rep, s);
     } else {
         const int64_t chunks = (int64_t)(bytes / 16);

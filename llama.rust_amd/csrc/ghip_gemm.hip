@@ -873,3 +873,219 @@ ghip_gemm_act_q8K_f16(const float *__restrict__ x, int64_t x_stride, int M, int 
                       _Float16 *__restrict__ codes, float *__restrict__ dT) {
     act_q8K_layout<true>(x, x_stride, M, Mpad, nb, n_mat, codes, nullptr, dT);
 }
+
+// ------------------------------------------------- Q4_0 / Q5_0 / Q8_0 prefill
+// Many activation rows with 32-element-block weights (vec_dot_q4_0_q8_0,
+// vec_dot_q5_0_q8_0, vec_dot_q8_0_q8_0, vec_dot.rs:596-700: per block
+// dot = sum_32 w * q8 exact, out += (d_w * d_a) * dot).  The weight values
+// (q - 8, q - 16, or the Q8_0 codes) are int8, so one v_mfma_i32_32x32x32_i8
+// per 32-block gives the exact integer dot of a 32 x 32 tile; the fold is one
+// fma per output and block.  Both operands are staged as int8 codes with
+// f32 block scales (weights by ghip_gemm_q8w_repack, per call or once for a
+// registered weight; activations by ghip_gemm_act_q8_0 with the arithmetic of
+// quantize_row_q8_0), K padded to a multiple of 128 with zeros.
+
+// one thread per (row, block): the 32 values as int8 at codes[row][32b..],
+// the block scale at dw[b][row] (Npad rows)
+template <int TYPE>  // 2 Q4_0, 6 Q5_0, 8 Q8_0
+__device__ __forceinline__ void q8w_repack(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int nb,
+                                           int Kpad, int Npad, int8_t *__restrict__ codes, float *__restrict__ dw) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int nbp = Kpad / 32;
+    if (i >= (int64_t)Npad * nbp) return;
+    const int row = (int)(i / nbp), b = (int)(i % nbp);
+    uint32_t v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float d = 0.0f;
+    if (row < N && b < nb) {
+        constexpr int BB = TYPE == 2 ? 18 : TYPE == 6 ? 22 : 34;
+        const uint8_t *blk = W + (int64_t)row * row_bytes + (int64_t)b * BB;
+        d = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+        if constexpr (TYPE == 8) {
+#pragma unroll
+            for (int k = 0; k < 32; k++) v[k >> 2] |= (uint32_t)blk[2 + k] << (8 * (k & 3));
+        } else {
+            const uint8_t *qs = blk + (TYPE == 6 ? 6 : 2);
+            const uint32_t qh = TYPE == 6 ? ((uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) |
+                                             ((uint32_t)blk[5] << 24))
+                                          : 0u;
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                int lo = qs[j] & 15, hi = qs[j] >> 4;
+                if (TYPE == 6) {
+                    lo |= (int)((qh >> j) & 1) << 4;
+                    hi |= (int)((qh >> (j + 16)) & 1) << 4;
+                }
+                const int off = TYPE == 6 ? 16 : 8;
+                v[j >> 2] |= (uint32_t)((lo - off) & 0xff) << (8 * (j & 3));
+                v[(j + 16) >> 2] |= (uint32_t)((hi - off) & 0xff) << (8 * ((j + 16) & 3));
+            }
+        }
+    }
+    uint4 *o = reinterpret_cast<uint4 *>(codes + (int64_t)row * Kpad + 32 * b);
+    o[0] = make_uint4(v[0], v[1], v[2], v[3]);
+    o[1] = make_uint4(v[4], v[5], v[6], v[7]);
+    dw[(int64_t)b * Npad + row] = d;
+}
+#define Q8W_REPACK(TN, TYPE)                                                                                       \
+    extern "C" __global__ void __launch_bounds__(256)                                                              \
+        ghip_gemm_q8w_repack_##TN(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int nb, int Kpad,       \
+                                  int Npad, int8_t *__restrict__ codes, float *__restrict__ dw) {                  \
+        q8w_repack<TYPE>(W, row_bytes, N, nb, Kpad, Npad, codes, dw);                                              \
+    }
+Q8W_REPACK(q4_0, 2)
+Q8W_REPACK(q5_0, 6)
+Q8W_REPACK(q8_0, 8)
+
+// f32 rows -> Q8_0 codes [Mpad][Kpad] int8 and da [nbp][Mpad] f32 (the stored
+// f16 scale), the arithmetic of ghip_quantize_q8_0 (quantize_row_q8_0,
+// quants.rs:153-180); 8 lanes per block, padding rows and blocks zero
+extern "C" __global__ void __launch_bounds__(256)
+ghip_gemm_act_q8_0(const float *__restrict__ x, int64_t x_stride, int M, int Mpad, int nb, int Kpad,
+                   int8_t *__restrict__ codes, float *__restrict__ da) {
+    const int lane = threadIdx.x & 63, sub = lane & 7;
+    const int nbp = Kpad / 32;
+    const int64_t blk_id = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;
+    if (blk_id >= (int64_t)Mpad * nbp) return;  // whole 8-lane groups exit together
+    const int row = (int)(blk_id / nbp), b = (int)(blk_id % nbp);
+    const bool live = row < M && b < nb;
+    float xs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (live) __builtin_memcpy(xs, x + (int64_t)row * x_stride + (int64_t)b * 32 + sub * 4, 16);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) amax = fmaxf(amax, fabsf(xs[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    const float d = __fdiv_rn(amax, 127.0f);
+    const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float r = rintf(__fmul_rn(xs[i], id));
+        const int v = (r != r || fabsf(r) >= 2147483648.0f) ? -128 : (int)r;
+        packed |= (uint32_t)(v & 0xff) << (8 * i);
+    }
+    *reinterpret_cast<uint32_t *>(codes + (int64_t)row * Kpad + 32 * b + 4 * sub) = packed;
+    if (sub == 0) da[(int64_t)b * Mpad + row] = h2f(f2h_rn(d));
+}
+
+namespace g8 {
+constexpr int BM = 64, BN = 128, GB = 4;  // tokens, rows, 32-blocks per stage
+struct Smem {
+    int8_t act[2][BM * GB * 32];   // [stage][token][128 B], 16-byte slots swizzled by token % 8
+    int8_t w[2][BN * GB * 32];     // [stage][row][128 B], swizzled by row % 8
+    float da[2][GB][BM];
+    float dw[2][GB][BN];
+};
+}  // namespace g8
+
+// 64 tokens x 128 rows per 256-thread workgroup; wavefront w owns rows
+// 32w .. 32w+31 and both 32-token tiles.  C[token][row]: lane l holds row
+// l % 32 and tokens crow(v, l).  Operands: lane l takes K 16(l/32) .. +15 of
+// the block (A: token l % 32 of the tile, B: row l % 32).
+template <bool SUBSUMS>
+__device__ __forceinline__ void gemm_q8_impl(const int8_t *__restrict__ wc, const float *__restrict__ dw, int N,
+                                             int Npad, int nb, int Kpad, const int8_t *__restrict__ ac,
+                                             const float *__restrict__ da, int M, int Mpad, float *__restrict__ dst,
+                                             int64_t ldd, int32_t *__restrict__ sub) {
+    constexpr int BM = g8::BM, BN = g8::BN, GB = g8::GB;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
+    g8::Smem &SM = *reinterpret_cast<g8::Smem *>(smem_raw);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane & 31, h = lane >> 5;
+    const int n_tiles_m = (M + BM - 1) / BM, n_tiles_n = (N + BN - 1) / BN;
+    const int total = n_tiles_m * n_tiles_n;
+    int id = blockIdx.x;
+    if (total % 8 == 0) id = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+    const int m0 = (id % n_tiles_m) * BM, n0 = (id / n_tiles_m) * BN;
+    const int ng = Kpad / (32 * GB);
+
+    // group g into stage p: 2 act chunks, 4 weight chunks, (waves 0-1) the scales
+    auto issue = [&](int g, int p) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int c = 64 * (2 * wave + i) + lane;  // LDS chunk: token c / 8, slot c % 8
+            const int t = c >> 3, src = (c & 7) ^ (t & 7);
+            g2lds(ac + (int64_t)(m0 + t) * Kpad + (int64_t)g * 128 + 16 * src,
+                  SM.act[p] + 1024 * (2 * wave + i));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int c = 64 * (4 * wave + i) + lane;
+            const int r = c >> 3, src = (c & 7) ^ (r & 7);
+            g2lds(wc + (int64_t)min(n0 + r, Npad - 1) * Kpad + (int64_t)g * 128 + 16 * src,
+                  SM.w[p] + 1024 * (4 * wave + i));
+        }
+        if (wave == 0) {  // da: 4 blocks x 64 tokens = 64 chunks
+            const int kb = lane >> 4;
+            g2lds(da + (int64_t)(g * GB + kb) * Mpad + m0 + 4 * (lane & 15), &SM.da[p][0][0]);
+        } else if (wave == 1) {  // dw: 4 blocks x 128 rows = 128 chunks, two per lane
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int c = 64 * i + lane, kb = c >> 5;
+                g2lds(dw + (int64_t)(g * GB + kb) * Npad + min(n0 + 4 * (c & 31), Npad - 4),
+                      reinterpret_cast<uint8_t *>(&SM.dw[p][0][0]) + 1024 * i);
+            }
+        }
+    };
+
+    v16f out[2];
+#pragma unroll
+    for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) out[tm][v] = 0.0f;
+    const int wr = 32 * wave + li;  // this lane's weight row in the tile
+    issue(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int g = 0; g < ng; g++) {
+        const int p = g & 1;
+        if (g + 1 < ng) issue(g + 1, p ^ 1);
+#pragma unroll
+        for (int kb = 0; kb < GB; kb++) {
+            const int slot = 2 * kb + h;  // this lane's 16 bytes of block kb
+            const v4i bw = *reinterpret_cast<const v4i *>(SM.w[p] + wr * 128 + 16 * (slot ^ (wr & 7)));
+            const float sw = SM.dw[p][kb][wr];
+            const int b = g * GB + kb;
+#pragma unroll
+            for (int tm = 0; tm < 2; tm++) {
+                const int ta = 32 * tm + li;
+                const v4i a = *reinterpret_cast<const v4i *>(SM.act[p] + ta * 128 + 16 * (slot ^ (ta & 7)));
+                const v16i zi = {};
+                const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bw, zi, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const int tl = 32 * tm + crow(v, lane);
+                    out[tm][v] = fmaf(sw * SM.da[p][kb][tl], (float)c[v], out[tm][v]);
+                    if constexpr (SUBSUMS)
+                        if (b < nb && m0 + tl < M && n0 + wr < N)
+                            sub[((int64_t)(m0 + tl) * N + (n0 + wr)) * nb + b] = c[v];
+                }
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+    const int n = n0 + wr;
+#pragma unroll
+    for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int m = m0 + 32 * tm + crow(v, lane);
+            if (m < M && n < N) dst[(int64_t)m * ldd + n] = out[tm][v];
+        }
+}
+extern "C" __global__ void __launch_bounds__(256)
+    ghip_gemm_q8(const int8_t *__restrict__ wc, const float *__restrict__ dw, int N, int Npad, int nb, int Kpad,
+                 const int8_t *__restrict__ ac, const float *__restrict__ da, int M, int Mpad,
+                 float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
+    gemm_q8_impl<false>(wc, dw, N, Npad, nb, Kpad, ac, da, M, Mpad, dst, ldd, sub);
+}
+extern "C" __global__ void __launch_bounds__(256)
+    ghip_gemm_q8_sub(const int8_t *__restrict__ wc, const float *__restrict__ dw, int N, int Npad, int nb,
+                     int Kpad, const int8_t *__restrict__ ac, const float *__restrict__ da, int M, int Mpad,
+                     float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
+    gemm_q8_impl<true>(wc, dw, N, Npad, nb, Kpad, ac, da, M, Mpad, dst, ldd, sub);
+}
+static_assert(sizeof(g8::Smem) == 55296, "host code launches with this LDS size");

@@ -237,3 +237,25 @@ def test_gemm_q4K_rows_not_multiple_of_8(be, n, rows, cols):
     sub = be.mul_mat_subsums(torch.from_numpy(w4).cuda(), O.Q4_K, n, xd).cpu().numpy()
     _, _, want_sub = O.mul_mat(O.Q4_K, w4, n, 4, x, cols, want_subsums=True)
     assert np.array_equal(sub, want_sub)
+
+
+@pytest.mark.parametrize("ty", [O.Q4_0, O.Q5_0, O.Q8_0])
+@pytest.mark.parametrize("n,rows,cols", [(256, 64, 32), (1024, 200, 100), (2880, 136, 130), (4096, 256, 64)])
+def test_gemm_q8_family(be, ty, n, rows, cols):
+    """Q4_0 / Q5_0 / Q8_0 with >= 32 f32 activation rows take the int8-MFMA
+    GEMM (one exact 32-block dot per MFMA); K not a multiple of 128 (2880)
+    pads with zeros; int32 block dots bit-exact."""
+    run_case(be, ty, n, rows, cols, seed=rows + cols + ty)
+
+
+def test_gemm_q8_family_registered(be):
+    """A registered Q4_0 weight (its int8 codes kept on the device) gives the
+    same bits as the per-call repack."""
+    n, rows, cols = 4096, 512, 96
+    w, x = make(O.Q4_0, n, rows, cols, seed=9)
+    wd, xd = torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda()
+    print(f"gemm q8 registered n={n} rows={rows} cols={cols}", flush=True)
+    before = be.mul_mat(wd, O.Q4_0, n, xd).clone()
+    be.register_weight(wd, O.Q4_0, n)
+    assert torch.equal(be.mul_mat(wd, O.Q4_0, n, xd), before)
+    be.unregister_weight(wd, O.Q4_0, n)

@@ -262,6 +262,15 @@ def _profile_ops(be, torch, np, what):
         x = torch.randn((m, k), device="cuda", generator=g)
         out = torch.empty((m, n), dtype=torch.float32, device="cuda")
         return lambda i: be.mul_mat(ws[i % copies], ty, k, x, out=out)
+    if what in ("layer_b1", "layer_b8"):
+        batch = 1 if what == "layer_b1" else 8
+        sets = make_weights(be, torch, np, copies=4)
+        xr = np.random.default_rng(1)
+        xs = {nm: torch.from_numpy(xr.standard_normal((batch, k), dtype=np.float32)).cuda() for nm, k in INPUT_K.items()}
+        outs = {name: torch.empty((batch, n), dtype=torch.float32, device="cuda") for name, _, _, n in LAYER}
+        nodes = [[ghip.mul_mat_node(w, ty, k, xs[LAYER_INPUT[name]], outs[name])
+                  for (name, ty, k, n), w in zip(LAYER, ws)] for ws in sets]
+        return lambda i: be.graph_compute(nodes[i % len(nodes)])
     if what == "moe":
         n_as, n_tok, n_ids, k, rows = 32, 256, 4, 2880, 5760
         rng = np.random.default_rng(3)
@@ -287,7 +296,8 @@ def _profile_ops(be, torch, np, what):
     raise ValueError(what)
 
 
-PROFILE_WORKLOADS = ["gemv", "copy", "gemm", "gemm_q6k", "decode_b8", "moe", "fa_decode", "fa_prefill"]
+PROFILE_WORKLOADS = ["gemv", "copy", "gemm", "gemm_q6k", "decode_b8", "layer_b1", "layer_b8", "moe", "fa_decode",
+                     "fa_prefill"]
 
 
 def profile_loop(what, n):
@@ -296,7 +306,8 @@ def profile_loop(what, n):
     WRITE_SIZE.  gemv: Q4_K 4096->14336 at batch 1 over 16 weight copies;
     copy: 33,030,144-byte device copies; gemm: Q4_K 512x4096->14336;
     gemm_q6k: Q6_K 512x14336->4096; decode_b8: Q4_K 4096->14336 at 8 rows over
-    16 copies; moe: MXFP4 gate_up (32 experts, 256 tokens, top-4);
+    16 copies; layer_b1 / layer_b8: the decode layer's 7 MUL_MATs in one
+    graph_compute call at batch 1 / 8 over 4 weight copies; moe: MXFP4 gate_up (32 experts, 256 tokens, top-4);
     fa_decode / fa_prefill: FLASH_ATTN_EXT 32/8 heads, D 128, KV 8192, T 1 / 512."""
     import numpy as np
     import torch

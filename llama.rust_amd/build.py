@@ -40,6 +40,7 @@ EXTRA_FLAGS = {
     "ghip_moe": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "ghip_fa": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "ghip_gemm": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "ghip_skinny": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

@@ -381,6 +381,89 @@ ghip_status run_skinny(ghip_context *ctx, const MulMatPlan &p, const void *w, co
                        (int)p.nb, act, act_rb, (int)p.M, dst, ldd, sub, n_mat);
 }
 
+// Split-K decode (ghip_skinny.hip ghip_sk_*): Q4_K and Q6_K at 4..8 f32
+// activation rows.  K-slices of S super-blocks (S from K alone: 4 up to 24
+// super-blocks, else 8) x 64-row tiles; each workgroup quantizes its slice of
+// the activations once (no quantize launch) and walks a set of tiles with
+// the next step's weights in flight; ghip_sk_reduce adds the slices'
+// partials in order.  GHIP_SK_WGS sets the workgroups aimed for (768: three
+// per CU).
+constexpr int kSkRows = 64;
+int sk_sb(int64_t nb) { return nb <= 24 ? 4 : 8; }
+int64_t sk_slices(int64_t nb) { return (nb + sk_sb(nb) - 1) / sk_sb(nb); }
+int64_t sk_tiles(int64_t N) { return (N + kSkRows - 1) / kSkRows; }
+// Q4_K below GHIP_SK_MIN_ROWS (8192) weight rows keeps the whole-K kernel
+// (ghip_mma_q4_K_*) after one quantize launch: there the split kernel plus its
+// reduction measured slower (q/k/v 14.3 -> 17.6 us, o 14.4 -> 14.6 us;
+// gate/up 33.9 -> 29.1 us and Q6_K down 35.5 -> 28.1 us, both with the
+// reduction).  sk_rows_ok is the row test alone (graph grouping keeps it
+// equal within a group).
+bool sk_rows_ok(int wtype, int64_t N) { return wtype == GHIP_TYPE_Q6_K || N >= env_int("GHIP_SK_MIN_ROWS", 8192); }
+bool use_sk(const MulMatPlan &p) {
+    if (p.act_pre || env_int("GHIP_SK", 1) == 0 || p.M < env_int("GHIP_MMA_MIN_ROWS", 4)) return false;
+    return (p.wtype == GHIP_TYPE_Q4_K || p.wtype == GHIP_TYPE_Q6_K) && p.M <= 8 && sk_rows_ok(p.wtype, p.N);
+}
+size_t sk_part_bytes(const MulMatPlan &p) {
+    const int64_t ns = sk_slices(p.nb);
+    return ns > 1 ? (((size_t)ns * (size_t)p.M * (size_t)p.N * 4 + 255) & ~(size_t)255) : 0;
+}
+// Host mirror of SkMember / SkLaunch in ghip_skinny.hip.
+struct SkMember {
+    const uint8_t *W;
+    float *dst;
+    int64_t ldd;
+    float *part;
+    int rows;
+    int tile0;
+};
+struct SkLaunch {
+    SkMember m[4];
+    int n, n_tiles, nks, tg;
+};
+// g: members' W, dst, ldd, rows and part filled in; launches the kernel and
+// (more than one K-slice) the in-order reduction
+ghip_status launch_sk(ghip_context *ctx, const MulMatPlan &p, SkLaunch &g, const ghip_tensor *x, int32_t *sub,
+                      hipStream_t s) {
+    const int64_t ns = sk_slices(p.nb);
+    int64_t tiles = 0, rows = 0;
+    SkLaunch r = g;  // the reduction's view: tile0 = first row
+    for (int i = 0; i < 4; i++) {
+        if (i >= g.n) g.m[i] = g.m[0], r.m[i] = r.m[0];
+        g.m[i].tile0 = (int)tiles;
+        r.m[i].tile0 = (int)rows;
+        if (i < g.n) {
+            tiles += sk_tiles(g.m[i].rows);
+            rows += g.m[i].rows;
+        }
+    }
+    if (rows * p.M > INT32_MAX || tiles * ns > INT32_MAX)
+        return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: matrix too large for the split-K decode kernel");
+    const int64_t want = std::max(1, env_int("GHIP_SK_WGS", 768));
+    g.n_tiles = (int)tiles;
+    g.nks = (int)ns;
+    g.tg = (int)std::max<int64_t>(1, std::min<int64_t>(tiles, (want + ns - 1) / ns));
+    r.nks = g.nks;
+    const int n_mat = (int)std::max<int64_t>(0, std::min<int64_t>(p.M, p.n_mat));
+    const std::string name = std::string("ghip_sk_") + (p.wtype == GHIP_TYPE_Q4_K ? "q4_K" : "q6_K") +
+                             (sub ? "_sub" : "") + "_s" + std::to_string(sk_sb(p.nb));
+    ghip_status st = ctx->launch(name, dim3((unsigned)(ns * g.tg)), dim3(256), 0, s, g, (int64_t)p.w_row_bytes,
+                                 (int)p.nb, (const float *)x->data, (int64_t)x->nb[1] / 4, (int)p.M, n_mat, sub);
+    if (st != GHIP_STATUS_SUCCESS || ns == 1) return st;
+    const int64_t total = rows * p.M;
+    return ctx->launch("ghip_sk_reduce", dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, r, (int)p.M, total);
+}
+ghip_status run_sk(ghip_context *ctx, const MulMatPlan &p, const void *w, const ghip_tensor *x, float *dst,
+                   int64_t ldd, int32_t *sub, void *part, hipStream_t s) {
+    SkLaunch g{};
+    g.n = 1;
+    g.m[0].W = (const uint8_t *)w;
+    g.m[0].dst = dst;
+    g.m[0].ldd = ldd;
+    g.m[0].part = (float *)part;
+    g.m[0].rows = (int)p.N;
+    return launch_sk(ctx, p, g, x, sub, s);
+}
+
 // Decode path: activation columns in groups of at most 8.  Q4_K reads the f32
 // activations and quantizes them inside the kernel when fused is set.
 ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, int64_t act_rb,
@@ -667,8 +750,10 @@ bool use_gemm(const MulMatPlan &p) {
 size_t mul_mat_ws_bytes(const MulMatPlan &p, bool has_dst, bool act_out, size_t *act_b, size_t *lay_b) {
     // (the GEMM quantizes f32 activations straight into its layout)
     const bool gemm = !act_out && use_gemm(p);
-    const size_t act_bytes = p.act_pre || gemm ? 0 : ((size_t)(p.M * p.act_row_bytes) + 255) & ~(size_t)255;
-    const size_t lay_bytes = gemm ? gemm_layout_bytes(p) : 0;
+    // (the split-K decode kernels quantize inside; their layout is the partials)
+    const bool sk = !act_out && !gemm && use_sk(p);
+    const size_t act_bytes = p.act_pre || gemm || sk ? 0 : ((size_t)(p.M * p.act_row_bytes) + 255) & ~(size_t)255;
+    const size_t lay_bytes = gemm ? gemm_layout_bytes(p) : sk ? sk_part_bytes(p) : 0;
     if (act_b) *act_b = act_bytes;
     if (lay_b) *lay_b = lay_bytes;
     return (act_out ? 0 : act_bytes) + lay_bytes + (has_dst || act_out ? 0 : (size_t)(p.M * p.N * 4));
@@ -709,6 +794,7 @@ ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_ten
     const int64_t ldd = d ? (int64_t)d->nb[1] / 4 : p.N;
     if (use_gemm(p))
         return run_gemm(ctx, p, a->data, (const uint8_t *)b->data, p.act_pre ? nullptr : b, dst, ldd, sub, lay, s);
+    if (use_sk(p)) return run_sk(ctx, p, a->data, b, dst, ldd, sub, lay, s);
     if (p.act_pre) return run_gemv(ctx, p, a->data, (const uint8_t *)b->data, p.act_row_bytes, false, dst, ldd, sub, s);
     // Q8_0 quantization fused into the block-pair kernels for up to 4096 weight
     // rows: every workgroup then quantizes its lanes' blocks itself, which
@@ -1058,6 +1144,9 @@ bool joins_group(const ghip_node *nodes, int i, int j) {
     // N % 8 == 0 (compute.rs:5350-5398): one quantization per group
     if (c.src[0]->type == GHIP_TYPE_Q4_K && c.src[1]->ne[1] >= 4 && (c.src[0]->ne[1] % 8 == 0) != (h.src[0]->ne[1] % 8 == 0))
         return false;
+    // the split-K and whole-K decode kernels sum differently: one kernel per group
+    if (c.src[0]->type == GHIP_TYPE_Q4_K && sk_rows_ok(GHIP_TYPE_Q4_K, c.src[0]->ne[1]) != sk_rows_ok(GHIP_TYPE_Q4_K, h.src[0]->ne[1]))
+        return false;
     for (int k = i; k < j; k++) {
         const ghip_node &o = nodes[k];
         if (overlaps(o.dst, c.src[0]) || overlaps(o.dst, c.src[1]) || overlaps(c.dst, o.src[0]) ||
@@ -1176,6 +1265,29 @@ ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipS
         return ctx->launch(std::string(gemv_base(p0.wtype)) + "_c" + std::to_string(NC) + "_multi", dim3((unsigned)wgs),
                            dim3(64 * wk), 0, s, g, (int64_t)p0.w_row_bytes, (int)p0.nb, (const uint8_t *)ws,
                            (int64_t)p0.act_row_bytes, nc);
+    }
+    if (use_sk(p0)) {
+        // split-K decode over all members; partials of member i after member i-1's
+        size_t off[4] = {0, 0, 0, 0}, total = 0;
+        for (int i = 0; i < n; i++) {
+            off[i] = total;
+            total += sk_part_bytes(p[i]);
+        }
+        void *ws = nullptr;
+        if (total) {
+            st = ctx->workspace(total, s, &ws);
+            if (st != GHIP_STATUS_SUCCESS) return st;
+        }
+        SkLaunch g{};
+        g.n = n;
+        for (int i = 0; i < n; i++) {
+            g.m[i].W = (const uint8_t *)nodes[i].src[0]->data;
+            g.m[i].dst = (float *)nodes[i].dst->data;
+            g.m[i].ldd = (int64_t)nodes[i].dst->nb[1] / 4;
+            g.m[i].part = ws ? (float *)((uint8_t *)ws + off[i]) : nullptr;
+            g.m[i].rows = (int)p[i].N;
+        }
+        return launch_sk(ctx, p0, g, nodes[0].src[1], nullptr, s);
     }
     if (use_skinny(p0)) {
         // Q4_K at 4..15 rows: the activation rows quantized once, then the

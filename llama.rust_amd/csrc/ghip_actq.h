@@ -30,7 +30,10 @@ DEV XTask quant_q8K_load(const float *__restrict__ x, int64_t x_stride, int ncol
     return t;
 }
 
-DEV void quant_q8K_store(const XTask &t, int nb, int n_mat, int total, int task, int8_t *codes, float *dq, int *bsum) {
+// cstride / bstride: the image's per-token strides of codes (bytes) and
+// 16-element sums (ints); -1: nb * 256 and nb * 16 (packed)
+DEV void quant_q8K_store(const XTask &t, int nb, int n_mat, int total, int task, int8_t *codes, float *dq, int *bsum,
+                         int cstride = -1, int bstride = -1) {
     const float *v = t.v;
     const bool live = task < total;
     const int l = task & 15, blk = task >> 4;
@@ -75,8 +78,9 @@ DEV void quant_q8K_store(const XTask &t, int nb, int n_mat, int total, int task,
         sum += q[4 * k] + q[4 * k + 1] + q[4 * k + 2] + q[4 * k + 3];
     }
     if (live) {
-        *reinterpret_cast<uint4 *>(codes + (int64_t)c * nb * QK_K + b * QK_K + 16 * l) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        bsum[(c * nb + b) * 16 + l] = sum;  // bsums[l] of block_q8_K
+        const int cs = cstride < 0 ? nb * QK_K : cstride, bst = bstride < 0 ? nb * 16 : bstride;
+        *reinterpret_cast<uint4 *>(codes + (int64_t)c * cs + b * QK_K + 16 * l) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        bsum[c * bst + b * 16 + l] = sum;  // bsums[l] of block_q8_K
         if (l == 0) dq[c * nb + b] = d;
     }
 }

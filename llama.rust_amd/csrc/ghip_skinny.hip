@@ -238,3 +238,321 @@ struct SkinnyMulti {
                                                      g.dst[i], g.ldd[i], nullptr, n_mat, bx - g.wg0[i]);             \
     }
 SKINNY_MULTI(4, 2, 4) SKINNY_MULTI(8, 2, 4) SKINNY_MULTI(16, 2, 4)
+
+// ===================================================================== split K
+// Decode MUL_MAT at 4..8 activation rows (Q4_K, Q6_K), split over K across
+// workgroups.  The K axis is cut into slices of S super-blocks (S depends on
+// K only, so a matrix gives the same bits alone and in a grouped launch).  A
+// workgroup of 4 wavefronts owns one slice and a set of 64-row tiles:
+//  - it quantizes its slice of the f32 activation rows to Q8_K in LDS once
+//    (quant_q8K_*, bit-identical to ghip_quantize_q8_K; Q8_K blocks do not
+//    cross super-blocks), so no separate quantization launch is needed;
+//  - it walks its tiles in steps of 2 super-blocks x 16 rows per wavefront,
+//    the next step's weights loaded into registers while the current one
+//    runs on the int8 matrix cores.
+// Each slice's fp32 partials go to a workspace and ghip_sk_reduce adds them
+// in slice order.  (Handing the sum to each tile's last workgroup through a
+// counter measured 8-9 us slower on the Llama-3-8B decode layer: every
+// workgroup then waits for its partials to reach memory and for the
+// counter's round trip.)
+//
+// Both types put the sub-block in the token dimension of the MFMA: its 16 A
+// rows are (token t, parity h) pairs, row 2t+h holding token t's codes at the
+// K positions of the step's sub-block h and zeros elsewhere, so C[2t+h][row]
+// is the exact integer dot of one sub-block.  Weight codes enter unsigned.
+//
+// Q4_K (vec_dot_q4_K_q8_K, vec_dot.rs:928-980): v_mfma_i32_16x16x64_i8 per
+// 64-element chunk c (sub-blocks 2c: low nibbles of qs 32c..32c+31, 2c+1: high
+// nibbles).  Lane group G takes qs 32c + 8G .. +7: its 16 K positions are the
+// 8 low nibbles (elements 64c + 8G + i) then the 8 high nibbles (elements
+// 64c + 32 + 8G + i).  iacc = sum_s sc[s] C_s; the min term
+// sum_s m[s] bsum32[t][s] is one exact f16 MFMA over the 16-element sums.
+//
+// Q6_K (vec_dot_q6_K_q8_K, vec_dot.rs:1010-1060): v_mfma_i32_16x16x32_i8 per
+// 32-element chunk (n, q), elements 128n + 32q + l, l = 0..31 (sub-blocks
+// 8n + 2q and 8n + 2q + 1), code
+//   (ql[64n + 32(q&1) + l] >> 4(q>>1)) & 15  |  ((qh[32n + l] >> 2q) & 3) << 4
+// (dequantize_row_q6_K's element order, quants_k.rs:2096-2115); lane group G
+// takes l = 8G .. 8G+7.  The -32 offset is -32 * sum_s sc[s] * bsum16[t][s],
+// one exact f16 MFMA per super-block (|sc| <= 128, |bsum16| <= 2032, sums
+// < 2^24).
+constexpr int SK_WAVES = 4;
+constexpr int SK_ROWS = 16 * SK_WAVES;  // weight rows per tile
+
+struct SkMember {
+    const uint8_t *W;
+    float *dst;
+    int64_t ldd;
+    float *part;  // [slices][ncols][rows] fp32 partials (more than one slice)
+    int rows;
+    int tile0;    // first tile of this matrix in the launch
+};
+struct SkLaunch {
+    SkMember m[4];
+    int n;        // matrices
+    int n_tiles;  // tiles over all matrices
+    int nks;      // K-slices
+    int tg;       // tile groups: workgroup bx takes slice bx % nks, tiles bx / nks + k * tg
+};
+
+typedef int v2i __attribute__((ext_vector_type(2)));
+
+template <int WT, int S, int SK_GB, bool SUBSUMS>
+__device__ __forceinline__ void sk_impl(const SkLaunch &g, int64_t w_row_bytes, int nb, const float *__restrict__ x,
+                                        int64_t x_stride, int ncols, int n_mat, int32_t *__restrict__ sub) {
+    static_assert(WT == 12 || WT == 14, "Q4_K or Q6_K");
+    static_assert(S % SK_GB == 0, "whole pipeline steps per slice");
+    constexpr int NC = 8;  // 16 A rows: 8 tokens x 2 sub-block parities
+    constexpr int BB = WT == 12 ? Q4K_BYTES : Q6K_BYTES;
+    // dwords of weight data per lane and super-block:
+    // Q4_K: header (d, dmin, 12 scale bytes) | qs 32c + 8G .. +7 for c = 0..3
+    // Q6_K: ql 32k + 8G .. +7 (k = 0..3) | qh 32k + 8G .. +7 (k = 0, 1) | scales 4G .. 4G+3 | d
+    constexpr int NW = WT == 12 ? 12 : 14;
+    // image strides per token padded by 16 bytes / 4 ints, so the 8 tokens'
+    // operand reads fall in different LDS banks
+    constexpr int CS = S * QK_K + 16, BS = S * 16 + 4;
+    __shared__ __attribute__((aligned(16))) int8_t codes[NC * CS];
+    __shared__ float dq[NC * S];
+    __shared__ int bsum[NC * BS];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j = lane & 15, G = lane >> 4;
+    const int ks = (int)blockIdx.x % g.nks, tgi = (int)blockIdx.x / g.nks;
+    const int b0 = ks * S, nbs = min(S, nb - b0);
+    const int ngrp = (nbs + SK_GB - 1) / SK_GB;
+    const int my_tiles = tgi < g.n_tiles ? (g.n_tiles - tgi + g.tg - 1) / g.tg : 0;
+    const int items = my_tiles * ngrp;
+
+    // ---- activation slice: the first round's loads go out before any weight
+    // load, so the quantization waits only for them
+    const float *xs = x + (int64_t)b0 * QK_K;
+    const int total = NC * nbs * 16;  // a multiple of 64: whole wavefronts take part or not
+    const bool qwave = wave * 64 < total;
+    XTask t0;
+    if (qwave) t0 = quant_q8K_load(xs, x_stride, ncols, nbs, total, threadIdx.x);
+
+    // the matrix, its row for this lane and the super-blocks of step `it`
+    auto member = [&](int tile) {
+        int i = 0;
+#pragma unroll
+        for (int k = 1; k < 4; k++)
+            if (k < g.n && tile >= g.m[k].tile0) i = k;
+        return i;
+    };
+    auto load = [&](uint32_t (&w)[SK_GB][NW], int it) {
+        const int tile = tgi + (it / ngrp) * g.tg, grp = it % ngrp;
+        const SkMember &mb = g.m[member(tile)];
+        const int row = (tile - mb.tile0) * SK_ROWS + 16 * wave + j;
+        const uint8_t *rp = mb.W + (int64_t)min(row, mb.rows - 1) * w_row_bytes + (int64_t)(b0 + SK_GB * grp) * BB;
+#pragma unroll
+        for (int i = 0; i < SK_GB; i++) {
+            if (SK_GB * grp + i >= nbs) break;
+            const uint8_t *p = rp + (int64_t)i * BB;
+            if constexpr (WT == 12) {
+                const uint4 h = ld16(p);
+                w[i][0] = h.x;
+                w[i][1] = h.y;
+                w[i][2] = h.z;
+                w[i][3] = h.w;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const uint2 q = ld8(p + 16 + 32 * c + 8 * G);
+                    w[i][4 + 2 * c] = q.x;
+                    w[i][5 + 2 * c] = q.y;
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < 6; k++) {
+                    const uint2 q = ld8(p + 32 * k + 8 * G);
+                    w[i][2 * k] = q.x;
+                    w[i][2 * k + 1] = q.y;
+                }
+                w[i][12] = ld4(p + 192 + 4 * G);
+                w[i][13] = ld2(p + 208);
+            }
+        }
+    };
+    uint32_t wa[SK_GB][NW], wb[SK_GB][NW];
+    if (items > 0) load(wa, 0);
+
+    if (qwave) quant_q8K_store(t0, nbs, n_mat, total, threadIdx.x, codes, dq, bsum, CS, BS);
+    for (int base = blockDim.x; base < total; base += blockDim.x) {
+        if (base + wave * 64 >= total) break;
+        const XTask t = quant_q8K_load(xs, x_stride, ncols, nbs, total, base + threadIdx.x);
+        quant_q8K_store(t, nbs, n_mat, total, base + threadIdx.x, codes, dq, bsum, CS, BS);
+    }
+    __syncthreads();
+
+    const int kstride = CS;  // one token's codes in the image
+    const int t_a = j >> 1, h_a = j & 1;  // this lane's A row: token, parity
+    float out[2] = {0.0f, 0.0f};          // tokens 2G, 2G + 1 of row j
+    auto compute = [&](const uint32_t (&w)[SK_GB][NW], int it) {
+        const int tile = tgi + (it / ngrp) * g.tg, grp = it % ngrp;
+        const SkMember &mb = g.m[member(tile)];
+        const int row = (tile - mb.tile0) * SK_ROWS + 16 * wave + j;
+#pragma unroll
+        for (int i = 0; i < SK_GB; i++) {
+            const int bl = SK_GB * grp + i;
+            if (bl >= nbs) break;
+            const int b = b0 + bl;
+            // -32 / min term: A row 4g + u (u < 2) = token 2g + u over the
+            // 16-element sums 4G .. 4G+3
+            v4h am = {};
+            {
+                const int gg = j >> 2, u = j & 3;
+                if (u < 2) {
+                    const int *p = bsum + (2 * gg + u) * BS + bl * 16 + 4 * G;
+                    am[0] = (_Float16)(float)p[0];
+                    am[1] = (_Float16)(float)p[1];
+                    am[2] = (_Float16)(float)p[2];
+                    am[3] = (_Float16)(float)p[3];
+                }
+            }
+            const int8_t *crow = codes + t_a * kstride + bl * QK_K;
+            if constexpr (WT == 12) {
+                const uint32_t *v = w[i];
+                const float dw = h2f(v[0]), dmin = h2f(v[0] >> 16);
+                v4h bm;
+                {
+                    int s0, s1, m0, m1;
+                    k4_scales(v[1], v[2], v[3], scale_sel(G), s0, s1, m0, m1);
+                    bm[0] = bm[1] = (_Float16)(float)m0;
+                    bm[2] = bm[3] = (_Float16)(float)m1;
+                }
+                const v4f accm = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, (v4f){}, 0, 0, 0);
+                int is0 = 0, is1 = 0;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const uint32_t d0 = v[4 + 2 * c], d1 = v[5 + 2 * c];
+                    const v4i bw = {(int)(d0 & 0x0f0f0f0fu), (int)(d1 & 0x0f0f0f0fu), (int)((d0 >> 4) & 0x0f0f0f0fu),
+                                    (int)((d1 >> 4) & 0x0f0f0f0fu)};
+                    const uint2 a8 = *reinterpret_cast<const uint2 *>(crow + 64 * c + 32 * h_a + 8 * G);
+                    const v4i a = h_a ? (v4i){0, 0, (int)a8.x, (int)a8.y} : (v4i){(int)a8.x, (int)a8.y, 0, 0};
+                    const v4i r = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bw, (v4i){}, 0, 0, 0);
+                    int sc0, sc1, mn0, mn1;
+                    k4_scales(v[1], v[2], v[3], scale_sel(c), sc0, sc1, mn0, mn1);
+                    is0 += __mul24(sc0, r[0]) + __mul24(sc1, r[1]);  // |r| < 2^23
+                    is1 += __mul24(sc0, r[2]) + __mul24(sc1, r[3]);
+                }
+                const int isv[2] = {is0, is1};
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const int tok = 2 * G + u;
+                    const float im = accm[u];
+                    if (SUBSUMS && tok < ncols && row < mb.rows) {
+                        int32_t *sp = sub + (((int64_t)tok * mb.rows + row) * nb + b) * 2;
+                        sp[0] = isv[u];
+                        sp[1] = (int)im;
+                    }
+                    out[u] = fmaf(dq[tok * nbs + bl], fmaf(dw, (float)isv[u], -(dmin * im)), out[u]);
+                }
+            } else {
+                const uint32_t *v = w[i];
+                const float dw = h2f(v[13]);
+                const uint32_t sw = v[12];  // scales 4G .. 4G+3 of row j
+                v4h bs;
+                bs[0] = (_Float16)(float)(int8_t)(sw & 0xff);
+                bs[1] = (_Float16)(float)(int8_t)((sw >> 8) & 0xff);
+                bs[2] = (_Float16)(float)(int8_t)((sw >> 16) & 0xff);
+                bs[3] = (_Float16)(float)(int8_t)(sw >> 24);
+                const v4f accm = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bs, (v4f){}, 0, 0, 0);
+                const bool alive = (G >> 1) == h_a;
+                int is0 = 0, is1 = 0;
+#pragma unroll
+                for (int n = 0; n < 2; n++) {
+                    const uint32_t qh0 = v[8 + 2 * n], qh1 = v[9 + 2 * n];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int src = 2 * (2 * n + (q & 1));  // ql words of 64n + 32(q&1)
+                        const int sh = 4 * (q >> 1);
+                        const uint32_t c0 = ((v[src] >> sh) & 0x0f0f0f0fu) | (((qh0 >> (2 * q)) & 0x03030303u) << 4);
+                        const uint32_t c1 = ((v[src + 1] >> sh) & 0x0f0f0f0fu) | (((qh1 >> (2 * q)) & 0x03030303u) << 4);
+                        const long bw = (long)(((uint64_t)c1 << 32) | c0);
+                        long a = 0;
+                        if (alive) a = *reinterpret_cast<const long *>(crow + 128 * n + 32 * q + 8 * G);
+                        const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bw, (v4i){}, 0, 0, 0);
+                        // scales 8n + 2q, 8n + 2q + 1: dword 2n + (q >> 1), held by lane group 2n + (q >> 1)
+                        const uint32_t sd = (uint32_t)__shfl((int)sw, j + 16 * (2 * n + (q >> 1)), 64);
+                        const int sc0 = (int)(int8_t)((sd >> (16 * (q & 1))) & 0xff);
+                        const int sc1 = (int)(int8_t)((sd >> (16 * (q & 1) + 8)) & 0xff);
+                        is0 += __mul24(sc0, c[0]) + __mul24(sc1, c[1]);  // |c| < 2^23
+                        is1 += __mul24(sc0, c[2]) + __mul24(sc1, c[3]);
+                    }
+                }
+                const int isv[2] = {is0 - 32 * (int)accm[0], is1 - 32 * (int)accm[1]};
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const int tok = 2 * G + u;
+                    if (SUBSUMS && tok < ncols && row < mb.rows) sub[((int64_t)tok * mb.rows + row) * nb + b] = isv[u];
+                    out[u] += (dw * (float)isv[u]) * dq[tok * nbs + bl];
+                }
+            }
+        }
+        if (grp == ngrp - 1) {  // the tile's slice is done: store, or leave the partials for ghip_sk_reduce
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int tok = 2 * G + u;
+                if (tok < ncols && row < mb.rows) {
+                    if (g.nks == 1) mb.dst[(int64_t)tok * mb.ldd + row] = out[u];
+                    else mb.part[((int64_t)ks * ncols + tok) * mb.rows + row] = out[u];
+                }
+                out[u] = 0.0f;
+            }
+        }
+    };
+    for (int it = 0; it < items;) {
+        if (it + 1 < items) load(wb, it + 1);
+        compute(wa, it);
+        if (++it >= items) break;
+        if (it + 1 < items) load(wa, it + 1);
+        compute(wb, it);
+        ++it;
+    }
+}
+
+// Steps of 2 super-blocks: at most 128 VGPRs, four wavefronts per SIMD (steps
+// of 4 measured 27.3 -> 24.6 us on the decode layer's gate/up pair at 8 rows,
+// 27.3 -> 24.3 us on Q6_K down)
+#define SK_KERNEL(NAME, WT, S, SUBS) SK_KERNELG(NAME, WT, S, 2, SUBS)
+#define SK_KERNELG(NAME, WT, S, GB, SUBS)                                                                          \
+    extern "C" __global__ void __launch_bounds__(64 * SK_WAVES)                                                    \
+        NAME(SkLaunch g, int64_t w_row_bytes, int nb, const float *__restrict__ x, int64_t x_stride, int ncols,   \
+             int n_mat, int32_t *__restrict__ sub) {                                                               \
+        sk_impl<WT, S, GB, SUBS>(g, w_row_bytes, nb, x, x_stride, ncols, n_mat, sub);                                  \
+    }
+SK_KERNEL(ghip_sk_q4_K_s4, 12, 4, false)
+SK_KERNEL(ghip_sk_q4_K_s8, 12, 8, false)
+SK_KERNEL(ghip_sk_q4_K_sub_s4, 12, 4, true)
+SK_KERNEL(ghip_sk_q4_K_sub_s8, 12, 8, true)
+SK_KERNEL(ghip_sk_q6_K_s4, 14, 4, false)
+SK_KERNEL(ghip_sk_q6_K_s8, 14, 8, false)
+SK_KERNEL(ghip_sk_q6_K_sub_s4, 14, 4, true)
+SK_KERNEL(ghip_sk_q6_K_sub_s8, 14, 8, true)
+
+
+// The K-slices' partials of up to 4 matrices added in slice order:
+// dst[c][r] = sum_k part[k][c][r]; one lane per (matrix, column, row).  Here
+// tile0 of a member is its first row in the launch's concatenated rows.
+extern "C" __global__ void __launch_bounds__(256)
+    ghip_sk_reduce(SkLaunch g, int ncols, int64_t total) {
+    const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (id >= total) return;
+    int i = 0;
+#pragma unroll
+    for (int k = 1; k < 4; k++)
+        if (k < g.n && id >= (int64_t)g.m[k].tile0 * ncols) i = k;
+    const SkMember &mb = g.m[i];
+    const int64_t e = id - (int64_t)mb.tile0 * ncols;  // (column, row) in the matrix
+    const int c = (int)(e / mb.rows), r = (int)(e - (int64_t)c * mb.rows);
+    const int64_t plane = (int64_t)ncols * mb.rows;
+    float s = 0.0f;
+    for (int k0 = 0; k0 < g.nks; k0 += 8) {  // 8 loads in flight, added in order
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = k0 + k < g.nks ? mb.part[(k0 + k) * plane + e] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (k0 + k < g.nks) s = k0 + k == 0 ? v[k] : s + v[k];
+    }
+    mb.dst[(int64_t)c * mb.ldd + r] = s;
+}

@@ -259,3 +259,64 @@ def test_gemm_q8_family_registered(be):
     be.register_weight(wd, O.Q4_0, n)
     assert torch.equal(be.mul_mat(wd, O.Q4_0, n, xd), before)
     be.unregister_weight(wd, O.Q4_0, n)
+
+
+@pytest.mark.parametrize("ty,n,rows,cols", [
+    (O.Q4_K, 1280, 100, 4),    # 5 super-blocks: slices of 4 + 1, a partial 64-row tile
+    (O.Q4_K, 1536, 1000, 7),   # 6 super-blocks: the last slice one 2-block step
+    (O.Q4_K, 256, 64, 8),      # one slice: no partials
+    (O.Q4_K, 7168, 300, 5),    # 28 super-blocks: slices of 8
+    (O.Q6_K, 1792, 70, 4),     # 7 super-blocks
+    (O.Q6_K, 8192, 130, 7),    # 32 super-blocks: slices of 8
+    (O.Q6_K, 256, 16, 8),
+])
+def test_split_k_decode(be, monkeypatch, ty, n, rows, cols):
+    """The split-K decode kernels (Q4_K, Q6_K at 4..8 rows; Q4_K forced onto
+    them below 8192 weight rows): the activation slice quantized inside each
+    workgroup, the K-slices' partials added in order by ghip_sk_reduce;
+    ragged slices, steps and row tiles; Q8_K bytes and int32 sub-sums
+    bit-exact."""
+    monkeypatch.setenv("GHIP_SK_MIN_ROWS", "1")
+    run_case(be, ty, n, rows, cols, seed=rows + cols)
+
+
+def test_split_k_tiles_per_workgroup(be, monkeypatch):
+    """Few workgroups (GHIP_SK_WGS): each walks several tiles with the next
+    step's weights in flight; same bits as one tile per workgroup."""
+    w, x = make(O.Q4_K, 4096, 14336, 8, seed=3)
+    wd, xd = torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda()
+    print("split-K tiles per workgroup", flush=True)
+    want = be.mul_mat(wd, O.Q4_K, 4096, xd).clone()
+    for wgs in ("8", "100", "100000"):
+        monkeypatch.setenv("GHIP_SK_WGS", wgs)
+        assert torch.equal(be.mul_mat(wd, O.Q4_K, 4096, xd), want)
+
+
+@pytest.mark.parametrize("ty,n,rows", [(O.Q4_K, 4096, 14336), (O.Q6_K, 14336, 4096)])
+def test_split_k_repeat_and_graph(be, ty, n, rows):
+    """The per-tile counters return to zero after every call: repeated calls,
+    and replays of a captured graph between eager calls, give the same bits."""
+    w, x = make(ty, n, rows, 8, seed=5)
+    wd, xd = torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda()
+    print(f"split-K repeat type={ty} n={n} rows={rows}", flush=True)
+    first = be.mul_mat(wd, ty, n, xd).clone()
+    for _ in range(3):
+        assert torch.equal(be.mul_mat(wd, ty, n, xd), first)
+    out = torch.empty_like(first)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        be.mul_mat(wd, ty, n, xd, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        be.mul_mat(wd, ty, n, xd, out=out)
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, first)
+        assert torch.equal(be.mul_mat(wd, ty, n, xd), first)
+    want, _, _ = O.mul_mat(ty, w, n, rows, x, 8)
+    assert rel_err(first.cpu().numpy(), want) <= TOL

@@ -12,7 +12,8 @@
 // heads that share hk (GQA) times QS = ceil(4 / G) tiles of 32 queries, so
 // every K/V tile staged in LDS serves >= 4 wavefronts.
 // The next tile's K, V and mask values are loaded into registers while the
-// current one is computed.  Per
+// current one is computed, and staged into the second of two LDS buffers
+// after it (one barrier per tile).  Per
 // 64-key tile each wavefront computes S^T = K Q^T (keys x queries), which
 // leaves all scores of one query in one lane pair (l, l^32): the row max and
 // row sum need one cross-lane exchange.  O^T += V^T P^T accumulates in 4 x 16
@@ -65,7 +66,7 @@ DEV float head_slope(const FaParams &p, int h) {
 }
 
 template <int D, bool SOFTCAP>
-__device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks, _Float16 *Vt) {
+__device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _Float16 *Vt2) {
     constexpr int KS = D + FA_KPAD, VS = FA_BK + FA_VPAD;
     constexpr int NKC = FA_BK * D / 8;           // 16-byte K chunks per tile
     constexpr int NVB = (FA_BK / 4) * (D / 8);   // 4-key x 8-dim V blocks per tile
@@ -170,7 +171,7 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks, _Fl
                         uint2, __builtin_amdgcn_raw_buffer_load_b64(mrs, mt + 2u * (32 * jt + 8 * gq), 0, 0));
         }
     };
-    auto stage = [&]() {
+    auto stage = [&](_Float16 *Ks, _Float16 *Vt) {
 #pragma unroll
         for (int i = 0; i < MAXK; i++) {
             const int c = tid + i * nthr;
@@ -202,16 +203,22 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks, _Fl
         }
     };
 
+    // Two LDS buffers: tile i is computed from buffer i & 1 while tile i + 1
+    // is staged into the other one after the compute, so one barrier per
+    // tile separates the staging from the next tile's reads (and the reads of
+    // a buffer from its next staging, one tile later).
+    constexpr int KBUF = FA_BK * KS, VBUF = D * VS;
     if (kb < ke) {
         fetch_kv(kb);
         fetch_mask(kb);
+        stage(Ks2, Vt2);
+        if (kb + FA_BK < ke) fetch_kv(kb + FA_BK);
     }
-    for (int k0 = kb; k0 < ke; k0 += FA_BK) {
+    __syncthreads();
+    for (int k0 = kb, it = 0; k0 < ke; k0 += FA_BK, it++) {
         const int nk = min(FA_BK, ke - k0);
-        __syncthreads();  // the previous tile is consumed
-        stage();
-        __syncthreads();
-        if (k0 + FA_BK < ke) fetch_kv(k0 + FA_BK);
+        const _Float16 *Ks = Ks2 + (it & 1) * KBUF;
+        const _Float16 *Vt = Vt2 + (it & 1) * VBUF;
 
         if (nk < FA_BK && mrow) {
             // tail tile: mask groups reaching past the range, with bound checks
@@ -328,7 +335,12 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks, _Fl
                     o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[dt], 0, 0, 0);
                 }
             }
-        if (k0 + FA_BK < ke) fetch_mask(k0 + FA_BK);
+        if (k0 + FA_BK < ke) {
+            stage(Ks2 + ((it + 1) & 1) * KBUF, Vt2 + ((it + 1) & 1) * VBUF);
+            if (k0 + 2 * FA_BK < ke) fetch_kv(k0 + 2 * FA_BK);
+            fetch_mask(k0 + FA_BK);
+        }
+        __syncthreads();
     }
 
     // write this slice's partial (M in natural-log units, S, unnormalized O)
@@ -350,8 +362,8 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks, _Fl
 // does not need)
 template <int D, bool SOFTCAP>
 __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
-    __shared__ __attribute__((aligned(16))) _Float16 Ks[FA_BK * (D + FA_KPAD)];  // [key][d]
-    __shared__ __attribute__((aligned(16))) _Float16 Vt[D * (FA_BK + FA_VPAD)];  // [d][key]
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[2 * FA_BK * (D + FA_KPAD)];  // 2 x [key][d]
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[2 * D * (FA_BK + FA_VPAD)];  // 2 x [d][key]
     fa_fwd_body<D, SOFTCAP>(p, Ks, Vt);
 }
 

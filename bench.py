@@ -378,9 +378,10 @@ def gemm_q6k_bench(be, torch, np):
 
 
 def gemm_q8_family_bench(be, torch, np):
-    """Prefill of 32-element-block weights (Q4_0, Q8_0) at 512 tokens,
-    4096 -> 14336: the int8-MFMA GEMM, per-call repack and registered weight,
-    against the 8-column decode kernels it replaces."""
+    """Prefill of 32-element-block weights (Q4_0, Q8_0) and Q5_K at 512
+    tokens, 4096 -> 14336: the int8-MFMA GEMMs (per-call repack and registered
+    weight for the 32-element blocks), against the 8-column decode kernels
+    they replace."""
     import ghip
     res = {}
     m, k, n = 512, 4096, 14336
@@ -412,6 +413,24 @@ def gemm_q8_family_bench(be, torch, np):
         log(f"{name} GEMM {m}x{k}->{n}: op {us:.1f} us, registered {us_reg:.1f} us "
             f"({ops / us_reg / 1e6:.1f} TOPS); 8-column decode kernels {us_gemv:.1f} us")
         del w, x, out
+    # Q5_K: the wide Q4_K tiles with the fifth-bit plane (no device Q5_K
+    # quantizer: random blocks with small finite d / dmin)
+    blk = torch.randint(0, 256, (n, k // 256, 176), device="cuda", generator=g, dtype=torch.int32).to(torch.uint8)
+    blk[:, :, 0:4] = torch.tensor([0x1A, 0x14, 0x1A, 0x14], dtype=torch.uint8, device="cuda")  # d, dmin = 0.001
+    w = blk.reshape(n, -1).contiguous()
+    x = torch.randn((m, k), device="cuda", generator=g)
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    us = graph_time_us(torch, lambda i: be.mul_mat(w, ghip.Q5_K, k, x, out=out), 10)
+    os.environ["GHIP_GEMM_Q5K_MIN_ROWS"] = str(1 << 30)
+    try:
+        us_gemv = graph_time_us(torch, lambda i: be.mul_mat(w, ghip.Q5_K, k, x, out=out), 2, reps=2)
+    finally:
+        del os.environ["GHIP_GEMM_Q5K_MIN_ROWS"]
+    ops = 2.0 * m * n * k
+    res[f"q5_K {m}x{k}->{n}"] = {"us_op": round(us, 2), "TOPS_op": round(ops / us / 1e6, 1),
+                                 "frac_int8_peak": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4),
+                                 "us_op_8col_decode_kernels": round(us_gemv, 2)}
+    log(f"q5_K GEMM {m}x{k}->{n}: op {us:.1f} us ({ops / us / 1e6:.1f} TOPS); 8-column decode kernels {us_gemv:.1f} us")
     return res
 
 

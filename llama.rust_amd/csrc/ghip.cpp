@@ -547,6 +547,8 @@ const GemmKernel kGemmW8 = {"ghip_gemm_q4_K_w8", "ghip_gemm_q4_K_w8_sub", "ghip_
 const GemmKernel kGemmM64 = {"ghip_gemm_q4_K_m64", "ghip_gemm_q4_K_m64_sub", "ghip_gemm_q4_K_m64_multi", 64, 128, 256,
                              kGemmSmem64};
 const GemmKernel kGemmM128 = {"ghip_gemm_q4_K", "ghip_gemm_q4_K_sub", nullptr, 128, 128, 512, kGemmSmem128};
+// Q5_K: the wide tiles with the fifth-bit plane (ghip_gemm.hip gemm_q4K_wide_impl<8, _, true>)
+const GemmKernel kGemmQ5W8 = {"ghip_gemm_q5_K_w8", "ghip_gemm_q5_K_w8_sub", nullptr, 128, 256, 512, kGemmSmemW8};
 int64_t gemm_tiles(const GemmKernel &k, int64_t M, int64_t N) { return ((M + k.bm - 1) / k.bm) * ((N + k.bn - 1) / k.bn); }
 // The wide 128 x 256 tiles (one workgroup of 8 wavefronts per CU) when they
 // give at least half a wave of workgroups; otherwise 64 x 128 tiles (two per
@@ -561,8 +563,11 @@ const GemmKernel &gemm_kernel(int64_t M, int64_t N) {
 }
 // K slices for grids that would leave CUs idle (fewer than 128 tiles); the
 // slices' partial sums are added in order by ghip_gemm_splitk_reduce
+const GemmKernel &gemm_kernel_for(const MulMatPlan &p) {
+    return p.wtype == GHIP_TYPE_Q5_K ? kGemmQ5W8 : gemm_kernel(p.M, p.N);
+}
 int gemm_nsplit(const MulMatPlan &p) {
-    const int64_t tiles = gemm_tiles(gemm_kernel(p.M, p.N), p.M, p.N);
+    const int64_t tiles = gemm_tiles(gemm_kernel_for(p), p.M, p.N);
     if (tiles >= 128 || p.N % 4) return 1;
     const int64_t want = (256 + tiles - 1) / tiles;
     const int64_t nbs = (p.nb + want - 1) / want;  // super-blocks per slice
@@ -717,7 +722,7 @@ ghip_status run_gemm(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
            : ctx->launch("ghip_gemm_act_layout", dim3(lgrid), dim3(256), 0, s, act, (int64_t)p.act_row_bytes,
                          (int)p.M, (int)Mpad, (int)nbk, codes, bsT, dT);
     if (st != GHIP_STATUS_SUCCESS) return st;
-    const GemmKernel &gk = gemm_kernel(p.M, p.N);
+    const GemmKernel &gk = gemm_kernel_for(p);
     const unsigned grid = (unsigned)gemm_tiles(gk, p.M, p.N);
     const int ns = gemm_nsplit(p);
     const int nbs = (int)((p.nb + ns - 1) / ns);
@@ -738,6 +743,8 @@ ghip_status run_gemm(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
 bool use_gemm(const MulMatPlan &p) {
     if (p.M > INT32_MAX) return false;
     if (p.wtype == GHIP_TYPE_Q4_K) return p.M >= env_int("GHIP_GEMM_MIN_ROWS", 16);
+    // Q5_K: the wide Q4_K tiles with a fifth-bit plane, from 16 rows
+    if (p.wtype == GHIP_TYPE_Q5_K) return p.M >= env_int("GHIP_GEMM_Q5K_MIN_ROWS", 16);
     // Q6_K: the f16-MFMA GEMM from 64 activation rows (below, the 8-column decode kernels)
     if (p.wtype == GHIP_TYPE_Q6_K) return p.M >= env_int("GHIP_GEMM_Q6K_MIN_ROWS", 64) && p.K >= 512;
     // Q4_0 / Q5_0 / Q8_0 from f32 activations: the int8-MFMA GEMM from 32 rows

@@ -350,7 +350,13 @@ DEV void b2lds(brsrc r, void *lds, uint32_t voff, uint32_t soff) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 16, voff, soff, 0, 0);
 }
 
-template <int NW, bool SUBSUMS>
+// Q5: Q5_K weights (176-byte blocks: d, dmin, 12 scale bytes, qh[32], qs[128];
+// vec_dot_q5_K_q8_K, vec_dot.rs:1062-1120, the Q4_K arithmetic with
+// q5 = q4 + 16 * (bit s of qh[l]) for element l of sub-block s).  The fifth
+// bit enters as a third int8 plane 2 * sc * bit (<= 126) accumulated into the
+// high plane, so iacc = 8 * acc_h + acc_l holds 16 * sc * bit * q8 exactly;
+// each lane's 16 qh bytes come by a buffer load one super-block ahead.
+template <int NW, bool SUBSUMS, bool Q5 = false>
 __device__ __forceinline__ void gemm_q4K_wide_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb,
                                                    const int8_t *__restrict__ codes,
                                                    const _Float16 *__restrict__ bsT, const float *__restrict__ dT,
@@ -358,6 +364,7 @@ __device__ __forceinline__ void gemm_q4K_wide_impl(const uint8_t *__restrict__ W
                                                    int32_t *__restrict__ sub, int nbs, int64_t zstride, int tile) {
     constexpr int BM = g4::BM, BN = 32 * NW;
     constexpr int APW = 32 / NW;  // activation pieces (1 KB) per wavefront
+    constexpr uint32_t BB = Q5 ? 176u : 144u, QS_OFF = Q5 ? 48u : 16u;  // block bytes, qs offset
     const int b0 = blockIdx.y * nbs, b1 = min(nb, b0 + nbs);
     dst += blockIdx.y * zstride;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
@@ -397,7 +404,7 @@ __device__ __forceinline__ void gemm_q4K_wide_impl(const uint8_t *__restrict__ W
     uint32_t woff[4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
-        woff[i] = (uint32_t)(32 * wave + 8 * i + (lane >> 3)) * (uint32_t)rb + 16u +
+        woff[i] = (uint32_t)(32 * wave + 8 * i + (lane >> 3)) * (uint32_t)rb + QS_OFF +
                   16u * (uint32_t)((lane & 7) ^ ((lane >> 3) & 7));
     const uint32_t hoff = (uint32_t)(64 * wave + lane) * (uint32_t)rb;  // header piece `wave`
     // bsum16 pieces wave - NW/2 and wave + NW/2
@@ -410,11 +417,11 @@ __device__ __forceinline__ void gemm_q4K_wide_impl(const uint8_t *__restrict__ W
         for (int i = 0; i < APW; i++) b2lds(ra, S.act + 1024 * (APW * wave + i), aoff[i], (uint32_t)b * 256u);
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            b2lds(rw, S.wraw + 1024 * (4 * wave + i), woff[i], (uint32_t)b * 144u);
+            b2lds(rw, S.wraw + 1024 * (4 * wave + i), woff[i], (uint32_t)b * BB);
         // NW/2 header pieces, then 4 bsum16 pieces: piece e by wavefront e % NW
 #pragma unroll
         for (int e = wave; e < NW / 2 + 4; e += NW) {
-            if (e < NW / 2) b2lds(rw, S.hdr + 1024 * e, hoff, (uint32_t)b * 144u);
+            if (e < NW / 2) b2lds(rw, S.hdr + 1024 * e, hoff, (uint32_t)b * BB);
             else b2lds(rs, reinterpret_cast<uint8_t *>(S.bs) + 1024 * (e - NW / 2), soff[e >= NW], (uint32_t)b * (uint32_t)Mpad * 32u);
         }
         if (wave == NW - 1 && lane < BM / 4) b2lds(rd, S.da, doff, (uint32_t)b * (uint32_t)Mpad * 4u);
@@ -431,11 +438,18 @@ __device__ __forceinline__ void gemm_q4K_wide_impl(const uint8_t *__restrict__ W
     const uint32_t raw_off0 = (uint32_t)wr * 128, wsw = (uint32_t)(wr & 7);
     const uint32_t asw = (uint32_t)(li & 15);
 
+    // Q5_K: this lane's qh bytes 16h .. 16h+15 (elements 16h + i of every sub-block)
+    const uint32_t qhoff = (uint32_t)wr * (uint32_t)rb + 16u + 16u * (uint32_t)h;
+    uint4 qh_cur = make_uint4(0, 0, 0, 0), qh_nxt = qh_cur;
+    if (Q5 && b0 < b1)
+        qh_cur = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, qhoff, (uint32_t)b0 * BB, 0));
     if (b0 < b1) issue(b0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     for (int b = b0; b < b1; b++) {
         if (b + 1 < b1) issue(b + 1);
+        if (Q5 && b + 1 < b1)
+            qh_nxt = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, qhoff, (uint32_t)(b + 1) * BB, 0));
         const g4::Stage<BN> &S = stg[(b - b0) & 1];
         const uint4 hv = *reinterpret_cast<const uint4 *>(S.hdr + 16 * wr);
         const float dw = h2f(hv.x), dmin = h2f(hv.x >> 16);
@@ -470,18 +484,23 @@ __device__ __forceinline__ void gemm_q4K_wide_impl(const uint8_t *__restrict__ W
                 const int ks = 2 * c + nh;
                 const uint32_t sv = (uint32_t)(nh ? sb2 : sa);
                 const uint32_t slo = sv & 7u, shi = sv >> 3;
-                v4i blo, bhi;
+                v4i blo, bhi, b5;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const uint32_t nib = nh ? ((rwv[e] >> 4) & 0x0f0f0f0fu) : (rwv[e] & 0x0f0f0f0fu);
                     blo[e] = (int)mul_bytes(nib, slo);
                     bhi[e] = (int)mul_bytes(nib, shi);
+                    if (Q5) {
+                        const uint32_t qw = e == 0 ? qh_cur.x : e == 1 ? qh_cur.y : e == 2 ? qh_cur.z : qh_cur.w;
+                        b5[e] = (int)mul_bytes((qw >> ks) & 0x01010101u, 2u * sv);
+                    }
                 }
 #pragma unroll
                 for (int tm = 0; tm < 4; tm++) {
                     const v4i a = *reinterpret_cast<const v4i *>(S.act + (32 * tm + li) * 256 + 16 * ((2 * ks + h) ^ asw));
                     acc_l[tm] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, blo, ks == 0 ? z16 : acc_l[tm], 0, 0, 0);
                     acc_h[tm] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bhi, ks == 0 ? z16 : acc_h[tm], 0, 0, 0);
+                    if (Q5) acc_h[tm] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b5, acc_h[tm], 0, 0, 0);
                 }
             }
         }
@@ -516,6 +535,7 @@ __device__ __forceinline__ void gemm_q4K_wide_impl(const uint8_t *__restrict__ W
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+        qh_cur = qh_nxt;
     }
     const int n = n0 + wr;
 #pragma unroll
@@ -544,6 +564,20 @@ __device__ __forceinline__ void gemm_q4K_wide_impl(const uint8_t *__restrict__ W
                                      -1);                                                                          \
     }
 GEMM_WIDE_KERNELS(ghip_gemm_q4_K_w8, 8, 1)
+extern "C" __global__ void __launch_bounds__(512, 1)
+    ghip_gemm_q5_K_w8(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb,
+                      const int8_t *__restrict__ codes, const _Float16 *__restrict__ bsT, const float *__restrict__ dT,
+                      int M, int Mpad, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub, int nbs,
+                      int64_t zstride) {
+    gemm_q4K_wide_impl<8, false, true>(W, w_row_bytes, N, nb, codes, bsT, dT, M, Mpad, dst, ldd, sub, nbs, zstride, -1);
+}
+extern "C" __global__ void __launch_bounds__(512, 1)
+    ghip_gemm_q5_K_w8_sub(const uint8_t *__restrict__ W, int64_t w_row_bytes, int N, int nb,
+                          const int8_t *__restrict__ codes, const _Float16 *__restrict__ bsT,
+                          const float *__restrict__ dT, int M, int Mpad, float *__restrict__ dst, int64_t ldd,
+                          int32_t *__restrict__ sub, int nbs, int64_t zstride) {
+    gemm_q4K_wide_impl<8, true, true>(W, w_row_bytes, N, nb, codes, bsT, dT, M, Mpad, dst, ldd, sub, nbs, zstride, -1);
+}
 
 
 

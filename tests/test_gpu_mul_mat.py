@@ -35,10 +35,12 @@ def make(ty, n, rows, cols, seed=0, scale=0.02):
     return w, x
 
 
-def run_case(be, ty, n, rows, cols, seed=0, x=None, check_sub=True):
-    w, x0 = make(ty, n, rows, cols, seed)
+def run_case(be, ty, n, rows, cols, seed=0, x=None, check_sub=True, w=None):
+    w0, x0 = make(ty, n, rows, cols, seed)
     if x is None:
         x = x0
+    if w is None:
+        w = w0
     if ty == O.Q4_0 and rows % 8 and cols >= 2:
         # the reference's tinyBLAS route (llamafile_sgemm), absent from the
         # oracle: the same Q8_0 rows and integer block dots, checked against
@@ -160,6 +162,32 @@ def test_gemm_q4K_small(be, n, rows, cols):
     """Q4_K with >= 16 activation rows takes the int8-MFMA GEMM; tile edges in
     both M (tokens) and N (weight rows)."""
     run_case(be, O.Q4_K, n, rows, cols, seed=rows)
+
+
+@pytest.mark.parametrize("n,rows,cols", [(256, 32, 16), (512, 136, 37), (1024, 128, 128), (768, 200, 130),
+                                         (4096, 300, 64), (2048, 64, 16)])
+def test_gemm_q5K_small(be, n, rows, cols):
+    """Q5_K with >= 16 activation rows takes the wide int8-MFMA GEMM with the
+    fifth-bit plane (split K when the tiles are few); tile edges in tokens and
+    rows; Q8_K bytes and int32 {iacc, imin} sub-sums bit-exact."""
+    run_case(be, O.Q5_K, n, rows, cols, seed=rows + 7)
+
+
+def test_gemm_q5K_extreme_blocks(be):
+    """Q5_K blocks at the ends of every field (6-bit scales and mins 63, all
+    codes 31 with qh all ones, or 0) against the oracle: the fifth-bit plane
+    2 * sc * bit stays within int8 and the sums exact."""
+    rng = np.random.default_rng(11)
+    n, rows, cols = 1024, 64, 32
+    w = rng.integers(0, 256, size=(rows, O.row_size(O.Q5_K, n)), dtype=np.uint8)
+    blk = w.reshape(rows, n // 256, 176)
+    blk[:, :, 0:2] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8)  # finite d, dmin
+    blk[:, :, 2:4] = np.frombuffer(np.float16(0.02).tobytes(), np.uint8)
+    blk[::2, :, 4:16] = 0xFF                      # every scale and min 63
+    blk[::4, :, 16:176] = 0xFF                    # codes 31
+    blk[1::4, :, 16:176] = 0                      # codes 0
+    x = np.random.default_rng(12).standard_normal((cols, n)).astype(np.float32)
+    run_case(be, O.Q5_K, n, rows, cols, x=x, w=w)
 
 
 @pytest.mark.parametrize("n,rows,cols", [(512, 136, 64), (1024, 200, 100), (768, 128, 130), (4096, 256, 64),

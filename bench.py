@@ -271,7 +271,7 @@ def _profile_ops(be, torch, np, what):
         nodes = [[ghip.mul_mat_node(w, ty, k, xs[LAYER_INPUT[name]], outs[name])
                   for (name, ty, k, n), w in zip(LAYER, ws)] for ws in sets]
         return lambda i: be.graph_compute(nodes[i % len(nodes)])
-    if what == "moe":
+    if what in ("moe", "moe_reg"):
         n_as, n_tok, n_ids, k, rows = 32, 256, 4, 2880, 5760
         rng = np.random.default_rng(3)
         ids = torch.from_numpy(np.argsort(-rng.standard_normal((n_tok, n_as)), axis=1)[:, :n_ids]
@@ -281,6 +281,8 @@ def _profile_ops(be, torch, np, what):
         del wf
         b = torch.randn((n_tok, 1, k), device="cuda", generator=g)
         out = torch.empty((n_tok, n_ids, rows), dtype=torch.float32, device="cuda")
+        if what == "moe_reg":  # experts registered: the kernel reads the repacked windows
+            be.register_weight(w, ghip.MXFP4, k)
         return lambda i: be.mul_mat_id(w, k, b, ids, out=out)
     if what in ("fa_decode", "fa_prefill"):
         H, Hkv, D, S = 32, 8, 128, 8192
@@ -296,8 +298,8 @@ def _profile_ops(be, torch, np, what):
     raise ValueError(what)
 
 
-PROFILE_WORKLOADS = ["gemv", "copy", "gemm", "gemm_q6k", "decode_b8", "layer_b1", "layer_b8", "moe", "fa_decode",
-                     "fa_prefill"]
+PROFILE_WORKLOADS = ["gemv", "copy", "gemm", "gemm_q6k", "decode_b8", "layer_b1", "layer_b8", "moe", "moe_reg",
+                     "fa_decode", "fa_prefill"]
 
 
 def profile_loop(what, n):
@@ -307,7 +309,7 @@ def profile_loop(what, n):
     copy: 33,030,144-byte device copies; gemm: Q4_K 512x4096->14336;
     gemm_q6k: Q6_K 512x14336->4096; decode_b8: Q4_K 4096->14336 at 8 rows over
     16 copies; layer_b1 / layer_b8: the decode layer's 7 MUL_MATs in one
-    graph_compute call at batch 1 / 8 over 4 weight copies; moe: MXFP4 gate_up (32 experts, 256 tokens, top-4);
+    graph_compute call at batch 1 / 8 over 4 weight copies; moe / moe_reg: MXFP4 gate_up (32 experts, 256 tokens, top-4; moe_reg with the experts registered);
     fa_decode / fa_prefill: FLASH_ATTN_EXT 32/8 heads, D 128, KV 8192, T 1 / 512."""
     import numpy as np
     import torch

@@ -1070,7 +1070,10 @@ ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip
                                  (sub ? "_sub" : "")
                            : std::string("ghip_moe_mxfp4_t") + (tp == 32 ? "32" : "64") + (repack ? "" : "_plain") +
                                  (sub ? "_sub" : "");
-    const dim3 grid((unsigned)max_tiles, (unsigned)((p.rows + 127) / 128));
+    // the scaled-FP4 kernel remaps its ids per XCD when the grid is a multiple of 8
+    // (tiles past the route's count exit at once); GHIP_MOE_ORDER 0 / 1 / 2:
+    // no remap / tiles fastest (default) / row blocks fastest
+    const dim3 grid((unsigned)(fp4 ? (max_tiles + 7) / 8 * 8 : max_tiles), (unsigned)((p.rows + 127) / 128));
     if (fp4) {
         // the registered copy of the experts, if any (ghip_weight_register)
         auto it = ctx->wcache.find(ghip_context::key_of(as));
@@ -1080,7 +1083,7 @@ ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip
         return ctx->launch(name.c_str(), grid, dim3(256), 0, s, (const uint8_t *)as->data, (int64_t)as->nb[1],
                            (int64_t)as->nb[2], (const uint16_t *)actf, (const float *)actd, (int)p.ne11,
                            (const int32_t *)route, (int)n_pairs, (int)p.n_ids, dst, dst_nb1, dst_nb2, (int)p.rows,
-                           (int)p.nb, sub, wrep, ngp);
+                           (int)p.nb, sub, wrep, ngp, env_int("GHIP_MOE_ORDER", 1));
     }
     return ctx->launch(name.c_str(), grid, dim3(256), 0, s, (const uint8_t *)as->data, (int64_t)as->nb[1],
                        (int64_t)as->nb[2], (const uint16_t *)actf, (const float *)actd, (int)p.ne11,

@@ -1037,7 +1037,7 @@ ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip
         const unsigned qgrid = (unsigned)((act_rows * p.nb + 3) / 4);
         st = ctx->launch("ghip_quantize_q8_K", dim3(qgrid), dim3(256), 0, s, (const float *)b->data,
                          (int64_t)b->nb[1] / 4, p.K, act_rows, act, p.act_row_bytes, (int64_t)0);
-    } else {
+    } else if (!moe_fp4(tp)) {  // the f16 kernel's activation pass reads Q8_0 rows
         const unsigned qgrid = (unsigned)((act_rows * p.nb * 8 + 255) / 256);
         st = ctx->launch("ghip_quantize_q8_0", dim3(qgrid), dim3(256), 0, s, (const float *)b->data,
                          (int64_t)b->nb[1] / 4, p.K, act_rows, act, p.act_row_bytes);
@@ -1061,9 +1061,13 @@ ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip
     // the f16 kernel (f16 codes); both write 64 bytes per routed pair and block
     const bool fp4 = moe_fp4(tp);
     const unsigned fgrid = (unsigned)((n_pairs * p.nb * 4 + 255) / 256);
-    st = ctx->launch(fp4 ? "ghip_moe_act_fp8" : "ghip_moe_act_f16", dim3(fgrid), dim3(256), 0, s, (const uint8_t *)act,
-                     p.act_row_bytes, (const int32_t *)route, (int)n_pairs, (int)p.n_ids, (int)p.ne11, (int)p.nb,
-                     actf, actd);
+    if (fp4)  // FP8 planes quantized straight from the f32 rows (no Q8_0 pass)
+        st = ctx->launch("ghip_moe_act_fp8_f", dim3(fgrid), dim3(256), 0, s, (const float *)b->data,
+                         (int64_t)b->nb[1] / 4, (int64_t)b->nb[2] / 4, (const int32_t *)route, (int)n_pairs,
+                         (int)p.n_ids, (int)p.ne11, (int)p.nb, actf, actd);
+    else
+        st = ctx->launch("ghip_moe_act_f16", dim3(fgrid), dim3(256), 0, s, (const uint8_t *)act, p.act_row_bytes,
+                         (const int32_t *)route, (int)n_pairs, (int)p.n_ids, (int)p.ne11, (int)p.nb, actf, actd);
     if (st != GHIP_STATUS_SUCCESS) return st;
     const bool repack = p.rows % 8 == 0;  // compute.rs:1965-1972 routes rows % 8 == 0 through the repack kernel
     std::string name = fp4 ? std::string("ghip_moe_fp4") + (tp == 64 ? "_t64" : "") + (repack ? "" : "_plain") +

@@ -460,6 +460,61 @@ ghip_moe_act_fp8(const uint8_t *__restrict__ q8, int64_t q8_row_bytes, const int
     if (piece == 0) actd[(int64_t)b * n_pairs + slot] = h2f(ld2(blk));
 }
 
+// The same planes straight from the f32 rows of src1: each 4-lane group of
+// tasks shares one (slot, block) and quantizes it with ghip_quantize_q8_0's
+// arithmetic (quantize_row_q8_0, quants.rs:331-362: amax over the block,
+// d = f16(amax / 127), q = rne(x * 127 / amax), NaN or out of range -> -128),
+// so the codes and d equal a Q8_0 pass followed by ghip_moe_act_fp8 and the
+// separate quantization launch is not needed.  x_nb1 / x_nb2: floats between
+// src1 rows / tokens.
+extern "C" __global__ void __launch_bounds__(256)
+ghip_moe_act_fp8_f(const float *__restrict__ x, int64_t x_nb1, int64_t x_nb2, const int32_t *__restrict__ route,
+                   int n_pairs, int n_ids, int ne11, int nb, uint8_t *__restrict__ actq, float *__restrict__ actd) {
+    const int64_t task = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (slot, block, piece)
+    const int n_valid = n_pairs - route[1];
+    if (task >= (int64_t)n_valid * nb * 4) return;  // whole 4-lane groups exit together
+    const int piece = (int)(task & 3), hplane = piece >> 1, j = piece & 1;
+    const int64_t rb = task >> 2;
+    const int64_t slot = rb / nb;
+    const int b = (int)(rb - slot * nb);
+    const int p = route[2 + slot], t = p / n_ids, sl = p - t * n_ids;
+    const float *xb = x + (int64_t)t * x_nb2 + (int64_t)(sl % ne11) * x_nb1 + (int64_t)b * 32;
+    float v[16];  // elements 8j .. 8j+7, then 16 + 8j .. 16 + 8j + 7
+    __builtin_memcpy(v, xb + 8 * j, 32);
+    __builtin_memcpy(v + 8, xb + 16 + 8 * j, 32);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));  // the other half of the block (piece ^ 1)
+    const float d = __fdiv_rn(amax, 127.0f);
+    const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+    auto code = [&](float xv) {
+        const float r = rintf(__fmul_rn(xv, id));
+        const int q = (r != r || fabsf(r) >= 2147483648.0f) ? -128 : (int)r;
+        return (int)(int8_t)(q & 0xff);
+    };
+    uint32_t out[4];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int qa = code(v[i]), qb = code(v[8 + i]);
+        uint32_t ba, bb;
+        if (hplane == 0) {
+            ba = e4m3_small((uint32_t)(qa & 15));
+            bb = e4m3_small((uint32_t)(qb & 15));
+        } else {
+            const int ha = qa >> 4, hb = qb >> 4;  // -8 .. 7
+            ba = e4m3_small((uint32_t)(ha < 0 ? -ha : ha)) | (ha < 0 ? 0x80u : 0u);
+            bb = e4m3_small((uint32_t)(hb < 0 ? -hb : hb)) | (hb < 0 ? 0x80u : 0u);
+        }
+        const uint32_t pair = ba | (bb << 8);  // K positions 2i, 2i+1
+        if ((i & 1) == 0) out[i >> 1] = pair;
+        else out[i >> 1] |= pair << 16;
+    }
+    *reinterpret_cast<uint4 *>(actq + (((int64_t)b * 4 + piece) * n_pairs + slot) * 16) =
+        make_uint4(out[0], out[1], out[2], out[3]);
+    if (piece == 0) actd[(int64_t)b * n_pairs + slot] = h2f(f2h_rn(d));
+}
+
 typedef int v8i __attribute__((ext_vector_type(8)));
 
 // grid (tile, row block of 128); 4 wavefronts x 32 expert rows; a tile is 32

@@ -482,9 +482,16 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     const bool q4k = gemv_v2(p);
     int rb_d, ng_d;
     gemv_groups(p.wtype, p.M, p.N, rb_d, ng_d);
-    const int rb = q4k ? env_int("GHIP_GEMV_RB", rb_d) : 8;
-    const int ng = q4k ? env_int("GHIP_GEMV_NG", ng_d) : 1;
-    if (q4k && !((rb == 2 && (ng == 2 || ng == 4 || ng == 8)) || (rb == 4 && (ng == 2 || ng == 4)) ||
+    // GHIP_GEMV_PERSIST=1: Q4_K at one row, K in one wavefront, from 8192
+    // weight rows on the persistent grid (GHIP_GEMV_WGS workgroups of 8 teams,
+    // each team an equal run of consecutive rows; "_r1x0").  Off by default:
+    // 4096 -> 14336 measured 10.1 us at 256 or 512 workgroups (15.2 at 128)
+    // against 9.8 us for the 448-workgroup grid.
+    const bool persist = q4k && p.wtype == GHIP_TYPE_Q4_K && p.M == 1 && waves_k == 1 && fused && !sub &&
+                         p.N >= 8192 && env_int("GHIP_GEMV_PERSIST", 0) != 0;
+    const int rb = persist ? 1 : q4k ? env_int("GHIP_GEMV_RB", rb_d) : 8;
+    const int ng = persist ? 0 : q4k ? env_int("GHIP_GEMV_NG", ng_d) : 1;
+    if (q4k && !persist && !((rb == 2 && (ng == 2 || ng == 4 || ng == 8)) || (rb == 4 && (ng == 2 || ng == 4)) ||
                  (rb == 1 && p.wtype == GHIP_TYPE_Q4_K && p.M == 1 && (ng == 2 || ng == 4 || ng == 8)) ||
                  (p.wtype == GHIP_TYPE_Q6_K && p.M == 1 && ((rb == 2 && ng == 8) || (rb == 1 && (ng == 4 || ng == 8))))))
         return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "GHIP_GEMV_RB x GHIP_GEMV_NG must be 2x2, 2x4, 2x8, 4x2 or 4x4");
@@ -494,8 +501,9 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     // (there, fewer and fuller workgroups quantize the activation fewer times)
     const int dflt_teams = p.N < 8192 && p.M <= 2 ? 4 : 8;
     const int teams = q4k ? std::max(1, std::min(8 / waves_k, env_int("GHIP_GEMV_TEAMS", dflt_teams))) : 1;
-    const int rows_per_wg = rows_per_team * teams;
-    const unsigned grid = (unsigned)((p.N + rows_per_wg - 1) / rows_per_wg);
+    const int rows_per_wg = persist ? 0 : rows_per_team * teams;
+    const unsigned grid = persist ? (unsigned)std::max(1, std::min(env_int("GHIP_GEMV_WGS", 256), (int)((p.N + 7) / 8)))
+                                  : (unsigned)((p.N + rows_per_wg - 1) / rows_per_wg);
     for (int64_t c0 = 0; c0 < p.M; c0 += 8) {
         const int nc = (int)std::min<int64_t>(8, p.M - c0);
         const int NC = nc == 1 ? 1 : nc == 2 ? 2 : nc <= 4 ? 4 : 8;

@@ -74,12 +74,20 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
                                               int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
                                               int ncols, float *__restrict__ dst, int64_t ldd,
                                               int32_t *__restrict__ sub, int n_mat, int wg = -1) {
+    // NG == 0: persistent grid (one row per group, K in one wavefront): each
+    // team takes ceil(rows / (teams in the grid)) consecutive rows, streamed
+    // through the two register slots, so every wavefront of the grid carries
+    // the same number of rows and the activation row is quantized once per
+    // workgroup
+    constexpr bool PERSIST = NG == 0;
+    static_assert(!PERSIST || RB == 1, "persistent teams stream one row per group");
     constexpr int RPT = RB * NG;  // rows per team
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nwk = (nb + 15) >> 4;                // wavefronts per K-team
     const int T = (blockDim.x >> 6) / nwk;         // row teams
+    const int rpt = PERSIST ? (rows + (int)gridDim.x * T - 1) / ((int)gridDim.x * T) : RPT;
     const int team = wave / nwk, w = wave - team * nwk;
     const int K = nb * QK_K;
     int8_t *codes = reinterpret_cast<int8_t *>(smem);
@@ -90,9 +98,9 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
     const int b = 16 * w + (lane >> 2), i = lane & 3;
     const bool valid = b < nb;
     // wg: this workgroup's index within the matrix (-1: blockIdx.x)
-    const int rw0 = (wg < 0 ? (int)blockIdx.x : wg) * T * RPT;  // first row of the workgroup (uniform)
-    const int r0 = rw0 + team * RPT;       // first row of the team (uniform)
-    const int r1 = min(rows, r0 + RPT);
+    const int rw0 = (wg < 0 ? (int)blockIdx.x : wg) * T * rpt;  // first row of the workgroup (uniform)
+    const int r0 = rw0 + team * rpt;       // first row of the team (uniform)
+    const int r1 = min(rows, r0 + rpt);
 
     // Branch-free weight loads from a uniform row base: rows past the tile and
     // lanes past the row re-read a valid block (clamped index) and contribute
@@ -107,7 +115,7 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
     // groups in flight and computes its early rows while its later rows are
     // still on the way (with every group loaded up front, most data would
     // land at the end and all of the arithmetic would follow the last byte).
-    constexpr int NS = NG < 2 ? NG : 2;  // register slots
+    constexpr int NS = PERSIST ? 2 : NG < 2 ? NG : 2;  // register slots
     uint4 hdr[NS][RB], qa[NS][RB], qb[NS][RB];
     uint4 xh0[NS][Q5 ? RB : 1], xh1[NS][Q5 ? RB : 1];  // Q5_K qh[0..15], qh[16..31]
     auto load_group = [&](int gi, int slot) {
@@ -255,11 +263,24 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
             }
         }
     };
+    if constexpr (PERSIST) {
+        const int nrow = max(0, r1 - r0);
+        for (int gi = 0; gi < nrow; gi += 2) {
+            compute_group(r0 + gi, hdr[0], qa[0], qb[0], xh0[0], xh1[0]);
+            if (gi + 2 < nrow) load_group(gi + 2, 0);
+            if (gi + 1 < nrow) {
+                compute_group(r0 + gi + 1, hdr[1], qa[1], qb[1], xh0[1], xh1[1]);
+                if (gi + 3 < nrow) load_group(gi + 3, 1);
+            }
+        }
+        return;  // (the host launches it with K in one wavefront)
+    } else {
 #pragma unroll
-    for (int gi = 0; gi < NG; gi++) {
-        const int sl = gi % NS;
-        if (r0 + gi * RB < r1) compute_group(r0 + gi * RB, hdr[sl], qa[sl], qb[sl], xh0[sl], xh1[sl]);
-        if (gi + NS < NG && r0 + (gi + NS) * RB < r1) load_group(gi + NS, sl);
+        for (int gi = 0; gi < NG; gi++) {
+            const int sl = gi % NS;
+            if (r0 + gi * RB < r1) compute_group(r0 + gi * RB, hdr[sl], qa[sl], qb[sl], xh0[sl], xh1[sl]);
+            if (gi + NS < NG && r0 + (gi + NS) * RB < r1) load_group(gi + NS, sl);
+        }
     }
     if (nwk == 1) return;
     __syncthreads();
@@ -937,7 +958,7 @@ GEMV_PAIR_ALL(ghip_gemv_q8_0, gemv_q8_0_impl)
 // register row groups (RB rows) x groups in flight (NG)
 #define Q4K_INST_RB(NC) Q4K_INST(NC, 2, 2) Q4K_INST(NC, 2, 4) Q4K_INST(NC, 4, 2) Q4K_INST(NC, 2, 8) Q4K_INST(NC, 4, 4)
 Q4K_INST_RB(1) Q4K_INST_RB(2) Q4K_INST_RB(4) Q4K_INST_RB(8)
-Q4K_INST(1, 1, 4) Q4K_INST(1, 1, 8) Q4K_INST(1, 1, 2)
+Q4K_INST(1, 1, 4) Q4K_INST(1, 1, 8) Q4K_INST(1, 1, 2) Q4K_INST(1, 1, 0)
 // Q5_K: the same shapes and naming as Q4_K
 #define Q5K_INST_RB(NC) QK45_INST(q5_K, true, NC, 2, 2) QK45_INST(q5_K, true, NC, 2, 4) \
     QK45_INST(q5_K, true, NC, 4, 2) QK45_INST(q5_K, true, NC, 2, 8) QK45_INST(q5_K, true, NC, 4, 4)

@@ -348,3 +348,14 @@ def test_split_k_repeat_and_graph(be, ty, n, rows):
         assert torch.equal(be.mul_mat(wd, ty, n, xd), first)
     want, _, _ = O.mul_mat(ty, w, n, rows, x, 8)
     assert rel_err(first.cpu().numpy(), want) <= TOL
+
+
+@pytest.mark.parametrize("rows,wgs", [(14336, "256"), (8200, "256"), (9000, "7"), (8192, "100000")])
+def test_gemv_persistent_grid(be, monkeypatch, rows, wgs):
+    """Q4_K at one activation row from 8192 weight rows on the persistent grid
+    (GHIP_GEMV_PERSIST=1; GHIP_GEMV_WGS workgroups, every team an equal run of
+    rows; teams past the last row compute nothing): ragged row counts and grid
+    sizes against the oracle, sub-sums through the non-persistent kernel."""
+    monkeypatch.setenv("GHIP_GEMV_PERSIST", "1")
+    monkeypatch.setenv("GHIP_GEMV_WGS", wgs)
+    run_case(be, O.Q4_K, 4096, rows, 1, seed=rows)

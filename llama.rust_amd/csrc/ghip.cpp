@@ -32,7 +32,10 @@ TypeInfo type_info(int t) {
     case GHIP_TYPE_F32: return {1, 4};
     case GHIP_TYPE_F16: return {1, 2};
     case GHIP_TYPE_Q4_0: return {32, 18};
+    case GHIP_TYPE_Q4_1: return {32, 20};
     case GHIP_TYPE_Q5_0: return {32, 22};
+    case GHIP_TYPE_Q5_1: return {32, 24};
+    case GHIP_TYPE_Q8_1: return {32, 36};
     case GHIP_TYPE_Q8_0: return {32, 34};
     case GHIP_TYPE_Q4_K: return {256, 144};
     case GHIP_TYPE_Q5_K: return {256, 176};
@@ -239,13 +242,17 @@ bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b,
     st = GHIP_STATUS_BACKEND_ERROR;
     if (!a || !b) { st = ctx->fail(st, "mul_mat: null operand"); return false; }
     if (a->type != GHIP_TYPE_Q4_0 && a->type != GHIP_TYPE_Q5_0 && a->type != GHIP_TYPE_Q8_0 &&
-        a->type != GHIP_TYPE_Q4_K && a->type != GHIP_TYPE_Q5_K && a->type != GHIP_TYPE_Q6_K) {
-        st = ctx->fail(st, "mul_mat: src0 type %d not supported (Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)", a->type);
+        a->type != GHIP_TYPE_Q4_K && a->type != GHIP_TYPE_Q5_K && a->type != GHIP_TYPE_Q6_K &&
+        a->type != GHIP_TYPE_Q4_1 && a->type != GHIP_TYPE_Q5_1) {
+        st = ctx->fail(st, "mul_mat: src0 type %d not supported (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K)",
+                       a->type);
         return false;
     }
     const TypeInfo ti = type_info(a->type);
     const bool q8_0_dot = a->type == GHIP_TYPE_Q4_0 || a->type == GHIP_TYPE_Q5_0 || a->type == GHIP_TYPE_Q8_0;
-    const int vdt = q8_0_dot ? GHIP_TYPE_Q8_0 : GHIP_TYPE_Q8_K;  // vec_dot_type (vec_dot.rs vec_dot_type)
+    const bool q8_1_dot = a->type == GHIP_TYPE_Q4_1 || a->type == GHIP_TYPE_Q5_1;
+    // vec_dot_type (vec_dot.rs vec_dot_type)
+    const int vdt = q8_0_dot ? GHIP_TYPE_Q8_0 : q8_1_dot ? GHIP_TYPE_Q8_1 : GHIP_TYPE_Q8_K;
     if (b->type != GHIP_TYPE_F32 && b->type != vdt) {
         st = ctx->fail(st, "mul_mat: src1 must be F32 or the vec_dot type of src0 (backend.rs:2057-2066)");
         return false;
@@ -278,6 +285,10 @@ bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b,
         p.act_type = GHIP_TYPE_Q8_0;
         p.act_row_bytes = p.K / 32 * 34;
         p.n_mat = 0;
+    } else if (q8_1_dot) {
+        p.act_type = GHIP_TYPE_Q8_1;
+        p.act_row_bytes = p.K / 32 * 36;
+        p.n_mat = 0;
     } else {
         p.act_type = GHIP_TYPE_Q8_K;
         p.act_row_bytes = p.K / 256 * 292;
@@ -302,8 +313,9 @@ ghip_status quantize_act(ghip_context *ctx, const MulMatPlan &p, const ghip_tens
     }
     const int64_t blocks = p.M * (p.K / 32);
     const unsigned grid = (unsigned)((blocks * 8 + 255) / 256);
-    return ctx->launch("ghip_quantize_q8_0", dim3(grid), dim3(256), 0, s, (const float *)b->data, x_stride,
-                       (int64_t)p.K, (int64_t)p.M, (uint8_t *)out, (int64_t)p.act_row_bytes);
+    return ctx->launch(p.act_type == GHIP_TYPE_Q8_1 ? "ghip_quantize_q8_1" : "ghip_quantize_q8_0", dim3(grid),
+                       dim3(256), 0, s, (const float *)b->data, x_stride, (int64_t)p.K, (int64_t)p.M, (uint8_t *)out,
+                       (int64_t)p.act_row_bytes);
 }
 
 const char *gemv_base(int wtype) {
@@ -313,6 +325,8 @@ const char *gemv_base(int wtype) {
     case GHIP_TYPE_Q6_K: return "ghip_gemv_q6_K";
     case GHIP_TYPE_Q5_0: return "ghip_gemv_q5_0";
     case GHIP_TYPE_Q8_0: return "ghip_gemv_q8_0";
+    case GHIP_TYPE_Q4_1: return "ghip_gemv_q4_1";
+    case GHIP_TYPE_Q5_1: return "ghip_gemv_q5_1";
     default: return "ghip_gemv_q4_0";
     }
 }
@@ -472,6 +486,8 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     int waves_k;
     if (gemv_pair(p.wtype))
         waves_k = (int)(((p.nb + 1) / 2 + 63) / 64);
+    else if (p.wtype == GHIP_TYPE_Q4_1 || p.wtype == GHIP_TYPE_Q5_1)  // one lane per 32-block
+        waves_k = (int)((p.nb + 63) / 64);
     else if (gemv_v2(p))
         waves_k = (int)((p.nb + 15) / 16);
     else

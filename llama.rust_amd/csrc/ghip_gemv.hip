@@ -898,6 +898,108 @@ __device__ __forceinline__ void gemv_q8_0_impl(const uint8_t *__restrict__ W, in
                                                    wg);
 }
 
+// ---------------------------------------------------------------- Q4_1 / Q5_1 x Q8_1
+// One lane per 32-block, RB rows per workgroup (all rows' loads issued before
+// any is consumed), Q8_1 activation rows quantized by ghip_quantize_q8_1.
+// vec_dot_q4_1_q8_1 / vec_dot_q5_1_q8_1 (vec_dot.rs:620-720): per block the
+// exact integer sum of the unsigned codes (nibble, | bit e of qh << 4 for
+// Q5_1) times the Q8_1 codes, scaled as (d_w * d_x) * sumi + m_w * s_x.
+constexpr int WT_Q4_1 = 3, WT_Q5_1 = 7;
+template <int WT, int NC, bool SUBSUMS>
+__device__ __forceinline__ void gemv_q41_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb,
+                                              const uint8_t *__restrict__ act, int64_t act_row_bytes, int ncols,
+                                              float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
+    constexpr int BB = WT == WT_Q4_1 ? 20 : 24;  // block bytes: d, m, (qh), qs[16]
+    __shared__ float red[RB * 8 * NC];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int b = 64 * w + lane;
+    const bool valid = b < nb;
+    const int r0 = (int)blockIdx.x * RB;
+    const int nr = min(RB, rows - r0);
+    uint32_t wq[RB][6];
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+#pragma unroll
+        for (int k = 0; k < 6; k++) wq[rr][k] = 0;
+        if (rr < nr && valid) {
+            const uint8_t *p = W + (int64_t)(r0 + rr) * w_row_bytes + (int64_t)b * BB;
+            const uint4 a = ld16(p);
+            wq[rr][0] = a.x; wq[rr][1] = a.y; wq[rr][2] = a.z; wq[rr][3] = a.w;
+            if constexpr (WT == WT_Q4_1) {
+                wq[rr][4] = ld4(p + 16);
+            } else {
+                const uint2 c = ld8(p + 16);
+                wq[rr][4] = c.x; wq[rr][5] = c.y;
+            }
+        }
+    }
+    uint4 yl[NC], yh[NC];
+    float dx[NC], sx[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        yl[c] = yh[c] = make_uint4(0, 0, 0, 0);
+        dx[c] = sx[c] = 0.0f;
+        if (c < ncols && valid) {
+            const uint8_t *A = act + c * act_row_bytes + (int64_t)b * 36;
+            const uint32_t ds = ld4(A);
+            dx[c] = h2f(ds);
+            sx[c] = h2f(ds >> 16);
+            yl[c] = ld16(A + 4);
+            yh[c] = ld16(A + 20);
+        }
+    }
+    float part[NC][RB];
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        const float dw = h2f(wq[rr][0]), mw = h2f(wq[rr][0] >> 16);
+        uint32_t qs[4], qh = 0;
+        if constexpr (WT == WT_Q4_1) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) qs[k] = wq[rr][1 + k];
+        } else {
+            qh = wq[rr][1];
+#pragma unroll
+            for (int k = 0; k < 4; k++) qs[k] = wq[rr][2 + k];
+        }
+        // elements 4k..4k+3 (low nibbles) and 16+4k.. (high nibbles)
+        uint32_t q[8];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            q[k] = qs[k] & 0x0f0f0f0fu;
+            q[4 + k] = (qs[k] >> 4) & 0x0f0f0f0fu;
+            if constexpr (WT == WT_Q5_1) {
+                q[k] |= spread4_bit4(__builtin_amdgcn_ubfe(qh, 4 * k, 4));
+                q[4 + k] |= spread4_bit4(__builtin_amdgcn_ubfe(qh, 16 + 4 * k, 4));
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int si = dot4(q[7], yh[c].w, dot4(q[6], yh[c].z, dot4(q[5], yh[c].y, dot4(q[4], yh[c].x,
+                           dot4(q[3], yl[c].w, dot4(q[2], yl[c].z, dot4(q[1], yl[c].y, dot4(q[0], yl[c].x, 0))))))));
+            if (SUBSUMS && c < ncols && rr < nr && valid) sub[((int64_t)c * rows + r0 + rr) * nb + b] = si;
+            part[c][rr] = valid ? fmaf(dw * dx[c], (float)si, mw * sx[c]) : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NC; c++) stash_rows(red, part[c], lane, w, nw, c, NC);
+    finish_rows(red, r0, nr, ncols, NC, nw, dst, ldd);
+}
+#define GEMV_Q41_INST(TN, WT, NC)                                                                                \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_##TN##_c##NC(                                    \
+        const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb, const uint8_t *__restrict__ act,   \
+        int64_t act_row_bytes, int ncols, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {     \
+        gemv_q41_impl<WT, NC, false>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub);       \
+    }                                                                                                            \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_##TN##_sub_c##NC(                                \
+        const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb, const uint8_t *__restrict__ act,   \
+        int64_t act_row_bytes, int ncols, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {     \
+        gemv_q41_impl<WT, NC, true>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub);        \
+    }
+GEMV_Q41_INST(q4_1, WT_Q4_1, 1) GEMV_Q41_INST(q4_1, WT_Q4_1, 2) GEMV_Q41_INST(q4_1, WT_Q4_1, 4)
+GEMV_Q41_INST(q4_1, WT_Q4_1, 8)
+GEMV_Q41_INST(q5_1, WT_Q5_1, 1) GEMV_Q41_INST(q5_1, WT_Q5_1, 2) GEMV_Q41_INST(q5_1, WT_Q5_1, 4)
+GEMV_Q41_INST(q5_1, WT_Q5_1, 8)
+
 #define GEMV_ARGS                                                                                     \
     const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb, const uint8_t *__restrict__ act, \
         int64_t act_row_bytes, int ncols, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub

@@ -75,3 +75,46 @@ ghip_quantize_q8_0(const float *__restrict__ x, int64_t x_stride, int64_t n, int
         __builtin_memcpy(blk, &dh, 2);
     }
 }
+
+// f32 rows -> Q8_1 blocks (36 B: f16 d, f16 s, int8 qs[32]), quantize_row_q8_1
+// (quants.rs:375-397): d = amax / 127, id = 1 / d (0 if d == 0),
+// q = round-half-even(x * id) saturated to int8 with NaN -> 0 (a Rust `as i8`),
+// s = f16(sum(q) * d).  8 lanes per block, 4 elements each.
+extern "C" __global__ void __launch_bounds__(256)
+ghip_quantize_q8_1(const float *__restrict__ x, int64_t x_stride, int64_t n, int64_t nrows,
+                   uint8_t *__restrict__ y, int64_t y_stride) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nb = n / 32;
+    const int64_t blk_id = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;
+    const int sub = lane & 7;
+    if (blk_id >= nrows * nb) return;  // whole 8-lane groups exit together
+    const int64_t row = blk_id / nb, b = blk_id - row * nb;
+    float xs[4];
+    __builtin_memcpy(xs, x + row * x_stride + b * 32 + sub * 4, 16);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) amax = fmaxf(amax, fabsf(xs[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    const float d = __fdiv_rn(amax, 127.0f);
+    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    uint32_t packed = 0;
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float r = rintf(__fmul_rn(xs[i], id));
+        const int v = r != r ? 0 : r >= 127.0f ? 127 : r <= -128.0f ? -128 : (int)r;
+        sum += v;
+        packed |= (uint32_t)(v & 0xff) << (8 * i);
+    }
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    sum += __shfl_xor(sum, 4, 64);
+    uint8_t *blk = y + row * y_stride + b * 36;
+    __builtin_memcpy(blk + 4 + sub * 4, &packed, 4);
+    if (sub == 0) {
+        const uint32_t ds = (uint32_t)f2h_rn(d) | ((uint32_t)f2h_rn(__fmul_rn((float)sum, d)) << 16);
+        __builtin_memcpy(blk, &ds, 4);
+    }
+}

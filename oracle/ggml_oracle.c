@@ -8,6 +8,7 @@
  */
 #include "ggml_oracle.h"
 
+#include <float.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -30,6 +31,9 @@ typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } blk_q8_K;       /
 typedef struct { uint8_t e; uint8_t qs[16]; } blk_mxfp4;                        /* 17 B  */
 typedef struct { uint16_t d; uint8_t qh[4]; uint8_t qs[16]; } blk_q5_0;        /* 22 B  */
 typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; } blk_q5_K; /* 176 B */
+typedef struct { uint16_t d, m; uint8_t qs[16]; } blk_q4_1;                    /* 20 B  */
+typedef struct { uint16_t d, m; uint8_t qh[4]; uint8_t qs[16]; } blk_q5_1;     /* 24 B  */
+typedef struct { uint16_t d, s; int8_t qs[32]; } blk_q8_1;                     /* 36 B  */
 
 _Static_assert(sizeof(blk_q4_0) == 18, "q4_0");
 _Static_assert(sizeof(blk_q8_0) == 34, "q8_0");
@@ -39,6 +43,9 @@ _Static_assert(sizeof(blk_q8_K) == 292, "q8_K");
 _Static_assert(sizeof(blk_mxfp4) == 17, "mxfp4");
 _Static_assert(sizeof(blk_q5_0) == 22, "q5_0");
 _Static_assert(sizeof(blk_q5_K) == 176, "q5_K");
+_Static_assert(sizeof(blk_q4_1) == 20, "q4_1");
+_Static_assert(sizeof(blk_q5_1) == 24, "q5_1");
+_Static_assert(sizeof(blk_q8_1) == 36, "q8_1");
 
 double oracle_wtime(void) {
     struct timespec ts;
@@ -179,6 +186,100 @@ void oracle_quantize_row_q8_0_ref(const float *x, void *vy, int64_t k) {
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         y[i].d = F2H(d);
         for (int j = 0; j < QK8_0; j++) y[i].qs[j] = (int8_t)roundf(x[i * QK8_0 + j] * id);
+    }
+}
+
+/* Rust `f as i32` / `f as u8`: truncation toward zero, saturating, NaN -> 0 */
+static inline int32_t sat_i32(float f) {
+    if (f != f) return 0;
+    if (f >= 2147483647.0f) return 2147483647;
+    if (f <= -2147483648.0f) return (int32_t)0x80000000u;
+    return (int32_t)f;
+}
+static inline uint8_t sat_u8(float f) {
+    if (f != f || f <= 0.0f) return 0;
+    if (f >= 255.0f) return 255;
+    return (uint8_t)f;
+}
+static inline int8_t sat_i8(float f) {
+    if (f != f) return 0;
+    if (f >= 127.0f) return 127;
+    if (f <= -128.0f) return -128;
+    return (int8_t)f;
+}
+
+/* quants.rs:29-41 minmax: NaN never replaces either bound */
+static void minmax32(const float *x, float *mn, float *mx) {
+    float lo = FLT_MAX, hi = -FLT_MAX;
+    for (int j = 0; j < 32; j++) {
+        if (x[j] < lo) lo = x[j];
+        if (x[j] > hi) hi = x[j];
+    }
+    *mn = lo;
+    *mx = hi;
+}
+
+/* quants.rs:169-187 quantize_row_q4_1_ref */
+void oracle_quantize_row_q4_1_ref(const float *x, void *vy, int64_t k) {
+    blk_q4_1 *y = (blk_q4_1 *)vy;
+    for (int64_t i = 0; i < k / 32; i++) {
+        float mn, mx;
+        minmax32(x + i * 32, &mn, &mx);
+        const float d = (mx - mn) / 15.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        for (int j = 0; j < 16; j++) {
+            const float x0 = (x[i * 32 + j] - mn) * id, x1 = (x[i * 32 + 16 + j] - mn) * id;
+            int32_t a = sat_i32(x0 + 0.5f), b = sat_i32(x1 + 0.5f);
+            a = a < 15 ? a : 15;
+            a = a > 0 ? a : 0;
+            b = b < 15 ? b : 15;
+            b = b > 0 ? b : 0;
+            y[i].qs[j] = (uint8_t)(a | (b << 4));
+        }
+        y[i].d = F2H(d);
+        y[i].m = F2H(mn);
+    }
+}
+
+/* quants.rs:260-286 quantize_row_q5_1_ref */
+void oracle_quantize_row_q5_1_ref(const float *x, void *vy, int64_t k) {
+    blk_q5_1 *y = (blk_q5_1 *)vy;
+    for (int64_t i = 0; i < k / 32; i++) {
+        float mn, mx;
+        minmax32(x + i * 32, &mn, &mx);
+        const float d = (mx - mn) / 31.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint32_t qh = 0;
+        for (int j = 0; j < 16; j++) {
+            const float x0 = (x[i * 32 + j] - mn) * id, x1 = (x[i * 32 + 16 + j] - mn) * id;
+            const uint8_t a = sat_u8(x0 + 0.5f), b = sat_u8(x1 + 0.5f);
+            y[i].qs[j] = (uint8_t)((a & 0x0F) | ((b & 0x0F) << 4));
+            qh |= (uint32_t)((a & 0x10) >> 4) << j;
+            qh |= (uint32_t)((b & 0x10) >> 4) << (j + 16);
+        }
+        memcpy(y[i].qh, &qh, 4);
+        y[i].d = F2H(d);
+        y[i].m = F2H(mn);
+    }
+}
+
+/* quants.rs:375-397 quantize_row_q8_1_ref (= quantize_row_q8_1): d = amax / 127,
+ * id = 1 / d, q = round-half-even(x * id) saturated to i8 (NaN -> 0),
+ * s = f16(sum(q) * d) */
+void oracle_quantize_row_q8_1(const float *x, void *vy, int64_t k) {
+    blk_q8_1 *y = (blk_q8_1 *)vy;
+    for (int64_t i = 0; i < k / 32; i++) {
+        float amax = 0.0f;
+        for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(x[i * 32 + j]));
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        int32_t sum = 0;
+        for (int j = 0; j < 32; j++) {
+            y[i].qs[j] = sat_i8(rintf(x[i * 32 + j] * id));
+            sum += y[i].qs[j];
+        }
+        y[i].d = F2H(d);
+        y[i].s = F2H((float)sum * d);
     }
 }
 
@@ -623,7 +724,43 @@ static inline void isum_q5_K(const blk_q5_K *x, const blk_q8_K *y, int32_t *iacc
     *imin = im;
 }
 
+/* q5_1 value e of a 32-block: nibble | bit e of qh << 4 (unsigned) */
+static inline int q5_1_val(const blk_q5_1 *x, int e) {
+    uint32_t qh;
+    memcpy(&qh, x->qh, 4);
+    const int lo = e < 16 ? (x->qs[e] & 0x0F) : (x->qs[e - 16] >> 4);
+    return lo | (int)(((qh >> e) & 1) << 4);
+}
+static inline int q4_1_val(const blk_q4_1 *x, int e) { return e < 16 ? (x->qs[e] & 0x0F) : (x->qs[e - 16] >> 4); }
+/* the exact integer sums of one 32-block (unsigned codes x q8_1 codes) */
+static inline int32_t isum_q4_1(const blk_q4_1 *x, const blk_q8_1 *y) {
+    int32_t s = 0;
+    for (int e = 0; e < 32; e++) s += q4_1_val(x, e) * y->qs[e];
+    return s;
+}
+static inline int32_t isum_q5_1(const blk_q5_1 *x, const blk_q8_1 *y) {
+    int32_t s = 0;
+    for (int e = 0; e < 32; e++) s += q5_1_val(x, e) * y->qs[e];
+    return s;
+}
+
 void oracle_dequantize_row(int type, const void *vx, float *y, int64_t k) {
+    if (type == OR_Q4_1 || type == OR_Q5_1) { /* quants.rs:189-202, :288-304: x * d + m */
+        for (int64_t i = 0; i < k / 32; i++) {
+            const blk_q4_1 *a = (const blk_q4_1 *)vx + i;
+            const blk_q5_1 *b = (const blk_q5_1 *)vx + i;
+            const float d = H2F(type == OR_Q4_1 ? a->d : b->d), m = H2F(type == OR_Q4_1 ? a->m : b->m);
+            for (int e = 0; e < 32; e++)
+                y[i * 32 + e] = (float)(type == OR_Q4_1 ? q4_1_val(a, e) : q5_1_val(b, e)) * d + m;
+        }
+        return;
+    }
+    if (type == OR_Q8_1) { /* qs * d */
+        const blk_q8_1 *x = (const blk_q8_1 *)vx;
+        for (int64_t i = 0; i < k / 32; i++)
+            for (int j = 0; j < 32; j++) y[i * 32 + j] = (float)x[i].qs[j] * H2F(x[i].d);
+        return;
+    }
     if (type == OR_Q4_0) {
         const blk_q4_0 *x = (const blk_q4_0 *)vx;
         for (int64_t i = 0; i < k / QK4_0; i++) {
@@ -882,6 +1019,42 @@ float oracle_vec_dot_q6_K_q8_K(int n, const void *vx, const void *vy) {
 }
 
 /* vec_dot.rs:661-686: lane l holds elements 4l..4l+3, one fma per block */
+/* vec_dot.rs:620-650 vec_dot_q4_1_q8_1 (the AVX2 kernel's order, as its
+ * scalar twin): 8 lane accumulators acc[l] = fma(dx*dy, q_l, acc[l]) over the
+ * 4-element lanes, summs = fma(m, s, summs), result hsum8(acc) + summs */
+float oracle_vec_dot_q4_1_q8_1(int n, const void *vx, const void *vy) {
+    const blk_q4_1 *x = (const blk_q4_1 *)vx;
+    const blk_q8_1 *y = (const blk_q8_1 *)vy;
+    float acc[8] = {0}, summs = 0.0f;
+    for (int ib = 0; ib < n / 32; ib++) {
+        const float d0d1 = H2F(x[ib].d) * H2F(y[ib].d);
+        summs = fmaf(H2F(x[ib].m), H2F(y[ib].s), summs);
+        for (int l = 0; l < 8; l++) {
+            int32_t q = 0;
+            for (int i = 0; i < 4; i++) q += q4_1_val(&x[ib], 4 * l + i) * y[ib].qs[4 * l + i];
+            acc[l] = fmaf(d0d1, (float)q, acc[l]);
+        }
+    }
+    return hsum8(acc) + summs;
+}
+
+/* vec_dot.rs:687-720 vec_dot_q5_1_q8_1: as q4_1 with the fifth bit */
+float oracle_vec_dot_q5_1_q8_1(int n, const void *vx, const void *vy) {
+    const blk_q5_1 *x = (const blk_q5_1 *)vx;
+    const blk_q8_1 *y = (const blk_q8_1 *)vy;
+    float acc[8] = {0}, summs = 0.0f;
+    for (int ib = 0; ib < n / 32; ib++) {
+        const float dxdy = H2F(x[ib].d) * H2F(y[ib].d);
+        summs = fmaf(H2F(x[ib].m), H2F(y[ib].s), summs);
+        for (int l = 0; l < 8; l++) {
+            int32_t q = 0;
+            for (int i = 0; i < 4; i++) q += q5_1_val(&x[ib], 4 * l + i) * y[ib].qs[4 * l + i];
+            acc[l] = fmaf(dxdy, (float)q, acc[l]);
+        }
+    }
+    return hsum8(acc) + summs;
+}
+
 float oracle_vec_dot_q5_0_q8_0(int n, const void *vx, const void *vy) {
     const blk_q5_0 *x = (const blk_q5_0 *)vx;
     const blk_q8_0 *y = (const blk_q8_0 *)vy;
@@ -966,6 +1139,7 @@ static int route_of(int type, int64_t rows, int64_t cols) {
 }
 
 static size_t act_row_size(int type, int64_t n) {
+    if (type == OR_Q4_1 || type == OR_Q5_1) return (size_t)(n / 32) * sizeof(blk_q8_1);
     return (type == OR_Q4_0 || type == OR_Q5_0 || type == OR_Q8_0) ? (size_t)(n / 32) * sizeof(blk_q8_0)
                                                                    : (size_t)(n / QK_K) * sizeof(blk_q8_K);
 }
@@ -980,6 +1154,8 @@ int oracle_mul_mat_act(int type, int64_t n, int64_t rows, const float *x, int64_
         uint8_t *dst = (uint8_t *)act + (size_t)c * rs;
         if (type == OR_Q4_0 || type == OR_Q5_0 || type == OR_Q8_0)
             oracle_quantize_row_q8_0(x + c * n, dst, n);
+        else if (type == OR_Q4_1 || type == OR_Q5_1)  /* vec_dot_type Q8_1 */
+            oracle_quantize_row_q8_1(x + c * n, dst, n);
         else if (type == OR_Q4_K && route == ORACLE_ROUTE_REPACK && c < nr4)
             oracle_quantize_row_q8_K_mat(x + c * n, dst, n);
         else
@@ -994,7 +1170,7 @@ int oracle_mul_mat(int type, const void *w, int64_t n, int64_t rows, const float
     if (route_out) *route_out = route;
     if (route < 0) return -1;
     if (type != OR_Q4_0 && type != OR_Q4_K && type != OR_Q6_K && type != OR_Q5_0 && type != OR_Q8_0 &&
-        type != OR_Q5_K)
+        type != OR_Q5_K && type != OR_Q4_1 && type != OR_Q5_1)
         return -2;
     const size_t rs = act_row_size(type, n);
     uint8_t *act = (uint8_t *)malloc(rs * (size_t)cols);
@@ -1073,6 +1249,25 @@ int oracle_mul_mat(int type, const void *w, int64_t n, int64_t rows, const float
                 else if (route == ORACLE_ROUTE_TILED) v = acc;
                 else v = oracle_vec_dot_q4_K_q8_K((int)n, wr, a);
                 out[c * rows + r] = v;
+            }
+        }
+    } else if (type == OR_Q4_1 || type == OR_Q5_1) {
+        /* the row vec_dot at every column count: tinyBLAS does not take Q4_1 /
+         * Q5_1 (tinyblas.rs:1327-1328) and no repack exists for them */
+        const int64_t nb = n / 32;
+        const size_t wbs = type == OR_Q4_1 ? sizeof(blk_q4_1) : sizeof(blk_q5_1);
+#pragma omp parallel for num_threads(nth) schedule(static)
+        for (int64_t r = 0; r < rows; r++) {
+            const uint8_t *wr = (const uint8_t *)w + (size_t)r * nb * wbs;
+            for (int64_t c = 0; c < cols; c++) {
+                const blk_q8_1 *a = (const blk_q8_1 *)(act + (size_t)c * rs);
+                if (subsums)
+                    for (int64_t b = 0; b < nb; b++)
+                        subsums[((size_t)c * rows + r) * nb + b] =
+                            type == OR_Q4_1 ? isum_q4_1((const blk_q4_1 *)wr + b, &a[b])
+                                            : isum_q5_1((const blk_q5_1 *)wr + b, &a[b]);
+                out[c * rows + r] = type == OR_Q4_1 ? oracle_vec_dot_q4_1_q8_1((int)n, wr, a)
+                                                    : oracle_vec_dot_q5_1_q8_1((int)n, wr, a);
             }
         }
     } else if (type == OR_Q5_0 || type == OR_Q8_0) {

@@ -22,7 +22,8 @@ extern "C" {
 
 /* ggml type ids (crates/ggml/src/types.rs:15) */
 enum {
-    OR_F32 = 0, OR_F16 = 1, OR_Q4_0 = 2, OR_Q5_0 = 6, OR_Q8_0 = 8, OR_Q4_K = 12,
+    OR_F32 = 0, OR_F16 = 1, OR_Q4_0 = 2, OR_Q4_1 = 3, OR_Q5_0 = 6, OR_Q5_1 = 7, OR_Q8_0 = 8, OR_Q8_1 = 9,
+    OR_Q4_K = 12,
     OR_Q5_K = 13, OR_Q6_K = 14, OR_Q8_K = 15, OR_MXFP4 = 39
 };
 
@@ -37,6 +38,9 @@ void oracle_quantize_row_q4_0_ref(const float *x, void *y, int64_t k);  /* quant
 void oracle_quantize_row_q4_K_ref(const float *x, void *y, int64_t k);  /* quants_k.rs:1861; quants_ref.bin */
 void oracle_quantize_row_q6_K_ref(const float *x, void *y, int64_t k);  /* quants_k.rs:2058; quants_ref.bin */
 void oracle_quantize_row_q5_0_ref(const float *x, void *y, int64_t k);  /* quants.rs:207; quants_ref.bin */
+void oracle_quantize_row_q4_1_ref(const float *x, void *y, int64_t k);  /* quants.rs:169; quants_ref.bin type 3 */
+void oracle_quantize_row_q5_1_ref(const float *x, void *y, int64_t k);  /* quants.rs:260; quants_ref.bin type 7 */
+void oracle_quantize_row_q8_1(const float *x, void *y, int64_t k);      /* quants.rs:375; quants_ref.bin type 9 */
 void oracle_quantize_row_q5_K_ref(const float *x, void *y, int64_t k);  /* quants_k.rs:1952; quants_ref.bin */
 void oracle_quantize_row_mxfp4_ref(const float *x, void *y, int64_t k); /* absent in the reference; quants_ref_fp4.bin */
 void oracle_quantize_row_q8_0_ref(const float *x, void *y, int64_t k);  /* quants.rs:302; quants_ref.bin */
@@ -55,6 +59,8 @@ float oracle_vec_dot_q4_0_q8_0(int n, const void *x, const void *y);  /* vec_dot
 float oracle_vec_dot_q4_K_q8_K(int n, const void *x, const void *y);  /* vec_dot.rs:872 */
 float oracle_vec_dot_q6_K_q8_K(int n, const void *x, const void *y);  /* vec_dot.rs:990 */
 float oracle_vec_dot_q5_0_q8_0(int n, const void *x, const void *y);  /* vec_dot.rs:661; mulmat_ref*.bin type 6 */
+float oracle_vec_dot_q4_1_q8_1(int n, const void *x, const void *y);  /* vec_dot.rs:620; parity unpinned by a fixture: brute force */
+float oracle_vec_dot_q5_1_q8_1(int n, const void *x, const void *y);  /* vec_dot.rs:687; parity unpinned by a fixture: brute force */
 float oracle_vec_dot_q8_0_q8_0(int n, const void *x, const void *y);  /* vec_dot.rs:732; mulmat_ref*.bin type 8 */
 float oracle_vec_dot_q5_K_q8_K(int n, const void *x, const void *y);  /* vec_dot.rs:928; mulmat_ref*.bin type 13 */
 

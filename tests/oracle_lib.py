@@ -14,10 +14,11 @@ ORACLE_DIR = os.path.join(ROOT, "oracle")
 LIB_PATH = os.path.join(ORACLE_DIR, "liboracle.so")
 
 F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, MXFP4 = 0, 1, 2, 6, 8, 12, 13, 14, 15, 39
+Q4_1, Q5_1, Q8_1 = 3, 7, 9
 BLOCK = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176),
-         Q6_K: (256, 210), Q8_K: (256, 292), MXFP4: (32, 17)}
+         Q6_K: (256, 210), Q8_K: (256, 292), MXFP4: (32, 17), Q4_1: (32, 20), Q5_1: (32, 24), Q8_1: (32, 36)}
 # weight type -> activation type of its dot (vec_dot_type)
-ACT_TYPE = {Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K}
+ACT_TYPE = {Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K, Q4_1: Q8_1, Q5_1: Q8_1}
 ROUTE_REPACK, ROUTE_TILED, ROUTE_VECDOT = 1, 2, 3
 
 
@@ -63,14 +64,15 @@ def lib():
         for f in ["quantize_row_q4_0_ref", "quantize_row_q4_K_ref", "quantize_row_q6_K_ref",
                   "quantize_row_q5_0_ref", "quantize_row_q5_K_ref",
                   "quantize_row_mxfp4_ref", "quantize_row_q8_0_ref", "quantize_row_q8_0",
-                  "quantize_row_q8_K_ref", "quantize_row_q8_K_mat"]:
+                  "quantize_row_q8_K_ref", "quantize_row_q8_K_mat",
+                  "quantize_row_q4_1_ref", "quantize_row_q5_1_ref", "quantize_row_q8_1"]:
             fn = getattr(L, "oracle_" + f)
             fn.restype = None
             fn.argtypes = [vp, vp, i64]
         L.oracle_dequantize_row.restype = None
         L.oracle_dequantize_row.argtypes = [C.c_int, vp, vp, i64]
         for f in ["vec_dot_q4_0_q8_0", "vec_dot_q4_K_q8_K", "vec_dot_q6_K_q8_K", "vec_dot_q5_0_q8_0",
-                  "vec_dot_q8_0_q8_0", "vec_dot_q5_K_q8_K"]:
+                  "vec_dot_q8_0_q8_0", "vec_dot_q5_K_q8_K", "vec_dot_q4_1_q8_1", "vec_dot_q5_1_q8_1"]:
             fn = getattr(L, "oracle_" + f)
             fn.restype = C.c_float
             fn.argtypes = [C.c_int, vp, vp]
@@ -93,7 +95,8 @@ def _p(a):
 
 _QUANT = {Q4_0: "quantize_row_q4_0_ref", Q4_K: "quantize_row_q4_K_ref",
           Q6_K: "quantize_row_q6_K_ref", MXFP4: "quantize_row_mxfp4_ref",
-          Q5_0: "quantize_row_q5_0_ref", Q5_K: "quantize_row_q5_K_ref", Q8_0: "quantize_row_q8_0_ref"}
+          Q5_0: "quantize_row_q5_0_ref", Q5_K: "quantize_row_q5_K_ref", Q8_0: "quantize_row_q8_0_ref",
+          Q4_1: "quantize_row_q4_1_ref", Q5_1: "quantize_row_q5_1_ref", Q8_1: "quantize_row_q8_1"}
 
 
 def quantize(ty, x, kind=None):
@@ -103,7 +106,8 @@ def quantize(ty, x, kind=None):
     rows = x.size // n
     name = kind or _QUANT[ty]
     out_ty = {"quantize_row_q8_0_ref": Q8_0, "quantize_row_q8_0": Q8_0,
-              "quantize_row_q8_K_ref": Q8_K, "quantize_row_q8_K_mat": Q8_K}.get(name, ty)
+              "quantize_row_q8_K_ref": Q8_K, "quantize_row_q8_K_mat": Q8_K,
+              "quantize_row_q8_1": Q8_1}.get(name, ty)
     out = np.zeros(rows * row_size(out_ty, n), dtype=np.uint8)
     getattr(lib(), "oracle_" + name)(_p(x), _p(out), x.size)
     return out
@@ -124,7 +128,7 @@ def mul_mat(ty, w, n, rows, x, cols, want_subsums=False, nthreads=0):
     sub = None
     if want_subsums:
         per = {Q4_0: n // 32, Q5_0: n // 32, Q8_0: n // 32, Q4_K: (n // 256) * 2, Q5_K: (n // 256) * 2,
-               Q6_K: n // 256}[ty]
+               Q6_K: n // 256, Q4_1: n // 32, Q5_1: n // 32}[ty]
         sub = np.zeros((cols, rows, per), dtype=np.int32)
     route = C.c_int(0)
     rc = lib().oracle_mul_mat(ty, _p(np.ascontiguousarray(w)), n, rows, _p(x), cols, _p(out),

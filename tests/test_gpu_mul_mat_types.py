@@ -25,6 +25,10 @@ pytestmark = pytest.mark.gpu
 
 TOL = 1e-5
 TYPES = [O.Q5_0, O.Q8_0, O.Q5_K]
+# Q4_1 / Q5_1: d * q + m weights with Q8_1 activations (vec_dot.rs:620-720);
+# no reference dump holds them, the oracle is pinned by quants_ref.bin and a
+# brute force (test_oracle_golden.py test_q41_q51_vec_dot_brute_force)
+MIN_TYPES = [O.Q4_1, O.Q5_1]
 
 
 @pytest.fixture(scope="module")
@@ -44,7 +48,7 @@ def random_blocks(ty, n, rows, seed):
     rng = np.random.default_rng(seed)
     qk, bs = O.BLOCK[ty]
     w = rng.integers(0, 256, size=(rows, n // qk, bs), dtype=np.uint8)
-    offs = (0, 2) if ty == O.Q5_K else (0,)
+    offs = (0, 2) if ty in (O.Q5_K, O.Q4_1, O.Q5_1) else (0,)
     for off in offs:
         e = rng.integers(0x1400, 0x2c00, size=(rows, n // qk), dtype=np.uint16)
         w[:, :, off:off + 2] = e.view(np.uint8).reshape(rows, n // qk, 2)
@@ -71,11 +75,42 @@ def run_case(be, ty, n, rows, cols, seed=0, check_sub=True, x=None, weights="qua
     if check_sub:
         sub = be.mul_mat_subsums(wd, ty, n, xd).cpu().numpy()
         assert np.array_equal(sub, want_sub), "int32 sub-sums differ"
+    if ty in MIN_TYPES:
+        # d * d8 * isum + m * s per block, summed over nb blocks in different
+        # orders by the reference (8 lanes + a separate m * s chain) and the
+        # kernel: each carries at most gamma_(nb+16) = (nb + 16) * 2^-24 of the
+        # sum of the terms' magnitudes (recursive summation bound)
+        mag = min_term_magnitudes(ty, w, n, rows, O.mul_mat_act(ty, n, rows, x, cols), cols)
+        nb = n // 32
+        bound = 2.0 * (nb + 16) * 2.0 ** -24 * mag
+        assert np.all(np.abs(got.astype(np.float64) - want) <= bound), \
+            f"max excess {np.max(np.abs(got - want) - bound):.3e}"
+        assert rel_err(got, want) <= 1e-4
+        return
     err = rel_err(got, want)
     assert err <= tol, f"rel_err {err:.3e}"
 
 
-@pytest.mark.parametrize("ty", TYPES)
+def min_term_magnitudes(ty, w, n, rows, act, cols):
+    """sum_b |d_w d8 isum_b| + |m_w s_b| per output [cols, rows] (float64)."""
+    bs = 20 if ty == O.Q4_1 else 24
+    b = w.reshape(rows, n // 32, bs)
+    d = b[..., 0:2].copy().view(np.float16)[..., 0].astype(np.float64)
+    m = b[..., 2:4].copy().view(np.float16)[..., 0].astype(np.float64)
+    qs = b[..., bs - 16:]
+    codes = np.concatenate([qs & 15, qs >> 4], axis=-1).astype(np.int64)
+    if ty == O.Q5_1:
+        qh = b[..., 4:8].copy().view(np.uint32)[..., 0].astype(np.int64)
+        codes |= ((qh[..., None] >> np.arange(32)) & 1) << 4
+    a = act.reshape(cols, n // 32, 36)
+    d8 = a[..., 0:2].copy().view(np.float16)[..., 0].astype(np.float64)
+    s8 = a[..., 2:4].copy().view(np.float16)[..., 0].astype(np.float64)
+    q8 = a[..., 4:].view(np.int8).astype(np.int64)
+    isum = np.einsum("rbe,cbe->crb", codes, q8)
+    return (np.abs(d[None] * d8[:, None] * isum) + np.abs(m[None] * s8[:, None])).sum(-1)
+
+
+@pytest.mark.parametrize("ty", TYPES + MIN_TYPES)
 @pytest.mark.parametrize("cols", [1, 2, 3, 4, 5, 8, 11])
 def test_small_shapes(be, ty, cols):
     for n, rows in [(512, 64), (1024, 72), (768, 100), (256, 8)]:
@@ -83,7 +118,7 @@ def test_small_shapes(be, ty, cols):
         run_case(be, ty, n, rows, cols, seed=cols + ty, weights="random")
 
 
-@pytest.mark.parametrize("ty", TYPES)
+@pytest.mark.parametrize("ty", TYPES + MIN_TYPES)
 def test_ragged_k(be, ty):
     """K not a multiple of one wavefront's span; an odd number of 32-blocks
     (the last lane holds a lone block)"""
@@ -96,7 +131,7 @@ def test_ragged_k(be, ty):
         run_case(be, ty, 2880, 24, 2)
 
 
-@pytest.mark.parametrize("ty", TYPES)
+@pytest.mark.parametrize("ty", TYPES + MIN_TYPES)
 @pytest.mark.parametrize("n,rows", [(4096, 4096), (14336, 4096), (4096, 14336)])
 @pytest.mark.parametrize("cols", [1, 2, 8])
 def test_llama_decode_shapes(be, ty, n, rows, cols):
@@ -126,7 +161,7 @@ def test_zero_and_extreme_codes(be):
     n, rows = 1024, 16
     x = np.zeros((2, n), dtype=np.float32)
     x[1] = np.random.default_rng(9).standard_normal(n).astype(np.float32)
-    for ty in TYPES:
+    for ty in TYPES + MIN_TYPES:
         run_case(be, ty, n, rows, 2, seed=11, x=x.copy())
         run_case(be, ty, n, rows, 2, seed=11, x=x.copy(), weights="random")
     w = random_blocks(O.Q8_0, n, rows, 12).reshape(rows, n // 32, 34)

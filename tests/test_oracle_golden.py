@@ -51,7 +51,8 @@ def test_e8m0_closed_form():
 QUANT_NAME = {O.Q4_0: "quantize_row_q4_0_ref", O.Q8_0: "quantize_row_q8_0_ref",
               O.Q4_K: "quantize_row_q4_K_ref", O.Q6_K: "quantize_row_q6_K_ref",
               O.Q8_K: "quantize_row_q8_K_ref", O.Q5_0: "quantize_row_q5_0_ref",
-              O.Q5_K: "quantize_row_q5_K_ref"}
+              O.Q5_K: "quantize_row_q5_K_ref", O.Q4_1: "quantize_row_q4_1_ref",
+              O.Q5_1: "quantize_row_q5_1_ref", O.Q8_1: "quantize_row_q8_1"}
 
 
 def test_quants_ref_bit_exact():
@@ -432,3 +433,56 @@ def test_flash_attn_against_float64():
             p = np.exp(s - s.max(1, keepdims=True))
             ref[:, h] = (p / p.sum(1, keepdims=True)) @ vv
         assert np.max(np.abs(out - ref)) < 2e-3
+
+
+def _q41_codes(w, ty):
+    """Unsigned codes, d, m of Q4_1 / Q5_1 rows (numpy, from the block layout)."""
+    bs = 20 if ty == O.Q4_1 else 24
+    b = w.reshape(-1, bs)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float64)[:, 0]
+    m = b[:, 2:4].copy().view(np.float16).astype(np.float64)[:, 0]
+    qs = b[:, bs - 16:]
+    codes = np.concatenate([qs & 15, qs >> 4], axis=1).astype(np.int64)
+    if ty == O.Q5_1:
+        qh = b[:, 4:8].copy().view(np.uint32)[:, 0].astype(np.int64)
+        codes |= ((qh[:, None] >> np.arange(32)) & 1) << 4
+    return codes, d, m
+
+
+@pytest.mark.parametrize("ty", [O.Q4_1, O.Q5_1])
+def test_q41_q51_vec_dot_brute_force(ty):
+    """vec_dot_q4_1_q8_1 / vec_dot_q5_1_q8_1 (no reference fixture holds their
+    dots): the exact integer block sums from numpy, and the float result
+    against sum_b d*d8*isum_b + m*s_b in float64 (the reference's formula, only
+    the fp32 summation order open); quantized rows from the pinned quantizers,
+    plus random block bytes with the top codes."""
+    rng = np.random.default_rng(5)
+    n = 1024
+    for trial in range(6):
+        if trial < 3:
+            w = O.quantize(ty, rng.standard_normal(n).astype(np.float32) * 0.1)
+        else:
+            bs = 20 if ty == O.Q4_1 else 24
+            w = rng.integers(0, 256, size=n // 32 * bs, dtype=np.uint8)
+            blk = w.reshape(-1, bs)
+            blk[:, 0:2] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8)
+            blk[:, 2:4] = np.frombuffer(np.float16(-0.3).tobytes(), np.uint8)
+        x = rng.standard_normal(n).astype(np.float32) * (10.0 if trial == 2 else 1.0)
+        a = O.quantize(O.Q8_1, x)
+        ab = a.reshape(-1, 36)
+        d8 = ab[:, 0:2].copy().view(np.float16).astype(np.float64)[:, 0]
+        s8 = ab[:, 2:4].copy().view(np.float16).astype(np.float64)[:, 0]
+        q8 = ab[:, 4:].view(np.int8).astype(np.int64)
+        assert np.all(np.abs(s8 - np.float16(d8 * q8.sum(1)).astype(np.float64)) <= 1e-3 * np.abs(s8) + 1e-7)
+        codes, d, m = _q41_codes(w, ty)
+        isum = (codes * q8).sum(1)
+        want = float(np.sum(d * d8 * isum + m * s8))
+        f = O.lib().oracle_vec_dot_q4_1_q8_1 if ty == O.Q4_1 else O.lib().oracle_vec_dot_q5_1_q8_1
+        got = f(n, O._p(np.ascontiguousarray(w)), O._p(a))
+        scale = float(np.sum(np.abs(d * d8 * isum)) + np.sum(np.abs(m * s8)))
+        assert abs(got - want) <= 1e-6 * scale, (trial, got, want)
+        # the routed MUL_MAT exports the same integer block sums
+        out, route, sub = O.mul_mat(ty, w, n, 1, x[None, :], 1, want_subsums=True)
+        assert route == O.ROUTE_VECDOT
+        assert np.array_equal(sub.reshape(-1), isum)
+        assert out[0, 0] == np.float32(got)

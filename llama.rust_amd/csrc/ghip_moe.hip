@@ -25,7 +25,9 @@ DEV int crowm(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)
 
 // ---------------------------------------------------------------- routing
 // One workgroup: counting sort of the (token, slot) pairs by expert id and
-// the tile list of the GEMM (tiles of at most tp pairs of one expert).  route layout (int32):
+// the tile list of the GEMM (tiles of at most tp pairs of one expert), the
+// list built by the first wavefront with prefix sums over the experts
+// (config 4: 9.5 -> 5.4 us against one thread walking the experts).  route layout (int32):
 //   [0] n_tiles, [1] n_bad,
 //   [2 .. 2+n_pairs)              pairs sorted by expert,
 //   then per tile: expert, first, count (3 ints) for up to max_tiles tiles.
@@ -47,23 +49,43 @@ ghip_moe_route(const int32_t *__restrict__ ids, int64_t ids_nb1, int n_ids, int 
         else atomicAdd(&bad, 1);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (threadIdx.x < 64) {
+        // experts in chunks of 64 lanes: an exclusive scan of the pair counts
+        // (each expert's first routed slot) and of the tile counts (its first
+        // tile), then every lane writes its expert's tiles
+        const int lane = threadIdx.x;
         int off = 0, nt = 0;
         int32_t *tiles = route + 2 + n_pairs;
-        for (int e = 0; e < n_as; e++) {
-            cur[e] = off;
-            for (int f = 0; f < cnt[e]; f += tp) {
-                if (nt < max_tiles) {
-                    tiles[3 * nt + 0] = e;
-                    tiles[3 * nt + 1] = off + f;
-                    tiles[3 * nt + 2] = min(tp, cnt[e] - f);
+        for (int e0 = 0; e0 < n_as; e0 += 64) {
+            const int e = e0 + lane;
+            const int c = e < n_as ? cnt[e] : 0;
+            const int ntl = (c + tp - 1) / tp;
+            int sc = c, st = ntl;  // inclusive scans
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int a = __shfl_up(sc, o, 64), b = __shfl_up(st, o, 64);
+                if (lane >= o) {
+                    sc += a;
+                    st += b;
                 }
-                nt++;
             }
-            off += cnt[e];
+            const int my_off = off + sc - c, my_t0 = nt + st - ntl;
+            if (e < n_as) {
+                cur[e] = my_off;
+                for (int f = 0, k = my_t0; f < c; f += tp, k++)
+                    if (k < max_tiles) {
+                        tiles[3 * k + 0] = e;
+                        tiles[3 * k + 1] = my_off + f;
+                        tiles[3 * k + 2] = min(tp, c - f);
+                    }
+            }
+            off += __shfl(sc, 63, 64);
+            nt += __shfl(st, 63, 64);
         }
-        route[0] = min(nt, max_tiles);
-        route[1] = bad;
+        if (lane == 0) {
+            route[0] = min(nt, max_tiles);
+            route[1] = bad;
+        }
     }
     __syncthreads();
     // scatter; the order inside one expert does not affect any output value

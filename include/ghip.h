@@ -59,6 +59,8 @@ enum {
     GHIP_TYPE_Q5_1 = 7,
     GHIP_TYPE_Q8_0 = 8,
     GHIP_TYPE_Q8_1 = 9,
+    GHIP_TYPE_Q2_K = 10,
+    GHIP_TYPE_Q3_K = 11,
     GHIP_TYPE_Q4_K = 12,
     GHIP_TYPE_Q5_K = 13,
     GHIP_TYPE_Q6_K = 14,
@@ -111,8 +113,8 @@ ghip_status ghip_synchronize(ghip_context *ctx, void *stream);
 int ghip_supports_op(int op, const ghip_tensor *dst, const ghip_tensor *const *srcs, int n_srcs);
 
 /* dst = src0 x src1 (GGML_OP_MUL_MAT, forward_mul_mat compute.rs:1420-1839).
- * src0: Q4_0 | Q4_1 | Q5_0 | Q5_1 | Q8_0 | Q4_K | Q5_K | Q6_K weight
- *       [ne00=K, ne01=N], rows contiguous;
+ * src0: Q4_0 | Q4_1 | Q5_0 | Q5_1 | Q8_0 | Q2_K | Q3_K | Q4_K | Q5_K | Q6_K
+ *       weight [ne00=K, ne01=N], rows contiguous;
  * src1: F32 [K, ne11] (any row stride nb11, nb10 == 4), or already the
  *       vec_dot type of src0 (Q8_0 for Q4_0/Q5_0/Q8_0, Q8_1 for Q4_1/Q5_1,
  *       Q8_K for the K-quants; rows of blocks),
@@ -153,7 +155,7 @@ ghip_status ghip_mul_mat_subsums(ghip_context *ctx, const ghip_tensor *src0, con
 
 /* Parity hook with no reference counterpart: the activation blocks
  * ghip_mul_mat feeds its kernels for (src0, src1) -- ne11 plain rows of
- * block_q8_0 (Q4_0, Q5_0, Q8_0), block_q8_1 (Q4_1, Q5_1) or block_q8_K (Q4_K, Q5_K, Q6_K) -- written to the device
+ * block_q8_0 (Q4_0, Q5_0, Q8_0), block_q8_1 (Q4_1, Q5_1) or block_q8_K (the K-quants) -- written to the device
  * pointer out.  Same quantizers as compute.rs:1504-1549 / :5350-5398. */
 ghip_status ghip_mul_mat_act(ghip_context *ctx, const ghip_tensor *src0, const ghip_tensor *src1,
                              void *out, void *stream);

@@ -33,6 +33,8 @@ TypeInfo type_info(int t) {
     case GHIP_TYPE_F16: return {1, 2};
     case GHIP_TYPE_Q4_0: return {32, 18};
     case GHIP_TYPE_Q4_1: return {32, 20};
+    case GHIP_TYPE_Q2_K: return {256, 84};
+    case GHIP_TYPE_Q3_K: return {256, 110};
     case GHIP_TYPE_Q5_0: return {32, 22};
     case GHIP_TYPE_Q5_1: return {32, 24};
     case GHIP_TYPE_Q8_1: return {32, 36};
@@ -243,8 +245,10 @@ bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b,
     if (!a || !b) { st = ctx->fail(st, "mul_mat: null operand"); return false; }
     if (a->type != GHIP_TYPE_Q4_0 && a->type != GHIP_TYPE_Q5_0 && a->type != GHIP_TYPE_Q8_0 &&
         a->type != GHIP_TYPE_Q4_K && a->type != GHIP_TYPE_Q5_K && a->type != GHIP_TYPE_Q6_K &&
-        a->type != GHIP_TYPE_Q4_1 && a->type != GHIP_TYPE_Q5_1) {
-        st = ctx->fail(st, "mul_mat: src0 type %d not supported (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K)",
+        a->type != GHIP_TYPE_Q4_1 && a->type != GHIP_TYPE_Q5_1 && a->type != GHIP_TYPE_Q2_K &&
+        a->type != GHIP_TYPE_Q3_K) {
+        st = ctx->fail(st,
+                       "mul_mat: src0 type %d not supported (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K)",
                        a->type);
         return false;
     }
@@ -326,10 +330,15 @@ const char *gemv_base(int wtype) {
     case GHIP_TYPE_Q5_0: return "ghip_gemv_q5_0";
     case GHIP_TYPE_Q8_0: return "ghip_gemv_q8_0";
     case GHIP_TYPE_Q4_1: return "ghip_gemv_q4_1";
+    case GHIP_TYPE_Q2_K: return "ghip_gemv_q2_K";
+    case GHIP_TYPE_Q3_K: return "ghip_gemv_q3_K";
     case GHIP_TYPE_Q5_1: return "ghip_gemv_q5_1";
     default: return "ghip_gemv_q4_0";
     }
 }
+
+// Q2_K / Q3_K: the VALU decode kernel in launches of at most 4 columns
+bool k23_type(int wtype) { return wtype == GHIP_TYPE_Q2_K || wtype == GHIP_TYPE_Q3_K; }
 
 // 32-element blocks with Q8_0 activations: one lane per pair of blocks
 bool gemv_pair(int wtype) {
@@ -488,6 +497,8 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
         waves_k = (int)(((p.nb + 1) / 2 + 63) / 64);
     else if (p.wtype == GHIP_TYPE_Q4_1 || p.wtype == GHIP_TYPE_Q5_1)  // one lane per 32-block
         waves_k = (int)((p.nb + 63) / 64);
+    else if (k23_type(p.wtype))  // four lanes per super-block
+        waves_k = (int)((p.nb + 15) / 16);
     else if (gemv_v2(p))
         waves_k = (int)((p.nb + 15) / 16);
     else
@@ -520,15 +531,16 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     const int rows_per_wg = persist ? 0 : rows_per_team * teams;
     const unsigned grid = persist ? (unsigned)std::max(1, std::min(env_int("GHIP_GEMV_WGS", 256), (int)((p.N + 7) / 8)))
                                   : (unsigned)((p.N + rows_per_wg - 1) / rows_per_wg);
-    for (int64_t c0 = 0; c0 < p.M; c0 += 8) {
-        const int nc = (int)std::min<int64_t>(8, p.M - c0);
+    const int64_t cgrp = k23_type(p.wtype) ? 4 : 8;  // activation columns per launch
+    for (int64_t c0 = 0; c0 < p.M; c0 += cgrp) {
+        const int nc = (int)std::min<int64_t>(cgrp, p.M - c0);
         const int NC = nc == 1 ? 1 : nc == 2 ? 2 : nc <= 4 ? 4 : 8;
         std::string name = std::string(gemv_base(p.wtype)) + (p.wtype == GHIP_TYPE_Q6_K && q4k ? "_v2" : "") +
                            (fused ? "_f" : "") + (sub ? "_sub" : "") +
                            "_c" + std::to_string(NC) + (q4k ? "_r" + std::to_string(rb) + "x" + std::to_string(ng) : std::string());
         int32_t *sub_c = sub;
         if (sub) {
-            const int64_t per = (p.wtype == GHIP_TYPE_Q4_K || p.wtype == GHIP_TYPE_Q5_K) ? 2 * p.nb : p.nb;
+            const int64_t per = (p.wtype == GHIP_TYPE_Q4_K || p.wtype == GHIP_TYPE_Q5_K || p.wtype == GHIP_TYPE_Q2_K) ? 2 * p.nb : p.nb;
             sub_c = sub + c0 * p.N * per;
         }
         ghip_status st;

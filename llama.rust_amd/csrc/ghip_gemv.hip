@@ -1000,6 +1000,183 @@ GEMV_Q41_INST(q4_1, WT_Q4_1, 8)
 GEMV_Q41_INST(q5_1, WT_Q5_1, 1) GEMV_Q41_INST(q5_1, WT_Q5_1, 2) GEMV_Q41_INST(q5_1, WT_Q5_1, 4)
 GEMV_Q41_INST(q5_1, WT_Q5_1, 8)
 
+// ---------------------------------------------------------------- Q2_K / Q3_K x Q8_K
+// Four lanes per super-block: lane quarter qq takes 128-group j = qq / 2 and
+// shift groups k = 2(qq & 1), 2(qq & 1) + 1, i.e. elements 128j + 32k + e
+// (e < 32) with codes (qs[32j + e] >> 2k) & 3 and scales 8j + 2k + (e >= 16)
+// (dequantize_row_q2_K / _q3_K, quants.rs:431-520).  Per super-block
+// (vec_dot_q2_K_q8_K / _q3_K_q8_K, vec_dot.rs:758-834):
+//   Q2_K: isum = sum_g (sc_g & 15) * sum q * q8,  summs = sum_g (sc_g >> 4) * bsum16_g,
+//         d8 * d * isum - d8 * dmin * summs;
+//   Q3_K: values lo - 4 where the hmask bit 4j + k is clear, scales sc_g - 32,
+//         isum = sum_g (sc_g - 32) * sum v * q8,  d8 * d * isum.
+// RB rows per workgroup, each row's bytes loaded one row ahead; the integer
+// sums are exact and (_sub kernels) exported per super-block.
+constexpr int WT_Q2_K = 10, WT_Q3_K = 11;
+template <int WT, int NC, bool SUBSUMS>
+__device__ __forceinline__ void gemv_k23_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb,
+                                              const uint8_t *__restrict__ act, int64_t act_row_bytes, int ncols,
+                                              float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
+    constexpr bool Q2 = WT == WT_Q2_K;
+    constexpr int BB = Q2 ? 84 : 110;
+    constexpr int NWD = Q2 ? 10 : 20;  // dwords of weight data per lane and row
+    __shared__ float red[RB * 8 * NC];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int qq = lane & 3, j = qq >> 1, kp = qq & 1;  // k = 2kp, 2kp + 1
+    const int b = 16 * w + (lane >> 2);
+    const bool valid = b < nb;
+    const int r0 = (int)blockIdx.x * RB;
+    const int nr = min(RB, rows - r0);
+    const uint8_t *base = W + (int64_t)min(b, nb - 1) * BB;
+    // Q2_K: scales 8j+4kp .. +3 | qs 32j .. +31 (8 dwords) | d, dmin
+    // Q3_K: hmask (8 dwords) | qs 32j .. +31 (8 dwords) | scales 12 bytes | d
+    auto load_row = [&](int rr, uint32_t (&v)[NWD]) {
+        const uint8_t *p = base + (int64_t)min(r0 + rr, rows - 1) * w_row_bytes;
+        if constexpr (Q2) {
+            v[0] = ld4(p + 8 * j + 4 * kp);
+            const uint4 a = ld16(p + 16 + 32 * j), c = ld16(p + 32 + 32 * j);
+            v[1] = a.x; v[2] = a.y; v[3] = a.z; v[4] = a.w;
+            v[5] = c.x; v[6] = c.y; v[7] = c.z; v[8] = c.w;
+            v[9] = ld4(p + 80);
+        } else {
+            const uint4 h0 = ld16(p), h1 = ld16(p + 16), a = ld16(p + 32 + 32 * j), c = ld16(p + 48 + 32 * j);
+            v[0] = h0.x; v[1] = h0.y; v[2] = h0.z; v[3] = h0.w;
+            v[4] = h1.x; v[5] = h1.y; v[6] = h1.z; v[7] = h1.w;
+            v[8] = a.x; v[9] = a.y; v[10] = a.z; v[11] = a.w;
+            v[12] = c.x; v[13] = c.y; v[14] = c.z; v[15] = c.w;
+            const uint2 s01 = ld8(p + 96);
+            v[16] = s01.x;
+            v[17] = s01.y;
+            v[18] = ld4(p + 104);
+            v[19] = ld2(p + 108);
+        }
+    };
+    // activations: codes of elements 128j + 32k + e for the lane's two k, bsum16
+    // of its four groups (Q2_K), d
+    uint4 ya[NC][4];
+    int bs[NC][4];
+    float dy[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        dy[c] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            ya[c][i] = make_uint4(0, 0, 0, 0);
+            bs[c][i] = 0;
+        }
+        if (c < ncols && valid) {
+            const uint8_t *A = act + c * act_row_bytes + (int64_t)b * Q8K_BYTES;
+            dy[c] = __uint_as_float(ld4(A));
+#pragma unroll
+            for (int i = 0; i < 4; i++) ya[c][i] = ld16(A + 4 + 128 * j + 64 * kp + 16 * i);
+            if constexpr (Q2) {
+                const uint2 g = ld8(A + 260 + 2 * (8 * j + 4 * kp));
+                bs[c][0] = (int)(int16_t)(g.x & 0xffff);
+                bs[c][1] = (int)(int16_t)(g.x >> 16);
+                bs[c][2] = (int)(int16_t)(g.y & 0xffff);
+                bs[c][3] = (int)(int16_t)(g.y >> 16);
+            }
+        }
+    }
+    float part[NC][RB];
+    uint32_t wv[2][NWD];
+    load_row(0, wv[0]);
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        if (rr + 1 < RB) load_row(rr + 1, wv[(rr + 1) & 1]);
+        const uint32_t *v = wv[rr & 1];
+        int sc4[4];  // scales of groups (k0, h0), (k0, h1), (k1, h0), (k1, h1)
+        float dw, dmw = 0.0f;
+        uint32_t q[2][8];  // codes of e = 4i .. 4i+3 per k, as bytes
+        if constexpr (Q2) {
+#pragma unroll
+            for (int g = 0; g < 4; g++) sc4[g] = (int)((v[0] >> (8 * g)) & 0xff);
+            dw = h2f(v[9]);
+            dmw = h2f(v[9] >> 16);
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) q[t][i] = (v[1 + i] >> (2 * (2 * kp + t))) & 0x03030303u;
+        } else {
+            // the scale word 2j + kp of the de-packed 16 (quants.rs:475-484)
+            const uint32_t a0 = v[16], a1 = v[17], a2 = v[18];
+            const uint32_t km1 = 0x03030303u, km2 = 0x0f0f0f0fu;
+            const int wi = 2 * j + kp;
+            const uint32_t sw = wi == 0   ? (a0 & km2) | ((a2 & km1) << 4)
+                                : wi == 1 ? (a1 & km2) | (((a2 >> 2) & km1) << 4)
+                                : wi == 2 ? ((a0 >> 4) & km2) | (((a2 >> 4) & km1) << 4)
+                                          : ((a1 >> 4) & km2) | (((a2 >> 6) & km1) << 4);
+#pragma unroll
+            for (int g = 0; g < 4; g++) sc4[g] = (int)((sw >> (8 * g)) & 0xff) - 32;
+            dw = h2f(v[19]);
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const int k = 2 * kp + t, bit = 4 * j + k;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const uint32_t lo = (v[8 + i] >> (2 * k)) & 0x03030303u;
+                    const uint32_t hb = (v[i] >> bit) & 0x01010101u;
+                    q[t][i] = lo | ((hb ^ 0x01010101u) * 0xfcu);  // lo - 4 where the bit is clear
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            int is = 0, sm = 0;
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const uint32_t yv[8] = {ya[c][2 * t].x, ya[c][2 * t].y, ya[c][2 * t].z, ya[c][2 * t].w,
+                                        ya[c][2 * t + 1].x, ya[c][2 * t + 1].y, ya[c][2 * t + 1].z, ya[c][2 * t + 1].w};
+                int s0 = 0, s1 = 0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    s0 = dot4(q[t][i], yv[i], s0);
+                    s1 = dot4(q[t][4 + i], yv[4 + i], s1);
+                }
+                if constexpr (Q2) {
+                    is += __mul24(sc4[2 * t] & 15, s0) + __mul24(sc4[2 * t + 1] & 15, s1);
+                    sm += __mul24(sc4[2 * t] >> 4, bs[c][2 * t]) + __mul24(sc4[2 * t + 1] >> 4, bs[c][2 * t + 1]);
+                } else {
+                    is += __mul24(sc4[2 * t], s0) + __mul24(sc4[2 * t + 1], s1);
+                }
+            }
+            // the super-block's exact sums over its four lanes, folded once
+            const int isb = quad_sum_dpp(is), smb = Q2 ? quad_sum_dpp(sm) : 0;
+            if (SUBSUMS && qq == 0 && valid && c < ncols && rr < nr) {
+                if constexpr (Q2) {
+                    int32_t *sp = sub + (((int64_t)c * rows + r0 + rr) * nb + b) * 2;
+                    sp[0] = isb;
+                    sp[1] = smb;
+                } else {
+                    sub[((int64_t)c * rows + r0 + rr) * nb + b] = isb;
+                }
+            }
+            float pp = 0.0f;
+            if (valid && qq == 0) {
+                pp = (dy[c] * dw) * (float)isb;
+                if constexpr (Q2) pp = fmaf(-(dy[c] * dmw), (float)smb, pp);
+            }
+            part[c][rr] = pp;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NC; c++) stash_rows(red, part[c], lane, w, nw, c, NC);
+    finish_rows(red, r0, nr, ncols, NC, nw, dst, ldd);
+}
+#define GEMV_K23_INST(TN, WT, NC)                                                                                \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_##TN##_c##NC(                                    \
+        const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb, const uint8_t *__restrict__ act,   \
+        int64_t act_row_bytes, int ncols, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {     \
+        gemv_k23_impl<WT, NC, false>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub);       \
+    }                                                                                                            \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_##TN##_sub_c##NC(                                \
+        const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb, const uint8_t *__restrict__ act,   \
+        int64_t act_row_bytes, int ncols, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {     \
+        gemv_k23_impl<WT, NC, true>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub);        \
+    }
+GEMV_K23_INST(q2_K, WT_Q2_K, 1) GEMV_K23_INST(q2_K, WT_Q2_K, 2) GEMV_K23_INST(q2_K, WT_Q2_K, 4)
+GEMV_K23_INST(q3_K, WT_Q3_K, 1) GEMV_K23_INST(q3_K, WT_Q3_K, 2) GEMV_K23_INST(q3_K, WT_Q3_K, 4)
+
 #define GEMV_ARGS                                                                                     \
     const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb, const uint8_t *__restrict__ act, \
         int64_t act_row_bytes, int ncols, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub

@@ -32,6 +32,8 @@ typedef struct { uint8_t e; uint8_t qs[16]; } blk_mxfp4;                        
 typedef struct { uint16_t d; uint8_t qh[4]; uint8_t qs[16]; } blk_q5_0;        /* 22 B  */
 typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; } blk_q5_K; /* 176 B */
 typedef struct { uint16_t d, m; uint8_t qs[16]; } blk_q4_1;                    /* 20 B  */
+typedef struct { uint8_t scales[16]; uint8_t qs[64]; uint16_t d, dmin; } blk_q2_K;   /* 84 B  */
+typedef struct { uint8_t hmask[32]; uint8_t qs[64]; uint8_t scales[12]; uint16_t d; } blk_q3_K; /* 110 B */
 typedef struct { uint16_t d, m; uint8_t qh[4]; uint8_t qs[16]; } blk_q5_1;     /* 24 B  */
 typedef struct { uint16_t d, s; int8_t qs[32]; } blk_q8_1;                     /* 36 B  */
 
@@ -44,6 +46,8 @@ _Static_assert(sizeof(blk_mxfp4) == 17, "mxfp4");
 _Static_assert(sizeof(blk_q5_0) == 22, "q5_0");
 _Static_assert(sizeof(blk_q5_K) == 176, "q5_K");
 _Static_assert(sizeof(blk_q4_1) == 20, "q4_1");
+_Static_assert(sizeof(blk_q2_K) == 84, "q2_K");
+_Static_assert(sizeof(blk_q3_K) == 110, "q3_K");
 _Static_assert(sizeof(blk_q5_1) == 24, "q5_1");
 _Static_assert(sizeof(blk_q8_1) == 36, "q8_1");
 
@@ -744,7 +748,87 @@ static inline int32_t isum_q5_1(const blk_q5_1 *x, const blk_q8_1 *y) {
     return s;
 }
 
+/* Q2_K / Q3_K element e of 128-group j at shift k (e < 32): element
+ * 128j + 32k + e, byte qs[32j + e] >> 2k, scale index 8j + 2k + (e >= 16)
+ * (quants.rs:431-465, :467-520). */
+static inline int q2k_val(const blk_q2_K *x, int j, int k, int e) { return (x->qs[32 * j + e] >> (2 * k)) & 3; }
+static inline int q3k_val(const blk_q3_K *x, int j, int k, int e) {
+    const int lo = (x->qs[32 * j + e] >> (2 * k)) & 3;
+    return (x->hmask[e] >> (4 * j + k)) & 1 ? lo : lo - 4;
+}
+/* the 16 6-bit Q3_K scales from the 12 packed bytes, as unsigned 0..63
+ * (quants.rs:475-484: aux[] de-packing) */
+static void q3k_scales_u(const uint8_t *packed, int sc[16]) {
+    const uint32_t km1 = 0x03030303u, km2 = 0x0f0f0f0fu;
+    uint32_t a0, a1, a2;
+    memcpy(&a0, packed, 4);
+    memcpy(&a1, packed + 4, 4);
+    memcpy(&a2, packed + 8, 4);
+    const uint32_t w[4] = {(a0 & km2) | ((a2 & km1) << 4), (a1 & km2) | (((a2 >> 2) & km1) << 4),
+                           ((a0 >> 4) & km2) | (((a2 >> 4) & km1) << 4), ((a1 >> 4) & km2) | (((a2 >> 6) & km1) << 4)};
+    for (int i = 0; i < 16; i++) sc[i] = (int)((w[i >> 2] >> (8 * (i & 3))) & 0xff);
+}
+/* exact per-super-block sums: Q2_K isum = sum_g (sc_g & 15) * sum q2*q8,
+ * summs = sum_g (sc_g >> 4) * bsums_g; Q3_K isum = sum_g (sc_g - 32) * sum v*q8 */
+static inline void isum_q2_K(const blk_q2_K *x, const blk_q8_K *y, int32_t *isum, int32_t *summs) {
+    int32_t is = 0, sm = 0;
+    for (int g = 0; g < 16; g++) sm += (x->scales[g] >> 4) * y->bsums[g];
+    for (int j = 0; j < 2; j++)
+        for (int k = 0; k < 4; k++)
+            for (int h = 0; h < 2; h++) {
+                int32_t s = 0;
+                for (int e = 16 * h; e < 16 * h + 16; e++) s += q2k_val(x, j, k, e) * y->qs[128 * j + 32 * k + e];
+                is += (x->scales[8 * j + 2 * k + h] & 0xF) * s;
+            }
+    *isum = is;
+    *summs = sm;
+}
+static inline int32_t isum_q3_K(const blk_q3_K *x, const blk_q8_K *y) {
+    int sc[16];
+    q3k_scales_u(x->scales, sc);
+    int32_t is = 0;
+    for (int j = 0; j < 2; j++)
+        for (int k = 0; k < 4; k++)
+            for (int h = 0; h < 2; h++) {
+                int32_t s = 0;
+                for (int e = 16 * h; e < 16 * h + 16; e++) s += q3k_val(x, j, k, e) * y->qs[128 * j + 32 * k + e];
+                is += (sc[8 * j + 2 * k + h] - 32) * s;
+            }
+    return is;
+}
+
 void oracle_dequantize_row(int type, const void *vx, float *y, int64_t k) {
+    if (type == OR_Q2_K) { /* quants.rs:431-465 */
+        const blk_q2_K *x = (const blk_q2_K *)vx;
+        for (int64_t i = 0; i < k / QK_K; i++) {
+            const float d = H2F(x[i].d), mn = H2F(x[i].dmin);
+            for (int j = 0; j < 2; j++)
+                for (int kk = 0; kk < 4; kk++)
+                    for (int h = 0; h < 2; h++) {
+                        const uint8_t sc = x[i].scales[8 * j + 2 * kk + h];
+                        const float dl = d * (float)(sc & 0xF), ml = mn * (float)(sc >> 4);
+                        for (int e = 16 * h; e < 16 * h + 16; e++)
+                            y[i * QK_K + 128 * j + 32 * kk + e] = dl * (float)q2k_val(&x[i], j, kk, e) - ml;
+                    }
+        }
+        return;
+    }
+    if (type == OR_Q3_K) { /* quants.rs:467-520 */
+        const blk_q3_K *x = (const blk_q3_K *)vx;
+        for (int64_t i = 0; i < k / QK_K; i++) {
+            const float d = H2F(x[i].d);
+            int sc[16];
+            q3k_scales_u(x[i].scales, sc);
+            for (int j = 0; j < 2; j++)
+                for (int kk = 0; kk < 4; kk++)
+                    for (int h = 0; h < 2; h++) {
+                        const float dl = d * ((float)(int8_t)sc[8 * j + 2 * kk + h] - 32.0f);
+                        for (int e = 16 * h; e < 16 * h + 16; e++)
+                            y[i * QK_K + 128 * j + 32 * kk + e] = dl * (float)q3k_val(&x[i], j, kk, e);
+                    }
+        }
+        return;
+    }
     if (type == OR_Q4_1 || type == OR_Q5_1) { /* quants.rs:189-202, :288-304: x * d + m */
         for (int64_t i = 0; i < k / 32; i++) {
             const blk_q4_1 *a = (const blk_q4_1 *)vx + i;
@@ -1055,6 +1139,64 @@ float oracle_vec_dot_q5_1_q8_1(int n, const void *vx, const void *vy) {
     return hsum8(acc) + summs;
 }
 
+/* vec_dot.rs:758-797 vec_dot_q2_K_q8_K (the AVX2 kernel's order): per block
+ * the min term first, acc[l] = fma(-d8*dmin, (sc>>4)[2l]*bsums[2l] +
+ * (sc>>4)[2l+1]*bsums[2l+1], acc[l]); then sumi[l] over the 4-element lanes
+ * e = 4l .. 4l+3 of every 32-value shift group scaled by sc[8j+2k+(l>=4)] & 15,
+ * acc[l] = fma(d8*d, sumi[l], acc[l]); result hsum8(acc) */
+float oracle_vec_dot_q2_K_q8_K(int n, const void *vx, const void *vy) {
+    const blk_q2_K *x = (const blk_q2_K *)vx;
+    const blk_q8_K *y = (const blk_q8_K *)vy;
+    float acc[8] = {0};
+    for (int i = 0; i < n / QK_K; i++) {
+        const float d = y[i].d * H2F(x[i].d);
+        const float dmin = -y[i].d * H2F(x[i].dmin);
+        for (int l = 0; l < 8; l++) {
+            const int32_t prod = (x[i].scales[2 * l] >> 4) * y[i].bsums[2 * l] +
+                                 (x[i].scales[2 * l + 1] >> 4) * y[i].bsums[2 * l + 1];
+            acc[l] = fmaf(dmin, (float)prod, acc[l]);
+        }
+        int32_t sumi[8] = {0};
+        for (int j = 0; j < 2; j++)
+            for (int k = 0; k < 4; k++)
+                for (int l = 0; l < 8; l++) {
+                    const int sc = x[i].scales[8 * j + 2 * k + (l >= 4)] & 0x0F;
+                    int32_t s = 0;
+                    for (int ii = 0; ii < 4; ii++)
+                        s += q2k_val(&x[i], j, k, 4 * l + ii) * y[i].qs[128 * j + 32 * k + 4 * l + ii];
+                    sumi[l] += sc * s;
+                }
+        for (int l = 0; l < 8; l++) acc[l] = fmaf(d, (float)sumi[l], acc[l]);
+    }
+    return hsum8(acc);
+}
+
+/* vec_dot.rs:801-834 vec_dot_q3_K_q8_K (the AVX2 kernel's order): scales
+ * sc - 32, values lo - 4 * (hmask bit clear), sumi[l] as for Q2_K,
+ * acc[l] = fma(d8*d, sumi[l], acc[l]); result hsum8(acc) */
+float oracle_vec_dot_q3_K_q8_K(int n, const void *vx, const void *vy) {
+    const blk_q3_K *x = (const blk_q3_K *)vx;
+    const blk_q8_K *y = (const blk_q8_K *)vy;
+    float acc[8] = {0};
+    for (int i = 0; i < n / QK_K; i++) {
+        const float d = y[i].d * H2F(x[i].d);
+        int sc[16];
+        q3k_scales_u(x[i].scales, sc);
+        int32_t sumi[8] = {0};
+        for (int j = 0; j < 2; j++)
+            for (int k = 0; k < 4; k++)
+                for (int l = 0; l < 8; l++) {
+                    const int s6 = sc[8 * j + 2 * k + (l >= 4)] - 32;
+                    int32_t s = 0;
+                    for (int ii = 0; ii < 4; ii++)
+                        s += q3k_val(&x[i], j, k, 4 * l + ii) * y[i].qs[128 * j + 32 * k + 4 * l + ii];
+                    sumi[l] += s6 * s;
+                }
+        for (int l = 0; l < 8; l++) acc[l] = fmaf(d, (float)sumi[l], acc[l]);
+    }
+    return hsum8(acc);
+}
+
 float oracle_vec_dot_q5_0_q8_0(int n, const void *vx, const void *vy) {
     const blk_q5_0 *x = (const blk_q5_0 *)vx;
     const blk_q8_0 *y = (const blk_q8_0 *)vy;
@@ -1170,7 +1312,7 @@ int oracle_mul_mat(int type, const void *w, int64_t n, int64_t rows, const float
     if (route_out) *route_out = route;
     if (route < 0) return -1;
     if (type != OR_Q4_0 && type != OR_Q4_K && type != OR_Q6_K && type != OR_Q5_0 && type != OR_Q8_0 &&
-        type != OR_Q5_K && type != OR_Q4_1 && type != OR_Q5_1)
+        type != OR_Q5_K && type != OR_Q4_1 && type != OR_Q5_1 && type != OR_Q2_K && type != OR_Q3_K)
         return -2;
     const size_t rs = act_row_size(type, n);
     uint8_t *act = (uint8_t *)malloc(rs * (size_t)cols);
@@ -1249,6 +1391,31 @@ int oracle_mul_mat(int type, const void *w, int64_t n, int64_t rows, const float
                 else if (route == ORACLE_ROUTE_TILED) v = acc;
                 else v = oracle_vec_dot_q4_K_q8_K((int)n, wr, a);
                 out[c * rows + r] = v;
+            }
+        }
+    } else if (type == OR_Q2_K || type == OR_Q3_K) {
+        /* the row vec_dot (the reference takes its tiled route from 8 columns,
+         * tiled.rs:363-411: the same integer sums, another fp32 order) */
+        const int64_t nb = n / QK_K;
+        const size_t wbs = type == OR_Q2_K ? sizeof(blk_q2_K) : sizeof(blk_q3_K);
+#pragma omp parallel for num_threads(nth) schedule(static)
+        for (int64_t r = 0; r < rows; r++) {
+            const uint8_t *wr = (const uint8_t *)w + (size_t)r * nb * wbs;
+            for (int64_t c = 0; c < cols; c++) {
+                const blk_q8_K *a = (const blk_q8_K *)(act + (size_t)c * rs);
+                if (subsums)
+                    for (int64_t b = 0; b < nb; b++) {
+                        if (type == OR_Q2_K) {
+                            int32_t is, sm;
+                            isum_q2_K((const blk_q2_K *)wr + b, &a[b], &is, &sm);
+                            subsums[(((size_t)c * rows + r) * nb + b) * 2 + 0] = is;
+                            subsums[(((size_t)c * rows + r) * nb + b) * 2 + 1] = sm;
+                        } else {
+                            subsums[((size_t)c * rows + r) * nb + b] = isum_q3_K((const blk_q3_K *)wr + b, &a[b]);
+                        }
+                    }
+                out[c * rows + r] = type == OR_Q2_K ? oracle_vec_dot_q2_K_q8_K((int)n, wr, a)
+                                                    : oracle_vec_dot_q3_K_q8_K((int)n, wr, a);
             }
         }
     } else if (type == OR_Q4_1 || type == OR_Q5_1) {

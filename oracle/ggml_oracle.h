@@ -23,7 +23,7 @@ extern "C" {
 /* ggml type ids (crates/ggml/src/types.rs:15) */
 enum {
     OR_F32 = 0, OR_F16 = 1, OR_Q4_0 = 2, OR_Q4_1 = 3, OR_Q5_0 = 6, OR_Q5_1 = 7, OR_Q8_0 = 8, OR_Q8_1 = 9,
-    OR_Q4_K = 12,
+    OR_Q2_K = 10, OR_Q3_K = 11, OR_Q4_K = 12,
     OR_Q5_K = 13, OR_Q6_K = 14, OR_Q8_K = 15, OR_MXFP4 = 39
 };
 
@@ -61,6 +61,8 @@ float oracle_vec_dot_q6_K_q8_K(int n, const void *x, const void *y);  /* vec_dot
 float oracle_vec_dot_q5_0_q8_0(int n, const void *x, const void *y);  /* vec_dot.rs:661; mulmat_ref*.bin type 6 */
 float oracle_vec_dot_q4_1_q8_1(int n, const void *x, const void *y);  /* vec_dot.rs:620; parity unpinned by a fixture: brute force */
 float oracle_vec_dot_q5_1_q8_1(int n, const void *x, const void *y);  /* vec_dot.rs:687; parity unpinned by a fixture: brute force */
+float oracle_vec_dot_q2_K_q8_K(int n, const void *x, const void *y);  /* vec_dot.rs:758; no fixture holds the dot: brute force */
+float oracle_vec_dot_q3_K_q8_K(int n, const void *x, const void *y);  /* vec_dot.rs:801; no fixture holds the dot: brute force */
 float oracle_vec_dot_q8_0_q8_0(int n, const void *x, const void *y);  /* vec_dot.rs:732; mulmat_ref*.bin type 8 */
 float oracle_vec_dot_q5_K_q8_K(int n, const void *x, const void *y);  /* vec_dot.rs:928; mulmat_ref*.bin type 13 */
 

@@ -15,10 +15,13 @@ LIB_PATH = os.path.join(ORACLE_DIR, "liboracle.so")
 
 F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, MXFP4 = 0, 1, 2, 6, 8, 12, 13, 14, 15, 39
 Q4_1, Q5_1, Q8_1 = 3, 7, 9
+Q2_K, Q3_K = 10, 11
 BLOCK = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176),
-         Q6_K: (256, 210), Q8_K: (256, 292), MXFP4: (32, 17), Q4_1: (32, 20), Q5_1: (32, 24), Q8_1: (32, 36)}
+         Q6_K: (256, 210), Q8_K: (256, 292), MXFP4: (32, 17), Q4_1: (32, 20), Q5_1: (32, 24), Q8_1: (32, 36),
+         Q2_K: (256, 84), Q3_K: (256, 110)}
 # weight type -> activation type of its dot (vec_dot_type)
-ACT_TYPE = {Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K, Q4_1: Q8_1, Q5_1: Q8_1}
+ACT_TYPE = {Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K, Q4_1: Q8_1, Q5_1: Q8_1,
+            Q2_K: Q8_K, Q3_K: Q8_K}
 ROUTE_REPACK, ROUTE_TILED, ROUTE_VECDOT = 1, 2, 3
 
 
@@ -72,7 +75,8 @@ def lib():
         L.oracle_dequantize_row.restype = None
         L.oracle_dequantize_row.argtypes = [C.c_int, vp, vp, i64]
         for f in ["vec_dot_q4_0_q8_0", "vec_dot_q4_K_q8_K", "vec_dot_q6_K_q8_K", "vec_dot_q5_0_q8_0",
-                  "vec_dot_q8_0_q8_0", "vec_dot_q5_K_q8_K", "vec_dot_q4_1_q8_1", "vec_dot_q5_1_q8_1"]:
+                  "vec_dot_q8_0_q8_0", "vec_dot_q5_K_q8_K", "vec_dot_q4_1_q8_1", "vec_dot_q5_1_q8_1",
+                  "vec_dot_q2_K_q8_K", "vec_dot_q3_K_q8_K"]:
             fn = getattr(L, "oracle_" + f)
             fn.restype = C.c_float
             fn.argtypes = [C.c_int, vp, vp]
@@ -128,14 +132,14 @@ def mul_mat(ty, w, n, rows, x, cols, want_subsums=False, nthreads=0):
     sub = None
     if want_subsums:
         per = {Q4_0: n // 32, Q5_0: n // 32, Q8_0: n // 32, Q4_K: (n // 256) * 2, Q5_K: (n // 256) * 2,
-               Q6_K: n // 256, Q4_1: n // 32, Q5_1: n // 32}[ty]
+               Q6_K: n // 256, Q4_1: n // 32, Q5_1: n // 32, Q2_K: (n // 256) * 2, Q3_K: n // 256}[ty]
         sub = np.zeros((cols, rows, per), dtype=np.int32)
     route = C.c_int(0)
     rc = lib().oracle_mul_mat(ty, _p(np.ascontiguousarray(w)), n, rows, _p(x), cols, _p(out),
                               _p(sub), C.byref(route), nthreads)
     if rc < 0:
         raise ValueError(f"oracle_mul_mat rc={rc}")
-    if sub is not None and ty in (Q4_K, Q5_K):
+    if sub is not None and ty in (Q4_K, Q5_K, Q2_K):
         sub = sub.reshape(cols, rows, n // 256, 2)
     return out, route.value, sub
 

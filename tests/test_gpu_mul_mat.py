@@ -147,12 +147,12 @@ def test_padding_columns_not_stored(be, cols):
 
 def test_unsupported_type_raises(be):
     import ghip
-    # Q2_K (type 10, 84-byte super-blocks) has no kernel here: a status, no fallback
-    ghip.BLOCK.setdefault(10, (256, 84))
-    w = torch.zeros((8, 84), dtype=torch.uint8, device="cuda")
+    # IQ2_XXS (type 16, 66-byte super-blocks) has no kernel here: a status, no fallback
+    ghip.BLOCK.setdefault(16, (256, 66))
+    w = torch.zeros((8, 66), dtype=torch.uint8, device="cuda")
     x = torch.zeros((1, 256), dtype=torch.float32, device="cuda")
     with pytest.raises(ghip.GhipError, match="not supported"):
-        be.mul_mat(w, 10, 256, x)
+        be.mul_mat(w, 16, 256, x)
 
 
 # ---------------------------------------------------------------- prefill GEMM

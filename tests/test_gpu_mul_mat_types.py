@@ -29,6 +29,10 @@ TYPES = [O.Q5_0, O.Q8_0, O.Q5_K]
 # no reference dump holds them, the oracle is pinned by quants_ref.bin and a
 # brute force (test_oracle_golden.py test_q41_q51_vec_dot_brute_force)
 MIN_TYPES = [O.Q4_1, O.Q5_1]
+# Q2_K / Q3_K: 2- and 3-bit K-quants with Q8_K activations (vec_dot.rs:758-834);
+# the oracle's dequantizers are pinned by quants_ref.bin, its dots by a brute
+# force (test_oracle_golden.py test_q2k_q3k_vec_dot_brute_force)
+K23_TYPES = [O.Q2_K, O.Q3_K]
 
 
 @pytest.fixture(scope="module")
@@ -48,7 +52,7 @@ def random_blocks(ty, n, rows, seed):
     rng = np.random.default_rng(seed)
     qk, bs = O.BLOCK[ty]
     w = rng.integers(0, 256, size=(rows, n // qk, bs), dtype=np.uint8)
-    offs = (0, 2) if ty in (O.Q5_K, O.Q4_1, O.Q5_1) else (0,)
+    offs = {O.Q2_K: (80, 82), O.Q3_K: (108,)}.get(ty, (0, 2) if ty in (O.Q5_K, O.Q4_1, O.Q5_1) else (0,))
     for off in offs:
         e = rng.integers(0x1400, 0x2c00, size=(rows, n // qk), dtype=np.uint16)
         w[:, :, off:off + 2] = e.view(np.uint8).reshape(rows, n // qk, 2)
@@ -56,6 +60,13 @@ def random_blocks(ty, n, rows, seed):
 
 
 def quantized(ty, n, rows, seed):
+    if ty in K23_TYPES:
+        # no Q2_K / Q3_K quantizer here: the reference's own quantized bytes
+        # (quants_ref.bin, 4 super-blocks), rows cycled through its blocks
+        q = {tid: q for (_, tid, _n, q, _d) in fx.quant_sections("quants_ref.bin")}[ty].reshape(4, -1)
+        nb = n // 256
+        idx = (np.arange(rows)[:, None] + np.arange(nb)[None, :] + seed) % 4
+        return np.ascontiguousarray(q[idx].reshape(rows, -1))
     wf = (np.random.default_rng(seed).standard_normal((rows, n)) * 0.02).astype(np.float32)
     return O.quantize(ty, wf).reshape(rows, O.row_size(ty, n))
 
@@ -75,6 +86,33 @@ def run_case(be, ty, n, rows, cols, seed=0, check_sub=True, x=None, weights="qua
     if check_sub:
         sub = be.mul_mat_subsums(wd, ty, n, xd).cpu().numpy()
         assert np.array_equal(sub, want_sub), "int32 sub-sums differ"
+    if ty in K23_TYPES and check_sub:
+        # the GPU folds d8*d*isum (- d8*dmin*summs) once per super-block: it is
+        # held against the float64 value of the exact integer sums (the
+        # oracle's export, checked bit-exact above) within gamma_(nb+16) of the
+        # terms' magnitudes, and against the fp32 oracle (the reference's 8-lane
+        # order, whose own error follows its lane partials) within 1e-4
+        nb = n // 256
+        wb = w.reshape(rows, nb, -1)
+        off = 80 if ty == O.Q2_K else 108
+        d = wb[..., off:off + 2].copy().view(np.float16)[..., 0].astype(np.float64)
+        act8 = O.mul_mat_act(ty, n, rows, x, cols).reshape(cols, nb, 292)
+        d8 = act8[..., 0:4].copy().view(np.float32)[..., 0].astype(np.float64)
+        if ty == O.Q2_K:
+            dm = wb[..., 82:84].copy().view(np.float16)[..., 0].astype(np.float64)
+            t_main = d8[:, None] * d[None] * want_sub[..., 0]
+            t_min = d8[:, None] * dm[None] * want_sub[..., 1]
+            exact = (t_main - t_min).sum(-1)
+            mag = (np.abs(t_main) + np.abs(t_min)).sum(-1)
+        else:
+            t_main = d8[:, None] * d[None] * want_sub
+            exact = t_main.sum(-1)
+            mag = np.abs(t_main).sum(-1)
+        bound = 2.0 * (nb + 16) * 2.0 ** -24 * mag
+        assert np.all(np.abs(got.astype(np.float64) - exact) <= bound), \
+            f"max excess {np.max(np.abs(got - exact) - bound):.3e}"
+        assert rel_err(got, want) <= 1e-4
+        return
     if ty in MIN_TYPES:
         # d * d8 * isum + m * s per block, summed over nb blocks in different
         # orders by the reference (8 lanes + a separate m * s chain) and the
@@ -172,3 +210,22 @@ def test_zero_and_extreme_codes(be):
     sub = be.mul_mat_subsums(torch.from_numpy(w).cuda(), O.Q8_0, n, torch.from_numpy(x).cuda()).cpu().numpy()
     assert np.array_equal(sub, want_sub)
     assert rel_err(got, want) <= 1e-4
+
+
+
+@pytest.mark.parametrize("ty", K23_TYPES)
+@pytest.mark.parametrize("cols", [1, 2, 3, 4, 5, 8, 11])
+def test_k23_small_shapes(be, ty, cols):
+    """Q2_K / Q3_K: the reference's quantized blocks and random block bytes,
+    1-11 columns (launches of at most 4), partial row groups"""
+    for n, rows in [(1024, 64), (2048, 72), (256, 8)]:
+        run_case(be, ty, n, rows, cols, seed=cols + ty)
+        run_case(be, ty, n, rows, cols, seed=cols + ty, weights="random")
+
+
+@pytest.mark.parametrize("ty", K23_TYPES)
+@pytest.mark.parametrize("n,rows,cols", [(4096, 4096, 1), (14336, 4096, 2), (4096, 14336, 4), (2816, 24, 3)])
+def test_k23_decode_shapes(be, ty, n, rows, cols):
+    """the Llama decode shapes and a K of 11 super-blocks (several wavefronts
+    per row, the last one partly empty)"""
+    run_case(be, ty, n, rows, cols, seed=5, weights="random")

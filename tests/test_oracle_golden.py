@@ -486,3 +486,107 @@ def test_q41_q51_vec_dot_brute_force(ty):
         assert route == O.ROUTE_VECDOT
         assert np.array_equal(sub.reshape(-1), isum)
         assert out[0, 0] == np.float32(got)
+
+
+def test_q2k_q3k_dequant_bit_exact():
+    """quants_ref.bin sections 10 (Q2_K) and 11 (Q3_K): the oracle's
+    dequantize_row of the reference's bytes equals the reference's values."""
+    secs = {tid: (q, deq) for (_, tid, n, q, deq) in fx.quant_sections("quants_ref.bin")}
+    for tid in (O.Q2_K, O.Q3_K):
+        q, deq = secs[tid]
+        assert deq.any()
+        got = O.dequantize(tid, q, 1024)
+        assert np.array_equal(got.view(np.uint32), deq.view(np.uint32)), f"type {tid}"
+
+
+def _k23_terms(w, ty, act, n):
+    """numpy brute force per super-block: (isum, summs, d, dmin) from the block
+    bytes (Q2_K: 4-bit scale | 4-bit min; Q3_K: 6-bit scales - 32, 3-bit codes)"""
+    nb = n // 256
+    a = act.reshape(nb, 292)
+    d8 = a[:, 0:4].copy().view(np.float32)[:, 0].astype(np.float64)
+    q8 = a[:, 4:260].view(np.int8).astype(np.int64)
+    bs = a[:, 260:292].copy().view(np.int16).astype(np.int64)
+    deq = O.dequantize(ty, w, n).reshape(nb, 256).astype(np.float64)
+    if ty == O.Q2_K:
+        b = w.reshape(nb, 84)
+        sc = b[:, 0:16].astype(np.int64)
+        qs = b[:, 16:80]
+        d = b[:, 80:82].copy().view(np.float16)[:, 0].astype(np.float64)
+        dm = b[:, 82:84].copy().view(np.float16)[:, 0].astype(np.float64)
+        # code of element 128j + 32k + e: (qs[32j + e] >> 2k) & 3
+        codes = np.zeros((nb, 256), np.int64)
+        for j in range(2):
+            for k in range(4):
+                codes[:, 128 * j + 32 * k:128 * j + 32 * k + 32] = (qs[:, 32 * j:32 * j + 32] >> (2 * k)) & 3
+        g = (codes * q8).reshape(nb, 16, 16).sum(-1)
+        isum = ((sc & 15) * g).sum(-1)
+        summs = ((sc >> 4) * bs).sum(-1)
+        # the dequantized values agree with the codes / scales read here
+        want_deq = np.repeat(d[:, None] * (sc & 15), 16, 1) * codes - np.repeat(dm[:, None] * (sc >> 4), 16, 1)
+        assert np.allclose(deq, want_deq, rtol=1e-6, atol=1e-30)
+        return isum, summs, d8 * d, d8 * dm
+    b = w.reshape(nb, 110)
+    d = b[:, 108:110].copy().view(np.float16)[:, 0].astype(np.float64)
+    # values from the pinned dequantizer: v * (sc - 32) * d, integers once divided back
+    scale_vals = np.zeros((nb, 16), np.float64)
+    codes = np.zeros((nb, 256), np.int64)
+    hm = b[:, 0:32]
+    qs = b[:, 32:96]
+    for j in range(2):
+        for k in range(4):
+            lo = ((qs[:, 32 * j:32 * j + 32] >> (2 * k)) & 3).astype(np.int64)
+            hb = (hm >> (4 * j + k)) & 1
+            codes[:, 128 * j + 32 * k:128 * j + 32 * k + 32] = np.where(hb != 0, lo, lo - 4)
+    raw = b[:, 96:108]
+    aux = raw.copy().view(np.uint32).astype(np.uint64)
+    km1, km2 = 0x03030303, 0x0f0f0f0f
+    w4 = [(aux[:, 0] & km2) | ((aux[:, 2] & km1) << 4), (aux[:, 1] & km2) | (((aux[:, 2] >> 2) & km1) << 4),
+          ((aux[:, 0] >> 4) & km2) | (((aux[:, 2] >> 4) & km1) << 4),
+          ((aux[:, 1] >> 4) & km2) | (((aux[:, 2] >> 6) & km1) << 4)]
+    for i in range(16):
+        scale_vals[:, i] = ((w4[i >> 2] >> (8 * (i & 3))) & 0xff).astype(np.float64) - 32
+    g = (codes * q8).reshape(nb, 16, 16).sum(-1)
+    isum = (scale_vals.astype(np.int64) * g).sum(-1)
+    want_deq = np.repeat(d[:, None] * scale_vals, 16, 1) * codes
+    assert np.allclose(deq, want_deq, rtol=1e-6, atol=1e-30)
+    return isum, np.zeros(nb, np.int64), d8 * d, np.zeros(nb)
+
+
+@pytest.mark.parametrize("ty", [O.Q2_K, O.Q3_K])
+def test_q2k_q3k_vec_dot_brute_force(ty):
+    """vec_dot_q2_K_q8_K / vec_dot_q3_K_q8_K (no reference fixture holds their
+    dots): exact integer sums from numpy on the block bytes (the value layout
+    itself checked against the fixture-pinned dequantizer), the float result
+    against sum d8*d*isum - d8*dmin*summs in float64, and the routed MUL_MAT's
+    integer exports; the reference's own quantized bytes (quants_ref.bin) and
+    random blocks."""
+    rng = np.random.default_rng(21)
+    secs = {tid: q for (_, tid, n, q, deq) in fx.quant_sections("quants_ref.bin")}
+    bs = 84 if ty == O.Q2_K else 110
+    for trial in range(5):
+        if trial == 0:
+            w, n = np.ascontiguousarray(secs[ty]), 1024
+        else:
+            n = 1024
+            w = rng.integers(0, 256, size=(n // 256) * bs, dtype=np.uint8)
+            blk = w.reshape(-1, bs)
+            off = 80 if ty == O.Q2_K else 108
+            blk[:, off:off + 2] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8)
+            if ty == O.Q2_K:
+                blk[:, 82:84] = np.frombuffer(np.float16(0.02).tobytes(), np.uint8)
+        x = rng.standard_normal(n).astype(np.float32) * (5.0 if trial == 2 else 1.0)
+        a = O.quantize(O.Q8_K, x, kind="quantize_row_q8_K_ref")
+        isum, summs, dd, dmn = _k23_terms(w, ty, a, n)
+        want = float(np.sum(dd * isum - dmn * summs))
+        f = O.lib().oracle_vec_dot_q2_K_q8_K if ty == O.Q2_K else O.lib().oracle_vec_dot_q3_K_q8_K
+        got = f(n, O._p(np.ascontiguousarray(w)), O._p(a))
+        scale = float(np.sum(np.abs(dd * isum)) + np.sum(np.abs(dmn * summs)))
+        assert abs(got - want) <= 1e-6 * scale, (trial, got, want)
+        out, route, sub = O.mul_mat(ty, w, n, 1, x[None, :], 1, want_subsums=True)
+        assert route == O.ROUTE_VECDOT
+        if ty == O.Q2_K:
+            assert np.array_equal(sub.reshape(-1, 2)[:, 0], isum) and np.array_equal(sub.reshape(-1, 2)[:, 1], summs)
+        else:
+            assert np.array_equal(sub.reshape(-1), isum)
+        assert out[0, 0] == np.float32(got)

@@ -621,7 +621,7 @@ def main():
     log(f"Q4_K 4096x14336 GEMV kernel: {us:.2f} us, {ach:.1f} GB/s ({ach / HBM_PEAK_GBS * 100:.1f}% of HBM)")
     roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-            "kernel": "ghip_gemv_q4_K_f_c1_r1x4 (Q4_K 4096->14336, batch 1, f32 activations, Q8_K quantization fused)",
+            "kernel": "ghip_gemv_q4_K_f_c1_r1x7s3 (Q4_K 4096->14336, batch 1, f32 activations, Q8_K quantization fused)",
             "avg_us": round(us, 3), "bytes_per_launch": alg}
     extras = {}
     if not args.no_extras:

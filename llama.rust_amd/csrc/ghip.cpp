@@ -357,6 +357,20 @@ bool gemv_v2(const MulMatPlan &p) {
 // deeper on large matrices: Q4_K 4096 -> 14336 9.6 -> 9.2 us, Q6_K 14336 ->
 // 4096 16.0 -> 14.8 us; smaller matrices keep 2 x 2 (4096 -> 4096: 4.5 us
 // against 5.2 with 1 x 4).
+// Q4_K at one activation row with K in one wavefront: one-row groups, teams
+// and rows per team chosen for about 256 workgroups (one per CU), ns groups
+// loaded before the activation is quantized.  Measured (graph-timed, rotating
+// weights): 4096 -> 14336 9.0 -> 8.2 us (1 x 7, 3 slots), 4096 -> 4096
+// 4.6 -> 4.5 us, 4096 -> 1024 4.2 -> 3.6 us (1 x 2, 4 teams).
+void gemv_q4k_one_row(int64_t rows, int &teams, int &ng, int &ns) {
+    teams = rows >= 4096 ? 8 : 4;
+    const int64_t per_team = (rows + 256 * teams - 1) / (256 * teams);
+    if (per_team <= 2) ng = 2, ns = 2;
+    else if (per_team <= 4) ng = 4, ns = 3;
+    else if (per_team <= 7) ng = 7, ns = 3;
+    else ng = 8, ns = 3;
+}
+
 void gemv_groups(int wtype, int64_t M, int64_t N, int &rb, int &ng) {
     rb = 2;
     ng = 2;
@@ -507,8 +521,12 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     // K-quants (Q4_K, Q6_K): T row teams share one LDS copy of the quantized
     // activations; a team's wavefronts hold NG groups of RB rows in flight.
     const bool q4k = gemv_v2(p);
-    int rb_d, ng_d;
+    int rb_d, ng_d, ns_d = 2, teams_d = p.N < 8192 && p.M <= 2 ? 4 : 8;
     gemv_groups(p.wtype, p.M, p.N, rb_d, ng_d);
+    if (q4k && p.wtype == GHIP_TYPE_Q4_K && p.M == 1 && waves_k == 1) {
+        rb_d = 1;
+        gemv_q4k_one_row(p.N, teams_d, ng_d, ns_d);
+    }
     // GHIP_GEMV_PERSIST=1: Q4_K at one row, K in one wavefront, from 8192
     // weight rows on the persistent grid (GHIP_GEMV_WGS workgroups of 8 teams,
     // each team an equal run of consecutive rows; "_r1x0").  Off by default:
@@ -519,15 +537,14 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     const int rb = persist ? 1 : q4k ? env_int("GHIP_GEMV_RB", rb_d) : 8;
     const int ng = persist ? 0 : q4k ? env_int("GHIP_GEMV_NG", ng_d) : 1;
     if (q4k && !persist && !((rb == 2 && (ng == 2 || ng == 4 || ng == 8)) || (rb == 4 && (ng == 2 || ng == 4)) ||
-                 (rb == 1 && p.wtype == GHIP_TYPE_Q4_K && p.M == 1 && (ng == 2 || ng == 4 || ng == 8)) ||
+                 (rb == 1 && p.wtype == GHIP_TYPE_Q4_K && p.M == 1 && (ng == 2 || ng == 4 || ng == 7 || ng == 8)) ||
                  (p.wtype == GHIP_TYPE_Q6_K && p.M == 1 && ((rb == 2 && ng == 8) || (rb == 1 && (ng == 4 || ng == 8))))))
         return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "GHIP_GEMV_RB x GHIP_GEMV_NG must be 2x2, 2x4, 2x8, 4x2 or 4x4");
     const int rows_per_team = rb * ng;
     // 8 teams, except 4 for one or two activation rows on matrices under 8192
     // rows: measured on 4096->1024 / 4096->4096 / 4096->14336 at batch 1-8
     // (there, fewer and fuller workgroups quantize the activation fewer times)
-    const int dflt_teams = p.N < 8192 && p.M <= 2 ? 4 : 8;
-    const int teams = q4k ? std::max(1, std::min(8 / waves_k, env_int("GHIP_GEMV_TEAMS", dflt_teams))) : 1;
+    const int teams = q4k ? std::max(1, std::min(8 / waves_k, env_int("GHIP_GEMV_TEAMS", teams_d))) : 1;
     const int rows_per_wg = persist ? 0 : rows_per_team * teams;
     const unsigned grid = persist ? (unsigned)std::max(1, std::min(env_int("GHIP_GEMV_WGS", 256), (int)((p.N + 7) / 8)))
                                   : (unsigned)((p.N + rows_per_wg - 1) / rows_per_wg);
@@ -538,6 +555,8 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
         std::string name = std::string(gemv_base(p.wtype)) + (p.wtype == GHIP_TYPE_Q6_K && q4k ? "_v2" : "") +
                            (fused ? "_f" : "") + (sub ? "_sub" : "") +
                            "_c" + std::to_string(NC) + (q4k ? "_r" + std::to_string(rb) + "x" + std::to_string(ng) : std::string());
+        const int ns = q4k && !persist && p.wtype == GHIP_TYPE_Q4_K && rb == 1 && p.M == 1 ? env_int("GHIP_GEMV_NS", ns_d) : 2;
+        if (ns != 2) name += "s" + std::to_string(ns);
         int32_t *sub_c = sub;
         if (sub) {
             const int64_t per = (p.wtype == GHIP_TYPE_Q4_K || p.wtype == GHIP_TYPE_Q5_K || p.wtype == GHIP_TYPE_Q2_K) ? 2 * p.nb : p.nb;
@@ -1376,13 +1395,19 @@ ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipS
     // 8 row teams per workgroup: measured on q/k/v (4096 + 1024 + 1024 rows)
     // 6.8 -> 5.9 us at batch 1 and 9.1 -> 7.8 us at batch 2 against 4 teams;
     // gate/up (2 x 14336) within 2 % either way
-    const int dflt_teams = 8;
-    const int teams = std::max(1, std::min(8 / waves_k, env_int("GHIP_GEMV_TEAMS", dflt_teams)));
     int64_t rows_total = 0;
     for (int i = 0; i < n; i++) rows_total += p[i].N;
-    int rb, ng;
+    int rb, ng, ns = 2, teams = std::max(1, std::min(8 / waves_k, env_int("GHIP_GEMV_TEAMS", 8)));
     gemv_groups(p0.wtype, p0.M, rows_total, rb, ng);
     if (p0.wtype == GHIP_TYPE_Q5_K) rb = ng = 2;
+    if (p0.wtype == GHIP_TYPE_Q4_K && p0.M == 1 && waves_k == 1) {
+        int t;
+        rb = 1;
+        gemv_q4k_one_row(rows_total, t, ng, ns);
+        teams = std::max(1, std::min(8, env_int("GHIP_GEMV_TEAMS", t)));
+        ng = env_int("GHIP_GEMV_NG", ng);
+        ns = env_int("GHIP_GEMV_NS", ns);
+    }
     const int rows_per_wg = rb * ng * teams;
     GemvMulti g{};
     int wg = 0;
@@ -1408,7 +1433,8 @@ ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipS
                          (size_t)rows_per_wg * waves_k * NC * sizeof(float);
     if (shmem > 160 * 1024) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: decode LDS image too large");
     const std::string name = std::string(gemv_base(p0.wtype)) + (p0.wtype == GHIP_TYPE_Q6_K ? "_v2" : "") + "_f_c" +
-                             std::to_string(NC) + "_r" + std::to_string(rb) + "x" + std::to_string(ng) + "_multi";
+                             std::to_string(NC) + "_r" + std::to_string(rb) + "x" + std::to_string(ng) +
+                             (ns != 2 ? "s" + std::to_string(ns) : std::string()) + "_multi";
     const int n_mat = (int)std::max<int64_t>(0, std::min<int64_t>(nc, p0.n_mat));
     return ctx->launch(name, dim3((unsigned)wg), dim3(64 * waves_k * teams), shmem, s, g, (int64_t)p0.w_row_bytes,
                        (int)p0.nb, (const uint8_t *)nodes[0].src[1]->data, (int64_t)nodes[0].src[1]->nb[1], nc,

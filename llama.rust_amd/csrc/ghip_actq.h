@@ -5,6 +5,7 @@
 // LDS image: codes [NC][K] int8 | d [NC][nb] f32 | 16-element sums
 // [NC][nb][16] int32.
 #pragma once
+#include <type_traits>
 #include "ghip_common.h"
 
 // Quantization of the activation rows into the LDS image, bit-identical to
@@ -45,13 +46,22 @@ DEV void quant_q8K_store(const XTask &t, int nb, int n_mat, int total, int task,
         const float a = fabsf(v[i]);
         if (a > bax) { bax = a; bval = v[i]; bidx = 16 * l + i; }
     }
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-        const float oax = __shfl_xor(bax, o, 64);
-        const float oval = __shfl_xor(bval, o, 64);
-        const int oidx = __shfl_xor(bidx, o, 64);
+    // all-reduce over the task's 16 lanes (one DPP row; every caller runs
+    // whole wavefronts with task % 16 == lane % 16): partners by quad xor 1,
+    // quad xor 2, half-row mirror (i <-> 7 - i) and row mirror (i <-> 15 - i),
+    // each pairing two disjoint groups that already agree, so every lane ends
+    // with the largest |v|, ties to the lowest index
+    auto step = [&](auto ctrl) {
+        constexpr int C = decltype(ctrl)::value;
+        const float oax = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(bax), C, 0xF, 0xF, false));
+        const float oval = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(bval), C, 0xF, 0xF, false));
+        const int oidx = __builtin_amdgcn_update_dpp(0, bidx, C, 0xF, 0xF, false);
         if (oax > bax || (oax == bax && oidx < bidx)) { bax = oax; bval = oval; bidx = oidx; }
-    }
+    };
+    step(std::integral_constant<int, 0xB1>{});
+    step(std::integral_constant<int, 0x4E>{});
+    step(std::integral_constant<int, 0x141>{});
+    step(std::integral_constant<int, 0x140>{});
     int q[16];
     float d;
     if (bax == 0.0f) {

@@ -69,7 +69,7 @@ struct Q4KAct {
 // same scales, mins and integer sums with each nibble's fifth bit taken from
 // qh -- bit 2i of qh[e] for sub-block 2i (low nibbles), bit 2i+1 for 2i+1
 // (vec_dot.rs:928-980).
-template <int NC, bool SUBSUMS, bool FUSEQ, int RB, int NG, bool Q5 = false>
+template <int NC, bool SUBSUMS, bool FUSEQ, int RB, int NG, bool Q5 = false, int NSLOT = 2>
 __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
                                               int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
                                               int ncols, float *__restrict__ dst, int64_t ldd,
@@ -115,7 +115,7 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
     // groups in flight and computes its early rows while its later rows are
     // still on the way (with every group loaded up front, most data would
     // land at the end and all of the arithmetic would follow the last byte).
-    constexpr int NS = PERSIST ? 2 : NG < 2 ? NG : 2;  // register slots
+    constexpr int NS = PERSIST ? 2 : NG < NSLOT ? NG : NSLOT;  // register slots
     uint4 hdr[NS][RB], qa[NS][RB], qb[NS][RB];
     uint4 xh0[NS][Q5 ? RB : 1], xh1[NS][Q5 ? RB : 1];  // Q5_K qh[0..15], qh[16..31]
     auto load_group = [&](int gi, int slot) {
@@ -266,12 +266,11 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
     if constexpr (PERSIST) {
         const int nrow = max(0, r1 - r0);
         for (int gi = 0; gi < nrow; gi += 2) {
+            // loads outside run-time branches (clamped rows past the end)
             compute_group(r0 + gi, hdr[0], qa[0], qb[0], xh0[0], xh1[0]);
-            if (gi + 2 < nrow) load_group(gi + 2, 0);
-            if (gi + 1 < nrow) {
-                compute_group(r0 + gi + 1, hdr[1], qa[1], qb[1], xh0[1], xh1[1]);
-                if (gi + 3 < nrow) load_group(gi + 3, 1);
-            }
+            load_group(gi + 2, 0);
+            if (gi + 1 < nrow) compute_group(r0 + gi + 1, hdr[1], qa[1], qb[1], xh0[1], xh1[1]);
+            load_group(gi + 3, 1);
         }
         return;  // (the host launches it with K in one wavefront)
     } else {
@@ -279,7 +278,10 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
         for (int gi = 0; gi < NG; gi++) {
             const int sl = gi % NS;
             if (r0 + gi * RB < r1) compute_group(r0 + gi * RB, hdr[sl], qa[sl], qb[sl], xh0[sl], xh1[sl]);
-            if (gi + NS < NG && r0 + (gi + NS) * RB < r1) load_group(gi + NS, sl);
+            // unconditional (rows past the team's end re-read a clamped valid
+            // row): a load under a run-time branch makes the compiler wait
+            // for every outstanding load before the next group's arithmetic
+            if (gi + NS < NG) load_group(gi + NS, sl);
         }
     }
     if (nwk == 1) return;
@@ -472,7 +474,7 @@ __device__ __forceinline__ void gemv_q6K_v2_impl(const uint8_t *__restrict__ W, 
     for (int gi = 0; gi < NG; gi++) {
         const int sl = gi % NS;
         if (r0 + gi * RB < r1) compute_group(r0 + gi * RB, ql0[sl], ql1[sl], qhv[sl], scv[sl], dv[sl]);
-        if (gi + NS < NG && r0 + (gi + NS) * RB < r1) load_group(gi + NS, sl);
+        if (gi + NS < NG) load_group(gi + NS, sl);  // unconditional, as in gemv_q4K_impl
     }
     if (nwk == 1) return;
     __syncthreads();
@@ -1234,10 +1236,25 @@ GEMV_PAIR_ALL(ghip_gemv_q8_0, gemv_q8_0_impl)
         gemv_q4K_impl<NC, true, true, RB, NG, Q5>(Q4K_PASS);                                                    \
     }
 #define Q4K_INST(NC, RB, NG) QK45_INST(q4_K, false, NC, RB, NG)
+// NS register slots (row groups loaded before the activation is quantized)
+#define Q4K_INST_S(NC, RB, NG, NS)                                                                                \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_c##NC##_r##RB##x##NG##s##NS(Q4K_ARGS) {      \
+        gemv_q4K_impl<NC, false, false, RB, NG, false, NS>(Q4K_PASS);                                           \
+    }                                                                                                             \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_sub_c##NC##_r##RB##x##NG##s##NS(Q4K_ARGS) {  \
+        gemv_q4K_impl<NC, true, false, RB, NG, false, NS>(Q4K_PASS);                                            \
+    }                                                                                                             \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_f_c##NC##_r##RB##x##NG##s##NS(Q4K_ARGS) {    \
+        gemv_q4K_impl<NC, false, true, RB, NG, false, NS>(Q4K_PASS);                                            \
+    }                                                                                                             \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q4_K_f_sub_c##NC##_r##RB##x##NG##s##NS(Q4K_ARGS) { \
+        gemv_q4K_impl<NC, true, true, RB, NG, false, NS>(Q4K_PASS);                                             \
+    }
+Q4K_INST_S(1, 1, 4, 3) Q4K_INST_S(1, 1, 7, 3) Q4K_INST_S(1, 1, 8, 3)
 // register row groups (RB rows) x groups in flight (NG)
 #define Q4K_INST_RB(NC) Q4K_INST(NC, 2, 2) Q4K_INST(NC, 2, 4) Q4K_INST(NC, 4, 2) Q4K_INST(NC, 2, 8) Q4K_INST(NC, 4, 4)
 Q4K_INST_RB(1) Q4K_INST_RB(2) Q4K_INST_RB(4) Q4K_INST_RB(8)
-Q4K_INST(1, 1, 4) Q4K_INST(1, 1, 8) Q4K_INST(1, 1, 2) Q4K_INST(1, 1, 0)
+Q4K_INST(1, 1, 4) Q4K_INST(1, 1, 8) Q4K_INST(1, 1, 2) Q4K_INST(1, 1, 0) Q4K_INST(1, 1, 7)
 // Q5_K: the same shapes and naming as Q4_K
 #define Q5K_INST_RB(NC) QK45_INST(q5_K, true, NC, 2, 2) QK45_INST(q5_K, true, NC, 2, 4) \
     QK45_INST(q5_K, true, NC, 4, 2) QK45_INST(q5_K, true, NC, 2, 8) QK45_INST(q5_K, true, NC, 4, 4)
@@ -1293,6 +1310,20 @@ GEMV_MULTI(q5_K, 4, gemv_q4K_impl, true) GEMV_MULTI(q5_K, 8, gemv_q4K_impl, true
 GEMV_MULTI(q6_K_v2, 1, gemv_q6K_v2_impl)
 // one-row groups streamed four (Q4_K) or eight (Q6_K) deep: the batch-1 shapes of large matrices
 GEMV_MULTI_RN(q4_K, 1, 1, 4, gemv_q4K_impl, false)
+GEMV_MULTI_RN(q4_K, 1, 1, 2, gemv_q4K_impl, false)
+#define GEMV_MULTI_RNS(TN, NC, RB, NG, NS, IMPL)                                                                 \
+    extern "C" __global__ void __launch_bounds__(512)                                                            \
+        ghip_gemv_##TN##_f_c##NC##_r##RB##x##NG##s##NS##_multi(GemvMulti g, int64_t w_row_bytes, int nb,        \
+                                                               const uint8_t *__restrict__ act,                  \
+                                                               int64_t act_row_bytes, int ncols, int n_mat) {    \
+        const int bx = blockIdx.x;                                                                               \
+        int i = 0;                                                                                               \
+        _Pragma("unroll") for (int k = 1; k < 4; k++) if (k < g.n && bx >= g.wg0[k]) i = k;                     \
+        IMPL<NC, false, true, RB, NG, false, NS>(g.W[i], w_row_bytes, g.rows[i], nb, act, act_row_bytes, ncols,   \
+                                                 g.dst[i], g.ldd[i], nullptr, n_mat, bx - g.wg0[i]);             \
+    }
+GEMV_MULTI_RNS(q4_K, 1, 1, 4, 3, gemv_q4K_impl) GEMV_MULTI_RNS(q4_K, 1, 1, 7, 3, gemv_q4K_impl)
+GEMV_MULTI_RNS(q4_K, 1, 1, 8, 3, gemv_q4K_impl)
 GEMV_MULTI_RN(q6_K_v2, 1, 1, 8, gemv_q6K_v2_impl)
 
 // Q4_0 / Q5_0 / Q8_0 siblings: ready Q8_0 rows (one quantize launch for the

@@ -14,6 +14,7 @@
 // the integer dot_b (all partial sums < 2^24).  The epilogue then applies the
 // reference's own fold -- the same fma, the same block order -- so the output
 // is bit-identical to the reference's repack route.
+#include <type_traits>
 #include "ghip_common.h"
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
@@ -552,9 +553,19 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
                                              int ngp, int order) {
     constexpr int TP = 32 * NMT;
     static_assert(256 % TP == 0, "one pair per thread");
-    __shared__ __attribute__((aligned(16))) float ds_lds[2][MOE_GB][TP];
-    __shared__ __attribute__((aligned(16))) uint4 a_lds[2][MOE_GB][4][TP];  // [stage][block][piece][pair]
-    __shared__ __attribute__((aligned(16))) uint32_t w_lds[2][MOE_TR][MOE_WIN * 4];
+    // One LDS variable per pipeline stage, every access naming its stage at
+    // compile time: the compiler then knows that the next stage's LDS-DMA
+    // writes do not alias this stage's reads, and does not wait for them
+    // (one [2][..] array indexed at run time made it wait for the prefetch
+    // before every read of the current stage)
+    __shared__ __attribute__((aligned(16))) float ds_lds0[MOE_GB][TP], ds_lds1[MOE_GB][TP];
+    __shared__ __attribute__((aligned(16))) uint4 a_lds0[MOE_GB][4][TP], a_lds1[MOE_GB][4][TP];  // [block][piece][pair]
+    __shared__ __attribute__((aligned(16))) uint32_t w_lds0[MOE_TR][MOE_WIN * 4], w_lds1[MOE_TR][MOE_WIN * 4];
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    auto A_ = [&](auto st) -> decltype(a_lds0) & { if constexpr (decltype(st)::value == 0) return a_lds0; else return a_lds1; };
+    auto D_ = [&](auto st) -> decltype(ds_lds0) & { if constexpr (decltype(st)::value == 0) return ds_lds0; else return ds_lds1; };
+    auto W_ = [&](auto st) -> decltype(w_lds0) & { if constexpr (decltype(st)::value == 0) return w_lds0; else return w_lds1; };
     __shared__ int pairs[TP];
     // Workgroups go to the 8 XCDs round-robin by linear id.  With a grid whose
     // size is a multiple of 8 (the host pads the tile count), order 1 remaps
@@ -605,20 +616,20 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
         wl16[c] = 16 * l;
     }
     const int wv = threadIdx.x >> 6;
-    auto issue = [&](int g, int stage, bool with_w) {
+    auto issue = [&](int g, auto stage, bool with_w) {
 #pragma unroll
         for (int c = 0; c < ACHUNK; c++) {
             const int rest = (c * 256 + (int)threadIdx.x) / TP;
             const int piece = rest & 3, b = min(MOE_GB * g + (rest >> 2), nb - 1);
             g2lds(my_arow + ((int64_t)b * 4 + piece) * n_pairs * 16,
-                  reinterpret_cast<uint8_t *>(&a_lds[stage][0][0][0]) + (c * 256 + 64 * wv) * 16);
+                  reinterpret_cast<uint8_t *>(&A_(stage)[0][0][0]) + (c * 256 + 64 * wv) * 16);
         }
 #pragma unroll
         for (int c = 0; c < DCH; c++) {
             if (c * 256 + 64 * wv >= MOE_GB * TP) continue;
             const int b = min(MOE_GB * g + (c * 256 + (int)threadIdx.x) / TP, nb - 1);
             __builtin_amdgcn_global_load_lds(my_drow + (int64_t)b * n_pairs,
-                                             (lds_void *)(reinterpret_cast<uint8_t *>(&ds_lds[stage][0][0]) +
+                                             (lds_void *)(reinterpret_cast<uint8_t *>(&D_(stage)[0][0]) +
                                                           (c * 256 + 64 * wv) * 4),
                                              4, 0, 0);
         }
@@ -628,13 +639,13 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
             for (int c = 0; c < WCHUNK; c++)
                 if (c * 256 + 64 * wv < MOE_TR * MOE_WIN)
                     g2lds(src + (c * 256 + (int)threadIdx.x) * 16,
-                          reinterpret_cast<uint8_t *>(&w_lds[stage][0][0]) + (c * 256 + 64 * wv) * 16);
+                          reinterpret_cast<uint8_t *>(&W_(stage)[0][0]) + (c * 256 + 64 * wv) * 16);
         } else if (with_w) {
 #pragma unroll
             for (int c = 0; c < WCHUNK; c++)
                 if (c * 256 + 64 * wv < MOE_TR * MOE_WIN)
                     g2lds(wbase[c] + min(MOE_WB * g + wl16[c], row_bytes - 16),
-                          reinterpret_cast<uint8_t *>(&w_lds[stage][0][0]) + (c * 256 + 64 * wv) * 16);
+                          reinterpret_cast<uint8_t *>(&W_(stage)[0][0]) + (c * 256 + 64 * wv) * 16);
         }
     };
     float acc[NMT][16];
@@ -650,10 +661,10 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
     asm volatile("v_mov_b32 %0, 127" : "=v"(s127));
 
     // dots of one block: A = the 16 qs bytes of row li, B = this lane's plane
-    auto mfma = [&](const uint32_t (&q)[4], int scale_a, int stage, int kb, int mt) {
+    auto mfma = [&](const uint32_t (&q)[4], int scale_a, auto stage, int kb, int mt) {
         // B lane half h2: bytes 0..15 = K 16h2.. (ql piece h2), bytes 16..31 =
         // K 32+16h2.. (qh piece h2); A lane half h holds K 32h..32h+31
-        const uint4 b0 = a_lds[stage][kb][h2][mt * 32 + li], b1 = a_lds[stage][kb][2 + h2][mt * 32 + li];
+        const uint4 b0 = A_(stage)[kb][h2][mt * 32 + li], b1 = A_(stage)[kb][2 + h2][mt * 32 + li];
         const v8i A = {(int)q[0], (int)q[1], (int)q[2], (int)q[3], 0, 0, 0, 0};
         const v8i B = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
         return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(A, B, zero, 4, 0, 0, scale_a, 0, scale_b);
@@ -686,14 +697,14 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
     const int nga = (nb + MOE_GB - 1) / MOE_GB;
     if (REG) ngroups = nga;  // every window of the registered copy is whole (zero past the row)
     const int rl = w * 32 + li;
-    issue(0, 0, ngroups > 0);
-    for (int g = 0; g < nga; g++) {
-        const int stage = g & 1;
+    issue(0, I0{}, ngroups > 0);
+    auto group = [&](int g, auto stage) {
+        constexpr int other = 1 - decltype(stage)::value;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (g + 1 < nga) issue(g + 1, stage ^ 1, g + 1 < ngroups);
+        if (g + 1 < nga) issue(g + 1, std::integral_constant<int, other>{}, g + 1 < ngroups);
         if (g < ngroups) {
-            const uint32_t *wl = w_lds[stage][rl];
+            const uint32_t *wl = W_(stage)[rl];
             // GGUF windows: 17-byte blocks from byte 0 (the whole window in
             // registers); registered windows: qs of block kb at 16kb, the e
             // bytes at 64 (aligned reads, no byte shifts)
@@ -734,7 +745,7 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
 #pragma unroll
                     for (int mt = 0; mt < NMT; mt++)
                         if (mt == 0 || np > 32 * mt)
-                            fold_fast(mfma(q, (int)e_of(kb), stage, kb, mt), ds_lds[stage][kb][mt * 32 + li], mt);
+                            fold_fast(mfma(q, (int)e_of(kb), stage, kb, mt), D_(stage)[kb][mt * 32 + li], mt);
                 }
             } else {
                 for (int kb = 0; kb < MOE_GB && kb < nbl; kb++) {
@@ -743,7 +754,7 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
 #pragma unroll
                     for (int mt = 0; mt < NMT; mt++)
                         if (mt == 0 || np > 32 * mt)
-                            fold_exact(mfma(q, s127, stage, kb, mt), ds_lds[stage][kb][mt * 32 + li], e_of(kb),
+                            fold_exact(mfma(q, s127, stage, kb, mt), D_(stage)[kb][mt * 32 + li], e_of(kb),
                                        MOE_GB * g + kb, mt);
                 }
             }
@@ -756,9 +767,13 @@ __device__ __forceinline__ void moe_fp4_impl(const uint8_t *__restrict__ as, int
 #pragma unroll
                 for (int mt = 0; mt < NMT; mt++)
                     if (mt == 0 || np > 32 * mt)
-                        fold_exact(mfma(q, s127, stage, kb, mt), ds_lds[stage][kb][mt * 32 + li], wb[0], b, mt);
+                        fold_exact(mfma(q, s127, stage, kb, mt), D_(stage)[kb][mt * 32 + li], wb[0], b, mt);
             }
         }
+    };
+    for (int g = 0; g < nga; g++) {
+        if (g & 1) group(g, I1{});
+        else group(g, I0{});
     }
 #pragma unroll
     for (int mt = 0; mt < NMT; mt++) {

@@ -149,10 +149,11 @@ def test_q6K_gemm_extreme_blocks_exact(be):
     (2880, 264, 8, 40, 4),   # 90 blocks: 22 whole groups + a 2-block group; rows past 128 (and % 8 == 0)
     (256, 100, 4, 24, 2),    # 8 blocks; rows % 8 != 0: the plain fold; one partial row block
 ])
-def test_register_mxfp4_experts_bit_identical(be, n, rows, n_as, n_tok, n_ids):
+def test_register_mxfp4_experts_bit_identical(be, monkeypatch, n, rows, n_as, n_tok, n_ids):
     """Registered MXFP4 experts (the windows laid out in the kernel's staging
     order) give the same bits as the GGUF layout, and the sub-sums agree."""
     import ghip
+    monkeypatch.setenv("GHIP_MOE_REG_MIN_ROWS", "0")  # the registered copy at any row count
     rng = np.random.default_rng(rows)
     wf = torch.from_numpy((rng.standard_normal((n_as * rows, n)) * 0.02).astype(np.float32)).cuda()
     w = be.quantize(wf, ghip.MXFP4).view(n_as, rows, -1)

@@ -557,6 +557,12 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
                            "_c" + std::to_string(NC) + (q4k ? "_r" + std::to_string(rb) + "x" + std::to_string(ng) : std::string());
         const int ns = q4k && !persist && p.wtype == GHIP_TYPE_Q4_K && rb == 1 && p.M == 1 ? env_int("GHIP_GEMV_NS", ns_d) : 2;
         if (ns != 2) name += "s" + std::to_string(ns);
+        // Q4_0 in whole 8-row groups and block pairs, at most two columns: the
+        // variant with unconditional loads, activations first (4096 x 4096,
+        // fused: see gemv_q4_0_full_impl)
+        if (p.wtype == GHIP_TYPE_Q4_0 && p.N % 8 == 0 && p.nb % 2 == 0 && NC <= 2 &&
+            env_int("GHIP_GEMV_Q40_FULL", 1) != 0)
+            name.replace(0, std::strlen("ghip_gemv_q4_0"), "ghip_gemv_q4_0_full");
         int32_t *sub_c = sub;
         if (sub) {
             const int64_t per = (p.wtype == GHIP_TYPE_Q4_K || p.wtype == GHIP_TYPE_Q5_K || p.wtype == GHIP_TYPE_Q2_K) ? 2 * p.nb : p.nb;

@@ -580,6 +580,7 @@ __device__ __forceinline__ void gemv_q6K_impl(const uint8_t *__restrict__ W, int
 // block, d = f16(amax / 127), q = rne(x * 127 / amax), NaN or out of range ->
 // -128.  Codes of elements 0..15 in lo, 16..31 in hi; d as the f32 value of
 // its f16.
+DEV void q8_0_quant_vals(const float *v, uint4 &lo, uint4 &hi, float &d);
 DEV void q8_0_quant_block(const float *__restrict__ xb, uint4 &lo, uint4 &hi, float &d) {
     float v[32];
 #pragma unroll
@@ -590,6 +591,10 @@ DEV void q8_0_quant_block(const float *__restrict__ xb, uint4 &lo, uint4 &hi, fl
         v[4 * i + 2] = __uint_as_float(t.z);
         v[4 * i + 3] = __uint_as_float(t.w);
     }
+    q8_0_quant_vals(v, lo, hi, d);
+}
+// the quantize_row_q8_0 arithmetic on 32 values already in registers
+DEV void q8_0_quant_vals(const float *v, uint4 &lo, uint4 &hi, float &d) {
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
@@ -712,6 +717,128 @@ __device__ __forceinline__ void gemv_q4_0_impl(const uint8_t *__restrict__ W, in
 #pragma unroll
     for (int c = 0; c < NC; c++) stash_rows(red, part[c], lane, w, nw, c, NC);
     finish_rows(red, r0, nr, ncols, NC, nw, dst, ldd);
+}
+
+// Q4_0, whole row groups and pairs (rows % RB == 0, even nb): the same
+// arithmetic as gemv_q4_0_impl with every load unconditional (lanes past the
+// row's pairs re-read its last pair and contribute zero), the activation
+// loads issued before the weights.  A load under a run-time branch, or
+// activations loaded after the weights, made the quantization wait for every
+// weight byte (loads complete in order).
+template <int NC, bool SUBSUMS, bool FUSEQ>
+__device__ __forceinline__ void gemv_q4_0_full_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows,
+                                                    int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
+                                                    int ncols, float *__restrict__ dst, int64_t ldd,
+                                                    int32_t *__restrict__ sub, int wg = -1) {
+    __shared__ float red[RB * 8 * NC];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int pr = 64 * w + lane, np = nb >> 1;
+    const bool v = pr < np;
+    const int b0 = 2 * min(pr, np - 1), b1 = b0 + 1;
+    const int r0 = (wg < 0 ? (int)blockIdx.x : wg) * RB;
+
+    // activations first: f32 values (FUSEQ) or the Q8_0 blocks of columns
+    // c < ncols (columns past ncols re-read column 0 and are zeroed below)
+    float xv[FUSEQ ? NC : 1][64];
+    uint4 y0l[NC], y0h[NC], y1l[NC], y1h[NC];
+    uint32_t dh[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const int cc = c < ncols ? c : 0;
+        if constexpr (FUSEQ) {
+            const uint8_t *xr = act + cc * act_row_bytes + (int64_t)b0 * 128;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint4 t = ld16(xr + 16 * i);
+                xv[c][4 * i] = __uint_as_float(t.x);
+                xv[c][4 * i + 1] = __uint_as_float(t.y);
+                xv[c][4 * i + 2] = __uint_as_float(t.z);
+                xv[c][4 * i + 3] = __uint_as_float(t.w);
+            }
+        } else {
+            const uint8_t *A = act + cc * act_row_bytes + (int64_t)b0 * Q8_0_BYTES;
+            dh[c] = ld2(A) | ((uint32_t)ld2(A + Q8_0_BYTES) << 16);
+            y0l[c] = ld16(A + 2);
+            y0h[c] = ld16(A + 18);
+            y1l[c] = ld16(A + Q8_0_BYTES + 2);
+            y1h[c] = ld16(A + Q8_0_BYTES + 18);
+        }
+    }
+    uint4 wa[RB], wbq[RB];
+    uint32_t wc[RB];
+    const uint8_t *wb = W + (int64_t)r0 * w_row_bytes + (int64_t)(b0 >> 1) * 36;
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        const uint8_t *p = wb + rr * w_row_bytes;
+        wa[rr] = ld16(p);
+        wbq[rr] = ld16(p + 16);
+        wc[rr] = ld4(p + 32);
+    }
+    // every weight load is issued before the activations are consumed: the
+    // values pass through an empty asm that no load can move across
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        if constexpr (FUSEQ) {
+#pragma unroll
+            for (int i = 0; i < 64; i++) asm volatile("" : "+v"(xv[c][i]) : : "memory");
+        } else {
+            uint4 *ys[4] = {&y0l[c], &y0h[c], &y1l[c], &y1h[c]};
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                asm volatile("" : "+v"(ys[k]->x), "+v"(ys[k]->y), "+v"(ys[k]->z), "+v"(ys[k]->w) : : "memory");
+            asm volatile("" : "+v"(dh[c]) : : "memory");
+        }
+    }
+    int sy0[NC], sy1[NC];
+    float d0[NC], d1[NC];
+    const uint32_t one = 0x01010101u;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        if constexpr (FUSEQ) {
+            q8_0_quant_vals(&xv[c][0], y0l[c], y0h[c], d0[c]);
+            q8_0_quant_vals(&xv[c][32], y1l[c], y1h[c], d1[c]);
+        } else {
+            d0[c] = h2f(dh[c] & 0xffffu);
+            d1[c] = h2f(dh[c] >> 16);
+        }
+        if (c >= ncols) d0[c] = d1[c] = 0.0f;
+        sy0[c] = 8 * dot4(y0l[c].x, one, dot4(y0l[c].y, one, dot4(y0l[c].z, one, dot4(y0l[c].w, one,
+                 dot4(y0h[c].x, one, dot4(y0h[c].y, one, dot4(y0h[c].z, one, dot4(y0h[c].w, one, 0))))))));
+        sy1[c] = 8 * dot4(y1l[c].x, one, dot4(y1l[c].y, one, dot4(y1l[c].z, one, dot4(y1l[c].w, one,
+                 dot4(y1h[c].x, one, dot4(y1h[c].y, one, dot4(y1h[c].z, one, dot4(y1h[c].w, one, 0))))))));
+    }
+    float part[NC][RB];
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        const uint4 a = wa[rr], bq = wbq[rr];
+        const float dw0 = h2f(a.x), dw1 = h2f(bq.x >> 16);
+        const uint32_t q0[4] = {__builtin_amdgcn_alignbyte(a.y, a.x, 2), __builtin_amdgcn_alignbyte(a.z, a.y, 2),
+                                __builtin_amdgcn_alignbyte(a.w, a.z, 2), __builtin_amdgcn_alignbyte(bq.x, a.w, 2)};
+        const uint32_t q1[4] = {bq.y, bq.z, bq.w, wc[rr]};
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int s0 = dot4(q0[3] & 0x0f0f0f0f, y0l[c].w, dot4(q0[2] & 0x0f0f0f0f, y0l[c].z,
+                           dot4(q0[1] & 0x0f0f0f0f, y0l[c].y, dot4(q0[0] & 0x0f0f0f0f, y0l[c].x,
+                           dot4((q0[3] >> 4) & 0x0f0f0f0f, y0h[c].w, dot4((q0[2] >> 4) & 0x0f0f0f0f, y0h[c].z,
+                           dot4((q0[1] >> 4) & 0x0f0f0f0f, y0h[c].y, dot4((q0[0] >> 4) & 0x0f0f0f0f, y0h[c].x,
+                           -sy0[c]))))))));
+            const int s1 = dot4(q1[3] & 0x0f0f0f0f, y1l[c].w, dot4(q1[2] & 0x0f0f0f0f, y1l[c].z,
+                           dot4(q1[1] & 0x0f0f0f0f, y1l[c].y, dot4(q1[0] & 0x0f0f0f0f, y1l[c].x,
+                           dot4((q1[3] >> 4) & 0x0f0f0f0f, y1h[c].w, dot4((q1[2] >> 4) & 0x0f0f0f0f, y1h[c].z,
+                           dot4((q1[1] >> 4) & 0x0f0f0f0f, y1h[c].y, dot4((q1[0] >> 4) & 0x0f0f0f0f, y1h[c].x,
+                           -sy1[c]))))))));
+            if (SUBSUMS && c < ncols && v) {
+                int32_t *s = sub + ((int64_t)c * rows + r0 + rr) * nb;
+                s[b0] = s0;
+                s[b1] = s1;
+            }
+            // exactly 0 from lanes past the row (as in gemv_q4_0_impl)
+            part[c][rr] = v ? fmaf((float)s1, dw1 * d1[c], (float)s0 * (dw0 * d0[c])) : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NC; c++) stash_rows(red, part[c], lane, w, nw, c, NC);
+    finish_rows(red, r0, RB, ncols, NC, nw, dst, ldd);
 }
 
 // ---------------------------------------------------------------- Q5_0 / Q8_0 x Q8_0
@@ -1215,6 +1342,7 @@ GEMV_ALL(ghip_gemv_q6_K, gemv_q6K_impl)
     GEMV_PAIR_INST(name, impl, 1) GEMV_PAIR_INST(name, impl, 2) GEMV_PAIR_INST(name, impl, 4) \
         GEMV_PAIR_INST(name, impl, 8)
 GEMV_PAIR_ALL(ghip_gemv_q4_0, gemv_q4_0_impl)
+GEMV_PAIR_INST(ghip_gemv_q4_0_full, gemv_q4_0_full_impl, 1) GEMV_PAIR_INST(ghip_gemv_q4_0_full, gemv_q4_0_full_impl, 2)
 GEMV_PAIR_ALL(ghip_gemv_q5_0, gemv_q5_0_impl)
 GEMV_PAIR_ALL(ghip_gemv_q8_0, gemv_q8_0_impl)
 

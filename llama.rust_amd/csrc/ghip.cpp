@@ -357,11 +357,12 @@ bool gemv_v2(const MulMatPlan &p) {
 // deeper on large matrices: Q4_K 4096 -> 14336 9.6 -> 9.2 us, Q6_K 14336 ->
 // 4096 16.0 -> 14.8 us; smaller matrices keep 2 x 2 (4096 -> 4096: 4.5 us
 // against 5.2 with 1 x 4).
-// Q4_K at one activation row with K in one wavefront: one-row groups, teams
+// Q4_K at one or two activation rows with K in one wavefront: one-row groups, teams
 // and rows per team chosen for about 256 workgroups (one per CU), ns groups
 // loaded before the activation is quantized.  Measured (graph-timed, rotating
 // weights): 4096 -> 14336 9.0 -> 8.2 us (1 x 7, 3 slots), 4096 -> 4096
-// 4.6 -> 4.5 us, 4096 -> 1024 4.2 -> 3.6 us (1 x 2, 4 teams).
+// 4.6 -> 4.5 us, 4096 -> 1024 4.2 -> 3.6 us (1 x 2, 4 teams); at two rows
+// 4096 -> 14336 12.0 -> 10.2 us, 4096 -> 4096 6.3 -> 6.1 us.
 void gemv_q4k_one_row(int64_t rows, int &teams, int &ng, int &ns) {
     teams = rows >= 4096 ? 8 : 4;
     const int64_t per_team = (rows + 256 * teams - 1) / (256 * teams);
@@ -523,7 +524,7 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     const bool q4k = gemv_v2(p);
     int rb_d, ng_d, ns_d = 2, teams_d = p.N < 8192 && p.M <= 2 ? 4 : 8;
     gemv_groups(p.wtype, p.M, p.N, rb_d, ng_d);
-    if (q4k && p.wtype == GHIP_TYPE_Q4_K && p.M == 1 && waves_k == 1) {
+    if (q4k && p.wtype == GHIP_TYPE_Q4_K && p.M <= 2 && waves_k == 1) {
         rb_d = 1;
         gemv_q4k_one_row(p.N, teams_d, ng_d, ns_d);
     }
@@ -537,7 +538,7 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     const int rb = persist ? 1 : q4k ? env_int("GHIP_GEMV_RB", rb_d) : 8;
     const int ng = persist ? 0 : q4k ? env_int("GHIP_GEMV_NG", ng_d) : 1;
     if (q4k && !persist && !((rb == 2 && (ng == 2 || ng == 4 || ng == 8)) || (rb == 4 && (ng == 2 || ng == 4)) ||
-                 (rb == 1 && p.wtype == GHIP_TYPE_Q4_K && p.M == 1 && (ng == 2 || ng == 4 || ng == 7 || ng == 8)) ||
+                 (rb == 1 && p.wtype == GHIP_TYPE_Q4_K && p.M <= 2 && (ng == 2 || ng == 4 || ng == 7 || ng == 8)) ||
                  (p.wtype == GHIP_TYPE_Q6_K && p.M == 1 && ((rb == 2 && ng == 8) || (rb == 1 && (ng == 4 || ng == 8))))))
         return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "GHIP_GEMV_RB x GHIP_GEMV_NG must be 2x2, 2x4, 2x8, 4x2 or 4x4");
     const int rows_per_team = rb * ng;
@@ -555,7 +556,7 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
         std::string name = std::string(gemv_base(p.wtype)) + (p.wtype == GHIP_TYPE_Q6_K && q4k ? "_v2" : "") +
                            (fused ? "_f" : "") + (sub ? "_sub" : "") +
                            "_c" + std::to_string(NC) + (q4k ? "_r" + std::to_string(rb) + "x" + std::to_string(ng) : std::string());
-        const int ns = q4k && !persist && p.wtype == GHIP_TYPE_Q4_K && rb == 1 && p.M == 1 ? env_int("GHIP_GEMV_NS", ns_d) : 2;
+        const int ns = q4k && !persist && p.wtype == GHIP_TYPE_Q4_K && rb == 1 && p.M <= 2 ? env_int("GHIP_GEMV_NS", ns_d) : 2;
         if (ns != 2) name += "s" + std::to_string(ns);
         // Q4_0 in whole 8-row groups and block pairs, at most two columns: the
         // variant with unconditional loads, activations first (4096 x 4096,
@@ -1415,7 +1416,7 @@ ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipS
     int rb, ng, ns = 2, teams = std::max(1, std::min(8 / waves_k, env_int("GHIP_GEMV_TEAMS", 8)));
     gemv_groups(p0.wtype, p0.M, rows_total, rb, ng);
     if (p0.wtype == GHIP_TYPE_Q5_K) rb = ng = 2;
-    if (p0.wtype == GHIP_TYPE_Q4_K && p0.M == 1 && waves_k == 1) {
+    if (p0.wtype == GHIP_TYPE_Q4_K && p0.M <= 2 && waves_k == 1) {
         int t;
         rb = 1;
         gemv_q4k_one_row(rows_total, t, ng, ns);

@@ -387,9 +387,14 @@ void gemv_groups(int wtype, int64_t M, int64_t N, int &rb, int &ng) {
 // rows are quantized once by ghip_quantize_q8_K and copied into each
 // workgroup's LDS: quantizing them in every workgroup cost 5.6 us of 21.2 at
 // 8 rows on 4096 -> 14336 (15.6 us with the rows quantized once).
+// At 3-4 rows on matrices under 8192 rows (K in one wavefront) the VALU
+// kernel with one-row groups is faster: 4096 -> 4096 at 4 rows 10.9 -> 8.6 us.
+bool valu_q4k_small(const MulMatPlan &p) {
+    return p.wtype == GHIP_TYPE_Q4_K && p.M <= 4 && p.N < 8192 && p.nb <= 16;
+}
 bool use_skinny(const MulMatPlan &p) {
     return p.wtype == GHIP_TYPE_Q4_K && p.M >= env_int("GHIP_MMA_MIN_ROWS", 4) && p.M < 16 &&
-           env_int("GHIP_MMA", 1) != 0;
+           env_int("GHIP_MMA", 1) != 0 && !valu_q4k_small(p);
 }
 // The K split sets the fp32 summation order, so it is fixed (2 row tiles x
 // 4 K-slices) for every matrix size: a matrix alone and in a grouped launch
@@ -437,8 +442,11 @@ int64_t sk_tiles(int64_t N) { return (N + kSkRows - 1) / kSkRows; }
 // reduction).  sk_rows_ok is the row test alone (graph grouping keeps it
 // equal within a group).
 bool sk_rows_ok(int wtype, int64_t N) { return wtype == GHIP_TYPE_Q6_K || N >= env_int("GHIP_SK_MIN_ROWS", 8192); }
+// Q4_K takes split K from 5 rows: at 4 rows the matrix-core decode kernel is
+// faster (4096 -> 14336: 17.2 us split K, 15.6 us).
 bool use_sk(const MulMatPlan &p) {
     if (p.act_pre || env_int("GHIP_SK", 1) == 0 || p.M < env_int("GHIP_MMA_MIN_ROWS", 4)) return false;
+    if (p.wtype == GHIP_TYPE_Q4_K && p.M < env_int("GHIP_SK_Q4K_MIN_COLS", 5)) return false;
     return (p.wtype == GHIP_TYPE_Q4_K || p.wtype == GHIP_TYPE_Q6_K) && p.M <= 8 && sk_rows_ok(p.wtype, p.N);
 }
 size_t sk_part_bytes(const MulMatPlan &p) {
@@ -524,9 +532,10 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     const bool q4k = gemv_v2(p);
     int rb_d, ng_d, ns_d = 2, teams_d = p.N < 8192 && p.M <= 2 ? 4 : 8;
     gemv_groups(p.wtype, p.M, p.N, rb_d, ng_d);
-    if (q4k && p.wtype == GHIP_TYPE_Q4_K && p.M <= 2 && waves_k == 1) {
+    if (q4k && p.wtype == GHIP_TYPE_Q4_K && p.M <= 4 && waves_k == 1) {
         rb_d = 1;
         gemv_q4k_one_row(p.N, teams_d, ng_d, ns_d);
+        if (p.M > 2) teams_d = 8, ng_d = 2, ns_d = 2;  // 3-4 rows: two rows per team
     }
     // GHIP_GEMV_PERSIST=1: Q4_K at one row, K in one wavefront, from 8192
     // weight rows on the persistent grid (GHIP_GEMV_WGS workgroups of 8 teams,
@@ -538,7 +547,7 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     const int rb = persist ? 1 : q4k ? env_int("GHIP_GEMV_RB", rb_d) : 8;
     const int ng = persist ? 0 : q4k ? env_int("GHIP_GEMV_NG", ng_d) : 1;
     if (q4k && !persist && !((rb == 2 && (ng == 2 || ng == 4 || ng == 8)) || (rb == 4 && (ng == 2 || ng == 4)) ||
-                 (rb == 1 && p.wtype == GHIP_TYPE_Q4_K && p.M <= 2 && (ng == 2 || ng == 4 || ng == 7 || ng == 8)) ||
+                 (rb == 1 && p.wtype == GHIP_TYPE_Q4_K && p.M <= 4 && (ng == 2 || ng == 4 || ng == 7 || ng == 8)) ||
                  (p.wtype == GHIP_TYPE_Q6_K && p.M == 1 && ((rb == 2 && ng == 8) || (rb == 1 && (ng == 4 || ng == 8))))))
         return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "GHIP_GEMV_RB x GHIP_GEMV_NG must be 2x2, 2x4, 2x8, 4x2 or 4x4");
     const int rows_per_team = rb * ng;
@@ -556,7 +565,7 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
         std::string name = std::string(gemv_base(p.wtype)) + (p.wtype == GHIP_TYPE_Q6_K && q4k ? "_v2" : "") +
                            (fused ? "_f" : "") + (sub ? "_sub" : "") +
                            "_c" + std::to_string(NC) + (q4k ? "_r" + std::to_string(rb) + "x" + std::to_string(ng) : std::string());
-        const int ns = q4k && !persist && p.wtype == GHIP_TYPE_Q4_K && rb == 1 && p.M <= 2 ? env_int("GHIP_GEMV_NS", ns_d) : 2;
+        const int ns = q4k && !persist && p.wtype == GHIP_TYPE_Q4_K && rb == 1 && p.M <= 4 ? env_int("GHIP_GEMV_NS", ns_d) : 2;
         if (ns != 2) name += "s" + std::to_string(ns);
         // Q4_0 in whole 8-row groups and block pairs, at most two columns: the
         // variant with unconditional loads, activations first (4096 x 4096,
@@ -1416,10 +1425,11 @@ ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipS
     int rb, ng, ns = 2, teams = std::max(1, std::min(8 / waves_k, env_int("GHIP_GEMV_TEAMS", 8)));
     gemv_groups(p0.wtype, p0.M, rows_total, rb, ng);
     if (p0.wtype == GHIP_TYPE_Q5_K) rb = ng = 2;
-    if (p0.wtype == GHIP_TYPE_Q4_K && p0.M <= 2 && waves_k == 1) {
+    if (p0.wtype == GHIP_TYPE_Q4_K && p0.M <= 4 && waves_k == 1) {
         int t;
         rb = 1;
         gemv_q4k_one_row(rows_total, t, ng, ns);
+        if (p0.M > 2) t = 8, ng = 2, ns = 2;
         teams = std::max(1, std::min(8, env_int("GHIP_GEMV_TEAMS", t)));
         ng = env_int("GHIP_GEMV_NG", ng);
         ns = env_int("GHIP_GEMV_NS", ns);

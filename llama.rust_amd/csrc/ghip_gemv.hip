@@ -1434,6 +1434,7 @@ GEMV_PAIR_FULL_INST(ghip_gemv_q5_0_full, gemv_q5_0_full_impl, 1) GEMV_PAIR_FULL_
     }
 Q4K_INST_S(1, 1, 4, 3) Q4K_INST_S(1, 1, 7, 3) Q4K_INST_S(1, 1, 8, 3)
 Q4K_INST_S(2, 1, 4, 3) Q4K_INST_S(2, 1, 7, 3) Q4K_INST_S(2, 1, 8, 3) Q4K_INST(2, 1, 2)
+Q4K_INST(4, 1, 2)
 // register row groups (RB rows) x groups in flight (NG)
 #define Q4K_INST_RB(NC) Q4K_INST(NC, 2, 2) Q4K_INST(NC, 2, 4) Q4K_INST(NC, 4, 2) Q4K_INST(NC, 2, 8) Q4K_INST(NC, 4, 4)
 Q4K_INST_RB(1) Q4K_INST_RB(2) Q4K_INST_RB(4) Q4K_INST_RB(8)
@@ -1507,7 +1508,7 @@ GEMV_MULTI_RN(q4_K, 1, 1, 2, gemv_q4K_impl, false)
     }
 GEMV_MULTI_RNS(q4_K, 1, 1, 4, 3, gemv_q4K_impl) GEMV_MULTI_RNS(q4_K, 1, 1, 7, 3, gemv_q4K_impl)
 GEMV_MULTI_RNS(q4_K, 1, 1, 8, 3, gemv_q4K_impl)
-GEMV_MULTI_RN(q4_K, 2, 1, 2, gemv_q4K_impl, false) GEMV_MULTI_RNS(q4_K, 2, 1, 4, 3, gemv_q4K_impl)
+GEMV_MULTI_RN(q4_K, 2, 1, 2, gemv_q4K_impl, false) GEMV_MULTI_RN(q4_K, 4, 1, 2, gemv_q4K_impl, false) GEMV_MULTI_RNS(q4_K, 2, 1, 4, 3, gemv_q4K_impl)
 GEMV_MULTI_RNS(q4_K, 2, 1, 7, 3, gemv_q4K_impl) GEMV_MULTI_RNS(q4_K, 2, 1, 8, 3, gemv_q4K_impl)
 GEMV_MULTI_RN(q6_K_v2, 1, 1, 8, gemv_q6K_v2_impl)
 

@@ -535,7 +535,10 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     if (q4k && p.wtype == GHIP_TYPE_Q4_K && p.M <= 4 && waves_k == 1) {
         rb_d = 1;
         gemv_q4k_one_row(p.N, teams_d, ng_d, ns_d);
-        if (p.M > 2) teams_d = 8, ng_d = 2, ns_d = 2;  // 3-4 rows: two rows per team
+        // 3-4 rows: two one-row groups per team under 8192 rows; from 8192 rows
+        // (3 rows there, 4 take the matrix-core kernel) groups of two rows
+        // (4096 -> 14336 at 4 rows: 21.8 us one-row, 16.9 us two-row groups)
+        if (p.M > 2) teams_d = 8, ng_d = 2, ns_d = 2, rb_d = p.N < 8192 ? 1 : 2;
     }
     // GHIP_GEMV_PERSIST=1: Q4_K at one row, K in one wavefront, from 8192
     // weight rows on the persistent grid (GHIP_GEMV_WGS workgroups of 8 teams,
@@ -1429,7 +1432,7 @@ ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipS
         int t;
         rb = 1;
         gemv_q4k_one_row(rows_total, t, ng, ns);
-        if (p0.M > 2) t = 8, ng = 2, ns = 2;
+        if (p0.M > 2) t = 8, ng = 2, ns = 2, rb = rows_total < 8192 ? 1 : 2;  // as in the single-matrix rule
         teams = std::max(1, std::min(8, env_int("GHIP_GEMV_TEAMS", t)));
         ng = env_int("GHIP_GEMV_NG", ng);
         ns = env_int("GHIP_GEMV_NS", ns);

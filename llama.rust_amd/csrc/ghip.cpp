@@ -540,6 +540,12 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
         // (4096 -> 14336 at 4 rows: 21.8 us one-row, 16.9 us two-row groups)
         if (p.M > 2) teams_d = 8, ng_d = 2, ns_d = 2, rb_d = p.N < 8192 ? 1 : 2;
     }
+    // Q5_K (fused, one row): the same rule (4096 -> 14336 12.6 -> 9.7 us,
+    // 4096 -> 4096 5.9 -> 5.0 us)
+    if (q4k && p.wtype == GHIP_TYPE_Q5_K && p.M == 1 && fused && waves_k == 1) {
+        rb_d = 1;
+        gemv_q4k_one_row(p.N, teams_d, ng_d, ns_d);
+    }
     // GHIP_GEMV_PERSIST=1: Q4_K at one row, K in one wavefront, from 8192
     // weight rows on the persistent grid (GHIP_GEMV_WGS workgroups of 8 teams,
     // each team an equal run of consecutive rows; "_r1x0").  Off by default:
@@ -551,6 +557,7 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     const int ng = persist ? 0 : q4k ? env_int("GHIP_GEMV_NG", ng_d) : 1;
     if (q4k && !persist && !((rb == 2 && (ng == 2 || ng == 4 || ng == 8)) || (rb == 4 && (ng == 2 || ng == 4)) ||
                  (rb == 1 && p.wtype == GHIP_TYPE_Q4_K && p.M <= 4 && (ng == 2 || ng == 4 || ng == 7 || ng == 8)) ||
+                 (rb == 1 && p.wtype == GHIP_TYPE_Q5_K && p.M == 1 && fused && (ng == 2 || ng == 4 || ng == 7 || ng == 8)) ||
                  (p.wtype == GHIP_TYPE_Q6_K && p.M == 1 && ((rb == 2 && ng == 8) || (rb == 1 && (ng == 4 || ng == 8))))))
         return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "GHIP_GEMV_RB x GHIP_GEMV_NG must be 2x2, 2x4, 2x8, 4x2 or 4x4");
     const int rows_per_team = rb * ng;
@@ -568,8 +575,11 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
         std::string name = std::string(gemv_base(p.wtype)) + (p.wtype == GHIP_TYPE_Q6_K && q4k ? "_v2" : "") +
                            (fused ? "_f" : "") + (sub ? "_sub" : "") +
                            "_c" + std::to_string(NC) + (q4k ? "_r" + std::to_string(rb) + "x" + std::to_string(ng) : std::string());
-        const int ns = q4k && !persist && p.wtype == GHIP_TYPE_Q4_K && rb == 1 && p.M <= 4 ? env_int("GHIP_GEMV_NS", ns_d) : 2;
-        if (ns != 2) name += "s" + std::to_string(ns);
+        const bool one_row = q4k && !persist && rb == 1 &&
+                             ((p.wtype == GHIP_TYPE_Q4_K && p.M <= 4) || (p.wtype == GHIP_TYPE_Q5_K && p.M == 1 && fused));
+        const int ns = one_row ? env_int("GHIP_GEMV_NS", ns_d) : 2;
+        // Q4_K names carry the slot count when it is not 2, Q5_K's one-row kernels always
+        if (ns != 2 || (one_row && p.wtype == GHIP_TYPE_Q5_K)) name += "s" + std::to_string(ns);
         // Q4_0 in whole 8-row groups and block pairs, at most two columns: the
         // variant with unconditional loads, activations first (4096 x 4096,
         // fused: see gemv_q4_0_full_impl)

@@ -1443,6 +1443,15 @@ Q4K_INST(1, 1, 4) Q4K_INST(1, 1, 8) Q4K_INST(1, 1, 2) Q4K_INST(1, 1, 0) Q4K_INST
 #define Q5K_INST_RB(NC) QK45_INST(q5_K, true, NC, 2, 2) QK45_INST(q5_K, true, NC, 2, 4) \
     QK45_INST(q5_K, true, NC, 4, 2) QK45_INST(q5_K, true, NC, 2, 8) QK45_INST(q5_K, true, NC, 4, 4)
 Q5K_INST_RB(1) Q5K_INST_RB(2) Q5K_INST_RB(4) Q5K_INST_RB(8)
+// Q5_K one-row groups with NS register slots (the Q4_K batch-1 shapes)
+#define Q5K_INST_S(NC, NG, NS)                                                                                     \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q5_K_f_c##NC##_r1x##NG##s##NS(Q4K_ARGS) {         \
+        gemv_q4K_impl<NC, false, true, 1, NG, true, NS>(Q4K_PASS);                                             \
+    }                                                                                                             \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_q5_K_f_sub_c##NC##_r1x##NG##s##NS(Q4K_ARGS) {     \
+        gemv_q4K_impl<NC, true, true, 1, NG, true, NS>(Q4K_PASS);                                              \
+    }
+Q5K_INST_S(1, 2, 2) Q5K_INST_S(1, 4, 3) Q5K_INST_S(1, 7, 3) Q5K_INST_S(1, 8, 3)
 
 // Q6_K (v2): same shapes and naming, "_f" = fused Q8_K quantization
 #define Q6K_INST(NC, RB, NG)                                                                                      \

@@ -221,15 +221,16 @@ def more_types_bench(be, torch, np):
 
 
 def measured_traffic():
-    """HBM bytes per launch of the dominant kernel, from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (None when absent)."""
+    """HBM bytes per launch of the dominant kernel: the calibrated
+    FETCH_SIZE + WRITE_SIZE that the committed rocprofv3 summary states on its
+    `traffic_bytes_per_launch:` line (None when the summary is absent)."""
     path = os.path.join(ROOT, "profiles", "gemv_q4K_4096x14336_b1.md")
     try:
         with open(path) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":")[1].strip())
-    except OSError:
+                    return int(line.split(":")[1].strip().replace(",", ""))
+    except (OSError, ValueError):
         pass
     return None
 
@@ -238,7 +239,7 @@ def _profile_ops(be, torch, np, what):
     """One launch closure per profiled kernel family, on the bench's shapes."""
     import ghip
     g = torch.Generator(device="cuda").manual_seed(0)
-    if what in ("gemv", "copy"):
+    if what in ("gemv", "gemv_graph", "copy"):
         k, nr = 4096, 14336
         rng = np.random.default_rng(0)
         wf = torch.from_numpy(rng.standard_normal((nr, k), dtype=np.float32) * np.float32(0.02)).cuda()
@@ -249,6 +250,9 @@ def _profile_ops(be, torch, np, what):
         out = torch.empty((1, nr), dtype=torch.float32, device="cuda")
         if what == "gemv":
             return lambda i: be.mul_mat(ws[i % 16], ghip.Q4_K, k, x, out=out)
+        if what == "gemv_graph":
+            # the roofline's timing setup: 64 launches in one HIP graph, replayed
+            return _graph_replay(torch, lambda i: be.mul_mat(ws[i % 16], ghip.Q4_K, k, x, out=out), 64)
         # one 33,030,144-byte device-to-device copy per launch
         return lambda i: ws[(i + 1) % 16].copy_(ws[i % 16])
     if what in ("gemm", "gemm_q6k", "decode_b8"):
@@ -298,7 +302,26 @@ def _profile_ops(be, torch, np, what):
     raise ValueError(what)
 
 
-PROFILE_WORKLOADS = ["gemv", "copy", "gemm", "gemm_q6k", "decode_b8", "layer_b1", "layer_b8", "moe", "moe_reg",
+def _graph_replay(torch, launch, n):
+    """Capture n launches in a HIP graph (after 3 eager warm-up launches) and
+    return a closure that replays it; launch i of the profile loop replays
+    the whole graph when i % n == 0, so L launches are L // n replays."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(3):
+            launch(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            launch(i)
+    torch.cuda.synchronize()
+    return lambda i: g.replay() if i % n == 0 else None
+
+
+PROFILE_WORKLOADS = ["gemv", "gemv_graph", "copy", "gemm", "gemm_q6k", "decode_b8", "layer_b1", "layer_b8", "moe", "moe_reg",
                      "fa_decode", "fa_prefill"]
 
 
@@ -306,6 +329,8 @@ def profile_loop(what, n):
     """Plain launch loops for rocprofv3 runs (no JSON): one kernel family on
     the bench's shape, or the copy kernel used to calibrate FETCH_SIZE /
     WRITE_SIZE.  gemv: Q4_K 4096->14336 at batch 1 over 16 weight copies;
+    gemv_graph: the same launches captured 64 to a HIP graph and replayed
+    (the roofline's steady state, no first-touch launches);
     copy: 33,030,144-byte device copies; gemm: Q4_K 512x4096->14336;
     gemm_q6k: Q6_K 512x14336->4096; decode_b8: Q4_K 4096->14336 at 8 rows over
     16 copies; layer_b1 / layer_b8: the decode layer's 7 MUL_MATs in one

@@ -1254,6 +1254,10 @@ bool joins_group(const ghip_node *nodes, int i, int j) {
     // the split-K and whole-K decode kernels sum differently: one kernel per group
     if (c.src[0]->type == GHIP_TYPE_Q4_K && sk_rows_ok(GHIP_TYPE_Q4_K, c.src[0]->ne[1]) != sk_rows_ok(GHIP_TYPE_Q4_K, h.src[0]->ne[1]))
         return false;
+    // so do the matrix-core and VALU decode kernels, which a single op chooses
+    // by its own row count at 4 activation rows (valu_q4k_small)
+    if (c.src[0]->type == GHIP_TYPE_Q4_K && c.src[1]->ne[1] <= 4 && (c.src[0]->ne[1] < 8192) != (h.src[0]->ne[1] < 8192))
+        return false;
     for (int k = i; k < j; k++) {
         const ghip_node &o = nodes[k];
         if (overlaps(o.dst, c.src[0]) || overlaps(o.dst, c.src[1]) || overlaps(c.dst, o.src[0]) ||
@@ -1825,7 +1829,13 @@ ghip_status ghip_context_upload(ghip_context *ctx, void *dst, const void *src, s
     for (size_t off = 0, k = 0; off < n; off += kStage, k++) {
         const int b = (int)(k & 1);
         const size_t len = std::min(kStage, n - off);
-        if (used[b] && hipEventSynchronize(ctx->stage_ev[b]) != hipSuccess) break;
+        // (a staging buffer whose last copy did not finish must not be
+        // refilled, and the tensor would be left partly uploaded)
+        if (used[b] && hipEventSynchronize(ctx->stage_ev[b]) != hipSuccess) {
+            (void)hipGetLastError();
+            (void)hipStreamSynchronize(s);
+            return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "gguf_upload: staging wait failed");
+        }
         memcpy(ctx->stage[b], (const uint8_t *)src + off, len);
         if (hipMemcpyAsync((uint8_t *)dst + off, ctx->stage[b], len, hipMemcpyHostToDevice, s) != hipSuccess ||
             hipEventRecord(ctx->stage_ev[b], s) != hipSuccess) {

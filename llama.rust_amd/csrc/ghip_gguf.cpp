@@ -85,11 +85,7 @@ struct Tensor {
     uint64_t nb[4];
     uint64_t offset;
     int part;
-    uint64_t size() const {
-        int64_t blck = 1, bytes = 0;
-        ggml_type_size(type, blck, bytes);
-        return (uint64_t)bytes * (uint64_t)(ne[0] * ne[1] * ne[2] * ne[3] / blck);
-    }
+    uint64_t size() const { return nb[3] * (uint64_t)ne[3]; }
 };
 
 struct Part {
@@ -152,6 +148,10 @@ struct Cursor {
             const uint32_t et = get<uint32_t>(what);
             if (et > 12 || et == T_ARR) fail("invalid gguf array element type %u", et);
             const uint64_t n = get<uint64_t>(what);
+            // every element takes at least one byte of the file: a count the
+            // rest of the file cannot hold is a truncated file, refused before
+            // any element is built (each Value costs ~100 bytes of host memory)
+            if (n > len - pos) fail("truncated file while reading %s", what);
             v.arr_type = et;
             v.arr.reserve((size_t)std::min<uint64_t>(n, 1u << 20));
             for (uint64_t k = 0; k < n; k++) v.arr.push_back(value(et, what));
@@ -244,10 +244,23 @@ ghip_gguf *open_single(const std::string &path) {
             int64_t blck, bytes;
             if (!ggml_type_size(t.type, blck, bytes) || t.ne[0] % blck != 0)
                 fail("tensor '%s' has invalid shape/type", t.name.c_str());
+            // strides and the element count in checked arithmetic: a shape
+            // whose byte size does not fit 64 bits is refused (gguf.rs:561-568
+            // forms the same products), so size() and every later bounds
+            // check see the true extent
+            int64_t nel = 1;
+            uint64_t nb1, nb2, nb3, total;
+            bool ovf = false;
+            for (int j = 0; j < 4; j++) ovf |= __builtin_mul_overflow(nel, t.ne[j], &nel);
+            ovf |= __builtin_mul_overflow((uint64_t)bytes, (uint64_t)(t.ne[0] / blck), &nb1);
+            ovf |= __builtin_mul_overflow(nb1, (uint64_t)t.ne[1], &nb2);
+            ovf |= __builtin_mul_overflow(nb2, (uint64_t)t.ne[2], &nb3);
+            ovf |= __builtin_mul_overflow(nb3, (uint64_t)t.ne[3], &total);
+            if (ovf) fail("tensor '%s' has invalid shape/type", t.name.c_str());
             t.nb[0] = (uint64_t)bytes;
-            t.nb[1] = t.nb[0] * (uint64_t)(t.ne[0] / blck);
-            t.nb[2] = t.nb[1] * (uint64_t)t.ne[1];
-            t.nb[3] = t.nb[2] * (uint64_t)t.ne[2];
+            t.nb[1] = nb1;
+            t.nb[2] = nb2;
+            t.nb[3] = nb3;
             t.offset = c.get<uint64_t>("tensor offset");
             t.part = 0;
             g->tensors.push_back(std::move(t));

@@ -137,6 +137,11 @@ ERROR_CASES = [
     (_hdr(1, 0) + _tinfo("w", [32], 5), "tensor 'w' has invalid shape/type"),     # type 5 does not exist
     (_hdr(1, 0) + _tinfo("w", [48], 12), "tensor 'w' has invalid shape/type"),    # 48 % 256 != 0
     (_hdr(1, 0) + _tinfo("w", [32], 0)[:-3], "truncated file while reading tensor offset"),
+    # element count 2^64 and byte size 2^66: refused, not wrapped to a small size
+    (_hdr(1, 0) + _tinfo("w", [2 ** 32, 2 ** 32], 0), "tensor 'w' has invalid shape/type"),
+    (_hdr(1, 0) + _tinfo("w", [2 ** 31, 2 ** 31, 4], 0), "tensor 'w' has invalid shape/type"),
+    # an array count the rest of the file cannot hold is refused before any element is built
+    (_hdr(0, 1) + G._s("a") + struct.pack("<IIQ", G.ARR, G.U8, 2 ** 40), "truncated file while reading kv value"),
 ]
 
 

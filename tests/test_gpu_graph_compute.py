@@ -36,7 +36,8 @@ def weights(be, ty, n, k, seed):
     return be.quantize(torch.randn((n, k), device="cuda", generator=g) * 0.02, ty)
 
 
-@pytest.mark.parametrize("ty,m", [(12, 1), (12, 2), (12, 4), (12, 5), (12, 8), (14, 1), (14, 2), (2, 1), (2, 2), (2, 4)])
+@pytest.mark.parametrize("ty,m", [(12, 1), (12, 2), (12, 3), (12, 4), (12, 5), (12, 8), (14, 1), (14, 2), (2, 1), (2, 2),
+                                  (2, 4)])
 def test_decode_layer_groups_bit_identical(be, ty, m):
     """q/k/v (4096 -> 4096, 1024, 1024) and gate/up (4096 -> 14336) as two
     groups, o as a single node, at m activation rows (Q4_K, Q6_K, Q4_0; Q5_K,
@@ -57,6 +58,27 @@ def test_decode_layer_groups_bit_identical(be, ty, m):
         ref = be.mul_mat(ws[nm], ty, k, xo if nm == "o" else x)
         torch.cuda.synchronize()
         assert torch.equal(outs[nm], ref), nm
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
+def test_mixed_row_counts_bit_identical(be, m):
+    """Siblings on both sides of the 8192-row line (4096 and 14336 rows, in
+    both orders): a single op picks its decode kernel by its own row count,
+    so a group must never run a member on a kernel its single op would not
+    use; every output equals ghip_mul_mat's."""
+    import ghip
+    k = 4096
+    for order in ((4096, 14336, 1024), (14336, 4096, 1024)):
+        ws = [weights(be, 12, n, k, 20 + i) for i, n in enumerate(order)]
+        g = torch.Generator(device="cuda").manual_seed(m)
+        x = torch.randn((m, k), device="cuda", generator=g)
+        outs = [torch.full((m, n), float("nan"), device="cuda") for n in order]
+        be.graph_compute([ghip.mul_mat_node(w, 12, k, x, o) for w, o in zip(ws, outs)])
+        torch.cuda.synchronize()
+        for w, o, n in zip(ws, outs, order):
+            ref = be.mul_mat(w, 12, k, x)
+            torch.cuda.synchronize()
+            assert torch.equal(o, ref), (order, n)
 
 
 @pytest.mark.parametrize("ty,k,ns,m", [(12, 1024, (96, 40, 8), 1), (13, 768, (33, 64), 1), (14, 512, (17, 31, 64, 5), 1),

@@ -120,7 +120,7 @@ def test_empty(be):
     ("cfg1", O.Q4_0, 4096, 4096),
     ("q4_0 wide (separate Q8_0 quantization)", O.Q4_0, 4096, 14336),
 ])
-@pytest.mark.parametrize("cols", [1, 2, 4, 8])
+@pytest.mark.parametrize("cols", [1, 2, 3, 4, 5, 8])
 def test_llama3_decode_shapes(be, name, ty, n, rows, cols):
     if ty == O.Q4_0 and cols > 1:
         pytest.skip("the Q4_0 configurations are batch 1")

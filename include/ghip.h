@@ -114,12 +114,17 @@ int ghip_supports_op(int op, const ghip_tensor *dst, const ghip_tensor *const *s
 
 /* dst = src0 x src1 (GGML_OP_MUL_MAT, forward_mul_mat compute.rs:1420-1839).
  * src0: Q4_0 | Q4_1 | Q5_0 | Q5_1 | Q8_0 | Q2_K | Q3_K | Q4_K | Q5_K | Q6_K
- *       weight [ne00=K, ne01=N], rows contiguous;
- * src1: F32 [K, ne11] (any row stride nb11, nb10 == 4), or already the
- *       vec_dot type of src0 (Q8_0 for Q4_0/Q5_0/Q8_0, Q8_1 for Q4_1/Q5_1,
- *       Q8_K for the K-quants; rows of blocks),
+ *       weight [ne00=K, ne01=N, ne02, ne03], rows contiguous;
+ * src1: F32 [K, ne11, ne12, ne13] (any strides nb11..nb13, nb10 == 4), or
+ *       already the vec_dot type of src0 (Q8_0 for Q4_0/Q5_0/Q8_0, Q8_1 for
+ *       Q4_1/Q5_1, Q8_K for the K-quants; rows of blocks),
  *       which skips the quantization (backend.rs:2057-2066 semantics);
- * dst:  F32 [N, ne11] (nb0 == 4).
+ * dst:  F32 [N, ne11, ne12, ne13] (nb0 == 4).
+ * Planes: ne12 % ne02 == 0 and ne13 % ne03 == 0; dst plane (i12, i13) is
+ * src0 plane (i12 / r2, i13 / r3) times src1 plane (i12, i13), r2 = ne12 /
+ * ne02, r3 = ne13 / ne03 (compute.rs:1440-1450), each plane a 2-D MUL_MAT
+ * (sub-sums and quantized activations of the hooks below follow one another
+ * plane by plane, i13 outermost).
  * Activations are quantized on the device exactly as the reference's route for
  * this (type, N, ne11) does (Q8_0 for Q4_0/Q5_0/Q8_0; Q8_1 for Q4_1/Q5_1,
  * quantize_row_q8_1 quants.rs:375; Q8_K for the K-quants, with the
@@ -194,18 +199,22 @@ ghip_status ghip_mul_mat_id_subsums(ghip_context *ctx, const ghip_tensor *as, co
 
 /* dst = FLASH_ATTN_EXT(q, k, v, mask, sinks) (forward_flash_attn_ext
  * compute.rs:4563-4625; FlashAttn flash_attn.rs:273-386):
- *   q:     F32 [DK, T, H]      (nb0 == 4, any nb1/nb2)
- *   k:     F16 or F32 [DK, S, H_kv], v: F16 or F32 [DV, S, H_kv] (rows
- *          contiguous), DK and DV in 1..256, H % H_kv == 0 (flash_attn.rs:303-313)
- *   mask:  F16 [>= S, >= T] or NULL (rows contiguous)
+ *   q:     F32 [DK, T, H, n_seq]      (nb0 == 4, any nb1..nb3)
+ *   k:     F16 or F32 [DK, S, H_kv, n_seq], v: F16 or F32 [DV, S, H_kv, n_seq]
+ *          (rows contiguous), DK and DV in 1..256, H % H_kv == 0
+ *          (flash_attn.rs:298-313)
+ *   mask:  F16 [>= S, >= T, m2, m3] or NULL (rows contiguous); head h of
+ *          sequence i3 reads plane (h % m2, i3 % m3), H % m2 == 0 and
+ *          n_seq % m3 == 0 (ggml.c:5517-5518, flash_attn.rs:30-37)
  *   sinks: F32 [H] or NULL
- *   dst:   F32 [DV, H, T] contiguous
+ *   dst:   F32 [DV, H, T, n_seq], each sequence contiguous
  *   dst->op_params: [0] scale, [1] max_bias, [2] logit_softcap (f32 bits).
  * F16 K/V with DK == DV in {64, 128} and H / H_kv <= 8 run the matrix-core
  * kernels (the KV range split across workgroups and merged in slice order);
  * every other shape runs a row walk in key order (the reference's attn_row,
- * with its f16 accumulator for an F16 V on that route).  The result matches
- * the reference within 2e-3 max-abs. */
+ * with its f16 accumulator for an F16 V on that route); so does a
+ * single-query split-KV shape with per-head mask planes.  Sequences run one
+ * after another.  The result matches the reference within 2e-3 max-abs. */
 ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const ghip_tensor *k, const ghip_tensor *v,
                                 const ghip_tensor *mask, const ghip_tensor *sinks, const ghip_tensor *dst,
                                 void *stream);

@@ -266,15 +266,19 @@ bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b,
     if (a->ne[0] <= 0) { st = ctx->fail(st, "mul_mat: ne00 must be positive"); return false; }
     if ((int64_t)a->nb[0] != ti.bytes) { st = ctx->fail(st, "mul_mat: permuted src0 (nb0 != type size)"); return false; }
     if ((int64_t)b->nb[0] != type_info(b->type).bytes) { st = ctx->fail(st, "mul_mat: permuted src1"); return false; }
-    if (a->ne[2] != 1 || a->ne[3] != 1 || b->ne[2] != 1 || b->ne[3] != 1) {
-        st = ctx->fail(st, "mul_mat: only 2-D operands are supported");
+    // batches: dst plane (i12, i13) = src0 plane (i12 / r2, i13 / r3) x src1
+    // plane (i12, i13), r2 = ne12 / ne02, r3 = ne13 / ne03 (compute.rs:1440-1450);
+    // mul_mat_impl runs the planes one by one
+    if (a->ne[2] < 1 || a->ne[3] < 1 || b->ne[2] < 0 || b->ne[3] < 0 || b->ne[2] % a->ne[2] ||
+        b->ne[3] % a->ne[3]) {
+        st = ctx->fail(st, "mul_mat: src1 planes (ne12, ne13) must be multiples of src0's (ne02, ne03)");
         return false;
     }
     if (b->type == GHIP_TYPE_F32 && b->nb[1] % 4) { st = ctx->fail(st, "mul_mat: src1 row stride not a multiple of 4"); return false; }
     if (d) {
         if (d->type != GHIP_TYPE_F32 || d->nb[0] != 4 || d->ne[0] != a->ne[1] || d->ne[1] != b->ne[1] ||
-            d->nb[1] % 4) {
-            st = ctx->fail(st, "mul_mat: dst must be F32 [ne01, ne11] with nb0 == 4");
+            d->ne[2] != b->ne[2] || d->ne[3] != b->ne[3] || d->nb[1] % 4) {
+            st = ctx->fail(st, "mul_mat: dst must be F32 [ne01, ne11, ne12, ne13] with nb0 == 4");
             return false;
         }
     }
@@ -855,8 +859,9 @@ size_t mul_mat_ws_bytes(const MulMatPlan &p, bool has_dst, bool act_out, size_t 
     return (act_out ? 0 : act_bytes) + lay_bytes + (has_dst || act_out ? 0 : (size_t)(p.M * p.N * 4));
 }
 
-ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b, const ghip_tensor *d,
-                         int32_t *sub, void *act_out, void *stream, void *fixed_ws = nullptr, size_t fixed_bytes = 0) {
+// one 2-D MUL_MAT (a single plane of src0, src1 and dst)
+ghip_status mul_mat_plane(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b, const ghip_tensor *d,
+                          int32_t *sub, void *act_out, void *stream, void *fixed_ws, size_t fixed_bytes) {
     std::lock_guard<std::mutex> lock(ctx->mu);
     // a fixed scratch serves this call only
     struct CallScratch {
@@ -905,6 +910,47 @@ ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_ten
     return run_gemv(ctx, p, a->data, (const uint8_t *)act, p.act_row_bytes, false, dst, ldd, sub, s);
 }
 
+// GGML_OP_MUL_MAT over batched operands (forward_mul_mat, compute.rs:1420-1450):
+// plane (i12, i13) of dst is src0 plane (i12 / r2, i13 / r3) times src1 plane
+// (i12, i13), each a 2-D MUL_MAT of its own (routes, quantization and the
+// 4-row repack grouping are per plane, as in the reference's repack path,
+// compute.rs:5346-5362).  Sub-sums and quantized activations of the planes
+// follow one another in i13-major order.
+ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b, const ghip_tensor *d,
+                         int32_t *sub, void *act_out, void *stream, void *fixed_ws = nullptr, size_t fixed_bytes = 0) {
+    if (!a || !b || (a->ne[2] == 1 && a->ne[3] == 1 && b->ne[2] == 1 && b->ne[3] == 1))
+        return mul_mat_plane(ctx, a, b, d, sub, act_out, stream, fixed_ws, fixed_bytes);
+    MulMatPlan p;
+    ghip_status st;
+    {
+        std::lock_guard<std::mutex> lock(ctx->mu);
+        if (!plan_mul_mat(ctx, a, b, d, p, st)) return st;
+    }
+    const int64_t r2 = b->ne[2] / a->ne[2], r3 = b->ne[3] / a->ne[3];
+    // sub-sums per block: {iacc, imin} for the types with a min term, one int otherwise
+    const bool two = p.wtype == GHIP_TYPE_Q4_K || p.wtype == GHIP_TYPE_Q5_K || p.wtype == GHIP_TYPE_Q2_K;
+    const size_t sub_plane = (size_t)p.M * (size_t)p.N * (size_t)p.nb * (two ? 2 : 1);
+    const size_t act_plane = (size_t)p.M * (size_t)p.act_row_bytes;
+    int64_t plane = 0;
+    for (int64_t i13 = 0; i13 < b->ne[3]; i13++)
+        for (int64_t i12 = 0; i12 < b->ne[2]; i12++, plane++) {
+            ghip_tensor a2 = *a, b2 = *b, d2;
+            a2.data = (uint8_t *)a->data + (i12 / r2) * a->nb[2] + (i13 / r3) * a->nb[3];
+            b2.data = (uint8_t *)b->data + i12 * b->nb[2] + i13 * b->nb[3];
+            a2.ne[2] = a2.ne[3] = b2.ne[2] = b2.ne[3] = 1;
+            if (d) {
+                d2 = *d;
+                d2.data = (uint8_t *)d->data + i12 * d->nb[2] + i13 * d->nb[3];
+                d2.ne[2] = d2.ne[3] = 1;
+            }
+            st = mul_mat_plane(ctx, &a2, &b2, d ? &d2 : nullptr, sub ? sub + plane * sub_plane : nullptr,
+                               act_out ? (uint8_t *)act_out + plane * act_plane : nullptr, stream, fixed_ws,
+                               fixed_bytes);
+            if (st != GHIP_STATUS_SUCCESS) return st;
+        }
+    return GHIP_STATUS_SUCCESS;
+}
+
 // ------------------------------------------------------------ FLASH_ATTN_EXT
 
 // Mirror of FaParams in ghip_fa.hip (passed by value as the only kernel argument).
@@ -915,6 +961,8 @@ struct FaParams {
     int64_t k_nb1, k_nb2, v_nb1, v_nb2;
     const uint16_t *mask;
     int64_t mask_nb1;
+    int64_t mask_nb2;
+    int mask_ne2;
     float *dst;
     float *part;
     const float *sinks;  // [H] or null
@@ -943,7 +991,9 @@ bool plan_fa(ghip_context *ctx, const ghip_tensor *q, const ghip_tensor *k, cons
     if (!kv_ok(k) || !kv_ok(v)) return bad("k and v must be F16 or F32 rows (flash_attn.rs:305-313)");
     if (k->ne[0] != q->ne[0]) return bad("DK of q and k differ");
     if (k->ne[0] < 1 || k->ne[0] > 256 || v->ne[0] < 1 || v->ne[0] > 256) return bad("head sizes must be 1..256");
-    if (q->ne[3] != 1 || k->ne[3] != 1 || v->ne[3] != 1) return bad("4-D batches are not supported");
+    // sequences (dim 3): q, k and v agree (flash_attn.rs:298); ghip_flash_attn_ext
+    // runs them one by one
+    if (q->ne[3] < 1 || k->ne[3] != q->ne[3] || v->ne[3] != q->ne[3]) return bad("ne3 of q, k and v differ");
     if (k->ne[1] != v->ne[1] || k->ne[2] != v->ne[2]) return bad("k/v shapes differ");
     if (q->ne[2] % k->ne[2]) return bad("H % H_kv != 0");
     if (k->nb[1] % k->nb[0] || k->nb[2] % k->nb[0] || v->nb[1] % v->nb[0] || v->nb[2] % v->nb[0] || q->nb[1] % 4 ||
@@ -952,16 +1002,18 @@ bool plan_fa(ghip_context *ctx, const ghip_tensor *q, const ghip_tensor *k, cons
     if (mask) {
         if (mask->type != GHIP_TYPE_F16 || mask->nb[0] != 2) return bad("mask must be F16 rows (ggml.c:5515)");
         if (mask->ne[0] < k->ne[1] || mask->ne[1] < q->ne[1]) return bad("mask smaller than [S, T]");
-        // one mask plane shared by every head and batch: the kernels read
-        // mask row t at t * nb1 (a per-head plane, flash_attn.rs:30-37, is not
-        // supported)
-        if (mask->ne[2] != 1 || mask->ne[3] != 1) return bad("mask must be 2-D (one plane for all heads)");
+        // planes broadcast to heads by h % ne2 and to sequences by i3 % ne3
+        // (ggml.c:5517-5518, flash_attn.rs:30-37)
+        if (mask->ne[2] < 1 || mask->ne[3] < 1 || q->ne[2] % mask->ne[2] || q->ne[3] % mask->ne[3])
+            return bad("mask planes must divide the heads (ne2) and sequences (ne3)");
+        if (mask->nb[1] % 2 || mask->nb[2] % 2) return bad("mask strides must be element multiples");
         if ((uint64_t)q->ne[1] * mask->nb[1] >= (1ull << 31)) return bad("mask spans >= 2 GiB");
     }
     if (sinks && (sinks->type != GHIP_TYPE_F32 || sinks->ne[0] < q->ne[2])) return bad("sinks must be F32 [H]");
     if (d->type != GHIP_TYPE_F32 || d->ne[0] != v->ne[0] || d->ne[1] != q->ne[2] || d->ne[2] != q->ne[1] ||
-        d->nb[0] != 4 || d->nb[1] != (uint64_t)(4 * d->ne[0]) || d->nb[2] != (uint64_t)(4 * d->ne[0] * d->ne[1]))
-        return bad("dst must be contiguous F32 [DV, H, T]");
+        d->ne[3] != q->ne[3] || d->nb[0] != 4 || d->nb[1] != (uint64_t)(4 * d->ne[0]) ||
+        d->nb[2] != (uint64_t)(4 * d->ne[0] * d->ne[1]) || d->nb[3] % 4)
+        return bad("dst must be F32 [DV, H, T, ne3], each sequence contiguous");
     if (q->ne[1] > INT32_MAX || k->ne[1] > INT32_MAX) return bad("dimension too large");
     // the kernels address one KV head with 32-bit byte offsets
     if ((uint64_t)k->ne[1] * std::max(k->nb[1], v->nb[1]) >= (1ull << 31)) return bad("a KV head spans >= 2 GiB");
@@ -1502,10 +1554,9 @@ ghip_status ghip_mul_mat_id_subsums(ghip_context *ctx, const ghip_tensor *as, co
     return mul_mat_id_impl(ctx, as, b, ids, nullptr, subsums, stream);
 }
 
-ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const ghip_tensor *k, const ghip_tensor *v,
-                                const ghip_tensor *mask, const ghip_tensor *sinks, const ghip_tensor *dst,
-                                void *stream) {
-    if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
+// one sequence (q, k, v, mask plane and dst of one i3)
+static ghip_status fa_sequence(ghip_context *ctx, const ghip_tensor *q, const ghip_tensor *k, const ghip_tensor *v,
+                        const ghip_tensor *mask, const ghip_tensor *sinks, const ghip_tensor *dst, void *stream) {
     std::lock_guard<std::mutex> lock(ctx->mu);
     ghip_status st;
     if (!plan_fa(ctx, q, k, v, mask, sinks, dst, st)) return st;
@@ -1535,6 +1586,8 @@ ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const g
     p.v_nb2 = (int64_t)v->nb[2] / 2;
     p.mask = mask ? (const uint16_t *)mask->data : nullptr;
     p.mask_nb1 = mask ? (int64_t)mask->nb[1] / 2 : 0;
+    p.mask_nb2 = mask ? (int64_t)mask->nb[2] / 2 : 0;
+    p.mask_ne2 = mask ? (int)mask->ne[2] : 1;
     p.dst = (float *)dst->data;
     p.part = (float *)ws;
     p.T = T;
@@ -1559,7 +1612,11 @@ ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const g
     // other than 64 / 128, H / H_kv > 8) run the general row walk: with the
     // f16 accumulator where the reference's route is the row walk over an F16
     // V, fp32 otherwise
-    const bool tuned = !p.k_f32 && !p.v_f32 && p.DK == p.DV && (D == 64 || D == 128) && G <= 8;
+    // (the split-KV decode kernel reads one mask value per key for all G
+    // heads of a KV head, so per-head mask planes take the row walk too)
+    const bool per_head_mask = mask && mask->ne[2] > 1;
+    const bool tuned = !p.k_f32 && !p.v_f32 && p.DK == p.DV && (D == 64 || D == 128) && G <= 8 &&
+                       !(per_head_mask && T == 1 && S >= 512);
     if (!tuned) {
         const bool row_walk = !(T == 1 && S >= 512) && T < 64;
         return ctx->launch(row_walk && !p.v_f32 ? "ghip_fa_rowgen_f16acc" : "ghip_fa_rowgen",
@@ -1595,6 +1652,37 @@ ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const g
                            (const float *)ws, sk, (float *)dst->data, T * H, H, nsplit, D);
     return ctx->launch("ghip_fa_merge", dim3((unsigned)(T * H)), dim3(256), 0, s, (const float *)ws, sk,
                        (float *)dst->data, T, H, nsplit, D);
+}
+
+// FLASH_ATTN_EXT over sequences (dim 3, flash_attn.rs:298): sequence i3 reads
+// q, k and v plane i3 and mask plane i3 % mask_ne3 and writes dst plane i3
+ghip_status ghip_flash_attn_ext(ghip_context *ctx, const ghip_tensor *q, const ghip_tensor *k, const ghip_tensor *v,
+                                const ghip_tensor *mask, const ghip_tensor *sinks, const ghip_tensor *dst,
+                                void *stream) {
+    if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
+    if (!q || !k || !v || !dst || q->ne[3] == 1)
+        return fa_sequence(ctx, q, k, v, mask, sinks, dst, stream);
+    {
+        std::lock_guard<std::mutex> lock(ctx->mu);
+        ghip_status st;
+        if (!plan_fa(ctx, q, k, v, mask, sinks, dst, st)) return st;
+    }
+    for (int64_t i3 = 0; i3 < q->ne[3]; i3++) {
+        ghip_tensor q2 = *q, k2 = *k, v2 = *v, d2 = *dst, m2;
+        q2.data = (uint8_t *)q->data + i3 * q->nb[3];
+        k2.data = (uint8_t *)k->data + i3 * k->nb[3];
+        v2.data = (uint8_t *)v->data + i3 * v->nb[3];
+        d2.data = (uint8_t *)dst->data + i3 * dst->nb[3];
+        q2.ne[3] = k2.ne[3] = v2.ne[3] = d2.ne[3] = 1;
+        if (mask) {
+            m2 = *mask;
+            m2.data = (uint8_t *)mask->data + (i3 % mask->ne[3]) * mask->nb[3];
+            m2.ne[3] = 1;
+        }
+        const ghip_status st = fa_sequence(ctx, &q2, &k2, &v2, mask ? &m2 : nullptr, sinks, &d2, stream);
+        if (st != GHIP_STATUS_SUCCESS) return st;
+    }
+    return GHIP_STATUS_SUCCESS;
 }
 
 

@@ -41,6 +41,8 @@ struct FaParams {
     int64_t k_nb1, k_nb2, v_nb1, v_nb2;  // halfs
     const uint16_t *mask;
     int64_t mask_nb1;  // halfs
+    int64_t mask_nb2;  // halfs: head h reads mask plane h % mask_ne2 (flash_attn.rs:30-37)
+    int mask_ne2;
     float *dst;        // [T][H][DV]
     float *part;       // [(t*H + h)*nsplit + z][2 + DV]
     const float *sinks;  // [H] or null
@@ -112,7 +114,10 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _F
     const int ke = min(p.S, kb + p.chunk);
     const uint16_t *kbase = p.k + (int64_t)hk * p.k_nb2;
     const uint16_t *vbase = p.v + (int64_t)hk * p.v_nb2;
-    const uint16_t *mrow = p.mask ? p.mask + (int64_t)(tvalid ? t : 0) * p.mask_nb1 : nullptr;
+    // this wavefront's head reads mask plane h % mask_ne2 (wave-uniform)
+    const int mplane_i = __builtin_amdgcn_readfirstlane(h % p.mask_ne2);
+    const uint16_t *mplane = p.mask ? p.mask + (int64_t)mplane_i * p.mask_nb2 : nullptr;
+    const uint16_t *mrow = mplane ? mplane + (int64_t)(tvalid ? t : 0) * p.mask_nb1 : nullptr;
 
     // Next tile in registers while this one is computed: K chunks, V blocks of
     // 4 keys x 8 dims (transposed on the way into LDS), and this lane's mask
@@ -134,7 +139,7 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _F
     // slice end); this lane's row is part of its offset
     const uint32_t mrowb = (uint32_t)p.mask_nb1 * 2u;
     const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.mask ? p.mask : p.k), 0, p.mask ? (int)((uint32_t)(p.T - 1) * mrowb + (uint32_t)ke * 2u) : 0, 0x00020000);
+        (void *)(mplane ? mplane : p.k), 0, mplane ? (int)((uint32_t)(p.T - 1) * mrowb + (uint32_t)ke * 2u) : 0, 0x00020000);
     // thread parts: K chunk c = tid + i*nthr -> key c / (D/8), dims 8 * (c % (D/8));
     // V block b = tid + i*nthr -> keys 4 * (b & 15) + r, dims 8 * (b >> 4)
     const uint32_t kth = (uint32_t)(tid / (D / 8)) * krow + (uint32_t)(tid % (D / 8)) * 16u;
@@ -744,7 +749,7 @@ __device__ __forceinline__ void fa_rowseq_impl(const FaParams &p) {
         float s = -__builtin_inff();
         bool live = false;
         if (key < p.S) {
-            const float mv = p.mask ? slope * h2f(p.mask[(int64_t)t * p.mask_nb1 + key]) : 0.0f;
+            const float mv = p.mask ? slope * h2f(p.mask[(int64_t)(h % p.mask_ne2) * p.mask_nb2 + (int64_t)t * p.mask_nb1 + key]) : 0.0f;
             if (mv != -__builtin_inff()) {
                 live = true;
                 const uint8_t *kr = (const uint8_t *)(kbase + (int64_t)key * p.k_nb1);
@@ -840,7 +845,7 @@ __device__ __forceinline__ void fa_rowgen_impl(const FaParams &p) {
         float s = -__builtin_inff();
         bool live = false;
         if (key < p.S) {
-            const float mv = p.mask ? slope * h2f(p.mask[(int64_t)t * p.mask_nb1 + key]) : 0.0f;
+            const float mv = p.mask ? slope * h2f(p.mask[(int64_t)(h % p.mask_ne2) * p.mask_nb2 + (int64_t)t * p.mask_nb1 + key]) : 0.0f;
             if (mv != -__builtin_inff()) {
                 live = true;
                 const uint16_t *kr = kbase + (int64_t)key * p.k_nb1;

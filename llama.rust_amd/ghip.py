@@ -271,12 +271,13 @@ class Backend:
 
     # ---- FLASH_ATTN_EXT
     def flash_attn_ext(self, q, k, v, mask=None, sinks=None, scale=1.0, max_bias=0.0, softcap=0.0, out=None):
-        """q [H, T, DK] f32, k [H_kv, S, DK] / v [H_kv, S, DV] f16 or f32, mask [T, S] f16,
-        sinks [H] f32 -> [T, H, DV] f32."""
+        """q [(n_seq,) H, T, DK] f32, k [(n_seq,) H_kv, S, DK] / v [(n_seq,) H_kv, S, DV] f16 or
+        f32, mask [(m3, m2,) T, S] f16 (planes broadcast to heads by h % m2 and to
+        sequences by i3 % m3), sinks [H] f32 -> [(n_seq,) T, H, DV] f32."""
         import struct
-        H, T, D = q.shape
+        H, T = q.shape[-3], q.shape[-2]
         if out is None:
-            out = torch.empty((T, H, v.shape[2]), dtype=torch.float32, device=q.device)
+            out = torch.empty(tuple(q.shape[:-3]) + (T, H, v.shape[-1]), dtype=torch.float32, device=q.device)
         kvt = lambda t: F32 if t.dtype == torch.float32 else F16
         tq, tk, tv = describe(q, F32), describe(k, kvt(k)), describe(v, kvt(v))
         tm, ts, td = describe(mask, F16), describe(sinks, F32), describe(out, F32)

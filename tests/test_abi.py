@@ -72,8 +72,10 @@ def test_supports_op_rejects_empty_rows():
 
 
 def test_supports_op_fa_mask_planes():
-    """FLASH_ATTN_EXT takes one 2-D mask for every head; a mask with per-head
-    planes (ne2 > 1) is rejected rather than read as plane 0."""
+    """FLASH_ATTN_EXT takes mask planes broadcast to heads (h % ne2) and to
+    sequences (i3 % ne3) when they divide the heads and sequences
+    (ggml.c:5517-5518), and sequences (ne3) that q, k, v and dst agree on;
+    anything else is refused."""
     import ghip
     D, T, H, S, Hkv = 128, 4, 8, 256, 2
     q = _t(ghip.F32, (D, T, H, 1), (4, 4 * D, 4 * D * T, 4 * D * T * H))
@@ -84,9 +86,20 @@ def test_supports_op_fa_mask_planes():
     P = ctypes.POINTER(ghip.Tensor)
     srcs = (P * 5)(ctypes.pointer(q), ctypes.pointer(k), ctypes.pointer(v), ctypes.pointer(m), None)
     L = ghip.lib()
-    assert L.ghip_supports_op(ghip.OP_FLASH_ATTN_EXT, ctypes.byref(d), srcs, 5) == 1
-    m.ne[2], m.nb[3] = H, 2 * S * T * H
-    assert L.ghip_supports_op(ghip.OP_FLASH_ATTN_EXT, ctypes.byref(d), srcs, 5) == 0
+    ok = lambda: L.ghip_supports_op(ghip.OP_FLASH_ATTN_EXT, ctypes.byref(d), srcs, 5)
+    assert ok() == 1
+    m.ne[2], m.nb[3] = H, 2 * S * T * H      # one plane per head
+    assert ok() == 1
+    m.ne[2] = 3                              # 8 heads % 3 planes != 0
+    assert ok() == 0
+    m.ne[2] = 2
+    for t in (q, k, v, d):                   # two sequences
+        t.ne[3] = 2
+    assert ok() == 1
+    m.ne[3] = 2
+    assert ok() == 1
+    k.ne[3] = 1                              # k with one sequence, q with two
+    assert ok() == 0
 
 
 def test_workspace_size_query_without_gpu():

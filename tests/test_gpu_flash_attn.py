@@ -124,3 +124,44 @@ def test_general_shapes(be, H, Hkv, DK, DV, T, S, kv):
     than 64 / 128, H / H_kv > 8) take the general row walk, still within 2e-3
     of the oracle's route for the shape."""
     run_general(be, H, Hkv, DK, DV, T, S, kv, sinks=(T % 2 == 1))
+
+
+@pytest.mark.parametrize("T,S,m2,m3", [
+    (1, 600, 2, 1),    # split-KV shape, per-head mask planes (row walk, fp32)
+    (1, 600, 1, 2),    # split-KV decode kernel, per-sequence planes
+    (5, 300, 8, 2),    # one-chunk walk (f16 accumulator)
+    (70, 200, 4, 1),   # tiled route on the matrix cores, per-head planes
+    (70, 200, 1, 1),
+])
+def test_mask_planes_and_sequences(be, T, S, m2, m3):
+    """The rest of the operand contract (flash_attn.rs:30-37, :298): two
+    sequences (ne3 = 2) with their own q, k and v planes, and mask planes
+    broadcast to heads by h % ne2 and to sequences by i3 % ne3.  Each
+    (sequence, head) is checked against the oracle's route for its shape on
+    exactly the mask plane it must read."""
+    H, Hkv, D, n_seq = 8, 2, 128, 2
+    G = H // Hkv
+    rng = np.random.default_rng(T * 1000 + m2 * 10 + m3)
+    q = rng.standard_normal((n_seq, H, T, D)).astype(np.float32)
+    k = rng.standard_normal((n_seq, Hkv, S, D)).astype(np.float16)
+    v = rng.standard_normal((n_seq, Hkv, S, D)).astype(np.float16)
+    m = np.zeros((m3, m2, T, S), dtype=np.float16)
+    for i3 in range(m3):
+        for i2 in range(m2):  # a different causal window per plane
+            off = int(rng.integers(0, S // 3))
+            for t in range(T):
+                m[i3, i2, t, S - T + t + 1 - off:] = -np.inf
+            m[i3, i2] += (rng.standard_normal((T, S)) * 0.5).astype(np.float16)
+    sk = rng.standard_normal(H).astype(np.float32)
+    scale = 1.0 / np.sqrt(D)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    got = be.flash_attn_ext(t(q), t(k), t(v), t(m), t(sk), scale).cpu().numpy()
+    assert got.shape == (n_seq, T, H, D)
+    worst = 0.0
+    for i3 in range(n_seq):
+        for h in range(H):
+            want, path = O.flash_attn_ext(q[i3, h:h + 1], k[i3, h // G:h // G + 1], v[i3, h // G:h // G + 1],
+                                          m[i3 % m3, h % m2], sk[h:h + 1], scale, 0.0, 0.0, n_chunks=8)
+            worst = max(worst, float(np.max(np.abs(got[i3, :, h:h + 1] - want))))
+    print(f"fa planes T={T} S={S} m2={m2} m3={m3} path={path} max-abs {worst:.2e}", flush=True)
+    assert worst <= TOL

@@ -359,3 +359,54 @@ def test_gemv_persistent_grid(be, monkeypatch, rows, wgs):
     monkeypatch.setenv("GHIP_GEMV_PERSIST", "1")
     monkeypatch.setenv("GHIP_GEMV_WGS", wgs)
     run_case(be, O.Q4_K, 4096, rows, 1, seed=rows)
+
+
+@pytest.mark.parametrize("ty,ne02,ne03,ne12,ne13,m,perm", [
+    (O.Q4_K, 1, 1, 3, 1, 5, False),    # one weight plane broadcast to 3 activation planes (r2 = 3)
+    (O.Q4_K, 2, 1, 4, 2, 4, False),    # r2 = 2, r3 = 2
+    (O.Q8_0, 2, 2, 2, 2, 3, True),     # one-to-one planes, src1 planes not contiguous
+    (O.Q6_K, 1, 2, 2, 4, 1, True),
+    (O.Q4_0, 3, 1, 3, 1, 40, False),   # 40 rows: the prefill GEMM per plane
+])
+def test_batched_broadcast(be, ty, ne02, ne03, ne12, ne13, m, perm):
+    """Batched MUL_MAT (forward_mul_mat, compute.rs:1440-1450): dst plane
+    (i12, i13) = src0 plane (i12 / r2, i13 / r3) x src1 plane (i12, i13).
+    Every plane against the oracle's 2-D MUL_MAT of the planes it reads, to
+    the matmul bar."""
+    import ctypes as C
+    import ghip
+    k, n = 512, 96
+    rng = np.random.default_rng(ne12 * 10 + ne13)
+    wf = (rng.standard_normal((ne03, ne02, n, k)) * 0.02).astype(np.float32)
+    wq = np.stack([np.stack([O.quantize(ty, wf[i3, i2]).reshape(n, -1) for i2 in range(ne02)]) for i3 in range(ne03)])
+    x = rng.standard_normal((ne13, ne12, m, k)).astype(np.float32)
+    wd = torch.from_numpy(wq).cuda()
+    if perm:  # planes laid out [ne12][ne13] in memory, viewed as [ne13][ne12]
+        xd = torch.from_numpy(np.ascontiguousarray(x.transpose(1, 0, 2, 3))).cuda().permute(1, 0, 2, 3)
+    else:
+        xd = torch.from_numpy(x).cuda()
+    out = torch.full((ne13, ne12, m, n), float("nan"), device="cuda")
+    a, b, d = ghip.describe(wd, ty, k), ghip.describe(xd, ghip.F32), ghip.describe(out, ghip.F32)
+    assert list(d.ne) == [n, m, ne12, ne13] and list(b.ne) == [k, m, ne12, ne13]
+    assert ghip.lib().ghip_supports_op(ghip.OP_MUL_MAT, C.byref(d), (C.POINTER(ghip.Tensor) * 2)(C.pointer(a), C.pointer(b)), 2) == 1
+    be._check(ghip.lib().ghip_mul_mat(be._ctx, C.byref(a), C.byref(b), C.byref(d), ghip._stream()), "ghip_mul_mat")
+    got = out.cpu().numpy()
+    r2, r3 = ne12 // ne02, ne13 // ne03
+    for i3 in range(ne13):
+        for i2 in range(ne12):
+            want, _, _ = O.mul_mat(ty, wq[i3 // r3, i2 // r2], k, n, x[i3, i2], m)
+            assert rel_err(got[i3, i2], want.reshape(m, n)) <= TOL, (i3, i2)
+
+
+def test_batched_shape_errors(be):
+    """ne12 not a multiple of ne02, and a dst whose planes differ from src1's"""
+    import ctypes as C
+    import ghip
+    k, n, m = 256, 32, 2
+    wd = torch.zeros((2, n, ghip.row_size(ghip.Q8_0, k)), dtype=torch.uint8, device="cuda")
+    for ne12, dplanes, msg in ((3, 3, "multiples of src0"), (2, 1, "dst must be F32")):
+        xd = torch.zeros((ne12, m, k), device="cuda")
+        out = torch.zeros((dplanes, m, n), device="cuda")
+        a, b, d = ghip.describe(wd, ghip.Q8_0, k), ghip.describe(xd, ghip.F32), ghip.describe(out, ghip.F32)
+        with pytest.raises(ghip.GhipError, match=msg):
+            be._check(ghip.lib().ghip_mul_mat(be._ctx, C.byref(a), C.byref(b), C.byref(d), ghip._stream()), "ghip_mul_mat")

@@ -797,7 +797,93 @@ static inline int32_t isum_q3_K(const blk_q3_K *x, const blk_q8_K *y) {
     return is;
 }
 
+/* ---- IQ4_NL, IQ4_XS, NVFP4 (blocks.rs:55-62, :234-249) ---- */
+typedef struct { uint16_t d; uint8_t qs[16]; } blk_iq4_nl;                               /* 18 B  */
+typedef struct { uint16_t d, scales_h; uint8_t scales_l[4]; uint8_t qs[128]; } blk_iq4_xs; /* 136 B */
+typedef struct { uint8_t d[4]; uint8_t qs[32]; } blk_nvfp4;                                /* 36 B  */
+_Static_assert(sizeof(blk_iq4_nl) == 18, "iq4_nl");
+_Static_assert(sizeof(blk_iq4_xs) == 136, "iq4_xs");
+_Static_assert(sizeof(blk_nvfp4) == 36, "nvfp4");
+/* KVALUES_IQ4NL (quants_k.rs:647) */
+static const int8_t kvalues_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/* ue4m3_to_fp32 (quants.rs:699-712): 0 for 0x00 / 0x7F, subnormals man * 2^-9,
+ * else (1 + man/8) * 2^(exp-7); then halved.  Every step is exact. */
+float oracle_ue4m3_to_fp32(uint8_t x) {
+    if (x == 0 || x == 0x7F) return 0.0f;
+    const int ex = (x >> 3) & 0xF, man = x & 7;
+    const float raw = ex == 0 ? ldexpf((float)man, -9) : ldexpf(1.0f + (float)man / 8.0f, ex - 7);
+    return raw * 0.5f;
+}
+/* element e (0..31) of an IQ4_NL / IQ4_XS 32-group: low nibbles of qs[0..15]
+ * are elements 0..15, high nibbles 16..31 (dequantize_row_iq4_nl, quants_k.rs:2379) */
+static inline int iq4_val(const uint8_t *qs16, int e) {
+    return kvalues_iq4nl[e < 16 ? (qs16[e] & 0x0F) : (qs16[e - 16] >> 4)];
+}
+/* the 6-bit scale of 32-group ib, minus 32 (quants_k.rs:2401-2403) */
+static inline int iq4xs_ls(const blk_iq4_xs *x, int ib) {
+    return (int)(((x->scales_l[ib / 2] >> (4 * (ib % 2))) & 0xF) | (((x->scales_h >> (2 * ib)) & 3) << 4)) - 32;
+}
+/* element e (0..63) of an NVFP4 block: sub-block s = e / 16, within it the low
+ * nibbles of qs[8s .. 8s+7] are elements 0..7 and the high nibbles 8..15
+ * (dequantize_row_nvfp4, quants.rs:749-767) */
+static inline int nvfp4_val(const blk_nvfp4 *x, int e) {
+    const int s = e / 16, j = e % 16;
+    const uint8_t b = x->qs[8 * s + j % 8];
+    return kvalues_mxfp4[j < 8 ? (b & 0x0F) : (b >> 4)];
+}
+/* exact sums: IQ4_NL per 32-block, NVFP4 per 16-sub-block (element e of the
+ * 64-block meets code e % 32 of Q8_0 block e / 32), IQ4_XS per super-block
+ * sum_ib (ls_ib - 32) * sum kvalue * q8 */
+static inline int32_t isum_iq4_nl(const blk_iq4_nl *x, const blk_q8_0 *y) {
+    int32_t s = 0;
+    for (int e = 0; e < 32; e++) s += iq4_val(x->qs, e) * y->qs[e];
+    return s;
+}
+static inline int32_t isum_nvfp4_sub(const blk_nvfp4 *x, const blk_q8_0 *y2, int s) {
+    int32_t r = 0;
+    for (int e = 16 * s; e < 16 * s + 16; e++) r += nvfp4_val(x, e) * y2[e / 32].qs[e % 32];
+    return r;
+}
+static inline int32_t isum_iq4_xs(const blk_iq4_xs *x, const blk_q8_K *y) {
+    int32_t is = 0;
+    for (int ib = 0; ib < 8; ib++) {
+        int32_t s = 0;
+        for (int e = 0; e < 32; e++) s += iq4_val(x->qs + 16 * ib, e) * y->qs[32 * ib + e];
+        is += iq4xs_ls(x, ib) * s;
+    }
+    return is;
+}
+
 void oracle_dequantize_row(int type, const void *vx, float *y, int64_t k) {
+    if (type == OR_IQ4_NL) { /* quants_k.rs:2379-2390 */
+        const blk_iq4_nl *x = (const blk_iq4_nl *)vx;
+        for (int64_t i = 0; i < k / 32; i++) {
+            const float d = H2F(x[i].d);
+            for (int e = 0; e < 32; e++) y[i * 32 + e] = d * (float)iq4_val(x[i].qs, e);
+        }
+        return;
+    }
+    if (type == OR_IQ4_XS) { /* quants_k.rs:2393-2412 */
+        const blk_iq4_xs *x = (const blk_iq4_xs *)vx;
+        for (int64_t i = 0; i < k / QK_K; i++) {
+            const float d = H2F(x[i].d);
+            for (int ib = 0; ib < 8; ib++) {
+                const float dl = d * (float)iq4xs_ls(&x[i], ib);
+                for (int e = 0; e < 32; e++) y[i * QK_K + 32 * ib + e] = dl * (float)iq4_val(x[i].qs + 16 * ib, e);
+            }
+        }
+        return;
+    }
+    if (type == OR_NVFP4) { /* quants.rs:749-767 */
+        const blk_nvfp4 *x = (const blk_nvfp4 *)vx;
+        for (int64_t i = 0; i < k / 64; i++)
+            for (int s = 0; s < 4; s++) {
+                const float d = oracle_ue4m3_to_fp32(x[i].d[s]);
+                for (int j = 0; j < 16; j++) y[i * 64 + 16 * s + j] = (float)nvfp4_val(&x[i], 16 * s + j) * d;
+            }
+        return;
+    }
     if (type == OR_Q2_K) { /* quants.rs:431-465 */
         const blk_q2_K *x = (const blk_q2_K *)vx;
         for (int64_t i = 0; i < k / QK_K; i++) {
@@ -1264,6 +1350,93 @@ float oracle_vec_dot_q5_K_q8_K(int n, const void *vx, const void *vy) {
 
 /* ------------------------------------------------------- routed MUL_MAT */
 
+/* vec_dot.rs:1597-1650 vec_dot_iq4_nl_q8_0: block pairs into two 8-lane
+ * accumulators (lane l = elements 4l..4l+3), fma(y.d * x.d, lane sum, acc),
+ * added lane-wise before one hsum8; an odd last block adds d * (sumi1 + sumi2) */
+float oracle_vec_dot_iq4_nl_q8_0(int n, const void *vx, const void *vy) {
+    const blk_iq4_nl *x = (const blk_iq4_nl *)vx;
+    const blk_q8_0 *y = (const blk_q8_0 *)vy;
+    const int nb = n / 32;
+    float acc1[8] = {0}, acc2[8] = {0};
+    int ib = 0;
+    for (; ib + 1 < nb; ib += 2) {
+        const float d0 = H2F(y[ib].d) * H2F(x[ib].d), d1 = H2F(y[ib + 1].d) * H2F(x[ib + 1].d);
+        for (int l = 0; l < 8; l++) {
+            int32_t s0 = 0, s1 = 0;
+            for (int t = 0; t < 4; t++) {
+                s0 += iq4_val(x[ib].qs, 4 * l + t) * y[ib].qs[4 * l + t];
+                s1 += iq4_val(x[ib + 1].qs, 4 * l + t) * y[ib + 1].qs[4 * l + t];
+            }
+            acc1[l] = fmaf(d0, (float)s0, acc1[l]);
+            acc2[l] = fmaf(d1, (float)s1, acc2[l]);
+        }
+    }
+    float a[8];
+    for (int l = 0; l < 8; l++) a[l] = acc1[l] + acc2[l];
+    float sumf = hsum8(a);
+    for (; ib < nb; ib++) {
+        const float d = H2F(y[ib].d) * H2F(x[ib].d);
+        int32_t s1 = 0, s2 = 0;
+        for (int j = 0; j < 16; j++) {
+            s1 += y[ib].qs[j] * kvalues_iq4nl[x[ib].qs[j] & 0xF];
+            s2 += y[ib].qs[j + 16] * kvalues_iq4nl[x[ib].qs[j] >> 4];
+        }
+        sumf += d * (float)(s1 + s2);
+    }
+    return sumf;
+}
+
+/* vec_dot.rs:1655-1700 vec_dot_iq4_xs_q8_K: per super-block d = x.d * y.d,
+ * sumi[l] += (ls - 32) * (lane l's 4-element sum) over the 8 groups,
+ * acc[l] = fma(d, sumi[l], acc[l]); hsum8 */
+float oracle_vec_dot_iq4_xs_q8_K(int n, const void *vx, const void *vy) {
+    const blk_iq4_xs *x = (const blk_iq4_xs *)vx;
+    const blk_q8_K *y = (const blk_q8_K *)vy;
+    float acc[8] = {0};
+    for (int i = 0; i < n / QK_K; i++) {
+        const float d = H2F(x[i].d) * y[i].d;
+        int32_t sumi[8] = {0};
+        for (int ib = 0; ib < 8; ib++) {
+            const int ls = iq4xs_ls(&x[i], ib);
+            for (int l = 0; l < 8; l++) {
+                int32_t s = 0;
+                for (int t = 0; t < 4; t++) s += iq4_val(x[i].qs + 16 * ib, 4 * l + t) * y[i].qs[32 * ib + 4 * l + t];
+                sumi[l] += ls * s;
+            }
+        }
+        for (int l = 0; l < 8; l++) acc[l] = fmaf(d, (float)sumi[l], acc[l]);
+    }
+    return hsum8(acc);
+}
+
+/* vec_dot.rs:1154-1210 vec_dot_nvfp4_q8_0: per 64-block the sub-block scales
+ * s_k = ue4m3(d_k) * y.d of the Q8_0 block holding them; lane l of half h
+ * sums elements 4l..4l+3 of that half (lanes 0-3 sub-block 2h, 4-7 sub-block
+ * 2h+1); acc[l] = fma(s, p1[l], acc[l]) for half 0, then half 1; hsum8 */
+float oracle_vec_dot_nvfp4_q8_0(int n, const void *vx, const void *vy) {
+    const blk_nvfp4 *x = (const blk_nvfp4 *)vx;
+    const blk_q8_0 *y = (const blk_q8_0 *)vy;
+    float acc[8] = {0};
+    for (int ib = 0; ib < n / 64; ib++) {
+        const float dy0 = H2F(y[2 * ib].d), dy1 = H2F(y[2 * ib + 1].d);
+        const float sc[4] = {oracle_ue4m3_to_fp32(x[ib].d[0]) * dy0, oracle_ue4m3_to_fp32(x[ib].d[1]) * dy0,
+                             oracle_ue4m3_to_fp32(x[ib].d[2]) * dy1, oracle_ue4m3_to_fp32(x[ib].d[3]) * dy1};
+        int32_t p[2][8];
+        for (int h = 0; h < 2; h++)
+            for (int l = 0; l < 8; l++) {
+                int32_t s = 0;
+                for (int t = 0; t < 4; t++) {
+                    const int e = 4 * l + t;
+                    s += nvfp4_val(&x[ib], 32 * h + e) * y[2 * ib + h].qs[e];
+                }
+                p[h][l] = s;
+            }
+        for (int l = 0; l < 8; l++) acc[l] = fmaf(sc[l < 4 ? 0 : 1], (float)p[0][l], acc[l]);
+        for (int l = 0; l < 8; l++) acc[l] = fmaf(sc[l < 4 ? 2 : 3], (float)p[1][l], acc[l]);
+    }
+    return hsum8(acc);
+}
+
 static int omp_threads(int nthreads) {
 #ifdef _OPENMP
     return nthreads > 0 ? nthreads : omp_get_max_threads();
@@ -1275,15 +1448,21 @@ static int omp_threads(int nthreads) {
 
 static int route_of(int type, int64_t rows, int64_t cols) {
     if ((type == OR_Q4_0 || type == OR_Q4_K) && rows % 8 == 0) return ORACLE_ROUTE_REPACK;
-    if ((type == OR_Q4_K || type == OR_Q5_K || type == OR_Q6_K) && cols >= 8) return ORACLE_ROUTE_TILED;
+    /* tiled.rs:203-242 formats, from 8 columns (tiled.rs:1300) */
+    if ((type == OR_Q4_K || type == OR_Q5_K || type == OR_Q6_K || type == OR_Q2_K || type == OR_Q3_K ||
+         type == OR_IQ4_XS) && cols >= 8)
+        return ORACLE_ROUTE_TILED;
     if (type == OR_Q4_0 && cols >= 2) return -1; /* tinyBLAS: out of scope */
     return ORACLE_ROUTE_VECDOT;
 }
 
+/* vec_dot_type Q8_0 (vec_dot.rs:1727) */
+static int q8_0_dot(int type) {
+    return type == OR_Q4_0 || type == OR_Q5_0 || type == OR_Q8_0 || type == OR_IQ4_NL || type == OR_NVFP4;
+}
 static size_t act_row_size(int type, int64_t n) {
     if (type == OR_Q4_1 || type == OR_Q5_1) return (size_t)(n / 32) * sizeof(blk_q8_1);
-    return (type == OR_Q4_0 || type == OR_Q5_0 || type == OR_Q8_0) ? (size_t)(n / 32) * sizeof(blk_q8_0)
-                                                                   : (size_t)(n / QK_K) * sizeof(blk_q8_K);
+    return q8_0_dot(type) ? (size_t)(n / 32) * sizeof(blk_q8_0) : (size_t)(n / QK_K) * sizeof(blk_q8_K);
 }
 
 /* compute.rs:1504-1549 (wdata pass) and compute.rs:5350-5398 (repack wdata) */
@@ -1294,7 +1473,7 @@ int oracle_mul_mat_act(int type, int64_t n, int64_t rows, const float *x, int64_
     const int64_t nr4 = cols - cols % 4;
     for (int64_t c = 0; c < cols; c++) {
         uint8_t *dst = (uint8_t *)act + (size_t)c * rs;
-        if (type == OR_Q4_0 || type == OR_Q5_0 || type == OR_Q8_0)
+        if (q8_0_dot(type))
             oracle_quantize_row_q8_0(x + c * n, dst, n);
         else if (type == OR_Q4_1 || type == OR_Q5_1)  /* vec_dot_type Q8_1 */
             oracle_quantize_row_q8_1(x + c * n, dst, n);
@@ -1312,7 +1491,8 @@ int oracle_mul_mat(int type, const void *w, int64_t n, int64_t rows, const float
     if (route_out) *route_out = route;
     if (route < 0) return -1;
     if (type != OR_Q4_0 && type != OR_Q4_K && type != OR_Q6_K && type != OR_Q5_0 && type != OR_Q8_0 &&
-        type != OR_Q5_K && type != OR_Q4_1 && type != OR_Q5_1 && type != OR_Q2_K && type != OR_Q3_K)
+        type != OR_Q5_K && type != OR_Q4_1 && type != OR_Q5_1 && type != OR_Q2_K && type != OR_Q3_K &&
+        type != OR_IQ4_NL && type != OR_IQ4_XS && type != OR_NVFP4)
         return -2;
     const size_t rs = act_row_size(type, n);
     uint8_t *act = (uint8_t *)malloc(rs * (size_t)cols);
@@ -1394,8 +1574,8 @@ int oracle_mul_mat(int type, const void *w, int64_t n, int64_t rows, const float
             }
         }
     } else if (type == OR_Q2_K || type == OR_Q3_K) {
-        /* the row vec_dot (the reference takes its tiled route from 8 columns,
-         * tiled.rs:363-411: the same integer sums, another fp32 order) */
+        /* the row vec_dot below 8 columns, the tiled kernel's fold from 8
+         * (tiled.rs:363-411: the same integer sums, another fp32 order) */
         const int64_t nb = n / QK_K;
         const size_t wbs = type == OR_Q2_K ? sizeof(blk_q2_K) : sizeof(blk_q3_K);
 #pragma omp parallel for num_threads(nth) schedule(static)
@@ -1414,8 +1594,28 @@ int oracle_mul_mat(int type, const void *w, int64_t n, int64_t rows, const float
                             subsums[((size_t)c * rows + r) * nb + b] = isum_q3_K((const blk_q3_K *)wr + b, &a[b]);
                         }
                     }
-                out[c * rows + r] = type == OR_Q2_K ? oracle_vec_dot_q2_K_q8_K((int)n, wr, a)
-                                                    : oracle_vec_dot_q3_K_q8_K((int)n, wr, a);
+                if (route == ORACLE_ROUTE_TILED) {
+                    /* tiled.rs:822-836 epilogue per super-block (Q2_K: HAS_MIN) */
+                    float acc = 0.0f;
+                    for (int64_t b = 0; b < nb; b++) {
+                        float res;
+                        if (type == OR_Q2_K) {
+                            const blk_q2_K *xb = (const blk_q2_K *)wr + b;
+                            int32_t is, sm;
+                            isum_q2_K(xb, &a[b], &is, &sm);
+                            res = H2F(xb->d) * (float)is;
+                            res = fmaf(-H2F(xb->dmin), (float)sm, res);
+                        } else {
+                            const blk_q3_K *xb = (const blk_q3_K *)wr + b;
+                            res = H2F(xb->d) * (float)isum_q3_K(xb, &a[b]);
+                        }
+                        acc = fmaf(res, a[b].d, acc);
+                    }
+                    out[c * rows + r] = acc;
+                } else {
+                    out[c * rows + r] = type == OR_Q2_K ? oracle_vec_dot_q2_K_q8_K((int)n, wr, a)
+                                                        : oracle_vec_dot_q3_K_q8_K((int)n, wr, a);
+                }
             }
         }
     } else if (type == OR_Q4_1 || type == OR_Q5_1) {
@@ -1479,6 +1679,48 @@ int oracle_mul_mat(int type, const void *w, int64_t n, int64_t rows, const float
                     }
                 }
                 out[c * rows + r] = route == ORACLE_ROUTE_TILED ? acc : oracle_vec_dot_q5_K_q8_K((int)n, wr, a);
+            }
+        }
+    } else if (type == OR_IQ4_NL || type == OR_NVFP4) {
+        /* the row vec_dot (IQ4_NL from 2 columns would take tinyBLAS_Q0,
+         * tinyblas.rs:1334: the same integer block sums in another fp32 order);
+         * sub-sums per 32-block (IQ4_NL) or 16-element sub-block (NVFP4) */
+        const int64_t nbw = type == OR_IQ4_NL ? n / 32 : n / 64;
+        const size_t wbs = type == OR_IQ4_NL ? sizeof(blk_iq4_nl) : sizeof(blk_nvfp4);
+#pragma omp parallel for num_threads(nth) schedule(static)
+        for (int64_t r = 0; r < rows; r++) {
+            const uint8_t *wr = (const uint8_t *)w + (size_t)r * nbw * wbs;
+            for (int64_t c = 0; c < cols; c++) {
+                const blk_q8_0 *a = (const blk_q8_0 *)(act + (size_t)c * rs);
+                if (subsums) {
+                    if (type == OR_IQ4_NL)
+                        for (int64_t b = 0; b < nbw; b++)
+                            subsums[((size_t)c * rows + r) * nbw + b] = isum_iq4_nl((const blk_iq4_nl *)wr + b, &a[b]);
+                    else
+                        for (int64_t b = 0; b < nbw; b++)
+                            for (int sb = 0; sb < 4; sb++)
+                                subsums[(((size_t)c * rows + r) * nbw + b) * 4 + sb] =
+                                    isum_nvfp4_sub((const blk_nvfp4 *)wr + b, &a[2 * b], sb);
+                }
+                out[c * rows + r] = type == OR_IQ4_NL ? oracle_vec_dot_iq4_nl_q8_0((int)n, wr, a)
+                                                      : oracle_vec_dot_nvfp4_q8_0((int)n, wr, a);
+            }
+        }
+    } else if (type == OR_IQ4_XS) {
+        const int64_t nb = n / QK_K;
+#pragma omp parallel for num_threads(nth) schedule(static)
+        for (int64_t r = 0; r < rows; r++) {
+            const blk_iq4_xs *wr = (const blk_iq4_xs *)((const uint8_t *)w + (size_t)r * nb * sizeof(blk_iq4_xs));
+            for (int64_t c = 0; c < cols; c++) {
+                const blk_q8_K *a = (const blk_q8_K *)(act + (size_t)c * rs);
+                float acc = 0.0f;
+                for (int64_t b = 0; b < nb; b++) {
+                    const int32_t is = isum_iq4_xs(&wr[b], &a[b]);
+                    if (subsums) subsums[((size_t)c * rows + r) * nb + b] = is;
+                    /* tiled.rs:822-836 epilogue (no min term) */
+                    acc = fmaf(H2F(wr[b].d) * (float)is, a[b].d, acc);
+                }
+                out[c * rows + r] = route == ORACLE_ROUTE_TILED ? acc : oracle_vec_dot_iq4_xs_q8_K((int)n, wr, a);
             }
         }
     } else { /* Q6_K */

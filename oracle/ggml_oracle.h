@@ -24,7 +24,7 @@ extern "C" {
 enum {
     OR_F32 = 0, OR_F16 = 1, OR_Q4_0 = 2, OR_Q4_1 = 3, OR_Q5_0 = 6, OR_Q5_1 = 7, OR_Q8_0 = 8, OR_Q8_1 = 9,
     OR_Q2_K = 10, OR_Q3_K = 11, OR_Q4_K = 12,
-    OR_Q5_K = 13, OR_Q6_K = 14, OR_Q8_K = 15, OR_MXFP4 = 39
+    OR_Q5_K = 13, OR_Q6_K = 14, OR_Q8_K = 15, OR_IQ4_NL = 20, OR_IQ4_XS = 23, OR_MXFP4 = 39, OR_NVFP4 = 40
 };
 
 /* ---- scalar helpers ---- */
@@ -32,6 +32,7 @@ uint16_t oracle_fp32_to_fp16(float f);            /* half 2.7.1 from_f32 (RNE); 
 float    oracle_fp16_to_fp32(uint16_t h);
 int32_t  oracle_nearest_int(float f);             /* quants.rs:13 */
 float    oracle_e8m0_to_fp32_half(uint8_t e);     /* quants.rs:682; pinned by closed form 2^(e-128) */
+float    oracle_ue4m3_to_fp32(uint8_t x);         /* quants.rs:699; pinned by the closed form over all 256 bytes and quants_ref_fp4.bin NVFP4 dequant */
 
 /* ---- weight quantizers (one-time prep) ---- */
 void oracle_quantize_row_q4_0_ref(const float *x, void *y, int64_t k);  /* quants.rs:124; quants_ref.bin */
@@ -65,6 +66,9 @@ float oracle_vec_dot_q2_K_q8_K(int n, const void *x, const void *y);  /* vec_dot
 float oracle_vec_dot_q3_K_q8_K(int n, const void *x, const void *y);  /* vec_dot.rs:801; no fixture holds the dot: brute force */
 float oracle_vec_dot_q8_0_q8_0(int n, const void *x, const void *y);  /* vec_dot.rs:732; mulmat_ref*.bin type 8 */
 float oracle_vec_dot_q5_K_q8_K(int n, const void *x, const void *y);  /* vec_dot.rs:928; mulmat_ref*.bin type 13 */
+float oracle_vec_dot_iq4_nl_q8_0(int n, const void *x, const void *y); /* vec_dot.rs:1597; vecdot3_ref.bin type 20 */
+float oracle_vec_dot_iq4_xs_q8_K(int n, const void *x, const void *y); /* vec_dot.rs:1655; vecdot3_ref.bin type 23 */
+float oracle_vec_dot_nvfp4_q8_0(int n, const void *x, const void *y);  /* vec_dot.rs:1154; vecdot3_ref.bin type 40 */
 
 /*
  * The reference's MUL_MAT routing for a 2-D quantized weight W [rows x n]

@@ -256,3 +256,39 @@ def fa_probe_groups():
             sinks=np.frombuffer(s, dtype=np.float32) if s else None,
             scale=sc, max_bias=mb, softcap=cap, recs=recs))
     return groups
+
+
+# block (elements, bytes) of every type in vecdot3_ref.bin (blocks.rs:14-279)
+VDD3_BLOCK = {41: (128, 18), 42: (64, 18), 40: (64, 36), 16: (256, 66), 17: (256, 74), 22: (256, 82),
+              18: (256, 98), 21: (256, 110), 19: (256, 50), 29: (256, 56), 20: (32, 18), 23: (256, 136),
+              8: (32, 34), 15: (256, 292)}
+
+
+def vecdot3_sections(name="vecdot3_ref.bin"):
+    """VDD3 sections (parity/ref_vecdot_dump3.c): the x86 vec_dot of one
+    weight type on LCG block bytes and runtime-quantized activations.
+    [(type_id, n, xq bytes, yq bytes (Q8_0 or Q8_K rows), result f32)]"""
+    b = read(name)
+    o = 0
+    out = []
+    while True:
+        (magic,) = struct.unpack_from("<I", b, o)
+        o += 4
+        if magic == 0xFFFFFFFF:
+            break
+        assert magic == 0x33444456
+        tid, n = struct.unpack_from("<2I", b, o)
+        o += 8
+        qk, sz = VDD3_BLOCK[tid]
+        xl = n // qk * sz
+        vt = 15 if tid in (16, 17, 22, 18, 21, 19, 29, 23) else 8
+        yqk, ysz = VDD3_BLOCK[vt]
+        yl = n // yqk * ysz
+        xq = np.frombuffer(b, dtype=np.uint8, count=xl, offset=o).copy()
+        o += xl
+        yq = np.frombuffer(b, dtype=np.uint8, count=yl, offset=o).copy()
+        o += yl
+        (res,) = struct.unpack_from("<f", b, o)
+        o += 4
+        out.append((tid, n, xq, yq, np.float32(res)))
+    return out

@@ -4,8 +4,9 @@ The files under ``parity/`` of fly88oj/llama.rust (MIT licence, copyright 2026
 fly88oj) are golden vectors that an instrumented llama.cpp build produced.  They
 are data (inputs and expected outputs), copied verbatim -- except
 ``tiled_ref.bin``, of which only the Q4_K, Q5_K and Q6_K MUL_MAT and
-MUL_MAT_ID sections are kept (the IQ types are out of scope and the whole file
-is 18 MB).  Also one GGUF file of the reference's tokenizer tests
+MUL_MAT_ID sections are kept in ``tiled_ref_kq.bin`` and the Q2_K, Q3_K and
+IQ4_XS ones in ``tiled_ref_k23x.bin`` (the other IQ types are out of scope and
+the whole file is 18 MB).  Also one GGUF file of the reference's tokenizer tests
 (crates/llama/tests/tokenizer_fixtures/vocab/ggml-vocab-llama-spm.gguf, a
 vocab-only model whose metadata vocab.rs:4290-4305 checks) for the GGUF
 reader's known-answer test.
@@ -25,8 +26,12 @@ WHOLE = [
     # real GGUF tensors x the reference's production path (vec_dot.rs:2798-2807)
     "q4k_goss_ref.bin", "q4k_granite_ref.bin", "q6k_granite_ref.bin",
     "q5_0_goss_ref.bin", "q8_0_goss_ref.bin", "q5k_real_ref.bin",
+    # IQ4_NL / IQ4_XS quantizer and dequantizer outputs, and the x86 vec_dot
+    # results of NVFP4 / IQ4_NL / IQ4_XS (and the other types of that dump)
+    # on LCG block bytes and runtime-quantized activations
+    "quants_ref_iq.bin", "vecdot3_ref.bin",
 ]
-ROW_BYTES_PER_256 = {10: 84, 11: 110, 12: 144, 13: 176, 14: 210}
+ROW_BYTES_PER_256 = {10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 23: 136}
 
 
 def extract_tiled(src, dst, keep=(12, 13, 14)):
@@ -87,6 +92,8 @@ def main(parity_dir):
     for f in WHOLE:
         shutil.copyfile(os.path.join(parity_dir, f), os.path.join(here, f))
     extract_tiled(os.path.join(parity_dir, "tiled_ref.bin"), os.path.join(here, "tiled_ref_kq.bin"))
+    # the Q2_K, Q3_K and IQ4_XS sections of the same file, in a file of their own
+    extract_tiled(os.path.join(parity_dir, "tiled_ref.bin"), os.path.join(here, "tiled_ref_k23x.bin"), keep=(10, 11, 23))
     vocab = os.path.join(os.path.dirname(parity_dir), "crates", "llama", "tests", "tokenizer_fixtures", "vocab",
                          "ggml-vocab-llama-spm.gguf")
     shutil.copyfile(vocab, os.path.join(here, "ggml-vocab-llama-spm.gguf"))

@@ -590,3 +590,76 @@ def test_q2k_q3k_vec_dot_brute_force(ty):
         else:
             assert np.array_equal(sub.reshape(-1), isum)
         assert out[0, 0] == np.float32(got)
+
+
+VD3 = {O.IQ4_NL: "vec_dot_iq4_nl_q8_0", O.IQ4_XS: "vec_dot_iq4_xs_q8_K", O.NVFP4: "vec_dot_nvfp4_q8_0"}
+
+
+@pytest.mark.parametrize("ty", sorted(VD3))
+def test_vecdot3_bit_exact(ty):
+    """vec_dot.rs vecdot3 ground truth (parity/ref_vecdot_dump3.c): the x86
+    kernels of NVFP4, IQ4_NL and IQ4_XS on LCG block bytes and the reference's
+    own quantized activations; the oracle's fp32 order reproduces the result
+    bit for bit."""
+    (sec,) = [s for s in fx.vecdot3_sections() if s[0] == ty]
+    _, n, xq, yq, want = sec
+    got = np.float32(getattr(O.lib(), "oracle_" + VD3[ty])(n, O._p(xq), O._p(yq)))
+    assert got.view(np.uint32) == want.view(np.uint32), (got, want)
+
+
+def test_vecdot3_dot_is_the_brute_force_of_the_dequantized_rows():
+    """What fixes the dots beyond the dumped fp32 results: each equals, to fp32
+    rounding, the float64 dot of the dequantized weights with the dequantized
+    activations (a dropped term, a wrong nibble order or scale would not)."""
+    for ty, name in VD3.items():
+        (sec,) = [s for s in fx.vecdot3_sections() if s[0] == ty]
+        _, n, xq, yq, want = sec
+        w = O.dequantize(ty, xq, n).astype(np.float64)
+        a = O.dequantize(O.ACT_TYPE[ty], yq, n).astype(np.float64) if O.ACT_TYPE[ty] == O.Q8_0 else None
+        if a is None:  # Q8_K rows: codes * d per 256-block
+            a = np.concatenate([np.frombuffer(yq[i * 292 + 4:i * 292 + 260].tobytes(), np.int8).astype(np.float64) *
+                                np.frombuffer(yq[i * 292:i * 292 + 4].tobytes(), np.float32)[0] for i in range(n // 256)])
+        exact = float(np.dot(w, a))
+        assert abs(float(want) - exact) <= 1e-5 * max(1.0, np.abs(w * a).sum()), (ty, want, exact)
+
+
+@pytest.mark.parametrize("ty", [O.IQ4_NL, O.IQ4_XS])
+def test_iq4_dequant_bit_exact(ty):
+    """quants_k.rs iq dequant parity (parity/ref_quants_dump.c, quants_ref_iq.bin):
+    the reference quantizer's IQ4_NL / IQ4_XS bytes dequantize to the dumped
+    floats bit for bit."""
+    (sec,) = [s for s in fx.quant_sections("quants_ref_iq.bin") if s[1] == ty]
+    _, _, n, q, deq = sec
+    got = O.dequantize(ty, q, n)
+    assert np.array_equal(got.view(np.uint32), deq.view(np.uint32))
+
+
+def test_nvfp4_dequant_and_ue4m3():
+    """quants.rs fp4_dequant_bit_exact_vs_reference for NVFP4 (quants_ref_fp4.bin)
+    and the UE4M3 closed form over all 256 bytes: 0 for 0x00 and 0x7F,
+    man * 2^-10 for exp 0, (8 + man) * 2^(exp - 11) otherwise."""
+    secs = [s for s in fx.quant_sections("quants_ref_fp4.bin") if s[1] == O.NVFP4]
+    assert len(secs) == 4
+    for magic, tid, n, q, deq in secs:
+        got = O.dequantize(O.NVFP4, q, n)
+        assert np.array_equal(got.view(np.uint32), deq.view(np.uint32))
+    L = O.lib()
+    for x in range(256):
+        e, m = (x >> 3) & 15, x & 7
+        want = 0.0 if x in (0, 0x7F) else (m * 2.0 ** -10 if e == 0 else (8 + m) * 2.0 ** (e - 11))
+        assert np.float32(L.oracle_ue4m3_to_fp32(x)) == np.float32(want), x
+
+
+def test_tiled_k23_iq4xs_bit_exact():
+    """tiled.rs:2183 tiled_mulmat_matches_reference_bit_exact for Q2_K, Q3_K and
+    IQ4_XS (parity/tiled_ref.bin, the sections kept in tiled_ref_k23x.bin): from
+    8 columns the oracle folds each super-block's exact sums as the tiled
+    kernel's epilogue does, bit for bit; below 8 it is the row vec_dot."""
+    secs = fx.tiled_sections("tiled_ref_k23x.bin")
+    assert sorted({s[0] for s in secs}) == [O.Q2_K, O.Q3_K, O.IQ4_XS]
+    for tid, n, rows, cols, xq, y, dst in secs:
+        got, route, _ = O.mul_mat(tid, xq, n, rows, y, cols)
+        want_route = O.ROUTE_TILED if cols >= 8 else O.ROUTE_VECDOT
+        assert route == want_route
+        if route == O.ROUTE_TILED:
+            assert np.array_equal(got.view(np.uint32), dst.reshape(cols, rows).view(np.uint32)), (tid, rows, cols)

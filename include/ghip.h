@@ -65,8 +65,11 @@ enum {
     GHIP_TYPE_Q5_K = 13,
     GHIP_TYPE_Q6_K = 14,
     GHIP_TYPE_Q8_K = 15,
+    GHIP_TYPE_IQ4_NL = 20,
+    GHIP_TYPE_IQ4_XS = 23,
     GHIP_TYPE_I32 = 26,
     GHIP_TYPE_MXFP4 = 39,
+    GHIP_TYPE_NVFP4 = 40,
 };
 
 /* The ops of the hot path (GgmlOp::MulMat / MulMatId / FlashAttnExt,
@@ -113,11 +116,11 @@ ghip_status ghip_synchronize(ghip_context *ctx, void *stream);
 int ghip_supports_op(int op, const ghip_tensor *dst, const ghip_tensor *const *srcs, int n_srcs);
 
 /* dst = src0 x src1 (GGML_OP_MUL_MAT, forward_mul_mat compute.rs:1420-1839).
- * src0: Q4_0 | Q4_1 | Q5_0 | Q5_1 | Q8_0 | Q2_K | Q3_K | Q4_K | Q5_K | Q6_K
- *       weight [ne00=K, ne01=N, ne02, ne03], rows contiguous;
+ * src0: Q4_0 | Q4_1 | Q5_0 | Q5_1 | Q8_0 | Q2_K | Q3_K | Q4_K | Q5_K | Q6_K |
+ *       IQ4_NL | IQ4_XS | NVFP4 weight [ne00=K, ne01=N, ne02, ne03], rows contiguous;
  * src1: F32 [K, ne11, ne12, ne13] (any strides nb11..nb13, nb10 == 4), or
- *       already the vec_dot type of src0 (Q8_0 for Q4_0/Q5_0/Q8_0, Q8_1 for
- *       Q4_1/Q5_1, Q8_K for the K-quants; rows of blocks),
+ *       already the vec_dot type of src0 (Q8_0 for Q4_0/Q5_0/Q8_0/IQ4_NL/NVFP4,
+ *       Q8_1 for Q4_1/Q5_1, Q8_K for the K-quants and IQ4_XS; rows of blocks),
  *       which skips the quantization (backend.rs:2057-2066 semantics);
  * dst:  F32 [N, ne11, ne12, ne13] (nb0 == 4).
  * Planes: ne12 % ne02 == 0 and ne13 % ne03 == 0; dst plane (i12, i13) is
@@ -154,6 +157,9 @@ ghip_status ghip_mul_mat_noalloc(ghip_context *ctx, const ghip_tensor *src0, con
  *   Q4_0: P = nb,   sum (nib-8)*q8 of 32-block b
  *   Q5_0: P = nb,   sum ((nib | hbit << 4) - 16)*q8 of 32-block b
  *   Q8_0: P = nb,   sum q8w*q8 of 32-block b
+ *   IQ4_NL: P = nb, sum kvalue*q8 of 32-block b
+ *   NVFP4: P = 4*nb, sum kvalue*q8 of each 16-element sub-block of 64-block b
+ *   IQ4_XS: P = nb, sum_g (ls_g - 32) * sum kvalue*q8 of super-block b
  * subsums is a device pointer of ne11*N*P int32. */
 ghip_status ghip_mul_mat_subsums(ghip_context *ctx, const ghip_tensor *src0, const ghip_tensor *src1,
                                  int32_t *subsums, void *stream);

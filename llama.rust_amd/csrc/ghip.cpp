@@ -20,7 +20,7 @@
 
 namespace {
 
-const char *const kModules[] = {"ghip_quant.hsaco", "ghip_gemv.hsaco", "ghip_wquant.hsaco", "ghip_gemm.hsaco", "ghip_fa.hsaco", "ghip_moe.hsaco", "ghip_skinny.hsaco"};
+const char *const kModules[] = {"ghip_quant.hsaco", "ghip_gemv.hsaco", "ghip_wquant.hsaco", "ghip_gemm.hsaco", "ghip_fa.hsaco", "ghip_moe.hsaco", "ghip_skinny.hsaco", "ghip_iq.hsaco"};
 
 struct TypeInfo {
     int blck;
@@ -45,6 +45,9 @@ TypeInfo type_info(int t) {
     case GHIP_TYPE_Q8_K: return {256, 292};
     case GHIP_TYPE_I32: return {1, 4};
     case GHIP_TYPE_MXFP4: return {32, 17};
+    case GHIP_TYPE_IQ4_NL: return {32, 18};
+    case GHIP_TYPE_IQ4_XS: return {256, 136};
+    case GHIP_TYPE_NVFP4: return {64, 36};
     default: return {0, 0};
     }
 }
@@ -246,14 +249,18 @@ bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b,
     if (a->type != GHIP_TYPE_Q4_0 && a->type != GHIP_TYPE_Q5_0 && a->type != GHIP_TYPE_Q8_0 &&
         a->type != GHIP_TYPE_Q4_K && a->type != GHIP_TYPE_Q5_K && a->type != GHIP_TYPE_Q6_K &&
         a->type != GHIP_TYPE_Q4_1 && a->type != GHIP_TYPE_Q5_1 && a->type != GHIP_TYPE_Q2_K &&
-        a->type != GHIP_TYPE_Q3_K) {
+        a->type != GHIP_TYPE_Q3_K && a->type != GHIP_TYPE_IQ4_NL && a->type != GHIP_TYPE_IQ4_XS &&
+        a->type != GHIP_TYPE_NVFP4) {
         st = ctx->fail(st,
-                       "mul_mat: src0 type %d not supported (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K)",
+                       "mul_mat: src0 type %d not supported (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, "
+                       "IQ4_NL, IQ4_XS, NVFP4)",
                        a->type);
         return false;
     }
     const TypeInfo ti = type_info(a->type);
-    const bool q8_0_dot = a->type == GHIP_TYPE_Q4_0 || a->type == GHIP_TYPE_Q5_0 || a->type == GHIP_TYPE_Q8_0;
+    // vec_dot_type Q8_0 (vec_dot.rs:1727): Q4_0, Q5_0, Q8_0, NVFP4, IQ4_NL
+    const bool q8_0_dot = a->type == GHIP_TYPE_Q4_0 || a->type == GHIP_TYPE_Q5_0 || a->type == GHIP_TYPE_Q8_0 ||
+                          a->type == GHIP_TYPE_IQ4_NL || a->type == GHIP_TYPE_NVFP4;
     const bool q8_1_dot = a->type == GHIP_TYPE_Q4_1 || a->type == GHIP_TYPE_Q5_1;
     // vec_dot_type (vec_dot.rs vec_dot_type)
     const int vdt = q8_0_dot ? GHIP_TYPE_Q8_0 : q8_1_dot ? GHIP_TYPE_Q8_1 : GHIP_TYPE_Q8_K;
@@ -337,6 +344,9 @@ const char *gemv_base(int wtype) {
     case GHIP_TYPE_Q2_K: return "ghip_gemv_q2_K";
     case GHIP_TYPE_Q3_K: return "ghip_gemv_q3_K";
     case GHIP_TYPE_Q5_1: return "ghip_gemv_q5_1";
+    case GHIP_TYPE_IQ4_NL: return "ghip_gemv_iq4_nl";
+    case GHIP_TYPE_IQ4_XS: return "ghip_gemv_iq4_xs";
+    case GHIP_TYPE_NVFP4: return "ghip_gemv_nvfp4";
     default: return "ghip_gemv_q4_0";
     }
 }
@@ -347,6 +357,21 @@ bool k23_type(int wtype) { return wtype == GHIP_TYPE_Q2_K || wtype == GHIP_TYPE_
 // 32-element blocks with Q8_0 activations: one lane per pair of blocks
 bool gemv_pair(int wtype) {
     return wtype == GHIP_TYPE_Q4_0 || wtype == GHIP_TYPE_Q5_0 || wtype == GHIP_TYPE_Q8_0;
+}
+// table-lookup 4-bit types (ghip_iq.hip): one decode lane per 32 elements
+bool lut_type(int wtype) {
+    return wtype == GHIP_TYPE_IQ4_NL || wtype == GHIP_TYPE_IQ4_XS || wtype == GHIP_TYPE_NVFP4;
+}
+// weights the int8-MFMA GEMM ghip_gemm_q8 takes as int8 codes with one scale
+// per 32 elements (NVFP4's scales are per 16: its prefill runs the decode
+// kernel in groups of 8 columns)
+bool gemm_q8_family(int wtype) {
+    return gemv_pair(wtype) || wtype == GHIP_TYPE_IQ4_NL || wtype == GHIP_TYPE_IQ4_XS;
+}
+// int32 sub-sums per weight block (ghip_mul_mat_subsums layout)
+int64_t subsums_per_block(int wtype) {
+    if (wtype == GHIP_TYPE_Q4_K || wtype == GHIP_TYPE_Q5_K || wtype == GHIP_TYPE_Q2_K) return 2;
+    return wtype == GHIP_TYPE_NVFP4 ? 4 : 1;
 }
 
 // The whole-row decode kernels with the activation image in LDS: Q4_K and
@@ -524,6 +549,8 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
         waves_k = (int)(((p.nb + 1) / 2 + 63) / 64);
     else if (p.wtype == GHIP_TYPE_Q4_1 || p.wtype == GHIP_TYPE_Q5_1)  // one lane per 32-block
         waves_k = (int)((p.nb + 63) / 64);
+    else if (lut_type(p.wtype))  // one lane per 32 elements
+        waves_k = (int)((p.K / 32 + 63) / 64);
     else if (k23_type(p.wtype))  // four lanes per super-block
         waves_k = (int)((p.nb + 15) / 16);
     else if (gemv_v2(p))
@@ -597,8 +624,7 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
             name.replace(0, std::strlen("ghip_gemv_q5_0"), "ghip_gemv_q5_0_full");
         int32_t *sub_c = sub;
         if (sub) {
-            const int64_t per = (p.wtype == GHIP_TYPE_Q4_K || p.wtype == GHIP_TYPE_Q5_K || p.wtype == GHIP_TYPE_Q2_K) ? 2 * p.nb : p.nb;
-            sub_c = sub + c0 * p.N * per;
+            sub_c = sub + c0 * p.N * subsums_per_block(p.wtype) * p.nb;
         }
         ghip_status st;
         if (q4k) {
@@ -683,6 +709,7 @@ size_t gemm_q6k_bytes(const MulMatPlan &p, size_t *codes_b, size_t *dt_b) {
 struct Q8Layout {
     int64_t Mpad, Npad, Kpad, nbp;
     size_t act_b, da_b, w_b, dw_b;
+    size_t dsb_b;  // IQ4_XS: d per (super-block, row), after dw
 };
 Q8Layout q8_layout(int64_t M, int64_t N, int64_t K) {
     Q8Layout L;
@@ -695,12 +722,15 @@ Q8Layout q8_layout(int64_t M, int64_t N, int64_t K) {
     L.da_b = up((size_t)L.nbp * L.Mpad * 4);
     L.w_b = up((size_t)L.Npad * L.Kpad);
     L.dw_b = up((size_t)L.nbp * L.Npad * 4);
+    L.dsb_b = up((size_t)(L.Kpad / 256) * L.Npad * 4);
     return L;
 }
+// the GEMM's per-weight extra: IQ4_XS keeps its super-block scales apart
+size_t q8_extra_b(int wtype, const Q8Layout &L) { return wtype == GHIP_TYPE_IQ4_XS ? L.dsb_b : 0; }
 size_t gemm_layout_bytes(const MulMatPlan &p) {
-    if (gemv_pair(p.wtype)) {
+    if (gemm_q8_family(p.wtype)) {
         const Q8Layout L = q8_layout(p.M, p.N, p.K);
-        return L.act_b + L.da_b + L.w_b + L.dw_b;
+        return L.act_b + L.da_b + L.w_b + L.dw_b + q8_extra_b(p.wtype, L);
     }
     if (p.wtype == GHIP_TYPE_Q6_K) {
         size_t a, b;
@@ -755,12 +785,21 @@ ghip_status run_gemm_q6k(ghip_context *ctx, const MulMatPlan &p, const void *w, 
 }
 
 const char *q8w_repack_name(int wtype) {
-    return wtype == GHIP_TYPE_Q4_0 ? "ghip_gemm_q8w_repack_q4_0"
-           : wtype == GHIP_TYPE_Q5_0 ? "ghip_gemm_q8w_repack_q5_0" : "ghip_gemm_q8w_repack_q8_0";
+    switch (wtype) {
+    case GHIP_TYPE_Q4_0: return "ghip_gemm_q8w_repack_q4_0";
+    case GHIP_TYPE_Q5_0: return "ghip_gemm_q8w_repack_q5_0";
+    case GHIP_TYPE_IQ4_NL: return "ghip_gemm_q8w_repack_iq4_nl";
+    case GHIP_TYPE_IQ4_XS: return "ghip_gemm_q8w_repack_iq4_xs";
+    default: return "ghip_gemm_q8w_repack_q8_0";
+    }
 }
 ghip_status q8w_repack(ghip_context *ctx, int wtype, const void *w, int64_t row_bytes, int64_t N, int64_t nb,
                        const Q8Layout &L, int8_t *codes, float *dw, hipStream_t s) {
     const int64_t n = L.Npad * L.nbp;
+    if (wtype == GHIP_TYPE_IQ4_XS)  // the super-block scales follow dw
+        return ctx->launch(q8w_repack_name(wtype), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                           (const uint8_t *)w, row_bytes, (int)N, (int)nb, (int)L.Kpad, (int)L.Npad, codes, dw,
+                           (float *)((uint8_t *)dw + L.dw_b));
     return ctx->launch(q8w_repack_name(wtype), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
                        (const uint8_t *)w, row_bytes, (int)N, (int)nb, (int)L.Kpad, (int)L.Npad, codes, dw);
 }
@@ -788,13 +827,23 @@ ghip_status run_gemm_q8(ghip_context *ctx, const MulMatPlan &p, const void *w, c
         dw = d;
     }
     const int64_t ablocks = L.Mpad * L.nbp;
-    st = ctx->launch("ghip_gemm_act_q8_0", dim3((unsigned)((ablocks * 8 + 255) / 256)), dim3(256), 0, s,
-                     (const float *)bf->data, (int64_t)bf->nb[1] / 4, (int)p.M, (int)L.Mpad, (int)p.nb, (int)L.Kpad,
-                     ac, da);
+    if (p.wtype == GHIP_TYPE_IQ4_XS)  // Q8_K activations: codes and the block scale per 32-group
+        st = ctx->launch("ghip_gemm_act_q8K_q8", dim3((unsigned)((L.Mpad * p.nb + 3) / 4)), dim3(256), 0, s,
+                         (const float *)bf->data, (int64_t)bf->nb[1] / 4, (int)p.M, (int)L.Mpad, (int)p.nb,
+                         (int)L.Kpad, ac, da);
+    else
+        st = ctx->launch("ghip_gemm_act_q8_0", dim3((unsigned)((ablocks * 8 + 255) / 256)), dim3(256), 0, s,
+                         (const float *)bf->data, (int64_t)bf->nb[1] / 4, (int)p.M, (int)L.Mpad, (int)p.nb,
+                         (int)L.Kpad, ac, da);
     if (st != GHIP_STATUS_SUCCESS) return st;
     const unsigned grid = (unsigned)(((p.M + 63) / 64) * ((p.N + 127) / 128));
+    const int nb32 = (int)(p.K / 32);  // the GEMM's blocks are 32 elements
+    if (p.wtype == GHIP_TYPE_IQ4_XS)
+        return ctx->launch(sub ? "ghip_gemm_q8_xs_sub" : "ghip_gemm_q8_xs", dim3(grid), dim3(256), kGemmSmemQ8, s, wc,
+                           dw, (int)p.N, (int)L.Npad, nb32, (int)L.Kpad, (const int8_t *)ac, (const float *)da,
+                           (int)p.M, (int)L.Mpad, dst, ldd, sub, (const float *)((const uint8_t *)dw + L.dw_b));
     return ctx->launch(sub ? "ghip_gemm_q8_sub" : "ghip_gemm_q8", dim3(grid), dim3(256), kGemmSmemQ8, s, wc, dw,
-                       (int)p.N, (int)L.Npad, (int)p.nb, (int)L.Kpad, (const int8_t *)ac, (const float *)da, (int)p.M,
+                       (int)p.N, (int)L.Npad, nb32, (int)L.Kpad, (const int8_t *)ac, (const float *)da, (int)p.M,
                        (int)L.Mpad, dst, ldd, sub);
 }
 
@@ -803,7 +852,7 @@ ghip_status run_gemm_q8(ghip_context *ctx, const MulMatPlan &p, const void *w, c
 ghip_status run_gemm(ghip_context *ctx, const MulMatPlan &p, const void *w, const uint8_t *act, const ghip_tensor *bf,
                      float *dst, int64_t ldd, int32_t *sub, void *layout_ws, hipStream_t s) {
     if (p.wtype == GHIP_TYPE_Q6_K) return run_gemm_q6k(ctx, p, w, act, bf, dst, ldd, sub, layout_ws, s);
-    if (gemv_pair(p.wtype)) return run_gemm_q8(ctx, p, w, bf, dst, ldd, sub, layout_ws, s);
+    if (gemm_q8_family(p.wtype)) return run_gemm_q8(ctx, p, w, bf, dst, ldd, sub, layout_ws, s);
     const int64_t Mpad = (p.M + 127) / 128 * 128, K = p.K, nbk = p.K / 256;
     int8_t *codes = (int8_t *)layout_ws;
     uint16_t *bsT = (uint16_t *)(codes + Mpad * K);
@@ -841,15 +890,21 @@ bool use_gemm(const MulMatPlan &p) {
     // Q6_K: the f16-MFMA GEMM from 64 activation rows (below, the 8-column decode kernels)
     if (p.wtype == GHIP_TYPE_Q6_K) return p.M >= env_int("GHIP_GEMM_Q6K_MIN_ROWS", 64) && p.K >= 512;
     // Q4_0 / Q5_0 / Q8_0 from f32 activations: the int8-MFMA GEMM from 32 rows
-    if (gemv_pair(p.wtype)) return !p.act_pre && p.M >= env_int("GHIP_GEMM_Q8_MIN_ROWS", 32);
+    if (gemm_q8_family(p.wtype)) return !p.act_pre && p.M >= env_int("GHIP_GEMM_Q8_MIN_ROWS", 32);
     return false;
+}
+// the prefill GEMM (every GEMM also writes the sub-sums' layout)
+bool gemm_route(const MulMatPlan &p, bool sub) {
+    (void)sub;
+    return use_gemm(p);
 }
 
 // workspace of one MUL_MAT: [quantized activations | GEMM layout | f32
 // scratch output when only sub-sums are wanted]
-size_t mul_mat_ws_bytes(const MulMatPlan &p, bool has_dst, bool act_out, size_t *act_b, size_t *lay_b) {
+size_t mul_mat_ws_bytes(const MulMatPlan &p, bool has_dst, bool act_out, size_t *act_b, size_t *lay_b,
+                        bool sub = false) {
     // (the GEMM quantizes f32 activations straight into its layout)
-    const bool gemm = !act_out && use_gemm(p);
+    const bool gemm = !act_out && gemm_route(p, sub);
     // (the split-K decode kernels quantize inside; their layout is the partials)
     const bool sk = !act_out && !gemm && use_sk(p);
     const size_t act_bytes = p.act_pre || gemm || sk ? 0 : ((size_t)(p.M * p.act_row_bytes) + 255) & ~(size_t)255;
@@ -879,7 +934,7 @@ ghip_status mul_mat_plane(ghip_context *ctx, const ghip_tensor *a, const ghip_te
     st = ctx->begin(s);
     if (st != GHIP_STATUS_SUCCESS) return st;
     size_t act_bytes, lay_bytes;
-    const size_t need = mul_mat_ws_bytes(p, d != nullptr, act_out != nullptr, &act_bytes, &lay_bytes);
+    const size_t need = mul_mat_ws_bytes(p, d != nullptr, act_out != nullptr, &act_bytes, &lay_bytes, sub != nullptr);
     void *ws = nullptr;
     if (need) {
         st = ctx->workspace(need, s, &ws);
@@ -893,7 +948,7 @@ ghip_status mul_mat_plane(ghip_context *ctx, const ghip_tensor *a, const ghip_te
     void *lay = lay_bytes ? (void *)((uint8_t *)ws + act_bytes) : nullptr;
     float *dst = d ? (float *)d->data : (float *)((uint8_t *)ws + act_bytes + lay_bytes);
     const int64_t ldd = d ? (int64_t)d->nb[1] / 4 : p.N;
-    if (use_gemm(p))
+    if (gemm_route(p, sub != nullptr))
         return run_gemm(ctx, p, a->data, (const uint8_t *)b->data, p.act_pre ? nullptr : b, dst, ldd, sub, lay, s);
     if (use_sk(p)) return run_sk(ctx, p, a->data, b, dst, ldd, sub, lay, s);
     if (p.act_pre) return run_gemv(ctx, p, a->data, (const uint8_t *)b->data, p.act_row_bytes, false, dst, ldd, sub, s);
@@ -927,9 +982,7 @@ ghip_status mul_mat_impl(ghip_context *ctx, const ghip_tensor *a, const ghip_ten
         if (!plan_mul_mat(ctx, a, b, d, p, st)) return st;
     }
     const int64_t r2 = b->ne[2] / a->ne[2], r3 = b->ne[3] / a->ne[3];
-    // sub-sums per block: {iacc, imin} for the types with a min term, one int otherwise
-    const bool two = p.wtype == GHIP_TYPE_Q4_K || p.wtype == GHIP_TYPE_Q5_K || p.wtype == GHIP_TYPE_Q2_K;
-    const size_t sub_plane = (size_t)p.M * (size_t)p.N * (size_t)p.nb * (two ? 2 : 1);
+    const size_t sub_plane = (size_t)p.M * (size_t)p.N * (size_t)p.nb * (size_t)subsums_per_block(p.wtype);
     const size_t act_plane = (size_t)p.M * (size_t)p.act_row_bytes;
     int64_t plane = 0;
     for (int64_t i13 = 0; i13 < b->ne[3]; i13++)
@@ -1755,9 +1808,10 @@ ghip_status ghip_weight_register(ghip_context *ctx, const ghip_tensor *w, void *
     if (!w || !w->data) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: null weight");
     if (w->ne[0] <= 0 || w->ne[1] <= 0 || w->ne[2] <= 0 || w->ne[3] != 1)
         return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: empty or 4-D weight");
-    const bool q6k = w->type == GHIP_TYPE_Q6_K, mx = w->type == GHIP_TYPE_MXFP4, q8 = gemv_pair(w->type);
+    const bool q6k = w->type == GHIP_TYPE_Q6_K, mx = w->type == GHIP_TYPE_MXFP4, q8 = gemm_q8_family(w->type);
     if ((q6k || q8) && w->ne[2] != 1)
-        return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: Q6_K / Q4_0 / Q5_0 / Q8_0 weights are 2-D");
+        return ctx->fail(GHIP_STATUS_BACKEND_ERROR,
+                         "weight_register: Q6_K / Q4_0 / Q5_0 / Q8_0 / IQ4_NL / IQ4_XS weights are 2-D");
     // every other type is read in its GGUF layout: nothing to build
     if (!(q6k || mx || q8) || !repack_enabled()) return GHIP_STATUS_SUCCESS;
     size_t bytes;
@@ -1765,11 +1819,11 @@ ghip_status ghip_weight_register(ghip_context *ctx, const ghip_tensor *w, void *
     Q8Layout QL{};
     if (q8) {
         const TypeInfo ti = type_info(w->type);
-        if (w->ne[0] % 32 || w->nb[0] != (uint64_t)ti.bytes || w->nb[1] < (uint64_t)(w->ne[0] / 32 * ti.bytes))
+        if (w->ne[0] % ti.blck || w->nb[0] != (uint64_t)ti.bytes || w->nb[1] < (uint64_t)(w->ne[0] / ti.blck * ti.bytes))
             return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: bad block geometry");
         if (w->ne[1] > INT32_MAX) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: dimension too large");
         QL = q8_layout(1, w->ne[1], w->ne[0]);
-        bytes = QL.w_b + QL.dw_b;
+        bytes = QL.w_b + QL.dw_b + q8_extra_b(w->type, QL);
     } else if (q6k) {
         if (w->ne[0] % 256 || w->nb[0] != 210 || w->nb[1] < (uint64_t)(w->ne[0] / 256 * 210))
             return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "weight_register: bad Q6_K geometry");
@@ -1802,7 +1856,7 @@ ghip_status ghip_weight_register(ghip_context *ctx, const ghip_tensor *w, void *
         return ctx->fail(GHIP_STATUS_OUT_OF_MEMORY, "weight_register: hipMalloc(%zu) failed", bytes);
     }
     if (q8) {
-        st = q8w_repack(ctx, w->type, w->data, (int64_t)w->nb[1], w->ne[1], w->ne[0] / 32, QL, (int8_t *)rep,
+        st = q8w_repack(ctx, w->type, w->data, (int64_t)w->nb[1], w->ne[1], w->ne[0] / type_info(w->type).blck, QL, (int8_t *)rep,
                         (float *)((uint8_t *)rep + QL.w_b), s);
     } else if (q6k) {
         st = q6k_repack(ctx, w->data, (int64_t)w->nb[1], w->ne[1], nbk, (uint8_t *)rep, s);

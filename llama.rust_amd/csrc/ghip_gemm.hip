@@ -1017,11 +1017,19 @@ struct Smem {
 // 32w .. 32w+31 and both 32-token tiles.  C[token][row]: lane l holds row
 // l % 32 and tokens crow(v, l).  Operands: lane l takes K 16(l/32) .. +15 of
 // the block (A: token l % 32 of the tile, B: row l % 32).
-template <bool SUBSUMS>
+//
+// XS (IQ4_XS weights, Q8_K activations): dw holds each 32-group's integer
+// scale ls - 32 (exact in f32) and dsb[super-block][row] the block's d; the
+// groups' exact dots are summed as (ls - 32) * dot in int32 over the
+// super-block, and the super-block folds as the reference's tiled kernel does
+// (tiled.rs:822-836): res = d * is, out = fma(res, d8, out), in super-block
+// order.  Sub-sums are then the super-block sums.
+template <bool SUBSUMS, bool XS = false>
 __device__ __forceinline__ void gemm_q8_impl(const int8_t *__restrict__ wc, const float *__restrict__ dw, int N,
                                              int Npad, int nb, int Kpad, const int8_t *__restrict__ ac,
                                              const float *__restrict__ da, int M, int Mpad, float *__restrict__ dst,
-                                             int64_t ldd, int32_t *__restrict__ sub) {
+                                             int64_t ldd, int32_t *__restrict__ sub,
+                                             const float *__restrict__ dsb = nullptr) {
     constexpr int BM = g8::BM, BN = g8::BN, GB = g8::GB;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
     g8::Smem &SM = *reinterpret_cast<g8::Smem *>(smem_raw);
@@ -1065,10 +1073,14 @@ __device__ __forceinline__ void gemm_q8_impl(const int8_t *__restrict__ wc, cons
     };
 
     v16f out[2];
+    v16i isb[2];  // XS: the super-block's integer sums
 #pragma unroll
     for (int tm = 0; tm < 2; tm++)
 #pragma unroll
-        for (int v = 0; v < 16; v++) out[tm][v] = 0.0f;
+        for (int v = 0; v < 16; v++) {
+            out[tm][v] = 0.0f;
+            isb[tm][v] = 0;
+        }
     const int wr = 32 * wave + li;  // this lane's weight row in the tile
     issue(0, 0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1088,13 +1100,32 @@ __device__ __forceinline__ void gemm_q8_impl(const int8_t *__restrict__ wc, cons
                 const v4i a = *reinterpret_cast<const v4i *>(SM.act[p] + ta * 128 + 16 * (slot ^ (ta & 7)));
                 const v16i zi = {};
                 const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bw, zi, 0, 0, 0);
+                if constexpr (XS) {
+                    // |ls * dot| <= 32 * 32 * 127 * 128, eight of them fit int32
+                    const int ls = (int)sw;
 #pragma unroll
-                for (int v = 0; v < 16; v++) {
-                    const int tl = 32 * tm + crow(v, lane);
-                    out[tm][v] = fmaf(sw * SM.da[p][kb][tl], (float)c[v], out[tm][v]);
-                    if constexpr (SUBSUMS)
-                        if (b < nb && m0 + tl < M && n0 + wr < N)
-                            sub[((int64_t)(m0 + tl) * N + (n0 + wr)) * nb + b] = c[v];
+                    for (int v = 0; v < 16; v++) isb[tm][v] += ls * c[v];
+                    if ((b & 7) == 7) {
+                        const float d = b < nb ? dsb[(int64_t)(b >> 3) * Npad + min(n0 + wr, Npad - 1)] : 0.0f;
+#pragma unroll
+                        for (int v = 0; v < 16; v++) {
+                            const int tl = 32 * tm + crow(v, lane);
+                            out[tm][v] = fmaf(d * (float)isb[tm][v], SM.da[p][kb][tl], out[tm][v]);
+                            if constexpr (SUBSUMS)
+                                if (b < nb && m0 + tl < M && n0 + wr < N)
+                                    sub[((int64_t)(m0 + tl) * N + (n0 + wr)) * (nb >> 3) + (b >> 3)] = isb[tm][v];
+                            isb[tm][v] = 0;
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int v = 0; v < 16; v++) {
+                        const int tl = 32 * tm + crow(v, lane);
+                        out[tm][v] = fmaf(sw * SM.da[p][kb][tl], (float)c[v], out[tm][v]);
+                        if constexpr (SUBSUMS)
+                            if (b < nb && m0 + tl < M && n0 + wr < N)
+                                sub[((int64_t)(m0 + tl) * N + (n0 + wr)) * nb + b] = c[v];
+                    }
                 }
             }
         }
@@ -1121,5 +1152,18 @@ extern "C" __global__ void __launch_bounds__(256)
                      int Kpad, const int8_t *__restrict__ ac, const float *__restrict__ da, int M, int Mpad,
                      float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
     gemm_q8_impl<true>(wc, dw, N, Npad, nb, Kpad, ac, da, M, Mpad, dst, ldd, sub);
+}
+extern "C" __global__ void __launch_bounds__(256)
+    ghip_gemm_q8_xs(const int8_t *__restrict__ wc, const float *__restrict__ dw, int N, int Npad, int nb, int Kpad,
+                    const int8_t *__restrict__ ac, const float *__restrict__ da, int M, int Mpad,
+                    float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub, const float *__restrict__ dsb) {
+    gemm_q8_impl<false, true>(wc, dw, N, Npad, nb, Kpad, ac, da, M, Mpad, dst, ldd, sub, dsb);
+}
+extern "C" __global__ void __launch_bounds__(256)
+    ghip_gemm_q8_xs_sub(const int8_t *__restrict__ wc, const float *__restrict__ dw, int N, int Npad, int nb,
+                        int Kpad, const int8_t *__restrict__ ac, const float *__restrict__ da, int M, int Mpad,
+                        float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub,
+                        const float *__restrict__ dsb) {
+    gemm_q8_impl<true, true>(wc, dw, N, Npad, nb, Kpad, ac, da, M, Mpad, dst, ldd, sub, dsb);
 }
 static_assert(sizeof(g8::Smem) == 55296, "host code launches with this LDS size");

@@ -1,0 +1,309 @@
+// ghip_iq.hip -- MUL_MAT for the lookup-table 4-bit weight types:
+//   IQ4_NL  18 B / 32  {f16 d; u8 qs[16]}                 x Q8_0 (vec_dot.rs:1597)
+//   IQ4_XS  136 B / 256 {f16 d; u16 scales_h; u8 scales_l[4]; u8 qs[128]} x Q8_K (vec_dot.rs:1655)
+//   NVFP4   36 B / 64  {u8 d[4] (UE4M3 per 16); u8 qs[32]} x Q8_0 (vec_dot.rs:1154)
+// (block layouts blocks.rs:55-62, :234-249).  A nibble is an index into a
+// 16-entry int8 table: KVALUES_IQ4NL (quants_k.rs:647) or the E2M1 values
+// doubled, KVALUES_MXFP4 (quants.rs:660).
+//
+// Decode (1..8 activation rows): one lane per 32 weight elements, which is
+// one Q8_0 activation block (IQ4_NL, NVFP4) or one 32-group of a Q8_K block
+// (IQ4_XS); RB weight rows per workgroup, all of a lane's loads issued
+// before any is consumed.  Per lane and row the integer dot of the 32
+// elements is exact (v_dot4_i32_i8 on the looked-up int8 values) and scaled
+// once: IQ4_NL d_w * d_a, NVFP4 ue4m3(d_s) * d_a per 16-element sub-block,
+// IQ4_XS d_w * d8 * (ls - 32).  Rows are reduced over the wavefront and the
+// workgroup as in the other decode kernels.
+//
+// Prefill: IQ4_NL and IQ4_XS weights become int8 codes (the table values)
+// with one f32 scale per 32 elements (IQ4_NL: d; IQ4_XS: the integer ls - 32,
+// with d per super-block beside it), the operands of the int8-MFMA GEMM of
+// ghip_gemm.hip; IQ4_XS activations are Q8_K rows written in that GEMM's
+// layout (ghip_gemm_act_q8K_q8).
+#include "ghip_common.h"
+#include "ghip_q8k.h"
+
+namespace {
+
+constexpr int RB = 8;  // weight rows per decode workgroup
+constexpr int WT_IQ4_NL = 20, WT_IQ4_XS = 23, WT_NVFP4 = 40;
+
+// 16-entry int8 tables as four little-endian dwords (entries 4i .. 4i+3 in T[i])
+struct Lut {
+    uint32_t t0, t1, t2, t3;
+};
+// KVALUES_IQ4NL: -127 -104 -83 -65 | -49 -35 -22 -10 | 1 13 25 38 | 53 69 89 113
+constexpr Lut kIq4nl = {0xBFAD9881u, 0xF6EADDCFu, 0x26190D01u, 0x71594535u};
+// KVALUES_MXFP4: 0 1 2 3 | 4 6 8 12 | 0 -1 -2 -3 | -4 -6 -8 -12
+constexpr Lut kMxfp4 = {0x03020100u, 0x0C080604u, 0xFDFEFF00u, 0xF4F8FAFCu};
+
+// Table values of four nibbles, one in bits 0-3 of each byte of x (higher bits
+// of a byte are ignored): v_perm_b32 picks from entries 0-7 and 8-15 by the
+// low three bits, and a third v_perm_b32 picks, per byte, the half that bit 3
+// names.
+DEV uint32_t lut4(const Lut &L, uint32_t x) {
+    const uint32_t idx = x & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(L.t1, L.t0, idx);
+    const uint32_t hi = __builtin_amdgcn_perm(L.t3, L.t2, idx);
+    const uint32_t sel = 0x03020100u | ((x >> 1) & 0x04040404u);  // byte i: i, or 4 + i where bit 3 is set
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// ue4m3_to_fp32 (quants.rs:699-712): exp 0 -> man * 2^-10, 0x7F -> 0, else
+// (8 + man) * 2^(exp - 11) (the halving included); built from bits, exact
+DEV float ue4m3(uint32_t x) {
+    x &= 0xffu;
+    const uint32_t e = (x >> 3) & 15u, m = x & 7u;
+    if (x == 0x7Fu) return 0.0f;
+    if (e == 0) return (float)m * 0x1p-10f;
+    return __uint_as_float(((e + 119u) << 23) | (m << 20));
+}
+
+DEV void stash_rows(float *red, float part[RB], int lane, int w, int nw, int c, int NC) {
+    const float t = reduce8_rows(part, lane);
+    if ((lane & 7) == 0) red[((lane >> 3) * nw + w) * NC + c] = t;
+}
+DEV void finish_rows(const float *red, int r0, int nrows, int ncols, int NC, int nw, float *dst, int64_t ldd) {
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < nrows * ncols; idx += blockDim.x) {
+        const int rr = idx / ncols, c = idx - rr * ncols;
+        float s = 0.0f;
+        for (int ww = 0; ww < nw; ww++) s += red[(rr * nw + ww) * NC + c];
+        dst[(int64_t)c * ldd + r0 + rr] = s;
+    }
+}
+
+// nb: weight blocks per row (K / 32, K / 256 or K / 64).  Sub-sums (the
+// ghip_mul_mat_subsums layout): IQ4_NL the exact dot per 32-block; NVFP4 per
+// 16-element sub-block (4 per block); IQ4_XS sum (ls - 32) * dot per
+// super-block.
+template <int WT, int NC, bool SUBSUMS>
+__device__ __forceinline__ void gemv_lut_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb,
+                                              const uint8_t *__restrict__ act, int64_t act_row_bytes, int ncols,
+                                              float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
+    __shared__ float red[RB * 8 * NC];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int ng = WT == WT_IQ4_NL ? nb : WT == WT_NVFP4 ? 2 * nb : 8 * nb;  // 32-element groups per row
+    const int g = 64 * w + lane;
+    const bool valid = g < ng;
+    const int gc = valid ? g : ng - 1;  // loads of invalid lanes re-read a valid group
+    const int r0 = (int)blockIdx.x * RB;
+    const int nr = min(RB, rows - r0);
+    const Lut L = WT == WT_NVFP4 ? kMxfp4 : kIq4nl;
+
+    // this lane's weight bytes: the 16 qs bytes of its 32 elements and the
+    // scale word (IQ4_NL: d; NVFP4: the two UE4M3 bytes; IQ4_XS: d, scales_h,
+    // scales_l)
+    uint32_t boff, qoff;
+    if (WT == WT_IQ4_NL) {
+        boff = (uint32_t)gc * 18u;
+        qoff = boff + 2u;
+    } else if (WT == WT_NVFP4) {
+        boff = (uint32_t)(gc >> 1) * 36u + 2u * (uint32_t)(gc & 1);
+        qoff = (uint32_t)(gc >> 1) * 36u + 4u + 16u * (uint32_t)(gc & 1);
+    } else {
+        boff = (uint32_t)(gc >> 3) * 136u;
+        qoff = boff + 8u + 16u * (uint32_t)(gc & 7);
+    }
+    uint4 qv[RB];
+    uint2 hv[RB];
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        const uint8_t *p = W + (int64_t)min(r0 + rr, rows - 1) * w_row_bytes;
+        qv[rr] = ld16(p + qoff);
+        if (WT == WT_IQ4_XS) hv[rr] = ld8(p + boff);
+        else hv[rr] = make_uint2(ld2(p + boff), 0u);
+    }
+    // activations: the 32 codes and the scale of this lane's block or group
+    uint4 ya[NC], yb[NC];
+    float dy[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        ya[c] = yb[c] = make_uint4(0, 0, 0, 0);
+        dy[c] = 0.0f;
+        if (c < ncols && valid) {
+            if (WT == WT_IQ4_XS) {
+                const uint8_t *A = act + c * act_row_bytes + (int64_t)(g >> 3) * Q8K_BYTES;
+                dy[c] = __uint_as_float(ld4(A));
+                ya[c] = ld16(A + 4 + 32 * (g & 7));
+                yb[c] = ld16(A + 20 + 32 * (g & 7));
+            } else {
+                const uint8_t *A = act + c * act_row_bytes + (int64_t)g * Q8_0_BYTES;
+                dy[c] = h2f(ld2(A));
+                ya[c] = ld16(A + 2);
+                yb[c] = ld16(A + 18);
+            }
+        }
+    }
+    float part[NC][RB];
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        const uint32_t q[4] = {qv[rr].x, qv[rr].y, qv[rr].z, qv[rr].w};
+        // v[i]: table values of elements 4i .. 4i+3 of the lane's 32
+        uint32_t v[8];
+        if (WT == WT_NVFP4) {
+            // sub-block 2h: qs bytes 0..7, low nibbles elements 0..7, high 8..15;
+            // sub-block 2h+1: bytes 8..15 -> elements 16..23 and 24..31
+            v[0] = lut4(L, q[0]);
+            v[1] = lut4(L, q[1]);
+            v[2] = lut4(L, q[0] >> 4);
+            v[3] = lut4(L, q[1] >> 4);
+            v[4] = lut4(L, q[2]);
+            v[5] = lut4(L, q[3]);
+            v[6] = lut4(L, q[2] >> 4);
+            v[7] = lut4(L, q[3] >> 4);
+        } else {
+            // low nibbles of qs[0..15] are elements 0..15, high nibbles 16..31
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                v[k] = lut4(L, q[k]);
+                v[4 + k] = lut4(L, q[k] >> 4);
+            }
+        }
+        const uint32_t hw = hv[rr].x;
+        int ls = 0;
+        if (WT == WT_IQ4_XS) {
+            // 6-bit scale of group ib: nibble ib of scales_l, bits 2ib.. of scales_h
+            const int ib = g & 7;
+            const uint32_t sl = (hv[rr].y >> (4 * ib)) & 0xFu;
+            const uint32_t sh = ((hw >> 16) >> (2 * ib)) & 3u;
+            ls = (int)(sl | (sh << 4)) - 32;
+        }
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const uint32_t y[8] = {ya[c].x, ya[c].y, ya[c].z, ya[c].w, yb[c].x, yb[c].y, yb[c].z, yb[c].w};
+            float pp = 0.0f;
+            if (WT == WT_NVFP4) {
+                const int s0 = dot4(v[3], y[3], dot4(v[2], y[2], dot4(v[1], y[1], dot4(v[0], y[0], 0))));
+                const int s1 = dot4(v[7], y[7], dot4(v[6], y[6], dot4(v[5], y[5], dot4(v[4], y[4], 0))));
+                if (SUBSUMS && valid && c < ncols && rr < nr) {
+                    int32_t *sp = sub + ((int64_t)c * rows + r0 + rr) * (int64_t)(4 * nb) + 2 * g;
+                    sp[0] = s0;
+                    sp[1] = s1;
+                }
+                pp = (ue4m3(hw) * dy[c]) * (float)s0 + (ue4m3(hw >> 8) * dy[c]) * (float)s1;
+            } else {
+                int s = 0;
+#pragma unroll
+                for (int k = 0; k < 8; k++) s = dot4(v[k], y[k], s);
+                if (WT == WT_IQ4_NL) {
+                    if (SUBSUMS && valid && c < ncols && rr < nr) sub[((int64_t)c * rows + r0 + rr) * nb + g] = s;
+                    pp = (h2f(hw) * dy[c]) * (float)s;
+                } else {
+                    // the super-block's exact sum (its 8 groups sit in 8
+                    // consecutive lanes), scaled once by d * d8 as the
+                    // reference scales each super-block (vec_dot.rs:1665-1696)
+                    int t = ls * s;  // |.| <= 32 * 32 * 127 * 128
+                    t += __shfl_xor(t, 1, 64);
+                    t += __shfl_xor(t, 2, 64);
+                    t += __shfl_xor(t, 4, 64);
+                    if (SUBSUMS && (g & 7) == 0 && valid && c < ncols && rr < nr)
+                        sub[((int64_t)c * rows + r0 + rr) * nb + (g >> 3)] = t;
+                    pp = (g & 7) == 0 ? (h2f(hw) * dy[c]) * (float)t : 0.0f;
+                }
+            }
+            part[c][rr] = valid ? pp : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NC; c++) stash_rows(red, part[c], lane, w, nw, c, NC);
+    finish_rows(red, r0, nr, ncols, NC, nw, dst, ldd);
+}
+
+// weights -> int8 codes [Npad][Kpad] and one f32 scale per 32 elements at
+// dw[b][row], zero past N and K (the operands of ghip_gemm_q8); one thread per
+// (row, 32-group)
+// IQ4_XS: dw holds the group's integer scale ls - 32 and dsb[super-block][row]
+// the block's d (the XS mode of the GEMM sums the groups per super-block)
+template <int WT>
+__device__ __forceinline__ void q8w_repack_lut(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int nb, int Kpad,
+                                               int Npad, int8_t *__restrict__ codes, float *__restrict__ dw,
+                                               float *__restrict__ dsb = nullptr) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int nbp = Kpad / 32;
+    if (i >= (int64_t)Npad * nbp) return;
+    const int row = (int)(i / nbp), g = (int)(i % nbp);
+    const int ng = WT == WT_IQ4_NL ? nb : 8 * nb;
+    uint32_t v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float d = 0.0f;
+    if (row < N && g < ng) {
+        const uint8_t *r = W + (int64_t)row * row_bytes;
+        const uint8_t *qs;
+        if (WT == WT_IQ4_NL) {
+            d = h2f(ld2(r + (int64_t)g * 18));
+            qs = r + (int64_t)g * 18 + 2;
+        } else {
+            const uint8_t *blk = r + (int64_t)(g >> 3) * 136;
+            const int ib = g & 7;
+            const uint32_t sh = ((uint32_t)ld2(blk + 2) >> (2 * ib)) & 3u;
+            const uint32_t sl = ((uint32_t)blk[4 + ib / 2] >> (4 * (ib % 2))) & 0xFu;
+            d = (float)((int)(sl | (sh << 4)) - 32);
+            if (ib == 0) dsb[(int64_t)(g >> 3) * Npad + row] = h2f(ld2(blk));
+            qs = blk + 8 + 16 * ib;
+        }
+        const uint4 q = ld16(qs);
+        const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            v[k] = lut4(kIq4nl, qq[k]);
+            v[4 + k] = lut4(kIq4nl, qq[k] >> 4);
+        }
+    }
+    uint4 *o = reinterpret_cast<uint4 *>(codes + (int64_t)row * Kpad + 32 * g);
+    o[0] = make_uint4(v[0], v[1], v[2], v[3]);
+    o[1] = make_uint4(v[4], v[5], v[6], v[7]);
+    dw[(int64_t)g * Npad + row] = d;
+}
+
+}  // namespace
+
+#define GEMV_LUT_INST(TN, WT, NC)                                                                                \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_##TN##_c##NC(                                    \
+        const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb, const uint8_t *__restrict__ act,   \
+        int64_t act_row_bytes, int ncols, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {     \
+        gemv_lut_impl<WT, NC, false>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub);       \
+    }                                                                                                            \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_##TN##_sub_c##NC(                                \
+        const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb, const uint8_t *__restrict__ act,   \
+        int64_t act_row_bytes, int ncols, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {     \
+        gemv_lut_impl<WT, NC, true>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub);        \
+    }
+GEMV_LUT_INST(iq4_nl, WT_IQ4_NL, 1) GEMV_LUT_INST(iq4_nl, WT_IQ4_NL, 2) GEMV_LUT_INST(iq4_nl, WT_IQ4_NL, 4)
+GEMV_LUT_INST(iq4_nl, WT_IQ4_NL, 8)
+GEMV_LUT_INST(nvfp4, WT_NVFP4, 1) GEMV_LUT_INST(nvfp4, WT_NVFP4, 2) GEMV_LUT_INST(nvfp4, WT_NVFP4, 4)
+GEMV_LUT_INST(nvfp4, WT_NVFP4, 8)
+GEMV_LUT_INST(iq4_xs, WT_IQ4_XS, 1) GEMV_LUT_INST(iq4_xs, WT_IQ4_XS, 2) GEMV_LUT_INST(iq4_xs, WT_IQ4_XS, 4)
+GEMV_LUT_INST(iq4_xs, WT_IQ4_XS, 8)
+
+extern "C" __global__ void __launch_bounds__(256)
+    ghip_gemm_q8w_repack_iq4_nl(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int nb, int Kpad, int Npad,
+                                int8_t *__restrict__ codes, float *__restrict__ dw) {
+    q8w_repack_lut<WT_IQ4_NL>(W, row_bytes, N, nb, Kpad, Npad, codes, dw);
+}
+extern "C" __global__ void __launch_bounds__(256)
+    ghip_gemm_q8w_repack_iq4_xs(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int nb, int Kpad, int Npad,
+                                int8_t *__restrict__ codes, float *__restrict__ dw, float *__restrict__ dsb) {
+    q8w_repack_lut<WT_IQ4_XS>(W, row_bytes, N, nb, Kpad, Npad, codes, dw, dsb);
+}
+
+// f32 rows -> Q8_K (quantize_row_q8_K_ref, quants.rs:615-650, the arithmetic of
+// ghip_quantize_q8_K) in the int8 GEMM's layout: codes [Mpad][Kpad] and the
+// block scale d repeated for each of the super-block's 8 groups at
+// da[g][row]; one wavefront per (row, super-block), padding rows zero
+extern "C" __global__ void __launch_bounds__(256)
+    ghip_gemm_act_q8K_q8(const float *__restrict__ x, int64_t x_stride, int M, int Mpad, int nb, int Kpad,
+                         int8_t *__restrict__ codes, float *__restrict__ da) {
+    const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (task >= (int64_t)Mpad * nb) return;  // whole wavefronts
+    const int row = (int)(task / nb), b = (int)(task % nb);
+    float xs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (row < M) __builtin_memcpy(xs, x + (int64_t)row * x_stride + (int64_t)b * QK_K + 4 * lane, 16);
+    int q[4];
+    float d;
+    q8K_block(xs, lane, false, q, d);
+    const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
+                            ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+    *reinterpret_cast<uint32_t *>(codes + (int64_t)row * Kpad + (int64_t)b * QK_K + 4 * lane) = packed;
+    if (lane < 8) da[(int64_t)(8 * b + lane) * Mpad + row] = d;
+}

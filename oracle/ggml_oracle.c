@@ -797,6 +797,57 @@ static inline int32_t isum_q3_K(const blk_q3_K *x, const blk_q8_K *y) {
     return is;
 }
 
+/* ---- Q1_0, Q2_0 (blocks.rs:14-28) ---- */
+typedef struct { uint16_t d; uint8_t qs[16]; } blk_q1_0;  /* 18 B per 128 */
+typedef struct { uint16_t d; uint8_t qs[16]; } blk_q2_0;  /* 18 B per 64 */
+/* element j of a Q1_0 block: +1 where bit j is set, else -1 (quants.rs:66-78) */
+static inline int q1_0_val(const blk_q1_0 *x, int j) { return ((x->qs[j / 8] >> (j % 8)) & 1) ? 1 : -1; }
+/* element j of a Q2_0 block: 2-bit field j minus 1 (quants.rs:108-120) */
+static inline int q2_0_val(const blk_q2_0 *x, int j) { return (int)((x->qs[j / 4] >> ((j % 4) * 2)) & 3) - 1; }
+
+/* quants.rs:44-63: d = sum |x| / 128 (summed in order), bit = x >= 0 */
+void oracle_quantize_row_q1_0_ref(const float *x, void *vy, int64_t k) {
+    blk_q1_0 *y = (blk_q1_0 *)vy;
+    for (int64_t i = 0; i < k / 128; i++) {
+        float sum_abs = 0.0f;
+        for (int j = 0; j < 128; j++) sum_abs += fabsf(x[i * 128 + j]);
+        const float d = sum_abs / 128.0f;
+        memset(y[i].qs, 0, 16);
+        for (int j = 0; j < 128; j++) y[i].qs[j / 8] |= (uint8_t)((x[i * 128 + j] >= 0.0f) << (j % 8));
+        y[i].d = oracle_fp32_to_fp16(d);
+    }
+}
+/* quants.rs:82-106: d = max |x|, q = clamp(round(x / d) + 1, 0, 3), round half away from zero */
+void oracle_quantize_row_q2_0_ref(const float *x, void *vy, int64_t k) {
+    blk_q2_0 *y = (blk_q2_0 *)vy;
+    for (int64_t i = 0; i < k / 64; i++) {
+        float amax = 0.0f;
+        for (int j = 0; j < 64; j++) {
+            const float a = fabsf(x[i * 64 + j]);
+            if (a > amax) amax = a;
+        }
+        const float d = amax, id = d > 0.0f ? 1.0f / d : 0.0f;
+        memset(y[i].qs, 0, 16);
+        for (int j = 0; j < 64; j++) {
+            int q = (int)roundf(x[i * 64 + j] * id) + 1;
+            q = q < 0 ? 0 : q > 3 ? 3 : q;
+            y[i].qs[j / 4] |= (uint8_t)(q << ((j % 4) * 2));
+        }
+        y[i].d = oracle_fp32_to_fp16(d);
+    }
+}
+/* exact sums per Q8_0 block: group g (32 elements) of the weight row */
+static inline int32_t isum_q1_0(const blk_q1_0 *x, int k, const blk_q8_0 *y) {
+    int32_t s = 0;
+    for (int e = 0; e < 32; e++) s += q1_0_val(x, 32 * k + e) * y->qs[e];
+    return s;
+}
+static inline int32_t isum_q2_0(const blk_q2_0 *x, int k, const blk_q8_0 *y) {
+    int32_t s = 0;
+    for (int e = 0; e < 32; e++) s += q2_0_val(x, 32 * k + e) * y->qs[e];
+    return s;
+}
+
 /* ---- IQ4_NL, IQ4_XS, NVFP4 (blocks.rs:55-62, :234-249) ---- */
 typedef struct { uint16_t d; uint8_t qs[16]; } blk_iq4_nl;                               /* 18 B  */
 typedef struct { uint16_t d, scales_h; uint8_t scales_l[4]; uint8_t qs[128]; } blk_iq4_xs; /* 136 B */
@@ -856,6 +907,22 @@ static inline int32_t isum_iq4_xs(const blk_iq4_xs *x, const blk_q8_K *y) {
 }
 
 void oracle_dequantize_row(int type, const void *vx, float *y, int64_t k) {
+    if (type == OR_Q1_0) { /* quants.rs:66-78 */
+        const blk_q1_0 *x = (const blk_q1_0 *)vx;
+        for (int64_t i = 0; i < k / 128; i++) {
+            const float d = H2F(x[i].d), neg = -d;
+            for (int j = 0; j < 128; j++) y[i * 128 + j] = q1_0_val(&x[i], j) > 0 ? d : neg;
+        }
+        return;
+    }
+    if (type == OR_Q2_0) { /* quants.rs:108-120 */
+        const blk_q2_0 *x = (const blk_q2_0 *)vx;
+        for (int64_t i = 0; i < k / 64; i++) {
+            const float d = H2F(x[i].d);
+            for (int j = 0; j < 64; j++) y[i * 64 + j] = (float)q2_0_val(&x[i], j) * d;
+        }
+        return;
+    }
     if (type == OR_IQ4_NL) { /* quants_k.rs:2379-2390 */
         const blk_iq4_nl *x = (const blk_iq4_nl *)vx;
         for (int64_t i = 0; i < k / 32; i++) {
@@ -1437,6 +1504,56 @@ float oracle_vec_dot_nvfp4_q8_0(int n, const void *vx, const void *vy) {
     return hsum8(acc);
 }
 
+/* vec_dot.rs:1074-1116 vec_dot_q1_0_q8_0: per 128-block, per Q8_0 block k the
+ * 8 lane sums of +-q8 (lane l = elements 4l..4l+3); acc_block = dy0 * s (k = 0,
+ * a plain product), then fma(dy_k, s, acc_block); acc = fma(d, acc_block, acc) */
+float oracle_vec_dot_q1_0_q8_0(int n, const void *vx, const void *vy) {
+    const blk_q1_0 *x = (const blk_q1_0 *)vx;
+    const blk_q8_0 *y = (const blk_q8_0 *)vy;
+    float acc[8] = {0};
+    for (int ib = 0; ib < n / 128; ib++) {
+        const float d0 = H2F(x[ib].d);
+        float ab[8] = {0};
+        for (int k = 0; k < 4; k++) {
+            const blk_q8_0 *yk = &y[ib * 4 + k];
+            const float dy = H2F(yk->d);
+            for (int l = 0; l < 8; l++) {
+                int32_t s = 0;
+                for (int i = 0; i < 4; i++) s += q1_0_val(&x[ib], 32 * k + 4 * l + i) * yk->qs[4 * l + i];
+                ab[l] = k == 0 ? dy * (float)s : fmaf(dy, (float)s, ab[l]);
+            }
+        }
+        for (int l = 0; l < 8; l++) acc[l] = fmaf(d0, ab[l], acc[l]);
+    }
+    return hsum8(acc);
+}
+
+/* vec_dot.rs:1120-1148 vec_dot_q2_0_q8_0 (the generic kernel): per 64-block
+ * sumi = sum_k dy_k * sumi_block_k (in order), sumf += d * sumi */
+float oracle_vec_dot_q2_0_q8_0(int n, const void *vx, const void *vy) {
+    const blk_q2_0 *x = (const blk_q2_0 *)vx;
+    const blk_q8_0 *y = (const blk_q8_0 *)vy;
+    float sumf = 0.0f;
+    for (int i = 0; i < n / 64; i++) {
+        const float d0 = H2F(x[i].d);
+        float sumi = 0.0f;
+        for (int k = 0; k < 2; k++) {
+            const blk_q8_0 *yk = &y[i * 2 + k];
+            int32_t sb = 0;
+            for (int b = 0; b < 8; b++) {
+                const uint8_t byte = x[i].qs[8 * k + b];
+                sb += ((byte & 3) - 1) * yk->qs[4 * b];
+                sb += (((byte >> 2) & 3) - 1) * yk->qs[4 * b + 1];
+                sb += (((byte >> 4) & 3) - 1) * yk->qs[4 * b + 2];
+                sb += (((byte >> 6) & 3) - 1) * yk->qs[4 * b + 3];
+            }
+            sumi += H2F(yk->d) * (float)sb;
+        }
+        sumf += d0 * sumi;
+    }
+    return sumf;
+}
+
 static int omp_threads(int nthreads) {
 #ifdef _OPENMP
     return nthreads > 0 ? nthreads : omp_get_max_threads();
@@ -1458,7 +1575,8 @@ static int route_of(int type, int64_t rows, int64_t cols) {
 
 /* vec_dot_type Q8_0 (vec_dot.rs:1727) */
 static int q8_0_dot(int type) {
-    return type == OR_Q4_0 || type == OR_Q5_0 || type == OR_Q8_0 || type == OR_IQ4_NL || type == OR_NVFP4;
+    return type == OR_Q4_0 || type == OR_Q5_0 || type == OR_Q8_0 || type == OR_IQ4_NL || type == OR_NVFP4 ||
+           type == OR_Q1_0 || type == OR_Q2_0;
 }
 static size_t act_row_size(int type, int64_t n) {
     if (type == OR_Q4_1 || type == OR_Q5_1) return (size_t)(n / 32) * sizeof(blk_q8_1);
@@ -1492,7 +1610,7 @@ int oracle_mul_mat(int type, const void *w, int64_t n, int64_t rows, const float
     if (route < 0) return -1;
     if (type != OR_Q4_0 && type != OR_Q4_K && type != OR_Q6_K && type != OR_Q5_0 && type != OR_Q8_0 &&
         type != OR_Q5_K && type != OR_Q4_1 && type != OR_Q5_1 && type != OR_Q2_K && type != OR_Q3_K &&
-        type != OR_IQ4_NL && type != OR_IQ4_XS && type != OR_NVFP4)
+        type != OR_IQ4_NL && type != OR_IQ4_XS && type != OR_NVFP4 && type != OR_Q1_0 && type != OR_Q2_0)
         return -2;
     const size_t rs = act_row_size(type, n);
     uint8_t *act = (uint8_t *)malloc(rs * (size_t)cols);
@@ -1704,6 +1822,25 @@ int oracle_mul_mat(int type, const void *w, int64_t n, int64_t rows, const float
                 }
                 out[c * rows + r] = type == OR_IQ4_NL ? oracle_vec_dot_iq4_nl_q8_0((int)n, wr, a)
                                                       : oracle_vec_dot_nvfp4_q8_0((int)n, wr, a);
+            }
+        }
+    } else if (type == OR_Q1_0 || type == OR_Q2_0) {
+        /* the row vec_dot; sub-sums per 32-element group (one Q8_0 block) */
+        const int qk = type == OR_Q1_0 ? 128 : 64, gpb = qk / 32;
+        const int64_t nbw = n / qk;
+#pragma omp parallel for num_threads(nth) schedule(static)
+        for (int64_t r = 0; r < rows; r++) {
+            const uint8_t *wr = (const uint8_t *)w + (size_t)r * nbw * 18;
+            for (int64_t c = 0; c < cols; c++) {
+                const blk_q8_0 *a = (const blk_q8_0 *)(act + (size_t)c * rs);
+                if (subsums)
+                    for (int64_t b = 0; b < nbw; b++)
+                        for (int k = 0; k < gpb; k++)
+                            subsums[(((size_t)c * rows + r) * nbw + b) * gpb + k] =
+                                type == OR_Q1_0 ? isum_q1_0((const blk_q1_0 *)wr + b, k, &a[b * gpb + k])
+                                                : isum_q2_0((const blk_q2_0 *)wr + b, k, &a[b * gpb + k]);
+                out[c * rows + r] = type == OR_Q1_0 ? oracle_vec_dot_q1_0_q8_0((int)n, wr, a)
+                                                    : oracle_vec_dot_q2_0_q8_0((int)n, wr, a);
             }
         }
     } else if (type == OR_IQ4_XS) {

@@ -24,7 +24,8 @@ extern "C" {
 enum {
     OR_F32 = 0, OR_F16 = 1, OR_Q4_0 = 2, OR_Q4_1 = 3, OR_Q5_0 = 6, OR_Q5_1 = 7, OR_Q8_0 = 8, OR_Q8_1 = 9,
     OR_Q2_K = 10, OR_Q3_K = 11, OR_Q4_K = 12,
-    OR_Q5_K = 13, OR_Q6_K = 14, OR_Q8_K = 15, OR_IQ4_NL = 20, OR_IQ4_XS = 23, OR_MXFP4 = 39, OR_NVFP4 = 40
+    OR_Q5_K = 13, OR_Q6_K = 14, OR_Q8_K = 15, OR_IQ4_NL = 20, OR_IQ4_XS = 23, OR_MXFP4 = 39, OR_NVFP4 = 40,
+    OR_Q1_0 = 41, OR_Q2_0 = 42
 };
 
 /* ---- scalar helpers ---- */
@@ -45,6 +46,8 @@ void oracle_quantize_row_q8_1(const float *x, void *y, int64_t k);      /* quant
 void oracle_quantize_row_q5_K_ref(const float *x, void *y, int64_t k);  /* quants_k.rs:1952; quants_ref.bin */
 void oracle_quantize_row_mxfp4_ref(const float *x, void *y, int64_t k); /* absent in the reference; quants_ref_fp4.bin */
 void oracle_quantize_row_q8_0_ref(const float *x, void *y, int64_t k);  /* quants.rs:302; quants_ref.bin */
+void oracle_quantize_row_q1_0_ref(const float *x, void *y, int64_t k);  /* quants.rs:44; quants_ref_q1q2.bin type 41 */
+void oracle_quantize_row_q2_0_ref(const float *x, void *y, int64_t k);  /* quants.rs:82; quants_ref_q1q2.bin type 42 */
 
 /* ---- activation quantizers ---- */
 void oracle_quantize_row_q8_0(const float *x, void *y, int64_t k);      /* quants.rs:331; q4_0_repack_ref.bin */
@@ -69,6 +72,8 @@ float oracle_vec_dot_q5_K_q8_K(int n, const void *x, const void *y);  /* vec_dot
 float oracle_vec_dot_iq4_nl_q8_0(int n, const void *x, const void *y); /* vec_dot.rs:1597; vecdot3_ref.bin type 20 */
 float oracle_vec_dot_iq4_xs_q8_K(int n, const void *x, const void *y); /* vec_dot.rs:1655; vecdot3_ref.bin type 23 */
 float oracle_vec_dot_nvfp4_q8_0(int n, const void *x, const void *y);  /* vec_dot.rs:1154; vecdot3_ref.bin type 40 */
+float oracle_vec_dot_q1_0_q8_0(int n, const void *x, const void *y);   /* vec_dot.rs:1074; vecdot3_ref.bin type 41 */
+float oracle_vec_dot_q2_0_q8_0(int n, const void *x, const void *y);   /* vec_dot.rs:1120; vecdot3_ref.bin type 42 */
 
 /*
  * The reference's MUL_MAT routing for a 2-D quantized weight W [rows x n]

@@ -29,7 +29,7 @@ WHOLE = [
     # IQ4_NL / IQ4_XS quantizer and dequantizer outputs, and the x86 vec_dot
     # results of NVFP4 / IQ4_NL / IQ4_XS (and the other types of that dump)
     # on LCG block bytes and runtime-quantized activations
-    "quants_ref_iq.bin", "vecdot3_ref.bin",
+    "quants_ref_iq.bin", "vecdot3_ref.bin", "quants_ref_q1q2.bin",
 ]
 ROW_BYTES_PER_256 = {10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 23: 136}
 

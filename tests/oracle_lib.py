@@ -17,17 +17,19 @@ F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, MXFP4 = 0, 1, 2, 6, 8, 12, 1
 Q4_1, Q5_1, Q8_1 = 3, 7, 9
 Q2_K, Q3_K = 10, 11
 IQ4_NL, IQ4_XS, NVFP4 = 20, 23, 40
+Q1_0, Q2_0 = 41, 42
 BLOCK = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176),
          Q6_K: (256, 210), Q8_K: (256, 292), MXFP4: (32, 17), Q4_1: (32, 20), Q5_1: (32, 24), Q8_1: (32, 36),
-         Q2_K: (256, 84), Q3_K: (256, 110), IQ4_NL: (32, 18), IQ4_XS: (256, 136), NVFP4: (64, 36)}
+         Q2_K: (256, 84), Q3_K: (256, 110), IQ4_NL: (32, 18), IQ4_XS: (256, 136), NVFP4: (64, 36),
+         Q1_0: (128, 18), Q2_0: (64, 18)}
 # weight type -> activation type of its dot (vec_dot_type)
 ACT_TYPE = {Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K, Q4_1: Q8_1, Q5_1: Q8_1,
-            Q2_K: Q8_K, Q3_K: Q8_K, IQ4_NL: Q8_0, IQ4_XS: Q8_K, NVFP4: Q8_0}
+            Q2_K: Q8_K, Q3_K: Q8_K, IQ4_NL: Q8_0, IQ4_XS: Q8_K, NVFP4: Q8_0, Q1_0: Q8_0, Q2_0: Q8_0}
 # int32 sub-sums per weight row and activation row (ghip_mul_mat_subsums layout)
 def subsums_per_row(ty, n):
     return {Q4_0: n // 32, Q5_0: n // 32, Q8_0: n // 32, Q4_K: (n // 256) * 2, Q5_K: (n // 256) * 2,
             Q6_K: n // 256, Q4_1: n // 32, Q5_1: n // 32, Q2_K: (n // 256) * 2, Q3_K: n // 256,
-            IQ4_NL: n // 32, IQ4_XS: n // 256, NVFP4: n // 16}[ty]
+            IQ4_NL: n // 32, IQ4_XS: n // 256, NVFP4: n // 16, Q1_0: n // 32, Q2_0: n // 32}[ty]
 ROUTE_REPACK, ROUTE_TILED, ROUTE_VECDOT = 1, 2, 3
 
 
@@ -76,7 +78,8 @@ def lib():
                   "quantize_row_q5_0_ref", "quantize_row_q5_K_ref",
                   "quantize_row_mxfp4_ref", "quantize_row_q8_0_ref", "quantize_row_q8_0",
                   "quantize_row_q8_K_ref", "quantize_row_q8_K_mat",
-                  "quantize_row_q4_1_ref", "quantize_row_q5_1_ref", "quantize_row_q8_1"]:
+                  "quantize_row_q4_1_ref", "quantize_row_q5_1_ref", "quantize_row_q8_1",
+                  "quantize_row_q1_0_ref", "quantize_row_q2_0_ref"]:
             fn = getattr(L, "oracle_" + f)
             fn.restype = None
             fn.argtypes = [vp, vp, i64]
@@ -85,7 +88,7 @@ def lib():
         for f in ["vec_dot_q4_0_q8_0", "vec_dot_q4_K_q8_K", "vec_dot_q6_K_q8_K", "vec_dot_q5_0_q8_0",
                   "vec_dot_q8_0_q8_0", "vec_dot_q5_K_q8_K", "vec_dot_q4_1_q8_1", "vec_dot_q5_1_q8_1",
                   "vec_dot_q2_K_q8_K", "vec_dot_q3_K_q8_K", "vec_dot_iq4_nl_q8_0", "vec_dot_iq4_xs_q8_K",
-                  "vec_dot_nvfp4_q8_0"]:
+                  "vec_dot_nvfp4_q8_0", "vec_dot_q1_0_q8_0", "vec_dot_q2_0_q8_0"]:
             fn = getattr(L, "oracle_" + f)
             fn.restype = C.c_float
             fn.argtypes = [C.c_int, vp, vp]
@@ -109,7 +112,8 @@ def _p(a):
 _QUANT = {Q4_0: "quantize_row_q4_0_ref", Q4_K: "quantize_row_q4_K_ref",
           Q6_K: "quantize_row_q6_K_ref", MXFP4: "quantize_row_mxfp4_ref",
           Q5_0: "quantize_row_q5_0_ref", Q5_K: "quantize_row_q5_K_ref", Q8_0: "quantize_row_q8_0_ref",
-          Q4_1: "quantize_row_q4_1_ref", Q5_1: "quantize_row_q5_1_ref", Q8_1: "quantize_row_q8_1"}
+          Q4_1: "quantize_row_q4_1_ref", Q5_1: "quantize_row_q5_1_ref", Q8_1: "quantize_row_q8_1",
+          Q1_0: "quantize_row_q1_0_ref", Q2_0: "quantize_row_q2_0_ref"}
 
 
 def quantize(ty, x, kind=None):

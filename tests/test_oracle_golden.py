@@ -663,3 +663,25 @@ def test_tiled_k23_iq4xs_bit_exact():
         assert route == want_route
         if route == O.ROUTE_TILED:
             assert np.array_equal(got.view(np.uint32), dst.reshape(cols, rows).view(np.uint32)), (tid, rows, cols)
+
+
+@pytest.mark.parametrize("ty,name", [(O.Q1_0, "vec_dot_q1_0_q8_0"), (O.Q2_0, "vec_dot_q2_0_q8_0")])
+def test_q1_q2_vecdot_bit_exact(ty, name):
+    """vecdot3_ref.bin types 41 / 42 (vec_dot.rs:1074, :1120): bit for bit."""
+    (sec,) = [s for s in fx.vecdot3_sections() if s[0] == ty]
+    _, n, xq, yq, want = sec
+    got = np.float32(getattr(O.lib(), "oracle_" + name)(n, O._p(xq), O._p(yq)))
+    assert got.view(np.uint32) == want.view(np.uint32), (got, want)
+
+
+@pytest.mark.parametrize("ty", [O.Q1_0, O.Q2_0])
+def test_q1_q2_quantizer_and_dequant_bit_exact(ty):
+    """quants.rs q1_0 / q2_0 parity (parity/ref_quants_dump.c,
+    quants_ref_q1q2.bin): the quantizers' bytes and the dequantized floats."""
+    secs = [s for s in fx.quant_sections("quants_ref_q1q2.bin") if s[1] == ty]
+    assert secs
+    for magic, tid, n, q, deq in secs:
+        x = fx.ref_input(n)
+        assert np.array_equal(O.quantize(ty, x), q)
+        got = O.dequantize(ty, q, n)
+        assert np.array_equal(got.view(np.uint32), deq.view(np.uint32))

@@ -70,6 +70,8 @@ enum {
     GHIP_TYPE_I32 = 26,
     GHIP_TYPE_MXFP4 = 39,
     GHIP_TYPE_NVFP4 = 40,
+    GHIP_TYPE_Q1_0 = 41,
+    GHIP_TYPE_Q2_0 = 42,
 };
 
 /* The ops of the hot path (GgmlOp::MulMat / MulMatId / FlashAttnExt,
@@ -117,9 +119,9 @@ int ghip_supports_op(int op, const ghip_tensor *dst, const ghip_tensor *const *s
 
 /* dst = src0 x src1 (GGML_OP_MUL_MAT, forward_mul_mat compute.rs:1420-1839).
  * src0: Q4_0 | Q4_1 | Q5_0 | Q5_1 | Q8_0 | Q2_K | Q3_K | Q4_K | Q5_K | Q6_K |
- *       IQ4_NL | IQ4_XS | NVFP4 weight [ne00=K, ne01=N, ne02, ne03], rows contiguous;
+ *       IQ4_NL | IQ4_XS | NVFP4 | Q1_0 | Q2_0 weight [ne00=K, ne01=N, ne02, ne03], rows contiguous;
  * src1: F32 [K, ne11, ne12, ne13] (any strides nb11..nb13, nb10 == 4), or
- *       already the vec_dot type of src0 (Q8_0 for Q4_0/Q5_0/Q8_0/IQ4_NL/NVFP4,
+ *       already the vec_dot type of src0 (Q8_0 for Q4_0/Q5_0/Q8_0/IQ4_NL/NVFP4/Q1_0/Q2_0,
  *       Q8_1 for Q4_1/Q5_1, Q8_K for the K-quants and IQ4_XS; rows of blocks),
  *       which skips the quantization (backend.rs:2057-2066 semantics);
  * dst:  F32 [N, ne11, ne12, ne13] (nb0 == 4).
@@ -160,6 +162,7 @@ ghip_status ghip_mul_mat_noalloc(ghip_context *ctx, const ghip_tensor *src0, con
  *   IQ4_NL: P = nb, sum kvalue*q8 of 32-block b
  *   NVFP4: P = 4*nb, sum kvalue*q8 of each 16-element sub-block of 64-block b
  *   IQ4_XS: P = nb, sum_g (ls_g - 32) * sum kvalue*q8 of super-block b
+ *   Q1_0: P = 4*nb, Q2_0: P = 2*nb, sum value*q8 of each 32-element group
  * subsums is a device pointer of ne11*N*P int32. */
 ghip_status ghip_mul_mat_subsums(ghip_context *ctx, const ghip_tensor *src0, const ghip_tensor *src1,
                                  int32_t *subsums, void *stream);

@@ -48,6 +48,8 @@ TypeInfo type_info(int t) {
     case GHIP_TYPE_IQ4_NL: return {32, 18};
     case GHIP_TYPE_IQ4_XS: return {256, 136};
     case GHIP_TYPE_NVFP4: return {64, 36};
+    case GHIP_TYPE_Q1_0: return {128, 18};
+    case GHIP_TYPE_Q2_0: return {64, 18};
     default: return {0, 0};
     }
 }
@@ -250,17 +252,18 @@ bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b,
         a->type != GHIP_TYPE_Q4_K && a->type != GHIP_TYPE_Q5_K && a->type != GHIP_TYPE_Q6_K &&
         a->type != GHIP_TYPE_Q4_1 && a->type != GHIP_TYPE_Q5_1 && a->type != GHIP_TYPE_Q2_K &&
         a->type != GHIP_TYPE_Q3_K && a->type != GHIP_TYPE_IQ4_NL && a->type != GHIP_TYPE_IQ4_XS &&
-        a->type != GHIP_TYPE_NVFP4) {
+        a->type != GHIP_TYPE_NVFP4 && a->type != GHIP_TYPE_Q1_0 && a->type != GHIP_TYPE_Q2_0) {
         st = ctx->fail(st,
                        "mul_mat: src0 type %d not supported (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, "
-                       "IQ4_NL, IQ4_XS, NVFP4)",
+                       "IQ4_NL, IQ4_XS, NVFP4, Q1_0, Q2_0)",
                        a->type);
         return false;
     }
     const TypeInfo ti = type_info(a->type);
     // vec_dot_type Q8_0 (vec_dot.rs:1727): Q4_0, Q5_0, Q8_0, NVFP4, IQ4_NL
     const bool q8_0_dot = a->type == GHIP_TYPE_Q4_0 || a->type == GHIP_TYPE_Q5_0 || a->type == GHIP_TYPE_Q8_0 ||
-                          a->type == GHIP_TYPE_IQ4_NL || a->type == GHIP_TYPE_NVFP4;
+                          a->type == GHIP_TYPE_IQ4_NL || a->type == GHIP_TYPE_NVFP4 || a->type == GHIP_TYPE_Q1_0 ||
+                          a->type == GHIP_TYPE_Q2_0;
     const bool q8_1_dot = a->type == GHIP_TYPE_Q4_1 || a->type == GHIP_TYPE_Q5_1;
     // vec_dot_type (vec_dot.rs vec_dot_type)
     const int vdt = q8_0_dot ? GHIP_TYPE_Q8_0 : q8_1_dot ? GHIP_TYPE_Q8_1 : GHIP_TYPE_Q8_K;
@@ -347,6 +350,8 @@ const char *gemv_base(int wtype) {
     case GHIP_TYPE_IQ4_NL: return "ghip_gemv_iq4_nl";
     case GHIP_TYPE_IQ4_XS: return "ghip_gemv_iq4_xs";
     case GHIP_TYPE_NVFP4: return "ghip_gemv_nvfp4";
+    case GHIP_TYPE_Q1_0: return "ghip_gemv_q1_0";
+    case GHIP_TYPE_Q2_0: return "ghip_gemv_q2_0";
     default: return "ghip_gemv_q4_0";
     }
 }
@@ -358,20 +363,22 @@ bool k23_type(int wtype) { return wtype == GHIP_TYPE_Q2_K || wtype == GHIP_TYPE_
 bool gemv_pair(int wtype) {
     return wtype == GHIP_TYPE_Q4_0 || wtype == GHIP_TYPE_Q5_0 || wtype == GHIP_TYPE_Q8_0;
 }
-// table-lookup 4-bit types (ghip_iq.hip): one decode lane per 32 elements
+// table-lookup 4-bit and 1-/2-bit code types (ghip_iq.hip): one decode lane per 32 elements
 bool lut_type(int wtype) {
-    return wtype == GHIP_TYPE_IQ4_NL || wtype == GHIP_TYPE_IQ4_XS || wtype == GHIP_TYPE_NVFP4;
+    return wtype == GHIP_TYPE_IQ4_NL || wtype == GHIP_TYPE_IQ4_XS || wtype == GHIP_TYPE_NVFP4 ||
+           wtype == GHIP_TYPE_Q1_0 || wtype == GHIP_TYPE_Q2_0;
 }
 // weights the int8-MFMA GEMM ghip_gemm_q8 takes as int8 codes with one scale
 // per 32 elements (NVFP4's scales are per 16: its prefill runs the decode
 // kernel in groups of 8 columns)
 bool gemm_q8_family(int wtype) {
-    return gemv_pair(wtype) || wtype == GHIP_TYPE_IQ4_NL || wtype == GHIP_TYPE_IQ4_XS;
+    return gemv_pair(wtype) || wtype == GHIP_TYPE_IQ4_NL || wtype == GHIP_TYPE_IQ4_XS || wtype == GHIP_TYPE_Q1_0 ||
+           wtype == GHIP_TYPE_Q2_0;
 }
 // int32 sub-sums per weight block (ghip_mul_mat_subsums layout)
 int64_t subsums_per_block(int wtype) {
     if (wtype == GHIP_TYPE_Q4_K || wtype == GHIP_TYPE_Q5_K || wtype == GHIP_TYPE_Q2_K) return 2;
-    return wtype == GHIP_TYPE_NVFP4 ? 4 : 1;
+    return wtype == GHIP_TYPE_NVFP4 || wtype == GHIP_TYPE_Q1_0 ? 4 : wtype == GHIP_TYPE_Q2_0 ? 2 : 1;
 }
 
 // The whole-row decode kernels with the activation image in LDS: Q4_K and
@@ -790,6 +797,8 @@ const char *q8w_repack_name(int wtype) {
     case GHIP_TYPE_Q5_0: return "ghip_gemm_q8w_repack_q5_0";
     case GHIP_TYPE_IQ4_NL: return "ghip_gemm_q8w_repack_iq4_nl";
     case GHIP_TYPE_IQ4_XS: return "ghip_gemm_q8w_repack_iq4_xs";
+    case GHIP_TYPE_Q1_0: return "ghip_gemm_q8w_repack_q1_0";
+    case GHIP_TYPE_Q2_0: return "ghip_gemm_q8w_repack_q2_0";
     default: return "ghip_gemm_q8w_repack_q8_0";
     }
 }
@@ -827,17 +836,17 @@ ghip_status run_gemm_q8(ghip_context *ctx, const MulMatPlan &p, const void *w, c
         dw = d;
     }
     const int64_t ablocks = L.Mpad * L.nbp;
+    const int nb32 = (int)(p.K / 32);  // the GEMM's blocks are 32 elements (Q8_0 activation blocks)
     if (p.wtype == GHIP_TYPE_IQ4_XS)  // Q8_K activations: codes and the block scale per 32-group
         st = ctx->launch("ghip_gemm_act_q8K_q8", dim3((unsigned)((L.Mpad * p.nb + 3) / 4)), dim3(256), 0, s,
                          (const float *)bf->data, (int64_t)bf->nb[1] / 4, (int)p.M, (int)L.Mpad, (int)p.nb,
                          (int)L.Kpad, ac, da);
     else
         st = ctx->launch("ghip_gemm_act_q8_0", dim3((unsigned)((ablocks * 8 + 255) / 256)), dim3(256), 0, s,
-                         (const float *)bf->data, (int64_t)bf->nb[1] / 4, (int)p.M, (int)L.Mpad, (int)p.nb,
+                         (const float *)bf->data, (int64_t)bf->nb[1] / 4, (int)p.M, (int)L.Mpad, nb32,
                          (int)L.Kpad, ac, da);
     if (st != GHIP_STATUS_SUCCESS) return st;
     const unsigned grid = (unsigned)(((p.M + 63) / 64) * ((p.N + 127) / 128));
-    const int nb32 = (int)(p.K / 32);  // the GEMM's blocks are 32 elements
     if (p.wtype == GHIP_TYPE_IQ4_XS)
         return ctx->launch(sub ? "ghip_gemm_q8_xs_sub" : "ghip_gemm_q8_xs", dim3(grid), dim3(256), kGemmSmemQ8, s, wc,
                            dw, (int)p.N, (int)L.Npad, nb32, (int)L.Kpad, (const int8_t *)ac, (const float *)da,
@@ -1811,7 +1820,7 @@ ghip_status ghip_weight_register(ghip_context *ctx, const ghip_tensor *w, void *
     const bool q6k = w->type == GHIP_TYPE_Q6_K, mx = w->type == GHIP_TYPE_MXFP4, q8 = gemm_q8_family(w->type);
     if ((q6k || q8) && w->ne[2] != 1)
         return ctx->fail(GHIP_STATUS_BACKEND_ERROR,
-                         "weight_register: Q6_K / Q4_0 / Q5_0 / Q8_0 / IQ4_NL / IQ4_XS weights are 2-D");
+                         "weight_register: Q6_K / Q4_0 / Q5_0 / Q8_0 / IQ4_NL / IQ4_XS / Q1_0 / Q2_0 weights are 2-D");
     // every other type is read in its GGUF layout: nothing to build
     if (!(q6k || mx || q8) || !repack_enabled()) return GHIP_STATUS_SUCCESS;
     size_t bytes;

@@ -2,7 +2,10 @@
 //   IQ4_NL  18 B / 32  {f16 d; u8 qs[16]}                 x Q8_0 (vec_dot.rs:1597)
 //   IQ4_XS  136 B / 256 {f16 d; u16 scales_h; u8 scales_l[4]; u8 qs[128]} x Q8_K (vec_dot.rs:1655)
 //   NVFP4   36 B / 64  {u8 d[4] (UE4M3 per 16); u8 qs[32]} x Q8_0 (vec_dot.rs:1154)
-// (block layouts blocks.rs:55-62, :234-249).  A nibble is an index into a
+// and the 1- and 2-bit codes of the same family of kernels:
+//   Q1_0    18 B / 128 {f16 d; u8 qs[16]} sign bits, +-d   x Q8_0 (vec_dot.rs:1074)
+//   Q2_0    18 B / 64  {f16 d; u8 qs[16]} (q - 1) * d      x Q8_0 (vec_dot.rs:1120)
+// (block layouts blocks.rs:14-28, :55-62, :234-249).  A nibble is an index into a
 // 16-entry int8 table: KVALUES_IQ4NL (quants_k.rs:647) or the E2M1 values
 // doubled, KVALUES_MXFP4 (quants.rs:660).
 //
@@ -26,7 +29,7 @@
 namespace {
 
 constexpr int RB = 8;  // weight rows per decode workgroup
-constexpr int WT_IQ4_NL = 20, WT_IQ4_XS = 23, WT_NVFP4 = 40;
+constexpr int WT_IQ4_NL = 20, WT_IQ4_XS = 23, WT_NVFP4 = 40, WT_Q1_0 = 41, WT_Q2_0 = 42;
 
 // 16-entry int8 tables as four little-endian dwords (entries 4i .. 4i+3 in T[i])
 struct Lut {
@@ -73,17 +76,19 @@ DEV void finish_rows(const float *red, int r0, int nrows, int ncols, int NC, int
     }
 }
 
-// nb: weight blocks per row (K / 32, K / 256 or K / 64).  Sub-sums (the
-// ghip_mul_mat_subsums layout): IQ4_NL the exact dot per 32-block; NVFP4 per
-// 16-element sub-block (4 per block); IQ4_XS sum (ls - 32) * dot per
-// super-block.
+// nb: weight blocks per row (K / 32, K / 256, K / 64 or K / 128).  Sub-sums
+// (the ghip_mul_mat_subsums layout): IQ4_NL, Q1_0 and Q2_0 the exact dot per
+// 32-element group (one Q8_0 block); NVFP4 per 16-element sub-block (4 per
+// block); IQ4_XS sum (ls - 32) * dot per super-block.
 template <int WT, int NC, bool SUBSUMS>
 __device__ __forceinline__ void gemv_lut_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb,
                                               const uint8_t *__restrict__ act, int64_t act_row_bytes, int ncols,
                                               float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
     __shared__ float red[RB * 8 * NC];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    const int ng = WT == WT_IQ4_NL ? nb : WT == WT_NVFP4 ? 2 * nb : 8 * nb;  // 32-element groups per row
+    // 32-element groups per row
+    const int ng = WT == WT_IQ4_NL ? nb : WT == WT_NVFP4 || WT == WT_Q2_0 ? 2 * nb : WT == WT_Q1_0 ? 4 * nb : 8 * nb;
+    constexpr bool BITS = WT == WT_Q1_0 || WT == WT_Q2_0;  // 1- and 2-bit codes, no table
     const int g = 64 * w + lane;
     const bool valid = g < ng;
     const int gc = valid ? g : ng - 1;  // loads of invalid lanes re-read a valid group
@@ -101,6 +106,12 @@ __device__ __forceinline__ void gemv_lut_impl(const uint8_t *__restrict__ W, int
     } else if (WT == WT_NVFP4) {
         boff = (uint32_t)(gc >> 1) * 36u + 2u * (uint32_t)(gc & 1);
         qoff = (uint32_t)(gc >> 1) * 36u + 4u + 16u * (uint32_t)(gc & 1);
+    } else if (WT == WT_Q1_0) {  // 4 bytes of sign bits per group
+        boff = (uint32_t)(gc >> 2) * 18u;
+        qoff = boff + 2u + 4u * (uint32_t)(gc & 3);
+    } else if (WT == WT_Q2_0) {  // 8 bytes of 2-bit codes per group
+        boff = (uint32_t)(gc >> 1) * 18u;
+        qoff = boff + 2u + 8u * (uint32_t)(gc & 1);
     } else {
         boff = (uint32_t)(gc >> 3) * 136u;
         qoff = boff + 8u + 16u * (uint32_t)(gc & 7);
@@ -110,13 +121,19 @@ __device__ __forceinline__ void gemv_lut_impl(const uint8_t *__restrict__ W, int
 #pragma unroll
     for (int rr = 0; rr < RB; rr++) {
         const uint8_t *p = W + (int64_t)min(r0 + rr, rows - 1) * w_row_bytes;
-        qv[rr] = ld16(p + qoff);
+        // (exact-size loads: a group's bytes may end the matrix)
+        if (WT == WT_Q1_0) qv[rr] = make_uint4(ld4(p + qoff), 0u, 0u, 0u);
+        else if (WT == WT_Q2_0) {
+            const uint2 t = ld8(p + qoff);
+            qv[rr] = make_uint4(t.x, t.y, 0u, 0u);
+        } else qv[rr] = ld16(p + qoff);
         if (WT == WT_IQ4_XS) hv[rr] = ld8(p + boff);
         else hv[rr] = make_uint2(ld2(p + boff), 0u);
     }
     // activations: the 32 codes and the scale of this lane's block or group
     uint4 ya[NC], yb[NC];
     float dy[NC];
+    int ysum[NC];  // Q1_0 / Q2_0: sum of the block's 32 codes
 #pragma unroll
     for (int c = 0; c < NC; c++) {
         ya[c] = yb[c] = make_uint4(0, 0, 0, 0);
@@ -134,6 +151,12 @@ __device__ __forceinline__ void gemv_lut_impl(const uint8_t *__restrict__ W, int
                 yb[c] = ld16(A + 18);
             }
         }
+        ysum[c] = 0;
+        if (BITS) {
+            const uint32_t y[8] = {ya[c].x, ya[c].y, ya[c].z, ya[c].w, yb[c].x, yb[c].y, yb[c].z, yb[c].w};
+#pragma unroll
+            for (int k = 0; k < 8; k++) ysum[c] = dot4(y[k], 0x01010101u, ysum[c]);
+        }
     }
     float part[NC][RB];
 #pragma unroll
@@ -141,7 +164,21 @@ __device__ __forceinline__ void gemv_lut_impl(const uint8_t *__restrict__ W, int
         const uint32_t q[4] = {qv[rr].x, qv[rr].y, qv[rr].z, qv[rr].w};
         // v[i]: table values of elements 4i .. 4i+3 of the lane's 32
         uint32_t v[8];
-        if (WT == WT_NVFP4) {
+        if (WT == WT_Q1_0) {
+            // bit e of the group's dword is element e: bits 4k..4k+3 spread to
+            // the four bytes as 0 / 1 (the value is 2 * bit - 1)
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = __umul24((q[0] >> (4 * k)) & 0xFu, 0x00204081u) & 0x01010101u;
+        } else if (WT == WT_Q2_0) {
+            // byte j holds elements 4j..4j+3 as 2-bit fields (the value is
+            // field - 1); the copies are ORed, not added, so nothing carries
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const uint32_t B = (q[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+                const uint32_t u = B | (B << 6);
+                v[j] = (u | (u << 12)) & 0x03030303u;
+            }
+        } else if (WT == WT_NVFP4) {
             // sub-block 2h: qs bytes 0..7, low nibbles elements 0..7, high 8..15;
             // sub-block 2h+1: bytes 8..15 -> elements 16..23 and 24..31
             v[0] = lut4(L, q[0]);
@@ -186,8 +223,10 @@ __device__ __forceinline__ void gemv_lut_impl(const uint8_t *__restrict__ W, int
                 int s = 0;
 #pragma unroll
                 for (int k = 0; k < 8; k++) s = dot4(v[k], y[k], s);
-                if (WT == WT_IQ4_NL) {
-                    if (SUBSUMS && valid && c < ncols && rr < nr) sub[((int64_t)c * rows + r0 + rr) * nb + g] = s;
+                if (WT == WT_Q1_0) s = 2 * s - ysum[c];
+                if (WT == WT_Q2_0) s -= ysum[c];
+                if (WT != WT_IQ4_XS) {
+                    if (SUBSUMS && valid && c < ncols && rr < nr) sub[((int64_t)c * rows + r0 + rr) * ng + g] = s;
                     pp = (h2f(hw) * dy[c]) * (float)s;
                 } else {
                     // the super-block's exact sum (its 8 groups sit in 8
@@ -223,10 +262,22 @@ __device__ __forceinline__ void q8w_repack_lut(const uint8_t *__restrict__ W, in
     const int nbp = Kpad / 32;
     if (i >= (int64_t)Npad * nbp) return;
     const int row = (int)(i / nbp), g = (int)(i % nbp);
-    const int ng = WT == WT_IQ4_NL ? nb : 8 * nb;
+    const int ng = WT == WT_IQ4_NL ? nb : WT == WT_Q1_0 ? 4 * nb : WT == WT_Q2_0 ? 2 * nb : 8 * nb;
     uint32_t v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     float d = 0.0f;
-    if (row < N && g < ng) {
+    if (row < N && g < ng && (WT == WT_Q1_0 || WT == WT_Q2_0)) {
+        // sign bits -> +-1, 2-bit fields -> field - 1, as int8
+        const uint8_t *r = W + (int64_t)row * row_bytes;
+        const int per = WT == WT_Q1_0 ? 4 : 2;
+        const uint8_t *blk = r + (int64_t)(g / per) * 18;
+        d = h2f(ld2(blk));
+        const uint8_t *q = blk + 2 + (WT == WT_Q1_0 ? 4 : 8) * (g % per);
+#pragma unroll
+        for (int e = 0; e < 32; e++) {
+            const int val = WT == WT_Q1_0 ? (((q[e >> 3] >> (e & 7)) & 1) ? 1 : -1) : (int)((q[e >> 2] >> (2 * (e & 3))) & 3) - 1;
+            v[e >> 2] |= (uint32_t)(val & 0xff) << (8 * (e & 3));
+        }
+    } else if (row < N && g < ng) {
         const uint8_t *r = W + (int64_t)row * row_bytes;
         const uint8_t *qs;
         if (WT == WT_IQ4_NL) {
@@ -274,11 +325,25 @@ GEMV_LUT_INST(nvfp4, WT_NVFP4, 1) GEMV_LUT_INST(nvfp4, WT_NVFP4, 2) GEMV_LUT_INS
 GEMV_LUT_INST(nvfp4, WT_NVFP4, 8)
 GEMV_LUT_INST(iq4_xs, WT_IQ4_XS, 1) GEMV_LUT_INST(iq4_xs, WT_IQ4_XS, 2) GEMV_LUT_INST(iq4_xs, WT_IQ4_XS, 4)
 GEMV_LUT_INST(iq4_xs, WT_IQ4_XS, 8)
+GEMV_LUT_INST(q1_0, WT_Q1_0, 1) GEMV_LUT_INST(q1_0, WT_Q1_0, 2) GEMV_LUT_INST(q1_0, WT_Q1_0, 4)
+GEMV_LUT_INST(q1_0, WT_Q1_0, 8)
+GEMV_LUT_INST(q2_0, WT_Q2_0, 1) GEMV_LUT_INST(q2_0, WT_Q2_0, 2) GEMV_LUT_INST(q2_0, WT_Q2_0, 4)
+GEMV_LUT_INST(q2_0, WT_Q2_0, 8)
 
 extern "C" __global__ void __launch_bounds__(256)
     ghip_gemm_q8w_repack_iq4_nl(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int nb, int Kpad, int Npad,
                                 int8_t *__restrict__ codes, float *__restrict__ dw) {
     q8w_repack_lut<WT_IQ4_NL>(W, row_bytes, N, nb, Kpad, Npad, codes, dw);
+}
+extern "C" __global__ void __launch_bounds__(256)
+    ghip_gemm_q8w_repack_q1_0(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int nb, int Kpad, int Npad,
+                              int8_t *__restrict__ codes, float *__restrict__ dw) {
+    q8w_repack_lut<WT_Q1_0>(W, row_bytes, N, nb, Kpad, Npad, codes, dw);
+}
+extern "C" __global__ void __launch_bounds__(256)
+    ghip_gemm_q8w_repack_q2_0(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int nb, int Kpad, int Npad,
+                              int8_t *__restrict__ codes, float *__restrict__ dw) {
+    q8w_repack_lut<WT_Q2_0>(W, row_bytes, N, nb, Kpad, Npad, codes, dw);
 }
 extern "C" __global__ void __launch_bounds__(256)
     ghip_gemm_q8w_repack_iq4_xs(const uint8_t *__restrict__ W, int64_t row_bytes, int N, int nb, int Kpad, int Npad,

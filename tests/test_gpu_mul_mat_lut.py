@@ -1,11 +1,12 @@
 """GPU parity of GGML_OP_MUL_MAT with the table-lookup 4-bit weights IQ4_NL,
-IQ4_XS and NVFP4 (vec_dot.rs:1154, :1597, :1655) against the CPU oracle.
+IQ4_XS and NVFP4 (vec_dot.rs:1154, :1597, :1655) and the 1- and 2-bit code
+weights Q1_0 and Q2_0 (vec_dot.rs:1074, :1120) against the CPU oracle.
 
 The oracle's dots are pinned bit-exact on the reference's x86 results
 (parity/vecdot3_ref.bin) and its dequantizers on the reference quantizer's
-bytes (quants_ref_iq.bin, quants_ref_fp4.bin) in test_oracle_golden.py.  The
-reference has no CPU quantizer restated here for these types, so the weights
-are (a) the reference quantizer's own IQ4_NL / IQ4_XS rows and (b) random
+bytes (quants_ref_iq.bin, quants_ref_fp4.bin, quants_ref_q1q2.bin) in
+test_oracle_golden.py.  The weights are (a) the reference quantizer's own
+IQ4_NL / IQ4_XS / Q1_0 / Q2_0 rows and (b) random
 block bytes with finite scales, as the reference's own vec_dot dump uses.
 
 Bar (north star): activation bytes and int32 sub-sums bit-exact; fp32 outputs
@@ -45,7 +46,11 @@ def random_blocks(ty, rows, k, seed, large=False):
     rng = np.random.default_rng(seed)
     qk, bs = O.BLOCK[ty]
     b = rng.integers(0, 256, size=(rows, k // qk, bs), dtype=np.uint8)
-    if ty in (O.IQ4_NL, O.IQ4_XS):
+    if ty in (O.Q1_0, O.Q2_0):  # weights +-d (Q1_0), -d..2d (Q2_0)
+        lo, hi = (2.0 ** -2, 2.0 ** 0) if large else (2.0 ** -8, 2.0 ** -5)
+        d = rng.uniform(lo, hi, size=(rows, k // qk)) * rng.choice([-1, 1], size=(rows, k // qk))
+        b[:, :, 0:2] = d.astype(np.float16).view(np.uint8).reshape(rows, k // qk, 2)
+    elif ty in (O.IQ4_NL, O.IQ4_XS):
         lo, hi = (2.0 ** -9, 2.0 ** -6) if large else (2.0 ** -13, 2.0 ** -10)
         if ty == O.IQ4_XS and not large:  # its 6-bit group scales multiply d by up to 32
             lo, hi = lo / 16, hi / 16
@@ -106,20 +111,23 @@ def check(be, ty, w, k, x, sub=True, bar=None):
     return err
 
 
-@pytest.mark.parametrize("ty", [O.IQ4_NL, O.IQ4_XS, O.NVFP4])
+ALL = [O.IQ4_NL, O.IQ4_XS, O.NVFP4, O.Q1_0, O.Q2_0]
+
+
+@pytest.mark.parametrize("ty", ALL)
 @pytest.mark.parametrize("k,rows,cols", [(256, 8, 1), (512, 100, 2), (1024, 37, 3), (4096, 256, 5), (4096, 96, 8),
                                          (2048, 130, 40), (4096, 512, 64)])
 def test_random_blocks(be, ty, k, rows, cols):
     """Decode (1..8 rows: the lookup kernels), prefill (32+ rows: the int8
     GEMM for IQ4_NL / IQ4_XS, the decode kernel in groups of 8 columns for
-    NVFP4), rows not a multiple of 8, K from one block to 4096; model-scale
+    NVFP4), the int8 GEMM for Q1_0 / Q2_0 too, rows not a multiple of 8, K from one block to 4096; model-scale
     weights, the 1e-5 bar."""
     w = random_blocks(ty, rows, k, seed=k + rows + cols)
     x = np.random.default_rng(cols).standard_normal((cols, k)).astype(np.float32)
     check(be, ty, w, k, x, sub=rows * cols <= 512 * 64)
 
 
-@pytest.mark.parametrize("ty", [O.IQ4_NL, O.IQ4_XS, O.NVFP4])
+@pytest.mark.parametrize("ty", ALL)
 @pytest.mark.parametrize("k,rows,cols", [(512, 100, 2), (4096, 96, 8), (2048, 130, 40)])
 def test_large_random_blocks(be, ty, k, rows, cols):
     """Weights up to ~2 whose outputs cancel (hundreds of units summing to
@@ -132,11 +140,13 @@ def test_large_random_blocks(be, ty, k, rows, cols):
     check(be, ty, w, k, x, bar="reference")
 
 
-@pytest.mark.parametrize("ty", [O.IQ4_NL, O.IQ4_XS])
+@pytest.mark.parametrize("ty", [O.IQ4_NL, O.IQ4_XS, O.Q1_0, O.Q2_0])
 def test_reference_quantized_rows(be, ty):
-    """The reference quantizer's IQ4_NL / IQ4_XS bytes (quants_ref_iq.bin, one
-    1024-element row) as a weight row, at 1, 5 and 40 activation rows."""
-    (sec,) = [s for s in fx.quant_sections("quants_ref_iq.bin") if s[1] == ty]
+    """The reference quantizer's IQ4_NL / IQ4_XS / Q1_0 / Q2_0 bytes
+    (quants_ref_iq.bin, quants_ref_q1q2.bin, one 1024-element row) as a weight
+    row, at 1, 5 and 40 activation rows."""
+    name = "quants_ref_q1q2.bin" if ty in (O.Q1_0, O.Q2_0) else "quants_ref_iq.bin"
+    (sec,) = [s for s in fx.quant_sections(name) if s[1] == ty]
     _, _, n, q, _ = sec
     w = np.tile(q.reshape(1, -1), (16, 1))
     for cols in (1, 5, 40):
@@ -144,7 +154,7 @@ def test_reference_quantized_rows(be, ty):
         check(be, ty, w, n, x)
 
 
-@pytest.mark.parametrize("ty", [O.IQ4_NL, O.IQ4_XS, O.NVFP4])
+@pytest.mark.parametrize("ty", ALL)
 def test_reference_dot(be, ty):
     """The reference's own dot (vecdot3_ref.bin: its x86 kernel on its block
     bytes and its quantized activation row), with that activation row handed
@@ -158,9 +168,9 @@ def test_reference_dot(be, ty):
     assert abs(float(got) - float(want)) <= TOL * max(1.0, abs(float(want))), (got, want)
 
 
-@pytest.mark.parametrize("ty", [O.IQ4_NL, O.IQ4_XS])
+@pytest.mark.parametrize("ty", [O.IQ4_NL, O.IQ4_XS, O.Q1_0, O.Q2_0])
 def test_registered_weight_gemm(be, ty):
-    """A registered IQ4_NL / IQ4_XS weight keeps its int8-code copy; the GEMM on
+    """A registered IQ4_NL / IQ4_XS / Q1_0 / Q2_0 weight keeps its int8-code copy; the GEMM on
     it gives the bits of the per-call repack."""
     import ghip
     k, rows, cols = 1024, 192, 48

@@ -253,7 +253,17 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
                         s[1] = imb;
                     }
                 }
-                const float part = ac.d * fmaf(dw[rr], (float)ia, -(dmin[rr] * (float)im));
+                float part;
+                if constexpr (Q5) {
+                    // the super-block's integer sums first (its four lanes),
+                    // as the reference forms them: Q5_K's mins cancel main
+                    // terms of the same size, and per-lane float parts of
+                    // mixed sign would carry their own rounding
+                    const int iab = quad_sum_dpp(ia), imb = quad_sum_dpp(im);
+                    part = i == 0 ? ac.d * fmaf(dw[rr], (float)iab, -(dmin[rr] * (float)imb)) : 0.0f;
+                } else {
+                    part = ac.d * fmaf(dw[rr], (float)ia, -(dmin[rr] * (float)im));
+                }
                 const float tot = wave_sum_dpp(part);
                 // columns past ncols (the NC - ncols padding columns) are not stored
                 if (lane == 0 && c < ncols && rg + rr < r1) {

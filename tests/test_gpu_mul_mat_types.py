@@ -1,5 +1,5 @@
 """GPU parity of GGML_OP_MUL_MAT for the further decode weight types Q5_0, Q8_0
-(Q8_0 activations) and Q5_K (Q8_K activations), against the CPU oracle and
+(Q8_0 activations), Q4_1 / Q5_1 (Q8_1) and Q5_K / Q2_K / Q3_K (Q8_K), against the CPU oracle and
 against the reference's own dumps (mulmat_ref.bin / mulmat_ref_c1.bin,
 types 6, 8, 13).
 
@@ -9,10 +9,11 @@ Two kinds of weights:
     bytes and int32 sub-sums bit-exact, fp32 within 1e-5 by
     rel_err = max |a-b| / max(|b|, 1) (vec_dot.rs:2355);
   * random block bytes with finite f16 scales, which reach every code, qh bit
-    and packed 6-bit scale: sub-sums bit-exact, fp32 within 1e-4.  Random
-    Q5_K mins up to 63 * dmin make the reference's own order (main and min
-    terms summed apart, subtracted at the end, vec_dot.rs:940-978) cancel
-    terms of ~1e3, so its fp32 result carries ~1e-3 of rounding of its own.
+    and packed 6-bit scale: sub-sums bit-exact, fp32 within 1e-5, or within
+    twice the distance of the reference's own fp32 result from the exact value
+    of its per-block formula where that is larger (random Q5_K / Q2_K mins up
+    to 63 * dmin make the reference's order -- main and min terms summed apart,
+    subtracted at the end, vec_dot.rs:940-978 -- cancel terms of ~1e3).
 """
 import numpy as np
 import pytest
@@ -73,10 +74,9 @@ def quantized(ty, n, rows, seed):
 
 def run_case(be, ty, n, rows, cols, seed=0, check_sub=True, x=None, weights="quant"):
     w = quantized(ty, n, rows, seed) if weights == "quant" else random_blocks(ty, n, rows, seed)
-    tol = TOL if weights == "quant" else 1e-4
     if x is None:
         x = np.random.default_rng(seed + 1).standard_normal((cols, n)).astype(np.float32)
-    want, route, want_sub = O.mul_mat(ty, w, n, rows, x, cols, want_subsums=check_sub)
+    want, route, want_sub = O.mul_mat(ty, w, n, rows, x, cols, want_subsums=True)
     wd = torch.from_numpy(w).cuda()
     xd = torch.from_numpy(x).cuda()
     print(f"case type={ty} n={n} rows={rows} cols={cols} route={route}", flush=True)
@@ -86,66 +86,60 @@ def run_case(be, ty, n, rows, cols, seed=0, check_sub=True, x=None, weights="qua
     if check_sub:
         sub = be.mul_mat_subsums(wd, ty, n, xd).cpu().numpy()
         assert np.array_equal(sub, want_sub), "int32 sub-sums differ"
-    if ty in K23_TYPES and check_sub:
-        # the GPU folds d8*d*isum (- d8*dmin*summs) once per super-block: it is
-        # held against the float64 value of the exact integer sums (the
-        # oracle's export, checked bit-exact above) within gamma_(nb+16) of the
-        # terms' magnitudes, and against the fp32 oracle (the reference's 8-lane
-        # order, whose own error follows its lane partials) within 1e-4
-        nb = n // 256
-        wb = w.reshape(rows, nb, -1)
-        off = 80 if ty == O.Q2_K else 108
-        d = wb[..., off:off + 2].copy().view(np.float16)[..., 0].astype(np.float64)
-        act8 = O.mul_mat_act(ty, n, rows, x, cols).reshape(cols, nb, 292)
-        d8 = act8[..., 0:4].copy().view(np.float32)[..., 0].astype(np.float64)
-        if ty == O.Q2_K:
-            dm = wb[..., 82:84].copy().view(np.float16)[..., 0].astype(np.float64)
-            t_main = d8[:, None] * d[None] * want_sub[..., 0]
-            t_min = d8[:, None] * dm[None] * want_sub[..., 1]
-            exact = (t_main - t_min).sum(-1)
-            mag = (np.abs(t_main) + np.abs(t_min)).sum(-1)
-        else:
-            t_main = d8[:, None] * d[None] * want_sub
-            exact = t_main.sum(-1)
-            mag = np.abs(t_main).sum(-1)
-        bound = 2.0 * (nb + 16) * 2.0 ** -24 * mag
-        assert np.all(np.abs(got.astype(np.float64) - exact) <= bound), \
-            f"max excess {np.max(np.abs(got - exact) - bound):.3e}"
-        assert rel_err(got, want) <= 1e-4
-        return
-    if ty in MIN_TYPES:
-        # d * d8 * isum + m * s per block, summed over nb blocks in different
-        # orders by the reference (8 lanes + a separate m * s chain) and the
-        # kernel: each carries at most gamma_(nb+16) = (nb + 16) * 2^-24 of the
-        # sum of the terms' magnitudes (recursive summation bound)
-        mag = min_term_magnitudes(ty, w, n, rows, O.mul_mat_act(ty, n, rows, x, cols), cols)
-        nb = n // 32
-        bound = 2.0 * (nb + 16) * 2.0 ** -24 * mag
-        assert np.all(np.abs(got.astype(np.float64) - want) <= bound), \
-            f"max excess {np.max(np.abs(got - want) - bound):.3e}"
-        assert rel_err(got, want) <= 1e-4
-        return
     err = rel_err(got, want)
-    assert err <= tol, f"rel_err {err:.3e}"
+    # held to the bar unless the reference's own fp32 order already sits
+    # further from the exact value of its formula (the float64 sum of the
+    # exact integer sub-sums, checked bit-exact against the GPU's where
+    # check_sub, times their scales): then to twice that distance.  (Q4_1 /
+    # Q5_1 at K = 14336 on quantized N(0, 0.02) rows: the reference is
+    # 1.0e-5 / 1.2e-5 from that value, its main and m*s sums cancelling.)
+    exact, mag = exact_from_subsums(ty, w, n, rows, O.mul_mat_act(ty, n, rows, x, cols), cols, want_sub)
+    # every fp32 evaluation order of the formula lies within the recursive
+    # summation bound gamma_(nb+16) of the terms' magnitudes of that value
+    nb = n // O.BLOCK[ty][0]
+    bound = 2.0 * (nb + 16) * 2.0 ** -24 * mag
+    assert np.all(np.abs(got.astype(np.float64) - exact) <= bound), \
+        f"max excess {np.max(np.abs(got - exact) - bound):.3e}"
+    bar = max(TOL, 2.0 * rel_err(want.astype(np.float64), exact))
+    if weights == "random":
+        # random block bytes (mins up to 63 * dmin against main terms of the
+        # same size): where the cancellation makes that bound wider than the
+        # bar, two valid orders may differ by it
+        bar = max(bar, float(np.max(bound / np.maximum(np.abs(want), 1.0))))
+    assert err <= bar, f"rel_err {err:.3e} (bar {bar:.3e})"
 
 
-def min_term_magnitudes(ty, w, n, rows, act, cols):
-    """sum_b |d_w d8 isum_b| + |m_w s_b| per output [cols, rows] (float64)."""
-    bs = 20 if ty == O.Q4_1 else 24
-    b = w.reshape(rows, n // 32, bs)
-    d = b[..., 0:2].copy().view(np.float16)[..., 0].astype(np.float64)
-    m = b[..., 2:4].copy().view(np.float16)[..., 0].astype(np.float64)
-    qs = b[..., bs - 16:]
-    codes = np.concatenate([qs & 15, qs >> 4], axis=-1).astype(np.int64)
-    if ty == O.Q5_1:
-        qh = b[..., 4:8].copy().view(np.uint32)[..., 0].astype(np.int64)
-        codes |= ((qh[..., None] >> np.arange(32)) & 1) << 4
-    a = act.reshape(cols, n // 32, 36)
-    d8 = a[..., 0:2].copy().view(np.float16)[..., 0].astype(np.float64)
-    s8 = a[..., 2:4].copy().view(np.float16)[..., 0].astype(np.float64)
-    q8 = a[..., 4:].view(np.int8).astype(np.int64)
-    isum = np.einsum("rbe,cbe->crb", codes, q8)
-    return (np.abs(d[None] * d8[:, None] * isum) + np.abs(m[None] * s8[:, None])).sum(-1)
+def _f16(a, off):
+    return a[..., off:off + 2].copy().view(np.float16)[..., 0].astype(np.float64)
+
+
+def exact_from_subsums(ty, w, n, rows, act, cols, sub):
+    """float64 value of the reference's per-block formula from the exact
+    integer sub-sums, and the sum of its terms' magnitudes, both [cols, rows]:
+    Q5_0 / Q8_0  sum_b d d8 isum_b;  Q4_1 / Q5_1  sum_b d d8 isum_b + m s8_b;
+    Q5_K / Q2_K  sum_b d8 (d isum_b - dmin imin_b);  Q3_K  sum_b d8 d isum_b."""
+    qk, bs = O.BLOCK[ty]
+    nb = n // qk
+    wb = w.reshape(rows, nb, bs)
+    at = O.ACT_TYPE[ty]
+    a = act.reshape(cols, nb, -1)
+    if at == O.Q8_K:
+        d8 = a[..., 0:4].copy().view(np.float32)[..., 0].astype(np.float64)
+    else:
+        d8 = _f16(a, 0)
+    sub = sub.reshape(cols, rows, nb, -1).astype(np.float64)
+    if ty in (O.Q5_0, O.Q8_0):
+        t = [_f16(wb, 0)[None] * d8[:, None] * sub[..., 0]]
+    elif ty in MIN_TYPES:
+        t = [_f16(wb, 0)[None] * d8[:, None] * sub[..., 0], _f16(wb, 2)[None] * _f16(a, 2)[:, None]]
+    elif ty in (O.Q5_K, O.Q2_K):
+        dd, dm = (_f16(wb, 0), _f16(wb, 2)) if ty == O.Q5_K else (_f16(wb, 80), _f16(wb, 82))
+        t = [d8[:, None] * dd[None] * sub[..., 0], -(d8[:, None] * dm[None] * sub[..., 1])]
+    else:
+        t = [d8[:, None] * _f16(wb, 108)[None] * sub[..., 0]]
+    exact = sum(x.sum(-1) for x in t)
+    mag = sum(np.abs(x).sum(-1) for x in t)
+    return exact, mag
 
 
 @pytest.mark.parametrize("ty", TYPES + MIN_TYPES)
@@ -209,8 +203,8 @@ def test_zero_and_extreme_codes(be):
     got = be.mul_mat(torch.from_numpy(w).cuda(), O.Q8_0, n, torch.from_numpy(x).cuda()).cpu().numpy()
     sub = be.mul_mat_subsums(torch.from_numpy(w).cuda(), O.Q8_0, n, torch.from_numpy(x).cuda()).cpu().numpy()
     assert np.array_equal(sub, want_sub)
-    assert rel_err(got, want) <= 1e-4
-
+    exact, _ = exact_from_subsums(O.Q8_0, w, n, rows, O.mul_mat_act(O.Q8_0, n, rows, x, 2), 2, want_sub)
+    assert rel_err(got, want) <= max(TOL, 2.0 * rel_err(want.astype(np.float64), exact))
 
 
 @pytest.mark.parametrize("ty", K23_TYPES)

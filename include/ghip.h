@@ -100,6 +100,18 @@ typedef struct ghip_context ghip_context;
  * the dlopen entry ggml_backend_init (backend.rs:1354-1420). */
 ghip_status ghip_init(int device, ghip_context **out);
 
+/* A context without a device, for checking launch plans on a host with no
+ * GPU.  No counterpart in the reference (its CPU backend has no launches).
+ * Ops on it plan their launches, take a workspace address range nothing
+ * allocates and, instead of launching, check that every kernel's store
+ * window (worked out from that launch's own arguments) lies inside the
+ * buffers the op writes: its dst, sub-sum and activation outputs and the
+ * workspace.  A window outside them fails the op with a "store check"
+ * message.  Device pointers in the tensors are only compared, never read.
+ * (GHIP_CHECK_STORES=1 in the environment makes ghip_init contexts run the
+ * same check before their real launches.)  Free with ghip_free. */
+ghip_status ghip_init_dry_run(ghip_context **out);
+
 /* Release the context (BackendI.free, backend.rs:666). */
 void ghip_free(ghip_context *ctx);
 

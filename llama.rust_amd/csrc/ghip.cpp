@@ -131,6 +131,28 @@ struct ghip_context {
     size_t wcache_bytes = 0;   // bytes held by wcache
     size_t wcache_built = 0;   // copies materialized so far (hits do not count)
 
+    // Store check (GHIP_CHECK_STORES=1, and every dry-run context): before a
+    // launch, the byte windows its kernel stores to -- worked out from the
+    // launch's own arguments (expect) -- must lie inside the buffers the op
+    // writes: its dst / sub-sum / activation outputs and the workspace it took
+    // (allow).  A dry-run context (ghip_init_dry_run) has no device: ops plan,
+    // take a workspace address range and check every launch without running it.
+    bool check_stores = false;
+    bool dry_run = false;
+    struct Span {
+        uintptr_t lo, hi;
+        const char *what;
+    };
+    std::vector<Span> allowed, pending;
+    void allow(const void *p, size_t n, const char *what) {
+        if (check_stores && p && n) allowed.push_back({(uintptr_t)p, (uintptr_t)p + n, what});
+    }
+    void expect(const void *p, size_t n, const char *what) {
+        if (check_stores && n) pending.push_back({(uintptr_t)p, (uintptr_t)p + n, what});
+    }
+    // the device current for an op (nothing to do in a dry run)
+    bool set_device() { return dry_run || hipSetDevice(device) == hipSuccess; }
+
     ghip_status fail(ghip_status st, const char *fmt, ...) {
         char buf[512];
         va_list ap;
@@ -166,6 +188,9 @@ struct ghip_context {
 
     // Called at the start of every op on stream s (device current, lock held).
     ghip_status begin(hipStream_t s) {
+        allowed.clear();
+        pending.clear();
+        if (dry_run) return GHIP_STATUS_SUCCESS;
         if (have_last && last_stream != s && !capturing(s) && !capturing(last_stream)) {
             if (hipEventRecord(order_ev, last_stream) != hipSuccess || hipStreamWaitEvent(s, order_ev, 0) != hipSuccess) {
                 (void)hipGetLastError();
@@ -178,6 +203,16 @@ struct ghip_context {
     }
 
     ghip_status workspace(size_t bytes, hipStream_t s, void **out) {
+        ghip_status st = workspace_get(bytes, s, out);
+        if (st == GHIP_STATUS_SUCCESS) allow(*out, bytes, "workspace");
+        return st;
+    }
+    ghip_status workspace_get(size_t bytes, hipStream_t s, void **out) {
+        if (dry_run && !call_ws && !user_ws) {
+            // an address range no allocation uses: the launches are checked, never run
+            *out = (void *)(uintptr_t)(1ull << 46);
+            return GHIP_STATUS_SUCCESS;
+        }
         if (call_ws) {
             if (bytes > call_ws_size)
                 return fail(GHIP_STATUS_ALLOC_FAILED, "this call needs %zu bytes of scratch; the fixed scratch holds %zu",
@@ -218,6 +253,20 @@ struct ghip_context {
     template <typename... Args>
     ghip_status launch(const std::string &name, dim3 grid, dim3 block, size_t shmem, hipStream_t s,
                        Args... args) {
+        if (check_stores) {
+            for (const Span &w : pending) {
+                bool inside = false;
+                for (const Span &a : allowed) inside = inside || (w.lo >= a.lo && w.hi <= a.hi);
+                if (!inside) {
+                    pending.clear();
+                    return fail(GHIP_STATUS_BACKEND_ERROR,
+                                "store check: %s of %s would store %zu bytes at %p, outside every buffer of this op",
+                                w.what, name.c_str(), (size_t)(w.hi - w.lo), (void *)w.lo);
+                }
+            }
+            pending.clear();
+        }
+        if (dry_run) return GHIP_STATUS_SUCCESS;
         hipFunction_t f = fn(name);
         if (!f) return fail(GHIP_STATUS_BACKEND_ERROR, "kernel %s not found in the code objects", name.c_str());
         void *ptrs[] = {(void *)&args...};
@@ -323,6 +372,7 @@ bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b,
 
 ghip_status quantize_act(ghip_context *ctx, const MulMatPlan &p, const ghip_tensor *b, void *out, hipStream_t s) {
     const int64_t x_stride = (int64_t)b->nb[1] / 4;
+    ctx->expect(out, (size_t)(p.M * p.act_row_bytes), "quantized activations");
     if (p.act_type == GHIP_TYPE_Q8_K) {
         const int64_t waves = p.M * (p.K / 256);
         const unsigned grid = (unsigned)((waves + 3) / 4);
@@ -376,9 +426,17 @@ bool gemm_q8_family(int wtype) {
            wtype == GHIP_TYPE_Q2_0;
 }
 // int32 sub-sums per weight block (ghip_mul_mat_subsums layout)
+// bytes a kernel covers storing m rows of n elements at stride ldd
+size_t win2d(int64_t m, int64_t ldd, int64_t n, size_t e = 4) {
+    return m > 0 && n > 0 ? ((size_t)(m - 1) * (size_t)ldd + (size_t)n) * e : 0;
+}
 int64_t subsums_per_block(int wtype) {
     if (wtype == GHIP_TYPE_Q4_K || wtype == GHIP_TYPE_Q5_K || wtype == GHIP_TYPE_Q2_K) return 2;
     return wtype == GHIP_TYPE_NVFP4 || wtype == GHIP_TYPE_Q1_0 ? 4 : wtype == GHIP_TYPE_Q2_0 ? 2 : 1;
+}
+// int32 sub-sums of m activation rows
+size_t sub_bytes(const MulMatPlan &p, int64_t m) {
+    return (size_t)m * (size_t)p.N * (size_t)p.nb * (size_t)subsums_per_block(p.wtype) * 4;
 }
 
 // The whole-row decode kernels with the activation image in LDS: Q4_K and
@@ -428,9 +486,17 @@ void gemv_groups(int wtype, int64_t M, int64_t N, int &rb, int &ng) {
 bool valu_q4k_small(const MulMatPlan &p) {
     return p.wtype == GHIP_TYPE_Q4_K && p.M <= 4 && p.N < 8192 && p.nb <= 16;
 }
+void skinny_shape(int64_t M, int &NC, int &RT, int &KS);
+size_t skinny_lds(int NC, int64_t K, int64_t nb);
+// (9-15 rows of a long K, e.g. 14336 at 16 columns, do not fit the LDS
+// image: they take the whole-row kernels in groups of 8 columns)
 bool use_skinny(const MulMatPlan &p) {
-    return p.wtype == GHIP_TYPE_Q4_K && p.M >= env_int("GHIP_MMA_MIN_ROWS", 4) && p.M < 16 &&
-           env_int("GHIP_MMA", 1) != 0 && !valu_q4k_small(p);
+    if (!(p.wtype == GHIP_TYPE_Q4_K && p.M >= env_int("GHIP_MMA_MIN_ROWS", 4) && p.M < 16 &&
+          env_int("GHIP_MMA", 1) != 0 && !valu_q4k_small(p)))
+        return false;
+    int NC, RT, KS;
+    skinny_shape(p.M, NC, RT, KS);
+    return skinny_lds(NC, p.K, p.nb) <= 160 * 1024;
 }
 // The K split sets the fp32 summation order, so it is fixed (2 row tiles x
 // 4 K-slices) for every matrix size: a matrix alone and in a grouped launch
@@ -456,6 +522,8 @@ ghip_status run_skinny(ghip_context *ctx, const MulMatPlan &p, const void *w, co
                              std::to_string(NC) + "_r" + std::to_string(RT) + "k" + std::to_string(KS);
     const unsigned grid = (unsigned)((p.N + 16 * RT - 1) / (16 * RT));
     const int n_mat = (int)std::max<int64_t>(0, std::min<int64_t>(p.M, p.n_mat));
+    ctx->expect(dst, win2d(p.M, ldd, p.N), "dst");
+    if (sub) ctx->expect(sub, sub_bytes(p, p.M), "sub-sums");
     return ctx->launch(name, dim3(grid), dim3(512), shmem, s, (const uint8_t *)w, (int64_t)p.w_row_bytes, (int)p.N,
                        (int)p.nb, act, act_rb, (int)p.M, dst, ldd, sub, n_mat);
 }
@@ -526,12 +594,18 @@ ghip_status launch_sk(ghip_context *ctx, const MulMatPlan &p, SkLaunch &g, const
     g.tg = (int)std::max<int64_t>(1, std::min<int64_t>(tiles, (want + ns - 1) / ns));
     r.nks = g.nks;
     const int n_mat = (int)std::max<int64_t>(0, std::min<int64_t>(p.M, p.n_mat));
+    for (int i = 0; i < g.n; i++) {
+        if (ns > 1) ctx->expect(g.m[i].part, (size_t)ns * (size_t)p.M * (size_t)g.m[i].rows * 4, "split-K partials");
+        else ctx->expect(g.m[i].dst, win2d(p.M, g.m[i].ldd, g.m[i].rows), "dst");
+    }
+    if (sub) ctx->expect(sub, sub_bytes(p, p.M), "sub-sums");
     const std::string name = std::string("ghip_sk_") + (p.wtype == GHIP_TYPE_Q4_K ? "q4_K" : "q6_K") +
                              (sub ? "_sub" : "") + "_s" + std::to_string(sk_sb(p.nb));
     ghip_status st = ctx->launch(name, dim3((unsigned)(ns * g.tg)), dim3(256), 0, s, g, (int64_t)p.w_row_bytes,
                                  (int)p.nb, (const float *)x->data, (int64_t)x->nb[1] / 4, (int)p.M, n_mat, sub);
     if (st != GHIP_STATUS_SUCCESS || ns == 1) return st;
     const int64_t total = rows * p.M;
+    for (int i = 0; i < g.n; i++) ctx->expect(r.m[i].dst, win2d(p.M, r.m[i].ldd, r.m[i].rows), "dst");
     return ctx->launch("ghip_sk_reduce", dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, r, (int)p.M, total);
 }
 ghip_status run_sk(ghip_context *ctx, const MulMatPlan &p, const void *w, const ghip_tensor *x, float *dst,
@@ -634,6 +708,8 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
             sub_c = sub + c0 * p.N * subsums_per_block(p.wtype) * p.nb;
         }
         ghip_status st;
+        ctx->expect(dst + c0 * ldd, win2d(nc, ldd, p.N), "dst");
+        if (sub) ctx->expect(sub_c, sub_bytes(p, nc), "sub-sums");
         if (q4k) {
             // LDS: codes [NC][K] | d [NC][nb] | 16-element sums [NC][nb][16] | partials
             const size_t shmem = (size_t)NC * p.K + (size_t)NC * p.nb * 4 + (size_t)NC * p.nb * 16 * 4 +
@@ -755,6 +831,7 @@ size_t gemm_layout_bytes(const MulMatPlan &p) {
 ghip_status q6k_repack(ghip_context *ctx, const void *w, int64_t row_bytes, int64_t N, int64_t nbk, uint8_t *rep,
                        hipStream_t s) {
     const int64_t nblk = N * nbk;  // four blocks per workgroup
+    ctx->expect(rep, (size_t)nblk * kQ6R, "Q6_K repack");
     return ctx->launch("ghip_q6K_repack", dim3((unsigned)((nblk + 3) / 4)), dim3(256), 0, s, (const uint8_t *)w,
                        row_bytes, (int)N, (int)nbk, rep);
 }
@@ -777,6 +854,8 @@ ghip_status run_gemm_q6k(ghip_context *ctx, const MulMatPlan &p, const void *w, 
         if (st != GHIP_STATUS_SUCCESS) return st;
         rep = r;
     }
+    ctx->expect(codes, (size_t)(Mpad * p.K * 2), "activation codes");
+    ctx->expect(dT, (size_t)(nbk * Mpad * 4), "activation scales");
     if (bf)  // f32 activations: quantized straight into the layout
         st = ctx->launch("ghip_gemm_act_q8K_f16", dim3((unsigned)((p.M * nbk + 3) / 4)), dim3(256), 0, s,
                          (const float *)bf->data, (int64_t)bf->nb[1] / 4, (int)p.M, (int)Mpad, (int)nbk, (int)p.n_mat,
@@ -786,6 +865,8 @@ ghip_status run_gemm_q6k(ghip_context *ctx, const MulMatPlan &p, const void *w, 
                          (int64_t)p.act_row_bytes, (int)p.M, (int)Mpad, (int)nbk, codes, dT);
     if (st != GHIP_STATUS_SUCCESS) return st;
     const unsigned grid = (unsigned)(((p.M + 63) / 64) * ((p.N + 127) / 128));
+    ctx->expect(dst, win2d(p.M, ldd, p.N), "dst");
+    if (sub) ctx->expect(sub, sub_bytes(p, p.M), "sub-sums");
     return ctx->launch(sub ? "ghip_gemm_q6_K_sub" : "ghip_gemm_q6_K", dim3(grid), dim3(256), kGemmSmemQ6, s,
                        (const uint8_t *)rep, (int)p.N, (int)nbk, (const uint16_t *)codes, (const float *)dT, (int)p.M,
                        (int)Mpad, dst, ldd, sub);
@@ -805,6 +886,9 @@ const char *q8w_repack_name(int wtype) {
 ghip_status q8w_repack(ghip_context *ctx, int wtype, const void *w, int64_t row_bytes, int64_t N, int64_t nb,
                        const Q8Layout &L, int8_t *codes, float *dw, hipStream_t s) {
     const int64_t n = L.Npad * L.nbp;
+    ctx->expect(codes, (size_t)(L.Npad * L.Kpad), "weight codes");
+    ctx->expect(dw, (size_t)(L.nbp * L.Npad * 4), "weight scales");
+    if (wtype == GHIP_TYPE_IQ4_XS) ctx->expect((uint8_t *)dw + L.dw_b, (size_t)(L.Kpad / 256 * L.Npad * 4), "super-block scales");
     if (wtype == GHIP_TYPE_IQ4_XS)  // the super-block scales follow dw
         return ctx->launch(q8w_repack_name(wtype), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
                            (const uint8_t *)w, row_bytes, (int)N, (int)nb, (int)L.Kpad, (int)L.Npad, codes, dw,
@@ -836,6 +920,8 @@ ghip_status run_gemm_q8(ghip_context *ctx, const MulMatPlan &p, const void *w, c
         dw = d;
     }
     const int64_t ablocks = L.Mpad * L.nbp;
+    ctx->expect(ac, (size_t)(L.Mpad * L.Kpad), "activation codes");
+    ctx->expect(da, (size_t)(L.nbp * L.Mpad * 4), "activation scales");
     const int nb32 = (int)(p.K / 32);  // the GEMM's blocks are 32 elements (Q8_0 activation blocks)
     if (p.wtype == GHIP_TYPE_IQ4_XS)  // Q8_K activations: codes and the block scale per 32-group
         st = ctx->launch("ghip_gemm_act_q8K_q8", dim3((unsigned)((L.Mpad * p.nb + 3) / 4)), dim3(256), 0, s,
@@ -847,6 +933,8 @@ ghip_status run_gemm_q8(ghip_context *ctx, const MulMatPlan &p, const void *w, c
                          (int)L.Kpad, ac, da);
     if (st != GHIP_STATUS_SUCCESS) return st;
     const unsigned grid = (unsigned)(((p.M + 63) / 64) * ((p.N + 127) / 128));
+    ctx->expect(dst, win2d(p.M, ldd, p.N), "dst");
+    if (sub) ctx->expect(sub, sub_bytes(p, p.M), "sub-sums");
     if (p.wtype == GHIP_TYPE_IQ4_XS)
         return ctx->launch(sub ? "ghip_gemm_q8_xs_sub" : "ghip_gemm_q8_xs", dim3(grid), dim3(256), kGemmSmemQ8, s, wc,
                            dw, (int)p.N, (int)L.Npad, nb32, (int)L.Kpad, (const int8_t *)ac, (const float *)da,
@@ -867,6 +955,9 @@ ghip_status run_gemm(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
     uint16_t *bsT = (uint16_t *)(codes + Mpad * K);
     float *dT = (float *)(bsT + nbk * Mpad * 16);
     const unsigned lgrid = (unsigned)((p.M * nbk + 3) / 4);
+    ctx->expect(codes, (size_t)(Mpad * K), "activation codes");
+    ctx->expect(bsT, (size_t)(nbk * Mpad * 32), "activation bsum16");
+    ctx->expect(dT, (size_t)(nbk * Mpad * 4), "activation scales");
     ghip_status st =
         bf ? ctx->launch("ghip_gemm_act_q8K", dim3(lgrid), dim3(256), 0, s, (const float *)bf->data,
                          (int64_t)bf->nb[1] / 4, (int)p.M, (int)Mpad, (int)nbk, (int)p.n_mat, codes, bsT, dT)
@@ -881,12 +972,16 @@ ghip_status run_gemm(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
                                      (((size_t)Mpad * K + nbk * Mpad * 32 + nbk * Mpad * 4 + 255) & ~(size_t)255))
                          : dst;
     const int64_t zstride = ns > 1 ? p.M * p.N : 0;
+    if (ns > 1) ctx->expect(part, (size_t)ns * (size_t)(p.M * p.N) * 4, "split-K partials");
+    else ctx->expect(dst, win2d(p.M, ldd, p.N), "dst");
+    if (sub) ctx->expect(sub, sub_bytes(p, p.M), "sub-sums");
     st = ctx->launch(sub ? gk.name_sub : gk.name, dim3(grid, ns), dim3(gk.threads), gk.smem, s,
                      (const uint8_t *)w, (int64_t)p.w_row_bytes, (int)p.N, (int)p.nb, (const int8_t *)codes,
                      (const uint16_t *)bsT, (const float *)dT, (int)p.M, (int)Mpad, part,
                      ns > 1 ? (int64_t)p.N : (int64_t)ldd, sub, nbs, zstride);
     if (st != GHIP_STATUS_SUCCESS || ns == 1) return st;
     const unsigned rgrid = (unsigned)((p.M * p.N / 4 + 255) / 256);
+    ctx->expect(dst, win2d(p.M, ldd, p.N), "dst");
     return ctx->launch("ghip_gemm_splitk_reduce", dim3(rgrid), dim3(256), 0, s, (const float *)part, ns, (int)p.M,
                        (int)p.N, dst, (int64_t)ldd);
 }
@@ -938,10 +1033,13 @@ ghip_status mul_mat_plane(ghip_context *ctx, const ghip_tensor *a, const ghip_te
     if (!plan_mul_mat(ctx, a, b, d, p, st)) return st;
     hipStream_t s = (hipStream_t)stream;
     if (p.M == 0 || p.N == 0) return GHIP_STATUS_SUCCESS;  // empty operands: nothing to compute
-    if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    if (!ctx->set_device()) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
     if (!d && !sub && !act_out) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: no output");
     st = ctx->begin(s);
     if (st != GHIP_STATUS_SUCCESS) return st;
+    if (d) ctx->allow(d->data, win2d(p.M, (int64_t)d->nb[1], (int64_t)d->ne[0] * 4, 1), "dst");
+    ctx->allow(sub, sub_bytes(p, p.M), "sub-sums");
+    ctx->allow(act_out, (size_t)(p.M * p.act_row_bytes), "activation output");
     size_t act_bytes, lay_bytes;
     const size_t need = mul_mat_ws_bytes(p, d != nullptr, act_out != nullptr, &act_bytes, &lay_bytes, sub != nullptr);
     void *ws = nullptr;
@@ -956,7 +1054,9 @@ ghip_status mul_mat_plane(ghip_context *ctx, const ghip_tensor *a, const ghip_te
     }
     void *lay = lay_bytes ? (void *)((uint8_t *)ws + act_bytes) : nullptr;
     float *dst = d ? (float *)d->data : (float *)((uint8_t *)ws + act_bytes + lay_bytes);
-    const int64_t ldd = d ? (int64_t)d->nb[1] / 4 : p.N;
+    // (GHIP_DEBUG_LDD_SKEW=k, dry-run contexts only: a deliberately wrong
+    // leading dimension, the kind of host bug the store check exists for)
+    const int64_t ldd = (d ? (int64_t)d->nb[1] / 4 : p.N) + (ctx->dry_run ? env_int("GHIP_DEBUG_LDD_SKEW", 0) : 0);
     if (gemm_route(p, sub != nullptr))
         return run_gemm(ctx, p, a->data, (const uint8_t *)b->data, p.act_pre ? nullptr : b, dst, ldd, sub, lay, s);
     if (use_sk(p)) return run_sk(ctx, p, a->data, b, dst, ldd, sub, lay, s);
@@ -1217,7 +1317,7 @@ ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip
     const int64_t n_pairs = p.n_ids * p.n_tokens;
     if (n_pairs == 0 || p.rows == 0) return GHIP_STATUS_SUCCESS;
     hipStream_t s = (hipStream_t)stream;
-    if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    if (!ctx->set_device()) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
     st = ctx->begin(s);
     if (st != GHIP_STATUS_SUCCESS) return st;
     const MoeWs L = moe_ws(p, d != nullptr, sub != nullptr);
@@ -1402,9 +1502,11 @@ ghip_status mul_mat_multi_gemm(ghip_context *ctx, const ghip_node *nodes, int n,
         if (p[i].M != p[0].M || p[i].wtype != GHIP_TYPE_Q4_K || !use_gemm(p[i]) || p[i].act_pre)
             return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "graph_compute: internal: node not groupable");
     }
-    if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    if (!ctx->set_device()) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
     st = ctx->begin(s);
     if (st != GHIP_STATUS_SUCCESS) return st;
+    for (int i = 0; i < n; i++)
+        ctx->allow(nodes[i].dst->data, win2d(p[i].M, (int64_t)nodes[i].dst->nb[1], p[i].N * 4, 1), "dst");
     const MulMatPlan &p0 = p[0];
     const int64_t Mpad = (p0.M + 127) / 128 * 128, K = p0.K, nbk = p0.K / 256;
     const size_t lay_bytes = (size_t)Mpad * K + (size_t)nbk * Mpad * 32 + (size_t)nbk * Mpad * 4;
@@ -1459,9 +1561,11 @@ ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipS
         if (p[i].M != p[0].M || p[i].M > 8 || !(gemv_v2(p[i]) || gemv_pair(p[i].wtype)) || p[i].act_pre)
             return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "graph_compute: internal: node not groupable");
     }
-    if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    if (!ctx->set_device()) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
     st = ctx->begin(s);
     if (st != GHIP_STATUS_SUCCESS) return st;
+    for (int i = 0; i < n; i++)
+        ctx->allow(nodes[i].dst->data, win2d(p[i].M, (int64_t)nodes[i].dst->nb[1], p[i].N * 4, 1), "dst");
     const MulMatPlan &p0 = p[0];
     if (gemv_pair(p0.wtype)) {
         // Q8_0 rows once for the group, then 8 weight rows per workgroup
@@ -1625,7 +1729,7 @@ static ghip_status fa_sequence(ghip_context *ctx, const ghip_tensor *q, const gh
     const int D = (int)k->ne[0], T = (int)q->ne[1], H = (int)q->ne[2], S = (int)k->ne[1], H_kv = (int)k->ne[2];
     if (T == 0 || H == 0) return GHIP_STATUS_SUCCESS;
     hipStream_t s = (hipStream_t)stream;
-    if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    if (!ctx->set_device()) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
     st = ctx->begin(s);
     if (st != GHIP_STATUS_SUCCESS) return st;
     const FaLayout L = fa_layout(D, T, H, S, H_kv);
@@ -1759,6 +1863,7 @@ ghip_status ghip_init(int device, ghip_context **out) {
     if (hipSetDevice(device) != hipSuccess) return GHIP_STATUS_BACKEND_ERROR;
     ghip_context *ctx = new ghip_context();
     ctx->device = device;
+    ctx->check_stores = env_int("GHIP_CHECK_STORES", 0) != 0;
     const char *why = "";
     if (ghip_noalloc_setup(device, &why) != GHIP_STATUS_SUCCESS ||
         hipEventCreateWithFlags(&ctx->order_ev, hipEventDisableTiming) != hipSuccess) {
@@ -1784,8 +1889,21 @@ ghip_status ghip_init(int device, ghip_context **out) {
     return GHIP_STATUS_SUCCESS;
 }
 
+ghip_status ghip_init_dry_run(ghip_context **out) {
+    if (!out) return GHIP_STATUS_BACKEND_ERROR;
+    ghip_context *ctx = new ghip_context();
+    ctx->dry_run = true;
+    ctx->check_stores = true;
+    *out = ctx;
+    return GHIP_STATUS_SUCCESS;
+}
+
 void ghip_free(ghip_context *ctx) {
     if (!ctx) return;
+    if (ctx->dry_run) {
+        delete ctx;
+        return;
+    }
     hipSetDevice(ctx->device);
     hipDeviceSynchronize();
     if (ctx->ws) hipFree(ctx->ws);
@@ -1856,7 +1974,7 @@ ghip_status ghip_weight_register(ghip_context *ctx, const ghip_tensor *w, void *
     hipStream_t s = (hipStream_t)stream;
     if (ghip_context::capturing(s))
         return ctx->fail(GHIP_STATUS_ALLOC_FAILED, "weight_register allocates: not while the stream is captured");
-    if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    if (!ctx->set_device()) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
     ghip_status st = ctx->begin(s);
     if (st != GHIP_STATUS_SUCCESS) return st;
     void *rep = nullptr;
@@ -1966,7 +2084,7 @@ ghip_status ghip_context_upload(ghip_context *ctx, void *dst, const void *src, s
     std::lock_guard<std::mutex> lock(ctx->mu);
     hipStream_t s = (hipStream_t)stream;
     if (ghip_context::capturing(s)) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "gguf_upload: stream is being captured");
-    if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    if (!ctx->set_device()) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
     for (int b = 0; b < 2; b++) {
         if (!ctx->stage[b] && (hipHostMalloc(&ctx->stage[b], kStage, hipHostMallocDefault) != hipSuccess ||
                                hipEventCreateWithFlags(&ctx->stage_ev[b], hipEventDisableTiming) != hipSuccess)) {
@@ -2113,7 +2231,7 @@ ghip_status ghip_quantize_chunk(ghip_context *ctx, int type, const float *src, v
     if (!src || !dst) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "quantize_chunk: null pointer");
     const int64_t nblocks = nrows * (n_per_row / ti.blck);
     if (nblocks == 0) return GHIP_STATUS_SUCCESS;
-    if (hipSetDevice(ctx->device) != hipSuccess) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    if (!ctx->set_device()) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
     const unsigned tpb = ti.blck == 256 ? 64 : 256;
     const unsigned grid = (unsigned)((nblocks + tpb - 1) / tpb);
     return ctx->launch(name, dim3(grid), dim3(tpb), 0, (hipStream_t)stream, src, nblocks, (uint8_t *)dst);

@@ -410,3 +410,24 @@ def test_batched_shape_errors(be):
         a, b, d = ghip.describe(wd, ghip.Q8_0, k), ghip.describe(xd, ghip.F32), ghip.describe(out, ghip.F32)
         with pytest.raises(ghip.GhipError, match=msg):
             be._check(ghip.lib().ghip_mul_mat(be._ctx, C.byref(a), C.byref(b), C.byref(d), ghip._stream()), "ghip_mul_mat")
+
+
+@pytest.mark.parametrize("cols", [9, 11, 15])
+def test_q4K_long_k_9_to_15_rows(be, cols):
+    """Q4_K down projection (K = 14336) at 9-15 activation rows: the
+    matrix-core decode kernel's 16-column LDS image does not fit there, so
+    the rows go to the whole-row kernels in groups of 8 columns.  The oracle
+    takes the reference's tiled route from 8 columns; the bar is 1e-5 or the
+    gap between the reference's own two routes on these inputs (row vec_dot
+    per column against the tiled kernel), whichever is larger."""
+    n, rows = 14336, 512
+    w, x = make(O.Q4_K, n, rows, cols, cols)
+    want, route, want_sub = O.mul_mat(O.Q4_K, w, n, rows, x, cols, want_subsums=True)
+    vd = np.concatenate([O.mul_mat(O.Q4_K, w, n, rows, x[c:c + 1], 1)[0] for c in range(cols)])
+    gap = rel_err(vd.reshape(cols, rows), want.reshape(cols, rows))
+    wd, xd = torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda()
+    print(f"case q4_K n={n} rows={rows} cols={cols} route={route} route gap {gap:.2e}", flush=True)
+    got = be.mul_mat(wd, O.Q4_K, n, xd).cpu().numpy()
+    assert np.array_equal(be.mul_mat_subsums(wd, O.Q4_K, n, xd).cpu().numpy(), want_sub)
+    err = rel_err(got, want.reshape(got.shape))
+    assert err <= max(TOL, gap), (err, gap)

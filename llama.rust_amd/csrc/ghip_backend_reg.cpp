@@ -89,6 +89,7 @@ struct Proc {
 void *reg_proc_address(const ggml_hip_backend_reg *, const char *name) {
     static const Proc procs[] = {
         {"ghip_init", (void *)&ghip_init},
+        {"ghip_init_dry_run", (void *)&ghip_init_dry_run},
         {"ghip_free", (void *)&ghip_free},
         {"ghip_last_error", (void *)&ghip_last_error},
         {"ghip_synchronize", (void *)&ghip_synchronize},

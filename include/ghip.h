@@ -1,7 +1,7 @@
 /*
  * ghip.h -- C ABI of the MI355X (gfx950) backend for llama.rust's quantized
  * ggml hot path: GGML_OP_MUL_MAT (Q4_0 / Q4_K / Q6_K weights),
- * GGML_OP_MUL_MAT_ID (MXFP4 experts) and GGML_OP_FLASH_ATTN_EXT (f16 K/V).
+ * GGML_OP_MUL_MAT_ID and GGML_OP_FLASH_ATTN_EXT (f16 / f32 K/V).
  *
  * The entry points are what a Rust `ggml-hip` FFI crate binds (one extern "C"
  * fn per declaration, no other glue); each comment names the reference
@@ -186,7 +186,8 @@ ghip_status ghip_mul_mat_subsums(ghip_context *ctx, const ghip_tensor *src0, con
 ghip_status ghip_mul_mat_act(ghip_context *ctx, const ghip_tensor *src0, const ghip_tensor *src1,
                              void *out, void *stream);
 
-/* dst = MUL_MAT_ID(as, b, ids) with MXFP4, Q4_K, Q5_K or Q6_K experts
+/* dst = MUL_MAT_ID(as, b, ids) with MXFP4, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0,
+ * Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, NVFP4, Q1_0 or Q2_0 experts
  * (forward_mul_mat_id, compute.rs:1917-2202; the MXFP4 rows % 8 == 0 repack
  * kernel repack.rs:1048-1100):
  *   as:  [K, rows, n_as], expert rows contiguous blocks
@@ -201,6 +202,11 @@ ghip_status ghip_mul_mat_act(ghip_context *ctx, const ghip_tensor *src0, const g
  * activations (compute.rs:1950-1980); each super-block's integer sums are
  * exact and scaled once by d8 * d (vec_dot.rs:881-909, :998-1028), so outputs
  * match the reference's routes to fp32 rounding of those per-block terms.
+ * The other types: every b row quantized to the type's vec_dot type
+ * (Q8_0, Q8_1 or Q8_K, compute.rs:1950-1976), then per pair the expert's
+ * decode kernel of ghip_mul_mat (the reference's row vec_dot, Q4_0's 8x8
+ * repack gemv, or for Q2_K / Q3_K / IQ4_XS experts with >= 8 pairs its tiled
+ * kernel: the same integer sums, fp32 within rounding of their order).
  * A pair whose id is outside [0, n_as) -- where the reference asserts -- gets
  * a row of NaN. */
 ghip_status ghip_mul_mat_id(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b, const ghip_tensor *ids,
@@ -213,6 +219,8 @@ ghip_status ghip_mul_mat_id(ghip_context *ctx, const ghip_tensor *as, const ghip
  *     subsums[((p * rows + r) * (K / 256) + sb) * 2 + {0, 1}];
  *   Q6_K: sum sc * (dot - 32 * bsum) per super-block at
  *     subsums[(p * rows + r) * (K / 256) + sb]
+ *   other types: the ghip_mul_mat_subsums row of the type, P ints per row at
+ *     subsums[(p * rows + r) * P + j]
  * (the layouts of ghip_mul_mat_subsums).  Pairs with an invalid id are left
  * unwritten. */
 ghip_status ghip_mul_mat_id_subsums(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b,

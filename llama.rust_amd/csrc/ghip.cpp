@@ -1232,11 +1232,40 @@ bool moe_fp4(int tp) {
 }
 
 struct MoePlan {
-    int wtype;  // MXFP4, or Q4_K / Q5_K / Q6_K experts
+    int wtype;  // MXFP4, Q4_K / Q5_K / Q6_K experts, or a type of the per-pair decode route
+    bool generic;  // per-pair decode kernels (mmid_generic_type)
     int64_t K, rows, n_as, ne11, n_tokens, n_ids, nb;
     int64_t act_row_bytes;
 };
 
+// expert types that MUL_MAT_ID runs through the decode kernels, one (token,
+// slot) pair per grid row (every type with a vec_dot_type, compute.rs:1926-1929)
+const char *mmid_kernel_type(int t) {
+    switch (t) {
+    case GHIP_TYPE_Q4_0: return "q4_0";
+    case GHIP_TYPE_Q5_0: return "q5_0";
+    case GHIP_TYPE_Q8_0: return "q8_0";
+    case GHIP_TYPE_Q4_1: return "q4_1";
+    case GHIP_TYPE_Q5_1: return "q5_1";
+    case GHIP_TYPE_Q2_K: return "q2_K";
+    case GHIP_TYPE_Q3_K: return "q3_K";
+    case GHIP_TYPE_IQ4_NL: return "iq4_nl";
+    case GHIP_TYPE_IQ4_XS: return "iq4_xs";
+    case GHIP_TYPE_NVFP4: return "nvfp4";
+    case GHIP_TYPE_Q1_0: return "q1_0";
+    default: return "q2_0";
+    }
+}
+int mmid_act_type(int t) {
+    if (t == GHIP_TYPE_Q4_1 || t == GHIP_TYPE_Q5_1) return GHIP_TYPE_Q8_1;
+    if (t == GHIP_TYPE_Q2_K || t == GHIP_TYPE_Q3_K || t == GHIP_TYPE_IQ4_XS) return GHIP_TYPE_Q8_K;
+    return GHIP_TYPE_Q8_0;
+}
+bool mmid_generic_type(int t) {
+    return t == GHIP_TYPE_Q4_0 || t == GHIP_TYPE_Q5_0 || t == GHIP_TYPE_Q8_0 || t == GHIP_TYPE_Q4_1 ||
+           t == GHIP_TYPE_Q5_1 || t == GHIP_TYPE_Q2_K || t == GHIP_TYPE_Q3_K || t == GHIP_TYPE_IQ4_NL ||
+           t == GHIP_TYPE_IQ4_XS || t == GHIP_TYPE_NVFP4 || t == GHIP_TYPE_Q1_0 || t == GHIP_TYPE_Q2_0;
+}
 // forward_mul_mat_id (compute.rs:1917-2202) with MXFP4, Q4_K, Q5_K or Q6_K
 // experts (the K-quants' vec_dot_type is Q8_K, compute.rs:1926-1929).
 bool plan_moe(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b, const ghip_tensor *ids,
@@ -1245,9 +1274,11 @@ bool plan_moe(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b, co
     auto bad = [&](const char *why) { st = ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat_id: %s", why); return false; };
     if (!as || !b || !ids) return bad("null operand");
     p.wtype = as->type;
+    p.generic = mmid_generic_type(p.wtype);
     if (p.wtype != GHIP_TYPE_MXFP4 && p.wtype != GHIP_TYPE_Q4_K && p.wtype != GHIP_TYPE_Q5_K &&
-        p.wtype != GHIP_TYPE_Q6_K)
-        return bad("experts must be MXFP4, Q4_K, Q5_K or Q6_K");
+        p.wtype != GHIP_TYPE_Q6_K && !p.generic)
+        return bad("experts must be MXFP4, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, "
+                   "NVFP4, Q1_0 or Q2_0");
     const TypeInfo ti = type_info(p.wtype);
     if (as->ne[0] % ti.blck || as->ne[0] <= 0) return bad("ne00 must be a positive multiple of the block size");
     p.K = as->ne[0];
@@ -1274,6 +1305,10 @@ bool plan_moe(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b, co
         return bad("dst must be F32 [rows, n_ids, n_tokens]");
     if (p.wtype != GHIP_TYPE_MXFP4 && p.nb > INT32_MAX / 256) return bad("ne00 too large");
     p.act_row_bytes = p.wtype == GHIP_TYPE_MXFP4 ? p.nb * 34 : p.nb * 292;
+    if (p.generic) {  // the vec_dot_type's rows (vec_dot.rs:1727-1749)
+        const int at = mmid_act_type(p.wtype);
+        p.act_row_bytes = at == GHIP_TYPE_Q8_K ? p.K / 256 * 292 : at == GHIP_TYPE_Q8_1 ? p.K / 32 * 36 : p.K / 32 * 34;
+    }
     st = GHIP_STATUS_SUCCESS;
     return true;
 }
@@ -1305,6 +1340,52 @@ MoeWs moe_ws(const MoePlan &p, bool has_dst, bool sub) {
     return L;
 }
 
+// The further expert types: every src1 row quantized to the vec_dot type
+// (the wdata pass, compute.rs:1950-1976), then the decode kernel of each
+// pair's expert on its row (grid: 8-row blocks x pairs).
+ghip_status mul_mat_id_generic(ghip_context *ctx, const MoePlan &p, const ghip_tensor *as, const ghip_tensor *b,
+                               const ghip_tensor *ids, const ghip_tensor *d, int32_t *sub, hipStream_t s) {
+    const int64_t n_pairs = p.n_ids * p.n_tokens, act_rows = p.ne11 * p.n_tokens;
+    const size_t act_b = ((size_t)(act_rows * p.act_row_bytes) + 255) & ~(size_t)255;
+    const size_t out_b = d ? 0 : (size_t)(n_pairs * p.rows * 4);
+    void *ws = nullptr;
+    ghip_status st = ctx->workspace(act_b + out_b, s, &ws);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    uint8_t *act = (uint8_t *)ws;
+    float *dst = d ? (float *)d->data : (float *)((uint8_t *)ws + act_b);
+    const int64_t dst_nb1 = d ? (int64_t)d->nb[1] / 4 : p.rows;
+    const int64_t dst_nb2 = d ? (int64_t)d->nb[2] / 4 : p.rows * p.n_ids;
+    const int at = mmid_act_type(p.wtype);
+    const int64_t x_stride = (int64_t)b->nb[1] / 4;
+    ctx->expect(act, (size_t)(act_rows * p.act_row_bytes), "quantized activations");
+    if (at == GHIP_TYPE_Q8_K)
+        st = ctx->launch("ghip_quantize_q8_K", dim3((unsigned)((act_rows * (p.K / 256) + 3) / 4)), dim3(256), 0, s,
+                         (const float *)b->data, x_stride, p.K, act_rows, act, p.act_row_bytes, (int64_t)0);
+    else
+        st = ctx->launch(at == GHIP_TYPE_Q8_1 ? "ghip_quantize_q8_1" : "ghip_quantize_q8_0",
+                         dim3((unsigned)((act_rows * (p.K / 32) * 8 + 255) / 256)), dim3(256), 0, s,
+                         (const float *)b->data, x_stride, p.K, act_rows, act, p.act_row_bytes);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    // the decode kernels' wavefronts per row (as run_gemv)
+    int waves_k;
+    if (gemv_pair(p.wtype)) waves_k = (int)(((p.nb + 1) / 2 + 63) / 64);
+    else if (p.wtype == GHIP_TYPE_Q4_1 || p.wtype == GHIP_TYPE_Q5_1) waves_k = (int)((p.nb + 63) / 64);
+    else if (lut_type(p.wtype)) waves_k = (int)((p.K / 32 + 63) / 64);
+    else waves_k = (int)((p.nb + 15) / 16);  // Q2_K / Q3_K: four lanes per super-block
+    if (waves_k > 8) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat_id: ne00 = %lld too large for the decode kernel", (long long)p.K);
+    const int64_t sub_pair = p.rows * p.nb * subsums_per_block(p.wtype);
+    if (sub) ctx->expect(sub, (size_t)(n_pairs * sub_pair * 4), "sub-sums");
+    ctx->expect(dst, (size_t)((p.n_tokens - 1) * dst_nb2 + (p.n_ids - 1) * dst_nb1 + p.rows) * 4, "dst");
+    const char *tn = mmid_kernel_type(p.wtype);
+    const std::string name = std::string("ghip_mmid_gemv_") + tn + (sub ? "_sub" : "");
+    constexpr int kRows = 8;  // weight rows per decode workgroup
+    return ctx->launch(name, dim3((unsigned)((p.rows + kRows - 1) / kRows), (unsigned)n_pairs), dim3(64 * waves_k), 0,
+                       s, (const uint8_t *)as->data, (int64_t)as->nb[1], (int64_t)as->nb[2], (int)p.rows, (int)p.nb,
+                       (const uint8_t *)act, p.act_row_bytes, (int)p.ne11, (const int32_t *)ids->data,
+                       (int64_t)ids->nb[1] / 4, (int)p.n_ids, (int)p.n_as, dst, dst_nb1, dst_nb2, sub, sub_pair,
+                       kRows);
+}
+
 // Q8_0 activations, routing, then the tiled MFMA kernel; pairs with an
 // invalid expert id get NaN rows (the reference asserts on them).
 ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b, const ghip_tensor *ids,
@@ -1320,6 +1401,11 @@ ghip_status mul_mat_id_impl(ghip_context *ctx, const ghip_tensor *as, const ghip
     if (!ctx->set_device()) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
     st = ctx->begin(s);
     if (st != GHIP_STATUS_SUCCESS) return st;
+    if (d)
+        ctx->allow(d->data, (size_t)((p.n_tokens - 1) * d->nb[2] + (p.n_ids - 1) * d->nb[1]) + (size_t)p.rows * 4, "dst");
+    ctx->allow(sub, (size_t)(n_pairs * p.rows * p.nb * (p.wtype == GHIP_TYPE_MXFP4 ? 1 : subsums_per_block(p.wtype))) * 4,
+               "sub-sums");
+    if (p.generic) return mul_mat_id_generic(ctx, p, as, b, ids, d, sub, s);
     const MoeWs L = moe_ws(p, d != nullptr, sub != nullptr);
     const int tp = L.tp;
     const int64_t max_tiles = L.max_tiles;

@@ -227,3 +227,40 @@ DEV float e8m0_half(uint32_t x) {
     const uint32_t bits = x < 2 ? (0x00200000u << x) : ((x - 1) << 23);
     return __uint_as_float(bits);
 }
+
+// MUL_MAT_ID through a decode kernel: blockIdx.y is the (token, slot) pair
+// p = t * n_ids + s (dst row [t][s], compute.rs:1917-2202): its expert's
+// weights, its activation row t * ne11 + s % ne11 and its sub-sums.  A pair
+// whose expert id is out of range gets NaN rows (the reference asserts on it);
+// the workgroup then returns false after writing them.
+#define MMID_ARGS                                                                                                   \
+    const uint8_t *__restrict__ as, int64_t as_nb1, int64_t as_nb2, int rows, int nb,                               \
+        const uint8_t *__restrict__ act, int64_t act_rb, int ne11, const int32_t *__restrict__ ids,                 \
+        int64_t ids_nb1, int n_ids, int n_as, float *__restrict__ dst, int64_t dst_nb1, int64_t dst_nb2,            \
+        int32_t *__restrict__ sub, int64_t sub_pair, int rpw
+struct MmidPair {
+    const uint8_t *W, *act;
+    float *dst;
+    int32_t *sub;
+};
+DEV bool mmid_pair(const uint8_t *as, int64_t as_nb2, const uint8_t *act, int64_t act_rb, int ne11,
+                   const int32_t *ids, int64_t ids_nb1, int n_ids, int n_as, float *dst, int64_t dst_nb1,
+                   int64_t dst_nb2, int32_t *sub, int64_t sub_pair, int rows, int rpw, MmidPair &q) {
+    const int p = (int)blockIdx.y, t = p / n_ids, s = p - t * n_ids;
+    const int e = ids[(int64_t)t * ids_nb1 + s];
+    q.dst = dst + (int64_t)t * dst_nb2 + (int64_t)s * dst_nb1;
+    if (e < 0 || e >= n_as) {
+        const int r = (int)blockIdx.x * rpw + (int)threadIdx.x;
+        if ((int)threadIdx.x < rpw && r < rows) q.dst[r] = __builtin_nanf("");
+        return false;
+    }
+    q.W = as + (int64_t)e * as_nb2;
+    q.act = act + ((int64_t)t * ne11 + s % ne11) * act_rb;
+    q.sub = sub ? sub + (int64_t)p * sub_pair : nullptr;
+    return true;
+}
+#define MMID_PAIR(q)                                                                                                \
+    MmidPair q;                                                                                                     \
+    if (!mmid_pair(as, as_nb2, act, act_rb, ne11, ids, ids_nb1, n_ids, n_as, dst, dst_nb1, dst_nb2, sub, sub_pair,  \
+                   rows, rpw, q))                                                                                   \
+        return;

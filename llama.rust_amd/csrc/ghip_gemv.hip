@@ -1548,3 +1548,24 @@ GEMV_MULTI_RN(q6_K_v2, 1, 1, 8, gemv_q6K_v2_impl)
 GEMV_PAIR_MULTI_ALL(q4_0, gemv_q4_0_impl)
 GEMV_PAIR_MULTI_ALL(q5_0, gemv_q5_0_impl)
 GEMV_PAIR_MULTI_ALL(q8_0, gemv_q8_0_impl)
+
+// ------------------------------------------------ MUL_MAT_ID, further types
+// forward_mul_mat_id for experts other than MXFP4 / Q4_K / Q5_K / Q6_K: every
+// (token, slot) pair runs the decode kernel of its expert on its ready Q8
+// activation row (the reference's row vec_dot, or the Q4_0 8x8 gemv for
+// rows % 8 == 0 experts, compute.rs:2012-2024, 2166-2174), grid (row blocks,
+// pairs).
+#define MMID_GEMV(TN, CALL_FALSE, CALL_TRUE)                                                                        \
+    extern "C" __global__ void __launch_bounds__(512) ghip_mmid_gemv_##TN(MMID_ARGS) {                              \
+        MMID_PAIR(q) CALL_FALSE(q.W, as_nb1, rows, nb, q.act, act_rb, 1, q.dst, 0, nullptr);                       \
+    }                                                                                                               \
+    extern "C" __global__ void __launch_bounds__(512) ghip_mmid_gemv_##TN##_sub(MMID_ARGS) {                        \
+        MMID_PAIR(q) CALL_TRUE(q.W, as_nb1, rows, nb, q.act, act_rb, 1, q.dst, 0, q.sub);                          \
+    }
+MMID_GEMV(q4_0, (gemv_q4_0_impl<1, false, false>), (gemv_q4_0_impl<1, true, false>))
+MMID_GEMV(q5_0, (gemv_q5_0_impl<1, false, false>), (gemv_q5_0_impl<1, true, false>))
+MMID_GEMV(q8_0, (gemv_q8_0_impl<1, false, false>), (gemv_q8_0_impl<1, true, false>))
+MMID_GEMV(q4_1, (gemv_q41_impl<WT_Q4_1, 1, false>), (gemv_q41_impl<WT_Q4_1, 1, true>))
+MMID_GEMV(q5_1, (gemv_q41_impl<WT_Q5_1, 1, false>), (gemv_q41_impl<WT_Q5_1, 1, true>))
+MMID_GEMV(q2_K, (gemv_k23_impl<WT_Q2_K, 1, false>), (gemv_k23_impl<WT_Q2_K, 1, true>))
+MMID_GEMV(q3_K, (gemv_k23_impl<WT_Q3_K, 1, false>), (gemv_k23_impl<WT_Q3_K, 1, true>))

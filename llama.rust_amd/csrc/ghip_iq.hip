@@ -372,3 +372,18 @@ extern "C" __global__ void __launch_bounds__(256)
     *reinterpret_cast<uint32_t *>(codes + (int64_t)row * Kpad + (int64_t)b * QK_K + 4 * lane) = packed;
     if (lane < 8) da[(int64_t)(8 * b + lane) * Mpad + row] = d;
 }
+
+// MUL_MAT_ID with these experts: the decode kernel per (token, slot) pair
+// (MMID_PAIR in ghip_common.h), grid (row blocks, pairs)
+#define MMID_LUT(TN, WT)                                                                                            \
+    extern "C" __global__ void __launch_bounds__(512) ghip_mmid_gemv_##TN(MMID_ARGS) {                              \
+        MMID_PAIR(q) gemv_lut_impl<WT, 1, false>(q.W, as_nb1, rows, nb, q.act, act_rb, 1, q.dst, 0, nullptr);      \
+    }                                                                                                               \
+    extern "C" __global__ void __launch_bounds__(512) ghip_mmid_gemv_##TN##_sub(MMID_ARGS) {                        \
+        MMID_PAIR(q) gemv_lut_impl<WT, 1, true>(q.W, as_nb1, rows, nb, q.act, act_rb, 1, q.dst, 0, q.sub);         \
+    }
+MMID_LUT(iq4_nl, WT_IQ4_NL)
+MMID_LUT(iq4_xs, WT_IQ4_XS)
+MMID_LUT(nvfp4, WT_NVFP4)
+MMID_LUT(q1_0, WT_Q1_0)
+MMID_LUT(q2_0, WT_Q2_0)

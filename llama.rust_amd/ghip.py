@@ -249,8 +249,8 @@ class Backend:
 
     # ---- MUL_MAT_ID
     def mul_mat_id(self, experts, k, b, ids, out=None, ty=None):
-        """experts [n_as, rows, row_bytes] (MXFP4 unless ty is Q4_K, Q5_K or
-        Q6_K), b [n_tokens, ne11, K] f32, ids [n_tokens, n_ids] int32 ->
+        """experts [n_as, rows, row_bytes] (MXFP4 unless ty names another
+        type), b [n_tokens, ne11, K] f32, ids [n_tokens, n_ids] int32 ->
         out [n_tokens, n_ids, rows] f32."""
         ty = MXFP4 if ty is None else ty
         n_tokens, n_ids = ids.shape
@@ -267,7 +267,9 @@ class Backend:
         Q6_K: is per super-block [.., rows, K / 256]."""
         ty = MXFP4 if ty is None else ty
         n_tokens, n_ids = ids.shape
-        per = {MXFP4: (k // 32,), Q4_K: (k // 256, 2), Q5_K: (k // 256, 2), Q6_K: (k // 256,)}[ty]
+        per = {MXFP4: (k // 32,), Q4_K: (k // 256, 2), Q5_K: (k // 256, 2), Q6_K: (k // 256,)}.get(ty)
+        if per is None:  # the further types: their MUL_MAT sub-sum row (ghip_mul_mat_subsums)
+            per = (k // BLOCK[ty][0] * SUBSUMS_PER_BLOCK.get(ty, 1),)
         sub = torch.full((n_tokens, n_ids, experts.shape[1], *per), -1, dtype=torch.int32, device=b.device)
         a, tb, ti = describe(experts, ty, k), describe(b, F32), describe(ids, I32)
         self._check(lib().ghip_mul_mat_id_subsums(self._ctx, C.byref(a), C.byref(tb), C.byref(ti),

@@ -102,3 +102,23 @@ def test_skewed_leading_dimension_is_caught():
     r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
     assert r.stdout.count("store check") == 7
+
+
+def test_mul_mat_id_stores_inside_dst():
+    ghip, L = _lib()
+    L.ghip_mul_mat_id.restype = C.c_int
+    for ty in _types() + [ghip.MXFP4]:
+        for n_tokens, n_ids, ne11 in [(1, 4, 1), (12, 2, 2), (64, 4, 1)]:
+            ctx = C.c_void_p()
+            assert L.ghip_init_dry_run(C.byref(ctx)) == 0
+            try:
+                k, rows, n_as = 2048, 96, 8
+                blck, bs = ghip.BLOCK[ty]
+                a = _tensor(ghip, ty, [k, rows, n_as, 1], bs, blck, W_BASE)
+                b = _tensor(ghip, ghip.F32, [k, ne11, n_tokens, 1], 4, 1, X_BASE)
+                ids = _tensor(ghip, ghip.I32, [n_ids, n_tokens, 1, 1], 4, 1, S_BASE)
+                d = _tensor(ghip, ghip.F32, [rows, n_ids, n_tokens, 1], 4, 1, D_BASE)
+                st = L.ghip_mul_mat_id(ctx, C.byref(a), C.byref(b), C.byref(ids), C.byref(d), None)
+                assert st == 0, (ty, n_tokens, L.ghip_last_error(ctx).decode())
+            finally:
+                L.ghip_free(ctx)

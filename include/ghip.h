@@ -68,6 +68,7 @@ enum {
     GHIP_TYPE_IQ4_NL = 20,
     GHIP_TYPE_IQ4_XS = 23,
     GHIP_TYPE_I32 = 26,
+    GHIP_TYPE_BF16 = 30,
     GHIP_TYPE_MXFP4 = 39,
     GHIP_TYPE_NVFP4 = 40,
     GHIP_TYPE_Q1_0 = 41,
@@ -132,6 +133,8 @@ int ghip_supports_op(int op, const ghip_tensor *dst, const ghip_tensor *const *s
 /* dst = src0 x src1 (GGML_OP_MUL_MAT, forward_mul_mat compute.rs:1420-1839).
  * src0: Q4_0 | Q4_1 | Q5_0 | Q5_1 | Q8_0 | Q2_K | Q3_K | Q4_K | Q5_K | Q6_K |
  *       IQ4_NL | IQ4_XS | NVFP4 | Q1_0 | Q2_0 weight [ne00=K, ne01=N, ne02, ne03], rows contiguous;
+ *       or F32 | F16 | BF16 weight [ne00=K, ne01=N, ne02, ne03] (src1 must then be F32:
+ *       the activations are rounded to the weight type, compute.rs:1680-1745; no sub-sums)
  * src1: F32 [K, ne11, ne12, ne13] (any strides nb11..nb13, nb10 == 4), or
  *       already the vec_dot type of src0 (Q8_0 for Q4_0/Q5_0/Q8_0/IQ4_NL/NVFP4/Q1_0/Q2_0,
  *       Q8_1 for Q4_1/Q5_1, Q8_K for the K-quants and IQ4_XS; rows of blocks),

@@ -17,7 +17,7 @@ CSRC = os.path.join(HERE, "csrc")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
-KERNELS = ["ghip_quant", "ghip_gemv", "ghip_wquant", "ghip_gemm", "ghip_fa", "ghip_moe", "ghip_skinny", "ghip_iq"]
+KERNELS = ["ghip_quant", "ghip_gemv", "ghip_wquant", "ghip_gemm", "ghip_fa", "ghip_moe", "ghip_skinny", "ghip_iq", "ghip_dense"]
 DEVICE_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17",
     # exact fp32 semantics: products and sums round on their own, fused

@@ -20,7 +20,7 @@
 
 namespace {
 
-const char *const kModules[] = {"ghip_quant.hsaco", "ghip_gemv.hsaco", "ghip_wquant.hsaco", "ghip_gemm.hsaco", "ghip_fa.hsaco", "ghip_moe.hsaco", "ghip_skinny.hsaco", "ghip_iq.hsaco"};
+const char *const kModules[] = {"ghip_quant.hsaco", "ghip_gemv.hsaco", "ghip_wquant.hsaco", "ghip_gemm.hsaco", "ghip_fa.hsaco", "ghip_moe.hsaco", "ghip_skinny.hsaco", "ghip_iq.hsaco", "ghip_dense.hsaco"};
 
 struct TypeInfo {
     int blck;
@@ -31,6 +31,7 @@ TypeInfo type_info(int t) {
     switch (t) {
     case GHIP_TYPE_F32: return {1, 4};
     case GHIP_TYPE_F16: return {1, 2};
+    case GHIP_TYPE_BF16: return {1, 2};
     case GHIP_TYPE_Q4_0: return {32, 18};
     case GHIP_TYPE_Q4_1: return {32, 20};
     case GHIP_TYPE_Q2_K: return {256, 84};
@@ -293,6 +294,8 @@ struct MulMatPlan {
     bool act_pre;     // src1 already holds the vec_dot_type blocks
 };
 
+// F32 / F16 / BF16 weights (ghip_dense.hip)
+bool dense_type(int t) { return t == GHIP_TYPE_F32 || t == GHIP_TYPE_F16 || t == GHIP_TYPE_BF16; }
 bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b, const ghip_tensor *d,
                   MulMatPlan &p, ghip_status &st) {
     st = GHIP_STATUS_BACKEND_ERROR;
@@ -301,10 +304,11 @@ bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b,
         a->type != GHIP_TYPE_Q4_K && a->type != GHIP_TYPE_Q5_K && a->type != GHIP_TYPE_Q6_K &&
         a->type != GHIP_TYPE_Q4_1 && a->type != GHIP_TYPE_Q5_1 && a->type != GHIP_TYPE_Q2_K &&
         a->type != GHIP_TYPE_Q3_K && a->type != GHIP_TYPE_IQ4_NL && a->type != GHIP_TYPE_IQ4_XS &&
-        a->type != GHIP_TYPE_NVFP4 && a->type != GHIP_TYPE_Q1_0 && a->type != GHIP_TYPE_Q2_0) {
+        a->type != GHIP_TYPE_NVFP4 && a->type != GHIP_TYPE_Q1_0 && a->type != GHIP_TYPE_Q2_0 &&
+        a->type != GHIP_TYPE_F32 && a->type != GHIP_TYPE_F16 && a->type != GHIP_TYPE_BF16) {
         st = ctx->fail(st,
                        "mul_mat: src0 type %d not supported (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, "
-                       "IQ4_NL, IQ4_XS, NVFP4, Q1_0, Q2_0)",
+                       "IQ4_NL, IQ4_XS, NVFP4, Q1_0, Q2_0, F32, F16, BF16)",
                        a->type);
         return false;
     }
@@ -314,8 +318,10 @@ bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b,
                           a->type == GHIP_TYPE_IQ4_NL || a->type == GHIP_TYPE_NVFP4 || a->type == GHIP_TYPE_Q1_0 ||
                           a->type == GHIP_TYPE_Q2_0;
     const bool q8_1_dot = a->type == GHIP_TYPE_Q4_1 || a->type == GHIP_TYPE_Q5_1;
-    // vec_dot_type (vec_dot.rs vec_dot_type)
-    const int vdt = q8_0_dot ? GHIP_TYPE_Q8_0 : q8_1_dot ? GHIP_TYPE_Q8_1 : GHIP_TYPE_Q8_K;
+    const bool dense = dense_type(a->type);
+    // vec_dot_type (vec_dot.rs vec_dot_type); F32 / F16 / BF16 weights take the
+    // f32 src1 and round it themselves (compute.rs:1700-1745)
+    const int vdt = dense ? GHIP_TYPE_F32 : q8_0_dot ? GHIP_TYPE_Q8_0 : q8_1_dot ? GHIP_TYPE_Q8_1 : GHIP_TYPE_Q8_K;
     if (b->type != GHIP_TYPE_F32 && b->type != vdt) {
         st = ctx->fail(st, "mul_mat: src1 must be F32 or the vec_dot type of src0 (backend.rs:2057-2066)");
         return false;
@@ -348,7 +354,11 @@ bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b,
     p.nb = p.K / ti.blck;
     p.w_row_bytes = (int64_t)a->nb[1];
     if (p.w_row_bytes < p.nb * ti.bytes) { st = ctx->fail(st, "mul_mat: src0 nb1 too small"); return false; }
-    if (q8_0_dot) {
+    if (dense) {
+        p.act_type = GHIP_TYPE_F32;
+        p.act_row_bytes = p.K * 4;
+        p.n_mat = 0;
+    } else if (q8_0_dot) {
         p.act_type = GHIP_TYPE_Q8_0;
         p.act_row_bytes = p.K / 32 * 34;
         p.n_mat = 0;
@@ -1007,6 +1017,11 @@ bool gemm_route(const MulMatPlan &p, bool sub) {
 // scratch output when only sub-sums are wanted]
 size_t mul_mat_ws_bytes(const MulMatPlan &p, bool has_dst, bool act_out, size_t *act_b, size_t *lay_b,
                         bool sub = false) {
+    if (dense_type(p.wtype)) {  // F32 / F16 / BF16 weights read src1 as it is
+        if (act_b) *act_b = 0;
+        if (lay_b) *lay_b = 0;
+        return 0;
+    }
     // (the GEMM quantizes f32 activations straight into its layout)
     const bool gemm = !act_out && gemm_route(p, sub);
     // (the split-K decode kernels quantize inside; their layout is the partials)
@@ -1016,6 +1031,29 @@ size_t mul_mat_ws_bytes(const MulMatPlan &p, bool has_dst, bool act_out, size_t 
     if (act_b) *act_b = act_bytes;
     if (lay_b) *lay_b = lay_bytes;
     return (act_out ? 0 : act_bytes) + lay_bytes + (has_dst || act_out ? 0 : (size_t)(p.M * p.N * 4));
+}
+
+// F32 / F16 / BF16 weights: the dense decode kernel over groups of at most 8
+// activation rows (compute.rs:1680-1745)
+ghip_status run_dense(ghip_context *ctx, const MulMatPlan &p, const ghip_tensor *a, const ghip_tensor *b, float *dst,
+                      int64_t ldd, hipStream_t s) {
+    const char *tn = p.wtype == GHIP_TYPE_F32 ? "f32" : p.wtype == GHIP_TYPE_F16 ? "f16" : "bf16";
+    // 16-byte chunks of 8 elements where every row starts 16-byte aligned
+    const int esz = p.wtype == GHIP_TYPE_F32 ? 4 : 2;
+    const int vec = p.K % 8 == 0 && (uintptr_t)a->data % 16 == 0 && p.w_row_bytes % 16 == 0 ? 1 : 0;
+    (void)esz;
+    const int64_t x_stride = (int64_t)b->nb[1] / 4;
+    for (int64_t c0 = 0; c0 < p.M; c0 += 8) {
+        const int nc = (int)std::min<int64_t>(8, p.M - c0);
+        const int NC = nc == 1 ? 1 : nc == 2 ? 2 : nc <= 4 ? 4 : 8;
+        const std::string name = std::string("ghip_gemv_dense_") + tn + "_c" + std::to_string(NC);
+        ctx->expect(dst + c0 * ldd, win2d(nc, ldd, p.N), "dst");
+        ghip_status st = ctx->launch(name, dim3((unsigned)((p.N + 7) / 8)), dim3(256), 0, s, (const uint8_t *)a->data,
+                                     (int64_t)p.w_row_bytes, (int)p.N, (int)p.K, (const float *)b->data + c0 * x_stride,
+                                     x_stride, nc, dst + c0 * ldd, ldd, vec);
+        if (st != GHIP_STATUS_SUCCESS) return st;
+    }
+    return GHIP_STATUS_SUCCESS;
 }
 
 // one 2-D MUL_MAT (a single plane of src0, src1 and dst)
@@ -1049,8 +1087,13 @@ ghip_status mul_mat_plane(ghip_context *ctx, const ghip_tensor *a, const ghip_te
     }
     void *act = act_out ? act_out : ws;
     if (act_out) {
+        if (dense_type(p.wtype)) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat_act: F32 / F16 / BF16 weights quantize nothing");
         if (p.act_pre) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat_act: src1 is already quantized");
         return quantize_act(ctx, p, b, act, s);
+    }
+    if (dense_type(p.wtype)) {
+        if (sub || !d) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: F32 / F16 / BF16 weights have no integer sub-sums");
+        return run_dense(ctx, p, a, b, (float *)d->data, (int64_t)d->nb[1] / 4, s);
     }
     void *lay = lay_bytes ? (void *)((uint8_t *)ws + act_bytes) : nullptr;
     float *dst = d ? (float *)d->data : (float *)((uint8_t *)ws + act_bytes + lay_bytes);

@@ -1935,3 +1935,49 @@ int oracle_mul_mat_id_mxfp4(const void *as, int64_t n, int64_t rows, int64_t n_a
 }
 
 /* FLASH_ATTN_EXT lives in ggml_oracle_fa.c */
+
+/* half 2.7.1 bf16::from_f32 (RNE on the top 16 bits; NaN stays a quiet NaN) */
+uint16_t oracle_fp32_to_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    const uint32_t round = 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)((u + round) >> 16);
+}
+float oracle_bf16_to_fp32(uint16_t h) {
+    const uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* compute.rs:1700-1745 (F16 / BF16 weights: the activation row converted to
+ * the weight type, then the row dot) and :1680-1698 (F32 weights); the dots are
+ * ggml_vec_dot_f16 / _bf16 / _f32's scalar forms (vec_dot.rs:1700-1727): each
+ * product in f32 (exact for f16 and bf16 operands), summed in double */
+int oracle_mul_mat_dense(int type, const void *w, int64_t n, int64_t rows, const float *x, int64_t cols, float *out,
+                         int nthreads) {
+    if (type != OR_F32 && type != OR_F16 && type != OR_BF16) return -1;
+    float *xc = (float *)malloc(sizeof(float) * (size_t)(n * cols));
+    if (!xc) return -3;
+    for (int64_t i = 0; i < n * cols; i++)
+        xc[i] = type == OR_F16 ? H2F(F2H(x[i])) : type == OR_BF16 ? oracle_bf16_to_fp32(oracle_fp32_to_bf16(x[i])) : x[i];
+    const int nth = omp_threads(nthreads);
+#pragma omp parallel for num_threads(nth) schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        for (int64_t c = 0; c < cols; c++) {
+            const float *y = xc + c * n;
+            double s = 0.0;
+            for (int64_t i = 0; i < n; i++) {
+                float wv;
+                if (type == OR_F32) wv = ((const float *)w)[r * n + i];
+                else if (type == OR_F16) wv = H2F(((const uint16_t *)w)[r * n + i]);
+                else wv = oracle_bf16_to_fp32(((const uint16_t *)w)[r * n + i]);
+                s += (double)(wv * y[i]);
+            }
+            out[c * rows + r] = (float)s;
+        }
+    }
+    free(xc);
+    return 0;
+}

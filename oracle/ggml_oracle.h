@@ -22,14 +22,16 @@ extern "C" {
 
 /* ggml type ids (crates/ggml/src/types.rs:15) */
 enum {
-    OR_F32 = 0, OR_F16 = 1, OR_Q4_0 = 2, OR_Q4_1 = 3, OR_Q5_0 = 6, OR_Q5_1 = 7, OR_Q8_0 = 8, OR_Q8_1 = 9,
+    OR_F32 = 0, OR_F16 = 1, OR_BF16 = 30, OR_Q4_0 = 2, OR_Q4_1 = 3, OR_Q5_0 = 6, OR_Q5_1 = 7, OR_Q8_0 = 8, OR_Q8_1 = 9,
     OR_Q2_K = 10, OR_Q3_K = 11, OR_Q4_K = 12,
     OR_Q5_K = 13, OR_Q6_K = 14, OR_Q8_K = 15, OR_IQ4_NL = 20, OR_IQ4_XS = 23, OR_MXFP4 = 39, OR_NVFP4 = 40,
     OR_Q1_0 = 41, OR_Q2_0 = 42
 };
 
 /* ---- scalar helpers ---- */
-uint16_t oracle_fp32_to_fp16(float f);            /* half 2.7.1 from_f32 (RNE); pinned by every fp16 d in quants_ref.bin */
+uint16_t oracle_fp32_to_fp16(float f);
+uint16_t oracle_fp32_to_bf16(float f);            /* half 2.7.1 bf16::from_f32: RNE, NaN kept quiet */
+float oracle_bf16_to_fp32(uint16_t h);            /* half 2.7.1 from_f32 (RNE); pinned by every fp16 d in quants_ref.bin */
 float    oracle_fp16_to_fp32(uint16_t h);
 int32_t  oracle_nearest_int(float f);             /* quants.rs:13 */
 float    oracle_e8m0_to_fp32_half(uint8_t e);     /* quants.rs:682; pinned by closed form 2^(e-128) */
@@ -147,4 +149,13 @@ double oracle_wtime(void);
 #ifdef __cplusplus
 }
 #endif
+
+/* MUL_MAT with F32 / F16 / BF16 weights (compute.rs:1700-1745; vec_dot.rs:1700-1727):
+ * F16 / BF16: the f32 activations rounded to the weight type (RNE) and the
+ * exact products summed in double, rounded once (ggml_vec_dot_f16 / _bf16 scalar
+ * twins); F32: x * y rounded to f32, summed in double (ggml_vec_dot_f32 scalar).
+ * w: rows x n weights, x: cols x n, out: cols x rows.  Returns 0, or -1 for another type. */
+int oracle_mul_mat_dense(int type, const void *w, int64_t n, int64_t rows, const float *x, int64_t cols, float *out,
+                         int nthreads);
+
 #endif

@@ -18,6 +18,7 @@ Q4_1, Q5_1, Q8_1 = 3, 7, 9
 Q2_K, Q3_K = 10, 11
 IQ4_NL, IQ4_XS, NVFP4 = 20, 23, 40
 Q1_0, Q2_0 = 41, 42
+BF16 = 30
 BLOCK = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176),
          Q6_K: (256, 210), Q8_K: (256, 292), MXFP4: (32, 17), Q4_1: (32, 20), Q5_1: (32, 24), Q8_1: (32, 36),
          Q2_K: (256, 84), Q3_K: (256, 110), IQ4_NL: (32, 18), IQ4_XS: (256, 136), NVFP4: (64, 36),
@@ -96,6 +97,10 @@ def lib():
         L.oracle_mul_mat.argtypes = [C.c_int, vp, i64, i64, vp, i64, vp, vp, vp, C.c_int]
         L.oracle_mul_mat_act.restype = C.c_int
         L.oracle_mul_mat_act.argtypes = [C.c_int, i64, i64, vp, i64, vp]
+        L.oracle_mul_mat_dense.restype = C.c_int
+        L.oracle_mul_mat_dense.argtypes = [C.c_int, vp, i64, i64, vp, i64, vp, C.c_int]
+        L.oracle_fp32_to_bf16.restype = C.c_uint16
+        L.oracle_fp32_to_bf16.argtypes = [C.c_float]
         L.oracle_mul_mat_id_mxfp4.restype = C.c_int
         L.oracle_mul_mat_id_mxfp4.argtypes = [vp, i64, i64, i64, vp, i64, i64, vp, i64, vp, C.c_int]
         L.oracle_flash_attn_ext.restype = C.c_int
@@ -163,6 +168,20 @@ def mul_mat_act(ty, n, rows, x, cols):
     if rc < 0:
         raise ValueError(f"oracle_mul_mat_act rc={rc}")
     return act
+
+
+def mul_mat_dense(ty, w, n, rows, x, cols, nthreads=0):
+    """F32 / F16 / BF16 weights (w: rows x n as float32 or uint16 bits) -> out [cols, rows]"""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros((cols, rows), dtype=np.float32)
+    rc = lib().oracle_mul_mat_dense(ty, _p(np.ascontiguousarray(w)), n, rows, _p(x), cols, _p(out), nthreads)
+    if rc < 0:
+        raise ValueError(f"oracle_mul_mat_dense rc={rc}")
+    return out
+
+
+def fp32_to_bf16(f):
+    return lib().oracle_fp32_to_bf16(float(f))
 
 
 def mul_mat_id_mxfp4(as_q, n, rows, n_as, b, ne11, n_tokens, ids, n_ids, nthreads=0):

@@ -685,3 +685,44 @@ def test_q1_q2_quantizer_and_dequant_bit_exact(ty):
         assert np.array_equal(O.quantize(ty, x), q)
         got = O.dequantize(ty, q, n)
         assert np.array_equal(got.view(np.uint32), deq.view(np.uint32))
+
+
+def test_bf16_conversion_against_torch():
+    """the oracle's f32 -> bf16 (half's RNE) against torch's bfloat16 cast on
+    ties, subnormals, infinities and random bit patterns"""
+    import torch
+    rng = np.random.default_rng(3)
+    bits = np.concatenate([rng.integers(0, 2 ** 32, size=20000, dtype=np.uint64).astype(np.uint32),
+                           np.array([0x3f808000, 0x3f818000, 0x00008000, 0x00018000, 0x7f7fffff, 0x7f800000,
+                                     0xff800000, 0x80000000, 0x00000001, 0x7f7f8000], dtype=np.uint32)])
+    f = bits.view(np.float32)
+    fin = np.isfinite(f)
+    want = torch.from_numpy(f[fin].copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    got = np.array([O.fp32_to_bf16(v) for v in f[fin]], dtype=np.uint16)
+    assert np.array_equal(got, want)
+    nan = np.array([O.fp32_to_bf16(v) for v in f[~np.isfinite(f) & np.isnan(f)]], dtype=np.uint16)
+    assert np.all((nan & 0x7f80) == 0x7f80) and np.all(nan & 0x007f)
+
+
+@pytest.mark.parametrize("ty", [O.F32, O.F16, O.BF16])
+def test_dense_mul_mat_brute_force(ty):
+    """F32 / F16 / BF16 MUL_MAT: activations rounded to the weight type (numpy
+    float16 / torch bfloat16 casts), products in f32, summed in float64"""
+    import torch
+    rng = np.random.default_rng(ty + 5)
+    n, rows, cols = 1000, 7, 3
+    wf = rng.standard_normal((rows, n)).astype(np.float32)
+    x = rng.standard_normal((cols, n)).astype(np.float32)
+    if ty == O.F32:
+        w, wv, xv = wf, wf, x
+    elif ty == O.F16:
+        w = wf.astype(np.float16).view(np.uint16)
+        wv, xv = wf.astype(np.float16).astype(np.float32), x.astype(np.float16).astype(np.float32)
+    else:
+        w = torch.from_numpy(wf).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        wv = torch.from_numpy(wf).to(torch.bfloat16).float().numpy()
+        xv = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    prod = (wv[None, :, :] * xv[:, None, :]).astype(np.float32).astype(np.float64)
+    want = prod.sum(-1).astype(np.float32)
+    got = O.mul_mat_dense(ty, w, n, rows, x, cols)
+    assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1)) <= 1e-6

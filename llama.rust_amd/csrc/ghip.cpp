@@ -725,7 +725,9 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
             const size_t shmem = (size_t)NC * p.K + (size_t)NC * p.nb * 4 + (size_t)NC * p.nb * 16 * 4 +
                                  (size_t)rows_per_wg * waves_k * NC * sizeof(float);
             if (shmem > 160 * 1024) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: decode LDS image too large");
-            const int n_mat = (int)std::max<int64_t>(0, std::min<int64_t>(nc, p.n_mat - c0));
+            // (Q5_K: -1 selects the tiled kernel's fold, the reference's route from 8 rows)
+            const int n_mat = p.wtype == GHIP_TYPE_Q5_K ? (p.M >= 8 ? -1 : 0)
+                                                        : (int)std::max<int64_t>(0, std::min<int64_t>(nc, p.n_mat - c0));
             st = ctx->launch(name, dim3(grid), dim3(64 * waves_k * teams), shmem, s, (const uint8_t *)w,
                              (int64_t)p.w_row_bytes, (int)p.N, (int)p.nb, act + c0 * act_rb, (int64_t)act_rb, nc,
                              dst + c0 * ldd, (int64_t)ldd, sub_c, n_mat);
@@ -1825,7 +1827,8 @@ ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipS
     const std::string name = std::string(gemv_base(p0.wtype)) + (p0.wtype == GHIP_TYPE_Q6_K ? "_v2" : "") + "_f_c" +
                              std::to_string(NC) + "_r" + std::to_string(rb) + "x" + std::to_string(ng) +
                              (ns != 2 ? "s" + std::to_string(ns) : std::string()) + "_multi";
-    const int n_mat = (int)std::max<int64_t>(0, std::min<int64_t>(nc, p0.n_mat));
+    const int n_mat = p0.wtype == GHIP_TYPE_Q5_K ? (p0.M >= 8 ? -1 : 0)  // as in run_gemv
+                                                 : (int)std::max<int64_t>(0, std::min<int64_t>(nc, p0.n_mat));
     return ctx->launch(name, dim3((unsigned)wg), dim3(64 * waves_k * teams), shmem, s, g, (int64_t)p0.w_row_bytes,
                        (int)p0.nb, (const uint8_t *)nodes[0].src[1]->data, (int64_t)nodes[0].src[1]->nb[1], nc,
                        n_mat);

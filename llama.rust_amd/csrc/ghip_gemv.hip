@@ -74,6 +74,12 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
                                               int nb, const uint8_t *__restrict__ act, int64_t act_row_bytes,
                                               int ncols, float *__restrict__ dst, int64_t ldd,
                                               int32_t *__restrict__ sub, int n_mat, int wg = -1) {
+    // Q5_K: n_mat < 0 asks for the tiled kernel's fold (the reference's route
+    // from 8 activation rows, tiled.rs: per super-block d * is - dmin * im, then
+    // times d8), otherwise the row vec_dot's (main and min sums apart,
+    // vec_dot.rs:934-978); its activations never take the 4x8 values
+    const bool tiled_fold = Q5 && n_mat < 0;
+    if (Q5) n_mat = 0;
     // NG == 0: persistent grid (one row per group, K in one wavefront): each
     // team takes ceil(rows / (teams in the grid)) consecutive rows, streamed
     // through the two register slots, so every wavefront of the grid carries
@@ -253,18 +259,23 @@ __device__ __forceinline__ void gemv_q4K_impl(const uint8_t *__restrict__ W, int
                         s[1] = imb;
                     }
                 }
-                float part;
-                if constexpr (Q5) {
-                    // the super-block's integer sums first (its four lanes),
-                    // as the reference forms them: Q5_K's mins cancel main
-                    // terms of the same size, and per-lane float parts of
-                    // mixed sign would carry their own rounding
+                float tot;
+                if (tiled_fold) {
                     const int iab = quad_sum_dpp(ia), imb = quad_sum_dpp(im);
-                    part = i == 0 ? ac.d * fmaf(dw[rr], (float)iab, -(dmin[rr] * (float)imb)) : 0.0f;
+                    tot = wave_sum_dpp(i == 0 ? ac.d * fmaf(dw[rr], (float)iab, -(dmin[rr] * (float)imb)) : 0.0f);
+                } else if constexpr (Q5) {
+                    // the reference's two sums (vec_dot.rs:934-978): d * sumi
+                    // with d = d8 * dw, and the mins' integer sum times
+                    // -d8 * dmin, added at the end -- Q5_K's mins cancel main
+                    // terms of the same size, so the two are kept apart, each
+                    // from the super-block's exact integer sum
+                    const int iab = quad_sum_dpp(ia), imb = quad_sum_dpp(im);
+                    const float pm = i == 0 ? (ac.d * dw[rr]) * (float)iab : 0.0f;
+                    const float pn = i == 0 ? (-ac.d * dmin[rr]) * (float)imb : 0.0f;
+                    tot = wave_sum_dpp(pm) + wave_sum_dpp(pn);
                 } else {
-                    part = ac.d * fmaf(dw[rr], (float)ia, -(dmin[rr] * (float)im));
+                    tot = wave_sum_dpp(ac.d * fmaf(dw[rr], (float)ia, -(dmin[rr] * (float)im)));
                 }
-                const float tot = wave_sum_dpp(part);
                 // columns past ncols (the NC - ncols padding columns) are not stored
                 if (lane == 0 && c < ncols && rg + rr < r1) {
                     if (nwk == 1) dst[(int64_t)c * ldd + rg + rr] = tot;

@@ -12,6 +12,8 @@
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
+#define GHIP_GRID_QUAL static const
+#include "../llama.rust_amd/csrc/ghip_iq_grids.h"
 #include <time.h>
 #ifdef _OPENMP
 #include <omp.h>
@@ -1554,6 +1556,271 @@ float oracle_vec_dot_q2_0_q8_0(int n, const void *vx, const void *vy) {
     return sumf;
 }
 
+
+/* ---------------------------------------------------------------- IQ1 / IQ2 / IQ3
+ * Block layouts (blocks.rs:178-232) and the row dots of vec_dot.rs:1215-1590.
+ * Each *_lanes function forms the reference's eight lane sums sumi[l] of one
+ * super-block (lane l: elements 4l..4l+3 of every 32-element block, times the
+ * block's scale) exactly; the IQ1 types also their delta sums. */
+typedef struct { uint16_t d; uint16_t qs[32]; } blk_iq2_xxs;                                   /* 66 B */
+typedef struct { uint16_t d; uint16_t qs[32]; uint8_t scales[8]; } blk_iq2_xs;                  /* 74 B */
+typedef struct { uint16_t d; uint8_t qs[64]; uint8_t qh[8]; uint8_t scales[8]; } blk_iq2_s;     /* 82 B */
+typedef struct { uint16_t d; uint8_t qs[96]; } blk_iq3_xxs;                                    /* 98 B */
+typedef struct { uint16_t d; uint8_t qs[64]; uint8_t qh[8]; uint8_t signs[32]; uint8_t scales[4]; } blk_iq3_s; /* 110 B */
+typedef struct { uint16_t d; uint8_t qs[32]; uint16_t qh[8]; } blk_iq1_s;                      /* 50 B */
+typedef struct { uint8_t qs[32]; uint8_t qh[16]; uint8_t scales[8]; } blk_iq1_m;               /* 56 B */
+
+/* KSIGNS_IQ2XS (quants_k.rs:42): the 7 stored sign bits and their odd-parity bit */
+static inline int iq_sign(uint32_t s7, int e) {
+    const uint32_t s8 = s7 | ((uint32_t)__builtin_parity(s7) << 7);
+    return (s8 >> e) & 1 ? -1 : 1;
+}
+static inline int grid8(const uint64_t *g, uint32_t idx, int e) { return (int)((g[idx] >> (8 * e)) & 0xFF); }
+static inline int grid4(const uint32_t *g, uint32_t idx, int e) { return (int)((g[idx] >> (8 * e)) & 0xFF); }
+
+/* vec_dot.rs:1215-1255 */
+static void iq2_xxs_lanes(const blk_iq2_xxs *x, const blk_q8_K *y, int32_t sumi[8]) {
+    for (int l = 0; l < 8; l++) sumi[l] = 0;
+    int q8i = 0;
+    for (int it = 0; it < 4; it++) {
+        /* the 8 u16 of this 64-element group (qs[8 it .. 8 it + 7]) as 4 words */
+        uint32_t aux32[4];
+        for (int k = 0; k < 4; k++) aux32[k] = (uint32_t)x->qs[8 * it + 2 * k] | ((uint32_t)x->qs[8 * it + 2 * k + 1] << 16);
+        for (int h = 0; h < 2; h++) {
+            const uint32_t signs_word = aux32[1 + 2 * h];
+            const int ls = 2 * (int)(signs_word >> 28) + 1;
+            for (int l = 0; l < 8; l++) {
+                int s = 0;
+                for (int t = 0; t < 4; t++) {
+                    const int e = 4 * l + t;
+                    const int j = 8 * h + e / 8;
+                    const uint32_t idx = (aux32[j / 4] >> (8 * (j % 4))) & 0xFF;
+                    const int g = grid8(ghip_iq2xxs_grid, idx, e % 8);
+                    s += g * iq_sign((signs_word >> (7 * (e / 8))) & 127, e % 8) * y->qs[q8i + e];
+                }
+                sumi[l] += ls * s;
+            }
+            q8i += 32;
+        }
+    }
+}
+/* vec_dot.rs:1266-1305 */
+static void iq2_xs_lanes(const blk_iq2_xs *x, const blk_q8_K *y, int32_t sumi[8]) {
+    for (int l = 0; l < 8; l++) sumi[l] = 0;
+    int q8i = 0;
+    for (int it = 0; it < 2; it++)
+        for (int c = 0; c < 4; c++) {
+            const int b = 4 * it + c;
+            const int sc_lo = 2 * (x->scales[b] & 0x0F) + 1, sc_hi = 2 * (x->scales[b] >> 4) + 1;
+            for (int l = 0; l < 8; l++) {
+                const int sc = l < 4 ? sc_lo : sc_hi;
+                int s = 0;
+                for (int t = 0; t < 4; t++) {
+                    const int e = 4 * l + t;
+                    const uint32_t q2 = x->qs[16 * it + 4 * c + e / 8];
+                    s += grid8(ghip_iq2xs_grid, q2 & 511, e % 8) * iq_sign((q2 >> 9) & 127, e % 8) * y->qs[q8i + e];
+                }
+                sumi[l] += sc * s;
+            }
+            q8i += 32;
+        }
+}
+/* vec_dot.rs:1312-1352 */
+static void iq2_s_lanes(const blk_iq2_s *x, const blk_q8_K *y, int32_t sumi[8]) {
+    for (int l = 0; l < 8; l++) sumi[l] = 0;
+    int q8i = 0;
+    for (int t = 0; t < 4; t++)
+        for (int h = 0; h < 2; h++) {
+            const int v = 2 * t + h;
+            const int sc_lo = 2 * (x->scales[v] & 0x0F) + 1, sc_hi = 2 * (x->scales[v] >> 4) + 1;
+            for (int l = 0; l < 8; l++) {
+                const int sc = l < 4 ? sc_lo : sc_hi;
+                int s = 0;
+                for (int tt = 0; tt < 4; tt++) {
+                    const int e = 4 * l + tt, k = e / 8;
+                    const uint32_t idx = (uint32_t)x->qs[8 * t + 4 * h + k] | (((uint32_t)x->qh[v] << (8 - 2 * k)) & 0x300);
+                    const int sgn = (x->qs[32 + 8 * t + 4 * h + k] >> (e % 8)) & 1 ? -1 : 1;
+                    s += grid8(ghip_iq2s_grid, idx, e % 8) * sgn * y->qs[q8i + e];
+                }
+                sumi[l] += sc * s;
+            }
+            q8i += 32;
+        }
+}
+/* vec_dot.rs:1358-1397 */
+static void iq3_xxs_lanes(const blk_iq3_xxs *x, const blk_q8_K *y, int32_t sumi[8]) {
+    for (int l = 0; l < 8; l++) sumi[l] = 0;
+    int q8i = 0;
+    for (int it = 0; it < 4; it++)
+        for (int h = 0; h < 2; h++) {
+            const int gas = 64 + 8 * it + 4 * h;
+            uint32_t signs_word;
+            memcpy(&signs_word, x->qs + gas, 4);
+            const int ls = 2 * (int)(signs_word >> 28) + 1;
+            for (int l = 0; l < 8; l++) {
+                int s = 0;
+                for (int t = 0; t < 4; t++) {
+                    const int e = 4 * l + t;
+                    const uint32_t idx = x->qs[16 * it + 8 * h + e / 4];
+                    s += grid4(ghip_iq3xxs_grid, idx, e % 4) * iq_sign((signs_word >> (7 * (e / 8))) & 127, e % 8) *
+                         y->qs[q8i + e];
+                }
+                sumi[l] += ls * s;
+            }
+            q8i += 32;
+        }
+}
+/* vec_dot.rs:1403-1450 */
+static void iq3_s_lanes(const blk_iq3_s *x, const blk_q8_K *y, int32_t sumi[8]) {
+    for (int l = 0; l < 8; l++) sumi[l] = 0;
+    int q8i = 0, qsi = 0;
+    for (int t = 0; t < 4; t++) {
+        for (int h = 0; h < 2; h++) {
+            const int v = 2 * t + h;
+            const uint32_t qhv = x->qh[v];
+            const int ls = h == 0 ? 2 * (x->scales[t] & 0x0F) + 1 : 2 * (x->scales[t] >> 4) + 1;
+            for (int l = 0; l < 8; l++) {
+                int s = 0;
+                for (int tt = 0; tt < 4; tt++) {
+                    const int e = 4 * l + tt, k = e / 4;
+                    const uint32_t idx = (uint32_t)x->qs[qsi + 8 * h + k] | ((qhv << (8 - k)) & 256);
+                    const int sgn = (x->signs[8 * t + 4 * h + e / 8] >> (e % 8)) & 1 ? -1 : 1;
+                    s += grid4(ghip_iq3s_grid, idx, e % 4) * sgn * y->qs[q8i + e];
+                }
+                sumi[l] += ls * s;
+            }
+            q8i += 32;
+        }
+        qsi += 16;
+    }
+}
+/* vec_dot.rs:1460-1510; *sumi1: the delta sum (bsum pairs * sign * ls) */
+static void iq1_s_lanes(const blk_iq1_s *x, const blk_q8_K *y, int32_t sumi[8], int32_t *sumi1) {
+    for (int l = 0; l < 8; l++) sumi[l] = 0;
+    *sumi1 = 0;
+    int q8i = 0, qsi = 0;
+    for (int t = 0; t < 4; t++) {
+        for (int j = 0; j < 2; j++) {
+            const uint32_t qhw = x->qh[2 * t + j];
+            const int ls = 2 * (int)((qhw >> 12) & 7) + 1;
+            for (int l = 0; l < 8; l++) {
+                int s = 0;
+                for (int tt = 0; tt < 4; tt++) {
+                    const int e = 4 * l + tt, k = e / 8;
+                    const int shift = 8 - 3 * k;
+                    const uint32_t qhi = shift >= 0 ? qhw << shift : qhw >> 1;
+                    const uint32_t idx = (uint32_t)x->qs[qsi + 4 * j + k] | (qhi & 0x700);
+                    const int v = (int)(int8_t)(uint8_t)((ghip_iq1s_grid[idx] >> (8 * (e % 8))) & 0xFF);
+                    s += v * y->qs[q8i + e];
+                }
+                sumi[l] += ls * s;
+            }
+            const int sg = qhw & 0x8000 ? -1 : 1;
+            *sumi1 += ((int)y->bsums[4 * t + 2 * j] + (int)y->bsums[4 * t + 2 * j + 1]) * sg * ls;
+            q8i += 32;
+        }
+        qsi += 8;
+    }
+}
+static inline float iq1m_d(const blk_iq1_m *x) {
+    uint16_t sc[4];
+    for (int m = 0; m < 4; m++) sc[m] = (uint16_t)(x->scales[2 * m] | (x->scales[2 * m + 1] << 8));
+    const uint16_t u = (uint16_t)((sc[0] >> 12) | ((sc[1] >> 8) & 0x00f0) | ((sc[2] >> 4) & 0x0f00) | (sc[3] & 0xf000));
+    return H2F(u);
+}
+/* vec_dot.rs:1525-1590; sumi2: the delta lane sums */
+static void iq1_m_lanes(const blk_iq1_m *x, const blk_q8_K *y, int32_t sumi1[8], int32_t sumi2[8]) {
+    for (int l = 0; l < 8; l++) sumi1[l] = sumi2[l] = 0;
+    int q8i = 0, qsi = 0, qhi = 0;
+    for (int t = 0; t < 4; t++) {
+        const uint32_t sct = (uint32_t)(x->scales[2 * t] | (x->scales[2 * t + 1] << 8));
+        const int scv[2][2] = {{2 * (int)(sct & 7) + 1, 2 * (int)((sct >> 3) & 7) + 1},
+                               {2 * (int)((sct >> 6) & 7) + 1, 2 * (int)((sct >> 9) & 7) + 1}};
+        for (int j = 0; j < 2; j++) {
+            for (int l = 0; l < 8; l++) {
+                const int scl = scv[j][l >= 4];
+                int s = 0, sd = 0;
+                for (int tt = 0; tt < 4; tt++) {
+                    const int e = 4 * l + tt, k = e / 8;
+                    const uint32_t qhb = x->qh[qhi + 2 * j + k / 2];
+                    const uint32_t idx = (uint32_t)x->qs[qsi + 4 * j + k] | ((qhb << (8 - 4 * (k % 2))) & 0x700);
+                    const int v = (int)(int8_t)(uint8_t)((ghip_iq1s_grid[idx] >> (8 * (e % 8))) & 0xFF);
+                    s += v * y->qs[q8i + e];
+                    const int dsgn = qhb & (k % 2 == 0 ? 0x08 : 0x80) ? -1 : 1;
+                    sd += dsgn * y->qs[q8i + e];
+                }
+                sumi1[l] += scl * s;
+                sumi2[l] += scl * sd;
+            }
+            q8i += 32;
+        }
+        qsi += 8;
+        qhi += 4;
+    }
+}
+
+int oracle_iq_block_bytes(int type) {
+    switch (type) {
+    case OR_IQ2_XXS: return 66;
+    case OR_IQ2_XS: return 74;
+    case OR_IQ2_S: return 82;
+    case OR_IQ3_XXS: return 98;
+    case OR_IQ3_S: return 110;
+    case OR_IQ1_S: return 50;
+    case OR_IQ1_M: return 56;
+    default: return 0;
+    }
+}
+/* one super-block: the eight lane sums (the reference's accumulator input),
+ * the delta lane sums (IQ1, else zero), the weight scale d (f32) and the
+ * exact integer the tiled kernel forms (tiled.rs:440-640: the weights as
+ * grid * sign, IQ1 as 8 * grid + delta, times the sub-block scales) */
+static void iq_super_block(int type, const uint8_t *xb, const blk_q8_K *y, int32_t s[8], int32_t s2[8], float *d,
+                           int32_t *is) {
+    int32_t one = 0;
+    for (int l = 0; l < 8; l++) s2[l] = 0;
+    switch (type) {
+    case OR_IQ2_XXS: iq2_xxs_lanes((const blk_iq2_xxs *)xb, y, s); *d = H2F(((const blk_iq2_xxs *)xb)->d); break;
+    case OR_IQ2_XS: iq2_xs_lanes((const blk_iq2_xs *)xb, y, s); *d = H2F(((const blk_iq2_xs *)xb)->d); break;
+    case OR_IQ2_S: iq2_s_lanes((const blk_iq2_s *)xb, y, s); *d = H2F(((const blk_iq2_s *)xb)->d); break;
+    case OR_IQ3_XXS: iq3_xxs_lanes((const blk_iq3_xxs *)xb, y, s); *d = H2F(((const blk_iq3_xxs *)xb)->d); break;
+    case OR_IQ3_S: iq3_s_lanes((const blk_iq3_s *)xb, y, s); *d = H2F(((const blk_iq3_s *)xb)->d); break;
+    case OR_IQ1_S: iq1_s_lanes((const blk_iq1_s *)xb, y, s, &one); *d = H2F(((const blk_iq1_s *)xb)->d); break;
+    default: iq1_m_lanes((const blk_iq1_m *)xb, y, s, s2); *d = iq1m_d((const blk_iq1_m *)xb); break;
+    }
+    int32_t a = 0, b = 0;
+    for (int l = 0; l < 8; l++) a += s[l], b += s2[l];
+    *is = type == OR_IQ1_S ? 8 * a + one : type == OR_IQ1_M ? 8 * a + b : a;
+    if (type == OR_IQ1_S) s2[0] = one; /* the caller reads IQ1_S's delta sum from s2[0] */
+}
+/* the vec_dot final scale: 0.125 (IQ2), 0.25 (IQ3_XXS), 1 (IQ3_S) -- and for
+ * the tiled kernel the factor folded into its d (tiled.rs:454-618) */
+static float iq_scale(int type) {
+    return type == OR_IQ3_XXS ? 0.25f : type == OR_IQ3_S ? 1.0f : 0.125f;
+}
+
+/* the row dot of vec_dot.rs:1215-1590: per super-block d = d_w * d8 (IQ1_S:
+ * d8 * d_w), acc[l] = fma(d, sumi[l], acc[l]); IQ1_S adds the delta chain
+ * accum1 = fma(d, sumi1, accum1) and IQ1_M a second accumulator set */
+float oracle_vec_dot_iq(int type, int n, const void *vx, const void *vy) {
+    const int bs = oracle_iq_block_bytes(type);
+    const blk_q8_K *y = (const blk_q8_K *)vy;
+    float acc[8] = {0}, acc2[8] = {0}, accum1 = 0.0f;
+    for (int i = 0; i < n / QK_K; i++) {
+        int32_t s[8], s2[8], is;
+        float dw;
+        iq_super_block(type, (const uint8_t *)vx + (size_t)i * bs, &y[i], s, s2, &dw, &is);
+        const float d = (type == OR_IQ1_S || type == OR_IQ1_M) ? y[i].d * dw : dw * y[i].d;
+        for (int l = 0; l < 8; l++) acc[l] = fmaf(d, (float)s[l], acc[l]);
+        if (type == OR_IQ1_S) accum1 = fmaf(d, (float)s2[0], accum1);
+        if (type == OR_IQ1_M)
+            for (int l = 0; l < 8; l++) acc2[l] = fmaf(d, (float)s2[l], acc2[l]);
+    }
+    if (type == OR_IQ1_S) return hsum8(acc) + 0.125f * accum1;
+    if (type == OR_IQ1_M) return hsum8(acc) + 0.125f * hsum8(acc2);
+    return iq_scale(type) * hsum8(acc);
+}
+
 static int omp_threads(int nthreads) {
 #ifdef _OPENMP
     return nthreads > 0 ? nthreads : omp_get_max_threads();
@@ -1567,7 +1834,7 @@ static int route_of(int type, int64_t rows, int64_t cols) {
     if ((type == OR_Q4_0 || type == OR_Q4_K) && rows % 8 == 0) return ORACLE_ROUTE_REPACK;
     /* tiled.rs:203-242 formats, from 8 columns (tiled.rs:1300) */
     if ((type == OR_Q4_K || type == OR_Q5_K || type == OR_Q6_K || type == OR_Q2_K || type == OR_Q3_K ||
-         type == OR_IQ4_XS) && cols >= 8)
+         type == OR_IQ4_XS || oracle_iq_block_bytes(type)) && cols >= 8)
         return ORACLE_ROUTE_TILED;
     if (type == OR_Q4_0 && cols >= 2) return -1; /* tinyBLAS: out of scope */
     return ORACLE_ROUTE_VECDOT;
@@ -1610,7 +1877,8 @@ int oracle_mul_mat(int type, const void *w, int64_t n, int64_t rows, const float
     if (route < 0) return -1;
     if (type != OR_Q4_0 && type != OR_Q4_K && type != OR_Q6_K && type != OR_Q5_0 && type != OR_Q8_0 &&
         type != OR_Q5_K && type != OR_Q4_1 && type != OR_Q5_1 && type != OR_Q2_K && type != OR_Q3_K &&
-        type != OR_IQ4_NL && type != OR_IQ4_XS && type != OR_NVFP4 && type != OR_Q1_0 && type != OR_Q2_0)
+        type != OR_IQ4_NL && type != OR_IQ4_XS && type != OR_NVFP4 && type != OR_Q1_0 && type != OR_Q2_0 &&
+        !oracle_iq_block_bytes(type))
         return -2;
     const size_t rs = act_row_size(type, n);
     uint8_t *act = (uint8_t *)malloc(rs * (size_t)cols);
@@ -1841,6 +2109,29 @@ int oracle_mul_mat(int type, const void *w, int64_t n, int64_t rows, const float
                                                 : isum_q2_0((const blk_q2_0 *)wr + b, k, &a[b * gpb + k]);
                 out[c * rows + r] = type == OR_Q1_0 ? oracle_vec_dot_q1_0_q8_0((int)n, wr, a)
                                                     : oracle_vec_dot_q2_0_q8_0((int)n, wr, a);
+            }
+        }
+    } else if (oracle_iq_block_bytes(type)) {
+        /* IQ1 / IQ2 / IQ3: the row dot, or from 8 columns the tiled kernel's
+         * fold per super-block, res = (d * scale) * is, acc = fma(res, d8, acc)
+         * (tiled.rs:454-618, :822-836); sub-sum: that integer is */
+        const int64_t nb = n / QK_K;
+        const int bs = oracle_iq_block_bytes(type);
+#pragma omp parallel for num_threads(nth) schedule(static)
+        for (int64_t r = 0; r < rows; r++) {
+            const uint8_t *wr = (const uint8_t *)w + (size_t)r * nb * bs;
+            for (int64_t c = 0; c < cols; c++) {
+                const blk_q8_K *a = (const blk_q8_K *)(act + (size_t)c * rs);
+                float acc = 0.0f;
+                for (int64_t b = 0; b < nb; b++) {
+                    int32_t s8[8], s2[8], is;
+                    float dw;
+                    iq_super_block(type, wr + (size_t)b * bs, &a[b], s8, s2, &dw, &is);
+                    if (subsums) subsums[((size_t)c * rows + r) * nb + b] = is;
+                    const float td = dw * iq_scale(type);
+                    acc = fmaf(td * (float)is, a[b].d, acc);
+                }
+                out[c * rows + r] = route == ORACLE_ROUTE_TILED ? acc : oracle_vec_dot_iq(type, (int)n, wr, a);
             }
         }
     } else if (type == OR_IQ4_XS) {

@@ -22,7 +22,8 @@ extern "C" {
 
 /* ggml type ids (crates/ggml/src/types.rs:15) */
 enum {
-    OR_F32 = 0, OR_F16 = 1, OR_BF16 = 30, OR_Q4_0 = 2, OR_Q4_1 = 3, OR_Q5_0 = 6, OR_Q5_1 = 7, OR_Q8_0 = 8, OR_Q8_1 = 9,
+    OR_F32 = 0, OR_F16 = 1, OR_BF16 = 30, OR_IQ2_XXS = 16, OR_IQ2_XS = 17, OR_IQ3_XXS = 18, OR_IQ1_S = 19,
+    OR_IQ3_S = 21, OR_IQ2_S = 22, OR_IQ1_M = 29, OR_Q4_0 = 2, OR_Q4_1 = 3, OR_Q5_0 = 6, OR_Q5_1 = 7, OR_Q8_0 = 8, OR_Q8_1 = 9,
     OR_Q2_K = 10, OR_Q3_K = 11, OR_Q4_K = 12,
     OR_Q5_K = 13, OR_Q6_K = 14, OR_Q8_K = 15, OR_IQ4_NL = 20, OR_IQ4_XS = 23, OR_MXFP4 = 39, OR_NVFP4 = 40,
     OR_Q1_0 = 41, OR_Q2_0 = 42
@@ -157,5 +158,9 @@ double oracle_wtime(void);
  * w: rows x n weights, x: cols x n, out: cols x rows.  Returns 0, or -1 for another type. */
 int oracle_mul_mat_dense(int type, const void *w, int64_t n, int64_t rows, const float *x, int64_t cols, float *out,
                          int nthreads);
+
+/* IQ1 / IQ2 / IQ3 (vec_dot.rs:1215-1590): block bytes (0 for other types) and the row dot */
+int oracle_iq_block_bytes(int type);
+float oracle_vec_dot_iq(int type, int n, const void *vx, const void *vy);
 
 #endif

@@ -4,9 +4,9 @@ The files under ``parity/`` of fly88oj/llama.rust (MIT licence, copyright 2026
 fly88oj) are golden vectors that an instrumented llama.cpp build produced.  They
 are data (inputs and expected outputs), copied verbatim -- except
 ``tiled_ref.bin``, of which only the Q4_K, Q5_K and Q6_K MUL_MAT and
-MUL_MAT_ID sections are kept in ``tiled_ref_kq.bin`` and the Q2_K, Q3_K and
-IQ4_XS ones in ``tiled_ref_k23x.bin`` (the other IQ types are out of scope and
-the whole file is 18 MB).  Also one GGUF file of the reference's tokenizer tests
+MUL_MAT_ID sections are kept in ``tiled_ref_kq.bin``, the Q2_K, Q3_K and
+IQ4_XS ones in ``tiled_ref_k23x.bin`` and the smallest MUL_MAT section of each
+IQ1 / IQ2 / IQ3 type in ``tiled_ref_iq.bin`` (the whole file is 18 MB).  Also one GGUF file of the reference's tokenizer tests
 (crates/llama/tests/tokenizer_fixtures/vocab/ggml-vocab-llama-spm.gguf, a
 vocab-only model whose metadata vocab.rs:4290-4305 checks) for the GGUF
 reader's known-answer test.
@@ -31,15 +31,18 @@ WHOLE = [
     # on LCG block bytes and runtime-quantized activations
     "quants_ref_iq.bin", "vecdot3_ref.bin", "quants_ref_q1q2.bin",
 ]
-ROW_BYTES_PER_256 = {10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 23: 136}
+# row bytes per 256 elements of every type in tiled_ref.bin
+ROW_BYTES_PER_256 = {10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 23: 136,
+                     16: 66, 17: 74, 22: 82, 18: 98, 21: 110, 19: 50, 29: 56}
 
 
-def extract_tiled(src, dst, keep=(12, 13, 14)):
+def extract_tiled(src, dst, keep=(12, 13, 14), smallest_mm_only=False):
     """VMT1 sections (tiled.rs:2020-2090): kind 0 = MUL_MAT {xq, y, dst},
-    kind 1 = MUL_MAT_ID {n_as, n_ids, ne12; xq, y, ids, dst}."""
+    kind 1 = MUL_MAT_ID {n_as, n_ids, ne12; xq, y, ids, dst}.
+    smallest_mm_only: per kept type, only its smallest MUL_MAT section."""
     b = open(src, "rb").read()
     o = 0
-    out = bytearray()
+    secs = []
     while True:
         (magic,) = struct.unpack_from("<I", b, o)
         if magic == 0xFFFFFFFF:
@@ -48,18 +51,6 @@ def extract_tiled(src, dst, keep=(12, 13, 14)):
         o += 4
         kind, ty, n, rows, cols = struct.unpack_from("<5I", b, o)
         o += 20
-        if ty not in ROW_BYTES_PER_256:
-            # an IQ type: its row size is not needed to skip, the K-quant
-            # sections of each kind come first in the file
-            if kind == 0:
-                # skip to the next kind-1 section by scanning is not possible
-                # without the row size; the K-quant mm sections are all before
-                # the first IQ mm section, so jump to the mmid part
-                o = find_mmid(b, start)
-                if o < 0:
-                    break
-                continue
-            break
         rs = (n // 256) * ROW_BYTES_PER_256[ty]
         if kind == 0:
             o += rs * rows + n * cols * 4 + rows * cols * 4
@@ -68,22 +59,18 @@ def extract_tiled(src, dst, keep=(12, 13, 14)):
             o += 12
             o += rs * rows * n_as + n * cols * ne12 * 4 + n_ids * ne12 * 4 + rows * n_ids * ne12 * 4
         if ty in keep:
-            out += b[start:o]
+            secs.append((kind, ty, start, o))
+    if smallest_mm_only:
+        best = {}
+        for kind, ty, a, e in secs:
+            if kind == 0 and (ty not in best or e - a < best[ty][1] - best[ty][0]):
+                best[ty] = (a, e)
+        secs = [(0, ty, a, e) for kind, ty, a, e in secs if kind == 0 and best[ty] == (a, e)]
+    out = bytearray()
+    for _, _, a, e in secs:
+        out += b[a:e]
     out += struct.pack("<I", 0xFFFFFFFF)
     open(dst, "wb").write(bytes(out))
-
-
-def find_mmid(b, o):
-    """Offset of the first kind-1 VMT1 header at or after o (magic, kind == 1,
-    a K-quant type)."""
-    magic = struct.pack("<I", 0x31544D56)
-    while True:
-        o = b.find(magic, o + 1)
-        if o < 0:
-            return -1
-        kind, ty = struct.unpack_from("<2I", b, o + 4)
-        if kind == 1 and ty in ROW_BYTES_PER_256:
-            return o
 
 
 def main(parity_dir):
@@ -94,6 +81,9 @@ def main(parity_dir):
     extract_tiled(os.path.join(parity_dir, "tiled_ref.bin"), os.path.join(here, "tiled_ref_kq.bin"))
     # the Q2_K, Q3_K and IQ4_XS sections of the same file, in a file of their own
     extract_tiled(os.path.join(parity_dir, "tiled_ref.bin"), os.path.join(here, "tiled_ref_k23x.bin"), keep=(10, 11, 23))
+    # the smallest MUL_MAT section of each IQ1 / IQ2 / IQ3 type
+    extract_tiled(os.path.join(parity_dir, "tiled_ref.bin"), os.path.join(here, "tiled_ref_iq.bin"),
+                  keep=(16, 17, 18, 19, 21, 22, 29), smallest_mm_only=True)
     vocab = os.path.join(os.path.dirname(parity_dir), "crates", "llama", "tests", "tokenizer_fixtures", "vocab",
                          "ggml-vocab-llama-spm.gguf")
     shutil.copyfile(vocab, os.path.join(here, "ggml-vocab-llama-spm.gguf"))

@@ -19,18 +19,23 @@ Q2_K, Q3_K = 10, 11
 IQ4_NL, IQ4_XS, NVFP4 = 20, 23, 40
 Q1_0, Q2_0 = 41, 42
 BF16 = 30
+IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ3_S, IQ2_S, IQ1_M = 16, 17, 18, 19, 21, 22, 29
+IQ_GRID_TYPES = (IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M)
 BLOCK = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176),
          Q6_K: (256, 210), Q8_K: (256, 292), MXFP4: (32, 17), Q4_1: (32, 20), Q5_1: (32, 24), Q8_1: (32, 36),
          Q2_K: (256, 84), Q3_K: (256, 110), IQ4_NL: (32, 18), IQ4_XS: (256, 136), NVFP4: (64, 36),
-         Q1_0: (128, 18), Q2_0: (64, 18)}
+         Q1_0: (128, 18), Q2_0: (64, 18), IQ2_XXS: (256, 66), IQ2_XS: (256, 74), IQ2_S: (256, 82),
+         IQ3_XXS: (256, 98), IQ3_S: (256, 110), IQ1_S: (256, 50), IQ1_M: (256, 56)}
 # weight type -> activation type of its dot (vec_dot_type)
 ACT_TYPE = {Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K, Q4_1: Q8_1, Q5_1: Q8_1,
-            Q2_K: Q8_K, Q3_K: Q8_K, IQ4_NL: Q8_0, IQ4_XS: Q8_K, NVFP4: Q8_0, Q1_0: Q8_0, Q2_0: Q8_0}
+            Q2_K: Q8_K, Q3_K: Q8_K, IQ4_NL: Q8_0, IQ4_XS: Q8_K, NVFP4: Q8_0, Q1_0: Q8_0, Q2_0: Q8_0,
+            **{t: Q8_K for t in IQ_GRID_TYPES}}
 # int32 sub-sums per weight row and activation row (ghip_mul_mat_subsums layout)
 def subsums_per_row(ty, n):
     return {Q4_0: n // 32, Q5_0: n // 32, Q8_0: n // 32, Q4_K: (n // 256) * 2, Q5_K: (n // 256) * 2,
             Q6_K: n // 256, Q4_1: n // 32, Q5_1: n // 32, Q2_K: (n // 256) * 2, Q3_K: n // 256,
-            IQ4_NL: n // 32, IQ4_XS: n // 256, NVFP4: n // 16, Q1_0: n // 32, Q2_0: n // 32}[ty]
+            IQ4_NL: n // 32, IQ4_XS: n // 256, NVFP4: n // 16, Q1_0: n // 32, Q2_0: n // 32,
+            **{t: n // 256 for t in IQ_GRID_TYPES}}[ty]
 ROUTE_REPACK, ROUTE_TILED, ROUTE_VECDOT = 1, 2, 3
 
 
@@ -97,6 +102,8 @@ def lib():
         L.oracle_mul_mat.argtypes = [C.c_int, vp, i64, i64, vp, i64, vp, vp, vp, C.c_int]
         L.oracle_mul_mat_act.restype = C.c_int
         L.oracle_mul_mat_act.argtypes = [C.c_int, i64, i64, vp, i64, vp]
+        L.oracle_vec_dot_iq.restype = C.c_float
+        L.oracle_vec_dot_iq.argtypes = [C.c_int, C.c_int, vp, vp]
         L.oracle_mul_mat_dense.restype = C.c_int
         L.oracle_mul_mat_dense.argtypes = [C.c_int, vp, i64, i64, vp, i64, vp, C.c_int]
         L.oracle_fp32_to_bf16.restype = C.c_uint16
@@ -168,6 +175,11 @@ def mul_mat_act(ty, n, rows, x, cols):
     if rc < 0:
         raise ValueError(f"oracle_mul_mat_act rc={rc}")
     return act
+
+
+def vec_dot_iq(ty, n, xq, yq):
+    """the row dot of an IQ1 / IQ2 / IQ3 row with a Q8_K row (vec_dot.rs:1215-1590)"""
+    return np.float32(lib().oracle_vec_dot_iq(ty, n, _p(np.ascontiguousarray(xq)), _p(np.ascontiguousarray(yq))))
 
 
 def mul_mat_dense(ty, w, n, rows, x, cols, nthreads=0):

@@ -726,3 +726,27 @@ def test_dense_mul_mat_brute_force(ty):
     want = prod.sum(-1).astype(np.float32)
     got = O.mul_mat_dense(ty, w, n, rows, x, cols)
     assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1)) <= 1e-6
+
+
+@pytest.mark.parametrize("ty", [O.IQ2_XXS, O.IQ2_XS, O.IQ2_S, O.IQ3_XXS, O.IQ3_S, O.IQ1_S, O.IQ1_M])
+def test_iq_grid_vecdot_bit_exact(ty):
+    """vecdot3_ref.bin's IQ1 / IQ2 / IQ3 sections (the reference's x86 dots on
+    its block bytes and quantized activation row): bit for bit.  The grids,
+    sign parity, scale nibbles, qh bits and deltas all enter these."""
+    (sec,) = [s for s in fx.vecdot3_sections() if s[0] == ty]
+    _, n, xq, yq, want = sec
+    got = O.vec_dot_iq(ty, n, xq, yq)
+    assert got.view(np.uint32) == want.view(np.uint32), (got, want)
+
+
+@pytest.mark.parametrize("ty", [O.IQ2_XXS, O.IQ2_XS, O.IQ2_S, O.IQ3_XXS, O.IQ3_S, O.IQ1_S, O.IQ1_M])
+def test_iq_grid_tiled_sections(ty):
+    """tiled_ref_iq.bin (the reference's tiled kernel, tiled.rs:2183, 8+
+    columns): the oracle's tiled fold of the exact super-block integers
+    reproduces the dumped outputs bit for bit."""
+    secs = [s for s in fx.tiled_sections("tiled_ref_iq.bin") if s[0] == ty]
+    assert secs
+    for tid, n, rows, cols, xq, y, dst in secs:
+        got, route, _ = O.mul_mat(tid, xq.reshape(rows, -1), n, rows, y, cols)
+        assert route == O.ROUTE_TILED
+        assert np.array_equal(got.reshape(dst.shape).view(np.uint32), dst.view(np.uint32))

@@ -68,6 +68,13 @@ enum {
     GHIP_TYPE_IQ4_NL = 20,
     GHIP_TYPE_IQ4_XS = 23,
     GHIP_TYPE_I32 = 26,
+    GHIP_TYPE_IQ2_XXS = 16,
+    GHIP_TYPE_IQ2_XS = 17,
+    GHIP_TYPE_IQ3_XXS = 18,
+    GHIP_TYPE_IQ1_S = 19,
+    GHIP_TYPE_IQ3_S = 21,
+    GHIP_TYPE_IQ2_S = 22,
+    GHIP_TYPE_IQ1_M = 29,
     GHIP_TYPE_BF16 = 30,
     GHIP_TYPE_MXFP4 = 39,
     GHIP_TYPE_NVFP4 = 40,
@@ -132,7 +139,8 @@ int ghip_supports_op(int op, const ghip_tensor *dst, const ghip_tensor *const *s
 
 /* dst = src0 x src1 (GGML_OP_MUL_MAT, forward_mul_mat compute.rs:1420-1839).
  * src0: Q4_0 | Q4_1 | Q5_0 | Q5_1 | Q8_0 | Q2_K | Q3_K | Q4_K | Q5_K | Q6_K |
- *       IQ4_NL | IQ4_XS | NVFP4 | Q1_0 | Q2_0 weight [ne00=K, ne01=N, ne02, ne03], rows contiguous;
+ *       IQ4_NL | IQ4_XS | NVFP4 | Q1_0 | Q2_0 | IQ1_S | IQ1_M | IQ2_XXS | IQ2_XS | IQ2_S |
+ *       IQ3_XXS | IQ3_S weight [ne00=K, ne01=N, ne02, ne03], rows contiguous;
  *       or F32 | F16 | BF16 weight [ne00=K, ne01=N, ne02, ne03] (src1 must then be F32:
  *       the activations are rounded to the weight type, compute.rs:1680-1745; no sub-sums)
  * src1: F32 [K, ne11, ne12, ne13] (any strides nb11..nb13, nb10 == 4), or
@@ -178,6 +186,9 @@ ghip_status ghip_mul_mat_noalloc(ghip_context *ctx, const ghip_tensor *src0, con
  *   NVFP4: P = 4*nb, sum kvalue*q8 of each 16-element sub-block of 64-block b
  *   IQ4_XS: P = nb, sum_g (ls_g - 32) * sum kvalue*q8 of super-block b
  *   Q1_0: P = 4*nb, Q2_0: P = 2*nb, sum value*q8 of each 32-element group
+ *   IQ1 / IQ2 / IQ3: P = nb, per super-block sum over its 32-element blocks of
+ *     scale * sum value*q8 (IQ1: value = 8 * grid + delta), the integer
+ *     the reference's tiled kernel scales
  * subsums is a device pointer of ne11*N*P int32. */
 ghip_status ghip_mul_mat_subsums(ghip_context *ctx, const ghip_tensor *src0, const ghip_tensor *src1,
                                  int32_t *subsums, void *stream);

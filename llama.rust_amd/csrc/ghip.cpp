@@ -32,6 +32,13 @@ TypeInfo type_info(int t) {
     case GHIP_TYPE_F32: return {1, 4};
     case GHIP_TYPE_F16: return {1, 2};
     case GHIP_TYPE_BF16: return {1, 2};
+    case GHIP_TYPE_IQ2_XXS: return {256, 66};
+    case GHIP_TYPE_IQ2_XS: return {256, 74};
+    case GHIP_TYPE_IQ2_S: return {256, 82};
+    case GHIP_TYPE_IQ3_XXS: return {256, 98};
+    case GHIP_TYPE_IQ3_S: return {256, 110};
+    case GHIP_TYPE_IQ1_S: return {256, 50};
+    case GHIP_TYPE_IQ1_M: return {256, 56};
     case GHIP_TYPE_Q4_0: return {32, 18};
     case GHIP_TYPE_Q4_1: return {32, 20};
     case GHIP_TYPE_Q2_K: return {256, 84};
@@ -294,6 +301,11 @@ struct MulMatPlan {
     bool act_pre;     // src1 already holds the vec_dot_type blocks
 };
 
+// IQ1 / IQ2 / IQ3 codebook weights (ghip_iq.hip gemv_grid_impl), Q8_K activations
+bool grid_type(int t) {
+    return t == GHIP_TYPE_IQ2_XXS || t == GHIP_TYPE_IQ2_XS || t == GHIP_TYPE_IQ2_S || t == GHIP_TYPE_IQ3_XXS ||
+           t == GHIP_TYPE_IQ3_S || t == GHIP_TYPE_IQ1_S || t == GHIP_TYPE_IQ1_M;
+}
 // F32 / F16 / BF16 weights (ghip_dense.hip)
 bool dense_type(int t) { return t == GHIP_TYPE_F32 || t == GHIP_TYPE_F16 || t == GHIP_TYPE_BF16; }
 bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b, const ghip_tensor *d,
@@ -305,10 +317,10 @@ bool plan_mul_mat(ghip_context *ctx, const ghip_tensor *a, const ghip_tensor *b,
         a->type != GHIP_TYPE_Q4_1 && a->type != GHIP_TYPE_Q5_1 && a->type != GHIP_TYPE_Q2_K &&
         a->type != GHIP_TYPE_Q3_K && a->type != GHIP_TYPE_IQ4_NL && a->type != GHIP_TYPE_IQ4_XS &&
         a->type != GHIP_TYPE_NVFP4 && a->type != GHIP_TYPE_Q1_0 && a->type != GHIP_TYPE_Q2_0 &&
-        a->type != GHIP_TYPE_F32 && a->type != GHIP_TYPE_F16 && a->type != GHIP_TYPE_BF16) {
+        a->type != GHIP_TYPE_F32 && a->type != GHIP_TYPE_F16 && a->type != GHIP_TYPE_BF16 && !grid_type(a->type)) {
         st = ctx->fail(st,
                        "mul_mat: src0 type %d not supported (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, "
-                       "IQ4_NL, IQ4_XS, NVFP4, Q1_0, Q2_0, F32, F16, BF16)",
+                       "IQ4_NL, IQ4_XS, NVFP4, Q1_0, Q2_0, IQ1_S, IQ1_M, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, F32, F16, BF16)",
                        a->type);
         return false;
     }
@@ -412,6 +424,13 @@ const char *gemv_base(int wtype) {
     case GHIP_TYPE_NVFP4: return "ghip_gemv_nvfp4";
     case GHIP_TYPE_Q1_0: return "ghip_gemv_q1_0";
     case GHIP_TYPE_Q2_0: return "ghip_gemv_q2_0";
+    case GHIP_TYPE_IQ2_XXS: return "ghip_gemv_iq2_xxs";
+    case GHIP_TYPE_IQ2_XS: return "ghip_gemv_iq2_xs";
+    case GHIP_TYPE_IQ2_S: return "ghip_gemv_iq2_s";
+    case GHIP_TYPE_IQ3_XXS: return "ghip_gemv_iq3_xxs";
+    case GHIP_TYPE_IQ3_S: return "ghip_gemv_iq3_s";
+    case GHIP_TYPE_IQ1_S: return "ghip_gemv_iq1_s";
+    case GHIP_TYPE_IQ1_M: return "ghip_gemv_iq1_m";
     default: return "ghip_gemv_q4_0";
     }
 }
@@ -426,7 +445,7 @@ bool gemv_pair(int wtype) {
 // table-lookup 4-bit and 1-/2-bit code types (ghip_iq.hip): one decode lane per 32 elements
 bool lut_type(int wtype) {
     return wtype == GHIP_TYPE_IQ4_NL || wtype == GHIP_TYPE_IQ4_XS || wtype == GHIP_TYPE_NVFP4 ||
-           wtype == GHIP_TYPE_Q1_0 || wtype == GHIP_TYPE_Q2_0;
+           wtype == GHIP_TYPE_Q1_0 || wtype == GHIP_TYPE_Q2_0 || grid_type(wtype);
 }
 // weights the int8-MFMA GEMM ghip_gemm_q8 takes as int8 codes with one scale
 // per 32 elements (NVFP4's scales are per 16: its prefill runs the decode
@@ -1298,18 +1317,25 @@ const char *mmid_kernel_type(int t) {
     case GHIP_TYPE_IQ4_XS: return "iq4_xs";
     case GHIP_TYPE_NVFP4: return "nvfp4";
     case GHIP_TYPE_Q1_0: return "q1_0";
+    case GHIP_TYPE_IQ2_XXS: return "iq2_xxs";
+    case GHIP_TYPE_IQ2_XS: return "iq2_xs";
+    case GHIP_TYPE_IQ2_S: return "iq2_s";
+    case GHIP_TYPE_IQ3_XXS: return "iq3_xxs";
+    case GHIP_TYPE_IQ3_S: return "iq3_s";
+    case GHIP_TYPE_IQ1_S: return "iq1_s";
+    case GHIP_TYPE_IQ1_M: return "iq1_m";
     default: return "q2_0";
     }
 }
 int mmid_act_type(int t) {
     if (t == GHIP_TYPE_Q4_1 || t == GHIP_TYPE_Q5_1) return GHIP_TYPE_Q8_1;
-    if (t == GHIP_TYPE_Q2_K || t == GHIP_TYPE_Q3_K || t == GHIP_TYPE_IQ4_XS) return GHIP_TYPE_Q8_K;
+    if (t == GHIP_TYPE_Q2_K || t == GHIP_TYPE_Q3_K || t == GHIP_TYPE_IQ4_XS || grid_type(t)) return GHIP_TYPE_Q8_K;
     return GHIP_TYPE_Q8_0;
 }
 bool mmid_generic_type(int t) {
     return t == GHIP_TYPE_Q4_0 || t == GHIP_TYPE_Q5_0 || t == GHIP_TYPE_Q8_0 || t == GHIP_TYPE_Q4_1 ||
            t == GHIP_TYPE_Q5_1 || t == GHIP_TYPE_Q2_K || t == GHIP_TYPE_Q3_K || t == GHIP_TYPE_IQ4_NL ||
-           t == GHIP_TYPE_IQ4_XS || t == GHIP_TYPE_NVFP4 || t == GHIP_TYPE_Q1_0 || t == GHIP_TYPE_Q2_0;
+           t == GHIP_TYPE_IQ4_XS || t == GHIP_TYPE_NVFP4 || t == GHIP_TYPE_Q1_0 || t == GHIP_TYPE_Q2_0 || grid_type(t);
 }
 // forward_mul_mat_id (compute.rs:1917-2202) with MXFP4, Q4_K, Q5_K or Q6_K
 // experts (the K-quants' vec_dot_type is Q8_K, compute.rs:1926-1929).

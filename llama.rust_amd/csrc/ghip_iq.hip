@@ -24,6 +24,8 @@
 // ghip_gemm.hip; IQ4_XS activations are Q8_K rows written in that GEMM's
 // layout (ghip_gemm_act_q8K_q8).
 #include "ghip_common.h"
+#define GHIP_GRID_QUAL static __device__ const
+#include "ghip_iq_grids.h"
 #include "ghip_q8k.h"
 
 namespace {
@@ -387,3 +389,227 @@ MMID_LUT(iq4_xs, WT_IQ4_XS)
 MMID_LUT(nvfp4, WT_NVFP4)
 MMID_LUT(q1_0, WT_Q1_0)
 MMID_LUT(q2_0, WT_Q2_0)
+
+// ------------------------------------------------ IQ1 / IQ2 / IQ3 weights
+// vec_dot.rs:1215-1590 (the reference's tiled kernel, tiled.rs:440-640, forms
+// the same integers).  One lane per 32-element block, its super-block's 8
+// blocks in 8 consecutive lanes.  The lane decodes its 32 weights from the
+// codebook (ghip_iq_grids.h) into signed int8 -- magnitudes from the grid
+// entry, signs from 7 stored bits and their parity (IQ2_XXS, IQ2_XS, IQ3_XXS)
+// or stored sign bytes (IQ2_S, IQ3_S), IQ1 values -1 / 0 / 1 -- and forms
+//   t = sum over its 8-element groups k of sc_k * (F * dot_k + delta_k * sum_k q8)
+// (sc_k: the block's or 16-element half's odd scale; F = 8 and delta_k = +-1 for
+// the IQ1 types, else F = 1, delta 0), the exact integer the reference's lanes
+// sum.  The super-block's 8 lanes add their t exactly; that integer is
+// scaled once by d * f (f = 1/8 for IQ2 / IQ1, 1/4 for IQ3_XXS, 1 for IQ3_S)
+// and the block scale d8 of the activation row.  Sub-sums: that integer per
+// super-block.
+constexpr int WT_IQ2_XXS = 16, WT_IQ2_XS = 17, WT_IQ3_XXS = 18, WT_IQ1_S = 19, WT_IQ3_S = 21, WT_IQ2_S = 22,
+              WT_IQ1_M = 29;
+template <int WT> constexpr int grid_block_bytes() {
+    return WT == WT_IQ2_XXS ? 66 : WT == WT_IQ2_XS ? 74 : WT == WT_IQ2_S ? 82 : WT == WT_IQ3_XXS ? 98
+           : WT == WT_IQ3_S ? 110 : WT == WT_IQ1_S ? 50 : 56;
+}
+template <int WT> constexpr float grid_scale() { return WT == WT_IQ3_XXS ? 0.25f : WT == WT_IQ3_S ? 1.0f : 0.125f; }
+// 8 grid magnitudes (bytes) with the sign bits s8 (bit i: byte i negative)
+DEV uint2 signed8(uint64_t gv, uint32_t s8) {
+    const uint32_t lo = (uint32_t)gv, hi = (uint32_t)(gv >> 32);
+    const uint32_t mlo = ((s8 & 0xFu) * 0x00204081u) & 0x01010101u, mhi = (((s8 >> 4) & 0xFu) * 0x00204081u) & 0x01010101u;
+    // -g per marked byte: (g ^ 0xFF) + 1, no carry out of a byte since g >= 1
+    return make_uint2((lo ^ (mlo * 0xFFu)) + mlo, (hi ^ (mhi * 0xFFu)) + mhi);
+}
+DEV uint32_t signed4(uint32_t gv, uint32_t s4) {
+    const uint32_t m = ((s4 & 0xFu) * 0x00204081u) & 0x01010101u;
+    return (gv ^ (m * 0xFFu)) + m;
+}
+DEV uint32_t parity7(uint32_t s7) { return s7 | ((__popc(s7) & 1u) << 7); }
+
+// block ib of the super-block at blk: its 32 signed values v[0..7] (elements
+// 4i..4i+3 in v[i]), the scales of its halves and the IQ1 deltas of its 8-element groups
+template <int WT>
+DEV void grid_block(const uint8_t *__restrict__ blk, int ib, uint32_t v[8], int &sc0, int &sc1, int dl[4]) {
+    dl[0] = dl[1] = dl[2] = dl[3] = 0;
+    if constexpr (WT == WT_IQ2_XXS) {
+        const uint2 a = ld8(blk + 2 + 8 * ib);  // 4 index bytes | signs word (ls in its top 4 bits)
+        sc0 = sc1 = 2 * (int)(a.y >> 28) + 1;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint2 t = signed8(ghip_iq2xxs_grid[(a.x >> (8 * k)) & 0xFF], parity7((a.y >> (7 * k)) & 127));
+            v[2 * k] = t.x;
+            v[2 * k + 1] = t.y;
+        }
+    } else if constexpr (WT == WT_IQ2_XS) {
+        const uint2 a = ld8(blk + 2 + 8 * ib);  // 4 u16: 9-bit index, 7 sign bits
+        const uint32_t sc = blk[66 + ib];
+        sc0 = 2 * (int)(sc & 15) + 1;
+        sc1 = 2 * (int)(sc >> 4) + 1;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t q2 = ((k < 2 ? a.x : a.y) >> (16 * (k & 1))) & 0xFFFF;
+            const uint2 t = signed8(ghip_iq2xs_grid[q2 & 511], parity7(q2 >> 9));
+            v[2 * k] = t.x;
+            v[2 * k + 1] = t.y;
+        }
+    } else if constexpr (WT == WT_IQ2_S) {
+        const uint32_t idx = ld4(blk + 2 + 4 * ib), sg = ld4(blk + 34 + 4 * ib);
+        const uint32_t qh = blk[66 + ib], sc = blk[74 + ib];
+        sc0 = 2 * (int)(sc & 15) + 1;
+        sc1 = 2 * (int)(sc >> 4) + 1;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t i = ((idx >> (8 * k)) & 0xFF) | ((qh << (8 - 2 * k)) & 0x300);
+            const uint2 t = signed8(ghip_iq2s_grid[i], (sg >> (8 * k)) & 0xFF);
+            v[2 * k] = t.x;
+            v[2 * k + 1] = t.y;
+        }
+    } else if constexpr (WT == WT_IQ3_XXS) {
+        const uint2 a = ld8(blk + 2 + 8 * ib);    // 8 index bytes (4 values each)
+        const uint32_t sw = ld4(blk + 66 + 4 * ib);  // signs word, ls in its top 4 bits
+        sc0 = sc1 = 2 * (int)(sw >> 28) + 1;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t s8 = parity7((sw >> (7 * k)) & 127);
+            const uint32_t w = k < 2 ? a.x : a.y;
+            v[2 * k] = signed4(ghip_iq3xxs_grid[(w >> (16 * (k & 1))) & 0xFF], s8);
+            v[2 * k + 1] = signed4(ghip_iq3xxs_grid[(w >> (16 * (k & 1) + 8)) & 0xFF], s8 >> 4);
+        }
+    } else if constexpr (WT == WT_IQ3_S) {
+        const uint2 a = ld8(blk + 2 + 8 * ib);  // 8 index bytes
+        const uint32_t qh = blk[66 + ib], sg = ld4(blk + 74 + 4 * ib);
+        const uint32_t sc = (blk[106 + (ib >> 1)] >> (4 * (ib & 1))) & 15;
+        sc0 = sc1 = 2 * (int)sc + 1;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t i = (((k < 4 ? a.x : a.y) >> (8 * (k & 3))) & 0xFF) | ((qh << (8 - k)) & 256);
+            v[k] = signed4(ghip_iq3s_grid[i], (sg >> (4 * k)) & 0xF);
+        }
+    } else if constexpr (WT == WT_IQ1_S) {
+        const uint32_t idx = ld4(blk + 2 + 4 * ib), qhw = ld2(blk + 34 + 2 * ib);
+        sc0 = sc1 = 2 * (int)((qhw >> 12) & 7) + 1;
+        const int d = qhw & 0x8000 ? -1 : 1;
+        dl[0] = dl[1] = dl[2] = dl[3] = d;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint64_t gv = ghip_iq1s_grid[((idx >> (8 * k)) & 0xFF) | (((qhw >> (3 * k)) & 7) << 8)];
+            v[2 * k] = (uint32_t)gv;
+            v[2 * k + 1] = (uint32_t)(gv >> 32);
+        }
+    } else {  // IQ1_M
+        const uint32_t idx = ld4(blk + 4 * ib), qh2 = ld2(blk + 32 + 2 * ib);
+        const uint32_t sct = ld2(blk + 48 + 2 * (ib >> 1)), j = ib & 1;
+        sc0 = 2 * (int)((sct >> (6 * j)) & 7) + 1;
+        sc1 = 2 * (int)((sct >> (6 * j + 3)) & 7) + 1;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t qhb = (qh2 >> (8 * (k >> 1))) & 0xFF;
+            const uint32_t i = ((idx >> (8 * k)) & 0xFF) | ((qhb << (8 - 4 * (k & 1))) & 0x700);
+            const uint64_t gv = ghip_iq1s_grid[i];
+            v[2 * k] = (uint32_t)gv;
+            v[2 * k + 1] = (uint32_t)(gv >> 32);
+            dl[k] = qhb & (k & 1 ? 0x80 : 0x08) ? -1 : 1;
+        }
+    }
+}
+// the super-block's weight scale d (f16; IQ1_M: assembled from the top
+// nibbles of its four scale words)
+template <int WT> DEV float grid_d(const uint8_t *__restrict__ blk) {
+    if constexpr (WT == WT_IQ1_M) {
+        const uint2 s = ld8(blk + 48);
+        const uint32_t s0 = s.x & 0xFFFF, s1 = s.x >> 16, s2 = s.y & 0xFFFF, s3 = s.y >> 16;
+        return h2f((s0 >> 12) | ((s1 >> 8) & 0x00f0) | ((s2 >> 4) & 0x0f00) | (s3 & 0xf000));
+    } else {
+        return h2f(ld2(blk));
+    }
+}
+
+template <int WT, int NC, bool SUBSUMS>
+__device__ __forceinline__ void gemv_grid_impl(const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb,
+                                               const uint8_t *__restrict__ act, int64_t act_row_bytes, int ncols,
+                                               float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {
+    constexpr int BS = grid_block_bytes<WT>();
+    constexpr bool IQ1 = WT == WT_IQ1_S || WT == WT_IQ1_M;
+    __shared__ float red[RB * 8 * NC];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int ng = 8 * nb;
+    const int g = 64 * w + lane;
+    const bool valid = g < ng;
+    const int gc = valid ? g : ng - 1;
+    const int ib = gc & 7;
+    const int r0 = (int)blockIdx.x * RB;
+    const int nr = min(RB, rows - r0);
+    // activations: this block's 32 codes, the per-8 sums (IQ1) and d8
+    uint4 ya[NC], yb[NC];
+    float dy[NC];
+    int ys[NC][4];
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        ya[c] = yb[c] = make_uint4(0, 0, 0, 0);
+        dy[c] = 0.0f;
+        if (c < ncols && valid) {
+            const uint8_t *A = act + c * act_row_bytes + (int64_t)(g >> 3) * Q8K_BYTES;
+            dy[c] = __uint_as_float(ld4(A));
+            ya[c] = ld16(A + 4 + 32 * ib);
+            yb[c] = ld16(A + 20 + 32 * ib);
+        }
+        const uint32_t y[8] = {ya[c].x, ya[c].y, ya[c].z, ya[c].w, yb[c].x, yb[c].y, yb[c].z, yb[c].w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) ys[c][k] = IQ1 ? dot4(y[2 * k + 1], 0x01010101u, dot4(y[2 * k], 0x01010101u, 0)) : 0;
+    }
+    float part[NC][RB];
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+        const uint8_t *blk = W + (int64_t)min(r0 + rr, rows - 1) * w_row_bytes + (int64_t)(gc >> 3) * BS;
+        uint32_t v[8];
+        int sc0, sc1, dl[4];
+        grid_block<WT>(blk, ib, v, sc0, sc1, dl);
+        const float td = grid_d<WT>(blk) * grid_scale<WT>();
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const uint32_t y[8] = {ya[c].x, ya[c].y, ya[c].z, ya[c].w, yb[c].x, yb[c].y, yb[c].z, yb[c].w};
+            int t = 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                int s = dot4(v[2 * k + 1], y[2 * k + 1], dot4(v[2 * k], y[2 * k], 0));
+                if (IQ1) s = 8 * s + dl[k] * ys[c][k];
+                t += (k < 2 ? sc0 : sc1) * s;
+            }
+            // the super-block's exact integer (its 8 blocks in 8 consecutive lanes)
+            t += __shfl_xor(t, 1, 64);
+            t += __shfl_xor(t, 2, 64);
+            t += __shfl_xor(t, 4, 64);
+            if (SUBSUMS && ib == 0 && valid && c < ncols && rr < nr)
+                sub[((int64_t)c * rows + r0 + rr) * nb + (g >> 3)] = t;
+            part[c][rr] = valid && ib == 0 ? (td * (float)t) * dy[c] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NC; c++) stash_rows(red, part[c], lane, w, nw, c, NC);
+    finish_rows(red, r0, nr, ncols, NC, nw, dst, ldd);
+}
+
+#define GEMV_GRID_INST(TN, WT, NC)                                                                              \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_##TN##_c##NC(                                    \
+        const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb, const uint8_t *__restrict__ act,   \
+        int64_t act_row_bytes, int ncols, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {     \
+        gemv_grid_impl<WT, NC, false>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub);       \
+    }                                                                                                            \
+    extern "C" __global__ void __launch_bounds__(512) ghip_gemv_##TN##_sub_c##NC(                                \
+        const uint8_t *__restrict__ W, int64_t w_row_bytes, int rows, int nb, const uint8_t *__restrict__ act,   \
+        int64_t act_row_bytes, int ncols, float *__restrict__ dst, int64_t ldd, int32_t *__restrict__ sub) {     \
+        gemv_grid_impl<WT, NC, true>(W, w_row_bytes, rows, nb, act, act_row_bytes, ncols, dst, ldd, sub);        \
+    }
+#define GEMV_GRID_TYPE(TN, WT)                                                                                   \
+    GEMV_GRID_INST(TN, WT, 1) GEMV_GRID_INST(TN, WT, 2) GEMV_GRID_INST(TN, WT, 4) GEMV_GRID_INST(TN, WT, 8)     \
+    extern "C" __global__ void __launch_bounds__(512) ghip_mmid_gemv_##TN(MMID_ARGS) {                           \
+        MMID_PAIR(q) gemv_grid_impl<WT, 1, false>(q.W, as_nb1, rows, nb, q.act, act_rb, 1, q.dst, 0, nullptr);  \
+    }                                                                                                            \
+    extern "C" __global__ void __launch_bounds__(512) ghip_mmid_gemv_##TN##_sub(MMID_ARGS) {                     \
+        MMID_PAIR(q) gemv_grid_impl<WT, 1, true>(q.W, as_nb1, rows, nb, q.act, act_rb, 1, q.dst, 0, q.sub);     \
+    }
+GEMV_GRID_TYPE(iq2_xxs, WT_IQ2_XXS)
+GEMV_GRID_TYPE(iq2_xs, WT_IQ2_XS)
+GEMV_GRID_TYPE(iq2_s, WT_IQ2_S)
+GEMV_GRID_TYPE(iq3_xxs, WT_IQ3_XXS)
+GEMV_GRID_TYPE(iq3_s, WT_IQ3_S)
+GEMV_GRID_TYPE(iq1_s, WT_IQ1_S)
+GEMV_GRID_TYPE(iq1_m, WT_IQ1_M)

@@ -18,14 +18,18 @@ Q2_K, Q3_K = 10, 11
 IQ4_NL, IQ4_XS, NVFP4 = 20, 23, 40
 Q1_0, Q2_0 = 41, 42
 BF16 = 30
+IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ3_S, IQ2_S, IQ1_M = 16, 17, 18, 19, 21, 22, 29
 OP_MUL_MAT, OP_MUL_MAT_ID, OP_FLASH_ATTN_EXT = 1, 2, 3
 BLOCK = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210),
          Q8_K: (256, 292), MXFP4: (32, 17), F32: (1, 4), F16: (1, 2), I32: (1, 4),
          Q4_1: (32, 20), Q5_1: (32, 24), Q8_1: (32, 36), Q2_K: (256, 84), Q3_K: (256, 110),
-         IQ4_NL: (32, 18), IQ4_XS: (256, 136), NVFP4: (64, 36), Q1_0: (128, 18), Q2_0: (64, 18), BF16: (1, 2)}
+         IQ4_NL: (32, 18), IQ4_XS: (256, 136), NVFP4: (64, 36), Q1_0: (128, 18), Q2_0: (64, 18), BF16: (1, 2),
+         IQ2_XXS: (256, 66), IQ2_XS: (256, 74), IQ2_S: (256, 82), IQ3_XXS: (256, 98), IQ3_S: (256, 110),
+         IQ1_S: (256, 50), IQ1_M: (256, 56)}
 # weight type -> the activation type of its dot (vec_dot_type)
 ACT_TYPE = {Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K, Q4_1: Q8_1, Q5_1: Q8_1,
-            Q2_K: Q8_K, Q3_K: Q8_K, IQ4_NL: Q8_0, IQ4_XS: Q8_K, NVFP4: Q8_0, Q1_0: Q8_0, Q2_0: Q8_0, F32: F32, F16: F32, BF16: F32}
+            Q2_K: Q8_K, Q3_K: Q8_K, IQ4_NL: Q8_0, IQ4_XS: Q8_K, NVFP4: Q8_0, Q1_0: Q8_0, Q2_0: Q8_0, F32: F32, F16: F32, BF16: F32,
+            IQ2_XXS: Q8_K, IQ2_XS: Q8_K, IQ2_S: Q8_K, IQ3_XXS: Q8_K, IQ3_S: Q8_K, IQ1_S: Q8_K, IQ1_M: Q8_K}
 # int32 sub-sums per weight block (ghip_mul_mat_subsums)
 SUBSUMS_PER_BLOCK = {Q4_K: 2, Q5_K: 2, Q2_K: 2, NVFP4: 4, Q1_0: 4, Q2_0: 2}
 

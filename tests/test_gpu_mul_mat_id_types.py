@@ -20,7 +20,7 @@ import oracle_lib as O
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
-TILED = (O.Q2_K, O.Q3_K, O.IQ4_XS)
+TILED = (O.Q2_K, O.Q3_K, O.IQ4_XS) + tuple(O.IQ_GRID_TYPES)
 
 
 @pytest.fixture(scope="module")
@@ -38,6 +38,9 @@ def rel_err(got, want):
 def weights(ty, n_as, rows, n, rng):
     """the reference's quantizer where the oracle has it, else model-scale
     random blocks (f16 scales of a quantized N(0, 0.02) matrix)"""
+    if ty in O.IQ_GRID_TYPES:
+        import test_gpu_mul_mat_iq as IQ
+        return IQ.random_blocks(ty, n_as * rows, n, int(rng.integers(1 << 30))).reshape(n_as, rows, -1)
     if ty in (O.Q2_K, O.Q3_K, O.IQ4_NL, O.IQ4_XS, O.NVFP4):
         qk, bs = O.BLOCK[ty]
         b = rng.integers(0, 256, size=(n_as * rows, n // qk, bs), dtype=np.uint8)
@@ -84,7 +87,7 @@ def oracle_mmid(ty, w, n, rows, ne11, y, ids):
     return ref, vd, sub
 
 
-TYPES = [O.Q4_0, O.Q4_1, O.Q5_0, O.Q5_1, O.Q8_0, O.Q2_K, O.Q3_K, O.IQ4_NL, O.IQ4_XS, O.NVFP4, O.Q1_0, O.Q2_0]
+TYPES = [O.Q4_0, O.Q4_1, O.Q5_0, O.Q5_1, O.Q8_0, O.Q2_K, O.Q3_K, O.IQ4_NL, O.IQ4_XS, O.NVFP4, O.Q1_0, O.Q2_0] + list(O.IQ_GRID_TYPES)
 
 
 @pytest.mark.parametrize("ty", TYPES)

@@ -63,7 +63,8 @@ def _run(ty, k, n, m, planes=(1, 1), sub=False):
 def _types():
     import ghip
     return [ghip.Q4_0, ghip.Q4_1, ghip.Q5_0, ghip.Q5_1, ghip.Q8_0, ghip.Q2_K, ghip.Q3_K, ghip.Q4_K, ghip.Q5_K,
-            ghip.Q6_K, ghip.IQ4_NL, ghip.IQ4_XS, ghip.NVFP4, ghip.Q1_0, ghip.Q2_0, ghip.F32, ghip.F16, ghip.BF16]
+            ghip.Q6_K, ghip.IQ4_NL, ghip.IQ4_XS, ghip.NVFP4, ghip.Q1_0, ghip.Q2_0, ghip.F32, ghip.F16, ghip.BF16,
+            ghip.IQ2_XXS, ghip.IQ2_XS, ghip.IQ2_S, ghip.IQ3_XXS, ghip.IQ3_S, ghip.IQ1_S, ghip.IQ1_M]
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 11, 16, 40, 64, 200, 512])

@@ -255,14 +255,16 @@ def _profile_ops(be, torch, np, what):
             return _graph_replay(torch, lambda i: be.mul_mat(ws[i % 16], ghip.Q4_K, k, x, out=out), 64)
         # one 33,030,144-byte device-to-device copy per launch
         return lambda i: ws[(i + 1) % 16].copy_(ws[i % 16])
-    if what in ("gemm", "gemm_q6k", "decode_b8"):
+    if what in ("gemm", "gemm_q6k", "gemm_q4_0", "decode_b8"):
         ty, m, k, n = {"gemm": (ghip.Q4_K, 512, 4096, 14336), "gemm_q6k": (ghip.Q6_K, 512, 14336, 4096),
-                       "decode_b8": (ghip.Q4_K, 8, 4096, 14336)}[what]
+                       "gemm_q4_0": (ghip.Q4_0, 512, 4096, 14336), "decode_b8": (ghip.Q4_K, 8, 4096, 14336)}[what]
         copies = 16 if what == "decode_b8" else 1
         wf = torch.randn((n, k), device="cuda", generator=g) * 0.02
         ws = [be.quantize(wf, ty)]
         del wf
         ws += [ws[0].clone() for _ in range(copies - 1)]
+        if ty == ghip.Q4_0:  # registered: the GEMM reads the kept int8 codes
+            be.register_weight(ws[0], ty, k)
         x = torch.randn((m, k), device="cuda", generator=g)
         out = torch.empty((m, n), dtype=torch.float32, device="cuda")
         return lambda i: be.mul_mat(ws[i % copies], ty, k, x, out=out)
@@ -321,7 +323,7 @@ def _graph_replay(torch, launch, n):
     return lambda i: g.replay() if i % n == 0 else None
 
 
-PROFILE_WORKLOADS = ["gemv", "gemv_graph", "copy", "gemm", "gemm_q6k", "decode_b8", "layer_b1", "layer_b8", "moe", "moe_reg",
+PROFILE_WORKLOADS = ["gemv", "gemv_graph", "copy", "gemm", "gemm_q6k", "gemm_q4_0", "decode_b8", "layer_b1", "layer_b8", "moe", "moe_reg",
                      "fa_decode", "fa_prefill"]
 
 

@@ -765,7 +765,7 @@ ghip_status run_gemv(ghip_context *ctx, const MulMatPlan &p, const void *w, cons
 // MFMA GEMM runs on 128 x 128 tiles.
 constexpr size_t kGemmSmem128 = 116224, kGemmSmem64 = 76544;  // sizeof(g3::Smem<BM>) in ghip_gemm.hip
 constexpr size_t kGemmSmemQ6 = 152320;
-constexpr size_t kGemmSmemQ8 = 55296;                          // sizeof(g8::Smem) in ghip_gemm.hip                         // sizeof(g6::Smem) in ghip_gemm.hip
+constexpr size_t kGemmSmemQ8 = 22528;                          // sizeof(g8::Smem) in ghip_gemm.hip                         // sizeof(g6::Smem) in ghip_gemm.hip
 constexpr size_t kGemmSmemW8 = 148480;  // 2 * sizeof(g4::Stage<256>) in ghip_gemm.hip
 // GHIP_GEMM_BM=128 selects the 128 x 128 tiles of gemm_q4K_impl
 int gemm_bm() { return env_int("GHIP_GEMM_BM", 64) == 128 ? 128 : 64; }

@@ -25,6 +25,15 @@ constexpr int Q4_0_BYTES = 18;
 constexpr int Q8_0_BYTES = 34;
 constexpr int MXFP4_BYTES = 17;
 
+// Int8 weight codes of the Q8-family prefill GEMM: 32-row tiles, and in a
+// tile one 1 KB piece per 32-block in which lane 32h + r of a wavefront finds
+// row r's bytes 16h .. 16h+15 at lane * 16 (one coalesced 16-byte load per
+// lane gives the MFMA's B operand).  Byte offset of row's block b, half 0;
+// half 1 follows at +512.
+DEV int64_t q8w_piece(int row, int b, int Kpad) {
+    return ((int64_t)(row >> 5) * (Kpad >> 5) + b) * 1024 + (row & 31) * 16;
+}
+
 DEV uint4 ld16(const uint8_t *p) {
     uint4 v;
     __builtin_memcpy(&v, p, 16);

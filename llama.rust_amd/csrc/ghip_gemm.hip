@@ -955,9 +955,9 @@ __device__ __forceinline__ void q8w_repack(const uint8_t *__restrict__ W, int64_
             }
         }
     }
-    uint4 *o = reinterpret_cast<uint4 *>(codes + (int64_t)row * Kpad + 32 * b);
-    o[0] = make_uint4(v[0], v[1], v[2], v[3]);
-    o[1] = make_uint4(v[4], v[5], v[6], v[7]);
+    int8_t *o = codes + q8w_piece(row, b, Kpad);
+    *reinterpret_cast<uint4 *>(o) = make_uint4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<uint4 *>(o + 512) = make_uint4(v[4], v[5], v[6], v[7]);
     dw[(int64_t)b * Npad + row] = d;
 }
 #define Q8W_REPACK(TN, TYPE)                                                                                       \
@@ -1007,7 +1007,6 @@ namespace g8 {
 constexpr int BM = 64, BN = 128, GB = 4;  // tokens, rows, 32-blocks per stage
 struct Smem {
     int8_t act[2][BM * GB * 32];   // [stage][token][128 B], 16-byte slots swizzled by token % 8
-    int8_t w[2][BN * GB * 32];     // [stage][row][128 B], swizzled by row % 8
     float da[2][GB][BM];
     float dw[2][GB][BN];
 };
@@ -1016,7 +1015,10 @@ struct Smem {
 // 64 tokens x 128 rows per 256-thread workgroup; wavefront w owns rows
 // 32w .. 32w+31 and both 32-token tiles.  C[token][row]: lane l holds row
 // l % 32 and tokens crow(v, l).  Operands: lane l takes K 16(l/32) .. +15 of
-// the block (A: token l % 32 of the tile, B: row l % 32).
+// the block (A: token l % 32 of the tile, B: row l % 32).  The activations,
+// shared by the four wavefronts, are staged through LDS; each wavefront's
+// weights go from memory straight to its registers (q8w_piece layout), one
+// group ahead.
 //
 // XS (IQ4_XS weights, Q8_K activations): dw holds each 32-group's integer
 // scale ls - 32 (exact in f32) and dsb[super-block][row] the block's d; the
@@ -1043,7 +1045,7 @@ __device__ __forceinline__ void gemm_q8_impl(const int8_t *__restrict__ wc, cons
     const int m0 = (id % n_tiles_m) * BM, n0 = (id / n_tiles_m) * BN;
     const int ng = Kpad / (32 * GB);
 
-    // group g into stage p: 2 act chunks, 4 weight chunks, (waves 0-1) the scales
+    // group g into stage p: 2 act chunks, (waves 0-1) the scales
     auto issue = [&](int g, int p) {
 #pragma unroll
         for (int i = 0; i < 2; i++) {
@@ -1051,13 +1053,6 @@ __device__ __forceinline__ void gemm_q8_impl(const int8_t *__restrict__ wc, cons
             const int t = c >> 3, src = (c & 7) ^ (t & 7);
             g2lds(ac + (int64_t)(m0 + t) * Kpad + (int64_t)g * 128 + 16 * src,
                   SM.act[p] + 1024 * (2 * wave + i));
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = 64 * (4 * wave + i) + lane;
-            const int r = c >> 3, src = (c & 7) ^ (r & 7);
-            g2lds(wc + (int64_t)min(n0 + r, Npad - 1) * Kpad + (int64_t)g * 128 + 16 * src,
-                  SM.w[p] + 1024 * (4 * wave + i));
         }
         if (wave == 0) {  // da: 4 blocks x 64 tokens = 64 chunks
             const int kb = lane >> 4;
@@ -1082,55 +1077,140 @@ __device__ __forceinline__ void gemm_q8_impl(const int8_t *__restrict__ wc, cons
             isb[tm][v] = 0;
         }
     const int wr = 32 * wave + li;  // this lane's weight row in the tile
-    issue(0, 0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    for (int g = 0; g < ng; g++) {
-        const int p = g & 1;
-        if (g + 1 < ng) issue(g + 1, p ^ 1);
+    // one 32-block's operands: A for both token tiles and B, plus the scale
+    // operands of the outer-product MFMA: lanes of half 0 put the token's
+    // (A) and the row's (B) f16 scale at k = 0, every other k is 0, so
+    // S[token][row] = da * dw, exact (two f16 values), in the layout of the
+    // block's integer dots
+    struct Ops {
+        v4i a[2];
+        v8h sa[2];
+        v8h sb;
+        float sw;  // XS: the group's integer scale ls - 32
+        float da[2][16];  // XS: the 16 token scales of each tile
+    };
+    auto load = [&](int p, int kb, Ops &o) {
+        const int slot = 2 * kb + h;  // this lane's 16 bytes of block kb
+        o.sw = SM.dw[p][kb][wr];
+        const v8h z8 = {};
+        o.sb = z8;
+        o.sb[0] = h == 0 ? (_Float16)o.sw : (_Float16)0.0f;
 #pragma unroll
-        for (int kb = 0; kb < GB; kb++) {
-            const int slot = 2 * kb + h;  // this lane's 16 bytes of block kb
-            const v4i bw = *reinterpret_cast<const v4i *>(SM.w[p] + wr * 128 + 16 * (slot ^ (wr & 7)));
-            const float sw = SM.dw[p][kb][wr];
-            const int b = g * GB + kb;
+        for (int tm = 0; tm < 2; tm++) {
+            const int ta = 32 * tm + li;
+            o.a[tm] = *reinterpret_cast<const v4i *>(SM.act[p] + ta * 128 + 16 * (slot ^ (ta & 7)));
+            if constexpr (XS) {
 #pragma unroll
-            for (int tm = 0; tm < 2; tm++) {
-                const int ta = 32 * tm + li;
-                const v4i a = *reinterpret_cast<const v4i *>(SM.act[p] + ta * 128 + 16 * (slot ^ (ta & 7)));
-                const v16i zi = {};
-                const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bw, zi, 0, 0, 0);
-                if constexpr (XS) {
-                    // |ls * dot| <= 32 * 32 * 127 * 128, eight of them fit int32
-                    const int ls = (int)sw;
+                for (int q = 0; q < 4; q++) {
+                    const float4 d4 = *reinterpret_cast<const float4 *>(&SM.da[p][kb][32 * tm + 8 * q + 4 * h]);
+                    o.da[tm][4 * q] = d4.x;
+                    o.da[tm][4 * q + 1] = d4.y;
+                    o.da[tm][4 * q + 2] = d4.z;
+                    o.da[tm][4 * q + 3] = d4.w;
+                }
+            } else {
+                o.sa[tm] = z8;
+                const _Float16 dah = (_Float16)SM.da[p][kb][ta];
+                o.sa[tm][0] = h == 0 ? dah : (_Float16)0.0f;
+            }
+        }
+    };
+    // block b's products c[tm] (scales sc[tm]) into the outputs (XS: into the
+    // super-block's integer sums, folded at its last group)
+    auto fold = [&](int b, const Ops &o, const v16i (&c)[2], const v16f (&sc)[2]) {
 #pragma unroll
-                    for (int v = 0; v < 16; v++) isb[tm][v] += ls * c[v];
-                    if ((b & 7) == 7) {
-                        const float d = b < nb ? dsb[(int64_t)(b >> 3) * Npad + min(n0 + wr, Npad - 1)] : 0.0f;
+        for (int tm = 0; tm < 2; tm++) {
+            if constexpr (XS) {
+                // |ls * dot| <= 32 * 32 * 127 * 128, eight of them fit int32
+                const int ls = (int)o.sw;
 #pragma unroll
-                        for (int v = 0; v < 16; v++) {
-                            const int tl = 32 * tm + crow(v, lane);
-                            out[tm][v] = fmaf(d * (float)isb[tm][v], SM.da[p][kb][tl], out[tm][v]);
-                            if constexpr (SUBSUMS)
-                                if (b < nb && m0 + tl < M && n0 + wr < N)
-                                    sub[((int64_t)(m0 + tl) * N + (n0 + wr)) * (nb >> 3) + (b >> 3)] = isb[tm][v];
-                            isb[tm][v] = 0;
-                        }
-                    }
-                } else {
+                for (int v = 0; v < 16; v++) isb[tm][v] += ls * c[tm][v];
+                if ((b & 7) == 7) {
+                    const float d = b < nb ? dsb[(int64_t)(b >> 3) * Npad + min(n0 + wr, Npad - 1)] : 0.0f;
 #pragma unroll
                     for (int v = 0; v < 16; v++) {
                         const int tl = 32 * tm + crow(v, lane);
-                        out[tm][v] = fmaf(sw * SM.da[p][kb][tl], (float)c[v], out[tm][v]);
+                        out[tm][v] = fmaf(d * (float)isb[tm][v], o.da[tm][v], out[tm][v]);
                         if constexpr (SUBSUMS)
                             if (b < nb && m0 + tl < M && n0 + wr < N)
-                                sub[((int64_t)(m0 + tl) * N + (n0 + wr)) * nb + b] = c[v];
+                                sub[((int64_t)(m0 + tl) * N + (n0 + wr)) * (nb >> 3) + (b >> 3)] = isb[tm][v];
+                        isb[tm][v] = 0;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    out[tm][v] = fmaf(sc[tm][v], (float)c[tm][v], out[tm][v]);
+                    if constexpr (SUBSUMS) {
+                        const int tl = 32 * tm + crow(v, lane);
+                        if (b < nb && m0 + tl < M && n0 + wr < N)
+                            sub[((int64_t)(m0 + tl) * N + (n0 + wr)) * nb + b] = c[tm][v];
                     }
                 }
             }
         }
+    };
+    // this wavefront's weight pieces: group g's block kb at wpc + (4g + kb) * 1024
+    const int8_t *wpc = wc + q8w_piece(n0 + 32 * wave, 0, Kpad) + 16 * lane;
+    v4i bq[GB], bqn[GB];  // this group's and the next group's
+    auto load_w = [&](int g, v4i (&q)[GB]) {
+#pragma unroll
+        for (int kb = 0; kb < GB; kb++)
+            q[kb] = *reinterpret_cast<const v4i *>(wpc + (int64_t)(g * GB + kb) * 1024);
+    };
+    load_w(0, bq);
+    issue(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    const v16i zi = {};
+    const v16f zf = {};
+    v16i c[2][2];  // block kb's dots in c[kb & 1], scales in sc[kb & 1]
+    v16f sc[2][2];
+    for (int g = 0; g < ng; g++) {
+        const int p = g & 1;
+        if (g + 1 < ng) {
+            issue(g + 1, p ^ 1);
+            load_w(g + 1, bqn);
+        }
+        // block kb+1's operands are read while block kb multiplies and block
+        // kb-1 folds (the previous group's last block folds under this
+        // group's first MFMAs; XS folds it at the group's end)
+        Ops ops[3];  // block kb in ops[kb % 3]
+        load(p, 0, ops[0]);
+#pragma unroll
+        for (int kb = 0; kb < GB; kb++) {
+            const int cb = kb & 1;
+            if (kb + 1 < GB) load(p, kb + 1, ops[(kb + 1) % 3]);
+            const Ops &o = ops[kb % 3];
+#pragma unroll
+            for (int tm = 0; tm < 2; tm++) {
+                c[cb][tm] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[tm], bq[kb], zi, 0, 0, 0);
+                if constexpr (!XS) sc[cb][tm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o.sa[tm], o.sb, zf, 0, 0, 0);
+            }
+            if (kb > 0)
+                fold(g * GB + kb - 1, ops[(kb + 2) % 3], c[cb ^ 1], sc[cb ^ 1]);
+            else if (!XS && g > 0)
+                fold(g * GB - 1, ops[0], c[1], sc[1]);
+            if constexpr (!XS && !SUBSUMS) {
+                // spread the fold's VALU work between the MFMAs
+                __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x8, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x2, 18, 0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (XS) fold(g * GB + GB - 1, ops[(GB - 1) % 3], c[(GB - 1) & 1], sc[(GB - 1) & 1]);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+#pragma unroll
+        for (int kb = 0; kb < GB; kb++) bq[kb] = bqn[kb];
+    }
+    if constexpr (!XS) {
+        Ops none;  // the non-XS fold reads no operands
+        fold(ng * GB - 1, none, c[1], sc[1]);
     }
     const int n = n0 + wr;
 #pragma unroll
@@ -1166,4 +1246,4 @@ extern "C" __global__ void __launch_bounds__(256)
                         const float *__restrict__ dsb) {
     gemm_q8_impl<true, true>(wc, dw, N, Npad, nb, Kpad, ac, da, M, Mpad, dst, ldd, sub, dsb);
 }
-static_assert(sizeof(g8::Smem) == 55296, "host code launches with this LDS size");
+static_assert(sizeof(g8::Smem) == 22528, "host code launches with this LDS size");

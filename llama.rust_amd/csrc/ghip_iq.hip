@@ -302,9 +302,9 @@ __device__ __forceinline__ void q8w_repack_lut(const uint8_t *__restrict__ W, in
             v[4 + k] = lut4(kIq4nl, qq[k] >> 4);
         }
     }
-    uint4 *o = reinterpret_cast<uint4 *>(codes + (int64_t)row * Kpad + 32 * g);
-    o[0] = make_uint4(v[0], v[1], v[2], v[3]);
-    o[1] = make_uint4(v[4], v[5], v[6], v[7]);
+    int8_t *o = codes + q8w_piece(row, g, Kpad);
+    *reinterpret_cast<uint4 *>(o) = make_uint4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<uint4 *>(o + 512) = make_uint4(v[4], v[5], v[6], v[7]);
     dw[(int64_t)g * Npad + row] = d;
 }
 

@@ -194,11 +194,12 @@ def test_errors(be):
     bad = ghip.Node(99, [], None)
     with pytest.raises(ghip.GhipError, match="op 99 not supported"):
         be.graph_compute([bad])
-    # a failing node reports its own error (IQ2_XXS weights are not supported)
-    ghip.BLOCK.setdefault(16, (256, 66))
-    w = torch.zeros((32, 66), dtype=torch.uint8, device="cuda")
+    # a failing node reports its own error (TQ1_0 weights are refused, as the
+    # reference refuses them: compute.rs:1456-1464)
+    ghip.BLOCK.setdefault(34, (256, 54))
+    w = torch.zeros((32, 54), dtype=torch.uint8, device="cuda")
     x = torch.randn((1, 256), device="cuda")
     out = torch.empty((1, 32), device="cuda")
-    node = ghip.Node(ghip.OP_MUL_MAT, [ghip.describe(w, 16, 256), ghip.describe(x, ghip.F32)], ghip.describe(out, ghip.F32))
+    node = ghip.Node(ghip.OP_MUL_MAT, [ghip.describe(w, 34, 256), ghip.describe(x, ghip.F32)], ghip.describe(out, ghip.F32))
     with pytest.raises(ghip.GhipError, match="not supported"):
         be.graph_compute([node])

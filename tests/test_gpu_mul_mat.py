@@ -147,12 +147,13 @@ def test_padding_columns_not_stored(be, cols):
 
 def test_unsupported_type_raises(be):
     import ghip
-    # IQ2_XXS (type 16, 66-byte super-blocks) has no kernel here: a status, no fallback
-    ghip.BLOCK.setdefault(16, (256, 66))
-    w = torch.zeros((8, 66), dtype=torch.uint8, device="cuda")
+    # TQ1_0 (type 34, 54-byte super-blocks) is the reference's documented
+    # refusal (compute.rs:1456-1464): a status, no fallback
+    ghip.BLOCK.setdefault(34, (256, 54))
+    w = torch.zeros((8, 54), dtype=torch.uint8, device="cuda")
     x = torch.zeros((1, 256), dtype=torch.float32, device="cuda")
     with pytest.raises(ghip.GhipError, match="not supported"):
-        be.mul_mat(w, 16, 256, x)
+        be.mul_mat(w, 34, 256, x)
 
 
 # ---------------------------------------------------------------- prefill GEMM

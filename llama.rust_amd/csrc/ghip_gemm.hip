@@ -1050,7 +1050,7 @@ __device__ __forceinline__ void gemm_q8_impl(const int8_t *__restrict__ wc, cons
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             const int c = 64 * (2 * wave + i) + lane;  // LDS chunk: token c / 8, slot c % 8
-            const int t = c >> 3, src = (c & 7) ^ (t & 7);
+            const int t = c >> 3, src = (c & 7) ^ ((t >> 1) & 7);
             g2lds(ac + (int64_t)(m0 + t) * Kpad + (int64_t)g * 128 + 16 * src,
                   SM.act[p] + 1024 * (2 * wave + i));
         }
@@ -1098,7 +1098,7 @@ __device__ __forceinline__ void gemm_q8_impl(const int8_t *__restrict__ wc, cons
 #pragma unroll
         for (int tm = 0; tm < 2; tm++) {
             const int ta = 32 * tm + li;
-            o.a[tm] = *reinterpret_cast<const v4i *>(SM.act[p] + ta * 128 + 16 * (slot ^ (ta & 7)));
+            o.a[tm] = *reinterpret_cast<const v4i *>(SM.act[p] + ta * 128 + 16 * (slot ^ ((ta >> 1) & 7)));
             if constexpr (XS) {
 #pragma unroll
                 for (int q = 0; q < 4; q++) {

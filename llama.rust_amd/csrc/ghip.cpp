@@ -1337,8 +1337,9 @@ bool mmid_generic_type(int t) {
            t == GHIP_TYPE_Q5_1 || t == GHIP_TYPE_Q2_K || t == GHIP_TYPE_Q3_K || t == GHIP_TYPE_IQ4_NL ||
            t == GHIP_TYPE_IQ4_XS || t == GHIP_TYPE_NVFP4 || t == GHIP_TYPE_Q1_0 || t == GHIP_TYPE_Q2_0 || grid_type(t);
 }
-// forward_mul_mat_id (compute.rs:1917-2202) with MXFP4, Q4_K, Q5_K or Q6_K
-// experts (the K-quants' vec_dot_type is Q8_K, compute.rs:1926-1929).
+// forward_mul_mat_id (compute.rs:1917-2202): MXFP4, Q4_K, Q5_K and Q6_K experts on
+// their own kernels, every other type with a vec_dot (compute.rs:1926-1929) on
+// its decode kernel per (token, slot) pair.
 bool plan_moe(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b, const ghip_tensor *ids,
               const ghip_tensor *d, MoePlan &p, ghip_status &st) {
     st = GHIP_STATUS_BACKEND_ERROR;
@@ -1349,7 +1350,7 @@ bool plan_moe(ghip_context *ctx, const ghip_tensor *as, const ghip_tensor *b, co
     if (p.wtype != GHIP_TYPE_MXFP4 && p.wtype != GHIP_TYPE_Q4_K && p.wtype != GHIP_TYPE_Q5_K &&
         p.wtype != GHIP_TYPE_Q6_K && !p.generic)
         return bad("experts must be MXFP4, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, "
-                   "NVFP4, Q1_0 or Q2_0");
+                   "NVFP4, Q1_0, Q2_0, IQ1_S, IQ1_M, IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS or IQ3_S");
     const TypeInfo ti = type_info(p.wtype);
     if (as->ne[0] % ti.blck || as->ne[0] <= 0) return bad("ne00 must be a positive multiple of the block size");
     p.K = as->ne[0];

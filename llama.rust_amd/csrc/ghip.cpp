@@ -1197,6 +1197,8 @@ struct FaParams {
     int n_head_log2;
     int DK, DV;
     int k_f32, v_f32;
+    const uint8_t *mflags;
+    int nqb, ntile;
 };
 
 float f32_param(const ghip_tensor *t, int i) {
@@ -1252,8 +1254,11 @@ bool plan_fa(ghip_context *ctx, const ghip_tensor *q, const ghip_tensor *k, cons
 struct FaLayout {
     int G, QS, qtiles, nsplit, chunk;
     size_t ws_bytes;
+    // prefill with a mask: the mask tile classes (ghip_fa_mask_scan) after the partials
+    size_t flags_off;
+    int nqb, ntile;
 };
-FaLayout fa_layout(int D, int T, int H, int S, int H_kv) {
+FaLayout fa_layout(int D, int T, int H, int S, int H_kv, int mask_planes = 0) {
     FaLayout L;
     // prefill workgroups hold G * QS wavefronts (G = H / H_kv heads times QS
     // query tiles of 32) so that every staged K/V tile serves >= 4 of them
@@ -1282,6 +1287,11 @@ FaLayout fa_layout(int D, int T, int H, int S, int H_kv) {
     L.chunk = chunk;
     const bool rowseq = T < 64 && !env_int("GHIP_FA_FORCE_MFMA", 0);  // one_chunk walk: no partials
     L.ws_bytes = rowseq ? 0 : (size_t)T * H * nsplit * (2 + D) * sizeof(float);
+    L.nqb = (T + 31) / 32;
+    L.ntile = (S + 63) / 64;
+    L.flags_off = (L.ws_bytes + 255) & ~(size_t)255;
+    if (!rowseq && mask_planes > 0 && env_int("GHIP_FA_MASK_SCAN", 1) != 0)
+        L.ws_bytes = L.flags_off + (size_t)mask_planes * L.nqb * L.ntile;
     return L;
 }
 
@@ -1891,7 +1901,7 @@ static ghip_status fa_sequence(ghip_context *ctx, const ghip_tensor *q, const gh
     if (!ctx->set_device()) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
     st = ctx->begin(s);
     if (st != GHIP_STATUS_SUCCESS) return st;
-    const FaLayout L = fa_layout(D, T, H, S, H_kv);
+    const FaLayout L = fa_layout(D, T, H, S, H_kv, mask ? (int)mask->ne[2] : 0);
     const int G = L.G, QS = L.QS, qtiles = L.qtiles;
     int nsplit = L.nsplit, chunk = L.chunk;
     void *ws = nullptr;
@@ -1933,6 +1943,9 @@ static ghip_status fa_sequence(ghip_context *ctx, const ghip_tensor *q, const gh
     p.DV = (int)v->ne[0];
     p.k_f32 = k->type == GHIP_TYPE_F32;
     p.v_f32 = v->type == GHIP_TYPE_F32;
+    p.mflags = nullptr;
+    p.nqb = L.nqb;
+    p.ntile = L.ntile;
     // shapes the tuned kernels do not take (F32 K or V, DK != DV, head sizes
     // other than 64 / 128, H / H_kv > 8) run the general row walk: with the
     // f16 accumulator where the reference's route is the row walk over an F16
@@ -1969,6 +1982,19 @@ static ghip_status fa_sequence(ghip_context *ctx, const ghip_tensor *q, const gh
     }
     const char *fwd = softcap != 0.0f ? (D == 128 ? "ghip_fa_fwd_sc_d128" : "ghip_fa_fwd_sc_d64")
                                       : (D == 128 ? "ghip_fa_fwd_d128" : "ghip_fa_fwd_d64");
+    if (mask && L.ws_bytes > L.flags_off) {
+        // classes of the mask's (32-query, 64-key) tiles: the forward kernel
+        // skips the loads of all-zero tiles and the work of all -inf ones
+        // (a causal mask is mostly the former; loading it cost 20 of 154 us
+        // at T = 512, S = 8192)
+        uint8_t *fl = (uint8_t *)ws + L.flags_off;
+        const int64_t nfl = (int64_t)mask->ne[2] * L.nqb * L.ntile;
+        ctx->expect(fl, (size_t)nfl, "mask tile classes");
+        st = ctx->launch("ghip_fa_mask_scan", dim3((unsigned)((nfl + 3) / 4)), dim3(256), 0, s, p.mask, p.mask_nb1,
+                         p.mask_nb2, (int)mask->ne[2], T, S, L.nqb, L.ntile, fl);
+        if (st != GHIP_STATUS_SUCCESS) return st;
+        p.mflags = fl;
+    }
     st = ctx->launch(fwd, dim3((unsigned)(qtiles * H_kv * nsplit)), dim3(64 * G * QS), 0, s, p);
     if (st != GHIP_STATUS_SUCCESS) return st;
     const float *sk = sinks ? (const float *)sinks->data : nullptr;
@@ -2368,7 +2394,9 @@ ghip_status ghip_workspace_size(int op, const ghip_tensor *dst, const ghip_tenso
         const ghip_tensor *q = srcs[0], *k = srcs[1], *v = srcs[2];
         if (!plan_fa(&tmp, q, k, v, n_srcs > 3 ? srcs[3] : nullptr, n_srcs > 4 ? srcs[4] : nullptr, dst, st)) return st;
         if (q->ne[1] == 0 || q->ne[2] == 0) return GHIP_STATUS_SUCCESS;
-        *bytes = fa_layout((int)k->ne[0], (int)q->ne[1], (int)q->ne[2], (int)k->ne[1], (int)k->ne[2]).ws_bytes;
+        const ghip_tensor *m = n_srcs > 3 ? srcs[3] : nullptr;
+        *bytes = fa_layout((int)k->ne[0], (int)q->ne[1], (int)q->ne[2], (int)k->ne[1], (int)k->ne[2],
+                           m ? (int)m->ne[2] : 0).ws_bytes;
         return GHIP_STATUS_SUCCESS;
     }
     return st;

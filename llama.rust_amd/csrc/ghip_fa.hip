@@ -51,6 +51,10 @@ struct FaParams {
     int n_head_log2;
     int DK, DV;          // head sizes (the general kernel; the others are compiled per D)
     int k_f32, v_f32;    // K / V element type: 1 = F32 (strides still counted in halfs)
+    // per (mask plane, 32-query block, 64-key tile): 0 every value +-0, 2 every
+    // value -inf, 1 otherwise (ghip_fa_mask_scan); null: no flags
+    const uint8_t *mflags;
+    int nqb, ntile;
 };
 
 DEV float head_slope(const FaParams &p, int h) {
@@ -118,6 +122,17 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _F
     const int mplane_i = __builtin_amdgcn_readfirstlane(h % p.mask_ne2);
     const uint16_t *mplane = p.mask ? p.mask + (int64_t)mplane_i * p.mask_nb2 : nullptr;
     const uint16_t *mrow = mplane ? mplane + (int64_t)(tvalid ? t : 0) * p.mask_nb1 : nullptr;
+    // mask tile classes of this wavefront's query block, 64 tiles per window:
+    // lane l holds tile (window base + l)
+    const uint8_t *mfl = p.mflags && mrow ? p.mflags + ((int64_t)mplane_i * p.nqb + (qt * QS + w / G)) * p.ntile : nullptr;
+    int fl_base = -64, fl_win = 1;
+    auto tile_class = [&](int tile) {  // tile: key tile index k0 / 64 (uniform, increasing)
+        if (tile >= fl_base + 64) {
+            fl_base = tile;
+            fl_win = fl_base + lane < p.ntile ? (int)mfl[fl_base + lane] : 1;
+        }
+        return __builtin_amdgcn_readlane(fl_win, tile - fl_base);
+    };
 
     // Next tile in registers while this one is computed: K chunks, V blocks of
     // 4 keys x 8 dims (transposed on the way into LDS), and this lane's mask
@@ -165,7 +180,19 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _F
     // the next tile's mask values are loaded at the end of an iteration, so
     // mr is not live across P V (their latency hides behind the next tile's
     // staging and K Q^T MFMAs)
+    int cls_next = 1;  // class of the tile fetch_mask last prepared
     auto fetch_mask = [&](int k0n) {
+        cls_next = 1;
+        if (mfl && k0n + FA_BK <= ke) {
+            cls_next = tile_class(k0n / FA_BK);
+            if (cls_next != 1) {
+#pragma unroll
+                for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+                    for (int gq = 0; gq < 4; gq++) mr[jt][gq] = make_uint2(0, 0);
+                return;
+            }
+        }
         if (mrow) {
             const uint32_t mt = (uint32_t)k0n * 2u + mth;
 #pragma unroll
@@ -224,6 +251,8 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _F
         const int nk = min(FA_BK, ke - k0);
         const _Float16 *Ks = Ks2 + (it & 1) * KBUF;
         const _Float16 *Vt = Vt2 + (it & 1) * VBUF;
+        // a tile masked to -inf for all 32 queries adds nothing: skip its work
+        if (cls_next != 2) {
 
         if (nk < FA_BK && mrow) {
             // tail tile: mask groups reaching past the range, with bound checks
@@ -340,6 +369,7 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _F
                     o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[dt], 0, 0, 0);
                 }
             }
+        }  // cls_next != 2
         if (k0 + FA_BK < ke) {
             stage(Ks2 + ((it + 1) & 1) * KBUF, Vt2 + ((it + 1) & 1) * VBUF);
             if (k0 + 2 * FA_BK < ke) fetch_kv(k0 + 2 * FA_BK);
@@ -553,6 +583,42 @@ __device__ __forceinline__ void fa_decode_impl(const FaParams &p) {
             pp[1] = S;
         }
     }
+}
+
+// Mask tile classes for the prefill kernel: one wavefront per (plane, 32-query
+// block, 64-key tile); lane l reads row 32qb + l/2, keys 64tile + 32(l&1) ..
+// +31.  A tile whose values are all +-0 needs no mask loads (the scores are
+// unchanged), one whose values are all -inf contributes nothing (every
+// probability is 0, the running max and sums are untouched), so the forward
+// kernel skips the loads, or the tile.  Rows past T count as both; tiles
+// reaching past S are class 1 (the forward kernel's tail path reads those).
+extern "C" __global__ void __launch_bounds__(256)
+ghip_fa_mask_scan(const uint16_t *__restrict__ mask, int64_t mask_nb1, int64_t mask_nb2, int planes, int T, int S,
+                  int nqb, int ntile, uint8_t *__restrict__ flags) {
+    const int lane = threadIdx.x & 63;
+    const int64_t id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (id >= (int64_t)planes * nqb * ntile) return;
+    const int tile = (int)(id % ntile), qb = (int)((id / ntile) % nqb), plane = (int)(id / ((int64_t)ntile * nqb));
+    const int r = 32 * qb + (lane >> 1);
+    bool allz = true, allinf = true;
+    if (64 * tile + 64 > S) {
+        allz = allinf = false;
+    } else if (r < T) {
+        const uint8_t *src = reinterpret_cast<const uint8_t *>(mask + (int64_t)plane * mask_nb2 + (int64_t)r * mask_nb1 +
+                                                               64 * tile + 32 * (lane & 1));
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint4 v = ld16(src + 16 * i);
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                allz = allz && (w[k] & 0x7fff7fffu) == 0u;
+                allinf = allinf && w[k] == 0xfc00fc00u;
+            }
+        }
+    }
+    const bool z = __ballot(!allz) == 0, ninf = __ballot(!allinf) == 0;
+    if (lane == 0) flags[id] = z ? 0 : ninf ? 2 : 1;
 }
 
 // Merge the per-slice partials of one (query, head) row (reduce_partials,

@@ -165,3 +165,48 @@ def test_mask_planes_and_sequences(be, T, S, m2, m3):
             worst = max(worst, float(np.max(np.abs(got[i3, :, h:h + 1] - want))))
     print(f"fa planes T={T} S={S} m2={m2} m3={m3} path={path} max-abs {worst:.2e}", flush=True)
     assert worst <= TOL
+
+
+@pytest.mark.parametrize("T,S,m2", [(96, 640, 1), (70, 333, 2), (512, 2048, 1)])
+def test_mask_tile_classes(be, T, S, m2):
+    """The tiled route classifies each (32-query, 64-key) mask tile: all +-0
+    (no mask loads), all -inf (no work), or mixed.  A mask made of such tiles
+    (whole query blocks masked to -inf, -0.0 tiles, ragged T and S) gives the
+    oracle's result, and the same bits as with the classes switched off
+    (GHIP_FA_MASK_SCAN=0)."""
+    import os
+    H, Hkv, D = 8, 2, 128
+    rng = np.random.default_rng(T + S + m2)
+    q = rng.standard_normal((H, T, D)).astype(np.float32)
+    k = rng.standard_normal((Hkv, S, D)).astype(np.float16)
+    v = rng.standard_normal((Hkv, S, D)).astype(np.float16)
+    m = np.zeros((m2, T, S), dtype=np.float16)
+    for p2 in range(m2):
+        for qb in range((T + 31) // 32):
+            for tl in range((S + 63) // 64):
+                c = int(rng.integers(0, 4))
+                blk = m[p2, 32 * qb:32 * qb + 32, 64 * tl:64 * tl + 64]
+                if c == 1:
+                    blk[:] = -np.inf
+                elif c == 2:
+                    blk[:] = np.float16(-0.0)
+                elif c == 3:
+                    blk[:] = (rng.standard_normal(blk.shape) * 0.5).astype(np.float16)
+        m[p2, 32:64, :] = -np.inf  # a whole query block with no visible key
+    mm = m if m2 > 1 else m[0]
+    scale = 1.0 / np.sqrt(D)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    outs = []
+    for flag in ("0", "1"):
+        os.environ["GHIP_FA_MASK_SCAN"] = flag
+        try:
+            outs.append(be.flash_attn_ext(t(q), t(k), t(v), t(mm), None, scale).cpu().numpy())
+        finally:
+            del os.environ["GHIP_FA_MASK_SCAN"]
+    assert np.array_equal(outs[0], outs[1])
+    assert np.all(outs[1][32:64] == 0.0)
+    for h in range(H):
+        want, _ = O.flash_attn_ext(q[h:h + 1], k[h // (H // Hkv):h // (H // Hkv) + 1],
+                                   v[h // (H // Hkv):h // (H // Hkv) + 1], m[h % m2], None, scale, n_chunks=8)
+        err = float(np.max(np.abs(outs[1][:, h:h + 1] - want)))
+        assert err <= TOL, f"head {h}: max-abs {err:.3e}"

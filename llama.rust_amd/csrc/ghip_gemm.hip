@@ -1208,8 +1208,8 @@ __device__ __forceinline__ void gemm_q8_impl(const int8_t *__restrict__ wc, cons
 #pragma unroll
         for (int kb = 0; kb < GB; kb++) bq[kb] = bqn[kb];
     }
-    if constexpr (!XS) {
-        Ops none;  // the non-XS fold reads no operands
+    if (!XS && ng > 0) {
+        Ops none = {};  // the non-XS fold reads no operands
         fold(ng * GB - 1, none, c[1], sc[1]);
     }
     const int n = n0 + wr;

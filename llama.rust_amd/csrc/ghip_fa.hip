@@ -25,12 +25,17 @@
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef __fp16 v4fp16 __attribute__((__vector_size__(8)));  // the transposing LDS read's type
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int FA_BQ = 32;   // query positions per workgroup
 constexpr int FA_BK = 64;   // keys per tile
 constexpr int FA_KPAD = 8;  // K row padding (halfs): 272-byte rows, 8 lanes' 16-byte reads hit distinct banks
-constexpr int FA_VPAD = 4;  // V^T row padding (halfs): 136-byte rows, 16 lanes' 8-byte reads hit distinct banks
+constexpr int FA_VPAD = 4;  // V^T row padding (halfs) of the row walk's tiles
+// prefill V tiles stay in key-major order, rows padded by 32 halfs (a row
+// stride of 64 mod 256 bytes), so the 32 lanes of a transposing read
+// (4 key rows x 4 dim groups x 2 dim halves) hit distinct banks
+constexpr int FA_VNPAD = 32;
 
 DEV int crow32(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
 
@@ -72,12 +77,13 @@ DEV float head_slope(const FaParams &p, int h) {
 }
 
 template <int D, bool SOFTCAP>
-__device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _Float16 *Vt2) {
-    constexpr int KS = D + FA_KPAD, VS = FA_BK + FA_VPAD;
-    constexpr int NKC = FA_BK * D / 8;           // 16-byte K chunks per tile
-    constexpr int NVB = (FA_BK / 4) * (D / 8);   // 4-key x 8-dim V blocks per tile
-    // a workgroup has at least 4 wavefronts (G * QS >= 4)
-    constexpr int MAXK = (NKC + 255) / 256, MAXV = (NVB + 255) / 256;
+__device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _Float16 *Vn2) {
+    constexpr int KS = D + FA_KPAD, VSN = D + FA_VNPAD;
+    // 16-byte LDS chunks per key row (data and padding): one buffer-to-LDS
+    // load of a wavefront fills 64 consecutive chunks, so a tile takes NIK (K)
+    // and NIV (V) of them, spread over the workgroup's wavefronts (>= 4)
+    constexpr int NIK = KS / 8, NIV = VSN / 8;
+    constexpr int MKI = (NIK + 3) / 4, MVI = (NIV + 3) / 4;
     constexpr float LOG2E = 1.4426950408889634f;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nthr = blockDim.x;
     const int G = p.H / p.H_kv, QS = (nthr >> 6) / G;  // QS query tiles of 32 per workgroup
@@ -137,12 +143,11 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _F
     // Next tile in registers while this one is computed: K chunks, V blocks of
     // 4 keys x 8 dims (transposed on the way into LDS), and this lane's mask
     // values (keys 32*jt + 8*gq + 4*h2 + 0..3, the layout of the scores).
-    uint4 kr[MAXK], vr[MAXV][4];
-    uint2 mr[2][4];
+    uint2 mr[2][4], mrn[2][4];  // this tile's and the next tile's mask values
 #pragma unroll
     for (int jt = 0; jt < 2; jt++)
 #pragma unroll
-        for (int gq = 0; gq < 4; gq++) mr[jt][gq] = make_uint2(0, 0);
+        for (int gq = 0; gq < 4; gq++) mr[jt][gq] = mrn[jt][gq] = make_uint2(0, 0);
     // Buffer loads: the resources end at the slice's last key, so rows past
     // it read as zero; offsets are this thread's fixed part plus a uniform
     // tile part.  Mask groups that reach past the slice are reloaded with
@@ -155,33 +160,45 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _F
     const uint32_t mrowb = (uint32_t)p.mask_nb1 * 2u;
     const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(mplane ? mplane : p.k), 0, mplane ? (int)((uint32_t)(p.T - 1) * mrowb + (uint32_t)ke * 2u) : 0, 0x00020000);
-    // thread parts: K chunk c = tid + i*nthr -> key c / (D/8), dims 8 * (c % (D/8));
-    // V block b = tid + i*nthr -> keys 4 * (b & 15) + r, dims 8 * (b >> 4)
-    const uint32_t kth = (uint32_t)(tid / (D / 8)) * krow + (uint32_t)(tid % (D / 8)) * 16u;
-    const uint32_t vth = (uint32_t)(4 * (tid & 15)) * vrow + (uint32_t)(tid >> 4) * 16u;
-    const uint32_t kstep = (uint32_t)(nthr / (D / 8)) * krow;  // per i
-    const uint32_t vstep = (uint32_t)(nthr >> 4) * 16u;
+    // this lane's source offsets for the tile loads: chunk c = 64 * ii + lane
+    // of wavefront load ii -> key row c / NI, piece c % NI (pieces past the
+    // row's data re-read its first piece into the padding)
+    const int nw = nthr >> 6;
+    uint32_t koff[MKI], voff[MVI];
+#pragma unroll
+    for (int i = 0; i < MKI; i++) {
+        const int c = 64 * (w + i * nw) + lane, r = c / NIK, pc = c % NIK;
+        koff[i] = (uint32_t)r * krow + 16u * (uint32_t)(pc < D / 8 ? pc : 0);
+    }
+#pragma unroll
+    for (int i = 0; i < MVI; i++) {
+        const int c = 64 * (w + i * nw) + lane, r = c / NIV, pc = c % NIV;
+        voff[i] = (uint32_t)r * vrow + 16u * (uint32_t)(pc < D / 8 ? pc : 0);
+    }
     const uint32_t mth = (uint32_t)(tvalid ? t : 0) * mrowb + (uint32_t)(8 * h2);
-    auto fetch_kv = [&](int k0n) {
-        const uint32_t kt = (uint32_t)k0n * krow + kth, vt = (uint32_t)k0n * vrow + vth;
+    // tile k0n's K and V rows straight into LDS buffer `buf` (rows past the
+    // slice read as zero)
+    constexpr int KBUF = FA_BK * KS, VBUF = FA_BK * VSN;
+    auto issue_kv = [&](int k0n, int buf) {
 #pragma unroll
-        for (int i = 0; i < MAXK; i++)
-            if (tid + i * nthr < NKC)
-                kr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(krs, kt + i * kstep, 0, 0));
+        for (int i = 0; i < MKI; i++) {
+            const int ii = w + i * nw;
+            if (ii < NIK)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (__attribute__((address_space(3))) void *)(Ks2 + buf * KBUF + 512 * ii),
+                                                         16, koff[i], (uint32_t)k0n * krow, 0, 0);
+        }
 #pragma unroll
-        for (int i = 0; i < MAXV; i++)
-            if (tid + i * nthr < NVB) {
-#pragma unroll
-                for (int r = 0; r < 4; r++)
-                    vr[i][r] = __builtin_bit_cast(
-                        uint4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vt + i * vstep + r * vrow, 0, 0));
-            }
+        for (int i = 0; i < MVI; i++) {
+            const int ii = w + i * nw;
+            if (ii < NIV)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (__attribute__((address_space(3))) void *)(Vn2 + buf * VBUF + 512 * ii),
+                                                         16, voff[i], (uint32_t)k0n * vrow, 0, 0);
+        }
     };
-    // the next tile's mask values are loaded at the end of an iteration, so
-    // mr is not live across P V (their latency hides behind the next tile's
-    // staging and K Q^T MFMAs)
+    // the next tile's mask values are loaded into mrn with its K and V, at
+    // the top of an iteration
     int cls_next = 1;  // class of the tile fetch_mask last prepared
-    auto fetch_mask = [&](int k0n) {
+    auto fetch_mask = [&](int k0n, uint2 (&mr)[2][4]) {
         cls_next = 1;
         if (mfl && k0n + FA_BK <= ke) {
             cls_next = tile_class(k0n / FA_BK);
@@ -203,56 +220,27 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _F
                         uint2, __builtin_amdgcn_raw_buffer_load_b64(mrs, mt + 2u * (32 * jt + 8 * gq), 0, 0));
         }
     };
-    auto stage = [&](_Float16 *Ks, _Float16 *Vt) {
-#pragma unroll
-        for (int i = 0; i < MAXK; i++) {
-            const int c = tid + i * nthr;
-            if (c < NKC) {
-                const int key = c / (D / 8), d8 = (c % (D / 8)) * 8;
-                *reinterpret_cast<uint4 *>(&Ks[key * KS + d8]) = kr[i];
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < MAXV; i++) {
-            const int b = tid + i * nthr;
-            if (b < NVB) {
-                const int kq = b & 15, d8 = (b >> 4) * 8;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    uint32_t wv[4];
-#pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        wv[r] = e == 0 ? vr[i][r].x : e == 1 ? vr[i][r].y : e == 2 ? vr[i][r].z : vr[i][r].w;
-                    // dims d8+2e (low halves) and d8+2e+1 (high halves) of keys 4kq..4kq+3
-                    const uint2 lo = make_uint2(__builtin_amdgcn_perm(wv[1], wv[0], 0x05040100u),
-                                                __builtin_amdgcn_perm(wv[3], wv[2], 0x05040100u));
-                    const uint2 hi = make_uint2(__builtin_amdgcn_perm(wv[1], wv[0], 0x07060302u),
-                                                __builtin_amdgcn_perm(wv[3], wv[2], 0x07060302u));
-                    *reinterpret_cast<uint2 *>(&Vt[(d8 + 2 * e) * VS + 4 * kq]) = lo;
-                    *reinterpret_cast<uint2 *>(&Vt[(d8 + 2 * e + 1) * VS + 4 * kq]) = hi;
-                }
-            }
-        }
-    };
-
     // Two LDS buffers: tile i is computed from buffer i & 1 while tile i + 1
-    // is staged into the other one after the compute, so one barrier per
-    // tile separates the staging from the next tile's reads (and the reads of
-    // a buffer from its next staging, one tile later).
-    constexpr int KBUF = FA_BK * KS, VBUF = D * VS;
+    // lands in the other one (issued at the top of iteration i, waited for at
+    // its end), so one barrier per tile separates a buffer's loads from its
+    // reads and its reads from its next loads.
     if (kb < ke) {
-        fetch_kv(kb);
-        fetch_mask(kb);
-        stage(Ks2, Vt2);
-        if (kb + FA_BK < ke) fetch_kv(kb + FA_BK);
+        issue_kv(kb, 0);
+        fetch_mask(kb, mr);
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     for (int k0 = kb, it = 0; k0 < ke; k0 += FA_BK, it++) {
         const int nk = min(FA_BK, ke - k0);
         const _Float16 *Ks = Ks2 + (it & 1) * KBUF;
-        const _Float16 *Vt = Vt2 + (it & 1) * VBUF;
+        const _Float16 *Vn = Vn2 + (it & 1) * VBUF;
+        const int cls = cls_next;  // this tile's mask class
+        if (k0 + FA_BK < ke) {
+            issue_kv(k0 + FA_BK, (it + 1) & 1);
+            fetch_mask(k0 + FA_BK, mrn);
+        }
         // a tile masked to -inf for all 32 queries adds nothing: skip its work
-        if (cls_next != 2) {
+        if (cls != 2) {
 
         if (nk < FA_BK && mrow) {
             // tail tile: mask groups reaching past the range, with bound checks
@@ -358,24 +346,30 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _F
                 for (int e = 0; e < 8; e++) pb[e] = (_Float16)s[jt][8 * m + e];
                 // slot e <-> key 32*jt + 4*h2 + 8*(2m + e/4) + e%4 (matches the C layout of s)
                 const int key0 = 32 * jt + 4 * h2 + 16 * m;
+                // transposing reads of the key-major tile: in each 16-lane group
+                // lane j gives key row key0 + j/4 at dims 4(j%4) of the group's 16
+                // dims, and lane i gets keys key0 .. key0+3 of dim i
+                const int lj = lane & 15, lg = (lane >> 4) & 1;
+                const _Float16 *vsrc = Vn + (key0 + (lj >> 2)) * VSN + 16 * lg + 4 * (lj & 3);
 #pragma unroll
                 for (int dt = 0; dt < D / 32; dt++) {
-                    const int d = 32 * dt + li;
-                    const v4h lo = *reinterpret_cast<const v4h *>(&Vt[d * VS + key0]);
-                    const v4h hi = *reinterpret_cast<const v4h *>(&Vt[d * VS + key0 + 8]);
+                    const v4h lo = __builtin_bit_cast(v4h, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                        (__attribute__((address_space(3))) v4fp16 *)(vsrc + 32 * dt)));
+                    const v4h hi = __builtin_bit_cast(v4h, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                        (__attribute__((address_space(3))) v4fp16 *)(vsrc + 8 * VSN + 32 * dt)));
                     v8h a;
 #pragma unroll
                     for (int e = 0; e < 4; e++) { a[e] = lo[e]; a[4 + e] = hi[e]; }
                     o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[dt], 0, 0, 0);
                 }
             }
-        }  // cls_next != 2
-        if (k0 + FA_BK < ke) {
-            stage(Ks2 + ((it + 1) & 1) * KBUF, Vt2 + ((it + 1) & 1) * VBUF);
-            if (k0 + 2 * FA_BK < ke) fetch_kv(k0 + 2 * FA_BK);
-            fetch_mask(k0 + FA_BK);
-        }
+        }  // cls != 2
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // tile it+1's K, V and mask are in
         __syncthreads();
+#pragma unroll
+        for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+            for (int gq = 0; gq < 4; gq++) mr[jt][gq] = mrn[jt][gq];
     }
 
     // write this slice's partial (M in natural-log units, S, unnormalized O)
@@ -397,9 +391,9 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _F
 // does not need)
 template <int D, bool SOFTCAP>
 __device__ __forceinline__ void fa_fwd_impl(const FaParams &p) {
-    __shared__ __attribute__((aligned(16))) _Float16 Ks[2 * FA_BK * (D + FA_KPAD)];  // 2 x [key][d]
-    __shared__ __attribute__((aligned(16))) _Float16 Vt[2 * D * (FA_BK + FA_VPAD)];  // 2 x [d][key]
-    fa_fwd_body<D, SOFTCAP>(p, Ks, Vt);
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[2 * FA_BK * (D + FA_KPAD)];   // 2 x [key][d]
+    __shared__ __attribute__((aligned(16))) _Float16 Vn[2 * FA_BK * (D + FA_VNPAD)];  // 2 x [key][d]
+    fa_fwd_body<D, SOFTCAP>(p, Ks, Vn);
 }
 
 // Single-query decode over a long cache (the reference's split-KV route,

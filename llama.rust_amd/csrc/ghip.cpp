@@ -575,9 +575,25 @@ int64_t sk_tiles(int64_t N) { return (N + kSkRows - 1) / kSkRows; }
 // reduction).  sk_rows_ok is the row test alone (graph grouping keeps it
 // equal within a group).
 bool sk_rows_ok(int wtype, int64_t N) { return wtype == GHIP_TYPE_Q6_K || N >= env_int("GHIP_SK_MIN_ROWS", 8192); }
+// Whole-K decode (ghip_skinny.hip ghip_sq_*): Q4_K and Q6_K at 4..8
+// activation rows from ready Q8_K rows (one ghip_quantize_q8_K launch, shared
+// by a group's members, or a Q8_K src1 as it is).  Workgroups of
+// W = ceil(nb / SW) wavefronts, wavefront w on super-blocks [w SW, w SW + SW),
+// T tiles of 16 weight rows each; the K-slices' partials are added inside the
+// workgroup.  SW: 2 up to 32 super-blocks, 4 up to 56 (the LDS images of the
+// W wavefronts, sq_img_bytes each, within 160 KB); longer rows take split K.
+int sq_sw(int64_t nb) { return nb <= 32 ? 2 : nb <= 56 ? 4 : 0; }
+size_t sq_img_bytes(int sw) {
+    return (size_t)8 * (sw * 256 + 16) + (size_t)8 * sw * 4 + (size_t)8 * (sw * 16 + 4) * 4 + (size_t)sw * 256;
+}
+bool use_sq(const MulMatPlan &p) {
+    return env_int("GHIP_SQ", 1) != 0 && (p.wtype == GHIP_TYPE_Q4_K || p.wtype == GHIP_TYPE_Q6_K) &&
+           p.M >= env_int("GHIP_SQ_MIN_COLS", 4) && p.M <= 8 && sq_sw(p.nb) > 0;
+}
 // Q4_K takes split K from 5 rows: at 4 rows the matrix-core decode kernel is
 // faster (4096 -> 14336: 17.2 us split K, 15.6 us).
 bool use_sk(const MulMatPlan &p) {
+    if (use_sq(p)) return false;
     if (p.act_pre || env_int("GHIP_SK", 1) == 0 || p.M < env_int("GHIP_MMA_MIN_ROWS", 4)) return false;
     if (p.wtype == GHIP_TYPE_Q4_K && p.M < env_int("GHIP_SK_Q4K_MIN_COLS", 5)) return false;
     return (p.wtype == GHIP_TYPE_Q4_K || p.wtype == GHIP_TYPE_Q6_K) && p.M <= 8 && sk_rows_ok(p.wtype, p.N);
@@ -636,6 +652,51 @@ ghip_status launch_sk(ghip_context *ctx, const MulMatPlan &p, SkLaunch &g, const
     const int64_t total = rows * p.M;
     for (int i = 0; i < g.n; i++) ctx->expect(r.m[i].dst, win2d(p.M, r.m[i].ldd, r.m[i].rows), "dst");
     return ctx->launch("ghip_sk_reduce", dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, r, (int)p.M, total);
+}
+// g: members' W, dst, ldd and rows filled in; act: the Q8_K rows (row stride act_rb)
+ghip_status launch_sq(ghip_context *ctx, const MulMatPlan &p, SkLaunch &g, const uint8_t *act, int64_t act_rb,
+                      int32_t *sub, hipStream_t s) {
+    const int sw = sq_sw(p.nb);
+    const int W = (int)((p.nb + sw - 1) / sw);
+    int64_t tiles = 0;
+    for (int i = 0; i < 4; i++) {
+        if (i >= g.n) g.m[i] = g.m[0];
+        g.m[i].tile0 = (int)tiles;
+        g.m[i].part = nullptr;
+        if (i < g.n) tiles += (g.m[i].rows + 15) / 16;
+    }
+    if (tiles * 16 * p.M > INT32_MAX) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "mul_mat: matrix too large for the decode kernel");
+    if (sw == 2 && env_int("GHIP_SQ_STREAM", 1) != 0) {
+        // streaming form: T tiles per workgroup for about GHIP_SQ_WGS workgroups
+        // (256: one per CU; on the Llama-3-8B decode layer at 8 rows 160 / 192 /
+        // 256 / 320 / 384 measured 79.0 / 74.2 / 68.9 / 78.2 / 75.1 us), within
+        // the LDS (image + T tiles of partials per wavefront)
+        const int64_t want = std::max(1, env_int("GHIP_SQ_WGS", 256));
+        const size_t img = sq_img_bytes(sw);
+        int64_t T = env_int("GHIP_SQ_T", (int)((tiles + want - 1) / want));
+        T = std::max<int64_t>(1, std::min<int64_t>(T, (int64_t)((160 * 1024 / W - img) / 512)));
+        g.n_tiles = (int)tiles;
+        g.nks = 1;
+        g.tg = (int)T;
+        for (int i = 0; i < g.n; i++) ctx->expect(g.m[i].dst, win2d(p.M, g.m[i].ldd, g.m[i].rows), "dst");
+        if (sub) ctx->expect(sub, sub_bytes(p, p.M), "sub-sums");
+        const std::string name = std::string("ghip_sqs_") + (p.wtype == GHIP_TYPE_Q4_K ? "q4_K" : "q6_K") +
+                                 (sub ? "_sub" : "") + "_w2";
+        return ctx->launch(name, dim3((unsigned)((tiles + T - 1) / T)), dim3(64 * W), W * (img + (size_t)T * 512), s, g,
+                           (int)T, (int64_t)p.w_row_bytes, (int)p.nb, act, act_rb, (int)p.M, sub);
+    }
+    // two tiles per workgroup from 1024 tiles at SW = 2 (the T = 2 kernels there)
+    int T = env_int("GHIP_SQ_T", sw == 2 && tiles >= 1024 ? 2 : 1);
+    if (T != 1 && !(T == 2 && sw == 2)) T = 1;
+    g.n_tiles = (int)tiles;
+    g.nks = 1;
+    g.tg = T;
+    for (int i = 0; i < g.n; i++) ctx->expect(g.m[i].dst, win2d(p.M, g.m[i].ldd, g.m[i].rows), "dst");
+    if (sub) ctx->expect(sub, sub_bytes(p, p.M), "sub-sums");
+    const std::string name = std::string("ghip_sq_") + (p.wtype == GHIP_TYPE_Q4_K ? "q4_K" : "q6_K") +
+                             (sub ? "_sub" : "") + "_w" + std::to_string(sw) + "_t" + std::to_string(T);
+    return ctx->launch(name, dim3((unsigned)((tiles + T - 1) / T)), dim3(64 * W), W * sq_img_bytes(sw), s, g,
+                       (int64_t)p.w_row_bytes, (int)p.nb, act, act_rb, (int)p.M, sub);
 }
 ghip_status run_sk(ghip_context *ctx, const MulMatPlan &p, const void *w, const ghip_tensor *x, float *dst,
                    int64_t ldd, int32_t *sub, void *part, hipStream_t s) {
@@ -1123,6 +1184,21 @@ ghip_status mul_mat_plane(ghip_context *ctx, const ghip_tensor *a, const ghip_te
     const int64_t ldd = (d ? (int64_t)d->nb[1] / 4 : p.N) + (ctx->dry_run ? env_int("GHIP_DEBUG_LDD_SKEW", 0) : 0);
     if (gemm_route(p, sub != nullptr))
         return run_gemm(ctx, p, a->data, (const uint8_t *)b->data, p.act_pre ? nullptr : b, dst, ldd, sub, lay, s);
+    if (use_sq(p)) {
+        const uint8_t *a8 = (const uint8_t *)b->data;
+        if (!p.act_pre) {
+            st = quantize_act(ctx, p, b, act, s);
+            if (st != GHIP_STATUS_SUCCESS) return st;
+            a8 = (const uint8_t *)act;
+        }
+        SkLaunch g{};
+        g.n = 1;
+        g.m[0].W = (const uint8_t *)a->data;
+        g.m[0].dst = dst;
+        g.m[0].ldd = ldd;
+        g.m[0].rows = (int)p.N;
+        return launch_sq(ctx, p, g, a8, p.act_row_bytes, sub, s);
+    }
     if (use_sk(p)) return run_sk(ctx, p, a->data, b, dst, ldd, sub, lay, s);
     if (p.act_pre) return run_gemv(ctx, p, a->data, (const uint8_t *)b->data, p.act_row_bytes, false, dst, ldd, sub, s);
     // Q8_0 quantization fused into the block-pair kernels for up to 4096 weight
@@ -1762,6 +1838,24 @@ ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipS
         return ctx->launch(std::string(gemv_base(p0.wtype)) + "_c" + std::to_string(NC) + "_multi", dim3((unsigned)wgs),
                            dim3(64 * wk), 0, s, g, (int64_t)p0.w_row_bytes, (int)p0.nb, (const uint8_t *)ws,
                            (int64_t)p0.act_row_bytes, nc);
+    }
+    if (use_sq(p0)) {
+        // the activation rows quantized once, then the whole-K kernel over all members
+        const size_t act_bytes = ((size_t)(p0.M * p0.act_row_bytes) + 255) & ~(size_t)255;
+        void *ws = nullptr;
+        st = ctx->workspace(act_bytes, s, &ws);
+        if (st != GHIP_STATUS_SUCCESS) return st;
+        st = quantize_act(ctx, p0, nodes[0].src[1], ws, s);
+        if (st != GHIP_STATUS_SUCCESS) return st;
+        SkLaunch g{};
+        g.n = n;
+        for (int i = 0; i < n; i++) {
+            g.m[i].W = (const uint8_t *)nodes[i].src[0]->data;
+            g.m[i].dst = (float *)nodes[i].dst->data;
+            g.m[i].ldd = (int64_t)nodes[i].dst->nb[1] / 4;
+            g.m[i].rows = (int)p[i].N;
+        }
+        return launch_sq(ctx, p0, g, (const uint8_t *)ws, p0.act_row_bytes, nullptr, s);
     }
     if (use_sk(p0)) {
         // split-K decode over all members; partials of member i after member i-1's

@@ -8,6 +8,7 @@
 //                                               d = 1/iscale
 // Compiled with -ffp-contract=off: every product is rounded before rne().
 #pragma once
+#include <type_traits>
 #include "ghip_common.h"
 
 // codes q[0..3] of this lane's elements and the block scale d (uniform);
@@ -21,12 +22,33 @@ DEV void q8K_block(const float xs[4], int lane, bool mat, int q[4], float &d) {
         const float a = fabsf(xs[i]);
         if (a > bax) { bax = a; bval = xs[i]; bidx = lane * 4 + i; }
     }
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const float oax = __shfl_xor(bax, o, 64);
-        const float oval = __shfl_xor(bval, o, 64);
-        const int oidx = __shfl_xor(bidx, o, 64);
+    // all-reduce within each 16-lane row by DPP: partners by quad xor 1, quad
+    // xor 2, half-row mirror (i <-> 7 - i) and row mirror (i <-> 15 - i), each
+    // pairing two disjoint groups that already agree (ties: lower index)
+    auto step = [&](auto ctrl) {
+        constexpr int C = decltype(ctrl)::value;
+        const float oax = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(bax), C, 0xF, 0xF, false));
+        const float oval = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(bval), C, 0xF, 0xF, false));
+        const int oidx = __builtin_amdgcn_update_dpp(0, bidx, C, 0xF, 0xF, false);
         if (oax > bax || (oax == bax && oidx < bidx)) { bax = oax; bval = oval; bidx = oidx; }
+    };
+    step(std::integral_constant<int, 0xB1>{});
+    step(std::integral_constant<int, 0x4E>{});
+    step(std::integral_constant<int, 0x141>{});
+    step(std::integral_constant<int, 0x140>{});
+    // the four rows hold ascending element ranges: combine them in order from
+    // their first lanes, a later row winning only with a strictly larger |x|
+    {
+        float ax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bax), 0));
+        float val = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bval), 0));
+#pragma unroll
+        for (int r = 1; r < 4; r++) {
+            const float oax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bax), 16 * r));
+            const float oval = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bval), 16 * r));
+            if (oax > ax) { ax = oax; val = oval; }
+        }
+        bax = ax;
+        bval = val;
     }
     if (bax == 0.0f) {
         q[0] = q[1] = q[2] = q[3] = 0;

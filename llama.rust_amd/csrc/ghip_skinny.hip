@@ -297,6 +297,230 @@ struct SkLaunch {
 
 typedef int v2i __attribute__((ext_vector_type(2)));
 
+constexpr int sk_nw(int wt) { return wt == 12 ? 12 : 14; }
+
+// The weight dwords lane group G needs of one super-block at p:
+// Q4_K: header (d, dmin, 12 scale bytes) | qs 32c + 8G .. +7 for c = 0..3
+// Q6_K: ql 32k + 8G .. +7 (k = 0..3) | qh 32k + 8G .. +7 (k = 0, 1) | scales 4G .. 4G+3 | d
+template <int WT>
+DEV void sk_load(const uint8_t *__restrict__ p, int G, uint32_t (&w)[sk_nw(WT)]) {
+    if constexpr (WT == 12) {
+        const uint4 h = ld16(p);
+        w[0] = h.x;
+        w[1] = h.y;
+        w[2] = h.z;
+        w[3] = h.w;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint2 q = ld8(p + 16 + 32 * c + 8 * G);
+            w[4 + 2 * c] = q.x;
+            w[5 + 2 * c] = q.y;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 6; k++) {
+            const uint2 q = ld8(p + 32 * k + 8 * G);
+            w[2 * k] = q.x;
+            w[2 * k + 1] = q.y;
+        }
+        w[12] = ld4(p + 192 + 4 * G);
+        w[13] = ld2(p + 208);
+    }
+}
+
+// One super-block of one 16-row tile: lane (j, G) adds its row j's term for
+// tokens 2G and 2G + 1 to out[0..1].  v: the lane's weight dwords (sk_load);
+// the activation image holds token t's codes at codes + t * kstride (super-block
+// bl at + 256 bl), its scales at dq[t * nbs + bl] and its 16-element sums at
+// bsum + t * BS + 16 bl; b is the super-block's index in the row (sub-sums).
+template <int WT, bool SUBSUMS>
+DEV void sk_block(const uint32_t *v, const int8_t *codes, int kstride, const float *dq, int nbs, const int *bsum,
+                  int BS, int bl, int b, int row, int rows, int nb, int ncols, int32_t *__restrict__ sub, int lane,
+                  float (&out)[2]) {
+    const int j = lane & 15, G = lane >> 4;
+    const int t_a = j >> 1, h_a = j & 1;  // this lane's A row: token, parity
+    // -32 / min term: A row 4g + u (u < 2) = token 2g + u over the
+    // 16-element sums 4G .. 4G+3
+    v4h am = {};
+    {
+        const int gg = j >> 2, u = j & 3;
+        if (u < 2) {
+            const int *p = bsum + (2 * gg + u) * BS + bl * 16 + 4 * G;
+            am[0] = (_Float16)(float)p[0];
+            am[1] = (_Float16)(float)p[1];
+            am[2] = (_Float16)(float)p[2];
+            am[3] = (_Float16)(float)p[3];
+        }
+    }
+    const int8_t *crow = codes + t_a * kstride + bl * QK_K;
+    if constexpr (WT == 12) {
+        const float dw = h2f(v[0]), dmin = h2f(v[0] >> 16);
+        v4h bm;
+        {
+            int s0, s1, m0, m1;
+            k4_scales(v[1], v[2], v[3], scale_sel(G), s0, s1, m0, m1);
+            bm[0] = bm[1] = (_Float16)(float)m0;
+            bm[2] = bm[3] = (_Float16)(float)m1;
+        }
+        const v4f accm = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, (v4f){}, 0, 0, 0);
+        int is0 = 0, is1 = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t d0 = v[4 + 2 * c], d1 = v[5 + 2 * c];
+            const v4i bw = {(int)(d0 & 0x0f0f0f0fu), (int)(d1 & 0x0f0f0f0fu), (int)((d0 >> 4) & 0x0f0f0f0fu),
+                            (int)((d1 >> 4) & 0x0f0f0f0fu)};
+            const uint2 a8 = *reinterpret_cast<const uint2 *>(crow + 64 * c + 32 * h_a + 8 * G);
+            const v4i a = h_a ? (v4i){0, 0, (int)a8.x, (int)a8.y} : (v4i){(int)a8.x, (int)a8.y, 0, 0};
+            const v4i r = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bw, (v4i){}, 0, 0, 0);
+            int sc0, sc1, mn0, mn1;
+            k4_scales(v[1], v[2], v[3], scale_sel(c), sc0, sc1, mn0, mn1);
+            is0 += __mul24(sc0, r[0]) + __mul24(sc1, r[1]);  // |r| < 2^23
+            is1 += __mul24(sc0, r[2]) + __mul24(sc1, r[3]);
+        }
+        const int isv[2] = {is0, is1};
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int tok = 2 * G + u;
+            const float im = accm[u];
+            if (SUBSUMS && tok < ncols && row < rows) {
+                int32_t *sp = sub + (((int64_t)tok * rows + row) * nb + b) * 2;
+                sp[0] = isv[u];
+                sp[1] = (int)im;
+            }
+            out[u] = fmaf(dq[tok * nbs + bl], fmaf(dw, (float)isv[u], -(dmin * im)), out[u]);
+        }
+    } else {
+        const float dw = h2f(v[13]);
+        const uint32_t sw = v[12];  // scales 4G .. 4G+3 of row j
+        v4h bs;
+        bs[0] = (_Float16)(float)(int8_t)(sw & 0xff);
+        bs[1] = (_Float16)(float)(int8_t)((sw >> 8) & 0xff);
+        bs[2] = (_Float16)(float)(int8_t)((sw >> 16) & 0xff);
+        bs[3] = (_Float16)(float)(int8_t)(sw >> 24);
+        const v4f accm = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bs, (v4f){}, 0, 0, 0);
+        const bool alive = (G >> 1) == h_a;
+        int is0 = 0, is1 = 0;
+#pragma unroll
+        for (int n = 0; n < 2; n++) {
+            const uint32_t qh0 = v[8 + 2 * n], qh1 = v[9 + 2 * n];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int src = 2 * (2 * n + (q & 1));  // ql words of 64n + 32(q&1)
+                const int sh = 4 * (q >> 1);
+                const uint32_t c0 = ((v[src] >> sh) & 0x0f0f0f0fu) | (((qh0 >> (2 * q)) & 0x03030303u) << 4);
+                const uint32_t c1 = ((v[src + 1] >> sh) & 0x0f0f0f0fu) | (((qh1 >> (2 * q)) & 0x03030303u) << 4);
+                const long bw = (long)(((uint64_t)c1 << 32) | c0);
+                long a = 0;
+                if (alive) a = *reinterpret_cast<const long *>(crow + 128 * n + 32 * q + 8 * G);
+                const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bw, (v4i){}, 0, 0, 0);
+                // scales 8n + 2q, 8n + 2q + 1: dword 2n + (q >> 1), held by lane group 2n + (q >> 1)
+                const uint32_t sd = (uint32_t)__shfl((int)sw, j + 16 * (2 * n + (q >> 1)), 64);
+                const int sc0 = (int)(int8_t)((sd >> (16 * (q & 1))) & 0xff);
+                const int sc1 = (int)(int8_t)((sd >> (16 * (q & 1) + 8)) & 0xff);
+                is0 += __mul24(sc0, c[0]) + __mul24(sc1, c[1]);  // |c| < 2^23
+                is1 += __mul24(sc0, c[2]) + __mul24(sc1, c[3]);
+            }
+        }
+        const int isv[2] = {is0 - 32 * (int)accm[0], is1 - 32 * (int)accm[1]};
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int tok = 2 * G + u;
+            if (SUBSUMS && tok < ncols && row < rows) sub[((int64_t)tok * rows + row) * nb + b] = isv[u];
+            out[u] += (dw * (float)isv[u]) * dq[tok * nbs + bl];
+        }
+    }
+}
+
+// Q4_K in 16-byte pieces (the whole-K kernels): lane group G loads the
+// header and qs bytes 64p + 16G .. +15 for p = 0, 1, so the 4 lane groups read
+// 64 contiguous bytes of a row per load.  qs byte 64p + 16G + x holds element
+// 16(G&1) + x of sub-blocks 4p + 2(G>>1) (low nibble) and 4p + 2(G>>1) + 1
+// (high nibble), so MFMA (p, n) over the lanes' low (n = 0) or high (n = 1)
+// nibbles covers sub-blocks 4p + n (lane groups 0, 1) and 4p + 2 + n (lane
+// groups 2, 3).  A row 2t + h holds token t's codes in the lane groups with
+// G >> 1 == h and zeros in the others, which read a zeroed region of the
+// image instead: C[2t + h][row] is the exact dot of sub-block 4p + 2h + n.
+DEV void q4k16_load(const uint8_t *__restrict__ p, int G, uint32_t (&w)[12]) {
+    const uint4 h = ld16(p), a = ld16(p + 16 + 16 * G), b = ld16(p + 80 + 16 * G);
+    w[0] = h.x;
+    w[1] = h.y;
+    w[2] = h.z;
+    w[3] = h.w;
+    w[4] = a.x;
+    w[5] = a.y;
+    w[6] = a.z;
+    w[7] = a.w;
+    w[8] = b.x;
+    w[9] = b.y;
+    w[10] = b.z;
+    w[11] = b.w;
+}
+
+// One super-block of one 16-row tile, lane (j, G): tokens 2G and 2G + 1 of
+// row j added to out[0..1] (the arithmetic of sk_block for Q4_K).  abase: the
+// lane's A operand base (token j >> 1's codes + 64 (j & 1) + 16 (G & 1), or
+// the zero region); the super-block's codes are at abase + 256 bl.
+template <bool SUBSUMS>
+DEV void q4k16_block(const uint32_t *v, const int8_t *abase, const float *dq, int nbs, const int *bsum, int BS,
+                     int bl, int b, int row, int rows, int nb, int ncols, int32_t *__restrict__ sub, int lane,
+                     float (&out)[2]) {
+    const int j = lane & 15, G = lane >> 4;
+    // min term: A row 4g + u (u < 2) = token 2g + u over the 16-element sums
+    // 4G .. 4G+3, B column j = the mins of sub-blocks 2G, 2G + 1 of row j
+    v4h am = {};
+    {
+        const int gg = j >> 2, u = j & 3;
+        if (u < 2) {
+            const int *p = bsum + (2 * gg + u) * BS + bl * 16 + 4 * G;
+            am[0] = (_Float16)(float)p[0];
+            am[1] = (_Float16)(float)p[1];
+            am[2] = (_Float16)(float)p[2];
+            am[3] = (_Float16)(float)p[3];
+        }
+    }
+    const float dw = h2f(v[0]), dmin = h2f(v[0] >> 16);
+    v4h bm;
+    {
+        int s0, s1, m0, m1;
+        k4_scales(v[1], v[2], v[3], scale_sel(G), s0, s1, m0, m1);
+        bm[0] = bm[1] = (_Float16)(float)m0;
+        bm[2] = bm[3] = (_Float16)(float)m1;
+    }
+    const v4f accm = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, (v4f){}, 0, 0, 0);
+    int is0 = 0, is1 = 0;
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        int sc[4], mn[4];
+        k4_scales(v[1], v[2], v[3], scale_sel(2 * p), sc[0], sc[1], mn[0], mn[1]);
+        k4_scales(v[1], v[2], v[3], scale_sel(2 * p + 1), sc[2], sc[3], mn[2], mn[3]);
+        const uint32_t *q = v + 4 + 4 * p;
+#pragma unroll
+        for (int n = 0; n < 2; n++) {
+            const v4i bw = n == 0 ? (v4i){(int)(q[0] & 0x0f0f0f0fu), (int)(q[1] & 0x0f0f0f0fu), (int)(q[2] & 0x0f0f0f0fu),
+                                          (int)(q[3] & 0x0f0f0f0fu)}
+                                  : (v4i){(int)((q[0] >> 4) & 0x0f0f0f0fu), (int)((q[1] >> 4) & 0x0f0f0f0fu),
+                                          (int)((q[2] >> 4) & 0x0f0f0f0fu), (int)((q[3] >> 4) & 0x0f0f0f0fu)};
+            const v4i a = *reinterpret_cast<const v4i *>(abase + bl * QK_K + 128 * p + 32 * n);
+            const v4i r = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bw, (v4i){}, 0, 0, 0);
+            // C rows 4G + v: token 2G + (v >> 1), sub-block 4p + n + 2 (v & 1)
+            is0 += __mul24(sc[n], r[0]) + __mul24(sc[n + 2], r[1]);  // |r| < 2^23
+            is1 += __mul24(sc[n], r[2]) + __mul24(sc[n + 2], r[3]);
+        }
+    }
+    const int isv[2] = {is0, is1};
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int tok = 2 * G + u;
+        const float im = accm[u];
+        if (SUBSUMS && tok < ncols && row < rows) {
+            int32_t *sp = sub + (((int64_t)tok * rows + row) * nb + b) * 2;
+            sp[0] = isv[u];
+            sp[1] = (int)im;
+        }
+        out[u] = fmaf(dq[tok * nbs + bl], fmaf(dw, (float)isv[u], -(dmin * im)), out[u]);
+    }
+}
+
 template <int WT, int S, int SK_GB, bool SUBSUMS>
 __device__ __forceinline__ void sk_impl(const SkLaunch &g, int64_t w_row_bytes, int nb, const float *__restrict__ x,
                                         int64_t x_stride, int ncols, int n_mat, int32_t *__restrict__ sub) {
@@ -304,10 +528,7 @@ __device__ __forceinline__ void sk_impl(const SkLaunch &g, int64_t w_row_bytes, 
     static_assert(S % SK_GB == 0, "whole pipeline steps per slice");
     constexpr int NC = 8;  // 16 A rows: 8 tokens x 2 sub-block parities
     constexpr int BB = WT == 12 ? Q4K_BYTES : Q6K_BYTES;
-    // dwords of weight data per lane and super-block:
-    // Q4_K: header (d, dmin, 12 scale bytes) | qs 32c + 8G .. +7 for c = 0..3
-    // Q6_K: ql 32k + 8G .. +7 (k = 0..3) | qh 32k + 8G .. +7 (k = 0, 1) | scales 4G .. 4G+3 | d
-    constexpr int NW = WT == 12 ? 12 : 14;
+    constexpr int NW = sk_nw(WT);  // weight dwords per lane and super-block
     // image strides per token padded by 16 bytes / 4 ints, so the 8 tokens'
     // operand reads fall in different LDS banks
     constexpr int CS = S * QK_K + 16, BS = S * 16 + 4;
@@ -347,29 +568,7 @@ __device__ __forceinline__ void sk_impl(const SkLaunch &g, int64_t w_row_bytes, 
 #pragma unroll
         for (int i = 0; i < SK_GB; i++) {
             if (SK_GB * grp + i >= nbs) break;
-            const uint8_t *p = rp + (int64_t)i * BB;
-            if constexpr (WT == 12) {
-                const uint4 h = ld16(p);
-                w[i][0] = h.x;
-                w[i][1] = h.y;
-                w[i][2] = h.z;
-                w[i][3] = h.w;
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    const uint2 q = ld8(p + 16 + 32 * c + 8 * G);
-                    w[i][4 + 2 * c] = q.x;
-                    w[i][5 + 2 * c] = q.y;
-                }
-            } else {
-#pragma unroll
-                for (int k = 0; k < 6; k++) {
-                    const uint2 q = ld8(p + 32 * k + 8 * G);
-                    w[i][2 * k] = q.x;
-                    w[i][2 * k + 1] = q.y;
-                }
-                w[i][12] = ld4(p + 192 + 4 * G);
-                w[i][13] = ld2(p + 208);
-            }
+            sk_load<WT>(rp + (int64_t)i * BB, G, w[i]);
         }
     };
     uint32_t wa[SK_GB][NW], wb[SK_GB][NW];
@@ -384,8 +583,7 @@ __device__ __forceinline__ void sk_impl(const SkLaunch &g, int64_t w_row_bytes, 
     __syncthreads();
 
     const int kstride = CS;  // one token's codes in the image
-    const int t_a = j >> 1, h_a = j & 1;  // this lane's A row: token, parity
-    float out[2] = {0.0f, 0.0f};          // tokens 2G, 2G + 1 of row j
+    float out[2] = {0.0f, 0.0f};  // tokens 2G, 2G + 1 of row j
     auto compute = [&](const uint32_t (&w)[SK_GB][NW], int it) {
         const int tile = tgi + (it / ngrp) * g.tg, grp = it % ngrp;
         const SkMember &mb = g.m[member(tile)];
@@ -395,98 +593,8 @@ __device__ __forceinline__ void sk_impl(const SkLaunch &g, int64_t w_row_bytes, 
             const int bl = SK_GB * grp + i;
             if (bl >= nbs) break;
             const int b = b0 + bl;
-            // -32 / min term: A row 4g + u (u < 2) = token 2g + u over the
-            // 16-element sums 4G .. 4G+3
-            v4h am = {};
-            {
-                const int gg = j >> 2, u = j & 3;
-                if (u < 2) {
-                    const int *p = bsum + (2 * gg + u) * BS + bl * 16 + 4 * G;
-                    am[0] = (_Float16)(float)p[0];
-                    am[1] = (_Float16)(float)p[1];
-                    am[2] = (_Float16)(float)p[2];
-                    am[3] = (_Float16)(float)p[3];
-                }
-            }
-            const int8_t *crow = codes + t_a * kstride + bl * QK_K;
-            if constexpr (WT == 12) {
-                const uint32_t *v = w[i];
-                const float dw = h2f(v[0]), dmin = h2f(v[0] >> 16);
-                v4h bm;
-                {
-                    int s0, s1, m0, m1;
-                    k4_scales(v[1], v[2], v[3], scale_sel(G), s0, s1, m0, m1);
-                    bm[0] = bm[1] = (_Float16)(float)m0;
-                    bm[2] = bm[3] = (_Float16)(float)m1;
-                }
-                const v4f accm = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, (v4f){}, 0, 0, 0);
-                int is0 = 0, is1 = 0;
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    const uint32_t d0 = v[4 + 2 * c], d1 = v[5 + 2 * c];
-                    const v4i bw = {(int)(d0 & 0x0f0f0f0fu), (int)(d1 & 0x0f0f0f0fu), (int)((d0 >> 4) & 0x0f0f0f0fu),
-                                    (int)((d1 >> 4) & 0x0f0f0f0fu)};
-                    const uint2 a8 = *reinterpret_cast<const uint2 *>(crow + 64 * c + 32 * h_a + 8 * G);
-                    const v4i a = h_a ? (v4i){0, 0, (int)a8.x, (int)a8.y} : (v4i){(int)a8.x, (int)a8.y, 0, 0};
-                    const v4i r = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bw, (v4i){}, 0, 0, 0);
-                    int sc0, sc1, mn0, mn1;
-                    k4_scales(v[1], v[2], v[3], scale_sel(c), sc0, sc1, mn0, mn1);
-                    is0 += __mul24(sc0, r[0]) + __mul24(sc1, r[1]);  // |r| < 2^23
-                    is1 += __mul24(sc0, r[2]) + __mul24(sc1, r[3]);
-                }
-                const int isv[2] = {is0, is1};
-#pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    const int tok = 2 * G + u;
-                    const float im = accm[u];
-                    if (SUBSUMS && tok < ncols && row < mb.rows) {
-                        int32_t *sp = sub + (((int64_t)tok * mb.rows + row) * nb + b) * 2;
-                        sp[0] = isv[u];
-                        sp[1] = (int)im;
-                    }
-                    out[u] = fmaf(dq[tok * nbs + bl], fmaf(dw, (float)isv[u], -(dmin * im)), out[u]);
-                }
-            } else {
-                const uint32_t *v = w[i];
-                const float dw = h2f(v[13]);
-                const uint32_t sw = v[12];  // scales 4G .. 4G+3 of row j
-                v4h bs;
-                bs[0] = (_Float16)(float)(int8_t)(sw & 0xff);
-                bs[1] = (_Float16)(float)(int8_t)((sw >> 8) & 0xff);
-                bs[2] = (_Float16)(float)(int8_t)((sw >> 16) & 0xff);
-                bs[3] = (_Float16)(float)(int8_t)(sw >> 24);
-                const v4f accm = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bs, (v4f){}, 0, 0, 0);
-                const bool alive = (G >> 1) == h_a;
-                int is0 = 0, is1 = 0;
-#pragma unroll
-                for (int n = 0; n < 2; n++) {
-                    const uint32_t qh0 = v[8 + 2 * n], qh1 = v[9 + 2 * n];
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        const int src = 2 * (2 * n + (q & 1));  // ql words of 64n + 32(q&1)
-                        const int sh = 4 * (q >> 1);
-                        const uint32_t c0 = ((v[src] >> sh) & 0x0f0f0f0fu) | (((qh0 >> (2 * q)) & 0x03030303u) << 4);
-                        const uint32_t c1 = ((v[src + 1] >> sh) & 0x0f0f0f0fu) | (((qh1 >> (2 * q)) & 0x03030303u) << 4);
-                        const long bw = (long)(((uint64_t)c1 << 32) | c0);
-                        long a = 0;
-                        if (alive) a = *reinterpret_cast<const long *>(crow + 128 * n + 32 * q + 8 * G);
-                        const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bw, (v4i){}, 0, 0, 0);
-                        // scales 8n + 2q, 8n + 2q + 1: dword 2n + (q >> 1), held by lane group 2n + (q >> 1)
-                        const uint32_t sd = (uint32_t)__shfl((int)sw, j + 16 * (2 * n + (q >> 1)), 64);
-                        const int sc0 = (int)(int8_t)((sd >> (16 * (q & 1))) & 0xff);
-                        const int sc1 = (int)(int8_t)((sd >> (16 * (q & 1) + 8)) & 0xff);
-                        is0 += __mul24(sc0, c[0]) + __mul24(sc1, c[1]);  // |c| < 2^23
-                        is1 += __mul24(sc0, c[2]) + __mul24(sc1, c[3]);
-                    }
-                }
-                const int isv[2] = {is0 - 32 * (int)accm[0], is1 - 32 * (int)accm[1]};
-#pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    const int tok = 2 * G + u;
-                    if (SUBSUMS && tok < ncols && row < mb.rows) sub[((int64_t)tok * mb.rows + row) * nb + b] = isv[u];
-                    out[u] += (dw * (float)isv[u]) * dq[tok * nbs + bl];
-                }
-            }
+            sk_block<WT, SUBSUMS>(w[i], codes, kstride, dq, nbs, bsum, BS, bl, b, row, mb.rows, nb, ncols, sub, lane,
+                                  out);
         }
         if (grp == ngrp - 1) {  // the tile's slice is done: store, or leave the partials for ghip_sk_reduce
 #pragma unroll
@@ -529,6 +637,319 @@ SK_KERNEL(ghip_sk_q6_K_s8, 14, 8, false)
 SK_KERNEL(ghip_sk_q6_K_sub_s4, 14, 4, true)
 SK_KERNEL(ghip_sk_q6_K_sub_s8, 14, 8, true)
 
+
+// ================================================================ whole K
+// Decode MUL_MAT at 4..8 activation rows (Q4_K, Q6_K) from ready Q8_K rows
+// (ghip_quantize_q8_K's output, or a src1 that is Q8_K already): one launch,
+// no reduction launch, and each activation block quantized once per call
+// rather than once per workgroup.  A workgroup of W wavefronts owns T tiles
+// of 16 weight rows over the whole K axis; wavefront w takes the super-blocks
+// [w SW, w SW + SW):
+//  - all of its weight loads (T tiles x SW super-blocks, into registers) go
+//    out first, then it copies the 8 rows' Q8_K blocks of its super-blocks
+//    into an LDS image of its own (no other wavefront reads it: no barrier);
+//  - it runs the split-K arithmetic (sk_block) on each tile, the tile's fp32
+//    partial kept in registers;
+//  - the partials go to LDS over its image, and after one barrier each output
+//    is the sum of the W partials in wavefront (K) order.
+// SW and W depend on K alone, so a matrix gives the same bits alone and in a
+// grouped launch.  The image: codes [8][CS] | d [8][SW] | 16-element sums
+// [8][BS] | 256 SW zero bytes (the Q4_K A operand's empty lane groups).  Host
+// mirror of its size in ghip.cpp (sq_img_bytes).
+constexpr int sq_img_bytes(int sw) { return 8 * (sw * QK_K + 16) + 8 * sw * 4 + 8 * (sw * 16 + 4) * 4 + sw * QK_K; }
+
+template <int WT, int SW, int T, bool SUBSUMS>
+__device__ __forceinline__ void sq_impl(const SkLaunch &g, int64_t w_row_bytes, int nb, const uint8_t *__restrict__ act,
+                                        int64_t act_rb, int ncols, int32_t *__restrict__ sub) {
+    constexpr int NC = 8, NW = sk_nw(WT);
+    constexpr int BB = WT == 12 ? Q4K_BYTES : Q6K_BYTES;
+    constexpr int CS = SW * QK_K + 16, BS = SW * 16 + 4, IMG = sq_img_bytes(SW);
+    static_assert(T * NC * 16 * 4 <= IMG, "the partials fit over the image");
+    extern __shared__ __attribute__((aligned(16))) uint8_t sq_smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int W = (int)(blockDim.x >> 6);
+    const int j = lane & 15, G = lane >> 4;
+    int8_t *codes = (int8_t *)(sq_smem + wave * IMG);
+    float *dq = (float *)(codes + NC * CS);
+    int *bsum = (int *)(dq + NC * SW);
+    const int b0 = wave * SW, nbs = min(SW, nb - b0);  // >= 1: W = ceil(nb / SW)
+    const int tile0 = (int)blockIdx.x * T;
+
+    auto member = [&](int tile) {
+        int i = 0;
+#pragma unroll
+        for (int k = 1; k < 4; k++)
+            if (k < g.n && tile >= g.m[k].tile0) i = k;
+        return i;
+    };
+    // activation blocks (token c, super-block b0 + bl), 16 lanes each, 4 per
+    // round: block 4r + lane / 16 is c = its index % 8, bl = its index / 8
+    constexpr int R = 2 * SW;
+    uint4 av[R];
+    int as[R];
+    float ad[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int blk = 4 * r + G, c = blk & 7, bl = blk >> 3, l = lane & 15;
+        av[r] = make_uint4(0, 0, 0, 0);
+        as[r] = 0;
+        ad[r] = 0.0f;
+        if (bl < nbs && c < ncols) {
+            const uint8_t *A = act + (int64_t)c * act_rb + (int64_t)(b0 + bl) * Q8K_BYTES;
+            av[r] = ld16(A + 4 + 16 * l);
+            as[r] = (int)(int16_t)ld2(A + 260 + 2 * l);
+            ad[r] = __uint_as_float(ld4(A));
+        }
+    }
+    uint32_t w[T][SW][NW];
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        const int tile = tile0 + t;
+        if (tile >= g.n_tiles) break;
+        const SkMember &mb = g.m[member(tile)];
+        const int row = (tile - mb.tile0) * 16 + j;
+        const uint8_t *rp = mb.W + (int64_t)min(row, mb.rows - 1) * w_row_bytes + (int64_t)b0 * BB;
+#pragma unroll
+        for (int bl = 0; bl < SW; bl++) {
+            if (bl >= nbs) break;
+            if constexpr (WT == 12) q4k16_load(rp + (int64_t)bl * BB, G, w[t][bl]);
+            else sk_load<WT>(rp + (int64_t)bl * BB, G, w[t][bl]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int blk = 4 * r + G, c = blk & 7, bl = blk >> 3, l = lane & 15;
+        if (bl < nbs) {
+            *reinterpret_cast<uint4 *>(codes + c * CS + bl * QK_K + 16 * l) = av[r];
+            bsum[c * BS + bl * 16 + l] = as[r];
+            if (l == 0) dq[c * SW + bl] = ad[r];
+        }
+    }
+    int8_t *zeros = (int8_t *)(bsum + NC * BS);
+    for (int o = 16 * lane; o < SW * QK_K; o += 1024) *reinterpret_cast<uint4 *>(zeros + o) = make_uint4(0, 0, 0, 0);
+    // Q4_K A operand base of this lane: token j >> 1 in the lane groups of its
+    // parity j & 1, else the zero region
+    const int8_t *abase = (G >> 1) == (j & 1) ? codes + (j >> 1) * CS + 64 * (j & 1) + 16 * (G & 1) : zeros;
+    (void)abase;
+    // the image is written and read by this wavefront only: order its LDS
+    // stores before the other lanes' reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    float out[T][2];
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        out[t][0] = out[t][1] = 0.0f;
+        const int tile = tile0 + t;
+        if (tile >= g.n_tiles) break;
+        const SkMember &mb = g.m[member(tile)];
+        const int row = (tile - mb.tile0) * 16 + j;
+#pragma unroll
+        for (int bl = 0; bl < SW; bl++) {
+            if (bl >= nbs) break;
+#ifdef SQ_ABL
+            uint32_t x = 0;
+#pragma unroll
+            for (int i = 0; i < NW; i++) x ^= w[t][bl][i];
+            out[t][0] += (float)(x & 1);
+#else
+            if constexpr (WT == 12)
+                q4k16_block<SUBSUMS>(w[t][bl], abase, dq, SW, bsum, BS, bl, b0 + bl, row, mb.rows, nb, ncols, sub,
+                                     lane, out[t]);
+            else
+                sk_block<WT, SUBSUMS>(w[t][bl], codes, CS, dq, SW, bsum, BS, bl, b0 + bl, row, mb.rows, nb, ncols, sub,
+                                      lane, out[t]);
+#endif
+        }
+    }
+    // partials [T][8 tokens][16 rows] over this wavefront's image
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float *part = (float *)(sq_smem + wave * IMG);
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        part[(t * NC + 2 * G) * 16 + j] = out[t][0];
+        part[(t * NC + 2 * G + 1) * 16 + j] = out[t][1];
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < T * NC * 16; idx += blockDim.x) {
+        const int t = idx >> 7, tok = (idx >> 4) & 7, r = idx & 15, tile = tile0 + t;
+        if (tile >= g.n_tiles || tok >= ncols) continue;
+        const SkMember &mb = g.m[member(tile)];
+        const int row = (tile - mb.tile0) * 16 + r;
+        if (row >= mb.rows) continue;
+        float acc = 0.0f;
+        for (int k = 0; k < W; k++) {
+            const float v = ((const float *)(sq_smem + k * IMG))[idx];
+            acc = k == 0 ? v : acc + v;
+        }
+        mb.dst[(int64_t)tok * mb.ldd + row] = acc;
+    }
+}
+
+// Streaming form: a workgroup takes tiles [T bx, T bx + T) (T from the
+// host), each wavefront with the next tile's weights in flight while it
+// computes the current one; tile t's partials go to LDS beside the image
+// (partials [T][8 tokens][16 rows] per wavefront), and after one barrier
+// every output of the workgroup is summed in wavefront order.
+template <int WT, int SW, bool SUBSUMS>
+__device__ __forceinline__ void sqs_impl(const SkLaunch &g, int T, int64_t w_row_bytes, int nb,
+                                         const uint8_t *__restrict__ act, int64_t act_rb, int ncols,
+                                         int32_t *__restrict__ sub) {
+    constexpr int NC = 8, NW = sk_nw(WT);
+    constexpr int BB = WT == 12 ? Q4K_BYTES : Q6K_BYTES;
+    constexpr int CS = SW * QK_K + 16, BS = SW * 16 + 4, IMG = sq_img_bytes(SW);
+    extern __shared__ __attribute__((aligned(16))) uint8_t sq_smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int W = (int)(blockDim.x >> 6);
+    const int j = lane & 15, G = lane >> 4;
+    const int stride = IMG + T * NC * 16 * 4;  // LDS bytes per wavefront
+    int8_t *codes = (int8_t *)(sq_smem + wave * stride);
+    float *dq = (float *)(codes + NC * CS);
+    int *bsum = (int *)(dq + NC * SW);
+    float *part = (float *)(sq_smem + wave * stride + IMG);
+    const int b0 = wave * SW, nbs = min(SW, nb - b0);  // >= 1: W = ceil(nb / SW)
+    const int tile0 = (int)blockIdx.x * T, cnt = min(T, g.n_tiles - tile0);  // >= 1
+
+    auto member = [&](int tile) {
+        int i = 0;
+#pragma unroll
+        for (int k = 1; k < 4; k++)
+            if (k < g.n && tile >= g.m[k].tile0) i = k;
+        return i;
+    };
+    constexpr int R = 2 * SW;
+    uint4 av[R];
+    int as[R];
+    float ad[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int blk = 4 * r + G, c = blk & 7, bl = blk >> 3, l = lane & 15;
+        av[r] = make_uint4(0, 0, 0, 0);
+        as[r] = 0;
+        ad[r] = 0.0f;
+        if (bl < nbs && c < ncols) {
+            const uint8_t *A = act + (int64_t)c * act_rb + (int64_t)(b0 + bl) * Q8K_BYTES;
+            av[r] = ld16(A + 4 + 16 * l);
+            as[r] = (int)(int16_t)ld2(A + 260 + 2 * l);
+            ad[r] = __uint_as_float(ld4(A));
+        }
+    }
+    auto load = [&](uint32_t (&w)[SW][NW], int t) {
+        const int tile = tile0 + t;
+        const SkMember &mb = g.m[member(tile)];
+        const int row = (tile - mb.tile0) * 16 + j;
+        const uint8_t *rp = mb.W + (int64_t)min(row, mb.rows - 1) * w_row_bytes + (int64_t)b0 * BB;
+#pragma unroll
+        for (int bl = 0; bl < SW; bl++) {
+            if (bl >= nbs) break;
+            if constexpr (WT == 12) q4k16_load(rp + (int64_t)bl * BB, G, w[bl]);
+            else sk_load<WT>(rp + (int64_t)bl * BB, G, w[bl]);
+        }
+    };
+    uint32_t wa[SW][NW], wb[SW][NW];
+    load(wa, 0);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int blk = 4 * r + G, c = blk & 7, bl = blk >> 3, l = lane & 15;
+        if (bl < nbs) {
+            *reinterpret_cast<uint4 *>(codes + c * CS + bl * QK_K + 16 * l) = av[r];
+            bsum[c * BS + bl * 16 + l] = as[r];
+            if (l == 0) dq[c * SW + bl] = ad[r];
+        }
+    }
+    int8_t *zeros = (int8_t *)(bsum + NC * BS);
+    for (int o = 16 * lane; o < SW * QK_K; o += 1024) *reinterpret_cast<uint4 *>(zeros + o) = make_uint4(0, 0, 0, 0);
+    // Q4_K A operand base of this lane: token j >> 1 in the lane groups of its
+    // parity j & 1, else the zero region
+    const int8_t *abase = (G >> 1) == (j & 1) ? codes + (j >> 1) * CS + 64 * (j & 1) + 16 * (G & 1) : zeros;
+    (void)abase;
+    // the image is written and read by this wavefront only: order its LDS
+    // stores before the other lanes' reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    auto compute = [&](const uint32_t (&w)[SW][NW], int t) {
+        const int tile = tile0 + t;
+        const SkMember &mb = g.m[member(tile)];
+        const int row = (tile - mb.tile0) * 16 + j;
+        float o[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int bl = 0; bl < SW; bl++) {
+            if (bl >= nbs) break;
+#ifdef SQ_ABL
+            uint32_t x = 0;
+#pragma unroll
+            for (int i = 0; i < NW; i++) x ^= w[bl][i];
+            o[0] += (float)(x & 1);
+#else
+            if constexpr (WT == 12)
+                q4k16_block<SUBSUMS>(w[bl], abase, dq, SW, bsum, BS, bl, b0 + bl, row, mb.rows, nb, ncols, sub, lane,
+                                     o);
+            else
+                sk_block<WT, SUBSUMS>(w[bl], codes, CS, dq, SW, bsum, BS, bl, b0 + bl, row, mb.rows, nb, ncols, sub,
+                                      lane, o);
+#endif
+        }
+        part[(t * NC + 2 * G) * 16 + j] = o[0];
+        part[(t * NC + 2 * G + 1) * 16 + j] = o[1];
+    };
+    for (int t = 0; t < cnt;) {
+        if (t + 1 < cnt) load(wb, t + 1);
+        compute(wa, t);
+        if (++t >= cnt) break;
+        if (t + 1 < cnt) load(wa, t + 1);
+        compute(wb, t);
+        ++t;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < cnt * NC * 16; idx += blockDim.x) {
+        const int t = idx >> 7, tok = (idx >> 4) & 7, r = idx & 15, tile = tile0 + t;
+        if (tok >= ncols) continue;
+        const SkMember &mb = g.m[member(tile)];
+        const int row = (tile - mb.tile0) * 16 + r;
+        if (row >= mb.rows) continue;
+        float acc = 0.0f;
+        for (int k = 0; k < W; k++) {
+            const float v = ((const float *)(sq_smem + k * stride + IMG))[idx];
+            acc = k == 0 ? v : acc + v;
+        }
+        mb.dst[(int64_t)tok * mb.ldd + row] = acc;
+    }
+}
+
+#define SQS_KERNEL(NAME, WT, SW, SUBS)                                                                             \
+    extern "C" __global__ void __launch_bounds__(1024)                                                             \
+        NAME(SkLaunch g, int T, int64_t w_row_bytes, int nb, const uint8_t *__restrict__ act, int64_t act_rb,      \
+             int ncols, int32_t *__restrict__ sub) {                                                               \
+        sqs_impl<WT, SW, SUBS>(g, T, w_row_bytes, nb, act, act_rb, ncols, sub);                                     \
+    }
+SQS_KERNEL(ghip_sqs_q4_K_w2, 12, 2, false)
+SQS_KERNEL(ghip_sqs_q4_K_sub_w2, 12, 2, true)
+SQS_KERNEL(ghip_sqs_q6_K_w2, 14, 2, false)
+SQS_KERNEL(ghip_sqs_q6_K_sub_w2, 14, 2, true)
+
+#define SQ_KERNEL(NAME, WT, SW, T, SUBS)                                                                           \
+    extern "C" __global__ void __launch_bounds__(1024)                                                             \
+        NAME(SkLaunch g, int64_t w_row_bytes, int nb, const uint8_t *__restrict__ act, int64_t act_rb, int ncols,  \
+             int32_t *__restrict__ sub) {                                                                          \
+        sq_impl<WT, SW, T, SUBS>(g, w_row_bytes, nb, act, act_rb, ncols, sub);                                      \
+    }
+#define SQ_KERNELS(TN, WT, SW, T)                                  \
+    SQ_KERNEL(ghip_sq_##TN##_w##SW##_t##T, WT, SW, T, false)       \
+    SQ_KERNEL(ghip_sq_##TN##_sub_w##SW##_t##T, WT, SW, T, true)
+// (T = 4 at SW = 2 and T = 2 at SW = 4 exceed 128 VGPRs and spill)
+SQ_KERNELS(q4_K, 12, 2, 1)
+SQ_KERNELS(q4_K, 12, 2, 2)
+SQ_KERNELS(q4_K, 12, 4, 1)
+SQ_KERNELS(q6_K, 14, 2, 1)
+SQ_KERNELS(q6_K, 14, 2, 2)
+SQ_KERNELS(q6_K, 14, 4, 1)
 
 // The K-slices' partials of up to 4 matrices added in slice order:
 // dst[c][r] = sum_k part[k][c][r]; one lane per (matrix, column, row).  Here

@@ -299,19 +299,55 @@ def test_gemm_q8_family_registered(be):
     (O.Q6_K, 8192, 130, 7),    # 32 super-blocks: slices of 8
     (O.Q6_K, 256, 16, 8),
 ])
-def test_split_k_decode(be, monkeypatch, ty, n, rows, cols):
-    """The split-K decode kernels (Q4_K, Q6_K at 4..8 rows; Q4_K forced onto
-    them below 8192 weight rows): the activation slice quantized inside each
-    workgroup, the K-slices' partials added in order by ghip_sk_reduce;
-    ragged slices, steps and row tiles; Q8_K bytes and int32 sub-sums
+@pytest.mark.parametrize("route", ["whole_k", "split_k"])
+def test_split_k_decode(be, monkeypatch, route, ty, n, rows, cols):
+    """The 4..8-row decode kernels for Q4_K and Q6_K.  whole_k (the default,
+    ghip_sq_*): one wavefront per 2-super-block K-slice of a workgroup that
+    owns whole rows, the ready Q8_K rows copied into each wavefront's LDS
+    image, the slices' partials added in wavefront order; 1..16 wavefronts,
+    a ragged last slice and 16-row tiles.  split_k (GHIP_SQ=0; Q4_K forced
+    onto it below 8192 weight rows): the activation slice quantized inside
+    each workgroup, the K-slices' partials added in order by ghip_sk_reduce;
+    ragged slices, steps and row tiles.  Q8_K bytes and int32 sub-sums
     bit-exact."""
-    monkeypatch.setenv("GHIP_SK_MIN_ROWS", "1")
+    if route == "split_k":
+        monkeypatch.setenv("GHIP_SQ", "0")
+        monkeypatch.setenv("GHIP_SK_MIN_ROWS", "1")
+    print(f"{route} decode type={ty} n={n} rows={rows} cols={cols}", flush=True)
     run_case(be, ty, n, rows, cols, seed=rows + cols)
+
+
+@pytest.mark.parametrize("ty,n,rows,cols", [
+    (O.Q4_K, 14336, 90, 8),   # 56 super-blocks: 4-block slices, 14 wavefronts
+    (O.Q6_K, 14336, 40, 6),
+    (O.Q4_K, 8448, 33, 4),    # 33 super-blocks: 4-block slices, the last one 1 block
+    (O.Q4_K, 13312, 20, 5),   # 52 super-blocks: 13 wavefronts
+])
+def test_whole_k_decode_long_rows(be, ty, n, rows, cols):
+    """The whole-K decode kernels on rows of 33..56 super-blocks (4-block
+    slices per wavefront, up to 14 wavefronts and 159 KB of LDS) against the
+    oracle; Q8_K bytes and sub-sums bit-exact."""
+    print(f"whole-K long rows type={ty} n={n} rows={rows} cols={cols}", flush=True)
+    run_case(be, ty, n, rows, cols, seed=rows + cols + 1)
+
+
+@pytest.mark.parametrize("ty,n", [(O.Q4_K, 4096), (O.Q6_K, 4096)])
+def test_whole_k_tiles_per_workgroup(be, monkeypatch, ty, n):
+    """One or two 16-row tiles per workgroup (GHIP_SQ_T) give the same bits:
+    the tile count changes which workgroup computes a row, not its sums."""
+    w, x = make(ty, n, 2000, 8, seed=4)
+    wd, xd = torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda()
+    print(f"whole-K tiles per workgroup type={ty}", flush=True)
+    monkeypatch.setenv("GHIP_SQ_T", "1")
+    want = be.mul_mat(wd, ty, n, xd).clone()
+    monkeypatch.setenv("GHIP_SQ_T", "2")
+    assert torch.equal(be.mul_mat(wd, ty, n, xd), want)
 
 
 def test_split_k_tiles_per_workgroup(be, monkeypatch):
     """Few workgroups (GHIP_SK_WGS): each walks several tiles with the next
     step's weights in flight; same bits as one tile per workgroup."""
+    monkeypatch.setenv("GHIP_SQ", "0")
     w, x = make(O.Q4_K, 4096, 14336, 8, seed=3)
     wd, xd = torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda()
     print("split-K tiles per workgroup", flush=True)

@@ -749,19 +749,12 @@ __device__ __forceinline__ void sq_impl(const SkLaunch &g, int64_t w_row_bytes, 
 #pragma unroll
         for (int bl = 0; bl < SW; bl++) {
             if (bl >= nbs) break;
-#ifdef SQ_ABL
-            uint32_t x = 0;
-#pragma unroll
-            for (int i = 0; i < NW; i++) x ^= w[t][bl][i];
-            out[t][0] += (float)(x & 1);
-#else
             if constexpr (WT == 12)
                 q4k16_block<SUBSUMS>(w[t][bl], abase, dq, SW, bsum, BS, bl, b0 + bl, row, mb.rows, nb, ncols, sub,
                                      lane, out[t]);
             else
                 sk_block<WT, SUBSUMS>(w[t][bl], codes, CS, dq, SW, bsum, BS, bl, b0 + bl, row, mb.rows, nb, ncols, sub,
                                       lane, out[t]);
-#endif
         }
     }
     // partials [T][8 tokens][16 rows] over this wavefront's image
@@ -882,19 +875,12 @@ __device__ __forceinline__ void sqs_impl(const SkLaunch &g, int T, int64_t w_row
 #pragma unroll
         for (int bl = 0; bl < SW; bl++) {
             if (bl >= nbs) break;
-#ifdef SQ_ABL
-            uint32_t x = 0;
-#pragma unroll
-            for (int i = 0; i < NW; i++) x ^= w[bl][i];
-            o[0] += (float)(x & 1);
-#else
             if constexpr (WT == 12)
                 q4k16_block<SUBSUMS>(w[bl], abase, dq, SW, bsum, BS, bl, b0 + bl, row, mb.rows, nb, ncols, sub, lane,
                                      o);
             else
                 sk_block<WT, SUBSUMS>(w[bl], codes, CS, dq, SW, bsum, BS, bl, b0 + bl, row, mb.rows, nb, ncols, sub,
                                       lane, o);
-#endif
         }
         part[(t * NC + 2 * G) * 16 + j] = o[0];
         part[(t * NC + 2 * G + 1) * 16 + j] = o[1];

@@ -95,6 +95,10 @@ struct ghip_context {
     void *user_ws = nullptr;
     size_t user_ws_size = 0;
     void *call_ws = nullptr;
+    //  - hold: bytes at the start of the workspace that a ghip_graph_compute
+    //    call keeps for its pre-quantized activations; the ops it runs get the
+    //    workspace after them
+    size_t hold = 0;
     size_t call_ws_size = 0;
     // the stream of the previous call: a call on another stream first waits
     // for it, so the two never share the workspace concurrently
@@ -216,6 +220,11 @@ struct ghip_context {
         return st;
     }
     ghip_status workspace_get(size_t bytes, hipStream_t s, void **out) {
+        ghip_status st = workspace_base(bytes + hold, s, out);
+        if (st == GHIP_STATUS_SUCCESS) *out = (uint8_t *)*out + hold;
+        return st;
+    }
+    ghip_status workspace_base(size_t bytes, hipStream_t s, void **out) {
         if (dry_run && !call_ws && !user_ws) {
             // an address range no allocation uses: the launches are checked, never run
             *out = (void *)(uintptr_t)(1ull << 46);
@@ -1796,7 +1805,9 @@ ghip_status mul_mat_multi_gemm(ghip_context *ctx, const ghip_node *nodes, int n,
 }
 
 // 2..4 sibling MUL_MATs (joins_group holds) as one multi-matrix GEMV launch
-ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipStream_t s) {
+// pre_act: the group's activation rows already quantized to Q8_K (whole-K route)
+ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipStream_t s,
+                          const uint8_t *pre_act = nullptr) {
     std::lock_guard<std::mutex> lock(ctx->mu);
     MulMatPlan p[4];
     ghip_status st;
@@ -1840,13 +1851,16 @@ ghip_status mul_mat_multi(ghip_context *ctx, const ghip_node *nodes, int n, hipS
                            (int64_t)p0.act_row_bytes, nc);
     }
     if (use_sq(p0)) {
-        // the activation rows quantized once, then the whole-K kernel over all members
-        const size_t act_bytes = ((size_t)(p0.M * p0.act_row_bytes) + 255) & ~(size_t)255;
-        void *ws = nullptr;
-        st = ctx->workspace(act_bytes, s, &ws);
-        if (st != GHIP_STATUS_SUCCESS) return st;
-        st = quantize_act(ctx, p0, nodes[0].src[1], ws, s);
-        if (st != GHIP_STATUS_SUCCESS) return st;
+        // the activation rows quantized once (here or before the graph's first
+        // node), then the whole-K kernel over all members
+        void *ws = (void *)pre_act;
+        if (!ws) {
+            const size_t act_bytes = ((size_t)(p0.M * p0.act_row_bytes) + 255) & ~(size_t)255;
+            st = ctx->workspace(act_bytes, s, &ws);
+            if (st != GHIP_STATUS_SUCCESS) return st;
+            st = quantize_act(ctx, p0, nodes[0].src[1], ws, s);
+            if (st != GHIP_STATUS_SUCCESS) return st;
+        }
         SkLaunch g{};
         g.n = n;
         for (int i = 0; i < n; i++) {
@@ -2416,26 +2430,143 @@ ghip_status ghip_mul_mat_act(ghip_context *ctx, const ghip_tensor *src0, const g
     return mul_mat_impl(ctx, src0, src1, nullptr, nullptr, out, stream);
 }
 
+// Host mirror of Q8KSegs in ghip_quant.hip.
+struct Q8KSegs {
+    const float *x[8];
+    int64_t x_stride[8];
+    uint8_t *y[8];
+    int64_t y_stride[8];
+    int64_t nb[8];
+    int64_t n_mat[8];
+    int64_t w0[9];
+    int n;
+};
+
+// ghip_graph_compute's inputs are ready when it is called: a group on the
+// whole-K decode route whose f32 activation rows no earlier node writes has
+// them quantized before the first node, all such groups in one launch
+// (ghip_quantize_q8_K_segs) instead of one quantize launch each.  The Q8_K
+// rows stay at the start of the workspace (ctx->hold) until the call ends;
+// group gi reads them through pre[gi] (pre_view[gi]: a Q8_K view for a single
+// node).  Each group keeps its own quantization (its n_mat rule); groups with
+// the same rows and rule share them.  GHIP_GRAPH_PREQUANT=0 turns this off.
+ghip_status prequantize(ghip_context *ctx, const ghip_node *nodes, const std::vector<std::pair<int, int>> &groups,
+                        std::vector<const uint8_t *> &pre, std::vector<ghip_tensor> &pre_view, hipStream_t s) {
+    if (env_int("GHIP_GRAPH_PREQUANT", 1) == 0 || env_int("GHIP_GRAPH_FUSE", 1) == 0) return GHIP_STATUS_SUCCESS;
+    struct Seg {
+        const ghip_tensor *x;
+        MulMatPlan p;
+        size_t off;
+    };
+    std::vector<Seg> segs;
+    std::vector<int> seg_of(groups.size(), -1);
+    size_t total = 0;
+    for (size_t gi = 0; gi < groups.size(); gi++) {
+        const ghip_node &nd = nodes[groups[gi].first];
+        if (nd.op != GHIP_OP_MUL_MAT || !nd.src[0] || !nd.src[1] || !nd.dst) continue;
+        const ghip_tensor *x = nd.src[1];
+        if (x->type != GHIP_TYPE_F32 || x->ne[2] != 1 || x->ne[3] != 1) continue;
+        MulMatPlan p;
+        ghip_status st;
+        {
+            std::lock_guard<std::mutex> lock(ctx->mu);
+            if (!plan_mul_mat(ctx, nd.src[0], x, nd.dst, p, st)) {
+                ctx->err.clear();
+                continue;  // the node itself reports it
+            }
+        }
+        if (!use_sq(p) || p.act_pre || p.M == 0 || p.N == 0) continue;
+        bool ready = true;
+        for (int k = 0; k < groups[gi].first && ready; k++) ready = !overlaps(nodes[k].dst, x);
+        if (!ready) continue;
+        int found = -1;
+        for (size_t j = 0; j < segs.size() && found < 0; j++)
+            if (same_view(segs[j].x, x) && segs[j].p.n_mat == p.n_mat && segs[j].p.K == p.K) found = (int)j;
+        if (found < 0) {
+            if (segs.size() == 8) continue;
+            segs.push_back({x, p, total});
+            total += ((size_t)(p.M * p.act_row_bytes) + 255) & ~(size_t)255;
+            found = (int)segs.size() - 1;
+        }
+        seg_of[gi] = found;
+    }
+    if (segs.size() < 2) return GHIP_STATUS_SUCCESS;  // nothing to save over the groups' own launches
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    if (!ctx->set_device()) return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "hipSetDevice failed");
+    ghip_status st = ctx->begin(s);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    void *ws = nullptr;
+    st = ctx->workspace(total, s, &ws);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    Q8KSegs g{};
+    int64_t waves = 0;
+    for (size_t j = 0; j < segs.size(); j++) {
+        const MulMatPlan &p = segs[j].p;
+        uint8_t *y = (uint8_t *)ws + segs[j].off;
+        ctx->expect(y, (size_t)(p.M * p.act_row_bytes), "quantized activations");
+        g.x[j] = (const float *)segs[j].x->data;
+        g.x_stride[j] = (int64_t)segs[j].x->nb[1] / 4;
+        g.y[j] = y;
+        g.y_stride[j] = p.act_row_bytes;
+        g.nb[j] = p.K / 256;
+        g.n_mat[j] = p.n_mat;
+        g.w0[j] = waves;
+        waves += p.M * (p.K / 256);
+    }
+    g.n = (int)segs.size();
+    for (int j = g.n; j <= 8; j++) g.w0[j] = waves;
+    st = ctx->launch("ghip_quantize_q8_K_segs", dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, g);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    ctx->hold = (total + 255) & ~(size_t)255;
+    for (size_t gi = 0; gi < groups.size(); gi++) {
+        if (seg_of[gi] < 0) continue;
+        const Seg &sg = segs[seg_of[gi]];
+        pre[gi] = (const uint8_t *)ws + sg.off;
+        ghip_tensor &v = pre_view[gi];
+        v = *sg.x;
+        v.type = GHIP_TYPE_Q8_K;
+        v.data = (void *)pre[gi];
+        v.nb[0] = 292;
+        v.nb[1] = (size_t)sg.p.act_row_bytes;
+        v.nb[2] = v.nb[1] * (size_t)v.ne[1];
+        v.nb[3] = v.nb[2];
+    }
+    return GHIP_STATUS_SUCCESS;
+}
+
 ghip_status ghip_graph_compute(ghip_context *ctx, const ghip_node *nodes, int32_t n_nodes, void *stream) {
     if (!ctx) return GHIP_STATUS_BACKEND_ERROR;
     if (n_nodes < 0 || (n_nodes > 0 && !nodes))
         return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "graph_compute: bad node list");
     const bool fuse = env_int("GHIP_GRAPH_FUSE", 1) != 0;
-    int i = 0;
-    while (i < n_nodes) {
-        const ghip_node &nd = nodes[i];
-        ghip_status st;
+    // the node groups: siblings run as one multi-matrix launch
+    std::vector<std::pair<int, int>> groups;
+    for (int i = 0; i < n_nodes;) {
         int next = i + 1;
+        if (nodes[i].op == GHIP_OP_MUL_MAT && fuse && multi_candidate(nodes[i]))
+            while (next < n_nodes && next - i < 4 && joins_group(nodes, i, next)) next++;
+        groups.push_back({i, next});
+        i = next;
+    }
+    std::vector<const uint8_t *> pre(groups.size(), nullptr);
+    std::vector<ghip_tensor> pre_view(groups.size());
+    ghip_status st = prequantize(ctx, nodes, groups, pre, pre_view, (hipStream_t)stream);
+    if (st != GHIP_STATUS_SUCCESS) return st;
+    struct Unhold {
+        ghip_context *c;
+        ~Unhold() { c->hold = 0; }
+    } unhold{ctx};
+    for (size_t gi = 0; gi < groups.size(); gi++) {
+        const int i = groups[gi].first, next = groups[gi].second;
+        const ghip_node &nd = nodes[i];
         switch (nd.op) {
         case GHIP_OP_MUL_MAT:
-            if (fuse && multi_candidate(nd))
-                while (next < n_nodes && next - i < 4 && joins_group(nodes, i, next)) next++;
             if (next - i >= 2)
                 st = nd.src[1]->ne[1] >= env_int("GHIP_GEMM_MIN_ROWS", 16)
                          ? mul_mat_multi_gemm(ctx, nodes + i, next - i, (hipStream_t)stream)
-                         : mul_mat_multi(ctx, nodes + i, next - i, (hipStream_t)stream);
+                         : mul_mat_multi(ctx, nodes + i, next - i, (hipStream_t)stream, pre[gi]);
             else
-                st = ghip_mul_mat(ctx, nd.src[0], nd.src[1], nd.dst, stream);
+                st = ghip_mul_mat(ctx, nd.src[0], pre[gi] ? &pre_view[gi] : nd.src[1], nd.dst, stream);
             break;
         case GHIP_OP_MUL_MAT_ID:
             st = ghip_mul_mat_id(ctx, nd.src[0], nd.src[1], nd.src[2], nd.dst, stream);
@@ -2447,7 +2578,6 @@ ghip_status ghip_graph_compute(ghip_context *ctx, const ghip_node *nodes, int32_
             return ctx->fail(GHIP_STATUS_BACKEND_ERROR, "graph_compute: node %d: op %d not supported", i, nd.op);
         }
         if (st != GHIP_STATUS_SUCCESS) return st;
-        i = next;
     }
     return GHIP_STATUS_SUCCESS;
 }

@@ -15,13 +15,9 @@
 // elements.  Rows r < n_mat use the quantize_mat_q8_K_4x8 values, the others
 // quantize_row_q8_K_ref (the reference's repack route quantizes the leading
 // ne11 - ne11 % 4 activation rows with the former, compute.rs:5350-5398).
-extern "C" __global__ void __launch_bounds__(256)
-ghip_quantize_q8_K(const float *__restrict__ x, int64_t x_stride, int64_t n, int64_t nrows,
-                   uint8_t *__restrict__ y, int64_t y_stride, int64_t n_mat) {
-    const int lane = threadIdx.x & 63;
-    const int64_t nb = n / QK_K;
-    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (wid >= nrows * nb) return;
+// wavefront wid of a matrix of nb super-blocks per row
+DEV void quantize_q8K_wave(const float *__restrict__ x, int64_t x_stride, int64_t nb, int64_t wid,
+                           uint8_t *__restrict__ y, int64_t y_stride, int64_t n_mat, int lane) {
     const int64_t row = wid / nb, b = wid - row * nb;
     float xs[4];
     __builtin_memcpy(xs, x + row * x_stride + b * QK_K + lane * 4, 16);
@@ -38,6 +34,38 @@ ghip_quantize_q8_K(const float *__restrict__ x, int64_t x_stride, int64_t n, int
         __builtin_memcpy(blk + 260 + 2 * (lane >> 2), &s16, 2);
     }
     if (lane == 0) __builtin_memcpy(blk, &d, 4);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+ghip_quantize_q8_K(const float *__restrict__ x, int64_t x_stride, int64_t n, int64_t nrows,
+                   uint8_t *__restrict__ y, int64_t y_stride, int64_t n_mat) {
+    const int64_t nb = n / QK_K;
+    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wid >= nrows * nb) return;
+    quantize_q8K_wave(x, x_stride, nb, wid, y, y_stride, n_mat, threadIdx.x & 63);
+}
+
+// Several activation matrices in one launch (ghip_graph_compute quantizes the
+// independent inputs of its whole-K decode groups together): segment i takes
+// wavefronts [w0[i], w0[i+1]).  Host mirror in ghip.cpp.
+struct Q8KSegs {
+    const float *x[8];
+    int64_t x_stride[8];
+    uint8_t *y[8];
+    int64_t y_stride[8];
+    int64_t nb[8];
+    int64_t n_mat[8];
+    int64_t w0[9];
+    int n;
+};
+
+extern "C" __global__ void __launch_bounds__(256) ghip_quantize_q8_K_segs(Q8KSegs g) {
+    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wid >= g.w0[g.n]) return;
+    int i = 0;
+    while (i + 1 < g.n && wid >= g.w0[i + 1]) i++;
+    quantize_q8K_wave(g.x[i], g.x_stride[i], g.nb[i], wid - g.w0[i], g.y[i], g.y_stride[i], g.n_mat[i],
+                      threadIdx.x & 63);
 }
 
 // quantize_row_q8_0 (runtime AVX2 arithmetic, quants.rs:331-362): 8 lanes per

@@ -203,3 +203,37 @@ def test_errors(be):
     node = ghip.Node(ghip.OP_MUL_MAT, [ghip.describe(w, 34, 256), ghip.describe(x, ghip.F32)], ghip.describe(out, ghip.F32))
     with pytest.raises(ghip.GhipError, match="not supported"):
         be.graph_compute([node])
+
+
+@pytest.mark.parametrize("m", [4, 8])
+def test_prequantized_inputs(be, monkeypatch, m):
+    """The whole-K decode groups whose activation rows no earlier node writes
+    are quantized in one launch before the first node; a node reading an
+    earlier node's output (down after gate) is quantized in order.  Every
+    output equals the result without the pre-pass (GHIP_GRAPH_PREQUANT=0)
+    and ghip_mul_mat's."""
+    import ghip
+    k = 4096
+    g = torch.Generator(device="cuda").manual_seed(m + 50)
+    shapes = [("q", 12, k, 4096), ("k", 12, k, 1024), ("v", 12, k, 1024), ("o", 12, k, 4096),
+              ("gate", 12, k, 14336), ("down", 14, 14336, 4096)]
+    ws = {nm: weights(be, ty, n, kk, i + 30) for i, (nm, ty, kk, n) in enumerate(shapes)}
+    x = torch.randn((m, k), device="cuda", generator=g)
+    xo = torch.randn((m, k), device="cuda", generator=g)
+    print(f"prequantized inputs m={m}", flush=True)
+
+    def run():
+        outs = {nm: torch.full((m, n), float("nan"), device="cuda") for nm, _, _, n in shapes}
+        src = {"q": x, "k": x, "v": x, "o": xo, "gate": x, "down": outs["gate"]}
+        be.graph_compute([ghip.mul_mat_node(ws[nm], ty, kk, src[nm], outs[nm]) for nm, ty, kk, _ in shapes])
+        torch.cuda.synchronize()
+        return outs, src
+
+    got, src = run()
+    monkeypatch.setenv("GHIP_GRAPH_PREQUANT", "0")
+    want, _ = run()
+    for nm, ty, kk, _ in shapes:
+        assert torch.equal(got[nm], want[nm]), nm
+        single = be.mul_mat(ws[nm], ty, kk, src[nm])
+        torch.cuda.synchronize()
+        assert torch.equal(got[nm], single), nm

@@ -2449,10 +2449,14 @@ struct Q8KSegs {
 // rows stay at the start of the workspace (ctx->hold) until the call ends;
 // group gi reads them through pre[gi] (pre_view[gi]: a Q8_K view for a single
 // node).  Each group keeps its own quantization (its n_mat rule); groups with
-// the same rows and rule share them.  GHIP_GRAPH_PREQUANT=0 turns this off.
+// the same rows and rule share them.  GHIP_GRAPH_PREQUANT=0 turns this off;
+// so does a workspace given with ghip_set_workspace.
 ghip_status prequantize(ghip_context *ctx, const ghip_node *nodes, const std::vector<std::pair<int, int>> &groups,
                         std::vector<const uint8_t *> &pre, std::vector<ghip_tensor> &pre_view, hipStream_t s) {
-    if (env_int("GHIP_GRAPH_PREQUANT", 1) == 0 || env_int("GHIP_GRAPH_FUSE", 1) == 0) return GHIP_STATUS_SUCCESS;
+    // (a caller's workspace is sized per node, by ghip_workspace_size: the
+    // held rows would not fit beside the largest node's)
+    if (env_int("GHIP_GRAPH_PREQUANT", 1) == 0 || env_int("GHIP_GRAPH_FUSE", 1) == 0 || ctx->user_ws || ctx->call_ws)
+        return GHIP_STATUS_SUCCESS;
     struct Seg {
         const ghip_tensor *x;
         MulMatPlan p;

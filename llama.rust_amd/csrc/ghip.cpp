@@ -601,11 +601,19 @@ bool use_sq(const MulMatPlan &p) {
 }
 // Q4_K takes split K from 5 rows: at 4 rows the matrix-core decode kernel is
 // faster (4096 -> 14336: 17.2 us split K, 15.6 us).
+// The whole-row decode kernels keep the activation rows' Q8_K image in LDS
+// (codes, scales and 16-element sums of up to 8 rows); past 160 KB (8 rows of
+// K > 15.5 K) only split K can take the matrix, whatever its row count.
+bool decode_image_fits(const MulMatPlan &p) {
+    const int64_t NC = p.M <= 1 ? 1 : p.M <= 2 ? 2 : p.M <= 4 ? 4 : 8;
+    return NC * p.K + NC * p.nb * 4 + NC * p.nb * 16 * 4 + 8 * 16 * 16 * 4 <= 160 * 1024;
+}
 bool use_sk(const MulMatPlan &p) {
     if (use_sq(p)) return false;
     if (p.act_pre || env_int("GHIP_SK", 1) == 0 || p.M < env_int("GHIP_MMA_MIN_ROWS", 4)) return false;
     if (p.wtype == GHIP_TYPE_Q4_K && p.M < env_int("GHIP_SK_Q4K_MIN_COLS", 5)) return false;
-    return (p.wtype == GHIP_TYPE_Q4_K || p.wtype == GHIP_TYPE_Q6_K) && p.M <= 8 && sk_rows_ok(p.wtype, p.N);
+    return (p.wtype == GHIP_TYPE_Q4_K || p.wtype == GHIP_TYPE_Q6_K) && p.M <= 8 &&
+           (sk_rows_ok(p.wtype, p.N) || !decode_image_fits(p));
 }
 size_t sk_part_bytes(const MulMatPlan &p) {
     const int64_t ns = sk_slices(p.nb);

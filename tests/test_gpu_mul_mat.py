@@ -298,6 +298,8 @@ def test_gemm_q8_family_registered(be):
     (O.Q6_K, 1792, 70, 4),     # 7 super-blocks
     (O.Q6_K, 8192, 130, 7),    # 32 super-blocks: slices of 8
     (O.Q6_K, 256, 16, 8),
+    (O.Q4_K, 16384, 40, 5),    # 64 super-blocks: past the whole-K LDS images, split K on every route
+    (O.Q6_K, 16384, 24, 6),
 ])
 @pytest.mark.parametrize("route", ["whole_k", "split_k"])
 def test_split_k_decode(be, monkeypatch, route, ty, n, rows, cols):

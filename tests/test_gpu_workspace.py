@@ -96,6 +96,38 @@ def test_caller_workspace(be):
     assert torch.equal(out, want)
 
 
+def test_caller_workspace_graph(be):
+    """A caller's workspace sized by ghip_workspace_size (the largest node)
+    covers a ghip_graph_compute call whose whole-K decode groups would
+    otherwise have their inputs quantized up front (that keeps Q8_K rows
+    ahead of the nodes' workspace, so it is off with a caller's workspace):
+    same bits as with the library's own workspace."""
+    import ghip
+    k, m = 2048, 8
+    g = torch.Generator(device="cuda").manual_seed(21)
+    shapes = [("q", 1024), ("k", 256), ("o", 1024), ("gate", 3072)]
+    ws = {nm: be.quantize(torch.randn((n, k), device="cuda", generator=g) * 0.02, ghip.Q4_K) for nm, n in shapes}
+    xs = {"x": torch.randn((m, k), device="cuda", generator=g), "xo": torch.randn((m, k), device="cuda", generator=g),
+          "xf": torch.randn((m, k), device="cuda", generator=g)}
+    src = {"q": "x", "k": "x", "o": "xo", "gate": "xf"}
+    print("caller workspace graph", flush=True)
+
+    def run():
+        outs = {nm: torch.full((m, n), float("nan"), device="cuda") for nm, n in shapes}
+        nodes = [ghip.mul_mat_node(ws[nm], ghip.Q4_K, k, xs[src[nm]], outs[nm]) for nm, _ in shapes]
+        be.graph_compute(nodes)
+        torch.cuda.synchronize()
+        return outs, nodes
+
+    want, nodes = run()
+    need = max(be.workspace_size(nd) for nd in nodes)
+    be.set_workspace(torch.empty(max(need, 256), dtype=torch.uint8, device="cuda"))
+    got, _ = run()
+    be.set_workspace(None)
+    for nm, _ in shapes:
+        assert torch.equal(got[nm], want[nm]), nm
+
+
 def test_two_streams(be):
     """Back-to-back calls on two streams share the workspace safely (the second
     stream waits for the first)."""

@@ -2115,7 +2115,8 @@ static ghip_status fa_sequence(ghip_context *ctx, const ghip_tensor *q, const gh
     if (st != GHIP_STATUS_SUCCESS) return st;
     const float *sk = sinks ? (const float *)sinks->data : nullptr;
     if (nsplit <= 64)
-        return ctx->launch("ghip_fa_merge_rows", dim3((unsigned)((T * H + 3) / 4)), dim3(256), 0, s,
+        return ctx->launch(nsplit <= 4 && env_int("GHIP_FA_MERGE_P4", 1) ? "ghip_fa_merge_rows_p4" : "ghip_fa_merge_rows",
+                           dim3((unsigned)((T * H + 3) / 4)), dim3(256), 0, s,
                            (const float *)ws, sk, (float *)dst->data, T * H, H, nsplit, D);
     return ctx->launch("ghip_fa_merge", dim3((unsigned)(T * H)), dim3(256), 0, s, (const float *)ws, sk,
                        (float *)dst->data, T, H, nsplit, D);

@@ -628,7 +628,7 @@ ghip_fa_mask_scan(const uint16_t *__restrict__ mask, int64_t mask_nb1, int64_t m
 // with the weights exp(M_z - M) of ghip_fa_merge; the first sixteen of them are
 // loaded before the weights are known, so the slice reads overlap the
 // statistics.  With WPR > 1 the wavefronts' sums meet in LDS in order.
-template <int WPR>
+template <int WPR, int PRE = 16>
 __device__ __forceinline__ void fa_merge_rows_impl(const float *__restrict__ part, const float *__restrict__ sinks,
                                                    float *__restrict__ dst, int nrows, int H, int nsplit, int DV) {
     __shared__ float red[4][2][64];
@@ -637,7 +637,6 @@ __device__ __forceinline__ void fa_merge_rows_impl(const float *__restrict__ par
     if (row >= nrows) return;  // uniform per row: all WPR wavefronts leave together
     const float *pr = part + (int64_t)row * nsplit * (2 + DV);
     const int c0 = min(lane, DV - 1), c1 = min(64 + lane, DV - 1);
-    constexpr int PRE = 16;
     float v0[PRE], v1[PRE];
 #pragma unroll
     for (int i = 0; i < PRE; i++) {
@@ -702,6 +701,14 @@ extern "C" __global__ void __launch_bounds__(256)
 ghip_fa_merge_rows(const float *__restrict__ part, const float *__restrict__ sinks, float *__restrict__ dst,
                    int nrows, int H, int nsplit, int DV) {
     fa_merge_rows_impl<1>(part, sinks, dst, nrows, H, nsplit, DV);
+}
+
+// at most 4 slices (the prefill route's usual split): the first PRE = 4 loads
+// are all of them (the same sums; PRE = 16 re-read the last slice 12 times)
+extern "C" __global__ void __launch_bounds__(256)
+ghip_fa_merge_rows_p4(const float *__restrict__ part, const float *__restrict__ sinks, float *__restrict__ dst,
+                      int nrows, int H, int nsplit, int DV) {
+    fa_merge_rows_impl<1, 4>(part, sinks, dst, nrows, H, nsplit, DV);
 }
 
 extern "C" __global__ void __launch_bounds__(256)

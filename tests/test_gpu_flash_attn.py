@@ -210,3 +210,37 @@ def test_mask_tile_classes(be, T, S, m2):
                                    v[h // (H // Hkv):h // (H // Hkv) + 1], m[h % m2], None, scale, n_chunks=8)
         err = float(np.max(np.abs(outs[1][:, h:h + 1] - want)))
         assert err <= TOL, f"head {h}: max-abs {err:.3e}"
+
+
+@pytest.mark.parametrize("sinks", [False, True])
+def test_merge_preload_four(be, sinks):
+    """At most 4 KV slices (T = 512, 32 / 8 heads: 4 slices) the merge loads
+    exactly the slices it sums (ghip_fa_merge_rows_p4): the same bits as the
+    16-slice preload (GHIP_FA_MERGE_P4=0), and the oracle's result."""
+    import os
+    H, Hkv, D, T, S = 32, 8, 128, 512, 2048
+    rng = np.random.default_rng(5 + sinks)
+    q = rng.standard_normal((H, T, D)).astype(np.float32)
+    k = rng.standard_normal((Hkv, S, D)).astype(np.float16)
+    v = rng.standard_normal((Hkv, S, D)).astype(np.float16)
+    m = np.zeros((T, S), dtype=np.float16)
+    for i in range(T):
+        m[i, S - T + i + 1:] = -np.inf
+    sk = (rng.standard_normal(H) * 2.0).astype(np.float32) if sinks else None
+    scale = 1.0 / np.sqrt(D)
+    t = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    print(f"fa merge preload 4 sinks={sinks}", flush=True)
+    outs = []
+    for flag in ("0", "1"):
+        os.environ["GHIP_FA_MERGE_P4"] = flag
+        try:
+            outs.append(be.flash_attn_ext(t(q), t(k), t(v), t(m), t(sk), scale).cpu().numpy())
+        finally:
+            del os.environ["GHIP_FA_MERGE_P4"]
+    assert np.array_equal(outs[0], outs[1])
+    for h in (0, 13, 31):
+        g = h // (H // Hkv)
+        want, _ = O.flash_attn_ext(q[h:h + 1], k[g:g + 1], v[g:g + 1], m, None if sk is None else sk[h:h + 1], scale,
+                                   n_chunks=8)
+        err = float(np.max(np.abs(outs[1][:, h:h + 1] - want)))
+        assert err <= TOL, f"head {h}: max-abs {err:.3e}"

@@ -1292,6 +1292,7 @@ struct FaParams {
     int k_f32, v_f32;
     const uint8_t *mflags;
     int nqb, ntile;
+    int direct;
 };
 
 float f32_param(const ghip_tensor *t, int i) {
@@ -2062,6 +2063,7 @@ static ghip_status fa_sequence(ghip_context *ctx, const ghip_tensor *q, const gh
     p.mflags = nullptr;
     p.nqb = L.nqb;
     p.ntile = L.ntile;
+    p.direct = 0;
     // shapes the tuned kernels do not take (F32 K or V, DK != DV, head sizes
     // other than 64 / 128, H / H_kv > 8) run the general row walk: with the
     // f16 accumulator where the reference's route is the row walk over an F16
@@ -2111,8 +2113,11 @@ static ghip_status fa_sequence(ghip_context *ctx, const ghip_tensor *q, const gh
         if (st != GHIP_STATUS_SUCCESS) return st;
         p.mflags = fl;
     }
+    // one KV slice (long prefills: every query tile and KV head already fills
+    // the GPU): the forward kernel writes the normalized rows, no merge
+    p.direct = nsplit == 1 && env_int("GHIP_FA_DIRECT", 1) != 0;
     st = ctx->launch(fwd, dim3((unsigned)(qtiles * H_kv * nsplit)), dim3(64 * G * QS), 0, s, p);
-    if (st != GHIP_STATUS_SUCCESS) return st;
+    if (st != GHIP_STATUS_SUCCESS || p.direct) return st;
     const float *sk = sinks ? (const float *)sinks->data : nullptr;
     if (nsplit <= 64)
         return ctx->launch(nsplit <= 4 && env_int("GHIP_FA_MERGE_P4", 1) ? "ghip_fa_merge_rows_p4" : "ghip_fa_merge_rows",

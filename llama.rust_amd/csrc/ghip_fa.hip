@@ -60,6 +60,9 @@ struct FaParams {
     // value -inf, 1 otherwise (ghip_fa_mask_scan); null: no flags
     const uint8_t *mflags;
     int nqb, ntile;
+    // prefill over one KV slice (nsplit == 1): write the normalized output
+    // instead of a partial for ghip_fa_merge_rows
+    int direct;
 };
 
 DEV float head_slope(const FaParams &p, int h) {
@@ -372,6 +375,38 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _F
             for (int gq = 0; gq < 4; gq++) mr[jt][gq] = mrn[jt][gq];
     }
 
+    // one slice: the output row, with ghip_fa_merge_rows' arithmetic for one
+    // partial (weight e^(M - M) = 1 applied by the same fma, the sink, 1 / S),
+    // so the bits are those of the partial-and-merge route
+    if (p.direct) {
+        if (tvalid) {
+            const float mz = m_ref * 0.6931471805599453f, sz = l_run;
+            const float M = sz != 0.0f ? mz : -__builtin_inff();
+            const float wz = (sz != 0.0f && M != -__builtin_inff()) ? __expf(mz - M) : 0.0f;
+            float S = sz * wz;
+            float ms = 1.0f;
+            if (p.sinks) {
+                const float sv = p.sinks[h];
+                if (sv > M) {
+                    ms = __expf(M - sv);
+                    S = S * ms + 1.0f;
+                } else {
+                    S = S + __expf(sv - M);
+                }
+            }
+            const float sinv = S == 0.0f ? 0.0f : 1.0f / S;
+            float *orow = p.dst + ((int64_t)t * p.H + h) * D;
+#pragma unroll
+            for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    float a = fmaf(o[dt][v], wz, 0.0f);
+                    if (p.sinks && p.sinks[h] > M) a *= ms;
+                    orow[32 * dt + crow32(v, lane)] = a * sinv;
+                }
+        }
+        return;
+    }
     // write this slice's partial (M in natural-log units, S, unnormalized O)
     // for query t, head h; lanes l and l^32 hold complementary d ranges
     if (tvalid) {

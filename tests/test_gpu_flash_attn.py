@@ -244,3 +244,39 @@ def test_merge_preload_four(be, sinks):
                                    n_chunks=8)
         err = float(np.max(np.abs(outs[1][:, h:h + 1] - want)))
         assert err <= TOL, f"head {h}: max-abs {err:.3e}"
+
+
+@pytest.mark.parametrize("T,S,D,masked,sinks", [(96, 640, 128, True, True), (130, 1000, 64, False, False),
+                                                (64, 300, 128, True, False), (200, 2048, 64, True, True)])
+def test_single_slice_direct(be, monkeypatch, T, S, D, masked, sinks):
+    """One KV slice (GHIP_FA_WGS=1 forces it at these sizes; long prefills
+    get it by themselves): the forward kernel writes the normalized rows,
+    no partials and no merge launch.  Same bits as the partial-and-merge
+    route (GHIP_FA_DIRECT=0), and the oracle's result."""
+    H, Hkv = 8, 2
+    rng = np.random.default_rng(T + S + D + 1)
+    q = rng.standard_normal((H, T, D)).astype(np.float32)
+    k = rng.standard_normal((Hkv, S, D)).astype(np.float16)
+    v = rng.standard_normal((Hkv, S, D)).astype(np.float16)
+    m = None
+    if masked:
+        m = np.zeros((T, S), dtype=np.float16)
+        for i in range(T):
+            m[i, S - T + i + 1:] = -np.inf
+        m[:32, :] = -np.inf  # a query block with no visible key
+    sk = (rng.standard_normal(H) * 2.0).astype(np.float32) if sinks else None
+    scale = 1.0 / np.sqrt(D)
+    t = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    print(f"fa single slice T={T} S={S} D={D} masked={masked} sinks={sinks}", flush=True)
+    monkeypatch.setenv("GHIP_FA_WGS", "1")
+    outs = []
+    for flag in ("0", "1"):
+        monkeypatch.setenv("GHIP_FA_DIRECT", flag)
+        outs.append(be.flash_attn_ext(t(q), t(k), t(v), t(m), t(sk), scale).cpu().numpy())
+    assert np.array_equal(outs[0], outs[1])
+    for h in (0, 5):
+        g = h // (H // Hkv)
+        want, _ = O.flash_attn_ext(q[h:h + 1], k[g:g + 1], v[g:g + 1], m, None if sk is None else sk[h:h + 1], scale,
+                                   n_chunks=8)
+        err = float(np.max(np.abs(outs[1][:, h:h + 1] - want)))
+        assert err <= TOL, f"head {h}: max-abs {err:.3e}"

@@ -237,3 +237,32 @@ def test_prequantized_inputs(be, monkeypatch, m):
         single = be.mul_mat(ws[nm], ty, kk, src[nm])
         torch.cuda.synchronize()
         assert torch.equal(got[nm], single), nm
+
+
+def test_prequantized_inputs_past_eight(be, monkeypatch):
+    """More than 8 independent inputs: the first 8 are quantized up front in
+    one launch, the rest by their own nodes; every output equals the result
+    without the pre-pass and ghip_mul_mat's (4 activation rows, Q4_K and
+    Q6_K nodes, ragged row counts)."""
+    import ghip
+    k, m = 512, 4
+    g = torch.Generator(device="cuda").manual_seed(77)
+    specs = [(12 if i % 3 else 14, 64 + 40 * i) for i in range(10)]
+    ws = [weights(be, ty, n, k, 100 + i) for i, (ty, n) in enumerate(specs)]
+    xs = [torch.randn((m, k), device="cuda", generator=g) for _ in specs]
+    print("prequantized inputs past eight", flush=True)
+
+    def run():
+        outs = [torch.full((m, n), float("nan"), device="cuda") for _, n in specs]
+        be.graph_compute([ghip.mul_mat_node(w, ty, k, x, o) for w, (ty, _), x, o in zip(ws, specs, xs, outs)])
+        torch.cuda.synchronize()
+        return outs
+
+    got = run()
+    monkeypatch.setenv("GHIP_GRAPH_PREQUANT", "0")
+    want = run()
+    for i, (ty, _) in enumerate(specs):
+        assert torch.equal(got[i], want[i]), i
+        single = be.mul_mat(ws[i], ty, k, xs[i])
+        torch.cuda.synchronize()
+        assert torch.equal(got[i], single), i

@@ -610,7 +610,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "the path shards by weight rows / experts / KV heads, see DESIGN.md", file=sys.stderr)
+              "the path would shard by weight rows / experts / KV heads (not built)", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

@@ -270,6 +270,10 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _F
         const bool mzero = __ballot(mor != 0) == 0;
         // scores of this lane: keys 32*jt + crow32(v), query t
         float s[2][16];
+        // the MFMA runs (K·Qᵀ here, P·V below) issue at raised wave priority, so
+        // the SIMD's other wavefront fills their gaps with its softmax work
+        // (measured: 138 -> 135 us on the T = 512, S = 8192 prefill)
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int jt = 0; jt < 2; jt++) {
             v16f acc;
@@ -280,6 +284,7 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _F
                 const v8h a = *reinterpret_cast<const v8h *>(&Ks[(32 * jt + li) * KS + 16 * kk + 8 * h2]);
                 acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[kk], acc, 0, 0, 0);
             }
+            if (jt == 1) __builtin_amdgcn_s_setprio(0);
 #pragma unroll
             for (int v = 0; v < 16; v++) {
                 // relative to the reference max: x' = s2 - m_ref
@@ -340,6 +345,7 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _F
         psum += __shfl_xor(psum, 32, 64);
         l_run += psum;
         // O^T += V^T P^T over the 64 keys: 4 MFMAs of 16 keys per d-tile
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int jt = 0; jt < 2; jt++)
 #pragma unroll
@@ -366,6 +372,7 @@ __device__ __forceinline__ void fa_fwd_body(const FaParams &p, _Float16 *Ks2, _F
                     o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb, o[dt], 0, 0, 0);
                 }
             }
+        __builtin_amdgcn_s_setprio(0);
         }  // cls != 2
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // tile it+1's K, V and mask are in
         __syncthreads();
